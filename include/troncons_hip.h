@@ -1,0 +1,172 @@
+/*
+ * troncons_hip.h — C-ABI of the MI355X (gfx950) expert hot path of troncons.
+ *
+ * Drop-in boundary: these entry points replace the CUDA launch layer of the reference engine,
+ * i.e. the methods of `trc_noyaux::Noyaux` (moteur/crates/trc-noyaux/src/lib.rs) and the host
+ * helpers of `trc_noyaux::abi` (moteur/crates/trc-noyaux/src/abi.rs). Arguments keep the
+ * reference's order and meaning; each declaration cites the function it replaces. A Rust crate
+ * binds them with `extern "C"`; nothing here uses torch or HIP types.
+ *
+ * Conventions (mirroring trc_cuda::Erreur, moteur/crates/trc-cuda/src/lib.rs:34-41):
+ *   - every launch function returns TRC_OK, TRC_ERREUR_USAGE (a contract violation found before any
+ *     HIP call: nothing was launched), TRC_ERREUR_HIP (a HIP call failed) or TRC_ERREUR_PILOTE (no
+ *     usable device); trc_derniere_erreur() gives the message of the calling thread's last error;
+ *   - launches are asynchronous on `flux` (a hipStream_t); data errors found by kernels are never
+ *     returned: they are counted into the caller's zeroed u32[4] control buffer
+ *     ([0] lanes not ending on L, [1] format errors, [2] tile word-pointer mismatches, [3] 0);
+ *   - the caller owns every allocation; a trc_vue borrows device memory for the call only.
+ */
+#ifndef TRONCONS_HIP_H
+#define TRONCONS_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TRC_OK 0
+#define TRC_ERREUR_USAGE 1
+#define TRC_ERREUR_HIP 2
+#define TRC_ERREUR_PILOTE 3
+
+/* VueCarte {u64 adresse; usize octets} (moteur/crates/trc-cuda/src/lib.rs:432-460): a device
+ * address and a size in bytes. adresse == 0 stands for an absent optional view (Option::None). */
+typedef struct {
+    uint64_t adresse;
+    uint64_t octets;
+} trc_vue;
+
+/* DimsExpert, 24 bytes, align 4 (abi.rs:8-13) */
+typedef struct {
+    uint32_t lignes[3];
+    uint32_t colonnes[3];
+} trc_dims_expert;
+
+/* DescGemv, 32 bytes (abi.rs:18-27) */
+typedef struct {
+    uint64_t matrice;
+    uint64_t x;
+    uint64_t y;
+    uint32_t lignes;
+    uint32_t colonnes;
+} trc_desc_gemv;
+
+/* DescDecodage, 32 bytes (abi.rs:33-42) */
+typedef struct {
+    uint64_t partie;
+    uint64_t emplacement;
+    uint64_t luts;
+    uint64_t controle;
+} trc_desc_decodage;
+
+/* Disposition of one matrix in the SoA slot (abi.rs:76-81) */
+typedef struct {
+    uint64_t base;
+    uint64_t echelles;
+    uint64_t biais;
+    uint64_t pas;
+} trc_disposition;
+
+/* Message of the calling thread's last error ("" if none). */
+const char* trc_derniere_erreur(void);
+
+/* ------------------------------------------------------------- host helpers (no device needed) */
+
+/* disposition_matrice (abi.rs:83-88) */
+trc_disposition trc_disposition_matrice(uint32_t lignes, uint32_t colonnes);
+/* DimsExpert::verifier (abi.rs:94-105): TRC_OK or TRC_ERREUR_USAGE */
+int trc_dims_verifier(const trc_dims_expert* dims);
+/* DimsExpert::disposition (abi.rs:108-111) */
+trc_disposition trc_disposition_j(const trc_dims_expert* dims, uint32_t j);
+/* DimsExpert::taille_emplacement (abi.rs:114-116) */
+uint64_t trc_taille_emplacement(const trc_dims_expert* dims);
+/* grilles_decodeur (abi.rs:137-141): grids (x, 3, 1) of decoder_echelles and decoder_codes */
+void trc_grilles_decodeur(const trc_dims_expert* dims, uint32_t g_echelles[3], uint32_t g_codes[3]);
+/* grilles_depuis_partie (abi.rs:149-176): grids sized on the tiles a part really has */
+int trc_grilles_depuis_partie(const uint8_t* partie, size_t octets, uint32_t g_echelles[3], uint32_t g_codes[3]);
+/* grille_brut (abi.rs:179-182) */
+void trc_grille_brut(const trc_dims_expert* dims, uint32_t g[3]);
+/* lut_geometrie1 (abi.rs:187-204): n must be 256, frequencies must sum to 4096 */
+int trc_lut_geometrie1(const uint16_t* freq, size_t n, uint32_t* lut /* [4096] */);
+/* luts_couche (abi.rs:210-221): freqs[j*4 + t] (t = 0 DELTA, 1 + kappa CODES_CTX) or NULL;
+ * luts receives u32[3][4][4096] */
+int trc_luts_couche(const uint16_t* const* freqs, uint32_t* luts);
+
+/* ---------------------------------------- launches: the reference kernel API (Noyaux methods) */
+
+/* Noyaux::decoder_expert (moteur/crates/trc-noyaux/src/lib.rs:118-135): decodes a level-0 part
+ * (v1.0/v1.2) into the SoA slot; two launches (scales, then codes) on flux. */
+int trc_decoder_expert(trc_vue partie, trc_vue emplacement, trc_vue luts, const trc_dims_expert* dims,
+                       trc_vue controle, void* flux);
+
+/* Noyaux::decoder_expert_grilles (lib.rs:142-184): same with explicit grids (any grid is right). */
+int trc_decoder_expert_grilles(trc_vue partie, trc_vue emplacement, trc_vue luts, const trc_dims_expert* dims,
+                               trc_vue controle, const uint32_t g_echelles[3], const uint32_t g_codes[3], void* flux);
+
+/* Noyaux::decoder_lot (lib.rs:190-205): n experts of the same dimensions, descs = DescDecodage[n]
+ * in device memory. */
+int trc_decoder_lot(trc_vue descs, uint32_t n, const trc_dims_expert* dims, void* flux);
+
+/* Noyaux::copier_brut (lib.rs:210-233): raw-file path (flag bit 2). */
+int trc_copier_brut(trc_vue partie, trc_vue emplacement, const trc_dims_expert* dims, trc_vue controle, void* flux);
+
+/* Noyaux::gemv (lib.rs:239-268): y = W x + b for one slot matrix; bit-identical to the
+ * reference's operation order (gemv.cuh:60-126). */
+int trc_gemv(trc_vue matrice, trc_vue x, trc_vue y, uint32_t lignes, uint32_t colonnes, void* flux);
+
+/* Noyaux::gemv_lot (lib.rs:274-284): n products from DescGemv[n] in device memory. */
+int trc_gemv_lot(trc_vue descs, uint32_t n, uint32_t lignes_max, void* flux);
+
+/* Noyaux::gemv_f32 (lib.rs:307-318): y = W x (+ b), W f32 row-major (the router). */
+int trc_gemv_f32(trc_vue w, trc_vue x, trc_vue biais, trc_vue y, uint32_t lignes, uint32_t colonnes, void* flux);
+
+/* Noyaux::routeur_topk (lib.rs:418-429): top-k indices and f64-softmax weights; boite = device
+ * address of a mapped mailbox or 0 (words 1..k indices, k+1..2k weights, then word 0 = sequence,
+ * written last after a system-scope fence). */
+int trc_routeur_topk(trc_vue logits, uint32_t experts, uint32_t k, trc_vue indices, trc_vue poids, uint64_t boite,
+                     uint32_t sequence, void* flux);
+
+/* Noyaux::swiglu_oai (lib.rs:451-458) */
+int trc_swiglu_oai(trc_vue g, trc_vue u, trc_vue y, uint32_t n, void* flux);
+
+/* Noyaux::combiner (lib.rs:463-476): residu[i] += ((w0 s0 + w1 s1) + w2 s2) + ..., no FMA. */
+int trc_combiner(trc_vue residu, trc_vue sorties, uint32_t pas, trc_vue poids, uint32_t n, uint32_t d, void* flux);
+
+/* ---------------------------------------- encoder front-end (host only; role of bins/trc-codeur) */
+
+/* The seeded synthetic workload (nibble law "A", E8M0 scales in [119,125], bf16 N(0,0.02) biases).
+ * One R x C matrix of 17-byte MXFP4 blocks [e, qs16] in beta order, plus R biases. */
+void trc_synth_matrice(uint64_t graine, uint32_t couche, uint32_t expert, uint32_t cle, uint32_t R, uint32_t C,
+                       uint8_t* blocs17, float* biais);
+/* n bf16-valued N(0, sigma) floats (activations, router weights). */
+void trc_synth_normale_bf16(uint64_t graine, uint32_t cle1, uint32_t cle2, uint32_t n, float sigma, float* out);
+/* Synthetic expert: gate_up generated as one (2R) x C interleaved matrix, de-interleaved into
+ * j = 0 (gate, even rows) and j = 1 (up, odd rows); down is j = 2. */
+int trc_synth_expert(uint64_t graine, uint32_t couche, uint32_t expert, const trc_dims_expert* dims,
+                     uint8_t* const* blocs17, float* const* biais);
+/* ComptesMatrice + tables() (moteur/crates/trc-codec/src/lib.rs:378-413): the 4 x 256 frequencies
+ * (DELTA, CODES_CTX kappa = 0, 1, 2) of one (layer, matrix) from its experts' blocks. */
+int trc_codeur_tables(const uint8_t* const* blocs17, uint32_t n_experts, uint32_t R, uint32_t B, int canonique,
+                      uint16_t* freqs4);
+/* coder_matrice_v10 x 3 + assembler_partie (lib.rs:417-428, trc-format/src/lib.rs:879-910):
+ * a level-0 part; N_delta / N_codes macro-steps per tile. Returns the part length (0 on error). */
+uint64_t trc_codeur_partie(uint16_t couche, uint16_t expert, const trc_dims_expert* dims,
+                           const uint8_t* const* blocs17, const float* const* biais, const uint16_t* const* freqs4,
+                           int canonique, uint32_t N_delta, uint32_t N_codes, uint8_t* out, uint64_t cap,
+                           uint32_t* utiles);
+/* A whole synthetic layer (tables from all its experts, v1.2 parts), built on n_fils threads. */
+typedef struct trc_couche_synth trc_couche_synth;
+trc_couche_synth* trc_synth_couche(uint64_t graine, uint32_t couche, uint32_t n_experts, const trc_dims_expert* dims,
+                                   uint32_t N_delta, uint32_t N_codes, uint32_t n_fils);
+uint64_t trc_synth_couche_taille(const trc_couche_synth* c, uint32_t expert);
+uint32_t trc_synth_couche_utiles(const trc_couche_synth* c, uint32_t expert);
+const uint8_t* trc_synth_couche_partie(const trc_couche_synth* c, uint32_t expert);
+const uint16_t* trc_synth_couche_freqs(const trc_couche_synth* c); /* [3][4][256] */
+void trc_synth_couche_liberer(trc_couche_synth* c);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

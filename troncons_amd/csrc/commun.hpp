@@ -1,0 +1,215 @@
+// commun.hpp — definitions shared by the host helpers and the gfx950 kernels of the expert hot path.
+//
+// Format facts restated from the reference's frozen seams (decisions/ARCHITECTURE.md §4.8-4.9, §5.6):
+// the level-0 part (64-byte header, 16-byte stream descriptors), the rANS stream header
+// (P, N, geometry, T, W, starts[T], states[32T], words[W]) and the SoA slot layout
+// (codes, scales at al256(R*B*16), biases at al256(scales + R*B), stride al256(biases + 4R)).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/troncons_hip.h"
+
+namespace trc {
+
+constexpr uint32_t PROBA_BITS = 12;
+constexpr uint32_t M = 1u << PROBA_BITS;  // 4096 slots
+constexpr uint32_t L = 1u << 16;          // lower bound of a lane state
+constexpr uint32_t VOIES = 32;            // lanes per tile
+constexpr uint32_t MAGIE_PARTIE0 = 0x30435254u;  // "TRC0"
+
+constexpr uint8_t SORTE_MEDIANES = 0x01;
+constexpr uint8_t SORTE_BIAIS = 0x02;
+constexpr uint8_t SORTE_DELTA = 0x03;
+constexpr uint8_t SORTE_CODES_CTX = 0x04;
+constexpr uint8_t SORTE_CODES_BRUTS = 0x06;
+constexpr uint8_t SORTE_ECHELLES_BRUTES = 0x07;
+
+// Control buffer slots (u32[4], zeroed by the caller).
+constexpr int CTL_HORS_L = 0;
+constexpr int CTL_FORMAT = 1;
+constexpr int CTL_POINTEUR = 2;
+
+// Threads per block of the reference-API kernels (abi.rs:56-61 keeps these a launch detail).
+constexpr uint32_t FILS_ECHELLES = 128;  // 2 wavefronts = 4 DELTA tiles
+constexpr uint32_t FILS_CODES = 256;     // 4 wavefronts = 8 CODES_CTX tiles
+constexpr uint32_t FILS_BRUT = 256;
+constexpr uint32_t GEMV_FILS = 256;
+constexpr uint32_t GEMV_LIGNES_PAR_BLOC = 32;  // 8 half-wavefronts x 4 rows
+constexpr uint32_t LUTS_PAR_COUCHE = 3 * 4 * 4096;
+constexpr uint32_t MACRO_PAR_TUILE = 256;  // what the reference encoder writes; used for grids only
+
+__host__ __device__ inline uint64_t al256(uint64_t x) { return (x + 255u) & ~uint64_t(255); }
+
+__host__ __device__ inline trc_disposition disposition_matrice(uint32_t lignes, uint32_t colonnes) {
+    const uint64_t blocs = uint64_t(lignes) * (colonnes / 32u);
+    trc_disposition d;
+    d.base = 0;
+    d.echelles = al256(blocs * 16u);
+    d.biais = al256(d.echelles + blocs);
+    d.pas = al256(d.biais + 4ull * lignes);
+    return d;
+}
+
+// Element j of a 3-array without a dynamic index (a dynamic index would spill it to scratch).
+__host__ __device__ __forceinline__ uint32_t choisir(const uint32_t (&a)[3], uint32_t j) {
+    return j == 0 ? a[0] : (j == 1 ? a[1] : a[2]);
+}
+
+__host__ __device__ inline trc_disposition disposition(const trc_dims_expert& dims, uint32_t j) {
+    uint64_t base = 0;
+#pragma unroll
+    for (uint32_t i = 0; i < 3; ++i)
+        if (i < j) base += disposition_matrice(dims.lignes[i], dims.colonnes[i]).pas;
+    trc_disposition d = disposition_matrice(choisir(dims.lignes, j), choisir(dims.colonnes, j));
+    d.base = base;
+    return d;
+}
+
+// ------------------------------------------------------------------------- device-side part reading
+
+__device__ __forceinline__ uint32_t lire_u32(const uint8_t* p) {
+    return uint32_t(p[0]) | (uint32_t(p[1]) << 8) | (uint32_t(p[2]) << 16) | (uint32_t(p[3]) << 24);
+}
+__device__ __forceinline__ uint32_t lire_u16(const uint8_t* p) { return uint32_t(p[0]) | (uint32_t(p[1]) << 8); }
+
+struct DescFlux {
+    const uint8_t* p;
+    uint32_t longueur;
+    uint32_t produits;
+};
+
+// Finds stream (kind, matrix) in a level-0 part; false if the part is malformed or the stream is
+// absent (same acceptance as the reference device reader, commun.cuh:111-129).
+__device__ inline bool trouver_flux(const uint8_t* partie, uint8_t sorte, uint32_t matrice, DescFlux& f) {
+    if (lire_u32(partie) != MAGIE_PARTIE0) return false;
+    if (partie[8] != 0) return false;
+    const uint32_t n_flux = lire_u16(partie + 10);
+    const uint32_t utiles = lire_u32(partie + 12);
+    if (n_flux > 64 || 64u + 16u * n_flux > utiles) return false;
+    for (uint32_t i = 0; i < n_flux; ++i) {
+        const uint8_t* e = partie + 64 + 16 * i;
+        if (e[0] == sorte && e[1] == matrice) {
+            const uint32_t dec = lire_u32(e + 4), lon = lire_u32(e + 8);
+            if ((dec & 15u) != 0 || uint64_t(dec) + lon > utiles) return false;
+            f.p = partie + dec;
+            f.longueur = lon;
+            f.produits = lire_u32(e + 12);
+            return true;
+        }
+    }
+    return false;
+}
+
+// A validated rANS stream header (geometry 1).
+struct EnteteRans {
+    uint32_t P, N, T, W;
+    const uint32_t* debut;   // T word indices
+    const uint32_t* etats;   // 32*T lane states
+    const uint16_t* mots;    // W 16-bit words
+};
+
+// `besoin`: bytes the caller needs; the stream produces P >= besoin with less than 128 bytes of
+// padding, and its descriptor announces P or besoin (commun.cuh:143-165).
+__device__ inline bool lire_entete(const DescFlux& f, uint32_t besoin, EnteteRans& h) {
+    if (f.longueur < 16) return false;
+    h.P = lire_u32(f.p);
+    h.N = lire_u16(f.p + 4);
+    const uint32_t geo = f.p[6];
+    h.T = lire_u32(f.p + 8);
+    h.W = lire_u32(f.p + 12);
+    if (geo != 1 || h.N == 0 || (h.P & 127u) != 0) return false;
+    if (h.P < besoin || h.P - besoin >= 128u) return false;
+    if (f.produits != h.P && f.produits != besoin) return false;
+    const uint32_t macro = h.P / 128u;
+    if (h.T != (macro + h.N - 1) / h.N) return false;
+    const uint64_t fin = 16ull + 132ull * h.T + 2ull * h.W;
+    if (fin > f.longueur) return false;
+    h.debut = reinterpret_cast<const uint32_t*>(f.p + 16);
+    h.etats = reinterpret_cast<const uint32_t*>(f.p + 16 + 4ull * h.T);
+    h.mots = reinterpret_cast<const uint16_t*>(f.p + 16 + 132ull * h.T);
+    return true;
+}
+
+// Scale class kappa of a block from its scale e and its row median (delta = e - med + 128 mod 256).
+__device__ __forceinline__ uint32_t classe_echelle(uint32_t e, uint32_t med) {
+    const uint32_t delta = (e - med + 128u) & 255u;
+    return delta < 128u ? 0u : (delta == 128u ? 1u : 2u);
+}
+
+// -------------------------------------------------------------------------------- the rANS step
+//
+// MI355X mapping: a wavefront (64 lanes) carries two tiles, lanes 0-31 tile 2w and lanes 32-63
+// tile 2w+1. Within a half, renormalising lanes take consecutive words of their tile's stream in
+// lane order: position = half pointer + popcount of the lower lanes of the same half that also
+// renormalise (one 64-bit ballot, the half's 32 bits, one masked bit count).
+struct DemiVague {
+    uint32_t masque_inf;  // lanes of my half below me
+    bool haut;            // upper half of the wavefront
+};
+
+__device__ __forceinline__ DemiVague demi_vague() {
+    const uint32_t lane = __lane_id();
+    DemiVague d;
+    d.haut = lane >= 32u;
+    d.masque_inf = (1u << (lane & 31u)) - 1u;
+    return d;
+}
+
+// One decode step with a reference-format LUT entry s | (f-1) << 8 | b << 20. Reads the word at
+// the half's pointer (0 past the stream, like the reference's bounded word reader). Returns s.
+__device__ __forceinline__ uint32_t pas_octet(uint32_t& x, uint32_t& ptr, const uint32_t* __restrict__ lut,
+                                              const uint16_t* __restrict__ mots, uint32_t W, DemiVague d,
+                                              bool actif) {
+    const uint32_t e = lut[x & (M - 1u)];
+    const uint32_t y = (((e >> 8) & 0xFFFu) + 1u) * (x >> PROBA_BITS) + (e >> 20);
+    const bool besoin = actif && (y < L);
+    const uint64_t vote = __ballot(besoin);
+    const uint32_t moitie = d.haut ? uint32_t(vote >> 32) : uint32_t(vote);
+    const uint32_t pos = ptr + __popc(moitie & d.masque_inf);
+    uint32_t w = 0;
+    if (besoin && pos < W) w = mots[pos];
+    if (actif) {
+        x = besoin ? ((y << 16) | w) : y;
+        ptr += __popc(moitie);
+    }
+    return e & 0xFFu;
+}
+
+// Integer wave sum, fixed tree (exact and deterministic).
+__device__ __forceinline__ uint32_t somme_vague_u32(uint32_t v) {
+#pragma unroll
+    for (int d = 32; d > 0; d >>= 1) v += __shfl_xor(v, d);
+    return v;
+}
+
+__device__ __forceinline__ void verser_controle(uint32_t* controle, uint32_t hors_l, uint32_t pointeur) {
+    hors_l = somme_vague_u32(hors_l);
+    pointeur = somme_vague_u32(pointeur);
+    if (__lane_id() == 0) {
+        if (hors_l) atomicAdd(&controle[CTL_HORS_L], hors_l);
+        if (pointeur) atomicAdd(&controle[CTL_POINTEUR], pointeur);
+    }
+}
+
+// 32-lane xor butterfly within each half-wavefront (the reference's warp reduction tree).
+__device__ __forceinline__ float somme_demi_f32(float v) {
+#pragma unroll
+    for (int d = 16; d > 0; d >>= 1) v += __shfl_xor(v, d);
+    return v;
+}
+
+// 2^(e-128) in f32, exact for every e (e = 0, 1 are subnormal).
+__device__ __forceinline__ float echelle_e8m0(uint32_t e) {
+    const uint32_t bits = e >= 2u ? (e - 1u) << 23 : (0x00200000u << e);
+    return __uint_as_float(bits);
+}
+
+// Doubled E2M1 magnitude (0xC8643210 nibble table), bit 3 = sign; code 8 reads as -0.
+__device__ __forceinline__ float valeur_e2m1x2(uint32_t c) {
+    const float g = float((0xC8643210u >> ((c & 7u) << 2)) & 15u);
+    return (c & 8u) ? -g : g;
+}
+
+}  // namespace trc
