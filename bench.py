@@ -1,0 +1,231 @@
+#!/usr/bin/env python3
+"""Benchmark of the fused MoE layer at batch 1 on one MI355X.
+
+128 rANS-coded experts of gpt-oss-120b shape (.trc v1.2 level-0 parts, seeded synthetic MXFP4)
+sit resident in HBM with a bf16 2880 x 128 router. A step is one token through the layer: router
+logits, top-4 with softmax weights, the 4 selected experts decoded inside their fused GEMVs
+(gate/up -> SwiGLU -> down), and the weighted combine; the token sweep uses 1000 seeded
+activations, so routing is uniform-random. Prints ONE JSON line (see DESIGN.md for every field).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import pathlib
+import struct
+import sys
+import threading
+import time
+
+RACINE = pathlib.Path(__file__).resolve().parent
+sys.path.insert(0, str(RACINE))
+
+METRIQUE = "MoE layer us/token @batch1 top-4; compressed-weight HBM GB/s (% of peak)"
+PIC_HBM = 8000.0  # GB/s, MI355X
+
+
+def lire_flux(partie: bytes):
+    """{(kind, matrix): (offset, length)} from a part's stream table (ARCHITECTURE.md §4.8)."""
+    n = struct.unpack_from("<H", partie, 10)[0]
+    out = {}
+    for i in range(n):
+        e = 64 + 16 * i
+        sorte, j = partie[e], partie[e + 1]
+        dec, lon = struct.unpack_from("<II", partie, e + 4)
+        out[(sorte, j)] = (dec, lon)
+    return out
+
+
+def baseline_cpu(couche, luts, x_tok, selections, budget_s: float, n_fils: int):
+    """The reference's CPU path on this host: decoder_matrice_v10 (rANS DELTA + CODES_CTX) then the
+    scalar f32 MXFP4 GEMV in the reference's order, SwiGLU and the ordered combine, for the first
+    tokens of the sweep until ~budget_s of work (single thread), then the same tokens with the 4
+    experts of a token on n_fils threads."""
+    sys.path.insert(0, str(RACINE / "tests"))
+    import numpy as np
+    import oracle_ffi as O
+
+    def expert(e, x):
+        p = bytes(couche.partie(int(e)))
+        slot, ctl = O.decoder_expert(p, luts, [2880] * 3, [2880] * 3)
+        d = [O.disposition_j([2880] * 3, [2880] * 3, j) for j in range(3)]
+        g = O.gemv_mxfp4(slot[d[0].base:d[0].base + d[0].pas], x, 2880, 2880)
+        u = O.gemv_mxfp4(slot[d[1].base:d[1].base + d[1].pas], x, 2880, 2880)
+        a = O.swiglu_oai(g, u)
+        return O.gemv_mxfp4(slot[d[2].base:d[2].base + d[2].pas], a, 2880, 2880)
+
+    t0 = time.perf_counter()
+    n_tok = 0
+    octets = 0
+    while n_tok < len(selections) and (time.perf_counter() - t0) < budget_s:
+        idx, w = selections[n_tok]
+        s = [expert(e, x_tok[n_tok]) for e in idx]
+        O.combiner(np.zeros(2880, np.float32), np.concatenate(s), 2880, w, len(idx), 2880)
+        octets += sum(couche.utiles(int(e)) for e in idx)
+        n_tok += 1
+    dt1 = time.perf_counter() - t0
+    # threaded: the 4 experts of a token in parallel (ctypes releases the GIL)
+    t0 = time.perf_counter()
+    for t in range(n_tok):
+        idx, w = selections[t]
+        res = [None] * len(idx)
+
+        def tache(i, e, t=t):
+            res[i] = expert(e, x_tok[t])
+        th = [threading.Thread(target=tache, args=(i, e)) for i, e in enumerate(idx)]
+        [h.start() for h in th]
+        [h.join() for h in th]
+    dtn = time.perf_counter() - t0
+    return {
+        "value": dt1 / n_tok * 1e6, "unit": "us/token", "cores": 1, "kind": "port",
+        "gbps_compressed": octets / dt1 / 1e9,
+        "threaded": {"value": dtn / n_tok * 1e6, "unit": "us/token", "cores": min(n_fils, 4)},
+        "sample": f"{n_tok} tokens of the sweep x 4 experts (decode DELTA+CODES_CTX, f32 GEMV x3, SwiGLU, combine)",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=1000)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--experts", type=int, default=128)
+    ap.add_argument("--k", type=int, default=4)
+    ap.add_argument("--n-codes", type=int, default=32, help="macro-steps per CODES_CTX tile written by the encoder")
+    ap.add_argument("--n-delta", type=int, default=16, help="macro-steps per DELTA tile written by the encoder")
+    ap.add_argument("--graine", type=int, default=2026)
+    ap.add_argument("--tokens", type=int, default=1000)
+    ap.add_argument("--sans-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--budget-cpu", type=float, default=12.0, help="seconds of single-thread CPU baseline work")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for {args.gpus}); the expert-parallel "
+              "sharding across GPUs is described in DESIGN.md, not run.", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    from troncons_amd import codeur, fusion
+    from troncons_amd.noyaux import DimsExpert, VueCarte
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    dev = torch.device("cuda:0")
+    dims = DimsExpert.gpt_oss()
+    E, k, C = args.experts, args.k, 2880
+    n_fils = min(16, os.cpu_count() or 1)
+
+    t = time.perf_counter()
+    couche = codeur.CoucheSynthetique(args.graine, 0, E, dims, N_delta=args.n_delta, N_codes=args.n_codes,
+                                      n_fils=n_fils)
+    t_gen = time.perf_counter() - t
+    tailles = [couche.taille(e) for e in range(E)]
+    utiles = np.array([couche.utiles(e) for e in range(E)], np.int64)
+    decal = np.concatenate([[0], np.cumsum(tailles)[:-1]]).astype(np.int64)
+    bloc = torch.empty(int(sum(tailles)) + 256, dtype=torch.uint8, device=dev)
+    base = bloc.data_ptr() + ((-bloc.data_ptr()) % 256)
+    octets_codes = np.zeros((E, 3), np.int64)
+    for e in range(E):
+        p = couche.partie(e)
+        off = int(decal[e]) + ((-bloc.data_ptr()) % 256)
+        bloc[off:off + p.size].copy_(torch.from_numpy(p))
+        fl = lire_flux(p[:64 + 16 * 12].tobytes())
+        for j in range(3):
+            octets_codes[e, j] = fl[(4, j)][1]
+    table = torch.from_numpy(np.array([base + int(d) for d in decal], np.uint64).view(np.int64)).to(dev)
+    freqs = couche.freqs()
+    from troncons_amd import noyaux as K
+    luts_np = K.luts_couche([[freqs[j][t] for t in range(4)] for j in range(3)])
+    luts = torch.from_numpy(luts_np.view(np.int32)).to(dev)
+    routeur = np.stack([codeur.synth_normale_bf16(args.graine, 3, e, C, 0.02) for e in range(E)])
+    r16 = torch.from_numpy((routeur.view(np.uint32) >> 16).astype(np.uint16).view(np.int16)).to(dev)
+    x_tok = np.stack([codeur.synth_normale_bf16(args.graine, 4, t, C, 1.0) for t in range(args.tokens)])
+    xs = torch.from_numpy(x_tok).to(dev)
+    residu = torch.zeros(C, dtype=torch.float32, device=dev)
+    n_sel = max(args.steps, args.warmup, 1)
+    sel_i = torch.zeros((n_sel, 8), dtype=torch.int32, device=dev)
+    sel_w = torch.zeros((n_sel, 8), dtype=torch.float32, device=dev)
+    ctl = torch.zeros(4, dtype=torch.int32, device=dev)
+    travail = torch.empty(fusion.taille_travail_couche(dims, E, k, args.n_codes) + 256, dtype=torch.uint8, device=dev)
+    tr = VueCarte(travail.data_ptr() + ((-travail.data_ptr()) % 256), fusion.taille_travail_couche(dims, E, k,
+                                                                                                  args.n_codes))
+    fz = fusion.Fusion()
+    flux = torch.cuda.current_stream()
+    V = VueCarte.de
+    vt, vl, vr, vres, vctl = V(table), V(luts), V(r16), V(residu), V(ctl)
+    vx = [V(xs, 4 * C * t, 4 * C) for t in range(args.tokens)]
+    vi = [V(sel_i, 32 * s, 32) for s in range(n_sel)]
+    vw = [V(sel_w, 32 * s, 32) for s in range(n_sel)]
+
+    def pas(s):
+        fz.couche_moe(vt, E, vl, dims, vr, None, vx[s % args.tokens], k, vres, vi[s], vw[s], vctl, tr,
+                      args.n_delta, args.n_codes, f=flux)
+
+    for s in range(args.warmup):
+        pas(s)
+    torch.cuda.synchronize()
+    debut, fin = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    debut.record(flux)
+    for s in range(args.steps):
+        pas(s)
+    fin.record(flux)
+    torch.cuda.synchronize()
+    ms = debut.elapsed_time(fin)
+    assert (ctl.cpu().numpy() == 0).all(), f"control words {ctl.cpu().numpy()}"
+    sel = sel_i[:args.steps, :k].cpu().numpy()
+    octets_tok = utiles[sel].sum(axis=1)
+    us_tok = ms * 1e3 / args.steps
+    gbps = octets_tok.sum() / (ms * 1e-3) / 1e9
+
+    # chronogram pass (separate from the timed region: events between kernels add gaps)
+    n_chrono = min(args.steps, 200)
+    fusion.chrono(True)
+    fusion.chrono_recolter(True)
+    for s in range(n_chrono):
+        pas(s)
+    torch.cuda.synchronize()
+    noyaux = fusion.chrono_recolter(True)
+    fusion.chrono(False)
+    sel_c = sel_i[:n_chrono, :k].cpu().numpy()
+    gu_ms, gu_n = noyaux.get("fusion_gemv/gate_up", (0.0, 1))
+    bas_ms, bas_n = noyaux.get("fusion_gemv/down", (0.0, 1))
+    octets_gu = octets_codes[sel_c][:, :, :2].sum() / n_chrono
+    octets_bas = octets_codes[sel_c][:, :, 2].sum() / n_chrono
+    duree_us = (gu_ms / gu_n + bas_ms / bas_n) * 1e3
+    atteint = (octets_gu + octets_bas) / (duree_us * 1e-6) / 1e9
+    roofline = {
+        "bound": "hbm", "kernel": "fusion_gemv (gate/up launch + down launch)",
+        "achieved": round(float(atteint), 1), "peak": PIC_HBM, "unit": "GB/s",
+        "frac": round(float(atteint / PIC_HBM), 4), "traffic": None,
+        "bytes_per_launch": {"gate_up": int(octets_gu), "down": int(octets_bas)},
+        "avg_launch_us": {"gate_up": round(gu_ms / gu_n * 1e3, 2), "down": round(bas_ms / bas_n * 1e3, 2)},
+    }
+    chrono_us = {nom: round(v[0] / v[1] * 1e3, 2) for nom, v in noyaux.items()}
+
+    ligne = {
+        "metric": METRIQUE, "value": round(us_tok, 3), "unit": "us/token", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms / args.steps, 5), "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": "u32 rANS / f32 GEMV",
+        "data": "synthetic (seeded MXFP4 law A, E8M0 in [119,125], bf16 N(0,1) activations, bf16 N(0,0.02) router)",
+        "config": {"workload": "config3: one MoE layer decode step, batch 1, top-4 of 128 gpt-oss-120b experts "
+                               "(3 x 2880x2880 MXFP4, .trc v1.2 rANS-coded), 1000-token seeded sweep",
+                   "experts": E, "k": k, "hidden": C, "n_codes": args.n_codes, "n_delta": args.n_delta,
+                   "tokens": args.tokens, "mean_part_bytes": int(utiles.mean())},
+        "gbps_compressed": round(float(gbps), 1),
+        "frac_hbm_layer": round(float(gbps / PIC_HBM), 4),
+        "compressed_bytes_per_token": int(octets_tok.mean()),
+        "kernel_us": chrono_us,
+        "roofline": roofline,
+        "setup_s": round(t_gen, 1),
+    }
+    if not args.sans_cpu:
+        selections = [(sel[t], sel_w[t, :k].cpu().numpy()) for t in range(min(args.steps, 20))]
+        ligne["cpu_baseline"] = baseline_cpu(couche, luts_np, x_tok, selections, args.budget_cpu, n_fils)
+    else:
+        ligne["cpu_baseline"] = None
+    print(json.dumps(ligne), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -134,6 +134,51 @@ int trc_swiglu_oai(trc_vue g, trc_vue u, trc_vue y, uint32_t n, void* flux);
 /* Noyaux::combiner (lib.rs:463-476): residu[i] += ((w0 s0 + w1 s1) + w2 s2) + ..., no FMA. */
 int trc_combiner(trc_vue residu, trc_vue sorties, uint32_t pas, trc_vue poids, uint32_t n, uint32_t d, void* flux);
 
+/* ------------------------------------- launches: the fused path (extensions of the launch API)
+ *
+ * Added functions, nothing existing changed (the reference's own rule for extending its seam,
+ * moteur/crates/trc-noyaux/noyaux/decodeur.cuh:227-231): the engine's caller of the expert hot
+ * path is Modele::fin_couche (moteur/crates/trc-modele/src/lib.rs:533-553), which runs, per
+ * selected expert, gemv(gate), gemv(up), swiglu_oai, gemv(down) over a decoded slot, then one
+ * combiner. These entry points compute the same results from the coded part directly: the
+ * decoded code bytes never reach device memory. `travail` is a caller-owned device workspace
+ * (256-byte aligned) of at least the size the matching trc_taille_travail_* returns; n_delta and
+ * n_codes are the macro-steps per tile of the DELTA and CODES_CTX streams (they size the grids
+ * only: the kernels read the true N from every stream). Data errors go to `controle` as above. */
+
+/* Workspace bytes of trc_gemv_fusionnee (0 if the shape is refused). */
+uint64_t trc_taille_travail_gemv_fusionnee(uint32_t lignes, uint32_t colonnes, uint32_t n_codes);
+/* Noyaux::decoder_expert + Noyaux::gemv for one matrix j of a part: y = W_j x + b_j. */
+int trc_gemv_fusionnee(trc_vue partie, uint32_t j, trc_vue luts, uint32_t lignes, uint32_t colonnes, trc_vue x,
+                       trc_vue y, trc_vue controle, trc_vue travail, uint32_t n_delta, uint32_t n_codes, void* flux);
+
+/* Workspace bytes of trc_expert_fusionne. */
+uint64_t trc_taille_travail_expert_fusionne(const trc_dims_expert* dims, uint32_t n_codes);
+/* One expert of Modele::fin_couche (trc-modele/src/lib.rs:546-549):
+ * sortie = W_down swiglu_oai(W_gate x + b_gate, W_up x + b_up) + b_down. */
+int trc_expert_fusionne(trc_vue partie, trc_vue luts, const trc_dims_expert* dims, trc_vue x, trc_vue sortie,
+                        trc_vue controle, trc_vue travail, uint32_t n_delta, uint32_t n_codes, void* flux);
+
+/* Workspace bytes of trc_couche_moe_fusionnee. */
+uint64_t trc_taille_travail_couche_moe(const trc_dims_expert* dims, uint32_t experts, uint32_t k, uint32_t n_codes);
+/* One MoE layer step at batch 1 (Modele::debut_couche's router, gemv_f32 + routeur_topk, then
+ * Modele::fin_couche): logits = routeur x (+ routeur_biais) with a bf16 experts x C router, top-k
+ * and softmax weights (written to indices / poids), the k fused experts, and
+ * residu[i] += ((w0 s0[i] + w1 s1[i]) + ...). parties: u64[experts] device addresses of the
+ * experts' level-0 parts; the selection never leaves the device. */
+int trc_couche_moe_fusionnee(trc_vue parties, uint32_t experts, trc_vue luts, const trc_dims_expert* dims,
+                             trc_vue routeur, trc_vue routeur_biais, trc_vue x, uint32_t k, trc_vue residu,
+                             trc_vue indices, trc_vue poids, trc_vue controle, trc_vue travail, uint32_t n_delta,
+                             uint32_t n_codes, void* flux);
+
+/* Chronogram of the fused entry points (role of the reference's --chronogramme, which records GPU
+ * event timestamps around each decode, moteur/crates/trc-ordo/src/lib.rs:205-222): off by
+ * default; when on, every kernel a fused entry point launches is bracketed by two HIP events on
+ * its stream. trc_chrono_recolter waits for the recorded pairs and copies out at most `max`
+ * (name[64], total ms, launches) entries; returns the number of names. */
+void trc_chrono(int actif);
+int trc_chrono_recolter(char* noms, double* ms, uint64_t* lancements, int max, int remettre_a_zero);
+
 /* ---------------------------------------- encoder front-end (host only; role of bins/trc-codeur) */
 
 /* The seeded synthetic workload (nibble law "A", E8M0 scales in [119,125], bf16 N(0,0.02) biases).

@@ -1,0 +1,190 @@
+"""GPU parity of the fused path (decode in registers + GEMV / SwiGLU / combine) against the CPU
+oracle, through the C-ABI.
+
+Tolerance (stated, the reference's own GEMV threshold, decisions/ARCHITECTURE.md §5.6 table):
+every output within 1e-5 * max|y| of the f64 computation from the uncompressed weights, and of the
+reference's f32 operation order. On the integer-exact fixture (scales in [117,123], x in {-2..2},
+tests/carte.rs:1-10) every partial sum is exact in f32, so the fused GEMV must match bit for bit
+whatever its summation order. Decoded-byte exactness is checked through the control words and
+that exact GEMV.
+"""
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+import oracle_ffi as O  # noqa: E402
+from gpu_outils import Expert, dev, hote, vue, zeros  # noqa: E402
+from troncons_amd import codeur, fusion  # noqa: E402
+from troncons_amd import noyaux as K  # noqa: E402
+from troncons_amd.noyaux import DimsExpert  # noqa: E402
+
+GPT = DimsExpert.gpt_oss()
+TOL = 1e-5
+
+
+@pytest.fixture(scope="module")
+def fz():
+    assert torch.cuda.is_available()
+    return fusion.Fusion()
+
+
+def _gemv(fz, partie, luts, j, R, C, x, n_delta, n_codes):
+    p, l, xd = dev(partie), dev(luts), dev(x)
+    y = zeros(4 * R)
+    ctl = zeros(16)
+    tr = zeros(fusion.taille_travail_gemv(R, C, n_codes))
+    fz.gemv_fusionnee(vue(p), j, vue(l), R, C, vue(xd), vue(y), vue(ctl), vue(tr), n_delta, n_codes)
+    return hote(y, np.float32), hote(ctl, np.uint32)
+
+
+def _slot_j(ex, j):
+    d = O.disposition_j([2880] * 3, [2880] * 3, j)
+    return ex.attendu[d.base:d.base + d.pas]
+
+
+@pytest.mark.parametrize("N", [(256, 256), (32, 32), (8, 16), (4, 1)])
+def test_fused_gemv_one_matrix_config1(fz, N):
+    ex = Expert(2026, GPT, N_delta=N[0], N_codes=N[1])
+    x = O.synth_normale_bf16(2026, 1, 0, 2880, 1.0)
+    for j in (2, 0):
+        y, ctl = _gemv(fz, ex.partie, ex.luts, j, 2880, 2880, x, *N)
+        assert list(ctl) == [0, 0, 0, 0]
+        y64 = O.gemv_mxfp4_f64(_slot_j(ex, j), x, 2880, 2880)
+        assert np.abs(y - y64).max() <= TOL * np.abs(y64).max()
+        yref = O.gemv_mxfp4(_slot_j(ex, j), x, 2880, 2880)
+        assert np.abs(y - yref).max() <= TOL * np.abs(y64).max()
+        y2, _ = _gemv(fz, ex.partie, ex.luts, j, 2880, 2880, x, *N)
+        assert (y.view(np.uint32) == y2.view(np.uint32)).all(), "fused GEMV not deterministic"
+
+
+def _expert_exact(seed, dims):
+    rng = np.random.default_rng(seed)
+    blocs, biais = [], []
+    for j in range(3):
+        r, c = dims.lignes[j], dims.colonnes[j]
+        nb = r * (c // 32)
+        e = rng.integers(117, 124, nb).astype(np.uint8)
+        u = rng.integers(0, 100, (nb, 32))
+        mag = np.where(u < 40, u % 2, np.where(u < 80, 2 + u % 3, 5 + u % 3))
+        code = mag | (rng.integers(0, 2, (nb, 32)) << 3)
+        bl = np.zeros((nb, 17), np.uint8)
+        bl[:, 0] = e
+        bl[:, 1:] = (code[:, :16] | (code[:, 16:] << 4)).astype(np.uint8)
+        blocs.append(bl.reshape(-1))
+        biais.append(((rng.integers(0, 2001, r) - 1000) / 2048.0).astype(np.float32))
+    return blocs, biais
+
+
+@pytest.mark.parametrize("N", [(256, 256), (16, 32), (3, 7)])
+def test_fused_gemv_bit_exact_on_integer_fixture(fz, N):
+    dims = GPT
+    blocs, biais = _expert_exact(7, dims)
+    freqs = [codeur.tables([blocs[j]], 2880, 90) for j in range(3)]
+    partie, _ = codeur.partie(blocs, biais, freqs, dims, N_delta=N[0], N_codes=N[1])
+    luts = O.luts_couche([[freqs[j][t] for t in range(4)] for j in range(3)])
+    x = (np.random.default_rng(11).integers(0, 5, 2880) - 2).astype(np.float32)
+    for j in range(3):
+        y, ctl = _gemv(fz, partie, luts, j, 2880, 2880, x, *N)
+        assert list(ctl) == [0, 0, 0, 0]
+        slot = O.blocs_vers_soa(blocs[j], 2880, 2880, biais[j], canonique=True)
+        y64 = O.gemv_mxfp4_f64(slot, x, 2880, 2880).astype(np.float32)
+        assert (y.view(np.uint32) == y64.view(np.uint32)).all()
+
+
+def test_fused_gemv_small_shapes_and_break(fz):
+    dims = DimsExpert.de([300, 300, 257], [256, 256, 320])
+    ex = Expert(5, dims, N_delta=2, N_codes=3)
+    for j in range(3):
+        R, C = dims.lignes[j], dims.colonnes[j]
+        x = O.synth_normale_bf16(5, 2, j, C, 1.0)
+        y, ctl = _gemv(fz, ex.partie, ex.luts, j, R, C, x, 2, 3)
+        assert list(ctl) == [0, 0, 0, 0]
+        d = O.disposition_j(list(dims.lignes), list(dims.colonnes), j)
+        y64 = O.gemv_mxfp4_f64(ex.attendu[d.base:d.base + d.pas], x, R, C)
+        assert np.abs(y - y64).max() <= TOL * np.abs(y64).max()
+    # break: a flipped bit in CODES_CTX of matrix 1 is seen by the control words
+    p = bytearray(ex.partie)
+    e = 64 + 16 * 7
+    dec = int.from_bytes(p[e + 4:e + 8], "little")
+    lon = int.from_bytes(p[e + 8:e + 12], "little")
+    p[dec + lon // 2] ^= 0x10
+    _, ctl = _gemv(fz, bytes(p), ex.luts, 1, 300, 256, O.synth_normale_bf16(5, 2, 1, 256, 1.0), 2, 3)
+    assert ctl[0] > 0
+    p = bytearray(ex.partie)
+    p[0] ^= 0xFF
+    _, ctl = _gemv(fz, bytes(p), ex.luts, 1, 300, 256, O.synth_normale_bf16(5, 2, 1, 256, 1.0), 2, 3)
+    assert ctl[1] > 0
+
+
+def _mlp_oracle(ex, x, dims):
+    """The reference chain in its own f32 order (gemv x2, swiglu_oai, gemv) and in f64."""
+    R, C = dims.lignes[0], dims.colonnes[0]
+    sl = [ex.attendu[O.disposition_j(list(dims.lignes), list(dims.colonnes), j).base:][
+          :O.disposition_j(list(dims.lignes), list(dims.colonnes), j).pas] for j in range(3)]
+    g = O.gemv_mxfp4(sl[0], x, R, C)
+    u = O.gemv_mxfp4(sl[1], x, R, C)
+    a = O.swiglu_oai(g, u)
+    s = O.gemv_mxfp4(sl[2], a, dims.lignes[2], dims.colonnes[2])
+    g64 = O.gemv_mxfp4_f64(sl[0], x, R, C)
+    u64 = O.gemv_mxfp4_f64(sl[1], x, R, C)
+    gg = np.minimum(g64, 7.0)
+    uu = np.clip(u64, -7.0, 7.0)
+    a64 = gg / (1.0 + np.exp(-1.702 * gg)) * (uu + 1.0)
+    s64 = O.gemv_mxfp4_f64(sl[2], a64.astype(np.float32), dims.lignes[2], dims.colonnes[2])
+    return s, s64
+
+
+@pytest.mark.parametrize("N", [(256, 256), (32, 32), (8, 16)])
+def test_fused_expert_config2(fz, N):
+    ex = Expert(2027, GPT, N_delta=N[0], N_codes=N[1])
+    x = O.synth_normale_bf16(2027, 1, 0, 2880, 1.0)
+    p, l, xd = dev(ex.partie), dev(ex.luts), dev(x)
+    s = zeros(4 * 2880)
+    ctl = zeros(16)
+    tr = zeros(fusion.taille_travail_expert(GPT, N[1]))
+    fz.expert_fusionne(vue(p), vue(l), GPT, vue(xd), vue(s), vue(ctl), vue(tr), *N)
+    got = hote(s, np.float32)
+    assert list(hote(ctl, np.uint32)) == [0, 0, 0, 0]
+    s_ref, s64 = _mlp_oracle(ex, x, GPT)
+    assert np.abs(got - s_ref).max() <= TOL * np.abs(s_ref).max()
+    assert np.abs(got - s64).max() <= TOL * np.abs(s64).max()
+
+
+def test_fused_moe_layer_config3(fz):
+    E, k, N = 12, 4, (16, 32)
+    couche = codeur.CoucheSynthetique(2028, 0, E, GPT, N_delta=N[0], N_codes=N[1])
+    freqs = couche.freqs()
+    luts = O.luts_couche([[freqs[j][t] for t in range(4)] for j in range(3)])
+    parts = [dev(couche.partie(e)) for e in range(E)]
+    table = dev(np.array([p.data_ptr() for p in parts], np.uint64))
+    routeur = np.stack([O.synth_normale_bf16(2028, 3, e, 2880, 0.02) for e in range(E)])
+    r16 = (routeur.view(np.uint32) >> 16).astype(np.uint16)
+    x = O.synth_normale_bf16(2028, 4, 0, 2880, 1.0)
+    residu0 = np.zeros(2880, np.float32)
+    l, rd, xd, res = dev(luts), dev(r16), dev(x), dev(residu0)
+    idx, w, ctl = zeros(32), zeros(32), zeros(16)
+    tr = zeros(fusion.taille_travail_couche(GPT, E, k, N[1]))
+    fz.couche_moe(vue(table), E, vue(l), GPT, vue(rd), None, vue(xd), k, vue(res), vue(idx), vue(w), vue(ctl),
+                  vue(tr), *N)
+    got = hote(res, np.float32)
+    assert list(hote(ctl, np.uint32)) == [0, 0, 0, 0]
+    logits = O.gemv_f32(routeur, x)
+    oi, ow = O.routeur_topk(logits, k)
+    gi, gw = hote(idx, np.uint32)[:k], hote(w, np.float32)[:k]
+    assert (gi == oi).all() and np.abs(gw - ow).max() <= 1e-6
+    sorties = []
+    sorties64 = []
+    for e in oi:
+        bl, bi = codeur.synth_expert(2028, 0, int(e), GPT)
+        ex = type("E", (), {})()
+        ex.attendu = np.concatenate([O.blocs_vers_soa(bl[j], 2880, 2880, bi[j], canonique=True) for j in range(3)])
+        s, s64 = _mlp_oracle(ex, x, GPT)
+        sorties.append(s)
+        sorties64.append(s64)
+    ref = O.combiner(residu0, np.concatenate(sorties), 2880, ow, k, 2880)
+    ref64 = sum(float(ow[i]) * sorties64[i] for i in range(k))
+    assert np.abs(got - ref).max() <= TOL * np.abs(ref).max()
+    assert np.abs(got - ref64).max() <= TOL * np.abs(ref64).max()
+    couche.liberer()

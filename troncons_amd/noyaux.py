@@ -10,7 +10,7 @@ kernels go to the caller's zeroed u32[4] control buffer. Device memory is borrow
 from __future__ import annotations
 
 import ctypes as C
-from dataclasses import dataclass
+from dataclasses import dataclass, field
 
 from . import _lib
 
@@ -73,9 +73,13 @@ class Disposition(C.Structure):
 
 @dataclass(frozen=True)
 class VueCarte:
-    """Non-owning view of device memory (trc-cuda/src/lib.rs:432-460)."""
+    """Non-owning view of device memory (trc-cuda/src/lib.rs:432-460). A view made from a torch
+    tensor keeps that tensor alive as long as the view lives, so a temporary cannot be freed (and
+    its memory handed to the next allocation) before the launch that borrows it is enqueued;
+    stream order protects it afterwards."""
     adresse: int
     octets: int
+    garde: object = field(default=None, compare=False, repr=False)
 
     @staticmethod
     def de(t, decalage: int = 0, octets: int | None = None) -> "VueCarte":
@@ -83,7 +87,7 @@ class VueCarte:
         total = t.numel() * t.element_size()
         n = total - decalage if octets is None else octets
         assert 0 <= decalage and decalage + n <= total
-        return VueCarte(t.data_ptr() + decalage, n)
+        return VueCarte(t.data_ptr() + decalage, n, t)
 
     def c(self) -> _Vue:
         return _Vue(self.adresse, self.octets)
