@@ -1,26 +1,32 @@
 // fusion.hip — the fused expert path for gfx950: rANS decoding of the .trc v1.2 streams feeds the
 // MXFP4 dequant and the GEMV directly; decoded code bytes live only in registers and are never
-// written to HBM. Built from four kernels chained on one stream:
+// written to device memory. Kernels, chained on one stream:
 //
 //   fusion_echelles  DELTA tiles -> E8M0 scales of the selected matrices (a small workspace);
 //   fusion_gemv      CODES_CTX tiles -> per-(row, tile) partial sums of y = W x, decoded bytes
 //                    dequantised and multiplied in registers;
 //   fusion_finir     y[r] = fixed-order sum of the row's tile partials + bias;
+//   fusion_swiglu    gpt-oss clamped SwiGLU of the gate/up outputs;
 //   fusion_routeur / fusion_taches  (MoE layer) router logits, then the job table of the
 //                    selected experts, built on the device from the top-k indices.
 //
-// Mapping: one wavefront = two rANS tiles (lanes 0-31, 32-63). In a macro-step, lane v of a tile
-// produces the 4 code bytes 4(v%4) .. 4(v%4)+3 of block 8m + v/4, i.e. the weights of columns
-// 32b + 4(v%4) + k (low nibbles) and 32b + 16 + 4(v%4) + k (high nibbles): two float4 of x. Each
-// lane accumulates its block contributions per row; rows are closed by a 32-lane reduction when
-// the tile's first block enters a new row (a row has >= 8 blocks, so one macro-step touches at
-// most two rows). Every (row, tile) partial is written exactly once and summed in tile order by
-// the finisher: results are deterministic, without floating-point atomics.
+// Mapping: one wavefront = two rANS tiles (lanes 0-31, 32-63), each tile's words staged in an LDS
+// ring (anneau.hpp). In a macro-step, lane v of a tile produces the 4 code bytes 4(v%4) ..
+// 4(v%4)+3 of block 8m + v/4, i.e. the weights of columns 32b + 4(v%4) + k (low nibbles) and
+// 32b + 16 + 4(v%4) + k (high nibbles): two float4 of x. Each lane accumulates its block
+// contributions per row; rows are closed by a 32-lane reduction when the tile's first block enters
+// a new row (a row has >= 8 blocks, so one macro-step touches at most two rows). Every (row, tile)
+// partial is written exactly once and summed in tile order by the finisher: results are
+// deterministic, without floating-point atomics.
 #include <hip/hip_runtime.h>
 
+#include <cstring>
+
+#include "anneau.hpp"
 #include "chrono.hpp"
 #include "commun.hpp"
 #include "erreurs.hpp"
+#include "fusion_corps.hpp"
 
 // Reference-API kernels (noyaux.hip) reused by the MoE layer.
 extern "C" __global__ void routeur_topk(const float* logits, uint32_t E, uint32_t k, uint32_t* indices, float* poids,
@@ -28,251 +34,31 @@ extern "C" __global__ void routeur_topk(const float* logits, uint32_t E, uint32_
 extern "C" __global__ void combiner(float* residu, const float* sorties, uint32_t pas, const float* poids, uint32_t n,
                                     uint32_t d);
 
-namespace trc {
-
-// One job of the fused path: matrix j of a level-0 part, against x (48 bytes).
-struct Tache {
-    uint64_t partie;    // level-0 part
-    uint64_t x;         // f32[colonnes], 16-byte aligned
-    uint64_t ech;       // u8[lignes * colonnes/32] scales (workspace, 4-byte aligned)
-    uint64_t partiels;  // f32[lignes * kmax] partial sums (workspace)
-    uint32_t j;         // matrix index in the part
-    uint32_t kmax;      // partial slots per row
-    uint32_t lignes, colonnes;
-};
-static_assert(sizeof(Tache) == 48, "Tache");
-
-__device__ __forceinline__ uint32_t premiere_tuile(uint32_t ligne, uint32_t B, uint32_t blocs_par_tuile) {
-    return (ligne * B) / blocs_par_tuile;
-}
-
-// ----------------------------------------------------------------------- DELTA -> scales only
-__device__ __forceinline__ void corps_echelles_fusion(const Tache& tc, const uint32_t* lut, uint8_t* med_lds,
-                                                      uint32_t* __restrict__ controle) {
-    const uint8_t* partie = reinterpret_cast<const uint8_t*>(tc.partie);
-    const uint32_t R = tc.lignes, C = tc.colonnes, B = C / 32u, nblocs = R * B;
-    DescFlux fd, fm;
-    EnteteRans h;
-    const bool bon = (C % 32u == 0) && B > 0 && R > 0 && trouver_flux(partie, SORTE_DELTA, tc.j, fd) &&
-                     trouver_flux(partie, SORTE_MEDIANES, tc.j, fm) && fm.produits == R && fm.longueur >= R &&
-                     lire_entete(fd, nblocs, h);
-    if (!bon) {
-        if (threadIdx.x == 0 && blockIdx.x == 0) atomicAdd(&controle[CTL_FORMAT], 1u);
-        return;
-    }
-    const uint8_t* med = fm.p;
-    if (R <= 8192u) {
-        for (uint32_t i = threadIdx.x; i < R; i += blockDim.x) med_lds[i] = fm.p[i];
-        med = med_lds;
-    }
-    __syncthreads();
-    uint8_t* ech = reinterpret_cast<uint8_t*>(tc.ech);
-    const DemiVague dv = demi_vague();
-    const uint32_t v = __lane_id() & 31u;
-    const uint32_t vagues_bloc = blockDim.x >> 6;
-    const uint32_t vague = blockIdx.x * vagues_bloc + (threadIdx.x >> 6);
-    const uint32_t n_vagues = gridDim.x * vagues_bloc;
-    const uint32_t nmacro = h.P / 128u;
-    uint32_t hors_l = 0, pointeur = 0;
-    for (uint32_t t0 = 2u * vague; t0 < h.T; t0 += 2u * n_vagues) {
-        const uint32_t t = t0 + (dv.haut ? 1u : 0u);
-        const bool tuile = t < h.T;
-        const uint32_t nb_a = min(h.N, nmacro - t0 * h.N);
-        const uint32_t nb = tuile ? min(h.N, nmacro - t * h.N) : 0u;
-        uint32_t x = tuile ? h.etats[t * VOIES + v] : L;
-        uint32_t ptr = tuile ? h.debut[t] : 0u;
-        uint32_t b0 = 4u * ((tuile ? t : t0) * h.N * VOIES + v);
-        uint32_t ligne = b0 / B, reste = b0 - ligne * B;
-        for (uint32_t m = 0; m < nb_a; ++m) {
-            const bool actif = m < nb;
-            uint32_t mot = 0;
-#pragma unroll
-            for (uint32_t k = 0; k < 4; ++k) mot |= pas_octet(x, ptr, lut, h.mots, h.W, dv, actif) << (8u * k);
-            if (actif) {
-                uint32_t sortie = 0;
-#pragma unroll
-                for (uint32_t k = 0; k < 4; ++k) {
-                    uint32_t rk = ligne, qk = reste + k;
-                    while (qk >= B) {
-                        qk -= B;
-                        ++rk;
-                    }
-                    const uint32_t mk = rk < R ? uint32_t(med[rk]) : 0u;
-                    sortie |= ((mk + ((mot >> (8u * k)) & 255u) - 128u) & 255u) << (8u * k);
-                }
-                if (b0 + 3u < nblocs) {
-                    reinterpret_cast<uint32_t*>(ech)[b0 >> 2] = sortie;
-                } else {
-                    for (uint32_t k = 0; k < 4; ++k)
-                        if (b0 + k < nblocs) ech[b0 + k] = uint8_t(sortie >> (8u * k));
-                }
-            }
-            b0 += 4u * VOIES;
-            reste += 4u * VOIES;
-            while (reste >= B) {
-                reste -= B;
-                ++ligne;
-            }
-        }
-        if (tuile) {
-            hors_l += (x != L) ? 1u : 0u;
-            const uint32_t attendu = (t + 1 < h.T) ? h.debut[t + 1] : h.W;
-            pointeur += (v == 0 && ptr != attendu) ? 1u : 0u;
-        }
-    }
-    verser_controle(controle, hors_l, pointeur);
-}
-
-// ------------------------------------------------------------ CODES_CTX -> partial sums of W x
-__device__ __forceinline__ void corps_gemv_fusion(const Tache& tc, const uint32_t (*lut)[M],
-                                                  uint32_t* __restrict__ controle) {
-    const uint8_t* partie = reinterpret_cast<const uint8_t*>(tc.partie);
-    const uint32_t R = tc.lignes, C = tc.colonnes, B = C / 32u, nblocs = R * B;
-    DescFlux fc, fm;
-    EnteteRans h;
-    bool bon = (C % 32u == 0) && B >= 8u && R > 0 && trouver_flux(partie, SORTE_CODES_CTX, tc.j, fc) &&
-               trouver_flux(partie, SORTE_MEDIANES, tc.j, fm) && fm.produits == R && fm.longueur >= R &&
-               lire_entete(fc, nblocs * 16u, h);
-    if (bon && (B - 1u) / (8u * h.N) + 2u > tc.kmax) bon = false;  // not enough partial slots
-    if (!bon) {
-        if (threadIdx.x == 0 && blockIdx.x == 0) atomicAdd(&controle[CTL_FORMAT], 1u);
-        return;
-    }
-    const uint8_t* __restrict__ med = fm.p;
-    const uint8_t* __restrict__ ech = reinterpret_cast<const uint8_t*>(tc.ech);
-    const float4* __restrict__ x4 = reinterpret_cast<const float4*>(tc.x);
-    float* __restrict__ partiels = reinterpret_cast<float*>(tc.partiels);
-    const uint32_t kmax = tc.kmax;
-    const uint32_t bpt = 8u * h.N;  // blocks per tile
-
-    const DemiVague dv = demi_vague();
-    const uint32_t v = __lane_id() & 31u;
-    const uint32_t q = v >> 2, q4 = v & 3u;
-    const uint32_t vagues_bloc = blockDim.x >> 6;
-    const uint32_t vague = blockIdx.x * vagues_bloc + (threadIdx.x >> 6);
-    const uint32_t n_vagues = gridDim.x * vagues_bloc;
-    const uint32_t nmacro = h.P / 128u;
-    uint32_t hors_l = 0, pointeur = 0;
-    for (uint32_t t0 = 2u * vague; t0 < h.T; t0 += 2u * n_vagues) {
-        const uint32_t t = t0 + (dv.haut ? 1u : 0u);
-        const bool tuile = t < h.T;
-        const uint32_t nb_a = min(h.N, nmacro - t0 * h.N);
-        const uint32_t nb = tuile ? min(h.N, nmacro - t * h.N) : 0u;
-        uint32_t x = tuile ? h.etats[t * VOIES + v] : L;
-        uint32_t ptr = tuile ? h.debut[t] : 0u;
-        const uint32_t m0 = (tuile ? t : t0) * h.N;
-        uint32_t bloc = m0 * 8u + q;
-        uint32_t ligne = bloc / B, b = bloc - ligne * B;
-        uint32_t rho = (m0 * 8u) / B, base_b = m0 * 8u - rho * B;  // row of the tile's first block
-        bool valide = tuile && bloc < nblocs;
-        uint32_t e_suiv = valide ? uint32_t(ech[bloc]) : 0u;
-        uint32_t m_suiv = valide ? uint32_t(med[ligne]) : 0u;
-        float acc_a = 0.0f, acc_b = 0.0f;
-        for (uint32_t m = 0; m < nb_a; ++m) {
-            const bool actif = m < nb;
-            const bool bloc_ok = valide;
-            const uint32_t e_cur = e_suiv;
-            const uint32_t ctx = bloc_ok ? classe_echelle(e_suiv, m_suiv) : 0u;
-            const uint32_t b_cur = b, ligne_cur = ligne;
-            bloc += 8u;
-            b += 8u;
-            while (b >= B) {
-                b -= B;
-                ++ligne;
-            }
-            valide = (m + 1u < nb) && bloc < nblocs;
-            if (valide) {
-                e_suiv = ech[bloc];
-                m_suiv = med[ligne];
-            }
-            float4 xa = make_float4(0.f, 0.f, 0.f, 0.f), xb = xa;
-            if (bloc_ok) {
-                xa = x4[8u * b_cur + q4];
-                xb = x4[8u * b_cur + 4u + q4];
-            }
-            const uint32_t* lt = lut[ctx];
-            uint32_t mot = 0;
-#pragma unroll
-            for (uint32_t k = 0; k < 4; ++k) mot |= pas_octet(x, ptr, lt, h.mots, h.W, dv, actif) << (8u * k);
-            if (actif && bloc_ok) {
-                float d = 0.0f;
-                d = fmaf(valeur_e2m1x2(mot & 15u), xa.x, d);
-                d = fmaf(valeur_e2m1x2((mot >> 4) & 15u), xb.x, d);
-                d = fmaf(valeur_e2m1x2((mot >> 8) & 15u), xa.y, d);
-                d = fmaf(valeur_e2m1x2((mot >> 12) & 15u), xb.y, d);
-                d = fmaf(valeur_e2m1x2((mot >> 16) & 15u), xa.z, d);
-                d = fmaf(valeur_e2m1x2((mot >> 20) & 15u), xb.z, d);
-                d = fmaf(valeur_e2m1x2((mot >> 24) & 15u), xa.w, d);
-                d = fmaf(valeur_e2m1x2(mot >> 28), xb.w, d);
-                const float c = d * echelle_e8m0(e_cur);
-                if (ligne_cur == rho)
-                    acc_a += c;
-                else
-                    acc_b += c;
-            }
-            base_b += 8u;
-            bool avance = false;
-            if (base_b >= B) {
-                base_b -= B;
-                avance = actif;
-            }
-            if (__ballot(avance) != 0) {
-                const float s = somme_demi_f32(acc_a);
-                if (avance) {
-                    if (v == 0 && rho < R) partiels[rho * kmax + (t - premiere_tuile(rho, B, bpt))] = s;
-                    acc_a = acc_b;
-                    acc_b = 0.0f;
-                    ++rho;
-                }
-            }
-        }
-        const float sa = somme_demi_f32(acc_a);
-        const float sb = somme_demi_f32(acc_b);
-        if (tuile) {
-            if (v == 0) {
-                const uint32_t fin = min((m0 + nb) * 8u, nblocs);
-                const uint32_t derniere = (fin - 1u) / B;
-                if (rho <= derniere && rho < R) partiels[rho * kmax + (t - premiere_tuile(rho, B, bpt))] = sa;
-                if (rho + 1u <= derniere && rho + 1u < R)
-                    partiels[(rho + 1u) * kmax + (t - premiere_tuile(rho + 1u, B, bpt))] = sb;
-            }
-            hors_l += (x != L) ? 1u : 0u;
-            const uint32_t attendu = (t + 1 < h.T) ? h.debut[t + 1] : h.W;
-            pointeur += (v == 0 && ptr != attendu) ? 1u : 0u;
-        }
-    }
-    verser_controle(controle, hors_l, pointeur);
-}
-
-}  // namespace trc
-
-// The job of block (x, y) is taches[y]; the layer's LUTs u32[3][4][4096] are shared by all jobs.
-extern "C" __global__ void __launch_bounds__(128)
-fusion_echelles(const trc::Tache* __restrict__ taches, const uint32_t* __restrict__ luts,
-                uint32_t* __restrict__ controle) {
-    __shared__ uint32_t lut[trc::M];
+// The layer's LUTs u32[3][4][4096] (reference format) are shared by all jobs of a launch.
+extern "C" __global__ void __launch_bounds__(trc::FILS_ECHELLES_FUSION)
+fusion_echelles(trc::Taches taches, const uint32_t* __restrict__ luts, uint32_t* __restrict__ controle) {
+    __shared__ uint2 lut[trc::M];
     __shared__ uint8_t med[8192];
+    __shared__ __attribute__((aligned(16))) uint8_t anneaux[(trc::FILS_ECHELLES_FUSION / 32) * trc::OCTETS_ANNEAU];
     const trc::Tache tc = taches[blockIdx.y];
-    const uint32_t* src = luts + (uint64_t(tc.j) * 4u + 0u) * trc::M;
-    for (uint32_t i = threadIdx.x; i < trc::M; i += blockDim.x) lut[i] = src[i];
+    trc::etendre_luts(luts + (uint64_t(tc.j) * 4u + 0u) * trc::M, lut, trc::M);
     __syncthreads();
-    trc::corps_echelles_fusion(tc, lut, med, controle);
+    trc::corps_echelles_fusion(tc, lut, med, anneaux, controle);
 }
 
-extern "C" __global__ void __launch_bounds__(256)
-fusion_gemv(const trc::Tache* __restrict__ taches, const uint32_t* __restrict__ luts, uint32_t* __restrict__ controle) {
-    __shared__ uint32_t lut[3][trc::M];
+extern "C" __global__ void __launch_bounds__(trc::FILS_GEMV_FUSION)
+fusion_gemv(trc::Taches taches, const uint32_t* __restrict__ luts, uint32_t* __restrict__ controle) {
+    __shared__ uint2 lut[3 * trc::M];
+    __shared__ __attribute__((aligned(16))) uint8_t anneaux[(trc::FILS_GEMV_FUSION / 32) * trc::OCTETS_ANNEAU];
     const trc::Tache tc = taches[blockIdx.y];
-    const uint32_t* src = luts + (uint64_t(tc.j) * 4u + 1u) * trc::M;
-    uint32_t* dst = &lut[0][0];
-    for (uint32_t i = threadIdx.x; i < 3u * trc::M; i += blockDim.x) dst[i] = src[i];
+    trc::etendre_luts(luts + (uint64_t(tc.j) * 4u + 1u) * trc::M, lut, 3u * trc::M);
     __syncthreads();
-    trc::corps_gemv_fusion(tc, lut, controle);
+    trc::corps_gemv_fusion(tc, lut, anneaux, controle);
 }
 
 // sorties[y * pas + r] = fixed-order sum of the partials of row r + bias[r], for job y.
 extern "C" __global__ void __launch_bounds__(256)
-fusion_finir(const trc::Tache* __restrict__ taches, float* __restrict__ sorties, uint32_t pas) {
+fusion_finir(trc::Taches taches, float* __restrict__ sorties, uint32_t pas) {
     using namespace trc;
     const Tache tc = taches[blockIdx.y];
     const uint32_t r = blockIdx.x * 256u + threadIdx.x;
@@ -327,7 +113,7 @@ fusion_routeur(const uint16_t* __restrict__ W, const float* __restrict__ x, cons
 }
 
 // Job tables of a MoE layer from the top-k indices: for selected expert i, jobs 2i (gate) and
-// 2i+1 (up) in table `gu` against x, job i (down) in table `bas` against act + i*lignes, and the
+// 2i+1 (up) in table `gu` against x, job i (down) in table `bas` against act + i*R, and the
 // DELTA jobs (3 per expert) in `delta`. Workspace pieces are laid out per (i, j).
 namespace trc {
 struct ParamsTaches {
@@ -335,8 +121,8 @@ struct ParamsTaches {
     uint64_t indices;   // u32[k]
     uint64_t x;         // f32[C]
     uint64_t act;       // f32[k * R]
-    uint64_t ech;       // scales: (i*3 + j) * pas_ech
-    uint64_t partiels;  // partials: (i*3 + j) * pas_partiels
+    uint64_t ech;       // scales: (i*3 + j) * pas
+    uint64_t partiels;  // partials: (i*3 + j) * pas
     uint64_t delta, gu, bas;  // Tache tables
     uint64_t pas;             // workspace bytes per (i, j)
     uint32_t lignes[3], colonnes[3], kmax[3];
@@ -390,8 +176,9 @@ fusion_swiglu(const float* __restrict__ gu, float* __restrict__ act, uint32_t R,
 // ============================================================================ C-ABI launch layer
 namespace {
 
-using trc::usage;
 using trc::Tache;
+using trc::Taches;
+using trc::usage;
 
 inline hipStream_t flux_de(void* f) { return reinterpret_cast<hipStream_t>(f); }
 
@@ -409,6 +196,9 @@ uint32_t grille_tuiles(uint64_t octets, uint32_t N, uint32_t tuiles_par_bloc) {
     return uint32_t(g < 1 ? 1 : g);
 }
 
+constexpr uint32_t TUILES_ECHELLES = trc::FILS_ECHELLES_FUSION / 32;
+constexpr uint32_t TUILES_GEMV = trc::FILS_GEMV_FUSION / 32;
+
 // Workspace of one matrix job: scales then partial sums.
 uint64_t pas_tache(uint32_t R, uint32_t C, uint32_t n_codes) {
     return al(uint64_t(R) * (C / 32)) + al(4ull * R * kmax_pour(C, n_codes));
@@ -424,21 +214,25 @@ int verifier_forme(const trc_dims_expert* dims, uint32_t n_codes) {
     return TRC_OK;
 }
 
-int lancer_chaine(const Tache* taches_dev, uint32_t n, const uint32_t* luts, uint32_t* ctl, uint32_t R, uint32_t C,
-                  uint32_t n_delta, uint32_t n_codes, bool echelles, hipStream_t f) {
-    const uint32_t B = C / 32;
-    if (echelles)
-        TRC_LANCER(fusion_echelles, dim3(grille_tuiles(uint64_t(R) * B, n_delta, 4), n), dim3(128), f, taches_dev, luts,
-                   ctl);
-    TRC_LANCER(fusion_gemv, dim3(grille_tuiles(16ull * R * B, n_codes, 8), n), dim3(256), f, taches_dev, luts, ctl);
-    return TRC_OK;
+Taches par_valeur(const Tache* t, uint32_t n) {
+    Taches l;
+    l.table = nullptr;
+    for (uint32_t i = 0; i < n && i < 3; ++i) l.locales[i] = t[i];
+    return l;
+}
+
+Taches par_table(uint64_t adresse) {
+    Taches l;
+    std::memset(&l, 0, sizeof(l));
+    l.table = reinterpret_cast<const Tache*>(adresse);
+    return l;
 }
 
 }  // namespace
 
 extern "C" uint64_t trc_taille_travail_gemv_fusionnee(uint32_t lignes, uint32_t colonnes, uint32_t n_codes) {
     if (colonnes / 32 < 8 || n_codes == 0) return 0;
-    return al(sizeof(Tache)) + pas_tache(lignes, colonnes, n_codes);
+    return pas_tache(lignes, colonnes, n_codes);
 }
 
 // Config 1: one matrix j of a part, y = W_j x + b_j, decoded in registers.
@@ -460,30 +254,31 @@ extern "C" int trc_gemv_fusionnee(trc_vue partie, uint32_t j, trc_vue luts, uint
     Tache t;
     t.partie = partie.adresse;
     t.x = x.adresse;
-    t.ech = travail.adresse + al(sizeof(Tache));
+    t.ech = travail.adresse;
     t.partiels = t.ech + al(uint64_t(lignes) * (colonnes / 32));
     t.j = j;
     t.kmax = kmax_pour(colonnes, n_codes);
     t.lignes = lignes;
     t.colonnes = colonnes;
+    const Taches tv = par_valeur(&t, 1);
     const hipStream_t f = flux_de(flux);
-    hipError_t e = hipMemcpyAsync(reinterpret_cast<void*>(travail.adresse), &t, sizeof(t), hipMemcpyHostToDevice, f);
-    if (e != hipSuccess) return trc::erreur_hip("hipMemcpyAsync", e);
-    const Tache* td = reinterpret_cast<const Tache*>(travail.adresse);
     auto ctl = reinterpret_cast<uint32_t*>(controle.adresse);
-    int r = lancer_chaine(td, 1, reinterpret_cast<const uint32_t*>(luts.adresse), ctl, lignes, colonnes, n_delta,
-                          n_codes, true, f);
-    if (r != TRC_OK) return r;
-    TRC_LANCER(fusion_finir, dim3((lignes + 255) / 256, 1), dim3(256), f, td, reinterpret_cast<float*>(y.adresse), 0u);
+    auto l = reinterpret_cast<const uint32_t*>(luts.adresse);
+    const uint32_t B = colonnes / 32;
+    TRC_LANCER(fusion_echelles, dim3(grille_tuiles(uint64_t(lignes) * B, n_delta, TUILES_ECHELLES), 1),
+               dim3(trc::FILS_ECHELLES_FUSION), f, tv, l, ctl);
+    TRC_LANCER(fusion_gemv, dim3(grille_tuiles(16ull * lignes * B, n_codes, TUILES_GEMV), 1),
+               dim3(trc::FILS_GEMV_FUSION), f, tv, l, ctl);
+    TRC_LANCER(fusion_finir, dim3((lignes + 255) / 256, 1), dim3(256), f, tv, reinterpret_cast<float*>(y.adresse), 0u);
     return TRC_OK;
 }
 
 extern "C" uint64_t trc_taille_travail_expert_fusionne(const trc_dims_expert* dims, uint32_t n_codes) {
     if (verifier_forme(dims, n_codes) != TRC_OK) return 0;
     const uint32_t R = dims->lignes[0], C = dims->colonnes[0];
-    return al(3 * sizeof(Tache)) + 3 * pas_tache(dims->lignes[2] > R ? dims->lignes[2] : R,
-                                                 dims->colonnes[2] > C ? dims->colonnes[2] : C, n_codes) +
-           al(4ull * 2 * R) + al(4ull * R);
+    const uint32_t Rm = dims->lignes[2] > R ? dims->lignes[2] : R;
+    const uint32_t Cm = dims->colonnes[2] > C ? dims->colonnes[2] : C;
+    return 3 * pas_tache(Rm, Cm, n_codes) + al(4ull * 2 * R) + al(4ull * R);
 }
 
 // Config 2: one expert, s = W_down swiglu(W_gate x + b_gate, W_up x + b_up) + b_down, every matrix
@@ -509,7 +304,7 @@ extern "C" int trc_expert_fusionne(trc_vue partie, trc_vue luts, const trc_dims_
     const uint32_t Rm = dims->lignes[2] > R ? dims->lignes[2] : R;
     const uint32_t Cm = dims->colonnes[2] > C ? dims->colonnes[2] : C;
     const uint64_t pas = pas_tache(Rm, Cm, n_codes);
-    const uint64_t base = travail.adresse + al(3 * sizeof(Tache));
+    const uint64_t base = travail.adresse;
     const uint64_t gu = base + 3 * pas, act = gu + al(4ull * 2 * R);
     Tache t[3];
     for (uint32_t j = 0; j < 3; ++j) {
@@ -522,21 +317,22 @@ extern "C" int trc_expert_fusionne(trc_vue partie, trc_vue luts, const trc_dims_
         t[j].partiels = t[j].ech + al(uint64_t(Rm) * (Cm / 32));
         t[j].x = j < 2 ? x.adresse : act;
     }
+    const Taches trois = par_valeur(t, 3), bas = par_valeur(t + 2, 1);
     const hipStream_t f = flux_de(flux);
-    hipError_t e = hipMemcpyAsync(reinterpret_cast<void*>(travail.adresse), t, sizeof(t), hipMemcpyHostToDevice, f);
-    if (e != hipSuccess) return trc::erreur_hip("hipMemcpyAsync", e);
-    const Tache* td = reinterpret_cast<const Tache*>(travail.adresse);
     const uint32_t* l = reinterpret_cast<const uint32_t*>(luts.adresse);
     auto ctl = reinterpret_cast<uint32_t*>(controle.adresse);
     const uint32_t B = C / 32;
-    TRC_LANCER(fusion_echelles, dim3(grille_tuiles(uint64_t(Rm) * (Cm / 32), n_delta, 4), 3), dim3(128), f, td, l, ctl);
-    TRC_LANCER(fusion_gemv, dim3(grille_tuiles(16ull * R * B, n_codes, 8), 2), dim3(256), f, td, l, ctl);
-    TRC_LANCER(fusion_finir, dim3((R + 255) / 256, 2), dim3(256), f, td, reinterpret_cast<float*>(gu), R);
+    TRC_LANCER(fusion_echelles, dim3(grille_tuiles(uint64_t(Rm) * (Cm / 32), n_delta, TUILES_ECHELLES), 3),
+               dim3(trc::FILS_ECHELLES_FUSION), f, trois, l, ctl);
+    TRC_LANCER(fusion_gemv, dim3(grille_tuiles(16ull * R * B, n_codes, TUILES_GEMV), 2), dim3(trc::FILS_GEMV_FUSION), f,
+               trois, l, ctl);
+    TRC_LANCER(fusion_finir, dim3((R + 255) / 256, 2), dim3(256), f, trois, reinterpret_cast<float*>(gu), R);
     TRC_LANCER(fusion_swiglu, dim3((R + 255) / 256, 1), dim3(256), f, reinterpret_cast<const float*>(gu),
                reinterpret_cast<float*>(act), R, 1u);
     const uint32_t R2 = dims->lignes[2], B2 = dims->colonnes[2] / 32;
-    TRC_LANCER(fusion_gemv, dim3(grille_tuiles(16ull * R2 * B2, n_codes, 8), 1), dim3(256), f, td + 2, l, ctl);
-    TRC_LANCER(fusion_finir, dim3((R2 + 255) / 256, 1), dim3(256), f, td + 2, reinterpret_cast<float*>(sortie.adresse),
+    TRC_LANCER(fusion_gemv, dim3(grille_tuiles(16ull * R2 * B2, n_codes, TUILES_GEMV), 1), dim3(trc::FILS_GEMV_FUSION),
+               f, bas, l, ctl);
+    TRC_LANCER(fusion_finir, dim3((R2 + 255) / 256, 1), dim3(256), f, bas, reinterpret_cast<float*>(sortie.adresse),
                0u);
     return TRC_OK;
 }
@@ -547,7 +343,7 @@ extern "C" uint64_t trc_taille_travail_couche_moe(const trc_dims_expert* dims, u
     const uint32_t R = dims->lignes[0], C = dims->colonnes[0];
     const uint32_t Rm = dims->lignes[2] > R ? dims->lignes[2] : R;
     const uint32_t Cm = dims->colonnes[2] > C ? dims->colonnes[2] : C;
-    return al(3ull * k * sizeof(Tache)) * 2 + al(4ull * experts) + 3ull * k * pas_tache(Rm, Cm, n_codes) +
+    return al(6ull * k * sizeof(Tache)) + al(4ull * experts) + 3ull * k * pas_tache(Rm, Cm, n_codes) +
            al(4ull * 2 * k * R) + al(4ull * k * R) + al(4ull * k * dims->lignes[2]);
 }
 
@@ -586,10 +382,10 @@ extern "C" int trc_couche_moe_fusionnee(trc_vue parties, uint32_t experts, trc_v
     const uint32_t Cm = C;
     const uint64_t pas = pas_tache(Rm, Cm, n_codes);
     uint64_t p = travail.adresse;
-    const uint64_t t_delta = p;                              // 3k jobs
+    const uint64_t t_delta = p;                                // 3k jobs
     const uint64_t t_gu = t_delta + 3ull * k * sizeof(Tache);  // 2k jobs
     const uint64_t t_bas = t_gu + 2ull * k * sizeof(Tache);    // k jobs
-    p += al(3ull * k * sizeof(Tache)) * 2;
+    p += al(6ull * k * sizeof(Tache));
     const uint64_t logits = p;
     p += al(4ull * experts);
     const uint64_t morceaux = p;
@@ -628,19 +424,19 @@ extern "C" int trc_couche_moe_fusionnee(trc_vue parties, uint32_t experts, trc_v
         pt.kmax[j] = kmax_pour(dims->colonnes[j], n_codes);
     }
     TRC_LANCER(fusion_taches, dim3(1), dim3(64), f, pt, ctl);
-    const Tache* td = reinterpret_cast<const Tache*>(t_delta);
     const uint32_t B = C / 32;
-    TRC_LANCER(fusion_echelles, dim3(grille_tuiles(uint64_t(R) * B, n_delta, 4), 3 * k), dim3(128), f, td, l, ctl);
-    TRC_LANCER_N("fusion_gemv/gate_up", fusion_gemv, dim3(grille_tuiles(16ull * R * B, n_codes, 8), 2 * k), dim3(256),
-                 f, reinterpret_cast<const Tache*>(t_gu), l, ctl);
-    TRC_LANCER(fusion_finir, dim3((R + 255) / 256, 2 * k), dim3(256), f, reinterpret_cast<const Tache*>(t_gu),
-               reinterpret_cast<float*>(gu), R);
+    TRC_LANCER(fusion_echelles, dim3(grille_tuiles(uint64_t(R) * B, n_delta, TUILES_ECHELLES), 3 * k),
+               dim3(trc::FILS_ECHELLES_FUSION), f, par_table(t_delta), l, ctl);
+    TRC_LANCER_N("fusion_gemv/gate_up", fusion_gemv, dim3(grille_tuiles(16ull * R * B, n_codes, TUILES_GEMV), 2 * k),
+                 dim3(trc::FILS_GEMV_FUSION), f, par_table(t_gu), l, ctl);
+    TRC_LANCER(fusion_finir, dim3((R + 255) / 256, 2 * k), dim3(256), f, par_table(t_gu), reinterpret_cast<float*>(gu),
+               R);
     TRC_LANCER(fusion_swiglu, dim3((R + 255) / 256, k), dim3(256), f, reinterpret_cast<const float*>(gu),
                reinterpret_cast<float*>(act), R, k);
-    TRC_LANCER_N("fusion_gemv/down", fusion_gemv, dim3(grille_tuiles(16ull * D * (R / 32), n_codes, 8), k), dim3(256),
-                 f, reinterpret_cast<const Tache*>(t_bas), l, ctl);
-    TRC_LANCER(fusion_finir, dim3((D + 255) / 256, k), dim3(256), f, reinterpret_cast<const Tache*>(t_bas),
-               reinterpret_cast<float*>(sorties), D);
+    TRC_LANCER_N("fusion_gemv/down", fusion_gemv, dim3(grille_tuiles(16ull * D * (R / 32), n_codes, TUILES_GEMV), k),
+                 dim3(trc::FILS_GEMV_FUSION), f, par_table(t_bas), l, ctl);
+    TRC_LANCER(fusion_finir, dim3((D + 255) / 256, k), dim3(256), f, par_table(t_bas), reinterpret_cast<float*>(sorties),
+               D);
     TRC_LANCER(combiner, dim3((D + 255) / 256), dim3(256), f, reinterpret_cast<float*>(residu.adresse),
                reinterpret_cast<const float*>(sorties), D, reinterpret_cast<const float*>(poids.adresse), k, D);
     return TRC_OK;
