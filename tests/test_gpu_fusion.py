@@ -118,6 +118,20 @@ def test_fused_gemv_small_shapes_and_break(fz):
     assert ctl[1] > 0
 
 
+def test_fused_gemv_wide_rows(fz):
+    """Rows wider than the LDS copy of x (3328 > 3072 columns) take the device-memory x variant."""
+    dims = DimsExpert.de([48, 48, 64], [3328, 3328, 256])
+    ex = Expert(9, dims, N_delta=3, N_codes=5)
+    for j in (0, 2):
+        R, C = dims.lignes[j], dims.colonnes[j]
+        x = O.synth_normale_bf16(9, 2, j, C, 1.0)
+        y, ctl = _gemv(fz, ex.partie, ex.luts, j, R, C, x, 3, 5)
+        assert list(ctl) == [0, 0, 0, 0]
+        d = O.disposition_j(list(dims.lignes), list(dims.colonnes), j)
+        y64 = O.gemv_mxfp4_f64(ex.attendu[d.base:d.base + d.pas], x, R, C)
+        assert np.abs(y - y64).max() <= TOL * np.abs(y64).max()
+
+
 def _mlp_oracle(ex, x, dims):
     """The reference chain in its own f32 order (gemv x2, swiglu_oai, gemv) and in f64."""
     R, C = dims.lignes[0], dims.colonnes[0]
@@ -187,4 +201,32 @@ def test_fused_moe_layer_config3(fz):
     ref64 = sum(float(ow[i]) * sorties64[i] for i in range(k))
     assert np.abs(got - ref).max() <= TOL * np.abs(ref).max()
     assert np.abs(got - ref64).max() <= TOL * np.abs(ref64).max()
+    couche.liberer()
+
+
+def test_fused_moe_layer_guards(fz):
+    """A control buffer whose arrival word is not zero means the selection does not run: the layer
+    then works from whatever the index buffer holds, and indices >= experts must only count format
+    errors (no part is read), leave the residual alone and leave controle[3] non-zero."""
+    E, k, N = 6, 4, (8, 8)
+    dims = DimsExpert.de([256, 256, 256], [256, 256, 256])
+    couche = codeur.CoucheSynthetique(77, 0, E, dims, N_delta=N[0], N_codes=N[1])
+    freqs = couche.freqs()
+    luts = O.luts_couche([[freqs[j][t] for t in range(4)] for j in range(3)])
+    parts = [dev(couche.partie(e)) for e in range(E)]
+    table = dev(np.array([p.data_ptr() for p in parts], np.uint64))
+    r16 = (np.stack([O.synth_normale_bf16(77, 3, e, 256, 0.02) for e in range(E)]).view(np.uint32) >> 16)
+    x = O.synth_normale_bf16(77, 4, 0, 256, 1.0)
+    residu0 = np.full(256, 0.5, np.float32)
+    l, rd, xd, res = dev(luts), dev(r16.astype(np.uint16)), dev(x), dev(residu0)
+    idx = dev(np.array([999, 7, 6, 1000] + [0] * 4, np.uint32))
+    w = zeros(32)
+    ctl = dev(np.array([0, 0, 0, 5], np.uint32))
+    tr = zeros(fusion.taille_travail_couche(dims, E, k, N[1]))
+    fz.couche_moe(vue(table), E, vue(l), dims, vue(rd), None, vue(xd), k, vue(res), vue(idx), vue(w), vue(ctl),
+                  vue(tr), *N)
+    c = hote(ctl, np.uint32)
+    assert c[1] > 0 and c[3] != 0
+    assert list(hote(idx, np.uint32)[:4]) == [999, 7, 6, 1000]
+    assert (hote(res, np.float32) == residu0).all()
     couche.liberer()

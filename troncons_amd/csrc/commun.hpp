@@ -30,6 +30,7 @@ constexpr uint8_t SORTE_ECHELLES_BRUTES = 0x07;
 constexpr int CTL_HORS_L = 0;
 constexpr int CTL_FORMAT = 1;
 constexpr int CTL_POINTEUR = 2;
+constexpr int CTL_ARRIVEES = 3;  // fused MoE layer only: router blocks done (back to 0 when the call ends)
 
 // Threads per block of the reference-API kernels (abi.rs:56-61 keeps these a launch detail).
 constexpr uint32_t FILS_ECHELLES = 128;  // 2 wavefronts = 4 DELTA tiles
@@ -69,10 +70,18 @@ __host__ __device__ inline trc_disposition disposition(const trc_dims_expert& di
 
 // ------------------------------------------------------------------------- device-side part reading
 
-__device__ __forceinline__ uint32_t lire_u32(const uint8_t* p) {
-    return uint32_t(p[0]) | (uint32_t(p[1]) << 8) | (uint32_t(p[2]) << 16) | (uint32_t(p[3]) << 24);
+// Global-address-space views: loads through them compile to global_load (vmcnt only) instead of
+// flat_load (which also counts in lgkmcnt and would make every LDS wait wait for them too).
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+template <typename T>
+using gptr = __attribute__((address_space(1))) const T*;
+template <typename T>
+__device__ __forceinline__ gptr<T> glob(const void* p) {
+    return (gptr<T>)(p);
 }
-__device__ __forceinline__ uint32_t lire_u16(const uint8_t* p) { return uint32_t(p[0]) | (uint32_t(p[1]) << 8); }
 
 struct DescFlux {
     const uint8_t* p;
@@ -81,25 +90,29 @@ struct DescFlux {
 };
 
 // Finds stream (kind, matrix) in a level-0 part; false if the part is malformed or the stream is
-// absent (same acceptance as the reference device reader, commun.cuh:111-129).
+// absent (same acceptance as the reference device reader, commun.cuh:111-129, which takes the first
+// matching descriptor). The part must be 16-byte aligned. Executed by a whole wavefront with uniform
+// arguments: lane i loads descriptor i (a part has at most 64), one ballot finds the first match, so
+// the lookup costs two dependent loads instead of one per descriptor.
 __device__ inline bool trouver_flux(const uint8_t* partie, uint8_t sorte, uint32_t matrice, DescFlux& f) {
-    if (lire_u32(partie) != MAGIE_PARTIE0) return false;
-    if (partie[8] != 0) return false;
-    const uint32_t n_flux = lire_u16(partie + 10);
-    const uint32_t utiles = lire_u32(partie + 12);
+    if (partie == nullptr || (reinterpret_cast<uintptr_t>(partie) & 15u) != 0) return false;
+    const u32x4 en = *glob<u32x4>(partie);  // magic | ... | byte 8, n_flux at 10 | utiles
+    const uint32_t n_flux = en.z >> 16, utiles = en.w;
+    if (en.x != MAGIE_PARTIE0 || (en.z & 0xFFu) != 0) return false;
     if (n_flux > 64 || 64u + 16u * n_flux > utiles) return false;
-    for (uint32_t i = 0; i < n_flux; ++i) {
-        const uint8_t* e = partie + 64 + 16 * i;
-        if (e[0] == sorte && e[1] == matrice) {
-            const uint32_t dec = lire_u32(e + 4), lon = lire_u32(e + 8);
-            if ((dec & 15u) != 0 || uint64_t(dec) + lon > utiles) return false;
-            f.p = partie + dec;
-            f.longueur = lon;
-            f.produits = lire_u32(e + 12);
-            return true;
-        }
-    }
-    return false;
+    const uint32_t lane = __lane_id();
+    u32x4 d = {0u, 0u, 0u, 0u};
+    if (lane < n_flux) d = *glob<u32x4>(partie + 64 + 16 * lane);
+    const bool ok = lane < n_flux && (d.x & 0xFFu) == sorte && ((d.x >> 8) & 0xFFu) == matrice;
+    const uint64_t vote = __builtin_amdgcn_ballot_w64(ok);
+    if (vote == 0) return false;
+    const uint32_t i = uint32_t(__builtin_ctzll(vote));
+    const uint32_t dec = uint32_t(__builtin_amdgcn_readlane(d.y, i)), lon = uint32_t(__builtin_amdgcn_readlane(d.z, i));
+    if ((dec & 15u) != 0 || uint64_t(dec) + lon > utiles) return false;
+    f.p = partie + dec;
+    f.longueur = lon;
+    f.produits = uint32_t(__builtin_amdgcn_readlane(d.w, i));
+    return true;
 }
 
 // A validated rANS stream header (geometry 1).
@@ -114,11 +127,12 @@ struct EnteteRans {
 // padding, and its descriptor announces P or besoin (commun.cuh:143-165).
 __device__ inline bool lire_entete(const DescFlux& f, uint32_t besoin, EnteteRans& h) {
     if (f.longueur < 16) return false;
-    h.P = lire_u32(f.p);
-    h.N = lire_u16(f.p + 4);
-    const uint32_t geo = f.p[6];
-    h.T = lire_u32(f.p + 8);
-    h.W = lire_u32(f.p + 12);
+    const u32x4 en = *glob<u32x4>(f.p);  // streams are 16-byte aligned in their part
+    h.P = en.x;
+    h.N = en.y & 0xFFFFu;
+    const uint32_t geo = (en.y >> 16) & 0xFFu;
+    h.T = en.z;
+    h.W = en.w;
     if (geo != 1 || h.N == 0 || (h.P & 127u) != 0) return false;
     if (h.P < besoin || h.P - besoin >= 128u) return false;
     if (f.produits != h.P && f.produits != besoin) return false;

@@ -6,9 +6,10 @@
 //   fusion_gemv      CODES_CTX tiles -> per-(row, tile) partial sums of y = W x, decoded bytes
 //                    dequantised and multiplied in registers;
 //   fusion_finir     y[r] = fixed-order sum of the row's tile partials + bias;
-//   fusion_swiglu    gpt-oss clamped SwiGLU of the gate/up outputs;
-//   fusion_routeur / fusion_taches  (MoE layer) router logits, then the job table of the
-//                    selected experts, built on the device from the top-k indices.
+//   fusion_finir_swiglu    the same for gate and up, then the gpt-oss clamped SwiGLU;
+//   fusion_finir_combiner  the same for the k down products, then the weighted combine;
+//   fusion_selection (MoE layer) router logits, then top-k with softmax weights; the other
+//                    kernels derive their jobs on the device from the chosen indices.
 //
 // Mapping: one wavefront = two rANS tiles (lanes 0-31, 32-63), each tile's words staged in an LDS
 // ring (anneau.hpp). In a macro-step, lane v of a tile produces the 4 code bytes 4(v%4) ..
@@ -27,150 +28,240 @@
 #include "commun.hpp"
 #include "erreurs.hpp"
 #include "fusion_corps.hpp"
+#include "selection.hpp"
 
-// Reference-API kernels (noyaux.hip) reused by the MoE layer.
-extern "C" __global__ void routeur_topk(const float* logits, uint32_t E, uint32_t k, uint32_t* indices, float* poids,
-                                       uint32_t* boite, uint32_t sequence);
-extern "C" __global__ void combiner(float* residu, const float* sorties, uint32_t pas, const float* poids, uint32_t n,
-                                    uint32_t d);
 
-// The layer's LUTs u32[3][4][4096] (reference format) are shared by all jobs of a launch.
+// The layer's LUTs u32[3][4][4096] (reference format) are shared by all jobs of a launch. A
+// block first parses its job's stream header, then stages the LUT (and the medians, or x) in LDS
+// with all loads of a batch in flight together.
 extern "C" __global__ void __launch_bounds__(trc::FILS_ECHELLES_FUSION)
 fusion_echelles(trc::Taches taches, const uint32_t* __restrict__ luts, uint32_t* __restrict__ controle) {
-    __shared__ uint2 lut[trc::M];
-    __shared__ uint8_t med[8192];
-    __shared__ __attribute__((aligned(16))) uint8_t anneaux[(trc::FILS_ECHELLES_FUSION / 32) * trc::OCTETS_ANNEAU];
-    const trc::Tache tc = taches[blockIdx.y];
-    trc::etendre_luts(luts + (uint64_t(tc.j) * 4u + 0u) * trc::M, lut, trc::M);
+    using namespace trc;
+    __shared__ uint2 lut[M];
+    __shared__ __attribute__((aligned(16))) uint8_t med[MED_LDS_MAX];
+    __shared__ __attribute__((aligned(16))) uint8_t anneaux[(FILS_ECHELLES_FUSION / 32) * OCTETS_ANNEAU];
+    const Tache tc = uniforme(taches[blockIdx.y]);
+    etendre_luts<4>(luts + (uint64_t(min(tc.j, 2u)) * 4u + 0u) * M, lut, M / 4u);
+    const PrepEchelles p = preparer_echelles(tc);
+    if (!p.bon) {
+        if (threadIdx.x == 0 && blockIdx.x == 0) atomicAdd(&controle[CTL_FORMAT], 1u);
+        return;
+    }
+    if (tc.lignes <= MED_LDS_MAX) copier_vers_lds(p.fm.p, tc.lignes, p.fm.longueur, med);
     __syncthreads();
-    trc::corps_echelles_fusion(tc, lut, med, anneaux, controle);
+    corps_echelles_fusion(tc, p, lut, med, anneaux, controle);
 }
 
-extern "C" __global__ void __launch_bounds__(trc::FILS_GEMV_FUSION)
-fusion_gemv(trc::Taches taches, const uint32_t* __restrict__ luts, uint32_t* __restrict__ controle) {
-    __shared__ uint2 lut[3 * trc::M];
-    __shared__ __attribute__((aligned(16))) uint8_t anneaux[(trc::FILS_GEMV_FUSION / 32) * trc::OCTETS_ANNEAU];
-    const trc::Tache tc = taches[blockIdx.y];
-    trc::etendre_luts(luts + (uint64_t(tc.j) * 4u + 1u) * trc::M, lut, 3u * trc::M);
+template <bool X_LDS>
+__device__ __forceinline__ void noyau_gemv(const trc::Taches& taches, const uint32_t* __restrict__ luts,
+                                           uint32_t* __restrict__ controle) {
+    using namespace trc;
+    __shared__ uint2 lut[3 * M];
+    __shared__ __attribute__((aligned(16))) uint8_t anneaux[(FILS_GEMV_MAX / 32) * OCTETS_ANNEAU];
+    __shared__ __attribute__((aligned(16))) uint16_t ech[(FILS_GEMV_MAX / 32) * ECH_PAR_TUILE];
+    __shared__ f32x4 xs[X_LDS ? X_LDS_MAX / 4 : 1];
+    const Tache tc = uniforme(taches[blockIdx.y]);
+    etendre_luts<3>(luts + (uint64_t(min(tc.j, 2u)) * 4u + 1u) * M, lut, 3u * M / 4u);
+    const PrepGemv p = preparer_gemv(tc);
+    if (!p.bon) {
+        if (threadIdx.x == 0 && blockIdx.x == 0) atomicAdd(&controle[CTL_FORMAT], 1u);
+        return;
+    }
+    if (X_LDS) copier_vers_lds(reinterpret_cast<const uint8_t*>(tc.x), 4u * tc.colonnes, 4u * tc.colonnes,
+                               reinterpret_cast<uint8_t*>(xs));
     __syncthreads();
-    trc::corps_gemv_fusion(tc, lut, anneaux, controle);
+    corps_gemv_fusion<X_LDS>(tc, p, lut, anneaux, ech, xs, controle);
 }
+
+// x staged in LDS (colonnes <= X_LDS_MAX).
+extern "C" __global__ void __launch_bounds__(trc::FILS_GEMV_MAX)
+fusion_gemv(trc::Taches taches, const uint32_t* __restrict__ luts, uint32_t* __restrict__ controle) {
+    noyau_gemv<true>(taches, luts, controle);
+}
+
+// x read from device memory (any width).
+extern "C" __global__ void __launch_bounds__(trc::FILS_GEMV_MAX)
+fusion_gemv_xg(trc::Taches taches, const uint32_t* __restrict__ luts, uint32_t* __restrict__ controle) {
+    noyau_gemv<false>(taches, luts, controle);
+}
+
+// ---------------------------------------------------------------------------------- finishers
+namespace trc {
+
+// What a finisher needs of a job: its biases, its partial sums and the tiles of each row.
+struct Fin {
+    const float* biais;
+    const float* partiels;
+    uint32_t kmax, B, bpt, lignes;
+    uint32_t bon;
+};
+
+// Whole wavefront (uniform job).
+__device__ __forceinline__ Fin preparer_fin(const Tache& tc) {
+    Fin f;
+    const uint8_t* partie = reinterpret_cast<const uint8_t*>(tc.partie);
+    const uint32_t B = tc.colonnes / 32u;
+    DescFlux fc, fb;
+    EnteteRans h;
+    f.bon = trouver_flux(partie, SORTE_CODES_CTX, tc.j, fc) && trouver_flux(partie, SORTE_BIAIS, tc.j, fb) &&
+            fb.longueur >= 4u * tc.lignes && lire_entete(fc, tc.lignes * B * 16u, h) && B >= 8u &&
+            (B - 1u) / (8u * h.N) + 2u <= tc.kmax;
+    f.biais = f.bon ? reinterpret_cast<const float*>(fb.p) : nullptr;
+    f.partiels = reinterpret_cast<const float*>(tc.partiels);
+    f.kmax = tc.kmax;
+    f.B = B;
+    f.bpt = f.bon ? 8u * h.N : 1u;
+    f.lignes = tc.lignes;
+    return f;
+}
+
+// y[r] = fixed-order sum of row r's tile partials + bias[r].
+__device__ __forceinline__ float somme_fin(const Fin& f, uint32_t r) {
+    const uint32_t t0 = (r * f.B) / f.bpt, t1 = (r * f.B + f.B - 1u) / f.bpt;
+    const float* p = f.partiels + uint64_t(r) * f.kmax;
+    float s = p[0];
+    for (uint32_t k = 1; k <= t1 - t0; ++k) s += p[k];
+    return s + f.biais[r];
+}
+
+// Jobs first + y*par .. of the block parsed by one wavefront each, shared through LDS.
+template <uint32_t N_MAX>
+__device__ __forceinline__ void preparer_fins(const Taches& taches, uint32_t premier, uint32_t n, Fin (&fins)[N_MAX]) {
+    const uint32_t w = threadIdx.x >> 6;
+    for (uint32_t i = w; i < n; i += blockDim.x >> 6) {
+        const Fin f = preparer_fin(uniforme(taches[premier + i]));
+        if (__lane_id() == 0) fins[i] = f;
+    }
+    __syncthreads();
+}
+
+}  // namespace trc
 
 // sorties[y * pas + r] = fixed-order sum of the partials of row r + bias[r], for job y.
 extern "C" __global__ void __launch_bounds__(256)
 fusion_finir(trc::Taches taches, float* __restrict__ sorties, uint32_t pas) {
     using namespace trc;
-    const Tache tc = taches[blockIdx.y];
+    __shared__ Fin fins[1];
+    preparer_fins(taches, blockIdx.y, 1, fins);
+    const Fin f = fins[0];
     const uint32_t r = blockIdx.x * 256u + threadIdx.x;
-    if (r >= tc.lignes) return;
-    const uint8_t* partie = reinterpret_cast<const uint8_t*>(tc.partie);
-    const uint32_t B = tc.colonnes / 32u;
-    DescFlux fc, fb;
-    EnteteRans h;
-    if (!(trouver_flux(partie, SORTE_CODES_CTX, tc.j, fc) && trouver_flux(partie, SORTE_BIAIS, tc.j, fb) &&
-          fb.longueur >= 4u * tc.lignes && lire_entete(fc, tc.lignes * B * 16u, h) && B >= 8u &&
-          (B - 1u) / (8u * h.N) + 2u <= tc.kmax))
-        return;  // counted by fusion_gemv
-    const uint32_t bpt = 8u * h.N;
-    const uint32_t t0 = (r * B) / bpt, t1 = (r * B + B - 1u) / bpt;
-    const float* p = reinterpret_cast<const float*>(tc.partiels) + uint64_t(r) * tc.kmax;
-    float s = p[0];
-    for (uint32_t k = 1; k <= t1 - t0; ++k) s += p[k];
-    sorties[uint64_t(blockIdx.y) * pas + r] = s + reinterpret_cast<const float*>(fb.p)[r];
+    if (!f.bon || r >= f.lignes) return;  // format errors are counted by fusion_gemv
+    sorties[uint64_t(blockIdx.y) * pas + r] = somme_fin(f, r);
 }
 
-// Router logits: y = W x (+ b) with W bf16 row-major (E x C), in the reference gemv_f32 order
-// (bf16 -> f32 is exact, so the bits equal gemv_f32 on the widened matrix).
+// act[i*R + r] = swiglu_oai(gate_i[r], up_i[r]) with gate_i, up_i the finished rows of jobs 2i and
+// 2i+1 (gpt-oss clamped SwiGLU in f64, one rounding: the reference swiglu_oai, passe.cuh:598-605).
 extern "C" __global__ void __launch_bounds__(256)
-fusion_routeur(const uint16_t* __restrict__ W, const float* __restrict__ x, const float* __restrict__ biais,
-               float* __restrict__ y, uint32_t R, uint32_t C) {
+fusion_finir_swiglu(trc::Taches taches, float* __restrict__ act, uint32_t R) {
+    using namespace trc;
+    __shared__ Fin fins[2];
+    const uint32_t i = blockIdx.y;
+    preparer_fins(taches, 2u * i, 2, fins);
+    const uint32_t r = blockIdx.x * 256u + threadIdx.x;
+    if (!fins[0].bon || !fins[1].bon || r >= R || r >= fins[0].lignes || r >= fins[1].lignes) return;
+    const double gv = fmin(double(somme_fin(fins[0], r)), 7.0);
+    const double uv = fmin(fmax(double(somme_fin(fins[1], r)), -7.0), 7.0);
+    act[uint64_t(i) * R + r] = float(gv / (1.0 + exp(-1.702 * gv)) * (uv + 1.0));
+}
+
+// residu[r] += ((w0 s0[r] + w1 s1[r]) + w2 s2[r]) + ..., s_i the finished rows of job i, each product
+// and sum rounded on its own (the reference combiner, passe.cuh:611-622).
+extern "C" __global__ void __launch_bounds__(256)
+fusion_finir_combiner(trc::Taches taches, float* __restrict__ residu, const float* __restrict__ poids, uint32_t D,
+                      uint32_t k) {
+#pragma clang fp contract(off)
+    using namespace trc;
+    __shared__ Fin fins[TOPK_MAX];
+    preparer_fins(taches, 0, k, fins);
+    const uint32_t r = blockIdx.x * 256u + threadIdx.x;
+    for (uint32_t i = 0; i < k; ++i)
+        if (!fins[i].bon || r >= fins[i].lignes) return;
+    if (r >= D) return;
+    float s = poids[0] * somme_fin(fins[0], r);
+    for (uint32_t i = 1; i < k; ++i) {
+        const float p = poids[i] * somme_fin(fins[i], r);
+        s = s + p;
+    }
+    residu[r] = residu[r] + s;
+}
+
+// ---------------------------------------------------------------------------- router + top-k
+namespace trc {
+
+// Router logits y = W x (+ b), W bf16 row-major (R x C), in the reference gemv_f32 order (bf16 ->
+// f32 is exact, so the bits equal gemv_f32 on the widened matrix, passe.cuh:104-130): one row per
+// half-wavefront, lane v taking float4 groups v, v+32, ..., its loads issued 8 groups at a time.
+__device__ __forceinline__ void routeur_ligne(const uint16_t* __restrict__ W, const float* __restrict__ x,
+                                              const float* __restrict__ biais, float* __restrict__ y, uint32_t R,
+                                              uint32_t C) {
     const uint32_t voie = threadIdx.x & 31u;
-    const uint32_t r0 = (blockIdx.x * 8u + (threadIdx.x >> 5)) * 4u;
-    if (r0 >= R) return;
+    const uint32_t r = blockIdx.x * (blockDim.x >> 5) + (threadIdx.x >> 5);
+    const uint32_t lig = min(r, R - 1u);
     const uint32_t C4 = C / 4u;
-    const float4* x4 = reinterpret_cast<const float4*>(x);
-    const uint2* W4 = reinterpret_cast<const uint2*>(W);
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    uint32_t lig[4];
+    const gptr<f32x4> x4 = glob<f32x4>(x);
+    const gptr<u32x2> W4 = glob<u32x2>(W + uint64_t(lig) * C);
+    constexpr uint32_t LOT = 8;
+    float acc = 0.0f;
+    for (uint32_t c0 = 0; c0 < C4; c0 += 32u * LOT) {
+        u32x2 w[LOT];
+        f32x4 xv[LOT];
 #pragma unroll
-    for (uint32_t i = 0; i < 4; ++i) lig[i] = min(r0 + i, R - 1u);
-    for (uint32_t c = voie; c < C4; c += 32u) {
-        const float4 xv = x4[c];
+        for (uint32_t i = 0; i < LOT; ++i) {
+            const uint32_t c = c0 + 32u * i + voie;
+            if (c < C4) {
+                w[i] = W4[c];
+                xv[i] = x4[c];
+            }
+        }
 #pragma unroll
-        for (uint32_t i = 0; i < 4; ++i) {
-            const uint2 w = W4[uint64_t(lig[i]) * C4 + c];
-            acc[i] = fmaf(__uint_as_float(w.x << 16), xv.x, acc[i]);
-            acc[i] = fmaf(__uint_as_float(w.x & 0xFFFF0000u), xv.y, acc[i]);
-            acc[i] = fmaf(__uint_as_float(w.y << 16), xv.z, acc[i]);
-            acc[i] = fmaf(__uint_as_float(w.y & 0xFFFF0000u), xv.w, acc[i]);
+        for (uint32_t i = 0; i < LOT; ++i) {
+            if (c0 + 32u * i + voie < C4) {
+                acc = fmaf(__uint_as_float(w[i].x << 16), xv[i].x, acc);
+                acc = fmaf(__uint_as_float(w[i].x & 0xFFFF0000u), xv[i].y, acc);
+                acc = fmaf(__uint_as_float(w[i].y << 16), xv[i].z, acc);
+                acc = fmaf(__uint_as_float(w[i].y & 0xFFFF0000u), xv[i].w, acc);
+            }
         }
     }
-#pragma unroll
-    for (uint32_t i = 0; i < 4; ++i) {
-        const float s = trc::somme_demi_f32(acc[i]);
-        if (voie == 0 && r0 + i < R) y[r0 + i] = biais != nullptr ? s + biais[r0 + i] : s;
-    }
+    const float s = somme_demi_f32(acc);
+    if (voie == 0 && r < R) y[r] = biais != nullptr ? s + biais[r] : s;
 }
 
-// Job tables of a MoE layer from the top-k indices: for selected expert i, jobs 2i (gate) and
-// 2i+1 (up) in table `gu` against x, job i (down) in table `bas` against act + i*R, and the
-// DELTA jobs (3 per expert) in `delta`. Workspace pieces are laid out per (i, j).
-namespace trc {
-struct ParamsTaches {
-    uint64_t parties;   // u64[E] part addresses
-    uint64_t indices;   // u32[k]
-    uint64_t x;         // f32[C]
-    uint64_t act;       // f32[k * R]
-    uint64_t ech;       // scales: (i*3 + j) * pas
-    uint64_t partiels;  // partials: (i*3 + j) * pas
-    uint64_t delta, gu, bas;  // Tache tables
-    uint64_t pas;             // workspace bytes per (i, j)
-    uint32_t lignes[3], colonnes[3], kmax[3];
-    uint32_t k, E;
-};
 }  // namespace trc
 
-extern "C" __global__ void __launch_bounds__(64) fusion_taches(trc::ParamsTaches p, uint32_t* __restrict__ controle) {
-    using namespace trc;
-    const uint32_t i = threadIdx.x;
-    if (i >= p.k) return;
-    const uint32_t e = reinterpret_cast<const uint32_t*>(p.indices)[i];
-    uint64_t partie = 0;
-    if (e < p.E) {
-        partie = reinterpret_cast<const uint64_t*>(p.parties)[e];
-    } else {
-        atomicAdd(&controle[CTL_FORMAT], 1u);
-    }
-    Tache* td = reinterpret_cast<Tache*>(p.delta);
-    Tache* tgu = reinterpret_cast<Tache*>(p.gu);
-    Tache* tb = reinterpret_cast<Tache*>(p.bas);
-    for (uint32_t j = 0; j < 3; ++j) {
-        Tache t;
-        t.partie = partie;
-        t.j = j;
-        t.kmax = p.kmax[j];
-        t.lignes = p.lignes[j];
-        t.colonnes = p.colonnes[j];
-        t.ech = p.ech + uint64_t(i * 3 + j) * p.pas;
-        t.partiels = p.partiels + uint64_t(i * 3 + j) * p.pas;
-        t.x = j < 2 ? p.x : p.act + uint64_t(i) * p.colonnes[2] * 4u;
-        td[i * 3 + j] = t;
-        if (j < 2)
-            tgu[i * 2 + j] = t;
-        else
-            tb[i] = t;
-    }
-}
-
-// act[i*R + r] = swiglu(gu[2i*R + r], gu[(2i+1)*R + r]) for the k experts (gpt-oss clamped SwiGLU,
-// f64, one rounding — the reference swiglu_oai).
+// The layer's expert selection in one launch: router logits (one row per half-wavefront), then the
+// last block to finish (arrival count in controle[3], which the caller zeroes with the rest of the
+// control buffer and which that block puts back to 0) runs the reference top-k with softmax
+// weights (routeur_topk) over all logits. No block waits for another.
 extern "C" __global__ void __launch_bounds__(256)
-fusion_swiglu(const float* __restrict__ gu, float* __restrict__ act, uint32_t R, uint32_t k) {
-    const uint32_t r = blockIdx.x * 256u + threadIdx.x, i = blockIdx.y;
-    if (r >= R || i >= k) return;
-    const double gv = fmin(double(gu[uint64_t(2 * i) * R + r]), 7.0);
-    const double uv = fmin(fmax(double(gu[uint64_t(2 * i + 1) * R + r]), -7.0), 7.0);
-    act[uint64_t(i) * R + r] = float(gv / (1.0 + exp(-1.702 * gv)) * (uv + 1.0));
+fusion_selection(const uint16_t* __restrict__ W, const float* __restrict__ x, const float* __restrict__ biais,
+                 float* logits, uint32_t E, uint32_t C, uint32_t k, uint32_t* __restrict__ indices,
+                 float* __restrict__ poids, uint32_t* __restrict__ controle) {
+    using namespace trc;
+    routeur_ligne(W, x, biais, logits, E, C);
+    __shared__ uint32_t dernier;
+    __threadfence();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint32_t n =
+            __hip_atomic_fetch_add(&controle[CTL_ARRIVEES], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        dernier = (n == gridDim.x - 1u) ? 1u : 0u;
+    }
+    __syncthreads();
+    if (dernier == 0u || threadIdx.x >= 64u) return;
+    __threadfence();
+    uint32_t choisi[TOPK_MAX];
+    float w[TOPK_MAX];
+    topk_vague(logits, E, k, choisi, w);
+    if (threadIdx.x == 0) {
+#pragma unroll
+        for (uint32_t r = 0; r < TOPK_MAX; ++r)
+            if (r < k) {
+                indices[r] = choisi[r];
+                poids[r] = w[r];
+            }
+        __hip_atomic_store(&controle[CTL_ARRIVEES], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
 }
 
 // ============================================================================ C-ABI launch layer
@@ -197,12 +288,40 @@ uint32_t grille_tuiles(uint64_t octets, uint32_t N, uint32_t tuiles_par_bloc) {
 }
 
 constexpr uint32_t TUILES_ECHELLES = trc::FILS_ECHELLES_FUSION / 32;
-constexpr uint32_t TUILES_GEMV = trc::FILS_GEMV_FUSION / 32;
 
-// Workspace of one matrix job: scales then partial sums.
+// Workspace of one matrix job: scale entries (u16 per block + staging margin), then partial sums.
+uint64_t octets_ech(uint32_t R, uint32_t C) { return al(2ull * (uint64_t(R) * (C / 32) + trc::ECH_MARGE)); }
+
 uint64_t pas_tache(uint32_t R, uint32_t C, uint32_t n_codes) {
-    return al(uint64_t(R) * (C / 32)) + al(4ull * R * kmax_pour(C, n_codes));
+    return octets_ech(R, C) + al(4ull * R * kmax_pour(C, n_codes));
 }
+
+// Launch shape of a CODES pass over `jobs` matrices of R x C: 1024, 512 or 256 threads (32, 16 or 8
+// tiles) per block, the largest that still gives every CU of the chip a block.
+struct FormeGemv {
+    dim3 grille, bloc;
+    bool x_lds;
+};
+
+FormeGemv forme_gemv(uint32_t R, uint32_t C, uint32_t N, uint32_t jobs) {
+    const uint64_t octets = 16ull * R * (C / 32);
+    const uint64_t T = ((octets + 127) / 128 + N - 1) / N;
+    uint32_t fils = trc::FILS_GEMV_MAX;
+    while (fils > 256 && ((T + fils / 32 - 1) / (fils / 32)) * jobs < 256) fils /= 2;
+    FormeGemv f;
+    f.grille = dim3(grille_tuiles(octets, N, fils / 32), jobs);
+    f.bloc = dim3(fils);
+    f.x_lds = C <= trc::X_LDS_MAX;
+    return f;
+}
+
+#define TRC_LANCER_GEMV(nom, forme, f, ...)                                                         \
+    do {                                                                                            \
+        if ((forme).x_lds)                                                                          \
+            TRC_LANCER_N(nom, fusion_gemv, (forme).grille, (forme).bloc, f, __VA_ARGS__);           \
+        else                                                                                        \
+            TRC_LANCER_N(nom "/xg", fusion_gemv_xg, (forme).grille, (forme).bloc, f, __VA_ARGS__); \
+    } while (0)
 
 int verifier_forme(const trc_dims_expert* dims, uint32_t n_codes) {
     if (dims == nullptr) return usage("dims absent");
@@ -216,15 +335,17 @@ int verifier_forme(const trc_dims_expert* dims, uint32_t n_codes) {
 
 Taches par_valeur(const Tache* t, uint32_t n) {
     Taches l;
-    l.table = nullptr;
+    std::memset(&l, 0, sizeof(l));
+    l.mode = trc::TACHES_LOCALES;
     for (uint32_t i = 0; i < n && i < 3; ++i) l.locales[i] = t[i];
     return l;
 }
 
-Taches par_table(uint64_t adresse) {
+Taches par_moe(const trc::ParamsMoe& pm, uint32_t mode) {
     Taches l;
     std::memset(&l, 0, sizeof(l));
-    l.table = reinterpret_cast<const Tache*>(adresse);
+    l.moe = pm;
+    l.mode = mode;
     return l;
 }
 
@@ -242,7 +363,8 @@ extern "C" int trc_gemv_fusionnee(trc_vue partie, uint32_t j, trc_vue luts, uint
     TRC_VERIFIER(j < 3, "matrice %u", j);
     TRC_VERIFIER(lignes > 0 && colonnes % 32 == 0 && colonnes / 32 >= 8, "forme %u x %u", lignes, colonnes);
     TRC_VERIFIER(n_delta > 0 && n_codes > 0 && n_delta <= 65535 && n_codes <= 65535, "N faux");
-    TRC_VERIFIER(partie.adresse && partie.octets >= 64, "partie trop courte");
+    TRC_VERIFIER(partie.adresse && partie.octets >= 64 && partie.adresse % 16 == 0,
+                 "partie trop courte ou non alignee sur 16");
     TRC_VERIFIER(luts.adresse && luts.octets >= uint64_t(trc::LUTS_PAR_COUCHE) * 4, "LUT trop courtes");
     TRC_VERIFIER(x.adresse && x.octets >= 4ull * colonnes && x.adresse % 16 == 0, "x trop court ou non aligne");
     TRC_VERIFIER(y.adresse && y.octets >= 4ull * lignes, "y trop court");
@@ -255,7 +377,7 @@ extern "C" int trc_gemv_fusionnee(trc_vue partie, uint32_t j, trc_vue luts, uint
     t.partie = partie.adresse;
     t.x = x.adresse;
     t.ech = travail.adresse;
-    t.partiels = t.ech + al(uint64_t(lignes) * (colonnes / 32));
+    t.partiels = t.ech + octets_ech(lignes, colonnes);
     t.j = j;
     t.kmax = kmax_pour(colonnes, n_codes);
     t.lignes = lignes;
@@ -267,8 +389,7 @@ extern "C" int trc_gemv_fusionnee(trc_vue partie, uint32_t j, trc_vue luts, uint
     const uint32_t B = colonnes / 32;
     TRC_LANCER(fusion_echelles, dim3(grille_tuiles(uint64_t(lignes) * B, n_delta, TUILES_ECHELLES), 1),
                dim3(trc::FILS_ECHELLES_FUSION), f, tv, l, ctl);
-    TRC_LANCER(fusion_gemv, dim3(grille_tuiles(16ull * lignes * B, n_codes, TUILES_GEMV), 1),
-               dim3(trc::FILS_GEMV_FUSION), f, tv, l, ctl);
+    TRC_LANCER_GEMV("fusion_gemv", forme_gemv(lignes, colonnes, n_codes, 1), f, tv, l, ctl);
     TRC_LANCER(fusion_finir, dim3((lignes + 255) / 256, 1), dim3(256), f, tv, reinterpret_cast<float*>(y.adresse), 0u);
     return TRC_OK;
 }
@@ -278,7 +399,7 @@ extern "C" uint64_t trc_taille_travail_expert_fusionne(const trc_dims_expert* di
     const uint32_t R = dims->lignes[0], C = dims->colonnes[0];
     const uint32_t Rm = dims->lignes[2] > R ? dims->lignes[2] : R;
     const uint32_t Cm = dims->colonnes[2] > C ? dims->colonnes[2] : C;
-    return 3 * pas_tache(Rm, Cm, n_codes) + al(4ull * 2 * R) + al(4ull * R);
+    return 3 * pas_tache(Rm, Cm, n_codes) + al(4ull * R);
 }
 
 // Config 2: one expert, s = W_down swiglu(W_gate x + b_gate, W_up x + b_up) + b_down, every matrix
@@ -292,7 +413,8 @@ extern "C" int trc_expert_fusionne(trc_vue partie, trc_vue luts, const trc_dims_
     TRC_VERIFIER(dims->lignes[1] == R && dims->colonnes[1] == C && dims->colonnes[2] == R,
                  "gate, up et down incompatibles (down doit lire les %u sorties de la SwiGLU)", R);
     TRC_VERIFIER(n_delta > 0 && n_delta <= 65535, "N de DELTA %u", n_delta);
-    TRC_VERIFIER(partie.adresse && partie.octets >= 64, "partie trop courte");
+    TRC_VERIFIER(partie.adresse && partie.octets >= 64 && partie.adresse % 16 == 0,
+                 "partie trop courte ou non alignee sur 16");
     TRC_VERIFIER(luts.adresse && luts.octets >= uint64_t(trc::LUTS_PAR_COUCHE) * 4, "LUT trop courtes");
     TRC_VERIFIER(x.adresse && x.octets >= 4ull * C && x.adresse % 16 == 0, "x trop court ou non aligne");
     TRC_VERIFIER(sortie.adresse && sortie.octets >= 4ull * dims->lignes[2], "sortie trop courte");
@@ -305,7 +427,7 @@ extern "C" int trc_expert_fusionne(trc_vue partie, trc_vue luts, const trc_dims_
     const uint32_t Cm = dims->colonnes[2] > C ? dims->colonnes[2] : C;
     const uint64_t pas = pas_tache(Rm, Cm, n_codes);
     const uint64_t base = travail.adresse;
-    const uint64_t gu = base + 3 * pas, act = gu + al(4ull * 2 * R);
+    const uint64_t act = base + 3 * pas;
     Tache t[3];
     for (uint32_t j = 0; j < 3; ++j) {
         t[j].partie = partie.adresse;
@@ -314,24 +436,19 @@ extern "C" int trc_expert_fusionne(trc_vue partie, trc_vue luts, const trc_dims_
         t[j].colonnes = dims->colonnes[j];
         t[j].kmax = kmax_pour(dims->colonnes[j], n_codes);
         t[j].ech = base + j * pas;
-        t[j].partiels = t[j].ech + al(uint64_t(Rm) * (Cm / 32));
+        t[j].partiels = t[j].ech + octets_ech(Rm, Cm);
         t[j].x = j < 2 ? x.adresse : act;
     }
     const Taches trois = par_valeur(t, 3), bas = par_valeur(t + 2, 1);
     const hipStream_t f = flux_de(flux);
     const uint32_t* l = reinterpret_cast<const uint32_t*>(luts.adresse);
     auto ctl = reinterpret_cast<uint32_t*>(controle.adresse);
-    const uint32_t B = C / 32;
     TRC_LANCER(fusion_echelles, dim3(grille_tuiles(uint64_t(Rm) * (Cm / 32), n_delta, TUILES_ECHELLES), 3),
                dim3(trc::FILS_ECHELLES_FUSION), f, trois, l, ctl);
-    TRC_LANCER(fusion_gemv, dim3(grille_tuiles(16ull * R * B, n_codes, TUILES_GEMV), 2), dim3(trc::FILS_GEMV_FUSION), f,
-               trois, l, ctl);
-    TRC_LANCER(fusion_finir, dim3((R + 255) / 256, 2), dim3(256), f, trois, reinterpret_cast<float*>(gu), R);
-    TRC_LANCER(fusion_swiglu, dim3((R + 255) / 256, 1), dim3(256), f, reinterpret_cast<const float*>(gu),
-               reinterpret_cast<float*>(act), R, 1u);
-    const uint32_t R2 = dims->lignes[2], B2 = dims->colonnes[2] / 32;
-    TRC_LANCER(fusion_gemv, dim3(grille_tuiles(16ull * R2 * B2, n_codes, TUILES_GEMV), 1), dim3(trc::FILS_GEMV_FUSION),
-               f, bas, l, ctl);
+    TRC_LANCER_GEMV("fusion_gemv", forme_gemv(R, C, n_codes, 2), f, trois, l, ctl);
+    TRC_LANCER(fusion_finir_swiglu, dim3((R + 255) / 256, 1), dim3(256), f, trois, reinterpret_cast<float*>(act), R);
+    const uint32_t R2 = dims->lignes[2];
+    TRC_LANCER_GEMV("fusion_gemv", forme_gemv(R2, dims->colonnes[2], n_codes, 1), f, bas, l, ctl);
     TRC_LANCER(fusion_finir, dim3((R2 + 255) / 256, 1), dim3(256), f, bas, reinterpret_cast<float*>(sortie.adresse),
                0u);
     return TRC_OK;
@@ -339,19 +456,20 @@ extern "C" int trc_expert_fusionne(trc_vue partie, trc_vue luts, const trc_dims_
 
 extern "C" uint64_t trc_taille_travail_couche_moe(const trc_dims_expert* dims, uint32_t experts, uint32_t k,
                                                   uint32_t n_codes) {
-    if (verifier_forme(dims, n_codes) != TRC_OK || k == 0 || k > 8 || experts == 0) return 0;
+    if (verifier_forme(dims, n_codes) != TRC_OK || k == 0 || k > trc::TOPK_MAX || experts == 0) return 0;
     const uint32_t R = dims->lignes[0], C = dims->colonnes[0];
     const uint32_t Rm = dims->lignes[2] > R ? dims->lignes[2] : R;
     const uint32_t Cm = dims->colonnes[2] > C ? dims->colonnes[2] : C;
-    return al(6ull * k * sizeof(Tache)) + al(4ull * experts) + 3ull * k * pas_tache(Rm, Cm, n_codes) +
-           al(4ull * 2 * k * R) + al(4ull * k * R) + al(4ull * k * dims->lignes[2]);
+    return al(4ull * experts) + 3ull * k * pas_tache(Rm, Cm, n_codes) + al(4ull * k * R);
 }
 
 // Config 3: one MoE layer decode step at batch 1. logits = W_r x (+ b_r) (W_r bf16, experts x C),
 // top-k with softmax weights (indices/poids written out), then for the k selected experts the fused
 // MLP, and residu[i] += ((w0 s0[i] + w1 s1[i]) + ...) in expert order. parties: u64[experts] device
 // addresses of the experts' level-0 parts; luts: the layer's u32[3][4][4096]. No host sync: the
-// selection flows from the router to the expert kernels through device memory.
+// selection flows from the router to the expert kernels through device memory, and every kernel
+// derives its jobs from the top-k indices (checked against `experts` before any part is read).
+// Six launches: selection, DELTA, gate/up, finish + SwiGLU, down, finish + combine.
 extern "C" int trc_couche_moe_fusionnee(trc_vue parties, uint32_t experts, trc_vue luts, const trc_dims_expert* dims,
                                         trc_vue routeur, trc_vue routeur_biais, trc_vue x, uint32_t k,
                                         trc_vue residu, trc_vue indices, trc_vue poids, trc_vue controle,
@@ -362,9 +480,11 @@ extern "C" int trc_couche_moe_fusionnee(trc_vue parties, uint32_t experts, trc_v
     TRC_VERIFIER(dims->lignes[1] == R && dims->colonnes[1] == C && dims->colonnes[2] == R,
                  "gate, up et down incompatibles");
     TRC_VERIFIER(D == C, "la sortie des experts (%u) doit avoir la taille de x (%u)", D, C);
-    TRC_VERIFIER(experts > 0 && experts <= 256 && k > 0 && k <= 8 && k <= experts, "top-%u sur %u", k, experts);
+    TRC_VERIFIER(experts > 0 && experts <= trc::EXPERTS_MAX && k > 0 && k <= trc::TOPK_MAX && k <= experts,
+                 "top-%u sur %u", k, experts);
     TRC_VERIFIER(n_delta > 0 && n_delta <= 65535, "N de DELTA %u", n_delta);
-    TRC_VERIFIER(parties.adresse && parties.octets >= 8ull * experts, "table des parties trop courte");
+    TRC_VERIFIER(parties.adresse && parties.octets >= 8ull * experts && parties.adresse % 8 == 0,
+                 "table des parties trop courte");
     TRC_VERIFIER(luts.adresse && luts.octets >= uint64_t(trc::LUTS_PAR_COUCHE) * 4, "LUT trop courtes");
     TRC_VERIFIER(routeur.adresse && routeur.octets >= 2ull * experts * C && routeur.adresse % 8 == 0,
                  "routeur bf16 trop court ou non aligne sur 8");
@@ -382,62 +502,43 @@ extern "C" int trc_couche_moe_fusionnee(trc_vue parties, uint32_t experts, trc_v
     const uint32_t Cm = C;
     const uint64_t pas = pas_tache(Rm, Cm, n_codes);
     uint64_t p = travail.adresse;
-    const uint64_t t_delta = p;                                // 3k jobs
-    const uint64_t t_gu = t_delta + 3ull * k * sizeof(Tache);  // 2k jobs
-    const uint64_t t_bas = t_gu + 2ull * k * sizeof(Tache);    // k jobs
-    p += al(6ull * k * sizeof(Tache));
     const uint64_t logits = p;
     p += al(4ull * experts);
     const uint64_t morceaux = p;
     p += 3ull * k * pas;
-    const uint64_t gu = p;
-    p += al(4ull * 2 * k * R);
     const uint64_t act = p;
-    p += al(4ull * k * R);
-    const uint64_t sorties = p;
 
+    trc::ParamsMoe pm;
+    std::memset(&pm, 0, sizeof(pm));
+    pm.parties = parties.adresse;
+    pm.indices = indices.adresse;
+    pm.x = x.adresse;
+    pm.act = act;
+    pm.ech = morceaux;
+    pm.partiels = morceaux + octets_ech(Rm, Cm);
+    pm.pas = pas;
+    pm.k = k;
+    pm.E = experts;
+    for (int j = 0; j < 3; ++j) {
+        pm.lignes[j] = dims->lignes[j];
+        pm.colonnes[j] = dims->colonnes[j];
+        pm.kmax[j] = kmax_pour(dims->colonnes[j], n_codes);
+    }
+    const Taches t_delta = par_moe(pm, trc::TACHES_MOE_DELTA), t_gu = par_moe(pm, trc::TACHES_MOE_GU),
+                 t_bas = par_moe(pm, trc::TACHES_MOE_BAS);
     const hipStream_t f = flux_de(flux);
     auto ctl = reinterpret_cast<uint32_t*>(controle.adresse);
     const uint32_t* l = reinterpret_cast<const uint32_t*>(luts.adresse);
-    TRC_LANCER(fusion_routeur, dim3((experts + 31) / 32), dim3(256), f,
+    TRC_LANCER(fusion_selection, dim3((experts + 7) / 8), dim3(256), f,
                reinterpret_cast<const uint16_t*>(routeur.adresse), reinterpret_cast<const float*>(x.adresse),
-               reinterpret_cast<const float*>(routeur_biais.adresse), reinterpret_cast<float*>(logits), experts, C);
-    TRC_LANCER(routeur_topk, dim3(1), dim3(64), f, reinterpret_cast<const float*>(logits), experts, k,
-               reinterpret_cast<uint32_t*>(indices.adresse), reinterpret_cast<float*>(poids.adresse),
-               static_cast<uint32_t*>(nullptr), 0u);
-    trc::ParamsTaches pt;
-    pt.parties = parties.adresse;
-    pt.indices = indices.adresse;
-    pt.x = x.adresse;
-    pt.act = act;
-    pt.ech = morceaux;
-    pt.partiels = morceaux + al(uint64_t(Rm) * (Cm / 32));
-    pt.delta = t_delta;
-    pt.gu = t_gu;
-    pt.bas = t_bas;
-    pt.k = k;
-    pt.E = experts;
-    pt.pas = pas;
-    for (int j = 0; j < 3; ++j) {
-        pt.lignes[j] = dims->lignes[j];
-        pt.colonnes[j] = dims->colonnes[j];
-        pt.kmax[j] = kmax_pour(dims->colonnes[j], n_codes);
-    }
-    TRC_LANCER(fusion_taches, dim3(1), dim3(64), f, pt, ctl);
-    const uint32_t B = C / 32;
-    TRC_LANCER(fusion_echelles, dim3(grille_tuiles(uint64_t(R) * B, n_delta, TUILES_ECHELLES), 3 * k),
-               dim3(trc::FILS_ECHELLES_FUSION), f, par_table(t_delta), l, ctl);
-    TRC_LANCER_N("fusion_gemv/gate_up", fusion_gemv, dim3(grille_tuiles(16ull * R * B, n_codes, TUILES_GEMV), 2 * k),
-                 dim3(trc::FILS_GEMV_FUSION), f, par_table(t_gu), l, ctl);
-    TRC_LANCER(fusion_finir, dim3((R + 255) / 256, 2 * k), dim3(256), f, par_table(t_gu), reinterpret_cast<float*>(gu),
-               R);
-    TRC_LANCER(fusion_swiglu, dim3((R + 255) / 256, k), dim3(256), f, reinterpret_cast<const float*>(gu),
-               reinterpret_cast<float*>(act), R, k);
-    TRC_LANCER_N("fusion_gemv/down", fusion_gemv, dim3(grille_tuiles(16ull * D * (R / 32), n_codes, TUILES_GEMV), k),
-                 dim3(trc::FILS_GEMV_FUSION), f, par_table(t_bas), l, ctl);
-    TRC_LANCER(fusion_finir, dim3((D + 255) / 256, k), dim3(256), f, par_table(t_bas), reinterpret_cast<float*>(sorties),
-               D);
-    TRC_LANCER(combiner, dim3((D + 255) / 256), dim3(256), f, reinterpret_cast<float*>(residu.adresse),
-               reinterpret_cast<const float*>(sorties), D, reinterpret_cast<const float*>(poids.adresse), k, D);
+               reinterpret_cast<const float*>(routeur_biais.adresse), reinterpret_cast<float*>(logits), experts, C, k,
+               reinterpret_cast<uint32_t*>(indices.adresse), reinterpret_cast<float*>(poids.adresse), ctl);
+    TRC_LANCER(fusion_echelles, dim3(grille_tuiles(uint64_t(R) * (C / 32), n_delta, TUILES_ECHELLES), 3 * k),
+               dim3(trc::FILS_ECHELLES_FUSION), f, t_delta, l, ctl);
+    TRC_LANCER_GEMV("fusion_gemv/gate_up", forme_gemv(R, C, n_codes, 2 * k), f, t_gu, l, ctl);
+    TRC_LANCER(fusion_finir_swiglu, dim3((R + 255) / 256, k), dim3(256), f, t_gu, reinterpret_cast<float*>(act), R);
+    TRC_LANCER_GEMV("fusion_gemv/down", forme_gemv(D, R, n_codes, k), f, t_bas, l, ctl);
+    TRC_LANCER(fusion_finir_combiner, dim3((D + 255) / 256), dim3(256), f, t_bas, reinterpret_cast<float*>(residu.adresse),
+               reinterpret_cast<const float*>(poids.adresse), D, k);
     return TRC_OK;
 }

@@ -1,6 +1,6 @@
 // fusion_corps.hpp — bodies of the fused-path kernels (gfx950): the DELTA pass that rebuilds the
-// E8M0 scales, and the CODES_CTX pass that decodes the code bytes into registers and multiplies
-// them against x on the fly.
+// E8M0 scales (and each block's CODES_CTX context), and the CODES_CTX pass that decodes the code
+// bytes into registers and multiplies them against x on the fly.
 //
 // Mapping: one wavefront = two rANS tiles (lanes 0-31, 32-63), each tile's words staged in an LDS
 // ring (anneau.hpp). In a macro-step, lane v of a tile produces the 4 code bytes 4(v%4) ..
@@ -23,7 +23,7 @@ namespace trc {
 struct Tache {
     uint64_t partie;    // level-0 part
     uint64_t x;         // f32[colonnes], 16-byte aligned
-    uint64_t ech;       // u8[lignes * colonnes/32] scales (workspace, 4-byte aligned)
+    uint64_t ech;       // u16[lignes * colonnes/32 + 256]: e | kappa << 8 per block (workspace)
     uint64_t partiels;  // f32[lignes * kmax] partial sums (workspace)
     uint32_t j;         // matrix index in the part
     uint32_t kmax;      // partial slots per row
@@ -31,16 +31,88 @@ struct Tache {
 };
 static_assert(sizeof(Tache) == 48, "Tache");
 
-// The jobs of a launch: a device table (MoE layer, built on the device) or up to 3 jobs passed by
-// value in the kernel arguments (one matrix, one expert). Job of block (x, y) = y.
+// A MoE layer's jobs, derived on the device from the router's top-k: selected expert i (index
+// indices[i] < E, else its jobs get a null part and count as format errors) has matrices j = 0, 1, 2
+// (gate, up, down), each with its own workspace piece (i*3 + j) * pas; gate/up read x, down reads
+// the SwiGLU output act + i*R.
+struct ParamsMoe {
+    uint64_t parties;   // u64[E] part addresses (caller's table)
+    uint64_t indices;   // u32[k] written by the router's top-k
+    uint64_t x;         // f32[C]
+    uint64_t act;       // f32[k * R]
+    uint64_t ech;       // scale entries of piece 0
+    uint64_t partiels;  // partial sums of piece 0
+    uint64_t pas;       // workspace bytes per piece
+    uint32_t lignes[3], colonnes[3], kmax[3];
+    uint32_t k, E;
+};
+
+enum ModeTaches : uint32_t {
+    TACHES_LOCALES = 0,  // up to 3 jobs passed by value (one matrix, one expert)
+    TACHES_MOE_DELTA = 1,  // job y = (expert y/3, matrix y%3)
+    TACHES_MOE_GU = 2,     // job y = (expert y/2, matrix y%2)
+    TACHES_MOE_BAS = 3,    // job y = (expert y, matrix 2)
+};
+
+// The jobs of a launch; job of block (x, y) = y.
 struct Taches {
-    const Tache* table;
     Tache locales[3];
-    __device__ __forceinline__ Tache operator[](uint32_t i) const { return table ? table[i] : locales[i]; }
+    ParamsMoe moe;
+    uint32_t mode;
+    __device__ __forceinline__ Tache operator[](uint32_t y) const {
+        if (mode == TACHES_LOCALES) return locales[y];
+        uint32_t i, j;
+        if (mode == TACHES_MOE_DELTA) {
+            i = y / 3u;
+            j = y - 3u * i;
+        } else if (mode == TACHES_MOE_GU) {
+            i = y >> 1;
+            j = y & 1u;
+        } else {
+            i = y;
+            j = 2u;
+        }
+        Tache t;
+        const uint32_t e = glob<uint32_t>(reinterpret_cast<const void*>(moe.indices))[i];
+        t.partie = e < moe.E ? glob<uint64_t>(reinterpret_cast<const void*>(moe.parties))[e] : 0ull;
+        t.j = j;
+        t.kmax = choisir(moe.kmax, j);
+        t.lignes = choisir(moe.lignes, j);
+        t.colonnes = choisir(moe.colonnes, j);
+        t.ech = moe.ech + uint64_t(i * 3u + j) * moe.pas;
+        t.partiels = moe.partiels + uint64_t(i * 3u + j) * moe.pas;
+        t.x = j < 2u ? moe.x : moe.act + 4ull * i * moe.colonnes[2];
+        return t;
+    }
 };
 
 constexpr uint32_t FILS_ECHELLES_FUSION = 256;  // 4 wavefronts, 8 DELTA tiles
-constexpr uint32_t FILS_GEMV_FUSION = 1024;     // 16 wavefronts, 32 CODES_CTX tiles
+constexpr uint32_t FILS_GEMV_MAX = 1024;        // up to 16 wavefronts, 32 CODES_CTX tiles
+constexpr uint32_t ECH_PAR_TUILE = 256;         // scale entries staged per tile (32 macro-steps)
+constexpr uint32_t ECH_MARGE = 256;             // entries past the last block that staging may read
+constexpr uint32_t X_LDS_MAX = 3072;            // columns of x that the CODES pass keeps in LDS
+constexpr uint32_t MED_LDS_MAX = 8192;          // rows whose medians the DELTA pass keeps in LDS
+
+// A job read by every lane (same address) made wave-uniform, so that the part reader and all the
+// job's scalars live in scalar registers.
+// (The builtin returns int: every result goes through uint32_t before any widening, otherwise an
+// address whose low word has bit 31 set would be sign-extended.)
+__device__ __forceinline__ uint32_t uniforme32(uint32_t v) { return uint32_t(__builtin_amdgcn_readfirstlane(v)); }
+__device__ __forceinline__ uint64_t uniforme64(uint64_t v) {
+    return uint64_t(uniforme32(uint32_t(v))) | (uint64_t(uniforme32(uint32_t(v >> 32))) << 32);
+}
+__device__ __forceinline__ Tache uniforme(const Tache& t) {
+    Tache u;
+    u.partie = uniforme64(t.partie);
+    u.x = uniforme64(t.x);
+    u.ech = uniforme64(t.ech);
+    u.partiels = uniforme64(t.partiels);
+    u.j = uniforme32(t.j);
+    u.kmax = uniforme32(t.kmax);
+    u.lignes = uniforme32(t.lignes);
+    u.colonnes = uniforme32(t.colonnes);
+    return u;
+}
 
 __device__ __forceinline__ uint32_t premiere_tuile(uint32_t ligne, uint32_t B, uint32_t blocs_par_tuile) {
     return (ligne * B) / blocs_par_tuile;
@@ -51,27 +123,34 @@ __device__ __forceinline__ void ecrire_global(void* p, T v) {
     *(__attribute__((address_space(1))) T*)(p) = v;
 }
 
-// ----------------------------------------------------------------------- DELTA -> scales only
-__device__ __forceinline__ void corps_echelles_fusion(const Tache& tc, const uint2* lut, uint8_t* med_lds,
-                                                      uint8_t* anneaux, uint32_t* __restrict__ controle) {
-    const uint8_t* partie = reinterpret_cast<const uint8_t*>(tc.partie);
-    const uint32_t R = tc.lignes, C = tc.colonnes, B = C / 32u, nblocs = R * B;
+// Context class of a block from its DELTA symbol (decodeur.cuh:185-192, rans.rs:481-486).
+__device__ __forceinline__ uint32_t classe_delta(uint32_t d) { return d < 128u ? 0u : (d == 128u ? 1u : 2u); }
+
+// ----------------------------------------------------------------------------- DELTA pass
+struct PrepEchelles {
     DescFlux fd, fm;
     EnteteRans h;
-    const bool bon = (C % 32u == 0) && B > 0 && R > 0 && trouver_flux(partie, SORTE_DELTA, tc.j, fd) &&
-                     trouver_flux(partie, SORTE_MEDIANES, tc.j, fm) && fm.produits == R && fm.longueur >= R &&
-                     lire_entete(fd, nblocs, h);
-    if (!bon) {
-        if (threadIdx.x == 0 && blockIdx.x == 0) atomicAdd(&controle[CTL_FORMAT], 1u);
-        return;
-    }
-    const uint8_t* med = fm.p;
-    if (R <= 8192u) {
-        for (uint32_t i = threadIdx.x; i < R; i += blockDim.x) med_lds[i] = glob<uint8_t>(fm.p)[i];
-        med = med_lds;
-    }
-    __syncthreads();
-    uint8_t* ech = reinterpret_cast<uint8_t*>(tc.ech);
+    bool bon;
+};
+
+__device__ __forceinline__ PrepEchelles preparer_echelles(const Tache& tc) {
+    PrepEchelles p;
+    const uint8_t* partie = reinterpret_cast<const uint8_t*>(tc.partie);
+    const uint32_t R = tc.lignes, C = tc.colonnes, B = C / 32u;
+    p.bon = (C % 32u == 0) && B > 0 && R > 0 && trouver_flux(partie, SORTE_DELTA, tc.j, p.fd) &&
+            trouver_flux(partie, SORTE_MEDIANES, tc.j, p.fm) && p.fm.produits == R && p.fm.longueur >= R &&
+            lire_entete(p.fd, R * B, p.h);
+    return p;
+}
+
+// DELTA tiles -> ech[b] = e | kappa << 8 with e = (med[row] + delta - 128) mod 256.
+__device__ __forceinline__ void corps_echelles_fusion(const Tache& tc, const PrepEchelles& p, const uint2* lut,
+                                                      const uint8_t* med_lds, uint8_t* anneaux,
+                                                      uint32_t* __restrict__ controle) {
+    const EnteteRans& h = p.h;
+    const uint32_t R = tc.lignes, B = tc.colonnes / 32u, nblocs = R * B;
+    const uint8_t* med = R <= MED_LDS_MAX ? med_lds : p.fm.p;
+    uint16_t* ech = reinterpret_cast<uint16_t*>(tc.ech);
     const uint32_t lane = __lane_id();
     const uint32_t v = lane & 31u;
     const bool haut = lane >= 32u;
@@ -90,7 +169,7 @@ __device__ __forceinline__ void corps_echelles_fusion(const Tache& tc, const uin
         const uint32_t nb = haut ? nb_b : nb_a;
         uint32_t x = tuile ? h.etats[t * VOIES + v] : L;
         const uint32_t debut = tuile ? h.debut[t] : 0u;
-        Anneau a = ouvrir_anneau(h, fd, debut, lds, anneaux, v, tuile);
+        Anneau a = ouvrir_anneau(h, p.fd, debut, lds, anneaux, v, tuile);
         const uint32_t o0 = a.o2;
         uint32_t b0 = 4u * ((tuile ? t : t0) * h.N * VOIES + v);
         uint32_t ligne = b0 / B, reste = b0 - ligne * B;
@@ -103,7 +182,7 @@ __device__ __forceinline__ void corps_echelles_fusion(const Tache& tc, const uin
                 mot |= (pas_anneau<TOUS>(x, a, lut, anneaux, decal, masque_inf, actif) >> 24) << (8u * k);
             avancer_anneau(a, anneaux, v, actif);
             if (actif) {
-                uint32_t sortie = 0;
+                uint32_t sortie[4];
 #pragma unroll
                 for (uint32_t k = 0; k < 4; ++k) {
                     uint32_t rk = ligne, qk = reste + k;
@@ -111,14 +190,15 @@ __device__ __forceinline__ void corps_echelles_fusion(const Tache& tc, const uin
                         qk -= B;
                         ++rk;
                     }
+                    const uint32_t d = (mot >> (8u * k)) & 255u;
                     const uint32_t mk = rk < R ? uint32_t(med[rk]) : 0u;
-                    sortie |= ((mk + ((mot >> (8u * k)) & 255u) - 128u) & 255u) << (8u * k);
+                    sortie[k] = ((mk + d - 128u) & 255u) | (classe_delta(d) << 8);
                 }
                 if (b0 + 3u < nblocs) {
-                    ecrire_global<uint32_t>(ech + b0, sortie);
+                    ecrire_global<u32x2>(ech + b0, u32x2{sortie[0] | (sortie[1] << 16), sortie[2] | (sortie[3] << 16)});
                 } else {
                     for (uint32_t k = 0; k < 4; ++k)
-                        if (b0 + k < nblocs) ecrire_global<uint8_t>(ech + b0 + k, uint8_t(sortie >> (8u * k)));
+                        if (b0 + k < nblocs) ecrire_global<uint16_t>(ech + b0 + k, uint16_t(sortie[k]));
                 }
             }
             b0 += 4u * VOIES;
@@ -141,27 +221,37 @@ __device__ __forceinline__ void corps_echelles_fusion(const Tache& tc, const uin
     verser_controle(controle, hors_l, pointeur);
 }
 
-// ------------------------------------------------------------ CODES_CTX -> partial sums of W x
-__device__ __forceinline__ void corps_gemv_fusion(const Tache& tc, const uint2* lut, uint8_t* anneaux,
-                                                  uint32_t* __restrict__ controle) {
-    const uint8_t* partie = reinterpret_cast<const uint8_t*>(tc.partie);
-    const uint32_t R = tc.lignes, C = tc.colonnes, B = C / 32u, nblocs = R * B;
-    DescFlux fc, fm;
+// ------------------------------------------------------------------------- CODES_CTX pass
+struct PrepGemv {
+    DescFlux fc;
     EnteteRans h;
-    bool bon = (C % 32u == 0) && B >= 8u && R > 0 && trouver_flux(partie, SORTE_CODES_CTX, tc.j, fc) &&
-               trouver_flux(partie, SORTE_MEDIANES, tc.j, fm) && fm.produits == R && fm.longueur >= R &&
-               lire_entete(fc, nblocs * 16u, h);
-    if (bon && (B - 1u) / (8u * h.N) + 2u > tc.kmax) bon = false;  // not enough partial slots
-    if (!bon) {
-        if (threadIdx.x == 0 && blockIdx.x == 0) atomicAdd(&controle[CTL_FORMAT], 1u);
-        return;
-    }
-    const gptr<uint8_t> med = glob<uint8_t>(fm.p);
-    const gptr<uint8_t> ech = glob<uint8_t>(reinterpret_cast<const void*>(tc.ech));
-    const gptr<f32x4> x4 = glob<f32x4>(reinterpret_cast<const void*>(tc.x));
+    bool bon;
+};
+
+__device__ __forceinline__ PrepGemv preparer_gemv(const Tache& tc) {
+    PrepGemv p;
+    const uint8_t* partie = reinterpret_cast<const uint8_t*>(tc.partie);
+    const uint32_t R = tc.lignes, C = tc.colonnes, B = C / 32u;
+    p.bon = (C % 32u == 0) && B >= 8u && R > 0 && trouver_flux(partie, SORTE_CODES_CTX, tc.j, p.fc) &&
+            lire_entete(p.fc, R * B * 16u, p.h);
+    if (p.bon && (B - 1u) / (8u * p.h.N) + 2u > tc.kmax) p.bon = false;  // not enough partial slots
+    return p;
+}
+
+// CODES_CTX tiles -> partial sums of W x. X_LDS: x staged in LDS (xs) by the caller, otherwise read
+// from device memory. ech_lds: ECH_PAR_TUILE entries per half-wavefront of the block.
+template <bool X_LDS>
+__device__ __forceinline__ void corps_gemv_fusion(const Tache& tc, const PrepGemv& p, const uint2* lut,
+                                                  uint8_t* anneaux, uint16_t* ech_lds, const f32x4* xs,
+                                                  uint32_t* __restrict__ controle) {
+    const EnteteRans& h = p.h;
+    const uint32_t R = tc.lignes, C = tc.colonnes, B = C / 32u, nblocs = R * B;
+    const gptr<u32x4> ech16 = glob<u32x4>(reinterpret_cast<const void*>(tc.ech));
+    const gptr<f32x4> xg = glob<f32x4>(reinterpret_cast<const void*>(tc.x));
     float* __restrict__ partiels = reinterpret_cast<float*>(tc.partiels);
     const uint32_t kmax = tc.kmax;
     const uint32_t bpt = 8u * h.N;  // blocks per tile
+    (void)C;
 
     const uint32_t lane = __lane_id();
     const uint32_t v = lane & 31u;
@@ -171,7 +261,9 @@ __device__ __forceinline__ void corps_gemv_fusion(const Tache& tc, const uint2* 
     const uint32_t vagues_bloc = blockDim.x >> 6;
     const uint32_t vague = blockIdx.x * vagues_bloc + (threadIdx.x >> 6);
     const uint32_t n_vagues = gridDim.x * vagues_bloc;
-    const uint32_t lds = ((threadIdx.x >> 5) & (2u * vagues_bloc - 1u)) * OCTETS_ANNEAU;
+    const uint32_t demi = (threadIdx.x >> 5) & (2u * vagues_bloc - 1u);
+    const uint32_t lds = demi * OCTETS_ANNEAU;
+    uint16_t* mes_ech = ech_lds + demi * ECH_PAR_TUILE;
     const uint32_t nmacro = h.P / 128u;
     uint32_t hors_l = 0, pointeur = 0;
     for (uint32_t t0 = 2u * vague; t0 < h.T; t0 += 2u * n_vagues) {
@@ -180,26 +272,44 @@ __device__ __forceinline__ void corps_gemv_fusion(const Tache& tc, const uint2* 
         const uint32_t nb_a = min(h.N, nmacro - t0 * h.N);
         const uint32_t nb_b = (t0 + 1u < h.T) ? min(h.N, nmacro - (t0 + 1u) * h.N) : 0u;
         const uint32_t nb = haut ? nb_b : nb_a;
+        const uint32_t m0 = (tuile ? t : t0) * h.N;
+        // entries of macro-steps m .. m+31 of the tile: blocks 8(m0+m) .. +255, 8 per lane (the
+        // workspace holds ECH_MARGE entries past the last block, so the load stays inside it)
+        auto stager = [&](uint32_t m) {
+            const u32x4 d = ech16[m0 + m + v];
+            *reinterpret_cast<u32x4*>(mes_ech + 8u * v) = d;
+        };
         uint32_t x = tuile ? h.etats[t * VOIES + v] : L;
         const uint32_t debut = tuile ? h.debut[t] : 0u;
-        Anneau a = ouvrir_anneau(h, fc, debut, lds, anneaux, v, tuile);
+        if (tuile) stager(0);
+        Anneau a = ouvrir_anneau(h, p.fc, debut, lds, anneaux, v, tuile);
         const uint32_t o0 = a.o2;
-        const uint32_t m0 = (tuile ? t : t0) * h.N;
         uint32_t bloc = m0 * 8u + q;
         uint32_t ligne = bloc / B, b = bloc - ligne * B;
         uint32_t rho = (m0 * 8u) / B, base_b = m0 * 8u - rho * B;  // row of the tile's first block
         bool valide = tuile && bloc < nblocs;
-        uint32_t e_suiv = valide ? uint32_t(ech[bloc]) : 0u;
-        uint32_t m_suiv = valide ? uint32_t(med[ligne]) : 0u;
+        uint32_t ec_suiv = tuile ? uint32_t(mes_ech[q]) : 0u;
         float acc_a = 0.0f, acc_b = 0.0f;
         auto macro = [&](auto tous, uint32_t m) {
             constexpr bool TOUS = decltype(tous)::value;
             const bool actif = TOUS || m < nb;
             const bool bloc_ok = valide;
-            const uint32_t e_cur = e_suiv;
-            const uint32_t ctx = bloc_ok ? classe_echelle(e_suiv, m_suiv) : 0u;
+            const uint32_t ec = ec_suiv;
+            const uint32_t ctx = bloc_ok ? (ec >> 8) : 0u;
             const uint32_t b_cur = b;
             const bool ligne_a = ligne == rho;
+            f32x4 xa, xb;
+            if (X_LDS) {
+                xa = xs[8u * b_cur + q4];
+                xb = xs[8u * b_cur + 4u + q4];
+            } else {
+                xa = f32x4{0.f, 0.f, 0.f, 0.f};
+                xb = xa;
+                if (bloc_ok) {
+                    xa = xg[8u * b_cur + q4];
+                    xb = xg[8u * b_cur + 4u + q4];
+                }
+            }
             bloc += 8u;
             b += 8u;
             if (b >= B) {  // B >= 8: at most one row per macro-step
@@ -207,15 +317,8 @@ __device__ __forceinline__ void corps_gemv_fusion(const Tache& tc, const uint2* 
                 ++ligne;
             }
             valide = (m + 1u < nb) && bloc < nblocs;
-            if (valide) {
-                e_suiv = ech[bloc];
-                m_suiv = med[ligne];
-            }
-            f32x4 xa = {0.f, 0.f, 0.f, 0.f}, xb = xa;
-            if (bloc_ok) {
-                xa = x4[8u * b_cur + q4];
-                xb = x4[8u * b_cur + 4u + q4];
-            }
+            if (((m + 1u) & 31u) == 0u && m + 1u < nb) stager(m + 1u);
+            ec_suiv = mes_ech[(8u * (m + 1u) + q) & (ECH_PAR_TUILE - 1u)];
             const uint2* lt = lut + ctx * M;
             const uint32_t e0 = pas_anneau<TOUS>(x, a, lt, anneaux, decal, masque_inf, actif);
             const uint32_t e1 = pas_anneau<TOUS>(x, a, lt, anneaux, decal, masque_inf, actif);
@@ -237,7 +340,7 @@ __device__ __forceinline__ void corps_gemv_fusion(const Tache& tc, const uint2* 
                 d = fmaf(w2.y, xb.z, d);
                 d = fmaf(w3.x, xa.w, d);
                 d = fmaf(w3.y, xb.w, d);
-                const float c = d * echelle_e8m0(e_cur);
+                const float c = d * echelle_e8m0(ec & 255u);
                 if (ligne_a)
                     acc_a += c;
                 else

@@ -11,6 +11,7 @@
 
 #include "commun.hpp"
 #include "erreurs.hpp"
+#include "selection.hpp"
 
 namespace trc {
 
@@ -375,67 +376,26 @@ gemv_f32(const float* __restrict__ W, const float* __restrict__ x, const float* 
     }
 }
 
-namespace trc {
-__device__ __forceinline__ bool meilleur(float va, uint32_t ia, float vb, uint32_t ib) {
-    return va > vb || (va == vb && ia < ib);
-}
-}  // namespace trc
-
 // Top-k of E logits by (value desc, index asc); weights = softmax of the k in f64 (m = first,
 // exp, ordered sum, division), rounded to f32. One wavefront: 64 lanes x 4 values (E <= 256).
 extern "C" __global__ void __launch_bounds__(64)
 routeur_topk(const float* __restrict__ logits, uint32_t E, uint32_t k, uint32_t* __restrict__ indices,
              float* __restrict__ poids, uint32_t* boite, uint32_t sequence) {
     using namespace trc;
-    const uint32_t voie = threadIdx.x;
-    if (E == 0 || E > 256u || k == 0 || k > 8u || k > E) return;
-    float v[4];
-    bool pris[4];
+    if (E == 0 || E > EXPERTS_MAX || k == 0 || k > TOPK_MAX || k > E) return;
+    uint32_t choisi[TOPK_MAX];
+    float w[TOPK_MAX];
+    topk_vague(logits, E, k, choisi, w);
+    if (threadIdx.x != 0) return;
 #pragma unroll
-    for (uint32_t i = 0; i < 4; ++i) {
-        const uint32_t e = voie + 64u * i;
-        v[i] = e < E ? logits[e] : -INFINITY;
-        pris[i] = e >= E;
-    }
-    float choisi_v[8];
-    uint32_t choisi_i[8];
-    for (uint32_t r = 0; r < k; ++r) {
-        float bv = -INFINITY;
-        uint32_t bi = 0xFFFFFFFFu;
-#pragma unroll
-        for (uint32_t i = 0; i < 4; ++i)
-            if (!pris[i] && meilleur(v[i], voie + 64u * i, bv, bi)) {
-                bv = v[i];
-                bi = voie + 64u * i;
+    for (uint32_t r = 0; r < TOPK_MAX; ++r) {
+        if (r < k) {
+            indices[r] = choisi[r];
+            poids[r] = w[r];
+            if (boite != nullptr) {
+                reinterpret_cast<volatile uint32_t*>(boite)[1 + r] = choisi[r];
+                reinterpret_cast<volatile uint32_t*>(boite)[1 + k + r] = __float_as_uint(w[r]);
             }
-#pragma unroll
-        for (int d = 32; d > 0; d >>= 1) {
-            const float ov = __shfl_xor(bv, d);
-            const uint32_t oi = __shfl_xor(bi, d);
-            if (meilleur(ov, oi, bv, bi)) {
-                bv = ov;
-                bi = oi;
-            }
-        }
-        if (bi != 0xFFFFFFFFu && (bi & 63u) == voie) pris[bi >> 6] = true;
-        choisi_v[r] = bv;
-        choisi_i[r] = bi;
-    }
-    if (voie != 0) return;
-    double e[8];
-    const double m = choisi_v[0];
-    double z = 0.0;
-    for (uint32_t r = 0; r < k; ++r) {
-        e[r] = exp(double(choisi_v[r]) - m);
-        z += e[r];
-    }
-    for (uint32_t r = 0; r < k; ++r) {
-        const float w = float(e[r] / z);
-        indices[r] = choisi_i[r];
-        poids[r] = w;
-        if (boite != nullptr) {
-            reinterpret_cast<volatile uint32_t*>(boite)[1 + r] = choisi_i[r];
-            reinterpret_cast<volatile uint32_t*>(boite)[1 + k + r] = __float_as_uint(w);
         }
     }
     if (boite != nullptr) {
@@ -502,6 +462,7 @@ extern "C" int trc_decoder_expert_grilles(trc_vue partie, trc_vue emplacement, t
     const uint64_t te = trc_taille_emplacement(dims);
     TRC_VERIFIER(partie.adresse != 0 && partie.octets >= 64, "partie de %llu o (en-tete de 64 o au moins)",
                  (unsigned long long)partie.octets);
+    TRC_VERIFIER(partie.adresse % 16 == 0, "partie non alignee sur 16");
     TRC_VERIFIER(emplacement.octets >= te, "emplacement de %llu o, %llu o demandes",
                  (unsigned long long)emplacement.octets, (unsigned long long)te);
     TRC_VERIFIER(emplacement.adresse != 0 && emplacement.adresse % 256 == 0, "emplacement non aligne sur 256");
@@ -542,6 +503,7 @@ extern "C" int trc_copier_brut(trc_vue partie, trc_vue emplacement, const trc_di
     int r = verifier_dims(dims);
     if (r != TRC_OK) return r;
     TRC_VERIFIER(partie.adresse != 0 && partie.octets >= 64, "partie trop courte");
+    TRC_VERIFIER(partie.adresse % 16 == 0, "partie non alignee sur 16");
     TRC_VERIFIER(emplacement.adresse != 0 && emplacement.octets >= trc_taille_emplacement(dims),
                  "emplacement trop court");
     TRC_VERIFIER(emplacement.adresse % 256 == 0, "emplacement non aligne sur 256");

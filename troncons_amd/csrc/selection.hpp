@@ -1,0 +1,79 @@
+// selection.hpp — the router's top-k with softmax weights, as one wavefront's device function
+// (shared by the reference-API kernel routeur_topk and the fused MoE layer).
+//
+// Order and arithmetic of the reference (passe.cuh:455-514): experts ranked by (logit desc, index
+// asc); weights = softmax of the k chosen logits in f64 (m = the first, exp, sum in rank order,
+// division), each rounded once to f32.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace trc {
+
+constexpr uint32_t TOPK_MAX = 8;
+constexpr uint32_t EXPERTS_MAX = 256;
+
+__device__ __forceinline__ bool meilleur(float va, uint32_t ia, float vb, uint32_t ib) {
+    return va > vb || (va == vb && ia < ib);
+}
+
+// Executed by one whole wavefront (64 lanes, uniform E <= 256 and 1 <= k <= 8); every lane gets
+// the same indices and weights.
+__device__ __forceinline__ void topk_vague(const float* logits, uint32_t E, uint32_t k, uint32_t (&indice)[TOPK_MAX],
+                                           float (&poids)[TOPK_MAX]) {
+    const uint32_t voie = __lane_id();
+    float v[4];
+    bool pris[4];
+#pragma unroll
+    for (uint32_t i = 0; i < 4; ++i) {
+        const uint32_t e = voie + 64u * i;
+        v[i] = e < E ? logits[e] : -INFINITY;
+        pris[i] = e >= E;
+    }
+    float choisi[TOPK_MAX];
+#pragma unroll
+    for (uint32_t r = 0; r < TOPK_MAX; ++r) {
+        choisi[r] = -INFINITY;
+        indice[r] = 0xFFFFFFFFu;
+        if (r < k) {
+            float bv = -INFINITY;
+            uint32_t bi = 0xFFFFFFFFu;
+#pragma unroll
+            for (uint32_t i = 0; i < 4; ++i)
+                if (!pris[i] && meilleur(v[i], voie + 64u * i, bv, bi)) {
+                    bv = v[i];
+                    bi = voie + 64u * i;
+                }
+#pragma unroll
+            for (int d = 32; d > 0; d >>= 1) {
+                const float ov = __shfl_xor(bv, d);
+                const uint32_t oi = __shfl_xor(bi, d);
+                if (meilleur(ov, oi, bv, bi)) {
+                    bv = ov;
+                    bi = oi;
+                }
+            }
+#pragma unroll
+            for (uint32_t i = 0; i < 4; ++i)
+                if (bi == voie + 64u * i) pris[i] = true;
+            choisi[r] = bv;
+            indice[r] = bi;
+        }
+    }
+    double e[TOPK_MAX];
+    const double m = choisi[0];
+    double z = 0.0;
+#pragma unroll
+    for (uint32_t r = 0; r < TOPK_MAX; ++r) {
+        e[r] = 0.0;
+        if (r < k) {
+            e[r] = exp(double(choisi[r]) - m);
+            z += e[r];
+        }
+    }
+#pragma unroll
+    for (uint32_t r = 0; r < TOPK_MAX; ++r) poids[r] = r < k ? float(e[r] / z) : 0.0f;
+}
+
+}  // namespace trc
