@@ -92,8 +92,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--experts", type=int, default=128)
     ap.add_argument("--k", type=int, default=4)
-    ap.add_argument("--n-codes", type=int, default=32, help="macro-steps per CODES_CTX tile written by the encoder")
-    ap.add_argument("--n-delta", type=int, default=16, help="macro-steps per DELTA tile written by the encoder")
+    ap.add_argument("--n-codes", type=int, default=16, help="macro-steps per CODES_CTX tile written by the encoder")
+    ap.add_argument("--n-delta", type=int, default=4, help="macro-steps per DELTA tile written by the encoder")
     ap.add_argument("--graine", type=int, default=2026)
     ap.add_argument("--tokens", type=int, default=1000)
     ap.add_argument("--sans-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -153,7 +153,12 @@ def main():
     fz = fusion.Fusion()
     flux = torch.cuda.current_stream()
     V = VueCarte.de
-    vt, vl, vr, vres, vctl = V(table), V(luts), V(r16), V(residu), V(ctl)
+    # mount the resident layer once: every part parsed into the device directory of stream locations
+    rep = torch.zeros(fusion.taille_repertoire(E), dtype=torch.uint8, device=dev)
+    fz.monter_couche(V(table), E, dims, V(rep), V(ctl), f=flux)
+    torch.cuda.synchronize()
+    assert (ctl.cpu().numpy() == 0).all(), f"mount control words {ctl.cpu().numpy()}"
+    vt, vl, vr, vres, vctl = V(rep), V(luts), V(r16), V(residu), V(ctl)
     vx = [V(xs, 4 * C * t, 4 * C) for t in range(args.tokens)]
     vi = [V(sel_i, 32 * s, 32) for s in range(n_sel)]
     vw = [V(sel_w, 32 * s, 32) for s in range(n_sel)]
@@ -178,7 +183,9 @@ def main():
     us_tok = ms * 1e3 / args.steps
     gbps = octets_tok.sum() / (ms * 1e-3) / 1e9
 
-    # chronogram pass (separate from the timed region: events between kernels add gaps)
+    # chronogram pass over the same steps: every kernel of the layer launched with start/stop events
+    # that the runtime records at the kernel's own start and end (hipExtLaunchKernel); kept out of
+    # the timed region so that `value` carries no timing machinery at all
     n_chrono = min(args.steps, 200)
     fusion.chrono(True)
     fusion.chrono_recolter(True)
@@ -199,7 +206,8 @@ def main():
         "achieved": round(float(atteint), 1), "peak": PIC_HBM, "unit": "GB/s",
         "frac": round(float(atteint / PIC_HBM), 4), "traffic": None,
         "bytes_per_launch": {"gate_up": int(octets_gu), "down": int(octets_bas)},
-        "avg_launch_us": {"gate_up": round(gu_ms / gu_n * 1e3, 2), "down": round(bas_ms / bas_n * 1e3, 2)},
+        "avg_launch_us": {"gate_up": round(gu_ms / gu_n * 1e3, 2), "down": round(bas_ms / bas_n * 1e3, 2),
+                          "both": round(duree_us / 2, 2)},
     }
     chrono_us = {nom: round(v[0] / v[1] * 1e3, 2) for nom, v in noyaux.items()}
 

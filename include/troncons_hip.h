@@ -164,14 +164,25 @@ uint64_t trc_taille_travail_expert_fusionne(const trc_dims_expert* dims, uint32_
 int trc_expert_fusionne(trc_vue partie, trc_vue luts, const trc_dims_expert* dims, trc_vue x, trc_vue sortie,
                         trc_vue controle, trc_vue travail, uint32_t n_delta, uint32_t n_codes, void* flux);
 
+/* Bytes of a layer directory for `experts` experts (3 entries of 128 bytes per expert). */
+uint64_t trc_taille_repertoire(uint32_t experts);
+/* Mounts a resident layer (no reference counterpart: the reference re-reads each part's header at
+ * every decode, commun.cuh:101-165): parses the level-0 part of each expert once (parties:
+ * u64[experts] device addresses of 16-byte aligned parts) into a device directory of stream
+ * locations and checked headers, so that per-token launches do not walk the parts. A part that
+ * fails a check counts one format error here and one more at each use. The parts must stay where
+ * they are while the directory is used. */
+int trc_monter_couche(trc_vue parties, uint32_t experts, const trc_dims_expert* dims, trc_vue repertoire,
+                      trc_vue controle, void* flux);
+
 /* Workspace bytes of trc_couche_moe_fusionnee. */
 uint64_t trc_taille_travail_couche_moe(const trc_dims_expert* dims, uint32_t experts, uint32_t k, uint32_t n_codes);
 /* One MoE layer step at batch 1 (Modele::debut_couche's router, gemv_f32 + routeur_topk, then
  * Modele::fin_couche): logits = routeur x (+ routeur_biais) with a bf16 experts x C router, top-k
  * and softmax weights (written to indices / poids), the k fused experts, and
- * residu[i] += ((w0 s0[i] + w1 s1[i]) + ...). parties: u64[experts] device addresses of the
- * experts' level-0 parts; the selection never leaves the device. */
-int trc_couche_moe_fusionnee(trc_vue parties, uint32_t experts, trc_vue luts, const trc_dims_expert* dims,
+ * residu[i] += ((w0 s0[i] + w1 s1[i]) + ...). repertoire: the layer's directory
+ * (trc_monter_couche); the selection never leaves the device. */
+int trc_couche_moe_fusionnee(trc_vue repertoire, uint32_t experts, trc_vue luts, const trc_dims_expert* dims,
                              trc_vue routeur, trc_vue routeur_biais, trc_vue x, uint32_t k, trc_vue residu,
                              trc_vue indices, trc_vue poids, trc_vue controle, trc_vue travail, uint32_t n_delta,
                              uint32_t n_codes, void* flux);

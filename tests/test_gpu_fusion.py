@@ -173,6 +173,9 @@ def test_fused_moe_layer_config3(fz):
     luts = O.luts_couche([[freqs[j][t] for t in range(4)] for j in range(3)])
     parts = [dev(couche.partie(e)) for e in range(E)]
     table = dev(np.array([p.data_ptr() for p in parts], np.uint64))
+    rep, ctl0 = zeros(fusion.taille_repertoire(E)), zeros(16)
+    fz.monter_couche(vue(table), E, GPT, vue(rep), vue(ctl0))
+    assert list(hote(ctl0, np.uint32)) == [0, 0, 0, 0]
     routeur = np.stack([O.synth_normale_bf16(2028, 3, e, 2880, 0.02) for e in range(E)])
     r16 = (routeur.view(np.uint32) >> 16).astype(np.uint16)
     x = O.synth_normale_bf16(2028, 4, 0, 2880, 1.0)
@@ -180,7 +183,7 @@ def test_fused_moe_layer_config3(fz):
     l, rd, xd, res = dev(luts), dev(r16), dev(x), dev(residu0)
     idx, w, ctl = zeros(32), zeros(32), zeros(16)
     tr = zeros(fusion.taille_travail_couche(GPT, E, k, N[1]))
-    fz.couche_moe(vue(table), E, vue(l), GPT, vue(rd), None, vue(xd), k, vue(res), vue(idx), vue(w), vue(ctl),
+    fz.couche_moe(vue(rep), E, vue(l), GPT, vue(rd), None, vue(xd), k, vue(res), vue(idx), vue(w), vue(ctl),
                   vue(tr), *N)
     got = hote(res, np.float32)
     assert list(hote(ctl, np.uint32)) == [0, 0, 0, 0]
@@ -207,7 +210,7 @@ def test_fused_moe_layer_config3(fz):
 def test_fused_moe_layer_guards(fz):
     """A control buffer whose arrival word is not zero means the selection does not run: the layer
     then works from whatever the index buffer holds, and indices >= experts must only count format
-    errors (no part is read), leave the residual alone and leave controle[3] non-zero."""
+    errors (no directory entry is read), leave the residual alone and leave controle[3] non-zero."""
     E, k, N = 6, 4, (8, 8)
     dims = DimsExpert.de([256, 256, 256], [256, 256, 256])
     couche = codeur.CoucheSynthetique(77, 0, E, dims, N_delta=N[0], N_codes=N[1])
@@ -215,6 +218,9 @@ def test_fused_moe_layer_guards(fz):
     luts = O.luts_couche([[freqs[j][t] for t in range(4)] for j in range(3)])
     parts = [dev(couche.partie(e)) for e in range(E)]
     table = dev(np.array([p.data_ptr() for p in parts], np.uint64))
+    rep, ctl0 = zeros(fusion.taille_repertoire(E)), zeros(16)
+    fz.monter_couche(vue(table), E, dims, vue(rep), vue(ctl0))
+    assert list(hote(ctl0, np.uint32)) == [0, 0, 0, 0]
     r16 = (np.stack([O.synth_normale_bf16(77, 3, e, 256, 0.02) for e in range(E)]).view(np.uint32) >> 16)
     x = O.synth_normale_bf16(77, 4, 0, 256, 1.0)
     residu0 = np.full(256, 0.5, np.float32)
@@ -223,10 +229,33 @@ def test_fused_moe_layer_guards(fz):
     w = zeros(32)
     ctl = dev(np.array([0, 0, 0, 5], np.uint32))
     tr = zeros(fusion.taille_travail_couche(dims, E, k, N[1]))
-    fz.couche_moe(vue(table), E, vue(l), dims, vue(rd), None, vue(xd), k, vue(res), vue(idx), vue(w), vue(ctl),
+    fz.couche_moe(vue(rep), E, vue(l), dims, vue(rd), None, vue(xd), k, vue(res), vue(idx), vue(w), vue(ctl),
                   vue(tr), *N)
     c = hote(ctl, np.uint32)
     assert c[1] > 0 and c[3] != 0
     assert list(hote(idx, np.uint32)[:4]) == [999, 7, 6, 1000]
     assert (hote(res, np.float32) == residu0).all()
+    couche.liberer()
+
+
+def test_mount_counts_bad_parts(fz):
+    """The layer mount checks every part once: a broken magic and a flipped header byte are format
+    errors, the good parts are mounted, and a layer step through a bad entry counts errors again."""
+    E, N = 3, (8, 8)
+    dims = DimsExpert.de([256, 256, 256], [256, 256, 256])
+    couche = codeur.CoucheSynthetique(78, 0, E, dims, N_delta=N[0], N_codes=N[1])
+    p0 = couche.partie(0).copy()
+    p1 = couche.partie(1).copy()
+    p1[0] ^= 0xFF                           # magic
+    p2 = couche.partie(2).copy()
+    e = 64 + 16 * 3                          # stream descriptor 3 (CODES_CTX of matrix 0): offset not 16-aligned
+    p2[e + 4] ^= 0x04
+    parts = [dev(p0), dev(p1), dev(p2)]
+    table = dev(np.array([p.data_ptr() for p in parts], np.uint64))
+    rep, ctl = zeros(fusion.taille_repertoire(E)), zeros(16)
+    fz.monter_couche(vue(table), E, dims, vue(rep), vue(ctl))
+    c = hote(ctl, np.uint32)
+    assert c[0] == 0 and c[2] == 0 and c[1] == 3 + 1   # 3 matrices of part 1, matrix 0 of part 2
+    bon = hote(rep, np.uint32).reshape(E * 3, 32)[:, 24]
+    assert list(bon) == [1, 1, 1, 0, 0, 0, 0, 1, 1]
     couche.liberer()

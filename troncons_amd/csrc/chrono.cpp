@@ -1,8 +1,10 @@
 // chrono.cpp — per-kernel GPU timing of the fused entry points, off by default. The role of the
 // reference's chronogram (trc-ordo records GPU event timestamps around each copy and decode,
 // moteur/crates/trc-ordo/src/lib.rs:205-222): when enabled, every kernel launched by a fused entry
-// point is bracketed by two HIP events on its own stream; trc_chrono_recolter() waits for them and
-// returns the summed milliseconds and launch count per kernel name.
+// point goes through hipExtLaunchKernel with a start and a stop event, which the runtime records
+// at the kernel's own start and end (the execution time a kernel trace reports, without the
+// dispatch gaps around it); trc_chrono_recolter() waits for them and returns the summed
+// milliseconds and launch count per kernel name.
 #include <hip/hip_runtime.h>
 
 #include <cstring>
@@ -50,23 +52,24 @@ hipEvent_t prendre(Chrono& c) {
 
 bool chrono_actif() { return chrono().actif; }
 
-void* chrono_debut(hipStream_t f) {
+bool chrono_paire(hipEvent_t* debut, hipEvent_t* fin) {
     Chrono& c = chrono();
     std::lock_guard<std::mutex> g(c.m);
-    if (!c.actif) return nullptr;
-    hipEvent_t e = prendre(c);
-    if (e) hipEventRecord(e, f);
-    return e;
+    if (!c.actif) return false;
+    *debut = prendre(c);
+    *fin = prendre(c);
+    if (*debut == nullptr || *fin == nullptr) {
+        if (*debut) c.libres.push_back(*debut);
+        if (*fin) c.libres.push_back(*fin);
+        return false;
+    }
+    return true;
 }
 
-void chrono_fin(void* jeton, const char* nom, hipStream_t f) {
-    if (jeton == nullptr) return;
+void chrono_classer(hipEvent_t debut, hipEvent_t fin, const char* nom) {
     Chrono& c = chrono();
     std::lock_guard<std::mutex> g(c.m);
-    hipEvent_t e = prendre(c);
-    if (e == nullptr) return;
-    hipEventRecord(e, f);
-    c.en_cours.push_back({nom, reinterpret_cast<hipEvent_t>(jeton), e});
+    c.en_cours.push_back({nom, debut, fin});
 }
 
 }  // namespace trc

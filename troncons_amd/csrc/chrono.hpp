@@ -1,24 +1,29 @@
-// chrono.hpp — optional per-kernel event timing of the fused entry points (see chrono.cpp).
+// chrono.hpp — optional per-kernel timing of the fused entry points (see chrono.cpp).
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 namespace trc {
 bool chrono_actif();
-// Records a start event on f if timing is on; returns a token (nullptr when off).
-void* chrono_debut(hipStream_t f);
-// Records the end event and files the pair under `nom` (a string literal).
-void chrono_fin(void* jeton, const char* nom, hipStream_t f);
+// Two events from the pool when timing is on (false when off).
+bool chrono_paire(hipEvent_t* debut, hipEvent_t* fin);
+// Files a recorded pair under `nom` (a string literal).
+void chrono_classer(hipEvent_t debut, hipEvent_t fin, const char* nom);
 }  // namespace trc
 
-// Launches a kernel on stream f, bracketed by chronogram events when timing is on, and returns
-// from the enclosing function on a launch error.
+// Launches a kernel on stream f — through hipExtLaunchKernel with start/stop events when timing is
+// on — and returns from the enclosing function on a launch error.
 #define TRC_LANCER_N(nom, noyau, grille, bloc, f, ...)                                    \
     do {                                                                                  \
-        void* jeton_ = ::trc::chrono_debut(f);                                            \
-        hipLaunchKernelGGL(noyau, grille, bloc, 0, f, __VA_ARGS__);                       \
+        hipEvent_t d_ = nullptr, e_ = nullptr;                                            \
+        const bool c_ = ::trc::chrono_paire(&d_, &e_);                                    \
+        if (c_)                                                                           \
+            hipExtLaunchKernelGGL(noyau, grille, bloc, 0, f, d_, e_, 0, __VA_ARGS__);     \
+        else                                                                              \
+            hipLaunchKernelGGL(noyau, grille, bloc, 0, f, __VA_ARGS__);                   \
         const int r_ = ::trc::apres_lancement(#noyau);                                    \
-        ::trc::chrono_fin(jeton_, nom, f);                                                \
+        if (c_) ::trc::chrono_classer(d_, e_, nom);                                       \
         if (r_ != TRC_OK) return r_;                                                      \
     } while (0)
 #define TRC_LANCER(noyau, grille, bloc, f, ...) TRC_LANCER_N(#noyau, noyau, grille, bloc, f, __VA_ARGS__)

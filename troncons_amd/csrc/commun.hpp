@@ -115,6 +115,40 @@ __device__ inline bool trouver_flux(const uint8_t* partie, uint8_t sorte, uint32
     return true;
 }
 
+// Finds streams (sortes[i], matrice) for i < n (n <= 4) in one pass over the descriptors: same
+// acceptance as trouver_flux for each (first matching descriptor); false unless all are present.
+// Whole wavefront, uniform arguments.
+__device__ inline bool trouver_flux_n(const uint8_t* partie, const uint8_t (&sortes)[4], uint32_t n, uint32_t matrice,
+                                      DescFlux (&f)[4]) {
+    if (partie == nullptr || (reinterpret_cast<uintptr_t>(partie) & 15u) != 0) return false;
+    const u32x4 en = *glob<u32x4>(partie);
+    const uint32_t n_flux = en.z >> 16, utiles = en.w;
+    if (en.x != MAGIE_PARTIE0 || (en.z & 0xFFu) != 0) return false;
+    if (n_flux > 64 || 64u + 16u * n_flux > utiles) return false;
+    const uint32_t lane = __lane_id();
+    u32x4 d = {0u, 0u, 0u, 0u};
+    if (lane < n_flux) d = *glob<u32x4>(partie + 64 + 16 * lane);
+    bool tous = true;
+#pragma unroll
+    for (uint32_t s = 0; s < 4; ++s) {
+        if (s >= n) break;
+        const bool ok = lane < n_flux && (d.x & 0xFFu) == sortes[s] && ((d.x >> 8) & 0xFFu) == matrice;
+        const uint64_t vote = __builtin_amdgcn_ballot_w64(ok);
+        if (vote == 0) {
+            tous = false;
+            continue;
+        }
+        const uint32_t i = uint32_t(__builtin_ctzll(vote));
+        const uint32_t dec = uint32_t(__builtin_amdgcn_readlane(d.y, i));
+        const uint32_t lon = uint32_t(__builtin_amdgcn_readlane(d.z, i));
+        if ((dec & 15u) != 0 || uint64_t(dec) + lon > utiles) tous = false;
+        f[s].p = partie + dec;
+        f[s].longueur = lon;
+        f[s].produits = uint32_t(__builtin_amdgcn_readlane(d.w, i));
+    }
+    return tous;
+}
+
 // A validated rANS stream header (geometry 1).
 struct EnteteRans {
     uint32_t P, N, T, W;
@@ -144,6 +178,19 @@ __device__ inline bool lire_entete(const DescFlux& f, uint32_t besoin, EnteteRan
     h.etats = reinterpret_cast<const uint32_t*>(f.p + 16 + 4ull * h.T);
     h.mots = reinterpret_cast<const uint16_t*>(f.p + 16 + 132ull * h.T);
     return true;
+}
+
+// The header of an already validated stream from its fields.
+__device__ __forceinline__ EnteteRans entete_de(const DescFlux& f, uint32_t P, uint32_t N, uint32_t T, uint32_t W) {
+    EnteteRans h;
+    h.P = P;
+    h.N = N;
+    h.T = T;
+    h.W = W;
+    h.debut = reinterpret_cast<const uint32_t*>(f.p + 16);
+    h.etats = reinterpret_cast<const uint32_t*>(f.p + 16 + 4ull * T);
+    h.mots = reinterpret_cast<const uint16_t*>(f.p + 16 + 132ull * T);
+    return h;
 }
 
 // Scale class kappa of a block from its scale e and its row median (delta = e - med + 128 mod 256).

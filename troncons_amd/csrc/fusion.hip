@@ -98,19 +98,15 @@ struct Fin {
 
 // Whole wavefront (uniform job).
 __device__ __forceinline__ Fin preparer_fin(const Tache& tc) {
-    Fin f;
-    const uint8_t* partie = reinterpret_cast<const uint8_t*>(tc.partie);
+    const MatricePartie m = obtenir_matrice(tc);
     const uint32_t B = tc.colonnes / 32u;
-    DescFlux fc, fb;
-    EnteteRans h;
-    f.bon = trouver_flux(partie, SORTE_CODES_CTX, tc.j, fc) && trouver_flux(partie, SORTE_BIAIS, tc.j, fb) &&
-            fb.longueur >= 4u * tc.lignes && lire_entete(fc, tc.lignes * B * 16u, h) && B >= 8u &&
-            (B - 1u) / (8u * h.N) + 2u <= tc.kmax;
-    f.biais = f.bon ? reinterpret_cast<const float*>(fb.p) : nullptr;
+    Fin f;
+    f.bon = m.bon != 0 && B >= 8u && (B - 1u) / (8u * m.cN) + 2u <= tc.kmax;
+    f.biais = f.bon ? reinterpret_cast<const float*>(m.biais.p) : nullptr;
     f.partiels = reinterpret_cast<const float*>(tc.partiels);
     f.kmax = tc.kmax;
     f.B = B;
-    f.bpt = f.bon ? 8u * h.N : 1u;
+    f.bpt = f.bon ? 8u * m.cN : 1u;
     f.lignes = tc.lignes;
     return f;
 }
@@ -264,6 +260,23 @@ fusion_selection(const uint16_t* __restrict__ W, const float* __restrict__ x, co
     }
 }
 
+// ---------------------------------------------------------------------------------- layer mount
+// Directory of a resident layer: for expert e (block x) and matrix j (block y), one wavefront walks
+// the part once and writes its MatricePartie to repertoire[e*3 + j]; a part that fails a check gets
+// bon = 0 there and one format error in controle (every later use of it counts one more).
+extern "C" __global__ void __launch_bounds__(64)
+fusion_monter(const uint64_t* __restrict__ parties, trc_dims_expert dims, trc::MatricePartie* __restrict__ repertoire,
+              uint32_t* __restrict__ controle) {
+    using namespace trc;
+    const uint32_t e = blockIdx.x, j = blockIdx.y;
+    const uint8_t* partie = reinterpret_cast<const uint8_t*>(uniforme64(parties[e]));
+    const MatricePartie m = analyser_matrice(partie, j, choisir(dims.lignes, j), choisir(dims.colonnes, j));
+    if (threadIdx.x == 0) {
+        repertoire[uint64_t(e) * 3u + j] = m;
+        if (!m.bon) atomicAdd(&controle[CTL_FORMAT], 1u);
+    }
+}
+
 // ============================================================================ C-ABI launch layer
 namespace {
 
@@ -297,7 +310,11 @@ uint64_t pas_tache(uint32_t R, uint32_t C, uint32_t n_codes) {
 }
 
 // Launch shape of a CODES pass over `jobs` matrices of R x C: 1024, 512 or 256 threads (32, 16 or 8
-// tiles) per block, the largest that still gives every CU of the chip a block.
+// tiles) per block, the largest that still gives every CU of the chip a block, and at most about one
+// block per CU over all jobs (a block's LDS holds the three LUTs, so one fits a CU): wavefronts then
+// loop over further tile pairs instead of new blocks paying the LUT staging and the header reads.
+constexpr uint32_t CUS = 256;
+
 struct FormeGemv {
     dim3 grille, bloc;
     bool x_lds;
@@ -307,9 +324,12 @@ FormeGemv forme_gemv(uint32_t R, uint32_t C, uint32_t N, uint32_t jobs) {
     const uint64_t octets = 16ull * R * (C / 32);
     const uint64_t T = ((octets + 127) / 128 + N - 1) / N;
     uint32_t fils = trc::FILS_GEMV_MAX;
-    while (fils > 256 && ((T + fils / 32 - 1) / (fils / 32)) * jobs < 256) fils /= 2;
+    while (fils > 256 && ((T + fils / 32 - 1) / (fils / 32)) * jobs < CUS) fils /= 2;
+    uint32_t gx = grille_tuiles(octets, N, fils / 32);
+    const uint32_t plafond = (CUS + jobs - 1) / jobs;
+    if (gx > plafond) gx = plafond;
     FormeGemv f;
-    f.grille = dim3(grille_tuiles(octets, N, fils / 32), jobs);
+    f.grille = dim3(gx, jobs);
     f.bloc = dim3(fils);
     f.x_lds = C <= trc::X_LDS_MAX;
     return f;
@@ -373,7 +393,7 @@ extern "C" int trc_gemv_fusionnee(trc_vue partie, uint32_t j, trc_vue luts, uint
     TRC_VERIFIER(travail.adresse && travail.octets >= besoin && travail.adresse % 256 == 0,
                  "travail de %llu o, %llu o demandes (aligne sur 256)", (unsigned long long)travail.octets,
                  (unsigned long long)besoin);
-    Tache t;
+    Tache t{};
     t.partie = partie.adresse;
     t.x = x.adresse;
     t.ech = travail.adresse;
@@ -428,7 +448,7 @@ extern "C" int trc_expert_fusionne(trc_vue partie, trc_vue luts, const trc_dims_
     const uint64_t pas = pas_tache(Rm, Cm, n_codes);
     const uint64_t base = travail.adresse;
     const uint64_t act = base + 3 * pas;
-    Tache t[3];
+    Tache t[3] = {};
     for (uint32_t j = 0; j < 3; ++j) {
         t[j].partie = partie.adresse;
         t[j].j = j;
@@ -454,6 +474,30 @@ extern "C" int trc_expert_fusionne(trc_vue partie, trc_vue luts, const trc_dims_
     return TRC_OK;
 }
 
+extern "C" uint64_t trc_taille_repertoire(uint32_t experts) {
+    return uint64_t(experts) * 3u * sizeof(trc::MatricePartie);
+}
+
+// Mounts a resident layer: parses the level-0 part of each of `experts` experts (u64[experts]
+// device addresses, 16-byte aligned) once into the directory that trc_couche_moe_fusionnee reads.
+extern "C" int trc_monter_couche(trc_vue parties, uint32_t experts, const trc_dims_expert* dims, trc_vue repertoire,
+                                 trc_vue controle, void* flux) {
+    if (dims == nullptr) return usage("dims absent");
+    int r = trc_dims_verifier(dims);
+    if (r != TRC_OK) return r;
+    TRC_VERIFIER(experts > 0 && experts <= trc::EXPERTS_MAX, "%u experts", experts);
+    TRC_VERIFIER(parties.adresse && parties.octets >= 8ull * experts && parties.adresse % 8 == 0,
+                 "table des parties trop courte");
+    TRC_VERIFIER(repertoire.adresse && repertoire.octets >= trc_taille_repertoire(experts) &&
+                     repertoire.adresse % 16 == 0,
+                 "repertoire trop court ou non aligne sur 16");
+    TRC_VERIFIER(controle.adresse && controle.octets >= 16, "controle de moins de 16 o");
+    TRC_LANCER(fusion_monter, dim3(experts, 3), dim3(64), flux_de(flux),
+               reinterpret_cast<const uint64_t*>(parties.adresse), *dims,
+               reinterpret_cast<trc::MatricePartie*>(repertoire.adresse), reinterpret_cast<uint32_t*>(controle.adresse));
+    return TRC_OK;
+}
+
 extern "C" uint64_t trc_taille_travail_couche_moe(const trc_dims_expert* dims, uint32_t experts, uint32_t k,
                                                   uint32_t n_codes) {
     if (verifier_forme(dims, n_codes) != TRC_OK || k == 0 || k > trc::TOPK_MAX || experts == 0) return 0;
@@ -465,12 +509,13 @@ extern "C" uint64_t trc_taille_travail_couche_moe(const trc_dims_expert* dims, u
 
 // Config 3: one MoE layer decode step at batch 1. logits = W_r x (+ b_r) (W_r bf16, experts x C),
 // top-k with softmax weights (indices/poids written out), then for the k selected experts the fused
-// MLP, and residu[i] += ((w0 s0[i] + w1 s1[i]) + ...) in expert order. parties: u64[experts] device
-// addresses of the experts' level-0 parts; luts: the layer's u32[3][4][4096]. No host sync: the
-// selection flows from the router to the expert kernels through device memory, and every kernel
-// derives its jobs from the top-k indices (checked against `experts` before any part is read).
+// MLP, and residu[i] += ((w0 s0[i] + w1 s1[i]) + ...) in expert order. repertoire: the layer's
+// directory (trc_monter_couche; the parts it points into stay resident); luts: the layer's
+// u32[3][4][4096]. No host sync: the selection flows from the router to the expert kernels through
+// device memory, and every kernel derives its jobs from the top-k indices (checked against
+// `experts` before the directory is read).
 // Six launches: selection, DELTA, gate/up, finish + SwiGLU, down, finish + combine.
-extern "C" int trc_couche_moe_fusionnee(trc_vue parties, uint32_t experts, trc_vue luts, const trc_dims_expert* dims,
+extern "C" int trc_couche_moe_fusionnee(trc_vue repertoire, uint32_t experts, trc_vue luts, const trc_dims_expert* dims,
                                         trc_vue routeur, trc_vue routeur_biais, trc_vue x, uint32_t k,
                                         trc_vue residu, trc_vue indices, trc_vue poids, trc_vue controle,
                                         trc_vue travail, uint32_t n_delta, uint32_t n_codes, void* flux) {
@@ -483,8 +528,9 @@ extern "C" int trc_couche_moe_fusionnee(trc_vue parties, uint32_t experts, trc_v
     TRC_VERIFIER(experts > 0 && experts <= trc::EXPERTS_MAX && k > 0 && k <= trc::TOPK_MAX && k <= experts,
                  "top-%u sur %u", k, experts);
     TRC_VERIFIER(n_delta > 0 && n_delta <= 65535, "N de DELTA %u", n_delta);
-    TRC_VERIFIER(parties.adresse && parties.octets >= 8ull * experts && parties.adresse % 8 == 0,
-                 "table des parties trop courte");
+    TRC_VERIFIER(repertoire.adresse && repertoire.octets >= trc_taille_repertoire(experts) &&
+                     repertoire.adresse % 16 == 0,
+                 "repertoire trop court ou non aligne sur 16");
     TRC_VERIFIER(luts.adresse && luts.octets >= uint64_t(trc::LUTS_PAR_COUCHE) * 4, "LUT trop courtes");
     TRC_VERIFIER(routeur.adresse && routeur.octets >= 2ull * experts * C && routeur.adresse % 8 == 0,
                  "routeur bf16 trop court ou non aligne sur 8");
@@ -510,7 +556,7 @@ extern "C" int trc_couche_moe_fusionnee(trc_vue parties, uint32_t experts, trc_v
 
     trc::ParamsMoe pm;
     std::memset(&pm, 0, sizeof(pm));
-    pm.parties = parties.adresse;
+    pm.repertoire = repertoire.adresse;
     pm.indices = indices.adresse;
     pm.x = x.adresse;
     pm.act = act;

@@ -19,24 +19,75 @@
 
 namespace trc {
 
-// One job of the fused path: matrix j of a level-0 part, against x (48 bytes).
+// One matrix j of a level-0 part, its four streams located and their headers checked: what every
+// fused kernel needs of a part. A mounted layer keeps one per (expert, matrix) in device memory
+// (trc_monter_couche), so that per-token kernels read 128 bytes instead of walking the part; the
+// single-part entry points build it in each block (analyser_matrice).
+struct MatricePartie {
+    DescFlux delta, codes, med, biais;
+    uint32_t dP, dN, dT, dW;  // DELTA stream header
+    uint32_t cP, cN, cT, cW;  // CODES_CTX stream header
+    uint32_t bon;             // 1: every check of the reference reader passed
+    uint32_t reserve[7];
+};
+static_assert(sizeof(MatricePartie) == 128, "MatricePartie");
+
+// Whole wavefront, uniform arguments: the checks of the reference's device reader
+// (commun.cuh:101-165, decodeur.cuh:44-70) for matrix j (R x C) of the part.
+__device__ inline MatricePartie analyser_matrice(const uint8_t* partie, uint32_t j, uint32_t R, uint32_t C) {
+    MatricePartie m;
+    m.bon = 0;
+    m.dP = m.dN = m.dT = m.dW = m.cP = m.cN = m.cT = m.cW = 0;
+    const uint32_t B = C / 32u;
+    DescFlux f[4];
+    const uint8_t sortes[4] = {SORTE_DELTA, SORTE_CODES_CTX, SORTE_MEDIANES, SORTE_BIAIS};
+    if (R == 0 || C % 32u != 0 || B == 0 || !trouver_flux_n(partie, sortes, 4, j, f)) return m;
+    m.delta = f[0];
+    m.codes = f[1];
+    m.med = f[2];
+    m.biais = f[3];
+    EnteteRans hd, hc;
+    const bool bon = lire_entete(f[0], R * B, hd) && lire_entete(f[1], R * B * 16u, hc) && f[2].produits == R &&
+                     f[2].longueur >= R && f[3].produits == 4u * R && f[3].longueur >= 4u * R;
+    if (!bon) return m;
+    m.dP = hd.P;
+    m.dN = hd.N;
+    m.dT = hd.T;
+    m.dW = hd.W;
+    m.cP = hc.P;
+    m.cN = hc.N;
+    m.cT = hc.T;
+    m.cW = hc.W;
+    m.bon = 1;
+    return m;
+}
+
+// One job of the fused path: matrix j of a level-0 part, against x (64 bytes).
 struct Tache {
-    uint64_t partie;    // level-0 part
+    uint64_t partie;    // level-0 part (read when `matrice` is 0)
+    uint64_t matrice;   // MatricePartie of a mounted layer, or 0
     uint64_t x;         // f32[colonnes], 16-byte aligned
     uint64_t ech;       // u16[lignes * colonnes/32 + 256]: e | kappa << 8 per block (workspace)
     uint64_t partiels;  // f32[lignes * kmax] partial sums (workspace)
     uint32_t j;         // matrix index in the part
     uint32_t kmax;      // partial slots per row
     uint32_t lignes, colonnes;
+    uint32_t reserve[2];
 };
-static_assert(sizeof(Tache) == 48, "Tache");
+static_assert(sizeof(Tache) == 64, "Tache");
+
+// The job's matrix: from the mounted layer (one 128-byte read) or parsed from the part.
+__device__ __forceinline__ MatricePartie obtenir_matrice(const Tache& tc) {
+    if (tc.matrice != 0) return *reinterpret_cast<const MatricePartie*>(tc.matrice);
+    return analyser_matrice(reinterpret_cast<const uint8_t*>(tc.partie), tc.j, tc.lignes, tc.colonnes);
+}
 
 // A MoE layer's jobs, derived on the device from the router's top-k: selected expert i (index
-// indices[i] < E, else its jobs get a null part and count as format errors) has matrices j = 0, 1, 2
+// indices[i] < E, else its jobs get no matrix and count as format errors) has matrices j = 0, 1, 2
 // (gate, up, down), each with its own workspace piece (i*3 + j) * pas; gate/up read x, down reads
 // the SwiGLU output act + i*R.
 struct ParamsMoe {
-    uint64_t parties;   // u64[E] part addresses (caller's table)
+    uint64_t repertoire;  // MatricePartie[E][3] of the mounted layer
     uint64_t indices;   // u32[k] written by the router's top-k
     uint64_t x;         // f32[C]
     uint64_t act;       // f32[k * R]
@@ -74,7 +125,8 @@ struct Taches {
         }
         Tache t;
         const uint32_t e = glob<uint32_t>(reinterpret_cast<const void*>(moe.indices))[i];
-        t.partie = e < moe.E ? glob<uint64_t>(reinterpret_cast<const void*>(moe.parties))[e] : 0ull;
+        t.partie = 0;
+        t.matrice = e < moe.E ? moe.repertoire + uint64_t(e * 3u + j) * sizeof(MatricePartie) : 0ull;
         t.j = j;
         t.kmax = choisir(moe.kmax, j);
         t.lignes = choisir(moe.lignes, j);
@@ -104,6 +156,7 @@ __device__ __forceinline__ uint64_t uniforme64(uint64_t v) {
 __device__ __forceinline__ Tache uniforme(const Tache& t) {
     Tache u;
     u.partie = uniforme64(t.partie);
+    u.matrice = uniforme64(t.matrice);
     u.x = uniforme64(t.x);
     u.ech = uniforme64(t.ech);
     u.partiels = uniforme64(t.partiels);
@@ -134,12 +187,12 @@ struct PrepEchelles {
 };
 
 __device__ __forceinline__ PrepEchelles preparer_echelles(const Tache& tc) {
+    const MatricePartie m = obtenir_matrice(tc);
     PrepEchelles p;
-    const uint8_t* partie = reinterpret_cast<const uint8_t*>(tc.partie);
-    const uint32_t R = tc.lignes, C = tc.colonnes, B = C / 32u;
-    p.bon = (C % 32u == 0) && B > 0 && R > 0 && trouver_flux(partie, SORTE_DELTA, tc.j, p.fd) &&
-            trouver_flux(partie, SORTE_MEDIANES, tc.j, p.fm) && p.fm.produits == R && p.fm.longueur >= R &&
-            lire_entete(p.fd, R * B, p.h);
+    p.bon = m.bon != 0 && tc.colonnes % 32u == 0 && tc.colonnes >= 32u && tc.lignes > 0;
+    p.fd = m.delta;
+    p.fm = m.med;
+    p.h = entete_de(m.delta, m.dP, m.dN, m.dT, m.dW);
     return p;
 }
 
@@ -229,12 +282,13 @@ struct PrepGemv {
 };
 
 __device__ __forceinline__ PrepGemv preparer_gemv(const Tache& tc) {
+    const MatricePartie m = obtenir_matrice(tc);
+    const uint32_t B = tc.colonnes / 32u;
     PrepGemv p;
-    const uint8_t* partie = reinterpret_cast<const uint8_t*>(tc.partie);
-    const uint32_t R = tc.lignes, C = tc.colonnes, B = C / 32u;
-    p.bon = (C % 32u == 0) && B >= 8u && R > 0 && trouver_flux(partie, SORTE_CODES_CTX, tc.j, p.fc) &&
-            lire_entete(p.fc, R * B * 16u, p.h);
-    if (p.bon && (B - 1u) / (8u * p.h.N) + 2u > tc.kmax) p.bon = false;  // not enough partial slots
+    p.bon = m.bon != 0 && tc.colonnes % 32u == 0 && B >= 8u && tc.lignes > 0 &&
+            (B - 1u) / (8u * m.cN) + 2u <= tc.kmax;  // enough partial slots per row
+    p.fc = m.codes;
+    p.h = entete_de(m.codes, m.cP, m.cN, m.cT, m.cW);
     return p;
 }
 

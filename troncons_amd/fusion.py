@@ -22,6 +22,9 @@ def _declarer(l):
     l.trc_taille_travail_couche_moe.restype = C.c_uint64
     l.trc_couche_moe_fusionnee.argtypes = [V, C.c_uint32, V, C.POINTER(DimsExpert), V, V, V, C.c_uint32, V, V, V, V,
                                            V, C.c_uint32, C.c_uint32, C.c_void_p]
+    l.trc_taille_repertoire.argtypes = [C.c_uint32]
+    l.trc_taille_repertoire.restype = C.c_uint64
+    l.trc_monter_couche.argtypes = [V, C.c_uint32, C.POINTER(DimsExpert), V, V, C.c_void_p]
     l.trc_chrono.argtypes = [C.c_int]
     l.trc_chrono_recolter.argtypes = [C.c_char_p, C.POINTER(C.c_double), C.POINTER(C.c_uint64), C.c_int, C.c_int]
     l._trc_fusion = True
@@ -63,6 +66,11 @@ def taille_travail_couche(dims: DimsExpert, experts: int, k: int, n_codes: int) 
     return _l().trc_taille_travail_couche_moe(C.byref(dims), experts, k, n_codes)
 
 
+def taille_repertoire(experts: int) -> int:
+    """Bytes of a mounted layer's directory (trc_monter_couche)."""
+    return _l().trc_taille_repertoire(experts)
+
+
 class Fusion:
     """Fused hot path; every call is asynchronous on ``f`` (torch stream, hipStream_t int, or None
     for torch's current stream)."""
@@ -80,9 +88,14 @@ class Fusion:
         _statut(self._l.trc_expert_fusionne(_vue(partie), _vue(luts), C.byref(dims), _vue(x), _vue(sortie),
                                             _vue(controle), _vue(travail), n_delta, n_codes, _flux(f)))
 
-    def couche_moe(self, parties, experts: int, luts, dims: DimsExpert, routeur, routeur_biais, x, k: int, residu,
+    def monter_couche(self, parties, experts: int, dims: DimsExpert, repertoire, controle, f=None) -> None:
+        """Parses the experts' parts (u64[experts] device addresses) once into `repertoire`."""
+        _statut(self._l.trc_monter_couche(_vue(parties), experts, C.byref(dims), _vue(repertoire), _vue(controle),
+                                          _flux(f)))
+
+    def couche_moe(self, repertoire, experts: int, luts, dims: DimsExpert, routeur, routeur_biais, x, k: int, residu,
                    indices, poids, controle, travail, n_delta: int, n_codes: int, f=None) -> None:
-        _statut(self._l.trc_couche_moe_fusionnee(_vue(parties), experts, _vue(luts), C.byref(dims), _vue(routeur),
+        _statut(self._l.trc_couche_moe_fusionnee(_vue(repertoire), experts, _vue(luts), C.byref(dims), _vue(routeur),
                                                  _vue(routeur_biais), _vue(x), k, _vue(residu), _vue(indices),
                                                  _vue(poids), _vue(controle), _vue(travail), n_delta, n_codes,
                                                  _flux(f)))
