@@ -25,6 +25,19 @@ METRIQUE = "MoE layer us/token @batch1 top-4; compressed-weight HBM GB/s (% of p
 PIC_HBM = 8000.0  # GB/s, MI355X
 
 
+def trafic_mesure():
+    """HBM bytes per fusion_gemv launch (mean of the two launches) from the committed counter
+    summary (two rocprofv3 --pmc runs, FETCH_SIZE then WRITE_SIZE, scaled by a copy kernel), or None."""
+    f = RACINE / "profiles" / "moe_config3_pmc.md"
+    try:
+        for ligne in f.read_text().splitlines():
+            if ligne.startswith("traffic_per_launch_bytes"):
+                return int(ligne.split("=")[1])
+    except (OSError, ValueError):
+        pass
+    return None
+
+
 def lire_flux(partie: bytes):
     """{(kind, matrix): (offset, length)} from a part's stream table (ARCHITECTURE.md §4.8)."""
     n = struct.unpack_from("<H", partie, 10)[0]
@@ -98,6 +111,8 @@ def main():
     ap.add_argument("--tokens", type=int, default=1000)
     ap.add_argument("--sans-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--budget-cpu", type=float, default=12.0, help="seconds of single-thread CPU baseline work")
+    ap.add_argument("--calibrer-copie", action="store_true",
+                    help="also run three plain 64 MiB device copies (counter calibration under rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for {args.gpus}); the expert-parallel "
@@ -159,6 +174,14 @@ def main():
     torch.cuda.synchronize()
     assert (ctl.cpu().numpy() == 0).all(), f"mount control words {ctl.cpu().numpy()}"
     vt, vl, vr, vres, vctl = V(rep), V(luts), V(r16), V(residu), V(ctl)
+    if args.calibrer_copie:
+        # a copy kernel of known size: FETCH_SIZE / WRITE_SIZE per dispatch should read 65536 KiB
+        src = torch.ones(16 << 20, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     vx = [V(xs, 4 * C * t, 4 * C) for t in range(args.tokens)]
     vi = [V(sel_i, 32 * s, 32) for s in range(n_sel)]
     vw = [V(sel_w, 32 * s, 32) for s in range(n_sel)]
@@ -204,7 +227,7 @@ def main():
     roofline = {
         "bound": "hbm", "kernel": "fusion_gemv (gate/up launch + down launch)",
         "achieved": round(float(atteint), 1), "peak": PIC_HBM, "unit": "GB/s",
-        "frac": round(float(atteint / PIC_HBM), 4), "traffic": None,
+        "frac": round(float(atteint / PIC_HBM), 4), "traffic": trafic_mesure(),
         "bytes_per_launch": {"gate_up": int(octets_gu), "down": int(octets_bas)},
         "avg_launch_us": {"gate_up": round(gu_ms / gu_n * 1e3, 2), "down": round(bas_ms / bas_n * 1e3, 2),
                           "both": round(duree_us / 2, 2)},
