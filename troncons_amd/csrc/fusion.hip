@@ -52,14 +52,33 @@ fusion_echelles(trc::Taches taches, const uint32_t* __restrict__ luts, uint32_t*
     corps_echelles_fusion(tc, p, lut, med, anneaux, controle);
 }
 
-template <bool X_LDS>
-__device__ __forceinline__ void noyau_gemv(const trc::Taches& taches, const uint32_t* __restrict__ luts,
-                                           uint32_t* __restrict__ controle) {
+// CODES pass, x in LDS (colonnes <= X_LDS_MAX): one 160 KiB LDS array laid out as LDS_* says.
+extern "C" __global__ void __launch_bounds__(trc::FILS_GEMV_MAX)
+fusion_gemv(trc::Taches taches, const uint32_t* __restrict__ luts, uint32_t* __restrict__ controle) {
+    using namespace trc;
+    __shared__ __attribute__((aligned(16384))) uint8_t lds[LDS_GEMV];
+    const Tache tc = uniforme(taches[blockIdx.y]);
+    etendre_luts<3>(luts + (uint64_t(min(tc.j, 2u)) * 4u + 1u) * M, reinterpret_cast<uint2*>(lds + LDS_LUT),
+                    3u * M / 4u);
+    const PrepGemv p = preparer_gemv(tc);
+    if (!p.bon || tc.colonnes > X_LDS_MAX) {
+        if (threadIdx.x == 0 && blockIdx.x == 0) atomicAdd(&controle[CTL_FORMAT], 1u);
+        return;
+    }
+    copier_vers_lds(reinterpret_cast<const uint8_t*>(tc.x), 4u * tc.colonnes, 4u * tc.colonnes, lds + LDS_X);
+    if (threadIdx.x < 8u)  // the zero slot (column block 127) that stream padding blocks read
+        *reinterpret_cast<u32x4*>(lds + LDS_X + COLONNE_NULLE * 128u + 16u * threadIdx.x) = u32x4{0u, 0u, 0u, 0u};
+    __syncthreads();
+    corps_gemv_rapide(tc, p, lds, controle);
+}
+
+// CODES pass, x read from device memory (rows of any width).
+extern "C" __global__ void __launch_bounds__(trc::FILS_GEMV_MAX)
+fusion_gemv_xg(trc::Taches taches, const uint32_t* __restrict__ luts, uint32_t* __restrict__ controle) {
     using namespace trc;
     __shared__ uint2 lut[3 * M];
     __shared__ __attribute__((aligned(16))) uint8_t anneaux[(FILS_GEMV_MAX / 32) * OCTETS_ANNEAU];
-    __shared__ __attribute__((aligned(16))) uint16_t ech[(FILS_GEMV_MAX / 32) * ECH_PAR_TUILE];
-    __shared__ f32x4 xs[X_LDS ? X_LDS_MAX / 4 : 1];
+    __shared__ __attribute__((aligned(16))) uint32_t ent[(FILS_GEMV_MAX / 32) * ENT_PAR_TUILE];
     const Tache tc = uniforme(taches[blockIdx.y]);
     etendre_luts<3>(luts + (uint64_t(min(tc.j, 2u)) * 4u + 1u) * M, lut, 3u * M / 4u);
     const PrepGemv p = preparer_gemv(tc);
@@ -67,22 +86,8 @@ __device__ __forceinline__ void noyau_gemv(const trc::Taches& taches, const uint
         if (threadIdx.x == 0 && blockIdx.x == 0) atomicAdd(&controle[CTL_FORMAT], 1u);
         return;
     }
-    if (X_LDS) copier_vers_lds(reinterpret_cast<const uint8_t*>(tc.x), 4u * tc.colonnes, 4u * tc.colonnes,
-                               reinterpret_cast<uint8_t*>(xs));
     __syncthreads();
-    corps_gemv_fusion<X_LDS>(tc, p, lut, anneaux, ech, xs, controle);
-}
-
-// x staged in LDS (colonnes <= X_LDS_MAX).
-extern "C" __global__ void __launch_bounds__(trc::FILS_GEMV_MAX)
-fusion_gemv(trc::Taches taches, const uint32_t* __restrict__ luts, uint32_t* __restrict__ controle) {
-    noyau_gemv<true>(taches, luts, controle);
-}
-
-// x read from device memory (any width).
-extern "C" __global__ void __launch_bounds__(trc::FILS_GEMV_MAX)
-fusion_gemv_xg(trc::Taches taches, const uint32_t* __restrict__ luts, uint32_t* __restrict__ controle) {
-    noyau_gemv<false>(taches, luts, controle);
+    corps_gemv_xg(tc, p, lut, anneaux, ent, controle);
 }
 
 // ---------------------------------------------------------------------------------- finishers
@@ -302,8 +307,8 @@ uint32_t grille_tuiles(uint64_t octets, uint32_t N, uint32_t tuiles_par_bloc) {
 
 constexpr uint32_t TUILES_ECHELLES = trc::FILS_ECHELLES_FUSION / 32;
 
-// Workspace of one matrix job: scale entries (u16 per block + staging margin), then partial sums.
-uint64_t octets_ech(uint32_t R, uint32_t C) { return al(2ull * (uint64_t(R) * (C / 32) + trc::ECH_MARGE)); }
+// Workspace of one matrix job: block entries (u32 per block + staging margin), then partial sums.
+uint64_t octets_ech(uint32_t R, uint32_t C) { return al(4ull * (uint64_t(R) * (C / 32) + trc::ECH_MARGE)); }
 
 uint64_t pas_tache(uint32_t R, uint32_t C, uint32_t n_codes) {
     return octets_ech(R, C) + al(4ull * R * kmax_pour(C, n_codes));

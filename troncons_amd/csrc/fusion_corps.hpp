@@ -62,12 +62,29 @@ __device__ inline MatricePartie analyser_matrice(const uint8_t* partie, uint32_t
     return m;
 }
 
+// Entry of one block (u32), written by the DELTA pass and read by the CODES pass:
+//   bits 7-13   column block b (x byte offset b * 128 in the LDS copy of x; 127 = the zero slot),
+//   bits 15-16  context kappa (LUT byte offset kappa * 32 KiB),
+//   bits 17-24  e - 128 as a signed byte (the block's scale is 2^(e-128)),
+//   bit 31      the block starts a row (b == 0).
+// Rows wider than 127 blocks keep b & 127 there (the device-memory-x variant recomputes b).
+constexpr uint32_t ENT_X = 0x3F80u;
+constexpr uint32_t ENT_CTX = 0x18000u;
+constexpr uint32_t ENT_EXP = 17u;
+constexpr uint32_t ENT_LIGNE = 0x80000000u;
+constexpr uint32_t COLONNE_NULLE = 127u;
+__host__ __device__ __forceinline__ uint32_t entree_bloc(uint32_t e, uint32_t ctx, uint32_t b, bool debut_ligne) {
+    return ((b & 127u) << 7) | (ctx << 15) | (((e - 128u) & 0xFFu) << ENT_EXP) | (debut_ligne ? ENT_LIGNE : 0u);
+}
+// Stream padding past the last block: zero x slot, scale 1, context 0.
+constexpr uint32_t ENTREE_BOURRAGE = COLONNE_NULLE << 7;
+
 // One job of the fused path: matrix j of a level-0 part, against x (64 bytes).
 struct Tache {
     uint64_t partie;    // level-0 part (read when `matrice` is 0)
     uint64_t matrice;   // MatricePartie of a mounted layer, or 0
     uint64_t x;         // f32[colonnes], 16-byte aligned
-    uint64_t ech;       // u16[lignes * colonnes/32 + 256]: e | kappa << 8 per block (workspace)
+    uint64_t ech;       // u32[lignes * colonnes/32 + ECH_MARGE] block entries (workspace)
     uint64_t partiels;  // f32[lignes * kmax] partial sums (workspace)
     uint32_t j;         // matrix index in the part
     uint32_t kmax;      // partial slots per row
@@ -140,9 +157,18 @@ struct Taches {
 
 constexpr uint32_t FILS_ECHELLES_FUSION = 256;  // 4 wavefronts, 8 DELTA tiles
 constexpr uint32_t FILS_GEMV_MAX = 1024;        // up to 16 wavefronts, 32 CODES_CTX tiles
-constexpr uint32_t ECH_PAR_TUILE = 256;         // scale entries staged per tile (32 macro-steps)
+constexpr uint32_t ENT_PAR_TUILE = 128;         // block entries staged per tile (16 macro-steps)
 constexpr uint32_t ECH_MARGE = 256;             // entries past the last block that staging may read
-constexpr uint32_t X_LDS_MAX = 3072;            // columns of x that the CODES pass keeps in LDS
+constexpr uint32_t X_LDS_MAX = 4064;            // columns of x the CODES pass keeps in LDS (127 blocks)
+
+// LDS of the CODES pass: one array aligned on 16 KiB, so that every region base keeps the alignment
+// the address arithmetic relies on (x: 16 KiB, rings: 1 KiB).
+constexpr uint32_t LDS_LUT = 0;                                  // 3 contexts x 4096 x 8 B
+constexpr uint32_t LDS_X = 3u * 4096u * 8u;                      // x (f32) + the zero slot: 16 KiB
+constexpr uint32_t LDS_ANNEAUX = LDS_X + 16384u;                 // 32 rings x 1 KiB
+constexpr uint32_t LDS_ENT = LDS_ANNEAUX + 32u * OCTETS_ANNEAU;  // 32 tiles x 128 entries x 4 B
+constexpr uint32_t LDS_GEMV = LDS_ENT + 32u * ENT_PAR_TUILE * 4u;
+static_assert(LDS_GEMV == 160u * 1024u, "the CODES pass uses all 160 KiB of a CU's LDS");
 constexpr uint32_t MED_LDS_MAX = 8192;          // rows whose medians the DELTA pass keeps in LDS
 
 // A job read by every lane (same address) made wave-uniform, so that the part reader and all the
@@ -196,14 +222,15 @@ __device__ __forceinline__ PrepEchelles preparer_echelles(const Tache& tc) {
     return p;
 }
 
-// DELTA tiles -> ech[b] = e | kappa << 8 with e = (med[row] + delta - 128) mod 256.
+// DELTA tiles -> one entry per block (entree_bloc) with e = (med[row] + delta - 128) mod 256 and
+// kappa = the class of delta; blocks past the matrix (stream padding) get the padding entry.
 __device__ __forceinline__ void corps_echelles_fusion(const Tache& tc, const PrepEchelles& p, const uint2* lut,
                                                       const uint8_t* med_lds, uint8_t* anneaux,
                                                       uint32_t* __restrict__ controle) {
     const EnteteRans& h = p.h;
     const uint32_t R = tc.lignes, B = tc.colonnes / 32u, nblocs = R * B;
     const uint8_t* med = R <= MED_LDS_MAX ? med_lds : p.fm.p;
-    uint16_t* ech = reinterpret_cast<uint16_t*>(tc.ech);
+    uint32_t* ech = reinterpret_cast<uint32_t*>(tc.ech);
     const uint32_t lane = __lane_id();
     const uint32_t v = lane & 31u;
     const bool haut = lane >= 32u;
@@ -235,7 +262,7 @@ __device__ __forceinline__ void corps_echelles_fusion(const Tache& tc, const Pre
                 mot |= (pas_anneau<TOUS>(x, a, lut, anneaux, decal, masque_inf, actif) >> 24) << (8u * k);
             avancer_anneau(a, anneaux, v, actif);
             if (actif) {
-                uint32_t sortie[4];
+                u32x4 sortie;
 #pragma unroll
                 for (uint32_t k = 0; k < 4; ++k) {
                     uint32_t rk = ligne, qk = reste + k;
@@ -245,14 +272,10 @@ __device__ __forceinline__ void corps_echelles_fusion(const Tache& tc, const Pre
                     }
                     const uint32_t d = (mot >> (8u * k)) & 255u;
                     const uint32_t mk = rk < R ? uint32_t(med[rk]) : 0u;
-                    sortie[k] = ((mk + d - 128u) & 255u) | (classe_delta(d) << 8);
+                    sortie[k] = b0 + k < nblocs ? entree_bloc((mk + d - 128u) & 255u, classe_delta(d), qk, qk == 0u)
+                                                : ENTREE_BOURRAGE;
                 }
-                if (b0 + 3u < nblocs) {
-                    ecrire_global<u32x2>(ech + b0, u32x2{sortie[0] | (sortie[1] << 16), sortie[2] | (sortie[3] << 16)});
-                } else {
-                    for (uint32_t k = 0; k < 4; ++k)
-                        if (b0 + k < nblocs) ecrire_global<uint16_t>(ech + b0 + k, uint16_t(sortie[k]));
-                }
+                ecrire_global<u32x4>(ech + b0, sortie);  // the workspace covers the stream's padding
             }
             b0 += 4u * VOIES;
             reste += 4u * VOIES;
@@ -292,20 +315,23 @@ __device__ __forceinline__ PrepGemv preparer_gemv(const Tache& tc) {
     return p;
 }
 
-// CODES_CTX tiles -> partial sums of W x. X_LDS: x staged in LDS (xs) by the caller, otherwise read
-// from device memory. ech_lds: ECH_PAR_TUILE entries per half-wavefront of the block.
-template <bool X_LDS>
-__device__ __forceinline__ void corps_gemv_fusion(const Tache& tc, const PrepGemv& p, const uint2* lut,
-                                                  uint8_t* anneaux, uint16_t* ech_lds, const f32x4* xs,
-                                                  uint32_t* __restrict__ controle) {
+// Row bookkeeping shared by both CODES bodies: the (row, tile) partial slot of row r for tile t.
+__device__ __forceinline__ void ecrire_partiel(float* partiels, uint32_t kmax, uint32_t r, uint32_t t, uint32_t B,
+                                               uint32_t bpt, float s) {
+    partiels[r * kmax + (t - premiere_tuile(r, B, bpt))] = s;
+}
+
+// CODES_CTX tiles -> partial sums of W x with x read from device memory (rows of any width; the
+// column of each block is tracked per lane). ent_lds: ENT_PAR_TUILE entries per half-wavefront.
+__device__ __forceinline__ void corps_gemv_xg(const Tache& tc, const PrepGemv& p, const uint2* lut, uint8_t* anneaux,
+                                              uint32_t* ent_lds, uint32_t* __restrict__ controle) {
     const EnteteRans& h = p.h;
-    const uint32_t R = tc.lignes, C = tc.colonnes, B = C / 32u, nblocs = R * B;
-    const gptr<u32x4> ech16 = glob<u32x4>(reinterpret_cast<const void*>(tc.ech));
+    const uint32_t R = tc.lignes, B = tc.colonnes / 32u, nblocs = R * B;
+    const gptr<u32x4> ent16 = glob<u32x4>(reinterpret_cast<const void*>(tc.ech));
     const gptr<f32x4> xg = glob<f32x4>(reinterpret_cast<const void*>(tc.x));
     float* __restrict__ partiels = reinterpret_cast<float*>(tc.partiels);
     const uint32_t kmax = tc.kmax;
     const uint32_t bpt = 8u * h.N;  // blocks per tile
-    (void)C;
 
     const uint32_t lane = __lane_id();
     const uint32_t v = lane & 31u;
@@ -317,7 +343,7 @@ __device__ __forceinline__ void corps_gemv_fusion(const Tache& tc, const PrepGem
     const uint32_t n_vagues = gridDim.x * vagues_bloc;
     const uint32_t demi = (threadIdx.x >> 5) & (2u * vagues_bloc - 1u);
     const uint32_t lds = demi * OCTETS_ANNEAU;
-    uint16_t* mes_ech = ech_lds + demi * ECH_PAR_TUILE;
+    uint32_t* mes_ent = ent_lds + demi * ENT_PAR_TUILE;
     const uint32_t nmacro = h.P / 128u;
     uint32_t hors_l = 0, pointeur = 0;
     for (uint32_t t0 = 2u * vague; t0 < h.T; t0 += 2u * n_vagues) {
@@ -327,12 +353,9 @@ __device__ __forceinline__ void corps_gemv_fusion(const Tache& tc, const PrepGem
         const uint32_t nb_b = (t0 + 1u < h.T) ? min(h.N, nmacro - (t0 + 1u) * h.N) : 0u;
         const uint32_t nb = haut ? nb_b : nb_a;
         const uint32_t m0 = (tuile ? t : t0) * h.N;
-        // entries of macro-steps m .. m+31 of the tile: blocks 8(m0+m) .. +255, 8 per lane (the
+        // entries of macro-steps m .. m+15 of the tile: blocks 8(m0+m) .. +127, 4 per lane (the
         // workspace holds ECH_MARGE entries past the last block, so the load stays inside it)
-        auto stager = [&](uint32_t m) {
-            const u32x4 d = ech16[m0 + m + v];
-            *reinterpret_cast<u32x4*>(mes_ech + 8u * v) = d;
-        };
+        auto stager = [&](uint32_t m) { *reinterpret_cast<u32x4*>(mes_ent + 4u * v) = ent16[2u * (m0 + m) + v]; };
         uint32_t x = tuile ? h.etats[t * VOIES + v] : L;
         const uint32_t debut = tuile ? h.debut[t] : 0u;
         if (tuile) stager(0);
@@ -342,27 +365,19 @@ __device__ __forceinline__ void corps_gemv_fusion(const Tache& tc, const PrepGem
         uint32_t ligne = bloc / B, b = bloc - ligne * B;
         uint32_t rho = (m0 * 8u) / B, base_b = m0 * 8u - rho * B;  // row of the tile's first block
         bool valide = tuile && bloc < nblocs;
-        uint32_t ec_suiv = tuile ? uint32_t(mes_ech[q]) : 0u;
+        uint32_t ent_suiv = tuile ? mes_ent[q] : 0u;
         float acc_a = 0.0f, acc_b = 0.0f;
         auto macro = [&](auto tous, uint32_t m) {
             constexpr bool TOUS = decltype(tous)::value;
             const bool actif = TOUS || m < nb;
             const bool bloc_ok = valide;
-            const uint32_t ec = ec_suiv;
-            const uint32_t ctx = bloc_ok ? (ec >> 8) : 0u;
+            const uint32_t ent = ent_suiv;
             const uint32_t b_cur = b;
             const bool ligne_a = ligne == rho;
-            f32x4 xa, xb;
-            if (X_LDS) {
-                xa = xs[8u * b_cur + q4];
-                xb = xs[8u * b_cur + 4u + q4];
-            } else {
-                xa = f32x4{0.f, 0.f, 0.f, 0.f};
-                xb = xa;
-                if (bloc_ok) {
-                    xa = xg[8u * b_cur + q4];
-                    xb = xg[8u * b_cur + 4u + q4];
-                }
+            f32x4 xa = {0.f, 0.f, 0.f, 0.f}, xb = xa;
+            if (bloc_ok) {
+                xa = xg[8u * b_cur + q4];
+                xb = xg[8u * b_cur + 4u + q4];
             }
             bloc += 8u;
             b += 8u;
@@ -371,17 +386,15 @@ __device__ __forceinline__ void corps_gemv_fusion(const Tache& tc, const PrepGem
                 ++ligne;
             }
             valide = (m + 1u < nb) && bloc < nblocs;
-            if (((m + 1u) & 31u) == 0u && m + 1u < nb) stager(m + 1u);
-            ec_suiv = mes_ech[(8u * (m + 1u) + q) & (ECH_PAR_TUILE - 1u)];
-            const uint2* lt = lut + ctx * M;
+            if (((m + 1u) & 15u) == 0u && m + 1u < nb) stager(m + 1u);
+            ent_suiv = mes_ent[(8u * (m + 1u) + q) & (ENT_PAR_TUILE - 1u)];
+            const uint2* lt = lut + (bloc_ok ? ((ent & ENT_CTX) >> 15) * M : 0u);
             const uint32_t e0 = pas_anneau<TOUS>(x, a, lt, anneaux, decal, masque_inf, actif);
             const uint32_t e1 = pas_anneau<TOUS>(x, a, lt, anneaux, decal, masque_inf, actif);
             const uint32_t e2 = pas_anneau<TOUS>(x, a, lt, anneaux, decal, masque_inf, actif);
             const uint32_t e3 = pas_anneau<TOUS>(x, a, lt, anneaux, decal, masque_inf, actif);
             avancer_anneau(a, anneaux, v, actif);
             if (actif && bloc_ok) {
-                // byte 3 of each LUT word is the decoded code byte: two E2M1 values, doubled by
-                // the 2.0 scale into the reference's k = {0,1,2,3,4,6,8,12} (exact)
                 const f32x2 w0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(e0, 2.0f, 3);
                 const f32x2 w1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(e1, 2.0f, 3);
                 const f32x2 w2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(e2, 2.0f, 3);
@@ -394,7 +407,7 @@ __device__ __forceinline__ void corps_gemv_fusion(const Tache& tc, const PrepGem
                 d = fmaf(w2.y, xb.z, d);
                 d = fmaf(w3.x, xa.w, d);
                 d = fmaf(w3.y, xb.w, d);
-                const float c = d * echelle_e8m0(ec & 255u);
+                const float c = __builtin_amdgcn_ldexpf(d, int(ent << 7) >> 24);  // d * 2^(e-128), exact
                 if (ligne_a)
                     acc_a += c;
                 else
@@ -409,7 +422,7 @@ __device__ __forceinline__ void corps_gemv_fusion(const Tache& tc, const PrepGem
             if (__builtin_amdgcn_ballot_w64(avance) != 0) {
                 const float s = somme_demi_f32(acc_a);
                 if (avance) {
-                    if (v == 0 && rho < R) partiels[rho * kmax + (t - premiere_tuile(rho, B, bpt))] = s;
+                    if (v == 0 && rho < R) ecrire_partiel(partiels, kmax, rho, t, B, bpt, s);
                     acc_a = acc_b;
                     acc_b = 0.0f;
                     ++rho;
@@ -426,10 +439,218 @@ __device__ __forceinline__ void corps_gemv_fusion(const Tache& tc, const PrepGem
             if (v == 0) {
                 const uint32_t fin = min((m0 + nb) * 8u, nblocs);
                 const uint32_t derniere = (fin - 1u) / B;
-                if (rho <= derniere && rho < R) partiels[rho * kmax + (t - premiere_tuile(rho, B, bpt))] = sa;
-                if (rho + 1u <= derniere && rho + 1u < R)
-                    partiels[(rho + 1u) * kmax + (t - premiere_tuile(rho + 1u, B, bpt))] = sb;
+                if (rho <= derniere && rho < R) ecrire_partiel(partiels, kmax, rho, t, B, bpt, sa);
+                if (rho + 1u <= derniere && rho + 1u < R) ecrire_partiel(partiels, kmax, rho + 1u, t, B, bpt, sb);
             }
+            hors_l += (x != L) ? 1u : 0u;
+            const uint32_t attendu = (t + 1 < h.T) ? h.debut[t + 1] : h.W;
+            pointeur += (v == 0 && debut + (a.o2 - o0) / 2u != attendu) ? 1u : 0u;
+        }
+    }
+    verser_controle(controle, hors_l, pointeur);
+}
+
+// ------------------------------------------------- CODES_CTX pass with x in LDS (the hot path)
+//
+// Same tiles and mapping; everything a macro-step needs besides the words comes from the block's
+// entry: the LUT base (context), the address of the two float4 of x (column), the scale and the
+// row start. Each lane keeps one accumulator for the tile's current row; a macro-step in which a
+// row starts (at most one per half: a row has >= 8 blocks) takes the slow path that closes the
+// row. Stream padding blocks read the zero slot of x, so no per-block validity test is needed.
+
+// LDS addresses (32-bit) of the single LDS array.
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
+__device__ __forceinline__ uint32_t adresse_lds(const void* p) {
+    return uint32_t(reinterpret_cast<uintptr_t>((const lds_u8*)(p)));  // address-space cast
+}
+template <typename T>
+__device__ __forceinline__ T lire_lds(uint32_t a) {
+    return *reinterpret_cast<const __attribute__((address_space(3))) T*>(uintptr_t(a));
+}
+template <typename T>
+__device__ __forceinline__ void ecrire_lds(uint32_t a, T v) {
+    *reinterpret_cast<__attribute__((address_space(3))) T*>(uintptr_t(a)) = v;
+}
+
+// A tile's word ring (as Anneau, with absolute LDS addresses; `lds` is 1 KiB aligned).
+struct AnneauR {
+    const uint8_t* g0;
+    const uint8_t* fin;
+    uint32_t lds;     // LDS address of the ring
+    uint32_t o2;      // byte offset from g0 of the next word (unwrapped)
+    uint32_t limite;  // refill when o2 > limite (= charge * 256 - FENETRE)
+    uint32_t charge;  // next chunk to request
+    uint32_t c_vol;
+    u32x2 vol;
+    bool en_vol;
+};
+
+__device__ __forceinline__ u32x2 lire_morceau_r(const AnneauR& a, uint32_t c, uint32_t v) {
+    const uint8_t* src = a.g0 + c * OCTETS_MORCEAU + v * 8u;
+    u32x2 d = {0u, 0u};
+    if (src + 8 <= a.fin) d = *glob<u32x2>(src);
+    return d;
+}
+
+__device__ __forceinline__ AnneauR ouvrir_anneau_r(const EnteteRans& h, const DescFlux& f, uint32_t debut,
+                                                   uint32_t lds, uint32_t v, bool tuile) {
+    AnneauR a;
+    const uint8_t* mot0 = reinterpret_cast<const uint8_t*>(h.mots) + 2ull * debut;
+    a.g0 = reinterpret_cast<const uint8_t*>(reinterpret_cast<uintptr_t>(mot0) & ~uintptr_t(15));
+    a.fin = f.p + f.longueur;
+    a.lds = lds;
+    a.o2 = uint32_t(mot0 - a.g0);
+    a.charge = OCTETS_ANNEAU / OCTETS_MORCEAU;
+    a.limite = a.charge * OCTETS_MORCEAU - FENETRE;
+    a.c_vol = 0;
+    a.vol = u32x2{0u, 0u};
+    a.en_vol = false;
+    if (tuile) {
+        const u32x2 d0 = lire_morceau_r(a, 0, v), d1 = lire_morceau_r(a, 1, v);
+        const u32x2 d2 = lire_morceau_r(a, 2, v), d3 = lire_morceau_r(a, 3, v);
+        ecrire_lds<u32x2>(lds + 0u * OCTETS_MORCEAU + v * 8u, d0);
+        ecrire_lds<u32x2>(lds + 1u * OCTETS_MORCEAU + v * 8u, d1);
+        ecrire_lds<u32x2>(lds + 2u * OCTETS_MORCEAU + v * 8u, d2);
+        ecrire_lds<u32x2>(lds + 3u * OCTETS_MORCEAU + v * 8u, d3);
+    }
+    return a;
+}
+
+// End of a macro-step: land the chunk requested one macro-step ago, request the next if due (the
+// same schedule as avancer_anneau).
+__device__ __forceinline__ void avancer_anneau_r(AnneauR& a, uint32_t v, bool actif) {
+    if (a.en_vol) {
+        ecrire_lds<u32x2>(a.lds + (a.c_vol & 3u) * OCTETS_MORCEAU + v * 8u, a.vol);
+        a.en_vol = false;
+    }
+    if (actif && a.o2 > a.limite) {
+        a.vol = lire_morceau_r(a, a.charge, v);
+        a.c_vol = a.charge;
+        a.charge += 1u;
+        a.limite += OCTETS_MORCEAU;
+        a.en_vol = true;
+    }
+}
+
+// One decode step: LUT entry at lut + 8 (x mod 4096) (lut: LDS address of the context's table),
+// the word of this lane at the half's pointer plus the renormalising lanes below it. Returns the
+// entry's low word (f | s << 24). The ring pointer is advanced by the caller from `compte`.
+template <bool TOUS_ACTIFS>
+__device__ __forceinline__ uint32_t pas_r(uint32_t& x, uint32_t o2, uint32_t& compte, uint32_t lut, uint32_t anneau,
+                                          uint32_t decal, uint32_t masque_inf, bool actif) {
+    const u32x2 e = lire_lds<u32x2>(lut + ((x & (M - 1u)) << 3));
+    const uint32_t y = __umul24(e.x, x >> PROBA_BITS) + e.y;
+    const bool besoin = (TOUS_ACTIFS || actif) && (y < L);
+    const uint64_t vote = __builtin_amdgcn_ballot_w64(besoin);
+    const uint32_t moitie = uint32_t(vote >> decal);
+    const uint32_t adr = ((o2 + 2u * (compte + __popc(moitie & masque_inf))) & (OCTETS_ANNEAU - 1u)) | anneau;
+    const uint32_t w = lire_lds<uint16_t>(adr);
+    const uint32_t suivant = besoin ? ((y << 16) | w) : y;
+    x = (TOUS_ACTIFS || actif) ? suivant : x;
+    compte += __popc(moitie);
+    return e.x;
+}
+
+__device__ __forceinline__ void corps_gemv_rapide(const Tache& tc, const PrepGemv& p, uint8_t* lds,
+                                                  uint32_t* __restrict__ controle) {
+    const EnteteRans& h = p.h;
+    const uint32_t R = tc.lignes, B = tc.colonnes / 32u, nblocs = R * B;
+    const gptr<u32x4> ent16 = glob<u32x4>(reinterpret_cast<const void*>(tc.ech));
+    float* __restrict__ partiels = reinterpret_cast<float*>(tc.partiels);
+    const uint32_t kmax = tc.kmax;
+    const uint32_t bpt = 8u * h.N;
+
+    const uint32_t lane = __lane_id();
+    const uint32_t v = lane & 31u;
+    const bool haut = lane >= 32u;
+    const uint32_t decal = haut ? 32u : 0u, masque_inf = (1u << v) - 1u;
+    const uint32_t q = v >> 2, q4 = v & 3u;
+    const uint32_t vagues_bloc = blockDim.x >> 6;
+    const uint32_t vague = blockIdx.x * vagues_bloc + (threadIdx.x >> 6);
+    const uint32_t n_vagues = gridDim.x * vagues_bloc;
+    const uint32_t demi = (threadIdx.x >> 5) & (2u * vagues_bloc - 1u);
+    const uint32_t base = adresse_lds(lds);
+    const uint32_t a_lut = base + LDS_LUT;
+    const uint32_t a_x = base + LDS_X + 16u * q4;          // | column offset from the entry
+    const uint32_t a_anneau = base + LDS_ANNEAUX + demi * OCTETS_ANNEAU;
+    const uint32_t a_ent = base + LDS_ENT + demi * (ENT_PAR_TUILE * 4u);
+    const uint32_t a_ent_q = a_ent + 4u * q;
+    const uint32_t nmacro = h.P / 128u;
+    uint32_t hors_l = 0, pointeur = 0;
+    for (uint32_t t0 = 2u * vague; t0 < h.T; t0 += 2u * n_vagues) {
+        const uint32_t t = t0 + (haut ? 1u : 0u);
+        const bool tuile = t < h.T;
+        const uint32_t nb_a = min(h.N, nmacro - t0 * h.N);
+        const uint32_t nb_b = (t0 + 1u < h.T) ? min(h.N, nmacro - (t0 + 1u) * h.N) : 0u;
+        const uint32_t nb = haut ? nb_b : nb_a;
+        const uint32_t m0 = (tuile ? t : t0) * h.N;
+        auto stager = [&](uint32_t m) { ecrire_lds<u32x4>(a_ent + 16u * v, ent16[2u * (m0 + m) + v]); };
+        uint32_t x = tuile ? h.etats[t * VOIES + v] : L;
+        const uint32_t debut = tuile ? h.debut[t] : 0u;
+        if (tuile) stager(0);
+        AnneauR a = ouvrir_anneau_r(h, p.fc, debut, a_anneau, v, tuile);
+        const uint32_t o0 = a.o2;
+        uint32_t rho = (m0 * 8u) / B;  // row of the tile's first block
+        uint32_t ent_suiv = tuile ? lire_lds<uint32_t>(a_ent_q) : ENTREE_BOURRAGE;
+        float acc = 0.0f;
+        auto macro = [&](auto tous, uint32_t m) {
+            constexpr bool TOUS = decltype(tous)::value;
+            const bool actif = TOUS || m < nb;
+            const uint32_t ent = actif ? ent_suiv : ENTREE_BOURRAGE;
+            const uint32_t ax = (ent & ENT_X) | a_x;
+            const f32x4 xa = lire_lds<f32x4>(ax);
+            const f32x4 xb = lire_lds<f32x4>(ax + 64u);
+            if (((m + 1u) & 15u) == 0u && m + 1u < nb) stager(m + 1u);
+            ent_suiv = lire_lds<uint32_t>(a_ent_q + 32u * ((m + 1u) & 15u));
+            const uint32_t lt = a_lut + (ent & ENT_CTX);
+            uint32_t compte = 0;
+            const uint32_t e0 = pas_r<TOUS>(x, a.o2, compte, lt, a_anneau, decal, masque_inf, actif);
+            const uint32_t e1 = pas_r<TOUS>(x, a.o2, compte, lt, a_anneau, decal, masque_inf, actif);
+            const uint32_t e2 = pas_r<TOUS>(x, a.o2, compte, lt, a_anneau, decal, masque_inf, actif);
+            const uint32_t e3 = pas_r<TOUS>(x, a.o2, compte, lt, a_anneau, decal, masque_inf, actif);
+            a.o2 += 2u * compte;  // no vote in an inactive half: its pointer stays
+            avancer_anneau_r(a, v, actif);
+            // byte 3 of each LUT word is the decoded code byte: two E2M1 values, doubled by the 2.0
+            // scale into the reference's k = {0,1,2,3,4,6,8,12} (exact)
+            const f32x2 w0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(e0, 2.0f, 3);
+            const f32x2 w1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(e1, 2.0f, 3);
+            const f32x2 w2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(e2, 2.0f, 3);
+            const f32x2 w3 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(e3, 2.0f, 3);
+            float d = w0.x * xa.x;
+            d = fmaf(w0.y, xb.x, d);
+            d = fmaf(w1.x, xa.y, d);
+            d = fmaf(w1.y, xb.y, d);
+            d = fmaf(w2.x, xa.z, d);
+            d = fmaf(w2.y, xb.z, d);
+            d = fmaf(w3.x, xa.w, d);
+            d = fmaf(w3.y, xb.w, d);
+            const float c = __builtin_amdgcn_ldexpf(d, int(ent << 7) >> 24);  // d * 2^(e-128), exact
+            // a row starts in this macro-step (not the tile's own first row at its first block)
+            const bool nouvelle = int(ent) < 0 && !(m == 0u && q == 0u && actif);
+            const uint64_t vote = __builtin_amdgcn_ballot_w64(nouvelle);
+            if (vote == 0) {
+                if (TOUS || actif) acc += c;
+            } else {
+                // the half's first lane in the new row; lanes at or after it belong to row rho + 1
+                const uint32_t moitie = uint32_t(vote >> decal);
+                const uint32_t premier = moitie != 0u ? uint32_t(__builtin_ctz(moitie)) : 32u;
+                const bool apres = v >= premier;
+                if (!apres && (TOUS || actif)) acc += c;
+                const float s = somme_demi_f32(acc);
+                if (moitie != 0u) {
+                    if (v == 0 && actif && rho < R) ecrire_partiel(partiels, kmax, rho, t, B, bpt, s);
+                    acc = apres ? c : 0.0f;
+                    ++rho;
+                }
+            }
+        };
+        const uint32_t nb_min = min(nb_a, nb_b);
+        uint32_t m = 0;
+        for (; m < nb_min; ++m) macro(std::true_type{}, m);
+        for (; m < nb_a; ++m) macro(std::false_type{}, m);
+        const float s = somme_demi_f32(acc);
+        if (tuile) {
+            if (v == 0 && rho < R) ecrire_partiel(partiels, kmax, rho, t, B, bpt, s);
             hors_l += (x != L) ? 1u : 0u;
             const uint32_t attendu = (t + 1 < h.T) ? h.debut[t + 1] : h.W;
             pointeur += (v == 0 && debut + (a.o2 - o0) / 2u != attendu) ? 1u : 0u;
