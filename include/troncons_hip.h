@@ -13,9 +13,7 @@
  *     usable device); trc_derniere_erreur() gives the message of the calling thread's last error;
  *   - launches are asynchronous on `flux` (a hipStream_t); data errors found by kernels are never
  *     returned: they are counted into the caller's zeroed u32[4] control buffer
- *     ([0] lanes not ending on L, [1] format errors, [2] tile word-pointer mismatches, [3] 0 after
- *     the call: trc_couche_moe_fusionnee counts its router blocks there and puts it back to 0, so a
- *     non-zero [3] means the buffer was not zeroed and the selection did not run);
+ *     ([0] lanes not ending on L, [1] format errors, [2] tile word-pointer mismatches, [3] 0);
  *   - level-0 parts are 16-byte aligned (the device reader loads their header and descriptors 16
  *     bytes at a time; a misaligned part is a usage error, or a format error when its address is
  *     only known on the device);

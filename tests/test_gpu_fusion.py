@@ -207,33 +207,36 @@ def test_fused_moe_layer_config3(fz):
     couche.liberer()
 
 
-def test_fused_moe_layer_guards(fz):
-    """A control buffer whose arrival word is not zero means the selection does not run: the layer
-    then works from whatever the index buffer holds, and indices >= experts must only count format
-    errors (no directory entry is read), leave the residual alone and leave controle[3] non-zero."""
+def test_fused_moe_layer_bad_parts(fz):
+    """A layer whose parts all fail the mount checks: the step counts format errors in every pass
+    that meets a bad directory entry and leaves the residual alone (nothing is combined)."""
     E, k, N = 6, 4, (8, 8)
     dims = DimsExpert.de([256, 256, 256], [256, 256, 256])
     couche = codeur.CoucheSynthetique(77, 0, E, dims, N_delta=N[0], N_codes=N[1])
     freqs = couche.freqs()
     luts = O.luts_couche([[freqs[j][t] for t in range(4)] for j in range(3)])
-    parts = [dev(couche.partie(e)) for e in range(E)]
-    table = dev(np.array([p.data_ptr() for p in parts], np.uint64))
+    mauvaises = []
+    for e in range(E):
+        p = couche.partie(e).copy()
+        p[0] ^= 0xFF  # magic
+        mauvaises.append(dev(p))
+    table = dev(np.array([p.data_ptr() for p in mauvaises], np.uint64))
     rep, ctl0 = zeros(fusion.taille_repertoire(E)), zeros(16)
     fz.monter_couche(vue(table), E, dims, vue(rep), vue(ctl0))
-    assert list(hote(ctl0, np.uint32)) == [0, 0, 0, 0]
+    assert hote(ctl0, np.uint32)[1] == 3 * E
     r16 = (np.stack([O.synth_normale_bf16(77, 3, e, 256, 0.02) for e in range(E)]).view(np.uint32) >> 16)
     x = O.synth_normale_bf16(77, 4, 0, 256, 1.0)
     residu0 = np.full(256, 0.5, np.float32)
     l, rd, xd, res = dev(luts), dev(r16.astype(np.uint16)), dev(x), dev(residu0)
-    idx = dev(np.array([999, 7, 6, 1000] + [0] * 4, np.uint32))
-    w = zeros(32)
-    ctl = dev(np.array([0, 0, 0, 5], np.uint32))
+    idx, w, ctl = zeros(32), zeros(32), zeros(16)
     tr = zeros(fusion.taille_travail_couche(dims, E, k, N[1]))
     fz.couche_moe(vue(rep), E, vue(l), dims, vue(rd), None, vue(xd), k, vue(res), vue(idx), vue(w), vue(ctl),
                   vue(tr), *N)
     c = hote(ctl, np.uint32)
-    assert c[1] > 0 and c[3] != 0
-    assert list(hote(idx, np.uint32)[:4]) == [999, 7, 6, 1000]
+    assert c[1] > 0 and c[0] == 0 and c[2] == 0 and c[3] == 0
+    logits = O.gemv_f32(np.stack([O.synth_normale_bf16(77, 3, e, 256, 0.02) for e in range(E)]), x)
+    oi, _ = O.routeur_topk(logits, k)
+    assert (hote(idx, np.uint32)[:k] == oi).all()
     assert (hote(res, np.float32) == residu0).all()
     couche.liberer()
 

@@ -30,7 +30,6 @@ constexpr uint8_t SORTE_ECHELLES_BRUTES = 0x07;
 constexpr int CTL_HORS_L = 0;
 constexpr int CTL_FORMAT = 1;
 constexpr int CTL_POINTEUR = 2;
-constexpr int CTL_ARRIVEES = 3;  // fused MoE layer only: router blocks done (back to 0 when the call ends)
 
 // Threads per block of the reference-API kernels (abi.rs:56-61 keeps these a launch detail).
 constexpr uint32_t FILS_ECHELLES = 128;  // 2 wavefronts = 4 DELTA tiles

@@ -6,10 +6,11 @@
 //   fusion_gemv      CODES_CTX tiles -> per-(row, tile) partial sums of y = W x, decoded bytes
 //                    dequantised and multiplied in registers;
 //   fusion_finir     y[r] = fixed-order sum of the row's tile partials + bias;
-//   fusion_finir_swiglu    the same for gate and up, then the gpt-oss clamped SwiGLU;
+//   fusion_finir_swiglu    the same for gate and up, then the gpt-oss clamped SwiGLU (one expert);
 //   fusion_finir_combiner  the same for the k down products, then the weighted combine;
-//   fusion_selection (MoE layer) router logits, then top-k with softmax weights; the other
-//                    kernels derive their jobs on the device from the chosen indices.
+//   fusion_routeur   (MoE layer) router logits; the DELTA pass runs the top-k, the other
+//                    kernels derive their jobs on the device from the chosen indices, and the
+//                    down pass finishes gate/up and applies the SwiGLU itself.
 //
 // Mapping: one wavefront = two rANS tiles (lanes 0-31, 32-63), each tile's words staged in an LDS
 // ring (anneau.hpp). In a macro-step, lane v of a tile produces the 4 code bytes 4(v%4) ..
@@ -32,16 +33,44 @@
 
 
 // The layer's LUTs u32[3][4][4096] (reference format) are shared by all jobs of a launch. A
-// block first parses its job's stream header, then stages the LUT (and the medians, or x) in LDS
-// with all loads of a batch in flight together.
+// block stages the LUT in LDS (all loads of a batch in flight together), reads its job's matrix,
+// then the medians. In a MoE layer (TACHES_MOE_DELTA) every block first runs the router's top-k on
+// the logits itself (wavefront 0; the result is deterministic, so all blocks agree) and block
+// (0, 0) publishes the indices and weights for the later passes: no block waits for another.
 extern "C" __global__ void __launch_bounds__(trc::FILS_ECHELLES_FUSION)
 fusion_echelles(trc::Taches taches, const uint32_t* __restrict__ luts, uint32_t* __restrict__ controle) {
     using namespace trc;
     __shared__ uint2 lut[M];
     __shared__ __attribute__((aligned(16))) uint8_t med[MED_LDS_MAX];
     __shared__ __attribute__((aligned(16))) uint8_t anneaux[(FILS_ECHELLES_FUSION / 32) * OCTETS_ANNEAU];
-    const Tache tc = uniforme(taches[blockIdx.y]);
-    etendre_luts<4>(luts + (uint64_t(min(tc.j, 2u)) * 4u + 0u) * M, lut, M / 4u);
+    __shared__ uint32_t choisis[TOPK_MAX];
+    const bool moe = taches.mode == TACHES_MOE_DELTA;
+    const uint32_t j_bloc = moe ? blockIdx.y % 3u : min(taches[blockIdx.y].j, 2u);
+    etendre_luts<4>(luts + (uint64_t(j_bloc) * 4u + 0u) * M, lut, M / 4u);
+    Tache tc;
+    if (moe) {
+        const ParamsMoe& pm = taches.moe;
+        if (threadIdx.x < 64u) {
+            uint32_t choisi[TOPK_MAX];
+            float w[TOPK_MAX];
+            topk_vague(reinterpret_cast<const float*>(pm.logits), pm.E, pm.k, choisi, w);
+            if (threadIdx.x == 0) {
+#pragma unroll
+                for (uint32_t r = 0; r < TOPK_MAX; ++r) {
+                    choisis[r] = choisi[r];
+                    if (r < pm.k && blockIdx.x == 0 && blockIdx.y == 0) {
+                        reinterpret_cast<uint32_t*>(pm.indices)[r] = choisi[r];
+                        reinterpret_cast<float*>(pm.poids)[r] = w[r];
+                    }
+                }
+            }
+        }
+        __syncthreads();
+        const uint32_t i = blockIdx.y / 3u;
+        tc = uniforme(tache_moe_e(pm, i, blockIdx.y - 3u * i, choisis[i]));
+    } else {
+        tc = uniforme(taches[blockIdx.y]);
+    }
     const PrepEchelles p = preparer_echelles(tc);
     if (!p.bon) {
         if (threadIdx.x == 0 && blockIdx.x == 0) atomicAdd(&controle[CTL_FORMAT], 1u);
@@ -52,7 +81,31 @@ fusion_echelles(trc::Taches taches, const uint32_t* __restrict__ luts, uint32_t*
     corps_echelles_fusion(tc, p, lut, med, anneaux, controle);
 }
 
+namespace trc {
+
+// residu[r] += ((w0 s0[r] + w1 s1[r]) + w2 s2[r]) + ..., s_i the finished rows of job i, each
+// product and sum rounded on its own (the reference combiner, passe.cuh:611-622).
+__device__ __forceinline__ void combiner_lignes(const Fin* fins, uint32_t k, const float* __restrict__ poids,
+                                                float* __restrict__ residu, uint32_t D, uint32_t r0, uint32_t pas) {
+#pragma clang fp contract(off)
+    for (uint32_t r = r0; r < D; r += pas) {
+        bool ok = true;
+        for (uint32_t i = 0; i < k; ++i) ok = ok && fins[i].bon && r < fins[i].lignes;
+        if (!ok) continue;
+        float s = poids[0] * somme_fin(fins[0], r);
+        for (uint32_t i = 1; i < k; ++i) {
+            const float p = poids[i] * somme_fin(fins[i], r);
+            s = s + p;
+        }
+        residu[r] = residu[r] + s;
+    }
+}
+
+}  // namespace trc
+
 // CODES pass, x in LDS (colonnes <= X_LDS_MAX): one 160 KiB LDS array laid out as LDS_* says.
+// Option (MoE down jobs): OPT_SWIGLU builds x in LDS as the SwiGLU of the expert's gate/up rows,
+// finished from their partial sums (no separate finisher launch, no act buffer).
 extern "C" __global__ void __launch_bounds__(trc::FILS_GEMV_MAX)
 fusion_gemv(trc::Taches taches, const uint32_t* __restrict__ luts, uint32_t* __restrict__ controle) {
     using namespace trc;
@@ -61,15 +114,30 @@ fusion_gemv(trc::Taches taches, const uint32_t* __restrict__ luts, uint32_t* __r
     etendre_luts<3>(luts + (uint64_t(min(tc.j, 2u)) * 4u + 1u) * M, reinterpret_cast<uint2*>(lds + LDS_LUT),
                     3u * M / 4u);
     const PrepGemv p = preparer_gemv(tc);
-    if (!p.bon || tc.colonnes > X_LDS_MAX) {
-        if (threadIdx.x == 0 && blockIdx.x == 0) atomicAdd(&controle[CTL_FORMAT], 1u);
-        return;
+    const bool bon = p.bon && tc.colonnes <= X_LDS_MAX;
+    if (!bon && threadIdx.x == 0 && blockIdx.x == 0) atomicAdd(&controle[CTL_FORMAT], 1u);
+    if (bon) {
+        if (taches.options & OPT_SWIGLU) {
+            Fin* fins = reinterpret_cast<Fin*>(lds + LDS_ENT);  // the entry area is free until the tiles start
+            const uint32_t w = threadIdx.x >> 6;
+            if (w < 2u) {
+                const Fin f = preparer_fin(uniforme(tache_moe(taches.moe, blockIdx.y, w)));
+                if (__lane_id() == 0) fins[w] = f;
+            }
+            __syncthreads();
+            const Fin g = fins[0], u = fins[1];
+            const bool ok = g.bon && u.bon;
+            float* xs = reinterpret_cast<float*>(lds + LDS_X);
+            for (uint32_t r = threadIdx.x; r < tc.colonnes; r += blockDim.x)
+                xs[r] = (ok && r < g.lignes && r < u.lignes) ? swiglu_oai_f(somme_fin(g, r), somme_fin(u, r)) : 0.0f;
+        } else {
+            copier_vers_lds(reinterpret_cast<const uint8_t*>(tc.x), 4u * tc.colonnes, 4u * tc.colonnes, lds + LDS_X);
+        }
+        if (threadIdx.x < 8u)  // the zero slot (column block 127) that stream padding blocks read
+            *reinterpret_cast<u32x4*>(lds + LDS_X + COLONNE_NULLE * 128u + 16u * threadIdx.x) = u32x4{0u, 0u, 0u, 0u};
     }
-    copier_vers_lds(reinterpret_cast<const uint8_t*>(tc.x), 4u * tc.colonnes, 4u * tc.colonnes, lds + LDS_X);
-    if (threadIdx.x < 8u)  // the zero slot (column block 127) that stream padding blocks read
-        *reinterpret_cast<u32x4*>(lds + LDS_X + COLONNE_NULLE * 128u + 16u * threadIdx.x) = u32x4{0u, 0u, 0u, 0u};
     __syncthreads();
-    corps_gemv_rapide(tc, p, lds, controle);
+    if (bon) corps_gemv_rapide(tc, p, lds, controle);
 }
 
 // CODES pass, x read from device memory (rows of any width).
@@ -91,52 +159,6 @@ fusion_gemv_xg(trc::Taches taches, const uint32_t* __restrict__ luts, uint32_t* 
 }
 
 // ---------------------------------------------------------------------------------- finishers
-namespace trc {
-
-// What a finisher needs of a job: its biases, its partial sums and the tiles of each row.
-struct Fin {
-    const float* biais;
-    const float* partiels;
-    uint32_t kmax, B, bpt, lignes;
-    uint32_t bon;
-};
-
-// Whole wavefront (uniform job).
-__device__ __forceinline__ Fin preparer_fin(const Tache& tc) {
-    const MatricePartie m = obtenir_matrice(tc);
-    const uint32_t B = tc.colonnes / 32u;
-    Fin f;
-    f.bon = m.bon != 0 && B >= 8u && (B - 1u) / (8u * m.cN) + 2u <= tc.kmax;
-    f.biais = f.bon ? reinterpret_cast<const float*>(m.biais.p) : nullptr;
-    f.partiels = reinterpret_cast<const float*>(tc.partiels);
-    f.kmax = tc.kmax;
-    f.B = B;
-    f.bpt = f.bon ? 8u * m.cN : 1u;
-    f.lignes = tc.lignes;
-    return f;
-}
-
-// y[r] = fixed-order sum of row r's tile partials + bias[r].
-__device__ __forceinline__ float somme_fin(const Fin& f, uint32_t r) {
-    const uint32_t t0 = (r * f.B) / f.bpt, t1 = (r * f.B + f.B - 1u) / f.bpt;
-    const float* p = f.partiels + uint64_t(r) * f.kmax;
-    float s = p[0];
-    for (uint32_t k = 1; k <= t1 - t0; ++k) s += p[k];
-    return s + f.biais[r];
-}
-
-// Jobs first + y*par .. of the block parsed by one wavefront each, shared through LDS.
-template <uint32_t N_MAX>
-__device__ __forceinline__ void preparer_fins(const Taches& taches, uint32_t premier, uint32_t n, Fin (&fins)[N_MAX]) {
-    const uint32_t w = threadIdx.x >> 6;
-    for (uint32_t i = w; i < n; i += blockDim.x >> 6) {
-        const Fin f = preparer_fin(uniforme(taches[premier + i]));
-        if (__lane_id() == 0) fins[i] = f;
-    }
-    __syncthreads();
-}
-
-}  // namespace trc
 
 // sorties[y * pas + r] = fixed-order sum of the partials of row r + bias[r], for job y.
 extern "C" __global__ void __launch_bounds__(256)
@@ -160,67 +182,60 @@ fusion_finir_swiglu(trc::Taches taches, float* __restrict__ act, uint32_t R) {
     preparer_fins(taches, 2u * i, 2, fins);
     const uint32_t r = blockIdx.x * 256u + threadIdx.x;
     if (!fins[0].bon || !fins[1].bon || r >= R || r >= fins[0].lignes || r >= fins[1].lignes) return;
-    const double gv = fmin(double(somme_fin(fins[0], r)), 7.0);
-    const double uv = fmin(fmax(double(somme_fin(fins[1], r)), -7.0), 7.0);
-    act[uint64_t(i) * R + r] = float(gv / (1.0 + exp(-1.702 * gv)) * (uv + 1.0));
+    act[uint64_t(i) * R + r] = swiglu_oai_f(somme_fin(fins[0], r), somme_fin(fins[1], r));
 }
 
-// residu[r] += ((w0 s0[r] + w1 s1[r]) + w2 s2[r]) + ..., s_i the finished rows of job i, each product
-// and sum rounded on its own (the reference combiner, passe.cuh:611-622).
+// residu[r] += ((w0 s0[r] + w1 s1[r]) + w2 s2[r]) + ... over the k down jobs (MoE layer).
 extern "C" __global__ void __launch_bounds__(256)
-fusion_finir_combiner(trc::Taches taches, float* __restrict__ residu, const float* __restrict__ poids, uint32_t D,
-                      uint32_t k) {
-#pragma clang fp contract(off)
+fusion_finir_combiner(trc::Taches taches) {
     using namespace trc;
     __shared__ Fin fins[TOPK_MAX];
-    preparer_fins(taches, 0, k, fins);
-    const uint32_t r = blockIdx.x * 256u + threadIdx.x;
-    for (uint32_t i = 0; i < k; ++i)
-        if (!fins[i].bon || r >= fins[i].lignes) return;
-    if (r >= D) return;
-    float s = poids[0] * somme_fin(fins[0], r);
-    for (uint32_t i = 1; i < k; ++i) {
-        const float p = poids[i] * somme_fin(fins[i], r);
-        s = s + p;
-    }
-    residu[r] = residu[r] + s;
+    const ParamsMoe& moe = taches.moe;
+    preparer_fins(taches, 0, moe.k, fins);
+    combiner_lignes(fins, moe.k, reinterpret_cast<const float*>(moe.poids), reinterpret_cast<float*>(moe.residu),
+                    moe.lignes[2], blockIdx.x * 256u + threadIdx.x, gridDim.x * 256u);
 }
 
 // ---------------------------------------------------------------------------- router + top-k
-namespace trc {
-
-// Router logits y = W x (+ b), W bf16 row-major (R x C), in the reference gemv_f32 order (bf16 ->
+// Router logits y = W x (+ b), W bf16 row-major (E x C), in the reference gemv_f32 order (bf16 ->
 // f32 is exact, so the bits equal gemv_f32 on the widened matrix, passe.cuh:104-130): one row per
-// half-wavefront, lane v taking float4 groups v, v+32, ..., its loads issued 8 groups at a time.
-__device__ __forceinline__ void routeur_ligne(const uint16_t* __restrict__ W, const float* __restrict__ x,
-                                              const float* __restrict__ biais, float* __restrict__ y, uint32_t R,
-                                              uint32_t C) {
+// half-wavefront, lane v taking float4 groups v, v+32, ...; a row's loads are all in flight while
+// the block stages x in LDS. The top-k runs at the start of the DELTA pass.
+template <bool X_LDS>
+__device__ __forceinline__ void routeur_lignes(const uint16_t* __restrict__ W, const float* __restrict__ x,
+                                               const float* __restrict__ biais, float* __restrict__ y, uint32_t R,
+                                               uint32_t C, trc::f32x4* xs) {
+    using namespace trc;
+    constexpr uint32_t LOT = 24;
     const uint32_t voie = threadIdx.x & 31u;
     const uint32_t r = blockIdx.x * (blockDim.x >> 5) + (threadIdx.x >> 5);
-    const uint32_t lig = min(r, R - 1u);
     const uint32_t C4 = C / 4u;
-    const gptr<f32x4> x4 = glob<f32x4>(x);
-    const gptr<u32x2> W4 = glob<u32x2>(W + uint64_t(lig) * C);
-    constexpr uint32_t LOT = 8;
+    const gptr<u32x2> W4 = glob<u32x2>(W + uint64_t(min(r, R - 1u)) * C);
+    const gptr<f32x4> xg = glob<f32x4>(x);
+    u32x2 w[LOT];
+#pragma unroll
+    for (uint32_t i = 0; i < LOT; ++i)
+        if (32u * i + voie < C4) w[i] = W4[32u * i + voie];
+    if (X_LDS) {
+        for (uint32_t i = threadIdx.x; i < C4; i += blockDim.x) xs[i] = xg[i];
+        __syncthreads();
+    }
     float acc = 0.0f;
     for (uint32_t c0 = 0; c0 < C4; c0 += 32u * LOT) {
-        u32x2 w[LOT];
-        f32x4 xv[LOT];
+        if (c0 > 0) {
+#pragma unroll
+            for (uint32_t i = 0; i < LOT; ++i)
+                if (c0 + 32u * i + voie < C4) w[i] = W4[c0 + 32u * i + voie];
+        }
 #pragma unroll
         for (uint32_t i = 0; i < LOT; ++i) {
             const uint32_t c = c0 + 32u * i + voie;
             if (c < C4) {
-                w[i] = W4[c];
-                xv[i] = x4[c];
-            }
-        }
-#pragma unroll
-        for (uint32_t i = 0; i < LOT; ++i) {
-            if (c0 + 32u * i + voie < C4) {
-                acc = fmaf(__uint_as_float(w[i].x << 16), xv[i].x, acc);
-                acc = fmaf(__uint_as_float(w[i].x & 0xFFFF0000u), xv[i].y, acc);
-                acc = fmaf(__uint_as_float(w[i].y << 16), xv[i].z, acc);
-                acc = fmaf(__uint_as_float(w[i].y & 0xFFFF0000u), xv[i].w, acc);
+                const f32x4 xv = X_LDS ? xs[c] : f32x4(xg[c]);
+                acc = fmaf(__uint_as_float(w[i].x << 16), xv.x, acc);
+                acc = fmaf(__uint_as_float(w[i].x & 0xFFFF0000u), xv.y, acc);
+                acc = fmaf(__uint_as_float(w[i].y << 16), xv.z, acc);
+                acc = fmaf(__uint_as_float(w[i].y & 0xFFFF0000u), xv.w, acc);
             }
         }
     }
@@ -228,41 +243,15 @@ __device__ __forceinline__ void routeur_ligne(const uint16_t* __restrict__ W, co
     if (voie == 0 && r < R) y[r] = biais != nullptr ? s + biais[r] : s;
 }
 
-}  // namespace trc
-
-// The layer's expert selection in one launch: router logits (one row per half-wavefront), then the
-// last block to finish (arrival count in controle[3], which the caller zeroes with the rest of the
-// control buffer and which that block puts back to 0) runs the reference top-k with softmax
-// weights (routeur_topk) over all logits. No block waits for another.
 extern "C" __global__ void __launch_bounds__(256)
-fusion_selection(const uint16_t* __restrict__ W, const float* __restrict__ x, const float* __restrict__ biais,
-                 float* logits, uint32_t E, uint32_t C, uint32_t k, uint32_t* __restrict__ indices,
-                 float* __restrict__ poids, uint32_t* __restrict__ controle) {
+fusion_routeur(const uint16_t* __restrict__ W, const float* __restrict__ x, const float* __restrict__ biais,
+               float* __restrict__ logits, uint32_t E, uint32_t C) {
     using namespace trc;
-    routeur_ligne(W, x, biais, logits, E, C);
-    __shared__ uint32_t dernier;
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const uint32_t n =
-            __hip_atomic_fetch_add(&controle[CTL_ARRIVEES], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-        dernier = (n == gridDim.x - 1u) ? 1u : 0u;
-    }
-    __syncthreads();
-    if (dernier == 0u || threadIdx.x >= 64u) return;
-    __threadfence();
-    uint32_t choisi[TOPK_MAX];
-    float w[TOPK_MAX];
-    topk_vague(logits, E, k, choisi, w);
-    if (threadIdx.x == 0) {
-#pragma unroll
-        for (uint32_t r = 0; r < TOPK_MAX; ++r)
-            if (r < k) {
-                indices[r] = choisi[r];
-                poids[r] = w[r];
-            }
-        __hip_atomic_store(&controle[CTL_ARRIVEES], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+    __shared__ f32x4 xs[X_LDS_MAX / 4];
+    if (C <= X_LDS_MAX)
+        routeur_lignes<true>(W, x, biais, logits, E, C, xs);
+    else
+        routeur_lignes<false>(W, x, biais, logits, E, C, xs);
 }
 
 // ---------------------------------------------------------------------------------- layer mount
@@ -366,11 +355,12 @@ Taches par_valeur(const Tache* t, uint32_t n) {
     return l;
 }
 
-Taches par_moe(const trc::ParamsMoe& pm, uint32_t mode) {
+Taches par_moe(const trc::ParamsMoe& pm, uint32_t mode, uint32_t options) {
     Taches l;
     std::memset(&l, 0, sizeof(l));
     l.moe = pm;
     l.mode = mode;
+    l.options = options;
     return l;
 }
 
@@ -509,7 +499,7 @@ extern "C" uint64_t trc_taille_travail_couche_moe(const trc_dims_expert* dims, u
     const uint32_t R = dims->lignes[0], C = dims->colonnes[0];
     const uint32_t Rm = dims->lignes[2] > R ? dims->lignes[2] : R;
     const uint32_t Cm = dims->colonnes[2] > C ? dims->colonnes[2] : C;
-    return al(4ull * experts) + 3ull * k * pas_tache(Rm, Cm, n_codes) + al(4ull * k * R);
+    return al(4ull * experts) + 3ull * k * pas_tache(Rm, Cm, n_codes);
 }
 
 // Config 3: one MoE layer decode step at batch 1. logits = W_r x (+ b_r) (W_r bf16, experts x C),
@@ -518,8 +508,10 @@ extern "C" uint64_t trc_taille_travail_couche_moe(const trc_dims_expert* dims, u
 // directory (trc_monter_couche; the parts it points into stay resident); luts: the layer's
 // u32[3][4][4096]. No host sync: the selection flows from the router to the expert kernels through
 // device memory, and every kernel derives its jobs from the top-k indices (checked against
-// `experts` before the directory is read).
-// Six launches: selection, DELTA, gate/up, finish + SwiGLU, down, finish + combine.
+// `experts` before the directory is read). Five launches: router logits; DELTA (3k matrices, each
+// block running the top-k first); gate/up CODES pass (2k); down CODES pass (k; builds its x as the
+// SwiGLU of the gate/up rows); finish + combine. No cross-block synchronisation inside a launch.
+// Rows are limited to X_LDS_MAX columns (x in LDS).
 extern "C" int trc_couche_moe_fusionnee(trc_vue repertoire, uint32_t experts, trc_vue luts, const trc_dims_expert* dims,
                                         trc_vue routeur, trc_vue routeur_biais, trc_vue x, uint32_t k,
                                         trc_vue residu, trc_vue indices, trc_vue poids, trc_vue controle,
@@ -549,6 +541,8 @@ extern "C" int trc_couche_moe_fusionnee(trc_vue repertoire, uint32_t experts, tr
     TRC_VERIFIER(travail.adresse && travail.octets >= besoin && travail.adresse % 256 == 0,
                  "travail de %llu o, %llu o demandes (aligne sur 256)", (unsigned long long)travail.octets,
                  (unsigned long long)besoin);
+    TRC_VERIFIER(C <= trc::X_LDS_MAX && R <= trc::X_LDS_MAX, "couche de %u x %u : au plus %u colonnes", R, C,
+                 trc::X_LDS_MAX);
     const uint32_t Rm = D > R ? D : R;
     const uint32_t Cm = C;
     const uint64_t pas = pas_tache(Rm, Cm, n_codes);
@@ -556,15 +550,15 @@ extern "C" int trc_couche_moe_fusionnee(trc_vue repertoire, uint32_t experts, tr
     const uint64_t logits = p;
     p += al(4ull * experts);
     const uint64_t morceaux = p;
-    p += 3ull * k * pas;
-    const uint64_t act = p;
 
     trc::ParamsMoe pm;
     std::memset(&pm, 0, sizeof(pm));
     pm.repertoire = repertoire.adresse;
+    pm.logits = logits;
     pm.indices = indices.adresse;
+    pm.poids = poids.adresse;
     pm.x = x.adresse;
-    pm.act = act;
+    pm.residu = residu.adresse;
     pm.ech = morceaux;
     pm.partiels = morceaux + octets_ech(Rm, Cm);
     pm.pas = pas;
@@ -575,21 +569,20 @@ extern "C" int trc_couche_moe_fusionnee(trc_vue repertoire, uint32_t experts, tr
         pm.colonnes[j] = dims->colonnes[j];
         pm.kmax[j] = kmax_pour(dims->colonnes[j], n_codes);
     }
-    const Taches t_delta = par_moe(pm, trc::TACHES_MOE_DELTA), t_gu = par_moe(pm, trc::TACHES_MOE_GU),
-                 t_bas = par_moe(pm, trc::TACHES_MOE_BAS);
+    const Taches t_delta = par_moe(pm, trc::TACHES_MOE_DELTA, 0), t_gu = par_moe(pm, trc::TACHES_MOE_GU, 0),
+                 t_bas = par_moe(pm, trc::TACHES_MOE_BAS, trc::OPT_SWIGLU);
     const hipStream_t f = flux_de(flux);
     auto ctl = reinterpret_cast<uint32_t*>(controle.adresse);
     const uint32_t* l = reinterpret_cast<const uint32_t*>(luts.adresse);
-    TRC_LANCER(fusion_selection, dim3((experts + 7) / 8), dim3(256), f,
+    TRC_LANCER(fusion_routeur, dim3((experts + 7) / 8), dim3(256), f,
                reinterpret_cast<const uint16_t*>(routeur.adresse), reinterpret_cast<const float*>(x.adresse),
-               reinterpret_cast<const float*>(routeur_biais.adresse), reinterpret_cast<float*>(logits), experts, C, k,
-               reinterpret_cast<uint32_t*>(indices.adresse), reinterpret_cast<float*>(poids.adresse), ctl);
+               reinterpret_cast<const float*>(routeur_biais.adresse), reinterpret_cast<float*>(logits), experts, C);
     TRC_LANCER(fusion_echelles, dim3(grille_tuiles(uint64_t(R) * (C / 32), n_delta, TUILES_ECHELLES), 3 * k),
                dim3(trc::FILS_ECHELLES_FUSION), f, t_delta, l, ctl);
-    TRC_LANCER_GEMV("fusion_gemv/gate_up", forme_gemv(R, C, n_codes, 2 * k), f, t_gu, l, ctl);
-    TRC_LANCER(fusion_finir_swiglu, dim3((R + 255) / 256, k), dim3(256), f, t_gu, reinterpret_cast<float*>(act), R);
-    TRC_LANCER_GEMV("fusion_gemv/down", forme_gemv(D, R, n_codes, k), f, t_bas, l, ctl);
-    TRC_LANCER(fusion_finir_combiner, dim3((D + 255) / 256), dim3(256), f, t_bas, reinterpret_cast<float*>(residu.adresse),
-               reinterpret_cast<const float*>(poids.adresse), D, k);
+    TRC_LANCER_N("fusion_gemv/gate_up", fusion_gemv, forme_gemv(R, C, n_codes, 2 * k).grille,
+                 forme_gemv(R, C, n_codes, 2 * k).bloc, f, t_gu, l, ctl);
+    TRC_LANCER_N("fusion_gemv/down", fusion_gemv, forme_gemv(D, R, n_codes, k).grille,
+                 forme_gemv(D, R, n_codes, k).bloc, f, t_bas, l, ctl);
+    TRC_LANCER(fusion_finir_combiner, dim3((D + 255) / 256), dim3(256), f, t_bas);
     return TRC_OK;
 }

@@ -102,15 +102,17 @@ __device__ __forceinline__ MatricePartie obtenir_matrice(const Tache& tc) {
 // A MoE layer's jobs, derived on the device from the router's top-k: selected expert i (index
 // indices[i] < E, else its jobs get no matrix and count as format errors) has matrices j = 0, 1, 2
 // (gate, up, down), each with its own workspace piece (i*3 + j) * pas; gate/up read x, down reads
-// the SwiGLU output act + i*R.
+// the SwiGLU of expert i's gate/up rows (computed by the down pass itself, see OPT_SWIGLU).
 struct ParamsMoe {
     uint64_t repertoire;  // MatricePartie[E][3] of the mounted layer
-    uint64_t indices;   // u32[k] written by the router's top-k
-    uint64_t x;         // f32[C]
-    uint64_t act;       // f32[k * R]
-    uint64_t ech;       // scale entries of piece 0
-    uint64_t partiels;  // partial sums of piece 0
-    uint64_t pas;       // workspace bytes per piece
+    uint64_t logits;      // f32[E] router logits (the DELTA pass runs the top-k on them)
+    uint64_t indices;     // u32[k] top-k indices, written by the DELTA pass
+    uint64_t poids;       // f32[k] softmax weights, written by the DELTA pass
+    uint64_t x;           // f32[C]
+    uint64_t residu;      // f32[D] the combine adds into
+    uint64_t ech;         // scale entries of piece 0
+    uint64_t partiels;    // partial sums of piece 0
+    uint64_t pas;         // workspace bytes per piece
     uint32_t lignes[3], colonnes[3], kmax[3];
     uint32_t k, E;
 };
@@ -122,11 +124,37 @@ enum ModeTaches : uint32_t {
     TACHES_MOE_BAS = 3,    // job y = (expert y, matrix 2)
 };
 
+// Option of a CODES pass over MoE down jobs: x = swiglu_oai(gate_i, up_i), finished from their
+// partial sums.
+constexpr uint32_t OPT_SWIGLU = 1u;
+
+// Job (expert i = expert e of the layer, matrix j) of a MoE layer.
+__device__ __forceinline__ Tache tache_moe_e(const ParamsMoe& moe, uint32_t i, uint32_t j, uint32_t e) {
+    Tache t;
+    t.partie = 0;
+    t.matrice = e < moe.E ? moe.repertoire + uint64_t(e * 3u + j) * sizeof(MatricePartie) : 0ull;
+    t.j = j;
+    t.kmax = choisir(moe.kmax, j);
+    t.lignes = choisir(moe.lignes, j);
+    t.colonnes = choisir(moe.colonnes, j);
+    t.ech = moe.ech + uint64_t(i * 3u + j) * moe.pas;
+    t.partiels = moe.partiels + uint64_t(i * 3u + j) * moe.pas;
+    t.x = j < 2u ? moe.x : 0ull;
+    t.reserve[0] = t.reserve[1] = 0;
+    return t;
+}
+
+// Job (expert i, matrix j), the expert read from the top-k indices in device memory.
+__device__ __forceinline__ Tache tache_moe(const ParamsMoe& moe, uint32_t i, uint32_t j) {
+    return tache_moe_e(moe, i, j, glob<uint32_t>(reinterpret_cast<const void*>(moe.indices))[i]);
+}
+
 // The jobs of a launch; job of block (x, y) = y.
 struct Taches {
     Tache locales[3];
     ParamsMoe moe;
     uint32_t mode;
+    uint32_t options;
     __device__ __forceinline__ Tache operator[](uint32_t y) const {
         if (mode == TACHES_LOCALES) return locales[y];
         uint32_t i, j;
@@ -140,22 +168,11 @@ struct Taches {
             i = y;
             j = 2u;
         }
-        Tache t;
-        const uint32_t e = glob<uint32_t>(reinterpret_cast<const void*>(moe.indices))[i];
-        t.partie = 0;
-        t.matrice = e < moe.E ? moe.repertoire + uint64_t(e * 3u + j) * sizeof(MatricePartie) : 0ull;
-        t.j = j;
-        t.kmax = choisir(moe.kmax, j);
-        t.lignes = choisir(moe.lignes, j);
-        t.colonnes = choisir(moe.colonnes, j);
-        t.ech = moe.ech + uint64_t(i * 3u + j) * moe.pas;
-        t.partiels = moe.partiels + uint64_t(i * 3u + j) * moe.pas;
-        t.x = j < 2u ? moe.x : moe.act + 4ull * i * moe.colonnes[2];
-        return t;
+        return tache_moe(moe, i, j);
     }
 };
 
-constexpr uint32_t FILS_ECHELLES_FUSION = 256;  // 4 wavefronts, 8 DELTA tiles
+constexpr uint32_t FILS_ECHELLES_FUSION = 1024;  // 16 wavefronts, 32 DELTA tiles
 constexpr uint32_t FILS_GEMV_MAX = 1024;        // up to 16 wavefronts, 32 CODES_CTX tiles
 constexpr uint32_t ENT_PAR_TUILE = 128;         // block entries staged per tile (16 macro-steps)
 constexpr uint32_t ECH_MARGE = 256;             // entries past the last block that staging may read
@@ -657,6 +674,59 @@ __device__ __forceinline__ void corps_gemv_rapide(const Tache& tc, const PrepGem
         }
     }
     verser_controle(controle, hors_l, pointeur);
+}
+
+// --------------------------------------------------------------------------- row finishing
+
+// What a finisher needs of a job: its biases, its partial sums and the tiles of each row.
+struct Fin {
+    const float* biais;
+    const float* partiels;
+    uint32_t kmax, B, bpt, lignes;
+    uint32_t bon;
+};
+
+// Whole wavefront (uniform job).
+__device__ __forceinline__ Fin preparer_fin(const Tache& tc) {
+    const MatricePartie m = obtenir_matrice(tc);
+    const uint32_t B = tc.colonnes / 32u;
+    Fin f;
+    f.bon = m.bon != 0 && B >= 8u && (B - 1u) / (8u * m.cN) + 2u <= tc.kmax;
+    f.biais = f.bon ? reinterpret_cast<const float*>(m.biais.p) : nullptr;
+    f.partiels = reinterpret_cast<const float*>(tc.partiels);
+    f.kmax = tc.kmax;
+    f.B = B;
+    f.bpt = f.bon ? 8u * m.cN : 1u;
+    f.lignes = tc.lignes;
+    return f;
+}
+
+// y[r] = fixed-order sum of row r's tile partials + bias[r].
+__device__ __forceinline__ float somme_fin(const Fin& f, uint32_t r) {
+    const uint32_t t0 = (r * f.B) / f.bpt, t1 = (r * f.B + f.B - 1u) / f.bpt;
+    const float* p = f.partiels + uint64_t(r) * f.kmax;
+    float s = p[0];
+    for (uint32_t k = 1; k <= t1 - t0; ++k) s += p[k];
+    return s + f.biais[r];
+}
+
+// Jobs first + y*par .. of the block parsed by one wavefront each, shared through LDS.
+template <uint32_t N_MAX>
+__device__ __forceinline__ void preparer_fins(const Taches& taches, uint32_t premier, uint32_t n, Fin (&fins)[N_MAX]) {
+    const uint32_t w = threadIdx.x >> 6;
+    for (uint32_t i = w; i < n; i += blockDim.x >> 6) {
+        const Fin f = preparer_fin(uniforme(taches[premier + i]));
+        if (__lane_id() == 0) fins[i] = f;
+    }
+    __syncthreads();
+}
+
+
+// gpt-oss clamped SwiGLU in f64, one rounding (the reference swiglu_oai, passe.cuh:598-605).
+__device__ __forceinline__ float swiglu_oai_f(float g, float u) {
+    const double gv = fmin(double(g), 7.0);
+    const double uv = fmin(fmax(double(u), -7.0), 7.0);
+    return float(gv / (1.0 + exp(-1.702 * gv)) * (uv + 1.0));
 }
 
 }  // namespace trc
