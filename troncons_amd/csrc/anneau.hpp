@@ -113,9 +113,10 @@ __device__ __forceinline__ uint2 entree8(uint32_t e) {
 }
 
 template <uint32_t LOT>
-__device__ __forceinline__ void etendre_luts(const uint32_t* __restrict__ src, uint2* dst, uint32_t n4) {
+__device__ __forceinline__ void etendre_luts(const uint32_t* __restrict__ src, uint2* dst, uint32_t n4,
+                                             uint32_t debut = 0) {
     const gptr<u32x4> s4 = glob<u32x4>(src);
-    for (uint32_t base = 0; base < n4; base += LOT * blockDim.x) {
+    for (uint32_t base = debut; base < n4; base += LOT * blockDim.x) {
         u32x4 t[LOT];
 #pragma unroll
         for (uint32_t k = 0; k < LOT; ++k) {
@@ -135,6 +136,35 @@ __device__ __forceinline__ void etendre_luts(const uint32_t* __restrict__ src, u
         }
     }
 }
+
+// The same in two halves, so that other loads are in flight meanwhile: demarrer() issues the first
+// batch's loads, poser() stores them and expands the rest (blocks smaller than n4 / LOT threads).
+template <uint32_t LOT>
+struct ChargeLut {
+    u32x4 t[LOT];
+    __device__ __forceinline__ void demarrer(const uint32_t* __restrict__ src, uint32_t n4) {
+        const gptr<u32x4> s4 = glob<u32x4>(src);
+#pragma unroll
+        for (uint32_t k = 0; k < LOT; ++k) {
+            const uint32_t i = k * blockDim.x + threadIdx.x;
+            if (i < n4) t[k] = s4[i];
+        }
+    }
+    __device__ __forceinline__ void poser(const uint32_t* __restrict__ src, uint2* dst, uint32_t n4) {
+#pragma unroll
+        for (uint32_t k = 0; k < LOT; ++k) {
+            const uint32_t i = k * blockDim.x + threadIdx.x;
+            if (i < n4) {
+                uint2* d = dst + 4u * i;
+                d[0] = entree8(t[k].x);
+                d[1] = entree8(t[k].y);
+                d[2] = entree8(t[k].z);
+                d[3] = entree8(t[k].w);
+            }
+        }
+        if (LOT * blockDim.x < n4) etendre_luts<LOT>(src, dst, n4, LOT * blockDim.x);
+    }
+};
 
 // Copies n bytes (n <= cap) from device memory to LDS with 16-byte loads where the source allows
 // it (src 16-byte aligned and the 16 bytes inside [src, src + lisible)), bytes otherwise.

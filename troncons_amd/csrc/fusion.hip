@@ -46,7 +46,8 @@ fusion_echelles(trc::Taches taches, const uint32_t* __restrict__ luts, uint32_t*
     __shared__ uint32_t choisis[TOPK_MAX];
     const bool moe = taches.mode == TACHES_MOE_DELTA;
     const uint32_t j_bloc = moe ? blockIdx.y % 3u : min(taches[blockIdx.y].j, 2u);
-    etendre_luts<4>(luts + (uint64_t(j_bloc) * 4u + 0u) * M, lut, M / 4u);
+    ChargeLut<1> charge_lut;
+    charge_lut.demarrer(luts + (uint64_t(j_bloc) * 4u + 0u) * M, M / 4u);
     Tache tc;
     if (moe) {
         const ParamsMoe& pm = taches.moe;
@@ -71,7 +72,11 @@ fusion_echelles(trc::Taches taches, const uint32_t* __restrict__ luts, uint32_t*
     } else {
         tc = uniforme(taches[blockIdx.y]);
     }
-    const PrepEchelles p = preparer_echelles(tc);
+    const MatricePartie m = obtenir_matrice(tc);
+    if (moe && blockIdx.x == 0 && threadIdx.x == 0)  // the later passes of the layer read this copy
+        ecrire_matrice(reinterpret_cast<void*>(taches.moe.resolus + uint64_t(blockIdx.y) * sizeof(MatricePartie)), m);
+    const PrepEchelles p = preparer_echelles(tc, m);
+    charge_lut.poser(luts + (uint64_t(j_bloc) * 4u + 0u) * M, lut, M / 4u);
     if (!p.bon) {
         if (threadIdx.x == 0 && blockIdx.x == 0) atomicAdd(&controle[CTL_FORMAT], 1u);
         return;
@@ -111,9 +116,11 @@ fusion_gemv(trc::Taches taches, const uint32_t* __restrict__ luts, uint32_t* __r
     using namespace trc;
     __shared__ __attribute__((aligned(16384))) uint8_t lds[LDS_GEMV];
     const Tache tc = uniforme(taches[blockIdx.y]);
-    etendre_luts<3>(luts + (uint64_t(min(tc.j, 2u)) * 4u + 1u) * M, reinterpret_cast<uint2*>(lds + LDS_LUT),
-                    3u * M / 4u);
-    const PrepGemv p = preparer_gemv(tc);
+    const uint32_t* lut_src = luts + (uint64_t(min(tc.j, 2u)) * 4u + 1u) * M;
+    ChargeLut<3> charge_lut;
+    charge_lut.demarrer(lut_src, 3u * M / 4u);
+    const PrepGemv p = preparer_gemv(tc, obtenir_matrice(tc));
+    charge_lut.poser(lut_src, reinterpret_cast<uint2*>(lds + LDS_LUT), 3u * M / 4u);
     const bool bon = p.bon && tc.colonnes <= X_LDS_MAX;
     if (!bon && threadIdx.x == 0 && blockIdx.x == 0) atomicAdd(&controle[CTL_FORMAT], 1u);
     if (bon) {
@@ -149,7 +156,7 @@ fusion_gemv_xg(trc::Taches taches, const uint32_t* __restrict__ luts, uint32_t* 
     __shared__ __attribute__((aligned(16))) uint32_t ent[(FILS_GEMV_MAX / 32) * ENT_PAR_TUILE];
     const Tache tc = uniforme(taches[blockIdx.y]);
     etendre_luts<3>(luts + (uint64_t(min(tc.j, 2u)) * 4u + 1u) * M, lut, 3u * M / 4u);
-    const PrepGemv p = preparer_gemv(tc);
+    const PrepGemv p = preparer_gemv(tc, obtenir_matrice(tc));
     if (!p.bon) {
         if (threadIdx.x == 0 && blockIdx.x == 0) atomicAdd(&controle[CTL_FORMAT], 1u);
         return;
@@ -266,7 +273,7 @@ fusion_monter(const uint64_t* __restrict__ parties, trc_dims_expert dims, trc::M
     const uint8_t* partie = reinterpret_cast<const uint8_t*>(uniforme64(parties[e]));
     const MatricePartie m = analyser_matrice(partie, j, choisir(dims.lignes, j), choisir(dims.colonnes, j));
     if (threadIdx.x == 0) {
-        repertoire[uint64_t(e) * 3u + j] = m;
+        ecrire_matrice(repertoire + uint64_t(e) * 3u + j, m);
         if (!m.bon) atomicAdd(&controle[CTL_FORMAT], 1u);
     }
 }
@@ -499,7 +506,7 @@ extern "C" uint64_t trc_taille_travail_couche_moe(const trc_dims_expert* dims, u
     const uint32_t R = dims->lignes[0], C = dims->colonnes[0];
     const uint32_t Rm = dims->lignes[2] > R ? dims->lignes[2] : R;
     const uint32_t Cm = dims->colonnes[2] > C ? dims->colonnes[2] : C;
-    return al(4ull * experts) + 3ull * k * pas_tache(Rm, Cm, n_codes);
+    return al(4ull * experts) + al(3ull * k * sizeof(trc::MatricePartie)) + 3ull * k * pas_tache(Rm, Cm, n_codes);
 }
 
 // Config 3: one MoE layer decode step at batch 1. logits = W_r x (+ b_r) (W_r bf16, experts x C),
@@ -549,11 +556,14 @@ extern "C" int trc_couche_moe_fusionnee(trc_vue repertoire, uint32_t experts, tr
     uint64_t p = travail.adresse;
     const uint64_t logits = p;
     p += al(4ull * experts);
+    const uint64_t resolus = p;
+    p += al(3ull * k * sizeof(trc::MatricePartie));
     const uint64_t morceaux = p;
 
     trc::ParamsMoe pm;
     std::memset(&pm, 0, sizeof(pm));
     pm.repertoire = repertoire.adresse;
+    pm.resolus = resolus;
     pm.logits = logits;
     pm.indices = indices.adresse;
     pm.poids = poids.adresse;

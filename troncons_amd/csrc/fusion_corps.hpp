@@ -93,6 +93,24 @@ struct Tache {
 };
 static_assert(sizeof(Tache) == 64, "Tache");
 
+// Stores a MatricePartie field by field (a struct copy would take the address of a value that
+// lives in registers and move it to scratch).
+__device__ __forceinline__ u32x4 quad_flux(const DescFlux& f) {
+    const uint64_t a = reinterpret_cast<uintptr_t>(f.p);
+    return u32x4{uint32_t(a), uint32_t(a >> 32), f.longueur, f.produits};
+}
+__device__ __forceinline__ void ecrire_matrice(void* dst, const MatricePartie& m) {
+    u32x4* d = reinterpret_cast<u32x4*>(dst);
+    d[0] = quad_flux(m.delta);
+    d[1] = quad_flux(m.codes);
+    d[2] = quad_flux(m.med);
+    d[3] = quad_flux(m.biais);
+    d[4] = u32x4{m.dP, m.dN, m.dT, m.dW};
+    d[5] = u32x4{m.cP, m.cN, m.cT, m.cW};
+    d[6] = u32x4{m.bon, 0u, 0u, 0u};
+    d[7] = u32x4{0u, 0u, 0u, 0u};
+}
+
 // The job's matrix: from the mounted layer (one 128-byte read) or parsed from the part.
 __device__ __forceinline__ MatricePartie obtenir_matrice(const Tache& tc) {
     if (tc.matrice != 0) return *reinterpret_cast<const MatricePartie*>(tc.matrice);
@@ -105,6 +123,7 @@ __device__ __forceinline__ MatricePartie obtenir_matrice(const Tache& tc) {
 // the SwiGLU of expert i's gate/up rows (computed by the down pass itself, see OPT_SWIGLU).
 struct ParamsMoe {
     uint64_t repertoire;  // MatricePartie[E][3] of the mounted layer
+    uint64_t resolus;     // MatricePartie[k][3] of the selected experts, copied by the DELTA pass
     uint64_t logits;      // f32[E] router logits (the DELTA pass runs the top-k on them)
     uint64_t indices;     // u32[k] top-k indices, written by the DELTA pass
     uint64_t poids;       // f32[k] softmax weights, written by the DELTA pass
@@ -144,9 +163,12 @@ __device__ __forceinline__ Tache tache_moe_e(const ParamsMoe& moe, uint32_t i, u
     return t;
 }
 
-// Job (expert i, matrix j), the expert read from the top-k indices in device memory.
+// Job (expert i, matrix j) of the later passes: the matrix is the one the DELTA pass resolved and
+// copied into the workspace, so no pass after it reads the top-k or the directory again.
 __device__ __forceinline__ Tache tache_moe(const ParamsMoe& moe, uint32_t i, uint32_t j) {
-    return tache_moe_e(moe, i, j, glob<uint32_t>(reinterpret_cast<const void*>(moe.indices))[i]);
+    Tache t = tache_moe_e(moe, i, j, 0u);
+    t.matrice = moe.resolus + uint64_t(i * 3u + j) * sizeof(MatricePartie);
+    return t;
 }
 
 // The jobs of a launch; job of block (x, y) = y.
@@ -229,8 +251,7 @@ struct PrepEchelles {
     bool bon;
 };
 
-__device__ __forceinline__ PrepEchelles preparer_echelles(const Tache& tc) {
-    const MatricePartie m = obtenir_matrice(tc);
+__device__ __forceinline__ PrepEchelles preparer_echelles(const Tache& tc, const MatricePartie& m) {
     PrepEchelles p;
     p.bon = m.bon != 0 && tc.colonnes % 32u == 0 && tc.colonnes >= 32u && tc.lignes > 0;
     p.fd = m.delta;
@@ -321,8 +342,7 @@ struct PrepGemv {
     bool bon;
 };
 
-__device__ __forceinline__ PrepGemv preparer_gemv(const Tache& tc) {
-    const MatricePartie m = obtenir_matrice(tc);
+__device__ __forceinline__ PrepGemv preparer_gemv(const Tache& tc, const MatricePartie& m) {
     const uint32_t B = tc.colonnes / 32u;
     PrepGemv p;
     p.bon = m.bon != 0 && tc.colonnes % 32u == 0 && B >= 8u && tc.lignes > 0 &&
@@ -489,37 +509,38 @@ __device__ __forceinline__ void ecrire_lds(uint32_t a, T v) {
     *reinterpret_cast<__attribute__((address_space(3))) T*>(uintptr_t(a)) = v;
 }
 
-// A tile's word ring (as Anneau, with absolute LDS addresses; `lds` is 1 KiB aligned).
+// A tile's word ring (as Anneau, with absolute LDS addresses; `lds` is 1 KiB aligned). Chunks are
+// addressed by 32-bit offsets from the stream's start, which both tiles of a wavefront share.
 struct AnneauR {
-    const uint8_t* g0;
-    const uint8_t* fin;
+    const uint8_t* flux;  // start of the stream (its descriptor's p)
+    uint32_t g0;      // offset from `flux` of the tile's 16-byte aligned word origin
+    uint32_t fin;     // length of the stream: chunk loads never pass it
     uint32_t lds;     // LDS address of the ring
     uint32_t o2;      // byte offset from g0 of the next word (unwrapped)
     uint32_t limite;  // refill when o2 > limite (= charge * 256 - FENETRE)
     uint32_t charge;  // next chunk to request
-    uint32_t c_vol;
     u32x2 vol;
     bool en_vol;
 };
 
 __device__ __forceinline__ u32x2 lire_morceau_r(const AnneauR& a, uint32_t c, uint32_t v) {
-    const uint8_t* src = a.g0 + c * OCTETS_MORCEAU + v * 8u;
+    const uint32_t o = a.g0 + c * OCTETS_MORCEAU + v * 8u;
     u32x2 d = {0u, 0u};
-    if (src + 8 <= a.fin) d = *glob<u32x2>(src);
+    if (o + 8u <= a.fin) d = *glob<u32x2>(a.flux + o);
     return d;
 }
 
 __device__ __forceinline__ AnneauR ouvrir_anneau_r(const EnteteRans& h, const DescFlux& f, uint32_t debut,
                                                    uint32_t lds, uint32_t v, bool tuile) {
     AnneauR a;
-    const uint8_t* mot0 = reinterpret_cast<const uint8_t*>(h.mots) + 2ull * debut;
-    a.g0 = reinterpret_cast<const uint8_t*>(reinterpret_cast<uintptr_t>(mot0) & ~uintptr_t(15));
-    a.fin = f.p + f.longueur;
+    const uint32_t mot0 = uint32_t(reinterpret_cast<const uint8_t*>(h.mots) - f.p) + 2u * debut;
+    a.flux = f.p;
+    a.g0 = mot0 & ~15u;  // f.p is 16-byte aligned
+    a.fin = f.longueur;
     a.lds = lds;
-    a.o2 = uint32_t(mot0 - a.g0);
+    a.o2 = mot0 - a.g0;
     a.charge = OCTETS_ANNEAU / OCTETS_MORCEAU;
     a.limite = a.charge * OCTETS_MORCEAU - FENETRE;
-    a.c_vol = 0;
     a.vol = u32x2{0u, 0u};
     a.en_vol = false;
     if (tuile) {
@@ -533,16 +554,15 @@ __device__ __forceinline__ AnneauR ouvrir_anneau_r(const EnteteRans& h, const De
     return a;
 }
 
-// End of a macro-step: land the chunk requested one macro-step ago, request the next if due (the
-// same schedule as avancer_anneau).
+// End of a macro-step: land the chunk requested one macro-step ago (chunk charge - 1), request the
+// next if due (the same schedule as avancer_anneau).
 __device__ __forceinline__ void avancer_anneau_r(AnneauR& a, uint32_t v, bool actif) {
     if (a.en_vol) {
-        ecrire_lds<u32x2>(a.lds + (a.c_vol & 3u) * OCTETS_MORCEAU + v * 8u, a.vol);
+        ecrire_lds<u32x2>(a.lds + ((a.charge - 1u) & 3u) * OCTETS_MORCEAU + v * 8u, a.vol);
         a.en_vol = false;
     }
     if (actif && a.o2 > a.limite) {
         a.vol = lire_morceau_r(a, a.charge, v);
-        a.c_vol = a.charge;
         a.charge += 1u;
         a.limite += OCTETS_MORCEAU;
         a.en_vol = true;
@@ -608,7 +628,12 @@ __device__ __forceinline__ void corps_gemv_rapide(const Tache& tc, const PrepGem
         AnneauR a = ouvrir_anneau_r(h, p.fc, debut, a_anneau, v, tuile);
         const uint32_t o0 = a.o2;
         uint32_t rho = (m0 * 8u) / B;  // row of the tile's first block
+        // partial slot of (row, t): rows that start inside tile t use slot 0, the tile's first row
+        // (which may start in an earlier tile) its own offset, computed once
+        const uint32_t rho0 = rho, case0 = t - premiere_tuile(rho0, B, bpt);
+        auto ecrire = [&](float s) { partiels[rho * kmax + (rho == rho0 ? case0 : 0u)] = s; };
         uint32_t ent_suiv = tuile ? lire_lds<uint32_t>(a_ent_q) : ENTREE_BOURRAGE;
+        const uint32_t nb_min = min(nb_a, nb_b);
         float acc = 0.0f;
         auto macro = [&](auto tous, uint32_t m) {
             constexpr bool TOUS = decltype(tous)::value;
@@ -617,7 +642,7 @@ __device__ __forceinline__ void corps_gemv_rapide(const Tache& tc, const PrepGem
             const uint32_t ax = (ent & ENT_X) | a_x;
             const f32x4 xa = lire_lds<f32x4>(ax);
             const f32x4 xb = lire_lds<f32x4>(ax + 64u);
-            if (((m + 1u) & 15u) == 0u && m + 1u < nb) stager(m + 1u);
+            if (((m + 1u) & 15u) == 0u && m + 1u < (TOUS ? nb_min : nb)) stager(m + 1u);
             ent_suiv = lire_lds<uint32_t>(a_ent_q + 32u * ((m + 1u) & 15u));
             const uint32_t lt = a_lut + (ent & ENT_CTX);
             uint32_t compte = 0;
@@ -655,19 +680,18 @@ __device__ __forceinline__ void corps_gemv_rapide(const Tache& tc, const PrepGem
                 if (!apres && (TOUS || actif)) acc += c;
                 const float s = somme_demi_f32(acc);
                 if (moitie != 0u) {
-                    if (v == 0 && actif && rho < R) ecrire_partiel(partiels, kmax, rho, t, B, bpt, s);
+                    if (v == 0 && actif && rho < R) ecrire(s);
                     acc = apres ? c : 0.0f;
                     ++rho;
                 }
             }
         };
-        const uint32_t nb_min = min(nb_a, nb_b);
         uint32_t m = 0;
         for (; m < nb_min; ++m) macro(std::true_type{}, m);
         for (; m < nb_a; ++m) macro(std::false_type{}, m);
         const float s = somme_demi_f32(acc);
         if (tuile) {
-            if (v == 0 && rho < R) ecrire_partiel(partiels, kmax, rho, t, B, bpt, s);
+            if (v == 0 && rho < R) ecrire(s);
             hors_l += (x != L) ? 1u : 0u;
             const uint32_t attendu = (t + 1 < h.T) ? h.debut[t + 1] : h.W;
             pointeur += (v == 0 && debut + (a.o2 - o0) / 2u != attendu) ? 1u : 0u;
