@@ -1,11 +1,16 @@
 #!/usr/bin/env python3
-"""Benchmark of the fused MoE layer at batch 1 on one MI355X.
+"""Benchmark of the fused expert path on one MI355X.
 
-128 rANS-coded experts of gpt-oss-120b shape (.trc v1.2 level-0 parts, seeded synthetic MXFP4)
-sit resident in HBM with a bf16 2880 x 128 router. A step is one token through the layer: router
-logits, top-4 with softmax weights, the 4 selected experts decoded inside their fused GEMVs
-(gate/up -> SwiGLU -> down), and the weighted combine; the token sweep uses 1000 seeded
-activations, so routing is uniform-random. Prints ONE JSON line (see DESIGN.md for every field).
+Default: 128 rANS-coded experts of gpt-oss-120b shape (.trc v1.2 level-0 parts,
+seeded synthetic MXFP4) sit resident in HBM with a bf16 2880 x 128 router. A step is one token
+through the MoE layer: router logits, top-4 with softmax weights, the 4 selected experts decoded
+inside their fused GEMVs (gate/up -> SwiGLU -> down), and the weighted combine; the token sweep
+uses 1000 seeded activations, so routing is uniform-random over the 1.45 GB layer. Prints ONE JSON
+line (fields described in DESIGN.md).
+
+Other measurement modes (not the driver's line): --config 1 (one down_proj matrix), --config 2 (one
+expert MLP), both rotating over the 128 experts; --config 4 (a token through L resident MoE layers,
+default 36, about 52 GB of parts).
 """
 from __future__ import annotations
 
@@ -23,6 +28,7 @@ sys.path.insert(0, str(RACINE))
 
 METRIQUE = "MoE layer us/token @batch1 top-4; compressed-weight HBM GB/s (% of peak)"
 PIC_HBM = 8000.0  # GB/s, MI355X
+C_GPT = 2880
 
 
 def trafic_mesure():
@@ -48,6 +54,58 @@ def lire_flux(partie: bytes):
         dec, lon = struct.unpack_from("<II", partie, e + 4)
         out[(sorte, j)] = (dec, lon)
     return out
+
+
+class CoucheResidente:
+    """One synthetic layer resident on the device: the experts' parts in one allocation (each
+    256-byte aligned), their address table, the mounted directory, the layer LUTs and the router."""
+
+    def __init__(self, graine, indice, E, dims, N_delta, N_codes, n_fils, dev, fz, flux):
+        import numpy as np
+        import torch
+
+        from troncons_amd import codeur, fusion
+        from troncons_amd import noyaux as K
+        from troncons_amd.noyaux import VueCarte
+
+        t = time.perf_counter()
+        self.hote = codeur.CoucheSynthetique(graine, indice, E, dims, N_delta=N_delta, N_codes=N_codes,
+                                             n_fils=n_fils)
+        self.t_gen = time.perf_counter() - t
+        tailles = [self.hote.taille(e) for e in range(E)]
+        self.utiles = np.array([self.hote.utiles(e) for e in range(E)], np.int64)
+        self.decal = np.concatenate([[0], np.cumsum(tailles)[:-1]]).astype(np.int64)
+        self.bloc = torch.empty(int(sum(tailles)) + 256, dtype=torch.uint8, device=dev)
+        self.o0 = (-self.bloc.data_ptr()) % 256
+        base = self.bloc.data_ptr() + self.o0
+        self.octets_codes = np.zeros((E, 3), np.int64)   # CODES_CTX stream bytes per matrix
+        self.octets_matrice = np.zeros((E, 3), np.int64)  # the 4 streams of the matrix + headers
+        for e in range(E):
+            p = self.hote.partie(e)
+            off = int(self.decal[e]) + self.o0
+            self.bloc[off:off + p.size].copy_(torch.from_numpy(p))
+            fl = lire_flux(p[:64 + 16 * 12].tobytes())
+            for j in range(3):
+                self.octets_codes[e, j] = fl[(4, j)][1]
+                self.octets_matrice[e, j] = 64 + 4 * 16 + sum(fl[(s, j)][1] for s in (1, 2, 3, 4))
+        self.table = torch.from_numpy(np.array([base + int(d) for d in self.decal], np.uint64).view(np.int64)).to(dev)
+        freqs = self.hote.freqs()
+        self.luts_np = K.luts_couche([[freqs[j][t] for t in range(4)] for j in range(3)])
+        self.luts = torch.from_numpy(self.luts_np.view(np.int32)).to(dev)
+        routeur = np.stack([codeur.synth_normale_bf16(graine + indice, 3, e, C_GPT, 0.02) for e in range(E)])
+        self.r16 = torch.from_numpy((routeur.view(np.uint32) >> 16).astype(np.uint16).view(np.int16)).to(dev)
+        # mount once: every part parsed into the device directory of stream locations
+        self.rep = torch.zeros(fusion.taille_repertoire(E), dtype=torch.uint8, device=dev)
+        ctl = torch.zeros(4, dtype=torch.int32, device=dev)
+        V = VueCarte.de
+        fz.monter_couche(V(self.table), E, dims, V(self.rep), V(ctl), f=flux)
+        torch.cuda.synchronize()
+        assert (ctl.cpu().numpy() == 0).all(), f"mount control words {ctl.cpu().numpy()}"
+        self.vrep, self.vluts, self.vr16 = V(self.rep), V(self.luts), V(self.r16)
+
+    def vue_partie(self, e):
+        from troncons_amd.noyaux import VueCarte
+        return VueCarte.de(self.bloc, int(self.decal[e]) + self.o0, int(self.hote.taille(e)))
 
 
 def baseline_cpu(couche, luts, x_tok, selections, budget_s: float, n_fils: int):
@@ -98,11 +156,42 @@ def baseline_cpu(couche, luts, x_tok, selections, budget_s: float, n_fils: int):
     }
 
 
+def chrono_passes(fusion, pas, n):
+    """Per-kernel durations over n steps: every kernel launched with the start/stop events that the
+    runtime records at the kernel's own start and end (hipExtLaunchKernel). Kept out of the timed
+    region, so that `value` carries no timing machinery."""
+    import torch
+    fusion.chrono(True)
+    fusion.chrono_recolter(True)
+    for s in range(n):
+        pas(s)
+    torch.cuda.synchronize()
+    noyaux = fusion.chrono_recolter(True)
+    fusion.chrono(False)
+    return noyaux
+
+
+def temps(pas, steps, warmup, flux):
+    import torch
+    for s in range(warmup):
+        pas(s)
+    torch.cuda.synchronize()
+    debut, fin = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    debut.record(flux)
+    for s in range(steps):
+        pas(s)
+    fin.record(flux)
+    torch.cuda.synchronize()
+    return debut.elapsed_time(fin)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--config", type=int, default=3, choices=(1, 2, 3, 4))
+    ap.add_argument("--couches", type=int, default=36, help="layers of --config 4")
     ap.add_argument("--experts", type=int, default=128)
     ap.add_argument("--k", type=int, default=4)
     ap.add_argument("--n-codes", type=int, default=16, help="macro-steps per CODES_CTX tile written by the encoder")
@@ -128,52 +217,24 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     dev = torch.device("cuda:0")
     dims = DimsExpert.gpt_oss()
-    E, k, C = args.experts, args.k, 2880
+    E, k, C = args.experts, args.k, C_GPT
     n_fils = min(16, os.cpu_count() or 1)
-
-    t = time.perf_counter()
-    couche = codeur.CoucheSynthetique(args.graine, 0, E, dims, N_delta=args.n_delta, N_codes=args.n_codes,
-                                      n_fils=n_fils)
-    t_gen = time.perf_counter() - t
-    tailles = [couche.taille(e) for e in range(E)]
-    utiles = np.array([couche.utiles(e) for e in range(E)], np.int64)
-    decal = np.concatenate([[0], np.cumsum(tailles)[:-1]]).astype(np.int64)
-    bloc = torch.empty(int(sum(tailles)) + 256, dtype=torch.uint8, device=dev)
-    base = bloc.data_ptr() + ((-bloc.data_ptr()) % 256)
-    octets_codes = np.zeros((E, 3), np.int64)
-    for e in range(E):
-        p = couche.partie(e)
-        off = int(decal[e]) + ((-bloc.data_ptr()) % 256)
-        bloc[off:off + p.size].copy_(torch.from_numpy(p))
-        fl = lire_flux(p[:64 + 16 * 12].tobytes())
-        for j in range(3):
-            octets_codes[e, j] = fl[(4, j)][1]
-    table = torch.from_numpy(np.array([base + int(d) for d in decal], np.uint64).view(np.int64)).to(dev)
-    freqs = couche.freqs()
-    from troncons_amd import noyaux as K
-    luts_np = K.luts_couche([[freqs[j][t] for t in range(4)] for j in range(3)])
-    luts = torch.from_numpy(luts_np.view(np.int32)).to(dev)
-    routeur = np.stack([codeur.synth_normale_bf16(args.graine, 3, e, C, 0.02) for e in range(E)])
-    r16 = torch.from_numpy((routeur.view(np.uint32) >> 16).astype(np.uint16).view(np.int16)).to(dev)
-    x_tok = np.stack([codeur.synth_normale_bf16(args.graine, 4, t, C, 1.0) for t in range(args.tokens)])
-    xs = torch.from_numpy(x_tok).to(dev)
-    residu = torch.zeros(C, dtype=torch.float32, device=dev)
-    n_sel = max(args.steps, args.warmup, 1)
-    sel_i = torch.zeros((n_sel, 8), dtype=torch.int32, device=dev)
-    sel_w = torch.zeros((n_sel, 8), dtype=torch.float32, device=dev)
-    ctl = torch.zeros(4, dtype=torch.int32, device=dev)
-    travail = torch.empty(fusion.taille_travail_couche(dims, E, k, args.n_codes) + 256, dtype=torch.uint8, device=dev)
-    tr = VueCarte(travail.data_ptr() + ((-travail.data_ptr()) % 256), fusion.taille_travail_couche(dims, E, k,
-                                                                                                  args.n_codes))
     fz = fusion.Fusion()
     flux = torch.cuda.current_stream()
     V = VueCarte.de
-    # mount the resident layer once: every part parsed into the device directory of stream locations
-    rep = torch.zeros(fusion.taille_repertoire(E), dtype=torch.uint8, device=dev)
-    fz.monter_couche(V(table), E, dims, V(rep), V(ctl), f=flux)
-    torch.cuda.synchronize()
-    assert (ctl.cpu().numpy() == 0).all(), f"mount control words {ctl.cpu().numpy()}"
-    vt, vl, vr, vres, vctl = V(rep), V(luts), V(r16), V(residu), V(ctl)
+
+    n_couches = args.couches if args.config == 4 else 1
+    couches = []
+    for l in range(n_couches):
+        couches.append(CoucheResidente(args.graine, l, E, dims, args.n_delta, args.n_codes, n_fils, dev, fz, flux))
+        print(f"bench: layer {l} encoded and mounted ({couches[-1].t_gen:.1f} s)", file=sys.stderr, flush=True)
+    t_gen = sum(c.t_gen for c in couches)
+    c0 = couches[0]
+    x_tok = np.stack([codeur.synth_normale_bf16(args.graine, 4, t, C, 1.0) for t in range(args.tokens)])
+    xs = torch.from_numpy(x_tok).to(dev)
+    vx = [V(xs, 4 * C * t, 4 * C) for t in range(args.tokens)]
+    ctl = torch.zeros(4, dtype=torch.int32, device=dev)
+    vctl = V(ctl)
     if args.calibrer_copie:
         # a copy kernel of known size: FETCH_SIZE / WRITE_SIZE per dispatch should read 65536 KiB
         src = torch.ones(16 << 20, dtype=torch.float32, device=dev)
@@ -182,77 +243,124 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
-    vx = [V(xs, 4 * C * t, 4 * C) for t in range(args.tokens)]
-    vi = [V(sel_i, 32 * s, 32) for s in range(n_sel)]
-    vw = [V(sel_w, 32 * s, 32) for s in range(n_sel)]
+
+    def espace(n):
+        t = torch.empty(n + 256, dtype=torch.uint8, device=dev)
+        return t, VueCarte(t.data_ptr() + ((-t.data_ptr()) % 256), n)
+
+    if args.config in (1, 2):
+        # one down_proj (config 1) or one expert MLP (config 2) per step, rotating over the experts
+        if args.config == 1:
+            n_tr = fusion.taille_travail_gemv(C, C, args.n_codes)
+        else:
+            n_tr = fusion.taille_travail_expert(dims, args.n_codes)
+        _tr, tr = espace(n_tr)
+        y = torch.zeros(C, dtype=torch.float32, device=dev)
+        vy = V(y)
+
+        def pas(s):
+            e = s % E
+            if args.config == 1:
+                fz.gemv_fusionnee(c0.vue_partie(e), 2, c0.vluts, C, C, vx[s % args.tokens], vy, vctl, tr,
+                                  args.n_delta, args.n_codes, f=flux)
+            else:
+                fz.expert_fusionne(c0.vue_partie(e), c0.vluts, dims, vx[s % args.tokens], vy, vctl, tr,
+                                   args.n_delta, args.n_codes, f=flux)
+
+        ms = temps(pas, args.steps, args.warmup, flux)
+        assert (ctl.cpu().numpy() == 0).all(), f"control words {ctl.cpu().numpy()}"
+        sel = np.arange(args.steps) % E
+        octets = (c0.octets_matrice[sel, 2] if args.config == 1 else c0.utiles[sel]).astype(np.float64)
+        noyaux = chrono_passes(fusion, pas, min(args.steps, 200))
+        us = ms * 1e3 / args.steps
+        nom = "one down_proj 2880x2880" if args.config == 1 else "one expert MLP (gate, up, down 2880x2880)"
+        ligne = {
+            "metric": f"config{args.config} us per {'matrix' if args.config == 1 else 'expert'}; "
+                      "compressed-weight GB/s",
+            "value": round(us, 3), "unit": "us/" + ("matrix" if args.config == 1 else "expert"), "n_gpus": 1,
+            "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms / args.steps, 5),
+            "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "u32 rANS / f32 GEMV",
+            "data": "synthetic (seeded MXFP4 law A, E8M0 in [119,125], bf16 N(0,1) activations)",
+            "config": {"workload": f"config{args.config}: {nom}, .trc v1.2 rANS-coded, rotating over {E} experts",
+                       "n_codes": args.n_codes, "n_delta": args.n_delta},
+            "gbps_compressed": round(float(octets.sum() / (ms * 1e-3) / 1e9), 1),
+            "compressed_bytes_per_step": int(octets.mean()),
+            "kernel_us": {nom_k: round(v[0] / v[1] * 1e3, 2) for nom_k, v in noyaux.items()},
+            "setup_s": round(t_gen, 1),
+        }
+        print(json.dumps(ligne), flush=True)
+        return
+
+    # configs 3 and 4: the MoE layer step (one layer, or a token through L layers)
+    residu = torch.zeros(C, dtype=torch.float32, device=dev)
+    vres = V(residu)
+    n_sel = max(args.steps, args.warmup, 1)
+    sel_i = torch.zeros((n_sel, n_couches, 8), dtype=torch.int32, device=dev)
+    sel_w = torch.zeros((n_sel, n_couches, 8), dtype=torch.float32, device=dev)
+    vi = [[V(sel_i, 32 * (s * n_couches + l), 32) for l in range(n_couches)] for s in range(n_sel)]
+    vw = [[V(sel_w, 32 * (s * n_couches + l), 32) for l in range(n_couches)] for s in range(n_sel)]
+    n_tr = fusion.taille_travail_couche(dims, E, k, args.n_codes)
+    _tr, tr = espace(n_tr)
 
     def pas(s):
-        fz.couche_moe(vt, E, vl, dims, vr, None, vx[s % args.tokens], k, vres, vi[s], vw[s], vctl, tr,
-                      args.n_delta, args.n_codes, f=flux)
+        for l, c in enumerate(couches):
+            fz.couche_moe(c.vrep, E, c.vluts, dims, c.vr16, None, vx[s % args.tokens], k, vres, vi[s][l], vw[s][l],
+                          vctl, tr, args.n_delta, args.n_codes, f=flux)
 
-    for s in range(args.warmup):
-        pas(s)
-    torch.cuda.synchronize()
-    debut, fin = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    debut.record(flux)
-    for s in range(args.steps):
-        pas(s)
-    fin.record(flux)
-    torch.cuda.synchronize()
-    ms = debut.elapsed_time(fin)
+    ms = temps(pas, args.steps, args.warmup, flux)
     assert (ctl.cpu().numpy() == 0).all(), f"control words {ctl.cpu().numpy()}"
-    sel = sel_i[:args.steps, :k].cpu().numpy()
-    octets_tok = utiles[sel].sum(axis=1)
+    sel = sel_i[:args.steps, :, :k].cpu().numpy()
+    octets_tok = sum(couches[l].utiles[sel[:, l, :]].sum(axis=1) for l in range(n_couches))
     us_tok = ms * 1e3 / args.steps
     gbps = octets_tok.sum() / (ms * 1e-3) / 1e9
+    histo = np.bincount(sel[:, 0, :].reshape(-1), minlength=E)
 
-    # chronogram pass over the same steps: every kernel of the layer launched with start/stop events
-    # that the runtime records at the kernel's own start and end (hipExtLaunchKernel); kept out of
-    # the timed region so that `value` carries no timing machinery at all
-    n_chrono = min(args.steps, 200)
-    fusion.chrono(True)
-    fusion.chrono_recolter(True)
-    for s in range(n_chrono):
-        pas(s)
-    torch.cuda.synchronize()
-    noyaux = fusion.chrono_recolter(True)
-    fusion.chrono(False)
-    sel_c = sel_i[:n_chrono, :k].cpu().numpy()
+    n_chrono = min(args.steps, 200 if n_couches == 1 else 20)
+    noyaux = chrono_passes(fusion, pas, n_chrono)
+    sel_c = sel_i[:n_chrono, :, :k].cpu().numpy()
     gu_ms, gu_n = noyaux.get("fusion_gemv/gate_up", (0.0, 1))
     bas_ms, bas_n = noyaux.get("fusion_gemv/down", (0.0, 1))
-    octets_gu = octets_codes[sel_c][:, :, :2].sum() / n_chrono
-    octets_bas = octets_codes[sel_c][:, :, 2].sum() / n_chrono
+    octets_gu = sum(couches[l].octets_codes[sel_c[:, l, :]][:, :, :2].sum() for l in range(n_couches)) / gu_n
+    octets_bas = sum(couches[l].octets_codes[sel_c[:, l, :]][:, :, 2].sum() for l in range(n_couches)) / bas_n
     duree_us = (gu_ms / gu_n + bas_ms / bas_n) * 1e3
     atteint = (octets_gu + octets_bas) / (duree_us * 1e-6) / 1e9
     roofline = {
         "bound": "hbm", "kernel": "fusion_gemv (gate/up launch + down launch)",
         "achieved": round(float(atteint), 1), "peak": PIC_HBM, "unit": "GB/s",
-        "frac": round(float(atteint / PIC_HBM), 4), "traffic": trafic_mesure(),
+        "frac": round(float(atteint / PIC_HBM), 4), "traffic": trafic_mesure() if n_couches == 1 else None,
         "bytes_per_launch": {"gate_up": int(octets_gu), "down": int(octets_bas)},
         "avg_launch_us": {"gate_up": round(gu_ms / gu_n * 1e3, 2), "down": round(bas_ms / bas_n * 1e3, 2),
                           "both": round(duree_us / 2, 2)},
     }
     chrono_us = {nom: round(v[0] / v[1] * 1e3, 2) for nom, v in noyaux.items()}
-
+    if n_couches == 1:
+        metrique, unite = METRIQUE, "us/token"
+        workload = ("config3: one MoE layer decode step, batch 1, top-4 of 128 gpt-oss-120b experts "
+                    "(3 x 2880x2880 MXFP4, .trc v1.2 rANS-coded), 1000-token seeded sweep")
+    else:
+        metrique, unite = f"config4 us/token for the MoE part of {n_couches} resident layers", "us/token"
+        workload = (f"config4: a token through {n_couches} resident MoE layers x 128 gpt-oss-120b experts "
+                    f"(.trc v1.2 rANS-coded, {sum(int(c.utiles.sum()) for c in couches) / 1e9:.1f} GB of parts)")
     ligne = {
-        "metric": METRIQUE, "value": round(us_tok, 3), "unit": "us/token", "n_gpus": 1, "steps": args.steps,
+        "metric": metrique, "value": round(us_tok, 3), "unit": unite, "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms / args.steps, 5), "higher_is_better": False,
         "scaling": "weak", "vs_baseline": None, "dtype": "u32 rANS / f32 GEMV",
         "data": "synthetic (seeded MXFP4 law A, E8M0 in [119,125], bf16 N(0,1) activations, bf16 N(0,0.02) router)",
-        "config": {"workload": "config3: one MoE layer decode step, batch 1, top-4 of 128 gpt-oss-120b experts "
-                               "(3 x 2880x2880 MXFP4, .trc v1.2 rANS-coded), 1000-token seeded sweep",
-                   "experts": E, "k": k, "hidden": C, "n_codes": args.n_codes, "n_delta": args.n_delta,
-                   "tokens": args.tokens, "mean_part_bytes": int(utiles.mean())},
+        "config": {"workload": workload, "experts": E, "k": k, "hidden": C, "layers": n_couches,
+                   "n_codes": args.n_codes, "n_delta": args.n_delta, "tokens": args.tokens,
+                   "mean_part_bytes": int(c0.utiles.mean())},
         "gbps_compressed": round(float(gbps), 1),
         "frac_hbm_layer": round(float(gbps / PIC_HBM), 4),
         "compressed_bytes_per_token": int(octets_tok.mean()),
+        "routing_histogram": {"experts_hit": int((histo > 0).sum()), "min": int(histo.min()),
+                              "max": int(histo.max()), "mean": round(float(histo.mean()), 2)},
         "kernel_us": chrono_us,
         "roofline": roofline,
         "setup_s": round(t_gen, 1),
     }
-    if not args.sans_cpu:
-        selections = [(sel[t], sel_w[t, :k].cpu().numpy()) for t in range(min(args.steps, 20))]
-        ligne["cpu_baseline"] = baseline_cpu(couche, luts_np, x_tok, selections, args.budget_cpu, n_fils)
+    if not args.sans_cpu and n_couches == 1:
+        selections = [(sel[t, 0], sel_w[t, 0, :k].cpu().numpy()) for t in range(min(args.steps, 20))]
+        ligne["cpu_baseline"] = baseline_cpu(c0.hote, c0.luts_np, x_tok, selections, args.budget_cpu, n_fils)
     else:
         ligne["cpu_baseline"] = None
     print(json.dumps(ligne), flush=True)
