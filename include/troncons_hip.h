@@ -185,6 +185,21 @@ int trc_couche_moe_fusionnee(trc_vue repertoire, uint32_t experts, trc_vue luts,
                              trc_vue indices, trc_vue poids, trc_vue controle, trc_vue travail, uint32_t n_delta,
                              uint32_t n_codes, void* flux);
 
+/* Workspace bytes of trc_prefill_moe (0 if the shape is refused). */
+uint64_t trc_taille_travail_prefill(const trc_dims_expert* dims, uint32_t experts, uint32_t positions, uint32_t k,
+                                    uint32_t n_codes);
+/* Batched prefill of one resident MoE layer: replaces the per-layer expert part of the reference's
+ * prefill, trc-ordo/src/lib.rs:814-941 (par_expert grouping of the positions' top-k, one decode per
+ * chosen expert, Modele::expert_pos per (position, slot) and Modele::combiner_pos per position,
+ * trc-modele/src/lib.rs:688-710). x: f32[positions][C]; indices / poids: u32 / f32 [positions][k]
+ * (the routers' output, debut_couche_pos); residus: f32[positions][D], residus[i] += ((w_i0 s_i0 +
+ * w_i1 s_i1) + ...). Each chosen expert is decoded once, into LDS, and applied to all its positions
+ * on the block-scaled FP4 MFMA; CODES_CTX tiles of at most 16 macro-steps (n_codes <= 16), rows of at
+ * most 4096 columns. An index >= experts counts one format error and leaves its position alone. */
+int trc_prefill_moe(trc_vue repertoire, uint32_t experts, trc_vue luts, const trc_dims_expert* dims, trc_vue x,
+                    uint32_t positions, trc_vue indices, trc_vue poids, uint32_t k, trc_vue residus,
+                    trc_vue controle, trc_vue travail, uint32_t n_delta, uint32_t n_codes, void* flux);
+
 /* Chronogram of the fused entry points (role of the reference's --chronogramme, which records GPU
  * event timestamps around each decode, moteur/crates/trc-ordo/src/lib.rs:205-222): off by
  * default; when on, every kernel a fused entry point launches is bracketed by two HIP events on

@@ -175,3 +175,22 @@ def test_wrappers_refuse_wrong_sizes_carte_rs_468():
     with pytest.raises(K.ErreurUsage):
         k.decoder_lot(petit, 0, dims, f=0)
     assert "usage" in K.bibliotheque().trc_derniere_erreur().decode()
+
+
+def test_prefill_refuses_unsupported_shapes_before_launching():
+    """The batched prefill holds a tile's decoded bytes in registers (at most 16 macro-steps per
+    CODES_CTX tile) and a row's blocks in LDS (at most 4096 columns): other shapes are usage errors,
+    returned before any HIP call."""
+    from troncons_amd import fusion
+
+    fz = fusion.Fusion()
+    dims = DimsExpert.gpt_oss()
+    v = VueCarte(1 << 20, 1 << 40)
+    assert fusion.taille_travail_prefill(dims, 128, 512, 4, 16) > 0
+    assert fusion.taille_travail_prefill(dims, 128, 512, 4, 32) == 0
+    assert fusion.taille_travail_prefill(DimsExpert.de([256, 256, 256], [8192, 8192, 256]), 8, 4, 4, 8) == 0
+    assert fusion.taille_travail_prefill(dims, 128, 8192, 4, 16) == 0  # more than 16384 pairs
+    with pytest.raises(K.ErreurUsage):
+        fz.prefill_moe(v, 128, v, dims, v, 512, v, v, 4, v, v, v, 4, 32, f=0)
+    with pytest.raises(K.ErreurUsage):  # workspace too small
+        fz.prefill_moe(v, 128, v, dims, v, 512, v, v, 4, v, v, VueCarte(1 << 20, 4096), 4, 16, f=0)

@@ -1,0 +1,175 @@
+"""GPU parity of the batched prefill (trc_prefill_moe), through the C-ABI.
+
+Each position's residual is checked against the reference's own chain run by the oracle for every
+(position, slot) — gemv_mxfp4 gate and up, swiglu_oai, gemv_mxfp4 down, then the ordered combine
+(trc-modele/src/lib.rs:688-710, passe.cuh:598-622) — and against the same computation in f64 from the
+uncompressed weights: within 1e-5 * max|change| of both, per position (the fused path's GEMV
+tolerance; the MFMA's block sums are exact by construction, so only the fp32 accumulation order and
+a 2^-20 activation remainder differ). Decoded weights are checked bit for bit by the other suites.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+import oracle_ffi as O  # noqa: E402
+from gpu_outils import dev, hote, vue, zeros  # noqa: E402
+from troncons_amd import codeur, fusion  # noqa: E402
+from troncons_amd.noyaux import DimsExpert  # noqa: E402
+
+TOL = 1e-5
+GPT = DimsExpert.gpt_oss()
+
+
+@pytest.fixture(scope="module")
+def fz():
+    return fusion.Fusion()
+
+
+def _routage(graine, T, E, k, zipf=None):
+    """k distinct experts per position (uniform or Zipf over the expert ranks) and softmax weights of
+    seeded logits, computed in f64 and rounded once."""
+    rng = np.random.default_rng(graine)
+    idx = np.zeros((T, k), np.uint32)
+    w = np.zeros((T, k), np.float32)
+    p = None
+    if zipf:
+        p = 1.0 / np.arange(1, E + 1, dtype=np.float64) ** zipf
+        p /= p.sum()
+    for i in range(T):
+        idx[i] = rng.choice(E, size=k, replace=False, p=p)
+        lg = np.sort(rng.standard_normal(k))[::-1]
+        ex = np.exp(lg - lg[0])
+        w[i] = (ex / ex.sum()).astype(np.float32)
+    return idx, w
+
+
+def _slots(graine, E, dims):
+    out = []
+    for e in range(E):
+        bl, bi = codeur.synth_expert(graine, 0, e, dims)
+        out.append([O.blocs_vers_soa(bl[j], dims.lignes[j], dims.colonnes[j], bi[j], canonique=True)
+                    for j in range(3)])
+    return out
+
+
+def _mlp(sl, x, dims):
+    R, C = dims.lignes[0], dims.colonnes[0]
+    g = O.gemv_mxfp4(sl[0], x, R, C)
+    u = O.gemv_mxfp4(sl[1], x, R, C)
+    s = O.gemv_mxfp4(sl[2], O.swiglu_oai(g, u), dims.lignes[2], dims.colonnes[2])
+    g64 = O.gemv_mxfp4_f64(sl[0], x, R, C)
+    u64 = O.gemv_mxfp4_f64(sl[1], x, R, C)
+    gg = np.minimum(g64, 7.0)
+    uu = np.clip(u64, -7.0, 7.0)
+    a64 = gg / (1.0 + np.exp(-1.702 * gg)) * (uu + 1.0)
+    s64 = O.gemv_mxfp4_f64(sl[2], a64.astype(np.float32), dims.lignes[2], dims.colonnes[2])
+    return s, s64
+
+
+class Couche:
+    """A synthetic layer mounted on the device (parts, directory, LUTs)."""
+
+    def __init__(self, fz, graine, E, dims, N):
+        self.c = codeur.CoucheSynthetique(graine, 0, E, dims, N_delta=N[0], N_codes=N[1])
+        freqs = self.c.freqs()
+        self.luts = dev(O.luts_couche([[freqs[j][t] for t in range(4)] for j in range(3)]))
+        self.parts = [dev(self.c.partie(e)) for e in range(E)]
+        self.table = dev(np.array([p.data_ptr() for p in self.parts], np.uint64))
+        self.rep = zeros(fusion.taille_repertoire(E))
+        ctl = zeros(16)
+        fz.monter_couche(vue(self.table), E, dims, vue(self.rep), vue(ctl))
+        assert list(hote(ctl, np.uint32)) == [0, 0, 0, 0]
+
+
+def _lancer(fz, couche, E, dims, x, idx, w, residu0, N):
+    T, k = idx.shape
+    xd, idd, wd, res = dev(x), dev(idx), dev(w), dev(residu0)
+    ctl = zeros(16)
+    tr = zeros(fusion.taille_travail_prefill(dims, E, T, k, N[1]))
+    print(f"prefill: T={T} k={k} E={E} dims={list(dims.lignes)}x{list(dims.colonnes)} N={N}", flush=True)
+    fz.prefill_moe(vue(couche.rep), E, vue(couche.luts), dims, vue(xd), T, vue(idd), vue(wd), k, vue(res), vue(ctl),
+                   vue(tr), *N)
+    return hote(res, np.float32).reshape(T, -1), hote(ctl, np.uint32)
+
+
+def _verifier(got, residu0, x, idx, w, slots, dims, valides=None):
+    T, k = idx.shape
+    D = dims.lignes[2]
+    for i in range(T):
+        if valides is not None and not valides[i]:
+            assert (got[i] == residu0[i]).all()
+            continue
+        s, s64 = zip(*[_mlp(slots[int(idx[i, q])], x[i], dims) for q in range(k)])
+        ref = O.combiner(residu0[i], np.concatenate(s), D, w[i], k, D)
+        ref64 = residu0[i].astype(np.float64) + sum(float(w[i, q]) * s64[q] for q in range(k))
+        d = ref - residu0[i]
+        assert np.abs(got[i] - ref).max() <= TOL * np.abs(d).max(), i
+        assert np.abs(got[i] - ref64).max() <= TOL * np.abs(ref64 - residu0[i]).max(), i
+
+
+@pytest.mark.parametrize("N", [(8, 8), (4, 16), (16, 3)])
+def test_prefill_small_layer_zipf_routing(fz, N):
+    """6 experts, 40 positions, Zipf routing (some experts take more than 16 positions: several
+    MFMA column tiles), 256-wide matrices."""
+    E, T, k = 6, 40, 4
+    dims = DimsExpert.de([256, 256, 256], [256, 256, 256])
+    couche = Couche(fz, 31, E, dims, N)
+    idx, w = _routage(32, T, E, k, zipf=1.1)
+    x = np.stack([O.synth_normale_bf16(33, 4, i, 256, 1.0) for i in range(T)])
+    residu0 = np.stack([O.synth_normale_bf16(33, 5, i, 256, 0.5) for i in range(T)])
+    got, ctl = _lancer(fz, couche, E, dims, x, idx, w, residu0, N)
+    assert list(ctl) == [0, 0, 0, 0]
+    _verifier(got, residu0, x, idx, w, _slots(31, E, dims), dims)
+    couche.c.liberer()
+
+
+def test_prefill_ragged_blocks(fz):
+    """Rows of 9 and 11 blocks (padded to 12 for the 4-block MFMA step), 288-wide layer."""
+    E, T, k, N = 5, 21, 3, (8, 8)
+    dims = DimsExpert.de([352, 352, 288], [288, 288, 352])
+    couche = Couche(fz, 41, E, dims, N)
+    idx, w = _routage(42, T, E, k)
+    x = np.stack([O.synth_normale_bf16(43, 4, i, 288, 1.0) for i in range(T)])
+    residu0 = np.zeros((T, 288), np.float32)
+    got, ctl = _lancer(fz, couche, E, dims, x, idx, w, residu0, N)
+    assert list(ctl) == [0, 0, 0, 0]
+    _verifier(got, residu0, x, idx, w, _slots(41, E, dims), dims)
+    couche.c.liberer()
+
+
+def test_prefill_gpt_oss_shape(fz):
+    """Config-5 shape family: 2880 x 2880 gpt-oss experts, N = 16 / 4, 16 positions over 8 experts
+    with Zipf routing; also determinism (a second call gives the same bits)."""
+    E, T, k, N = 8, 16, 4, (4, 16)
+    couche = Couche(fz, 51, E, GPT, N)
+    idx, w = _routage(52, T, E, k, zipf=1.1)
+    x = np.stack([O.synth_normale_bf16(53, 4, i, 2880, 1.0) for i in range(T)])
+    residu0 = np.zeros((T, 2880), np.float32)
+    got, ctl = _lancer(fz, couche, E, GPT, x, idx, w, residu0, N)
+    assert list(ctl) == [0, 0, 0, 0]
+    got2, _ = _lancer(fz, couche, E, GPT, x, idx, w, residu0, N)
+    assert (got == got2).all()
+    _verifier(got, residu0, x, idx, w, _slots(51, E, GPT), GPT)
+    couche.c.liberer()
+
+
+def test_prefill_bad_indices_counted_and_skipped(fz):
+    """Indices >= experts are format errors: counted once each, their positions untouched; the other
+    positions are still right."""
+    E, T, k, N = 4, 12, 2, (8, 8)
+    dims = DimsExpert.de([256, 256, 256], [256, 256, 256])
+    couche = Couche(fz, 61, E, dims, N)
+    idx, w = _routage(62, T, E, k)
+    idx[3, 1] = E
+    idx[7, 0] = 1000
+    x = np.stack([O.synth_normale_bf16(63, 4, i, 256, 1.0) for i in range(T)])
+    residu0 = np.stack([O.synth_normale_bf16(63, 5, i, 256, 0.5) for i in range(T)])
+    got, ctl = _lancer(fz, couche, E, dims, x, idx, w, residu0, N)
+    assert ctl[1] == 2 and ctl[0] == 0 and ctl[2] == 0 and ctl[3] == 0
+    valides = [i not in (3, 7) for i in range(T)]
+    _verifier(got, residu0, x, idx, w, _slots(61, E, dims), dims, valides)
+    couche.c.liberer()

@@ -45,7 +45,9 @@ fusion_echelles(trc::Taches taches, const uint32_t* __restrict__ luts, uint32_t*
     __shared__ __attribute__((aligned(16))) uint8_t anneaux[(FILS_ECHELLES_FUSION / 32) * OCTETS_ANNEAU];
     __shared__ uint32_t choisis[TOPK_MAX];
     const bool moe = taches.mode == TACHES_MOE_DELTA;
-    const uint32_t j_bloc = moe ? blockIdx.y % 3u : min(taches[blockIdx.y].j, 2u);
+    const bool prefill = taches.mode == TACHES_PREFILL_DELTA;
+    if (prefill && reinterpret_cast<const uint32_t*>(taches.moe.compte)[blockIdx.y / 3u] == 0u) return;
+    const uint32_t j_bloc = (moe || prefill) ? blockIdx.y % 3u : min(taches[blockIdx.y].j, 2u);
     ChargeLut<1> charge_lut;
     charge_lut.demarrer(luts + (uint64_t(j_bloc) * 4u + 0u) * M, M / 4u);
     Tache tc;
@@ -69,6 +71,9 @@ fusion_echelles(trc::Taches taches, const uint32_t* __restrict__ luts, uint32_t*
         __syncthreads();
         const uint32_t i = blockIdx.y / 3u;
         tc = uniforme(tache_moe_e(pm, i, blockIdx.y - 3u * i, choisis[i]));
+    } else if (prefill) {
+        const uint32_t e = blockIdx.y / 3u;
+        tc = uniforme(tache_moe_e(taches.moe, e, blockIdx.y - 3u * e, e));
     } else {
         tc = uniforme(taches[blockIdx.y]);
     }
@@ -372,6 +377,20 @@ Taches par_moe(const trc::ParamsMoe& pm, uint32_t mode, uint32_t options) {
 }
 
 }  // namespace
+
+namespace trc {
+// DELTA pass of a batched prefill (prefill.hip): matrices (e, j) of every expert with compte[e] > 0,
+// block entries into workspace piece e*3 + j.
+int lancer_echelles_prefill(const ParamsMoe& pm, uint32_t R, uint32_t C, uint32_t n_delta, const uint32_t* luts,
+                            uint32_t* ctl, hipStream_t f) {
+    const Taches t = par_moe(pm, TACHES_PREFILL_DELTA, 0);
+    TRC_LANCER_N("fusion_echelles/prefill", fusion_echelles,
+                 dim3(grille_tuiles(uint64_t(R) * (C / 32), n_delta, TUILES_ECHELLES), 3 * pm.E),
+                 dim3(FILS_ECHELLES_FUSION), f, t, luts, ctl);
+    return TRC_OK;
+}
+uint64_t octets_entrees(uint32_t R, uint32_t C) { return octets_ech(R, C); }
+}  // namespace trc
 
 extern "C" uint64_t trc_taille_travail_gemv_fusionnee(uint32_t lignes, uint32_t colonnes, uint32_t n_codes) {
     if (colonnes / 32 < 8 || n_codes == 0) return 0;

@@ -132,6 +132,7 @@ struct ParamsMoe {
     uint64_t ech;         // scale entries of piece 0
     uint64_t partiels;    // partial sums of piece 0
     uint64_t pas;         // workspace bytes per piece
+    uint64_t compte;      // (prefill) u32[E] positions that chose expert e; experts with 0 are skipped
     uint32_t lignes[3], colonnes[3], kmax[3];
     uint32_t k, E;
 };
@@ -141,6 +142,7 @@ enum ModeTaches : uint32_t {
     TACHES_MOE_DELTA = 1,  // job y = (expert y/3, matrix y%3)
     TACHES_MOE_GU = 2,     // job y = (expert y/2, matrix y%2)
     TACHES_MOE_BAS = 3,    // job y = (expert y, matrix 2)
+    TACHES_PREFILL_DELTA = 4,  // job y = (expert y/3, matrix y%3), workspace piece y, if chosen
 };
 
 // Option of a CODES pass over MoE down jobs: x = swiglu_oai(gate_i, up_i), finished from their

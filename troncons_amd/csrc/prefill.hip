@@ -1,0 +1,687 @@
+// prefill.hip — batched prefill of a resident MoE layer on gfx950 (T positions, top-k each): every
+// chosen expert is rANS-decoded once, band of rows by band of rows, into LDS as MXFP4 (E2M1 codes,
+// E8M0 block scales) and multiplied against all the positions that chose it on the block-scaled FP4
+// MFMA (v_mfma_scale_f32_16x16x128_f8f6f4, fp32 accumulation). The reference runs the same layer as
+// one decode per chosen expert then one GEMV chain per (position, slot) (trc-ordo/src/lib.rs:782-945,
+// expert_pos and combiner_pos, trc-modele/src/lib.rs:688-710). Launches, one stream:
+//
+//   prefill_grouper       (position, slot) pairs grouped by expert, in position order within an
+//                         expert (the reference's par_expert lists, trc-ordo/src/lib.rs:815-823);
+//   prefill_quant_x       each position's x split into fp8 pieces with E8M0 block scales;
+//   fusion_echelles       (prefill mode) DELTA -> block entries of every chosen expert's matrices;
+//   prefill_mfma_gu       gate and up: bands decoded into LDS, MFMA against the expert's positions,
+//                         + bias -> gu;
+//   prefill_swiglu_quant  act = swiglu_oai(gate, up) per pair, split into fp8 pieces;
+//   prefill_mfma_bas      down -> s, one row of D per pair (the reference's pos.s layout);
+//   prefill_combiner      x_i += ((w0 s_i0 + w1 s_i1) + ...) in slot order, no FMA.
+//
+// Activations in pieces. The MFMA's B operand here is fp8 E4M3 with one E8M0 scale per 32 values,
+// and the MFMA adds the 32 products of a block in a fixed-point sum that keeps about 14 bits below
+// the block's largest product. A block of activations a is written as a = sum_p q_p 2^k_p: piece p
+// takes, at scale 2^k_p (the residual's maximum in [128, 256) * 2^k_p), the round-to-nearest E4M3 of
+// every residual value whose scaled magnitude is at least 8 and leaves the smaller ones to the next
+// piece. Piece values stay in {0} u [8, 256], so products (E2M1 x E4M3, 6 significant bits) span at
+// most 8 binades and every block sum is exact; each piece takes at least 4 bits off the residual, and
+// pieces stop once it is below 2^-20 of the block's maximum (5 pieces at most). y then differs from
+// the f32 GEMV by the fp32 accumulation order and that 2^-20 remainder.
+//
+// MFMA operand layout (16x16x128, measured on gfx950): A (fp4, 16 bytes per lane): lane g*16 + r
+// holds row r, K = 32 g + j at nibble j (low nibble first). B (fp8, 32 bytes per lane): lane g*16 + n
+// holds column n, K = 16 g + b at bytes b < 16 and K = 64 + 16 g + (b - 16) at bytes b >= 16. Scales:
+// lane g*16 + r (+n) gives the scale of 32-block g. C: lane g*16 + n holds rows 4 g .. 4 g + 3 of
+// column n. A weight block (16 code bytes: byte i holds weights i and 16 + i) is one lane's A data,
+// so piece byte j of a block holds activation (j >> 1) + 16 (j & 1).
+#include <hip/hip_runtime.h>
+
+#include <cstring>
+
+#include "anneau.hpp"
+#include "chrono.hpp"
+#include "commun.hpp"
+#include "erreurs.hpp"
+#include "fusion_corps.hpp"
+#include "selection.hpp"
+
+namespace trc {
+
+constexpr uint32_t PF_FILS = 1024;        // 16 wavefronts: 32 tiles decoded per band
+constexpr uint32_t PF_NMAX = 16;          // macro-steps per CODES_CTX tile held in registers
+constexpr uint32_t PF_PIECES = 5;         // fp8 pieces per activation block
+constexpr uint32_t PF_BP_MAX = 128;       // padded blocks per row (4096 columns)
+constexpr uint32_t PF_PAIRES_MAX = 16384; // positions x k per call
+constexpr uint32_t PF_TRANCHES = 4;       // chunks of the pair list per expert in prefill_grouper
+constexpr uint32_t ECHELLE_UN = 127u;     // E8M0 1.0
+
+// LDS of prefill_mfma after the decode (the LUT, x and ring regions are free then; the block
+// entries at LDS_ENT are still read while the codes are stored).
+constexpr uint32_t PF_A = 0;                            // codes [RB][Bp][16 B]
+constexpr uint32_t PF_SA = 32u * PF_BP_MAX * 16u;       // scales [RB][Bp]
+constexpr uint32_t PF_PART = PF_SA + 32u * PF_BP_MAX;   // partial sums: 16 waves x 2 x 64 lanes x 16 B
+static_assert(PF_PART + 16u * 2u * 64u * 16u <= LDS_ENT, "prefill LDS regions");
+
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+
+struct ParamsPrefill {
+    uint64_t repertoire;   // MatricePartie[E][3] of the mounted layer
+    uint64_t ech;          // block entries of matrix (e, j) at ech + (e*3 + j) * pas_ech
+    uint64_t pas_ech;
+    uint64_t compte;       // u32[E] pairs per expert
+    uint64_t debut;        // u32[E] first pair of expert e in `paires`
+    uint64_t paires;       // u32[T*k] pair c = i*k + slot, grouped by expert
+    uint64_t pieces;       // u32[4]: [0] pieces used by x, [1] by act
+    uint64_t indices;      // u32[T*k] chosen experts
+    uint64_t poids;        // f32[T*k] their weights
+    uint64_t x;            // f32[T][C]
+    uint64_t residus;      // f32[T][D]
+    uint64_t xq, xs;       // x pieces: xq[((i*PF_PIECES + p)*bp[0] + b)*32], xs[(i*PF_PIECES + p)*bp[0] + b]
+    uint64_t gu;           // f32[T*k][2][R]
+    uint64_t aq, as;       // act pieces per pair, bp[2] blocks per row
+    uint64_t s;            // f32[T*k][D]
+    uint32_t lignes[3], colonnes[3];
+    uint32_t bp[3];        // padded blocks per row (multiple of 4)
+    uint32_t rb[3];        // rows per band (16 or 32)
+    uint32_t T, k, E, D;
+};
+
+// Splits 32 values (natural order a[0..31]) into pieces: writes PF_PIECES x 32 bytes (piece stride
+// `pas_q` bytes, byte j = value (j >> 1) + 16 (j & 1)) and PF_PIECES scale bytes (stride `pas_s`);
+// returns the pieces used.
+__device__ __forceinline__ uint32_t pieces_bloc(const float (&a)[32], uint8_t* q, uint64_t pas_q, uint8_t* sc,
+                                                uint64_t pas_s) {
+    float r[32];
+#pragma unroll
+    for (uint32_t j = 0; j < 32; ++j) r[j] = a[(j >> 1) + 16u * (j & 1u)];
+    float m0 = 0.0f;
+#pragma unroll
+    for (uint32_t j = 0; j < 32; ++j) m0 = fmaxf(m0, fabsf(r[j]));
+    const float seuil = m0 * 0x1p-20f;
+    uint32_t P = 0;
+    for (uint32_t p = 0; p < PF_PIECES; ++p) {
+        float mr = 0.0f;
+#pragma unroll
+        for (uint32_t j = 0; j < 32; ++j) mr = fmaxf(mr, fabsf(r[j]));
+        const int E = int((__float_as_uint(mr) >> 23) & 255u) - 127;
+        const bool fini = !(mr > seuil) || E < -119;
+        u32x4 mots[2] = {u32x4{0u, 0u, 0u, 0u}, u32x4{0u, 0u, 0u, 0u}};
+        int k = 0;
+        if (!fini) {
+            k = E - 7;  // |r| 2^-k < 256
+#pragma unroll
+            for (uint32_t g = 0; g < 8; ++g) {
+                float v[4];
+#pragma unroll
+                for (uint32_t i = 0; i < 4; ++i) {
+                    const float t = __builtin_amdgcn_ldexpf(r[4 * g + i], -k);
+                    v[i] = fabsf(t) >= 8.0f ? t : 0.0f;  // smaller values wait for the next piece
+                }
+                int w = __builtin_amdgcn_cvt_pk_fp8_f32(v[0], v[1], 0, false);
+                w = __builtin_amdgcn_cvt_pk_fp8_f32(v[2], v[3], w, true);
+                r[4 * g + 0] -= __builtin_amdgcn_ldexpf(__builtin_amdgcn_cvt_f32_fp8(w, 0), k);  // exact
+                r[4 * g + 1] -= __builtin_amdgcn_ldexpf(__builtin_amdgcn_cvt_f32_fp8(w, 1), k);
+                r[4 * g + 2] -= __builtin_amdgcn_ldexpf(__builtin_amdgcn_cvt_f32_fp8(w, 2), k);
+                r[4 * g + 3] -= __builtin_amdgcn_ldexpf(__builtin_amdgcn_cvt_f32_fp8(w, 3), k);
+                mots[g >> 2][g & 3u] = uint32_t(w);
+            }
+            P = p + 1;
+        }
+        *reinterpret_cast<u32x4*>(q + p * pas_q) = mots[0];
+        *reinterpret_cast<u32x4*>(q + p * pas_q + 16) = mots[1];
+        sc[p * pas_s] = uint8_t(fini ? ECHELLE_UN : uint32_t(k + 127));
+    }
+    return P;
+}
+
+__device__ __forceinline__ uint32_t max_vague(uint32_t v) {
+#pragma unroll
+    for (int d = 32; d > 0; d >>= 1) v = max(v, uint32_t(__shfl_xor(int(v), d)));
+    return v;
+}
+
+}  // namespace trc
+
+using trc::ParamsPrefill;
+
+// One block of 1024 threads: thread (chunk c, expert e) counts and then lists the pairs of chunk c
+// that chose e; chunks are concatenated in order, so each expert's pairs keep position order. Also
+// clears the piece counters of the call. Indices >= E are format errors (the reference bails,
+// trc-ordo/src/lib.rs:817-819) and join no list.
+extern "C" __global__ void __launch_bounds__(1024)
+prefill_grouper(ParamsPrefill pp, uint32_t* __restrict__ controle) {
+    using namespace trc;
+    __shared__ uint32_t idx[PF_PAIRES_MAX];
+    __shared__ uint32_t cpt[PF_TRANCHES][EXPERTS_MAX];
+    __shared__ uint32_t deb[EXPERTS_MAX];
+    const uint32_t n = pp.T * pp.k, E = pp.E;
+    const uint32_t* indices = reinterpret_cast<const uint32_t*>(pp.indices);
+    uint32_t mauvais = 0;
+    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
+        const uint32_t v = indices[i];
+        idx[i] = v;
+        mauvais += v >= E ? 1u : 0u;
+    }
+    if (threadIdx.x < 4u) reinterpret_cast<uint32_t*>(pp.pieces)[threadIdx.x] = 0u;
+    mauvais = somme_vague_u32(mauvais);
+    if (__lane_id() == 0 && mauvais) atomicAdd(&controle[CTL_FORMAT], mauvais);
+    __syncthreads();
+    const uint32_t e = threadIdx.x % EXPERTS_MAX, c = threadIdx.x / EXPERTS_MAX;
+    const uint32_t lo = uint32_t(uint64_t(c) * n / PF_TRANCHES), hi = uint32_t(uint64_t(c + 1) * n / PF_TRANCHES);
+    uint32_t nb = 0;
+    if (e < E)
+        for (uint32_t i = lo; i < hi; ++i) nb += idx[i] == e ? 1u : 0u;
+    cpt[c][e] = nb;
+    __syncthreads();
+    if (threadIdx.x < 64u) {  // exclusive prefix over experts, 4 per lane
+        uint32_t tot[EXPERTS_MAX / 64];
+        uint32_t local = 0;
+#pragma unroll
+        for (uint32_t q = 0; q < EXPERTS_MAX / 64; ++q) {
+            const uint32_t ee = threadIdx.x * (EXPERTS_MAX / 64) + q;
+            uint32_t t = 0;
+            for (uint32_t cc = 0; cc < PF_TRANCHES; ++cc) t += cpt[cc][ee];
+            tot[q] = t;
+            local += t;
+        }
+        uint32_t incl = local;
+        for (int d = 1; d < 64; d <<= 1) {
+            const uint32_t t = uint32_t(__shfl_up(int(incl), d));
+            if (int(threadIdx.x) >= d) incl += t;
+        }
+        uint32_t s = incl - local;
+#pragma unroll
+        for (uint32_t q = 0; q < EXPERTS_MAX / 64; ++q) {
+            const uint32_t ee = threadIdx.x * (EXPERTS_MAX / 64) + q;
+            deb[ee] = s;
+            if (ee < E) {
+                reinterpret_cast<uint32_t*>(pp.debut)[ee] = s;
+                reinterpret_cast<uint32_t*>(pp.compte)[ee] = tot[q];
+            }
+            s += tot[q];
+        }
+    }
+    __syncthreads();
+    if (e < E) {
+        uint32_t pos = deb[e];
+        for (uint32_t cc = 0; cc < c; ++cc) pos += cpt[cc][e];
+        uint32_t* paires = reinterpret_cast<uint32_t*>(pp.paires);
+        for (uint32_t i = lo; i < hi; ++i)
+            if (idx[i] == e) paires[pos++] = i;
+    }
+}
+
+// x pieces: block (position i), thread b = column block b (padding blocks b >= B get zeros).
+extern "C" __global__ void __launch_bounds__(trc::PF_BP_MAX)
+prefill_quant_x(ParamsPrefill pp) {
+    using namespace trc;
+    const uint32_t i = blockIdx.x, b = threadIdx.x;
+    const uint32_t C = pp.colonnes[0], B = C / 32u, Bp = pp.bp[0];
+    uint32_t P = 0;
+    if (b < Bp) {
+        float a[32];
+        const gptr<f32x4> x4 = glob<f32x4>(reinterpret_cast<const float*>(pp.x) + uint64_t(i) * C + 32u * b);
+#pragma unroll
+        for (uint32_t g = 0; g < 8; ++g) {
+            f32x4 v = {0.f, 0.f, 0.f, 0.f};
+            if (b < B) v = x4[g];
+            a[4 * g] = v.x;
+            a[4 * g + 1] = v.y;
+            a[4 * g + 2] = v.z;
+            a[4 * g + 3] = v.w;
+        }
+        const uint64_t base = uint64_t(i) * PF_PIECES * Bp + b;
+        P = pieces_bloc(a, reinterpret_cast<uint8_t*>(pp.xq) + base * 32u, uint64_t(Bp) * 32u,
+                        reinterpret_cast<uint8_t*>(pp.xs) + base, Bp);
+    }
+    P = max_vague(P);
+    if (__lane_id() == 0 && P) atomicMax(reinterpret_cast<uint32_t*>(pp.pieces), P);
+}
+
+// act pieces: block (pair c), thread b = block b of act = swiglu_oai(gate, up) rows 32b .. 32b+31.
+extern "C" __global__ void __launch_bounds__(trc::PF_BP_MAX)
+prefill_swiglu_quant(ParamsPrefill pp) {
+    using namespace trc;
+    const uint32_t c = blockIdx.x, b = threadIdx.x;
+    const uint32_t R = pp.lignes[0], B2 = R / 32u, Bp = pp.bp[2];
+    if (reinterpret_cast<const uint32_t*>(pp.indices)[c] >= pp.E) return;
+    uint32_t P = 0;
+    if (b < Bp) {
+        float a[32];
+        const float* g = reinterpret_cast<const float*>(pp.gu) + uint64_t(c) * 2u * R;
+        const float* u = g + R;
+#pragma unroll
+        for (uint32_t t = 0; t < 32; ++t) a[t] = 0.0f;
+        if (b < B2) {
+#pragma unroll
+            for (uint32_t t = 0; t < 32; ++t) a[t] = swiglu_oai_f(g[32u * b + t], u[32u * b + t]);
+        }
+        const uint64_t base = uint64_t(c) * PF_PIECES * Bp + b;
+        P = pieces_bloc(a, reinterpret_cast<uint8_t*>(pp.aq) + base * 32u, uint64_t(Bp) * 32u,
+                        reinterpret_cast<uint8_t*>(pp.as) + base, Bp);
+    }
+    P = max_vague(P);
+    if (__lane_id() == 0 && P) atomicMax(reinterpret_cast<uint32_t*>(pp.pieces) + 1, P);
+}
+
+namespace trc {
+
+// One band of rows [r0, r0 + nl) of matrix j of expert e against the expert's pairs.
+template <uint32_t J>
+__device__ __forceinline__ void prefill_bande(const ParamsPrefill& pp, const uint32_t* __restrict__ luts,
+                                              uint32_t* __restrict__ controle, uint8_t* lds) {
+    const uint32_t e = blockIdx.y / J, j = J == 2u ? (blockIdx.y & 1u) : 2u;
+    const uint32_t n_e = uniforme32(reinterpret_cast<const uint32_t*>(pp.compte)[e]);
+    if (n_e == 0u) return;
+    const uint32_t R = choisir(pp.lignes, j), C = choisir(pp.colonnes, j), B = C / 32u;
+    const uint32_t Bp = choisir(pp.bp, j), RB = choisir(pp.rb, j);
+    const uint32_t r0 = blockIdx.x * RB;
+    if (r0 >= R) return;
+    const uint32_t nl = min(RB, R - r0);
+    const uint32_t* lut_src = luts + (uint64_t(j) * 4u + 1u) * M;
+    ChargeLut<3> charge_lut;
+    charge_lut.demarrer(lut_src, 3u * M / 4u);
+    const MatricePartie m = *reinterpret_cast<const MatricePartie*>(pp.repertoire + uint64_t(e * 3u + j) * sizeof(MatricePartie));
+    const EnteteRans h = entete_de(m.codes, m.cP, m.cN, m.cT, m.cW);
+    const uint32_t N = h.N;
+    const uint32_t ba = r0 * B, bb = (r0 + nl) * B;  // the band's blocks
+    const uint32_t t_a = N ? (ba / 8u) / N : 0u, t_b = N ? ((bb - 1u) / 8u) / N : 0u;
+    const bool bon = m.bon != 0u && N >= 1u && N <= PF_NMAX && t_b < h.T && t_b - t_a < 32u;
+    charge_lut.poser(lut_src, reinterpret_cast<uint2*>(lds + LDS_LUT), 3u * M / 4u);
+    if (!bon) {
+        if (blockIdx.x == 0 && threadIdx.x == 0) atomicAdd(&controle[CTL_FORMAT], 1u);
+        return;
+    }
+    __syncthreads();
+
+    // ---- decode: half-wavefront h2 of wave w decodes tile t_a + 2w + h2, codes in registers
+    const uint32_t lane = __lane_id();
+    const uint32_t v = lane & 31u;
+    const bool haut = lane >= 32u;
+    const uint32_t decal = haut ? 32u : 0u, masque_inf = (1u << v) - 1u;
+    const uint32_t q = v >> 2;
+    const uint32_t w = threadIdx.x >> 6;
+    const uint32_t demi = threadIdx.x >> 5;
+    const uint32_t base = adresse_lds(lds);
+    const uint32_t a_lut = base + LDS_LUT;
+    const uint32_t a_anneau = base + LDS_ANNEAUX + demi * OCTETS_ANNEAU;
+    const uint32_t a_ent = base + LDS_ENT + demi * (ENT_PAR_TUILE * 4u);
+    const uint32_t a_ent_q = a_ent + 4u * q;
+    const uint32_t t0 = t_a + 2u * w;
+    const uint32_t t = t0 + (haut ? 1u : 0u);
+    const bool vague_active = t0 <= t_b;
+    const bool tuile = t <= t_b;
+    const uint32_t nmacro = h.P / 128u;
+    const uint32_t nb_a = vague_active ? min(N, nmacro - t0 * N) : 0u;
+    const uint32_t nb_b = t0 + 1u <= t_b ? min(N, nmacro - (t0 + 1u) * N) : 0u;
+    const uint32_t nb = haut ? nb_b : nb_a;
+    const uint32_t m0 = t * N;
+    uint32_t codes[PF_NMAX];
+    uint32_t hors_l = 0, pointeur = 0;
+    if (vague_active) {
+        const gptr<u32x4> ent16 = glob<u32x4>(reinterpret_cast<const void*>(pp.ech + uint64_t(e * 3u + j) * pp.pas_ech));
+        if (tuile) ecrire_lds<u32x4>(a_ent + 16u * v, ent16[2u * m0 + v]);
+        uint32_t x = tuile ? h.etats[t * VOIES + v] : L;
+        const uint32_t debut = tuile ? h.debut[t] : 0u;
+        AnneauR a = ouvrir_anneau_r(h, m.codes, debut, a_anneau, v, tuile);
+        const uint32_t o0 = a.o2;
+        uint32_t ent_suiv = tuile ? lire_lds<uint32_t>(a_ent_q) : ENTREE_BOURRAGE;
+        const uint32_t nb_min = min(nb_a, nb_b);
+        auto macro = [&](auto tous, uint32_t mm) -> uint32_t {
+            constexpr bool TOUS = decltype(tous)::value;
+            const bool actif = TOUS || mm < nb;
+            const uint32_t ent = actif ? ent_suiv : ENTREE_BOURRAGE;
+            ent_suiv = lire_lds<uint32_t>(a_ent_q + 32u * ((mm + 1u) & 15u));
+            const uint32_t lt = a_lut + (ent & ENT_CTX);
+            uint32_t compte = 0;
+            const uint32_t e0 = pas_r<TOUS>(x, a.o2, compte, lt, a_anneau, decal, masque_inf, actif);
+            const uint32_t e1 = pas_r<TOUS>(x, a.o2, compte, lt, a_anneau, decal, masque_inf, actif);
+            const uint32_t e2 = pas_r<TOUS>(x, a.o2, compte, lt, a_anneau, decal, masque_inf, actif);
+            const uint32_t e3 = pas_r<TOUS>(x, a.o2, compte, lt, a_anneau, decal, masque_inf, actif);
+            a.o2 += 2u * compte;
+            avancer_anneau_r(a, v, actif);
+            // byte 3 of each LUT word is the decoded byte
+            return __builtin_amdgcn_perm(e1, e0, 0x0C0C0703u) | __builtin_amdgcn_perm(e3, e2, 0x07030C0Cu);
+        };
+#pragma unroll
+        for (uint32_t mm = 0; mm < PF_NMAX; ++mm) {
+            if (mm < nb_min)
+                codes[mm] = macro(std::true_type{}, mm);
+            else if (mm < nb_a)
+                codes[mm] = macro(std::false_type{}, mm);
+            else
+                codes[mm] = 0u;
+        }
+        // a tile is checked by the band that holds its first block
+        if (tuile && m0 * 8u >= ba) {
+            hors_l += (x != L) ? 1u : 0u;
+            const uint32_t attendu = (t + 1 < h.T) ? h.debut[t + 1] : h.W;
+            pointeur += (v == 0 && debut + (a.o2 - o0) / 2u != attendu) ? 1u : 0u;
+        }
+    }
+    verser_controle(controle, hors_l, pointeur);
+    __syncthreads();  // every tile decoded: the LUT, x and ring regions are free
+
+    // ---- store the band's codes and scales: codes [row][Bp][16 B], scales [row][Bp]
+    if (vague_active && tuile) {
+        uint32_t beta = 8u * m0 + q;
+        uint32_t ligne = beta / B, blk = beta - ligne * B;
+#pragma unroll
+        for (uint32_t mm = 0; mm < PF_NMAX; ++mm) {
+            if (mm < nb && beta >= ba && beta < bb) {
+                const uint32_t o = (ligne - r0) * Bp + blk;
+                ecrire_lds<uint32_t>(base + PF_A + 16u * o + 4u * (v & 3u), codes[mm]);
+                if ((v & 3u) == 0u) {
+                    const uint32_t ent = lire_lds<uint32_t>(a_ent_q + 32u * mm);
+                    ecrire_lds<uint8_t>(base + PF_SA + o, uint8_t((ent >> ENT_EXP) + 128u));
+                }
+            }
+            beta += 8u;
+            blk += 8u;
+            if (blk >= B) {  // B >= 8: one row at most
+                blk -= B;
+                ++ligne;
+            }
+        }
+    }
+    for (uint32_t i = threadIdx.x; i < RB * Bp; i += blockDim.x) {  // padding blocks and rows
+        const uint32_t rl = i / Bp, blk = i - rl * Bp;
+        if (blk >= B || rl >= nl) {
+            ecrire_lds<u32x4>(base + PF_A + 16u * i, u32x4{0u, 0u, 0u, 0u});
+            ecrire_lds<uint8_t>(base + PF_SA + i, uint8_t(ECHELLE_UN));
+        }
+    }
+    __syncthreads();
+
+    // ---- MFMA: wave w takes the k-steps ks = w, w + 16 (4 blocks each) of both 16-row tiles for
+    // every 16-pair tile; the 16 waves' partial sums are added in wave order.
+    const uint32_t nks = Bp / 4u, nrt = RB / 16u;
+    const uint32_t lr = lane & 15u, lg = lane >> 4;
+    u32x4 af[2][2];
+    uint32_t sa[2][2];
+#pragma unroll
+    for (uint32_t rt = 0; rt < 2; ++rt)
+#pragma unroll
+        for (uint32_t i = 0; i < 2; ++i) {
+            const uint32_t ks = w + 16u * i;
+            if (rt < nrt && ks < nks) {
+                const uint32_t o = (16u * rt + lr) * Bp + 4u * ks + lg;
+                af[rt][i] = lire_lds<u32x4>(base + PF_A + 16u * o);
+                sa[rt][i] = lire_lds<uint8_t>(base + PF_SA + o);
+            } else {
+                af[rt][i] = u32x4{0u, 0u, 0u, 0u};
+                sa[rt][i] = ECHELLE_UN;
+            }
+        }
+    const uint32_t P = uniforme32(min(reinterpret_cast<const uint32_t*>(pp.pieces)[J == 2u ? 0 : 1], PF_PIECES));
+    const uint32_t debut_e = uniforme32(reinterpret_cast<const uint32_t*>(pp.debut)[e]);
+    const uint32_t* paires = reinterpret_cast<const uint32_t*>(pp.paires);
+    const uint8_t* bq = reinterpret_cast<const uint8_t*>(J == 2u ? pp.xq : pp.aq);
+    const uint8_t* bs = reinterpret_cast<const uint8_t*>(J == 2u ? pp.xs : pp.as);
+    const float* biais = reinterpret_cast<const float*>(m.biais.p);
+    // this lane's B bytes 0-15: half (lg & 1) of block 4 ks + (lg >> 1); bytes 16-31: of block
+    // 4 ks + 2 + (lg >> 1); its scale: block 4 ks + lg
+    const uint32_t demi_b = 16u * (lg & 1u), bloc_b = lg >> 1;
+    const uint32_t n_tt = (n_e + 15u) / 16u;
+    for (uint32_t tt = 0; tt < n_tt; ++tt) {
+        const uint32_t tok = 16u * tt + lr;
+        const bool valide = tok < n_e;
+        const uint32_t c = valide ? paires[debut_e + tok] : 0u;
+        const uint32_t src = J == 2u ? c / pp.k : c;
+        const uint64_t ligne_b = uint64_t(src) * PF_PIECES * Bp;
+        f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (uint32_t i = 0; i < 2; ++i) {
+            const uint32_t ks = w + 16u * i;
+            if (ks >= nks) continue;  // wave-uniform
+            for (uint32_t p = 0; p < P; ++p) {
+                const uint64_t o = ligne_b + uint64_t(p) * Bp + 4u * ks;
+                u32x4 b0 = {0u, 0u, 0u, 0u}, b1 = {0u, 0u, 0u, 0u};
+                uint32_t sb = ECHELLE_UN;
+                if (valide) {
+                    b0 = *glob<u32x4>(bq + (o + bloc_b) * 32u + demi_b);
+                    b1 = *glob<u32x4>(bq + (o + 2u + bloc_b) * 32u + demi_b);
+                    sb = bs[o + lg];
+                }
+                const i32x8 rb = {int(b0.x), int(b0.y), int(b0.z), int(b0.w), int(b1.x), int(b1.y), int(b1.z), int(b1.w)};
+                const i32x8 ra0 = {int(af[0][i].x), int(af[0][i].y), int(af[0][i].z), int(af[0][i].w), 0, 0, 0, 0};
+                acc0 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ra0, rb, acc0, 4, 0, 0, int(sa[0][i]), 0,
+                                                                        int(sb));
+                if (nrt == 2u) {
+                    const i32x8 ra1 = {int(af[1][i].x), int(af[1][i].y), int(af[1][i].z), int(af[1][i].w), 0, 0, 0, 0};
+                    acc1 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ra1, rb, acc1, 4, 0, 0, int(sa[1][i]),
+                                                                            0, int(sb));
+                }
+            }
+        }
+        ecrire_lds<f32x4>(base + PF_PART + ((w * 2u + 0u) * 64u + lane) * 16u, acc0);
+        ecrire_lds<f32x4>(base + PF_PART + ((w * 2u + 1u) * 64u + lane) * 16u, acc1);
+        __syncthreads();
+        if (threadIdx.x < nrt * 256u) {
+            const uint32_t rt = threadIdx.x >> 8, reste = threadIdx.x & 255u;
+            const uint32_t ln = reste >> 2, r = reste & 3u;
+            float s = 0.0f;
+            for (uint32_t ww = 0; ww < 16u; ++ww)
+                s += lire_lds<float>(base + PF_PART + ((ww * 2u + rt) * 64u + ln) * 16u + 4u * r);
+            const uint32_t ligne = 16u * rt + 4u * (ln >> 4) + r, jeton = 16u * tt + (ln & 15u);
+            if (ligne < nl && jeton < n_e) {
+                const uint32_t cc = paires[debut_e + jeton];
+                const float y = s + biais[r0 + ligne];
+                if (J == 2u)
+                    reinterpret_cast<float*>(pp.gu)[(uint64_t(cc) * 2u + j) * R + r0 + ligne] = y;
+                else
+                    reinterpret_cast<float*>(pp.s)[uint64_t(cc) * pp.D + r0 + ligne] = y;
+            }
+        }
+        __syncthreads();
+    }
+}
+
+}  // namespace trc
+
+extern "C" __global__ void __launch_bounds__(trc::PF_FILS)
+prefill_mfma_gu(ParamsPrefill pp, const uint32_t* __restrict__ luts, uint32_t* __restrict__ controle) {
+    __shared__ __attribute__((aligned(16384))) uint8_t lds[trc::LDS_GEMV];
+    trc::prefill_bande<2>(pp, luts, controle, lds);
+}
+
+extern "C" __global__ void __launch_bounds__(trc::PF_FILS)
+prefill_mfma_bas(ParamsPrefill pp, const uint32_t* __restrict__ luts, uint32_t* __restrict__ controle) {
+    __shared__ __attribute__((aligned(16384))) uint8_t lds[trc::LDS_GEMV];
+    trc::prefill_bande<1>(pp, luts, controle, lds);
+}
+
+// x_i[r] += ((w0 s_i0[r] + w1 s_i1[r]) + w2 s_i2[r]) + ..., each product and sum rounded on its own
+// (combiner_pos, trc-modele/src/lib.rs:706-710 -> passe.cuh:611-622); positions whose experts are
+// not all valid, mounted matrices are left alone.
+extern "C" __global__ void __launch_bounds__(256)
+prefill_combiner(ParamsPrefill pp) {
+#pragma clang fp contract(off)
+    using namespace trc;
+    const uint32_t i = blockIdx.y, r = blockIdx.x * 256u + threadIdx.x;
+    const uint32_t k = pp.k, D = pp.D;
+    const uint32_t* idx = reinterpret_cast<const uint32_t*>(pp.indices) + uint64_t(i) * k;
+    bool ok = true;
+    for (uint32_t s = 0; s < k; ++s) {
+        const uint32_t e = idx[s];
+        ok = ok && e < pp.E;
+        if (ok)
+            for (uint32_t j = 0; j < 3; ++j)
+                ok = ok && reinterpret_cast<const MatricePartie*>(pp.repertoire)[e * 3u + j].bon != 0u;
+    }
+    if (!ok || r >= D) return;
+    const float* w = reinterpret_cast<const float*>(pp.poids) + uint64_t(i) * k;
+    const float* s = reinterpret_cast<const float*>(pp.s) + uint64_t(i) * k * D;
+    float acc = w[0] * s[r];
+    for (uint32_t q = 1; q < k; ++q) {
+        const float p = w[q] * s[uint64_t(q) * D + r];
+        acc = acc + p;
+    }
+    float* x = reinterpret_cast<float*>(pp.residus) + uint64_t(i) * D;
+    x[r] = x[r] + acc;
+}
+
+// ============================================================================ C-ABI launch layer
+namespace trc {
+int lancer_echelles_prefill(const ParamsMoe& pm, uint32_t R, uint32_t C, uint32_t n_delta, const uint32_t* luts,
+                            uint32_t* ctl, hipStream_t f);
+uint64_t octets_entrees(uint32_t R, uint32_t C);
+}  // namespace trc
+
+namespace {
+
+using trc::usage;
+
+uint64_t al(uint64_t x) { return (x + 255u) & ~uint64_t(255); }
+uint32_t bp_de(uint32_t C) { return ((C / 32u + 3u) / 4u) * 4u; }
+
+// Rows per band such that a band's CODES_CTX tiles (N macro-steps of 8 blocks each) fit the 32
+// tiles a block decodes: 32 rows when they do, else 16, else 0.
+uint32_t rb_de(uint32_t B, uint32_t N) {
+    for (uint32_t rb = 32; rb >= 16; rb -= 16)
+        if ((rb * B - 1u) / (8u * N) + 2u <= 32u) return rb;
+    return 0;
+}
+
+struct Disposition {
+    uint64_t pieces, compte, debut, paires, ech, pas_ech, xq, xs, gu, aq, as, s, total;
+};
+
+int disposer(const trc_dims_expert* dims, uint32_t E, uint32_t T, uint32_t k, uint32_t n_codes, Disposition& d) {
+    if (dims == nullptr) return usage("dims absent");
+    int r = trc_dims_verifier(dims);
+    if (r != TRC_OK) return r;
+    const uint32_t R = dims->lignes[0], C = dims->colonnes[0], D = dims->lignes[2];
+    if (dims->lignes[1] != R || dims->colonnes[1] != C || dims->colonnes[2] != R)
+        return usage("gate, up et down incompatibles");
+    if (D != C) return usage("la sortie des experts (%u) doit avoir la taille de x (%u)", D, C);
+    if (C > 32u * trc::PF_BP_MAX || R > 32u * trc::PF_BP_MAX)
+        return usage("prefill : au plus %u colonnes (%u x %u)", 32u * trc::PF_BP_MAX, R, C);
+    for (int j = 0; j < 3; ++j)
+        if (dims->colonnes[j] / 32 < 8) return usage("matrice %d : moins de 8 blocs par ligne", j);
+    if (n_codes == 0 || n_codes > trc::PF_NMAX)
+        return usage("prefill : N de CODES_CTX %u (1 a %u macro-pas par tuile)", n_codes, trc::PF_NMAX);
+    for (int j = 0; j < 3; ++j)
+        if (rb_de(dims->colonnes[j] / 32, n_codes) == 0) return usage("prefill : N = %u trop petit", n_codes);
+    if (E == 0 || E > trc::EXPERTS_MAX || k == 0 || k > trc::TOPK_MAX || k > E) return usage("top-%u sur %u", k, E);
+    if (T == 0 || uint64_t(T) * k > trc::PF_PAIRES_MAX)
+        return usage("prefill : %u positions x %u (au plus %u paires)", T, k, trc::PF_PAIRES_MAX);
+    const uint32_t Rm = D > R ? D : R;
+    const uint64_t n = uint64_t(T) * k;
+    const uint64_t bp0 = bp_de(C), bp2 = bp_de(R);
+    uint64_t p = 0;
+    d.pieces = p;
+    p += al(16);
+    d.compte = p;
+    p += al(4ull * E);
+    d.debut = p;
+    p += al(4ull * E);
+    d.paires = p;
+    p += al(4ull * n);
+    d.pas_ech = trc::octets_entrees(Rm, C);
+    d.ech = p;
+    p += 3ull * E * d.pas_ech;
+    d.xq = p;
+    p += al(32ull * T * trc::PF_PIECES * bp0);
+    d.xs = p;
+    p += al(1ull * T * trc::PF_PIECES * bp0);
+    d.gu = p;
+    p += al(4ull * n * 2u * R);
+    d.aq = p;
+    p += al(32ull * n * trc::PF_PIECES * bp2);
+    d.as = p;
+    p += al(1ull * n * trc::PF_PIECES * bp2);
+    d.s = p;
+    p += al(4ull * n * D);
+    d.total = p;
+    return TRC_OK;
+}
+
+}  // namespace
+
+extern "C" uint64_t trc_taille_travail_prefill(const trc_dims_expert* dims, uint32_t experts, uint32_t positions,
+                                               uint32_t k, uint32_t n_codes) {
+    Disposition d;
+    if (disposer(dims, experts, positions, k, n_codes, d) != TRC_OK) return 0;
+    return d.total;
+}
+
+// Config 5: batched prefill of one resident MoE layer. For each position i < T, slot q < k:
+// s_iq = W_down swiglu(W_gate x_i + b_gate, W_up x_i + b_up) + b_down of expert indices[i*k + q],
+// then residus_i += ((w_i0 s_i0 + w_i1 s_i1) + ...). Each chosen expert is decoded once, by bands of
+// rows, and applied to all its positions on the MFMA. No host sync.
+extern "C" int trc_prefill_moe(trc_vue repertoire, uint32_t experts, trc_vue luts, const trc_dims_expert* dims,
+                               trc_vue x, uint32_t positions, trc_vue indices, trc_vue poids, uint32_t k,
+                               trc_vue residus, trc_vue controle, trc_vue travail, uint32_t n_delta,
+                               uint32_t n_codes, void* flux) {
+    Disposition d;
+    int r = disposer(dims, experts, positions, k, n_codes, d);
+    if (r != TRC_OK) return r;
+    const uint32_t R = dims->lignes[0], C = dims->colonnes[0], D = dims->lignes[2], T = positions;
+    TRC_VERIFIER(n_delta > 0 && n_delta <= 65535, "N de DELTA %u", n_delta);
+    TRC_VERIFIER(repertoire.adresse && repertoire.octets >= 3ull * experts * sizeof(trc::MatricePartie) &&
+                     repertoire.adresse % 16 == 0,
+                 "repertoire trop court ou non aligne sur 16");
+    TRC_VERIFIER(luts.adresse && luts.octets >= uint64_t(trc::LUTS_PAR_COUCHE) * 4, "LUT trop courtes");
+    TRC_VERIFIER(x.adresse && x.octets >= 4ull * T * C && x.adresse % 16 == 0, "x trop court ou non aligne");
+    TRC_VERIFIER(indices.adresse && indices.octets >= 4ull * T * k && poids.adresse && poids.octets >= 4ull * T * k,
+                 "indices ou poids trop courts");
+    TRC_VERIFIER(residus.adresse && residus.octets >= 4ull * T * D, "residus trop courts");
+    TRC_VERIFIER(controle.adresse && controle.octets >= 16, "controle de moins de 16 o");
+    TRC_VERIFIER(travail.adresse && travail.octets >= d.total && travail.adresse % 256 == 0,
+                 "travail de %llu o, %llu o demandes (aligne sur 256)", (unsigned long long)travail.octets,
+                 (unsigned long long)d.total);
+    const uint64_t b = travail.adresse;
+    ParamsPrefill pp;
+    std::memset(&pp, 0, sizeof(pp));
+    pp.repertoire = repertoire.adresse;
+    pp.ech = b + d.ech;
+    pp.pas_ech = d.pas_ech;
+    pp.compte = b + d.compte;
+    pp.debut = b + d.debut;
+    pp.paires = b + d.paires;
+    pp.pieces = b + d.pieces;
+    pp.indices = indices.adresse;
+    pp.poids = poids.adresse;
+    pp.x = x.adresse;
+    pp.residus = residus.adresse;
+    pp.xq = b + d.xq;
+    pp.xs = b + d.xs;
+    pp.gu = b + d.gu;
+    pp.aq = b + d.aq;
+    pp.as = b + d.as;
+    pp.s = b + d.s;
+    for (int j = 0; j < 3; ++j) {
+        pp.lignes[j] = dims->lignes[j];
+        pp.colonnes[j] = dims->colonnes[j];
+        pp.bp[j] = bp_de(dims->colonnes[j]);
+        pp.rb[j] = rb_de(dims->colonnes[j] / 32, n_codes);
+    }
+    pp.T = T;
+    pp.k = k;
+    pp.E = experts;
+    pp.D = D;
+
+    trc::ParamsMoe pm;
+    std::memset(&pm, 0, sizeof(pm));
+    pm.repertoire = repertoire.adresse;
+    pm.ech = pp.ech;
+    pm.pas = d.pas_ech;
+    pm.compte = pp.compte;
+    pm.k = k;
+    pm.E = experts;
+    for (int j = 0; j < 3; ++j) {
+        pm.lignes[j] = dims->lignes[j];
+        pm.colonnes[j] = dims->colonnes[j];
+    }
+    const hipStream_t f = reinterpret_cast<hipStream_t>(flux);
+    auto ctl = reinterpret_cast<uint32_t*>(controle.adresse);
+    const uint32_t* l = reinterpret_cast<const uint32_t*>(luts.adresse);
+    const uint32_t Rm = D > R ? D : R;
+    TRC_LANCER(prefill_grouper, dim3(1), dim3(1024), f, pp, ctl);
+    TRC_LANCER(prefill_quant_x, dim3(T), dim3(trc::PF_BP_MAX), f, pp);
+    r = trc::lancer_echelles_prefill(pm, Rm, C, n_delta, l, ctl, f);
+    if (r != TRC_OK) return r;
+    TRC_LANCER(prefill_mfma_gu, dim3((R + pp.rb[0] - 1) / pp.rb[0], 2 * experts), dim3(trc::PF_FILS), f, pp, l, ctl);
+    TRC_LANCER(prefill_swiglu_quant, dim3(T * k), dim3(trc::PF_BP_MAX), f, pp);
+    TRC_LANCER(prefill_mfma_bas, dim3((D + pp.rb[2] - 1) / pp.rb[2], experts), dim3(trc::PF_FILS), f, pp, l, ctl);
+    TRC_LANCER(prefill_combiner, dim3((D + 255) / 256, T), dim3(256), f, pp);
+    return TRC_OK;
+}

@@ -25,6 +25,10 @@ def _declarer(l):
     l.trc_taille_repertoire.argtypes = [C.c_uint32]
     l.trc_taille_repertoire.restype = C.c_uint64
     l.trc_monter_couche.argtypes = [V, C.c_uint32, C.POINTER(DimsExpert), V, V, C.c_void_p]
+    l.trc_taille_travail_prefill.argtypes = [C.POINTER(DimsExpert), C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32]
+    l.trc_taille_travail_prefill.restype = C.c_uint64
+    l.trc_prefill_moe.argtypes = [V, C.c_uint32, V, C.POINTER(DimsExpert), V, C.c_uint32, V, V, C.c_uint32, V, V, V,
+                                  C.c_uint32, C.c_uint32, C.c_void_p]
     l.trc_chrono.argtypes = [C.c_int]
     l.trc_chrono_recolter.argtypes = [C.c_char_p, C.POINTER(C.c_double), C.POINTER(C.c_uint64), C.c_int, C.c_int]
     l._trc_fusion = True
@@ -66,6 +70,10 @@ def taille_travail_couche(dims: DimsExpert, experts: int, k: int, n_codes: int) 
     return _l().trc_taille_travail_couche_moe(C.byref(dims), experts, k, n_codes)
 
 
+def taille_travail_prefill(dims: DimsExpert, experts: int, positions: int, k: int, n_codes: int) -> int:
+    return _l().trc_taille_travail_prefill(C.byref(dims), experts, positions, k, n_codes)
+
+
 def taille_repertoire(experts: int) -> int:
     """Bytes of a mounted layer's directory (trc_monter_couche)."""
     return _l().trc_taille_repertoire(experts)
@@ -99,3 +107,11 @@ class Fusion:
                                                  _vue(routeur_biais), _vue(x), k, _vue(residu), _vue(indices),
                                                  _vue(poids), _vue(controle), _vue(travail), n_delta, n_codes,
                                                  _flux(f)))
+
+    def prefill_moe(self, repertoire, experts: int, luts, dims: DimsExpert, x, positions: int, indices, poids, k: int,
+                    residus, controle, travail, n_delta: int, n_codes: int, f=None) -> None:
+        """Batched prefill of one resident layer: residus[i] += the weighted outputs of position i's
+        k experts (indices / poids: [positions][k])."""
+        _statut(self._l.trc_prefill_moe(_vue(repertoire), experts, _vue(luts), C.byref(dims), _vue(x), positions,
+                                        _vue(indices), _vue(poids), k, _vue(residus), _vue(controle), _vue(travail),
+                                        n_delta, n_codes, _flux(f)))
