@@ -10,7 +10,8 @@ line (fields described in DESIGN.md).
 
 Other measurement modes (not the driver's line): --config 1 (one down_proj matrix), --config 2 (one
 expert MLP), both rotating over the 128 experts; --config 4 (a token through L resident MoE layers,
-default 36, about 52 GB of parts).
+default 36, about 52 GB of parts); --config 5 (a batched prefill of 512 positions with Zipf routing,
+grouped GEMM on the block-scaled FP4 MFMA).
 """
 from __future__ import annotations
 
@@ -156,6 +157,133 @@ def baseline_cpu(couche, luts, x_tok, selections, budget_s: float, n_fils: int):
     }
 
 
+def routage_zipf(graine, T, E, k, a=1.1):
+    """Config 5 routing: per position k distinct experts drawn from Zipf(a) over the E expert ranks
+    without replacement (rank r = expert r), and softmax weights of seeded logits (f64, rounded once)."""
+    import numpy as np
+    rng = np.random.default_rng(graine)
+    p = 1.0 / np.arange(1, E + 1, dtype=np.float64) ** a
+    p /= p.sum()
+    idx = np.zeros((T, k), np.uint32)
+    w = np.zeros((T, k), np.float32)
+    for i in range(T):
+        idx[i] = rng.choice(E, size=k, replace=False, p=p)
+        lg = np.sort(rng.standard_normal(k))[::-1]
+        ex = np.exp(lg - lg[0])
+        w[i] = (ex / ex.sum()).astype(np.float32)
+    return idx, w
+
+
+def baseline_cpu_prefill(couche, luts, x_tok, idx, budget_s: float):
+    """The reference's CPU path for a prefill batch, timed on a sample and scaled: one
+    decoder_matrice_v10 of every distinct chosen expert, then per (position, slot) the f32 GEMV chain
+    (gate, up, SwiGLU, down) in the reference's order; single thread."""
+    sys.path.insert(0, str(RACINE / "tests"))
+    import numpy as np
+    import oracle_ffi as O
+    d = [O.disposition_j([2880] * 3, [2880] * 3, j) for j in range(3)]
+    distincts = sorted(set(int(e) for e in idx.reshape(-1)))
+    t0 = time.perf_counter()
+    slots = {}
+    for e in distincts:
+        slots[e], _ = O.decoder_expert(bytes(couche.partie(e)), luts, [2880] * 3, [2880] * 3)
+        if time.perf_counter() - t0 > budget_s / 3:
+            break
+    t_dec = (time.perf_counter() - t0) / len(slots)
+    t0 = time.perf_counter()
+    n = 0
+    for i in range(idx.shape[0]):
+        for q in range(idx.shape[1]):
+            e = int(idx[i, q])
+            if e not in slots:
+                continue
+            sl = slots[e]
+            g = O.gemv_mxfp4(sl[d[0].base:d[0].base + d[0].pas], x_tok[i % len(x_tok)], 2880, 2880)
+            u = O.gemv_mxfp4(sl[d[1].base:d[1].base + d[1].pas], x_tok[i % len(x_tok)], 2880, 2880)
+            O.gemv_mxfp4(sl[d[2].base:d[2].base + d[2].pas], O.swiglu_oai(g, u), 2880, 2880)
+            n += 1
+            if time.perf_counter() - t0 > 2 * budget_s / 3:
+                break
+        if time.perf_counter() - t0 > 2 * budget_s / 3:
+            break
+    t_chaine = (time.perf_counter() - t0) / max(n, 1)
+    total = len(distincts) * t_dec + idx.size * t_chaine
+    return {
+        "value": round(total * 1e6, 1), "unit": "us/batch", "cores": 1, "kind": "port",
+        "tokens_per_s": round(idx.shape[0] / total, 2),
+        "sample": f"{len(slots)} expert decodes ({t_dec * 1e3:.0f} ms each) and {n} GEMV chains "
+                  f"({t_chaine * 1e3:.1f} ms each), scaled to {len(distincts)} decodes + {idx.size} chains",
+    }
+
+
+def bench_prefill(args, c0, dims, E, k, C, fz, flux, dev, espace, x_tok, n_fils):
+    """Config 5: one batched prefill of `positions` tokens through the resident layer."""
+    import numpy as np
+    import torch
+
+    from troncons_amd import codeur, fusion
+    from troncons_amd.noyaux import VueCarte
+    V = VueCarte.de
+    T = args.positions
+    idx, w = routage_zipf(args.graine + 5, T, E, k)
+    xs = np.stack([codeur.synth_normale_bf16(args.graine, 6, t, C, 1.0) for t in range(T)])
+    xd = torch.from_numpy(xs).to(dev)
+    idd = torch.from_numpy(idx.view(np.int32)).to(dev)
+    wd = torch.from_numpy(w).to(dev)
+    res = torch.zeros((T, C), dtype=torch.float32, device=dev)
+    ctl = torch.zeros(4, dtype=torch.int32, device=dev)
+    _tr, tr = espace(fusion.taille_travail_prefill(dims, E, T, k, args.n_codes))
+
+    def pas(s):
+        fz.prefill_moe(c0.vrep, E, c0.vluts, dims, V(xd), T, V(idd), V(wd), k, V(res), V(ctl), tr,
+                       args.n_delta, args.n_codes, f=flux)
+
+    ms = temps(pas, args.steps, args.warmup, flux)
+    assert (ctl.cpu().numpy() == 0).all(), f"control words {ctl.cpu().numpy()}"
+    us = ms * 1e3 / args.steps
+    o = tr.adresse - _tr.data_ptr()  # the workspace starts with the piece counters (x, act)
+    pieces = _tr[o:o + 8].cpu().numpy().view(np.uint32)
+    noyaux = chrono_passes(fusion, pas, min(args.steps, 10))
+    kern = {nom: round(v[0] / v[1] * 1e3, 2) for nom, v in noyaux.items()}
+    comptes = np.bincount(idx.reshape(-1), minlength=E)
+    choisis = np.nonzero(comptes)[0]
+    octets = int(c0.utiles[choisis].sum())
+    octets_codes = int(c0.octets_codes[choisis].sum())
+    flops = 2.0 * 3 * C * C * idx.size
+    t_mfma = (kern.get("prefill_mfma_gu", 0.0) + kern.get("prefill_mfma_bas", 0.0)) * 1e-6
+    ligne = {
+        "metric": f"config5 us per {T}-position prefill batch (top-{k} of {E}, Zipf 1.1)",
+        "value": round(us, 1), "unit": "us/batch", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms / args.steps, 4), "higher_is_better": False, "scaling": "weak",
+        "vs_baseline": None, "dtype": "u32 rANS / fp4 x fp8-pieces MFMA, f32 accumulate",
+        "data": "synthetic (seeded MXFP4 law A, E8M0 in [119,125], bf16 N(0,1) activations, Zipf(1.1) routing)",
+        "config": {"workload": f"config5: batched prefill, {T} positions, top-{k} of {E} gpt-oss-120b experts "
+                               "(.trc v1.2 rANS-coded), each chosen expert decoded once into LDS, grouped GEMM "
+                               "on block-scaled FP4 MFMA", "positions": T, "experts": E, "k": k,
+                   "n_codes": args.n_codes, "n_delta": args.n_delta},
+        "tokens_per_s": round(T / (us * 1e-6), 1),
+        "experts_decoded": int(len(choisis)),
+        "per_expert_positions": {"max": int(comptes.max()), "median": float(np.median(comptes[choisis])),
+                                 "min": int(comptes[choisis].min())},
+        "compressed_bytes": octets,
+        "gbps_compressed": round(octets / (us * 1e-6) / 1e9, 1),
+        "useful_tflops": round(flops / (us * 1e-6) / 1e12, 2),
+        "fp8_pieces": {"x": int(pieces[0]), "act": int(pieces[1])},
+        "kernel_us": kern,
+        "roofline": {
+            "bound": "hbm", "kernel": "prefill_mfma (gate/up launch + down launch: decode + MFMA)",
+            "achieved": round(octets_codes / t_mfma / 1e9, 1) if t_mfma else None, "peak": PIC_HBM, "unit": "GB/s",
+            "frac": round(octets_codes / t_mfma / 1e9 / PIC_HBM, 4) if t_mfma else None, "traffic": None,
+            "mfma_useful_tflops": round(flops / t_mfma / 1e12, 2) if t_mfma else None,
+            "mfma_peak_tflops": 5000.0,
+        },
+        "setup_s": round(c0.t_gen, 1),
+    }
+    ligne["cpu_baseline"] = None if args.sans_cpu else baseline_cpu_prefill(c0.hote, c0.luts_np, xs, idx,
+                                                                             args.budget_cpu)
+    return ligne
+
+
 def chrono_passes(fusion, pas, n):
     """Per-kernel durations over n steps: every kernel launched with the start/stop events that the
     runtime records at the kernel's own start and end (hipExtLaunchKernel). Kept out of the timed
@@ -190,7 +318,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--config", type=int, default=3, choices=(1, 2, 3, 4))
+    ap.add_argument("--config", type=int, default=3, choices=(1, 2, 3, 4, 5))
+    ap.add_argument("--positions", type=int, default=512, help="positions of a --config 5 prefill batch")
     ap.add_argument("--couches", type=int, default=36, help="layers of --config 4")
     ap.add_argument("--experts", type=int, default=128)
     ap.add_argument("--k", type=int, default=4)
@@ -288,6 +417,11 @@ def main():
             "kernel_us": {nom_k: round(v[0] / v[1] * 1e3, 2) for nom_k, v in noyaux.items()},
             "setup_s": round(t_gen, 1),
         }
+        print(json.dumps(ligne), flush=True)
+        return
+
+    if args.config == 5:
+        ligne = bench_prefill(args, c0, dims, E, k, C, fz, flux, dev, espace, x_tok, n_fils)
         print(json.dumps(ligne), flush=True)
         return
 

@@ -49,7 +49,6 @@ constexpr uint32_t PF_NMAX = 16;          // macro-steps per CODES_CTX tile held
 constexpr uint32_t PF_PIECES = 5;         // fp8 pieces per activation block
 constexpr uint32_t PF_BP_MAX = 128;       // padded blocks per row (4096 columns)
 constexpr uint32_t PF_PAIRES_MAX = 16384; // positions x k per call
-constexpr uint32_t PF_TRANCHES = 4;       // chunks of the pair list per expert in prefill_grouper
 constexpr uint32_t ECHELLE_UN = 127u;     // E8M0 1.0
 
 // LDS of prefill_mfma after the decode (the LUT, x and ring regions are free then; the block
@@ -142,33 +141,38 @@ __device__ __forceinline__ uint32_t max_vague(uint32_t v) {
 using trc::ParamsPrefill;
 
 // One block of 1024 threads: thread (chunk c, expert e) counts and then lists the pairs of chunk c
-// that chose e; chunks are concatenated in order, so each expert's pairs keep position order. Also
-// clears the piece counters of the call. Indices >= E are format errors (the reference bails,
-// trc-ordo/src/lib.rs:817-819) and join no list.
+// that chose e (8 chunks when E <= 128, else 4); chunks are concatenated in order, so each expert's
+// pairs keep position order. Also clears the piece counters of the call. Indices >= E are format
+// errors (the reference bails, trc-ordo/src/lib.rs:817-819) and join no list.
 extern "C" __global__ void __launch_bounds__(1024)
 prefill_grouper(ParamsPrefill pp, uint32_t* __restrict__ controle) {
     using namespace trc;
-    __shared__ uint32_t idx[PF_PAIRES_MAX];
-    __shared__ uint32_t cpt[PF_TRANCHES][EXPERTS_MAX];
+    __shared__ u32x4 idx4[PF_PAIRES_MAX / 4];
+    __shared__ uint32_t cpt[1024];
     __shared__ uint32_t deb[EXPERTS_MAX];
-    const uint32_t n = pp.T * pp.k, E = pp.E;
+    const uint32_t n = pp.T * pp.k, E = pp.E, n4 = (n + 3u) / 4u;
     const uint32_t* indices = reinterpret_cast<const uint32_t*>(pp.indices);
+    uint32_t* idx = reinterpret_cast<uint32_t*>(idx4);
     uint32_t mauvais = 0;
-    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
-        const uint32_t v = indices[i];
+    for (uint32_t i = threadIdx.x; i < 4u * n4; i += blockDim.x) {
+        const uint32_t v = i < n ? indices[i] : 0xFFFFFFFFu;  // padding joins no list
         idx[i] = v;
-        mauvais += v >= E ? 1u : 0u;
+        mauvais += (i < n && v >= E) ? 1u : 0u;
     }
     if (threadIdx.x < 4u) reinterpret_cast<uint32_t*>(pp.pieces)[threadIdx.x] = 0u;
     mauvais = somme_vague_u32(mauvais);
     if (__lane_id() == 0 && mauvais) atomicAdd(&controle[CTL_FORMAT], mauvais);
     __syncthreads();
-    const uint32_t e = threadIdx.x % EXPERTS_MAX, c = threadIdx.x / EXPERTS_MAX;
-    const uint32_t lo = uint32_t(uint64_t(c) * n / PF_TRANCHES), hi = uint32_t(uint64_t(c + 1) * n / PF_TRANCHES);
+    const uint32_t Ep = E <= 128u ? 128u : EXPERTS_MAX, tranches = 1024u / Ep;
+    const uint32_t e = threadIdx.x % Ep, c = threadIdx.x / Ep;
+    const uint32_t lo = uint32_t(uint64_t(c) * n4 / tranches), hi = uint32_t(uint64_t(c + 1) * n4 / tranches);
     uint32_t nb = 0;
     if (e < E)
-        for (uint32_t i = lo; i < hi; ++i) nb += idx[i] == e ? 1u : 0u;
-    cpt[c][e] = nb;
+        for (uint32_t i = lo; i < hi; ++i) {
+            const u32x4 v = idx4[i];
+            nb += (v.x == e ? 1u : 0u) + (v.y == e ? 1u : 0u) + (v.z == e ? 1u : 0u) + (v.w == e ? 1u : 0u);
+        }
+    cpt[threadIdx.x] = nb;
     __syncthreads();
     if (threadIdx.x < 64u) {  // exclusive prefix over experts, 4 per lane
         uint32_t tot[EXPERTS_MAX / 64];
@@ -177,7 +181,8 @@ prefill_grouper(ParamsPrefill pp, uint32_t* __restrict__ controle) {
         for (uint32_t q = 0; q < EXPERTS_MAX / 64; ++q) {
             const uint32_t ee = threadIdx.x * (EXPERTS_MAX / 64) + q;
             uint32_t t = 0;
-            for (uint32_t cc = 0; cc < PF_TRANCHES; ++cc) t += cpt[cc][ee];
+            if (ee < Ep)
+                for (uint32_t cc = 0; cc < tranches; ++cc) t += cpt[cc * Ep + ee];
             tot[q] = t;
             local += t;
         }
@@ -201,10 +206,15 @@ prefill_grouper(ParamsPrefill pp, uint32_t* __restrict__ controle) {
     __syncthreads();
     if (e < E) {
         uint32_t pos = deb[e];
-        for (uint32_t cc = 0; cc < c; ++cc) pos += cpt[cc][e];
+        for (uint32_t cc = 0; cc < c; ++cc) pos += cpt[cc * Ep + e];
         uint32_t* paires = reinterpret_cast<uint32_t*>(pp.paires);
-        for (uint32_t i = lo; i < hi; ++i)
-            if (idx[i] == e) paires[pos++] = i;
+        for (uint32_t i = lo; i < hi; ++i) {
+            const u32x4 v = idx4[i];
+            if (v.x == e) paires[pos++] = 4u * i;
+            if (v.y == e) paires[pos++] = 4u * i + 1u;
+            if (v.z == e) paires[pos++] = 4u * i + 2u;
+            if (v.w == e) paires[pos++] = 4u * i + 3u;
+        }
     }
 }
 
@@ -262,6 +272,58 @@ prefill_swiglu_quant(ParamsPrefill pp) {
 }
 
 namespace trc {
+
+// B operand source of one column (pair) of a 16-pair tile: its pieces, PF_PIECES x Bp blocks of 32
+// bytes, and their scales.
+struct Operande_b {
+    const uint8_t* q;
+    const uint8_t* s;
+    uint32_t Bp, bloc, demi, lg;
+    bool valide;
+};
+
+// acc_rt += A_rt (k-step ks) x B over pieces p0 .. p0 + NP - 1: their loads are issued before the MFMAs.
+// This lane's B bytes 0-15 are half `demi` of block 4 ks + `bloc`, bytes 16-31 the same half of block
+// 4 ks + 2 + `bloc`; its scale is block 4 ks + lg's.
+template <uint32_t NP>
+__device__ __forceinline__ void produit_pieces(f32x4& acc0, f32x4& acc1, const u32x4& a0, const u32x4& a1,
+                                               uint32_t sa0, uint32_t sa1, const Operande_b& ob, uint32_t p0,
+                                               uint32_t ks, uint32_t nrt) {
+    u32x4 b0[NP], b1[NP];
+    uint32_t sb[NP];
+#pragma unroll
+    for (uint32_t p = 0; p < NP; ++p) {
+        const uint64_t o = uint64_t(p0 + p) * ob.Bp + 4u * ks;
+        b0[p] = u32x4{0u, 0u, 0u, 0u};
+        b1[p] = u32x4{0u, 0u, 0u, 0u};
+        sb[p] = ECHELLE_UN;
+        if (ob.valide) {
+            b0[p] = *glob<u32x4>(ob.q + (o + ob.bloc) * 32u + ob.demi);
+            b1[p] = *glob<u32x4>(ob.q + (o + 2u + ob.bloc) * 32u + ob.demi);
+            sb[p] = ob.s[o + ob.lg];
+        }
+    }
+    const i32x8 ra0 = {int(a0.x), int(a0.y), int(a0.z), int(a0.w), 0, 0, 0, 0};
+    const i32x8 ra1 = {int(a1.x), int(a1.y), int(a1.z), int(a1.w), 0, 0, 0, 0};
+    i32x8 rb[NP];
+#pragma unroll
+    for (uint32_t p = 0; p < NP; ++p)
+        rb[p] = i32x8{int(b0[p].x), int(b0[p].y), int(b0[p].z), int(b0[p].w),
+                      int(b1[p].x), int(b1[p].y), int(b1[p].z), int(b1[p].w)};
+#pragma unroll
+    for (uint32_t p = 0; p < NP; ++p) {
+        acc0 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ra0, rb[p], acc0, 4, 0, 0, int(sa0), 0, int(sb[p]));
+        if (nrt == 2u)
+            acc1 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ra1, rb[p], acc1, 4, 0, 0, int(sa1), 0,
+                                                                    int(sb[p]));
+    }
+    // The result of this MFMA (A fp4, B fp8) reaches its registers 11 to 12 wait states after issue
+    // (measured); the compiler's hazard padding before a VALU read of it can be shorter. 16 wait states
+    // here, fenced so that nothing is scheduled across them, cover every reader.
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_nop 15");
+    __builtin_amdgcn_sched_barrier(0);
+}
 
 // One band of rows [r0, r0 + nl) of matrix j of expert e against the expert's pairs.
 template <uint32_t J>
@@ -416,39 +478,28 @@ __device__ __forceinline__ void prefill_bande(const ParamsPrefill& pp, const uin
     const uint8_t* bq = reinterpret_cast<const uint8_t*>(J == 2u ? pp.xq : pp.aq);
     const uint8_t* bs = reinterpret_cast<const uint8_t*>(J == 2u ? pp.xs : pp.as);
     const float* biais = reinterpret_cast<const float*>(m.biais.p);
-    // this lane's B bytes 0-15: half (lg & 1) of block 4 ks + (lg >> 1); bytes 16-31: of block
-    // 4 ks + 2 + (lg >> 1); its scale: block 4 ks + lg
     const uint32_t demi_b = 16u * (lg & 1u), bloc_b = lg >> 1;
     const uint32_t n_tt = (n_e + 15u) / 16u;
+    uint32_t c_suiv = n_e > lr ? paires[debut_e + lr] : 0u;
     for (uint32_t tt = 0; tt < n_tt; ++tt) {
         const uint32_t tok = 16u * tt + lr;
         const bool valide = tok < n_e;
-        const uint32_t c = valide ? paires[debut_e + tok] : 0u;
+        const uint32_t c = c_suiv;
+        c_suiv = tok + 16u < n_e ? paires[debut_e + tok + 16u] : 0u;
         const uint32_t src = J == 2u ? c / pp.k : c;
-        const uint64_t ligne_b = uint64_t(src) * PF_PIECES * Bp;
+        const Operande_b ob{bq + uint64_t(src) * PF_PIECES * Bp * 32u, bs + uint64_t(src) * PF_PIECES * Bp, Bp,
+                            bloc_b, demi_b, lg, valide};
         f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (uint32_t i = 0; i < 2; ++i) {
             const uint32_t ks = w + 16u * i;
             if (ks >= nks) continue;  // wave-uniform
-            for (uint32_t p = 0; p < P; ++p) {
-                const uint64_t o = ligne_b + uint64_t(p) * Bp + 4u * ks;
-                u32x4 b0 = {0u, 0u, 0u, 0u}, b1 = {0u, 0u, 0u, 0u};
-                uint32_t sb = ECHELLE_UN;
-                if (valide) {
-                    b0 = *glob<u32x4>(bq + (o + bloc_b) * 32u + demi_b);
-                    b1 = *glob<u32x4>(bq + (o + 2u + bloc_b) * 32u + demi_b);
-                    sb = bs[o + lg];
-                }
-                const i32x8 rb = {int(b0.x), int(b0.y), int(b0.z), int(b0.w), int(b1.x), int(b1.y), int(b1.z), int(b1.w)};
-                const i32x8 ra0 = {int(af[0][i].x), int(af[0][i].y), int(af[0][i].z), int(af[0][i].w), 0, 0, 0, 0};
-                acc0 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ra0, rb, acc0, 4, 0, 0, int(sa[0][i]), 0,
-                                                                        int(sb));
-                if (nrt == 2u) {
-                    const i32x8 ra1 = {int(af[1][i].x), int(af[1][i].y), int(af[1][i].z), int(af[1][i].w), 0, 0, 0, 0};
-                    acc1 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ra1, rb, acc1, 4, 0, 0, int(sa[1][i]),
-                                                                            0, int(sb));
-                }
+            // pieces two at a time: their four loads in flight together, then their MFMAs
+            for (uint32_t p0 = 0; p0 < P; p0 += 2u) {
+                if (p0 + 1u < P)
+                    produit_pieces<2>(acc0, acc1, af[0][i], af[1][i], sa[0][i], sa[1][i], ob, p0, ks, nrt);
+                else
+                    produit_pieces<1>(acc0, acc1, af[0][i], af[1][i], sa[0][i], sa[1][i], ob, p0, ks, nrt);
             }
         }
         ecrire_lds<f32x4>(base + PF_PART + ((w * 2u + 0u) * 64u + lane) * 16u, acc0);
