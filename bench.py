@@ -284,6 +284,132 @@ def bench_prefill(args, c0, dims, E, k, C, fz, flux, dev, espace, x_tok, n_fils)
     return ligne
 
 
+def bench_flux(args, E, k, C, dims, dev, flux, fz, x_tok, n_fils):
+    """Config 4, streaming variant: the layers' parts live in pinned host memory. Per layer and token:
+    router (gemv_f32 + routeur_topk) on the compute stream, the k indices copied to the host (the
+    per-layer host sync of the reference scheduler, trc-ordo/src/lib.rs:1054-1370), the k chosen parts
+    copied by hipMemcpyAsync on a side stream, each expert decoded and applied (trc_expert_fusionne) as
+    soon as its copy has landed, then the ordered combine. Also timed: the copies alone and the
+    compute alone (parts already on the device), for the overlap."""
+    import numpy as np
+    import torch
+
+    from troncons_amd import codeur, fusion
+    from troncons_amd import noyaux as K
+    from troncons_amd.noyaux import VueCarte
+    V = VueCarte.de
+    nk = K.Noyaux()
+    L = args.couches
+    epingles, decal, tailles, vluts, routeurs = [], [], [], [], []
+    t0 = time.perf_counter()
+    for l in range(L):
+        h = codeur.CoucheSynthetique(args.graine, l, E, dims, N_delta=args.n_delta, N_codes=args.n_codes,
+                                     n_fils=n_fils)
+        t = np.array([h.taille(e) for e in range(E)], np.int64)
+        d = np.concatenate([[0], np.cumsum((t + 255) // 256 * 256)[:-1]]).astype(np.int64)
+        pin = torch.empty(int(d[-1] + t[-1]), dtype=torch.uint8, pin_memory=True)
+        vue_pin = pin.numpy()
+        for e in range(E):
+            vue_pin[d[e]:d[e] + t[e]] = h.partie(e)
+        freqs = h.freqs()
+        luts = torch.from_numpy(K.luts_couche([[freqs[j][q] for q in range(4)] for j in range(3)]).view(np.int32)).to(dev)
+        r = np.stack([codeur.synth_normale_bf16(args.graine + l, 3, e, C, 0.02) for e in range(E)])
+        routeurs.append(torch.from_numpy(r).to(dev))
+        h.liberer()
+        epingles.append(pin)
+        decal.append(d)
+        tailles.append(t)
+        vluts.append((luts, V(luts)))
+        print(f"bench: layer {l} encoded into pinned host memory ({pin.numel() / 1e9:.2f} GB)", file=sys.stderr,
+              flush=True)
+    t_gen = time.perf_counter() - t0
+    tmax = int(max(t.max() for t in tailles))
+    arrivees = [torch.empty(tmax + 256, dtype=torch.uint8, device=dev) for _ in range(k)]
+    arr = [a[(-a.data_ptr()) % 256:][:tmax] for a in arrivees]
+    xs = torch.from_numpy(x_tok).to(dev)
+    vx = [V(xs, 4 * C * t, 4 * C) for t in range(len(x_tok))]
+    logits = torch.zeros(E, dtype=torch.float32, device=dev)
+    idx = torch.zeros(8, dtype=torch.int32, device=dev)
+    poids = torch.zeros(8, dtype=torch.float32, device=dev)
+    idx_h = torch.zeros(8, dtype=torch.int32, pin_memory=True)
+    sorties = torch.zeros(k * C, dtype=torch.float32, device=dev)
+    residu = torch.zeros(C, dtype=torch.float32, device=dev)
+    ctl = torch.zeros(4, dtype=torch.int32, device=dev)
+    tr_t = torch.empty(fusion.taille_travail_expert(dims, args.n_codes) + 256, dtype=torch.uint8, device=dev)
+    tr = VueCarte(tr_t.data_ptr() + (-tr_t.data_ptr()) % 256, fusion.taille_travail_expert(dims, args.n_codes))
+    copie = torch.cuda.Stream(device=dev)
+    ev_idx = torch.cuda.Event()
+    ev_arr = [torch.cuda.Event() for _ in range(k)]
+    copie_ok, calcul_ok = [True], [True]
+    octets = [0]
+
+    def pas(s):
+        x = vx[s % len(vx)]
+        for l in range(L):
+            nk.gemv_f32(V(routeurs[l]), x, None, V(logits), E, C, f=flux)
+            nk.routeur_topk(V(logits), E, k, V(idx), V(poids), f=flux)
+            idx_h.copy_(idx, non_blocking=True)
+            ev_idx.record(flux)
+            ev_idx.synchronize()
+            sel = idx_h.numpy()[:k]
+            if copie_ok[0]:
+                with torch.cuda.stream(copie):
+                    for q, e in enumerate(sel):
+                        n = int(tailles[l][e])
+                        o = int(decal[l][e])
+                        arr[q][:n].copy_(epingles[l][o:o + n], non_blocking=True)
+                        ev_arr[q].record(copie)
+                        octets[0] += n
+            if calcul_ok[0]:
+                for q, e in enumerate(sel):
+                    if copie_ok[0]:
+                        flux.wait_event(ev_arr[q])
+                    # compute alone: the arrival buffers keep layer 0's parts 0..k-1 (and its LUTs)
+                    n = int(tailles[l][e]) if copie_ok[0] else int(tailles[0][q])
+                    lut = vluts[l][1] if copie_ok[0] else vluts[0][1]
+                    fz.expert_fusionne(VueCarte(arr[q].data_ptr(), n), lut, dims, x, V(sorties, 4 * C * q, 4 * C),
+                                       V(ctl), tr, args.n_delta, args.n_codes, f=flux)
+                nk.combiner(V(residu), V(sorties), C, V(poids), k, C, f=flux)
+            elif copie_ok[0]:
+                for q in range(k):
+                    flux.wait_event(ev_arr[q])
+
+    # the arrival buffers hold valid parts before the compute-only pass
+    with torch.cuda.stream(copie):
+        for q in range(k):
+            n = int(tailles[0][q])
+            arr[q][:n].copy_(epingles[0][int(decal[0][q]):int(decal[0][q]) + n], non_blocking=True)
+    torch.cuda.synchronize()
+    ms = temps(pas, args.steps, args.warmup, flux)
+    assert (ctl.cpu().numpy() == 0).all(), f"control words {ctl.cpu().numpy()}"
+    octets_tok = octets[0] / (args.steps + args.warmup)
+    calcul_ok[0] = False
+    ms_copie = temps(pas, args.steps, args.warmup, flux)
+    calcul_ok[0], copie_ok[0] = True, False
+    ms_calcul = temps(pas, args.steps, args.warmup, flux)
+    us, us_c, us_k = (m * 1e3 / args.steps for m in (ms, ms_copie, ms_calcul))
+    recouvrement = (us_c + us_k - us) / min(us_c, us_k)
+    return {
+        "metric": f"config4 streaming us/token for the MoE part of {L} layers (experts in pinned host memory)",
+        "value": round(us, 1), "unit": "us/token", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms / args.steps, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "u32 rANS / f32 GEMV",
+        "data": "synthetic (seeded MXFP4 law A, E8M0 in [119,125], bf16 N(0,1) activations, bf16 N(0,0.02) router)",
+        "config": {"workload": f"config4 streaming variant: a token through {L} MoE layers x {E} gpt-oss-120b "
+                               "experts kept in pinned host memory; per layer the router's top-4 is read by the "
+                               "host, the 4 parts are copied (hipMemcpyAsync, side stream) and each expert is "
+                               "decoded as soon as its copy lands", "layers": L, "experts": E, "k": k,
+                   "n_codes": args.n_codes, "n_delta": args.n_delta},
+        "h2d_bytes_per_token": int(octets_tok),
+        "h2d_gbps": round(octets_tok / (us * 1e-6) / 1e9, 2),
+        "copies_only_us": round(us_c, 1), "h2d_gbps_copies_only": round(octets_tok / (us_c * 1e-6) / 1e9, 2),
+        "compute_only_us": round(us_k, 1),
+        "overlap": round(recouvrement, 3),
+        "per_layer_us": round(us / L, 1),
+        "setup_s": round(t_gen, 1),
+    }
+
+
 def chrono_passes(fusion, pas, n):
     """Per-kernel durations over n steps: every kernel launched with the start/stop events that the
     runtime records at the kernel's own start and end (hipExtLaunchKernel). Kept out of the timed
@@ -321,6 +447,9 @@ def main():
     ap.add_argument("--config", type=int, default=3, choices=(1, 2, 3, 4, 5))
     ap.add_argument("--positions", type=int, default=512, help="positions of a --config 5 prefill batch")
     ap.add_argument("--couches", type=int, default=36, help="layers of --config 4")
+    ap.add_argument("--flux", action="store_true",
+                    help="--config 4 variant: the experts stay in pinned host memory and the chosen ones are "
+                         "copied per layer on a side stream, overlapped with the decode")
     ap.add_argument("--experts", type=int, default=128)
     ap.add_argument("--k", type=int, default=4)
     ap.add_argument("--n-codes", type=int, default=16, help="macro-steps per CODES_CTX tile written by the encoder")
@@ -351,6 +480,11 @@ def main():
     fz = fusion.Fusion()
     flux = torch.cuda.current_stream()
     V = VueCarte.de
+
+    if args.config == 4 and args.flux:
+        x_tok = np.stack([codeur.synth_normale_bf16(args.graine, 4, t, C, 1.0) for t in range(args.tokens)])
+        print(json.dumps(bench_flux(args, E, k, C, dims, dev, flux, fz, x_tok, n_fils)), flush=True)
+        return
 
     n_couches = args.couches if args.config == 4 else 1
     couches = []
