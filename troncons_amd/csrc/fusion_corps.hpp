@@ -378,7 +378,8 @@ __device__ __forceinline__ void corps_gemv_xg(const Tache& tc, const PrepGemv& p
     const uint32_t decal = haut ? 32u : 0u, masque_inf = (1u << v) - 1u;
     const uint32_t q = v >> 2, q4 = v & 3u;
     const uint32_t vagues_bloc = blockDim.x >> 6;
-    const uint32_t vague = blockIdx.x * vagues_bloc + (threadIdx.x >> 6);
+    // wave-uniform (scalar registers): the tile loop and its macro-step counts run on SALU
+    const uint32_t vague = uniforme32(blockIdx.x * vagues_bloc + (threadIdx.x >> 6));
     const uint32_t n_vagues = gridDim.x * vagues_bloc;
     const uint32_t demi = (threadIdx.x >> 5) & (2u * vagues_bloc - 1u);
     const uint32_t lds = demi * OCTETS_ANNEAU;
@@ -605,7 +606,8 @@ __device__ __forceinline__ void corps_gemv_rapide(const Tache& tc, const PrepGem
     const uint32_t decal = haut ? 32u : 0u, masque_inf = (1u << v) - 1u;
     const uint32_t q = v >> 2, q4 = v & 3u;
     const uint32_t vagues_bloc = blockDim.x >> 6;
-    const uint32_t vague = blockIdx.x * vagues_bloc + (threadIdx.x >> 6);
+    // wave-uniform (scalar registers): the tile loop and its macro-step counts run on SALU
+    const uint32_t vague = uniforme32(blockIdx.x * vagues_bloc + (threadIdx.x >> 6));
     const uint32_t n_vagues = gridDim.x * vagues_bloc;
     const uint32_t demi = (threadIdx.x >> 5) & (2u * vagues_bloc - 1u);
     const uint32_t base = adresse_lds(lds);
@@ -614,15 +616,16 @@ __device__ __forceinline__ void corps_gemv_rapide(const Tache& tc, const PrepGem
     const uint32_t a_anneau = base + LDS_ANNEAUX + demi * OCTETS_ANNEAU;
     const uint32_t a_ent = base + LDS_ENT + demi * (ENT_PAR_TUILE * 4u);
     const uint32_t a_ent_q = a_ent + 4u * q;
-    const uint32_t nmacro = h.P / 128u;
+    // the stream header's counts, wave-uniform (scalar registers)
+    const uint32_t hN = uniforme32(h.N), hT = uniforme32(h.T), nmacro = uniforme32(h.P / 128u);
     uint32_t hors_l = 0, pointeur = 0;
-    for (uint32_t t0 = 2u * vague; t0 < h.T; t0 += 2u * n_vagues) {
+    for (uint32_t t0 = 2u * vague; t0 < hT; t0 += 2u * n_vagues) {
         const uint32_t t = t0 + (haut ? 1u : 0u);
-        const bool tuile = t < h.T;
-        const uint32_t nb_a = min(h.N, nmacro - t0 * h.N);
-        const uint32_t nb_b = (t0 + 1u < h.T) ? min(h.N, nmacro - (t0 + 1u) * h.N) : 0u;
+        const bool tuile = t < hT;
+        const uint32_t nb_a = min(hN, nmacro - t0 * hN);
+        const uint32_t nb_b = (t0 + 1u < hT) ? min(hN, nmacro - (t0 + 1u) * hN) : 0u;
         const uint32_t nb = haut ? nb_b : nb_a;
-        const uint32_t m0 = (tuile ? t : t0) * h.N;
+        const uint32_t m0 = (tuile ? t : t0) * hN;
         auto stager = [&](uint32_t m) { ecrire_lds<u32x4>(a_ent + 16u * v, ent16[2u * (m0 + m) + v]); };
         uint32_t x = tuile ? h.etats[t * VOIES + v] : L;
         const uint32_t debut = tuile ? h.debut[t] : 0u;
@@ -689,13 +692,17 @@ __device__ __forceinline__ void corps_gemv_rapide(const Tache& tc, const PrepGem
             }
         };
         uint32_t m = 0;
-        for (; m < nb_min; ++m) macro(std::true_type{}, m);
+        for (; m + 1u < nb_min; m += 2u) {  // two macro-steps per iteration: no register copies at the latch
+            macro(std::true_type{}, m);
+            macro(std::true_type{}, m + 1u);
+        }
+        if (m < nb_min) macro(std::true_type{}, m++);
         for (; m < nb_a; ++m) macro(std::false_type{}, m);
         const float s = somme_demi_f32(acc);
         if (tuile) {
             if (v == 0 && rho < R) ecrire(s);
             hors_l += (x != L) ? 1u : 0u;
-            const uint32_t attendu = (t + 1 < h.T) ? h.debut[t + 1] : h.W;
+            const uint32_t attendu = (t + 1 < hT) ? h.debut[t + 1] : h.W;
             pointeur += (v == 0 && debut + (a.o2 - o0) / 2u != attendu) ? 1u : 0u;
         }
     }
