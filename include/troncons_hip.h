@@ -208,6 +208,228 @@ int trc_prefill_moe(trc_vue repertoire, uint32_t experts, trc_vue luts, const tr
 void trc_chrono(int actif);
 int trc_chrono_recolter(char* noms, double* ms, uint64_t* lancements, int max, int remettre_a_zero);
 
+/* ------------------------------------------- the .trc v1.2 file container (host only; trc-format)
+ *
+ * Replaces the Rust crate trc-format (moteur/crates/trc-format/src/lib.rs) for the scheduler's
+ * side of the path: Fichier::ouvrir and its accessors (lib.rs:957-1140), lire_partie
+ * (lib.rs:813-866), assembler_partie (lib.rs:879-910), the Ecrivain (lib.rs:1149-1239) and
+ * empreinte64 (lib.rs:111-127). The reader refuses what the reference refuses; its status codes
+ * are the classes of ErreurFormat (lib.rs:129-148), with the message in trc_derniere_erreur(). */
+
+#define TRC_FORMAT_ES 16        /* read/write error, short file */
+#define TRC_FORMAT_MAGIE 17     /* not a .trc file */
+#define TRC_FORMAT_VERSION 18   /* major != 1 or minor > 2 */
+#define TRC_FORMAT_DRAPEAUX 19  /* unknown or inconsistent flags */
+#define TRC_FORMAT_SORTE 20     /* unknown stream kind (0x05 is reserved) */
+#define TRC_FORMAT_CHAMP 21     /* a field with a wrong value */
+#define TRC_FORMAT_EMPREINTE 22 /* a fingerprint mismatch */
+#define TRC_FORMAT_RESERVE 23   /* non-zero reserved bytes */
+#define TRC_FORMAT_LIMITES 24   /* truncated or out-of-bounds structure */
+
+#define TRC_DRAPEAU_ALIGNE 1u
+#define TRC_DRAPEAU_NIVEAUX 2u
+#define TRC_DRAPEAU_BRUT 4u
+#define TRC_DRAPEAU_CANONIQUE 8u
+#define TRC_DRAPEAU_RAPIDE 32u
+
+#define TRC_SECTION_META 0
+#define TRC_SECTION_RESIDENTS 1
+#define TRC_SECTION_TABLES 2
+#define TRC_SECTION_REPERTOIRE 3
+#define TRC_SECTION_TRONCONS 4
+
+#define TRC_SORTE_MEDIANES 0x01
+#define TRC_SORTE_BIAIS 0x02
+#define TRC_SORTE_DELTA 0x03
+#define TRC_SORTE_CODES_CTX 0x04
+#define TRC_SORTE_CODES_BRUTS 0x06
+#define TRC_SORTE_ECHELLES_BRUTES 0x07
+#define TRC_SORTE_BASE_CTX 0x10
+#define TRC_SORTE_COMPL_CTX 0x11
+#define TRC_SORTE_CENTRES 0x12
+#define TRC_CONTEXTE_AUCUN 0xFF
+
+typedef struct {
+    uint64_t decalage;
+    uint64_t longueur;
+} trc_section;
+
+/* Entete (lib.rs:250-272), read: the 4 096 on-disk bytes minus magic, alignment, header size and
+ * fingerprint, which the reader checks. */
+typedef struct {
+    uint16_t version_majeure;
+    uint16_t version_mineure;
+    uint32_t drapeaux;
+    uint64_t taille_fichier;
+    uint8_t sha256_source[32];
+    uint64_t taille_source;
+    uint16_t couches;
+    uint16_t experts;
+    uint16_t k;
+    uint16_t matrices;
+    uint32_t lignes[4];
+    uint32_t colonnes[4];
+    uint32_t poids_par_bloc;  /* 32 */
+    uint32_t octets_par_bloc; /* 17 */
+    uint8_t type_ggml;        /* 39 (MXFP4) */
+    uint8_t niveaux;
+    uint8_t classes_echelle;
+    uint8_t reserve0;
+    uint8_t partition[8];
+    uint32_t reserve1;
+    trc_section sections[8];
+} trc_entete_fichier;
+
+/* EntreeRepertoire (lib.rs:444-500): exactly the 64 on-disk bytes. */
+typedef struct {
+    uint64_t decalage;
+    uint32_t longueur[2];
+    uint32_t utiles[2];
+    uint64_t empreinte_origine;
+    uint64_t empreinte_niveau[2];
+    uint16_t couche;
+    uint16_t expert;
+    uint32_t reserve;
+    uint64_t empreinte_canonique; /* v1.2 CANONIQUE files; 0 otherwise */
+} trc_entree_repertoire;
+
+/* TenseurResident (lib.rs:683-693): exactly the 128 on-disk bytes (name NUL-padded, not always
+ * NUL-terminated: 64 bytes is a valid length). */
+typedef struct {
+    char nom[64];
+    uint32_t type_ggml;
+    uint32_t n_dims;
+    uint64_t ne[4];
+    uint64_t decalage; /* from the start of the data zone, multiple of 256 */
+    uint64_t octets;
+    uint64_t empreinte;
+} trc_resident;
+
+/* Table (lib.rs:518-560): the 8-byte record header, then the payload (type 1: 16 u16 frequencies,
+ * 2: 256 u16 frequencies, 3: 4 f32 centres). */
+typedef struct {
+    uint16_t couche;
+    uint8_t matrice;
+    uint8_t sorte;
+    uint8_t contexte;
+    uint8_t type_charge;
+    uint16_t reserve;
+    union {
+        uint16_t frequences[256];
+        float centres[4];
+    } charge;
+} trc_table;
+
+/* A GGUF v3 key/value pair of MÉTA (PaireMeta, meta.rs:21-30). Offsets count from the first pair
+ * (byte 8 of trc_fichier_meta()'s bytes). */
+typedef struct {
+    uint64_t debut;     /* extent of the whole pair */
+    uint64_t fin;
+    uint64_t cle;       /* key bytes (UTF-8, not NUL-terminated) */
+    uint64_t lg_cle;
+    uint32_t type;      /* GGUF value type 0..12 */
+    uint32_t type_elem; /* type 9: element type */
+    uint64_t n;         /* type 9: element count; type 8: string length */
+    uint64_t chaine;    /* type 8: offset of the string bytes */
+    uint64_t u;         /* types 0, 2, 4, 10 and 7 (bool) */
+    int64_t i;          /* types 1, 3, 5, 11 */
+    double f;           /* types 6, 12 */
+} trc_paire_meta;
+
+/* DescFlux (lib.rs:780-787): exactly the 16 on-disk bytes of a stream descriptor. */
+typedef struct {
+    uint8_t sorte;
+    uint8_t matrice;
+    uint8_t contexte;
+    uint8_t reserve;
+    uint32_t decalage;
+    uint32_t longueur;
+    uint32_t produits;
+} trc_desc_flux;
+
+/* Partie (lib.rs:790-799): the part header; its descriptors are the trc_desc_flux at byte 64. */
+typedef struct {
+    uint16_t couche;
+    uint16_t expert;
+    uint8_t niveau;
+    uint8_t n_matrices;
+    uint16_t n_flux;
+    uint32_t utiles;
+} trc_partie_info;
+
+/* empreinte64 (lib.rs:111-114): the first 8 bytes of SHA-256, little-endian. */
+uint64_t trc_empreinte64(const void* octets, uint64_t n);
+void trc_sha256(const void* octets, uint64_t n, uint8_t sortie[32]);
+/* empreinte64 of an expert (ARCHITECTURE.md §4.12): 17-byte blocks of j = 0, 1, 2 in beta order,
+ * then the f32 biases of j = 0, 1, 2. */
+uint64_t trc_empreinte_expert(const uint8_t* const* blocs17, const float* const* biais, const trc_dims_expert* dims);
+/* empreinte_emplacement (trc-ordo/src/lib.rs:238-262): the same from a decoded SoA slot; on a
+ * CANONIQUE file it equals the directory's empreinte_canonique. */
+uint64_t trc_empreinte_emplacement(const uint8_t* emplacement, const trc_dims_expert* dims);
+/* lire_partie (lib.rs:813-866): structure checks of one part. */
+int trc_partie_lire(const uint8_t* octets, uint64_t n, trc_partie_info* info);
+
+/* Fichier::ouvrir (lib.rs:957-1090): header, size, sections, MÉTA, resident table, TABLES and
+ * RÉPERTOIRE read and checked; parts and resident data are not read. */
+typedef struct trc_fichier trc_fichier;
+int trc_fichier_ouvrir(const char* chemin, trc_fichier** fichier);
+void trc_fichier_fermer(trc_fichier* f);
+const trc_entete_fichier* trc_fichier_entete(const trc_fichier* f);
+/* Fichier::meta (lib.rs:1099-1101): u64 n then the pairs, fingerprint excluded. */
+uint64_t trc_fichier_meta(const trc_fichier* f, const uint8_t** octets);
+uint64_t trc_fichier_n_paires(const trc_fichier* f);
+const trc_paire_meta* trc_fichier_paires(const trc_fichier* f);
+/* Fichier::paire (lib.rs:1107-1109): index of the first pair with this key, -1 if none. */
+int64_t trc_fichier_chercher_paire(const trc_fichier* f, const char* cle);
+uint32_t trc_fichier_n_residents(const trc_fichier* f);
+const trc_resident* trc_fichier_residents(const trc_fichier* f);
+/* Fichier::debut_donnees_residentes (lib.rs:1114-1116): absolute offset of the data zone. */
+uint64_t trc_fichier_debut_donnees(const trc_fichier* f);
+/* Fichier::toutes_tables (lib.rs:1127-1129): sorted by (couche, matrice, sorte, contexte). */
+uint32_t trc_fichier_n_tables(const trc_fichier* f);
+const trc_table* trc_fichier_tables(const trc_fichier* f);
+/* Fichier::table (lib.rs:1123-1125): NULL if absent. */
+const trc_table* trc_fichier_table(const trc_fichier* f, uint16_t couche, uint8_t matrice, uint8_t sorte,
+                                   uint8_t contexte);
+/* luts_couche (trc-ordo/src/lib.rs:265-273): u16[3][4][256] = DELTA ctx 0, CODES_CTX ctx 0..2 of
+ * each matrix, the input of trc_luts_couche. */
+int trc_fichier_freqs_couche(const trc_fichier* f, uint16_t couche, uint16_t* freqs);
+/* Fichier::repertoire / entree (lib.rs:1130-1137): couches x experts entries, (couche, expert) order. */
+const trc_entree_repertoire* trc_fichier_repertoire(const trc_fichier* f);
+const trc_entree_repertoire* trc_fichier_entree(const trc_fichier* f, uint16_t couche, uint16_t expert);
+/* Fichier::octets_lus_a_l_ouverture (lib.rs:1138-1140) */
+uint64_t trc_fichier_octets_lus(const trc_fichier* f);
+/* Reads [decalage, decalage + octets) with pread (thread-safe). */
+int trc_fichier_lire(const trc_fichier* f, uint64_t decalage, uint64_t octets, void* dst);
+/* Levels 0 .. niveaux-1 of (couche, expert) in one read (longueur_jusqua, lib.rs:497-500); with
+ * verifier != 0 each level is checked as trc-codec's verifier_partie and reconstruire do
+ * (trc-codec/src/lib.rs:264-297): fingerprint of the useful bytes, structure, identity. */
+int trc_fichier_lire_partie(const trc_fichier* f, uint16_t couche, uint16_t expert, uint32_t niveaux, void* dst,
+                            uint64_t cap, int verifier, uint64_t* octets);
+int trc_fichier_verifier_partie(const trc_fichier* f, uint16_t couche, uint16_t expert, uint32_t niveau,
+                                const uint8_t* octets, uint64_t n);
+
+/* Ecrivain (lib.rs:1149-1239), section by section: MÉTA, RÉSIDENTS, TABLES, then TRONÇONS
+ * (directory reserved), one call per expert, terminer (directory, header). TABLES may instead come
+ * after the last part, for an encoder that learns its tables layer by layer. */
+typedef struct trc_ecrivain trc_ecrivain;
+trc_ecrivain* trc_ecrivain_creer(const char* chemin);
+void trc_ecrivain_abandonner(trc_ecrivain* w);
+/* serialiser_meta (lib.rs:915-926): `paires` are n serialised GGUF v3 pairs (additions included). */
+int trc_ecrivain_meta(trc_ecrivain* w, const uint8_t* paires, uint64_t octets, uint64_t n_paires);
+/* disposer_residents + serialiser_table_residents (lib.rs:696-735): fills decalage and empreinte. */
+int trc_ecrivain_residents(trc_ecrivain* w, trc_resident* residents, const uint8_t* const* donnees, uint32_t n);
+/* serialiser_tables (lib.rs:563-583), records in the given order (the reader sorts them). */
+int trc_ecrivain_tables(trc_ecrivain* w, const trc_table* tables, uint32_t n);
+int trc_ecrivain_troncons(trc_ecrivain* w, uint16_t couches, uint16_t experts);
+/* One expert: level 0 (level 1 after it, or NULL), each checked, written to its useful bytes and
+ * padded to 4 096; the directory entry is returned in `ecrite` (may be NULL). */
+int trc_ecrivain_partie(trc_ecrivain* w, uint16_t couche, uint16_t expert, const uint8_t* niveau0, uint64_t octets0,
+                        const uint8_t* niveau1, uint64_t octets1, uint64_t empreinte_origine,
+                        uint64_t empreinte_canonique, trc_entree_repertoire* ecrite);
+/* Ecrivain::terminer (lib.rs:1227-1239): sections, size and fingerprint are filled in; frees w. */
+int trc_ecrivain_terminer(trc_ecrivain* w, const trc_entete_fichier* entete, uint64_t* taille);
+
 /* ---------------------------------------- encoder front-end (host only; role of bins/trc-codeur) */
 
 /* The seeded synthetic workload (nibble law "A", E8M0 scales in [119,125], bf16 N(0,0.02) biases).
@@ -238,7 +460,33 @@ uint64_t trc_synth_couche_taille(const trc_couche_synth* c, uint32_t expert);
 uint32_t trc_synth_couche_utiles(const trc_couche_synth* c, uint32_t expert);
 const uint8_t* trc_synth_couche_partie(const trc_couche_synth* c, uint32_t expert);
 const uint16_t* trc_synth_couche_freqs(const trc_couche_synth* c); /* [3][4][256] */
+/* empreinte64 of expert e as generated (canonique = 0) or with its nibbles 8 set to 0 (1). */
+uint64_t trc_synth_couche_empreinte(const trc_couche_synth* c, uint32_t expert, int canonique);
 void trc_synth_couche_liberer(trc_couche_synth* c);
+
+/* FluxAEcrire (trc-format/src/lib.rs:869-876) */
+typedef struct {
+    uint8_t sorte;
+    uint8_t matrice;
+    uint8_t contexte;
+    uint8_t reserve;
+    uint32_t produits;
+    const uint8_t* octets;
+    uint64_t longueur;
+} trc_flux_a_ecrire;
+/* assembler_partie (trc-format/src/lib.rs:879-910): the part (length a multiple of 4 096) into
+ * `out` when cap suffices; returns its length, 0 on error. */
+uint64_t trc_assembler_partie(uint16_t couche, uint16_t expert, uint8_t niveau, uint8_t n_matrices,
+                              const trc_flux_a_ecrire* flux, uint32_t n, uint8_t* out, uint64_t cap,
+                              uint32_t* utiles);
+/* A whole synthetic model as a v1.2 CANONIQUE .trc file (role of bins/trc-codeur/src/coder.rs:114-
+ * 390 on a GGUF): layer c's experts are those of trc_synth_couche(graine, c, ...), its router
+ * "blk.<c>.ffn_gate_inp.weight" (bf16, experts x colonnes[0]) the bf16 N(0, 0.02) rows
+ * trc_synth_normale_bf16(graine + c, 3, e, ...), MÉTA holds gpt-oss-style hyper-parameters, TABLES
+ * follow the parts. Layers are generated one at a time on n_fils threads. */
+int trc_synth_fichier(const char* chemin, uint64_t graine, uint16_t couches, uint16_t experts, uint16_t k,
+                      const trc_dims_expert* dims, uint32_t N_delta, uint32_t N_codes, uint32_t n_fils,
+                      uint64_t* taille);
 
 #ifdef __cplusplus
 }

@@ -39,6 +39,8 @@ def _declarer(l):
     l.trc_synth_couche_freqs.argtypes = [C.c_void_p]
     l.trc_synth_couche_freqs.restype = C.c_void_p
     l.trc_synth_couche_liberer.argtypes = [C.c_void_p]
+    l.trc_synth_couche_empreinte.argtypes = [C.c_void_p, C.c_uint32, C.c_int]
+    l.trc_synth_couche_empreinte.restype = C.c_uint64
     l._trc_codeur = True
     return l
 
@@ -122,6 +124,10 @@ class CoucheSynthetique:
 
     def taille(self, e: int) -> int:
         return _l().trc_synth_couche_taille(self._h, e)
+
+    def empreinte(self, e: int, canonique: bool) -> int:
+        """empreinte64 of expert e as generated, or with every nibble 8 of its codes set to 0."""
+        return int(_l().trc_synth_couche_empreinte(self._h, e, int(canonique)))
 
     def freqs(self) -> np.ndarray:
         p = _l().trc_synth_couche_freqs(self._h)

@@ -261,9 +261,10 @@ struct FluxEcrit {
     std::vector<uint8_t> octets;
 };
 
-// assembler_partie (trc-format/src/lib.rs:879-910)
+// assembler_partie (trc-format/src/lib.rs:879-910): header, descriptors, streams on 16-byte
+// boundaries, zeros up to a multiple of 4 096. Magic "TRC0" for level 0, "TRC1" for level 1.
 std::vector<uint8_t> assembler(uint16_t couche, uint16_t expert, uint8_t n_mat, const std::vector<FluxEcrit>& flux,
-                               uint32_t& utiles) {
+                               uint32_t& utiles, uint8_t niveau = 0) {
     size_t p = 64 + 16 * flux.size();
     std::vector<size_t> dec(flux.size());
     for (size_t i = 0; i < flux.size(); ++i) {
@@ -275,10 +276,10 @@ std::vector<uint8_t> assembler(uint16_t couche, uint16_t expert, uint8_t n_mat, 
     std::vector<uint8_t> b((p + 4095) / 4096 * 4096, 0);
     auto w16 = [&](size_t q, uint32_t v) { b[q] = uint8_t(v); b[q + 1] = uint8_t(v >> 8); };
     auto w32 = [&](size_t q, uint32_t v) { std::memcpy(&b[q], &v, 4); };
-    w32(0, trc::MAGIE_PARTIE0);
+    w32(0, niveau == 0 ? trc::MAGIE_PARTIE0 : 0x31435254u);
     w16(4, couche);
     w16(6, expert);
-    b[8] = 0;
+    b[8] = niveau;
     b[9] = n_mat;
     w16(10, uint32_t(flux.size()));
     w32(12, utiles);
@@ -334,6 +335,8 @@ void en_parallele(uint32_t n, uint32_t n_fils, F&& f) {
 struct trc_couche_synth {
     std::vector<std::vector<uint8_t>> parties;
     std::vector<uint32_t> utiles;
+    std::vector<uint64_t> empreinte_origine;    // of the generated expert
+    std::vector<uint64_t> empreinte_canonique;  // of the same with every nibble 8 of qs set to 0
     uint16_t freqs[3][4][256];
 };
 
@@ -456,6 +459,8 @@ trc_couche_synth* trc_synth_couche(uint64_t graine, uint32_t couche, uint32_t n_
     // pass 2: regenerate and code
     c->parties.resize(n_experts);
     c->utiles.resize(n_experts);
+    c->empreinte_origine.resize(n_experts);
+    c->empreinte_canonique.resize(n_experts);
     std::atomic<bool> echec{false};
     en_parallele(n_experts, n_fils, [&](uint32_t e) {
         std::vector<uint8_t> bl[3];
@@ -469,6 +474,18 @@ trc_couche_synth* trc_synth_couche(uint64_t graine, uint32_t couche, uint32_t n_
             pi[j] = bi[j].data();
         }
         trc_synth_expert(graine, couche, e, dims, pb, pi);
+        c->empreinte_origine[e] = trc_empreinte_expert(pb, pi, dims);
+        {
+            std::vector<uint8_t> cb[3];
+            const uint8_t* pc[3];
+            for (int j = 0; j < 3; ++j) {
+                cb[j] = bl[j];
+                for (size_t q = 0; q < cb[j].size(); q += 17)
+                    for (int t = 1; t < 17; ++t) cb[j][q + t] = canonique(cb[j][q + t]);
+                pc[j] = cb[j].data();
+            }
+            c->empreinte_canonique[e] = trc_empreinte_expert(pc, pi, dims);
+        }
         std::vector<FluxEcrit> flux;
         for (uint8_t j = 0; j < 3; ++j) {
             Prepa p;
@@ -486,10 +503,168 @@ trc_couche_synth* trc_synth_couche(uint64_t graine, uint32_t couche, uint32_t n_
     return c.release();
 }
 
+uint64_t trc_synth_couche_empreinte(const trc_couche_synth* c, uint32_t e, int canon) {
+    return canon ? c->empreinte_canonique[e] : c->empreinte_origine[e];
+}
 uint64_t trc_synth_couche_taille(const trc_couche_synth* c, uint32_t e) { return c->parties[e].size(); }
 uint32_t trc_synth_couche_utiles(const trc_couche_synth* c, uint32_t e) { return c->utiles[e]; }
 const uint8_t* trc_synth_couche_partie(const trc_couche_synth* c, uint32_t e) { return c->parties[e].data(); }
 const uint16_t* trc_synth_couche_freqs(const trc_couche_synth* c) { return &c->freqs[0][0][0]; }
 void trc_synth_couche_liberer(trc_couche_synth* c) { delete c; }
+
+uint64_t trc_assembler_partie(uint16_t couche, uint16_t expert, uint8_t niveau, uint8_t n_matrices,
+                              const trc_flux_a_ecrire* flux, uint32_t n, uint8_t* out, uint64_t cap,
+                              uint32_t* utiles) {
+    if (niveau > 1 || (n && flux == nullptr) || n > 65535) {
+        trc::usage("assembler_partie : niveau %u, %u flux", niveau, n);
+        return 0;
+    }
+    std::vector<FluxEcrit> v(n);
+    for (uint32_t i = 0; i < n; ++i) {
+        v[i].sorte = flux[i].sorte;
+        v[i].matrice = flux[i].matrice;
+        v[i].contexte = flux[i].contexte;
+        v[i].produits = flux[i].produits;
+        v[i].octets.assign(flux[i].octets, flux[i].octets + flux[i].longueur);
+    }
+    uint32_t u;
+    const std::vector<uint8_t> b = assembler(couche, expert, n_matrices, v, u, niveau);
+    if (utiles) *utiles = u;
+    if (out && cap >= b.size()) std::memcpy(out, b.data(), b.size());
+    return b.size();
+}
+
+int trc_synth_fichier(const char* chemin, uint64_t graine, uint16_t couches, uint16_t experts, uint16_t k,
+                      const trc_dims_expert* dims, uint32_t N_delta, uint32_t N_codes, uint32_t n_fils,
+                      uint64_t* taille) {
+    if (chemin == nullptr || dims == nullptr || couches == 0 || experts == 0 || k == 0 || k > experts)
+        return trc::usage("fichier synthetique : arguments faux");
+    const int rd = trc_dims_verifier(dims);
+    if (rd != TRC_OK) return rd;
+    const uint32_t D = dims->colonnes[0];
+    // MÉTA: gpt-oss-style hyper-parameters, then the encoder's additions (coder.rs:124-131)
+    std::vector<uint8_t> meta;
+    uint64_t n_paires = 0;
+    auto cle = [&](const char* c, uint32_t type) {
+        const uint64_t n = std::strlen(c);
+        meta.insert(meta.end(), reinterpret_cast<const uint8_t*>(&n), reinterpret_cast<const uint8_t*>(&n) + 8);
+        meta.insert(meta.end(), c, c + n);
+        meta.insert(meta.end(), reinterpret_cast<const uint8_t*>(&type), reinterpret_cast<const uint8_t*>(&type) + 4);
+        ++n_paires;
+    };
+    auto chaine = [&](const char* c, const char* v) {
+        cle(c, 8);
+        const uint64_t n = std::strlen(v);
+        meta.insert(meta.end(), reinterpret_cast<const uint8_t*>(&n), reinterpret_cast<const uint8_t*>(&n) + 8);
+        meta.insert(meta.end(), v, v + n);
+    };
+    auto u32 = [&](const char* c, uint32_t v) {
+        cle(c, 4);
+        meta.insert(meta.end(), reinterpret_cast<const uint8_t*>(&v), reinterpret_cast<const uint8_t*>(&v) + 4);
+    };
+    auto u64 = [&](const char* c, uint64_t v) {
+        cle(c, 10);
+        meta.insert(meta.end(), reinterpret_cast<const uint8_t*>(&v), reinterpret_cast<const uint8_t*>(&v) + 8);
+    };
+    chaine("general.architecture", "gpt-oss");
+    chaine("general.name", "synthetique");
+    u32("gpt-oss.block_count", couches);
+    u32("gpt-oss.embedding_length", D);
+    u32("gpt-oss.expert_feed_forward_length", dims->lignes[0]);
+    u32("gpt-oss.expert_count", experts);
+    u32("gpt-oss.expert_used_count", k);
+    chaine("troncons.codeur.version", "troncons_amd codeur synthetique");
+    chaine("troncons.source.nom", "synthetique");
+    u64("troncons.synth.graine", graine);
+    u32("troncons.synth.pas_delta", N_delta);
+    u32("troncons.synth.pas_codes", N_codes);
+
+    trc_ecrivain* w = trc_ecrivain_creer(chemin);
+    if (w == nullptr) return TRC_FORMAT_ES;
+    int r = trc_ecrivain_meta(w, meta.data(), meta.size(), n_paires);
+    // RÉSIDENTS: the routers, bf16 rows of D values per expert
+    std::vector<std::vector<uint8_t>> routeurs(couches);
+    std::vector<trc_resident> res(couches);
+    std::vector<const uint8_t*> donnees(couches);
+    if (r == TRC_OK) {
+        std::vector<float> ligne(D);
+        for (uint32_t c = 0; c < couches; ++c) {
+            routeurs[c].resize(size_t(experts) * D * 2);
+            for (uint32_t e = 0; e < experts; ++e) {
+                trc_synth_normale_bf16(graine + c, 3, e, D, 0.02f, ligne.data());
+                for (uint32_t i = 0; i < D; ++i) {
+                    uint32_t bits;
+                    std::memcpy(&bits, &ligne[i], 4);
+                    const uint16_t h = uint16_t(bits >> 16);  // the values are bf16-exact
+                    std::memcpy(&routeurs[c][(size_t(e) * D + i) * 2], &h, 2);
+                }
+            }
+            std::memset(&res[c], 0, sizeof(trc_resident));
+            std::snprintf(res[c].nom, sizeof(res[c].nom), "blk.%u.ffn_gate_inp.weight", c);
+            res[c].type_ggml = 30;  // GGML_TYPE_BF16
+            res[c].n_dims = 2;
+            res[c].ne[0] = D;
+            res[c].ne[1] = experts;
+            res[c].ne[2] = res[c].ne[3] = 1;
+            res[c].octets = routeurs[c].size();
+            donnees[c] = routeurs[c].data();
+        }
+        r = trc_ecrivain_residents(w, res.data(), donnees.data(), couches);
+    }
+    if (r == TRC_OK) r = trc_ecrivain_troncons(w, couches, experts);
+    // TRONÇONS layer by layer; each layer's 12 tables are kept for the TABLES section
+    std::vector<trc_table> tables;
+    for (uint32_t c = 0; c < couches && r == TRC_OK; ++c) {
+        trc_couche_synth* cs = trc_synth_couche(graine, c, experts, dims, N_delta, N_codes, n_fils);
+        if (cs == nullptr) {
+            r = TRC_ERREUR_USAGE;
+            break;
+        }
+        for (uint32_t e = 0; e < experts && r == TRC_OK; ++e)
+            r = trc_ecrivain_partie(w, uint16_t(c), uint16_t(e), cs->parties[e].data(), cs->parties[e].size(), nullptr,
+                                    0, cs->empreinte_origine[e], cs->empreinte_canonique[e], nullptr);
+        for (uint8_t j = 0; j < 3; ++j)
+            for (int t = 0; t < 4; ++t) {
+                trc_table tb;
+                std::memset(&tb, 0, sizeof(tb));
+                tb.couche = uint16_t(c);
+                tb.matrice = j;
+                tb.sorte = t == 0 ? trc::SORTE_DELTA : trc::SORTE_CODES_CTX;
+                tb.contexte = uint8_t(t == 0 ? 0 : t - 1);
+                tb.type_charge = 2;
+                std::memcpy(tb.charge.frequences, cs->freqs[j][t], 512);
+                tables.push_back(tb);
+            }
+        trc_synth_couche_liberer(cs);
+    }
+    if (r == TRC_OK) r = trc_ecrivain_tables(w, tables.data(), uint32_t(tables.size()));
+    if (r != TRC_OK) {
+        const std::string m = trc::derniere_erreur();
+        trc_ecrivain_abandonner(w);
+        trc::derniere_erreur() = m;
+        return r;
+    }
+    trc_entete_fichier en;
+    std::memset(&en, 0, sizeof(en));
+    en.version_majeure = 1;
+    en.version_mineure = 2;
+    en.drapeaux = TRC_DRAPEAU_ALIGNE | TRC_DRAPEAU_CANONIQUE;
+    trc_sha256(meta.data(), meta.size(), en.sha256_source);  // no source GGUF: the MÉTA pairs stand for it
+    en.taille_source = 0;
+    en.couches = couches;
+    en.experts = experts;
+    en.k = k;
+    en.matrices = 3;
+    for (int j = 0; j < 3; ++j) {
+        en.lignes[j] = dims->lignes[j];
+        en.colonnes[j] = dims->colonnes[j];
+    }
+    en.poids_par_bloc = 32;
+    en.octets_par_bloc = 17;
+    en.type_ggml = 39;
+    en.niveaux = 1;
+    en.classes_echelle = 3;
+    return trc_ecrivain_terminer(w, &en, taille);
+}
 
 }  // extern "C"
