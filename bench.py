@@ -57,22 +57,91 @@ def lire_flux(partie: bytes):
     return out
 
 
-class CoucheResidente:
-    """One synthetic layer resident on the device: the experts' parts in one allocation (each
-    256-byte aligned), their address table, the mounted directory, the layer LUTs and the router."""
+class SourceSynth:
+    """A layer generated in memory by the encoder (parts, tables) with its seeded bf16 router."""
 
-    def __init__(self, graine, indice, E, dims, N_delta, N_codes, n_fils, dev, fz, flux):
+    def __init__(self, graine, indice, E, dims, N_delta, N_codes, n_fils):
+        import numpy as np
+
+        from troncons_amd import codeur
+        self.h = codeur.CoucheSynthetique(graine, indice, E, dims, N_delta=N_delta, N_codes=N_codes, n_fils=n_fils)
+        r = np.stack([codeur.synth_normale_bf16(graine + indice, 3, e, dims.colonnes[0], 0.02) for e in range(E)])
+        self.r16 = (r.view(np.uint32) >> 16).astype(np.uint16)
+        self.taille, self.utiles, self.partie, self.freqs = self.h.taille, self.h.utiles, self.h.partie, self.h.freqs
+
+    def liberer(self):
+        self.h.liberer()
+
+
+class SourceFichier:
+    """One layer of an opened .trc file, read the way the reference scheduler reads it
+    (trc-ordo/src/lib.rs:265-273, 389-420, 746-760): LUT frequencies from TABLES, each part read
+    with its directory fingerprint and structure checked, the router from RÉSIDENTS."""
+
+    def __init__(self, fichier, couche, E):
+        import numpy as np
+        self.f, self.c = fichier, couche
+        self.entrees = [fichier.entree(couche, e) for e in range(E)]
+        (r,) = [r for r in fichier.residents() if r.nom == f"blk.{couche}.ffn_gate_inp.weight"]
+        assert r.type_ggml == 30 and r.ne[1] == E, "router resident: bf16, one row per expert"
+        self.r16 = fichier.donnees_resident(r).view(np.uint16).reshape(E, -1)
+
+    def taille(self, e):
+        return self.entrees[e].longueur[0]
+
+    def utiles(self, e):
+        return self.entrees[e].utiles[0]
+
+    def partie(self, e, dst=None):
+        return self.f.lire_partie(self.c, e, dst=dst)
+
+    def freqs(self):
+        return self.f.freqs_couche(self.c)
+
+    def liberer(self):
+        pass
+
+
+def ouvrir_fichier(args, E, k, dims, n_couches, n_fils):
+    """Opens --fichier, writing it first (the synthetic model, one layer at a time) if it is absent."""
+    from troncons_amd import conteneur
+    chemin = pathlib.Path(args.fichier)
+    t_ecr = 0.0
+    if not chemin.exists():
+        t = time.perf_counter()
+        conteneur.synth_fichier(chemin, args.graine, n_couches, E, k, dims, N_delta=args.n_delta,
+                                N_codes=args.n_codes, n_fils=n_fils)
+        t_ecr = time.perf_counter() - t
+        print(f"bench: wrote {chemin} ({chemin.stat().st_size / 1e9:.2f} GB, {t_ecr:.1f} s)", file=sys.stderr,
+              flush=True)
+    t = time.perf_counter()
+    f = conteneur.Fichier.ouvrir(chemin)
+    t_ouv = time.perf_counter() - t
+    e = f.entete()
+    attendu = (n_couches, E, k, args.graine, args.n_delta, args.n_codes)
+    lu = (e.couches, e.experts, e.k, f.paire("troncons.synth.graine").entier(),
+          f.paire("troncons.synth.pas_delta").entier(), f.paire("troncons.synth.pas_codes").entier())
+    assert lu == attendu, f"{chemin}: (layers, experts, k, seed, N_delta, N_codes) = {lu}, expected {attendu}"
+    assert list(e.lignes[:3]) == list(dims.lignes) and list(e.colonnes[:3]) == list(dims.colonnes)
+    info = {"path": str(chemin), "bytes": int(e.taille_fichier), "write_s": round(t_ecr, 1),
+            "open_s": round(t_ouv, 4), "opened_bytes_read": f.octets_lus_a_l_ouverture()}
+    return f, info
+
+
+class CoucheResidente:
+    """One layer resident on the device: the experts' parts in one allocation (each 256-byte
+    aligned), their address table, the mounted directory, the layer LUTs and the router."""
+
+    def __init__(self, source, E, dims, dev, fz, flux):
         import numpy as np
         import torch
 
-        from troncons_amd import codeur, fusion
+        from troncons_amd import fusion
         from troncons_amd import noyaux as K
         from troncons_amd.noyaux import VueCarte
 
         t = time.perf_counter()
-        self.hote = codeur.CoucheSynthetique(graine, indice, E, dims, N_delta=N_delta, N_codes=N_codes,
-                                             n_fils=n_fils)
-        self.t_gen = time.perf_counter() - t
+        self.hote = source
         tailles = [self.hote.taille(e) for e in range(E)]
         self.utiles = np.array([self.hote.utiles(e) for e in range(E)], np.int64)
         self.decal = np.concatenate([[0], np.cumsum(tailles)[:-1]]).astype(np.int64)
@@ -93,8 +162,7 @@ class CoucheResidente:
         freqs = self.hote.freqs()
         self.luts_np = K.luts_couche([[freqs[j][t] for t in range(4)] for j in range(3)])
         self.luts = torch.from_numpy(self.luts_np.view(np.int32)).to(dev)
-        routeur = np.stack([codeur.synth_normale_bf16(graine + indice, 3, e, C_GPT, 0.02) for e in range(E)])
-        self.r16 = torch.from_numpy((routeur.view(np.uint32) >> 16).astype(np.uint16).view(np.int16)).to(dev)
+        self.r16 = torch.from_numpy(np.ascontiguousarray(self.hote.r16).view(np.int16)).to(dev)
         # mount once: every part parsed into the device directory of stream locations
         self.rep = torch.zeros(fusion.taille_repertoire(E), dtype=torch.uint8, device=dev)
         ctl = torch.zeros(4, dtype=torch.int32, device=dev)
@@ -103,6 +171,7 @@ class CoucheResidente:
         torch.cuda.synchronize()
         assert (ctl.cpu().numpy() == 0).all(), f"mount control words {ctl.cpu().numpy()}"
         self.vrep, self.vluts, self.vr16 = V(self.rep), V(self.luts), V(self.r16)
+        self.t_charge = time.perf_counter() - t
 
     def vue_partie(self, e):
         from troncons_amd.noyaux import VueCarte
@@ -118,9 +187,11 @@ def baseline_cpu(couche, luts, x_tok, selections, budget_s: float, n_fils: int):
     import numpy as np
     import oracle_ffi as O
 
+    # the parts are fetched before the clock starts: the baseline times decode and compute, not reads
+    parts = {e: bytes(couche.partie(e)) for e in sorted({int(e) for idx, _w in selections for e in idx})}
+
     def expert(e, x):
-        p = bytes(couche.partie(int(e)))
-        slot, ctl = O.decoder_expert(p, luts, [2880] * 3, [2880] * 3)
+        slot, ctl = O.decoder_expert(parts[int(e)], luts, [2880] * 3, [2880] * 3)
         d = [O.disposition_j([2880] * 3, [2880] * 3, j) for j in range(3)]
         g = O.gemv_mxfp4(slot[d[0].base:d[0].base + d[0].pas], x, 2880, 2880)
         u = O.gemv_mxfp4(slot[d[1].base:d[1].base + d[1].pas], x, 2880, 2880)
@@ -301,19 +372,25 @@ def bench_flux(args, E, k, C, dims, dev, flux, fz, x_tok, n_fils):
     nk = K.Noyaux()
     L = args.couches
     epingles, decal, tailles, vluts, routeurs = [], [], [], [], []
+    fichier, info_fichier = (ouvrir_fichier(args, E, k, dims, L, n_fils) if args.fichier else (None, None))
     t0 = time.perf_counter()
     for l in range(L):
-        h = codeur.CoucheSynthetique(args.graine, l, E, dims, N_delta=args.n_delta, N_codes=args.n_codes,
-                                     n_fils=n_fils)
+        if fichier is None:
+            h = SourceSynth(args.graine, l, E, dims, args.n_delta, args.n_codes, n_fils)
+        else:
+            h = SourceFichier(fichier, l, E)
         t = np.array([h.taille(e) for e in range(E)], np.int64)
         d = np.concatenate([[0], np.cumsum((t + 255) // 256 * 256)[:-1]]).astype(np.int64)
         pin = torch.empty(int(d[-1] + t[-1]), dtype=torch.uint8, pin_memory=True)
         vue_pin = pin.numpy()
         for e in range(E):
-            vue_pin[d[e]:d[e] + t[e]] = h.partie(e)
+            if fichier is None:
+                vue_pin[d[e]:d[e] + t[e]] = h.partie(e)
+            else:  # read (and checked) straight into pinned memory, as the reference's readers do
+                h.partie(e, dst=vue_pin[d[e]:d[e] + t[e]])
         freqs = h.freqs()
         luts = torch.from_numpy(K.luts_couche([[freqs[j][q] for q in range(4)] for j in range(3)]).view(np.int32)).to(dev)
-        r = np.stack([codeur.synth_normale_bf16(args.graine + l, 3, e, C, 0.02) for e in range(E)])
+        r = (np.ascontiguousarray(h.r16).astype(np.uint32) << 16).view(np.float32)
         routeurs.append(torch.from_numpy(r).to(dev))
         h.liberer()
         epingles.append(pin)
@@ -389,7 +466,7 @@ def bench_flux(args, E, k, C, dims, dev, flux, fz, x_tok, n_fils):
     ms_calcul = temps(pas, args.steps, args.warmup, flux)
     us, us_c, us_k = (m * 1e3 / args.steps for m in (ms, ms_copie, ms_calcul))
     recouvrement = (us_c + us_k - us) / min(us_c, us_k)
-    return {
+    ligne = {
         "metric": f"config4 streaming us/token for the MoE part of {L} layers (experts in pinned host memory)",
         "value": round(us, 1), "unit": "us/token", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(ms / args.steps, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
@@ -408,6 +485,10 @@ def bench_flux(args, E, k, C, dims, dev, flux, fz, x_tok, n_fils):
         "per_layer_us": round(us / L, 1),
         "setup_s": round(t_gen, 1),
     }
+    if info_fichier is not None:
+        ligne["config"]["source"] = ".trc v1.2 file: parts read with fingerprints checked into pinned memory"
+        ligne["trc_file"] = info_fichier
+    return ligne
 
 
 def chrono_passes(fusion, pas, n):
@@ -450,6 +531,9 @@ def main():
     ap.add_argument("--flux", action="store_true",
                     help="--config 4 variant: the experts stay in pinned host memory and the chosen ones are "
                          "copied per layer on a side stream, overlapped with the decode")
+    ap.add_argument("--fichier", default=None,
+                    help="load the layers from this .trc file (written first from the seeded model if absent), "
+                         "as the reference engine loads them, instead of encoding them in memory")
     ap.add_argument("--experts", type=int, default=128)
     ap.add_argument("--k", type=int, default=4)
     ap.add_argument("--n-codes", type=int, default=16, help="macro-steps per CODES_CTX tile written by the encoder")
@@ -487,11 +571,20 @@ def main():
         return
 
     n_couches = args.couches if args.config == 4 else 1
+    fichier, info_fichier = (ouvrir_fichier(args, E, k, dims, n_couches, n_fils) if args.fichier else (None, None))
     couches = []
+    t_gen = 0.0
     for l in range(n_couches):
-        couches.append(CoucheResidente(args.graine, l, E, dims, args.n_delta, args.n_codes, n_fils, dev, fz, flux))
-        print(f"bench: layer {l} encoded and mounted ({couches[-1].t_gen:.1f} s)", file=sys.stderr, flush=True)
-    t_gen = sum(c.t_gen for c in couches)
+        t = time.perf_counter()
+        if fichier is None:
+            source = SourceSynth(args.graine, l, E, dims, args.n_delta, args.n_codes, n_fils)
+        else:
+            source = SourceFichier(fichier, l, E)
+        t_gen += time.perf_counter() - t
+        couches.append(CoucheResidente(source, E, dims, dev, fz, flux))
+        t_gen += couches[-1].t_charge
+        print(f"bench: layer {l} {'encoded' if fichier is None else 'read from the file'} and mounted "
+              f"({t_gen:.1f} s so far)", file=sys.stderr, flush=True)
     c0 = couches[0]
     x_tok = np.stack([codeur.synth_normale_bf16(args.graine, 4, t, C, 1.0) for t in range(args.tokens)])
     xs = torch.from_numpy(x_tok).to(dev)
@@ -626,6 +719,9 @@ def main():
         "roofline": roofline,
         "setup_s": round(t_gen, 1),
     }
+    if info_fichier is not None:
+        ligne["config"]["source"] = ".trc v1.2 file: parts read with fingerprints checked, tables, router resident"
+        ligne["trc_file"] = info_fichier
     if not args.sans_cpu and n_couches == 1:
         selections = [(sel[t, 0], sel_w[t, 0, :k].cpu().numpy()) for t in range(min(args.steps, 20))]
         ligne["cpu_baseline"] = baseline_cpu(c0.hote, c0.luts_np, x_tok, selections, args.budget_cpu, n_fils)
