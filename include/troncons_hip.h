@@ -430,6 +430,88 @@ int trc_ecrivain_partie(trc_ecrivain* w, uint16_t couche, uint16_t expert, const
 /* Ecrivain::terminer (lib.rs:1227-1239): sections, size and fingerprint are filled in; frees w. */
 int trc_ecrivain_terminer(trc_ecrivain* w, const trc_entete_fichier* entete, uint64_t* taille);
 
+/* ----------------------------------------------- the expert slot cache (host only; trc-cache)
+ *
+ * Replaces moteur/crates/trc-cache (lib.rs:1-321, politiques.rs, trace.rs): a two-stage cache —
+ * VRAM slots of decoded experts, warm-RAM entries of coded parts — with LRU, FIFO or Belady
+ * replacement, and the simulator that replays a routing trace through the same code. Ids are
+ * (couche << 16) | expert. */
+
+#define TRC_POLITIQUE_LRU 0
+#define TRC_POLITIQUE_BELADY 1 /* offline optimum: needs the trace of the future */
+#define TRC_POLITIQUE_FIFO 2   /* LRU whose hits do not refresh */
+
+#define TRC_CACHE_LIBRE 0
+#define TRC_CACHE_EN_VOL 1  /* being decoded: never evicted */
+#define TRC_CACHE_PRESENT 2
+
+#define TRC_DECISION_SUCCES 0       /* the expert is (or will be, if in flight) in `emplacement` */
+#define TRC_DECISION_DEFAUT_RAM 1   /* VRAM miss; the coded part is in warm entry `tiede` */
+#define TRC_DECISION_DEFAUT_DISQUE 2 /* read the part (into `tiede` if >= 0), copy, decode */
+
+/* ErreurTrace (trace.rs:140-152) */
+#define TRC_TRACE_LIGNE 32
+#define TRC_TRACE_HORS_BORNES 33
+#define TRC_TRACE_VIDE 34
+
+/* Decision (lib.rs:74-84) */
+typedef struct {
+    uint32_t sorte;
+    uint32_t emplacement;
+    int32_t tiede; /* -1: none */
+    uint32_t reserve;
+} trc_decision;
+
+/* Compteurs (lib.rs:87-102), plus the RAM stage's evictions */
+typedef struct {
+    uint64_t succes_vram;
+    uint64_t succes_ram;
+    uint64_t defauts_disque;
+    uint64_t octets_disque;
+    uint64_t octets_copies;
+    uint64_t evictions;
+    uint64_t evictions_ram;
+} trc_compteurs_cache;
+
+typedef struct trc_trace trc_trace;
+/* Trace::depuis_texte (trace.rs:51-130): one token per line, layers split by '|', experts by
+ * blanks, '#' comments, optional "E=<n>". */
+int trc_trace_depuis_texte(const char* texte, uint64_t n, trc_trace** trace);
+/* choix[(t * couches + l) * k + i] */
+int trc_trace_creer(uint16_t experts, uint16_t couches, uint16_t k, uint32_t jetons, const uint16_t* choix,
+                    trc_trace** trace);
+void trc_trace_dimensions(const trc_trace* t, uint32_t dims[4]); /* experts, couches, k, jetons */
+const uint16_t* trc_trace_groupe(const trc_trace* t, uint32_t jeton, uint32_t couche);
+void trc_trace_liberer(trc_trace* t);
+
+typedef struct trc_cache trc_cache;
+/* Cache::nouveau (lib.rs:111-128); `avenir` only for Belady. */
+int trc_cache_creer(uint32_t emplacements, uint32_t tiedes, int politique_vram, int politique_ram,
+                    const trc_trace* avenir, trc_cache** cache);
+void trc_cache_detruire(trc_cache* c);
+/* Cache::fixer_tailles (lib.rs:131-133): bytes read for each (couche, expert). */
+int trc_cache_fixer_tailles(trc_cache* c, uint16_t couches, uint16_t experts, const uint64_t* tailles);
+/* Cache::demander (lib.rs:139-180): pins the layer's experts, one decision each, in order.
+ * TRC_ERREUR_USAGE when a miss finds no free or evictable slot (the cache is then unusable). */
+int trc_cache_demander(trc_cache* c, uint16_t couche, const uint16_t* experts, uint32_t n, uint64_t t,
+                       trc_decision* decisions);
+/* Cache::pret (lib.rs:233-239): the slot's decode is done (EN_VOL -> PRESENT). */
+int trc_cache_pret(trc_cache* c, uint32_t emplacement);
+/* Cache::liberer (lib.rs:242-244): the layer's experts are unpinned. */
+void trc_cache_liberer_couche(trc_cache* c, uint16_t couche);
+trc_compteurs_cache trc_cache_compteurs(const trc_cache* c);
+int trc_cache_etat(const trc_cache* c, uint32_t emplacement);
+int64_t trc_cache_occupant(const trc_cache* c, uint32_t emplacement);                  /* -1: free */
+int64_t trc_cache_emplacement_de(const trc_cache* c, uint16_t couche, uint16_t expert); /* -1: absent */
+int64_t trc_cache_tiede_de(const trc_cache* c, uint16_t couche, uint16_t expert);      /* -1: absent */
+uint32_t trc_cache_epingles(const trc_cache* c, uint32_t* ids, uint32_t max);
+/* Lru::ordre (politiques.rs:93-101): VRAM ids oldest first (LRU/FIFO only, else 0). */
+uint32_t trc_cache_ordre_vram(const trc_cache* c, uint32_t* ids, uint32_t max);
+/* rejouer / rejouer_dans (lib.rs:282-309): the simulator. */
+int trc_cache_rejouer(const trc_trace* t, uint32_t emplacements, uint32_t tiedes, int politique_vram,
+                      int politique_ram, trc_compteurs_cache* compteurs);
+int trc_cache_rejouer_dans(trc_cache* c, const trc_trace* t, trc_compteurs_cache* compteurs);
+
 /* ---------------------------------------- encoder front-end (host only; role of bins/trc-codeur) */
 
 /* The seeded synthetic workload (nibble law "A", E8M0 scales in [119,125], bf16 N(0,0.02) biases).
