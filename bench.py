@@ -491,6 +491,88 @@ def bench_flux(args, E, k, C, dims, dev, flux, fz, x_tok, n_fils):
     return ligne
 
 
+def bench_ordo(args, E, k, C, dims, dev, n_fils):
+    """Config 4, native streaming scheduler with the slot cache (csrc/ordo.cpp): the layers' parts
+    stay in the .trc file; per layer the router's top-k goes through a mapped mailbox, the cache
+    decides, misses are read from the file (pread, reader threads) into pinned memory, copied and
+    decoded into VRAM slots, then the layer's MLPs run over the decoded slots (reference GEMV
+    order) and the combine. Warm-up tokens fill the cache; the timed tokens follow."""
+    import numpy as np
+    import torch
+
+    from troncons_amd import cache as K
+    from troncons_amd import codeur
+    from troncons_amd.ordo import Ordonnanceur
+    L = args.couches
+    if not args.fichier:
+        args.fichier = f"/tmp/trc_bench_L{L}_E{E}_g{args.graine}_n{args.n_delta}-{args.n_codes}.trc"
+    fichier, info_fichier = ouvrir_fichier(args, E, k, dims, L, n_fils)
+    n_empl = args.emplacements or L * E
+    t0 = time.perf_counter()
+    o = Ordonnanceur(fichier, emplacements=n_empl, tiedes=args.tiedes, verifier=args.verifier)
+    t_creer = time.perf_counter() - t0
+    n_tok = args.warmup + args.steps
+    x_tok = np.stack([codeur.synth_normale_bf16(args.graine, 4, t, C, 1.0) for t in range(n_tok)])
+    xs = torch.from_numpy(x_tok).to(dev)
+    residu = torch.zeros(dims.lignes[2], dtype=torch.float32, device=dev)
+    vx = [VueCarte_de(xs, 4 * C * t, 4 * C) for t in range(n_tok)]
+    for t in range(args.warmup):
+        o.jeton(vx[t], residu)
+    torch.cuda.synchronize()
+    c0, s0 = o.compteurs(), o.stats()
+    t0 = time.perf_counter()
+    for t in range(args.warmup, n_tok):
+        o.jeton(vx[t], residu)
+        if (t - args.warmup) % 100 == 99:
+            print(f"bench: {t - args.warmup + 1} timed tokens", file=sys.stderr, flush=True)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    ctl = o.controle()
+    assert (ctl == 0).all(), f"control words {ctl}"
+    c1, s1 = o.compteurs(), o.stats()
+    n = args.steps
+    acces = (c1.acces() - c0.acces())
+    tr = o.trace()
+    sim = K.Cache(n_empl, args.tiedes)
+    sim.fixer_tailles(np.array([[fichier.entree(l, e).longueur[0] for e in range(E)] for l in range(L)], np.uint64))
+    accord = sim.rejouer_dans(K.Trace.de(E, tr)).tuple() == c1.tuple()
+    belady = K.rejouer(K.Trace.de(E, tr), n_empl, 0, K.BELADY, K.BELADY)
+    us = dt / n * 1e6
+    ligne = {
+        "metric": f"config4 native streaming us/token for the MoE part of {L} layers (slot cache, parts read from "
+                  "the .trc file)",
+        "value": round(us, 1), "unit": "us/token", "n_gpus": 1, "steps": n, "warmup": args.warmup,
+        "ms_per_step": round(dt / n * 1e3, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "u32 rANS decode into slots / f32 GEMV",
+        "data": "synthetic (seeded MXFP4 law A, E8M0 in [119,125], bf16 N(0,1) activations, bf16 N(0,0.02) router)",
+        "config": {"workload": f"config4 streaming, native scheduler: {L} layers x {E} experts in a .trc file, "
+                               f"{n_empl} decoded-expert slots in HBM ({n_empl * 13.254144e-3:.1f} GB), "
+                               f"{args.tiedes} pinned warm entries, LRU", "layers": L, "experts": E, "k": k,
+                   "slots": n_empl, "warm_entries": args.tiedes, "n_codes": args.n_codes, "n_delta": args.n_delta,
+                   "verify_reads": bool(args.verifier)},
+        "hit_rate_vram": round((c1.succes_vram - c0.succes_vram) / acces, 4),
+        "hit_rate_ram": round((c1.succes_ram - c0.succes_ram) / acces, 4),
+        "disk_misses_per_token": round((c1.defauts_disque - c0.defauts_disque) / n, 3),
+        "bytes_read_per_token": int((s1.octets_lus - s0.octets_lus) / n),
+        "bytes_copied_per_token": int((s1.octets_copies - s0.octets_copies) / n),
+        "host_us_per_layer": {"router_wait": round((s1.us_attente_routeur - s0.us_attente_routeur) / (n * L), 2),
+                              "reads_and_sends": round((s1.us_lectures - s0.us_lectures) / (n * L), 2),
+                              "issue": round((s1.us_emission - s0.us_emission) / (n * L), 2)},
+        "per_layer_us": round(us / L, 2),
+        "simulator_agrees": bool(accord),
+        "belady_hit_rate_whole_run": round(belady.succes_vram / belady.acces(), 4),
+        "lru_hit_rate_whole_run": round(c1.succes_vram / c1.acces(), 4),
+        "trc_file": info_fichier, "setup_s": round(t_creer, 2),
+    }
+    o.detruire()
+    return ligne
+
+
+def VueCarte_de(t, decalage, octets):
+    from troncons_amd.noyaux import VueCarte
+    return VueCarte.de(t, decalage, octets)
+
+
 def chrono_passes(fusion, pas, n):
     """Per-kernel durations over n steps: every kernel launched with the start/stop events that the
     runtime records at the kernel's own start and end (hipExtLaunchKernel). Kept out of the timed
@@ -534,6 +616,12 @@ def main():
     ap.add_argument("--fichier", default=None,
                     help="load the layers from this .trc file (written first from the seeded model if absent), "
                          "as the reference engine loads them, instead of encoding them in memory")
+    ap.add_argument("--ordo", action="store_true",
+                    help="--config 4 variant: the native streaming scheduler with the slot cache, parts read from "
+                         "the .trc file (--fichier, written first if absent)")
+    ap.add_argument("--emplacements", type=int, default=0, help="--ordo: decoded-expert slots in HBM (0: all)")
+    ap.add_argument("--tiedes", type=int, default=0, help="--ordo: pinned warm-RAM entries of coded parts")
+    ap.add_argument("--verifier", action="store_true", help="--ordo: check every part read against its fingerprint")
     ap.add_argument("--experts", type=int, default=128)
     ap.add_argument("--k", type=int, default=4)
     ap.add_argument("--n-codes", type=int, default=16, help="macro-steps per CODES_CTX tile written by the encoder")
@@ -564,6 +652,10 @@ def main():
     fz = fusion.Fusion()
     flux = torch.cuda.current_stream()
     V = VueCarte.de
+
+    if args.config == 4 and args.ordo:
+        print(json.dumps(bench_ordo(args, E, k, C, dims, dev, n_fils)), flush=True)
+        return
 
     if args.config == 4 and args.flux:
         x_tok = np.stack([codeur.synth_normale_bf16(args.graine, 4, t, C, 1.0) for t in range(args.tokens)])

@@ -512,6 +512,55 @@ int trc_cache_rejouer(const trc_trace* t, uint32_t emplacements, uint32_t tiedes
                       int politique_ram, trc_compteurs_cache* compteurs);
 int trc_cache_rejouer_dans(trc_cache* c, const trc_trace* t, trc_compteurs_cache* compteurs);
 
+/* ------------------------------------------ the streaming scheduler (host over HIP; trc-ordo)
+ *
+ * The expert path of Moteur::pas (moteur/crates/trc-ordo/src/lib.rs:1054-1280) as a native
+ * engine over an opened .trc file: per layer, router + top-k into a mapped mailbox, one wait on
+ * the router's event, the cache's decisions, disk misses read at once by reader threads (pread)
+ * into pinned warm entries, each part copied on a copy stream and decoded into its VRAM slot as
+ * soon as it is on the host, then the layer's expert MLPs over the decoded slots (gemv_lot gate/up,
+ * swiglu_oai, gemv_lot down) and the ordered combine (trc-modele/src/lib.rs:533-553). The engine
+ * owns its device slots, arrival buffers, pinned entries, mailbox and copy stream (it allocates at
+ * creation); the compute stream is the caller's `flux`. An error leaves the engine unusable. */
+
+typedef struct {
+    uint32_t emplacements; /* VRAM slots of decoded experts (at least k) */
+    uint32_t tiedes;       /* pinned warm-RAM entries of coded parts (0: none) */
+    int politique;         /* TRC_POLITIQUE_LRU or TRC_POLITIQUE_FIFO */
+    int verifier;          /* check each part read against its directory fingerprint */
+    uint32_t lecteurs;     /* reader threads (0: k) */
+} trc_config_ordo;
+
+/* CompteursMoteur (trc-ordo/src/lib.rs:586-594), the expert path's share */
+typedef struct {
+    uint64_t jetons;
+    uint64_t lectures;
+    uint64_t octets_lus;
+    uint64_t octets_copies;
+    uint64_t decodages;
+    double us_attente_routeur; /* host time waiting for the router's event */
+    double us_lectures;        /* host time from submitting the reads to the last part sent */
+    double us_emission;        /* host time issuing the router and the layer's MLPs */
+} trc_stats_ordo;
+
+typedef struct trc_ordo trc_ordo;
+/* Moteur::nouveau (lib.rs:376-560), the expert path: slots, LUTs and routers of every layer. */
+int trc_ordo_creer(const trc_fichier* f, const trc_config_ordo* cfg, trc_ordo** ordo);
+/* One token through every layer's MoE part: residu += combine of the k experts chosen from x. */
+int trc_ordo_jeton(trc_ordo* o, trc_vue x, trc_vue residu, void* flux);
+/* Waits for flux and copies out the control words (all zero on a good run). */
+int trc_ordo_controle(trc_ordo* o, uint32_t mots[4], void* flux);
+trc_compteurs_cache trc_ordo_compteurs(const trc_ordo* o);
+trc_stats_ordo trc_ordo_stats(const trc_ordo* o);
+/* The routing the engine saw, jetons x couches x k ids (Moteur::texte_trace, lib.rs:633-649). */
+uint64_t trc_ordo_trace(const trc_ordo* o, uint16_t* choix, uint64_t max);
+/* The VRAM slot of a present expert (for the witness: trc_empreinte_emplacement). */
+int trc_ordo_emplacement(const trc_ordo* o, uint16_t couche, uint16_t expert, trc_vue* vue);
+/* The witness (trc-ordo/src/lib.rs:238-262): waits for flux, copies a present expert's slot to the
+ * host and returns its empreinte64 (to compare with the directory's canonical fingerprint). */
+int trc_ordo_temoin(const trc_ordo* o, uint16_t couche, uint16_t expert, void* flux, uint64_t* empreinte);
+void trc_ordo_detruire(trc_ordo* o);
+
 /* ---------------------------------------- encoder front-end (host only; role of bins/trc-codeur) */
 
 /* The seeded synthetic workload (nibble law "A", E8M0 scales in [119,125], bf16 N(0,0.02) biases).
