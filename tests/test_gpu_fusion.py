@@ -207,6 +207,42 @@ def test_fused_moe_layer_config3(fz):
     couche.liberer()
 
 
+def test_fused_moe_router_ties_and_order(fz):
+    """The fused layer's top-k on tied logits: experts 2 and 9 get identical router rows, as do 5 and
+    6, all scaled to win; the selection must be the reference's (logit desc, index asc), i.e. the
+    oracle's routeur_topk on the same logits, and the weights its f64 softmax."""
+    E, k, N = 12, 4, (16, 32)
+    couche = codeur.CoucheSynthetique(2029, 0, E, GPT, N_delta=N[0], N_codes=N[1])
+    freqs = couche.freqs()
+    luts = O.luts_couche([[freqs[j][t] for t in range(4)] for j in range(3)])
+    parts = [dev(couche.partie(e)) for e in range(E)]
+    table = dev(np.array([p.data_ptr() for p in parts], np.uint64))
+    rep, ctl0 = zeros(fusion.taille_repertoire(E)), zeros(16)
+    fz.monter_couche(vue(table), E, GPT, vue(rep), vue(ctl0))
+    base = np.stack([O.synth_normale_bf16(2029, 3, e, 2880, 0.02) for e in range(E)])
+    for t in range(3):
+        x = O.synth_normale_bf16(2029, 4, t, 2880, 1.0)
+        # rows 2 = 9 and 5 = 6, turned towards x and scaled by 4 (a power of two: still bf16-exact),
+        # so that the top-4 is exactly the two tied pairs
+        routeur = base.copy()
+        for a, b in ((2, 9), (5, 6)):
+            r = base[a] * (4.0 if float(base[a] @ x) > 0 else -4.0)
+            routeur[a] = routeur[b] = r
+        r16 = (routeur.view(np.uint32) >> 16).astype(np.uint16)
+        l, rd, xd, res = dev(luts), dev(r16), dev(x), dev(np.zeros(2880, np.float32))
+        idx, w, ctl = zeros(32), zeros(32), zeros(16)
+        tr = zeros(fusion.taille_travail_couche(GPT, E, k, N[1]))
+        fz.couche_moe(vue(rep), E, vue(l), GPT, vue(rd), None, vue(xd), k, vue(res), vue(idx), vue(w), vue(ctl),
+                      vue(tr), *N)
+        logits = O.gemv_f32(routeur, x)
+        oi, ow = O.routeur_topk(logits, k)
+        assert sorted(oi) == [2, 5, 6, 9] and logits[2] == logits[9] and logits[5] == logits[6]
+        assert (hote(idx, np.uint32)[:k] == oi).all(), (t, hote(idx, np.uint32)[:k], oi)
+        assert np.abs(hote(w, np.float32)[:k] - ow).max() <= 1e-6
+        assert list(hote(ctl, np.uint32)) == [0, 0, 0, 0]
+    couche.liberer()
+
+
 def test_fused_moe_layer_bad_parts(fz):
     """A layer whose parts all fail the mount checks: the step counts format errors in every pass
     that meets a bad directory entry and leaves the residual alone (nothing is combined)."""

@@ -245,6 +245,7 @@ __device__ __forceinline__ uint32_t somme_vague_u32(uint32_t v) {
 }
 
 __device__ __forceinline__ void verser_controle(uint32_t* controle, uint32_t hors_l, uint32_t pointeur) {
+    if (__builtin_amdgcn_ballot_w64((hors_l | pointeur) != 0u) == 0) return;  // the usual case: nothing to count
     hors_l = somme_vague_u32(hors_l);
     pointeur = somme_vague_u32(pointeur);
     if (__lane_id() == 0) {

@@ -44,31 +44,41 @@ fusion_echelles(trc::Taches taches, const uint32_t* __restrict__ luts, uint32_t*
     __shared__ __attribute__((aligned(16))) uint8_t med[MED_LDS_MAX];
     __shared__ __attribute__((aligned(16))) uint8_t anneaux[(FILS_ECHELLES_FUSION / 32) * OCTETS_ANNEAU];
     __shared__ uint32_t choisis[TOPK_MAX];
+    __shared__ float lg[EXPERTS_MAX];
+    __shared__ uint32_t rangs[EXPERTS_MAX];
     const bool moe = taches.mode == TACHES_MOE_DELTA;
     const bool prefill = taches.mode == TACHES_PREFILL_DELTA;
     if (prefill && reinterpret_cast<const uint32_t*>(taches.moe.compte)[blockIdx.y / 3u] == 0u) return;
     const uint32_t j_bloc = (moe || prefill) ? blockIdx.y % 3u : min(taches[blockIdx.y].j, 2u);
-    ChargeLut<1> charge_lut;
+    ChargeLut<LOT_LUT_ECHELLES> charge_lut;
     charge_lut.demarrer(luts + (uint64_t(j_bloc) * 4u + 0u) * M, M / 4u);
     Tache tc;
     if (moe) {
+        // the router's top-k, by ranks over the whole block (selection.hpp); only block (0, 0)
+        // computes the weights and publishes the selection for the later passes
         const ParamsMoe& pm = taches.moe;
-        if (threadIdx.x < 64u) {
-            uint32_t choisi[TOPK_MAX];
+        const float* logits = reinterpret_cast<const float*>(pm.logits);
+        for (uint32_t e = threadIdx.x; e < pm.E; e += blockDim.x) {
+            lg[e] = logits[e];
+            rangs[e] = 0u;
+        }
+        if (threadIdx.x < TOPK_MAX) choisis[threadIdx.x] = 0xFFFFFFFFu;
+        __syncthreads();
+        compter_rangs(lg, pm.E, rangs);
+        __syncthreads();
+        choisir_rangs(lg, rangs, pm.E, pm.k, choisis);
+        __syncthreads();
+        if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x < 64u) {
             float w[TOPK_MAX];
-            topk_vague(reinterpret_cast<const float*>(pm.logits), pm.E, pm.k, choisi, w);
-            if (threadIdx.x == 0) {
+            poids_topk(lg, choisis, pm.k, w);
+            if (threadIdx.x < pm.k) {
+                float wr = w[0];
 #pragma unroll
-                for (uint32_t r = 0; r < TOPK_MAX; ++r) {
-                    choisis[r] = choisi[r];
-                    if (r < pm.k && blockIdx.x == 0 && blockIdx.y == 0) {
-                        reinterpret_cast<uint32_t*>(pm.indices)[r] = choisi[r];
-                        reinterpret_cast<float*>(pm.poids)[r] = w[r];
-                    }
-                }
+                for (uint32_t r = 1; r < TOPK_MAX; ++r) wr = threadIdx.x == r ? w[r] : wr;
+                reinterpret_cast<uint32_t*>(pm.indices)[threadIdx.x] = choisis[threadIdx.x];
+                reinterpret_cast<float*>(pm.poids)[threadIdx.x] = wr;
             }
         }
-        __syncthreads();
         const uint32_t i = blockIdx.y / 3u;
         tc = uniforme(tache_moe_e(pm, i, blockIdx.y - 3u * i, choisis[i]));
     } else if (prefill) {
@@ -81,14 +91,15 @@ fusion_echelles(trc::Taches taches, const uint32_t* __restrict__ luts, uint32_t*
     if (moe && blockIdx.x == 0 && threadIdx.x == 0)  // the later passes of the layer read this copy
         ecrire_matrice(reinterpret_cast<void*>(taches.moe.resolus + uint64_t(blockIdx.y) * sizeof(MatricePartie)), m);
     const PrepEchelles p = preparer_echelles(tc, m);
-    charge_lut.poser(luts + (uint64_t(j_bloc) * 4u + 0u) * M, lut, M / 4u);
     if (!p.bon) {
         if (threadIdx.x == 0 && blockIdx.x == 0) atomicAdd(&controle[CTL_FORMAT], 1u);
         return;
     }
+    const TeteTuile tete0 = premiere_tete(p.h);  // in flight with the medians
     if (tc.lignes <= MED_LDS_MAX) copier_vers_lds(p.fm.p, tc.lignes, p.fm.longueur, med);
+    charge_lut.poser(luts + (uint64_t(j_bloc) * 4u + 0u) * M, lut, M / 4u);
     __syncthreads();
-    corps_echelles_fusion(tc, p, lut, med, anneaux, controle);
+    corps_echelles_fusion(tc, p, lut, med, anneaux, controle, tete0);
 }
 
 namespace trc {
@@ -122,14 +133,28 @@ fusion_gemv(trc::Taches taches, const uint32_t* __restrict__ luts, uint32_t* __r
     __shared__ __attribute__((aligned(16384))) uint8_t lds[LDS_GEMV];
     const Tache tc = uniforme(taches[blockIdx.y]);
     const uint32_t* lut_src = luts + (uint64_t(min(tc.j, 2u)) * 4u + 1u) * M;
+    // Every load that does not depend on the part is issued first: the LUT, and x (16-byte loads of
+    // a 16-byte aligned vector of colonnes % 32 == 0 floats; at most 4 per thread, blocks have at
+    // least 256 threads and x at most X_LDS_MAX columns), then the matrix record.
     ChargeLut<3> charge_lut;
     charge_lut.demarrer(lut_src, 3u * M / 4u);
+    const bool swiglu = (taches.options & OPT_SWIGLU) != 0u;
+    const bool x_lds = tc.colonnes <= X_LDS_MAX;
+    const uint32_t n16 = x_lds ? tc.colonnes / 4u : 0u;
+    u32x4 xv[4];
+#pragma unroll
+    for (uint32_t i = 0; i < 4; ++i) {
+        const uint32_t k = threadIdx.x + i * blockDim.x;
+        if (!swiglu && k < n16) xv[i] = glob<u32x4>(reinterpret_cast<const void*>(tc.x))[k];
+    }
     const PrepGemv p = preparer_gemv(tc, obtenir_matrice(tc));
+    const bool bon = p.bon && x_lds;
+    // the first tile's head, needed right after the barrier
+    const TeteTuile tete0 = bon ? premiere_tete(p.h) : TeteTuile{L, 0u, 0u};
     charge_lut.poser(lut_src, reinterpret_cast<uint2*>(lds + LDS_LUT), 3u * M / 4u);
-    const bool bon = p.bon && tc.colonnes <= X_LDS_MAX;
     if (!bon && threadIdx.x == 0 && blockIdx.x == 0) atomicAdd(&controle[CTL_FORMAT], 1u);
     if (bon) {
-        if (taches.options & OPT_SWIGLU) {
+        if (swiglu) {
             Fin* fins = reinterpret_cast<Fin*>(lds + LDS_ENT);  // the entry area is free until the tiles start
             const uint32_t w = threadIdx.x >> 6;
             if (w < 2u) {
@@ -137,19 +162,19 @@ fusion_gemv(trc::Taches taches, const uint32_t* __restrict__ luts, uint32_t* __r
                 if (__lane_id() == 0) fins[w] = f;
             }
             __syncthreads();
-            const Fin g = fins[0], u = fins[1];
-            const bool ok = g.bon && u.bon;
-            float* xs = reinterpret_cast<float*>(lds + LDS_X);
-            for (uint32_t r = threadIdx.x; r < tc.colonnes; r += blockDim.x)
-                xs[r] = (ok && r < g.lignes && r < u.lignes) ? swiglu_oai_f(somme_fin(g, r), somme_fin(u, r)) : 0.0f;
+            swiglu_vers_lds(fins[0], fins[1], tc.colonnes, reinterpret_cast<float*>(lds + LDS_X));
         } else {
-            copier_vers_lds(reinterpret_cast<const uint8_t*>(tc.x), 4u * tc.colonnes, 4u * tc.colonnes, lds + LDS_X);
+#pragma unroll
+            for (uint32_t i = 0; i < 4; ++i) {
+                const uint32_t k = threadIdx.x + i * blockDim.x;
+                if (k < n16) *reinterpret_cast<u32x4*>(lds + LDS_X + 16u * k) = xv[i];
+            }
         }
         if (threadIdx.x < 8u)  // the zero slot (column block 127) that stream padding blocks read
             *reinterpret_cast<u32x4*>(lds + LDS_X + COLONNE_NULLE * 128u + 16u * threadIdx.x) = u32x4{0u, 0u, 0u, 0u};
     }
     __syncthreads();
-    if (bon) corps_gemv_rapide(tc, p, lds, controle);
+    if (bon) corps_gemv_rapide(tc, p, lds, controle, tete0);
 }
 
 // CODES pass, x read from device memory (rows of any width).

@@ -196,7 +196,14 @@ struct Taches {
     }
 };
 
-constexpr uint32_t FILS_ECHELLES_FUSION = 1024;  // 16 wavefronts, 32 DELTA tiles
+#ifndef TRC_FILS_ECHELLES
+#define TRC_FILS_ECHELLES 1024
+#endif
+constexpr uint32_t FILS_ECHELLES_FUSION = TRC_FILS_ECHELLES;  // default 16 wavefronts, 32 DELTA tiles
+static_assert(FILS_ECHELLES_FUSION % 64 == 0 && FILS_ECHELLES_FUSION <= 1024, "whole wavefronts, one block");
+// LUT loads in flight per thread when a DELTA block stages its 4096-entry table (one 16-byte load
+// per thread at 1024 threads)
+constexpr uint32_t LOT_LUT_ECHELLES = (1024u + FILS_ECHELLES_FUSION - 1u) / FILS_ECHELLES_FUSION;
 constexpr uint32_t FILS_GEMV_MAX = 1024;        // up to 16 wavefronts, 32 CODES_CTX tiles
 constexpr uint32_t ENT_PAR_TUILE = 128;         // block entries staged per tile (16 macro-steps)
 constexpr uint32_t ECH_MARGE = 256;             // entries past the last block that staging may read
@@ -253,6 +260,29 @@ struct PrepEchelles {
     bool bon;
 };
 
+// A tile's head: its lanes' initial states, its first word, and the word its decode must end on
+// (the next tile's first, or W). Read one tile ahead, so that no decode waits for these loads.
+struct TeteTuile {
+    uint32_t x, debut, attendu;
+};
+
+__device__ __forceinline__ TeteTuile lire_tete(const EnteteRans& h, uint32_t t, uint32_t v) {
+    TeteTuile r{L, 0u, 0u};
+    if (t < h.T) {
+        r.x = h.etats[t * VOIES + v];
+        r.debut = h.debut[t];
+        r.attendu = (t + 1u < h.T) ? h.debut[t + 1u] : h.W;
+    }
+    return r;
+}
+
+// The head of the first tile of the calling lane's half-wavefront (the tile loops below start at
+// tile 2 * (global wavefront index), the upper half one further).
+__device__ __forceinline__ TeteTuile premiere_tete(const EnteteRans& h) {
+    const uint32_t vague = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    return lire_tete(h, 2u * vague + (__lane_id() >= 32u ? 1u : 0u), __lane_id() & 31u);
+}
+
 __device__ __forceinline__ PrepEchelles preparer_echelles(const Tache& tc, const MatricePartie& m) {
     PrepEchelles p;
     p.bon = m.bon != 0 && tc.colonnes % 32u == 0 && tc.colonnes >= 32u && tc.lignes > 0;
@@ -264,9 +294,10 @@ __device__ __forceinline__ PrepEchelles preparer_echelles(const Tache& tc, const
 
 // DELTA tiles -> one entry per block (entree_bloc) with e = (med[row] + delta - 128) mod 256 and
 // kappa = the class of delta; blocks past the matrix (stream padding) get the padding entry.
+// `tete0`: premiere_tete(p.h), read by the caller before its barrier.
 __device__ __forceinline__ void corps_echelles_fusion(const Tache& tc, const PrepEchelles& p, const uint2* lut,
                                                       const uint8_t* med_lds, uint8_t* anneaux,
-                                                      uint32_t* __restrict__ controle) {
+                                                      uint32_t* __restrict__ controle, const TeteTuile& tete0) {
     const EnteteRans& h = p.h;
     const uint32_t R = tc.lignes, B = tc.colonnes / 32u, nblocs = R * B;
     const uint8_t* med = R <= MED_LDS_MAX ? med_lds : p.fm.p;
@@ -281,14 +312,16 @@ __device__ __forceinline__ void corps_echelles_fusion(const Tache& tc, const Pre
     const uint32_t lds = ((threadIdx.x >> 5) & (2u * vagues_bloc - 1u)) * OCTETS_ANNEAU;
     const uint32_t nmacro = h.P / 128u;
     uint32_t hors_l = 0, pointeur = 0;
+    TeteTuile tete = tete0;
     for (uint32_t t0 = 2u * vague; t0 < h.T; t0 += 2u * n_vagues) {
         const uint32_t t = t0 + (haut ? 1u : 0u);
         const bool tuile = t < h.T;
         const uint32_t nb_a = min(h.N, nmacro - t0 * h.N);
         const uint32_t nb_b = (t0 + 1u < h.T) ? min(h.N, nmacro - (t0 + 1u) * h.N) : 0u;
         const uint32_t nb = haut ? nb_b : nb_a;
-        uint32_t x = tuile ? h.etats[t * VOIES + v] : L;
-        const uint32_t debut = tuile ? h.debut[t] : 0u;
+        uint32_t x = tete.x;
+        const uint32_t debut = tete.debut, attendu = tete.attendu;
+        tete = lire_tete(h, t + 2u * n_vagues, v);
         Anneau a = ouvrir_anneau(h, p.fd, debut, lds, anneaux, v, tuile);
         const uint32_t o0 = a.o2;
         uint32_t b0 = 4u * ((tuile ? t : t0) * h.N * VOIES + v);
@@ -330,7 +363,6 @@ __device__ __forceinline__ void corps_echelles_fusion(const Tache& tc, const Pre
         for (; m < nb_a; ++m) macro(std::false_type{}, m);
         if (tuile) {
             hors_l += (x != L) ? 1u : 0u;
-            const uint32_t attendu = (t + 1 < h.T) ? h.debut[t + 1] : h.W;
             pointeur += (v == 0 && debut + (a.o2 - o0) / 2u != attendu) ? 1u : 0u;
         }
     }
@@ -591,8 +623,9 @@ __device__ __forceinline__ uint32_t pas_r(uint32_t& x, uint32_t o2, uint32_t& co
     return e.x;
 }
 
+// `tete0`: premiere_tete(p.h), read by the caller before its barrier.
 __device__ __forceinline__ void corps_gemv_rapide(const Tache& tc, const PrepGemv& p, uint8_t* lds,
-                                                  uint32_t* __restrict__ controle) {
+                                                  uint32_t* __restrict__ controle, const TeteTuile& tete0) {
     const EnteteRans& h = p.h;
     const uint32_t R = tc.lignes, B = tc.colonnes / 32u, nblocs = R * B;
     const gptr<u32x4> ent16 = glob<u32x4>(reinterpret_cast<const void*>(tc.ech));
@@ -619,6 +652,7 @@ __device__ __forceinline__ void corps_gemv_rapide(const Tache& tc, const PrepGem
     // the stream header's counts, wave-uniform (scalar registers)
     const uint32_t hN = uniforme32(h.N), hT = uniforme32(h.T), nmacro = uniforme32(h.P / 128u);
     uint32_t hors_l = 0, pointeur = 0;
+    TeteTuile tete = tete0;
     for (uint32_t t0 = 2u * vague; t0 < hT; t0 += 2u * n_vagues) {
         const uint32_t t = t0 + (haut ? 1u : 0u);
         const bool tuile = t < hT;
@@ -627,8 +661,9 @@ __device__ __forceinline__ void corps_gemv_rapide(const Tache& tc, const PrepGem
         const uint32_t nb = haut ? nb_b : nb_a;
         const uint32_t m0 = (tuile ? t : t0) * hN;
         auto stager = [&](uint32_t m) { ecrire_lds<u32x4>(a_ent + 16u * v, ent16[2u * (m0 + m) + v]); };
-        uint32_t x = tuile ? h.etats[t * VOIES + v] : L;
-        const uint32_t debut = tuile ? h.debut[t] : 0u;
+        uint32_t x = tete.x;
+        const uint32_t debut = tete.debut, attendu = tete.attendu;
+        tete = lire_tete(h, t + 2u * n_vagues, v);
         if (tuile) stager(0);
         AnneauR a = ouvrir_anneau_r(h, p.fc, debut, a_anneau, v, tuile);
         const uint32_t o0 = a.o2;
@@ -702,7 +737,6 @@ __device__ __forceinline__ void corps_gemv_rapide(const Tache& tc, const PrepGem
         if (tuile) {
             if (v == 0 && rho < R) ecrire(s);
             hors_l += (x != L) ? 1u : 0u;
-            const uint32_t attendu = (t + 1 < hT) ? h.debut[t + 1] : h.W;
             pointeur += (v == 0 && debut + (a.o2 - o0) / 2u != attendu) ? 1u : 0u;
         }
     }
@@ -760,6 +794,52 @@ __device__ __forceinline__ float swiglu_oai_f(float g, float u) {
     const double gv = fmin(double(g), 7.0);
     const double uv = fmin(fmax(double(u), -7.0), 7.0);
     return float(gv / (1.0 + exp(-1.702 * gv)) * (uv + 1.0));
+}
+
+// x[r] = swiglu_oai(gate row r, up row r) for the rows of the calling thread (r = threadIdx.x +
+// i * blockDim.x), finished from the gate/up partial sums as somme_fin does (same order), with the
+// loads of up to 4 rows issued together. 0 for rows past either matrix, or when a job is bad.
+__device__ __forceinline__ void swiglu_vers_lds(const Fin& g, const Fin& u, uint32_t n, float* xs) {
+    const bool ok = g.bon && u.bon;
+    const uint32_t lim = min(n, min(g.lignes, u.lignes));
+    for (uint32_t r0 = threadIdx.x; r0 < n; r0 += 4u * blockDim.x) {
+        float g0[4], g1[4], gb[4], u0[4], u1[4], ub[4];
+#pragma unroll
+        for (uint32_t i = 0; i < 4; ++i) {
+            const uint32_t r = r0 + i * blockDim.x;
+            g0[i] = g1[i] = gb[i] = u0[i] = u1[i] = ub[i] = 0.0f;
+            if (ok && r < lim) {
+                // kmax >= 2 for a good job: the second slot of a row is always inside its slots
+                const float* pg = g.partiels + uint64_t(r) * g.kmax;
+                const float* pu = u.partiels + uint64_t(r) * u.kmax;
+                g0[i] = pg[0];
+                g1[i] = pg[1];
+                gb[i] = g.biais[r];
+                u0[i] = pu[0];
+                u1[i] = pu[1];
+                ub[i] = u.biais[r];
+            }
+        }
+#pragma unroll
+        for (uint32_t i = 0; i < 4; ++i) {
+            const uint32_t r = r0 + i * blockDim.x;
+            if (r >= n) continue;
+            float sg = 0.0f, su = 0.0f;
+            if (ok && r < lim) {
+                const uint32_t ng = (r * g.B + g.B - 1u) / g.bpt - (r * g.B) / g.bpt;
+                const uint32_t nu = (r * u.B + u.B - 1u) / u.bpt - (r * u.B) / u.bpt;
+                sg = g0[i];
+                if (ng >= 1u) sg += g1[i];
+                for (uint32_t k = 2; k <= ng; ++k) sg += g.partiels[uint64_t(r) * g.kmax + k];
+                su = u0[i];
+                if (nu >= 1u) su += u1[i];
+                for (uint32_t k = 2; k <= nu; ++k) su += u.partiels[uint64_t(r) * u.kmax + k];
+                xs[r] = swiglu_oai_f(sg + gb[i], su + ub[i]);
+            } else {
+                xs[r] = 0.0f;
+            }
+        }
+    }
 }
 
 }  // namespace trc

@@ -76,4 +76,55 @@ __device__ __forceinline__ void topk_vague(const float* logits, uint32_t E, uint
     for (uint32_t r = 0; r < TOPK_MAX; ++r) poids[r] = r < k ? float(e[r] / z) : 0.0f;
 }
 
+// Block-wide top-k by ranks (the selection of topk_vague without its serial rounds): the rank of
+// expert i is the number of experts ordered before it by (logit desc, index asc); the expert of
+// rank r < k is the r-th chosen. A NaN logit is never before another and is never chosen; slots
+// past the number of non-NaN logits keep 0xFFFFFFFF, as in topk_vague.
+// compter_rangs: rangs[0..E) zeroed and lg[0..E) in LDS before the call, barrier after it.
+__device__ __forceinline__ void compter_rangs(const float* lg, uint32_t E, uint32_t* rangs) {
+    const uint32_t par = blockDim.x >= E ? blockDim.x / E : 1u;  // threads per expert
+    for (uint32_t q = threadIdx.x; q < E * par; q += blockDim.x) {
+        const uint32_t i = q % E, c = q / E;
+        const uint32_t j0 = (c * E) / par, j1 = ((c + 1u) * E) / par;
+        const float vi = lg[i];
+        if (vi != vi) continue;
+        uint32_t n = 0;
+        for (uint32_t j = j0; j < j1; ++j) {
+            const float vj = lg[j];
+            n += (vj > vi || (vj == vi && j < i)) ? 1u : 0u;
+        }
+        if (n) atomicAdd(&rangs[i], n);
+    }
+}
+
+// choisis[0..TOPK_MAX) set to 0xFFFFFFFF before the call, barrier after it.
+__device__ __forceinline__ void choisir_rangs(const float* lg, const uint32_t* rangs, uint32_t E, uint32_t k,
+                                              uint32_t* choisis) {
+    for (uint32_t i = threadIdx.x; i < E; i += blockDim.x) {
+        const float vi = lg[i];
+        if (vi == vi && rangs[i] < k) choisis[rangs[i]] = i;
+    }
+}
+
+// The weights of topk_vague from the chosen experts' logits (same f64 softmax, one rounding each).
+__device__ __forceinline__ void poids_topk(const float* lg, const uint32_t* choisis, uint32_t k,
+                                           float (&poids)[TOPK_MAX]) {
+    float choisi[TOPK_MAX];
+#pragma unroll
+    for (uint32_t r = 0; r < TOPK_MAX; ++r) choisi[r] = (r < k && choisis[r] != 0xFFFFFFFFu) ? lg[choisis[r]] : -INFINITY;
+    double e[TOPK_MAX];
+    const double m = choisi[0];
+    double z = 0.0;
+#pragma unroll
+    for (uint32_t r = 0; r < TOPK_MAX; ++r) {
+        e[r] = 0.0;
+        if (r < k) {
+            e[r] = exp(double(choisi[r]) - m);
+            z += e[r];
+        }
+    }
+#pragma unroll
+    for (uint32_t r = 0; r < TOPK_MAX; ++r) poids[r] = r < k ? float(e[r] / z) : 0.0f;
+}
+
 }  // namespace trc
