@@ -105,7 +105,8 @@ fusion_echelles(trc::Taches taches, const uint32_t* __restrict__ luts, uint32_t*
 namespace trc {
 
 // residu[r] += ((w0 s0[r] + w1 s1[r]) + w2 s2[r]) + ..., s_i the finished rows of job i, each
-// product and sum rounded on its own (the reference combiner, passe.cuh:611-622).
+// product and sum rounded on its own (the reference combiner, passe.cuh:611-622); s_i is summed as
+// somme_fin does, with every job's first two partial sums and bias of the row loaded together.
 __device__ __forceinline__ void combiner_lignes(const Fin* fins, uint32_t k, const float* __restrict__ poids,
                                                 float* __restrict__ residu, uint32_t D, uint32_t r0, uint32_t pas) {
 #pragma clang fp contract(off)
@@ -113,12 +114,34 @@ __device__ __forceinline__ void combiner_lignes(const Fin* fins, uint32_t k, con
         bool ok = true;
         for (uint32_t i = 0; i < k; ++i) ok = ok && fins[i].bon && r < fins[i].lignes;
         if (!ok) continue;
-        float s = poids[0] * somme_fin(fins[0], r);
-        for (uint32_t i = 1; i < k; ++i) {
-            const float p = poids[i] * somme_fin(fins[i], r);
-            s = s + p;
+        const float res = residu[r];
+        float p0[TOPK_MAX], p1[TOPK_MAX], bi[TOPK_MAX];
+#pragma unroll
+        for (uint32_t i = 0; i < TOPK_MAX; ++i) {
+            p0[i] = p1[i] = bi[i] = 0.0f;
+            if (i < k) {
+                // kmax >= 2 for a good job: the second slot of a row is always inside its slots
+                const float* p = fins[i].partiels + uint64_t(r) * fins[i].kmax;
+                p0[i] = p[0];
+                p1[i] = p[1];
+                bi[i] = fins[i].biais[r];
+            }
         }
-        residu[r] = residu[r] + s;
+        float s = 0.0f;
+#pragma unroll
+        for (uint32_t i = 0; i < TOPK_MAX; ++i) {
+            if (i < k) {
+                const Fin& f = fins[i];
+                const uint32_t n = (r * f.B + f.B - 1u) / f.bpt - (r * f.B) / f.bpt;
+                float si = p0[i];
+                if (n >= 1u) si += p1[i];
+                for (uint32_t j = 2; j <= n; ++j) si += f.partiels[uint64_t(r) * f.kmax + j];
+                si = si + bi[i];
+                const float pr = poids[i] * si;
+                s = i == 0 ? pr : s + pr;
+            }
+        }
+        residu[r] = res + s;
     }
 }
 
