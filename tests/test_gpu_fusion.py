@@ -243,6 +243,42 @@ def test_fused_moe_router_ties_and_order(fz):
     couche.liberer()
 
 
+def test_fused_moe_router_nan_never_chosen(fz):
+    """A router row of NaN weights gives a NaN logit: the fused layer's top-k must pass over it as the
+    reference does (a NaN is never ordered before another logit), and rank the others unchanged:
+    rows 2 = 9 tied and scaled to win, row 5 NaN, row 6 scaled to win, so the fourth choice is the
+    best of the rest; indices and weights equal the oracle's routeur_topk."""
+    E, k, N = 12, 4, (16, 32)
+    couche = codeur.CoucheSynthetique(2031, 0, E, GPT, N_delta=N[0], N_codes=N[1])
+    freqs = couche.freqs()
+    luts = O.luts_couche([[freqs[j][t] for t in range(4)] for j in range(3)])
+    parts = [dev(couche.partie(e)) for e in range(E)]
+    table = dev(np.array([p.data_ptr() for p in parts], np.uint64))
+    rep, ctl0 = zeros(fusion.taille_repertoire(E)), zeros(16)
+    fz.monter_couche(vue(table), E, GPT, vue(rep), vue(ctl0))
+    base = np.stack([O.synth_normale_bf16(2031, 3, e, 2880, 0.02) for e in range(E)])
+    for t in range(2):
+        x = O.synth_normale_bf16(2031, 4, t, 2880, 1.0)
+        routeur = base.copy()
+        for a in (2, 6):
+            routeur[a] = base[a] * (4.0 if float(base[a] @ x) > 0 else -4.0)
+        routeur[9] = routeur[2]
+        routeur[5] = np.float32(np.nan)
+        r16 = (routeur.view(np.uint32) >> 16).astype(np.uint16)
+        l, rd, xd, res = dev(luts), dev(r16), dev(x), dev(np.zeros(2880, np.float32))
+        idx, w, ctl = zeros(32), zeros(32), zeros(16)
+        tr = zeros(fusion.taille_travail_couche(GPT, E, k, N[1]))
+        fz.couche_moe(vue(rep), E, vue(l), GPT, vue(rd), None, vue(xd), k, vue(res), vue(idx), vue(w), vue(ctl),
+                      vue(tr), *N)
+        logits = O.gemv_f32(routeur, x)
+        oi, ow = O.routeur_topk(logits, k)
+        assert np.isnan(logits[5]) and 5 not in list(oi) and {2, 6, 9} <= set(int(i) for i in oi)
+        assert (hote(idx, np.uint32)[:k] == oi).all(), (t, hote(idx, np.uint32)[:k], oi)
+        assert np.abs(hote(w, np.float32)[:k] - ow).max() <= 1e-6
+        assert list(hote(ctl, np.uint32)) == [0, 0, 0, 0]
+    couche.liberer()
+
+
 def test_fused_moe_layer_bad_parts(fz):
     """A layer whose parts all fail the mount checks: the step counts format errors in every pass
     that meets a bad directory entry and leaves the residual alone (nothing is combined)."""

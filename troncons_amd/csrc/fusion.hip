@@ -45,7 +45,6 @@ fusion_echelles(trc::Taches taches, const uint32_t* __restrict__ luts, uint32_t*
     __shared__ __attribute__((aligned(16))) uint8_t anneaux[(FILS_ECHELLES_FUSION / 32) * OCTETS_ANNEAU];
     __shared__ uint32_t choisis[TOPK_MAX];
     __shared__ float lg[EXPERTS_MAX];
-    __shared__ uint32_t rangs[EXPERTS_MAX];
     const bool moe = taches.mode == TACHES_MOE_DELTA;
     const bool prefill = taches.mode == TACHES_PREFILL_DELTA;
     if (prefill && reinterpret_cast<const uint32_t*>(taches.moe.compte)[blockIdx.y / 3u] == 0u) return;
@@ -58,15 +57,10 @@ fusion_echelles(trc::Taches taches, const uint32_t* __restrict__ luts, uint32_t*
         // computes the weights and publishes the selection for the later passes
         const ParamsMoe& pm = taches.moe;
         const float* logits = reinterpret_cast<const float*>(pm.logits);
-        for (uint32_t e = threadIdx.x; e < pm.E; e += blockDim.x) {
-            lg[e] = logits[e];
-            rangs[e] = 0u;
-        }
+        for (uint32_t e = threadIdx.x; e < pm.E; e += blockDim.x) lg[e] = logits[e];
         if (threadIdx.x < TOPK_MAX) choisis[threadIdx.x] = 0xFFFFFFFFu;
         __syncthreads();
-        compter_rangs(lg, pm.E, rangs);
-        __syncthreads();
-        choisir_rangs(lg, rangs, pm.E, pm.k, choisis);
+        choisir_topk(lg, pm.E, pm.k, choisis);
         __syncthreads();
         if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x < 64u) {
             float w[TOPK_MAX];

@@ -80,29 +80,29 @@ __device__ __forceinline__ void topk_vague(const float* logits, uint32_t E, uint
 // expert i is the number of experts ordered before it by (logit desc, index asc); the expert of
 // rank r < k is the r-th chosen. A NaN logit is never before another and is never chosen; slots
 // past the number of non-NaN logits keep 0xFFFFFFFF, as in topk_vague.
-// compter_rangs: rangs[0..E) zeroed and lg[0..E) in LDS before the call, barrier after it.
-__device__ __forceinline__ void compter_rangs(const float* lg, uint32_t E, uint32_t* rangs) {
-    const uint32_t par = blockDim.x >= E ? blockDim.x / E : 1u;  // threads per expert
-    for (uint32_t q = threadIdx.x; q < E * par; q += blockDim.x) {
-        const uint32_t i = q % E, c = q / E;
-        const uint32_t j0 = (c * E) / par, j1 = ((c + 1u) * E) / par;
+// Each expert gets a group of `par` consecutive lanes (par a power of two, at most 64, par * E at
+// most the block when it can be): lane c of the group counts over its share of the experts, the
+// group adds its counts with lane exchanges, and its first lane writes the choice. No division,
+// no LDS atomics. lg[0..E) in LDS and choisis[0..TOPK_MAX) set to 0xFFFFFFFF before the call,
+// barrier after it.
+__device__ __forceinline__ void choisir_topk(const float* lg, uint32_t E, uint32_t k, uint32_t* choisis) {
+    uint32_t lpar = 0;
+    while (lpar < 6u && (E << (lpar + 1u)) <= blockDim.x) ++lpar;
+    const uint32_t par = 1u << lpar;
+    const uint32_t part = (E + par - 1u) >> lpar;  // experts counted per lane
+    // every lane of a group takes the same trips: the exchanges below see only active lanes
+    for (uint32_t q0 = threadIdx.x & ~(par - 1u); q0 < (E << lpar); q0 += blockDim.x) {
+        const uint32_t q = q0 + (threadIdx.x & (par - 1u));
+        const uint32_t i = q >> lpar, c = q & (par - 1u);
         const float vi = lg[i];
-        if (vi != vi) continue;
+        const uint32_t j0 = c * part, j1 = min(E, j0 + part);
         uint32_t n = 0;
         for (uint32_t j = j0; j < j1; ++j) {
             const float vj = lg[j];
             n += (vj > vi || (vj == vi && j < i)) ? 1u : 0u;
         }
-        if (n) atomicAdd(&rangs[i], n);
-    }
-}
-
-// choisis[0..TOPK_MAX) set to 0xFFFFFFFF before the call, barrier after it.
-__device__ __forceinline__ void choisir_rangs(const float* lg, const uint32_t* rangs, uint32_t E, uint32_t k,
-                                              uint32_t* choisis) {
-    for (uint32_t i = threadIdx.x; i < E; i += blockDim.x) {
-        const float vi = lg[i];
-        if (vi == vi && rangs[i] < k) choisis[rangs[i]] = i;
+        for (uint32_t d = 1; d < par; d <<= 1) n += uint32_t(__shfl_xor(int(n), int(d)));
+        if (c == 0u && vi == vi && n < k) choisis[n] = i;
     }
 }
 
