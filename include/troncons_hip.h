@@ -97,6 +97,24 @@ int trc_lut_geometrie1(const uint16_t* freq, size_t n, uint32_t* lut /* [4096] *
  * luts receives u32[3][4][4096] */
 int trc_luts_couche(const uint16_t* const* freqs, uint32_t* luts);
 
+/* ParamsRope (moteur/crates/trc-noyaux/src/abi.rs:229-251): YaRN parameters, 48 bytes; gpt-oss:
+ * {150000, 32, 4096, 32, 1, 64, 0}. variante 0: OpenAI ramp bounds (the model); 1: llama.cpp's. */
+typedef struct {
+    double base, facteur, ctx_origine, beta_rapide, beta_lent;
+    uint32_t dim_tete, variante;
+} trc_params_rope;
+
+/* ParamsAttention (abi.rs:253-291): one decode position's attention, 32 bytes. Positions
+ * [debut, fin) are read; position pos lives in cache slot pos, or pos mod anneau when anneau > 0
+ * (sliding-window layers). dim_tete must be 64; echelle = 1/sqrt(64). */
+typedef struct {
+    uint32_t tetes, tetes_kv, dim_tete, debut, fin, anneau;
+    float echelle;
+    uint32_t reserve;
+} trc_params_attention;
+
+#define TRC_ATTENTION_POSITIONS_MAX 8192 /* abi.rs:296-298 */
+
 /* ---------------------------------------- launches: the reference kernel API (Noyaux methods) */
 
 /* Noyaux::decoder_expert (moteur/crates/trc-noyaux/src/lib.rs:118-135): decodes a level-0 part
@@ -172,6 +190,32 @@ uint64_t trc_taille_repertoire(uint32_t experts);
  * they are while the directory is used. */
 int trc_monter_couche(trc_vue parties, uint32_t experts, const trc_dims_expert* dims, trc_vue repertoire,
                       trc_vue controle, void* flux);
+
+/* ------------------------------- launches: the rest of the layer step (Noyaux, passe.cuh) */
+
+/* Noyaux::gemv_q8_0 (lib.rs:291-302): y = W x (+ biais), W Q8_0 (rows of colonnes/32 blocks of 34
+ * bytes: f16 d, 32 x i8), in the reference's operation order (lane l of 32 takes blocks l, l + 32,
+ * ...; butterfly). w 2-byte aligned, x 16-byte aligned; biais may be absent (adresse 0). */
+int trc_gemv_q8_0(trc_vue w, trc_vue x, trc_vue biais, trc_vue y, uint32_t lignes, uint32_t colonnes, void* flux);
+/* Noyaux::ligne_q8_0 (lib.rs:478-486): row `ligne` of a Q8_0 matrix (the embedding) -> f32, exact. */
+int trc_ligne_q8_0(trc_vue w, uint32_t ligne, uint32_t colonnes, trc_vue y, void* flux);
+/* Noyaux::rmsnorm (lib.rs:322-330): `lignes` rows of n, y = x * r * w with r = 1/sqrt(mean(x^2) +
+ * eps), sums and products in f64 (fixed tree), rounded once; y may equal x. */
+int trc_rmsnorm(trc_vue x, trc_vue w, trc_vue y, uint32_t n, uint32_t lignes, float eps, void* flux);
+/* Noyaux::rope_yarn (lib.rs:334-343): NEOX YaRN rotation of tetes_q heads of q and tetes_k heads
+ * of k, in place, at `position`, in f64. */
+int trc_rope_yarn(trc_vue q, trc_vue k, uint32_t tetes_q, uint32_t tetes_k, uint32_t position,
+                  const trc_params_rope* p, void* flux);
+/* Noyaux::ecrire_kv (lib.rs:348-357): k, v (f32[dkv]) rounded to f16 (nearest even) into slot
+ * case_kv of the layer's caches ([slot][kv head][64]). */
+int trc_ecrire_kv(trc_vue k, trc_vue v, trc_vue cache_k, trc_vue cache_v, uint32_t dkv, uint32_t case_kv, void* flux);
+/* Noyaux::attention (lib.rs:362-379): decode attention of one position, every query head, with
+ * the per-head sinks in the softmax denominator; puits f32[tetes], sortie f32[tetes * 64]. */
+int trc_attention(trc_vue q, trc_vue cache_k, trc_vue cache_v, trc_vue puits, trc_vue sortie,
+                  const trc_params_attention* p, void* flux);
+/* Noyaux::argmax (lib.rs:490-496): index of the largest of n floats (ties: lower index; NaN never
+ * chosen; all NaN: 0xFFFFFFFF) into sortie (u32). */
+int trc_argmax(trc_vue v, uint32_t n, trc_vue sortie, void* flux);
 
 /* Workspace bytes of trc_couche_moe_fusionnee. */
 uint64_t trc_taille_travail_couche_moe(const trc_dims_expert* dims, uint32_t experts, uint32_t k, uint32_t n_codes);

@@ -190,6 +190,54 @@ void orc_combiner(float* residu, const float* sorties, uint32_t pas, const float
  * the k in f64 (m = first), rounded to f32. */
 void orc_routeur_topk(const float* logits, uint32_t E, uint32_t k, uint32_t* indices, float* poids);
 
+/* ------------------------------------------------------------- forward pass around the experts */
+/* (passe.c) The rest of a gpt-oss layer step, in each reference kernel's operation order. */
+
+/* ParamsRope (trc-noyaux/src/abi.rs:229-251, passe.cuh:134-143): 48 bytes. */
+typedef struct {
+    double base, facteur, ctx_origine, beta_rapide, beta_lent;
+    uint32_t dim_tete, variante;
+} orc_params_rope;
+/* ParamsAttention (abi.rs:253-291, passe.cuh:171-181): 32 bytes. */
+typedef struct {
+    uint32_t tetes, tetes_kv, dim_tete, debut, fin, anneau;
+    float echelle;
+    uint32_t reserve;
+} orc_params_attention;
+
+/* f16 <-> f32: f32 -> f16 rounds to nearest even (overflow to inf, subnormals kept).
+ * KAT: the eight values of tests/passe.rs:146-159; MATH: numpy's float16 on every f16 and on
+ * random f32 (tests/test_oracle_passe.py). */
+float orc_f32_depuis_f16(uint16_t h);
+uint16_t orc_f16_depuis_f32(float f);
+/* gemv_q8_0 (passe.cuh:52-97): KAT integer-exact fixture of tests/passe.rs:83-118 (equal to the
+ * f64 sum, bias included); MATH: f64 within 1e-6 on random data. The lane order itself is the
+ * reference text's (no reference output pins it): the GPU kernel, written apart, must equal it
+ * bit for bit. */
+void orc_gemv_q8_0(const uint8_t* W, const float* x, const float* biais, float* y, uint32_t R, uint32_t C);
+/* ligne_q8_0 (passe.cuh:627-637): KAT tests/passe.rs:127-145 (d = 2^e, exact). */
+void orc_ligne_q8_0(const uint8_t* W, uint32_t ligne, uint32_t C, float* y);
+/* rmsnorm (passe.cuh:235-259): MATH: the f64 closed form of ops.rs:8-18 within 1e-6
+ * (tests/passe.rs:163-176). */
+void orc_rmsnorm(const float* x, const float* w, float* y, uint32_t n, uint32_t lignes, float eps);
+/* YaRN inv_freq (passe.cuh:145-167): KAT ramp bounds 8.0928 / 17.3981 and 8 / 18 (llama.cpp
+ * variant), concentration 0.1 ln 32 + 1, variants equal outside the ramp (ops.rs:146-163). */
+double orc_inv_freq_yarn(const orc_params_rope* p, uint32_t i, double* concentration, double* bas, double* haut);
+/* rope_yarn (passe.cuh:261-284): KAT position 0 = times the concentration, factor 1 at position
+ * 1000 = plain RoPE (tests/passe.rs:177-200); MATH: norm times concentration^2 (ops.rs:165-173). */
+void orc_rope_yarn(float* q, float* k, uint32_t tetes_q, uint32_t tetes_k, uint32_t position,
+                   const orc_params_rope* p);
+/* ecrire_kv (passe.cuh:286-296): via orc_f16_depuis_f32; slot placement checked by the KAT. */
+void orc_ecrire_kv(const float* k, const float* v, uint16_t* cache_k, uint16_t* cache_v, uint32_t dkv,
+                   uint32_t case_kv);
+/* attention (passe.cuh:298-373): KAT sink in the denominator (ops.rs:175-186), ring of 128 at
+ * position 200 (mean 63.5) and 4096 positions (mean 1023.5) of tests/passe.rs:217-272; MATH: the
+ * f64 definition of ops.rs:87-118 within 1e-5 on random heads. */
+void orc_attention(const float* q, const uint16_t* cache_k, const uint16_t* cache_v, const float* puits,
+                   float* sortie, const orc_params_attention* p);
+/* argmax (passe.cuh:639-666): KAT tests/passe.rs:296-302 (tie -> lower index, NaN never). */
+uint32_t orc_argmax(const float* v, uint32_t n);
+
 /* ------------------------------------------------------------------------------ generators */
 
 /* splitmix64 as in moteur/crates/trc-noyaux/tests/carte.rs:22-31 (state advanced first). */

@@ -69,6 +69,33 @@ class Partie(C.Structure):
                 ("n_flux", C.c_uint32), ("utiles", C.c_uint32), ("flux", DescFlux * 64)]
 
 
+class ParamsRope(C.Structure):
+    """ParamsRope (trc-noyaux/src/abi.rs:229-251): 48 bytes."""
+    _fields_ = [("base", C.c_double), ("facteur", C.c_double), ("ctx_origine", C.c_double),
+                ("beta_rapide", C.c_double), ("beta_lent", C.c_double), ("dim_tete", C.c_uint32),
+                ("variante", C.c_uint32)]
+
+
+def rope_gpt_oss(**k) -> ParamsRope:
+    """ParamsRope::GPT_OSS (abi.rs:249-250), fields overridable."""
+    v = dict(base=150000.0, facteur=32.0, ctx_origine=4096.0, beta_rapide=32.0, beta_lent=1.0, dim_tete=64, variante=0)
+    v.update(k)
+    return ParamsRope(**v)
+
+
+class ParamsAttention(C.Structure):
+    """ParamsAttention (abi.rs:253-291): 32 bytes."""
+    _fields_ = [("tetes", C.c_uint32), ("tetes_kv", C.c_uint32), ("dim_tete", C.c_uint32), ("debut", C.c_uint32),
+                ("fin", C.c_uint32), ("anneau", C.c_uint32), ("echelle", C.c_float), ("reserve", C.c_uint32)]
+
+
+def attention_gpt_oss(position: int, fenetre: int, tetes: int = 64, tetes_kv: int = 8) -> ParamsAttention:
+    """ParamsAttention::gpt_oss (abi.rs:278-284)."""
+    fin = position + 1
+    debut = max(fin - fenetre, 0) if fenetre > 0 else 0
+    return ParamsAttention(tetes, tetes_kv, 64, debut, fin, fenetre, 0.125, 0)
+
+
 class Disposition(C.Structure):
     _fields_ = [("base", C.c_uint64), ("echelles", C.c_uint64), ("biais", C.c_uint64), ("pas", C.c_uint64)]
 
@@ -115,6 +142,20 @@ def _declarer(l: C.CDLL) -> None:
     l.orc_swiglu_oai.argtypes = [f32p, f32p, f32p, C.c_uint32]
     l.orc_combiner.argtypes = [f32p, f32p, C.c_uint32, f32p, C.c_uint32, C.c_uint32]
     l.orc_routeur_topk.argtypes = [f32p, C.c_uint32, C.c_uint32, u32p, f32p]
+    l.orc_f32_depuis_f16.argtypes = [C.c_uint16]
+    l.orc_f32_depuis_f16.restype = C.c_float
+    l.orc_f16_depuis_f32.argtypes = [C.c_float]
+    l.orc_f16_depuis_f32.restype = C.c_uint16
+    l.orc_gemv_q8_0.argtypes = [u8p, f32p, f32p, f32p, C.c_uint32, C.c_uint32]
+    l.orc_ligne_q8_0.argtypes = [u8p, C.c_uint32, C.c_uint32, f32p]
+    l.orc_rmsnorm.argtypes = [f32p, f32p, f32p, C.c_uint32, C.c_uint32, C.c_float]
+    l.orc_inv_freq_yarn.argtypes = [C.POINTER(ParamsRope), C.c_uint32, f64p, f64p, f64p]
+    l.orc_inv_freq_yarn.restype = C.c_double
+    l.orc_rope_yarn.argtypes = [f32p, f32p, C.c_uint32, C.c_uint32, C.c_uint32, C.POINTER(ParamsRope)]
+    l.orc_ecrire_kv.argtypes = [f32p, f32p, u16p, u16p, C.c_uint32, C.c_uint32]
+    l.orc_attention.argtypes = [f32p, u16p, u16p, f32p, f32p, C.POINTER(ParamsAttention)]
+    l.orc_argmax.argtypes = [f32p, C.c_uint32]
+    l.orc_argmax.restype = C.c_uint32
     l.orc_splitmix64.argtypes = [u64p]
     l.orc_splitmix64.restype = C.c_uint64
     l.orc_xorshift64s.argtypes = [u64p]
@@ -424,3 +465,76 @@ def blocs_vers_soa(blocs17: np.ndarray, R: int, C_: int, biais: np.ndarray, cano
     out[d.echelles:d.echelles + nb] = b[:, 0]
     out[d.biais:d.biais + 4 * R] = np.asarray(biais, dtype=np.float32).view(np.uint8)
     return out
+
+
+# ---------------------------------------------------------------- forward pass around the experts
+
+def f16_depuis_f32(v) -> np.ndarray:
+    a = np.ascontiguousarray(v, dtype=np.float32).ravel()
+    return np.array([lib().orc_f16_depuis_f32(float(x)) for x in a], dtype=np.uint16)
+
+
+def f32_depuis_f16(h) -> np.ndarray:
+    a = np.ascontiguousarray(h, dtype=np.uint16).ravel()
+    return np.array([lib().orc_f32_depuis_f16(int(x)) for x in a], dtype=np.float32)
+
+
+def gemv_q8_0(W: np.ndarray, x: np.ndarray, biais, R: int, C_: int) -> np.ndarray:
+    w = np.ascontiguousarray(W, dtype=np.uint8)
+    xx = np.ascontiguousarray(x, dtype=np.float32)
+    b = np.ascontiguousarray(biais, dtype=np.float32) if biais is not None else None
+    y = np.zeros(R, dtype=np.float32)
+    lib().orc_gemv_q8_0(_p(w, u8p), _p(xx, f32p), _p(b, f32p) if b is not None else f32p(), _p(y, f32p), R, C_)
+    return y
+
+
+def ligne_q8_0(W: np.ndarray, ligne: int, C_: int) -> np.ndarray:
+    w = np.ascontiguousarray(W, dtype=np.uint8)
+    y = np.zeros(C_, dtype=np.float32)
+    lib().orc_ligne_q8_0(_p(w, u8p), ligne, C_, _p(y, f32p))
+    return y
+
+
+def rmsnorm(x: np.ndarray, w: np.ndarray, n: int, lignes: int, eps: float) -> np.ndarray:
+    xx = np.ascontiguousarray(x, dtype=np.float32)
+    ww = np.ascontiguousarray(w, dtype=np.float32)
+    y = np.zeros(n * lignes, dtype=np.float32)
+    lib().orc_rmsnorm(_p(xx, f32p), _p(ww, f32p), _p(y, f32p), n, lignes, eps)
+    return y
+
+
+def inv_freq_yarn(p: ParamsRope, i: int):
+    m, b, h = C.c_double(), C.c_double(), C.c_double()
+    f = lib().orc_inv_freq_yarn(C.byref(p), i, C.byref(m), C.byref(b), C.byref(h))
+    return f, m.value, b.value, h.value
+
+
+def rope_yarn(q: np.ndarray, k: np.ndarray, tetes_q: int, tetes_k: int, position: int, p: ParamsRope):
+    qq = np.array(q, dtype=np.float32)
+    kk = np.array(k, dtype=np.float32)
+    lib().orc_rope_yarn(_p(qq, f32p), _p(kk, f32p), tetes_q, tetes_k, position, C.byref(p))
+    return qq, kk
+
+
+def ecrire_kv(k, v, cache_k, cache_v, dkv: int, case_kv: int):
+    kk = np.ascontiguousarray(k, dtype=np.float32)
+    vv = np.ascontiguousarray(v, dtype=np.float32)
+    ck = np.array(cache_k, dtype=np.uint16)
+    cv = np.array(cache_v, dtype=np.uint16)
+    lib().orc_ecrire_kv(_p(kk, f32p), _p(vv, f32p), _p(ck, u16p), _p(cv, u16p), dkv, case_kv)
+    return ck, cv
+
+
+def attention(q, cache_k, cache_v, puits, p: ParamsAttention) -> np.ndarray:
+    qq = np.ascontiguousarray(q, dtype=np.float32)
+    ck = np.ascontiguousarray(cache_k, dtype=np.uint16)
+    cv = np.ascontiguousarray(cache_v, dtype=np.uint16)
+    pu = np.ascontiguousarray(puits, dtype=np.float32)
+    s = np.zeros(64 * p.tetes, dtype=np.float32)
+    lib().orc_attention(_p(qq, f32p), _p(ck, u16p), _p(cv, u16p), _p(pu, f32p), _p(s, f32p), C.byref(p))
+    return s
+
+
+def argmax(v) -> int:
+    vv = np.ascontiguousarray(v, dtype=np.float32)
+    return int(lib().orc_argmax(_p(vv, f32p), vv.size))

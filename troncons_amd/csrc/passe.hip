@@ -1,0 +1,403 @@
+// passe.hip — the rest of a gpt-oss layer step around the expert path, for gfx950: the Q8_0 GEMV
+// (attention projections, output head) and row (embedding), RMSNorm, the YaRN rotation, the f16
+// KV-cache write, decode attention with per-head sinks, argmax. Same names, arguments and results
+// as the reference's kernels (moteur/crates/trc-noyaux/noyaux/passe.cuh), each in the reference's
+// operation order so that results are bit-identical where the reference is exact: the Q8_0 GEMV
+// runs two reference "warps" per wavefront (one per 32-lane half, four rows each) with the lane
+// order and butterfly of the reference; the single-vector operations keep their f64 arithmetic and
+// their fixed reduction trees.
+//
+// Determinism: no atomics; every reduction follows a tree that depends on sizes only.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+
+#include "commun.hpp"
+#include "erreurs.hpp"
+
+namespace trc {
+
+constexpr uint32_t Q8_OCTETS_BLOC = 34;  // f16 d, then 32 x i8 (ggml Q8_0)
+constexpr uint32_t FILS_PASSE = 256;
+constexpr uint32_t FILS_ARGMAX = 1024;
+constexpr uint32_t ATTENTION_DIM = 64;
+constexpr uint32_t ATTENTION_POSITIONS_MAX = TRC_ATTENTION_POSITIONS_MAX;
+
+__device__ __forceinline__ float f16_vers_f32(uint32_t bits) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits)));
+}
+__device__ __forceinline__ uint16_t f32_vers_f16(float f) {  // round to nearest even
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+}
+
+// Best of two (value, index): larger value, then lower index; a NaN is never better.
+__device__ __forceinline__ bool meilleur(float va, uint32_t ia, float vb, uint32_t ib) {
+    return va > vb || (va == vb && ia < ib);
+}
+
+// Fixed tree over FILS_PASSE values in LDS (max or sum); every thread gets the result.
+template <bool MAX>
+__device__ __forceinline__ float reduire_bloc(float* part, float v) {
+    const uint32_t t = threadIdx.x;
+    part[t] = v;
+    __syncthreads();
+#pragma unroll
+    for (uint32_t k = FILS_PASSE / 2u; k > 0; k >>= 1) {
+        if (t < k) part[t] = MAX ? fmaxf(part[t], part[t + k]) : part[t] + part[t + k];
+        __syncthreads();
+    }
+    const float r = part[0];
+    __syncthreads();
+    return r;
+}
+
+// YaRN inv_freq of pair i and the concentration, in f64 (passe.cuh:145-167).
+__device__ inline double inv_freq_yarn(const trc_params_rope& p, uint32_t i, double& concentration) {
+    const uint32_t demi = p.dim_tete / 2u;
+    const double freq = pow(p.base, double(2u * i) / double(p.dim_tete));
+    if (p.facteur <= 1.0) {
+        concentration = 1.0;
+        return 1.0 / freq;
+    }
+    concentration = 0.1 * log(p.facteur) + 1.0;
+    const double deux_pi = 6.283185307179586476925286766559;
+    double bas = double(demi) * log(p.ctx_origine / (p.beta_rapide * deux_pi)) / log(p.base);
+    double haut = double(demi) * log(p.ctx_origine / (p.beta_lent * deux_pi)) / log(p.base);
+    if (p.variante == 1u) {
+        bas = fmax(floor(bas), 0.0);
+        haut = fmin(ceil(haut), double(p.dim_tete - 1u));
+    }
+    const double interpolation = 1.0 / (p.facteur * freq);
+    const double extrapolation = 1.0 / freq;
+    const double rampe = fmin(fmax((double(i) - bas) / (haut - bas), 0.0), 1.0);
+    const double masque = 1.0 - rampe;
+    return interpolation * (1.0 - masque) + extrapolation * masque;
+}
+
+}  // namespace trc
+
+// y = W x (+ b), W Q8_0; half-wavefront w of the block takes rows 4w .. 4w + 3 of its 32; lane l
+// of the half takes blocks b = l, l + 32, ...; in a block s = sum of q_i x_i (one fmaf chain, low
+// byte then high byte of each 16-bit word), then acc = fmaf(d, s, acc); butterfly over the half
+// (passe.cuh:52-97, 213-222). Block addresses are even (34 b): 16-bit loads.
+extern "C" __global__ void __launch_bounds__(trc::FILS_PASSE)
+gemv_q8_0(const uint8_t* __restrict__ W, const float* __restrict__ x, const float* __restrict__ biais,
+          float* __restrict__ y, uint32_t R, uint32_t C) {
+    using namespace trc;
+    const uint32_t voie = threadIdx.x & 31u;
+    const uint32_t r0 = (blockIdx.x * (FILS_PASSE / 32u) + (threadIdx.x >> 5)) * 4u;
+    if (r0 >= R) return;
+    const uint32_t B = C / 32u;
+    const uint64_t octets_ligne = uint64_t(B) * Q8_OCTETS_BLOC;
+    const f32x4* x4 = reinterpret_cast<const f32x4*>(x);
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    uint32_t lig[4];
+#pragma unroll
+    for (uint32_t i = 0; i < 4; ++i) lig[i] = min(r0 + i, R - 1u);
+    for (uint32_t b = voie; b < B; b += 32u) {
+        float xv[32];
+#pragma unroll
+        for (uint32_t k = 0; k < 8; ++k) {
+            const f32x4 t = x4[b * 8u + k];
+            xv[4 * k] = t.x;
+            xv[4 * k + 1] = t.y;
+            xv[4 * k + 2] = t.z;
+            xv[4 * k + 3] = t.w;
+        }
+#pragma unroll
+        for (uint32_t i = 0; i < 4; ++i) {
+            const uint16_t* blk =
+                reinterpret_cast<const uint16_t*>(W + uint64_t(lig[i]) * octets_ligne + uint64_t(b) * Q8_OCTETS_BLOC);
+            uint32_t mots[17];
+#pragma unroll
+            for (uint32_t t = 0; t < 17; ++t) mots[t] = blk[t];
+            const float d = f16_vers_f32(mots[0]);
+            float s = 0.0f;
+#pragma unroll
+            for (uint32_t t = 0; t < 16; ++t) {
+                s = fmaf(float(int8_t(mots[1 + t] & 0xFFu)), xv[2 * t], s);
+                s = fmaf(float(int8_t(mots[1 + t] >> 8)), xv[2 * t + 1], s);
+            }
+            acc[i] = fmaf(d, s, acc[i]);
+        }
+    }
+#pragma unroll
+    for (uint32_t i = 0; i < 4; ++i) {
+        const float s = somme_demi_f32(acc[i]);
+        if (voie == 0 && r0 + i < R) y[r0 + i] = biais != nullptr ? s + biais[r0 + i] : s;
+    }
+}
+
+// Row `ligne` of a Q8_0 matrix -> f32, exact (d has 11 significant bits, q 7: passe.cuh:627-637).
+extern "C" __global__ void __launch_bounds__(trc::FILS_PASSE)
+ligne_q8_0(const uint8_t* __restrict__ W, uint32_t ligne, uint32_t C, float* __restrict__ y) {
+    using namespace trc;
+    const uint32_t i = blockIdx.x * FILS_PASSE + threadIdx.x;
+    if (i >= C) return;
+    const uint8_t* b = W + uint64_t(ligne) * (C / 32u) * Q8_OCTETS_BLOC + uint64_t(i / 32u) * Q8_OCTETS_BLOC;
+    const float d = f16_vers_f32(uint32_t(b[0]) | (uint32_t(b[1]) << 8));
+    y[i] = d * float(int8_t(b[2 + (i & 31u)]));
+}
+
+// RMSNorm of one row per block: thread t adds x_i^2 for i = t, t + 256, ... (f64 fma), fixed tree,
+// r = 1/sqrt(sum/n + eps), y_i = (x_i r) w_i in f64, rounded once (passe.cuh:235-259). x is read
+// in full before the first write (y may be x).
+extern "C" __global__ void __launch_bounds__(trc::FILS_PASSE)
+rmsnorm(const float* __restrict__ x, const float* __restrict__ w, float* y, uint32_t n, float eps) {
+    __shared__ double part[trc::FILS_PASSE];
+    const uint32_t t = threadIdx.x;
+    const float* xr = x + uint64_t(blockIdx.x) * n;
+    float* yr = y + uint64_t(blockIdx.x) * n;
+    double s = 0.0;
+    for (uint32_t i = t; i < n; i += trc::FILS_PASSE) {
+        const double v = xr[i];
+        s = fma(v, v, s);
+    }
+    part[t] = s;
+    __syncthreads();
+#pragma unroll
+    for (uint32_t k = trc::FILS_PASSE / 2u; k > 0; k >>= 1) {
+        if (t < k) part[t] += part[t + k];
+        __syncthreads();
+    }
+    const double r = 1.0 / sqrt(part[0] / double(n) + double(eps));
+    for (uint32_t i = t; i < n; i += trc::FILS_PASSE) yr[i] = float(double(xr[i]) * r * double(w[i]));
+}
+
+// YaRN rotation (NEOX halves) of one head per block, in place: pair i < d/2 of the head,
+// o1 = x1 c - x2 s, o2 = x2 c + x1 s, c and s the cosine and sine of position * inv_freq_i times the
+// concentration, all in f64 (passe.cuh:261-284). Heads 0 .. tetes_q - 1 are q's, then k's.
+extern "C" __global__ void __launch_bounds__(64)
+rope_yarn(float* __restrict__ q, float* __restrict__ k, uint32_t tetes_q, uint32_t tetes_k, uint32_t position,
+          trc_params_rope p) {
+    using namespace trc;
+    const uint32_t demi = p.dim_tete / 2u;
+    const uint32_t i = threadIdx.x;
+    if (i >= demi || blockIdx.x >= tetes_q + tetes_k) return;
+    double m;
+    const double inv = inv_freq_yarn(p, i, m);
+    double s, c;
+    sincos(double(position) * inv, &s, &c);
+    c *= m;
+    s *= m;
+    float* xh = blockIdx.x < tetes_q ? q + uint64_t(blockIdx.x) * p.dim_tete
+                                     : k + uint64_t(blockIdx.x - tetes_q) * p.dim_tete;
+    const double a = xh[i], b = xh[i + demi];
+    xh[i] = float(a * c - b * s);
+    xh[i + demi] = float(b * c + a * s);
+}
+
+// k and v rounded to f16 (nearest even) into slot case_kv of the caches (passe.cuh:286-296).
+extern "C" __global__ void __launch_bounds__(trc::FILS_PASSE)
+ecrire_kv(const float* __restrict__ k, const float* __restrict__ v, uint16_t* __restrict__ cache_k,
+          uint16_t* __restrict__ cache_v, uint32_t dkv, uint32_t case_kv) {
+    const uint32_t i = blockIdx.x * trc::FILS_PASSE + threadIdx.x;
+    if (i >= dkv) return;
+    const uint64_t o = uint64_t(case_kv) * dkv + i;
+    cache_k[o] = trc::f32_vers_f16(k[i]);
+    cache_v[o] = trc::f32_vers_f16(v[i]);
+}
+
+// Decode attention of one position, one query head per block of 256 threads (passe.cuh:298-373):
+//   score_j = (q . k_j) * scale (fmaf chain over d = 0..63), j in [debut, fin);
+//   m = max(max_j score_j, sink); e_j = expf(score_j - m); z = tree over the threads' sums + expf(sink - m);
+//   out[t] = ((G0 + G1) + (G2 + G3)) / z, G_g the fmaf chain over j = g, g + 4, ... of e_j v_j[t].
+// Query head h reads kv head h / (heads / kv heads); scores live in dynamic LDS (4 bytes each).
+extern "C" __global__ void __launch_bounds__(trc::FILS_PASSE)
+attention(const float* __restrict__ q, const uint16_t* __restrict__ cache_k, const uint16_t* __restrict__ cache_v,
+          const float* __restrict__ puits, float* __restrict__ sortie, trc_params_attention p) {
+    using namespace trc;
+    extern __shared__ float scores[];
+    __shared__ float qs[ATTENTION_DIM];
+    __shared__ float part[FILS_PASSE];
+    __shared__ float groupes[4][ATTENTION_DIM];
+    const uint32_t t = threadIdx.x;
+    const uint32_t h = blockIdx.x;
+    const uint32_t hk = h / (p.tetes / p.tetes_kv);
+    const uint32_t dkv = p.tetes_kv * ATTENTION_DIM;
+    const uint32_t n = p.fin - p.debut;
+    if (t < ATTENTION_DIM) qs[t] = q[uint64_t(h) * ATTENTION_DIM + t];
+    __syncthreads();
+
+    for (uint32_t j = t; j < n; j += FILS_PASSE) {
+        const uint32_t pos = p.debut + j;
+        const uint32_t c = p.anneau ? pos % p.anneau : pos;
+        const u32x4* kr = reinterpret_cast<const u32x4*>(cache_k + uint64_t(c) * dkv + uint64_t(hk) * ATTENTION_DIM);
+        float s = 0.0f;
+#pragma unroll
+        for (uint32_t b = 0; b < 8; ++b) {
+            const u32x4 w = kr[b];
+#pragma unroll
+            for (uint32_t u = 0; u < 4; ++u) {
+                s = fmaf(qs[8 * b + 2 * u], f16_vers_f32(w[u] & 0xFFFFu), s);
+                s = fmaf(qs[8 * b + 2 * u + 1], f16_vers_f32(w[u] >> 16), s);
+            }
+        }
+        scores[j] = s * p.echelle;
+    }
+    __syncthreads();
+
+    float m = -INFINITY;
+    for (uint32_t j = t; j < n; j += FILS_PASSE) m = fmaxf(m, scores[j]);
+    const float puits_h = puits[h];
+    m = fmaxf(reduire_bloc<true>(part, m), puits_h);
+    float z = 0.0f;
+    for (uint32_t j = t; j < n; j += FILS_PASSE) {
+        const float e = expf(scores[j] - m);
+        scores[j] = e;
+        z += e;
+    }
+    z = reduire_bloc<false>(part, z) + expf(puits_h - m);
+
+    const uint32_t dd = t & (ATTENTION_DIM - 1u);
+    const uint32_t g = t / ATTENTION_DIM;  // 0..3
+    float a = 0.0f;
+    for (uint32_t j = g; j < n; j += 4u) {
+        const uint32_t pos = p.debut + j;
+        const uint32_t c = p.anneau ? pos % p.anneau : pos;
+        a = fmaf(scores[j], f16_vers_f32(cache_v[uint64_t(c) * dkv + uint64_t(hk) * ATTENTION_DIM + dd]), a);
+    }
+    groupes[g][dd] = a;
+    __syncthreads();
+    if (t < ATTENTION_DIM)
+        sortie[uint64_t(h) * ATTENTION_DIM + t] = ((groupes[0][t] + groupes[1][t]) + (groupes[2][t] + groupes[3][t])) / z;
+}
+
+// Index of the largest of n floats: thread t scans i = t, t + 1024, ..., then a fixed tree; ties go
+// to the lower index, NaN is never chosen (passe.cuh:639-666).
+extern "C" __global__ void __launch_bounds__(trc::FILS_ARGMAX)
+argmax(const float* __restrict__ v, uint32_t n, uint32_t* __restrict__ sortie) {
+    using namespace trc;
+    __shared__ float pv[FILS_ARGMAX];
+    __shared__ uint32_t pi[FILS_ARGMAX];
+    const uint32_t t = threadIdx.x;
+    float bv = -INFINITY;
+    uint32_t bi = 0xFFFFFFFFu;
+    for (uint32_t i = t; i < n; i += FILS_ARGMAX) {
+        const float xv = v[i];
+        if (meilleur(xv, i, bv, bi)) {
+            bv = xv;
+            bi = i;
+        }
+    }
+    pv[t] = bv;
+    pi[t] = bi;
+    __syncthreads();
+    for (uint32_t k = FILS_ARGMAX / 2u; k > 0; k >>= 1) {
+        if (t < k && meilleur(pv[t + k], pi[t + k], pv[t], pi[t])) {
+            pv[t] = pv[t + k];
+            pi[t] = pi[t + k];
+        }
+        __syncthreads();
+    }
+    if (t == 0) sortie[0] = pi[0];
+}
+
+// ============================================================================ C-ABI launch layer
+namespace {
+inline hipStream_t flux_de(void* f) { return reinterpret_cast<hipStream_t>(f); }
+}  // namespace
+
+extern "C" int trc_gemv_q8_0(trc_vue w, trc_vue x, trc_vue biais, trc_vue y, uint32_t lignes, uint32_t colonnes,
+                             void* flux) {
+    TRC_VERIFIER(lignes > 0 && colonnes > 0 && colonnes % 32 == 0, "forme %u x %u", lignes, colonnes);
+    const uint64_t octets = uint64_t(lignes) * (colonnes / 32) * trc::Q8_OCTETS_BLOC;
+    TRC_VERIFIER(w.adresse != 0 && w.octets >= octets && w.adresse % 2 == 0,
+                 "matrice Q8_0 de %llu o, %llu o demandes (adresse paire)", (unsigned long long)w.octets,
+                 (unsigned long long)octets);
+    TRC_VERIFIER(x.adresse != 0 && x.octets >= 4ull * colonnes && x.adresse % 16 == 0,
+                 "x trop court ou non aligne sur 16");
+    TRC_VERIFIER(y.adresse != 0 && y.octets >= 4ull * lignes, "y trop court");
+    TRC_VERIFIER(biais.adresse == 0 || biais.octets >= 4ull * lignes, "biais trop court");
+    hipLaunchKernelGGL(gemv_q8_0, dim3((lignes + 31) / 32), dim3(trc::FILS_PASSE), 0, flux_de(flux),
+                       reinterpret_cast<const uint8_t*>(w.adresse), reinterpret_cast<const float*>(x.adresse),
+                       reinterpret_cast<const float*>(biais.adresse), reinterpret_cast<float*>(y.adresse), lignes,
+                       colonnes);
+    return trc::apres_lancement("gemv_q8_0");
+}
+
+extern "C" int trc_ligne_q8_0(trc_vue w, uint32_t ligne, uint32_t colonnes, trc_vue y, void* flux) {
+    TRC_VERIFIER(colonnes > 0 && colonnes % 32 == 0, "%u colonnes", colonnes);
+    const uint64_t ol = uint64_t(colonnes / 32) * trc::Q8_OCTETS_BLOC;
+    TRC_VERIFIER(w.adresse != 0 && y.adresse != 0 && w.octets >= (uint64_t(ligne) + 1) * ol &&
+                     y.octets >= 4ull * colonnes,
+                 "ligne_q8_0 : vues trop courtes");
+    hipLaunchKernelGGL(ligne_q8_0, dim3((colonnes + trc::FILS_PASSE - 1) / trc::FILS_PASSE), dim3(trc::FILS_PASSE),
+                       0, flux_de(flux), reinterpret_cast<const uint8_t*>(w.adresse), ligne, colonnes,
+                       reinterpret_cast<float*>(y.adresse));
+    return trc::apres_lancement("ligne_q8_0");
+}
+
+extern "C" int trc_rmsnorm(trc_vue x, trc_vue w, trc_vue y, uint32_t n, uint32_t lignes, float eps, void* flux) {
+    TRC_VERIFIER(n > 0 && lignes > 0, "rmsnorm de %u x %u", lignes, n);
+    const uint64_t o = 4ull * n * lignes;
+    TRC_VERIFIER(x.adresse && w.adresse && y.adresse && x.octets >= o && y.octets >= o && w.octets >= 4ull * n,
+                 "rmsnorm : vues trop courtes");
+    hipLaunchKernelGGL(rmsnorm, dim3(lignes), dim3(trc::FILS_PASSE), 0, flux_de(flux),
+                       reinterpret_cast<const float*>(x.adresse), reinterpret_cast<const float*>(w.adresse),
+                       reinterpret_cast<float*>(y.adresse), n, eps);
+    return trc::apres_lancement("rmsnorm");
+}
+
+extern "C" int trc_rope_yarn(trc_vue q, trc_vue k, uint32_t tetes_q, uint32_t tetes_k, uint32_t position,
+                             const trc_params_rope* p, void* flux) {
+    if (p == nullptr) return trc::usage("parametres de YaRN absents");
+    TRC_VERIFIER(p->dim_tete > 0 && p->dim_tete % 2 == 0 && p->dim_tete <= 128, "dimension de tete %u", p->dim_tete);
+    TRC_VERIFIER(p->variante <= 1, "variante de YaRN %u", p->variante);
+    TRC_VERIFIER(tetes_q + tetes_k > 0, "aucune tete");
+    const uint64_t d = p->dim_tete;
+    TRC_VERIFIER((tetes_q == 0 || (q.adresse && q.octets >= 4 * d * tetes_q)) &&
+                     (tetes_k == 0 || (k.adresse && k.octets >= 4 * d * tetes_k)),
+                 "rope : vues trop courtes");
+    hipLaunchKernelGGL(rope_yarn, dim3(tetes_q + tetes_k), dim3(64), 0, flux_de(flux),
+                       reinterpret_cast<float*>(q.adresse), reinterpret_cast<float*>(k.adresse), tetes_q, tetes_k,
+                       position, *p);
+    return trc::apres_lancement("rope_yarn");
+}
+
+extern "C" int trc_ecrire_kv(trc_vue k, trc_vue v, trc_vue cache_k, trc_vue cache_v, uint32_t dkv, uint32_t case_kv,
+                             void* flux) {
+    TRC_VERIFIER(dkv > 0, "dkv nul");
+    const uint64_t fin = 2ull * (uint64_t(case_kv) + 1) * dkv;
+    TRC_VERIFIER(k.adresse && v.adresse && k.octets >= 4ull * dkv && v.octets >= 4ull * dkv, "k ou v trop court");
+    TRC_VERIFIER(cache_k.adresse && cache_v.adresse && cache_k.octets >= fin && cache_v.octets >= fin,
+                 "case %u hors du cache", case_kv);
+    hipLaunchKernelGGL(ecrire_kv, dim3((dkv + trc::FILS_PASSE - 1) / trc::FILS_PASSE), dim3(trc::FILS_PASSE), 0,
+                       flux_de(flux), reinterpret_cast<const float*>(k.adresse),
+                       reinterpret_cast<const float*>(v.adresse), reinterpret_cast<uint16_t*>(cache_k.adresse),
+                       reinterpret_cast<uint16_t*>(cache_v.adresse), dkv, case_kv);
+    return trc::apres_lancement("ecrire_kv");
+}
+
+extern "C" int trc_attention(trc_vue q, trc_vue cache_k, trc_vue cache_v, trc_vue puits, trc_vue sortie,
+                             const trc_params_attention* p, void* flux) {
+    if (p == nullptr) return trc::usage("parametres d'attention absents");
+    TRC_VERIFIER(p->dim_tete == 64 && p->tetes_kv > 0 && p->tetes > 0 && p->tetes % p->tetes_kv == 0,
+                 "tetes %u / %u de dimension %u", p->tetes, p->tetes_kv, p->dim_tete);
+    TRC_VERIFIER(p->fin >= p->debut && p->fin - p->debut <= trc::ATTENTION_POSITIONS_MAX, "positions [%u, %u)",
+                 p->debut, p->fin);
+    TRC_VERIFIER(p->anneau == 0 || p->fin - p->debut <= p->anneau, "plus de positions que de cases dans l'anneau");
+    const uint64_t cases = p->anneau > 0 ? p->anneau : p->fin;
+    const uint64_t dkv = uint64_t(p->tetes_kv) * 64;
+    TRC_VERIFIER(cache_k.adresse && cache_v.adresse && cache_k.octets >= 2 * cases * dkv &&
+                     cache_v.octets >= 2 * cases * dkv,
+                 "cache trop court");
+    TRC_VERIFIER(cache_k.adresse % 16 == 0, "cache des cles non aligne sur 16");
+    TRC_VERIFIER(q.adresse && sortie.adresse && puits.adresse && q.octets >= 4ull * 64 * p->tetes &&
+                     sortie.octets >= 4ull * 64 * p->tetes && puits.octets >= 4ull * p->tetes,
+                 "attention : vues trop courtes");
+    const size_t lds = 4u * size_t(p->fin - p->debut);
+    hipLaunchKernelGGL(attention, dim3(p->tetes), dim3(trc::FILS_PASSE), lds, flux_de(flux),
+                       reinterpret_cast<const float*>(q.adresse), reinterpret_cast<const uint16_t*>(cache_k.adresse),
+                       reinterpret_cast<const uint16_t*>(cache_v.adresse), reinterpret_cast<const float*>(puits.adresse),
+                       reinterpret_cast<float*>(sortie.adresse), *p);
+    return trc::apres_lancement("attention");
+}
+
+extern "C" int trc_argmax(trc_vue v, uint32_t n, trc_vue sortie, void* flux) {
+    TRC_VERIFIER(n > 0 && v.adresse && sortie.adresse && v.octets >= 4ull * n && sortie.octets >= 4,
+                 "argmax : vues trop courtes");
+    hipLaunchKernelGGL(argmax, dim3(1), dim3(trc::FILS_ARGMAX), 0, flux_de(flux),
+                       reinterpret_cast<const float*>(v.adresse), n, reinterpret_cast<uint32_t*>(sortie.adresse));
+    return trc::apres_lancement("argmax");
+}

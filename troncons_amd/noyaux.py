@@ -52,6 +52,42 @@ class DimsExpert(C.Structure):
         return cls.de([2880] * 3, [2880] * 3)
 
 
+class ParamsRope(C.Structure):
+    """abi.rs:229-251 — YaRN parameters, 48 bytes."""
+    _fields_ = [("base", C.c_double), ("facteur", C.c_double), ("ctx_origine", C.c_double),
+                ("beta_rapide", C.c_double), ("beta_lent", C.c_double), ("dim_tete", C.c_uint32),
+                ("variante", C.c_uint32)]
+
+    @classmethod
+    def gpt_oss(cls, **changes) -> "ParamsRope":
+        """ParamsRope::GPT_OSS (abi.rs:249-250), fields overridable."""
+        v = dict(base=150000.0, facteur=32.0, ctx_origine=4096.0, beta_rapide=32.0, beta_lent=1.0, dim_tete=64,
+                 variante=0)
+        v.update(changes)
+        return cls(**v)
+
+
+FENETRE_GPT_OSS = 128  # abi.rs:275
+
+
+class ParamsAttention(C.Structure):
+    """abi.rs:253-291 — one decode position's attention, 32 bytes."""
+    _fields_ = [("tetes", C.c_uint32), ("tetes_kv", C.c_uint32), ("dim_tete", C.c_uint32), ("debut", C.c_uint32),
+                ("fin", C.c_uint32), ("anneau", C.c_uint32), ("echelle", C.c_float), ("reserve", C.c_uint32)]
+
+    @classmethod
+    def gpt_oss(cls, position: int, fenetre: int) -> "ParamsAttention":
+        """ParamsAttention::gpt_oss (abi.rs:278-284)."""
+        fin = position + 1
+        debut = max(fin - fenetre, 0) if fenetre > 0 else 0
+        return cls(64, 8, 64, debut, fin, fenetre, 0.125, 0)
+
+    @staticmethod
+    def case(position: int, anneau: int) -> int:
+        """abi.rs:287-289: the cache slot of a position."""
+        return position % anneau if anneau > 0 else position
+
+
 class DescGemv(C.Structure):
     """abi.rs:18-27 — 32 bytes."""
     _fields_ = [("matrice", C.c_uint64), ("x", C.c_uint64), ("y", C.c_uint64), ("lignes", C.c_uint32),
@@ -132,6 +168,13 @@ def _declarer(l: C.CDLL) -> C.CDLL:
     l.trc_routeur_topk.argtypes = [V, C.c_uint32, C.c_uint32, V, V, C.c_uint64, C.c_uint32, C.c_void_p]
     l.trc_swiglu_oai.argtypes = [V, V, V, C.c_uint32, C.c_void_p]
     l.trc_combiner.argtypes = [V, V, C.c_uint32, V, C.c_uint32, C.c_uint32, C.c_void_p]
+    l.trc_gemv_q8_0.argtypes = [V, V, V, V, C.c_uint32, C.c_uint32, C.c_void_p]
+    l.trc_ligne_q8_0.argtypes = [V, C.c_uint32, C.c_uint32, V, C.c_void_p]
+    l.trc_rmsnorm.argtypes = [V, V, V, C.c_uint32, C.c_uint32, C.c_float, C.c_void_p]
+    l.trc_rope_yarn.argtypes = [V, V, C.c_uint32, C.c_uint32, C.c_uint32, C.POINTER(ParamsRope), C.c_void_p]
+    l.trc_ecrire_kv.argtypes = [V, V, V, V, C.c_uint32, C.c_uint32, C.c_void_p]
+    l.trc_attention.argtypes = [V, V, V, V, V, C.POINTER(ParamsAttention), C.c_void_p]
+    l.trc_argmax.argtypes = [V, C.c_uint32, V, C.c_void_p]
     l._trc_declare = True
     return l
 
@@ -286,3 +329,34 @@ class Noyaux:
     def combiner(self, residu, sorties, pas: int, poids, n: int, d: int, f=None) -> None:
         """lib.rs:463"""
         _statut(self._l.trc_combiner(_vue(residu), _vue(sorties), pas, _vue(poids), n, d, _flux(f)))
+
+    # the rest of the layer step (passe.cuh)
+
+    def gemv_q8_0(self, w, x, biais, y, lignes: int, colonnes: int, f=None) -> None:
+        """lib.rs:291"""
+        _statut(self._l.trc_gemv_q8_0(_vue(w), _vue(x), _vue(biais), _vue(y), lignes, colonnes, _flux(f)))
+
+    def ligne_q8_0(self, w, ligne: int, colonnes: int, y, f=None) -> None:
+        """lib.rs:478"""
+        _statut(self._l.trc_ligne_q8_0(_vue(w), ligne, colonnes, _vue(y), _flux(f)))
+
+    def rmsnorm(self, x, w, y, n: int, lignes: int, eps: float, f=None) -> None:
+        """lib.rs:322"""
+        _statut(self._l.trc_rmsnorm(_vue(x), _vue(w), _vue(y), n, lignes, eps, _flux(f)))
+
+    def rope_yarn(self, q, k, tetes_q: int, tetes_k: int, position: int, p: ParamsRope, f=None) -> None:
+        """lib.rs:334"""
+        _statut(self._l.trc_rope_yarn(_vue(q), _vue(k), tetes_q, tetes_k, position, C.byref(p), _flux(f)))
+
+    def ecrire_kv(self, k, v, cache_k, cache_v, dkv: int, case_kv: int, f=None) -> None:
+        """lib.rs:348"""
+        _statut(self._l.trc_ecrire_kv(_vue(k), _vue(v), _vue(cache_k), _vue(cache_v), dkv, case_kv, _flux(f)))
+
+    def attention(self, q, cache_k, cache_v, puits, sortie, p: ParamsAttention, f=None) -> None:
+        """lib.rs:362"""
+        _statut(self._l.trc_attention(_vue(q), _vue(cache_k), _vue(cache_v), _vue(puits), _vue(sortie), C.byref(p),
+                                      _flux(f)))
+
+    def argmax(self, v, n: int, sortie, f=None) -> None:
+        """lib.rs:490"""
+        _statut(self._l.trc_argmax(_vue(v), n, _vue(sortie), _flux(f)))
