@@ -588,6 +588,64 @@ def chrono_passes(fusion, pas, n):
     return noyaux
 
 
+VOCAB_GPT = 201088
+
+
+def bench_modele(args, dims, flux):
+    """Config 6: a whole decode step of a gpt-oss-120b-shaped model held resident — embedding row,
+    36 layers (Q8_0 attention with sinks and YaRN, even layers windowed on a ring of 128, f16 KV
+    cache; then the fused compressed MoE layer), the 201088-row Q8_0 head and argmax — issued by the
+    native driver (csrc/modele.cpp, one call per token). Synthetic weights; positions 0, 1, ... of a seeded token
+    sequence (teacher forced, so every step does the same work as a real one)."""
+    import numpy as np
+
+    from troncons_amd import modele as Mo
+    from troncons_amd.noyaux import ParamsRope
+    h = Mo.Hyper(couches=args.couches, d=C_GPT, tetes=64, tetes_kv=8, experts=args.experts, actifs=args.k,
+                 vocab=VOCAB_GPT, eps=1e-5, rope=ParamsRope.gpt_oss(), fenetre=128, contexte=4096, dims=dims,
+                 n_delta=args.n_delta, n_codes=args.n_codes)
+    if args.steps + args.warmup > h.contexte:
+        raise SystemExit(f"--steps + --warmup above the context of {h.contexte} positions")
+    t0 = time.perf_counter()
+    m = Mo.Modele.synthetique(h, args.graine, f=flux, progres=lambda l: print(
+        f"bench: layer {l} encoded, uploaded and mounted ({time.perf_counter() - t0:.1f} s)", file=sys.stderr,
+        flush=True))
+    t_gen = time.perf_counter() - t0
+    jetons = np.random.default_rng(args.graine).integers(0, h.vocab, args.steps + args.warmup)
+    position = [0]
+
+    def pas(_s):
+        m.pas_natif(int(jetons[position[0]]), position[0])
+        position[0] += 1
+
+    ms = temps(pas, args.steps, args.warmup, flux)
+    ctl = m.controles_natif()
+    assert (ctl == 0).all(), f"control words {ctl}"
+    us = ms * 1e3 / args.steps
+    q8 = lambda r, c: r * (c // 32) * 34
+    attention = h.couches * (q8(h.dq, h.d) + 2 * q8(h.dkv, h.d) + q8(h.d, h.dq))
+    tete = q8(h.vocab, h.d) + q8(1, h.d)
+    parties = float(np.mean([t.numel() for t in m.c[0]["parties"]]))
+    experts = h.couches * h.actifs * parties
+    return {
+        "metric": f"config6 us/token for a whole decode step of {h.couches} layers", "value": round(us, 2),
+        "unit": "us/token", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms / args.steps, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "Q8_0 / f16 KV / u32 rANS / f32 GEMV", "tokens_per_s": round(1e6 / us, 1),
+        "data": "synthetic (seeded Q8_0 attention and head, f32 norms, biases and sinks, bf16 router, "
+                "rANS-coded MXFP4 experts)",
+        "config": {"workload": f"config6: embedding, {h.couches} layers (Q8_0 attention, 64/8 heads, sinks, YaRN, "
+                               "even layers windowed on 128, f16 KV; fused compressed MoE top-4 of 128), "
+                               f"{h.vocab}-row Q8_0 head, argmax", "layers": h.couches, "hidden": h.d,
+                   "experts": h.experts, "k": h.actifs, "vocab": h.vocab, "n_codes": h.n_codes,
+                   "n_delta": h.n_delta, "positions": f"0..{args.steps + args.warmup - 1}"},
+        "bytes_per_token": {"attention_q8_0": int(attention), "head_q8_0": int(tete),
+                            "experts_compressed_estimate": int(experts)},
+        "gbps_effective": round((attention + tete + experts) / (us * 1e-6) / 1e9, 1),
+        "roofline": None, "cpu_baseline": None, "setup_s": round(t_gen, 1),
+    }
+
+
 def temps(pas, steps, warmup, flux):
     import torch
     for s in range(warmup):
@@ -607,9 +665,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--config", type=int, default=3, choices=(1, 2, 3, 4, 5))
+    ap.add_argument("--config", type=int, default=3, choices=(1, 2, 3, 4, 5, 6))
     ap.add_argument("--positions", type=int, default=512, help="positions of a --config 5 prefill batch")
-    ap.add_argument("--couches", type=int, default=36, help="layers of --config 4")
+    ap.add_argument("--couches", type=int, default=36, help="layers of --config 4 and 6")
     ap.add_argument("--flux", action="store_true",
                     help="--config 4 variant: the experts stay in pinned host memory and the chosen ones are "
                          "copied per layer on a side stream, overlapped with the decode")
@@ -652,6 +710,10 @@ def main():
     fz = fusion.Fusion()
     flux = torch.cuda.current_stream()
     V = VueCarte.de
+
+    if args.config == 6:
+        print(json.dumps(bench_modele(args, dims, flux)), flush=True)
+        return
 
     if args.config == 4 and args.ordo:
         print(json.dumps(bench_ordo(args, E, k, C, dims, dev, n_fils)), flush=True)

@@ -217,6 +217,49 @@ int trc_attention(trc_vue q, trc_vue cache_k, trc_vue cache_v, trc_vue puits, tr
  * chosen; all NaN: 0xFFFFFFFF) into sortie (u32). */
 int trc_argmax(trc_vue v, uint32_t n, trc_vue sortie, void* flux);
 
+/* ------------------------------------------------ the decode step of a model (trc_modele::Modele) */
+
+/* Hyper (trc-modele/src/lib.rs:60-79): a gpt-oss-shaped model; heads of 64 (rope.dim_tete = 64);
+ * even layers are windowed on a ring of `fenetre` positions, odd ones keep `contexte` positions. */
+typedef struct {
+    uint32_t couches, d, tetes, tetes_kv, experts, actifs, vocab, fenetre, contexte, n_delta, n_codes;
+    float eps;
+    trc_params_rope rope;
+    trc_dims_expert dims;
+} trc_hyper;
+
+/* One layer's device views, owned by the caller (Modele's CoucheResidente, lib.rs:300-360):
+ * attention weights in Q8_0 and f32, the sinks, the router (bf16, experts x d, 8-byte aligned) and
+ * its optional bias, the layer's mounted directory (trc_monter_couche) and LUTs, the f16 KV caches
+ * (ring of fenetre slots on even layers, contexte slots on odd ones). */
+typedef struct {
+    trc_vue attn_norm, wq, bq, wk, bk, wv, bv, wo, bo, puits, post_norm;
+    trc_vue routeur, routeur_biais, repertoire, luts, cache_k, cache_v;
+} trc_couche_modele;
+
+typedef struct trc_modele trc_modele;
+
+/* Workspace bytes of trc_modele_creer (0 if the shape is refused). */
+uint64_t trc_modele_taille_travail(const trc_hyper* h);
+/* Modele::charger's device side (lib.rs:366-455) over resident weights: keeps the views and cuts
+ * `travail` (256-aligned) into the step's buffers. The caller keeps every view alive. */
+int trc_modele_creer(const trc_hyper* h, const trc_couche_modele* couches, trc_vue enchassement,
+                     trc_vue norme_sortie, trc_vue sortie, trc_vue travail, trc_modele** m);
+void trc_modele_detruire(trc_modele* m);
+/* Views of the residual x, the logits (f32[vocab]), the greedy token (u32), the last layer's
+ * top-k indices (u32[8]) and the control words (u32[4], to be zeroed by the caller). */
+int trc_modele_vues(const trc_modele* m, trc_vue* x, trc_vue* logits, trc_vue* jeton, trc_vue* indices,
+                    trc_vue* controle);
+/* Modele::enchasser (lib.rs:481-487): x = row `jeton` of the Q8_0 embedding. */
+int trc_modele_enchasser(trc_modele* m, uint32_t jeton, void* flux);
+/* Layer l at `position`: Modele::debut_couche (lib.rs:498-530) with the router and
+ * Modele::fin_couche (lib.rs:533-555) as one fused compressed MoE layer. */
+int trc_modele_couche(trc_modele* m, uint32_t l, uint32_t position, void* flux);
+/* Modele::sortie (lib.rs:557-568): output norm, Q8_0 logits, argmax. */
+int trc_modele_sortie(trc_modele* m, void* flux);
+/* One decode step: enchasser, every layer, sortie (asynchronous on flux, no host sync). */
+int trc_modele_pas(trc_modele* m, uint32_t jeton, uint32_t position, void* flux);
+
 /* Workspace bytes of trc_couche_moe_fusionnee. */
 uint64_t trc_taille_travail_couche_moe(const trc_dims_expert* dims, uint32_t experts, uint32_t k, uint32_t n_codes);
 /* One MoE layer step at batch 1 (Modele::debut_couche's router, gemv_f32 + routeur_topk, then

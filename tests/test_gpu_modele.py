@@ -5,7 +5,9 @@ whose ring wraps, and a full-cache layer), output projection and residual, post-
 the k experts decoded from their .trc parts (the oracle's decoder and GEMV in the reference order),
 SwiGLU and the ordered combine; then the output norm, Q8_0 logits and argmax.
 
-Teacher forcing (a fixed token sequence) keeps both chains on the same inputs. Per step: the
+The same step issued by the native driver (csrc/modele.cpp, one call per token) gives the Python
+driver's logits bit for bit. Teacher forcing (a fixed token sequence) keeps both chains on the same
+inputs. Per step: the
 router's choices equal the oracle's in every layer, the logits are within 1e-4 * max|z| of the
 oracle's (each layer's experts meet 1e-5; attention and the projections follow the reference order),
 and the greedy token is the oracle's wherever its margin over the runner-up exceeds that tolerance.
@@ -88,6 +90,7 @@ def test_decode_steps_equal_the_oracle_chain(graine):
     h = _hyper()
     couches, emb, norme, sortie = Mo.poids_synthetiques(h, graine)
     m = Mo.Modele(h, couches, emb, norme, sortie)
+    mn = Mo.Modele(h, couches, emb, norme, sortie)  # the same step issued by the native driver
     ref = ChaineOracle(h, couches, emb, norme, sortie)
     jetons = np.random.default_rng(graine).integers(0, h.vocab, 14)
     choix_gpu = []
@@ -102,13 +105,16 @@ def test_decode_steps_equal_the_oracle_chain(graine):
             choix_gpu.append(m.indices())
         m.sortie()
         z = m.logits()
+        mn.pas_natif(int(tok), pos)
+        assert (mn.logits_natif().view(np.uint32) == z.view(np.uint32)).all(), pos
+        assert mn.jeton_natif() == m.jeton()
         for l in range(h.couches):
             assert (choix_gpu[l] == choix[l]).all(), (pos, l, choix_gpu[l], choix[l])
         assert np.abs(z - z_ref).max() <= 1e-4 * np.abs(z_ref).max(), pos
         deux = np.sort(z_ref)[-2:]
         if deux[1] - deux[0] > 1e-4 * np.abs(z_ref).max():
             assert m.jeton() == int(np.argmax(z_ref)), pos
-    assert (m.controles() == 0).all()
+    assert (m.controles() == 0).all() and (mn.controles_natif() == 0).all()
 
 
 def test_model_refuses_position_past_context():
@@ -118,3 +124,7 @@ def test_model_refuses_position_past_context():
     m = Mo.Modele(h, couches, emb, norme, sortie)
     with pytest.raises(ErreurUsage):
         m.debut_couche(0, 4)
+    with pytest.raises(ErreurUsage):
+        m.pas_natif(0, 4)
+    with pytest.raises(ErreurUsage):
+        m.pas_natif(h.vocab, 0)

@@ -12,6 +12,7 @@ gpt-oss-shaped set (attention in Q8_0, experts coded by this library's encoder).
 """
 from __future__ import annotations
 
+import ctypes as C
 from dataclasses import dataclass, field
 
 import numpy as np
@@ -82,33 +83,45 @@ def _q8_0(rng, lignes: int, colonnes: int, echelle: float) -> np.ndarray:
     return np.concatenate([d.view(np.uint8).reshape(-1, 2), q.view(np.uint8)], axis=1).ravel()
 
 
+def _ech(c: int) -> float:
+    return 1.0 / (73.0 * np.sqrt(c))  # |q| ~ 73 on average: rows of unit gain
+
+
+def couche_synthetique(h: Hyper, graine: int, l: int, rng) -> PoidsCouche:
+    """Layer `l` of a seeded model: attention drawn from `rng`, experts coded by the encoder."""
+    d, dq, dkv = h.d, h.dq, h.dkv
+    synth = codeur.CoucheSynthetique(graine, l, h.experts, h.dims, N_delta=h.n_delta, N_codes=h.n_codes)
+    routeur = (rng.standard_normal((h.experts, d)) * (1.0 / np.sqrt(d))).astype(np.float32)
+    p = PoidsCouche(
+        attn_norm=(1.0 + 0.1 * rng.standard_normal(d)).astype(np.float32),
+        wq=_q8_0(rng, dq, d, _ech(d)), bq=(0.1 * rng.standard_normal(dq)).astype(np.float32),
+        wk=_q8_0(rng, dkv, d, _ech(d)), bk=(0.1 * rng.standard_normal(dkv)).astype(np.float32),
+        wv=_q8_0(rng, dkv, d, _ech(d)), bv=(0.1 * rng.standard_normal(dkv)).astype(np.float32),
+        wo=_q8_0(rng, d, dq, _ech(dq)), bo=(0.1 * rng.standard_normal(d)).astype(np.float32),
+        puits=rng.standard_normal(h.tetes).astype(np.float32),
+        post_norm=(1.0 + 0.1 * rng.standard_normal(d)).astype(np.float32),
+        routeur=(routeur.view(np.uint32) >> 16).astype(np.uint16),
+        routeur_biais=(0.1 * rng.standard_normal(h.experts)).astype(np.float32),
+        parties=[synth.partie(e).copy() for e in range(h.experts)],
+        freqs=[[np.array(f) if f is not None else None for f in fj] for fj in synth.freqs()],
+    )
+    synth.liberer()
+    return p
+
+
+def tete_synthetique(h: Hyper, rng):
+    """(embedding, output norm, output head) of a seeded model."""
+    enchassement = _q8_0(rng, h.vocab, h.d, 0.02)
+    norme_sortie = (1.0 + 0.1 * rng.standard_normal(h.d)).astype(np.float32)
+    sortie = _q8_0(rng, h.vocab, h.d, _ech(h.d))
+    return enchassement, norme_sortie, sortie
+
+
 def poids_synthetiques(h: Hyper, graine: int):
     """Seeded weights of the shape `h`: (layers, embedding, output norm, output head)."""
     rng = np.random.default_rng(graine)
-    d, dq, dkv = h.d, h.dq, h.dkv
-    ech = lambda c: 1.0 / (73.0 * np.sqrt(c))  # |q| ~ 73 on average: rows of unit gain
-    couches = []
-    for l in range(h.couches):
-        synth = codeur.CoucheSynthetique(graine, l, h.experts, h.dims, N_delta=h.n_delta, N_codes=h.n_codes)
-        routeur = (rng.standard_normal((h.experts, d)) * (1.0 / np.sqrt(d))).astype(np.float32)
-        couches.append(PoidsCouche(
-            attn_norm=(1.0 + 0.1 * rng.standard_normal(d)).astype(np.float32),
-            wq=_q8_0(rng, dq, d, ech(d)), bq=(0.1 * rng.standard_normal(dq)).astype(np.float32),
-            wk=_q8_0(rng, dkv, d, ech(d)), bk=(0.1 * rng.standard_normal(dkv)).astype(np.float32),
-            wv=_q8_0(rng, dkv, d, ech(d)), bv=(0.1 * rng.standard_normal(dkv)).astype(np.float32),
-            wo=_q8_0(rng, d, dq, ech(dq)), bo=(0.1 * rng.standard_normal(d)).astype(np.float32),
-            puits=rng.standard_normal(h.tetes).astype(np.float32),
-            post_norm=(1.0 + 0.1 * rng.standard_normal(d)).astype(np.float32),
-            routeur=(routeur.view(np.uint32) >> 16).astype(np.uint16),
-            routeur_biais=(0.1 * rng.standard_normal(h.experts)).astype(np.float32),
-            parties=[synth.partie(e).copy() for e in range(h.experts)],
-            freqs=[[np.array(f) if f is not None else None for f in fj] for fj in synth.freqs()],
-        ))
-        synth.liberer()
-    enchassement = _q8_0(rng, h.vocab, d, 0.02)
-    norme_sortie = (1.0 + 0.1 * rng.standard_normal(d)).astype(np.float32)
-    sortie = _q8_0(rng, h.vocab, d, ech(d))
-    return couches, enchassement, norme_sortie, sortie
+    couches = [couche_synthetique(h, graine, l, rng) for l in range(h.couches)]
+    return (couches, *tete_synthetique(h, rng))
 
 
 class _Tampons:
@@ -134,6 +147,39 @@ def _v(t) -> VueCarte:
     return VueCarte.de(t)
 
 
+class _Hyper(C.Structure):
+    """trc_hyper (include/troncons_hip.h)."""
+    _fields_ = [(n, C.c_uint32) for n in ("couches", "d", "tetes", "tetes_kv", "experts", "actifs", "vocab", "fenetre",
+                                          "contexte", "n_delta", "n_codes")] + [
+        ("eps", C.c_float), ("rope", ParamsRope), ("dims", DimsExpert)]
+
+
+_CHAMPS_COUCHE = ("attn_norm", "wq", "bq", "wk", "bk", "wv", "bv", "wo", "bo", "puits", "post_norm", "routeur",
+                  "routeur_biais", "repertoire", "luts", "cache_k", "cache_v")
+
+
+class _CoucheModele(C.Structure):
+    """trc_couche_modele (include/troncons_hip.h)."""
+    _fields_ = [(n, noyaux._Vue) for n in _CHAMPS_COUCHE]
+
+
+def _declarer(l):
+    if getattr(l, "_trc_modele", False):
+        return l
+    V = noyaux._Vue
+    l.trc_modele_taille_travail.argtypes = [C.POINTER(_Hyper)]
+    l.trc_modele_taille_travail.restype = C.c_uint64
+    l.trc_modele_creer.argtypes = [C.POINTER(_Hyper), C.POINTER(_CoucheModele), V, V, V, V, C.POINTER(C.c_void_p)]
+    l.trc_modele_detruire.argtypes = [C.c_void_p]
+    l.trc_modele_vues.argtypes = [C.c_void_p] + [C.POINTER(V)] * 5
+    l.trc_modele_enchasser.argtypes = [C.c_void_p, C.c_uint32, C.c_void_p]
+    l.trc_modele_couche.argtypes = [C.c_void_p, C.c_uint32, C.c_uint32, C.c_void_p]
+    l.trc_modele_sortie.argtypes = [C.c_void_p, C.c_void_p]
+    l.trc_modele_pas.argtypes = [C.c_void_p, C.c_uint32, C.c_uint32, C.c_void_p]
+    l._trc_modele = True
+    return l
+
+
 class Modele:
     """Modele (lib.rs:366-602) for a model held resident: attention weights and KV caches in HBM,
     each layer's experts as resident coded parts mounted for the fused MoE layer."""
@@ -142,26 +188,15 @@ class Modele:
                  sortie: np.ndarray, f=None):
         if h.dt != 64 or h.tetes % h.tetes_kv != 0 or h.d % 32 != 0:
             raise noyaux.ErreurUsage(f"forme d'attention {h.d} / {h.tetes} / {h.tetes_kv} / {h.dt}")
-        if len(couches) != h.couches:
+        if couches is not None and len(couches) != h.couches:
             raise noyaux.ErreurUsage(f"{len(couches)} couches pour {h.couches}")
+        couches = couches or []
         self.h, self.f = h, f
         self.n, self.fz = Noyaux.charger(), fusion.Fusion()
         T = self.T = _Tampons()
         self.c = []
-        for l, p in enumerate(couches):
-            c = {k: T.copie(getattr(p, k)) for k in ("attn_norm", "wq", "bq", "wk", "bk", "wv", "bv", "wo", "bo",
-                                                     "puits", "post_norm", "routeur")}
-            c["routeur_biais"] = T.copie(p.routeur_biais) if p.routeur_biais is not None else None
-            cases = h.anneau(l) or h.contexte
-            c["ck"], c["cv"] = T.zeros(2 * cases * h.dkv), T.zeros(2 * cases * h.dkv)
-            c["parties"] = [T.copie(np.asarray(pt, np.uint8)) for pt in p.parties]
-            table = T.copie(np.array([t.data_ptr() for t in c["parties"]], np.uint64))
-            c["rep"] = T.zeros(fusion.taille_repertoire(h.experts))
-            ctl = T.zeros(16)
-            self.fz.monter_couche(_v(table), h.experts, h.dims, _v(c["rep"]), _v(ctl), f)
-            c["ctl_montage"] = ctl
-            c["luts"] = T.copie(noyaux.luts_couche(p.freqs))
-            self.c.append(c)
+        for p in couches:
+            self.ajouter_couche(p)
         self.emb, self.norme_sortie, self.w_sortie = T.copie(enchassement), T.copie(norme_sortie), T.copie(sortie)
         d, dq, dkv = h.d, h.dq, h.dkv
         self.x, self.hh, self.h2 = T.zeros(4 * d), T.zeros(4 * d), T.zeros(4 * d)
@@ -170,6 +205,99 @@ class Modele:
         self.controle = T.zeros(16)
         self.travail = T.zeros(fusion.taille_travail_couche(h.dims, h.experts, h.actifs, h.n_codes) + 256)
         self.z, self.tok = T.zeros(4 * h.vocab), T.zeros(4)
+
+    def ajouter_couche(self, p: PoidsCouche) -> None:
+        """Uploads the next layer: attention weights, empty KV caches (the ring of a windowed layer,
+        the context otherwise), the experts' parts mounted for the fused MoE layer, its LUTs."""
+        h, T, f, l = self.h, self.T, self.f, len(self.c)
+        c = {k: T.copie(getattr(p, k)) for k in ("attn_norm", "wq", "bq", "wk", "bk", "wv", "bv", "wo", "bo",
+                                                 "puits", "post_norm", "routeur")}
+        c["routeur_biais"] = T.copie(p.routeur_biais) if p.routeur_biais is not None else None
+        cases = h.anneau(l) or h.contexte
+        c["ck"], c["cv"] = T.zeros(2 * cases * h.dkv), T.zeros(2 * cases * h.dkv)
+        c["parties"] = [T.copie(np.asarray(pt, np.uint8)) for pt in p.parties]
+        table = T.copie(np.array([t.data_ptr() for t in c["parties"]], np.uint64))
+        c["rep"] = T.zeros(fusion.taille_repertoire(h.experts))
+        ctl = T.zeros(16)
+        self.fz.monter_couche(_v(table), h.experts, h.dims, _v(c["rep"]), _v(ctl), f)
+        c["ctl_montage"] = ctl
+        c["luts"] = T.copie(noyaux.luts_couche(p.freqs))
+        self.c.append(c)
+
+    @classmethod
+    def synthetique(cls, h: Hyper, graine: int, progres=None, f=None) -> "Modele":
+        """A seeded model of shape `h` built layer by layer (one layer's host copy at a time)."""
+        rng = np.random.default_rng(graine)
+        tete = tete_synthetique(h, rng)
+        m = cls(h, None, *tete, f=f)
+        for l in range(h.couches):
+            m.ajouter_couche(couche_synthetique(h, graine, l, rng))
+            if progres is not None:
+                progres(l)
+        return m
+
+    def natif(self):
+        """The native driver (csrc/modele.cpp) over this model's device buffers, created once the
+        last layer is in: one C call per token."""
+        if getattr(self, "_natif", None) is not None:
+            return self._natif
+        h = self.h
+        if len(self.c) != h.couches:
+            raise noyaux.ErreurUsage(f"{len(self.c)} couches montees sur {h.couches}")
+        l = _declarer(noyaux.bibliotheque())
+        hy = _Hyper(h.couches, h.d, h.tetes, h.tetes_kv, h.experts, h.actifs, h.vocab, h.fenetre, h.contexte,
+                    h.n_delta, h.n_codes, h.eps, h.rope, h.dims)
+        couches = (_CoucheModele * h.couches)()
+        for i, c in enumerate(self.c):
+            for n in _CHAMPS_COUCHE:
+                t = {"repertoire": c["rep"], "cache_k": c["ck"], "cache_v": c["cv"]}.get(n, c.get(n))
+                setattr(couches[i], n, noyaux._vue(t))
+        octets = l.trc_modele_taille_travail(C.byref(hy))
+        if octets == 0:
+            raise noyaux.ErreurUsage("forme refusee par le pilote natif")
+        self._travail_natif = self.T.zeros(octets + 256)
+        tv = _v(self._travail_natif)
+        dec = (-tv.adresse) % 256
+        p = C.c_void_p()
+        noyaux._statut(l.trc_modele_creer(C.byref(hy), couches, noyaux._vue(self.emb), noyaux._vue(self.norme_sortie),
+                                          noyaux._vue(self.w_sortie), VueCarte(tv.adresse + dec, octets).c(),
+                                          C.byref(p)))
+        self._natif, self._l = p, l
+        vues = [noyaux._Vue() for _ in range(5)]
+        noyaux._statut(l.trc_modele_vues(p, *[C.byref(v) for v in vues]))
+        self._vues_natif = [VueCarte(v.adresse, v.octets) for v in vues]
+        return p
+
+    def pas_natif(self, jeton: int, position: int) -> None:
+        """trc_modele_pas: the same step issued by the native driver."""
+        p = self.natif()
+        noyaux._statut(self._l.trc_modele_pas(p, jeton, position, noyaux._flux(self.f)))
+
+    def _lire_natif(self, i: int, dtype, n: int) -> np.ndarray:
+        """Reads one of the native driver's buffers (a piece of the workspace tensor)."""
+        import torch
+        v = self._vues_natif[i]
+        dec = v.adresse - self._travail_natif.data_ptr()
+        octets = n * np.dtype(dtype).itemsize
+        torch.cuda.synchronize()
+        return self._travail_natif[dec:dec + octets].cpu().numpy().view(dtype).copy()
+
+    def logits_natif(self) -> np.ndarray:
+        return self._lire_natif(1, np.float32, self.h.vocab)
+
+    def jeton_natif(self) -> int:
+        return int(self._lire_natif(2, np.uint32, 1)[0])
+
+    def controles_natif(self) -> np.ndarray:
+        return self._lire_natif(4, np.uint32, 4)
+
+    def __del__(self):
+        try:
+            if getattr(self, "_natif", None) is not None:
+                self._l.trc_modele_detruire(self._natif)
+                self._natif = None
+        except Exception:
+            pass
 
     def _travail(self) -> VueCarte:
         v = _v(self.travail)
