@@ -57,6 +57,23 @@ def test_gemv_q8_0_bit_exact_against_oracle(k, r, c):
     assert (_q8(k, o, x, None, r, c).view(np.uint32) == O.gemv_q8_0(o, x, None, r, c).view(np.uint32)).all()
 
 
+def test_gemv_q8_0_unaligned_matrix_and_last_block(k):
+    # a matrix starting 2 bytes past a 4-byte boundary (the contract allows any even address), with
+    # the last block's window reaching past the matrix end on a view that ends there
+    rng = np.random.default_rng(12)
+    for r, c in ((33, 64), (7, 2880)):
+        nb = c // 32
+        d = (rng.standard_normal(r * nb) * 0.05).astype(np.float16)
+        q = rng.integers(-128, 128, size=(r * nb, 32)).astype(np.int8)
+        o = np.concatenate([d.view(np.uint8).reshape(-1, 2), q.view(np.uint8)], axis=1).ravel()
+        x = rng.standard_normal(c).astype(np.float32)
+        base = zeros(o.size + 2)
+        base[2:].copy_(torch.from_numpy(o.copy()).to(base.device))
+        y = zeros(4 * r)
+        k.gemv_q8_0(vue(base, 2, o.size), vue(dev(x)), None, vue(y), r, c)
+        assert (hote(y, np.float32).view(np.uint32) == O.gemv_q8_0(o, x, None, r, c).view(np.uint32)).all()
+
+
 def test_ligne_q8_0_exact(k):
     a = Alea(7)
     lignes, c = 5, 64

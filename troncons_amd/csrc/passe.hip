@@ -77,9 +77,12 @@ __device__ inline double inv_freq_yarn(const trc_params_rope& p, uint32_t i, dou
 }  // namespace trc
 
 // y = W x (+ b), W Q8_0; half-wavefront w of the block takes rows 4w .. 4w + 3 of its 32; lane l
-// of the half takes blocks b = l, l + 32, ...; in a block s = sum of q_i x_i (one fmaf chain, low
-// byte then high byte of each 16-bit word), then acc = fmaf(d, s, acc); butterfly over the half
-// (passe.cuh:52-97, 213-222). Block addresses are even (34 b): 16-bit loads.
+// of the half takes blocks b = l, l + 32, ...; in a block s = sum of q_i x_i (one fmaf chain in
+// element order), then acc = fmaf(d, s, acc); butterfly over the half (passe.cuh:52-97, 213-222).
+// A block (34 bytes, even address) is read as the nine dwords of the 4-byte aligned window that
+// holds it (d at byte 0 or 2 of the window, the codes after it), realigned by a 64-bit shift; the
+// window's last dword may pass the block by 2 bytes, so the matrix's very last block reads it as
+// 16 bits.
 extern "C" __global__ void __launch_bounds__(trc::FILS_PASSE)
 gemv_q8_0(const uint8_t* __restrict__ W, const float* __restrict__ x, const float* __restrict__ biais,
           float* __restrict__ y, uint32_t R, uint32_t C) {
@@ -89,6 +92,7 @@ gemv_q8_0(const uint8_t* __restrict__ W, const float* __restrict__ x, const floa
     if (r0 >= R) return;
     const uint32_t B = C / 32u;
     const uint64_t octets_ligne = uint64_t(B) * Q8_OCTETS_BLOC;
+    const uint64_t octets_matrice = uint64_t(R) * octets_ligne;
     const f32x4* x4 = reinterpret_cast<const f32x4*>(x);
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     uint32_t lig[4];
@@ -106,17 +110,31 @@ gemv_q8_0(const uint8_t* __restrict__ W, const float* __restrict__ x, const floa
         }
 #pragma unroll
         for (uint32_t i = 0; i < 4; ++i) {
-            const uint16_t* blk =
-                reinterpret_cast<const uint16_t*>(W + uint64_t(lig[i]) * octets_ligne + uint64_t(b) * Q8_OCTETS_BLOC);
-            uint32_t mots[17];
+            // absolute addresses: W is only 2-byte aligned; a window starting 2 bytes before W stays
+            // in W's 4-byte word, hence in its page
+            const uintptr_t a = reinterpret_cast<uintptr_t>(W) + uint64_t(lig[i]) * octets_ligne +
+                                uint64_t(b) * Q8_OCTETS_BLOC;
+            const uintptr_t a4 = a & ~uintptr_t(3);
+            const uint32_t decal = uint32_t(a - a4);  // 0 or 2: where d starts in the window
+            const uint32_t* fen = reinterpret_cast<const uint32_t*>(a4);
+            uint32_t w[9];
 #pragma unroll
-            for (uint32_t t = 0; t < 17; ++t) mots[t] = blk[t];
-            const float d = f16_vers_f32(mots[0]);
+            for (uint32_t t = 0; t < 8; ++t) w[t] = fen[t];
+            // dword 8 holds the last codes; past the block by 2 bytes when d sits at byte 0
+            w[8] = a4 + 36u <= reinterpret_cast<uintptr_t>(W) + octets_matrice
+                       ? fen[8]
+                       : uint32_t(reinterpret_cast<const uint16_t*>(fen + 8)[0]);
+            const float d = f16_vers_f32(decal ? (w[0] >> 16) : (w[0] & 0xFFFFu));
+            // the 32 codes start at byte 2 + decal of the window: realign dwords by 16 or 32 bits
+            const uint32_t bits = 8u * (2u + decal);
             float s = 0.0f;
 #pragma unroll
-            for (uint32_t t = 0; t < 16; ++t) {
-                s = fmaf(float(int8_t(mots[1 + t] & 0xFFu)), xv[2 * t], s);
-                s = fmaf(float(int8_t(mots[1 + t] >> 8)), xv[2 * t + 1], s);
+            for (uint32_t t = 0; t < 8; ++t) {
+                const uint64_t paire = (uint64_t(w[t + 1]) << 32) | w[t];
+                const uint32_t q4 = uint32_t(paire >> bits);
+#pragma unroll
+                for (uint32_t u = 0; u < 4; ++u)
+                    s = fmaf(float(int32_t(q4 << (24u - 8u * u)) >> 24), xv[4 * t + u], s);
             }
             acc[i] = fmaf(d, s, acc[i]);
         }
@@ -273,13 +291,36 @@ argmax(const float* __restrict__ v, uint32_t n, uint32_t* __restrict__ sortie) {
     const uint32_t t = threadIdx.x;
     float bv = -INFINITY;
     uint32_t bi = 0xFFFFFFFFu;
-    for (uint32_t i = t; i < n; i += FILS_ARGMAX) {
-        const float xv = v[i];
+    auto voir = [&](float xv, uint32_t i) {
         if (meilleur(xv, i, bv, bi)) {
             bv = xv;
             bi = i;
         }
+    };
+    // The result does not depend on the order the values are seen in: the scalar head up to a
+    // 16-byte boundary, then 16-byte loads, four in flight per thread, then the scalar tail.
+    const uint32_t tete = min(n, uint32_t((16u - (reinterpret_cast<uintptr_t>(v) & 15u)) & 15u) / 4u);
+    for (uint32_t i = t; i < tete; i += FILS_ARGMAX) voir(v[i], i);
+    const uint32_t n4 = (n - tete) / 4u;
+    const f32x4* v4 = reinterpret_cast<const f32x4*>(v + tete);
+    for (uint32_t j0 = t; j0 < n4; j0 += 4u * FILS_ARGMAX) {
+        f32x4 c[4];
+#pragma unroll
+        for (uint32_t u = 0; u < 4; ++u)
+            if (j0 + u * FILS_ARGMAX < n4) c[u] = v4[j0 + u * FILS_ARGMAX];
+#pragma unroll
+        for (uint32_t u = 0; u < 4; ++u) {
+            const uint32_t j = j0 + u * FILS_ARGMAX;
+            if (j < n4) {
+                const uint32_t i = tete + 4u * j;
+                voir(c[u].x, i);
+                voir(c[u].y, i + 1u);
+                voir(c[u].z, i + 2u);
+                voir(c[u].w, i + 3u);
+            }
+        }
     }
+    for (uint32_t i = tete + 4u * n4 + t; i < n; i += FILS_ARGMAX) voir(v[i], i);
     pv[t] = bv;
     pi[t] = bi;
     __syncthreads();
