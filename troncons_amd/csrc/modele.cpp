@@ -16,6 +16,7 @@
 
 #include "../../include/troncons_hip.h"
 #include "erreurs.hpp"
+#include "passe.hpp"
 
 struct trc_modele {
     trc_hyper h;
@@ -139,6 +140,8 @@ extern "C" int trc_modele_enchasser(trc_modele* m, uint32_t jeton, void* flux) {
 }
 
 // Modele::debut_couche up to the post-attention norm (lib.rs:498-521), then the fused MoE half.
+// The norm and the three projections, the rotation and the KV write, the output projection and
+// the residual add each go out as one launch, with the values of the separate kernels.
 extern "C" int trc_modele_couche(trc_modele* m, uint32_t l, uint32_t position, void* flux) {
     if (m == nullptr) return trc::usage("modele nul");
     const trc_hyper& h = m->h;
@@ -152,12 +155,12 @@ extern "C" int trc_modele_couche(trc_modele* m, uint32_t l, uint32_t position, v
         r = (appel);              \
         if (r != TRC_OK) return r; \
     } while (0)
-    TRC_ETAPE(trc_rmsnorm(m->x, c.attn_norm, m->hh, d, 1, h.eps, flux));
-    TRC_ETAPE(trc_gemv_q8_0(c.wq, m->hh, c.bq, m->q, dq, d, flux));
-    TRC_ETAPE(trc_gemv_q8_0(c.wk, m->hh, c.bk, m->k, dkv, d, flux));
-    TRC_ETAPE(trc_gemv_q8_0(c.wv, m->hh, c.bv, m->v, dkv, d, flux));
-    TRC_ETAPE(trc_rope_yarn(m->q, m->k, h.tetes, h.tetes_kv, position, &h.rope, flux));
-    TRC_ETAPE(trc_ecrire_kv(m->k, m->v, c.cache_k, c.cache_v, dkv, an ? position % an : position, flux));
+    // rmsnorm + the q, k, v GEMVs in one launch; then rope_yarn + ecrire_kv in one
+    const trc_vue w[3] = {c.wq, c.wk, c.wv}, b[3] = {c.bq, c.bk, c.bv}, y[3] = {m->q, m->k, m->v};
+    const uint32_t lignes[3] = {dq, dkv, dkv};
+    TRC_ETAPE(trc::lancer_qkv_q8_0(m->x, c.attn_norm, h.eps, d, w, b, y, lignes, flux));
+    TRC_ETAPE(trc::lancer_rope_yarn_kv(m->q, m->k, m->v, c.cache_k, c.cache_v, h.tetes, h.tetes_kv, position,
+                                       an ? position % an : position, &h.rope, flux));
     trc_params_attention pa;
     pa.tetes = h.tetes;
     pa.tetes_kv = h.tetes_kv;
@@ -168,8 +171,8 @@ extern "C" int trc_modele_couche(trc_modele* m, uint32_t l, uint32_t position, v
     pa.echelle = 0.125f;
     pa.reserve = 0;
     TRC_ETAPE(trc_attention(m->q, c.cache_k, c.cache_v, c.puits, m->a, &pa, flux));
-    TRC_ETAPE(trc_gemv_q8_0(c.wo, m->a, c.bo, m->o, d, dq, flux));
-    TRC_ETAPE(trc_combiner(m->x, m->o, d, trc_vue{0, 0}, 1, d, flux));
+    // the output projection adds itself into the residual (gemv_q8_0 + combiner)
+    TRC_ETAPE(trc::lancer_gemv_q8_0_residu(c.wo, m->a, c.bo, m->x, d, dq, flux));
     TRC_ETAPE(trc_rmsnorm(m->x, c.post_norm, m->h2, d, 1, h.eps, flux));
     TRC_ETAPE(trc_couche_moe_fusionnee(c.repertoire, h.experts, c.luts, &h.dims, c.routeur, c.routeur_biais, m->h2,
                                        h.actifs, m->x, m->idx, m->pw, m->controle, m->moe, h.n_delta, h.n_codes, flux));

@@ -14,6 +14,7 @@
 
 #include "commun.hpp"
 #include "erreurs.hpp"
+#include "passe.hpp"
 
 namespace trc {
 
@@ -22,6 +23,15 @@ constexpr uint32_t FILS_PASSE = 256;
 constexpr uint32_t FILS_ARGMAX = 1024;
 constexpr uint32_t ATTENTION_DIM = 64;
 constexpr uint32_t ATTENTION_POSITIONS_MAX = TRC_ATTENTION_POSITIONS_MAX;
+constexpr uint32_t QKV_COLONNES_MAX = 16384;  // the normed row lives in LDS (64 KiB)
+
+// The three projections of qkv_q8_0 (q, k, v in that order).
+struct Q8Projections {
+    const uint8_t* w[3];
+    const float* biais[3];
+    float* y[3];
+    uint32_t lignes[3];
+};
 
 __device__ __forceinline__ float f16_vers_f32(uint32_t bits) {
     return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits)));
@@ -35,20 +45,26 @@ __device__ __forceinline__ bool meilleur(float va, uint32_t ia, float vb, uint32
     return va > vb || (va == vb && ia < ib);
 }
 
-// Fixed tree over FILS_PASSE values in LDS (max or sum); every thread gets the result.
+// Fixed tree over FILS_PASSE values (max or sum; level k: value t op= value t + k for t < k,
+// k = 128 .. 1): levels 128 and 64 in LDS, levels 32 .. 1 as shuffles in wave 0 (lane t takes lane
+// t + k, the same association). part holds FILS_PASSE + 1 floats; every thread gets the result.
 template <bool MAX>
 __device__ __forceinline__ float reduire_bloc(float* part, float v) {
     const uint32_t t = threadIdx.x;
     part[t] = v;
     __syncthreads();
+    if (t < 64u) {
+        float a = MAX ? fmaxf(fmaxf(part[t], part[t + 128u]), fmaxf(part[t + 64u], part[t + 192u]))
+                      : (part[t] + part[t + 128u]) + (part[t + 64u] + part[t + 192u]);
 #pragma unroll
-    for (uint32_t k = FILS_PASSE / 2u; k > 0; k >>= 1) {
-        if (t < k) part[t] = MAX ? fmaxf(part[t], part[t + k]) : part[t] + part[t + k];
-        __syncthreads();
+        for (uint32_t k = 32; k > 0; k >>= 1) {
+            const float b = __shfl_down(a, k, 64);
+            a = MAX ? fmaxf(a, b) : a + b;
+        }
+        if (t == 0) part[FILS_PASSE] = a;
     }
-    const float r = part[0];
     __syncthreads();
-    return r;
+    return part[FILS_PASSE];
 }
 
 // YaRN inv_freq of pair i and the concentration, in f64 (passe.cuh:145-167).
@@ -76,23 +92,191 @@ __device__ inline double inv_freq_yarn(const trc_params_rope& p, uint32_t i, dou
 
 }  // namespace trc
 
-// y = W x (+ b), W Q8_0; half-wavefront w of the block takes rows 4w .. 4w + 3 of its 32; lane l
-// of the half takes blocks b = l, l + 32, ...; in a block s = sum of q_i x_i (one fmaf chain in
-// element order), then acc = fmaf(d, s, acc); butterfly over the half (passe.cuh:52-97, 213-222).
-// A block (34 bytes, even address) is read as the nine dwords of the 4-byte aligned window that
-// holds it (d at byte 0 or 2 of the window, the codes after it), realigned by a 64-bit shift; the
-// window's last dword may pass the block by 2 bytes, so the matrix's very last block reads it as
-// 16 bits.
+// y = W x (+ b), W Q8_0 (passe.cuh:52-97, 213-222): row r is taken by one half-wavefront, lane l
+// of which takes blocks b = l, l + 32, ...; in a block s = sum of q_i x_i (one fmaf chain in
+// element order), then acc = fmaf(d, s, acc) in increasing b; butterfly over the half. A
+// half-wavefront takes LIGNES consecutive rows (the reference's warp takes four; the result of a
+// row does not depend on it), and each lane issues the loads of DEPLI of its blocks before using
+// them. A block (34 bytes, even address) is read as the 4-byte aligned window that holds it
+// (d at byte 0 or 2 of the window, the codes after it): eight dwords and two halves, realigned by a
+// 64-bit shift. With `residu`, row r adds its y value into residu[r] (residu[r] + y_r, the
+// unweighted combine of one output) instead of storing y. x may be in LDS or global memory.
+namespace trc {
+template <uint32_t LIGNES, uint32_t DEPLI>
+__device__ __forceinline__ void gemv_q8_0_rangees(const uint8_t* __restrict__ W, const float* __restrict__ x,
+                                                  const float* __restrict__ biais, float* __restrict__ y,
+                                                  float* __restrict__ residu, uint32_t R, uint32_t C, uint32_t bloc) {
+    const uint32_t voie = threadIdx.x & 31u;
+    const uint32_t r0 = (bloc * (FILS_PASSE / 32u) + (threadIdx.x >> 5)) * LIGNES;
+    if (r0 >= R) return;
+    const uint32_t B = C / 32u;
+    const uint64_t octets_ligne = uint64_t(B) * Q8_OCTETS_BLOC;
+    const uintptr_t fin_matrice = reinterpret_cast<uintptr_t>(W) + uint64_t(R) * octets_ligne;
+    const f32x4* x4 = reinterpret_cast<const f32x4*>(x);
+    float acc[LIGNES];
+    uintptr_t lig[LIGNES];
+#pragma unroll
+    for (uint32_t i = 0; i < LIGNES; ++i) {
+        acc[i] = 0.0f;
+        lig[i] = reinterpret_cast<uintptr_t>(W) + uint64_t(min(r0 + i, R - 1u)) * octets_ligne;
+    }
+    for (uint32_t b0 = voie; b0 < B; b0 += 32u * DEPLI) {
+        uint32_t w[DEPLI][LIGNES][9];
+        uint32_t decal[DEPLI][LIGNES];
+#pragma unroll
+        for (uint32_t it = 0; it < DEPLI; ++it) {
+            // past the row's end the lane reads its last block again and leaves it unused
+            const uint32_t b = min(b0 + 32u * it, B - 1u);
+#pragma unroll
+            for (uint32_t i = 0; i < LIGNES; ++i) {
+                // absolute addresses: W is only 2-byte aligned; a window starting 2 bytes before W
+                // stays in W's 4-byte word, hence in its page
+                const uintptr_t a = lig[i] + uint64_t(b) * Q8_OCTETS_BLOC;
+                const uintptr_t a4 = a & ~uintptr_t(3);
+                decal[it][i] = uint32_t(a - a4);  // 0 or 2: where d starts in the window
+                const uint32_t* fen = reinterpret_cast<const uint32_t*>(a4);
+#pragma unroll
+                for (uint32_t t = 0; t < 8; ++t) w[it][i][t] = fen[t];
+                // dword 8 holds the last codes, read as two halves: the high one lies past the block
+                // when d sits at byte 0 and is then unused, so its address is clamped to the matrix
+                // (no branch around a load, so no load waits for another)
+                const uint16_t* h8 = reinterpret_cast<const uint16_t*>(fen + 8);
+                const uint16_t* h9 = reinterpret_cast<const uint16_t*>(min(a4 + 34u, fin_matrice - 2u));
+                w[it][i][8] = uint32_t(h8[0]) | (uint32_t(h9[0]) << 16);
+            }
+        }
+#pragma unroll
+        for (uint32_t it = 0; it < DEPLI; ++it) {
+            const uint32_t b = b0 + 32u * it;
+            if (b >= B) break;
+            float xv[32];
+#pragma unroll
+            for (uint32_t k = 0; k < 8; ++k) {
+                const f32x4 t = x4[b * 8u + k];
+                xv[4 * k] = t.x;
+                xv[4 * k + 1] = t.y;
+                xv[4 * k + 2] = t.z;
+                xv[4 * k + 3] = t.w;
+            }
+#pragma unroll
+            for (uint32_t i = 0; i < LIGNES; ++i) {
+                const uint32_t* wi = w[it][i];
+                const float d = f16_vers_f32(decal[it][i] ? (wi[0] >> 16) : (wi[0] & 0xFFFFu));
+                // the 32 codes start at byte 2 + decal of the window: realign dwords by 16 or 32 bits
+                const uint32_t bits = 8u * (2u + decal[it][i]);
+                float s = 0.0f;
+#pragma unroll
+                for (uint32_t t = 0; t < 8; ++t) {
+                    const uint64_t paire = (uint64_t(wi[t + 1]) << 32) | wi[t];
+                    const uint32_t q4 = uint32_t(paire >> bits);
+#pragma unroll
+                    for (uint32_t u = 0; u < 4; ++u)
+                        s = fmaf(float(int32_t(q4 << (24u - 8u * u)) >> 24), xv[4 * t + u], s);
+                }
+                acc[i] = fmaf(d, s, acc[i]);
+            }
+        }
+    }
+#pragma unroll
+    for (uint32_t i = 0; i < LIGNES; ++i) {
+        const float s = somme_demi_f32(acc[i]);
+        if (voie == 0 && r0 + i < R) {
+            const float v = biais != nullptr ? s + biais[r0 + i] : s;
+            if (residu != nullptr)
+                residu[r0 + i] = residu[r0 + i] + v;
+            else
+                y[r0 + i] = v;
+        }
+    }
+}
+
+// Rows of a launch per block.
+template <uint32_t LIGNES>
+constexpr uint32_t lignes_bloc() {
+    return FILS_PASSE / 32u * LIGNES;
+}
+
+// x (C floats, C a multiple of 32) copied into the block's LDS with 16-byte loads.
+__device__ __forceinline__ void x_vers_lds(const float* __restrict__ x, f32x4* xs, uint32_t C) {
+    const f32x4* x4 = reinterpret_cast<const f32x4*>(x);
+    for (uint32_t j = threadIdx.x; j < C / 4u; j += FILS_PASSE) xs[j] = x4[j];
+    __syncthreads();
+}
+
+// Sum of the block's 256 f64 values by the fixed tree (level k: value t += value t + k for t < k,
+// k = 128 .. 1): levels 128 and 64 in LDS, levels 32 .. 1 as shuffles in wave 0 (lane t adds lane
+// t + k, the same association). Every thread gets the sum.
+__device__ __forceinline__ double somme_arbre_f64(double* part, double* total, double v) {
+    const uint32_t t = threadIdx.x;
+    part[t] = v;
+    __syncthreads();
+    if (t < 64u) {
+        double u = (part[t] + part[t + 128u]) + (part[t + 64u] + part[t + 192u]);
+#pragma unroll
+        for (uint32_t k = 32; k > 0; k >>= 1) u += __shfl_down(u, k, 64);
+        if (t == 0) *total = u;
+    }
+    __syncthreads();
+    return *total;
+}
+
+// RMSNorm of one row of n: thread t adds x_i^2 for i = t, t + 256, ... (f64 fma), fixed tree,
+// r = 1/sqrt(sum/n + eps), y_i = (x_i r) w_i in f64, rounded once (passe.cuh:235-259). x is read
+// in full before the first write (y may be x). Up to NORME_PAR_FIL * 256 elements a thread holds
+// its x and w values in registers, so all its loads go out together.
+constexpr uint32_t NORME_PAR_FIL = 16;
+__device__ __forceinline__ void norme_ligne(const float* __restrict__ x, const float* __restrict__ w, float* y,
+                                            uint32_t n, float eps, double* part, double* total) {
+    const uint32_t t = threadIdx.x;
+    if (n <= NORME_PAR_FIL * FILS_PASSE) {
+        // indices clamped to the row (no branch around a load, so none waits for another); the
+        // copies past the row are not used
+        float xv[NORME_PAR_FIL], wv[NORME_PAR_FIL];
+#pragma unroll
+        for (uint32_t u = 0; u < NORME_PAR_FIL; ++u) {
+            const uint32_t i = min(t + u * FILS_PASSE, n - 1u);
+            xv[u] = x[i];
+            wv[u] = w[i];
+        }
+        double s = 0.0;
+#pragma unroll
+        for (uint32_t u = 0; u < NORME_PAR_FIL; ++u)
+            if (t + u * FILS_PASSE < n) s = fma(double(xv[u]), double(xv[u]), s);
+        const double r = 1.0 / sqrt(somme_arbre_f64(part, total, s) / double(n) + double(eps));
+#pragma unroll
+        for (uint32_t u = 0; u < NORME_PAR_FIL; ++u) {
+            const uint32_t i = t + u * FILS_PASSE;
+            if (i < n) y[i] = float(double(xv[u]) * r * double(wv[u]));
+        }
+        return;
+    }
+    double s = 0.0;
+    for (uint32_t i = t; i < n; i += FILS_PASSE) {
+        const double v = x[i];
+        s = fma(v, v, s);
+    }
+    const double r = 1.0 / sqrt(somme_arbre_f64(part, total, s) / double(n) + double(eps));
+    for (uint32_t i = t; i < n; i += FILS_PASSE) y[i] = float(double(x[i]) * r * double(w[i]));
+}
+}  // namespace trc
+
+// One launch of y = W x (+ b). gemv_q8_0: four rows per half-wavefront, x read from global memory
+// (large matrices: the output head streams its weights with many waves resident);
+// gemv_q8_0_court: one row per half-wavefront, x staged in LDS when it fits (C <= QKV_COLONNES_MAX)
+// and four of a lane's blocks' loads in flight (small matrices, where a launch has few blocks and
+// each wave's chain of loads sets the time).
 extern "C" __global__ void __launch_bounds__(trc::FILS_PASSE)
 gemv_q8_0(const uint8_t* __restrict__ W, const float* __restrict__ x, const float* __restrict__ biais,
-          float* __restrict__ y, uint32_t R, uint32_t C) {
+          float* __restrict__ y, float* __restrict__ residu, uint32_t R, uint32_t C) {
     using namespace trc;
+    // the same rows, blocks and operation order as gemv_q8_0_rangees, with each row's window
+    // loaded right before its use (fewer registers, more waves resident to stream the matrix)
     const uint32_t voie = threadIdx.x & 31u;
     const uint32_t r0 = (blockIdx.x * (FILS_PASSE / 32u) + (threadIdx.x >> 5)) * 4u;
     if (r0 >= R) return;
     const uint32_t B = C / 32u;
     const uint64_t octets_ligne = uint64_t(B) * Q8_OCTETS_BLOC;
-    const uint64_t octets_matrice = uint64_t(R) * octets_ligne;
+    const uintptr_t fin_matrice = reinterpret_cast<uintptr_t>(W) + uint64_t(R) * octets_ligne;
     const f32x4* x4 = reinterpret_cast<const f32x4*>(x);
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     uint32_t lig[4];
@@ -110,22 +294,17 @@ gemv_q8_0(const uint8_t* __restrict__ W, const float* __restrict__ x, const floa
         }
 #pragma unroll
         for (uint32_t i = 0; i < 4; ++i) {
-            // absolute addresses: W is only 2-byte aligned; a window starting 2 bytes before W stays
-            // in W's 4-byte word, hence in its page
             const uintptr_t a = reinterpret_cast<uintptr_t>(W) + uint64_t(lig[i]) * octets_ligne +
                                 uint64_t(b) * Q8_OCTETS_BLOC;
             const uintptr_t a4 = a & ~uintptr_t(3);
-            const uint32_t decal = uint32_t(a - a4);  // 0 or 2: where d starts in the window
+            const uint32_t decal = uint32_t(a - a4);
             const uint32_t* fen = reinterpret_cast<const uint32_t*>(a4);
             uint32_t w[9];
 #pragma unroll
             for (uint32_t t = 0; t < 8; ++t) w[t] = fen[t];
-            // dword 8 holds the last codes; past the block by 2 bytes when d sits at byte 0
-            w[8] = a4 + 36u <= reinterpret_cast<uintptr_t>(W) + octets_matrice
-                       ? fen[8]
-                       : uint32_t(reinterpret_cast<const uint16_t*>(fen + 8)[0]);
+            // past the block by 2 bytes when d sits at byte 0: the matrix's last block reads 16 bits
+            w[8] = a4 + 36u <= fin_matrice ? fen[8] : uint32_t(reinterpret_cast<const uint16_t*>(fen + 8)[0]);
             const float d = f16_vers_f32(decal ? (w[0] >> 16) : (w[0] & 0xFFFFu));
-            // the 32 codes start at byte 2 + decal of the window: realign dwords by 16 or 32 bits
             const uint32_t bits = 8u * (2u + decal);
             float s = 0.0f;
 #pragma unroll
@@ -142,8 +321,51 @@ gemv_q8_0(const uint8_t* __restrict__ W, const float* __restrict__ x, const floa
 #pragma unroll
     for (uint32_t i = 0; i < 4; ++i) {
         const float s = somme_demi_f32(acc[i]);
-        if (voie == 0 && r0 + i < R) y[r0 + i] = biais != nullptr ? s + biais[r0 + i] : s;
+        if (voie == 0 && r0 + i < R) {
+            const float v = biais != nullptr ? s + biais[r0 + i] : s;
+            if (residu != nullptr)
+                residu[r0 + i] = residu[r0 + i] + v;
+            else
+                y[r0 + i] = v;
+        }
     }
+}
+
+extern "C" __global__ void __launch_bounds__(trc::FILS_PASSE)
+gemv_q8_0_court(const uint8_t* __restrict__ W, const float* __restrict__ x, const float* __restrict__ biais,
+                float* __restrict__ y, float* __restrict__ residu, uint32_t R, uint32_t C) {
+    using namespace trc;
+    extern __shared__ f32x4 xs[];
+    if (C <= QKV_COLONNES_MAX) {
+        x_vers_lds(x, xs, C);
+        gemv_q8_0_rangees<1, 4>(W, reinterpret_cast<const float*>(xs), biais, y, residu, R, C, blockIdx.x);
+    } else {
+        gemv_q8_0_rangees<1, 4>(W, x, biais, y, residu, R, C, blockIdx.x);
+    }
+}
+
+// The attention projections of one layer in one launch: each block takes the RMSNorm of x with
+// `norme` into LDS (the same values as rmsnorm), then its rows of q, k or v (blocks in that order),
+// one row per half-wavefront as in gemv_q8_0_court.
+extern "C" __global__ void __launch_bounds__(trc::FILS_PASSE)
+qkv_q8_0(const float* __restrict__ x, const float* __restrict__ norme, float eps, uint32_t C, trc::Q8Projections m) {
+    using namespace trc;
+    extern __shared__ f32x4 hh4[];
+    __shared__ double part[FILS_PASSE];
+    __shared__ double total;
+    float* hh = reinterpret_cast<float*>(hh4);
+    norme_ligne(x, norme, hh, C, eps, part, &total);
+    __syncthreads();
+    uint32_t bloc = blockIdx.x, j = 0;
+#pragma unroll
+    for (uint32_t u = 0; u < 2; ++u) {
+        const uint32_t nb = (m.lignes[j] + lignes_bloc<1>() - 1u) / lignes_bloc<1>();
+        if (bloc >= nb) {
+            bloc -= nb;
+            ++j;
+        }
+    }
+    gemv_q8_0_rangees<1, 4>(m.w[j], hh, m.biais[j], m.y[j], nullptr, m.lignes[j], C, bloc);
 }
 
 // Row `ligne` of a Q8_0 matrix -> f32, exact (d has 11 significant bits, q 7: passe.cuh:627-637).
@@ -157,52 +379,68 @@ ligne_q8_0(const uint8_t* __restrict__ W, uint32_t ligne, uint32_t C, float* __r
     y[i] = d * float(int8_t(b[2 + (i & 31u)]));
 }
 
-// RMSNorm of one row per block: thread t adds x_i^2 for i = t, t + 256, ... (f64 fma), fixed tree,
-// r = 1/sqrt(sum/n + eps), y_i = (x_i r) w_i in f64, rounded once (passe.cuh:235-259). x is read
-// in full before the first write (y may be x).
+// RMSNorm of one row per block (passe.cuh:235-259; the arithmetic is norme_ligne's).
 extern "C" __global__ void __launch_bounds__(trc::FILS_PASSE)
 rmsnorm(const float* __restrict__ x, const float* __restrict__ w, float* y, uint32_t n, float eps) {
     __shared__ double part[trc::FILS_PASSE];
-    const uint32_t t = threadIdx.x;
-    const float* xr = x + uint64_t(blockIdx.x) * n;
-    float* yr = y + uint64_t(blockIdx.x) * n;
-    double s = 0.0;
-    for (uint32_t i = t; i < n; i += trc::FILS_PASSE) {
-        const double v = xr[i];
-        s = fma(v, v, s);
-    }
-    part[t] = s;
-    __syncthreads();
-#pragma unroll
-    for (uint32_t k = trc::FILS_PASSE / 2u; k > 0; k >>= 1) {
-        if (t < k) part[t] += part[t + k];
-        __syncthreads();
-    }
-    const double r = 1.0 / sqrt(part[0] / double(n) + double(eps));
-    for (uint32_t i = t; i < n; i += trc::FILS_PASSE) yr[i] = float(double(xr[i]) * r * double(w[i]));
+    __shared__ double total;
+    trc::norme_ligne(x + uint64_t(blockIdx.x) * n, w, y + uint64_t(blockIdx.x) * n, n, eps, part, &total);
 }
 
-// YaRN rotation (NEOX halves) of one head per block, in place: pair i < d/2 of the head,
-// o1 = x1 c - x2 s, o2 = x2 c + x1 s, c and s the cosine and sine of position * inv_freq_i times the
-// concentration, all in f64 (passe.cuh:261-284). Heads 0 .. tetes_q - 1 are q's, then k's.
-extern "C" __global__ void __launch_bounds__(64)
-rope_yarn(float* __restrict__ q, float* __restrict__ k, uint32_t tetes_q, uint32_t tetes_k, uint32_t position,
-          trc_params_rope p) {
-    using namespace trc;
+namespace trc {
+// YaRN rotation (NEOX halves) of pair i < d/2 of head xh, in place: o1 = x1 c - x2 s,
+// o2 = x2 c + x1 s, c and s the cosine and sine of position * inv_freq_i times the concentration,
+// all in f64 (passe.cuh:261-284).
+__device__ __forceinline__ void tourner_paire(float* xh, uint32_t i, uint32_t position, const trc_params_rope& p,
+                                              float& o1, float& o2) {
     const uint32_t demi = p.dim_tete / 2u;
-    const uint32_t i = threadIdx.x;
-    if (i >= demi || blockIdx.x >= tetes_q + tetes_k) return;
     double m;
     const double inv = inv_freq_yarn(p, i, m);
     double s, c;
     sincos(double(position) * inv, &s, &c);
     c *= m;
     s *= m;
+    const double a = xh[i], b = xh[i + demi];
+    o1 = float(a * c - b * s);
+    o2 = float(b * c + a * s);
+    xh[i] = o1;
+    xh[i + demi] = o2;
+}
+}  // namespace trc
+
+// YaRN rotation of one head per block, in place; heads 0 .. tetes_q - 1 are q's, then k's.
+extern "C" __global__ void __launch_bounds__(64)
+rope_yarn(float* __restrict__ q, float* __restrict__ k, uint32_t tetes_q, uint32_t tetes_k, uint32_t position,
+          trc_params_rope p) {
+    const uint32_t i = threadIdx.x;
+    if (i >= p.dim_tete / 2u || blockIdx.x >= tetes_q + tetes_k) return;
     float* xh = blockIdx.x < tetes_q ? q + uint64_t(blockIdx.x) * p.dim_tete
                                      : k + uint64_t(blockIdx.x - tetes_q) * p.dim_tete;
-    const double a = xh[i], b = xh[i + demi];
-    xh[i] = float(a * c - b * s);
-    xh[i + demi] = float(b * c + a * s);
+    float o1, o2;
+    trc::tourner_paire(xh, i, position, p, o1, o2);
+}
+
+// rope_yarn then ecrire_kv in one launch (head dimension at most 64): the block of k head j also
+// writes that head's rotated k and v's head j, rounded to f16, into slot case_kv of the caches.
+extern "C" __global__ void __launch_bounds__(64)
+rope_yarn_kv(float* __restrict__ q, float* __restrict__ k, const float* __restrict__ v,
+             uint16_t* __restrict__ cache_k, uint16_t* __restrict__ cache_v, uint32_t tetes_q, uint32_t tetes_k,
+             uint32_t position, uint32_t case_kv, trc_params_rope p) {
+    const uint32_t i = threadIdx.x, dt = p.dim_tete, demi = dt / 2u;
+    if (blockIdx.x >= tetes_q + tetes_k) return;
+    const bool cle = blockIdx.x >= tetes_q;
+    const uint32_t j = cle ? blockIdx.x - tetes_q : blockIdx.x;
+    float* xh = (cle ? k : q) + uint64_t(j) * dt;
+    const uint64_t base = (uint64_t(case_kv) * tetes_k + j) * dt;
+    if (i < demi) {
+        float o1, o2;
+        trc::tourner_paire(xh, i, position, p, o1, o2);
+        if (cle) {
+            cache_k[base + i] = trc::f32_vers_f16(o1);
+            cache_k[base + i + demi] = trc::f32_vers_f16(o2);
+        }
+    }
+    if (cle && i < dt) cache_v[base + i] = trc::f32_vers_f16(v[uint64_t(j) * dt + i]);
 }
 
 // k and v rounded to f16 (nearest even) into slot case_kv of the caches (passe.cuh:286-296).
@@ -227,7 +465,7 @@ attention(const float* __restrict__ q, const uint16_t* __restrict__ cache_k, con
     using namespace trc;
     extern __shared__ float scores[];
     __shared__ float qs[ATTENTION_DIM];
-    __shared__ float part[FILS_PASSE];
+    __shared__ float part[FILS_PASSE + 1];
     __shared__ float groupes[4][ATTENTION_DIM];
     const uint32_t t = threadIdx.x;
     const uint32_t h = blockIdx.x;
@@ -267,13 +505,23 @@ attention(const float* __restrict__ q, const uint16_t* __restrict__ cache_k, con
     }
     z = reduire_bloc<false>(part, z) + expf(puits_h - m);
 
+    // the value loads of eight positions go out together (positions clamped to the last one, so no
+    // branch stands around a load; the copies past it are unused); the chain keeps j = g, g + 4, ...
     const uint32_t dd = t & (ATTENTION_DIM - 1u);
     const uint32_t g = t / ATTENTION_DIM;  // 0..3
     float a = 0.0f;
-    for (uint32_t j = g; j < n; j += 4u) {
-        const uint32_t pos = p.debut + j;
-        const uint32_t c = p.anneau ? pos % p.anneau : pos;
-        a = fmaf(scores[j], f16_vers_f32(cache_v[uint64_t(c) * dkv + uint64_t(hk) * ATTENTION_DIM + dd]), a);
+    constexpr uint32_t LOT = 8;
+    for (uint32_t j0 = g; j0 < n; j0 += 4u * LOT) {
+        uint16_t vv[LOT];
+#pragma unroll
+        for (uint32_t u = 0; u < LOT; ++u) {
+            const uint32_t pos = p.debut + min(j0 + 4u * u, n - 1u);
+            const uint32_t c = p.anneau ? pos % p.anneau : pos;
+            vv[u] = cache_v[uint64_t(c) * dkv + uint64_t(hk) * ATTENTION_DIM + dd];
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < LOT; ++u)
+            if (j0 + 4u * u < n) a = fmaf(scores[j0 + 4u * u], f16_vers_f32(vv[u]), a);
     }
     groupes[g][dd] = a;
     __syncthreads();
@@ -337,6 +585,23 @@ argmax(const float* __restrict__ v, uint32_t n, uint32_t* __restrict__ sortie) {
 // ============================================================================ C-ABI launch layer
 namespace {
 inline hipStream_t flux_de(void* f) { return reinterpret_cast<hipStream_t>(f); }
+
+// Below this many rows a GEMV takes one row per half-wavefront (more waves, shorter load chains).
+constexpr uint32_t GEMV_COURT_LIGNES = 32768;
+
+void lancer_gemv(const uint8_t* W, const float* x, const float* biais, float* y, float* residu, uint32_t R, uint32_t C,
+                 hipStream_t f) {
+    if (R < GEMV_COURT_LIGNES) {
+        const size_t lds = C <= trc::QKV_COLONNES_MAX ? 4u * size_t(C) : 0u;
+        constexpr uint32_t rb = trc::lignes_bloc<1>();
+        hipLaunchKernelGGL(gemv_q8_0_court, dim3((R + rb - 1) / rb), dim3(trc::FILS_PASSE), lds, f, W, x, biais, y,
+                           residu, R, C);
+    } else {
+        constexpr uint32_t rb = trc::lignes_bloc<4>();
+        hipLaunchKernelGGL(gemv_q8_0, dim3((R + rb - 1) / rb), dim3(trc::FILS_PASSE), 0, f, W, x, biais, y, residu, R,
+                           C);
+    }
+}
 }  // namespace
 
 extern "C" int trc_gemv_q8_0(trc_vue w, trc_vue x, trc_vue biais, trc_vue y, uint32_t lignes, uint32_t colonnes,
@@ -350,10 +615,9 @@ extern "C" int trc_gemv_q8_0(trc_vue w, trc_vue x, trc_vue biais, trc_vue y, uin
                  "x trop court ou non aligne sur 16");
     TRC_VERIFIER(y.adresse != 0 && y.octets >= 4ull * lignes, "y trop court");
     TRC_VERIFIER(biais.adresse == 0 || biais.octets >= 4ull * lignes, "biais trop court");
-    hipLaunchKernelGGL(gemv_q8_0, dim3((lignes + 31) / 32), dim3(trc::FILS_PASSE), 0, flux_de(flux),
-                       reinterpret_cast<const uint8_t*>(w.adresse), reinterpret_cast<const float*>(x.adresse),
-                       reinterpret_cast<const float*>(biais.adresse), reinterpret_cast<float*>(y.adresse), lignes,
-                       colonnes);
+    lancer_gemv(reinterpret_cast<const uint8_t*>(w.adresse), reinterpret_cast<const float*>(x.adresse),
+                reinterpret_cast<const float*>(biais.adresse), reinterpret_cast<float*>(y.adresse), nullptr, lignes,
+                colonnes, flux_de(flux));
     return trc::apres_lancement("gemv_q8_0");
 }
 
@@ -442,3 +706,69 @@ extern "C" int trc_argmax(trc_vue v, uint32_t n, trc_vue sortie, void* flux) {
                        reinterpret_cast<const float*>(v.adresse), n, reinterpret_cast<uint32_t*>(sortie.adresse));
     return trc::apres_lancement("argmax");
 }
+
+// ============================================================================ fused launches of the native driver
+// No reference counterpart: the decode-step driver issues these in place of rmsnorm + three
+// gemv_q8_0, rope_yarn + ecrire_kv and gemv_q8_0 + combiner; the values are the same.
+namespace trc {
+
+int lancer_qkv_q8_0(trc_vue x, trc_vue norme, float eps, uint32_t colonnes, const trc_vue w[3],
+                    const trc_vue biais[3], const trc_vue y[3], const uint32_t lignes[3], void* flux) {
+    TRC_VERIFIER(colonnes > 0 && colonnes % 32 == 0 && colonnes <= QKV_COLONNES_MAX, "qkv : %u colonnes", colonnes);
+    TRC_VERIFIER(x.adresse && norme.adresse && x.octets >= 4ull * colonnes && norme.octets >= 4ull * colonnes,
+                 "qkv : x ou norme trop court");
+    Q8Projections m;
+    uint32_t blocs = 0;
+    for (int j = 0; j < 3; ++j) {
+        const uint64_t octets = uint64_t(lignes[j]) * (colonnes / 32) * Q8_OCTETS_BLOC;
+        TRC_VERIFIER(lignes[j] > 0 && w[j].adresse && w[j].octets >= octets && w[j].adresse % 2 == 0,
+                     "qkv : matrice %d", j);
+        TRC_VERIFIER(y[j].adresse && y[j].octets >= 4ull * lignes[j], "qkv : sortie %d trop courte", j);
+        TRC_VERIFIER(biais[j].adresse == 0 || biais[j].octets >= 4ull * lignes[j], "qkv : biais %d trop court", j);
+        m.w[j] = reinterpret_cast<const uint8_t*>(w[j].adresse);
+        m.biais[j] = reinterpret_cast<const float*>(biais[j].adresse);
+        m.y[j] = reinterpret_cast<float*>(y[j].adresse);
+        m.lignes[j] = lignes[j];
+        blocs += (lignes[j] + lignes_bloc<1>() - 1) / lignes_bloc<1>();
+    }
+    hipLaunchKernelGGL(qkv_q8_0, dim3(blocs), dim3(FILS_PASSE), 4u * colonnes, flux_de(flux),
+                       reinterpret_cast<const float*>(x.adresse), reinterpret_cast<const float*>(norme.adresse), eps,
+                       colonnes, m);
+    return apres_lancement("qkv_q8_0");
+}
+
+int lancer_rope_yarn_kv(trc_vue q, trc_vue k, trc_vue v, trc_vue cache_k, trc_vue cache_v, uint32_t tetes_q,
+                        uint32_t tetes_k, uint32_t position, uint32_t case_kv, const trc_params_rope* p, void* flux) {
+    TRC_VERIFIER(p && p->dim_tete > 0 && p->dim_tete % 2 == 0 && p->dim_tete <= 64 && p->variante <= 1,
+                 "rope_kv : parametres");
+    TRC_VERIFIER(tetes_q > 0 && tetes_k > 0, "rope_kv : tetes %u / %u", tetes_q, tetes_k);
+    const uint64_t dq = uint64_t(tetes_q) * p->dim_tete, dkv = uint64_t(tetes_k) * p->dim_tete;
+    const uint64_t fin = 2ull * (uint64_t(case_kv) + 1) * dkv;
+    TRC_VERIFIER(q.adresse && k.adresse && v.adresse && q.octets >= 4 * dq && k.octets >= 4 * dkv &&
+                     v.octets >= 4 * dkv,
+                 "rope_kv : q, k ou v trop court");
+    TRC_VERIFIER(cache_k.adresse && cache_v.adresse && cache_k.octets >= fin && cache_v.octets >= fin,
+                 "rope_kv : case %u hors du cache", case_kv);
+    hipLaunchKernelGGL(rope_yarn_kv, dim3(tetes_q + tetes_k), dim3(64), 0, flux_de(flux),
+                       reinterpret_cast<float*>(q.adresse), reinterpret_cast<float*>(k.adresse),
+                       reinterpret_cast<const float*>(v.adresse), reinterpret_cast<uint16_t*>(cache_k.adresse),
+                       reinterpret_cast<uint16_t*>(cache_v.adresse), tetes_q, tetes_k, position, case_kv, *p);
+    return apres_lancement("rope_yarn_kv");
+}
+
+int lancer_gemv_q8_0_residu(trc_vue w, trc_vue x, trc_vue biais, trc_vue residu, uint32_t lignes, uint32_t colonnes,
+                            void* flux) {
+    TRC_VERIFIER(lignes > 0 && colonnes > 0 && colonnes % 32 == 0, "forme %u x %u", lignes, colonnes);
+    const uint64_t octets = uint64_t(lignes) * (colonnes / 32) * Q8_OCTETS_BLOC;
+    TRC_VERIFIER(w.adresse != 0 && w.octets >= octets && w.adresse % 2 == 0, "matrice Q8_0 trop courte");
+    TRC_VERIFIER(x.adresse != 0 && x.octets >= 4ull * colonnes && x.adresse % 16 == 0,
+                 "x trop court ou non aligne sur 16");
+    TRC_VERIFIER(residu.adresse != 0 && residu.octets >= 4ull * lignes, "residu trop court");
+    TRC_VERIFIER(biais.adresse == 0 || biais.octets >= 4ull * lignes, "biais trop court");
+    lancer_gemv(reinterpret_cast<const uint8_t*>(w.adresse), reinterpret_cast<const float*>(x.adresse),
+                reinterpret_cast<const float*>(biais.adresse), nullptr, reinterpret_cast<float*>(residu.adresse), lignes,
+                colonnes, flux_de(flux));
+    return apres_lancement("gemv_q8_0");
+}
+
+}  // namespace trc
