@@ -509,7 +509,8 @@ def bench_ordo(args, E, k, C, dims, dev, n_fils):
     fichier, info_fichier = ouvrir_fichier(args, E, k, dims, L, n_fils)
     n_empl = args.emplacements or L * E
     t0 = time.perf_counter()
-    o = Ordonnanceur(fichier, emplacements=n_empl, tiedes=args.tiedes, verifier=args.verifier)
+    o = Ordonnanceur(fichier, emplacements=n_empl, tiedes=args.tiedes, verifier=args.verifier,
+                     prechargement=args.prechargement)
     t_creer = time.perf_counter() - t0
     n_tok = args.warmup + args.steps
     x_tok = np.stack([codeur.synth_normale_bf16(args.graine, 4, t, C, 1.0) for t in range(n_tok)])
@@ -549,12 +550,15 @@ def bench_ordo(args, E, k, C, dims, dev, n_fils):
                                f"{n_empl} decoded-expert slots in HBM ({n_empl * 13.254144e-3:.1f} GB), "
                                f"{args.tiedes} pinned warm entries, LRU", "layers": L, "experts": E, "k": k,
                    "slots": n_empl, "warm_entries": args.tiedes, "n_codes": args.n_codes, "n_delta": args.n_delta,
-                   "verify_reads": bool(args.verifier)},
+                   "verify_reads": bool(args.verifier), "prefetch": bool(args.prechargement)},
         "hit_rate_vram": round((c1.succes_vram - c0.succes_vram) / acces, 4),
         "hit_rate_ram": round((c1.succes_ram - c0.succes_ram) / acces, 4),
         "disk_misses_per_token": round((c1.defauts_disque - c0.defauts_disque) / n, 3),
         "bytes_read_per_token": int((s1.octets_lus - s0.octets_lus) / n),
         "bytes_copied_per_token": int((s1.octets_copies - s0.octets_copies) / n),
+        "prefetch_per_token": {"issued": round((s1.pf_emis - s0.pf_emis) / n, 3),
+                               "useful": round((s1.pf_utiles - s0.pf_utiles) / n, 3),
+                               "bytes": int((s1.pf_octets - s0.pf_octets) / n)},
         "host_us_per_layer": {"router_wait": round((s1.us_attente_routeur - s0.us_attente_routeur) / (n * L), 2),
                               "reads_and_sends": round((s1.us_lectures - s0.us_lectures) / (n * L), 2),
                               "issue": round((s1.us_emission - s0.us_emission) / (n * L), 2)},
@@ -680,6 +684,9 @@ def main():
     ap.add_argument("--emplacements", type=int, default=0, help="--ordo: decoded-expert slots in HBM (0: all)")
     ap.add_argument("--tiedes", type=int, default=0, help="--ordo: pinned warm-RAM entries of coded parts")
     ap.add_argument("--verifier", action="store_true", help="--ordo: check every part read against its fingerprint")
+    ap.add_argument("--prechargement", action="store_true",
+                    help="--ordo: each layer predicts the next layer's experts (its router over the normed residual) "
+                         "and reads their parts ahead")
     ap.add_argument("--experts", type=int, default=128)
     ap.add_argument("--k", type=int, default=4)
     ap.add_argument("--n-codes", type=int, default=16, help="macro-steps per CODES_CTX tile written by the encoder")

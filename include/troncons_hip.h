@@ -616,6 +616,13 @@ typedef struct {
     int politique;         /* TRC_POLITIQUE_LRU or TRC_POLITIQUE_FIFO */
     int verifier;          /* check each part read against its directory fingerprint */
     uint32_t lecteurs;     /* reader threads (0: k) */
+    int prechargement;     /* prefetch (Config::prechargement, trc-ordo/src/lib.rs:77,1104-1215): per
+                            * layer l, layer l+1's router over the residual normed with l+1's
+                            * post-attention norm (blk.N.post_attention_norm.weight if the file holds it,
+                            * else unit weights; eps 1e-5) predicts its top-k; the predicted parts that
+                            * are neither in VRAM nor in warm RAM are read into pinned prefetch buffers
+                            * behind layer l's own reads, and a disk miss of layer l+1 without a warm
+                            * entry takes its bytes from there */
 } trc_config_ordo;
 
 /* CompteursMoteur (trc-ordo/src/lib.rs:586-594), the expert path's share */
@@ -628,6 +635,9 @@ typedef struct {
     double us_attente_routeur; /* host time waiting for the router's event */
     double us_lectures;        /* host time from submitting the reads to the last part sent */
     double us_emission;        /* host time issuing the router and the layer's MLPs */
+    uint64_t pf_emis;          /* prefetch reads issued (counted in lectures and octets_lus too) */
+    uint64_t pf_utiles;        /* disk misses served from a prefetch buffer (no read of their own) */
+    uint64_t pf_octets;        /* bytes of the prefetch reads */
 } trc_stats_ordo;
 
 typedef struct trc_ordo trc_ordo;

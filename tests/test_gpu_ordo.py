@@ -190,3 +190,64 @@ def test_engine_gpt_oss_shape(tmp_path_factory):
     _run(m, o, xs[1:], verifier_residus=False)
     _temoins(m, o, 10, 4)
     o.detruire()
+
+
+@pytest.fixture(scope="module")
+def deux(tmp_path_factory):
+    d = DimsExpert.de([256, 256, 256], [256, 256, 256])
+    return Modele(tmp_path_factory.mktemp("ordo2") / "deux.trc", 2032, 2, 16, 4, d)
+
+
+def test_prefetch_reads_ahead_and_changes_no_result(deux):
+    """Config::prechargement (trc-ordo/src/lib.rs:1104-1215, trc-modele/src/lib.rs:570-579): layer 0
+    predicts layer 1's experts with layer 1's router over the residual normed with layer 1's
+    post-attention norm (unit weights: the file holds none), and the predicted parts are read ahead.
+    The router input x is taken as that same norm of the incoming residual, so the prediction is
+    layer 1's routing: every part read ahead serves a disk miss of layer 1 (on the first token, with
+    an empty cache, all k of them). Residuals are bit-identical with and without prefetch, the
+    cache counters equal each other and the simulator's replay, and every read is accounted for."""
+    from troncons_amd.noyaux import Noyaux
+    m = deux
+    D, C = m.dims.lignes[2], m.dims.colonnes[0]
+    n = Noyaux()
+    un = dev(np.ones(D, np.float32))
+    a = Ordonnanceur(m.f, emplacements=8, tiedes=0, verifier=True)
+    b = Ordonnanceur(m.f, emplacements=8, tiedes=0, verifier=True, prechargement=True)
+    for t in range(8):
+        print(f"token {t}", flush=True)
+        r0 = O.synth_normale_bf16(2033, 5, t, D, 3.0)
+        x = zeros(4 * C)
+        n.rmsnorm(dev(r0), un, x, D, 1, 1e-5)
+        ra, rb = dev(r0), dev(r0)
+        a.jeton(x, ra)
+        b.jeton(x, rb)
+        assert (hote(ra, np.uint32) == hote(rb, np.uint32)).all(), t
+        if t == 0:
+            assert b.stats().pf_utiles == b.stats().pf_emis == m.k
+    assert (a.trace() == b.trace()).all()
+    assert list(b.controle()) == [0, 0, 0, 0]
+    sa, sb = a.stats(), b.stats()
+    assert sa.pf_emis == sa.pf_utiles == sa.pf_octets == 0
+    ca, cb = a.compteurs(), b.compteurs()
+    assert ca.tuple() == cb.tuple()
+    # every read ahead was used: the same parts and bytes are read, layer 1's a layer earlier
+    assert sb.pf_utiles == sb.pf_emis > m.k
+    assert sb.lectures == cb.defauts_disque - sb.pf_utiles + sb.pf_emis == sa.lectures
+    assert sb.octets_lus == sa.octets_lus == ca.octets_disque and 0 < sb.pf_octets < sb.octets_lus
+    assert sb.octets_copies == sa.octets_copies and sb.decodages == sa.decodages
+    _temoins_cache(m, b, 8, 0)
+
+
+def _temoins_cache(m, o, emplacements, tiedes):
+    """The cache counters against the simulator's replay of the engine's trace, and the decoded
+    slots against the canonical fingerprints (reads are not compared: prefetch adds its own)."""
+    c = o.compteurs()
+    tr = o.trace()
+    sim = K.Cache(emplacements, tiedes)
+    sim.fixer_tailles(np.array([[m.f.entree(l, e).longueur[0] for e in range(m.E)] for l in range(m.L)], np.uint64))
+    assert c.tuple() == sim.rejouer_dans(K.Trace.de(m.E, tr)).tuple()
+    for l in range(m.L):
+        for e in range(m.E):
+            h = o.temoin(l, e)
+            if h is not None:
+                assert h == m.f.entree(l, e).empreinte_canonique, (l, e)

@@ -164,6 +164,25 @@ struct trc_ordo {
     uint64_t jeton = 0;
     trc_stats_ordo st{};
     std::vector<uint16_t> trace;
+    // prefetch (cfg.prechargement): two sets of k pinned buffers, set l % 2 for layer l's parts
+    struct Prechargement {
+        int32_t couche = -1;  // -1: empty
+        uint16_t expert = 0;
+        bool en_vol = false;       // its read has not landed
+        bool pris = false;         // a miss of its layer took it
+        int32_t attendu_par = -1;  // the miss waiting for its read to land
+        int statut = TRC_OK;
+        uint64_t octets = 0;
+        std::string message;
+    };
+    static constexpr uint32_t PF_JETON = 1u << 16;     // reader requests from here on are prefetches
+    static constexpr uint32_t BOITE_PREDICTION = 64;  // the prediction's mailbox, 256 bytes in
+    static constexpr float EPS_PREDICTION = 1e-5f;    // gpt-oss's RMSNorm epsilon
+    std::vector<Prechargement> pf;
+    uint8_t* pf_hote = nullptr;
+    float* normes = nullptr;  // L x D post-attention norm weights
+    float *h2p = nullptr, *logits_p = nullptr, *poids_p = nullptr;
+    uint32_t* idx_p = nullptr;
 
     ~trc_ordo() {
         lecteurs.reset();
@@ -172,12 +191,13 @@ struct trc_ordo {
         for (hipEvent_t e : ev_copie) (void)hipEventDestroy(e);
         if (ev_routeur) (void)hipEventDestroy(ev_routeur);
         if (copie) (void)hipStreamDestroy(copie);
-        void* dev[] = {emplacements, luts, routeurs, logits, idx, poids, g, u, a, sorties, descs, controle};
+        void* dev[] = {emplacements, luts, routeurs, logits, idx, poids, g, u, a, sorties, descs, controle,
+                       normes, h2p, logits_p, poids_p, idx_p};
         for (void* p : dev)
             if (p) (void)hipFree(p);
         for (uint8_t* p : arrivees)
             if (p) (void)hipFree(p);
-        void* hote[] = {tiedes, arrivees_hote, boite, descs_hote};
+        void* hote[] = {tiedes, arrivees_hote, boite, descs_hote, pf_hote};
         for (void* p : hote)
             if (p) (void)hipHostFree(p);
     }
@@ -239,6 +259,32 @@ struct trc_ordo {
             }
             TRC_HIP(hipMemcpy(routeurs + uint64_t(l) * E * C, rf.data(), rf.size() * 4, hipMemcpyHostToDevice));
         }
+        if (cfg.prechargement) {
+            pf.assign(2 * K, Prechargement{});
+            TRC_HIP(hipHostMalloc(&pf_hote, uint64_t(2 * K) * lg_max, hipHostMallocDefault));
+            TRC_HIP(hipMalloc(&normes, uint64_t(L) * D * 4));
+            TRC_HIP(hipMalloc(&h2p, 4ull * D));
+            TRC_HIP(hipMalloc(&logits_p, 4ull * E));
+            TRC_HIP(hipMalloc(&idx_p, 64));
+            TRC_HIP(hipMalloc(&poids_p, 64));
+            // the post-attention norms from RÉSIDENTS (f32[D]) when the file holds them, else 1
+            std::vector<float> w(D);
+            for (uint32_t l = 0; l < L; ++l) {
+                char nom[64];
+                snprintf(nom, sizeof(nom), "blk.%u.post_attention_norm.weight", l);
+                const trc_resident* r = nullptr;
+                for (uint32_t i = 0; i < n_res; ++i)
+                    if (strncmp(res[i].nom, nom, 64) == 0) r = &res[i];
+                if (r == nullptr) {
+                    std::fill(w.begin(), w.end(), 1.0f);
+                } else {
+                    if (r->type_ggml != 0 || r->ne[0] != D || r->octets != 4ull * D)
+                        return trc::usage("norme %s : f32 de %u attendu", nom, D);
+                    TRC_OK_OU_RENDRE(trc_fichier_lire(f, trc_fichier_debut_donnees(f) + r->decalage, r->octets, w.data()));
+                }
+                TRC_HIP(hipMemcpy(normes + uint64_t(l) * D, w.data(), 4ull * D, hipMemcpyHostToDevice));
+            }
+        }
         return TRC_OK;
     }
 
@@ -272,6 +318,18 @@ struct trc_ordo {
                                       vue(logits, 4ull * E), E, C, flux));
         TRC_OK_OU_RENDRE(trc_routeur_topk(vue(logits, 4ull * E), E, k, vue(idx, 64), vue(poids, 64),
                                           uint64_t(reinterpret_cast<uintptr_t>(boite_carte)), seq, flux));
+        // Modele::predire (trc-modele/src/lib.rs:570-579): layer l+1's router over the residual
+        // normed with l+1's post-attention norm, into the second mailbox; x and the residual untouched
+        const bool predire = cfg.prechargement && l + 1 < L;
+        if (predire) {
+            TRC_OK_OU_RENDRE(trc_rmsnorm(residu, vue(normes + uint64_t(l + 1) * D, 4ull * D), vue(h2p, 4ull * D), D, 1,
+                                         EPS_PREDICTION, flux));
+            TRC_OK_OU_RENDRE(trc_gemv_f32(vue(routeurs + uint64_t(l + 1) * E * C, 4ull * E * C), vue(h2p, 4ull * C),
+                                          trc_vue{0, 0}, vue(logits_p, 4ull * E), E, C, flux));
+            TRC_OK_OU_RENDRE(trc_routeur_topk(vue(logits_p, 4ull * E), E, k, vue(idx_p, 64), vue(poids_p, 64),
+                                              uint64_t(reinterpret_cast<uintptr_t>(boite_carte + BOITE_PREDICTION)),
+                                              seq, flux));
+        }
         TRC_HIP(hipEventRecord(ev_routeur, fl));
         st.us_emission += us_depuis(t_emis);
         const auto t0 = horloge::now();
@@ -284,16 +342,37 @@ struct trc_ordo {
             if (e >= E) return trc::usage("couche %u : expert %u hors de [0, %u)", l, e, E);
             experts[i] = uint16_t(e);
         }
+        uint16_t predits[8] = {};
+        if (predire) {
+            if (bv[BOITE_PREDICTION] != seq)
+                return trc::usage("couche %u : boite de prediction a la sequence %u, %u attendue", l, bv[BOITE_PREDICTION],
+                                  seq);
+            for (uint32_t i = 0; i < k; ++i) predits[i] = uint16_t(bv[BOITE_PREDICTION + 1 + i]);
+        }
         st.us_attente_routeur += us_depuis(t0);
         trace.insert(trace.end(), experts, experts + k);
         // 2. decisions
         trc_decision d[8];
         TRC_OK_OU_RENDRE(trc_cache_demander(cache, uint16_t(l), experts, k, jeton * L + l, d));
-        // 3. misses: disk reads submitted at once; RAM hits sent at once; disk misses sent as they land
+        // 3. misses: disk reads submitted at once; RAM hits sent at once; disk misses sent as they land.
+        // With prefetch, a disk miss without a warm entry whose part was read ahead (set l % 2) takes
+        // it from the prefetch buffer: at once if the read has landed, else when it lands.
         const auto t_es = horloge::now();
-        uint32_t en_vol = 0;
+        int32_t pf_de[8];
         for (uint32_t i = 0; i < k; ++i) {
-            if (d[i].sorte != TRC_DECISION_DEFAUT_DISQUE) continue;
+            pf_de[i] = -1;
+            if (!cfg.prechargement || d[i].sorte != TRC_DECISION_DEFAUT_DISQUE || d[i].tiede >= 0) continue;
+            for (uint32_t s = (l % 2u) * k; s < (l % 2u + 1u) * k; ++s)
+                if (pf[s].couche == int32_t(l) && pf[s].expert == experts[i] && !pf[s].pris) {
+                    pf_de[i] = int32_t(s);
+                    pf[s].pris = true;
+                    st.pf_utiles += 1;
+                    break;
+                }
+        }
+        uint32_t en_vol = 0;  // completions this layer waits for: its own reads and the prefetches it took
+        for (uint32_t i = 0; i < k; ++i) {
+            if (d[i].sorte != TRC_DECISION_DEFAUT_DISQUE || pf_de[i] >= 0) continue;
             uint8_t* dst = d[i].tiede >= 0 ? tiedes + uint64_t(d[i].tiede) * lg_max : arrivees_hote + uint64_t(i) * lg_max;
             lecteurs->soumettre({uint16_t(l), experts[i], dst, lg_max, cfg.verifier, i});
             ++en_vol;
@@ -304,27 +383,88 @@ struct trc_ordo {
             TRC_OK_OU_RENDRE(envoyer_et_decoder(l, i, tiedes + uint64_t(d[i].tiede) * lg_max, en->longueur[0],
                                                 d[i].emplacement, flux));
         }
+        for (uint32_t i = 0; i < k; ++i) {
+            if (pf_de[i] < 0) continue;
+            Prechargement& p = pf[pf_de[i]];
+            if (p.en_vol) {
+                p.attendu_par = int32_t(i);
+                ++en_vol;
+                continue;
+            }
+            if (p.statut != TRC_OK) {
+                trc::derniere_erreur() = p.message;
+                return p.statut;
+            }
+            TRC_OK_OU_RENDRE(envoyer_et_decoder(l, i, pf_hote + uint64_t(pf_de[i]) * lg_max, p.octets,
+                                                d[i].emplacement, flux));
+        }
         int echec = TRC_OK;
         std::string message;
-        while (en_vol > 0) {
-            Lecteurs::Fin x = lecteurs->attendre();
+        auto traiter = [&](Lecteurs::Fin x) {
+            const uint8_t* src;
+            uint32_t i;
+            if (x.n >= PF_JETON) {
+                Prechargement& p = pf[x.n - PF_JETON];
+                p.en_vol = false;
+                p.statut = x.statut;
+                p.octets = x.octets;
+                if (x.statut != TRC_OK) p.message = x.message;
+                if (p.attendu_par < 0) return;  // a read ahead nobody waits for (yet)
+                i = uint32_t(p.attendu_par);
+                p.attendu_par = -1;
+                src = pf_hote + uint64_t(x.n - PF_JETON) * lg_max;
+            } else {
+                i = x.n;
+                if (x.statut == TRC_OK) {
+                    st.octets_lus += x.octets;
+                    st.lectures += 1;
+                }
+                src = d[i].tiede >= 0 ? tiedes + uint64_t(d[i].tiede) * lg_max : arrivees_hote + uint64_t(i) * lg_max;
+            }
             --en_vol;
             if (x.statut != TRC_OK) {
                 echec = x.statut;
                 message = x.message;
-                continue;
+                return;
             }
-            st.octets_lus += x.octets;
-            st.lectures += 1;
-            if (echec != TRC_OK) continue;
-            const uint32_t i = x.n;
-            const uint8_t* src = d[i].tiede >= 0 ? tiedes + uint64_t(d[i].tiede) * lg_max : arrivees_hote + uint64_t(i) * lg_max;
+            if (echec != TRC_OK) return;
             const int r = envoyer_et_decoder(l, i, src, x.octets, d[i].emplacement, flux);
             if (r != TRC_OK) {
                 echec = r;
                 message = trc_derniere_erreur();
             }
+        };
+        // the reads ahead for layer l+1, queued behind layer l's own (Moteur::pas, lib.rs:1194-1215):
+        // set (l+1) % 2 is reused once the reads still landing in it have landed; its copies to the
+        // device (layer l-1) are over, since the router event waited for above follows the decodes
+        // that waited for them
+        if (predire) {
+            const uint32_t ens = (l + 1u) % 2u;
+            auto ensemble_en_vol = [&] {
+                for (uint32_t s = ens * k; s < (ens + 1u) * k; ++s)
+                    if (pf[s].en_vol) return true;
+                return false;
+            };
+            while (ensemble_en_vol()) traiter(lecteurs->attendre());
+            for (uint32_t i = 0; i < k; ++i) {
+                const uint32_t s = ens * k + i;
+                pf[s] = Prechargement{};
+                const uint16_t e = predits[i];
+                if (e >= E || trc_cache_emplacement_de(cache, uint16_t(l + 1), e) >= 0 ||
+                    trc_cache_tiede_de(cache, uint16_t(l + 1), e) >= 0)
+                    continue;
+                lecteurs->soumettre({uint16_t(l + 1), e, pf_hote + uint64_t(s) * lg_max, lg_max, cfg.verifier, PF_JETON + s});
+                pf[s].couche = int32_t(l + 1);
+                pf[s].expert = e;
+                pf[s].en_vol = true;
+                const uint64_t lg = trc_fichier_entree(f, uint16_t(l + 1), e)->longueur[0];
+                st.pf_emis += 1;
+                st.pf_octets += lg;
+                st.lectures += 1;
+                st.octets_lus += lg;
+            }
         }
+        while (en_vol > 0) traiter(lecteurs->attendre());
         if (echec != TRC_OK) {
             trc::derniere_erreur() = message;
             return echec;
@@ -381,6 +521,8 @@ int trc_ordo_creer(const trc_fichier* f, const trc_config_ordo* cfg, trc_ordo** 
         return trc::usage("formes : gate et up R x C, down D x R attendues");
     if (o->C % 4 != 0 || o->R % 4 != 0) return trc::usage("colonnes et lignes multiples de 4");
     if (o->k > 8 || o->E > 256) return trc::usage("top-%u sur %u experts (au plus 8 sur 256)", o->k, o->E);
+    if (cfg->prechargement && o->C != o->D)
+        return trc::usage("prechargement : le residu (%u) doit avoir la largeur de l'entree du routeur (%u)", o->D, o->C);
     if (cfg->emplacements < o->k)
         return trc::usage("%u emplacements pour %u experts epingles par couche", cfg->emplacements, o->k);
     if (cfg->politique != TRC_POLITIQUE_LRU && cfg->politique != TRC_POLITIQUE_FIFO)

@@ -15,13 +15,14 @@ from .noyaux import VueCarte, _flux, _statut, _vue, bibliotheque, _Vue  # noqa: 
 
 class ConfigOrdo(C.Structure):
     _fields_ = [("emplacements", C.c_uint32), ("tiedes", C.c_uint32), ("politique", C.c_int), ("verifier", C.c_int),
-                ("lecteurs", C.c_uint32)]
+                ("lecteurs", C.c_uint32), ("prechargement", C.c_int)]
 
 
 class StatsOrdo(C.Structure):
     _fields_ = [("jetons", C.c_uint64), ("lectures", C.c_uint64), ("octets_lus", C.c_uint64),
                 ("octets_copies", C.c_uint64), ("decodages", C.c_uint64), ("us_attente_routeur", C.c_double),
-                ("us_lectures", C.c_double), ("us_emission", C.c_double)]
+                ("us_lectures", C.c_double), ("us_emission", C.c_double), ("pf_emis", C.c_uint64),
+                ("pf_utiles", C.c_uint64), ("pf_octets", C.c_uint64)]
 
     def dict(self) -> dict:
         return {n: getattr(self, n) for n, _t in self._fields_}
@@ -53,14 +54,15 @@ def _l():
 class Ordonnanceur:
     """Moteur (trc-ordo/src/lib.rs:300-560), expert path. `emplacements` VRAM slots of decoded
     experts, `tiedes` pinned warm entries of coded parts (0: none), LRU or FIFO, `verifier`: each
-    part read is checked against its directory fingerprint."""
+    part read is checked against its directory fingerprint, `prechargement`: each layer predicts the
+    next layer's experts and reads the predicted parts ahead (Config::prechargement)."""
 
     def __init__(self, fichier: Fichier, emplacements: int, tiedes: int = 0, politique: int = LRU,
-                 verifier: bool = False, lecteurs: int = 0):
+                 verifier: bool = False, lecteurs: int = 0, prechargement: bool = False):
         self.fichier = fichier  # kept alive: the engine reads from it
         e = fichier.entete()
         self.L, self.E, self.k = e.couches, e.experts, e.k
-        cfg = ConfigOrdo(emplacements, tiedes, politique, int(verifier), lecteurs)
+        cfg = ConfigOrdo(emplacements, tiedes, politique, int(verifier), lecteurs, int(prechargement))
         p = C.c_void_p()
         _verifier(_l().trc_ordo_creer(fichier._p, C.byref(cfg), C.byref(p)))
         self._p = p
