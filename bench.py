@@ -510,7 +510,7 @@ def bench_ordo(args, E, k, C, dims, dev, n_fils):
     n_empl = args.emplacements or L * E
     t0 = time.perf_counter()
     o = Ordonnanceur(fichier, emplacements=n_empl, tiedes=args.tiedes, verifier=args.verifier,
-                     prechargement=args.prechargement)
+                     prechargement=args.prechargement, biais_cache=args.biais_cache)
     t_creer = time.perf_counter() - t0
     n_tok = args.warmup + args.steps
     x_tok = np.stack([codeur.synth_normale_bf16(args.graine, 4, t, C, 1.0) for t in range(n_tok)])
@@ -550,7 +550,8 @@ def bench_ordo(args, E, k, C, dims, dev, n_fils):
                                f"{n_empl} decoded-expert slots in HBM ({n_empl * 13.254144e-3:.1f} GB), "
                                f"{args.tiedes} pinned warm entries, LRU", "layers": L, "experts": E, "k": k,
                    "slots": n_empl, "warm_entries": args.tiedes, "n_codes": args.n_codes, "n_delta": args.n_delta,
-                   "verify_reads": bool(args.verifier), "prefetch": bool(args.prechargement)},
+                   "verify_reads": bool(args.verifier), "prefetch": bool(args.prechargement),
+                   "cache_bias": args.biais_cache},
         "hit_rate_vram": round((c1.succes_vram - c0.succes_vram) / acces, 4),
         "hit_rate_ram": round((c1.succes_ram - c0.succes_ram) / acces, 4),
         "disk_misses_per_token": round((c1.defauts_disque - c0.defauts_disque) / n, 3),
@@ -684,6 +685,9 @@ def main():
     ap.add_argument("--emplacements", type=int, default=0, help="--ordo: decoded-expert slots in HBM (0: all)")
     ap.add_argument("--tiedes", type=int, default=0, help="--ordo: pinned warm-RAM entries of coded parts")
     ap.add_argument("--verifier", action="store_true", help="--ordo: check every part read against its fingerprint")
+    ap.add_argument("--biais-cache", type=float, default=None, dest="biais_cache",
+                    help="--ordo: beta added to the router score of each expert already in VRAM for the choice of "
+                         "the k (the mixing weights stay unbiased)")
     ap.add_argument("--prechargement", action="store_true",
                     help="--ordo: each layer predicts the next layer's experts (its router over the normed residual) "
                          "and reads their parts ahead")

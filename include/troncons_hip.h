@@ -149,6 +149,12 @@ int trc_gemv_f32(trc_vue w, trc_vue x, trc_vue biais, trc_vue y, uint32_t lignes
 int trc_routeur_topk(trc_vue logits, uint32_t experts, uint32_t k, trc_vue indices, trc_vue poids, uint64_t boite,
                      uint32_t sequence, void* flux);
 
+/* Noyaux::routeur_topk_biais (lib.rs:437-448, passe.cuh:516-580): the k chosen on logit + biais
+ * (f32[experts]: beta for an expert already in VRAM), returned by unbiased logit with the softmax of
+ * the unbiased logits; routeur_topk's bits when biais is zero. Same mailbox protocol. */
+int trc_routeur_topk_biais(trc_vue logits, trc_vue biais, uint32_t experts, uint32_t k, trc_vue indices,
+                           trc_vue poids, uint64_t boite, uint32_t sequence, void* flux);
+
 /* Noyaux::swiglu_oai (lib.rs:451-458) */
 int trc_swiglu_oai(trc_vue g, trc_vue u, trc_vue y, uint32_t n, void* flux);
 
@@ -623,6 +629,11 @@ typedef struct {
                             * are neither in VRAM nor in warm RAM are read into pinned prefetch buffers
                             * behind layer l's own reads, and a disk miss of layer l+1 without a warm
                             * entry takes its bytes from there */
+    int avec_biais_cache;  /* Config::biais_cache is Some (lib.rs:110-118): the router chooses on
+                            * logit + biais_cache for the layer's experts already in a VRAM slot just
+                            * before the layer's cache request (routeur_topk_biais); the mixing
+                            * weights stay the unbiased softmax. Refused with prechargement */
+    float biais_cache;     /* beta, in raw logit units (finite) */
 } trc_config_ordo;
 
 /* CompteursMoteur (trc-ordo/src/lib.rs:586-594), the expert path's share */

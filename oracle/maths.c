@@ -169,3 +169,48 @@ void orc_routeur_topk(const float* logits, uint32_t E, uint32_t k, uint32_t* ind
     }
     free(pris);
 }
+
+/* routeur_topk_biais, passe.cuh:516-580 (the cache-biased router): the k are chosen on the f32
+ * score logit + biais (score desc, index asc), then returned by unbiased logit desc, index asc
+ * (insertion sort), weights = f64 softmax of the unbiased logits, max = the first. A slot left
+ * unchosen (NaN scores) keeps index 0xFFFFFFFF and reads as logit -inf. */
+void orc_routeur_topk_biais(const float* logits, const float* biais, uint32_t E, uint32_t k, uint32_t* indices,
+                            float* poids) {
+    unsigned char* pris = (unsigned char*)calloc(E, 1);
+    uint32_t idx[8];
+    float u[8];
+    for (uint32_t r = 0; r < k; ++r) {
+        float bv = -INFINITY;
+        uint32_t bi = 0xFFFFFFFFu;
+        for (uint32_t e = 0; e < E; ++e) {
+            const volatile float sc = logits[e] + biais[e];
+            if (!pris[e] && meilleur(sc, e, bv, bi)) {
+                bv = sc;
+                bi = e;
+            }
+        }
+        if (bi != 0xFFFFFFFFu) pris[bi] = 1;
+        idx[r] = bi;
+        u[r] = bi < E ? logits[bi] : -INFINITY;
+    }
+    for (uint32_t r = 1; r < k; ++r)
+        for (uint32_t j = r; j > 0 && meilleur(u[j], idx[j], u[j - 1], idx[j - 1]); --j) {
+            const float tv = u[j];
+            u[j] = u[j - 1];
+            u[j - 1] = tv;
+            const uint32_t ti = idx[j];
+            idx[j] = idx[j - 1];
+            idx[j - 1] = ti;
+        }
+    double ex[8], z = 0.0;
+    const double m = u[0];
+    for (uint32_t r = 0; r < k; ++r) {
+        ex[r] = exp((double)u[r] - m);
+        z += ex[r];
+    }
+    for (uint32_t r = 0; r < k; ++r) {
+        indices[r] = idx[r];
+        poids[r] = (float)(ex[r] / z);
+    }
+    free(pris);
+}

@@ -189,6 +189,11 @@ void orc_combiner(float* residu, const float* sorties, uint32_t pas, const float
 /* routeur_topk (passe.cuh:455-514, ops.rs:121-131): top-k by (value desc, index asc), softmax of
  * the k in f64 (m = first), rounded to f32. */
 void orc_routeur_topk(const float* logits, uint32_t E, uint32_t k, uint32_t* indices, float* poids);
+/* routeur_topk_biais (passe.cuh:516-580). Pinned by: zero bias gives orc_routeur_topk bit for bit;
+ * a sort-based restatement (the reference's host version, tests/passe.rs:328-337) on tie-forcing
+ * draws; a hand case whose weights are a closed-form softmax. */
+void orc_routeur_topk_biais(const float* logits, const float* biais, uint32_t E, uint32_t k, uint32_t* indices,
+                            float* poids);
 
 /* ------------------------------------------------------------- forward pass around the experts */
 /* (passe.c) The rest of a gpt-oss layer step, in each reference kernel's operation order. */

@@ -142,6 +142,7 @@ def _declarer(l: C.CDLL) -> None:
     l.orc_swiglu_oai.argtypes = [f32p, f32p, f32p, C.c_uint32]
     l.orc_combiner.argtypes = [f32p, f32p, C.c_uint32, f32p, C.c_uint32, C.c_uint32]
     l.orc_routeur_topk.argtypes = [f32p, C.c_uint32, C.c_uint32, u32p, f32p]
+    l.orc_routeur_topk_biais.argtypes = [f32p, f32p, C.c_uint32, C.c_uint32, u32p, f32p]
     l.orc_f32_depuis_f16.argtypes = [C.c_uint16]
     l.orc_f32_depuis_f16.restype = C.c_float
     l.orc_f16_depuis_f32.argtypes = [C.c_float]
@@ -413,6 +414,16 @@ def routeur_topk(logits, k):
     idx = np.zeros(k, dtype=np.uint32)
     w = np.zeros(k, dtype=np.float32)
     lib().orc_routeur_topk(_p(lg, f32p), lg.size, k, _p(idx, u32p), _p(w, f32p))
+    return idx, w
+
+
+def routeur_topk_biais(logits, biais, k):
+    lg = np.ascontiguousarray(logits, dtype=np.float32)
+    b = np.ascontiguousarray(biais, dtype=np.float32)
+    assert b.size == lg.size
+    idx = np.zeros(k, dtype=np.uint32)
+    w = np.zeros(k, dtype=np.float32)
+    lib().orc_routeur_topk_biais(_p(lg, f32p), _p(b, f32p), lg.size, k, _p(idx, u32p), _p(w, f32p))
     return idx, w
 
 

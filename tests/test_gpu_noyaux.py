@@ -249,3 +249,46 @@ def test_swiglu_router_mailbox_combiner_passe_rs(k):
     xv = dev(x)
     k.combiner(vue(xv), vue(dev(s)), d, vue(dev(w)), 4, d)
     assert (hote(xv, np.uint32) == O.combiner(x, s, d, w, 4, d).view(np.uint32)).all()
+
+
+def test_biased_router_equals_oracle_and_plain_router_without_bias():
+    """tests/passe.rs:320-393: routeur_topk_biais equals the oracle bit for bit (indices and
+    weights) on tie-forcing draws (logits on a 0.25 grid, E in {6, 32, 256}, beta in {0, 0.041,
+    0.3, 1}, random masks); with a zero bias it equals routeur_topk; the inverted mask gives a
+    different answer several times (the test bites) and the bias changes several sets."""
+    k = K.Noyaux()
+    rng = np.random.default_rng(20261027)
+    changes = inverses = 0
+    iv, pv, jv, qv = zeros(32), zeros(32), zeros(32), zeros(32)
+    for essai in range(160):
+        E = [6, 32, 32, 256][essai % 4]
+        beta = [0.0, 0.041, 0.3, 1.0][(essai // 4) % 4]
+        l = (rng.integers(-40, 41, E) * 0.25).astype(np.float32)
+        m = rng.integers(0, 2, E) == 1
+        b = np.where(m, beta, 0.0).astype(np.float32)
+        bi = np.where(m, 0.0, beta).astype(np.float32)
+        lv = dev(l)
+        k.routeur_topk_biais(vue(lv), vue(dev(b)), E, 4, vue(iv), vue(pv))
+        oi, ow = O.routeur_topk_biais(l, b, 4)
+        assert (hote(iv, np.uint32)[:4] == oi).all(), essai
+        assert (hote(pv, np.uint32)[:4] == ow.view(np.uint32)).all(), essai
+        k.routeur_topk_biais(vue(lv), vue(dev(np.zeros(E, np.float32))), E, 4, vue(iv), vue(pv))
+        k.routeur_topk(vue(lv), E, 4, vue(jv), vue(qv))
+        assert (hote(iv, np.uint32)[:4] == hote(jv, np.uint32)[:4]).all(), essai
+        assert (hote(pv, np.uint32)[:4] == hote(qv, np.uint32)[:4]).all(), essai
+        if beta > 0:
+            if sorted(O.routeur_topk(l, 4)[0]) != sorted(oi):
+                changes += 1
+            k.routeur_topk_biais(vue(lv), vue(dev(bi)), E, 4, vue(iv), vue(pv))
+            if (hote(iv, np.uint32)[:4] != oi).any():
+                inverses += 1
+    assert changes > 5 and inverses > 5
+    # mailbox: the same words as routeur_topk's
+    l = np.array([1.0, 3.0, 3.0, 0.0, 2.0, -1.0], np.float32)
+    boite = torch.zeros(1024, dtype=torch.int32).pin_memory()
+    k.routeur_topk_biais(vue(dev(l)), vue(dev(np.array([0, 0, 0, 5, 0, 0], np.float32))), 6, 4, vue(iv), vue(pv),
+                         boite.data_ptr(), 91)
+    torch.cuda.synchronize()
+    mots = boite.numpy()[:9].view(np.uint32)
+    assert mots[0] == 91 and list(mots[1:5]) == [1, 2, 4, 3]
+    assert (mots[5:9] == hote(pv, np.uint32)[:4]).all()

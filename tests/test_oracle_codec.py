@@ -270,6 +270,57 @@ def test_router_fixture_passe_rs_275():
     assert list(idx) == [1, 2, 4] and abs(float(w.sum()) - 1.0) < 1e-6 and w[0] == w[1]
 
 
+def _topk_biais_par_tri(l, b, k):
+    """The reference's host version (tests/passe.rs:328-337): sort by f32 score desc then index,
+    keep k, sort those by logit desc then index, f64 softmax of the logits."""
+    l = np.asarray(l, np.float32)
+    sc = (l + np.asarray(b, np.float32)).astype(np.float32)
+    ids = sorted(range(l.size), key=lambda i: (-float(sc[i]), i))[:k]
+    ids = sorted(ids, key=lambda i: (-float(l[i]), i))
+    m = float(l[ids[0]])
+    e = [math.exp(float(l[i]) - m) for i in ids]
+    z = 0.0
+    for v in e:
+        z += v
+    return ids, [float(np.float32(v / z)) for v in e]
+
+
+def test_biased_router_hand_case_and_zero_bias():
+    # scores [1, 3, 3, 5, 2, -1]: chosen {3, 1, 2, 4}, returned by logit: 1, 2 (3.0), 4 (2.0), 3 (0.0)
+    l = [1.0, 3.0, 3.0, 0.0, 2.0, -1.0]
+    idx, w = O.routeur_topk_biais(l, [0, 0, 0, 5.0, 0, 0], 4)
+    assert list(idx) == [1, 2, 4, 3]
+    e = [1.0, 1.0, math.exp(-1.0), math.exp(-3.0)]
+    z = ((e[0] + e[1]) + e[2]) + e[3]
+    assert [float(v) for v in w] == [float(np.float32(v / z)) for v in e]
+    # zero bias: routeur_topk bit for bit
+    rng = np.random.default_rng(7)
+    for E in (6, 32, 256):
+        lg = (rng.integers(-40, 41, E) * 0.25).astype(np.float32)
+        i0, w0 = O.routeur_topk(lg, 4)
+        i1, w1 = O.routeur_topk_biais(lg, np.zeros(E, np.float32), 4)
+        assert (i0 == i1).all() and (w0.view(np.uint32) == w1.view(np.uint32)).all()
+
+
+def test_biased_router_equals_sort_based_restatement():
+    """Tie-forcing draws as tests/passe.rs:339-393: logits on a 0.25 grid, E in {6, 32, 256},
+    beta in {0, 0.041, 0.3, 1}, random masks; the bias changes some sets."""
+    rng = np.random.default_rng(20261027)
+    changes = 0
+    for essai in range(160):
+        E = [6, 32, 32, 256][essai % 4]
+        beta = [0.0, 0.041, 0.3, 1.0][(essai // 4) % 4]
+        l = (rng.integers(-40, 41, E) * 0.25).astype(np.float32)
+        b = np.where(rng.integers(0, 2, E) == 1, beta, 0.0).astype(np.float32)
+        idx, w = O.routeur_topk_biais(l, b, 4)
+        ri, rw = _topk_biais_par_tri(l, b, 4)
+        assert list(idx) == ri, essai
+        assert [float(v) for v in w] == rw, essai
+        if sorted(ri) != sorted(_topk_biais_par_tri(l, np.zeros(E), 4)[0]):
+            changes += 1
+    assert changes > 5
+
+
 # ------------------------------------------------------------------------------ generators
 
 def test_splitmix64_kat():

@@ -404,6 +404,58 @@ routeur_topk(const float* __restrict__ logits, uint32_t E, uint32_t k, uint32_t*
     }
 }
 
+// The cache-biased router (passe.cuh:516-580): the k are chosen on the f32 score logit + biais
+// (biais[e] = beta for an expert already in a VRAM slot, 0 else; score desc, index asc), then
+// returned by unbiased logit desc, index asc, with the f64 softmax of the unbiased logits as
+// weights. With a zero bias: routeur_topk's indices and weights, bit for bit. Same outputs and
+// mailbox protocol as routeur_topk. A slot left unchosen (NaN scores) keeps index 0xFFFFFFFF and
+// sorts last with weight 0.
+extern "C" __global__ void __launch_bounds__(64)
+routeur_topk_biais(const float* __restrict__ logits, const float* __restrict__ biais, uint32_t E, uint32_t k,
+                   uint32_t* __restrict__ indices, float* __restrict__ poids, uint32_t* boite, uint32_t sequence) {
+    using namespace trc;
+    if (E == 0 || E > EXPERTS_MAX || k == 0 || k > TOPK_MAX || k > E) return;
+    __shared__ float score[EXPERTS_MAX];
+    for (uint32_t e = threadIdx.x; e < E; e += blockDim.x) score[e] = logits[e] + biais[e];
+    __syncthreads();
+    uint32_t choisi[TOPK_MAX];
+    float w_score[TOPK_MAX];  // softmax of the scores: not used
+    topk_vague(score, E, k, choisi, w_score);
+    if (threadIdx.x != 0) return;
+    float u[TOPK_MAX];
+#pragma unroll
+    for (uint32_t r = 0; r < TOPK_MAX; ++r) u[r] = r < k && choisi[r] < E ? logits[choisi[r]] : -INFINITY;
+    for (uint32_t r = 1; r < k; ++r)
+        for (uint32_t j = r; j > 0 && meilleur(u[j], choisi[j], u[j - 1], choisi[j - 1]); --j) {
+            const float tv = u[j];
+            u[j] = u[j - 1];
+            u[j - 1] = tv;
+            const uint32_t ti = choisi[j];
+            choisi[j] = choisi[j - 1];
+            choisi[j - 1] = ti;
+        }
+    double ex[TOPK_MAX];
+    const double m = u[0];
+    double z = 0.0;
+    for (uint32_t r = 0; r < k; ++r) {
+        ex[r] = exp(double(u[r]) - m);
+        z += ex[r];
+    }
+    for (uint32_t r = 0; r < k; ++r) {
+        const float w = float(ex[r] / z);
+        indices[r] = choisi[r];
+        poids[r] = w;
+        if (boite != nullptr) {
+            reinterpret_cast<volatile uint32_t*>(boite)[1 + r] = choisi[r];
+            reinterpret_cast<volatile uint32_t*>(boite)[1 + k + r] = __float_as_uint(w);
+        }
+    }
+    if (boite != nullptr) {
+        __threadfence_system();
+        reinterpret_cast<volatile uint32_t*>(boite)[0] = sequence;
+    }
+}
+
 // gpt-oss clamped SwiGLU in f64, rounded once: g <- min(g,7); u <- clamp(u,-7,7);
 // y = g / (1 + exp(-1.702 g)) * (u + 1).
 extern "C" __global__ void __launch_bounds__(256)
@@ -568,6 +620,20 @@ extern "C" int trc_routeur_topk(trc_vue logits, uint32_t experts, uint32_t k, tr
                        experts, k, reinterpret_cast<uint32_t*>(indices.adresse), reinterpret_cast<float*>(poids.adresse),
                        reinterpret_cast<uint32_t*>(boite), sequence);
     return trc::apres_lancement("routeur_topk");
+}
+
+extern "C" int trc_routeur_topk_biais(trc_vue logits, trc_vue biais, uint32_t experts, uint32_t k, trc_vue indices,
+                                      trc_vue poids, uint64_t boite, uint32_t sequence, void* flux) {
+    TRC_VERIFIER(experts > 0 && experts <= 256 && k > 0 && k <= 8 && k <= experts, "top-%u sur %u", k, experts);
+    TRC_VERIFIER(logits.adresse != 0 && logits.octets >= 4ull * experts && biais.adresse != 0 &&
+                     biais.octets >= 4ull * experts && indices.adresse != 0 && indices.octets >= 4ull * k &&
+                     poids.adresse != 0 && poids.octets >= 4ull * k,
+                 "routeur biaise : vues trop courtes");
+    hipLaunchKernelGGL(routeur_topk_biais, dim3(1), dim3(64), 0, flux_de(flux),
+                       reinterpret_cast<const float*>(logits.adresse), reinterpret_cast<const float*>(biais.adresse),
+                       experts, k, reinterpret_cast<uint32_t*>(indices.adresse), reinterpret_cast<float*>(poids.adresse),
+                       reinterpret_cast<uint32_t*>(boite), sequence);
+    return trc::apres_lancement("routeur_topk_biais");
 }
 
 extern "C" int trc_swiglu_oai(trc_vue g, trc_vue u, trc_vue y, uint32_t n, void* flux) {

@@ -22,6 +22,8 @@
 // router of layer l + 1, whose mailbox the host waits for before reusing any buffer of layer l.
 #include <hip/hip_runtime.h>
 
+#include <cmath>
+
 #include <algorithm>
 #include <atomic>
 #include <chrono>
@@ -183,6 +185,9 @@ struct trc_ordo {
     float* normes = nullptr;  // L x D post-attention norm weights
     float *h2p = nullptr, *logits_p = nullptr, *poids_p = nullptr;
     uint32_t* idx_p = nullptr;
+    // cache-biased router (cfg.avec_biais_cache): beta per expert of the layer, pinned then device
+    float* biais_hote = nullptr;
+    float* biais_carte = nullptr;
 
     ~trc_ordo() {
         lecteurs.reset();
@@ -192,12 +197,12 @@ struct trc_ordo {
         if (ev_routeur) (void)hipEventDestroy(ev_routeur);
         if (copie) (void)hipStreamDestroy(copie);
         void* dev[] = {emplacements, luts, routeurs, logits, idx, poids, g, u, a, sorties, descs, controle,
-                       normes, h2p, logits_p, poids_p, idx_p};
+                       normes, h2p, logits_p, poids_p, idx_p, biais_carte};
         for (void* p : dev)
             if (p) (void)hipFree(p);
         for (uint8_t* p : arrivees)
             if (p) (void)hipFree(p);
-        void* hote[] = {tiedes, arrivees_hote, boite, descs_hote, pf_hote};
+        void* hote[] = {tiedes, arrivees_hote, boite, descs_hote, pf_hote, biais_hote};
         for (void* p : hote)
             if (p) (void)hipHostFree(p);
     }
@@ -259,6 +264,10 @@ struct trc_ordo {
             }
             TRC_HIP(hipMemcpy(routeurs + uint64_t(l) * E * C, rf.data(), rf.size() * 4, hipMemcpyHostToDevice));
         }
+        if (cfg.avec_biais_cache) {
+            TRC_HIP(hipHostMalloc(&biais_hote, 4ull * E, hipHostMallocDefault));
+            TRC_HIP(hipMalloc(&biais_carte, 4ull * E));
+        }
         if (cfg.prechargement) {
             pf.assign(2 * K, Prechargement{});
             TRC_HIP(hipHostMalloc(&pf_hote, uint64_t(2 * K) * lg_max, hipHostMallocDefault));
@@ -316,8 +325,20 @@ struct trc_ordo {
         const uint32_t seq = sequence;
         TRC_OK_OU_RENDRE(trc_gemv_f32(vue(routeurs + uint64_t(l) * E * C, 4ull * E * C), x, trc_vue{0, 0},
                                       vue(logits, 4ull * E), E, C, flux));
-        TRC_OK_OU_RENDRE(trc_routeur_topk(vue(logits, 4ull * E), E, k, vue(idx, 64), vue(poids, 64),
-                                          uint64_t(reinterpret_cast<uintptr_t>(boite_carte)), seq, flux));
+        if (cfg.avec_biais_cache) {
+            // beta on each of layer l's experts in a VRAM slot just before its request (the cache
+            // after layer l-1 of this token: causal), sent before the router (lib.rs:1089-1100); the
+            // pinned vector is free again: its previous copy precedes the router event waited for
+            for (uint32_t e = 0; e < E; ++e)
+                biais_hote[e] = trc_cache_emplacement_de(cache, uint16_t(l), uint16_t(e)) >= 0 ? cfg.biais_cache : 0.0f;
+            TRC_HIP(hipMemcpyAsync(biais_carte, biais_hote, 4ull * E, hipMemcpyHostToDevice, fl));
+            TRC_OK_OU_RENDRE(trc_routeur_topk_biais(vue(logits, 4ull * E), vue(biais_carte, 4ull * E), E, k, vue(idx, 64),
+                                                    vue(poids, 64), uint64_t(reinterpret_cast<uintptr_t>(boite_carte)),
+                                                    seq, flux));
+        } else {
+            TRC_OK_OU_RENDRE(trc_routeur_topk(vue(logits, 4ull * E), E, k, vue(idx, 64), vue(poids, 64),
+                                              uint64_t(reinterpret_cast<uintptr_t>(boite_carte)), seq, flux));
+        }
         // Modele::predire (trc-modele/src/lib.rs:570-579): layer l+1's router over the residual
         // normed with l+1's post-attention norm, into the second mailbox; x and the residual untouched
         const bool predire = cfg.prechargement && l + 1 < L;
@@ -521,6 +542,10 @@ int trc_ordo_creer(const trc_fichier* f, const trc_config_ordo* cfg, trc_ordo** 
         return trc::usage("formes : gate et up R x C, down D x R attendues");
     if (o->C % 4 != 0 || o->R % 4 != 0) return trc::usage("colonnes et lignes multiples de 4");
     if (o->k > 8 || o->E > 256) return trc::usage("top-%u sur %u experts (au plus 8 sur 256)", o->k, o->E);
+    if (cfg->avec_biais_cache && !std::isfinite(cfg->biais_cache))
+        return trc::usage("biais de cache : beta = %g n'est pas un nombre fini", double(cfg->biais_cache));
+    if (cfg->avec_biais_cache && cfg->prechargement)
+        return trc::usage("biais de cache et prechargement ne se combinent pas : la prediction est faite sans biais");
     if (cfg->prechargement && o->C != o->D)
         return trc::usage("prechargement : le residu (%u) doit avoir la largeur de l'entree du routeur (%u)", o->D, o->C);
     if (cfg->emplacements < o->k)

@@ -166,6 +166,7 @@ def _declarer(l: C.CDLL) -> C.CDLL:
     l.trc_gemv_lot.argtypes = [V, C.c_uint32, C.c_uint32, C.c_void_p]
     l.trc_gemv_f32.argtypes = [V, V, V, V, C.c_uint32, C.c_uint32, C.c_void_p]
     l.trc_routeur_topk.argtypes = [V, C.c_uint32, C.c_uint32, V, V, C.c_uint64, C.c_uint32, C.c_void_p]
+    l.trc_routeur_topk_biais.argtypes = [V, V, C.c_uint32, C.c_uint32, V, V, C.c_uint64, C.c_uint32, C.c_void_p]
     l.trc_swiglu_oai.argtypes = [V, V, V, C.c_uint32, C.c_void_p]
     l.trc_combiner.argtypes = [V, V, C.c_uint32, V, C.c_uint32, C.c_uint32, C.c_void_p]
     l.trc_gemv_q8_0.argtypes = [V, V, V, V, C.c_uint32, C.c_uint32, C.c_void_p]
@@ -321,6 +322,12 @@ class Noyaux:
         """lib.rs:418"""
         _statut(self._l.trc_routeur_topk(_vue(logits), experts, k, _vue(indices), _vue(poids), boite, sequence,
                                          _flux(f)))
+
+    def routeur_topk_biais(self, logits, biais, experts: int, k: int, indices, poids, boite: int = 0,
+                           sequence: int = 0, f=None) -> None:
+        """lib.rs:437"""
+        _statut(self._l.trc_routeur_topk_biais(_vue(logits), _vue(biais), experts, k, _vue(indices), _vue(poids),
+                                               boite, sequence, _flux(f)))
 
     def swiglu_oai(self, g, u, y, n: int, f=None) -> None:
         """lib.rs:451"""

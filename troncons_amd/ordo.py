@@ -15,7 +15,8 @@ from .noyaux import VueCarte, _flux, _statut, _vue, bibliotheque, _Vue  # noqa: 
 
 class ConfigOrdo(C.Structure):
     _fields_ = [("emplacements", C.c_uint32), ("tiedes", C.c_uint32), ("politique", C.c_int), ("verifier", C.c_int),
-                ("lecteurs", C.c_uint32), ("prechargement", C.c_int)]
+                ("lecteurs", C.c_uint32), ("prechargement", C.c_int), ("avec_biais_cache", C.c_int),
+                ("biais_cache", C.c_float)]
 
 
 class StatsOrdo(C.Structure):
@@ -55,14 +56,18 @@ class Ordonnanceur:
     """Moteur (trc-ordo/src/lib.rs:300-560), expert path. `emplacements` VRAM slots of decoded
     experts, `tiedes` pinned warm entries of coded parts (0: none), LRU or FIFO, `verifier`: each
     part read is checked against its directory fingerprint, `prechargement`: each layer predicts the
-    next layer's experts and reads the predicted parts ahead (Config::prechargement)."""
+    next layer's experts and reads the predicted parts ahead (Config::prechargement), `biais_cache`:
+    beta added to the router's score of the layer's experts already in VRAM for the choice of the k
+    (Config::biais_cache; None: the plain router)."""
 
     def __init__(self, fichier: Fichier, emplacements: int, tiedes: int = 0, politique: int = LRU,
-                 verifier: bool = False, lecteurs: int = 0, prechargement: bool = False):
+                 verifier: bool = False, lecteurs: int = 0, prechargement: bool = False,
+                 biais_cache: float | None = None):
         self.fichier = fichier  # kept alive: the engine reads from it
         e = fichier.entete()
         self.L, self.E, self.k = e.couches, e.experts, e.k
-        cfg = ConfigOrdo(emplacements, tiedes, politique, int(verifier), lecteurs, int(prechargement))
+        cfg = ConfigOrdo(emplacements, tiedes, politique, int(verifier), lecteurs, int(prechargement),
+                         int(biais_cache is not None), 0.0 if biais_cache is None else float(biais_cache))
         p = C.c_void_p()
         _verifier(_l().trc_ordo_creer(fichier._p, C.byref(cfg), C.byref(p)))
         self._p = p
