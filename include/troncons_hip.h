@@ -219,6 +219,14 @@ int trc_ecrire_kv(trc_vue k, trc_vue v, trc_vue cache_k, trc_vue cache_v, uint32
  * the per-head sinks in the softmax denominator; puits f32[tetes], sortie f32[tetes * 64]. */
 int trc_attention(trc_vue q, trc_vue cache_k, trc_vue cache_v, trc_vue puits, trc_vue sortie,
                   const trc_params_attention* p, void* flux);
+
+/* Noyaux::ecrire_kv_f32 / attention_kvf32 (lib.rs:383-411, passe.cuh:374-445): the trial f32 KV
+ * cache: k and v stored unrounded, then the same attention arithmetic in the same order (the
+ * f16 path's bits whenever the keys and values are exact in f16). Cache views: f32[cases][dkv]. */
+int trc_ecrire_kv_f32(trc_vue k, trc_vue v, trc_vue cache_k, trc_vue cache_v, uint32_t dkv, uint32_t case_kv,
+                      void* flux);
+int trc_attention_kvf32(trc_vue q, trc_vue cache_k, trc_vue cache_v, trc_vue puits, trc_vue sortie,
+                        const trc_params_attention* p, void* flux);
 /* Noyaux::argmax (lib.rs:490-496): index of the largest of n floats (ties: lower index; NaN never
  * chosen; all NaN: 0xFFFFFFFF) into sortie (u32). */
 int trc_argmax(trc_vue v, uint32_t n, trc_vue sortie, void* flux);

@@ -222,3 +222,33 @@ def test_usage_errors_are_refused(k):
                     ParamsAttention.gpt_oss(8192, 0))  # 8193 positions
     with pytest.raises(ErreurUsage):
         k.rope_yarn(vue(zeros(256)), vue(zeros(256)), 1, 1, 0, ParamsRope.gpt_oss(variante=2))
+
+
+@pytest.mark.parametrize("anneau,representable", [(0, True), (128, True), (0, False)])
+def test_kv_f32_equals_f16_path_on_representable_values(k, anneau, representable):
+    """tests/passe.rs:395-433: with keys and values m / 256, |m| <= 1024 (exact in f16), the f32
+    cache path (ecrire_kv_f32 + attention_kvf32) gives the f16 path's outputs bit for bit, on a full
+    cache and on a 128-slot ring at position 300; values 1e-3 off that grid make the paths differ."""
+    dkv, position = 8 * 64, 300
+    rng = np.random.default_rng(20261016 + anneau + int(representable))
+    cases = anneau if anneau else position + 1
+    c16k, c16v = zeros(2 * cases * dkv), zeros(2 * cases * dkv)
+    c32k, c32v = zeros(4 * cases * dkv), zeros(4 * cases * dkv)
+    for p in range(position + 1):
+        kv = [(rng.integers(-1024, 1025, dkv) / 256.0 + (0.0 if representable else 1e-3)).astype(np.float32)
+              for _ in range(2)]
+        kd, vd = dev(kv[0]), dev(kv[1])
+        case = ParamsAttention.case(p, anneau)
+        k.ecrire_kv(vue(kd), vue(vd), vue(c16k), vue(c16v), dkv, case)
+        k.ecrire_kv_f32(vue(kd), vue(vd), vue(c32k), vue(c32v), dkv, case)
+    q = (rng.integers(-1000, 1001, 64 * 64) / 333.0).astype(np.float32)
+    puits = (rng.integers(-300, 301, 64) / 100.0).astype(np.float32)
+    pa = ParamsAttention.gpt_oss(position, anneau)
+    s16, s32 = zeros(4 * 64 * 64), zeros(4 * 64 * 64)
+    k.attention(vue(dev(q)), vue(c16k), vue(c16v), vue(dev(puits)), vue(s16), pa)
+    k.attention_kvf32(vue(dev(q)), vue(c32k), vue(c32v), vue(dev(puits)), vue(s32), pa)
+    differents = int((hote(s16, np.uint32) != hote(s32, np.uint32)).sum())
+    if representable:
+        assert differents == 0
+    else:
+        assert differents > 0

@@ -459,10 +459,45 @@ ecrire_kv(const float* __restrict__ k, const float* __restrict__ v, uint16_t* __
 //   m = max(max_j score_j, sink); e_j = expf(score_j - m); z = tree over the threads' sums + expf(sink - m);
 //   out[t] = ((G0 + G1) + (G2 + G3)) / z, G_g the fmaf chain over j = g, g + 4, ... of e_j v_j[t].
 // Query head h reads kv head h / (heads / kv heads); scores live in dynamic LDS (4 bytes each).
-extern "C" __global__ void __launch_bounds__(trc::FILS_PASSE)
-attention(const float* __restrict__ q, const uint16_t* __restrict__ cache_k, const uint16_t* __restrict__ cache_v,
-          const float* __restrict__ puits, float* __restrict__ sortie, trc_params_attention p) {
-    using namespace trc;
+// The caches hold f16 (attention) or f32 (attention_kvf32, passe.cuh:374-445: the same arithmetic
+// in the same order, only the stored keys and values differ).
+namespace trc {
+__device__ __forceinline__ float lire_kv(uint16_t b) { return f16_vers_f32(b); }
+__device__ __forceinline__ float lire_kv(float v) { return v; }
+
+// q . k_j over d = 0..63 in order, k_j one row of 64 stored values
+__device__ __forceinline__ float produit_cle(const float* qs, const uint16_t* kr) {
+    const u32x4* k4 = reinterpret_cast<const u32x4*>(kr);
+    float s = 0.0f;
+#pragma unroll
+    for (uint32_t b = 0; b < 8; ++b) {
+        const u32x4 w = k4[b];
+#pragma unroll
+        for (uint32_t u = 0; u < 4; ++u) {
+            s = fmaf(qs[8 * b + 2 * u], f16_vers_f32(w[u] & 0xFFFFu), s);
+            s = fmaf(qs[8 * b + 2 * u + 1], f16_vers_f32(w[u] >> 16), s);
+        }
+    }
+    return s;
+}
+__device__ __forceinline__ float produit_cle(const float* qs, const float* kr) {
+    const f32x4* k4 = reinterpret_cast<const f32x4*>(kr);
+    float s = 0.0f;
+#pragma unroll
+    for (uint32_t b = 0; b < 16; ++b) {
+        const f32x4 w = k4[b];
+        s = fmaf(qs[4 * b], w.x, s);
+        s = fmaf(qs[4 * b + 1], w.y, s);
+        s = fmaf(qs[4 * b + 2], w.z, s);
+        s = fmaf(qs[4 * b + 3], w.w, s);
+    }
+    return s;
+}
+
+template <typename T>
+__device__ __forceinline__ void attention_tete(const float* __restrict__ q, const T* __restrict__ cache_k,
+                                               const T* __restrict__ cache_v, const float* __restrict__ puits,
+                                               float* __restrict__ sortie, const trc_params_attention& p) {
     extern __shared__ float scores[];
     __shared__ float qs[ATTENTION_DIM];
     __shared__ float part[FILS_PASSE + 1];
@@ -478,18 +513,7 @@ attention(const float* __restrict__ q, const uint16_t* __restrict__ cache_k, con
     for (uint32_t j = t; j < n; j += FILS_PASSE) {
         const uint32_t pos = p.debut + j;
         const uint32_t c = p.anneau ? pos % p.anneau : pos;
-        const u32x4* kr = reinterpret_cast<const u32x4*>(cache_k + uint64_t(c) * dkv + uint64_t(hk) * ATTENTION_DIM);
-        float s = 0.0f;
-#pragma unroll
-        for (uint32_t b = 0; b < 8; ++b) {
-            const u32x4 w = kr[b];
-#pragma unroll
-            for (uint32_t u = 0; u < 4; ++u) {
-                s = fmaf(qs[8 * b + 2 * u], f16_vers_f32(w[u] & 0xFFFFu), s);
-                s = fmaf(qs[8 * b + 2 * u + 1], f16_vers_f32(w[u] >> 16), s);
-            }
-        }
-        scores[j] = s * p.echelle;
+        scores[j] = produit_cle(qs, cache_k + uint64_t(c) * dkv + uint64_t(hk) * ATTENTION_DIM) * p.echelle;
     }
     __syncthreads();
 
@@ -512,7 +536,7 @@ attention(const float* __restrict__ q, const uint16_t* __restrict__ cache_k, con
     float a = 0.0f;
     constexpr uint32_t LOT = 8;
     for (uint32_t j0 = g; j0 < n; j0 += 4u * LOT) {
-        uint16_t vv[LOT];
+        T vv[LOT];
 #pragma unroll
         for (uint32_t u = 0; u < LOT; ++u) {
             const uint32_t pos = p.debut + min(j0 + 4u * u, n - 1u);
@@ -521,12 +545,36 @@ attention(const float* __restrict__ q, const uint16_t* __restrict__ cache_k, con
         }
 #pragma unroll
         for (uint32_t u = 0; u < LOT; ++u)
-            if (j0 + 4u * u < n) a = fmaf(scores[j0 + 4u * u], f16_vers_f32(vv[u]), a);
+            if (j0 + 4u * u < n) a = fmaf(scores[j0 + 4u * u], lire_kv(vv[u]), a);
     }
     groupes[g][dd] = a;
     __syncthreads();
     if (t < ATTENTION_DIM)
         sortie[uint64_t(h) * ATTENTION_DIM + t] = ((groupes[0][t] + groupes[1][t]) + (groupes[2][t] + groupes[3][t])) / z;
+}
+}  // namespace trc
+
+extern "C" __global__ void __launch_bounds__(trc::FILS_PASSE)
+attention(const float* __restrict__ q, const uint16_t* __restrict__ cache_k, const uint16_t* __restrict__ cache_v,
+          const float* __restrict__ puits, float* __restrict__ sortie, trc_params_attention p) {
+    trc::attention_tete(q, cache_k, cache_v, puits, sortie, p);
+}
+
+extern "C" __global__ void __launch_bounds__(trc::FILS_PASSE)
+attention_kvf32(const float* __restrict__ q, const float* __restrict__ cache_k, const float* __restrict__ cache_v,
+                const float* __restrict__ puits, float* __restrict__ sortie, trc_params_attention p) {
+    trc::attention_tete(q, cache_k, cache_v, puits, sortie, p);
+}
+
+// k and v copied unrounded into slot case_kv of f32 caches (passe.cuh:379-387).
+extern "C" __global__ void __launch_bounds__(trc::FILS_PASSE)
+ecrire_kv_f32(const float* __restrict__ k, const float* __restrict__ v, float* __restrict__ cache_k,
+              float* __restrict__ cache_v, uint32_t dkv, uint32_t case_kv) {
+    const uint32_t i = blockIdx.x * trc::FILS_PASSE + threadIdx.x;
+    if (i >= dkv) return;
+    const uint64_t o = uint64_t(case_kv) * dkv + i;
+    cache_k[o] = k[i];
+    cache_v[o] = v[i];
 }
 
 // Index of the largest of n floats: thread t scans i = t, t + 1024, ..., then a fixed tree; ties go
@@ -674,8 +722,11 @@ extern "C" int trc_ecrire_kv(trc_vue k, trc_vue v, trc_vue cache_k, trc_vue cach
     return trc::apres_lancement("ecrire_kv");
 }
 
-extern "C" int trc_attention(trc_vue q, trc_vue cache_k, trc_vue cache_v, trc_vue puits, trc_vue sortie,
-                             const trc_params_attention* p, void* flux) {
+namespace {
+// Noyaux::attention / attention_kvf32 (lib.rs:366-381, 396-411): the reference's checks, then one
+// block per query head; `octets` = bytes per stored value (2 or 4).
+int verifier_attention(trc_vue q, trc_vue cache_k, trc_vue cache_v, trc_vue puits, trc_vue sortie,
+                       const trc_params_attention* p, uint64_t octets) {
     if (p == nullptr) return trc::usage("parametres d'attention absents");
     TRC_VERIFIER(p->dim_tete == 64 && p->tetes_kv > 0 && p->tetes > 0 && p->tetes % p->tetes_kv == 0,
                  "tetes %u / %u de dimension %u", p->tetes, p->tetes_kv, p->dim_tete);
@@ -684,19 +735,51 @@ extern "C" int trc_attention(trc_vue q, trc_vue cache_k, trc_vue cache_v, trc_vu
     TRC_VERIFIER(p->anneau == 0 || p->fin - p->debut <= p->anneau, "plus de positions que de cases dans l'anneau");
     const uint64_t cases = p->anneau > 0 ? p->anneau : p->fin;
     const uint64_t dkv = uint64_t(p->tetes_kv) * 64;
-    TRC_VERIFIER(cache_k.adresse && cache_v.adresse && cache_k.octets >= 2 * cases * dkv &&
-                     cache_v.octets >= 2 * cases * dkv,
+    TRC_VERIFIER(cache_k.adresse && cache_v.adresse && cache_k.octets >= octets * cases * dkv &&
+                     cache_v.octets >= octets * cases * dkv,
                  "cache trop court");
     TRC_VERIFIER(cache_k.adresse % 16 == 0, "cache des cles non aligne sur 16");
     TRC_VERIFIER(q.adresse && sortie.adresse && puits.adresse && q.octets >= 4ull * 64 * p->tetes &&
                      sortie.octets >= 4ull * 64 * p->tetes && puits.octets >= 4ull * p->tetes,
                  "attention : vues trop courtes");
-    const size_t lds = 4u * size_t(p->fin - p->debut);
-    hipLaunchKernelGGL(attention, dim3(p->tetes), dim3(trc::FILS_PASSE), lds, flux_de(flux),
+    return TRC_OK;
+}
+}  // namespace
+
+extern "C" int trc_attention(trc_vue q, trc_vue cache_k, trc_vue cache_v, trc_vue puits, trc_vue sortie,
+                             const trc_params_attention* p, void* flux) {
+    const int r = verifier_attention(q, cache_k, cache_v, puits, sortie, p, 2);
+    if (r != TRC_OK) return r;
+    hipLaunchKernelGGL(attention, dim3(p->tetes), dim3(trc::FILS_PASSE), 4u * size_t(p->fin - p->debut), flux_de(flux),
                        reinterpret_cast<const float*>(q.adresse), reinterpret_cast<const uint16_t*>(cache_k.adresse),
                        reinterpret_cast<const uint16_t*>(cache_v.adresse), reinterpret_cast<const float*>(puits.adresse),
                        reinterpret_cast<float*>(sortie.adresse), *p);
     return trc::apres_lancement("attention");
+}
+
+extern "C" int trc_attention_kvf32(trc_vue q, trc_vue cache_k, trc_vue cache_v, trc_vue puits, trc_vue sortie,
+                                   const trc_params_attention* p, void* flux) {
+    const int r = verifier_attention(q, cache_k, cache_v, puits, sortie, p, 4);
+    if (r != TRC_OK) return r;
+    hipLaunchKernelGGL(attention_kvf32, dim3(p->tetes), dim3(trc::FILS_PASSE), 4u * size_t(p->fin - p->debut),
+                       flux_de(flux), reinterpret_cast<const float*>(q.adresse),
+                       reinterpret_cast<const float*>(cache_k.adresse), reinterpret_cast<const float*>(cache_v.adresse),
+                       reinterpret_cast<const float*>(puits.adresse), reinterpret_cast<float*>(sortie.adresse), *p);
+    return trc::apres_lancement("attention_kvf32");
+}
+
+extern "C" int trc_ecrire_kv_f32(trc_vue k, trc_vue v, trc_vue cache_k, trc_vue cache_v, uint32_t dkv,
+                                 uint32_t case_kv, void* flux) {
+    TRC_VERIFIER(dkv > 0, "dkv nul");
+    const uint64_t fin = 4ull * (uint64_t(case_kv) + 1) * dkv;
+    TRC_VERIFIER(k.adresse && v.adresse && k.octets >= 4ull * dkv && v.octets >= 4ull * dkv, "k ou v trop court");
+    TRC_VERIFIER(cache_k.adresse && cache_v.adresse && cache_k.octets >= fin && cache_v.octets >= fin,
+                 "case %u hors du cache f32", case_kv);
+    hipLaunchKernelGGL(ecrire_kv_f32, dim3((dkv + trc::FILS_PASSE - 1) / trc::FILS_PASSE), dim3(trc::FILS_PASSE), 0,
+                       flux_de(flux), reinterpret_cast<const float*>(k.adresse),
+                       reinterpret_cast<const float*>(v.adresse), reinterpret_cast<float*>(cache_k.adresse),
+                       reinterpret_cast<float*>(cache_v.adresse), dkv, case_kv);
+    return trc::apres_lancement("ecrire_kv_f32");
 }
 
 extern "C" int trc_argmax(trc_vue v, uint32_t n, trc_vue sortie, void* flux) {

@@ -175,6 +175,8 @@ def _declarer(l: C.CDLL) -> C.CDLL:
     l.trc_rope_yarn.argtypes = [V, V, C.c_uint32, C.c_uint32, C.c_uint32, C.POINTER(ParamsRope), C.c_void_p]
     l.trc_ecrire_kv.argtypes = [V, V, V, V, C.c_uint32, C.c_uint32, C.c_void_p]
     l.trc_attention.argtypes = [V, V, V, V, V, C.POINTER(ParamsAttention), C.c_void_p]
+    l.trc_ecrire_kv_f32.argtypes = [V, V, V, V, C.c_uint32, C.c_uint32, C.c_void_p]
+    l.trc_attention_kvf32.argtypes = [V, V, V, V, V, C.POINTER(ParamsAttention), C.c_void_p]
     l.trc_argmax.argtypes = [V, C.c_uint32, V, C.c_void_p]
     l._trc_declare = True
     return l
@@ -363,6 +365,15 @@ class Noyaux:
         """lib.rs:362"""
         _statut(self._l.trc_attention(_vue(q), _vue(cache_k), _vue(cache_v), _vue(puits), _vue(sortie), C.byref(p),
                                       _flux(f)))
+
+    def ecrire_kv_f32(self, k, v, cache_k, cache_v, dkv: int, case_kv: int, f=None) -> None:
+        """lib.rs:383 (the trial f32 KV cache)"""
+        _statut(self._l.trc_ecrire_kv_f32(_vue(k), _vue(v), _vue(cache_k), _vue(cache_v), dkv, case_kv, _flux(f)))
+
+    def attention_kvf32(self, q, cache_k, cache_v, puits, sortie, p: ParamsAttention, f=None) -> None:
+        """lib.rs:396 (the trial f32 KV cache)"""
+        _statut(self._l.trc_attention_kvf32(_vue(q), _vue(cache_k), _vue(cache_v), _vue(puits), _vue(sortie),
+                                            C.byref(p), _flux(f)))
 
     def argmax(self, v, n: int, sortie, f=None) -> None:
         """lib.rs:490"""
