@@ -23,7 +23,8 @@ struct trc_modele {
     std::vector<trc_couche_modele> c;
     trc_vue emb, norme_sortie, sortie;
     // workspace pieces
-    trc_vue x, hh, h2, q, k, v, a, o, idx, pw, controle, moe, z, jeton;
+    trc_vue x, hh, h2, q, k, v, a, o, idx, pw, controle, moe, z, jeton, table;
+    int64_t position_table = -1;  // the position whose rotation table is in `table` (-1: none yet)
 };
 
 namespace {
@@ -49,7 +50,7 @@ uint64_t taille_moe(const trc_hyper& h) {
 uint64_t taille_travail(const trc_hyper& h) {
     const uint64_t d = h.d, dq = uint64_t(h.tetes) * 64, dkv = uint64_t(h.tetes_kv) * 64;
     return al(4 * d) * 3 + al(4 * dq) * 2 + al(4 * dkv) * 2 + al(4 * d) + al(4 * 8) * 2 + al(16) + al(taille_moe(h)) +
-           al(4ull * h.vocab) + al(4);
+           al(4ull * h.vocab) + al(4) + al(16 * 32);
 }
 
 int verifier_hyper(const trc_hyper* h) {
@@ -115,6 +116,7 @@ extern "C" int trc_modele_creer(const trc_hyper* h, const trc_couche_modele* cou
     n->moe = t.prendre(taille_moe(*h));
     n->z = t.prendre(4ull * h->vocab);
     n->jeton = t.prendre(4);
+    n->table = t.prendre(16 * 32);
     *m = n;
     return TRC_OK;
 }
@@ -140,8 +142,8 @@ extern "C" int trc_modele_enchasser(trc_modele* m, uint32_t jeton, void* flux) {
 }
 
 // Modele::debut_couche up to the post-attention norm (lib.rs:498-521), then the fused MoE half.
-// The norm and the three projections, the rotation and the KV write, the output projection and
-// the residual add each go out as one launch, with the values of the separate kernels.
+// The norm, the three projections, the rotation and the KV write go out as one launch, the output
+// projection and the residual add as another, with the values of the separate kernels.
 extern "C" int trc_modele_couche(trc_modele* m, uint32_t l, uint32_t position, void* flux) {
     if (m == nullptr) return trc::usage("modele nul");
     const trc_hyper& h = m->h;
@@ -155,12 +157,16 @@ extern "C" int trc_modele_couche(trc_modele* m, uint32_t l, uint32_t position, v
         r = (appel);              \
         if (r != TRC_OK) return r; \
     } while (0)
-    // rmsnorm + the q, k, v GEMVs in one launch; then rope_yarn + ecrire_kv in one
+    // the rotation coefficients once per position (every layer shares them), then rmsnorm, the
+    // q, k, v GEMVs, rope_yarn and ecrire_kv in one launch
+    if (m->position_table != int64_t(position)) {
+        TRC_ETAPE(trc::lancer_table_rope(&h.rope, position, m->table, flux));
+        m->position_table = position;
+    }
     const trc_vue w[3] = {c.wq, c.wk, c.wv}, b[3] = {c.bq, c.bk, c.bv}, y[3] = {m->q, m->k, m->v};
     const uint32_t lignes[3] = {dq, dkv, dkv};
-    TRC_ETAPE(trc::lancer_qkv_q8_0(m->x, c.attn_norm, h.eps, d, w, b, y, lignes, flux));
-    TRC_ETAPE(trc::lancer_rope_yarn_kv(m->q, m->k, m->v, c.cache_k, c.cache_v, h.tetes, h.tetes_kv, position,
-                                       an ? position % an : position, &h.rope, flux));
+    TRC_ETAPE(trc::lancer_qkv_q8_0(m->x, c.attn_norm, h.eps, d, w, b, y, lignes, c.cache_k, c.cache_v, m->table,
+                                   an ? position % an : position, flux));
     trc_params_attention pa;
     pa.tetes = h.tetes;
     pa.tetes_kv = h.tetes_kv;

@@ -99,15 +99,13 @@ __device__ inline double inv_freq_yarn(const trc_params_rope& p, uint32_t i, dou
 // row does not depend on it), and each lane issues the loads of DEPLI of its blocks before using
 // them. A block (34 bytes, even address) is read as the 4-byte aligned window that holds it
 // (d at byte 0 or 2 of the window, the codes after it): eight dwords and two halves, realigned by a
-// 64-bit shift. With `residu`, row r adds its y value into residu[r] (residu[r] + y_r, the
-// unweighted combine of one output) instead of storing y. x may be in LDS or global memory.
+// 64-bit shift. The half-wavefront's rows are r0 .. r0 + LIGNES - 1; lane 0 hands each row's sum
+// (bias not added) to `ecrire(r, s)`. x may be in LDS or global memory.
 namespace trc {
-template <uint32_t LIGNES, uint32_t DEPLI>
+template <uint32_t LIGNES, uint32_t DEPLI, class Ecrire>
 __device__ __forceinline__ void gemv_q8_0_rangees(const uint8_t* __restrict__ W, const float* __restrict__ x,
-                                                  const float* __restrict__ biais, float* __restrict__ y,
-                                                  float* __restrict__ residu, uint32_t R, uint32_t C, uint32_t bloc) {
+                                                  uint32_t R, uint32_t C, uint32_t r0, Ecrire ecrire) {
     const uint32_t voie = threadIdx.x & 31u;
-    const uint32_t r0 = (bloc * (FILS_PASSE / 32u) + (threadIdx.x >> 5)) * LIGNES;
     if (r0 >= R) return;
     const uint32_t B = C / 32u;
     const uint64_t octets_ligne = uint64_t(B) * Q8_OCTETS_BLOC;
@@ -180,13 +178,7 @@ __device__ __forceinline__ void gemv_q8_0_rangees(const uint8_t* __restrict__ W,
 #pragma unroll
     for (uint32_t i = 0; i < LIGNES; ++i) {
         const float s = somme_demi_f32(acc[i]);
-        if (voie == 0 && r0 + i < R) {
-            const float v = biais != nullptr ? s + biais[r0 + i] : s;
-            if (residu != nullptr)
-                residu[r0 + i] = residu[r0 + i] + v;
-            else
-                y[r0 + i] = v;
-        }
+        if (voie == 0 && r0 + i < R) ecrire(r0 + i, s);
     }
 }
 
@@ -336,36 +328,119 @@ gemv_q8_0_court(const uint8_t* __restrict__ W, const float* __restrict__ x, cons
                 float* __restrict__ y, float* __restrict__ residu, uint32_t R, uint32_t C) {
     using namespace trc;
     extern __shared__ f32x4 xs[];
+    // y = W x + b, or with `residu`, residu[r] = residu[r] + (W x + b)[r] (the unweighted combine
+    // of one output) instead of storing y
+    auto ecrire = [&](uint32_t r, float s) {
+        const float v = biais != nullptr ? s + biais[r] : s;
+        if (residu != nullptr)
+            residu[r] = residu[r] + v;
+        else
+            y[r] = v;
+    };
+    const uint32_t r0 = blockIdx.x * lignes_bloc<1>() + (threadIdx.x >> 5);
     if (C <= QKV_COLONNES_MAX) {
         x_vers_lds(x, xs, C);
-        gemv_q8_0_rangees<1, 4>(W, reinterpret_cast<const float*>(xs), biais, y, residu, R, C, blockIdx.x);
+        gemv_q8_0_rangees<1, 4>(W, reinterpret_cast<const float*>(xs), R, C, r0, ecrire);
     } else {
-        gemv_q8_0_rangees<1, 4>(W, x, biais, y, residu, R, C, blockIdx.x);
+        gemv_q8_0_rangees<1, 4>(W, x, R, C, r0, ecrire);
     }
 }
 
-// The attention projections of one layer in one launch: each block takes the RMSNorm of x with
-// `norme` into LDS (the same values as rmsnorm), then its rows of q, k or v (blocks in that order),
-// one row per half-wavefront as in gemv_q8_0_court.
+namespace trc {
+// YaRN rotation (NEOX halves) of pair i < d/2 of head xh, in place: o1 = x1 c - x2 s,
+// o2 = x2 c + x1 s, c and s the cosine and sine of position * inv_freq_i times the concentration,
+// all in f64 (passe.cuh:261-284).
+// The pair's coefficients: c and s times the concentration, in f64.
+__device__ __forceinline__ void coefficients_paire(uint32_t i, uint32_t position, const trc_params_rope& p, double& c,
+                                                   double& s) {
+    double m;
+    const double inv = inv_freq_yarn(p, i, m);
+    sincos(double(position) * inv, &s, &c);
+    c *= m;
+    s *= m;
+}
+__device__ __forceinline__ void rotation_paire(float x1, float x2, double c, double s, float& o1, float& o2) {
+    const double a = x1, b = x2;
+    o1 = float(a * c - b * s);
+    o2 = float(b * c + a * s);
+}
+__device__ __forceinline__ void tourner_paire(float* xh, uint32_t i, uint32_t position, const trc_params_rope& p,
+                                              float& o1, float& o2) {
+    const uint32_t demi = p.dim_tete / 2u;
+    double c, sn;
+    coefficients_paire(i, position, p, c, sn);
+    rotation_paire(xh[i], xh[i + demi], c, sn, o1, o2);
+    xh[i] = o1;
+    xh[i + demi] = o2;
+}
+}  // namespace trc
+
+// The rotation coefficients of one position, (c, s) for pairs 0 .. d/2 - 1 (the same for every
+// layer: computed once per position by the decode-step driver).
+extern "C" __global__ void __launch_bounds__(64)
+table_rope(trc_params_rope p, uint32_t position, double* __restrict__ table) {
+    const uint32_t i = threadIdx.x;
+    if (i >= p.dim_tete / 2u) return;
+    double c, s;
+    trc::coefficients_paire(i, position, p, c, s);
+    table[2u * i] = c;
+    table[2u * i + 1u] = s;
+}
+
+// The attention projections of one layer in one launch, with the YaRN rotation and the KV write:
+// each block takes the RMSNorm of x with `norme` into LDS (the same values as rmsnorm), then
+//  - q or k (heads of 64 rows): block b of head h takes the four row pairs (i, i + 32),
+//    i = 4b .. 4b + 3, one row per half-wavefront; the eight values (bias added) meet in LDS and
+//    four threads rotate the pairs with the position's coefficients (table_rope: rope_yarn's
+//    arithmetic) into y, and for k also into the cache slot, rounded to f16 (ecrire_kv);
+//  - v: eight consecutive rows into y and, rounded to f16, into the cache slot.
+// The values are those of rmsnorm, three gemv_q8_0, rope_yarn and ecrire_kv.
 extern "C" __global__ void __launch_bounds__(trc::FILS_PASSE)
-qkv_q8_0(const float* __restrict__ x, const float* __restrict__ norme, float eps, uint32_t C, trc::Q8Projections m) {
+qkv_q8_0(const float* __restrict__ x, const float* __restrict__ norme, float eps, uint32_t C, trc::Q8Projections m,
+         uint16_t* __restrict__ cache_k, uint16_t* __restrict__ cache_v, const double* __restrict__ table,
+         uint32_t case_kv) {
     using namespace trc;
     extern __shared__ f32x4 hh4[];
     __shared__ double part[FILS_PASSE];
     __shared__ double total;
+    __shared__ float paires[8];
     float* hh = reinterpret_cast<float*>(hh4);
     norme_ligne(x, norme, hh, C, eps, part, &total);
     __syncthreads();
-    uint32_t bloc = blockIdx.x, j = 0;
-#pragma unroll
-    for (uint32_t u = 0; u < 2; ++u) {
-        const uint32_t nb = (m.lignes[j] + lignes_bloc<1>() - 1u) / lignes_bloc<1>();
-        if (bloc >= nb) {
-            bloc -= nb;
-            ++j;
+    const uint32_t hw = threadIdx.x >> 5;  // half-wavefront 0..7
+    const uint32_t nbq = m.lignes[0] / 8u, nbk = m.lignes[1] / 8u, dkv = m.lignes[1];
+    uint32_t bloc = blockIdx.x;
+    if (bloc < nbq + nbk) {
+        const uint32_t j = bloc < nbq ? 0u : 1u;
+        if (j == 1u) bloc -= nbq;
+        const uint32_t h = bloc / 8u, b = bloc % 8u;
+        const float* bj = m.biais[j];
+        gemv_q8_0_rangees<1, 4>(m.w[j], hh, m.lignes[j], C, h * 64u + 32u * (hw >> 2) + 4u * b + (hw & 3u),
+                                [&](uint32_t r, float s) { paires[hw] = bj != nullptr ? s + bj[r] : s; });
+        __syncthreads();
+        if (threadIdx.x < 4u) {
+            const uint32_t i = 4u * b + threadIdx.x;
+            float o1, o2;
+            rotation_paire(paires[threadIdx.x], paires[threadIdx.x + 4u], table[2u * i], table[2u * i + 1u], o1, o2);
+            float* yh = m.y[j] + uint64_t(h) * 64u;
+            yh[i] = o1;
+            yh[i + 32u] = o2;
+            if (j == 1u) {
+                const uint64_t base = uint64_t(case_kv) * dkv + uint64_t(h) * 64u;
+                cache_k[base + i] = f32_vers_f16(o1);
+                cache_k[base + i + 32u] = f32_vers_f16(o2);
+            }
         }
+    } else {
+        bloc -= nbq + nbk;
+        const float* bv = m.biais[2];
+        float* yv = m.y[2];
+        gemv_q8_0_rangees<1, 4>(m.w[2], hh, m.lignes[2], C, bloc * 8u + hw, [&](uint32_t r, float s) {
+            const float v = bv != nullptr ? s + bv[r] : s;
+            yv[r] = v;
+            cache_v[uint64_t(case_kv) * dkv + r] = f32_vers_f16(v);
+        });
     }
-    gemv_q8_0_rangees<1, 4>(m.w[j], hh, m.biais[j], m.y[j], nullptr, m.lignes[j], C, bloc);
 }
 
 // Row `ligne` of a Q8_0 matrix -> f32, exact (d has 11 significant bits, q 7: passe.cuh:627-637).
@@ -387,26 +462,6 @@ rmsnorm(const float* __restrict__ x, const float* __restrict__ w, float* y, uint
     trc::norme_ligne(x + uint64_t(blockIdx.x) * n, w, y + uint64_t(blockIdx.x) * n, n, eps, part, &total);
 }
 
-namespace trc {
-// YaRN rotation (NEOX halves) of pair i < d/2 of head xh, in place: o1 = x1 c - x2 s,
-// o2 = x2 c + x1 s, c and s the cosine and sine of position * inv_freq_i times the concentration,
-// all in f64 (passe.cuh:261-284).
-__device__ __forceinline__ void tourner_paire(float* xh, uint32_t i, uint32_t position, const trc_params_rope& p,
-                                              float& o1, float& o2) {
-    const uint32_t demi = p.dim_tete / 2u;
-    double m;
-    const double inv = inv_freq_yarn(p, i, m);
-    double s, c;
-    sincos(double(position) * inv, &s, &c);
-    c *= m;
-    s *= m;
-    const double a = xh[i], b = xh[i + demi];
-    o1 = float(a * c - b * s);
-    o2 = float(b * c + a * s);
-    xh[i] = o1;
-    xh[i + demi] = o2;
-}
-}  // namespace trc
 
 // YaRN rotation of one head per block, in place; heads 0 .. tetes_q - 1 are q's, then k's.
 extern "C" __global__ void __launch_bounds__(64)
@@ -418,29 +473,6 @@ rope_yarn(float* __restrict__ q, float* __restrict__ k, uint32_t tetes_q, uint32
                                      : k + uint64_t(blockIdx.x - tetes_q) * p.dim_tete;
     float o1, o2;
     trc::tourner_paire(xh, i, position, p, o1, o2);
-}
-
-// rope_yarn then ecrire_kv in one launch (head dimension at most 64): the block of k head j also
-// writes that head's rotated k and v's head j, rounded to f16, into slot case_kv of the caches.
-extern "C" __global__ void __launch_bounds__(64)
-rope_yarn_kv(float* __restrict__ q, float* __restrict__ k, const float* __restrict__ v,
-             uint16_t* __restrict__ cache_k, uint16_t* __restrict__ cache_v, uint32_t tetes_q, uint32_t tetes_k,
-             uint32_t position, uint32_t case_kv, trc_params_rope p) {
-    const uint32_t i = threadIdx.x, dt = p.dim_tete, demi = dt / 2u;
-    if (blockIdx.x >= tetes_q + tetes_k) return;
-    const bool cle = blockIdx.x >= tetes_q;
-    const uint32_t j = cle ? blockIdx.x - tetes_q : blockIdx.x;
-    float* xh = (cle ? k : q) + uint64_t(j) * dt;
-    const uint64_t base = (uint64_t(case_kv) * tetes_k + j) * dt;
-    if (i < demi) {
-        float o1, o2;
-        trc::tourner_paire(xh, i, position, p, o1, o2);
-        if (cle) {
-            cache_k[base + i] = trc::f32_vers_f16(o1);
-            cache_k[base + i + demi] = trc::f32_vers_f16(o2);
-        }
-    }
-    if (cle && i < dt) cache_v[base + i] = trc::f32_vers_f16(v[uint64_t(j) * dt + i]);
 }
 
 // k and v rounded to f16 (nearest even) into slot case_kv of the caches (passe.cuh:286-296).
@@ -792,51 +824,48 @@ extern "C" int trc_argmax(trc_vue v, uint32_t n, trc_vue sortie, void* flux) {
 
 // ============================================================================ fused launches of the native driver
 // No reference counterpart: the decode-step driver issues these in place of rmsnorm + three
-// gemv_q8_0, rope_yarn + ecrire_kv and gemv_q8_0 + combiner; the values are the same.
+// gemv_q8_0 + rope_yarn + ecrire_kv, and gemv_q8_0 + combiner; the values are the same.
 namespace trc {
 
 int lancer_qkv_q8_0(trc_vue x, trc_vue norme, float eps, uint32_t colonnes, const trc_vue w[3],
-                    const trc_vue biais[3], const trc_vue y[3], const uint32_t lignes[3], void* flux) {
+                    const trc_vue biais[3], const trc_vue y[3], const uint32_t lignes[3], trc_vue cache_k,
+                    trc_vue cache_v, trc_vue table, uint32_t case_kv, void* flux) {
     TRC_VERIFIER(colonnes > 0 && colonnes % 32 == 0 && colonnes <= QKV_COLONNES_MAX, "qkv : %u colonnes", colonnes);
     TRC_VERIFIER(x.adresse && norme.adresse && x.octets >= 4ull * colonnes && norme.octets >= 4ull * colonnes,
                  "qkv : x ou norme trop court");
+    TRC_VERIFIER(table.adresse && table.adresse % 8 == 0 && table.octets >= 16 * 32, "qkv : table de rotation");
+    TRC_VERIFIER(lignes[0] > 0 && lignes[0] % 64 == 0 && lignes[1] > 0 && lignes[1] % 64 == 0 && lignes[2] == lignes[1],
+                 "qkv : %u / %u / %u lignes (tetes de 64, v comme k)", lignes[0], lignes[1], lignes[2]);
+    const uint64_t fin = 2ull * (uint64_t(case_kv) + 1) * lignes[1];
+    TRC_VERIFIER(cache_k.adresse && cache_v.adresse && cache_k.octets >= fin && cache_v.octets >= fin,
+                 "qkv : case %u hors du cache", case_kv);
     Q8Projections m;
     uint32_t blocs = 0;
     for (int j = 0; j < 3; ++j) {
         const uint64_t octets = uint64_t(lignes[j]) * (colonnes / 32) * Q8_OCTETS_BLOC;
-        TRC_VERIFIER(lignes[j] > 0 && w[j].adresse && w[j].octets >= octets && w[j].adresse % 2 == 0,
-                     "qkv : matrice %d", j);
+        TRC_VERIFIER(w[j].adresse && w[j].octets >= octets && w[j].adresse % 2 == 0, "qkv : matrice %d", j);
         TRC_VERIFIER(y[j].adresse && y[j].octets >= 4ull * lignes[j], "qkv : sortie %d trop courte", j);
         TRC_VERIFIER(biais[j].adresse == 0 || biais[j].octets >= 4ull * lignes[j], "qkv : biais %d trop court", j);
         m.w[j] = reinterpret_cast<const uint8_t*>(w[j].adresse);
         m.biais[j] = reinterpret_cast<const float*>(biais[j].adresse);
         m.y[j] = reinterpret_cast<float*>(y[j].adresse);
         m.lignes[j] = lignes[j];
-        blocs += (lignes[j] + lignes_bloc<1>() - 1) / lignes_bloc<1>();
+        blocs += lignes[j] / 8;
     }
     hipLaunchKernelGGL(qkv_q8_0, dim3(blocs), dim3(FILS_PASSE), 4u * colonnes, flux_de(flux),
                        reinterpret_cast<const float*>(x.adresse), reinterpret_cast<const float*>(norme.adresse), eps,
-                       colonnes, m);
+                       colonnes, m, reinterpret_cast<uint16_t*>(cache_k.adresse),
+                       reinterpret_cast<uint16_t*>(cache_v.adresse), reinterpret_cast<const double*>(table.adresse),
+                       case_kv);
     return apres_lancement("qkv_q8_0");
 }
 
-int lancer_rope_yarn_kv(trc_vue q, trc_vue k, trc_vue v, trc_vue cache_k, trc_vue cache_v, uint32_t tetes_q,
-                        uint32_t tetes_k, uint32_t position, uint32_t case_kv, const trc_params_rope* p, void* flux) {
-    TRC_VERIFIER(p && p->dim_tete > 0 && p->dim_tete % 2 == 0 && p->dim_tete <= 64 && p->variante <= 1,
-                 "rope_kv : parametres");
-    TRC_VERIFIER(tetes_q > 0 && tetes_k > 0, "rope_kv : tetes %u / %u", tetes_q, tetes_k);
-    const uint64_t dq = uint64_t(tetes_q) * p->dim_tete, dkv = uint64_t(tetes_k) * p->dim_tete;
-    const uint64_t fin = 2ull * (uint64_t(case_kv) + 1) * dkv;
-    TRC_VERIFIER(q.adresse && k.adresse && v.adresse && q.octets >= 4 * dq && k.octets >= 4 * dkv &&
-                     v.octets >= 4 * dkv,
-                 "rope_kv : q, k ou v trop court");
-    TRC_VERIFIER(cache_k.adresse && cache_v.adresse && cache_k.octets >= fin && cache_v.octets >= fin,
-                 "rope_kv : case %u hors du cache", case_kv);
-    hipLaunchKernelGGL(rope_yarn_kv, dim3(tetes_q + tetes_k), dim3(64), 0, flux_de(flux),
-                       reinterpret_cast<float*>(q.adresse), reinterpret_cast<float*>(k.adresse),
-                       reinterpret_cast<const float*>(v.adresse), reinterpret_cast<uint16_t*>(cache_k.adresse),
-                       reinterpret_cast<uint16_t*>(cache_v.adresse), tetes_q, tetes_k, position, case_kv, *p);
-    return apres_lancement("rope_yarn_kv");
+int lancer_table_rope(const trc_params_rope* p, uint32_t position, trc_vue table, void* flux) {
+    TRC_VERIFIER(p && p->dim_tete == 64 && p->variante <= 1, "table de rotation : tetes de 64 seulement");
+    TRC_VERIFIER(table.adresse && table.adresse % 8 == 0 && table.octets >= 16 * 32, "table de rotation trop courte");
+    hipLaunchKernelGGL(table_rope, dim3(1), dim3(64), 0, flux_de(flux), *p, position,
+                       reinterpret_cast<double*>(table.adresse));
+    return apres_lancement("table_rope");
 }
 
 int lancer_gemv_q8_0_residu(trc_vue w, trc_vue x, trc_vue biais, trc_vue residu, uint32_t lignes, uint32_t colonnes,
