@@ -6,7 +6,7 @@ seeded synthetic MXFP4) sit resident in HBM with a bf16 2880 x 128 router. A ste
 through the MoE layer: router logits, top-4 with softmax weights, the 4 selected experts decoded
 inside their fused GEMVs (gate/up -> SwiGLU -> down), and the weighted combine; the token sweep
 uses 1000 seeded activations, so routing is uniform-random over the 1.45 GB layer. Prints ONE JSON
-line (fields described in DESIGN.md).
+line: metric, value, unit, timing, config, the roofline of the dominant kernel and the CPU baseline.
 
 Other measurement modes (not the driver's line): --config 1 (one down_proj matrix), --config 2 (one
 expert MLP), both rotating over the 128 experts; --config 4 (a token through L resident MoE layers,
@@ -704,7 +704,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for {args.gpus}); the expert-parallel "
-              "sharding across GPUs is described in DESIGN.md, not run.", file=sys.stderr)
+              "sharding across GPUs is a design, not run here.", file=sys.stderr)
         sys.exit(2)
 
     import numpy as np

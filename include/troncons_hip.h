@@ -5,7 +5,7 @@
  * i.e. the methods of `trc_noyaux::Noyaux` (moteur/crates/trc-noyaux/src/lib.rs) and the host
  * helpers of `trc_noyaux::abi` (moteur/crates/trc-noyaux/src/abi.rs). Arguments keep the
  * reference's order and meaning; each declaration cites the function it replaces. A Rust crate
- * binds them with `extern "C"` (see INTEGRATION.md); nothing here uses torch or HIP types.
+ * binds them with `extern "C"`; nothing here uses torch or HIP types.
  *
  * Conventions (mirroring trc_cuda::Erreur, moteur/crates/trc-cuda/src/lib.rs:34-41):
  *   - every launch function returns TRC_OK, TRC_ERREUR_USAGE (a contract violation found before any

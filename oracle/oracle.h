@@ -254,7 +254,8 @@ uint64_t orc_xorshift64s(uint64_t* etat);
 uint16_t orc_bf16_depuis_f32(float f);
 float orc_f32_depuis_bf16(uint16_t h);
 
-/* The synthetic workload of this build, defined once in DESIGN.md:
+/* The synthetic workload of this build (the benchmark configurations: MXFP4 law A, E8M0 in
+ * [119, 125], bf16 N(0, 1) activations, bf16 N(0, 0.02) router):
  * orc_synth_matrice fills blocks17 (R*B x 17) and bias (R f32, bf16-valued) for a
  * (seed, layer, expert, matrix-slot) key; see synth.c for the exact draw order. */
 void orc_synth_matrice(uint64_t graine, uint32_t couche, uint32_t expert, uint32_t cle, uint32_t R, uint32_t C,
