@@ -30,6 +30,8 @@
 #include "erreurs.hpp"
 #include "fusion_corps.hpp"
 #include "selection.hpp"
+#include "norme.hpp"
+#include "passe.hpp"
 
 
 // The layer's LUTs u32[3][4][4096] (reference format) are shared by all jobs of a launch. A
@@ -255,10 +257,13 @@ fusion_finir_combiner(trc::Taches taches) {
 // f32 is exact, so the bits equal gemv_f32 on the widened matrix, passe.cuh:104-130): one row per
 // half-wavefront, lane v taking float4 groups v, v+32, ...; a row's loads are all in flight while
 // the block stages x in LDS. The top-k runs at the start of the DELTA pass.
-template <bool X_LDS>
+// With NORME (x then the raw residual), the block stages RMSNorm(x) with `norme` (norme_ligne: the
+// rmsnorm kernel's bits) instead of x, and block 0 writes it to h2 for the later passes.
+template <bool X_LDS, bool NORME = false>
 __device__ __forceinline__ void routeur_lignes(const uint16_t* __restrict__ W, const float* __restrict__ x,
                                                const float* __restrict__ biais, float* __restrict__ y, uint32_t R,
-                                               uint32_t C, trc::f32x4* xs) {
+                                               uint32_t C, trc::f32x4* xs, const float* __restrict__ norme = nullptr,
+                                               float eps = 0.0f, float* __restrict__ h2 = nullptr) {
     using namespace trc;
     constexpr uint32_t LOT = 24;
     const uint32_t voie = threadIdx.x & 31u;
@@ -270,7 +275,14 @@ __device__ __forceinline__ void routeur_lignes(const uint16_t* __restrict__ W, c
 #pragma unroll
     for (uint32_t i = 0; i < LOT; ++i)
         if (32u * i + voie < C4) w[i] = W4[32u * i + voie];
-    if (X_LDS) {
+    if (NORME) {
+        __shared__ double part[FILS_NORME];
+        __shared__ double total;
+        norme_ligne(x, norme, reinterpret_cast<float*>(xs), C, eps, part, &total);
+        __syncthreads();
+        if (blockIdx.x == 0)
+            for (uint32_t i = threadIdx.x; i < C4; i += blockDim.x) reinterpret_cast<f32x4*>(h2)[i] = xs[i];
+    } else if (X_LDS) {
         for (uint32_t i = threadIdx.x; i < C4; i += blockDim.x) xs[i] = xg[i];
         __syncthreads();
     }
@@ -285,7 +297,7 @@ __device__ __forceinline__ void routeur_lignes(const uint16_t* __restrict__ W, c
         for (uint32_t i = 0; i < LOT; ++i) {
             const uint32_t c = c0 + 32u * i + voie;
             if (c < C4) {
-                const f32x4 xv = X_LDS ? xs[c] : f32x4(xg[c]);
+                const f32x4 xv = X_LDS || NORME ? xs[c] : f32x4(xg[c]);
                 acc = fmaf(__uint_as_float(w[i].x << 16), xv.x, acc);
                 acc = fmaf(__uint_as_float(w[i].x & 0xFFFF0000u), xv.y, acc);
                 acc = fmaf(__uint_as_float(w[i].y << 16), xv.z, acc);
@@ -306,6 +318,18 @@ fusion_routeur(const uint16_t* __restrict__ W, const float* __restrict__ x, cons
         routeur_lignes<true>(W, x, biais, logits, E, C, xs);
     else
         routeur_lignes<false>(W, x, biais, logits, E, C, xs);
+}
+
+// The router over RMSNorm(residual) (C <= X_LDS_MAX): the decode step's post-attention norm folded
+// into the router; block 0 leaves the normed row in h2 for the DELTA and GEMV passes.
+extern "C" __global__ void __launch_bounds__(256)
+fusion_routeur_norme(const uint16_t* __restrict__ W, const float* __restrict__ residu, const float* __restrict__ norme,
+                     float eps, float* __restrict__ h2, const float* __restrict__ biais, float* __restrict__ logits,
+                     uint32_t E, uint32_t C) {
+    using namespace trc;
+    static_assert(FILS_NORME == 256, "one router block runs the norm");
+    __shared__ f32x4 xs[X_LDS_MAX / 4];
+    routeur_lignes<true, true>(W, residu, biais, logits, E, C, xs, norme, eps, h2);
 }
 
 // ---------------------------------------------------------------------------------- layer mount
@@ -580,10 +604,13 @@ extern "C" uint64_t trc_taille_travail_couche_moe(const trc_dims_expert* dims, u
 // block running the top-k first); gate/up CODES pass (2k); down CODES pass (k; builds its x as the
 // SwiGLU of the gate/up rows); finish + combine. No cross-block synchronisation inside a launch.
 // Rows are limited to X_LDS_MAX columns (x in LDS).
-extern "C" int trc_couche_moe_fusionnee(trc_vue repertoire, uint32_t experts, trc_vue luts, const trc_dims_expert* dims,
-                                        trc_vue routeur, trc_vue routeur_biais, trc_vue x, uint32_t k,
-                                        trc_vue residu, trc_vue indices, trc_vue poids, trc_vue controle,
-                                        trc_vue travail, uint32_t n_delta, uint32_t n_codes, void* flux) {
+namespace {
+// The fused MoE layer; with `norme`, the router takes RMSNorm(residu) with `norme` into x first
+// (x is then written, not read, by the router).
+int couche_moe(trc_vue repertoire, uint32_t experts, trc_vue luts, const trc_dims_expert* dims, trc_vue routeur,
+               trc_vue routeur_biais, trc_vue x, uint32_t k, trc_vue residu, trc_vue indices, trc_vue poids,
+               trc_vue controle, trc_vue travail, uint32_t n_delta, uint32_t n_codes, trc_vue norme, float eps,
+               void* flux) {
     int r = verifier_forme(dims, n_codes);
     if (r != TRC_OK) return r;
     const uint32_t R = dims->lignes[0], C = dims->colonnes[0], D = dims->lignes[2];
@@ -645,9 +672,18 @@ extern "C" int trc_couche_moe_fusionnee(trc_vue repertoire, uint32_t experts, tr
     const hipStream_t f = flux_de(flux);
     auto ctl = reinterpret_cast<uint32_t*>(controle.adresse);
     const uint32_t* l = reinterpret_cast<const uint32_t*>(luts.adresse);
-    TRC_LANCER(fusion_routeur, dim3((experts + 7) / 8), dim3(256), f,
-               reinterpret_cast<const uint16_t*>(routeur.adresse), reinterpret_cast<const float*>(x.adresse),
-               reinterpret_cast<const float*>(routeur_biais.adresse), reinterpret_cast<float*>(logits), experts, C);
+    if (norme.adresse != 0) {
+        TRC_VERIFIER(norme.octets >= 4ull * C, "norme trop courte");
+        TRC_VERIFIER(residu.adresse % 16 == 0 && residu.adresse != x.adresse, "residu non aligne ou confondu avec x");
+        TRC_LANCER(fusion_routeur_norme, dim3((experts + 7) / 8), dim3(256), f,
+                   reinterpret_cast<const uint16_t*>(routeur.adresse), reinterpret_cast<const float*>(residu.adresse),
+                   reinterpret_cast<const float*>(norme.adresse), eps, reinterpret_cast<float*>(x.adresse),
+                   reinterpret_cast<const float*>(routeur_biais.adresse), reinterpret_cast<float*>(logits), experts, C);
+    } else {
+        TRC_LANCER(fusion_routeur, dim3((experts + 7) / 8), dim3(256), f,
+                   reinterpret_cast<const uint16_t*>(routeur.adresse), reinterpret_cast<const float*>(x.adresse),
+                   reinterpret_cast<const float*>(routeur_biais.adresse), reinterpret_cast<float*>(logits), experts, C);
+    }
     TRC_LANCER(fusion_echelles, dim3(grille_tuiles(uint64_t(R) * (C / 32), n_delta, TUILES_ECHELLES), 3 * k),
                dim3(trc::FILS_ECHELLES_FUSION), f, t_delta, l, ctl);
     TRC_LANCER_N("fusion_gemv/gate_up", fusion_gemv, forme_gemv(R, C, n_codes, 2 * k).grille,
@@ -656,4 +692,22 @@ extern "C" int trc_couche_moe_fusionnee(trc_vue repertoire, uint32_t experts, tr
                  forme_gemv(D, R, n_codes, k).bloc, f, t_bas, l, ctl);
     TRC_LANCER(fusion_finir_combiner, dim3((D + 255) / 256), dim3(256), f, t_bas);
     return TRC_OK;
+}
+}  // namespace
+
+extern "C" int trc_couche_moe_fusionnee(trc_vue repertoire, uint32_t experts, trc_vue luts, const trc_dims_expert* dims,
+                                        trc_vue routeur, trc_vue routeur_biais, trc_vue x, uint32_t k,
+                                        trc_vue residu, trc_vue indices, trc_vue poids, trc_vue controle,
+                                        trc_vue travail, uint32_t n_delta, uint32_t n_codes, void* flux) {
+    return couche_moe(repertoire, experts, luts, dims, routeur, routeur_biais, x, k, residu, indices, poids, controle,
+                      travail, n_delta, n_codes, trc_vue{0, 0}, 0.0f, flux);
+}
+
+int trc::lancer_couche_moe_normee(trc_vue repertoire, uint32_t experts, trc_vue luts, const trc_dims_expert* dims,
+                                  trc_vue routeur, trc_vue routeur_biais, trc_vue norme, float eps, trc_vue h2,
+                                  uint32_t k, trc_vue residu, trc_vue indices, trc_vue poids, trc_vue controle,
+                                  trc_vue travail, uint32_t n_delta, uint32_t n_codes, void* flux) {
+    TRC_VERIFIER(norme.adresse != 0, "norme absente");
+    return couche_moe(repertoire, experts, luts, dims, routeur, routeur_biais, h2, k, residu, indices, poids, controle,
+                      travail, n_delta, n_codes, norme, eps, flux);
 }

@@ -179,9 +179,10 @@ extern "C" int trc_modele_couche(trc_modele* m, uint32_t l, uint32_t position, v
     TRC_ETAPE(trc_attention(m->q, c.cache_k, c.cache_v, c.puits, m->a, &pa, flux));
     // the output projection adds itself into the residual (gemv_q8_0 + combiner)
     TRC_ETAPE(trc::lancer_gemv_q8_0_residu(c.wo, m->a, c.bo, m->x, d, dq, flux));
-    TRC_ETAPE(trc_rmsnorm(m->x, c.post_norm, m->h2, d, 1, h.eps, flux));
-    TRC_ETAPE(trc_couche_moe_fusionnee(c.repertoire, h.experts, c.luts, &h.dims, c.routeur, c.routeur_biais, m->h2,
-                                       h.actifs, m->x, m->idx, m->pw, m->controle, m->moe, h.n_delta, h.n_codes, flux));
+    // the post-attention norm goes into the MoE router's launch, which leaves h2 for the later passes
+    TRC_ETAPE(trc::lancer_couche_moe_normee(c.repertoire, h.experts, c.luts, &h.dims, c.routeur, c.routeur_biais,
+                                            c.post_norm, h.eps, m->h2, h.actifs, m->x, m->idx, m->pw, m->controle,
+                                            m->moe, h.n_delta, h.n_codes, flux));
 #undef TRC_ETAPE
     return TRC_OK;
 }

@@ -14,12 +14,14 @@
 
 #include "commun.hpp"
 #include "erreurs.hpp"
+#include "norme.hpp"
 #include "passe.hpp"
 
 namespace trc {
 
 constexpr uint32_t Q8_OCTETS_BLOC = 34;  // f16 d, then 32 x i8 (ggml Q8_0)
 constexpr uint32_t FILS_PASSE = 256;
+static_assert(FILS_PASSE == FILS_NORME, "rmsnorm and the Q/K/V launch run the norm with its block size");
 constexpr uint32_t FILS_ARGMAX = 1024;
 constexpr uint32_t ATTENTION_DIM = 64;
 constexpr uint32_t ATTENTION_POSITIONS_MAX = TRC_ATTENTION_POSITIONS_MAX;
@@ -195,61 +197,6 @@ __device__ __forceinline__ void x_vers_lds(const float* __restrict__ x, f32x4* x
     __syncthreads();
 }
 
-// Sum of the block's 256 f64 values by the fixed tree (level k: value t += value t + k for t < k,
-// k = 128 .. 1): levels 128 and 64 in LDS, levels 32 .. 1 as shuffles in wave 0 (lane t adds lane
-// t + k, the same association). Every thread gets the sum.
-__device__ __forceinline__ double somme_arbre_f64(double* part, double* total, double v) {
-    const uint32_t t = threadIdx.x;
-    part[t] = v;
-    __syncthreads();
-    if (t < 64u) {
-        double u = (part[t] + part[t + 128u]) + (part[t + 64u] + part[t + 192u]);
-#pragma unroll
-        for (uint32_t k = 32; k > 0; k >>= 1) u += __shfl_down(u, k, 64);
-        if (t == 0) *total = u;
-    }
-    __syncthreads();
-    return *total;
-}
-
-// RMSNorm of one row of n: thread t adds x_i^2 for i = t, t + 256, ... (f64 fma), fixed tree,
-// r = 1/sqrt(sum/n + eps), y_i = (x_i r) w_i in f64, rounded once (passe.cuh:235-259). x is read
-// in full before the first write (y may be x). Up to NORME_PAR_FIL * 256 elements a thread holds
-// its x and w values in registers, so all its loads go out together.
-constexpr uint32_t NORME_PAR_FIL = 16;
-__device__ __forceinline__ void norme_ligne(const float* __restrict__ x, const float* __restrict__ w, float* y,
-                                            uint32_t n, float eps, double* part, double* total) {
-    const uint32_t t = threadIdx.x;
-    if (n <= NORME_PAR_FIL * FILS_PASSE) {
-        // indices clamped to the row (no branch around a load, so none waits for another); the
-        // copies past the row are not used
-        float xv[NORME_PAR_FIL], wv[NORME_PAR_FIL];
-#pragma unroll
-        for (uint32_t u = 0; u < NORME_PAR_FIL; ++u) {
-            const uint32_t i = min(t + u * FILS_PASSE, n - 1u);
-            xv[u] = x[i];
-            wv[u] = w[i];
-        }
-        double s = 0.0;
-#pragma unroll
-        for (uint32_t u = 0; u < NORME_PAR_FIL; ++u)
-            if (t + u * FILS_PASSE < n) s = fma(double(xv[u]), double(xv[u]), s);
-        const double r = 1.0 / sqrt(somme_arbre_f64(part, total, s) / double(n) + double(eps));
-#pragma unroll
-        for (uint32_t u = 0; u < NORME_PAR_FIL; ++u) {
-            const uint32_t i = t + u * FILS_PASSE;
-            if (i < n) y[i] = float(double(xv[u]) * r * double(wv[u]));
-        }
-        return;
-    }
-    double s = 0.0;
-    for (uint32_t i = t; i < n; i += FILS_PASSE) {
-        const double v = x[i];
-        s = fma(v, v, s);
-    }
-    const double r = 1.0 / sqrt(somme_arbre_f64(part, total, s) / double(n) + double(eps));
-    for (uint32_t i = t; i < n; i += FILS_PASSE) y[i] = float(double(x[i]) * r * double(w[i]));
-}
 }  // namespace trc
 
 // One launch of y = W x (+ b). gemv_q8_0: four rows per half-wavefront, x read from global memory

@@ -25,4 +25,12 @@ int lancer_qkv_q8_0(trc_vue x, trc_vue norme, float eps, uint32_t colonnes, cons
 int lancer_gemv_q8_0_residu(trc_vue w, trc_vue x, trc_vue biais, trc_vue residu, uint32_t lignes, uint32_t colonnes,
                             void* flux);
 
+// (fusion.hip) trc_couche_moe_fusionnee over RMSNorm(residu) with `norme`: the router launch
+// takes the norm (the rmsnorm kernel's bits) and leaves it in h2, which the later passes read as
+// their x; residu then receives the combine. The post-attention norm and the MoE half in one.
+int lancer_couche_moe_normee(trc_vue repertoire, uint32_t experts, trc_vue luts, const trc_dims_expert* dims,
+                             trc_vue routeur, trc_vue routeur_biais, trc_vue norme, float eps, trc_vue h2, uint32_t k,
+                             trc_vue residu, trc_vue indices, trc_vue poids, trc_vue controle, trc_vue travail,
+                             uint32_t n_delta, uint32_t n_codes, void* flux);
+
 }  // namespace trc
