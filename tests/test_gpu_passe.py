@@ -74,6 +74,25 @@ def test_gemv_q8_0_unaligned_matrix_and_last_block(k):
         assert (hote(y, np.float32).view(np.uint32) == O.gemv_q8_0(o, x, None, r, c).view(np.uint32)).all()
 
 
+@pytest.mark.parametrize("r,c,decalage", [(32769, 96, 0), (32770, 96, 2), (40000, 2880, 0), (32800, 2880, 2)])
+def test_gemv_q8_0_large_matrices(k, r, c, decalage):
+    """From 32768 rows the launch takes four rows per half-wavefront (the output head's kernel):
+    bit-identical to the oracle, with the matrix at a 4-byte boundary or 2 bytes past one, and
+    ending 2 bytes into a dword (32769 x 96 aligned, 32770 x 96 offset) or on one."""
+    rng = np.random.default_rng(r + decalage)
+    nb = c // 32
+    d = (rng.standard_normal(r * nb) * 0.05).astype(np.float16)
+    q = rng.integers(-128, 128, size=(r * nb, 32)).astype(np.int8)
+    o = np.concatenate([d.view(np.uint8).reshape(-1, 2), q.view(np.uint8)], axis=1).ravel()
+    x = rng.standard_normal(c).astype(np.float32)
+    base = zeros(o.size + decalage)
+    base[decalage:].copy_(torch.from_numpy(o.copy()).to(base.device))
+    b = rng.standard_normal(r).astype(np.float32)
+    y = zeros(4 * r)
+    k.gemv_q8_0(vue(base, decalage, o.size), vue(dev(x)), vue(dev(b)), vue(y), r, c)
+    assert (hote(y, np.float32).view(np.uint32) == O.gemv_q8_0(o, x, b, r, c).view(np.uint32)).all()
+
+
 def test_ligne_q8_0_exact(k):
     a = Alea(7)
     lignes, c = 5, 64

@@ -241,8 +241,11 @@ gemv_q8_0(const uint8_t* __restrict__ W, const float* __restrict__ x, const floa
             uint32_t w[9];
 #pragma unroll
             for (uint32_t t = 0; t < 8; ++t) w[t] = fen[t];
-            // past the block by 2 bytes when d sits at byte 0: the matrix's last block reads 16 bits
-            w[8] = a4 + 36u <= fin_matrice ? fen[8] : uint32_t(reinterpret_cast<const uint16_t*>(fen + 8)[0]);
+            // dword 8 as two halves: the high one lies past the block when d sits at byte 0 and is
+            // then unused, so its address is clamped to the matrix (no branch around a load)
+            const uint16_t* h8 = reinterpret_cast<const uint16_t*>(fen + 8);
+            const uint16_t* h9 = reinterpret_cast<const uint16_t*>(min(a4 + 34u, fin_matrice - 2u));
+            w[8] = uint32_t(h8[0]) | (uint32_t(h9[0]) << 16);
             const float d = f16_vers_f32(decal ? (w[0] >> 16) : (w[0] & 0xFFFFu));
             const uint32_t bits = 8u * (2u + decal);
             float s = 0.0f;
