@@ -117,6 +117,26 @@ def test_decode_steps_equal_the_oracle_chain(graine):
     assert (m.controles() == 0).all() and (mn.controles_natif() == 0).all()
 
 
+def test_decode_step_head_from_32768_rows():
+    """A vocabulary of 33001 rows takes the head through the four-rows-per-half-wavefront GEMV: the
+    logits equal the oracle's Q8_0 GEMV of the normed row the step left in hh, bit for bit, and the
+    native driver's logits equal the Python driver's."""
+    from gpu_outils import hote
+    h = _hyper(vocab=33001, couches=1)
+    couches, emb, norme, sortie = Mo.poids_synthetiques(h, 2042)
+    m = Mo.Modele(h, couches, emb, norme, sortie)
+    mn = Mo.Modele(h, couches, emb, norme, sortie)
+    for pos, tok in enumerate([7, 33000, 12345]):
+        print(f"position {pos}", flush=True)
+        m.pas(tok, pos)
+        z = m.logits()
+        hh = hote(m.hh, np.float32)
+        assert (O.gemv_q8_0(sortie, hh, None, h.vocab, h.d).view(np.uint32) == z.view(np.uint32)).all(), pos
+        mn.pas_natif(tok, pos)
+        assert (mn.logits_natif().view(np.uint32) == z.view(np.uint32)).all(), pos
+        assert mn.jeton_natif() == m.jeton()
+
+
 def test_model_refuses_position_past_context():
     from troncons_amd.noyaux import ErreurUsage
     h = _hyper(couches=1, contexte=4)
