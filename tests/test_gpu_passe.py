@@ -74,6 +74,21 @@ def test_gemv_q8_0_unaligned_matrix_and_last_block(k):
         assert (hote(y, np.float32).view(np.uint32) == O.gemv_q8_0(o, x, None, r, c).view(np.uint32)).all()
 
 
+def test_gemv_q8_0_wide_rows_read_x_from_global_memory(k):
+    """Past 16384 columns x does not fit the LDS staging: the short launch reads it from global
+    memory, with the same values."""
+    rng = np.random.default_rng(16416)
+    r, c = 40, 16416
+    nb = c // 32
+    d = (rng.standard_normal(r * nb) * 0.05).astype(np.float16)
+    q = rng.integers(-128, 128, size=(r * nb, 32)).astype(np.int8)
+    o = np.concatenate([d.view(np.uint8).reshape(-1, 2), q.view(np.uint8)], axis=1).ravel()
+    x = rng.standard_normal(c).astype(np.float32)
+    y = zeros(4 * r)
+    k.gemv_q8_0(vue(dev(o)), vue(dev(x)), None, vue(y), r, c)
+    assert (hote(y, np.float32).view(np.uint32) == O.gemv_q8_0(o, x, None, r, c).view(np.uint32)).all()
+
+
 @pytest.mark.parametrize("r,c,decalage", [(32769, 96, 0), (32770, 96, 2), (40000, 2880, 0), (32800, 2880, 2)])
 def test_gemv_q8_0_large_matrices(k, r, c, decalage):
     """From 32768 rows the launch takes four rows per half-wavefront (the output head's kernel):
@@ -140,7 +155,8 @@ def test_rmsnorm_bit_exact_and_in_place(k):
     k.rmsnorm(vue(xd), vue(wd), vue(xd), n, 2, 1e-5)  # y = x
     assert (hote(xd, np.float32).view(np.uint32) == ref.view(np.uint32)).all()
     rng = np.random.default_rng(4)
-    for n2, l2 in ((64, 64), (4096, 3), (1000, 1)):
+    # up to 4096 a thread keeps its values in registers; past it the loop form (5000, 8191)
+    for n2, l2 in ((64, 64), (4096, 3), (1000, 1), (5000, 2), (8191, 1)):
         x2 = rng.standard_normal(n2 * l2).astype(np.float32)
         w2 = rng.standard_normal(n2).astype(np.float32)
         y2 = zeros(4 * n2 * l2)
