@@ -230,23 +230,6 @@ def baseline_cpu(couche, luts, x_tok, selections, budget_s: float, n_fils: int):
     }
 
 
-def routage_zipf(graine, T, E, k, a=1.1):
-    """Config 5 routing: per position k distinct experts drawn from Zipf(a) over the E expert ranks
-    without replacement (rank r = expert r), and softmax weights of seeded logits (f64, rounded once)."""
-    import numpy as np
-    rng = np.random.default_rng(graine)
-    p = 1.0 / np.arange(1, E + 1, dtype=np.float64) ** a
-    p /= p.sum()
-    idx = np.zeros((T, k), np.uint32)
-    w = np.zeros((T, k), np.float32)
-    for i in range(T):
-        idx[i] = rng.choice(E, size=k, replace=False, p=p)
-        lg = np.sort(rng.standard_normal(k))[::-1]
-        ex = np.exp(lg - lg[0])
-        w[i] = (ex / ex.sum()).astype(np.float32)
-    return idx, w
-
-
 def baseline_cpu_prefill(couche, luts, x_tok, idx, budget_s: float):
     """The reference's CPU path for a prefill batch, timed on a sample and scaled: one
     decoder_matrice_v10 of every distinct chosen expert, then per (position, slot) the f32 GEMV chain
@@ -298,7 +281,7 @@ def bench_prefill(args, c0, dims, E, k, C, fz, flux, dev, espace, x_tok, n_fils)
     from troncons_amd.noyaux import VueCarte
     V = VueCarte.de
     T = args.positions
-    idx, w = routage_zipf(args.graine + 5, T, E, k)
+    idx, w = codeur.routage_zipf(args.graine + 5, T, E, k)
     xs = np.stack([codeur.synth_normale_bf16(args.graine, 6, t, C, 1.0) for t in range(T)])
     xd = torch.from_numpy(xs).to(dev)
     idd = torch.from_numpy(idx.view(np.int32)).to(dev)

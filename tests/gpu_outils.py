@@ -72,3 +72,42 @@ class Expert:
             O.blocs_vers_soa(self.blocs[j], self.dims.lignes[j], self.dims.colonnes[j], self.biais[j], canonique=False)
             for j in range(3)])
         return p, attendu
+
+
+# Doubled E2M1 magnitudes (codes 0-7; bit 3 is the sign): the reference's k table.
+K_E2M1X2 = np.array([0.0, 1.0, 2.0, 3.0, 4.0, 6.0, 8.0, 12.0])
+
+
+def poids_f64(blocs17: np.ndarray, R: int, C_: int) -> np.ndarray:
+    """The R x C matrix of an uncompressed MXFP4 matrix (17-byte blocks: E8M0 scale, then 16 code
+    bytes, byte i = weight i in its low nibble and weight 16 + i in its high one) in f64:
+    k[c & 7] * (-1 if c & 8) * 2^(e - 128). Code 8 reads as 0, as in the reference."""
+    b = np.asarray(blocs17, np.uint8).reshape(R * (C_ // 32), 17)
+    qs = b[:, 1:]
+    codes = np.empty((b.shape[0], 32), np.uint8)
+    codes[:, :16] = qs & 15
+    codes[:, 16:] = qs >> 4
+    v = K_E2M1X2[codes & 7] * np.where(codes & 8, -1.0, 1.0)
+    v *= np.ldexp(1.0, b[:, 0].astype(np.int32) - 128)[:, None]
+    return v.reshape(R, C_)
+
+
+def mlp_f64(blocs, biais, X: np.ndarray) -> np.ndarray:
+    """gpt-oss expert MLP in f64 from uncompressed weights, for the columns of X (C x n):
+    down(swiglu_oai(gate X + b_g, up X + b_u)) + b_d, SwiGLU with alpha 1.702, limit 7, up + 1."""
+    R, C_ = biais[0].size, X.shape[0]
+    g = poids_f64(blocs[0], R, C_) @ X + biais[0].astype(np.float64)[:, None]
+    u = poids_f64(blocs[1], R, C_) @ X + biais[1].astype(np.float64)[:, None]
+    g = np.minimum(g, 7.0)
+    u = np.clip(u, -7.0, 7.0)
+    a = g / (1.0 + np.exp(-1.702 * g)) * (u + 1.0)
+    D = biais[2].size
+    return poids_f64(blocs[2], D, R) @ a + biais[2].astype(np.float64)[:, None]
+
+
+def carte_parallele(f, elements, fils: int = 16):
+    """[f(e) for e in elements] on a thread pool (the oracle's and the generator's C calls release
+    the GIL, and so does numpy's BLAS)."""
+    from concurrent.futures import ThreadPoolExecutor
+    with ThreadPoolExecutor(max_workers=fils) as ex:
+        return list(ex.map(f, elements))

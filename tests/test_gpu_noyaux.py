@@ -132,7 +132,7 @@ def test_gemv_bit_exact_and_batch_equals_single_carte_rs_330(k):
         mats.append(O.blocs_vers_soa(bl, r, c, bi, canonique=False))
     pas = mats[0].size
     empl = dev(np.concatenate(mats))
-    xs = (np.random.default_rng(11).integers(0, 5, 3 * c) - 2).astype(np.float32)
+    xs = np.random.default_rng(11).choice(np.array([-2.0, -1.0, 1.0, 2.0], np.float32), 3 * c)
     x = dev(xs)
     y = zeros(12 * r)
     yl = zeros(12 * r)

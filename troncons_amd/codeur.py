@@ -100,6 +100,23 @@ def partie(blocs, biais, freqs, dims: DimsExpert, couche=0, expert=0, canonique=
     return out.tobytes(), u.value
 
 
+def routage_zipf(graine: int, T: int, E: int, k: int, a: float = 1.1):
+    """Config 5 routing: per position k distinct experts drawn from Zipf(a) over the E expert ranks
+    without replacement (rank r = expert r), and the softmax weights of k seeded logits sorted in
+    decreasing order (f64, rounded once to f32). Returns (indices u32[T, k], weights f32[T, k])."""
+    rng = np.random.default_rng(graine)
+    p = 1.0 / np.arange(1, E + 1, dtype=np.float64) ** a
+    p /= p.sum()
+    idx = np.zeros((T, k), np.uint32)
+    w = np.zeros((T, k), np.float32)
+    for i in range(T):
+        idx[i] = rng.choice(E, size=k, replace=False, p=p)
+        lg = np.sort(rng.standard_normal(k))[::-1]
+        ex = np.exp(lg - lg[0])
+        w[i] = (ex / ex.sum()).astype(np.float32)
+    return idx, w
+
+
 class CoucheSynthetique:
     """A synthetic layer: n experts' level-0 parts (v1.2) and the layer's tables."""
 
