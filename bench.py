@@ -23,7 +23,6 @@ import os
 import pathlib
 import struct
 import sys
-import threading
 import time
 
 RACINE = pathlib.Path(__file__).resolve().parent
@@ -34,12 +33,14 @@ PIC_HBM = 8000.0  # GB/s, MI355X
 C_GPT = 2880
 
 
+FICHIER_PMC = RACINE / "profiles" / "moe_config3_pmc.md"
+
+
 def trafic_mesure():
     """HBM bytes per fusion_gemv launch (mean of the two launches) from the committed counter
     summary (two rocprofv3 --pmc runs, FETCH_SIZE then WRITE_SIZE, scaled by a copy kernel), or None."""
-    f = RACINE / "profiles" / "moe_config3_pmc.md"
     try:
-        for ligne in f.read_text().splitlines():
+        for ligne in FICHIER_PMC.read_text().splitlines():
             if ligne.startswith("traffic_per_launch_bytes"):
                 return int(ligne.split("=")[1])
     except (OSError, ValueError):
@@ -180,53 +181,108 @@ class CoucheResidente:
         return VueCarte.de(self.bloc, int(self.decal[e]) + self.o0, int(self.hote.taille(e)))
 
 
-def baseline_cpu(couche, luts, x_tok, selections, budget_s: float, n_fils: int):
+def planifier(selections, n: int, distance: int) -> list:
+    """n token indices of the sweep (selections: [tokens][k] experts, as routed by the layer) in
+    sweep order, cycling, a token being taken only if none of its experts appears in the previous
+    `distance` taken tokens; when a whole cycle of the sweep offers none, the constraint is relaxed
+    for that step (the next token in order is taken)."""
+    T = len(selections)
+    derniere: dict = {}
+    plan: list = []
+    t = 0
+    while len(plan) < n:
+        pris = False
+        for essai in range(T):
+            c = (t + essai) % T
+            if all(len(plan) - derniere.get(int(e), -10**9) > distance for e in selections[c]):
+                pris = True
+                break
+        if not pris:
+            c = t % T
+        for e in selections[c]:
+            derniere[int(e)] = len(plan)
+        plan.append(c)
+        t = c + 1
+    return plan
+
+
+def description_hote() -> dict:
+    """The host the CPU baseline runs on: CPU model, logical CPUs, the CPUs this process may use."""
+    modele = None
+    try:
+        for ligne in pathlib.Path("/proc/cpuinfo").read_text().splitlines():
+            if ligne.startswith("model name"):
+                modele = ligne.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    utilisables = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    return {"cpu_model": modele, "nproc": os.cpu_count(), "usable_cpus": utilisables}
+
+
+def baseline_cpu(couche, luts, selections, budget_s: float, n_fils: int):
     """The reference's CPU path on this host: decoder_matrice_v10 (rANS DELTA + CODES_CTX) then the
-    scalar f32 MXFP4 GEMV in the reference's order, SwiGLU and the ordered combine, for the first
-    tokens of the sweep until ~budget_s of work (single thread), then the same tokens with the 4
-    experts of a token on n_fils threads."""
+    scalar f32 MXFP4 GEMV in the reference's order, SwiGLU and the ordered combine, over the first
+    timed tokens (selections: (experts, weights, x) per token). Timed twice on a steady clock: one
+    thread until ~budget_s / 2 of work, then every (token, expert) of as many tokens on n_fils threads
+    (the experts of a token and the tokens are independent; the reference decoder walks a stream's
+    tiles in order, as the oracle does, so no tile-parallel variant is timed)."""
     sys.path.insert(0, str(RACINE / "tests"))
     import numpy as np
     import oracle_ffi as O
+    from concurrent.futures import ThreadPoolExecutor
 
     # the parts are fetched before the clock starts: the baseline times decode and compute, not reads
-    parts = {e: bytes(couche.partie(e)) for e in sorted({int(e) for idx, _w in selections for e in idx})}
+    parts = {e: bytes(couche.partie(e)) for e in sorted({int(e) for idx, _w, _x in selections for e in idx})}
+    d = [O.disposition_j([2880] * 3, [2880] * 3, j) for j in range(3)]
 
     def expert(e, x):
         slot, ctl = O.decoder_expert(parts[int(e)], luts, [2880] * 3, [2880] * 3)
-        d = [O.disposition_j([2880] * 3, [2880] * 3, j) for j in range(3)]
         g = O.gemv_mxfp4(slot[d[0].base:d[0].base + d[0].pas], x, 2880, 2880)
         u = O.gemv_mxfp4(slot[d[1].base:d[1].base + d[1].pas], x, 2880, 2880)
         a = O.swiglu_oai(g, u)
         return O.gemv_mxfp4(slot[d[2].base:d[2].base + d[2].pas], a, 2880, 2880)
 
-    t0 = time.perf_counter()
-    n_tok = 0
-    octets = 0
-    while n_tok < len(selections) and (time.perf_counter() - t0) < budget_s:
-        idx, w = selections[n_tok]
-        s = [expert(e, x_tok[n_tok]) for e in idx]
-        O.combiner(np.zeros(2880, np.float32), np.concatenate(s), 2880, w, len(idx), 2880)
-        octets += sum(couche.utiles(int(e)) for e in idx)
-        n_tok += 1
-    dt1 = time.perf_counter() - t0
-    # threaded: the 4 experts of a token in parallel (ctypes releases the GIL)
-    t0 = time.perf_counter()
-    for t in range(n_tok):
-        idx, w = selections[t]
-        res = [None] * len(idx)
+    def jeton(t):
+        idx, w, x = selections[t]
+        s = [expert(e, x) for e in idx]
+        return O.combiner(np.zeros(2880, np.float32), np.concatenate(s), 2880, w, len(idx), 2880)
 
-        def tache(i, e, t=t):
-            res[i] = expert(e, x_tok[t])
-        th = [threading.Thread(target=tache, args=(i, e)) for i, e in enumerate(idx)]
-        [h.start() for h in th]
-        [h.join() for h in th]
+    t0 = time.perf_counter()
+    n1 = 0
+    octets1 = 0
+    temps1 = []
+    while n1 < len(selections) and (time.perf_counter() - t0) < budget_s / 2:
+        ti = time.perf_counter()
+        jeton(n1)
+        temps1.append(time.perf_counter() - ti)
+        octets1 += sum(couche.utiles(int(e)) for e in selections[n1][0])
+        n1 += 1
+    dt1 = time.perf_counter() - t0
+    # all cores: (token, expert) tasks of up to len(selections) tokens on n_fils threads, then the
+    # combines; as many tokens as fit in the other half of the budget at the measured rate
+    n_tok = max(1, min(len(selections), int(n_fils * (budget_s / 2) / (dt1 / n1))))
+    taches = [(t, q) for t in range(n_tok) for q in range(len(selections[t][0]))]
+    t0 = time.perf_counter()
+    with ThreadPoolExecutor(max_workers=n_fils) as ex:
+        sorties = list(ex.map(lambda tq: expert(selections[tq[0]][0][tq[1]], selections[tq[0]][2]), taches))
+    for t in range(n_tok):
+        k = len(selections[t][0])
+        s = [sorties[i] for i, (tt, _q) in enumerate(taches) if tt == t]
+        O.combiner(np.zeros(2880, np.float32), np.concatenate(s), 2880, selections[t][1], k, 2880)
     dtn = time.perf_counter() - t0
+    octetsn = sum(couche.utiles(int(e)) for t in range(n_tok) for e in selections[t][0])
     return {
-        "value": dt1 / n_tok * 1e6, "unit": "us/token", "cores": 1, "kind": "port",
-        "gbps_compressed": octets / dt1 / 1e9,
-        "threaded": {"value": dtn / n_tok * 1e6, "unit": "us/token", "cores": min(n_fils, 4)},
-        "sample": f"{n_tok} tokens of the sweep x 4 experts (decode DELTA+CODES_CTX, f32 GEMV x3, SwiGLU, combine)",
+        "value": round(dtn / n_tok * 1e6, 1), "unit": "us/token", "cores": n_fils, "kind": "port",
+        "gbps_compressed": round(octetsn / dtn / 1e9, 4),
+        "sample": f"{n_tok} timed tokens x 4 experts as independent tasks on {n_fils} threads "
+                  "(decode DELTA+CODES_CTX, f32 GEMV x3, SwiGLU), then the ordered combines",
+        "single_core": {"value": round(dt1 / n1 * 1e6, 1), "unit": "us/token", "cores": 1,
+                        "gbps_compressed": round(octets1 / dt1 / 1e9, 4),
+                        "median_token_us": round(float(np.median(temps1)) * 1e6, 1),
+                        "worst_token_us": round(float(np.max(temps1)) * 1e6, 1),
+                        "sample": f"{n1} timed tokens x 4 experts, one thread"},
+        "host": description_hote(),
     }
 
 
@@ -636,11 +692,24 @@ def bench_modele(args, dims, flux):
     }
 
 
+def evincer_caches():
+    """A 2 x 512 MiB device copy: evicts the Infinity Cache (256 MB) and the L2s before a timed region."""
+    import torch
+    t = torch.empty(2 * (512 << 20), dtype=torch.uint8, device="cuda:0")
+    t[512 << 20:].copy_(t[:512 << 20])
+    torch.cuda.synchronize()
+    del t
+
+
 def temps(pas, steps, warmup, flux):
+    """Milliseconds of steps pas(0) .. pas(steps - 1) between two events on `flux`, after `warmup`
+    untimed steps pas(steps) .. pas(steps + warmup - 1) (other inputs than the timed ones) and a
+    cache eviction."""
     import torch
     for s in range(warmup):
-        pas(s)
+        pas(steps + s)
     torch.cuda.synchronize()
+    evincer_caches()
     debut, fin = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     debut.record(flux)
     for s in range(steps):
@@ -681,7 +750,9 @@ def main():
     ap.add_argument("--n-codes", type=int, default=16, help="macro-steps per CODES_CTX tile written by the encoder")
     ap.add_argument("--n-delta", type=int, default=4, help="macro-steps per DELTA tile written by the encoder")
     ap.add_argument("--graine", type=int, default=2026)
-    ap.add_argument("--tokens", type=int, default=1000)
+    ap.add_argument("--tokens", type=int, default=1000, help="seeded activations of the sweep")
+    ap.add_argument("--distance-octets", type=float, default=512e6, dest="distance_octets",
+                    help="config 3: compressed bytes of other parts read between two uses of an expert")
     ap.add_argument("--sans-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--budget-cpu", type=float, default=12.0, help="seconds of single-thread CPU baseline work")
     ap.add_argument("--calibrer-copie", action="store_true",
@@ -805,7 +876,7 @@ def main():
     # configs 3 and 4: the MoE layer step (one layer, or a token through L layers)
     residu = torch.zeros(C, dtype=torch.float32, device=dev)
     vres = V(residu)
-    n_sel = max(args.steps, args.warmup, 1)
+    n_sel = max(args.steps, args.tokens, 1)
     sel_i = torch.zeros((n_sel, n_couches, 8), dtype=torch.int32, device=dev)
     sel_w = torch.zeros((n_sel, n_couches, 8), dtype=torch.float32, device=dev)
     vi = [[V(sel_i, 32 * (s * n_couches + l), 32) for l in range(n_couches)] for s in range(n_sel)]
@@ -813,21 +884,64 @@ def main():
     n_tr = fusion.taille_travail_couche(dims, E, k, args.n_codes)
     _tr, tr = espace(n_tr)
 
-    def pas(s):
+    def jeton(t, ligne):
+        """Token t of the sweep through the layer(s); its selection lands in row `ligne`."""
         for l, c in enumerate(couches):
-            fz.couche_moe(c.vrep, E, c.vluts, dims, c.vr16, None, vx[s % args.tokens], k, vres, vi[s][l], vw[s][l],
+            fz.couche_moe(c.vrep, E, c.vluts, dims, c.vr16, None, vx[t], k, vres, vi[ligne][l], vw[ligne][l],
                           vctl, tr, args.n_delta, args.n_codes, f=flux)
 
-    ms = temps(pas, args.steps, args.warmup, flux)
+    # The routing of the whole sweep, read from the product path itself (untimed), then the timed
+    # schedule: tokens of the sweep in order, a token taken only if none of its experts (layer 0) was
+    # used by the previous `distance` scheduled tokens, cycling over the sweep until `steps` tokens;
+    # warm-up on sweep tokens outside the schedule; then a copy of 2 x 512 MiB evicts the Infinity
+    # Cache (256 MB) and the L2s before the timed region, so that no part is served from a cache.
+    for t in range(args.tokens):
+        jeton(t, t)
+    torch.cuda.synchronize()
+    sel_balayage = sel_i[:args.tokens, 0, :k].cpu().numpy().astype(np.int64)
+    octets_tok_moyen = float(c0.utiles[sel_balayage].sum(axis=1).mean())
+    distance = max(1, int(np.ceil(args.distance_octets / octets_tok_moyen))) if n_couches == 1 else 0
+    plan = planifier(sel_balayage, args.steps, distance)
+    dans_plan = set(plan)
+    hors_plan = [t for t in range(args.tokens) if t not in dans_plan] or list(range(args.tokens))
+    chasse = torch.empty(2 * (512 << 20), dtype=torch.uint8, device=dev)
+
+    def evincer():
+        chasse[512 << 20:].copy_(chasse[:512 << 20])
+
+    for s in range(args.warmup):
+        jeton(hors_plan[s % len(hors_plan)], (args.steps + s) % n_sel)
+    evincer()
+    torch.cuda.synchronize()
+    debut, fin = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    debut.record(flux)
+    for s in range(args.steps):
+        jeton(plan[s], s)
+    fin.record(flux)
+    torch.cuda.synchronize()
+    ms = debut.elapsed_time(fin)
     assert (ctl.cpu().numpy() == 0).all(), f"control words {ctl.cpu().numpy()}"
     sel = sel_i[:args.steps, :, :k].cpu().numpy()
     octets_tok = sum(couches[l].utiles[sel[:, l, :]].sum(axis=1) for l in range(n_couches))
     us_tok = ms * 1e3 / args.steps
     gbps = octets_tok.sum() / (ms * 1e-3) / 1e9
     histo = np.bincount(sel[:, 0, :].reshape(-1), minlength=E)
+    distincts = np.unique(sel[:, 0, :])
+    octets_distincts = int(sum(couches[l].utiles[np.unique(sel[:, l, :])].sum() for l in range(n_couches)))
+    # per-token distribution: the same timed steps again after another eviction, one event per token
+    evincer()
+    torch.cuda.synchronize()
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
+    evs[0].record(flux)
+    for s in range(args.steps):
+        jeton(plan[s], s)
+        evs[s + 1].record(flux)
+    torch.cuda.synchronize()
+    par_jeton = np.array([evs[s].elapsed_time(evs[s + 1]) * 1e3 for s in range(args.steps)])
 
     n_chrono = min(args.steps, 200 if n_couches == 1 else 20)
-    noyaux = chrono_passes(fusion, pas, n_chrono)
+    evincer()
+    noyaux = chrono_passes(fusion, lambda s: jeton(plan[s], s), n_chrono)
     sel_c = sel_i[:n_chrono, :, :k].cpu().numpy()
     gu_ms, gu_n = noyaux.get("fusion_gemv/gate_up", (0.0, 1))
     bas_ms, bas_n = noyaux.get("fusion_gemv/down", (0.0, 1))
@@ -835,10 +949,14 @@ def main():
     octets_bas = sum(couches[l].octets_codes[sel_c[:, l, :]][:, :, 2].sum() for l in range(n_couches)) / bas_n
     duree_us = (gu_ms / gu_n + bas_ms / bas_n) * 1e3
     atteint = (octets_gu + octets_bas) / (duree_us * 1e-6) / 1e9
+    trafic = trafic_mesure() if n_couches == 1 else None
     roofline = {
         "bound": "hbm", "kernel": "fusion_gemv (gate/up launch + down launch)",
         "achieved": round(float(atteint), 1), "peak": PIC_HBM, "unit": "GB/s",
-        "frac": round(float(atteint / PIC_HBM), 4), "traffic": trafic_mesure() if n_couches == 1 else None,
+        "frac": round(float(atteint / PIC_HBM), 4), "traffic": trafic,
+        "traffic_source": (f"{FICHIER_PMC.relative_to(RACINE)}: rocprofv3 --pmc FETCH_SIZE then WRITE_SIZE per "
+                           "dispatch of the same command, scaled by a 64 MiB copy kernel; not measured in this run")
+        if trafic else None,
         "bytes_per_launch": {"gate_up": int(octets_gu), "down": int(octets_bas)},
         "avg_launch_us": {"gate_up": round(gu_ms / gu_n * 1e3, 2), "down": round(bas_ms / bas_n * 1e3, 2),
                           "both": round(duree_us / 2, 2)},
@@ -846,8 +964,9 @@ def main():
     chrono_us = {nom: round(v[0] / v[1] * 1e3, 2) for nom, v in noyaux.items()}
     if n_couches == 1:
         metrique, unite = METRIQUE, "us/token"
-        workload = ("config3: one MoE layer decode step, batch 1, top-4 of 128 gpt-oss-120b experts "
-                    "(3 x 2880x2880 MXFP4, .trc v1.2 rANS-coded), 1000-token seeded sweep")
+        workload = (f"config3: one MoE layer decode step, batch 1, top-{k} of {E} gpt-oss-120b experts "
+                    f"(3 x 2880x2880 MXFP4, .trc v1.2 rANS-coded); {args.steps} timed tokens from a "
+                    f"{args.tokens}-token seeded sweep, no expert reused within {distance} tokens")
     else:
         metrique, unite = f"config4 us/token for the MoE part of {n_couches} resident layers", "us/token"
         workload = (f"config4: a token through {n_couches} resident MoE layers x 128 gpt-oss-120b experts "
@@ -858,12 +977,21 @@ def main():
         "scaling": "weak", "vs_baseline": None, "dtype": "u32 rANS / f32 GEMV",
         "data": "synthetic (seeded MXFP4 law A, E8M0 in [119,125], bf16 N(0,1) activations, bf16 N(0,0.02) router)",
         "config": {"workload": workload, "experts": E, "k": k, "hidden": C, "layers": n_couches,
-                   "n_codes": args.n_codes, "n_delta": args.n_delta, "tokens": args.tokens,
-                   "mean_part_bytes": int(c0.utiles.mean())},
+                   "n_codes": args.n_codes, "n_delta": args.n_delta, "tokens": args.steps,
+                   "sweep_tokens": args.tokens, "mean_part_bytes": int(c0.utiles.mean())},
         "gbps_compressed": round(float(gbps), 1),
         "frac_hbm_layer": round(float(gbps / PIC_HBM), 4),
         "compressed_bytes_per_token": int(octets_tok.mean()),
-        "routing_histogram": {"experts_hit": int((histo > 0).sum()), "min": int(histo.min()),
+        "timed_distinct_part_bytes": octets_distincts,
+        "cache": ("a 2 x 512 MiB device copy evicts the Infinity Cache and the L2s before the timed region; "
+                  + (f"no expert recurs within {distance} scheduled tokens "
+                     f"({distance * octets_tok_moyen / 1e9:.2f} GB of other parts)" if distance else
+                     "each token reads every layer's parts once")),
+        "token_us": {"median": round(float(np.median(par_jeton)), 2),
+                     "p90": round(float(np.percentile(par_jeton, 90)), 2),
+                     "worst": round(float(par_jeton.max()), 2), "best": round(float(par_jeton.min()), 2),
+                     "method": "the timed steps again after another eviction, one HIP event per token"},
+        "routing_histogram": {"experts_hit": int(len(distincts)), "min": int(histo.min()),
                               "max": int(histo.max()), "mean": round(float(histo.mean()), 2)},
         "kernel_us": chrono_us,
         "roofline": roofline,
@@ -873,8 +1001,8 @@ def main():
         ligne["config"]["source"] = ".trc v1.2 file: parts read with fingerprints checked, tables, router resident"
         ligne["trc_file"] = info_fichier
     if not args.sans_cpu and n_couches == 1:
-        selections = [(sel[t, 0], sel_w[t, 0, :k].cpu().numpy()) for t in range(min(args.steps, 20))]
-        ligne["cpu_baseline"] = baseline_cpu(c0.hote, c0.luts_np, x_tok, selections, args.budget_cpu, n_fils)
+        selections = [(sel[s, 0], sel_w[s, 0, :k].cpu().numpy(), x_tok[plan[s]]) for s in range(min(args.steps, 64))]
+        ligne["cpu_baseline"] = baseline_cpu(c0.hote, c0.luts_np, selections, args.budget_cpu, n_fils)
     else:
         ligne["cpu_baseline"] = None
     print(json.dumps(ligne), flush=True)
