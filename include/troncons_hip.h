@@ -75,6 +75,94 @@ typedef struct {
 /* Message of the calling thread's last error ("" if none). */
 const char* trc_derniere_erreur(void);
 
+/* The hipError_t of the calling thread's last error when it was a HIP error (the `code` of
+ * Erreur::Cuda, trc-cuda/src/lib.rs:34-41; its name and text are in trc_derniere_erreur()), else 0. */
+int trc_dernier_code_hip(void);
+
+/* ----------------------------------------------------- driver half (replaces the trc_cuda crate)
+ *
+ * Context, streams, events, device memory, pinned and mapped host memory, asynchronous copies and
+ * fills on HIP, mirroring trc_cuda (moteur/crates/trc-cuda/src/lib.rs:160-623, api.rs:106-146).
+ * A stream or an event is a HIP handle passed as void* (what every launch entry point takes as
+ * `flux`). A trc_contexte names a device; each entry point that takes one makes its device current
+ * on the calling thread first. Every stream is created at the device's default priority. */
+typedef struct trc_contexte trc_contexte;
+
+#define TRC_ATTENTE_AUTO 0      /* Attente::Auto (lib.rs:91-100): the runtime chooses */
+#define TRC_ATTENTE_ACTIVE 1    /* Attente::Active: spin */
+#define TRC_ATTENTE_CEDE 2      /* Attente::Cede: spin and yield */
+#define TRC_ATTENTE_BLOQUANTE 3 /* Attente::Bloquante: the host thread sleeps */
+
+#define TRC_ATTRIBUT_CAPACITE_MAJEURE 0 /* Attribut (lib.rs:251-276) */
+#define TRC_ATTRIBUT_CAPACITE_MINEURE 1
+#define TRC_ATTRIBUT_MOTEURS_DE_COPIE 2
+#define TRC_ATTRIBUT_PROJECTION_HOTE 3
+#define TRC_ATTRIBUT_ADRESSAGE_UNIFIE 4
+#define TRC_ATTRIBUT_UNITES_DE_CALCUL 5 /* compute units (no counterpart in the reference) */
+#define TRC_ATTRIBUT_LDS_PAR_BLOC 6     /* LDS bytes per workgroup (no counterpart in the reference) */
+
+/* Contexte::nouveau_avec (lib.rs:166-201): device `ordinal` with host wait mode `attente`
+ * (TRC_ATTENTE_*; kept by the runtime only if the device is not active yet). */
+int trc_contexte_creer(uint32_t ordinal, uint32_t attente, trc_contexte** sortie);
+void trc_contexte_detruire(trc_contexte* c);
+/* Contexte::memoire (lib.rs:204-213): free and total device memory in bytes */
+int trc_contexte_memoire(const trc_contexte* c, uint64_t* libre, uint64_t* totale);
+/* Contexte::nom, version_pilote, attente_effective (lib.rs:215-232) */
+const char* trc_contexte_nom(const trc_contexte* c);
+int trc_contexte_version_pilote(const trc_contexte* c);
+uint32_t trc_contexte_attente(const trc_contexte* c);
+/* Contexte::attribut (lib.rs:235-240) */
+int trc_contexte_attribut(const trc_contexte* c, uint32_t attribut, int32_t* valeur);
+/* Contexte::synchroniser (lib.rs:243-246) */
+int trc_contexte_synchroniser(const trc_contexte* c);
+
+/* Flux::nouveau (lib.rs:290-302): a non-blocking stream; `priorite_haute` is accepted for the
+ * signature, every stream gets the default priority. Drop for Flux (lib.rs:334-340). */
+int trc_flux_creer(const trc_contexte* c, int priorite_haute, void** flux);
+int trc_flux_detruire(void* flux);
+/* Flux::attendre (lib.rs:305-308): `flux` waits for the last record of `evenement` */
+int trc_flux_attendre(void* flux, void* evenement);
+/* Flux::synchroniser (lib.rs:311-314) */
+int trc_flux_synchroniser(void* flux);
+/* Flux::fini (lib.rs:318-326): *fini = 1 when everything queued on the stream is over */
+int trc_flux_fini(void* flux, int* fini);
+/* Flux::priorite (lib.rs:329-331) */
+int trc_flux_priorite(void* flux, int* priorite);
+
+/* Evenement::nouveau / nouveau_bloquant (lib.rs:361-379); Drop for Evenement (lib.rs:417-423) */
+int trc_evenement_creer(const trc_contexte* c, int horodate, int bloquant, void** evenement);
+int trc_evenement_detruire(void* evenement);
+/* Evenement::enregistrer (lib.rs:382-385) */
+int trc_evenement_enregistrer(void* evenement, void* flux);
+/* Evenement::fini (lib.rs:388-396) */
+int trc_evenement_fini(void* evenement, int* fini);
+/* Evenement::attendre (lib.rs:399-402) */
+int trc_evenement_attendre(void* evenement);
+/* Evenement::ms_depuis (lib.rs:406-414): milliseconds from `debut` to `fin` (timed events) */
+int trc_evenement_ms_depuis(void* fin, void* debut, float* ms);
+
+/* MemoireCarte::allouer (lib.rs:448-458) and its Drop (lib.rs:490-496): device memory as a view */
+int trc_carte_allouer(const trc_contexte* c, uint64_t octets, trc_vue* vue);
+int trc_carte_liberer(const trc_contexte* c, trc_vue vue);
+/* MemoireCarte::remplir (lib.rs:481-487): every byte of `vue` set to `octet`, asynchronously on
+ * `flux`, by a fill kernel (a graph capture of the stream records a kernel node) */
+int trc_carte_remplir(trc_vue vue, uint8_t octet, void* flux);
+
+/* HoteEpingle::allouer (lib.rs:521-545): pinned portable host memory rounded up to 4096 bytes
+ * (*octets_reels), mapped into the device when `projetee` (its device address in *carte, else 0);
+ * Drop for HoteEpingle (lib.rs:582-588) */
+int trc_hote_allouer(const trc_contexte* c, uint64_t octets, int projetee, void** hote, uint64_t* octets_reels,
+                     uint64_t* carte);
+int trc_hote_liberer(void* hote);
+/* HoteEpingle::lire_volatil_u32 (lib.rs:575-579): a mailbox word written by the device */
+uint32_t trc_hote_lire_volatil_u32(const void* hote, uint64_t decalage);
+
+/* copier_vers_carte, copier_vers_hote, copier_carte_carte (lib.rs:591-623): asynchronous on `flux`;
+ * host memory is pinned memory from trc_hote_allouer */
+int trc_copier_vers_carte(trc_vue dst, const void* src, uint64_t octets, void* flux);
+int trc_copier_vers_hote(void* dst, trc_vue src, void* flux);
+int trc_copier_carte_carte(trc_vue dst, trc_vue src, void* flux);
+
 /* ------------------------------------------------------------- host helpers (no device needed) */
 
 /* disposition_matrice (abi.rs:83-88) */

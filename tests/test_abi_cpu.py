@@ -194,3 +194,24 @@ def test_prefill_refuses_unsupported_shapes_before_launching():
         fz.prefill_moe(v, 128, v, dims, v, 512, v, v, 4, v, v, v, 4, 32, f=0)
     with pytest.raises(K.ErreurUsage):  # workspace too small
         fz.prefill_moe(v, 128, v, dims, v, 512, v, v, 4, v, v, VueCarte(1 << 20, 4096), 4, 16, f=0)
+
+
+def test_driver_half_refuses_bad_arguments_before_any_hip_call():
+    """The driver half's contract checks (trc-cuda/src/lib.rs:448-451, 521-524, 591-623) run before
+    the runtime is touched, so they answer without a device."""
+    l = _lib.charger()
+    from troncons_amd import pilote  # noqa: F401  (declares the argument types)
+    V = K._Vue
+    h = C.c_void_p()
+    assert l.trc_contexte_creer(0, 9, C.byref(h)) == 1 and b"attente" in l.trc_derniere_erreur()
+    assert l.trc_dernier_code_hip() == 0
+    assert l.trc_carte_remplir(V(0, 16), 0, None) == 1
+    assert l.trc_carte_remplir(V(0, 0), 0, None) == 0  # an empty view is nothing to do
+    assert l.trc_copier_carte_carte(V(4096, 4), V(8192, 8), None) == 1
+    assert l.trc_copier_vers_carte(V(4096, 4), None, 4, None) == 1
+    assert l.trc_copier_vers_carte(V(4096, 4), C.c_void_p(8192), 8, None) == 1
+    assert l.trc_copier_vers_hote(None, V(4096, 4), None) == 1
+    assert l.trc_flux_attendre(None, None) == 1
+    assert l.trc_evenement_ms_depuis(None, None, None) == 1
+    assert l.trc_hote_allouer(None, 0, 0, C.byref(h), None, None) == 1
+    assert l.trc_carte_allouer(None, 0, C.byref(V())) == 1

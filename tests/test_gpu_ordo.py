@@ -23,7 +23,7 @@ import oracle_ffi as O  # noqa: E402
 from gpu_outils import dev, hote, zeros  # noqa: E402
 from troncons_amd import cache as K  # noqa: E402
 from troncons_amd import conteneur as T  # noqa: E402
-from troncons_amd.noyaux import DimsExpert  # noqa: E402
+from troncons_amd.noyaux import DimsExpert, ErreurUsage  # noqa: E402
 from troncons_amd.ordo import Ordonnanceur  # noqa: E402
 
 TOL = 1e-5
@@ -177,6 +177,9 @@ def test_damaged_part_refused_or_counted(petit, tmp_path):
         for x in xs[:n]:
             o.jeton(dev(x), zeros(4 * 256))
     assert e.value.classe == "Empreinte"
+    # fail-stop: the failed token's reads were drained and every later token is refused
+    with pytest.raises(ErreurUsage, match="erreur precedente"):
+        o.jeton(dev(xs[0]), zeros(4 * 256))
     o.detruire()
     o = Ordonnanceur(f, emplacements=64, tiedes=0, verifier=False)
     for x in xs[:n]:

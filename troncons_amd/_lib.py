@@ -14,7 +14,7 @@ RACINE = PAQUET.parent
 CSRC = PAQUET / "csrc"
 LIB_PATH = PAQUET / "libtroncons_hip.so"
 
-SOURCES_HIP = ["noyaux.hip", "fusion.hip", "prefill.hip", "passe.hip"]
+SOURCES_HIP = ["noyaux.hip", "fusion.hip", "prefill.hip", "passe.hip", "pilote.hip"]
 SOURCES_CPP = ["hote.cpp", "codeur.cpp", "chrono.cpp", "conteneur.cpp", "cache.cpp", "ordo.cpp", "modele.cpp"]
 
 # -packed-fp32-ops off: v_pk_* f32 forms are avoided on these boxes (the host pass warns that it

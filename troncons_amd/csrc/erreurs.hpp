@@ -13,6 +13,7 @@
 namespace trc {
 
 std::string& derniere_erreur();
+int& dernier_code_hip();  // hipError_t of the thread's last error, 0 when it was not a HIP error
 
 inline int usage(const char* fmt, ...) {
     char buf[512];
@@ -21,6 +22,7 @@ inline int usage(const char* fmt, ...) {
     vsnprintf(buf, sizeof(buf), fmt, ap);
     va_end(ap);
     derniere_erreur() = std::string("usage : ") + buf;
+    dernier_code_hip() = 0;
     return TRC_ERREUR_USAGE;
 }
 
@@ -28,6 +30,7 @@ inline int erreur_hip(const char* appel, hipError_t e) {
     char buf[512];
     snprintf(buf, sizeof(buf), "%s : %s (%d) : %s", appel, hipGetErrorName(e), int(e), hipGetErrorString(e));
     derniere_erreur() = buf;
+    dernier_code_hip() = int(e);
     return e == hipErrorNoDevice || e == hipErrorInsufficientDriver ? TRC_ERREUR_PILOTE : TRC_ERREUR_HIP;
 }
 

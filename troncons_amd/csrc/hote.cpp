@@ -11,11 +11,17 @@ std::string& derniere_erreur() {
     thread_local std::string message;
     return message;
 }
+int& dernier_code_hip() {
+    thread_local int code = 0;
+    return code;
+}
 }  // namespace trc
 
 using trc::usage;
 
 extern "C" const char* trc_derniere_erreur(void) { return trc::derniere_erreur().c_str(); }
+
+extern "C" int trc_dernier_code_hip(void) { return trc::dernier_code_hip(); }
 
 extern "C" trc_disposition trc_disposition_matrice(uint32_t lignes, uint32_t colonnes) {
     return trc::disposition_matrice(lignes, colonnes);

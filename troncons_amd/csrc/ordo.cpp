@@ -86,11 +86,13 @@ public:
         cv_.notify_all();
         for (auto& t : fils_) t.join();
     }
+    // soumettre / attendre / vider are called by the engine's thread only.
     void soumettre(const Requete& r) {
         {
             std::lock_guard<std::mutex> g(m_);
             file_.push_back(r);
         }
+        ++en_cours_;
         cv_.notify_one();
     }
     Fin attendre() {
@@ -98,7 +100,13 @@ public:
         cv_fini_.wait(g, [this] { return !finis_.empty(); });
         Fin x = std::move(finis_.front());
         finis_.pop_front();
+        --en_cours_;
         return x;
+    }
+    // Waits for every submitted read that has not been taken by attendre(): after an error, no
+    // reader thread writes into the engine's buffers any more.
+    void vider() {
+        while (en_cours_ > 0) attendre();
     }
 
 private:
@@ -129,6 +137,7 @@ private:
     std::deque<Requete> file_;
     std::deque<Fin> finis_;
     bool fin_ = false;
+    uint64_t en_cours_ = 0;
 };
 
 }  // namespace
@@ -142,6 +151,8 @@ struct trc_ordo {
     trc_disposition disp[3];
     trc_cache* cache = nullptr;
     std::unique_ptr<Lecteurs> lecteurs;
+    bool en_echec = false;       // an error stopped a token: every later token is refused
+    std::string message_echec;
     hipStream_t copie = nullptr;
     hipEvent_t ev_routeur = nullptr;
     std::vector<hipEvent_t> ev_copie;
@@ -572,7 +583,22 @@ int trc_ordo_jeton(trc_ordo* o, trc_vue x, trc_vue residu, void* flux) {
     if (o == nullptr) return trc::usage("ordonnanceur nul");
     TRC_VERIFIER(x.adresse != 0 && x.adresse % 16 == 0 && x.octets >= 4ull * o->C, "x : %u f32 alignes sur 16", o->C);
     TRC_VERIFIER(residu.adresse != 0 && residu.octets >= 4ull * o->D, "residu : %u f32", o->D);
-    for (uint32_t l = 0; l < o->L; ++l) TRC_OK_OU_RENDRE(o->couche(l, x, residu, flux));
+    if (o->en_echec) return trc::usage("ordonnanceur arrete par une erreur precedente : %s", o->message_echec.c_str());
+    for (uint32_t l = 0; l < o->L; ++l) {
+        const int r = o->couche(l, x, residu, flux);
+        if (r != TRC_OK) {
+            // fail-stop (the reference engine panics): the layer's reads still in flight are drained
+            // so that no reader writes into the buffers later, and the engine refuses every later
+            // token, since its cache holds slots that were never made ready
+            const std::string m = trc_derniere_erreur();
+            o->lecteurs->vider();
+            hipStreamSynchronize(o->copie);
+            o->en_echec = true;
+            o->message_echec = m;
+            trc::derniere_erreur() = m;
+            return r;
+        }
+    }
     o->jeton += 1;
     o->st.jetons += 1;
     return TRC_OK;

@@ -24,7 +24,12 @@ class ErreurUsage(Erreur):
 
 
 class ErreurHip(Erreur):
-    """Erreur::Cuda, on HIP — a runtime call failed."""
+    """Erreur::Cuda, on HIP — a runtime call failed; ``code`` is its hipError_t (the message holds
+    the call, the runtime's error name and its text)."""
+
+    def __init__(self, message: str, code: int = 0):
+        super().__init__(message)
+        self.code = code
 
 
 class ErreurPilote(Erreur):
@@ -146,6 +151,7 @@ def _declarer(l: C.CDLL) -> C.CDLL:
     V = _Vue
     u32p = C.POINTER(C.c_uint32)
     l.trc_derniere_erreur.restype = C.c_char_p
+    l.trc_dernier_code_hip.restype = C.c_int
     l.trc_disposition_matrice.argtypes = [C.c_uint32, C.c_uint32]
     l.trc_disposition_matrice.restype = Disposition
     l.trc_dims_verifier.argtypes = [C.POINTER(DimsExpert)]
@@ -194,7 +200,7 @@ def _statut(r: int) -> None:
         raise ErreurUsage(msg)
     if r == 3:
         raise ErreurPilote(msg)
-    raise ErreurHip(msg)
+    raise ErreurHip(msg, bibliotheque().trc_dernier_code_hip())
 
 
 def _flux(f) -> int:
