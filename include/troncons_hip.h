@@ -374,6 +374,19 @@ int trc_couche_moe_fusionnee(trc_vue repertoire, uint32_t experts, trc_vue luts,
                              trc_vue indices, trc_vue poids, trc_vue controle, trc_vue travail, uint32_t n_delta,
                              uint32_t n_codes, void* flux);
 
+/* No counterpart in the reference. For callers that cannot allocate (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc): trc_couche_moe_fusionnee with the library's
+ * static device scratch (trc_octets_scratch() bytes, 16 MiB, one per device, held until the process
+ * ends) as its workspace; it calls no allocating routine. A step needing more than the scratch
+ * (trc_taille_travail_couche_moe) is a usage error. Every call on a device shares that device's
+ * scratch: calls that overlap on one device (two streams, two threads) race; serialise them. The
+ * scratch is taken on the device of `flux` (the current device if flux is null). */
+uint64_t trc_octets_scratch(void);
+int trc_couche_moe_fusionnee_sans_alloc(trc_vue repertoire, uint32_t experts, trc_vue luts,
+                                        const trc_dims_expert* dims, trc_vue routeur, trc_vue routeur_biais,
+                                        trc_vue x, uint32_t k, trc_vue residu, trc_vue indices, trc_vue poids,
+                                        trc_vue controle, uint32_t n_delta, uint32_t n_codes, void* flux);
+
 /* Workspace bytes of trc_prefill_moe (0 if the shape is refused). */
 uint64_t trc_taille_travail_prefill(const trc_dims_expert* dims, uint32_t experts, uint32_t positions, uint32_t k,
                                     uint32_t n_codes);

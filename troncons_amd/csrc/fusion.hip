@@ -23,6 +23,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstring>
+#include <mutex>
 
 #include "anneau.hpp"
 #include "chrono.hpp"
@@ -699,6 +700,67 @@ extern "C" int trc_couche_moe_fusionnee(trc_vue repertoire, uint32_t experts, tr
                                         trc_vue routeur, trc_vue routeur_biais, trc_vue x, uint32_t k,
                                         trc_vue residu, trc_vue indices, trc_vue poids, trc_vue controle,
                                         trc_vue travail, uint32_t n_delta, uint32_t n_codes, void* flux) {
+    return couche_moe(repertoire, experts, luts, dims, routeur, routeur_biais, x, k, residu, indices, poids, controle,
+                      travail, n_delta, n_codes, trc_vue{0, 0}, 0.0f, flux);
+}
+
+// ------------------------------------------------------------ the allocation-free MoE layer step
+// A file-scope device array stands in for the caller's workspace. In host code `scratch` names a
+// host-side stand-in, not device memory: its device address is taken once per device, with that
+// device current, by hipGetSymbolAddress, and only that address (adresse_scratch) is used.
+namespace {
+constexpr uint64_t OCTETS_SCRATCH = 16ull << 20;  // holds a gpt-oss layer step at k <= 4 (N_codes >= 16)
+constexpr int CARTES_MAX = 64;
+__device__ __align__(256) uint8_t scratch[OCTETS_SCRATCH];
+std::mutex verrou_scratch;
+void* adresse_scratch[CARTES_MAX] = {};
+
+// The device address of `scratch` on the device of `flux`, taken once per device.
+int scratch_de(void* flux, void** adresse) {
+    int d = -1;
+    hipDevice_t dh = 0;
+    if (flux != nullptr && hipStreamGetDevice(reinterpret_cast<hipStream_t>(flux), &dh) == hipSuccess) {
+        d = int(dh);
+    } else {
+        const hipError_t e = hipGetDevice(&d);
+        if (e != hipSuccess) return trc::erreur_hip("hipGetDevice", e);
+    }
+    if (d < 0 || d >= CARTES_MAX) return usage("carte %d hors des %d que la memoire statique couvre", d, CARTES_MAX);
+    std::lock_guard<std::mutex> g(verrou_scratch);
+    if (adresse_scratch[d] == nullptr) {
+        int courante = -1;
+        hipError_t e = hipGetDevice(&courante);
+        if (e != hipSuccess) return trc::erreur_hip("hipGetDevice", e);
+        if (courante != d && (e = hipSetDevice(d)) != hipSuccess) return trc::erreur_hip("hipSetDevice", e);
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (courante != d) (void)hipSetDevice(courante);
+        if (e != hipSuccess) return trc::erreur_hip("hipGetSymbolAddress(scratch)", e);
+        if (p == nullptr) return usage("adresse nulle pour la memoire statique de la carte %d", d);
+        adresse_scratch[d] = p;
+    }
+    *adresse = adresse_scratch[d];
+    return TRC_OK;
+}
+}  // namespace
+
+extern "C" uint64_t trc_octets_scratch(void) { return OCTETS_SCRATCH; }
+
+// trc_couche_moe_fusionnee with the device's static scratch as its workspace: no allocation.
+extern "C" int trc_couche_moe_fusionnee_sans_alloc(trc_vue repertoire, uint32_t experts, trc_vue luts,
+                                                   const trc_dims_expert* dims, trc_vue routeur,
+                                                   trc_vue routeur_biais, trc_vue x, uint32_t k, trc_vue residu,
+                                                   trc_vue indices, trc_vue poids, trc_vue controle, uint32_t n_delta,
+                                                   uint32_t n_codes, void* flux) {
+    const uint64_t besoin = trc_taille_travail_couche_moe(dims, experts, k, n_codes);
+    if (besoin == 0) return usage("forme, top-k ou N refuses");
+    if (besoin > OCTETS_SCRATCH)
+        return usage("l'etape demande %llu o de travail, la memoire statique en a %llu",
+                     (unsigned long long)besoin, (unsigned long long)OCTETS_SCRATCH);
+    void* p = nullptr;
+    const int r = scratch_de(flux, &p);
+    if (r != TRC_OK) return r;
+    const trc_vue travail{uint64_t(reinterpret_cast<uintptr_t>(p)), OCTETS_SCRATCH};
     return couche_moe(repertoire, experts, luts, dims, routeur, routeur_biais, x, k, residu, indices, poids, controle,
                       travail, n_delta, n_codes, trc_vue{0, 0}, 0.0f, flux);
 }

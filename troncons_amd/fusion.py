@@ -22,6 +22,9 @@ def _declarer(l):
     l.trc_taille_travail_couche_moe.restype = C.c_uint64
     l.trc_couche_moe_fusionnee.argtypes = [V, C.c_uint32, V, C.POINTER(DimsExpert), V, V, V, C.c_uint32, V, V, V, V,
                                            V, C.c_uint32, C.c_uint32, C.c_void_p]
+    l.trc_couche_moe_fusionnee_sans_alloc.argtypes = [V, C.c_uint32, V, C.POINTER(DimsExpert), V, V, V, C.c_uint32,
+                                                      V, V, V, V, C.c_uint32, C.c_uint32, C.c_void_p]
+    l.trc_octets_scratch.restype = C.c_uint64
     l.trc_taille_repertoire.argtypes = [C.c_uint32]
     l.trc_taille_repertoire.restype = C.c_uint64
     l.trc_monter_couche.argtypes = [V, C.c_uint32, C.POINTER(DimsExpert), V, V, C.c_void_p]
@@ -74,6 +77,11 @@ def taille_travail_prefill(dims: DimsExpert, experts: int, positions: int, k: in
     return _l().trc_taille_travail_prefill(C.byref(dims), experts, positions, k, n_codes)
 
 
+def octets_scratch() -> int:
+    """Bytes of the static device scratch of couche_moe_sans_alloc."""
+    return _l().trc_octets_scratch()
+
+
 def taille_repertoire(experts: int) -> int:
     """Bytes of a mounted layer's directory (trc_monter_couche)."""
     return _l().trc_taille_repertoire(experts)
@@ -107,6 +115,14 @@ class Fusion:
                                                  _vue(routeur_biais), _vue(x), k, _vue(residu), _vue(indices),
                                                  _vue(poids), _vue(controle), _vue(travail), n_delta, n_codes,
                                                  _flux(f)))
+
+    def couche_moe_sans_alloc(self, repertoire, experts: int, luts, dims: DimsExpert, routeur, routeur_biais, x,
+                              k: int, residu, indices, poids, controle, n_delta: int, n_codes: int, f=None) -> None:
+        """couche_moe with the library's static device scratch as workspace (no allocation; calls
+        that overlap on one device race)."""
+        _statut(self._l.trc_couche_moe_fusionnee_sans_alloc(
+            _vue(repertoire), experts, _vue(luts), C.byref(dims), _vue(routeur), _vue(routeur_biais), _vue(x), k,
+            _vue(residu), _vue(indices), _vue(poids), _vue(controle), n_delta, n_codes, _flux(f)))
 
     def prefill_moe(self, repertoire, experts: int, luts, dims: DimsExpert, x, positions: int, indices, poids, k: int,
                     residus, controle, travail, n_delta: int, n_codes: int, f=None) -> None:
