@@ -152,6 +152,7 @@ class CoucheResidente:
         self.o0 = (-self.bloc.data_ptr()) % 256
         base = self.bloc.data_ptr() + self.o0
         self.octets_codes = np.zeros((E, 3), np.int64)   # CODES_CTX stream bytes per matrix
+        self.octets_echelles = np.zeros((E, 3), np.int64)  # DELTA + MEDIANES stream bytes per matrix
         self.octets_matrice = np.zeros((E, 3), np.int64)  # the 4 streams of the matrix + headers
         for e in range(E):
             p = self.hote.partie(e)
@@ -160,6 +161,7 @@ class CoucheResidente:
             fl = lire_flux(p[:64 + 16 * 12].tobytes())
             for j in range(3):
                 self.octets_codes[e, j] = fl[(4, j)][1]
+                self.octets_echelles[e, j] = fl[(3, j)][1] + fl[(1, j)][1]
                 self.octets_matrice[e, j] = 64 + 4 * 16 + sum(fl[(s, j)][1] for s in (1, 2, 3, 4))
         self.table = torch.from_numpy(np.array([base + int(d) for d in self.decal], np.uint64).view(np.int64)).to(dev)
         freqs = self.hote.freqs()
@@ -748,7 +750,7 @@ def main():
     ap.add_argument("--experts", type=int, default=128)
     ap.add_argument("--k", type=int, default=4)
     ap.add_argument("--n-codes", type=int, default=16, help="macro-steps per CODES_CTX tile written by the encoder")
-    ap.add_argument("--n-delta", type=int, default=4, help="macro-steps per DELTA tile written by the encoder")
+    ap.add_argument("--n-delta", type=int, default=2, help="macro-steps per DELTA tile written by the encoder")
     ap.add_argument("--graine", type=int, default=2026)
     ap.add_argument("--tokens", type=int, default=1000, help="seeded activations of the sweep")
     ap.add_argument("--distance-octets", type=float, default=512e6, dest="distance_octets",
@@ -943,15 +945,22 @@ def main():
     evincer()
     noyaux = chrono_passes(fusion, lambda s: jeton(plan[s], s), n_chrono)
     sel_c = sel_i[:n_chrono, :, :k].cpu().numpy()
-    gu_ms, gu_n = noyaux.get("fusion_gemv/gate_up", (0.0, 1))
-    bas_ms, bas_n = noyaux.get("fusion_gemv/down", (0.0, 1))
-    octets_gu = sum(couches[l].octets_codes[sel_c[:, l, :]][:, :, :2].sum() for l in range(n_couches)) / gu_n
-    octets_bas = sum(couches[l].octets_codes[sel_c[:, l, :]][:, :, 2].sum() for l in range(n_couches)) / bas_n
+    # the CODES launches: fusion_codes (each tile's DELTA decoded in the kernel) or, for other tile
+    # lengths, fusion_gemv after the DELTA pass
+    gu_ms, gu_n = noyaux.get("fusion_codes/gate_up", noyaux.get("fusion_gemv/gate_up", (0.0, 1)))
+    bas_ms, bas_n = noyaux.get("fusion_codes/down", noyaux.get("fusion_gemv/down", (0.0, 1)))
+    nom_codes = "fusion_codes" if "fusion_codes/gate_up" in noyaux else "fusion_gemv"
+    # algorithmic bytes of a launch: the CODES_CTX streams it decodes, plus, when it decodes each
+    # tile's DELTA itself (fusion_codes), the DELTA and MEDIANES streams
+    lus = [couches[l].octets_codes + (couches[l].octets_echelles if nom_codes == "fusion_codes" else 0)
+           for l in range(n_couches)]
+    octets_gu = sum(lus[l][sel_c[:, l, :]][:, :, :2].sum() for l in range(n_couches)) / gu_n
+    octets_bas = sum(lus[l][sel_c[:, l, :]][:, :, 2].sum() for l in range(n_couches)) / bas_n
     duree_us = (gu_ms / gu_n + bas_ms / bas_n) * 1e3
     atteint = (octets_gu + octets_bas) / (duree_us * 1e-6) / 1e9
     trafic = trafic_mesure() if n_couches == 1 else None
     roofline = {
-        "bound": "hbm", "kernel": "fusion_gemv (gate/up launch + down launch)",
+        "bound": "hbm", "kernel": f"{nom_codes} (gate/up launch + down launch)",
         "achieved": round(float(atteint), 1), "peak": PIC_HBM, "unit": "GB/s",
         "frac": round(float(atteint / PIC_HBM), 4), "traffic": trafic,
         "traffic_source": (f"{FICHIER_PMC.relative_to(RACINE)}: rocprofv3 --pmc FETCH_SIZE then WRITE_SIZE per "

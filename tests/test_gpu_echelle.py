@@ -1,7 +1,8 @@
 """GPU parity at the workloads' real sizes, through the C-ABI.
 
-- Config 3: the fused MoE layer over 128 resident gpt-oss-120b experts (N_delta 4, N_codes 16, the
-  bench's encoding), 20 seeded tokens, some with tied router rows and some with NaN rows. Indices
+- Config 3: the fused MoE layer over 128 resident gpt-oss-120b experts (N_delta 2, N_codes 16, the
+  bench's encoding: each tile's DELTA decoded inside the CODES kernels), 20 seeded tokens, some
+  with tied router rows and some with NaN rows. Indices
   must equal the oracle's routeur_topk on the oracle's router logits (reference gemv_f32 order),
   weights within 1e-6, and the residual within 1e-5 * max|change| of the f64 MLP chain computed from
   the uncompressed weights (and, for the first tokens, of the reference's own f32 chain).
@@ -32,7 +33,7 @@ from troncons_amd.noyaux import DimsExpert, VueCarte  # noqa: E402
 
 GPT = DimsExpert.gpt_oss()
 C_ = 2880
-E, KTOP, N = 128, 4, (4, 16)
+E, KTOP, N = 128, 4, (2, 16)
 GRAINE = 2040
 TOL = 1e-5
 

@@ -44,7 +44,7 @@ def _slot_j(ex, j):
     return ex.attendu[d.base:d.base + d.pas]
 
 
-@pytest.mark.parametrize("N", [(256, 256), (32, 32), (8, 16), (4, 1)])
+@pytest.mark.parametrize("N", [(256, 256), (32, 32), (8, 16), (4, 1), (1, 16), (2, 16)])
 def test_fused_gemv_one_matrix_config1(fz, N):
     ex = Expert(2026, GPT, N_delta=N[0], N_codes=N[1])
     x = O.synth_normale_bf16(2026, 1, 0, 2880, 1.0)
@@ -77,7 +77,7 @@ def _expert_exact(seed, dims):
     return blocs, biais
 
 
-@pytest.mark.parametrize("N", [(256, 256), (16, 32), (3, 7)])
+@pytest.mark.parametrize("N", [(256, 256), (16, 32), (3, 7), (1, 16), (2, 16)])
 def test_fused_gemv_bit_exact_on_integer_fixture(fz, N):
     dims = GPT
     blocs, biais = _expert_exact(7, dims)
@@ -94,13 +94,14 @@ def test_fused_gemv_bit_exact_on_integer_fixture(fz, N):
         assert (y.view(np.uint32) == y64.view(np.uint32)).all()
 
 
-def test_fused_gemv_small_shapes_and_break(fz):
+@pytest.mark.parametrize("N", [(2, 3), (1, 16), (2, 16)])
+def test_fused_gemv_small_shapes_and_break(fz, N):
     dims = DimsExpert.de([300, 300, 257], [256, 256, 320])
-    ex = Expert(5, dims, N_delta=2, N_codes=3)
+    ex = Expert(5, dims, N_delta=N[0], N_codes=N[1])
     for j in range(3):
         R, C = dims.lignes[j], dims.colonnes[j]
         x = O.synth_normale_bf16(5, 2, j, C, 1.0)
-        y, ctl = _gemv(fz, ex.partie, ex.luts, j, R, C, x, 2, 3)
+        y, ctl = _gemv(fz, ex.partie, ex.luts, j, R, C, x, *N)
         assert list(ctl) == [0, 0, 0, 0]
         d = O.disposition_j(list(dims.lignes), list(dims.colonnes), j)
         y64 = O.gemv_mxfp4_f64(ex.attendu[d.base:d.base + d.pas], x, R, C)
@@ -111,11 +112,19 @@ def test_fused_gemv_small_shapes_and_break(fz):
     dec = int.from_bytes(p[e + 4:e + 8], "little")
     lon = int.from_bytes(p[e + 8:e + 12], "little")
     p[dec + lon // 2] ^= 0x10
-    _, ctl = _gemv(fz, bytes(p), ex.luts, 1, 300, 256, O.synth_normale_bf16(5, 2, 1, 256, 1.0), 2, 3)
+    _, ctl = _gemv(fz, bytes(p), ex.luts, 1, 300, 256, O.synth_normale_bf16(5, 2, 1, 256, 1.0), *N)
     assert ctl[0] > 0
+    # a flipped bit in the DELTA stream of matrix 1 (its descriptor is 6)
+    p = bytearray(ex.partie)
+    e = 64 + 16 * 6
+    dec = int.from_bytes(p[e + 4:e + 8], "little")
+    lon = int.from_bytes(p[e + 8:e + 12], "little")
+    p[dec + lon - 8] ^= 0x21
+    _, ctl = _gemv(fz, bytes(p), ex.luts, 1, 300, 256, O.synth_normale_bf16(5, 2, 1, 256, 1.0), *N)
+    assert ctl[0] + ctl[2] > 0
     p = bytearray(ex.partie)
     p[0] ^= 0xFF
-    _, ctl = _gemv(fz, bytes(p), ex.luts, 1, 300, 256, O.synth_normale_bf16(5, 2, 1, 256, 1.0), 2, 3)
+    _, ctl = _gemv(fz, bytes(p), ex.luts, 1, 300, 256, O.synth_normale_bf16(5, 2, 1, 256, 1.0), *N)
     assert ctl[1] > 0
 
 
@@ -151,7 +160,7 @@ def _mlp_oracle(ex, x, dims):
     return s, s64
 
 
-@pytest.mark.parametrize("N", [(256, 256), (32, 32), (8, 16)])
+@pytest.mark.parametrize("N", [(256, 256), (32, 32), (8, 16), (1, 16), (2, 16)])
 def test_fused_expert_config2(fz, N):
     ex = Expert(2027, GPT, N_delta=N[0], N_codes=N[1])
     x = O.synth_normale_bf16(2027, 1, 0, 2880, 1.0)
@@ -167,8 +176,9 @@ def test_fused_expert_config2(fz, N):
     assert np.abs(got - s64).max() <= TOL * np.abs(s64).max()
 
 
-def test_fused_moe_layer_config3(fz):
-    E, k, N = 12, 4, (16, 32)
+@pytest.mark.parametrize("N", [(16, 32), (1, 16), (2, 16)])
+def test_fused_moe_layer_config3(fz, N):
+    E, k = 12, 4
     couche = codeur.CoucheSynthetique(2028, 0, E, GPT, N_delta=N[0], N_codes=N[1])
     freqs = couche.freqs()
     luts = O.luts_couche([[freqs[j][t] for t in range(4)] for j in range(3)])
@@ -208,11 +218,12 @@ def test_fused_moe_layer_config3(fz):
     couche.liberer()
 
 
-def test_fused_moe_router_ties_and_order(fz):
+@pytest.mark.parametrize("N", [(16, 32), (2, 16)])
+def test_fused_moe_router_ties_and_order(fz, N):
     """The fused layer's top-k on tied logits: experts 2 and 9 get identical router rows, as do 5 and
     6, all scaled to win; the selection must be the reference's (logit desc, index asc), i.e. the
     oracle's routeur_topk on the same logits, and the weights its f64 softmax."""
-    E, k, N = 12, 4, (16, 32)
+    E, k = 12, 4
     couche = codeur.CoucheSynthetique(2029, 0, E, GPT, N_delta=N[0], N_codes=N[1])
     freqs = couche.freqs()
     luts = O.luts_couche([[freqs[j][t] for t in range(4)] for j in range(3)])
@@ -249,7 +260,7 @@ def test_fused_moe_router_nan_never_chosen(fz):
     reference does (a NaN is never ordered before another logit), and rank the others unchanged:
     rows 2 = 9 tied and scaled to win, row 5 NaN, row 6 scaled to win, so the fourth choice is the
     best of the rest; indices and weights equal the oracle's routeur_topk."""
-    E, k, N = 12, 4, (16, 32)
+    E, k, N = 12, 4, (2, 16)
     couche = codeur.CoucheSynthetique(2031, 0, E, GPT, N_delta=N[0], N_codes=N[1])
     freqs = couche.freqs()
     luts = O.luts_couche([[freqs[j][t] for t in range(4)] for j in range(3)])
@@ -280,10 +291,11 @@ def test_fused_moe_router_nan_never_chosen(fz):
     couche.liberer()
 
 
-def test_fused_moe_layer_bad_parts(fz):
+@pytest.mark.parametrize("N", [(8, 8), (1, 16)])
+def test_fused_moe_layer_bad_parts(fz, N):
     """A layer whose parts all fail the mount checks: the step counts format errors in every pass
     that meets a bad directory entry and leaves the residual alone (nothing is combined)."""
-    E, k, N = 6, 4, (8, 8)
+    E, k = 6, 4
     dims = DimsExpert.de([256, 256, 256], [256, 256, 256])
     couche = codeur.CoucheSynthetique(77, 0, E, dims, N_delta=N[0], N_codes=N[1])
     freqs = couche.freqs()

@@ -48,7 +48,7 @@ def _pas(fz, couche, E, dims, k, N, x, residu0, sans_alloc):
 
 def test_allocation_free_step_equals_the_allocating_one():
     fz = fusion.Fusion()
-    cas = [(2050, 16, DimsExpert.gpt_oss(), 4, (4, 16)),
+    cas = [(2050, 16, DimsExpert.gpt_oss(), 4, (2, 16)),
            (2051, 6, DimsExpert.de([256, 256, 320], [320, 320, 256]), 2, (2, 8))]
     for graine, E, dims, k, N in cas:
         assert fusion.taille_travail_couche(dims, E, k, N[1]) <= fusion.octets_scratch()

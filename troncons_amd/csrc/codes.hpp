@@ -1,0 +1,314 @@
+// codes.hpp — the CODES_CTX pass of the fused path with each CODES tile's DELTA decoded by the same
+// half-wavefront right before it (gfx950). No block entry goes through device memory and no DELTA
+// pass is launched.
+//
+// Streams of N_codes = 16 macro-steps per CODES tile: tile t covers blocks 128t .. 128t + 127, and
+// its E8M0 scales and contexts are DELTA macro-step t. With N_delta = 1 that is DELTA tile t; with
+// N_delta = 2 it is the first or second macro-step of DELTA tile t / 2 (the half-wavefront decodes
+// that tile from its start). Everything a tile start needs from device memory is read one tile
+// ahead into registers (Avance): the CODES lane states, the first 1 KiB of the CODES tile's words,
+// the DELTA lane states and the first 512 bytes of its words, the row medians. At the tile start
+// the half-wavefront
+//   1. lands the DELTA words in its ring and decodes the DELTA macro-step(s) with the layer's
+//      reference-format DELTA LUT (read through the L1: 4 to 8 steps per tile, against 64 CODES
+//      steps), giving 4 delta bytes per lane (blocks 4v .. 4v + 3 of the tile);
+//   2. turns them into the tile's 128 block entries (entree_bloc: e = (med + delta - 128) mod 256,
+//      the context class of delta, column, row start) in its LDS entry area;
+//   3. lands the CODES words in the ring (over the DELTA words) and decodes the tile as
+//      corps_gemv_rapide does.
+// A DELTA tile's end checks (every lane back to L, word pointer on the next tile's start) are made
+// by the half-wavefront that decodes its last macro-step.
+#pragma once
+
+#include "fusion_corps.hpp"
+
+namespace trc {
+
+// A tile's streams read one tile ahead (per half-wavefront, lane v of the half).
+struct Avance {
+    TeteTuile tete;        // CODES: lane state, first word, word the decode must end on
+    u32x4 mots0, mots1;    // CODES: bytes 16v and 512 + 16v of the tile's 16-aligned word area
+    uint32_t xd;           // DELTA: lane state at the start of the DELTA tile
+    uint32_t dDebut;       // DELTA: its first word
+    uint32_t dAttendu;     // DELTA: the word its decode must end on
+    u32x4 dmots;           // DELTA: bytes 16v of its 16-aligned word area (its first 512 bytes)
+    uint32_t med0, med1;   // medians of the rows of blocks 4v and 4v + 3 of the CODES tile
+};
+
+// 16 bytes at byte `o` of a stream of `n` bytes (f.p 16-aligned), read at an address clamped to the
+// stream's last 16-aligned 16 bytes: loads never leave the stream (the clamped lanes' bytes lie past
+// the last word and are never decoded).
+__device__ __forceinline__ u32x4 lire16_flux(const uint8_t* p, uint32_t n, uint32_t o) {
+    const uint32_t dernier = n >= 16u ? ((n - 16u) & ~15u) : 0u;
+    return *glob<u32x4>(p + min(o, dernier));
+}
+
+// Streams of CODES tile t (and, with DELTA, its DELTA tile) for lane v of a half-wavefront.
+template <bool DELTA>
+__device__ __forceinline__ Avance lire_avance(const EnteteRans& hc, const DescFlux& fc, const EnteteRans& hd,
+                                              const DescFlux& fd, const uint8_t* med, uint32_t R, uint32_t B,
+                                              uint32_t t, uint32_t v) {
+    Avance a;
+    a.tete = lire_tete(hc, t, v);
+    const bool tuile = t < hc.T;
+    const uint32_t base_c = uint32_t(reinterpret_cast<const uint8_t*>(hc.mots) - fc.p) + 2u * a.tete.debut;
+    const uint32_t g0c = base_c & ~15u;
+    a.mots0 = tuile ? lire16_flux(fc.p, fc.longueur, g0c + 16u * v) : u32x4{0u, 0u, 0u, 0u};
+    a.mots1 = tuile ? lire16_flux(fc.p, fc.longueur, g0c + 512u + 16u * v) : u32x4{0u, 0u, 0u, 0u};
+    a.xd = L;
+    a.dDebut = a.dAttendu = 0;
+    a.dmots = u32x4{0u, 0u, 0u, 0u};
+    a.med0 = a.med1 = 0;
+    if (DELTA) {
+        const uint32_t tau = t / hd.N;  // N_delta is 1 or 2
+        const TeteTuile td = lire_tete(hd, tau, v);
+        a.xd = td.x;
+        a.dDebut = td.debut;
+        a.dAttendu = td.attendu;
+        const uint32_t base_d = uint32_t(reinterpret_cast<const uint8_t*>(hd.mots) - fd.p) + 2u * td.debut;
+        if (tuile && tau < hd.T) a.dmots = lire16_flux(fd.p, fd.longueur, (base_d & ~15u) + 16u * v);
+        const uint32_t bloc0 = 128u * t + 4u * v;
+        a.med0 = tuile ? uint32_t(glob<uint8_t>(med)[min(bloc0 / B, R - 1u)]) : 0u;
+        a.med1 = tuile ? uint32_t(glob<uint8_t>(med)[min((bloc0 + 3u) / B, R - 1u)]) : 0u;
+    }
+    return a;
+}
+
+// One DELTA step with the reference-format LUT s | (f-1) << 8 | b << 20 read from device memory
+// (its lines stay in the L1: every tile start of the block reads it), words from the ring.
+template <bool TOUS_ACTIFS>
+__device__ __forceinline__ uint32_t pas_delta(uint32_t& x, uint32_t o2, uint32_t& compte, gptr<uint32_t> lutd,
+                                              uint32_t anneau, uint32_t decal, uint32_t masque_inf, bool actif) {
+    const uint32_t e = lutd[x & (M - 1u)];
+    const uint32_t y = __umul24(((e >> 8) & 0xFFFu) + 1u, x >> PROBA_BITS) + (e >> 20);
+    const bool besoin = (TOUS_ACTIFS || actif) && (y < L);
+    const uint64_t vote = __builtin_amdgcn_ballot_w64(besoin);
+    const uint32_t moitie = uint32_t(vote >> decal);
+    const uint32_t adr = ((o2 + 2u * (compte + __popc(moitie & masque_inf))) & (OCTETS_ANNEAU - 1u)) | anneau;
+    const uint32_t w = lire_lds<uint16_t>(adr);
+    const uint32_t suivant = besoin ? ((y << 16) | w) : y;
+    x = (TOUS_ACTIFS || actif) ? suivant : x;
+    compte += __popc(moitie);
+    return e & 0xFFu;
+}
+
+// The 4 block entries of lane v (blocks 4v .. 4v + 3 of CODES tile t) from its 4 delta bytes.
+__device__ __forceinline__ u32x4 entrees_de_delta(uint32_t mot, const Avance& a, uint32_t bloc0, uint32_t nblocs,
+                                                  uint32_t B) {
+    u32x4 s;
+    const uint32_t ligne0 = bloc0 / B;
+    uint32_t col = bloc0 - ligne0 * B, ligne = ligne0;
+#pragma unroll
+    for (uint32_t k = 0; k < 4; ++k) {
+        const uint32_t d = (mot >> (8u * k)) & 255u;
+        const uint32_t med = ligne == ligne0 ? a.med0 : a.med1;
+        s[k] = bloc0 + k < nblocs ? entree_bloc((med + d - 128u) & 255u, classe_delta(d), col, col == 0u)
+                                  : ENTREE_BOURRAGE;
+        ++col;
+        if (col == B) {  // B >= 8: four blocks span at most two rows
+            col = 0;
+            ++ligne;
+        }
+    }
+    return s;
+}
+
+// What the CODES pass needs of a job in the internal-DELTA mode: both streams' headers, the
+// medians, the DELTA LUT. bon: every check passed and the tile lengths are the mode's.
+struct PrepCodes {
+    DescFlux fc, fd;
+    EnteteRans hc, hd;
+    const uint8_t* med;
+    bool bon;
+};
+
+__device__ __forceinline__ PrepCodes preparer_codes(const Tache& tc, const MatricePartie& m) {
+    const uint32_t B = tc.colonnes / 32u;
+    PrepCodes p;
+    p.bon = m.bon != 0 && tc.colonnes % 32u == 0 && B >= 8u && tc.lignes > 0 && m.cN == 16u &&
+            (m.dN == 1u || m.dN == 2u) && (B - 1u) / (8u * m.cN) + 2u <= tc.kmax;
+    p.fc = m.codes;
+    p.fd = m.delta;
+    p.hc = entete_de(m.codes, m.cP, m.cN, m.cT, m.cW);
+    p.hd = entete_de(m.delta, m.dP, m.dN, m.dT, m.dW);
+    p.med = m.med.p;
+    return p;
+}
+
+// The first tile of the calling lane's half-wavefront (tile loops start at 2 * global wavefront).
+template <bool DELTA>
+__device__ __forceinline__ Avance premiere_avance(const PrepCodes& p, uint32_t R, uint32_t B) {
+    const uint32_t vague = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    return lire_avance<DELTA>(p.hc, p.fc, p.hd, p.fd, p.med, R, B, 2u * vague + (__lane_id() >= 32u ? 1u : 0u),
+                              __lane_id() & 31u);
+}
+
+// CODES_CTX tiles -> partial sums of W x, x in LDS, the tiles' entries decoded here from DELTA.
+// `avance0`: premiere_avance(p), read by the caller before its barrier. lutd: the job's DELTA LUT
+// (reference format) in device memory.
+__device__ __forceinline__ void corps_codes(const Tache& tc, const PrepCodes& p, uint8_t* lds, const uint32_t* lutd_,
+                                            uint32_t* __restrict__ controle, const Avance& avance0) {
+    const EnteteRans& h = p.hc;
+    const EnteteRans& hd = p.hd;
+    const uint32_t R = tc.lignes, B = tc.colonnes / 32u, nblocs = R * B;
+    const gptr<uint32_t> lutd = glob<uint32_t>(lutd_);
+    float* __restrict__ partiels = reinterpret_cast<float*>(tc.partiels);
+    const uint32_t kmax = tc.kmax;
+    const uint32_t bpt = 8u * h.N;
+
+    const uint32_t lane = __lane_id();
+    const uint32_t v = lane & 31u;
+    const bool haut = lane >= 32u;
+    const uint32_t decal = haut ? 32u : 0u, masque_inf = (1u << v) - 1u;
+    const uint32_t q = v >> 2, q4 = v & 3u;
+    const uint32_t vagues_bloc = blockDim.x >> 6;
+    const uint32_t vague = uniforme32(blockIdx.x * vagues_bloc + (threadIdx.x >> 6));
+    const uint32_t n_vagues = gridDim.x * vagues_bloc;
+    const uint32_t demi = (threadIdx.x >> 5) & (2u * vagues_bloc - 1u);
+    const uint32_t base = adresse_lds(lds);
+    const uint32_t a_lut = base + LDS_LUT;
+    const uint32_t a_x = base + LDS_X + 16u * q4;
+    const uint32_t a_anneau = base + LDS_ANNEAUX + demi * OCTETS_ANNEAU;
+    const uint32_t a_ent = base + LDS_ENT + demi * (ENT_PAR_TUILE * 4u);
+    const uint32_t a_ent_q = a_ent + 4u * q;
+    const uint32_t hN = uniforme32(h.N), hT = uniforme32(h.T), nmacro = uniforme32(h.P / 128u);
+    const uint32_t dN = uniforme32(hd.N), dT = uniforme32(hd.T), nmacro_d = uniforme32(hd.P / 128u);
+    const uint32_t mots_c = uint32_t(reinterpret_cast<const uint8_t*>(h.mots) - p.fc.p);
+    const uint32_t mots_d = uint32_t(reinterpret_cast<const uint8_t*>(hd.mots) - p.fd.p);
+    uint32_t hors_l = 0, pointeur = 0;
+    Avance av = avance0;
+    for (uint32_t t0 = 2u * vague; t0 < hT; t0 += 2u * n_vagues) {
+        const uint32_t t = t0 + (haut ? 1u : 0u);
+        const bool tuile = t < hT;
+        const uint32_t nb_a = min(hN, nmacro - t0 * hN);
+        const uint32_t nb_b = (t0 + 1u < hT) ? min(hN, nmacro - (t0 + 1u) * hN) : 0u;
+        const uint32_t nb = haut ? nb_b : nb_a;
+        const uint32_t m0 = (tuile ? t : t0) * hN;
+        const Avance cur = av;
+
+        // 1. DELTA: the half's DELTA tile from its start to macro-step t mod N_delta (DELTA tile
+        // t / N_delta covers CODES tiles t - t mod N_delta ..), words from the ring
+        const uint32_t saut = t - (t / dN) * dN;   // DELTA macro-steps before this tile's
+        const uint32_t saut_max = uniforme32(dN == 1u ? 0u : 1u);
+        ecrire_lds<u32x4>(a_anneau + 16u * v, cur.dmots);
+        {
+            // two DELTA macro-steps can read up to 512 + 15 bytes: when the DELTA tile's words pass
+            // the 512 read ahead (rare: about 50 bytes per macro-step here), the rest is read now
+            const uint32_t o_d = (mots_d + 2u * cur.dDebut) & 15u;
+            const bool long_d = tuile && o_d + 2u * (cur.dAttendu - cur.dDebut) > 512u;
+            if (__builtin_amdgcn_ballot_w64(long_d) != 0) {
+                const uint32_t g0d = (mots_d + 2u * cur.dDebut) & ~15u;
+                const u32x4 suite = long_d ? lire16_flux(p.fd.p, p.fd.longueur, g0d + 512u + 16u * v)
+                                           : u32x4{0u, 0u, 0u, 0u};
+                if (long_d) ecrire_lds<u32x4>(a_anneau + 512u + 16u * v, suite);
+            }
+        }
+        uint32_t xd = cur.xd, od = ((mots_d + 2u * cur.dDebut) & 15u), mot = 0;
+        for (uint32_t md = 0; md <= saut_max; ++md) {
+            const bool actif = tuile && md <= saut;
+            uint32_t compte = 0, m4 = 0;
+#pragma unroll
+            for (uint32_t k = 0; k < 4; ++k)
+                m4 |= pas_delta<false>(xd, od, compte, lutd, a_anneau, decal, masque_inf, actif) << (8u * k);
+            od += 2u * compte;
+            if (md == saut) mot = m4;
+        }
+        // the DELTA tile's end checks, by the half that decoded its last macro-step
+        const uint32_t tau = t / dN;
+        const uint32_t nbd = tau < dT ? min(dN, nmacro_d - tau * dN) : 0u;
+        if (tuile && saut + 1u == nbd) {
+            hors_l += (xd != L) ? 1u : 0u;
+            pointeur += (v == 0 && cur.dDebut + (od - ((mots_d + 2u * cur.dDebut) & 15u)) / 2u != cur.dAttendu) ? 1u : 0u;
+        }
+        // 2. the tile's 128 block entries
+        if (tuile) ecrire_lds<u32x4>(a_ent + 16u * v, entrees_de_delta(mot, cur, 128u * t + 4u * v, nblocs, B));
+        // 3. the CODES words over the DELTA ones, and the next pair's streams read ahead
+        ecrire_lds<u32x4>(a_anneau + 16u * v, cur.mots0);
+        ecrire_lds<u32x4>(a_anneau + 512u + 16u * v, cur.mots1);
+        av = lire_avance<true>(h, p.fc, hd, p.fd, p.med, R, B, t + 2u * n_vagues, v);
+        AnneauR a;
+        {
+            const uint32_t mot0 = mots_c + 2u * cur.tete.debut;
+            a.flux = p.fc.p;
+            a.g0 = mot0 & ~15u;
+            a.fin = p.fc.longueur;
+            a.lds = a_anneau;
+            a.o2 = mot0 - a.g0;
+            a.charge = OCTETS_ANNEAU / OCTETS_MORCEAU;
+            a.limite = a.charge * OCTETS_MORCEAU - FENETRE;
+            a.vol = u32x2{0u, 0u};
+            a.en_vol = false;
+        }
+        uint32_t x = cur.tete.x;
+        const uint32_t debut = cur.tete.debut, attendu = cur.tete.attendu;
+        const uint32_t o0 = a.o2;
+        uint32_t rho = (m0 * 8u) / B;
+        const uint32_t rho0 = rho, case0 = t - premiere_tuile(rho0, B, bpt);
+        auto ecrire = [&](float s) { partiels[rho * kmax + (rho == rho0 ? case0 : 0u)] = s; };
+        uint32_t ent_suiv = tuile ? lire_lds<uint32_t>(a_ent_q) : ENTREE_BOURRAGE;
+        const uint32_t nb_min = min(nb_a, nb_b);
+        float acc = 0.0f;
+        auto macro = [&](auto tous, uint32_t m) {
+            constexpr bool TOUS = decltype(tous)::value;
+            const bool actif = TOUS || m < nb;
+            const uint32_t ent = actif ? ent_suiv : ENTREE_BOURRAGE;
+            const uint32_t ax = (ent & ENT_X) | a_x;
+            const f32x4 xa = lire_lds<f32x4>(ax);
+            const f32x4 xb = lire_lds<f32x4>(ax + 64u);
+            ent_suiv = lire_lds<uint32_t>(a_ent_q + 32u * ((m + 1u) & 15u));
+            const uint32_t lt = a_lut + (ent & ENT_CTX);
+            uint32_t compte = 0;
+            const uint32_t e0 = pas_r<TOUS>(x, a.o2, compte, lt, a_anneau, decal, masque_inf, actif);
+            const uint32_t e1 = pas_r<TOUS>(x, a.o2, compte, lt, a_anneau, decal, masque_inf, actif);
+            const uint32_t e2 = pas_r<TOUS>(x, a.o2, compte, lt, a_anneau, decal, masque_inf, actif);
+            const uint32_t e3 = pas_r<TOUS>(x, a.o2, compte, lt, a_anneau, decal, masque_inf, actif);
+            a.o2 += 2u * compte;
+            avancer_anneau_r(a, v, actif);
+            const f32x2 w0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(e0, 2.0f, 3);
+            const f32x2 w1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(e1, 2.0f, 3);
+            const f32x2 w2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(e2, 2.0f, 3);
+            const f32x2 w3 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(e3, 2.0f, 3);
+            float d = w0.x * xa.x;
+            d = fmaf(w0.y, xb.x, d);
+            d = fmaf(w1.x, xa.y, d);
+            d = fmaf(w1.y, xb.y, d);
+            d = fmaf(w2.x, xa.z, d);
+            d = fmaf(w2.y, xb.z, d);
+            d = fmaf(w3.x, xa.w, d);
+            d = fmaf(w3.y, xb.w, d);
+            const float c = __builtin_amdgcn_ldexpf(d, int(ent << 7) >> 24);
+            const bool nouvelle = int(ent) < 0 && !(m == 0u && q == 0u && actif);
+            const uint64_t vote = __builtin_amdgcn_ballot_w64(nouvelle);
+            if (vote == 0) {
+                if (TOUS || actif) acc += c;
+            } else {
+                const uint32_t moitie = uint32_t(vote >> decal);
+                const uint32_t premier = moitie != 0u ? uint32_t(__builtin_ctz(moitie)) : 32u;
+                const bool apres = v >= premier;
+                if (!apres && (TOUS || actif)) acc += c;
+                const float s = somme_demi_f32(acc);
+                if (moitie != 0u) {
+                    if (v == 0 && actif && rho < R) ecrire(s);
+                    acc = apres ? c : 0.0f;
+                    ++rho;
+                }
+            }
+        };
+        uint32_t m = 0;
+        for (; m + 1u < nb_min; m += 2u) {
+            macro(std::true_type{}, m);
+            macro(std::true_type{}, m + 1u);
+        }
+        if (m < nb_min) macro(std::true_type{}, m++);
+        for (; m < nb_a; ++m) macro(std::false_type{}, m);
+        const float s = somme_demi_f32(acc);
+        if (tuile) {
+            if (v == 0 && rho < R) ecrire(s);
+            hors_l += (x != L) ? 1u : 0u;
+            pointeur += (v == 0 && debut + (a.o2 - o0) / 2u != attendu) ? 1u : 0u;
+        }
+    }
+    verser_controle(controle, hors_l, pointeur);
+}
+
+}  // namespace trc

@@ -27,6 +27,7 @@
 
 #include "anneau.hpp"
 #include "chrono.hpp"
+#include "codes.hpp"
 #include "commun.hpp"
 #include "erreurs.hpp"
 #include "fusion_corps.hpp"
@@ -195,6 +196,102 @@ fusion_gemv(trc::Taches taches, const uint32_t* __restrict__ luts, uint32_t* __r
     }
     __syncthreads();
     if (bon) corps_gemv_rapide(tc, p, lds, controle, tete0);
+}
+
+// CODES pass with each tile's DELTA decoded in the kernel (codes.hpp; streams with N_codes = 16 and
+// N_delta 1 or 2), x in LDS. MoE gate/up launches with OPT_TOPK run the router's top-k first (every
+// block, by ranks over the logits: the reference's order and tie rule, deterministic, so all blocks
+// agree; block (0, 0) publishes indices and weights), take their expert's matrix from the directory
+// and publish the selected experts' three records (resolus) for the down pass and the combine.
+// Down launches (OPT_SWIGLU) build x in LDS as the SwiGLU of the expert's gate/up rows.
+constexpr uint32_t OPT_TOPK = 2u;
+
+extern "C" __global__ void __launch_bounds__(trc::FILS_GEMV_MAX)
+fusion_codes(trc::Taches taches, const uint32_t* __restrict__ luts, uint32_t* __restrict__ controle) {
+    using namespace trc;
+    __shared__ __attribute__((aligned(16384))) uint8_t lds[LDS_GEMV];
+    const bool topk = (taches.options & OPT_TOPK) != 0u;
+    const bool swiglu = (taches.options & OPT_SWIGLU) != 0u;
+    const uint32_t j = topk ? (blockIdx.y & 1u) : min(uniforme32(taches[blockIdx.y].j), 2u);
+    const uint32_t* lut_src = luts + (uint64_t(j) * 4u + 1u) * M;
+    ChargeLut<3> charge_lut;
+    charge_lut.demarrer(lut_src, 3u * M / 4u);
+    Tache tc;
+    if (topk) {
+        // the top-k in the entry area (free until the tiles start)
+        const ParamsMoe& pm = taches.moe;
+        float* lg = reinterpret_cast<float*>(lds + LDS_ENT);
+        uint32_t* choisis = reinterpret_cast<uint32_t*>(lds + LDS_ENT + 4u * EXPERTS_MAX);
+        const float* logits = reinterpret_cast<const float*>(pm.logits);
+        for (uint32_t e = threadIdx.x; e < pm.E; e += blockDim.x) lg[e] = logits[e];
+        if (threadIdx.x < TOPK_MAX) choisis[threadIdx.x] = 0xFFFFFFFFu;
+        __syncthreads();
+        choisir_topk(lg, pm.E, pm.k, choisis);
+        __syncthreads();
+        if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x < 64u) {
+            float w[TOPK_MAX];
+            poids_topk(lg, choisis, pm.k, w);
+            if (threadIdx.x < pm.k) {
+                float wr = w[0];
+#pragma unroll
+                for (uint32_t r = 1; r < TOPK_MAX; ++r) wr = threadIdx.x == r ? w[r] : wr;
+                reinterpret_cast<uint32_t*>(pm.indices)[threadIdx.x] = choisis[threadIdx.x];
+                reinterpret_cast<float*>(pm.poids)[threadIdx.x] = wr;
+            }
+        }
+        const uint32_t i = blockIdx.y >> 1;
+        const uint32_t e = choisis[i];
+        tc = uniforme(tache_moe_e(pm, i, j, e));
+        // the selected experts' records for the later passes: gate (with down) and up
+        if (blockIdx.x == 0 && threadIdx.x < 64u) {
+            const uint32_t jj = threadIdx.x == 0 ? j : 2u;
+            if (threadIdx.x == 0 || (threadIdx.x == 1 && j == 0)) {
+                MatricePartie r;
+                std::memset(&r, 0, sizeof(r));
+                if (e < pm.E)
+                    r = *reinterpret_cast<const MatricePartie*>(pm.repertoire + uint64_t(e * 3u + jj) * sizeof(MatricePartie));
+                ecrire_matrice(reinterpret_cast<void*>(pm.resolus + uint64_t(i * 3u + jj) * sizeof(MatricePartie)), r);
+            }
+        }
+    } else {
+        tc = uniforme(taches[blockIdx.y]);
+    }
+    const bool x_lds = tc.colonnes <= X_LDS_MAX;
+    const uint32_t n16 = x_lds ? tc.colonnes / 4u : 0u;
+    u32x4 xv[4];
+#pragma unroll
+    for (uint32_t i = 0; i < 4; ++i) {
+        const uint32_t k = threadIdx.x + i * blockDim.x;
+        if (!swiglu && k < n16) xv[i] = glob<u32x4>(reinterpret_cast<const void*>(tc.x))[k];
+    }
+    const PrepCodes p = preparer_codes(tc, obtenir_matrice(tc));
+    const bool bon = p.bon && x_lds;
+    const uint32_t B = tc.colonnes / 32u;
+    const Avance avance0 = bon ? premiere_avance<true>(p, tc.lignes, B) : Avance{};
+    charge_lut.poser(lut_src, reinterpret_cast<uint2*>(lds + LDS_LUT), 3u * M / 4u);
+    if (!bon && threadIdx.x == 0 && blockIdx.x == 0) atomicAdd(&controle[CTL_FORMAT], 1u);
+    if (bon) {
+        if (swiglu) {
+            Fin* fins = reinterpret_cast<Fin*>(lds + LDS_ENT);
+            const uint32_t w = threadIdx.x >> 6;
+            if (w < 2u) {
+                const Fin f = preparer_fin(uniforme(tache_moe(taches.moe, blockIdx.y, w)));
+                if (__lane_id() == 0) fins[w] = f;
+            }
+            __syncthreads();
+            swiglu_vers_lds(fins[0], fins[1], tc.colonnes, reinterpret_cast<float*>(lds + LDS_X));
+        } else {
+#pragma unroll
+            for (uint32_t i = 0; i < 4; ++i) {
+                const uint32_t k = threadIdx.x + i * blockDim.x;
+                if (k < n16) *reinterpret_cast<u32x4*>(lds + LDS_X + 16u * k) = xv[i];
+            }
+        }
+        if (threadIdx.x < 8u)
+            *reinterpret_cast<u32x4*>(lds + LDS_X + COLONNE_NULLE * 128u + 16u * threadIdx.x) = u32x4{0u, 0u, 0u, 0u};
+    }
+    __syncthreads();
+    if (bon) corps_codes(tc, p, lds, luts + uint64_t(j) * 4u * M, controle, avance0);
 }
 
 // CODES pass, x read from device memory (rows of any width).
@@ -382,6 +479,14 @@ uint64_t pas_tache(uint32_t R, uint32_t C, uint32_t n_codes) {
     return octets_ech(R, C) + al(4ull * R * kmax_pour(C, n_codes));
 }
 
+// The CODES pass decodes each tile's DELTA itself (fusion_codes, codes.hpp) for streams of 16
+// macro-steps per CODES tile and 1 or 2 per DELTA tile: no DELTA launch, no block entries. Other
+// tile lengths take the DELTA pass, whose block entries go through the workspace.
+bool delta_interne(uint32_t n_delta, uint32_t n_codes) { return n_codes == 16 && (n_delta == 1 || n_delta == 2); }
+
+// Workspace piece of one matrix job in the internal-DELTA mode: its partial sums only.
+uint64_t pas_tache_interne(uint32_t R, uint32_t C) { return al(4ull * R * kmax_pour(C, 16)); }
+
 // Launch shape of a CODES pass over `jobs` matrices of R x C: 1024, 512 or 256 threads (32, 16 or 8
 // tiles) per block, the largest that still gives every CU of the chip a block, and at most about one
 // block per CU over all jobs (a block's LDS holds the three LUTs, so one fits a CU): wavefronts then
@@ -490,11 +595,20 @@ extern "C" int trc_gemv_fusionnee(trc_vue partie, uint32_t j, trc_vue luts, uint
     t.kmax = kmax_pour(colonnes, n_codes);
     t.lignes = lignes;
     t.colonnes = colonnes;
-    const Taches tv = par_valeur(&t, 1);
     const hipStream_t f = flux_de(flux);
     auto ctl = reinterpret_cast<uint32_t*>(controle.adresse);
     auto l = reinterpret_cast<const uint32_t*>(luts.adresse);
     const uint32_t B = colonnes / 32;
+    if (delta_interne(n_delta, n_codes) && colonnes <= trc::X_LDS_MAX) {
+        t.ech = 0;
+        t.partiels = travail.adresse;
+        const Taches tv = par_valeur(&t, 1);
+        const FormeGemv fo = forme_gemv(lignes, colonnes, n_codes, 1);
+        TRC_LANCER_N("fusion_codes", fusion_codes, fo.grille, fo.bloc, f, tv, l, ctl);
+        TRC_LANCER(fusion_finir, dim3((lignes + 255) / 256, 1), dim3(256), f, tv, reinterpret_cast<float*>(y.adresse), 0u);
+        return TRC_OK;
+    }
+    const Taches tv = par_valeur(&t, 1);
     TRC_LANCER(fusion_echelles, dim3(grille_tuiles(uint64_t(lignes) * B, n_delta, TUILES_ECHELLES), 1),
                dim3(trc::FILS_ECHELLES_FUSION), f, tv, l, ctl);
     TRC_LANCER_GEMV("fusion_gemv", forme_gemv(lignes, colonnes, n_codes, 1), f, tv, l, ctl);
@@ -547,10 +661,27 @@ extern "C" int trc_expert_fusionne(trc_vue partie, trc_vue luts, const trc_dims_
         t[j].partiels = t[j].ech + octets_ech(Rm, Cm);
         t[j].x = j < 2 ? x.adresse : act;
     }
-    const Taches trois = par_valeur(t, 3), bas = par_valeur(t + 2, 1);
     const hipStream_t f = flux_de(flux);
     const uint32_t* l = reinterpret_cast<const uint32_t*>(luts.adresse);
     auto ctl = reinterpret_cast<uint32_t*>(controle.adresse);
+    if (delta_interne(n_delta, n_codes) && Cm <= trc::X_LDS_MAX) {
+        const uint64_t pi = pas_tache_interne(Rm, Cm);
+        for (uint32_t j = 0; j < 3; ++j) {
+            t[j].ech = 0;
+            t[j].partiels = base + j * pi;
+        }
+        const Taches deux = par_valeur(t, 2), bas = par_valeur(t + 2, 1);
+        const FormeGemv fgu = forme_gemv(R, C, n_codes, 2);
+        TRC_LANCER_N("fusion_codes", fusion_codes, fgu.grille, fgu.bloc, f, deux, l, ctl);
+        TRC_LANCER(fusion_finir_swiglu, dim3((R + 255) / 256, 1), dim3(256), f, deux, reinterpret_cast<float*>(act), R);
+        const uint32_t R2 = dims->lignes[2];
+        const FormeGemv fb = forme_gemv(R2, dims->colonnes[2], n_codes, 1);
+        TRC_LANCER_N("fusion_codes", fusion_codes, fb.grille, fb.bloc, f, bas, l, ctl);
+        TRC_LANCER(fusion_finir, dim3((R2 + 255) / 256, 1), dim3(256), f, bas,
+                   reinterpret_cast<float*>(sortie.adresse), 0u);
+        return TRC_OK;
+    }
+    const Taches trois = par_valeur(t, 3), bas = par_valeur(t + 2, 1);
     TRC_LANCER(fusion_echelles, dim3(grille_tuiles(uint64_t(Rm) * (Cm / 32), n_delta, TUILES_ECHELLES), 3),
                dim3(trc::FILS_ECHELLES_FUSION), f, trois, l, ctl);
     TRC_LANCER_GEMV("fusion_gemv", forme_gemv(R, C, n_codes, 2), f, trois, l, ctl);
@@ -668,8 +799,15 @@ int couche_moe(trc_vue repertoire, uint32_t experts, trc_vue luts, const trc_dim
         pm.colonnes[j] = dims->colonnes[j];
         pm.kmax[j] = kmax_pour(dims->colonnes[j], n_codes);
     }
+    const bool interne = delta_interne(n_delta, n_codes);
+    if (interne) {  // partial sums only: no block entries in the workspace
+        pm.ech = 0;
+        pm.partiels = morceaux;
+        pm.pas = pas_tache_interne(Rm, Cm);
+    }
     const Taches t_delta = par_moe(pm, trc::TACHES_MOE_DELTA, 0), t_gu = par_moe(pm, trc::TACHES_MOE_GU, 0),
-                 t_bas = par_moe(pm, trc::TACHES_MOE_BAS, trc::OPT_SWIGLU);
+                 t_bas = par_moe(pm, trc::TACHES_MOE_BAS, trc::OPT_SWIGLU),
+                 t_gu_topk = par_moe(pm, trc::TACHES_MOE_GU, OPT_TOPK);
     const hipStream_t f = flux_de(flux);
     auto ctl = reinterpret_cast<uint32_t*>(controle.adresse);
     const uint32_t* l = reinterpret_cast<const uint32_t*>(luts.adresse);
@@ -684,6 +822,14 @@ int couche_moe(trc_vue repertoire, uint32_t experts, trc_vue luts, const trc_dim
         TRC_LANCER(fusion_routeur, dim3((experts + 7) / 8), dim3(256), f,
                    reinterpret_cast<const uint16_t*>(routeur.adresse), reinterpret_cast<const float*>(x.adresse),
                    reinterpret_cast<const float*>(routeur_biais.adresse), reinterpret_cast<float*>(logits), experts, C);
+    }
+    if (interne) {
+        // four launches: router, gate/up (top-k, DELTA and CODES), down (SwiGLU, DELTA, CODES), combine
+        const FormeGemv fgu = forme_gemv(R, C, n_codes, 2 * k), fb = forme_gemv(D, R, n_codes, k);
+        TRC_LANCER_N("fusion_codes/gate_up", fusion_codes, fgu.grille, fgu.bloc, f, t_gu_topk, l, ctl);
+        TRC_LANCER_N("fusion_codes/down", fusion_codes, fb.grille, fb.bloc, f, t_bas, l, ctl);
+        TRC_LANCER(fusion_finir_combiner, dim3((D + 255) / 256), dim3(256), f, t_bas);
+        return TRC_OK;
     }
     TRC_LANCER(fusion_echelles, dim3(grille_tuiles(uint64_t(R) * (C / 32), n_delta, TUILES_ECHELLES), 3 * k),
                dim3(trc::FILS_ECHELLES_FUSION), f, t_delta, l, ctl);
