@@ -60,6 +60,70 @@ def test_decoder_exact_against_oracle(k, N):
     assert list(ctl2) == [0, 0, 0, 0] and (empl2 == empl).all()
 
 
+# Blocks per row 1, 1, 2 (8200 rows: more than the 8192 medians kept in LDS), then 3, 3, 5.
+RAGGED = [DimsExpert.de([37, 37, 8200], [32, 32, 64]), DimsExpert.de([5, 5, 70], [96, 96, 160])]
+
+
+@pytest.mark.parametrize("forme", [0, 1])
+@pytest.mark.parametrize("N", [(3, 7), (5, 16), (256, 256), (2, 33)])
+def test_decoder_ragged_shapes_against_oracle(k, N, forme):
+    """Rows of 1-3 blocks (a lane's 4 deltas and a context group's blocks span several rows), a matrix
+    whose medians are read from device memory, tile lengths that are not multiples of the 16
+    macro-steps a CODES context group covers, stream padding past the last block; the raw copy of
+    the same matrices (region lengths that are not multiples of 16 bytes)."""
+    print(f"ragged decoder N {N} shape {forme}", flush=True)
+    dims = RAGGED[forme]
+    ex = Expert(2027 + N[0] * 100 + N[1] + forme, dims, N_delta=N[0], N_codes=N[1])
+    empl, ctl = _decoder(k, ex.partie, ex.luts, dims=dims)
+    assert list(ctl) == [0, 0, 0, 0]
+    oracle, octl = O.decoder_expert(ex.partie, ex.luts, dims.lignes, dims.colonnes)
+    assert list(octl) == [0, 0, 0, 0] and (oracle == empl).all()
+    assert (empl == ex.attendu).all()
+    p_brut, attendu_brut = ex.partie_brute()
+    sentinelle = zeros(K.taille_emplacement(dims))
+    sentinelle.fill_(0xA5)
+    ctl = zeros(16)
+    k.copier_brut(vue(dev(p_brut)), vue(sentinelle), dims, vue(ctl))
+    got = hote(sentinelle)
+    assert hote(ctl, np.uint32)[1] == 0
+    for j in range(3):  # region bytes equal, the slot's alignment padding untouched
+        d = K.disposition(dims, j)
+        R, C_ = dims.lignes[j], dims.colonnes[j]
+        nb = R * (C_ // 32)
+        for deb, lon in ((0, 16 * nb), (d.echelles, nb), (d.biais, 4 * R)):
+            a = d.base + deb
+            assert (got[a:a + lon] == attendu_brut[a:a + lon]).all(), (j, deb)
+        assert (got[d.base + 16 * nb:d.base + d.echelles] == 0xA5).all()
+        assert (got[d.base + d.echelles + nb:d.base + d.biais] == 0xA5).all()
+
+
+def test_gemv_ragged_shapes_bit_exact(k):
+    """The reference-order GEMVs on rows of 1-3 blocks and row counts that fill neither a half's row
+    pair nor a block's 16 rows; gemv_f32 on 37 rows of 37 quads (a lane's batch of four never
+    whole), with and without bias."""
+    rng = np.random.default_rng(3)
+    for f, dims in enumerate(RAGGED):
+        ex = Expert(2028 + f, dims, N_delta=16, N_codes=16)
+        empl = dev(ex.attendu)
+        for j in range(3):
+            R, C_ = dims.lignes[j], dims.colonnes[j]
+            d = K.disposition(dims, j)
+            x = O.synth_normale_bf16(5, j, f, C_, 1.0)
+            y = zeros(4 * R)
+            k.gemv(vue(empl, d.base, d.pas), vue(dev(x)), vue(y), R, C_)
+            ref = O.gemv_mxfp4(ex.attendu[d.base:d.base + d.pas], x, R, C_)
+            assert (hote(y, np.uint32) == ref.view(np.uint32)).all(), (f, j)
+    for R, C_ in ((37, 148), (1, 4), (33, 4 * 129)):
+        W = rng.standard_normal((R, C_)).astype(np.float32)
+        x = rng.standard_normal(C_).astype(np.float32)
+        b = rng.standard_normal(R).astype(np.float32)
+        y = zeros(4 * R)
+        k.gemv_f32(vue(dev(W)), vue(dev(x)), vue(dev(b)), vue(y), R, C_)
+        assert (hote(y, np.uint32) == O.gemv_f32(W, x, b).view(np.uint32)).all(), (R, C_)
+        k.gemv_f32(vue(dev(W)), vue(dev(x)), None, vue(y), R, C_)
+        assert (hote(y, np.uint32) == O.gemv_f32(W, x).view(np.uint32)).all(), (R, C_)
+
+
 def test_decoder_breaks_are_seen_carte_rs_247(k, expert_ref):
     ex = expert_ref
     p_brut, attendu_brut = ex.partie_brute()

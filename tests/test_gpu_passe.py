@@ -7,7 +7,8 @@
 - rmsnorm bit for bit against the oracle (same f64 tree), in place too;
 - rope_yarn within 1e-6 of the oracle (f64 libm functions may differ in the last bit), and the
   fixture's closed forms;
-- attention: the fixture's three cases, random heads within 1e-6 of the oracle and 1e-5 of f64;
+- attention: the fixture's three cases, random heads within 1e-6 of f64 and 3e-6 of the oracle's
+  reference-order result;
 - argmax: the fixture's tie and NaN, random vectors.
 """
 import numpy as np
@@ -226,9 +227,12 @@ def test_attention_random_against_oracle(k, position, fenetre):
     puits = rng.standard_normal(64).astype(np.float32)
     got = _attention(k, q, ck, cv, puits, p)
     ref = O.attention(q, ck, cv, puits, po)
-    assert np.abs(got - ref).max() <= 1e-6 * np.abs(ref).max()
     ref64 = attention_f64(q, ck, cv, puits, po)
-    assert np.abs(got - ref64).max() <= 1e-5 * np.abs(ref64).max()
+    # The one-pass running softmax adds its terms in 64-position chunks, the reference in four
+    # chains of every fourth position: it lands closer to f64 (at 8192 positions 2.4e-7 of max|out|
+    # against the reference order's 1.3e-6), and the two f32 results differ by about their sum.
+    assert np.abs(got - ref64).max() <= 1e-6 * np.abs(ref64).max()
+    assert np.abs(got - ref).max() <= 3e-6 * np.abs(ref).max()
 
 
 def test_argmax_ties_nan_and_random(k):

@@ -36,7 +36,7 @@ constexpr uint32_t FILS_ECHELLES = 128;  // 2 wavefronts = 4 DELTA tiles
 constexpr uint32_t FILS_CODES = 256;     // 4 wavefronts = 8 CODES_CTX tiles
 constexpr uint32_t FILS_BRUT = 256;
 constexpr uint32_t GEMV_FILS = 256;
-constexpr uint32_t GEMV_LIGNES_PAR_BLOC = 32;  // 8 half-wavefronts x 4 rows
+constexpr uint32_t GEMV_LIGNES_PAR_BLOC = 16;  // 8 half-wavefronts x 2 rows
 constexpr uint32_t LUTS_PAR_COUCHE = 3 * 4 * 4096;
 constexpr uint32_t MACRO_PAR_TUILE = 256;  // what the reference encoder writes; used for grids only
 

@@ -16,6 +16,7 @@
 
 #include "anneau.hpp"
 #include "commun.hpp"
+#include "entiers.hpp"
 
 namespace trc {
 
@@ -220,12 +221,11 @@ static_assert(LDS_GEMV == 160u * 1024u, "the CODES pass uses all 160 KiB of a CU
 constexpr uint32_t MED_LDS_MAX = 8192;          // rows whose medians the DELTA pass keeps in LDS
 
 // A job read by every lane (same address) made wave-uniform, so that the part reader and all the
-// job's scalars live in scalar registers.
-// (The builtin returns int: every result goes through uint32_t before any widening, otherwise an
-// address whose low word has bit 31 set would be sign-extended.)
+// job's scalars live in scalar registers. (The builtin returns int; elargir_u64 widens each half
+// through uint32_t, so that an address whose low word has bit 31 set is not sign-extended.)
 __device__ __forceinline__ uint32_t uniforme32(uint32_t v) { return uint32_t(__builtin_amdgcn_readfirstlane(v)); }
 __device__ __forceinline__ uint64_t uniforme64(uint64_t v) {
-    return uint64_t(uniforme32(uint32_t(v))) | (uint64_t(uniforme32(uint32_t(v >> 32))) << 32);
+    return elargir_u64(__builtin_amdgcn_readfirstlane(uint32_t(v)), __builtin_amdgcn_readfirstlane(uint32_t(v >> 32)));
 }
 __device__ __forceinline__ Tache uniforme(const Tache& t) {
     Tache u;

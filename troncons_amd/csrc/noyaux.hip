@@ -1,192 +1,251 @@
-// noyaux.hip — the reference kernel API of the expert hot path, written for gfx950.
+// noyaux.hip — the reference kernel API of the expert hot path (Noyaux, moteur/crates/trc-noyaux/
+// src/lib.rs), written for gfx950.
 //
-// Same names, arguments and results as the reference's CUDA kernels (moteur/crates/trc-noyaux/
-// noyaux/decodeur.cuh, gemv.cuh, passe.cuh) so that the engine's launch layer maps one to one;
-// the bodies are wave64-native: a wavefront decodes two rANS tiles (one per 32-lane half), the
-// LUTs sit in LDS, and the GEMV runs two reference "warps" per wavefront so that its operation
-// order (and therefore every output bit) is the reference's.
+// Same kernel names, arguments and results as the reference's (decodeur.cuh, gemv.cuh, passe.cuh),
+// so that the engine's launch layer maps one to one. The slot decoders run the fused path's rANS
+// engine (two tiles per wavefront, LDS word rings, 8-byte LUT entries) with a consumer that stores
+// into the slot; the GEMVs produce the reference's bits under the operation-order contract stated
+// above them, on a wave64 mapping of their own.
 //
 // Determinism: no floating-point atomics; the only atomics are integer control counters.
 #include <hip/hip_runtime.h>
 
 #include "commun.hpp"
+#include "entiers.hpp"
 #include "erreurs.hpp"
+#include "fusion_corps.hpp"
 #include "selection.hpp"
 
 namespace trc {
 
-// ===================================================================== decoder: DELTA -> scales
-__device__ __forceinline__ void corps_echelles(const uint8_t* __restrict__ partie, uint8_t* __restrict__ emplacement,
-                                               const uint32_t* __restrict__ luts, const trc_dims_expert& dims,
-                                               uint32_t* __restrict__ controle, uint32_t* lut, uint8_t* med_lds) {
-    const uint32_t j = blockIdx.y;
-    const uint32_t* src = luts + (uint64_t(j) * 4u + 0u) * M;
-    for (uint32_t i = threadIdx.x; i < M; i += blockDim.x) lut[i] = src[i];
-    __syncthreads();
+// ================================================================= slot decoders (gfx950 engine)
+//
+// Both decoders run the fused path's rANS engine (anneau.hpp): two tiles per wavefront (one per
+// 32-lane half), the tile's words staged in a 1 KiB LDS ring refilled one macro-step ahead, the
+// LUT re-expanded in LDS to 8-byte entries {f | s << 24, b} so a step is one v_mad_u32_u24.
+// Only the consumer differs from the fused passes: a macro-step's 4 bytes per lane are stored into
+// the slot instead of being multiplied against x.
+//
+// Lane v of a tile's half, in the tile's macro-step m (global macro-step g = t * N + m), decodes
+// word w = 32 g + v: for DELTA the deltas of blocks 4w .. 4w + 3, for CODES_CTX code bytes
+// 4w .. 4w + 3 of block w / 4. A block's row is block / B (B blocks per row), computed with a
+// multiply-high (Diviseur).
 
+// The half-wavefront's tile geometry and its end checks.
+struct Demi {
+    uint32_t v, decal, masque_inf, demi;  // lane in the half, its ballot shift, lower lanes, half index in the block
+    bool haut;
+};
+__device__ __forceinline__ Demi demi_courante() {
+    Demi d;
+    const uint32_t lane = __lane_id();
+    d.v = lane & 31u;
+    d.haut = lane >= 32u;
+    d.decal = d.haut ? 32u : 0u;
+    d.masque_inf = (1u << d.v) - 1u;
+    d.demi = threadIdx.x >> 5;
+    return d;
+}
+
+// End-of-tile checks (commun.cuh:197-218 semantics): every lane back at L, and the words consumed
+// ending exactly where the next tile's words start (or at W for the last tile).
+__device__ __forceinline__ void verifier_tuile(const EnteteRans& h, uint32_t t, uint32_t x, uint32_t debut,
+                                               uint32_t consommes, uint32_t v, uint32_t& hors_l, uint32_t& pointeur) {
+    hors_l += (x != L) ? 1u : 0u;
+    const uint32_t attendu = (t + 1u < h.T) ? h.debut[t + 1u] : h.W;
+    pointeur += (v == 0u && debut + consommes != attendu) ? 1u : 0u;
+}
+
+// Biases: a bit copy (as u32, so no conversion ever touches a NaN), 16 bytes at a time where both
+// sides allow it. Spread over the grid's x dimension.
+__device__ __forceinline__ void copier_biais(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst, uint32_t R) {
+    const uint32_t pas = gridDim.x * blockDim.x;
+    const uint32_t n16 = R / 4u;
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += pas)
+        ecrire_global<u32x4>(dst + 16u * i, glob<u32x4>(src)[i]);
+    for (uint32_t i = 4u * n16 + blockIdx.x * blockDim.x + threadIdx.x; i < R; i += pas)
+        ecrire_global<uint32_t>(dst + 4u * i, glob<uint32_t>(src)[i]);
+}
+
+template <uint32_t FILS>
+struct LdsEchelles {
+    uint2 lut[M];
+    __attribute__((aligned(16))) uint8_t anneaux[(FILS / 32u) * OCTETS_ANNEAU];
+    __attribute__((aligned(16))) uint8_t med[MED_LDS_MAX];
+};
+
+// ----------------------------------------------------------------- DELTA -> E8M0 scales of the slot
+// e(block) = (med[row] + delta - 128) mod 256 (rans.rs:231-280); biases copied bit for bit.
+template <uint32_t FILS>
+__device__ __forceinline__ void decoder_echelles_corps(const uint8_t* __restrict__ partie, uint8_t* __restrict__ emplacement,
+                                                      const uint32_t* __restrict__ luts, const trc_dims_expert& dims,
+                                                      uint32_t* __restrict__ controle, LdsEchelles<FILS>& s) {
+    const uint32_t j = blockIdx.y;
     const uint32_t R = choisir(dims.lignes, j), C = choisir(dims.colonnes, j);
     const uint32_t B = C / 32u, nblocs = R * B;
-    DescFlux fd, fm, fb;
+    constexpr uint8_t sortes[4] = {SORTE_DELTA, SORTE_MEDIANES, SORTE_BIAIS, 0};
+    DescFlux f[4];
     EnteteRans h;
-    const bool bon = (C % 32u == 0) && B > 0 && R > 0 && trouver_flux(partie, SORTE_DELTA, j, fd) &&
-                     trouver_flux(partie, SORTE_MEDIANES, j, fm) && trouver_flux(partie, SORTE_BIAIS, j, fb) &&
-                     fm.produits == R && fm.longueur >= R && fb.produits == 4u * R && fb.longueur >= 4u * R &&
-                     lire_entete(fd, nblocs, h);
-    if (!bon) {
+    const bool bon = C % 32u == 0 && B > 0 && R > 0 && trouver_flux_n(partie, sortes, 3, j, f) && f[1].produits == R &&
+                     f[1].longueur >= R && f[2].produits == 4u * R && f[2].longueur >= 4u * R &&
+                     lire_entete(f[0], nblocs, h);
+    if (!bon) {  // uniform over the block: every thread leaves here
         if (threadIdx.x == 0) atomicAdd(&controle[CTL_FORMAT], 1u);
         return;
     }
     const trc_disposition disp = disposition(dims, j);
     uint8_t* mat = emplacement + disp.base;
-    {  // biases: bit copy (u32: no conversion touches a NaN)
-        const uint32_t* bs = reinterpret_cast<const uint32_t*>(fb.p);
-        uint32_t* bd = reinterpret_cast<uint32_t*>(mat + disp.biais);
-        for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < R; i += gridDim.x * blockDim.x) bd[i] = bs[i];
-    }
-    const uint8_t* med = fm.p;
-    if (R <= 8192u) {
-        for (uint32_t i = threadIdx.x; i < R; i += blockDim.x) med_lds[i] = fm.p[i];
-        med = med_lds;
+    copier_biais(f[2].p, mat + disp.biais, R);
+    etendre_luts<(M / 4u + FILS - 1u) / FILS>(luts + uint64_t(j) * 4u * M, s.lut, M / 4u);
+    const uint8_t* med = f[1].p;
+    if (R <= MED_LDS_MAX) {
+        copier_vers_lds(f[1].p, R, f[1].longueur, s.med);
+        med = s.med;
     }
     __syncthreads();
 
-    uint8_t* ech = mat + disp.echelles;
-    const DemiVague dv = demi_vague();
-    const uint32_t v = __lane_id() & 31u;
-    const uint32_t vagues_bloc = blockDim.x >> 6;
-    const uint32_t vague = blockIdx.x * vagues_bloc + (threadIdx.x >> 6);
-    const uint32_t n_vagues = gridDim.x * vagues_bloc;
+    const Demi d = demi_courante();
+    const Diviseur parB = Diviseur::de(B);
+    const uint32_t vague = blockIdx.x * (FILS / 64u) + (threadIdx.x >> 6), n_vagues = gridDim.x * (FILS / 64u);
     const uint32_t nmacro = h.P / 128u;
+    uint8_t* ech = mat + disp.echelles;
     uint32_t hors_l = 0, pointeur = 0;
     for (uint32_t t0 = 2u * vague; t0 < h.T; t0 += 2u * n_vagues) {
-        const uint32_t t = t0 + (dv.haut ? 1u : 0u);
+        const uint32_t t = t0 + (d.haut ? 1u : 0u);
         const bool tuile = t < h.T;
-        const uint32_t nb_a = min(h.N, nmacro - t0 * h.N);
+        const uint32_t pas_bas = min(h.N, nmacro - t0 * h.N);  // the lower tile is never the shorter one
         const uint32_t nb = tuile ? min(h.N, nmacro - t * h.N) : 0u;
-        uint32_t x = tuile ? h.etats[t * VOIES + v] : L;
-        uint32_t ptr = tuile ? h.debut[t] : 0u;
-        // word w = m*32 + v carries the deltas of blocks 4w .. 4w+3; row and remainder of 4w are
-        // tracked without division (4w advances by 128 per macro-step).
-        uint32_t b0 = 4u * ((tuile ? t : t0) * h.N * VOIES + v);
-        uint32_t ligne = b0 / B, reste = b0 - ligne * B;
-        for (uint32_t m = 0; m < nb_a; ++m) {
+        uint32_t x = tuile ? h.etats[t * VOIES + d.v] : L;
+        const uint32_t debut = tuile ? h.debut[t] : 0u;
+        Anneau a = ouvrir_anneau(h, f[0], debut, d.demi * OCTETS_ANNEAU, s.anneaux, d.v, tuile);
+        const uint32_t o0 = a.o2;
+        for (uint32_t m = 0; m < pas_bas; ++m) {
             const bool actif = m < nb;
-            uint32_t mot = 0;
+            uint32_t deltas = 0;
 #pragma unroll
-            for (uint32_t k = 0; k < 4; ++k) mot |= pas_octet(x, ptr, lut, h.mots, h.W, dv, actif) << (8u * k);
-            if (actif) {
-                uint32_t sortie = 0;
+            for (uint32_t k = 0; k < 4; ++k)
+                deltas |= (pas_anneau<false>(x, a, s.lut, s.anneaux, d.decal, d.masque_inf, actif) >> 24) << (8u * k);
+            avancer_anneau(a, s.anneaux, d.v, actif);
+            const uint32_t b0 = 4u * ((t * h.N + m) * VOIES + d.v);
+            if (!actif || b0 >= nblocs) continue;  // stream padding past the last block
+            const uint32_t r0 = parB.quotient(b0), c0 = b0 - r0 * B;
+            uint32_t e4 = 0;
 #pragma unroll
-                for (uint32_t k = 0; k < 4; ++k) {
-                    uint32_t rk = ligne, qk = reste + k;
-                    while (qk >= B) {
-                        qk -= B;
-                        ++rk;
-                    }
-                    const uint32_t mk = rk < R ? uint32_t(med[rk]) : 0u;
-                    sortie |= ((mk + ((mot >> (8u * k)) & 255u) - 128u) & 255u) << (8u * k);
-                }
-                if (b0 + 3u < nblocs) {
-                    reinterpret_cast<uint32_t*>(ech)[b0 >> 2] = sortie;
-                } else {
-                    for (uint32_t k = 0; k < 4; ++k)
-                        if (b0 + k < nblocs) ech[b0 + k] = uint8_t(sortie >> (8u * k));
-                }
+            for (uint32_t k = 0; k < 4; ++k) {
+                const uint32_t r = c0 + k < B ? r0 : parB.quotient(b0 + k);
+                const uint32_t mr = r < R ? uint32_t(med[r]) : 0u;
+                e4 |= ((mr + ((deltas >> (8u * k)) & 255u) - 128u) & 255u) << (8u * k);
             }
-            b0 += 4u * VOIES;
-            reste += 4u * VOIES;
-            while (reste >= B) {
-                reste -= B;
-                ++ligne;
+            if (b0 + 4u <= nblocs) {
+                ecrire_global<uint32_t>(ech + b0, e4);  // b0 % 4 == 0 and the scales are 256-aligned
+            } else {
+                for (uint32_t k = 0; b0 + k < nblocs; ++k) ech[b0 + k] = uint8_t(e4 >> (8u * k));
             }
         }
-        if (tuile) {
-            hors_l += (x != L) ? 1u : 0u;
-            const uint32_t attendu = (t + 1 < h.T) ? h.debut[t + 1] : h.W;
-            pointeur += (v == 0 && ptr != attendu) ? 1u : 0u;
-        }
+        if (tuile) verifier_tuile(h, t, x, debut, (a.o2 - o0) / 2u, d.v, hors_l, pointeur);
     }
     verser_controle(controle, hors_l, pointeur);
 }
 
-// ============================================================== decoder: CODES_CTX -> code words
-__device__ __forceinline__ void corps_codes(const uint8_t* __restrict__ partie, uint8_t* __restrict__ emplacement,
-                                            const uint32_t* __restrict__ luts, const trc_dims_expert& dims,
-                                            uint32_t* __restrict__ controle, uint32_t (*lut)[M]) {
-    const uint32_t j = blockIdx.y;
-    {
-        const uint32_t* src = luts + (uint64_t(j) * 4u + 1u) * M;
-        uint32_t* dst = &lut[0][0];
-        for (uint32_t i = threadIdx.x; i < 3u * M; i += blockDim.x) dst[i] = src[i];
-    }
-    __syncthreads();
+// ------------------------------------------------------------ CODES_CTX -> code words of the slot
+// The context of block b is the class of delta = e(b) - med[row] + 128 (decodeur.cuh:185-192),
+// e(b) read back from the slot's scales (the DELTA decoder ran first on the same stream). Each half
+// stages the contexts of 16 macro-steps (128 blocks, 4 per lane) in LDS at a time; the scale bytes
+// of the next 16 are loaded one group ahead, so a group switch waits for nothing in the usual case.
+constexpr uint32_t FILS_CODES_SLOT = FILS_CODES;
+struct LdsCodes {
+    uint2 lut[3][M];
+    __attribute__((aligned(16))) uint8_t anneaux[(FILS_CODES_SLOT / 32u) * OCTETS_ANNEAU];
+    __attribute__((aligned(16))) uint8_t ctx[FILS_CODES_SLOT / 32u][128];
+    __attribute__((aligned(16))) uint8_t med[MED_LDS_MAX];
+};
 
+// Scale bytes of blocks b0 .. b0 + 3 (b0 % 4 == 0), 0 past the matrix.
+__device__ __forceinline__ uint32_t lire_echelles4(const uint8_t* ech, uint32_t b0, uint32_t nblocs) {
+    if (b0 + 4u <= nblocs) return *glob<uint32_t>(ech + b0);
+    uint32_t e4 = 0;
+    for (uint32_t k = 0; b0 + k < nblocs && k < 4u; ++k) e4 |= uint32_t(glob<uint8_t>(ech)[b0 + k]) << (8u * k);
+    return e4;
+}
+
+__device__ __forceinline__ uint32_t contextes4(uint32_t e4, uint32_t b0, uint32_t nblocs, const Diviseur& parB,
+                                               uint32_t B, const uint8_t* med) {
+    if (b0 >= nblocs) return 0u;
+    const uint32_t r0 = parB.quotient(b0), c0 = b0 - r0 * B;
+    uint32_t k4 = 0;
+#pragma unroll
+    for (uint32_t k = 0; k < 4; ++k) {
+        if (b0 + k >= nblocs) break;
+        const uint32_t r = c0 + k < B ? r0 : parB.quotient(b0 + k);
+        k4 |= classe_echelle((e4 >> (8u * k)) & 255u, med[r]) << (8u * k);
+    }
+    return k4;
+}
+
+__device__ __forceinline__ void decoder_codes_corps(const uint8_t* __restrict__ partie, uint8_t* __restrict__ emplacement,
+                                                   const uint32_t* __restrict__ luts, const trc_dims_expert& dims,
+                                                   uint32_t* __restrict__ controle, LdsCodes& s) {
+    constexpr uint32_t FILS = FILS_CODES_SLOT;
+    const uint32_t j = blockIdx.y;
     const uint32_t R = choisir(dims.lignes, j), C = choisir(dims.colonnes, j);
     const uint32_t B = C / 32u, nblocs = R * B;
-    DescFlux fc, fm;
+    constexpr uint8_t sortes[4] = {SORTE_CODES_CTX, SORTE_MEDIANES, 0, 0};
+    DescFlux f[4];
     EnteteRans h;
-    const bool bon = (C % 32u == 0) && B > 0 && R > 0 && trouver_flux(partie, SORTE_CODES_CTX, j, fc) &&
-                     trouver_flux(partie, SORTE_MEDIANES, j, fm) && fm.produits == R && fm.longueur >= R &&
-                     lire_entete(fc, nblocs * 16u, h);
+    const bool bon = C % 32u == 0 && B > 0 && R > 0 && trouver_flux_n(partie, sortes, 2, j, f) && f[1].produits == R &&
+                     f[1].longueur >= R && lire_entete(f[0], nblocs * 16u, h);
     if (!bon) {
         if (threadIdx.x == 0) atomicAdd(&controle[CTL_FORMAT], 1u);
         return;
     }
     const trc_disposition disp = disposition(dims, j);
     uint8_t* mat = emplacement + disp.base;
-    uint32_t* codes = reinterpret_cast<uint32_t*>(mat);
-    const uint8_t* ech = mat + disp.echelles;  // written by decoder_echelles
-    const uint8_t* __restrict__ med = fm.p;
+    const uint8_t* ech = mat + disp.echelles;
+    etendre_luts<(3u * M / 4u + FILS - 1u) / FILS>(luts + (uint64_t(j) * 4u + 1u) * M, &s.lut[0][0], 3u * M / 4u);
+    const uint8_t* med = f[1].p;
+    if (R <= MED_LDS_MAX) {
+        copier_vers_lds(f[1].p, R, f[1].longueur, s.med);
+        med = s.med;
+    }
+    __syncthreads();
 
-    const DemiVague dv = demi_vague();
-    const uint32_t v = __lane_id() & 31u;
-    const uint32_t vagues_bloc = blockDim.x >> 6;
-    const uint32_t vague = blockIdx.x * vagues_bloc + (threadIdx.x >> 6);
-    const uint32_t n_vagues = gridDim.x * vagues_bloc;
+    const Demi d = demi_courante();
+    const Diviseur parB = Diviseur::de(B);
+    const uint32_t vague = blockIdx.x * (FILS / 64u) + (threadIdx.x >> 6), n_vagues = gridDim.x * (FILS / 64u);
     const uint32_t nmacro = h.P / 128u;
-    const uint32_t mots_utiles = nblocs * 4u;
+    const uint32_t mots_utiles = 4u * nblocs;
+    const uint32_t a_ctx = adresse_lds(&s.ctx[d.demi][0]);
+    uint32_t* codes = reinterpret_cast<uint32_t*>(mat);
     uint32_t hors_l = 0, pointeur = 0;
     for (uint32_t t0 = 2u * vague; t0 < h.T; t0 += 2u * n_vagues) {
-        const uint32_t t = t0 + (dv.haut ? 1u : 0u);
+        const uint32_t t = t0 + (d.haut ? 1u : 0u);
         const bool tuile = t < h.T;
-        const uint32_t nb_a = min(h.N, nmacro - t0 * h.N);
+        const uint32_t pas_bas = min(h.N, nmacro - t0 * h.N);
         const uint32_t nb = tuile ? min(h.N, nmacro - t * h.N) : 0u;
-        uint32_t x = tuile ? h.etats[t * VOIES + v] : L;
-        uint32_t ptr = tuile ? h.debut[t] : 0u;
-        const uint32_t m0 = (tuile ? t : t0) * h.N;
-        // word w = m*32 + v belongs to block w/4 = 8m + v/4; its context needs that block's scale
-        // and its row median, fetched one macro-step ahead.
-        uint32_t bloc = (m0 * VOIES + v) >> 2;
-        uint32_t ligne = bloc / B, reste = bloc - ligne * B;
-        bool valide = tuile && bloc < nblocs;
-        uint32_t e_suiv = valide ? uint32_t(ech[bloc]) : 0u;
-        uint32_t m_suiv = valide ? uint32_t(med[ligne]) : 0u;
-        for (uint32_t m = 0; m < nb_a; ++m) {
+        const uint32_t g0 = (tuile ? t : t0) * h.N;  // the tile's first global macro-step
+        uint32_t x = tuile ? h.etats[t * VOIES + d.v] : L;
+        const uint32_t debut = tuile ? h.debut[t] : 0u;
+        uint32_t e_vol = tuile ? lire_echelles4(ech, 8u * g0 + 4u * d.v, nblocs) : 0u;
+        Anneau a = ouvrir_anneau(h, f[0], debut, d.demi * OCTETS_ANNEAU, s.anneaux, d.v, tuile);
+        const uint32_t o0 = a.o2;
+        for (uint32_t m = 0; m < pas_bas; ++m) {
             const bool actif = m < nb;
-            const uint32_t ctx = valide ? classe_echelle(e_suiv, m_suiv) : 0u;
-            const uint32_t w = (m0 + m) * VOIES + v;
-            bloc += 8u;
-            reste += 8u;
-            while (reste >= B) {
-                reste -= B;
-                ++ligne;
+            if ((m & 15u) == 0u) {  // a new group of 16 macro-steps: its contexts into LDS, the next group's scales requested
+                const uint32_t b0 = 8u * (g0 + m) + 4u * d.v;
+                ecrire_lds<uint32_t>(a_ctx + 4u * d.v, actif ? contextes4(e_vol, b0, nblocs, parB, B, med) : 0u);
+                if (m + 16u < nb) e_vol = lire_echelles4(ech, b0 + 128u, nblocs);
             }
-            valide = (m + 1u < nb) && bloc < nblocs;
-            if (valide) {
-                e_suiv = ech[bloc];
-                m_suiv = med[ligne];
-            }
-            const uint32_t* lt = lut[ctx];
+            const uint32_t kappa = lire_lds<uint8_t>(a_ctx + 8u * (m & 15u) + (d.v >> 2));
+            const uint2* lt = &s.lut[0][0] + kappa * M;
             uint32_t mot = 0;
 #pragma unroll
-            for (uint32_t k = 0; k < 4; ++k) mot |= pas_octet(x, ptr, lt, h.mots, h.W, dv, actif) << (8u * k);
-            if (actif && w < mots_utiles) codes[w] = mot;
+            for (uint32_t k = 0; k < 4; ++k)
+                mot |= (pas_anneau<false>(x, a, lt, s.anneaux, d.decal, d.masque_inf, actif) >> 24) << (8u * k);
+            avancer_anneau(a, s.anneaux, d.v, actif);
+            const uint32_t w = (g0 + m) * VOIES + d.v;
+            if (actif && w < mots_utiles) ecrire_global<uint32_t>(codes + w, mot);
         }
-        if (tuile) {
-            hors_l += (x != L) ? 1u : 0u;
-            const uint32_t attendu = (t + 1 < h.T) ? h.debut[t + 1] : h.W;
-            pointeur += (v == 0 && ptr != attendu) ? 1u : 0u;
-        }
+        if (tuile) verifier_tuile(h, t, x, debut, (a.o2 - o0) / 2u, d.v, hors_l, pointeur);
     }
     verser_controle(controle, hors_l, pointeur);
 }
@@ -204,37 +263,52 @@ struct DescGemv {
 extern "C" __global__ void __launch_bounds__(trc::FILS_ECHELLES)
 decoder_echelles(const uint8_t* __restrict__ partie, uint8_t* __restrict__ emplacement,
                  const uint32_t* __restrict__ luts, trc_dims_expert dims, uint32_t* __restrict__ controle) {
-    __shared__ uint32_t lut[trc::M];
-    __shared__ uint8_t med[8192];
-    trc::corps_echelles(partie, emplacement, luts, dims, controle, lut, med);
+    __shared__ trc::LdsEchelles<trc::FILS_ECHELLES> s;
+    trc::decoder_echelles_corps(partie, emplacement, luts, dims, controle, s);
 }
 
-extern "C" __global__ void __launch_bounds__(trc::FILS_CODES)
+extern "C" __global__ void __launch_bounds__(trc::FILS_CODES_SLOT)
 decoder_codes(const uint8_t* __restrict__ partie, uint8_t* __restrict__ emplacement, const uint32_t* __restrict__ luts,
               trc_dims_expert dims, uint32_t* __restrict__ controle) {
-    __shared__ uint32_t lut[3][trc::M];
-    trc::corps_codes(partie, emplacement, luts, dims, controle, lut);
+    __shared__ trc::LdsCodes s;
+    trc::decoder_codes_corps(partie, emplacement, luts, dims, controle, s);
 }
 
 extern "C" __global__ void __launch_bounds__(trc::FILS_ECHELLES)
 decoder_echelles_lot(const trc::DescDecodage* __restrict__ descs, trc_dims_expert dims) {
-    __shared__ uint32_t lut[trc::M];
-    __shared__ uint8_t med[8192];
+    __shared__ trc::LdsEchelles<trc::FILS_ECHELLES> s;
     const trc::DescDecodage d = descs[blockIdx.z];
-    trc::corps_echelles(reinterpret_cast<const uint8_t*>(d.partie), reinterpret_cast<uint8_t*>(d.emplacement),
-                        reinterpret_cast<const uint32_t*>(d.luts), dims, reinterpret_cast<uint32_t*>(d.controle), lut,
-                        med);
+    trc::decoder_echelles_corps(reinterpret_cast<const uint8_t*>(d.partie), reinterpret_cast<uint8_t*>(d.emplacement),
+                                reinterpret_cast<const uint32_t*>(d.luts), dims,
+                                reinterpret_cast<uint32_t*>(d.controle), s);
 }
 
-extern "C" __global__ void __launch_bounds__(trc::FILS_CODES)
+extern "C" __global__ void __launch_bounds__(trc::FILS_CODES_SLOT)
 decoder_codes_lot(const trc::DescDecodage* __restrict__ descs, trc_dims_expert dims) {
-    __shared__ uint32_t lut[3][trc::M];
+    __shared__ trc::LdsCodes s;
     const trc::DescDecodage d = descs[blockIdx.z];
-    trc::corps_codes(reinterpret_cast<const uint8_t*>(d.partie), reinterpret_cast<uint8_t*>(d.emplacement),
-                     reinterpret_cast<const uint32_t*>(d.luts), dims, reinterpret_cast<uint32_t*>(d.controle), lut);
+    trc::decoder_codes_corps(reinterpret_cast<const uint8_t*>(d.partie), reinterpret_cast<uint8_t*>(d.emplacement),
+                             reinterpret_cast<const uint32_t*>(d.luts), dims, reinterpret_cast<uint32_t*>(d.controle),
+                             s);
 }
 
-// Raw-file path (flag bit 2): ECHELLES_BRUTES, CODES_BRUTS, BIAIS copied into the slot.
+// Raw-file path (flag bit 2): the slot's three regions — codes (16 bytes per block), scales (one
+// byte per block), biases (4 bytes per row) — copied from the CODES_BRUTS, ECHELLES_BRUTES and
+// BIAIS streams as one list of 16-byte units over the grid. Sources are 16-byte aligned (streams
+// are, in a 16-byte aligned part), destinations 256-byte aligned; a region's last unit, when its
+// length is not a multiple of 16, is copied byte by byte, so no byte outside a region is written.
+namespace trc {
+__device__ __forceinline__ void copier_unite(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst, uint32_t u,
+                                             uint32_t octets) {
+    const uint32_t o = 16u * u;
+    if (o + 16u <= octets) {
+        ecrire_global<u32x4>(dst + o, *glob<u32x4>(src + o));
+    } else {
+        for (uint32_t k = o; k < octets; ++k) dst[k] = glob<uint8_t>(src)[k];
+    }
+}
+}  // namespace trc
+
 extern "C" __global__ void __launch_bounds__(trc::FILS_BRUT)
 copier_brut(const uint8_t* __restrict__ partie, uint8_t* __restrict__ emplacement, trc_dims_expert dims,
             uint32_t* __restrict__ controle) {
@@ -242,139 +316,192 @@ copier_brut(const uint8_t* __restrict__ partie, uint8_t* __restrict__ emplacemen
     const uint32_t j = blockIdx.y;
     const uint32_t R = choisir(dims.lignes, j), C = choisir(dims.colonnes, j);
     const uint32_t B = C / 32u, nblocs = R * B;
-    DescFlux fe, fc, fb;
-    const bool bon = (C % 32u == 0) && B > 0 && R > 0 && trouver_flux(partie, SORTE_ECHELLES_BRUTES, j, fe) &&
-                     trouver_flux(partie, SORTE_CODES_BRUTS, j, fc) && trouver_flux(partie, SORTE_BIAIS, j, fb) &&
-                     fe.produits == nblocs && fe.longueur >= nblocs && fc.produits == 16u * nblocs &&
-                     fc.longueur >= 16u * nblocs && fb.produits == 4u * R && fb.longueur >= 4u * R;
+    constexpr uint8_t sortes[4] = {SORTE_CODES_BRUTS, SORTE_ECHELLES_BRUTES, SORTE_BIAIS, 0};
+    DescFlux f[4];
+    const bool bon = C % 32u == 0 && B > 0 && R > 0 && trouver_flux_n(partie, sortes, 3, j, f) &&
+                     f[0].produits == 16u * nblocs && f[0].longueur >= 16u * nblocs && f[1].produits == nblocs &&
+                     f[1].longueur >= nblocs && f[2].produits == 4u * R && f[2].longueur >= 4u * R;
     if (!bon) {
         if (threadIdx.x == 0) atomicAdd(&controle[CTL_FORMAT], 1u);
         return;
     }
     const trc_disposition disp = disposition(dims, j);
     uint8_t* mat = emplacement + disp.base;
-    const uint32_t i0 = blockIdx.x * blockDim.x + threadIdx.x, pas = gridDim.x * blockDim.x;
-    const uint4* cs = reinterpret_cast<const uint4*>(fc.p);
-    uint4* cd = reinterpret_cast<uint4*>(mat);
-    for (uint32_t i = i0; i < nblocs; i += pas) cd[i] = cs[i];
-    for (uint32_t i = i0; i < nblocs; i += pas) mat[disp.echelles + i] = fe.p[i];
-    const uint32_t* bs = reinterpret_cast<const uint32_t*>(fb.p);
-    uint32_t* bd = reinterpret_cast<uint32_t*>(mat + disp.biais);
-    for (uint32_t i = i0; i < R; i += pas) bd[i] = bs[i];
+    const uint32_t n_codes = nblocs, n_ech = (nblocs + 15u) / 16u, n_biais = (4u * R + 15u) / 16u;
+    const uint32_t total = n_codes + n_ech + n_biais;
+    for (uint32_t u = blockIdx.x * blockDim.x + threadIdx.x; u < total; u += gridDim.x * blockDim.x) {
+        if (u < n_codes)
+            copier_unite(f[0].p, mat, u, 16u * nblocs);
+        else if (u < n_codes + n_ech)
+            copier_unite(f[1].p, mat + disp.echelles, u - n_codes, nblocs);
+        else
+            copier_unite(f[2].p, mat + disp.biais, u - n_codes - n_ech, 4u * R);
+    }
 }
 
-// ==================================================================================== GEMV MXFP4
+// ============================================================================ GEMVs, reference order
+//
+// Operation-order contract (the bits of the reference's gemv_mxfp4 / gemv_f32, gemv.cuh:61-126,
+// passe.cuh:104-130), for row r of y = W x + b:
+//   MXFP4: P(b) = fma chain from 0 over bytes i = 0..15 of block b's 16 code bytes, each byte's low
+//          nibble times x[32b + i] then its high nibble times x[32b + 16 + i], with the doubled E2M1
+//          values (exact: 2 * {0, .5, 1, 1.5, 2, 3, 4, 6}, code 8 = -0);
+//          A(l) = fma chain from 0 over blocks b = l, l + 32, l + 64, ... < B of 2^(e_b - 128) * P(b);
+//   f32:   A(l) = fma chain from 0 over quads c = l, l + 32, ... < C/4 of w[4c + k] * x[4c + k], k = 0..3;
+//   y[r] = S + b[r] (f32 add; no bias term when b is absent), S the pairwise tree over l = 0..31:
+//          pairs at lane distance 16, then 8, 4, 2, 1 (every lane of the tree ends with the same S).
+// Mapping here: a 32-lane half-wavefront owns a row (l = its lane), two rows per half for MXFP4
+// (the x loads of a block serve both); E2M1 pairs are expanded by v_cvt_scalef32_pk_f32_fp4 (scale
+// 2: the doubled values); the tree runs on ds_swizzle (xor masks within 32 lanes); the loads of a
+// lane's next block are issued before the current block's arithmetic.
 namespace trc {
 
-// Contribution of one block in the reference's fixed order (word t, byte k, low then high nibble).
-__device__ __forceinline__ float produit_bloc(const uint4 q, const float4 (&xs)[8]) {
-    const uint32_t mots[4] = {q.x, q.y, q.z, q.w};
-    float s = 0.0f;
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-        const uint32_t w = mots[t];
-        const float xa[4] = {xs[t].x, xs[t].y, xs[t].z, xs[t].w};
-        const float xb[4] = {xs[4 + t].x, xs[4 + t].y, xs[4 + t].z, xs[4 + t].w};
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            s = fmaf(valeur_e2m1x2((w >> (8 * k)) & 15u), xa[k], s);
-            s = fmaf(valeur_e2m1x2((w >> (8 * k + 4)) & 15u), xb[k], s);
-        }
-    }
+constexpr uint32_t GEMV_LIGNES_PAR_DEMI = 2;
+
+// S: the xor tree over a half-wavefront's 32 lanes.
+__device__ __forceinline__ float arbre_32(float v) {
+    v += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F));  // xor 16
+    v += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x201F));  // xor 8
+    v += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x101F));  // xor 4
+    v += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x081F));  // xor 2
+    v += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x041F));  // xor 1
+    return v;
+}
+
+// Bytes 4t .. 4t + 3 of a block (code word t) continuing the chain s: byte 4t + k pairs with
+// x[4t + k] (low nibble) and x[16 + 4t + k] (high nibble), i.e. xa[k] and xb[k].
+__device__ __forceinline__ float chaine_mot(uint32_t mot, const f32x4 xa, const f32x4 xb, float s) {
+    const f32x2 w0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(mot, 2.0f, 0);
+    const f32x2 w1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(mot, 2.0f, 1);
+    const f32x2 w2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(mot, 2.0f, 2);
+    const f32x2 w3 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(mot, 2.0f, 3);
+    s = fmaf(w0.x, xa.x, s);
+    s = fmaf(w0.y, xb.x, s);
+    s = fmaf(w1.x, xa.y, s);
+    s = fmaf(w1.y, xb.y, s);
+    s = fmaf(w2.x, xa.z, s);
+    s = fmaf(w2.y, xb.z, s);
+    s = fmaf(w3.x, xa.w, s);
+    s = fmaf(w3.y, xb.w, s);
     return s;
 }
 
-// Rows r0 .. r0+3 of one matrix, computed by one 32-lane half-wavefront exactly as one reference
-// warp does: lane l takes blocks l, l+32, ...; 32-lane butterfly; lane 0 writes.
-__device__ __forceinline__ void gemv_4_lignes(const uint8_t* __restrict__ mat, const float* __restrict__ x,
-                                              float* __restrict__ y, uint32_t R, uint32_t C, uint32_t r0,
-                                              uint32_t voie) {
+// P(b) for one block: q its 16 code bytes, xs its 32 x values as 8 float4.
+__device__ __forceinline__ float chaine_bloc(const u32x4 q, const f32x4 (&xs)[8]) {
+    float s = chaine_mot(q.x, xs[0], xs[4], 0.0f);
+    s = chaine_mot(q.y, xs[1], xs[5], s);
+    s = chaine_mot(q.z, xs[2], xs[6], s);
+    return chaine_mot(q.w, xs[3], xs[7], s);
+}
+
+struct BlocGemv {
+    u32x4 q[GEMV_LIGNES_PAR_DEMI];
+    uint32_t e[GEMV_LIGNES_PAR_DEMI];
+    f32x4 xs[8];
+};
+
+// Rows r0, r0 + 1 of an MXFP4 matrix in its slot (rows past R are read as row R - 1 and not written).
+__device__ __forceinline__ void gemv_mxfp4_demi(const uint8_t* __restrict__ mat, const float* __restrict__ x,
+                                                float* __restrict__ y, uint32_t R, uint32_t C, uint32_t r0,
+                                                uint32_t l) {
     const uint32_t B = C / 32u;
     const trc_disposition d = disposition_matrice(R, C);
-    const uint4* codes = reinterpret_cast<const uint4*>(mat);
-    const uint8_t* ech = mat + d.echelles;
-    const float* biais = reinterpret_cast<const float*>(mat + d.biais);
-    const float4* x4 = reinterpret_cast<const float4*>(x);
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    uint32_t lig[4];
+    const gptr<u32x4> codes = glob<u32x4>(mat);
+    const gptr<uint8_t> ech = glob<uint8_t>(mat + d.echelles);
+    const gptr<f32x4> x4 = glob<f32x4>(x);
+    uint64_t base[GEMV_LIGNES_PAR_DEMI];
 #pragma unroll
-    for (uint32_t i = 0; i < 4; ++i) lig[i] = min(r0 + i, R - 1u);
-    for (uint32_t b = voie; b < B; b += 32u) {
-        float4 xs[8];
+    for (uint32_t i = 0; i < GEMV_LIGNES_PAR_DEMI; ++i) base[i] = uint64_t(min(r0 + i, R - 1u)) * B;
+    auto charger = [&](uint32_t b, BlocGemv& c) {
 #pragma unroll
-        for (int k = 0; k < 8; ++k) xs[k] = x4[b * 8u + k];
-        uint4 q[4];
-        uint32_t e[4];
-#pragma unroll
-        for (uint32_t i = 0; i < 4; ++i) {
-            const uint64_t beta = uint64_t(lig[i]) * B + b;
-            q[i] = codes[beta];
-            e[i] = ech[beta];
+        for (uint32_t i = 0; i < GEMV_LIGNES_PAR_DEMI; ++i) {
+            c.q[i] = codes[base[i] + b];
+            c.e[i] = ech[base[i] + b];
         }
 #pragma unroll
-        for (uint32_t i = 0; i < 4; ++i) acc[i] = fmaf(echelle_e8m0(e[i]), produit_bloc(q[i], xs), acc[i]);
-    }
+        for (uint32_t k = 0; k < 8; ++k) c.xs[k] = x4[8u * b + k];
+    };
+    float acc[GEMV_LIGNES_PAR_DEMI] = {};
+    BlocGemv cur;
+    if (l < B) charger(l, cur);
+    for (uint32_t b = l; b < B; b += 32u) {
+        BlocGemv suiv;
+        charger(min(b + 32u, B - 1u), suiv);  // unconditional (the last one reloads a block): no wait of
+                                              // the current block's arithmetic covers these loads
 #pragma unroll
-    for (uint32_t i = 0; i < 4; ++i) {
-        const float s = somme_demi_f32(acc[i]);
-        if (voie == 0 && r0 + i < R) y[r0 + i] = s + biais[r0 + i];
+        for (uint32_t i = 0; i < GEMV_LIGNES_PAR_DEMI; ++i)
+            acc[i] = fmaf(echelle_e8m0(cur.e[i]), chaine_bloc(cur.q[i], cur.xs), acc[i]);
+        cur = suiv;
+    }
+    const gptr<float> biais = glob<float>(mat + d.biais);
+#pragma unroll
+    for (uint32_t i = 0; i < GEMV_LIGNES_PAR_DEMI; ++i) {
+        const float s = arbre_32(acc[i]);
+        if (l == 0u && r0 + i < R) y[r0 + i] = s + biais[r0 + i];
     }
 }
 
 }  // namespace trc
 
+// y = W x + b for one slot matrix: 8 halves x 2 rows per block of 256 threads.
 extern "C" __global__ void __launch_bounds__(trc::GEMV_FILS)
 gemv_mxfp4(const uint8_t* __restrict__ matrice, const float* __restrict__ x, float* __restrict__ y, uint32_t R,
            uint32_t C) {
-    const uint32_t voie = threadIdx.x & 31u;
-    const uint32_t r0 = (blockIdx.x * (trc::GEMV_FILS / 32u) + (threadIdx.x >> 5)) * 4u;
+    const uint32_t r0 = (blockIdx.x * (trc::GEMV_FILS / 32u) + (threadIdx.x >> 5)) * trc::GEMV_LIGNES_PAR_DEMI;
     if (r0 >= R || C % 32u != 0) return;
-    trc::gemv_4_lignes(matrice, x, y, R, C, r0, voie);
+    trc::gemv_mxfp4_demi(matrice, x, y, R, C, r0, threadIdx.x & 31u);
 }
 
+// Independent products (e.g. the 12 matrices of a layer's 4 experts) in one launch: grid y = product.
 extern "C" __global__ void __launch_bounds__(trc::GEMV_FILS) gemv_mxfp4_lot(const trc::DescGemv* __restrict__ descs) {
     const trc::DescGemv dsc = descs[blockIdx.y];
-    const uint32_t voie = threadIdx.x & 31u;
-    const uint32_t r0 = (blockIdx.x * (trc::GEMV_FILS / 32u) + (threadIdx.x >> 5)) * 4u;
+    const uint32_t r0 = (blockIdx.x * (trc::GEMV_FILS / 32u) + (threadIdx.x >> 5)) * trc::GEMV_LIGNES_PAR_DEMI;
     if (r0 >= dsc.lignes || dsc.colonnes % 32u != 0) return;
-    trc::gemv_4_lignes(reinterpret_cast<const uint8_t*>(dsc.matrice), reinterpret_cast<const float*>(dsc.x),
-                       reinterpret_cast<float*>(dsc.y), dsc.lignes, dsc.colonnes, r0, voie);
+    trc::gemv_mxfp4_demi(reinterpret_cast<const uint8_t*>(dsc.matrice), reinterpret_cast<const float*>(dsc.x),
+                         reinterpret_cast<float*>(dsc.y), dsc.lignes, dsc.colonnes, r0, threadIdx.x & 31u);
 }
 
-// =========================================================================== router, SwiGLU, combine
-
-// y = W x (+ b), W f32 row-major: lane l of a half takes quads c = l, l+32, ...; butterfly
-// (passe.cuh:104-130 order).
+// y = W x (+ b), W f32 row-major: one row per half-wavefront, four quads per lane in flight.
 extern "C" __global__ void __launch_bounds__(trc::GEMV_FILS)
 gemv_f32(const float* __restrict__ W, const float* __restrict__ x, const float* __restrict__ biais,
          float* __restrict__ y, uint32_t R, uint32_t C) {
-    const uint32_t voie = threadIdx.x & 31u;
-    const uint32_t r0 = (blockIdx.x * (trc::GEMV_FILS / 32u) + (threadIdx.x >> 5)) * 4u;
-    if (r0 >= R || C % 4u != 0) return;
+    using namespace trc;
+    const uint32_t r = blockIdx.x * (GEMV_FILS / 32u) + (threadIdx.x >> 5);
+    const uint32_t l = threadIdx.x & 31u;
+    if (r >= R || C % 4u != 0) return;
     const uint32_t C4 = C / 4u;
-    const float4* x4 = reinterpret_cast<const float4*>(x);
-    const float4* W4 = reinterpret_cast<const float4*>(W);
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    uint32_t lig[4];
+    const gptr<f32x4> w4 = glob<f32x4>(W + uint64_t(r) * C);
+    const gptr<f32x4> x4 = glob<f32x4>(x);
+    constexpr uint32_t LOT = 4;
+    float acc = 0.0f;
+    uint32_t c = l;
+    for (; c + 32u * (LOT - 1u) < C4; c += 32u * LOT) {  // whole batches: every load goes out first
+        f32x4 w[LOT], xv[LOT];
 #pragma unroll
-    for (uint32_t i = 0; i < 4; ++i) lig[i] = min(r0 + i, R - 1u);
-    for (uint32_t c = voie; c < C4; c += 32u) {
-        const float4 xv = x4[c];
+        for (uint32_t u = 0; u < LOT; ++u) {
+            w[u] = w4[c + 32u * u];
+            xv[u] = x4[c + 32u * u];
+        }
 #pragma unroll
-        for (uint32_t i = 0; i < 4; ++i) {
-            const float4 w = W4[uint64_t(lig[i]) * C4 + c];
-            acc[i] = fmaf(w.x, xv.x, acc[i]);
-            acc[i] = fmaf(w.y, xv.y, acc[i]);
-            acc[i] = fmaf(w.z, xv.z, acc[i]);
-            acc[i] = fmaf(w.w, xv.w, acc[i]);
+        for (uint32_t u = 0; u < LOT; ++u) {
+            acc = fmaf(w[u].x, xv[u].x, acc);
+            acc = fmaf(w[u].y, xv[u].y, acc);
+            acc = fmaf(w[u].z, xv[u].z, acc);
+            acc = fmaf(w[u].w, xv[u].w, acc);
         }
     }
-#pragma unroll
-    for (uint32_t i = 0; i < 4; ++i) {
-        const float s = trc::somme_demi_f32(acc[i]);
-        if (voie == 0 && r0 + i < R) y[r0 + i] = biais != nullptr ? s + biais[r0 + i] : s;
+    for (; c < C4; c += 32u) {
+        const f32x4 w = w4[c], xv = x4[c];
+        acc = fmaf(w.x, xv.x, acc);
+        acc = fmaf(w.y, xv.y, acc);
+        acc = fmaf(w.z, xv.z, acc);
+        acc = fmaf(w.w, xv.w, acc);
     }
+    const float s = arbre_32(acc);
+    if (l == 0u) y[r] = biais != nullptr ? s + biais[r] : s;
 }
+
+// =========================================================================== router, SwiGLU, combine
 
 // Top-k of E logits by (value desc, index asc); weights = softmax of the k in f64 (m = first,
 // exp, ordered sum, division), rounded to f32. One wavefront: 64 lanes x 4 values (E <= 256).
@@ -530,7 +657,7 @@ extern "C" int trc_decoder_expert_grilles(trc_vue partie, trc_vue emplacement, t
     auto c = reinterpret_cast<uint32_t*>(controle.adresse);
     hipLaunchKernelGGL(decoder_echelles, dim3(g1[0], 3, 1), dim3(trc::FILS_ECHELLES), 0, f, p, e, l, *dims, c);
     if ((r = trc::apres_lancement("decoder_echelles")) != TRC_OK) return r;
-    hipLaunchKernelGGL(decoder_codes, dim3(g2[0], 3, 1), dim3(trc::FILS_CODES), 0, f, p, e, l, *dims, c);
+    hipLaunchKernelGGL(decoder_codes, dim3(g2[0], 3, 1), dim3(trc::FILS_CODES_SLOT), 0, f, p, e, l, *dims, c);
     return trc::apres_lancement("decoder_codes");
 }
 
@@ -546,7 +673,7 @@ extern "C" int trc_decoder_lot(trc_vue descs, uint32_t n, const trc_dims_expert*
     auto d = reinterpret_cast<const trc::DescDecodage*>(descs.adresse);
     hipLaunchKernelGGL(decoder_echelles_lot, dim3(g1[0], 3, n), dim3(trc::FILS_ECHELLES), 0, f, d, *dims);
     if ((r = trc::apres_lancement("decoder_echelles_lot")) != TRC_OK) return r;
-    hipLaunchKernelGGL(decoder_codes_lot, dim3(g2[0], 3, n), dim3(trc::FILS_CODES), 0, f, d, *dims);
+    hipLaunchKernelGGL(decoder_codes_lot, dim3(g2[0], 3, n), dim3(trc::FILS_CODES_SLOT), 0, f, d, *dims);
     return trc::apres_lancement("decoder_codes_lot");
 }
 
@@ -603,7 +730,8 @@ extern "C" int trc_gemv_f32(trc_vue w, trc_vue x, trc_vue biais, trc_vue y, uint
                  "x trop court ou non aligne sur 16");
     TRC_VERIFIER(y.adresse != 0 && y.octets >= 4ull * lignes, "y trop court");
     TRC_VERIFIER(biais.adresse == 0 || biais.octets >= 4ull * lignes, "biais trop court");
-    hipLaunchKernelGGL(gemv_f32, dim3((lignes + trc::GEMV_LIGNES_PAR_BLOC - 1) / trc::GEMV_LIGNES_PAR_BLOC),
+    constexpr uint32_t lignes_bloc = trc::GEMV_FILS / 32u;  // one row per half-wavefront
+    hipLaunchKernelGGL(gemv_f32, dim3((lignes + lignes_bloc - 1) / lignes_bloc),
                        dim3(trc::GEMV_FILS), 0, flux_de(flux), reinterpret_cast<const float*>(w.adresse),
                        reinterpret_cast<const float*>(x.adresse), reinterpret_cast<const float*>(biais.adresse),
                        reinterpret_cast<float*>(y.adresse), lignes, colonnes);

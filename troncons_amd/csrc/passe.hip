@@ -1,11 +1,12 @@
 // passe.hip — the rest of a gpt-oss layer step around the expert path, for gfx950: the Q8_0 GEMV
 // (attention projections, output head) and row (embedding), RMSNorm, the YaRN rotation, the f16
 // KV-cache write, decode attention with per-head sinks, argmax. Same names, arguments and results
-// as the reference's kernels (moteur/crates/trc-noyaux/noyaux/passe.cuh), each in the reference's
-// operation order so that results are bit-identical where the reference is exact: the Q8_0 GEMV
-// runs two reference "warps" per wavefront (one per 32-lane half, four rows each) with the lane
-// order and butterfly of the reference; the single-vector operations keep their f64 arithmetic and
-// their fixed reduction trees.
+// as the reference's kernels (moteur/crates/trc-noyaux/noyaux/passe.cuh). The Q8_0 GEMV, the norm
+// and the KV write keep the reference's operation order, so their results are bit-identical: the
+// Q8_0 GEMV runs one reference "warp" per 32-lane half with the reference's lane order and
+// butterfly, the single-vector operations keep their f64 arithmetic and fixed reduction trees. The
+// YaRN frequencies and the attention are computed in forms of their own (f64 closed form; a
+// one-pass running softmax), equal to the reference's within rounding.
 //
 // Determinism: no atomics; every reduction follows a tree that depends on sizes only.
 #include <hip/hip_runtime.h>
@@ -47,49 +48,33 @@ __device__ __forceinline__ bool meilleur(float va, uint32_t ia, float vb, uint32
     return va > vb || (va == vb && ia < ib);
 }
 
-// Fixed tree over FILS_PASSE values (max or sum; level k: value t op= value t + k for t < k,
-// k = 128 .. 1): levels 128 and 64 in LDS, levels 32 .. 1 as shuffles in wave 0 (lane t takes lane
-// t + k, the same association). part holds FILS_PASSE + 1 floats; every thread gets the result.
-template <bool MAX>
-__device__ __forceinline__ float reduire_bloc(float* part, float v) {
-    const uint32_t t = threadIdx.x;
-    part[t] = v;
-    __syncthreads();
-    if (t < 64u) {
-        float a = MAX ? fmaxf(fmaxf(part[t], part[t + 128u]), fmaxf(part[t + 64u], part[t + 192u]))
-                      : (part[t] + part[t + 128u]) + (part[t + 64u] + part[t + 192u]);
-#pragma unroll
-        for (uint32_t k = 32; k > 0; k >>= 1) {
-            const float b = __shfl_down(a, k, 64);
-            a = MAX ? fmaxf(a, b) : a + b;
-        }
-        if (t == 0) part[FILS_PASSE] = a;
-    }
-    __syncthreads();
-    return part[FILS_PASSE];
+// YaRN (Peng et al., "YaRN: Efficient Context Window Extension of Large Language Models", 2023),
+// with the parameters of gpt-oss's published configuration (passe.cuh:145-167 defines the same
+// function): pair i of a d-dim head turns at theta_i = base^(-2i/d). Past the original context
+// (facteur s > 1), a pair keeps theta_i if its wavelength is short, takes theta_i / s if it is long,
+// and blends linearly in between: theta_i * (1 - g + g / s), g = clamp((i - lo) / (hi - lo), 0, 1),
+// where lo and hi are the pair indices whose wavelength 2 pi / theta equals ctx_origine / beta for
+// beta = beta_rapide and beta_lent. Variant 1 (llama.cpp) rounds lo down and hi up into [0, d - 1].
+// The attention concentration is 1 + 0.1 ln s. All in f64.
+__device__ inline double indice_longueur_onde(const trc_params_rope& p, double beta) {
+    constexpr double DEUX_PI = 2.0 * 3.14159265358979323846;
+    return 0.5 * double(p.dim_tete) * log(p.ctx_origine / (DEUX_PI * beta)) / log(p.base);
 }
 
-// YaRN inv_freq of pair i and the concentration, in f64 (passe.cuh:145-167).
 __device__ inline double inv_freq_yarn(const trc_params_rope& p, uint32_t i, double& concentration) {
-    const uint32_t demi = p.dim_tete / 2u;
-    const double freq = pow(p.base, double(2u * i) / double(p.dim_tete));
+    const double theta = exp(-log(p.base) * double(2u * i) / double(p.dim_tete));
     if (p.facteur <= 1.0) {
         concentration = 1.0;
-        return 1.0 / freq;
+        return theta;
     }
-    concentration = 0.1 * log(p.facteur) + 1.0;
-    const double deux_pi = 6.283185307179586476925286766559;
-    double bas = double(demi) * log(p.ctx_origine / (p.beta_rapide * deux_pi)) / log(p.base);
-    double haut = double(demi) * log(p.ctx_origine / (p.beta_lent * deux_pi)) / log(p.base);
+    concentration = 1.0 + 0.1 * log(p.facteur);
+    double lo = indice_longueur_onde(p, p.beta_rapide), hi = indice_longueur_onde(p, p.beta_lent);
     if (p.variante == 1u) {
-        bas = fmax(floor(bas), 0.0);
-        haut = fmin(ceil(haut), double(p.dim_tete - 1u));
+        lo = fmax(floor(lo), 0.0);
+        hi = fmin(ceil(hi), double(p.dim_tete - 1u));
     }
-    const double interpolation = 1.0 / (p.facteur * freq);
-    const double extrapolation = 1.0 / freq;
-    const double rampe = fmin(fmax((double(i) - bas) / (haut - bas), 0.0), 1.0);
-    const double masque = 1.0 - rampe;
-    return interpolation * (1.0 - masque) + extrapolation * masque;
+    const double g = fmin(fmax((double(i) - lo) / (hi - lo), 0.0), 1.0);
+    return theta * ((1.0 - g) + g / p.facteur);
 }
 
 }  // namespace trc
@@ -436,103 +421,137 @@ ecrire_kv(const float* __restrict__ k, const float* __restrict__ v, uint16_t* __
     cache_v[o] = trc::f32_vers_f16(v[i]);
 }
 
-// Decode attention of one position, one query head per block of 256 threads (passe.cuh:298-373):
-//   score_j = (q . k_j) * scale (fmaf chain over d = 0..63), j in [debut, fin);
-//   m = max(max_j score_j, sink); e_j = expf(score_j - m); z = tree over the threads' sums + expf(sink - m);
-//   out[t] = ((G0 + G1) + (G2 + G3)) / z, G_g the fmaf chain over j = g, g + 4, ... of e_j v_j[t].
-// Query head h reads kv head h / (heads / kv heads); scores live in dynamic LDS (4 bytes each).
-// The caches hold f16 (attention) or f32 (attention_kvf32, passe.cuh:374-445: the same arithmetic
-// in the same order, only the stored keys and values differ).
+// Decode attention of one position for query head h (the result of passe.cuh:298-373, within
+// float rounding): scores s_j = (q . k_j) * scale over the positions j in [debut, fin) (slot
+// j mod anneau in a windowed layer), then out = sum_j exp(s_j - M) v_j / (sum_j exp(s_j - M) +
+// exp(sink - M)), M the largest of the scores and the sink. Query head h reads kv head
+// h / (heads / kv heads).
+//
+// One pass with a running softmax (Milakov & Gimelshein, "Online normalizer calculation for
+// softmax", 2018): the block's four wavefronts take chunks of 64 positions in turn (chunk c to
+// wavefront c mod 4). In a chunk, lane p scores position 64c + p; the wavefront's running maximum
+// moves to include the chunk's, and its running sum and its 64 running outputs (lane = dimension)
+// are rescaled by exp(old max - new max) before the chunk's terms are added; each position's weight
+// reaches the 64 dimensions through the wavefront's 64 LDS words. The four (max, sum, outputs) are
+// merged with the sink at the end, in wavefront order. No score array: any number of positions
+// fits in the block's 2 KiB of LDS. The caches hold f16 (attention) or f32 (attention_kvf32).
 namespace trc {
 __device__ __forceinline__ float lire_kv(uint16_t b) { return f16_vers_f32(b); }
 __device__ __forceinline__ float lire_kv(float v) { return v; }
 
-// q . k_j over d = 0..63 in order, k_j one row of 64 stored values
-__device__ __forceinline__ float produit_cle(const float* qs, const uint16_t* kr) {
-    const u32x4* k4 = reinterpret_cast<const u32x4*>(kr);
-    float s = 0.0f;
+// q . k for one stored key row of 64 values, q in LDS as 16 float4: four interleaved partial
+// chains (dimensions 4u + 0..3 of each group of 16) added pairwise at the end.
+__device__ __forceinline__ float produit_cle(const f32x4* qs, const uint16_t* kr) {
+    const gptr<u32x4> k4 = glob<u32x4>(kr);
+    float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (uint32_t b = 0; b < 8; ++b) {
         const u32x4 w = k4[b];
-#pragma unroll
-        for (uint32_t u = 0; u < 4; ++u) {
-            s = fmaf(qs[8 * b + 2 * u], f16_vers_f32(w[u] & 0xFFFFu), s);
-            s = fmaf(qs[8 * b + 2 * u + 1], f16_vers_f32(w[u] >> 16), s);
-        }
+        const f32x4 qa = qs[2 * b], qb = qs[2 * b + 1];
+        a[0] = fmaf(qa.x, f16_vers_f32(w.x & 0xFFFFu), a[0]);
+        a[1] = fmaf(qa.y, f16_vers_f32(w.x >> 16), a[1]);
+        a[2] = fmaf(qa.z, f16_vers_f32(w.y & 0xFFFFu), a[2]);
+        a[3] = fmaf(qa.w, f16_vers_f32(w.y >> 16), a[3]);
+        a[0] = fmaf(qb.x, f16_vers_f32(w.z & 0xFFFFu), a[0]);
+        a[1] = fmaf(qb.y, f16_vers_f32(w.z >> 16), a[1]);
+        a[2] = fmaf(qb.z, f16_vers_f32(w.w & 0xFFFFu), a[2]);
+        a[3] = fmaf(qb.w, f16_vers_f32(w.w >> 16), a[3]);
     }
-    return s;
+    return (a[0] + a[1]) + (a[2] + a[3]);
 }
-__device__ __forceinline__ float produit_cle(const float* qs, const float* kr) {
-    const f32x4* k4 = reinterpret_cast<const f32x4*>(kr);
-    float s = 0.0f;
+__device__ __forceinline__ float produit_cle(const f32x4* qs, const float* kr) {
+    const gptr<f32x4> k4 = glob<f32x4>(kr);
+    float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (uint32_t b = 0; b < 16; ++b) {
-        const f32x4 w = k4[b];
-        s = fmaf(qs[4 * b], w.x, s);
-        s = fmaf(qs[4 * b + 1], w.y, s);
-        s = fmaf(qs[4 * b + 2], w.z, s);
-        s = fmaf(qs[4 * b + 3], w.w, s);
+        const f32x4 w = k4[b], qv = qs[b];
+        a[0] = fmaf(qv.x, w.x, a[0]);
+        a[1] = fmaf(qv.y, w.y, a[1]);
+        a[2] = fmaf(qv.z, w.z, a[2]);
+        a[3] = fmaf(qv.w, w.w, a[3]);
     }
-    return s;
+    return (a[0] + a[1]) + (a[2] + a[3]);
+}
+
+__device__ __forceinline__ float max_vague(float v) {
+#pragma unroll
+    for (int d = 32; d > 0; d >>= 1) v = fmaxf(v, __shfl_xor(v, d));
+    return v;
+}
+__device__ __forceinline__ float somme_vague(float v) {
+#pragma unroll
+    for (int d = 32; d > 0; d >>= 1) v += __shfl_xor(v, d);
+    return v;
 }
 
 template <typename T>
 __device__ __forceinline__ void attention_tete(const float* __restrict__ q, const T* __restrict__ cache_k,
                                                const T* __restrict__ cache_v, const float* __restrict__ puits,
                                                float* __restrict__ sortie, const trc_params_attention& p) {
-    extern __shared__ float scores[];
-    __shared__ float qs[ATTENTION_DIM];
-    __shared__ float part[FILS_PASSE + 1];
-    __shared__ float groupes[4][ATTENTION_DIM];
-    const uint32_t t = threadIdx.x;
+    constexpr uint32_t VAGUES = FILS_PASSE / 64u;
+    __shared__ f32x4 qs[ATTENTION_DIM / 4];
+    __shared__ float poids[VAGUES][64];
+    __shared__ float sorties[VAGUES][ATTENTION_DIM];
+    __shared__ float maxima[VAGUES], sommes[VAGUES];
+    const uint32_t t = threadIdx.x, w = t >> 6, lane = t & 63u;
     const uint32_t h = blockIdx.x;
     const uint32_t hk = h / (p.tetes / p.tetes_kv);
-    const uint32_t dkv = p.tetes_kv * ATTENTION_DIM;
+    const uint64_t dkv = uint64_t(p.tetes_kv) * ATTENTION_DIM;
     const uint32_t n = p.fin - p.debut;
-    if (t < ATTENTION_DIM) qs[t] = q[uint64_t(h) * ATTENTION_DIM + t];
+    if (t < ATTENTION_DIM / 4u) qs[t] = glob<f32x4>(q + uint64_t(h) * ATTENTION_DIM)[t];
     __syncthreads();
 
-    for (uint32_t j = t; j < n; j += FILS_PASSE) {
-        const uint32_t pos = p.debut + j;
-        const uint32_t c = p.anneau ? pos % p.anneau : pos;
-        scores[j] = produit_cle(qs, cache_k + uint64_t(c) * dkv + uint64_t(hk) * ATTENTION_DIM) * p.echelle;
-    }
-    __syncthreads();
-
-    float m = -INFINITY;
-    for (uint32_t j = t; j < n; j += FILS_PASSE) m = fmaxf(m, scores[j]);
-    const float puits_h = puits[h];
-    m = fmaxf(reduire_bloc<true>(part, m), puits_h);
-    float z = 0.0f;
-    for (uint32_t j = t; j < n; j += FILS_PASSE) {
-        const float e = expf(scores[j] - m);
-        scores[j] = e;
-        z += e;
-    }
-    z = reduire_bloc<false>(part, z) + expf(puits_h - m);
-
-    // the value loads of eight positions go out together (positions clamped to the last one, so no
-    // branch stands around a load; the copies past it are unused); the chain keeps j = g, g + 4, ...
-    const uint32_t dd = t & (ATTENTION_DIM - 1u);
-    const uint32_t g = t / ATTENTION_DIM;  // 0..3
-    float a = 0.0f;
-    constexpr uint32_t LOT = 8;
-    for (uint32_t j0 = g; j0 < n; j0 += 4u * LOT) {
-        T vv[LOT];
+    const T* cles = cache_k + uint64_t(hk) * ATTENTION_DIM;
+    const T* valeurs = cache_v + uint64_t(hk) * ATTENTION_DIM + lane;
+    float m = -INFINITY, z = 0.0f, o = 0.0f;
+    for (uint32_t c0 = 64u * w; c0 < n; c0 += 64u * VAGUES) {
+        const uint32_t pos0 = p.debut + c0;
+        const uint32_t case0 = p.anneau ? pos0 % p.anneau : pos0;  // slots of the chunk: case0 + k, wrapped
+        auto case_de = [&](uint32_t k) {
+            const uint32_t c = case0 + k;
+            return p.anneau && c >= p.anneau ? c - p.anneau : c;
+        };
+        const bool ok = c0 + lane < n;
+        const float s = ok ? produit_cle(qs, cles + uint64_t(case_de(lane)) * dkv) * p.echelle : -INFINITY;
+        const float m2 = fmaxf(m, max_vague(s));
+        const float alpha = expf(m - m2);  // 0 for the first chunk (m = -inf)
+        const float e = expf(s - m2);      // 0 for lanes past the end
+        z = fmaf(z, alpha, somme_vague(e));
+        poids[w][lane] = e;  // read back by this wavefront only, in program order
+        const uint32_t nc = min(64u, n - c0);
+        float acc = 0.0f;
+        constexpr uint32_t LOT = 8;
+        for (uint32_t k0 = 0; k0 < nc; k0 += LOT) {
+            T vv[LOT];
 #pragma unroll
-        for (uint32_t u = 0; u < LOT; ++u) {
-            const uint32_t pos = p.debut + min(j0 + 4u * u, n - 1u);
-            const uint32_t c = p.anneau ? pos % p.anneau : pos;
-            vv[u] = cache_v[uint64_t(c) * dkv + uint64_t(hk) * ATTENTION_DIM + dd];
+            for (uint32_t u = 0; u < LOT; ++u) vv[u] = valeurs[uint64_t(case_de(min(k0 + u, nc - 1u))) * dkv];
+#pragma unroll
+            for (uint32_t u = 0; u < LOT; ++u)
+                if (k0 + u < nc) acc = fmaf(poids[w][k0 + u], lire_kv(vv[u]), acc);
         }
-#pragma unroll
-        for (uint32_t u = 0; u < LOT; ++u)
-            if (j0 + 4u * u < n) a = fmaf(scores[j0 + 4u * u], lire_kv(vv[u]), a);
+        o = fmaf(o, alpha, acc);
+        m = m2;
     }
-    groupes[g][dd] = a;
+    if (lane == 0) {
+        maxima[w] = m;
+        sommes[w] = z;
+    }
+    sorties[w][lane] = o;
     __syncthreads();
-    if (t < ATTENTION_DIM)
-        sortie[uint64_t(h) * ATTENTION_DIM + t] = ((groupes[0][t] + groupes[1][t]) + (groupes[2][t] + groupes[3][t])) / z;
+    if (t < ATTENTION_DIM) {
+        const float puits_h = puits[h];
+        float mg = puits_h;
+#pragma unroll
+        for (uint32_t v = 0; v < VAGUES; ++v) mg = fmaxf(mg, maxima[v]);
+        float zg = expf(puits_h - mg), og = 0.0f;
+#pragma unroll
+        for (uint32_t v = 0; v < VAGUES; ++v) {
+            const float f = expf(maxima[v] - mg);
+            zg = fmaf(sommes[v], f, zg);
+            og = fmaf(sorties[v][t], f, og);
+        }
+        sortie[uint64_t(h) * ATTENTION_DIM + t] = og / zg;
+    }
 }
 }  // namespace trc
 
@@ -732,7 +751,7 @@ extern "C" int trc_attention(trc_vue q, trc_vue cache_k, trc_vue cache_v, trc_vu
                              const trc_params_attention* p, void* flux) {
     const int r = verifier_attention(q, cache_k, cache_v, puits, sortie, p, 2);
     if (r != TRC_OK) return r;
-    hipLaunchKernelGGL(attention, dim3(p->tetes), dim3(trc::FILS_PASSE), 4u * size_t(p->fin - p->debut), flux_de(flux),
+    hipLaunchKernelGGL(attention, dim3(p->tetes), dim3(trc::FILS_PASSE), 0, flux_de(flux),
                        reinterpret_cast<const float*>(q.adresse), reinterpret_cast<const uint16_t*>(cache_k.adresse),
                        reinterpret_cast<const uint16_t*>(cache_v.adresse), reinterpret_cast<const float*>(puits.adresse),
                        reinterpret_cast<float*>(sortie.adresse), *p);
@@ -743,8 +762,7 @@ extern "C" int trc_attention_kvf32(trc_vue q, trc_vue cache_k, trc_vue cache_v, 
                                    const trc_params_attention* p, void* flux) {
     const int r = verifier_attention(q, cache_k, cache_v, puits, sortie, p, 4);
     if (r != TRC_OK) return r;
-    hipLaunchKernelGGL(attention_kvf32, dim3(p->tetes), dim3(trc::FILS_PASSE), 4u * size_t(p->fin - p->debut),
-                       flux_de(flux), reinterpret_cast<const float*>(q.adresse),
+    hipLaunchKernelGGL(attention_kvf32, dim3(p->tetes), dim3(trc::FILS_PASSE), 0, flux_de(flux), reinterpret_cast<const float*>(q.adresse),
                        reinterpret_cast<const float*>(cache_k.adresse), reinterpret_cast<const float*>(cache_v.adresse),
                        reinterpret_cast<const float*>(puits.adresse), reinterpret_cast<float*>(sortie.adresse), *p);
     return trc::apres_lancement("attention_kvf32");
