@@ -8,9 +8,8 @@
 //   fusion_finir     y[r] = fixed-order sum of the row's tile partials + bias;
 //   fusion_finir_swiglu    the same for gate and up, then the gpt-oss clamped SwiGLU (one expert);
 //   fusion_finir_combiner  the same for the k down products, then the weighted combine;
-//   fusion_routeur   (MoE layer) router logits; the DELTA pass runs the top-k, the other
-//                    kernels derive their jobs on the device from the chosen indices, and the
-//                    down pass finishes gate/up and applies the SwiGLU itself.
+//   fusion_routeur   (MoE layer) router logits; the first pass after it runs the top-k, and every
+//                    later kernel derives its jobs on the device from the chosen indices.
 //
 // Mapping: one wavefront = two rANS tiles (lanes 0-31, 32-63), each tile's words staged in an LDS
 // ring (anneau.hpp). In a macro-step, lane v of a tile produces the 4 code bytes 4(v%4) ..
@@ -130,7 +129,7 @@ __device__ __forceinline__ void combiner_lignes(const Fin* fins, uint32_t k, con
         for (uint32_t i = 0; i < TOPK_MAX; ++i) {
             if (i < k) {
                 const Fin& f = fins[i];
-                const uint32_t n = (r * f.B + f.B - 1u) / f.bpt - (r * f.B) / f.bpt;
+                const uint32_t n = partiels_en_plus(f, r);
                 float si = p0[i];
                 if (n >= 1u) si += p1[i];
                 for (uint32_t j = 2; j <= n; ++j) si += f.partiels[uint64_t(r) * f.kmax + j];
@@ -146,8 +145,6 @@ __device__ __forceinline__ void combiner_lignes(const Fin* fins, uint32_t k, con
 }  // namespace trc
 
 // CODES pass, x in LDS (colonnes <= X_LDS_MAX): one 160 KiB LDS array laid out as LDS_* says.
-// Option (MoE down jobs): OPT_SWIGLU builds x in LDS as the SwiGLU of the expert's gate/up rows,
-// finished from their partial sums (no separate finisher launch, no act buffer).
 extern "C" __global__ void __launch_bounds__(trc::FILS_GEMV_MAX)
 fusion_gemv(trc::Taches taches, const uint32_t* __restrict__ luts, uint32_t* __restrict__ controle) {
     using namespace trc;
@@ -159,14 +156,13 @@ fusion_gemv(trc::Taches taches, const uint32_t* __restrict__ luts, uint32_t* __r
     // least 256 threads and x at most X_LDS_MAX columns), then the matrix record.
     ChargeLut<3> charge_lut;
     charge_lut.demarrer(lut_src, 3u * M / 4u);
-    const bool swiglu = (taches.options & OPT_SWIGLU) != 0u;
     const bool x_lds = tc.colonnes <= X_LDS_MAX;
     const uint32_t n16 = x_lds ? tc.colonnes / 4u : 0u;
     u32x4 xv[4];
 #pragma unroll
     for (uint32_t i = 0; i < 4; ++i) {
         const uint32_t k = threadIdx.x + i * blockDim.x;
-        if (!swiglu && k < n16) xv[i] = glob<u32x4>(reinterpret_cast<const void*>(tc.x))[k];
+        if (k < n16) xv[i] = glob<u32x4>(reinterpret_cast<const void*>(tc.x))[k];
     }
     const PrepGemv p = preparer_gemv(tc, obtenir_matrice(tc));
     const bool bon = p.bon && x_lds;
@@ -175,21 +171,10 @@ fusion_gemv(trc::Taches taches, const uint32_t* __restrict__ luts, uint32_t* __r
     charge_lut.poser(lut_src, reinterpret_cast<uint2*>(lds + LDS_LUT), 3u * M / 4u);
     if (!bon && threadIdx.x == 0 && blockIdx.x == 0) atomicAdd(&controle[CTL_FORMAT], 1u);
     if (bon) {
-        if (swiglu) {
-            Fin* fins = reinterpret_cast<Fin*>(lds + LDS_ENT);  // the entry area is free until the tiles start
-            const uint32_t w = threadIdx.x >> 6;
-            if (w < 2u) {
-                const Fin f = preparer_fin(uniforme(tache_moe(taches.moe, blockIdx.y, w)));
-                if (__lane_id() == 0) fins[w] = f;
-            }
-            __syncthreads();
-            swiglu_vers_lds(fins[0], fins[1], tc.colonnes, reinterpret_cast<float*>(lds + LDS_X));
-        } else {
 #pragma unroll
-            for (uint32_t i = 0; i < 4; ++i) {
-                const uint32_t k = threadIdx.x + i * blockDim.x;
-                if (k < n16) *reinterpret_cast<u32x4*>(lds + LDS_X + 16u * k) = xv[i];
-            }
+        for (uint32_t i = 0; i < 4; ++i) {
+            const uint32_t k = threadIdx.x + i * blockDim.x;
+            if (k < n16) *reinterpret_cast<u32x4*>(lds + LDS_X + 16u * k) = xv[i];
         }
         if (threadIdx.x < 8u)  // the zero slot (column block 127) that stream padding blocks read
             *reinterpret_cast<u32x4*>(lds + LDS_X + COLONNE_NULLE * 128u + 16u * threadIdx.x) = u32x4{0u, 0u, 0u, 0u};
@@ -203,7 +188,7 @@ fusion_gemv(trc::Taches taches, const uint32_t* __restrict__ luts, uint32_t* __r
 // block, by ranks over the logits: the reference's order and tie rule, deterministic, so all blocks
 // agree; block (0, 0) publishes indices and weights), take their expert's matrix from the directory
 // and publish the selected experts' three records (resolus) for the down pass and the combine.
-// Down launches (OPT_SWIGLU) build x in LDS as the SwiGLU of the expert's gate/up rows.
+// Down launches read x from the experts' SwiGLU rows (fusion_finir_swiglu).
 constexpr uint32_t OPT_TOPK = 2u;
 
 extern "C" __global__ void __launch_bounds__(trc::FILS_GEMV_MAX)
@@ -211,7 +196,6 @@ fusion_codes(trc::Taches taches, const uint32_t* __restrict__ luts, uint32_t* __
     using namespace trc;
     __shared__ __attribute__((aligned(16384))) uint8_t lds[LDS_GEMV];
     const bool topk = (taches.options & OPT_TOPK) != 0u;
-    const bool swiglu = (taches.options & OPT_SWIGLU) != 0u;
     const uint32_t j = topk ? (blockIdx.y & 1u) : min(uniforme32(taches[blockIdx.y].j), 2u);
     const uint32_t* lut_src = luts + (uint64_t(j) * 4u + 1u) * M;
     ChargeLut<3> charge_lut;
@@ -262,7 +246,7 @@ fusion_codes(trc::Taches taches, const uint32_t* __restrict__ luts, uint32_t* __
 #pragma unroll
     for (uint32_t i = 0; i < 4; ++i) {
         const uint32_t k = threadIdx.x + i * blockDim.x;
-        if (!swiglu && k < n16) xv[i] = glob<u32x4>(reinterpret_cast<const void*>(tc.x))[k];
+        if (k < n16) xv[i] = glob<u32x4>(reinterpret_cast<const void*>(tc.x))[k];
     }
     const PrepCodes p = preparer_codes(tc, obtenir_matrice(tc));
     const bool bon = p.bon && x_lds;
@@ -271,21 +255,10 @@ fusion_codes(trc::Taches taches, const uint32_t* __restrict__ luts, uint32_t* __
     charge_lut.poser(lut_src, reinterpret_cast<uint2*>(lds + LDS_LUT), 3u * M / 4u);
     if (!bon && threadIdx.x == 0 && blockIdx.x == 0) atomicAdd(&controle[CTL_FORMAT], 1u);
     if (bon) {
-        if (swiglu) {
-            Fin* fins = reinterpret_cast<Fin*>(lds + LDS_ENT);
-            const uint32_t w = threadIdx.x >> 6;
-            if (w < 2u) {
-                const Fin f = preparer_fin(uniforme(tache_moe(taches.moe, blockIdx.y, w)));
-                if (__lane_id() == 0) fins[w] = f;
-            }
-            __syncthreads();
-            swiglu_vers_lds(fins[0], fins[1], tc.colonnes, reinterpret_cast<float*>(lds + LDS_X));
-        } else {
 #pragma unroll
-            for (uint32_t i = 0; i < 4; ++i) {
-                const uint32_t k = threadIdx.x + i * blockDim.x;
-                if (k < n16) *reinterpret_cast<u32x4*>(lds + LDS_X + 16u * k) = xv[i];
-            }
+        for (uint32_t i = 0; i < 4; ++i) {
+            const uint32_t k = threadIdx.x + i * blockDim.x;
+            if (k < n16) *reinterpret_cast<u32x4*>(lds + LDS_X + 16u * k) = xv[i];
         }
         if (threadIdx.x < 8u)
             *reinterpret_cast<u32x4*>(lds + LDS_X + COLONNE_NULLE * 128u + 16u * threadIdx.x) = u32x4{0u, 0u, 0u, 0u};
@@ -723,7 +696,8 @@ extern "C" uint64_t trc_taille_travail_couche_moe(const trc_dims_expert* dims, u
     const uint32_t R = dims->lignes[0], C = dims->colonnes[0];
     const uint32_t Rm = dims->lignes[2] > R ? dims->lignes[2] : R;
     const uint32_t Cm = dims->colonnes[2] > C ? dims->colonnes[2] : C;
-    return al(4ull * experts) + al(3ull * k * sizeof(trc::MatricePartie)) + 3ull * k * pas_tache(Rm, Cm, n_codes);
+    return al(4ull * experts) + al(3ull * k * sizeof(trc::MatricePartie)) + al(4ull * k * R) +
+           3ull * k * pas_tache(Rm, Cm, n_codes);
 }
 
 // Config 3: one MoE layer decode step at batch 1. logits = W_r x (+ b_r) (W_r bf16, experts x C),
@@ -732,10 +706,12 @@ extern "C" uint64_t trc_taille_travail_couche_moe(const trc_dims_expert* dims, u
 // directory (trc_monter_couche; the parts it points into stay resident); luts: the layer's
 // u32[3][4][4096]. No host sync: the selection flows from the router to the expert kernels through
 // device memory, and every kernel derives its jobs from the top-k indices (checked against
-// `experts` before the directory is read). Five launches: router logits; DELTA (3k matrices, each
-// block running the top-k first); gate/up CODES pass (2k); down CODES pass (k; builds its x as the
-// SwiGLU of the gate/up rows); finish + combine. No cross-block synchronisation inside a launch.
-// Rows are limited to X_LDS_MAX columns (x in LDS).
+// `experts` before the directory is read). Streams of 16 macro-steps per CODES tile and 1 or 2 per
+// DELTA tile take five launches: router logits; gate/up CODES pass (2k jobs, each block running the
+// top-k first, each tile's DELTA decoded in the kernel); the k SwiGLU rows; down CODES pass (k, x
+// = the expert's SwiGLU row); finish + combine. Other tile lengths add a DELTA pass (3k matrices,
+// with the top-k) before the gate/up pass. No cross-block synchronisation inside a launch. Rows are
+// limited to X_LDS_MAX columns (x in LDS).
 namespace {
 // The fused MoE layer; with `norme`, the router takes RMSNorm(residu) with `norme` into x first
 // (x is then written, not read, by the router).
@@ -778,6 +754,8 @@ int couche_moe(trc_vue repertoire, uint32_t experts, trc_vue luts, const trc_dim
     p += al(4ull * experts);
     const uint64_t resolus = p;
     p += al(3ull * k * sizeof(trc::MatricePartie));
+    const uint64_t act = p;
+    p += al(4ull * k * R);
     const uint64_t morceaux = p;
 
     trc::ParamsMoe pm;
@@ -805,9 +783,9 @@ int couche_moe(trc_vue repertoire, uint32_t experts, trc_vue luts, const trc_dim
         pm.partiels = morceaux;
         pm.pas = pas_tache_interne(Rm, Cm);
     }
+    pm.act = act;  // the down jobs' x: the experts' SwiGLU rows
     const Taches t_delta = par_moe(pm, trc::TACHES_MOE_DELTA, 0), t_gu = par_moe(pm, trc::TACHES_MOE_GU, 0),
-                 t_bas = par_moe(pm, trc::TACHES_MOE_BAS, trc::OPT_SWIGLU),
-                 t_gu_topk = par_moe(pm, trc::TACHES_MOE_GU, OPT_TOPK);
+                 t_bas = par_moe(pm, trc::TACHES_MOE_BAS, 0), t_gu_topk = par_moe(pm, trc::TACHES_MOE_GU, OPT_TOPK);
     const hipStream_t f = flux_de(flux);
     auto ctl = reinterpret_cast<uint32_t*>(controle.adresse);
     const uint32_t* l = reinterpret_cast<const uint32_t*>(luts.adresse);
@@ -823,10 +801,14 @@ int couche_moe(trc_vue repertoire, uint32_t experts, trc_vue luts, const trc_dim
                    reinterpret_cast<const uint16_t*>(routeur.adresse), reinterpret_cast<const float*>(x.adresse),
                    reinterpret_cast<const float*>(routeur_biais.adresse), reinterpret_cast<float*>(logits), experts, C);
     }
+    // The k SwiGLU rows are finished once per expert (fusion_finir_swiglu) between gate/up and down:
+    // measured against every down block building them, that launch saves more than it costs.
     if (interne) {
-        // four launches: router, gate/up (top-k, DELTA and CODES), down (SwiGLU, DELTA, CODES), combine
+        // five launches: router, gate/up (top-k, DELTA and CODES), the k SwiGLU rows, down (DELTA and
+        // CODES), combine
         const FormeGemv fgu = forme_gemv(R, C, n_codes, 2 * k), fb = forme_gemv(D, R, n_codes, k);
         TRC_LANCER_N("fusion_codes/gate_up", fusion_codes, fgu.grille, fgu.bloc, f, t_gu_topk, l, ctl);
+        TRC_LANCER(fusion_finir_swiglu, dim3((R + 255) / 256, k), dim3(256), f, t_gu, reinterpret_cast<float*>(act), R);
         TRC_LANCER_N("fusion_codes/down", fusion_codes, fb.grille, fb.bloc, f, t_bas, l, ctl);
         TRC_LANCER(fusion_finir_combiner, dim3((D + 255) / 256), dim3(256), f, t_bas);
         return TRC_OK;
@@ -835,6 +817,7 @@ int couche_moe(trc_vue repertoire, uint32_t experts, trc_vue luts, const trc_dim
                dim3(trc::FILS_ECHELLES_FUSION), f, t_delta, l, ctl);
     TRC_LANCER_N("fusion_gemv/gate_up", fusion_gemv, forme_gemv(R, C, n_codes, 2 * k).grille,
                  forme_gemv(R, C, n_codes, 2 * k).bloc, f, t_gu, l, ctl);
+    TRC_LANCER(fusion_finir_swiglu, dim3((R + 255) / 256, k), dim3(256), f, t_gu, reinterpret_cast<float*>(act), R);
     TRC_LANCER_N("fusion_gemv/down", fusion_gemv, forme_gemv(D, R, n_codes, k).grille,
                  forme_gemv(D, R, n_codes, k).bloc, f, t_bas, l, ctl);
     TRC_LANCER(fusion_finir_combiner, dim3((D + 255) / 256), dim3(256), f, t_bas);

@@ -121,7 +121,7 @@ __device__ __forceinline__ MatricePartie obtenir_matrice(const Tache& tc) {
 // A MoE layer's jobs, derived on the device from the router's top-k: selected expert i (index
 // indices[i] < E, else its jobs get no matrix and count as format errors) has matrices j = 0, 1, 2
 // (gate, up, down), each with its own workspace piece (i*3 + j) * pas; gate/up read x, down reads
-// the SwiGLU of expert i's gate/up rows (computed by the down pass itself, see OPT_SWIGLU).
+// expert i's SwiGLU row (act, finished once per expert between the gate/up and down passes).
 struct ParamsMoe {
     uint64_t repertoire;  // MatricePartie[E][3] of the mounted layer
     uint64_t resolus;     // MatricePartie[k][3] of the selected experts, copied by the DELTA pass
@@ -134,6 +134,7 @@ struct ParamsMoe {
     uint64_t partiels;    // partial sums of piece 0
     uint64_t pas;         // workspace bytes per piece
     uint64_t compte;      // (prefill) u32[E] positions that chose expert e; experts with 0 are skipped
+    uint64_t act;         // f32[k][colonnes[2]] the experts' SwiGLU rows, the down jobs' x (0: built by the down pass)
     uint32_t lignes[3], colonnes[3], kmax[3];
     uint32_t k, E;
 };
@@ -146,9 +147,6 @@ enum ModeTaches : uint32_t {
     TACHES_PREFILL_DELTA = 4,  // job y = (expert y/3, matrix y%3), workspace piece y, if chosen
 };
 
-// Option of a CODES pass over MoE down jobs: x = swiglu_oai(gate_i, up_i), finished from their
-// partial sums.
-constexpr uint32_t OPT_SWIGLU = 1u;
 
 // Job (expert i = expert e of the layer, matrix j) of a MoE layer.
 __device__ __forceinline__ Tache tache_moe_e(const ParamsMoe& moe, uint32_t i, uint32_t j, uint32_t e) {
@@ -161,7 +159,7 @@ __device__ __forceinline__ Tache tache_moe_e(const ParamsMoe& moe, uint32_t i, u
     t.colonnes = choisir(moe.colonnes, j);
     t.ech = moe.ech + uint64_t(i * 3u + j) * moe.pas;
     t.partiels = moe.partiels + uint64_t(i * 3u + j) * moe.pas;
-    t.x = j < 2u ? moe.x : 0ull;
+    t.x = j < 2u ? moe.x : (moe.act != 0 ? moe.act + 4ull * i * moe.colonnes[2] : 0ull);
     t.reserve[0] = t.reserve[1] = 0;
     return t;
 }
@@ -753,6 +751,11 @@ struct Fin {
     uint32_t bon;
 };
 
+// The partial sums of row r after its first: tiles (rB + B - 1) / bpt - rB / bpt.
+__device__ __forceinline__ uint32_t partiels_en_plus(const Fin& f, uint32_t r) {
+    return (r * f.B + f.B - 1u) / f.bpt - (r * f.B) / f.bpt;
+}
+
 // Whole wavefront (uniform job).
 __device__ __forceinline__ Fin preparer_fin(const Tache& tc) {
     const MatricePartie m = obtenir_matrice(tc);
@@ -770,10 +773,10 @@ __device__ __forceinline__ Fin preparer_fin(const Tache& tc) {
 
 // y[r] = fixed-order sum of row r's tile partials + bias[r].
 __device__ __forceinline__ float somme_fin(const Fin& f, uint32_t r) {
-    const uint32_t t0 = (r * f.B) / f.bpt, t1 = (r * f.B + f.B - 1u) / f.bpt;
+    const uint32_t n = partiels_en_plus(f, r);
     const float* p = f.partiels + uint64_t(r) * f.kmax;
     float s = p[0];
-    for (uint32_t k = 1; k <= t1 - t0; ++k) s += p[k];
+    for (uint32_t k = 1; k <= n; ++k) s += p[k];
     return s + f.biais[r];
 }
 
@@ -794,52 +797,6 @@ __device__ __forceinline__ float swiglu_oai_f(float g, float u) {
     const double gv = fmin(double(g), 7.0);
     const double uv = fmin(fmax(double(u), -7.0), 7.0);
     return float(gv / (1.0 + exp(-1.702 * gv)) * (uv + 1.0));
-}
-
-// x[r] = swiglu_oai(gate row r, up row r) for the rows of the calling thread (r = threadIdx.x +
-// i * blockDim.x), finished from the gate/up partial sums as somme_fin does (same order), with the
-// loads of up to 4 rows issued together. 0 for rows past either matrix, or when a job is bad.
-__device__ __forceinline__ void swiglu_vers_lds(const Fin& g, const Fin& u, uint32_t n, float* xs) {
-    const bool ok = g.bon && u.bon;
-    const uint32_t lim = min(n, min(g.lignes, u.lignes));
-    for (uint32_t r0 = threadIdx.x; r0 < n; r0 += 4u * blockDim.x) {
-        float g0[4], g1[4], gb[4], u0[4], u1[4], ub[4];
-#pragma unroll
-        for (uint32_t i = 0; i < 4; ++i) {
-            const uint32_t r = r0 + i * blockDim.x;
-            g0[i] = g1[i] = gb[i] = u0[i] = u1[i] = ub[i] = 0.0f;
-            if (ok && r < lim) {
-                // kmax >= 2 for a good job: the second slot of a row is always inside its slots
-                const float* pg = g.partiels + uint64_t(r) * g.kmax;
-                const float* pu = u.partiels + uint64_t(r) * u.kmax;
-                g0[i] = pg[0];
-                g1[i] = pg[1];
-                gb[i] = g.biais[r];
-                u0[i] = pu[0];
-                u1[i] = pu[1];
-                ub[i] = u.biais[r];
-            }
-        }
-#pragma unroll
-        for (uint32_t i = 0; i < 4; ++i) {
-            const uint32_t r = r0 + i * blockDim.x;
-            if (r >= n) continue;
-            float sg = 0.0f, su = 0.0f;
-            if (ok && r < lim) {
-                const uint32_t ng = (r * g.B + g.B - 1u) / g.bpt - (r * g.B) / g.bpt;
-                const uint32_t nu = (r * u.B + u.B - 1u) / u.bpt - (r * u.B) / u.bpt;
-                sg = g0[i];
-                if (ng >= 1u) sg += g1[i];
-                for (uint32_t k = 2; k <= ng; ++k) sg += g.partiels[uint64_t(r) * g.kmax + k];
-                su = u0[i];
-                if (nu >= 1u) su += u1[i];
-                for (uint32_t k = 2; k <= nu; ++k) su += u.partiels[uint64_t(r) * u.kmax + k];
-                xs[r] = swiglu_oai_f(sg + gb[i], su + ub[i]);
-            } else {
-                xs[r] = 0.0f;
-            }
-        }
-    }
 }
 
 }  // namespace trc
