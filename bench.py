@@ -37,7 +37,7 @@ FICHIER_PMC = RACINE / "profiles" / "moe_config3_pmc.md"
 
 
 def trafic_mesure():
-    """HBM bytes per fusion_gemv launch (mean of the two launches) from the committed counter
+    """HBM bytes per CODES launch (mean of the gate/up and down launches) from the committed counter
     summary (two rocprofv3 --pmc runs, FETCH_SIZE then WRITE_SIZE, scaled by a copy kernel), or None."""
     try:
         for ligne in FICHIER_PMC.read_text().splitlines():
@@ -750,7 +750,7 @@ def main():
     ap.add_argument("--experts", type=int, default=128)
     ap.add_argument("--k", type=int, default=4)
     ap.add_argument("--n-codes", type=int, default=16, help="macro-steps per CODES_CTX tile written by the encoder")
-    ap.add_argument("--n-delta", type=int, default=2, help="macro-steps per DELTA tile written by the encoder")
+    ap.add_argument("--n-delta", type=int, default=1, help="macro-steps per DELTA tile written by the encoder")
     ap.add_argument("--graine", type=int, default=2026)
     ap.add_argument("--tokens", type=int, default=1000, help="seeded activations of the sweep")
     ap.add_argument("--distance-octets", type=float, default=512e6, dest="distance_octets",
