@@ -88,35 +88,12 @@ struct DescFlux {
     uint32_t produits;
 };
 
-// Finds stream (kind, matrix) in a level-0 part; false if the part is malformed or the stream is
-// absent (same acceptance as the reference device reader, commun.cuh:111-129, which takes the first
-// matching descriptor). The part must be 16-byte aligned. Executed by a whole wavefront with uniform
-// arguments: lane i loads descriptor i (a part has at most 64), one ballot finds the first match, so
-// the lookup costs two dependent loads instead of one per descriptor.
-__device__ inline bool trouver_flux(const uint8_t* partie, uint8_t sorte, uint32_t matrice, DescFlux& f) {
-    if (partie == nullptr || (reinterpret_cast<uintptr_t>(partie) & 15u) != 0) return false;
-    const u32x4 en = *glob<u32x4>(partie);  // magic | ... | byte 8, n_flux at 10 | utiles
-    const uint32_t n_flux = en.z >> 16, utiles = en.w;
-    if (en.x != MAGIE_PARTIE0 || (en.z & 0xFFu) != 0) return false;
-    if (n_flux > 64 || 64u + 16u * n_flux > utiles) return false;
-    const uint32_t lane = __lane_id();
-    u32x4 d = {0u, 0u, 0u, 0u};
-    if (lane < n_flux) d = *glob<u32x4>(partie + 64 + 16 * lane);
-    const bool ok = lane < n_flux && (d.x & 0xFFu) == sorte && ((d.x >> 8) & 0xFFu) == matrice;
-    const uint64_t vote = __builtin_amdgcn_ballot_w64(ok);
-    if (vote == 0) return false;
-    const uint32_t i = uint32_t(__builtin_ctzll(vote));
-    const uint32_t dec = uint32_t(__builtin_amdgcn_readlane(d.y, i)), lon = uint32_t(__builtin_amdgcn_readlane(d.z, i));
-    if ((dec & 15u) != 0 || uint64_t(dec) + lon > utiles) return false;
-    f.p = partie + dec;
-    f.longueur = lon;
-    f.produits = uint32_t(__builtin_amdgcn_readlane(d.w, i));
-    return true;
-}
-
-// Finds streams (sortes[i], matrice) for i < n (n <= 4) in one pass over the descriptors: same
-// acceptance as trouver_flux for each (first matching descriptor); false unless all are present.
-// Whole wavefront, uniform arguments.
+// Finds streams (sortes[i], matrice) for i < n (n <= 4) of a level-0 part in one pass over its
+// descriptors, with the acceptance of the reference device reader (commun.cuh:111-129): for each
+// kind the first matching descriptor, whose offset is 16-aligned and whose bytes lie inside the part.
+// False if the part is malformed or a stream is absent. The part must be 16-byte aligned. Executed
+// by a whole wavefront with uniform arguments: lane i loads descriptor i (a part has at most 64),
+// one ballot per kind finds the first match.
 __device__ inline bool trouver_flux_n(const uint8_t* partie, const uint8_t (&sortes)[4], uint32_t n, uint32_t matrice,
                                       DescFlux (&f)[4]) {
     if (partie == nullptr || (reinterpret_cast<uintptr_t>(partie) & 15u) != 0) return false;
@@ -198,45 +175,6 @@ __device__ __forceinline__ uint32_t classe_echelle(uint32_t e, uint32_t med) {
     return delta < 128u ? 0u : (delta == 128u ? 1u : 2u);
 }
 
-// -------------------------------------------------------------------------------- the rANS step
-//
-// MI355X mapping: a wavefront (64 lanes) carries two tiles, lanes 0-31 tile 2w and lanes 32-63
-// tile 2w+1. Within a half, renormalising lanes take consecutive words of their tile's stream in
-// lane order: position = half pointer + popcount of the lower lanes of the same half that also
-// renormalise (one 64-bit ballot, the half's 32 bits, one masked bit count).
-struct DemiVague {
-    uint32_t masque_inf;  // lanes of my half below me
-    bool haut;            // upper half of the wavefront
-};
-
-__device__ __forceinline__ DemiVague demi_vague() {
-    const uint32_t lane = __lane_id();
-    DemiVague d;
-    d.haut = lane >= 32u;
-    d.masque_inf = (1u << (lane & 31u)) - 1u;
-    return d;
-}
-
-// One decode step with a reference-format LUT entry s | (f-1) << 8 | b << 20. Reads the word at
-// the half's pointer (0 past the stream, like the reference's bounded word reader). Returns s.
-__device__ __forceinline__ uint32_t pas_octet(uint32_t& x, uint32_t& ptr, const uint32_t* __restrict__ lut,
-                                              const uint16_t* __restrict__ mots, uint32_t W, DemiVague d,
-                                              bool actif) {
-    const uint32_t e = lut[x & (M - 1u)];
-    const uint32_t y = (((e >> 8) & 0xFFFu) + 1u) * (x >> PROBA_BITS) + (e >> 20);
-    const bool besoin = actif && (y < L);
-    const uint64_t vote = __ballot(besoin);
-    const uint32_t moitie = d.haut ? uint32_t(vote >> 32) : uint32_t(vote);
-    const uint32_t pos = ptr + __popc(moitie & d.masque_inf);
-    uint32_t w = 0;
-    if (besoin && pos < W) w = mots[pos];
-    if (actif) {
-        x = besoin ? ((y << 16) | w) : y;
-        ptr += __popc(moitie);
-    }
-    return e & 0xFFu;
-}
-
 // Integer wave sum, fixed tree (exact and deterministic).
 __device__ __forceinline__ uint32_t somme_vague_u32(uint32_t v) {
 #pragma unroll
@@ -265,12 +203,6 @@ __device__ __forceinline__ float somme_demi_f32(float v) {
 __device__ __forceinline__ float echelle_e8m0(uint32_t e) {
     const uint32_t bits = e >= 2u ? (e - 1u) << 23 : (0x00200000u << e);
     return __uint_as_float(bits);
-}
-
-// Doubled E2M1 magnitude (0xC8643210 nibble table), bit 3 = sign; code 8 reads as -0.
-__device__ __forceinline__ float valeur_e2m1x2(uint32_t c) {
-    const float g = float((0xC8643210u >> ((c & 7u) << 2)) & 15u);
-    return (c & 8u) ? -g : g;
 }
 
 }  // namespace trc

@@ -443,7 +443,15 @@ uint32_t grille_tuiles(uint64_t octets, uint32_t N, uint32_t tuiles_par_bloc) {
     return uint32_t(g < 1 ? 1 : g);
 }
 
+
 constexpr uint32_t TUILES_ECHELLES = trc::FILS_ECHELLES_FUSION / 32;
+
+// Grid of a DELTA pass over `blocs` blocks: sized as for tiles of at least 4 macro-steps, so that with
+// shorter tiles each wavefront loops over several tile pairs and a block's prologue (LUT, record,
+// medians, top-k) serves more than one tile pair.
+uint32_t grille_echelles(uint64_t blocs, uint32_t n_delta) {
+    return grille_tuiles(blocs, n_delta > 4u ? n_delta : 4u, TUILES_ECHELLES);
+}
 
 // Workspace of one matrix job: block entries (u32 per block + staging margin), then partial sums.
 uint64_t octets_ech(uint32_t R, uint32_t C) { return al(4ull * (uint64_t(R) * (C / 32) + trc::ECH_MARGE)); }
@@ -530,7 +538,7 @@ int lancer_echelles_prefill(const ParamsMoe& pm, uint32_t R, uint32_t C, uint32_
                             uint32_t* ctl, hipStream_t f) {
     const Taches t = par_moe(pm, TACHES_PREFILL_DELTA, 0);
     TRC_LANCER_N("fusion_echelles/prefill", fusion_echelles,
-                 dim3(grille_tuiles(uint64_t(R) * (C / 32), n_delta, TUILES_ECHELLES), 3 * pm.E),
+                 dim3(grille_echelles(uint64_t(R) * (C / 32), n_delta), 3 * pm.E),
                  dim3(FILS_ECHELLES_FUSION), f, t, luts, ctl);
     return TRC_OK;
 }
@@ -582,7 +590,7 @@ extern "C" int trc_gemv_fusionnee(trc_vue partie, uint32_t j, trc_vue luts, uint
         return TRC_OK;
     }
     const Taches tv = par_valeur(&t, 1);
-    TRC_LANCER(fusion_echelles, dim3(grille_tuiles(uint64_t(lignes) * B, n_delta, TUILES_ECHELLES), 1),
+    TRC_LANCER(fusion_echelles, dim3(grille_echelles(uint64_t(lignes) * B, n_delta), 1),
                dim3(trc::FILS_ECHELLES_FUSION), f, tv, l, ctl);
     TRC_LANCER_GEMV("fusion_gemv", forme_gemv(lignes, colonnes, n_codes, 1), f, tv, l, ctl);
     TRC_LANCER(fusion_finir, dim3((lignes + 255) / 256, 1), dim3(256), f, tv, reinterpret_cast<float*>(y.adresse), 0u);
@@ -655,7 +663,7 @@ extern "C" int trc_expert_fusionne(trc_vue partie, trc_vue luts, const trc_dims_
         return TRC_OK;
     }
     const Taches trois = par_valeur(t, 3), bas = par_valeur(t + 2, 1);
-    TRC_LANCER(fusion_echelles, dim3(grille_tuiles(uint64_t(Rm) * (Cm / 32), n_delta, TUILES_ECHELLES), 3),
+    TRC_LANCER(fusion_echelles, dim3(grille_echelles(uint64_t(Rm) * (Cm / 32), n_delta), 3),
                dim3(trc::FILS_ECHELLES_FUSION), f, trois, l, ctl);
     TRC_LANCER_GEMV("fusion_gemv", forme_gemv(R, C, n_codes, 2), f, trois, l, ctl);
     TRC_LANCER(fusion_finir_swiglu, dim3((R + 255) / 256, 1), dim3(256), f, trois, reinterpret_cast<float*>(act), R);
@@ -813,7 +821,7 @@ int couche_moe(trc_vue repertoire, uint32_t experts, trc_vue luts, const trc_dim
         TRC_LANCER(fusion_finir_combiner, dim3((D + 255) / 256), dim3(256), f, t_bas);
         return TRC_OK;
     }
-    TRC_LANCER(fusion_echelles, dim3(grille_tuiles(uint64_t(R) * (C / 32), n_delta, TUILES_ECHELLES), 3 * k),
+    TRC_LANCER(fusion_echelles, dim3(grille_echelles(uint64_t(R) * (C / 32), n_delta), 3 * k),
                dim3(trc::FILS_ECHELLES_FUSION), f, t_delta, l, ctl);
     TRC_LANCER_N("fusion_gemv/gate_up", fusion_gemv, forme_gemv(R, C, n_codes, 2 * k).grille,
                  forme_gemv(R, C, n_codes, 2 * k).bloc, f, t_gu, l, ctl);
