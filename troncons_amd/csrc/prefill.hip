@@ -51,12 +51,17 @@ constexpr uint32_t PF_BP_MAX = 128;       // padded blocks per row (4096 columns
 constexpr uint32_t PF_PAIRES_MAX = 16384; // positions x k per call
 constexpr uint32_t ECHELLE_UN = 127u;     // E8M0 1.0
 
+constexpr uint32_t PF_TOURS = 2;          // decode rounds per band: a band's tiles are at most 64
+constexpr uint32_t PF_RB_MAX = 64;         // rows per band
+
 // LDS of prefill_mfma after the decode (the LUT, x and ring regions are free then; the block
-// entries at LDS_ENT are still read while the codes are stored).
-constexpr uint32_t PF_A = 0;                            // codes [RB][Bp][16 B]
-constexpr uint32_t PF_SA = 32u * PF_BP_MAX * 16u;       // scales [RB][Bp]
-constexpr uint32_t PF_PART = PF_SA + 32u * PF_BP_MAX;   // partial sums: 16 waves x 2 x 64 lanes x 16 B
-static_assert(PF_PART + 16u * 2u * 64u * 16u <= LDS_ENT, "prefill LDS regions");
+// entries at LDS_ENT stay free of them): codes [RB][Bp][16 B] at 0, scales [RB][Bp] after them,
+// then the partial sums of the MFMA phase (16 waves x 2 row tiles x 64 lanes x 16 B).
+constexpr uint32_t PF_A = 0;
+constexpr uint32_t PF_PART_OCTETS = 16u * 2u * 64u * 16u;
+__host__ __device__ inline uint32_t pf_sa(uint32_t rb, uint32_t bp) { return rb * bp * 16u; }
+__host__ __device__ inline uint32_t pf_part(uint32_t rb, uint32_t bp) { return (pf_sa(rb, bp) + rb * bp + 15u) & ~15u; }
+__host__ __device__ inline bool pf_lds_tient(uint32_t rb, uint32_t bp) { return pf_part(rb, bp) + PF_PART_OCTETS <= LDS_ENT; }
 
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 
@@ -78,7 +83,7 @@ struct ParamsPrefill {
     uint64_t s;            // f32[T*k][D]
     uint32_t lignes[3], colonnes[3];
     uint32_t bp[3];        // padded blocks per row (multiple of 4)
-    uint32_t rb[3];        // rows per band (16 or 32)
+    uint32_t rb[3];        // rows per band (16, 32 or 64)
     uint32_t T, k, E, D;
 };
 
@@ -285,22 +290,25 @@ struct Operande_b {
 // acc_rt += A_rt (k-step ks) x B over pieces p0 .. p0 + NP - 1: their loads are issued before the MFMAs.
 // This lane's B bytes 0-15 are half `demi` of block 4 ks + `bloc`, bytes 16-31 the same half of block
 // 4 ks + 2 + `bloc`; its scale is block 4 ks + lg's.
+// Pieces p0 .. p0 + NP - 1 with p < P take part (P wave-uniform); every load of the batch goes out
+// before the first MFMA (addresses of invalid columns or unused pieces are clamped to piece 0 of the
+// column's first valid source, so no load sits under a branch).
 template <uint32_t NP>
 __device__ __forceinline__ void produit_pieces(f32x4& acc0, f32x4& acc1, const u32x4& a0, const u32x4& a1,
                                                uint32_t sa0, uint32_t sa1, const Operande_b& ob, uint32_t p0,
-                                               uint32_t ks, uint32_t nrt) {
+                                               uint32_t ks, uint32_t nrt, uint32_t P = PF_PIECES) {
     u32x4 b0[NP], b1[NP];
     uint32_t sb[NP];
 #pragma unroll
     for (uint32_t p = 0; p < NP; ++p) {
-        const uint64_t o = uint64_t(p0 + p) * ob.Bp + 4u * ks;
-        b0[p] = u32x4{0u, 0u, 0u, 0u};
-        b1[p] = u32x4{0u, 0u, 0u, 0u};
-        sb[p] = ECHELLE_UN;
-        if (ob.valide) {
-            b0[p] = *glob<u32x4>(ob.q + (o + ob.bloc) * 32u + ob.demi);
-            b1[p] = *glob<u32x4>(ob.q + (o + 2u + ob.bloc) * 32u + ob.demi);
-            sb[p] = ob.s[o + ob.lg];
+        const bool pris = ob.valide && p0 + p < P;
+        const uint64_t o = uint64_t(pris ? p0 + p : 0u) * ob.Bp + 4u * ks;
+        b0[p] = *glob<u32x4>(ob.q + (o + ob.bloc) * 32u + ob.demi);
+        b1[p] = *glob<u32x4>(ob.q + (o + 2u + ob.bloc) * 32u + ob.demi);
+        sb[p] = ob.s[o + ob.lg];
+        if (!pris) {
+            b0[p] = b1[p] = u32x4{0u, 0u, 0u, 0u};
+            sb[p] = ECHELLE_UN;
         }
     }
     const i32x8 ra0 = {int(a0.x), int(a0.y), int(a0.z), int(a0.w), 0, 0, 0, 0};
@@ -312,6 +320,7 @@ __device__ __forceinline__ void produit_pieces(f32x4& acc0, f32x4& acc1, const u
                       int(b1[p].x), int(b1[p].y), int(b1[p].z), int(b1[p].w)};
 #pragma unroll
     for (uint32_t p = 0; p < NP; ++p) {
+        if (p0 + p >= P) break;  // wave-uniform
         acc0 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ra0, rb[p], acc0, 4, 0, 0, int(sa0), 0, int(sb[p]));
         if (nrt == 2u)
             acc1 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ra1, rb[p], acc1, 4, 0, 0, int(sa1), 0,
@@ -325,7 +334,112 @@ __device__ __forceinline__ void produit_pieces(f32x4& acc0, f32x4& acc1, const u
     __builtin_amdgcn_sched_barrier(0);
 }
 
-// One band of rows [r0, r0 + nl) of matrix j of expert e against the expert's pairs.
+// One decode round of a band: the half-wavefront decodes tile t (its lane's 4 code bytes of each
+// macro-step kept in registers) and keeps, for lanes v % 4 == 0, the E8M0 byte of its block in each
+// macro-step (4 per word), so that the round's entries may be overwritten by the next round.
+struct TourBande {
+    uint32_t codes[PF_NMAX];
+    uint32_t ech[PF_NMAX / 4];
+    uint32_t nb;  // macro-steps of the tile (0: no tile)
+};
+
+__device__ __forceinline__ void decoder_tour(const EnteteRans& h, const DescFlux& fc, const gptr<u32x4> ent16,
+                                             uint32_t t0, uint32_t t_b, uint32_t ba, uint32_t base, TourBande& tb,
+                                             uint32_t& hors_l, uint32_t& pointeur) {
+    const uint32_t lane = __lane_id();
+    const uint32_t v = lane & 31u;
+    const bool haut = lane >= 32u;
+    const uint32_t decal = haut ? 32u : 0u, masque_inf = (1u << v) - 1u;
+    const uint32_t q = v >> 2;
+    const uint32_t demi = threadIdx.x >> 5;
+    const uint32_t a_lut = base + LDS_LUT;
+    const uint32_t a_anneau = base + LDS_ANNEAUX + demi * OCTETS_ANNEAU;
+    const uint32_t a_ent = base + LDS_ENT + demi * (ENT_PAR_TUILE * 4u);
+    const uint32_t a_ent_q = a_ent + 4u * q;
+    const uint32_t N = h.N;
+    const uint32_t t = t0 + (haut ? 1u : 0u);
+    const bool tuile = t <= t_b;
+    const uint32_t nmacro = h.P / 128u;
+    const uint32_t nb_a = min(N, nmacro - t0 * N);
+    const uint32_t nb_b = t0 + 1u <= t_b ? min(N, nmacro - (t0 + 1u) * N) : 0u;
+    const uint32_t nb = haut ? nb_b : nb_a;
+    const uint32_t m0 = t * N;
+    tb.nb = tuile ? nb : 0u;
+    if (tuile) ecrire_lds<u32x4>(a_ent + 16u * v, ent16[2u * m0 + v]);
+    uint32_t x = tuile ? h.etats[t * VOIES + v] : L;
+    const uint32_t debut = tuile ? h.debut[t] : 0u;
+    AnneauR a = ouvrir_anneau_r(h, fc, debut, a_anneau, v, tuile);
+    const uint32_t o0 = a.o2;
+    uint32_t ent_suiv = tuile ? lire_lds<uint32_t>(a_ent_q) : ENTREE_BOURRAGE;
+    const uint32_t nb_min = min(nb_a, nb_b);
+    auto macro = [&](auto tous, uint32_t mm) -> uint32_t {
+        constexpr bool TOUS = decltype(tous)::value;
+        const bool actif = TOUS || mm < nb;
+        const uint32_t ent = actif ? ent_suiv : ENTREE_BOURRAGE;
+        ent_suiv = lire_lds<uint32_t>(a_ent_q + 32u * ((mm + 1u) & 15u));
+        const uint32_t lt = a_lut + (ent & ENT_CTX);
+        uint32_t compte = 0;
+        const uint32_t e0 = pas_r<TOUS>(x, a.o2, compte, lt, a_anneau, decal, masque_inf, actif);
+        const uint32_t e1 = pas_r<TOUS>(x, a.o2, compte, lt, a_anneau, decal, masque_inf, actif);
+        const uint32_t e2 = pas_r<TOUS>(x, a.o2, compte, lt, a_anneau, decal, masque_inf, actif);
+        const uint32_t e3 = pas_r<TOUS>(x, a.o2, compte, lt, a_anneau, decal, masque_inf, actif);
+        a.o2 += 2u * compte;
+        avancer_anneau_r(a, v, actif);
+        // byte 3 of each LUT word is the decoded byte
+        return __builtin_amdgcn_perm(e1, e0, 0x0C0C0703u) | __builtin_amdgcn_perm(e3, e2, 0x07030C0Cu);
+    };
+#pragma unroll
+    for (uint32_t mm = 0; mm < PF_NMAX; ++mm) {
+        if (mm < nb_min)
+            tb.codes[mm] = macro(std::true_type{}, mm);
+        else if (mm < nb_a)
+            tb.codes[mm] = macro(std::false_type{}, mm);
+        else
+            tb.codes[mm] = 0u;
+    }
+#pragma unroll
+    for (uint32_t i = 0; i < PF_NMAX / 4u; ++i) {
+        uint32_t w = 0;
+#pragma unroll
+        for (uint32_t k = 0; k < 4; ++k)
+            w |= ((lire_lds<uint32_t>(a_ent_q + 32u * (4u * i + k)) >> ENT_EXP) + 128u & 255u) << (8u * k);
+        tb.ech[i] = w;
+    }
+    // a tile is checked by the band that holds its first block
+    if (tuile && m0 * 8u >= ba) {
+        hors_l += (x != L) ? 1u : 0u;
+        const uint32_t attendu = (t + 1 < h.T) ? h.debut[t + 1] : h.W;
+        pointeur += (v == 0 && debut + (a.o2 - o0) / 2u != attendu) ? 1u : 0u;
+    }
+}
+
+// A round's codes and scales into the band's LDS arrays: codes [row][Bp][16 B], scales [row][Bp].
+__device__ __forceinline__ void poser_tour(const TourBande& tb, uint32_t t, uint32_t N, uint32_t B, uint32_t Bp,
+                                           uint32_t r0, uint32_t ba, uint32_t bb, uint32_t base, uint32_t a_sa) {
+    const uint32_t v = __lane_id() & 31u, q = v >> 2;
+    uint32_t beta = 8u * t * N + q;
+    uint32_t ligne = beta / B, blk = beta - ligne * B;
+#pragma unroll
+    for (uint32_t mm = 0; mm < PF_NMAX; ++mm) {
+        if (mm < tb.nb && beta >= ba && beta < bb) {
+            const uint32_t o = (ligne - r0) * Bp + blk;
+            ecrire_lds<uint32_t>(base + PF_A + 16u * o + 4u * (v & 3u), tb.codes[mm]);
+            if ((v & 3u) == 0u) ecrire_lds<uint8_t>(a_sa + o, uint8_t(tb.ech[mm >> 2] >> (8u * (mm & 3u))));
+        }
+        beta += 8u;
+        blk += 8u;
+        if (blk >= B) {  // B >= 8: one row at most
+            blk -= B;
+            ++ligne;
+        }
+    }
+}
+
+// One band of rows [r0, r0 + nl) of matrix j of expert e against the expert's pairs: its tiles
+// decoded in up to two rounds of 32 (one tile per half-wavefront a round), stored in LDS as MXFP4,
+// then the block-scaled MFMA. With 64-row bands (4 row tiles) waves 0-7 take row tiles 0-1 and
+// waves 8-15 row tiles 2-3, each group splitting K over its 8 waves; with 16 or 32 rows all 16
+// waves split K.
 template <uint32_t J>
 __device__ __forceinline__ void prefill_bande(const ParamsPrefill& pp, const uint32_t* __restrict__ luts,
                                               uint32_t* __restrict__ controle, uint8_t* lds) {
@@ -345,7 +459,7 @@ __device__ __forceinline__ void prefill_bande(const ParamsPrefill& pp, const uin
     const uint32_t N = h.N;
     const uint32_t ba = r0 * B, bb = (r0 + nl) * B;  // the band's blocks
     const uint32_t t_a = N ? (ba / 8u) / N : 0u, t_b = N ? ((bb - 1u) / 8u) / N : 0u;
-    const bool bon = m.bon != 0u && N >= 1u && N <= PF_NMAX && t_b < h.T && t_b - t_a < 32u;
+    const bool bon = m.bon != 0u && N >= 1u && N <= PF_NMAX && t_b < h.T && t_b - t_a < 32u * PF_TOURS;
     charge_lut.poser(lut_src, reinterpret_cast<uint2*>(lds + LDS_LUT), 3u * M / 4u);
     if (!bon) {
         if (blockIdx.x == 0 && threadIdx.x == 0) atomicAdd(&controle[CTL_FORMAT], 1u);
@@ -353,125 +467,59 @@ __device__ __forceinline__ void prefill_bande(const ParamsPrefill& pp, const uin
     }
     __syncthreads();
 
-    // ---- decode: half-wavefront h2 of wave w decodes tile t_a + 2w + h2, codes in registers
+    // ---- decode: in round r, half-wavefront h2 of wave w decodes tile t_a + 32 r + 2w + h2
     const uint32_t lane = __lane_id();
-    const uint32_t v = lane & 31u;
-    const bool haut = lane >= 32u;
-    const uint32_t decal = haut ? 32u : 0u, masque_inf = (1u << v) - 1u;
-    const uint32_t q = v >> 2;
     const uint32_t w = threadIdx.x >> 6;
-    const uint32_t demi = threadIdx.x >> 5;
     const uint32_t base = adresse_lds(lds);
-    const uint32_t a_lut = base + LDS_LUT;
-    const uint32_t a_anneau = base + LDS_ANNEAUX + demi * OCTETS_ANNEAU;
-    const uint32_t a_ent = base + LDS_ENT + demi * (ENT_PAR_TUILE * 4u);
-    const uint32_t a_ent_q = a_ent + 4u * q;
-    const uint32_t t0 = t_a + 2u * w;
-    const uint32_t t = t0 + (haut ? 1u : 0u);
-    const bool vague_active = t0 <= t_b;
-    const bool tuile = t <= t_b;
-    const uint32_t nmacro = h.P / 128u;
-    const uint32_t nb_a = vague_active ? min(N, nmacro - t0 * N) : 0u;
-    const uint32_t nb_b = t0 + 1u <= t_b ? min(N, nmacro - (t0 + 1u) * N) : 0u;
-    const uint32_t nb = haut ? nb_b : nb_a;
-    const uint32_t m0 = t * N;
-    uint32_t codes[PF_NMAX];
+    const gptr<u32x4> ent16 = glob<u32x4>(reinterpret_cast<const void*>(pp.ech + uint64_t(e * 3u + j) * pp.pas_ech));
     uint32_t hors_l = 0, pointeur = 0;
-    if (vague_active) {
-        const gptr<u32x4> ent16 = glob<u32x4>(reinterpret_cast<const void*>(pp.ech + uint64_t(e * 3u + j) * pp.pas_ech));
-        if (tuile) ecrire_lds<u32x4>(a_ent + 16u * v, ent16[2u * m0 + v]);
-        uint32_t x = tuile ? h.etats[t * VOIES + v] : L;
-        const uint32_t debut = tuile ? h.debut[t] : 0u;
-        AnneauR a = ouvrir_anneau_r(h, m.codes, debut, a_anneau, v, tuile);
-        const uint32_t o0 = a.o2;
-        uint32_t ent_suiv = tuile ? lire_lds<uint32_t>(a_ent_q) : ENTREE_BOURRAGE;
-        const uint32_t nb_min = min(nb_a, nb_b);
-        auto macro = [&](auto tous, uint32_t mm) -> uint32_t {
-            constexpr bool TOUS = decltype(tous)::value;
-            const bool actif = TOUS || mm < nb;
-            const uint32_t ent = actif ? ent_suiv : ENTREE_BOURRAGE;
-            ent_suiv = lire_lds<uint32_t>(a_ent_q + 32u * ((mm + 1u) & 15u));
-            const uint32_t lt = a_lut + (ent & ENT_CTX);
-            uint32_t compte = 0;
-            const uint32_t e0 = pas_r<TOUS>(x, a.o2, compte, lt, a_anneau, decal, masque_inf, actif);
-            const uint32_t e1 = pas_r<TOUS>(x, a.o2, compte, lt, a_anneau, decal, masque_inf, actif);
-            const uint32_t e2 = pas_r<TOUS>(x, a.o2, compte, lt, a_anneau, decal, masque_inf, actif);
-            const uint32_t e3 = pas_r<TOUS>(x, a.o2, compte, lt, a_anneau, decal, masque_inf, actif);
-            a.o2 += 2u * compte;
-            avancer_anneau_r(a, v, actif);
-            // byte 3 of each LUT word is the decoded byte
-            return __builtin_amdgcn_perm(e1, e0, 0x0C0C0703u) | __builtin_amdgcn_perm(e3, e2, 0x07030C0Cu);
-        };
-#pragma unroll
-        for (uint32_t mm = 0; mm < PF_NMAX; ++mm) {
-            if (mm < nb_min)
-                codes[mm] = macro(std::true_type{}, mm);
-            else if (mm < nb_a)
-                codes[mm] = macro(std::false_type{}, mm);
-            else
-                codes[mm] = 0u;
-        }
-        // a tile is checked by the band that holds its first block
-        if (tuile && m0 * 8u >= ba) {
-            hors_l += (x != L) ? 1u : 0u;
-            const uint32_t attendu = (t + 1 < h.T) ? h.debut[t + 1] : h.W;
-            pointeur += (v == 0 && debut + (a.o2 - o0) / 2u != attendu) ? 1u : 0u;
-        }
-    }
+    TourBande tour0, tour1;
+    tour0.nb = tour1.nb = 0u;
+    const uint32_t t00 = t_a + 2u * w, t01 = t00 + 32u;
+    if (t00 <= t_b) decoder_tour(h, m.codes, ent16, t00, t_b, ba, base, tour0, hors_l, pointeur);
+    if (t01 <= t_b) decoder_tour(h, m.codes, ent16, t01, t_b, ba, base, tour1, hors_l, pointeur);
     verser_controle(controle, hors_l, pointeur);
     __syncthreads();  // every tile decoded: the LUT, x and ring regions are free
 
-    // ---- store the band's codes and scales: codes [row][Bp][16 B], scales [row][Bp]
-    if (vague_active && tuile) {
-        uint32_t beta = 8u * m0 + q;
-        uint32_t ligne = beta / B, blk = beta - ligne * B;
-#pragma unroll
-        for (uint32_t mm = 0; mm < PF_NMAX; ++mm) {
-            if (mm < nb && beta >= ba && beta < bb) {
-                const uint32_t o = (ligne - r0) * Bp + blk;
-                ecrire_lds<uint32_t>(base + PF_A + 16u * o + 4u * (v & 3u), codes[mm]);
-                if ((v & 3u) == 0u) {
-                    const uint32_t ent = lire_lds<uint32_t>(a_ent_q + 32u * mm);
-                    ecrire_lds<uint8_t>(base + PF_SA + o, uint8_t((ent >> ENT_EXP) + 128u));
-                }
-            }
-            beta += 8u;
-            blk += 8u;
-            if (blk >= B) {  // B >= 8: one row at most
-                blk -= B;
-                ++ligne;
-            }
+    // ---- store the band's codes and scales
+    const uint32_t a_sa = base + pf_sa(RB, Bp), a_part = base + pf_part(RB, Bp);
+    const uint32_t haut = lane >= 32u ? 1u : 0u;
+    poser_tour(tour0, t00 + haut, N, B, Bp, r0, ba, bb, base, a_sa);
+    poser_tour(tour1, t01 + haut, N, B, Bp, r0, ba, bb, base, a_sa);
+    // padding: blocks B .. Bp - 1 of every row, then rows nl .. RB - 1 (zero codes, scale 1)
+    const uint32_t pad = Bp - B;
+    for (uint32_t i = threadIdx.x; i < nl * pad + (RB - nl) * Bp; i += blockDim.x) {
+        uint32_t o;
+        if (i < nl * pad) {
+            const uint32_t rl = i / pad;
+            o = rl * Bp + B + (i - rl * pad);
+        } else {
+            o = nl * Bp + (i - nl * pad);
         }
-    }
-    for (uint32_t i = threadIdx.x; i < RB * Bp; i += blockDim.x) {  // padding blocks and rows
-        const uint32_t rl = i / Bp, blk = i - rl * Bp;
-        if (blk >= B || rl >= nl) {
-            ecrire_lds<u32x4>(base + PF_A + 16u * i, u32x4{0u, 0u, 0u, 0u});
-            ecrire_lds<uint8_t>(base + PF_SA + i, uint8_t(ECHELLE_UN));
-        }
+        ecrire_lds<u32x4>(base + PF_A + 16u * o, u32x4{0u, 0u, 0u, 0u});
+        ecrire_lds<uint8_t>(a_sa + o, uint8_t(ECHELLE_UN));
     }
     __syncthreads();
 
-    // ---- MFMA: wave w takes the k-steps ks = w, w + 16 (4 blocks each) of both 16-row tiles for
-    // every 16-pair tile; the 16 waves' partial sums are added in wave order.
+    // ---- MFMA: the waves of group g take row tiles 2g, 2g + 1 and the k-steps ks = (w mod VG) +
+    // VG i (4 blocks each) for every 16-pair tile; a group's partial sums are added in wave order.
     const uint32_t nks = Bp / 4u, nrt = RB / 16u;
+    const uint32_t groupes = nrt > 2u ? 2u : 1u, VG = 16u / groupes;
+    const uint32_t g = w / VG, wg = w - g * VG;
+    const uint32_t nrt_g = min(2u, nrt - 2u * g);  // row tiles of this wave's group
     const uint32_t lr = lane & 15u, lg = lane >> 4;
-    u32x4 af[2][2];
-    uint32_t sa[2][2];
-#pragma unroll
-    for (uint32_t rt = 0; rt < 2; ++rt)
-#pragma unroll
-        for (uint32_t i = 0; i < 2; ++i) {
-            const uint32_t ks = w + 16u * i;
-            if (rt < nrt && ks < nks) {
-                const uint32_t o = (16u * rt + lr) * Bp + 4u * ks + lg;
-                af[rt][i] = lire_lds<u32x4>(base + PF_A + 16u * o);
-                sa[rt][i] = lire_lds<uint8_t>(base + PF_SA + o);
-            } else {
-                af[rt][i] = u32x4{0u, 0u, 0u, 0u};
-                sa[rt][i] = ECHELLE_UN;
-            }
+    constexpr uint32_t KS_MAX = PF_BP_MAX / 4u / 8u;  // k-steps per wave, 8 waves per group
+    // the A operands of k-step ks for this wave's row tiles, read from LDS where they are used
+    auto operande_a = [&](uint32_t rt, uint32_t ks, u32x4& a, uint32_t& sc) {
+        if (rt < nrt_g) {
+            const uint32_t o = (16u * (2u * g + rt) + lr) * Bp + 4u * ks + lg;
+            a = lire_lds<u32x4>(base + PF_A + 16u * o);
+            sc = lire_lds<uint8_t>(a_sa + o);
+        } else {
+            a = u32x4{0u, 0u, 0u, 0u};
+            sc = ECHELLE_UN;
         }
+    };
     const uint32_t P = uniforme32(min(reinterpret_cast<const uint32_t*>(pp.pieces)[J == 2u ? 0 : 1], PF_PIECES));
     const uint32_t debut_e = uniforme32(reinterpret_cast<const uint32_t*>(pp.debut)[e]);
     const uint32_t* paires = reinterpret_cast<const uint32_t*>(pp.paires);
@@ -491,26 +539,30 @@ __device__ __forceinline__ void prefill_bande(const ParamsPrefill& pp, const uin
                             bloc_b, demi_b, lg, valide};
         f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (uint32_t i = 0; i < 2; ++i) {
-            const uint32_t ks = w + 16u * i;
+        for (uint32_t i = 0; i < KS_MAX; ++i) {
+            const uint32_t ks = wg + VG * i;
             if (ks >= nks) continue;  // wave-uniform
-            // pieces two at a time: their four loads in flight together, then their MFMAs
+            u32x4 a0, a1;
+            uint32_t s0, s1;
+            operande_a(0u, ks, a0, s0);
+            operande_a(1u, ks, a1, s1);
             for (uint32_t p0 = 0; p0 < P; p0 += 2u) {
                 if (p0 + 1u < P)
-                    produit_pieces<2>(acc0, acc1, af[0][i], af[1][i], sa[0][i], sa[1][i], ob, p0, ks, nrt);
+                    produit_pieces<2>(acc0, acc1, a0, a1, s0, s1, ob, p0, ks, nrt_g, P);
                 else
-                    produit_pieces<1>(acc0, acc1, af[0][i], af[1][i], sa[0][i], sa[1][i], ob, p0, ks, nrt);
+                    produit_pieces<1>(acc0, acc1, a0, a1, s0, s1, ob, p0, ks, nrt_g, P);
             }
         }
-        ecrire_lds<f32x4>(base + PF_PART + ((w * 2u + 0u) * 64u + lane) * 16u, acc0);
-        ecrire_lds<f32x4>(base + PF_PART + ((w * 2u + 1u) * 64u + lane) * 16u, acc1);
+        ecrire_lds<f32x4>(a_part + ((w * 2u + 0u) * 64u + lane) * 16u, acc0);
+        ecrire_lds<f32x4>(a_part + ((w * 2u + 1u) * 64u + lane) * 16u, acc1);
         __syncthreads();
         if (threadIdx.x < nrt * 256u) {
             const uint32_t rt = threadIdx.x >> 8, reste = threadIdx.x & 255u;
+            const uint32_t gg = rt >> 1, rl = rt & 1u;  // the row tile's group and its tile in the group
             const uint32_t ln = reste >> 2, r = reste & 3u;
             float s = 0.0f;
-            for (uint32_t ww = 0; ww < 16u; ++ww)
-                s += lire_lds<float>(base + PF_PART + ((ww * 2u + rt) * 64u + ln) * 16u + 4u * r);
+            for (uint32_t ww = 0; ww < VG; ++ww)
+                s += lire_lds<float>(a_part + (((gg * VG + ww) * 2u + rl) * 64u + ln) * 16u + 4u * r);
             const uint32_t ligne = 16u * rt + 4u * (ln >> 4) + r, jeton = 16u * tt + (ln & 15u);
             if (ligne < nl && jeton < n_e) {
                 const uint32_t cc = paires[debut_e + jeton];
@@ -583,11 +635,13 @@ using trc::usage;
 uint64_t al(uint64_t x) { return (x + 255u) & ~uint64_t(255); }
 uint32_t bp_de(uint32_t C) { return ((C / 32u + 3u) / 4u) * 4u; }
 
-// Rows per band such that a band's CODES_CTX tiles (N macro-steps of 8 blocks each) fit the 32
-// tiles a block decodes: 32 rows when they do, else 16, else 0.
+// Rows per band: 64, 32 or 16, the most whose CODES_CTX tiles (N macro-steps of 8 blocks each) fit
+// the 64 tiles a block decodes in two rounds and whose codes, scales and partial sums fit the LDS;
+// 0 if none does.
 uint32_t rb_de(uint32_t B, uint32_t N) {
-    for (uint32_t rb = 32; rb >= 16; rb -= 16)
-        if ((rb * B - 1u) / (8u * N) + 2u <= 32u) return rb;
+    const uint32_t bp = ((B + 3u) / 4u) * 4u;
+    for (uint32_t rb = trc::PF_RB_MAX; rb >= 16; rb /= 2)
+        if ((rb * B - 1u) / (8u * N) + 2u <= 32u * trc::PF_TOURS && trc::pf_lds_tient(rb, bp)) return rb;
     return 0;
 }
 
