@@ -139,16 +139,16 @@ __device__ __forceinline__ void etendre_luts(const uint32_t* __restrict__ src, u
 
 // The same in two halves, so that other loads are in flight meanwhile: demarrer() issues the first
 // batch's loads, poser() stores them and expands the rest (blocks smaller than n4 / LOT threads).
+// The first batch's loads are unconditional (index clamped; poser stores only the real ones): with
+// no branch around them the compiler's wait counts stay exact, so waiting for a load issued before
+// them does not also wait for them.
 template <uint32_t LOT>
 struct ChargeLut {
     u32x4 t[LOT];
     __device__ __forceinline__ void demarrer(const uint32_t* __restrict__ src, uint32_t n4) {
         const gptr<u32x4> s4 = glob<u32x4>(src);
 #pragma unroll
-        for (uint32_t k = 0; k < LOT; ++k) {
-            const uint32_t i = k * blockDim.x + threadIdx.x;
-            if (i < n4) t[k] = s4[i];
-        }
+        for (uint32_t k = 0; k < LOT; ++k) t[k] = s4[min(k * blockDim.x + threadIdx.x, n4 - 1u)];
     }
     __device__ __forceinline__ void poser(const uint32_t* __restrict__ src, uint2* dst, uint32_t n4) {
 #pragma unroll
@@ -163,6 +163,32 @@ struct ChargeLut {
             }
         }
         if (LOT * blockDim.x < n4) etendre_luts<LOT>(src, dst, n4, LOT * blockDim.x);
+    }
+};
+
+// The three decode LUTs of a block of FILS threads (a compile-time size dividing 3 x 4096 / 4) in
+// one batch of 3072 / FILS unconditional 16-byte loads per thread, expanded into LDS by poser():
+// no loop and no branch, so the compiler's wait counts stay exact around them.
+template <uint32_t FILS>
+struct ChargeLutBloc {
+    static constexpr uint32_t N4 = 3u * M / 4u;
+    static constexpr uint32_t LOT = N4 / FILS;
+    static_assert(N4 % FILS == 0, "the block size divides the LUT's 16-byte groups");
+    u32x4 t[LOT];
+    __device__ __forceinline__ void demarrer(const uint32_t* __restrict__ src) {
+        const gptr<u32x4> s4 = glob<u32x4>(src);
+#pragma unroll
+        for (uint32_t k = 0; k < LOT; ++k) t[k] = s4[k * FILS + threadIdx.x];
+    }
+    __device__ __forceinline__ void poser(uint2* dst) const {
+#pragma unroll
+        for (uint32_t k = 0; k < LOT; ++k) {
+            uint2* d = dst + 4u * (k * FILS + threadIdx.x);
+            d[0] = entree8(t[k].x);
+            d[1] = entree8(t[k].y);
+            d[2] = entree8(t[k].z);
+            d[3] = entree8(t[k].w);
+        }
     }
 };
 

@@ -43,33 +43,35 @@ __device__ __forceinline__ u32x4 lire16_flux(const uint8_t* p, uint32_t n, uint3
     return *glob<u32x4>(p + min(o, dernier));
 }
 
-// Streams of CODES tile t (and, with DELTA, its DELTA tile) for lane v of a half-wavefront.
+// Streams of CODES tile t (and, with DELTA, its DELTA tile) for lane v of a half-wavefront. Every
+// load is unconditional, at an index clamped inside its stream (h.T >= 1): no branch surrounds
+// them, so the compiler can count them, and a wait for an earlier load leaves these in flight. A
+// tile past the stream reads the last tile's data, which its half never decodes nor checks.
 template <bool DELTA>
 __device__ __forceinline__ Avance lire_avance(const EnteteRans& hc, const DescFlux& fc, const EnteteRans& hd,
-                                              const DescFlux& fd, const uint8_t* med, uint32_t R, uint32_t B,
+                                              const DescFlux& fd, const uint8_t* med, uint32_t R, const Diviseur& B,
                                               uint32_t t, uint32_t v) {
     Avance a;
-    a.tete = lire_tete(hc, t, v);
-    const bool tuile = t < hc.T;
+    a.tete = lire_tete_borne(hc, t, v);
     const uint32_t base_c = uint32_t(reinterpret_cast<const uint8_t*>(hc.mots) - fc.p) + 2u * a.tete.debut;
     const uint32_t g0c = base_c & ~15u;
-    a.mots0 = tuile ? lire16_flux(fc.p, fc.longueur, g0c + 16u * v) : u32x4{0u, 0u, 0u, 0u};
-    a.mots1 = tuile ? lire16_flux(fc.p, fc.longueur, g0c + 512u + 16u * v) : u32x4{0u, 0u, 0u, 0u};
+    a.mots0 = lire16_flux(fc.p, fc.longueur, g0c + 16u * v);
+    a.mots1 = lire16_flux(fc.p, fc.longueur, g0c + 512u + 16u * v);
     a.xd = L;
     a.dDebut = a.dAttendu = 0;
     a.dmots = u32x4{0u, 0u, 0u, 0u};
     a.med0 = a.med1 = 0;
     if (DELTA) {
-        const uint32_t tau = t / hd.N;  // N_delta is 1 or 2
-        const TeteTuile td = lire_tete(hd, tau, v);
+        const uint32_t tau = t >> (hd.N - 1u);  // t / N_delta, N_delta being 1 or 2
+        const TeteTuile td = lire_tete_borne(hd, tau, v);
         a.xd = td.x;
         a.dDebut = td.debut;
         a.dAttendu = td.attendu;
         const uint32_t base_d = uint32_t(reinterpret_cast<const uint8_t*>(hd.mots) - fd.p) + 2u * td.debut;
-        if (tuile && tau < hd.T) a.dmots = lire16_flux(fd.p, fd.longueur, (base_d & ~15u) + 16u * v);
+        a.dmots = lire16_flux(fd.p, fd.longueur, (base_d & ~15u) + 16u * v);
         const uint32_t bloc0 = 128u * t + 4u * v;
-        a.med0 = tuile ? uint32_t(glob<uint8_t>(med)[min(bloc0 / B, R - 1u)]) : 0u;
-        a.med1 = tuile ? uint32_t(glob<uint8_t>(med)[min((bloc0 + 3u) / B, R - 1u)]) : 0u;
+        a.med0 = uint32_t(glob<uint8_t>(med)[min(B.quotient(bloc0), R - 1u)]);
+        a.med1 = uint32_t(glob<uint8_t>(med)[min(B.quotient(bloc0 + 3u), R - 1u)]);
     }
     return a;
 }
@@ -94,9 +96,10 @@ __device__ __forceinline__ uint32_t pas_delta(uint32_t& x, uint32_t o2, uint32_t
 
 // The 4 block entries of lane v (blocks 4v .. 4v + 3 of CODES tile t) from its 4 delta bytes.
 __device__ __forceinline__ u32x4 entrees_de_delta(uint32_t mot, const Avance& a, uint32_t bloc0, uint32_t nblocs,
-                                                  uint32_t B) {
+                                                  const Diviseur& divB) {
     u32x4 s;
-    const uint32_t ligne0 = bloc0 / B;
+    const uint32_t B = divB.d;
+    const uint32_t ligne0 = divB.quotient(bloc0);
     uint32_t col = bloc0 - ligne0 * B, ligne = ligne0;
 #pragma unroll
     for (uint32_t k = 0; k < 4; ++k) {
@@ -113,12 +116,20 @@ __device__ __forceinline__ u32x4 entrees_de_delta(uint32_t mot, const Avance& a,
     return s;
 }
 
+// The launch's block size (a kernel's compile-time constant) and x-extent, the latter read once at
+// kernel start into a scalar register: read later, after a barrier, it can come from a vector load
+// of the dispatch packet whose wait would also drain the tile read-ahead in flight.
+struct Grille {
+    uint32_t fils, blocs_x;
+};
+
 // What the CODES pass needs of a job in the internal-DELTA mode: both streams' headers, the
 // medians, the DELTA LUT. bon: every check passed and the tile lengths are the mode's.
 struct PrepCodes {
     DescFlux fc, fd;
     EnteteRans hc, hd;
     const uint8_t* med;
+    Diviseur B;  // blocks per row
     bool bon;
 };
 
@@ -132,14 +143,15 @@ __device__ __forceinline__ PrepCodes preparer_codes(const Tache& tc, const Matri
     p.hc = entete_de(m.codes, m.cP, m.cN, m.cT, m.cW);
     p.hd = entete_de(m.delta, m.dP, m.dN, m.dT, m.dW);
     p.med = m.med.p;
+    p.B = Diviseur::de(B);
     return p;
 }
 
 // The first tile of the calling lane's half-wavefront (tile loops start at 2 * global wavefront).
 template <bool DELTA>
-__device__ __forceinline__ Avance premiere_avance(const PrepCodes& p, uint32_t R, uint32_t B) {
-    const uint32_t vague = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    return lire_avance<DELTA>(p.hc, p.fc, p.hd, p.fd, p.med, R, B, 2u * vague + (__lane_id() >= 32u ? 1u : 0u),
+__device__ __forceinline__ Avance premiere_avance(const PrepCodes& p, uint32_t R, const Grille& g) {
+    const uint32_t vague = blockIdx.x * (g.fils >> 6) + (threadIdx.x >> 6);
+    return lire_avance<DELTA>(p.hc, p.fc, p.hd, p.fd, p.med, R, p.B, 2u * vague + (__lane_id() >= 32u ? 1u : 0u),
                               __lane_id() & 31u);
 }
 
@@ -147,23 +159,22 @@ __device__ __forceinline__ Avance premiere_avance(const PrepCodes& p, uint32_t R
 // `avance0`: premiere_avance(p), read by the caller before its barrier. lutd: the job's DELTA LUT
 // (reference format) in device memory.
 __device__ __forceinline__ void corps_codes(const Tache& tc, const PrepCodes& p, uint8_t* lds, const uint32_t* lutd_,
-                                            uint32_t* __restrict__ controle, const Avance& avance0) {
+                                            uint32_t* __restrict__ controle, const Avance& avance0, const Grille& g) {
     const EnteteRans& h = p.hc;
     const EnteteRans& hd = p.hd;
     const uint32_t R = tc.lignes, B = tc.colonnes / 32u, nblocs = R * B;
     const gptr<uint32_t> lutd = glob<uint32_t>(lutd_);
     float* __restrict__ partiels = reinterpret_cast<float*>(tc.partiels);
     const uint32_t kmax = tc.kmax;
-    const uint32_t bpt = 8u * h.N;
 
     const uint32_t lane = __lane_id();
     const uint32_t v = lane & 31u;
     const bool haut = lane >= 32u;
     const uint32_t decal = haut ? 32u : 0u, masque_inf = (1u << v) - 1u;
     const uint32_t q = v >> 2, q4 = v & 3u;
-    const uint32_t vagues_bloc = blockDim.x >> 6;
+    const uint32_t vagues_bloc = g.fils >> 6;
     const uint32_t vague = uniforme32(blockIdx.x * vagues_bloc + (threadIdx.x >> 6));
-    const uint32_t n_vagues = gridDim.x * vagues_bloc;
+    const uint32_t n_vagues = g.blocs_x * vagues_bloc;
     const uint32_t demi = (threadIdx.x >> 5) & (2u * vagues_bloc - 1u);
     const uint32_t base = adresse_lds(lds);
     const uint32_t a_lut = base + LDS_LUT;
@@ -188,7 +199,7 @@ __device__ __forceinline__ void corps_codes(const Tache& tc, const PrepCodes& p,
 
         // 1. DELTA: the half's DELTA tile from its start to macro-step t mod N_delta (DELTA tile
         // t / N_delta covers CODES tiles t - t mod N_delta ..), words from the ring
-        const uint32_t saut = t - (t / dN) * dN;   // DELTA macro-steps before this tile's
+        const uint32_t saut = t & (dN - 1u);   // DELTA macro-steps before this tile's (N_delta 1 or 2)
         const uint32_t saut_max = uniforme32(dN == 1u ? 0u : 1u);
         ecrire_lds<u32x4>(a_anneau + 16u * v, cur.dmots);
         {
@@ -214,18 +225,18 @@ __device__ __forceinline__ void corps_codes(const Tache& tc, const PrepCodes& p,
             if (md == saut) mot = m4;
         }
         // the DELTA tile's end checks, by the half that decoded its last macro-step
-        const uint32_t tau = t / dN;
+        const uint32_t tau = t >> (dN - 1u);
         const uint32_t nbd = tau < dT ? min(dN, nmacro_d - tau * dN) : 0u;
         if (tuile && saut + 1u == nbd) {
             hors_l += (xd != L) ? 1u : 0u;
             pointeur += (v == 0 && cur.dDebut + (od - ((mots_d + 2u * cur.dDebut) & 15u)) / 2u != cur.dAttendu) ? 1u : 0u;
         }
         // 2. the tile's 128 block entries
-        if (tuile) ecrire_lds<u32x4>(a_ent + 16u * v, entrees_de_delta(mot, cur, 128u * t + 4u * v, nblocs, B));
+        if (tuile) ecrire_lds<u32x4>(a_ent + 16u * v, entrees_de_delta(mot, cur, 128u * t + 4u * v, nblocs, p.B));
         // 3. the CODES words over the DELTA ones, and the next pair's streams read ahead
         ecrire_lds<u32x4>(a_anneau + 16u * v, cur.mots0);
         ecrire_lds<u32x4>(a_anneau + 512u + 16u * v, cur.mots1);
-        av = lire_avance<true>(h, p.fc, hd, p.fd, p.med, R, B, t + 2u * n_vagues, v);
+        av = lire_avance<true>(h, p.fc, hd, p.fd, p.med, R, p.B, t + 2u * n_vagues, v);
         AnneauR a;
         {
             const uint32_t mot0 = mots_c + 2u * cur.tete.debut;
@@ -242,8 +253,8 @@ __device__ __forceinline__ void corps_codes(const Tache& tc, const PrepCodes& p,
         uint32_t x = cur.tete.x;
         const uint32_t debut = cur.tete.debut, attendu = cur.tete.attendu;
         const uint32_t o0 = a.o2;
-        uint32_t rho = (m0 * 8u) / B;
-        const uint32_t rho0 = rho, case0 = t - premiere_tuile(rho0, B, bpt);
+        uint32_t rho = p.B.quotient(m0 * 8u);
+        const uint32_t rho0 = rho, case0 = t - (rho0 * B) / 128u;  // first tile of row rho0 (128 blocks per tile)
         auto ecrire = [&](float s) { partiels[rho * kmax + (rho == rho0 ? case0 : 0u)] = s; };
         uint32_t ent_suiv = tuile ? lire_lds<uint32_t>(a_ent_q) : ENTREE_BOURRAGE;
         const uint32_t nb_min = min(nb_a, nb_b);

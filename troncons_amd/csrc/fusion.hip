@@ -47,7 +47,7 @@ fusion_echelles(trc::Taches taches, const uint32_t* __restrict__ luts, uint32_t*
     __shared__ __attribute__((aligned(16))) uint8_t med[MED_LDS_MAX];
     __shared__ __attribute__((aligned(16))) uint8_t anneaux[(FILS_ECHELLES_FUSION / 32) * OCTETS_ANNEAU];
     __shared__ uint32_t choisis[TOPK_MAX];
-    __shared__ float lg[EXPERTS_MAX];
+    __shared__ __attribute__((aligned(16))) float lg[EXPERTS_MAX];
     const bool moe = taches.mode == TACHES_MOE_DELTA;
     const bool prefill = taches.mode == TACHES_PREFILL_DELTA;
     if (prefill && reinterpret_cast<const uint32_t*>(taches.moe.compte)[blockIdx.y / 3u] == 0u) return;
@@ -191,27 +191,44 @@ fusion_gemv(trc::Taches taches, const uint32_t* __restrict__ luts, uint32_t* __r
 // Down launches read x from the experts' SwiGLU rows (fusion_finir_swiglu).
 constexpr uint32_t OPT_TOPK = 2u;
 
-extern "C" __global__ void __launch_bounds__(trc::FILS_GEMV_MAX)
-fusion_codes(trc::Taches taches, const uint32_t* __restrict__ luts, uint32_t* __restrict__ controle) {
+template <uint32_t FILS>
+__device__ __forceinline__ void codes_bloc(const trc::Taches& taches, const uint32_t* __restrict__ luts,
+                                           uint32_t* __restrict__ controle) {
     using namespace trc;
     __shared__ __attribute__((aligned(16384))) uint8_t lds[LDS_GEMV];
+    const Grille g{FILS, uniforme32(gridDim.x)};
     const bool topk = (taches.options & OPT_TOPK) != 0u;
     const uint32_t j = topk ? (blockIdx.y & 1u) : min(uniforme32(taches[blockIdx.y].j), 2u);
     const uint32_t* lut_src = luts + (uint64_t(j) * 4u + 1u) * M;
-    ChargeLut<3> charge_lut;
-    charge_lut.demarrer(lut_src, 3u * M / 4u);
+    const ParamsMoe& pm = taches.moe;
+    // The prologue is a chain of dependent device-memory reads (logits -> top-k -> the expert's
+    // record -> its first tiles' heads -> their words). Everything that does not depend on the
+    // top-k's outcome is issued first, unconditionally (indices clamped), in the order it is waited
+    // for: the logits; the job's DELTA LUT, which every tile start then reads through the caches
+    // (loaded here only to bring its lines in, and waited for with the decode LUTs); the decode
+    // LUTs; x (its address and width do not depend on the expert).
+    const gptr<float> lg_src = glob<float>(topk ? reinterpret_cast<const void*>(pm.logits) : reinterpret_cast<const void*>(luts));
+    const float lg_v = lg_src[min(threadIdx.x, (topk ? pm.E : 1u) - 1u)];
+    const uint32_t lutd_chaud = glob<uint32_t>(luts + uint64_t(j) * 4u * M)[4u * min(threadIdx.x, M / 4u - 1u)];
+    ChargeLutBloc<FILS> charge_lut;
+    charge_lut.demarrer(lut_src);
+    const Tache tx = topk ? uniforme(tache_moe_e(pm, blockIdx.y >> 1, j, 0u)) : uniforme(taches[blockIdx.y]);
+    const bool x_lds = tx.colonnes <= X_LDS_MAX && tx.x != 0;
+    const uint32_t n16 = x_lds ? tx.colonnes / 4u : 0u;
+    const gptr<u32x4> x_src = glob<u32x4>(x_lds ? reinterpret_cast<const void*>(tx.x) : reinterpret_cast<const void*>(luts));
+    u32x4 xv[4];
+#pragma unroll
+    for (uint32_t i = 0; i < 4; ++i) xv[i] = x_src[min(threadIdx.x + i * FILS, n16 > 0u ? n16 - 1u : 0u)];
     Tache tc;
     if (topk) {
         // the top-k in the entry area (free until the tiles start)
-        const ParamsMoe& pm = taches.moe;
         float* lg = reinterpret_cast<float*>(lds + LDS_ENT);
         uint32_t* choisis = reinterpret_cast<uint32_t*>(lds + LDS_ENT + 4u * EXPERTS_MAX);
-        const float* logits = reinterpret_cast<const float*>(pm.logits);
-        for (uint32_t e = threadIdx.x; e < pm.E; e += blockDim.x) lg[e] = logits[e];
+        if (threadIdx.x < pm.E) lg[threadIdx.x] = lg_v;
         if (threadIdx.x < TOPK_MAX) choisis[threadIdx.x] = 0xFFFFFFFFu;
-        __syncthreads();
+        barriere_lds();
         choisir_topk(lg, pm.E, pm.k, choisis);
-        __syncthreads();
+        barriere_lds();
         if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x < 64u) {
             float w[TOPK_MAX];
             poids_topk(lg, choisis, pm.k, w);
@@ -219,53 +236,76 @@ fusion_codes(trc::Taches taches, const uint32_t* __restrict__ luts, uint32_t* __
                 float wr = w[0];
 #pragma unroll
                 for (uint32_t r = 1; r < TOPK_MAX; ++r) wr = threadIdx.x == r ? w[r] : wr;
-                reinterpret_cast<uint32_t*>(pm.indices)[threadIdx.x] = choisis[threadIdx.x];
-                reinterpret_cast<float*>(pm.poids)[threadIdx.x] = wr;
+                typedef __attribute__((address_space(1))) uint32_t* GU32;
+                typedef __attribute__((address_space(1))) float* GF32;
+                ((GU32)(pm.indices))[threadIdx.x] = choisis[threadIdx.x];
+                ((GF32)(pm.poids))[threadIdx.x] = wr;
             }
         }
         const uint32_t i = blockIdx.y >> 1;
-        const uint32_t e = choisis[i];
+        const uint32_t e = uniforme32(choisis[i]);
         tc = uniforme(tache_moe_e(pm, i, j, e));
-        // the selected experts' records for the later passes: gate (with down) and up
+        // the selected experts' records for the later passes (gate with down, and up), read with
+        // scalar loads from the directory, which nothing writes during the step
         if (blockIdx.x == 0 && threadIdx.x < 64u) {
-            const uint32_t jj = threadIdx.x == 0 ? j : 2u;
-            if (threadIdx.x == 0 || (threadIdx.x == 1 && j == 0)) {
-                MatricePartie r;
-                std::memset(&r, 0, sizeof(r));
-                if (e < pm.E)
-                    r = *reinterpret_cast<const MatricePartie*>(pm.repertoire + uint64_t(e * 3u + jj) * sizeof(MatricePartie));
-                ecrire_matrice(reinterpret_cast<void*>(pm.resolus + uint64_t(i * 3u + jj) * sizeof(MatricePartie)), r);
+            const MatricePartie r = tc.matrice != 0 ? lire_matrice_constante(tc.matrice) : MatricePartie{};
+            if (threadIdx.x == 0) ecrire_matrice(reinterpret_cast<void*>(pm.resolus + uint64_t(i * 3u + j) * sizeof(MatricePartie)), r);
+            if (j == 0) {
+                const MatricePartie r2 = e < pm.E ? lire_matrice_constante(pm.repertoire + uint64_t(e * 3u + 2u) * sizeof(MatricePartie))
+                                                  : MatricePartie{};
+                if (threadIdx.x == 0) ecrire_matrice(reinterpret_cast<void*>(pm.resolus + uint64_t(i * 3u + 2u) * sizeof(MatricePartie)), r2);
             }
         }
     } else {
-        tc = uniforme(taches[blockIdx.y]);
+        tc = tx;
     }
-    const bool x_lds = tc.colonnes <= X_LDS_MAX;
-    const uint32_t n16 = x_lds ? tc.colonnes / 4u : 0u;
-    u32x4 xv[4];
+    const PrepCodes p = preparer_codes(tc, obtenir_matrice_scalaire(tc));
+    const bool bon = p.bon && x_lds;  // uniform over the block
+    if (!bon) {
+        if (threadIdx.x == 0 && blockIdx.x == 0) atomicAdd(&controle[CTL_FORMAT], 1u);
+        return;
+    }
+    // the first tile pair's streams (one branch-free batch of loads, left in flight), then x and
+    // the decode LUTs into LDS: their loads were issued before, so no wait here drains the
+    // read-ahead
+    const Avance avance0 = premiere_avance<true>(p, tc.lignes, g);
+    asm volatile("" ::"v"(lutd_chaud));  // complete before the decode LUTs, issued after it
 #pragma unroll
     for (uint32_t i = 0; i < 4; ++i) {
-        const uint32_t k = threadIdx.x + i * blockDim.x;
-        if (k < n16) xv[i] = glob<u32x4>(reinterpret_cast<const void*>(tc.x))[k];
+        const uint32_t k = threadIdx.x + i * FILS;
+        if (k < n16) *reinterpret_cast<u32x4*>(lds + LDS_X + 16u * k) = xv[i];
     }
-    const PrepCodes p = preparer_codes(tc, obtenir_matrice(tc));
-    const bool bon = p.bon && x_lds;
-    const uint32_t B = tc.colonnes / 32u;
-    const Avance avance0 = bon ? premiere_avance<true>(p, tc.lignes, B) : Avance{};
-    charge_lut.poser(lut_src, reinterpret_cast<uint2*>(lds + LDS_LUT), 3u * M / 4u);
-    if (!bon && threadIdx.x == 0 && blockIdx.x == 0) atomicAdd(&controle[CTL_FORMAT], 1u);
-    if (bon) {
-#pragma unroll
-        for (uint32_t i = 0; i < 4; ++i) {
-            const uint32_t k = threadIdx.x + i * blockDim.x;
-            if (k < n16) *reinterpret_cast<u32x4*>(lds + LDS_X + 16u * k) = xv[i];
-        }
-        if (threadIdx.x < 8u)
-            *reinterpret_cast<u32x4*>(lds + LDS_X + COLONNE_NULLE * 128u + 16u * threadIdx.x) = u32x4{0u, 0u, 0u, 0u};
-    }
-    __syncthreads();
-    if (bon) corps_codes(tc, p, lds, luts + uint64_t(j) * 4u * M, controle, avance0);
+    if (threadIdx.x < 8u)
+        *reinterpret_cast<u32x4*>(lds + LDS_X + COLONNE_NULLE * 128u + 16u * threadIdx.x) = u32x4{0u, 0u, 0u, 0u};
+    charge_lut.poser(reinterpret_cast<uint2*>(lds + LDS_LUT));
+    // LDS-only barrier: the read-ahead stays in flight into the tile loop
+    barriere_lds();
+    corps_codes(tc, p, lds, luts + uint64_t(j) * 4u * M, controle, avance0, g);
 }
+
+extern "C" __global__ void __launch_bounds__(1024)
+fusion_codes(trc::Taches taches, const uint32_t* __restrict__ luts, uint32_t* __restrict__ controle) {
+    codes_bloc<1024>(taches, luts, controle);
+}
+extern "C" __global__ void __launch_bounds__(512)
+fusion_codes_512(trc::Taches taches, const uint32_t* __restrict__ luts, uint32_t* __restrict__ controle) {
+    codes_bloc<512>(taches, luts, controle);
+}
+extern "C" __global__ void __launch_bounds__(256)
+fusion_codes_256(trc::Taches taches, const uint32_t* __restrict__ luts, uint32_t* __restrict__ controle) {
+    codes_bloc<256>(taches, luts, controle);
+}
+
+// The CODES kernel compiled for the launch's block size (1024, 512 or 256 threads).
+#define TRC_LANCER_CODES(nom, forme, f, ...)                                                     \
+    do {                                                                                         \
+        if ((forme).bloc.x == 1024)                                                              \
+            TRC_LANCER_N(nom, fusion_codes, (forme).grille, (forme).bloc, f, __VA_ARGS__);       \
+        else if ((forme).bloc.x == 512)                                                          \
+            TRC_LANCER_N(nom, fusion_codes_512, (forme).grille, (forme).bloc, f, __VA_ARGS__);   \
+        else                                                                                     \
+            TRC_LANCER_N(nom, fusion_codes_256, (forme).grille, (forme).bloc, f, __VA_ARGS__);   \
+    } while (0)
 
 // CODES pass, x read from device memory (rows of any width).
 extern "C" __global__ void __launch_bounds__(trc::FILS_GEMV_MAX)
@@ -585,7 +625,7 @@ extern "C" int trc_gemv_fusionnee(trc_vue partie, uint32_t j, trc_vue luts, uint
         t.partiels = travail.adresse;
         const Taches tv = par_valeur(&t, 1);
         const FormeGemv fo = forme_gemv(lignes, colonnes, n_codes, 1);
-        TRC_LANCER_N("fusion_codes", fusion_codes, fo.grille, fo.bloc, f, tv, l, ctl);
+        TRC_LANCER_CODES("fusion_codes", fo, f, tv, l, ctl);
         TRC_LANCER(fusion_finir, dim3((lignes + 255) / 256, 1), dim3(256), f, tv, reinterpret_cast<float*>(y.adresse), 0u);
         return TRC_OK;
     }
@@ -653,11 +693,11 @@ extern "C" int trc_expert_fusionne(trc_vue partie, trc_vue luts, const trc_dims_
         }
         const Taches deux = par_valeur(t, 2), bas = par_valeur(t + 2, 1);
         const FormeGemv fgu = forme_gemv(R, C, n_codes, 2);
-        TRC_LANCER_N("fusion_codes", fusion_codes, fgu.grille, fgu.bloc, f, deux, l, ctl);
+        TRC_LANCER_CODES("fusion_codes", fgu, f, deux, l, ctl);
         TRC_LANCER(fusion_finir_swiglu, dim3((R + 255) / 256, 1), dim3(256), f, deux, reinterpret_cast<float*>(act), R);
         const uint32_t R2 = dims->lignes[2];
         const FormeGemv fb = forme_gemv(R2, dims->colonnes[2], n_codes, 1);
-        TRC_LANCER_N("fusion_codes", fusion_codes, fb.grille, fb.bloc, f, bas, l, ctl);
+        TRC_LANCER_CODES("fusion_codes", fb, f, bas, l, ctl);
         TRC_LANCER(fusion_finir, dim3((R2 + 255) / 256, 1), dim3(256), f, bas,
                    reinterpret_cast<float*>(sortie.adresse), 0u);
         return TRC_OK;
@@ -815,9 +855,9 @@ int couche_moe(trc_vue repertoire, uint32_t experts, trc_vue luts, const trc_dim
         // five launches: router, gate/up (top-k, DELTA and CODES), the k SwiGLU rows, down (DELTA and
         // CODES), combine
         const FormeGemv fgu = forme_gemv(R, C, n_codes, 2 * k), fb = forme_gemv(D, R, n_codes, k);
-        TRC_LANCER_N("fusion_codes/gate_up", fusion_codes, fgu.grille, fgu.bloc, f, t_gu_topk, l, ctl);
+        TRC_LANCER_CODES("fusion_codes/gate_up", fgu, f, t_gu_topk, l, ctl);
         TRC_LANCER(fusion_finir_swiglu, dim3((R + 255) / 256, k), dim3(256), f, t_gu, reinterpret_cast<float*>(act), R);
-        TRC_LANCER_N("fusion_codes/down", fusion_codes, fb.grille, fb.bloc, f, t_bas, l, ctl);
+        TRC_LANCER_CODES("fusion_codes/down", fb, f, t_bas, l, ctl);
         TRC_LANCER(fusion_finir_combiner, dim3((D + 255) / 256), dim3(256), f, t_bas);
         return TRC_OK;
     }

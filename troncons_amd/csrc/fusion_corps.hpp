@@ -101,7 +101,7 @@ __device__ __forceinline__ u32x4 quad_flux(const DescFlux& f) {
     return u32x4{uint32_t(a), uint32_t(a >> 32), f.longueur, f.produits};
 }
 __device__ __forceinline__ void ecrire_matrice(void* dst, const MatricePartie& m) {
-    u32x4* d = reinterpret_cast<u32x4*>(dst);
+    __attribute__((address_space(1))) u32x4* d = (__attribute__((address_space(1))) u32x4*)(dst);
     d[0] = quad_flux(m.delta);
     d[1] = quad_flux(m.codes);
     d[2] = quad_flux(m.med);
@@ -115,6 +115,24 @@ __device__ __forceinline__ void ecrire_matrice(void* dst, const MatricePartie& m
 // The job's matrix: from the mounted layer (one 128-byte read) or parsed from the part.
 __device__ __forceinline__ MatricePartie obtenir_matrice(const Tache& tc) {
     if (tc.matrice != 0) return *reinterpret_cast<const MatricePartie*>(tc.matrice);
+    return analyser_matrice(reinterpret_cast<const uint8_t*>(tc.partie), tc.j, tc.lignes, tc.colonnes);
+}
+
+// The same, a resolved record read with scalar loads (constant address space): it lands in SGPRs
+// and is waited for on the scalar counter, so vector loads in flight are not drained for it. Only
+// for records that nothing writes while the kernel runs (the layer's directory, or the selected
+// experts' records written by an earlier launch).
+__device__ __forceinline__ MatricePartie lire_matrice_constante(uint64_t adresse) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    typedef const __attribute__((address_space(4))) MatricePartie* MatriceConstante;
+    const MatricePartie m = *reinterpret_cast<MatriceConstante>(adresse);
+    return m;
+#else
+    return *reinterpret_cast<const MatricePartie*>(adresse);  // host pass of a device function: never run
+#endif
+}
+__device__ __forceinline__ MatricePartie obtenir_matrice_scalaire(const Tache& tc) {
+    if (tc.matrice != 0) return lire_matrice_constante(tc.matrice);
     return analyser_matrice(reinterpret_cast<const uint8_t*>(tc.partie), tc.j, tc.lignes, tc.colonnes);
 }
 
@@ -222,6 +240,14 @@ constexpr uint32_t MED_LDS_MAX = 8192;          // rows whose medians the DELTA 
 // job's scalars live in scalar registers. (The builtin returns int; elargir_u64 widens each half
 // through uint32_t, so that an address whose low word has bit 31 set is not sign-extended.)
 __device__ __forceinline__ uint32_t uniforme32(uint32_t v) { return uint32_t(__builtin_amdgcn_readfirstlane(v)); }
+// Workgroup barrier that orders LDS accesses only. __syncthreads() fences every address space, so
+// each wave first waits for all of its outstanding device-memory loads; this one leaves loads that
+// are meant to stay in flight across the barrier (read-ahead of the first tiles) in flight.
+__device__ __forceinline__ void barriere_lds() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
 __device__ __forceinline__ uint64_t uniforme64(uint64_t v) {
     return elargir_u64(__builtin_amdgcn_readfirstlane(uint32_t(v)), __builtin_amdgcn_readfirstlane(uint32_t(v >> 32)));
 }
@@ -271,6 +297,20 @@ __device__ __forceinline__ TeteTuile lire_tete(const EnteteRans& h, uint32_t t, 
         r.debut = h.debut[t];
         r.attendu = (t + 1u < h.T) ? h.debut[t + 1u] : h.W;
     }
+    return r;
+}
+
+// The same with its loads unconditional (tile index clamped to the last tile, h.T >= 1), so that no
+// branch surrounds them: a tile past the stream gets the last tile's head, which its half never
+// decodes nor checks.
+__device__ __forceinline__ TeteTuile lire_tete_borne(const EnteteRans& h, uint32_t t, uint32_t v) {
+    const uint32_t tt = min(t, h.T - 1u);
+    const gptr<uint32_t> debut = glob<uint32_t>(h.debut);
+    const uint32_t apres = debut[min(tt + 1u, h.T - 1u)];
+    TeteTuile r;
+    r.x = glob<uint32_t>(h.etats)[tt * VOIES + v];
+    r.debut = debut[tt];
+    r.attendu = tt + 1u < h.T ? apres : h.W;
     return r;
 }
 

@@ -83,13 +83,14 @@ __device__ __forceinline__ void topk_vague(const float* logits, uint32_t E, uint
 // Each expert gets a group of `par` consecutive lanes (par a power of two, at most 64, par * E at
 // most the block when it can be): lane c of the group counts over its share of the experts, the
 // group adds its counts with lane exchanges, and its first lane writes the choice. No division,
-// no LDS atomics. lg[0..E) in LDS and choisis[0..TOPK_MAX) set to 0xFFFFFFFF before the call,
-// barrier after it.
+// no LDS atomics. lg[0..E) in LDS (16-byte aligned) and choisis[0..TOPK_MAX) set to 0xFFFFFFFF
+// before the call, barrier after it.
 __device__ __forceinline__ void choisir_topk(const float* lg, uint32_t E, uint32_t k, uint32_t* choisis) {
     uint32_t lpar = 0;
     while (lpar < 6u && (E << (lpar + 1u)) <= blockDim.x) ++lpar;
     const uint32_t par = 1u << lpar;
     const uint32_t part = (E + par - 1u) >> lpar;  // experts counted per lane
+    const bool quatre = (part & 3u) == 0u && (E & 3u) == 0u;  // lanes' shares in whole 16-byte groups
     // every lane of a group takes the same trips: the exchanges below see only active lanes
     for (uint32_t q0 = threadIdx.x & ~(par - 1u); q0 < (E << lpar); q0 += blockDim.x) {
         const uint32_t q = q0 + (threadIdx.x & (par - 1u));
@@ -97,9 +98,21 @@ __device__ __forceinline__ void choisir_topk(const float* lg, uint32_t E, uint32
         const float vi = lg[i];
         const uint32_t j0 = c * part, j1 = min(E, j0 + part);
         uint32_t n = 0;
-        for (uint32_t j = j0; j < j1; ++j) {
-            const float vj = lg[j];
-            n += (vj > vi || (vj == vi && j < i)) ? 1u : 0u;
+        if (quatre) {
+            // 16-byte reads, four in flight: the counts do not wait on one LDS read after another
+#pragma unroll 4
+            for (uint32_t j = j0; j < j1; j += 4u) {
+                const float4 w = *reinterpret_cast<const float4*>(lg + j);
+                n += (w.x > vi || (w.x == vi && j < i)) ? 1u : 0u;
+                n += (w.y > vi || (w.y == vi && j + 1u < i)) ? 1u : 0u;
+                n += (w.z > vi || (w.z == vi && j + 2u < i)) ? 1u : 0u;
+                n += (w.w > vi || (w.w == vi && j + 3u < i)) ? 1u : 0u;
+            }
+        } else {
+            for (uint32_t j = j0; j < j1; ++j) {
+                const float vj = lg[j];
+                n += (vj > vi || (vj == vi && j < i)) ? 1u : 0u;
+            }
         }
         for (uint32_t d = 1; d < par; d <<= 1) n += uint32_t(__shfl_xor(int(n), int(d)));
         if (c == 0u && vi == vi && n < k) choisis[n] = i;
