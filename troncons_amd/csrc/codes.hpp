@@ -143,7 +143,8 @@ __device__ __forceinline__ PrepCodes preparer_codes(const Tache& tc, const Matri
     p.hc = entete_de(m.codes, m.cP, m.cN, m.cT, m.cW);
     p.hd = entete_de(m.delta, m.dP, m.dN, m.dT, m.dW);
     p.med = m.med.p;
-    p.B = Diviseur::de(B);
+    // the record carries the divider of B (computed once, where the record was made)
+    p.B = m.div_m != 0u ? Diviseur{B, m.div_m, m.div_s & 255u, m.div_s >> 8} : Diviseur::de(B);
     return p;
 }
 
@@ -156,8 +157,10 @@ __device__ __forceinline__ Avance premiere_avance(const PrepCodes& p, uint32_t R
 }
 
 // CODES_CTX tiles -> partial sums of W x, x in LDS, the tiles' entries decoded here from DELTA.
-// `avance0`: premiere_avance(p), read by the caller before its barrier. lutd: the job's DELTA LUT
-// (reference format) in device memory.
+// `avance0`: premiere_avance(p), read by the caller. lutd: the job's DELTA LUT (reference format) in
+// device memory. The caller stages the decode LUTs and x in LDS and does not wait: each wavefront
+// decodes its first tiles' DELTA (its own ring and entry areas, the DELTA LUT from device memory)
+// and only then passes the block's barrier, once, before its first CODES step reads them.
 __device__ __forceinline__ void corps_codes(const Tache& tc, const PrepCodes& p, uint8_t* lds, const uint32_t* lutd_,
                                             uint32_t* __restrict__ controle, const Avance& avance0, const Grille& g) {
     const EnteteRans& h = p.hc;
@@ -188,6 +191,7 @@ __device__ __forceinline__ void corps_codes(const Tache& tc, const PrepCodes& p,
     const uint32_t mots_d = uint32_t(reinterpret_cast<const uint8_t*>(hd.mots) - p.fd.p);
     uint32_t hors_l = 0, pointeur = 0;
     Avance av = avance0;
+    bool barriere = true;  // wave-uniform: the block's LUT and x barrier is still to pass
     for (uint32_t t0 = 2u * vague; t0 < hT; t0 += 2u * n_vagues) {
         const uint32_t t = t0 + (haut ? 1u : 0u);
         const bool tuile = t < hT;
@@ -233,6 +237,10 @@ __device__ __forceinline__ void corps_codes(const Tache& tc, const PrepCodes& p,
         }
         // 2. the tile's 128 block entries
         if (tuile) ecrire_lds<u32x4>(a_ent + 16u * v, entrees_de_delta(mot, cur, 128u * t + 4u * v, nblocs, p.B));
+        if (barriere) {
+            barriere_lds();
+            barriere = false;
+        }
         // 3. the CODES words over the DELTA ones, and the next pair's streams read ahead
         ecrire_lds<u32x4>(a_anneau + 16u * v, cur.mots0);
         ecrire_lds<u32x4>(a_anneau + 512u + 16u * v, cur.mots1);
@@ -319,6 +327,7 @@ __device__ __forceinline__ void corps_codes(const Tache& tc, const PrepCodes& p,
             pointeur += (v == 0 && debut + (a.o2 - o0) / 2u != attendu) ? 1u : 0u;
         }
     }
+    if (barriere) barriere_lds();  // a wavefront without tiles still takes its part in it
     verser_controle(controle, hors_l, pointeur);
 }
 

@@ -63,7 +63,7 @@ fusion_echelles(trc::Taches taches, const uint32_t* __restrict__ luts, uint32_t*
         for (uint32_t e = threadIdx.x; e < pm.E; e += blockDim.x) lg[e] = logits[e];
         if (threadIdx.x < TOPK_MAX) choisis[threadIdx.x] = 0xFFFFFFFFu;
         __syncthreads();
-        choisir_topk(lg, pm.E, pm.k, choisis);
+        choisir_topk(lg, pm.E, pm.k, choisis, blockDim.x);
         __syncthreads();
         if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x < 64u) {
             float w[TOPK_MAX];
@@ -210,6 +210,11 @@ __device__ __forceinline__ void codes_bloc(const trc::Taches& taches, const uint
     const gptr<float> lg_src = glob<float>(topk ? reinterpret_cast<const void*>(pm.logits) : reinterpret_cast<const void*>(luts));
     const float lg_v = lg_src[min(threadIdx.x, (topk ? pm.E : 1u) - 1u)];
     const uint32_t lutd_chaud = glob<uint32_t>(luts + uint64_t(j) * 4u * M)[4u * min(threadIdx.x, M / 4u - 1u)];
+    // gate/up: the directory's records of matrix j, one 128-byte line each, so that the one the
+    // top-k picks is read from the caches
+    const uint32_t rep_chaud =
+        glob<uint32_t>(topk ? reinterpret_cast<const void*>(pm.repertoire) : reinterpret_cast<const void*>(luts))
+            [topk ? 32u * (3u * min(threadIdx.x, pm.E - 1u) + j) : 0u];
     ChargeLutBloc<FILS> charge_lut;
     charge_lut.demarrer(lut_src);
     const Tache tx = topk ? uniforme(tache_moe_e(pm, blockIdx.y >> 1, j, 0u)) : uniforme(taches[blockIdx.y]);
@@ -227,7 +232,7 @@ __device__ __forceinline__ void codes_bloc(const trc::Taches& taches, const uint
         if (threadIdx.x < pm.E) lg[threadIdx.x] = lg_v;
         if (threadIdx.x < TOPK_MAX) choisis[threadIdx.x] = 0xFFFFFFFFu;
         barriere_lds();
-        choisir_topk(lg, pm.E, pm.k, choisis);
+        choisir_topk(lg, pm.E, pm.k, choisis, FILS);
         barriere_lds();
         if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x < 64u) {
             float w[TOPK_MAX];
@@ -244,6 +249,8 @@ __device__ __forceinline__ void codes_bloc(const trc::Taches& taches, const uint
         }
         const uint32_t i = blockIdx.y >> 1;
         const uint32_t e = uniforme32(choisis[i]);
+        // every wave has read the top-k from the entry area before any overwrites it
+        barriere_lds();
         tc = uniforme(tache_moe_e(pm, i, j, e));
         // the selected experts' records for the later passes (gate with down, and up), read with
         // scalar loads from the directory, which nothing writes during the step
@@ -269,7 +276,10 @@ __device__ __forceinline__ void codes_bloc(const trc::Taches& taches, const uint
     // the decode LUTs into LDS: their loads were issued before, so no wait here drains the
     // read-ahead
     const Avance avance0 = premiere_avance<true>(p, tc.lignes, g);
-    asm volatile("" ::"v"(lutd_chaud));  // complete before the decode LUTs, issued after it
+    // issued here, ahead of the LDS staging below (which waits on the earlier loads only)
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("" ::"v"(lutd_chaud), "v"(rep_chaud));  // complete before the decode LUTs, issued after them
 #pragma unroll
     for (uint32_t i = 0; i < 4; ++i) {
         const uint32_t k = threadIdx.x + i * FILS;
@@ -278,8 +288,8 @@ __device__ __forceinline__ void codes_bloc(const trc::Taches& taches, const uint
     if (threadIdx.x < 8u)
         *reinterpret_cast<u32x4*>(lds + LDS_X + COLONNE_NULLE * 128u + 16u * threadIdx.x) = u32x4{0u, 0u, 0u, 0u};
     charge_lut.poser(reinterpret_cast<uint2*>(lds + LDS_LUT));
-    // LDS-only barrier: the read-ahead stays in flight into the tile loop
-    barriere_lds();
+    // the block's barrier (LDS only: the read-ahead stays in flight) is passed in corps_codes,
+    // after each wavefront's first DELTA decode
     corps_codes(tc, p, lds, luts + uint64_t(j) * 4u * M, controle, avance0, g);
 }
 

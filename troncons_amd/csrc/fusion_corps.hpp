@@ -29,7 +29,8 @@ struct MatricePartie {
     uint32_t dP, dN, dT, dW;  // DELTA stream header
     uint32_t cP, cN, cT, cW;  // CODES_CTX stream header
     uint32_t bon;             // 1: every check of the reference reader passed
-    uint32_t reserve[7];
+    uint32_t div_m, div_s;    // Diviseur of the blocks per row (multiplier; shifts s1 | s2 << 8)
+    uint32_t reserve[5];
 };
 static_assert(sizeof(MatricePartie) == 128, "MatricePartie");
 
@@ -39,6 +40,7 @@ __device__ inline MatricePartie analyser_matrice(const uint8_t* partie, uint32_t
     MatricePartie m;
     m.bon = 0;
     m.dP = m.dN = m.dT = m.dW = m.cP = m.cN = m.cT = m.cW = 0;
+    m.div_m = m.div_s = 0;
     const uint32_t B = C / 32u;
     DescFlux f[4];
     const uint8_t sortes[4] = {SORTE_DELTA, SORTE_CODES_CTX, SORTE_MEDIANES, SORTE_BIAIS};
@@ -59,6 +61,9 @@ __device__ inline MatricePartie analyser_matrice(const uint8_t* partie, uint32_t
     m.cN = hc.N;
     m.cT = hc.T;
     m.cW = hc.W;
+    const Diviseur dv = Diviseur::de(B);  // once per matrix, where the record is made
+    m.div_m = dv.m;
+    m.div_s = dv.s1 | (dv.s2 << 8);
     m.bon = 1;
     return m;
 }
@@ -108,7 +113,7 @@ __device__ __forceinline__ void ecrire_matrice(void* dst, const MatricePartie& m
     d[3] = quad_flux(m.biais);
     d[4] = u32x4{m.dP, m.dN, m.dT, m.dW};
     d[5] = u32x4{m.cP, m.cN, m.cT, m.cW};
-    d[6] = u32x4{m.bon, 0u, 0u, 0u};
+    d[6] = u32x4{m.bon, m.div_m, m.div_s, 0u};
     d[7] = u32x4{0u, 0u, 0u, 0u};
 }
 

@@ -84,15 +84,17 @@ __device__ __forceinline__ void topk_vague(const float* logits, uint32_t E, uint
 // most the block when it can be): lane c of the group counts over its share of the experts, the
 // group adds its counts with lane exchanges, and its first lane writes the choice. No division,
 // no LDS atomics. lg[0..E) in LDS (16-byte aligned) and choisis[0..TOPK_MAX) set to 0xFFFFFFFF
-// before the call, barrier after it.
-__device__ __forceinline__ void choisir_topk(const float* lg, uint32_t E, uint32_t k, uint32_t* choisis) {
+// before the call, barrier after it. fils: the block's thread count (a constant where the caller
+// has one, so that it is not read from the dispatch packet).
+__device__ __forceinline__ void choisir_topk(const float* lg, uint32_t E, uint32_t k, uint32_t* choisis,
+                                             uint32_t fils) {
     uint32_t lpar = 0;
-    while (lpar < 6u && (E << (lpar + 1u)) <= blockDim.x) ++lpar;
+    while (lpar < 6u && (E << (lpar + 1u)) <= fils) ++lpar;
     const uint32_t par = 1u << lpar;
     const uint32_t part = (E + par - 1u) >> lpar;  // experts counted per lane
     const bool quatre = (part & 3u) == 0u && (E & 3u) == 0u;  // lanes' shares in whole 16-byte groups
     // every lane of a group takes the same trips: the exchanges below see only active lanes
-    for (uint32_t q0 = threadIdx.x & ~(par - 1u); q0 < (E << lpar); q0 += blockDim.x) {
+    for (uint32_t q0 = threadIdx.x & ~(par - 1u); q0 < (E << lpar); q0 += fils) {
         const uint32_t q = q0 + (threadIdx.x & (par - 1u));
         const uint32_t i = q >> lpar, c = q & (par - 1u);
         const float vi = lg[i];
