@@ -54,14 +54,14 @@ constexpr uint32_t ECHELLE_UN = 127u;     // E8M0 1.0
 constexpr uint32_t PF_TOURS = 2;          // decode rounds per band: a band's tiles are at most 64
 constexpr uint32_t PF_RB_MAX = 64;         // rows per band
 
-// LDS of prefill_mfma after the decode (the LUT, x and ring regions are free then; the block
-// entries at LDS_ENT stay free of them): codes [RB][Bp][16 B] at 0, scales [RB][Bp] after them,
-// then the partial sums of the MFMA phase (16 waves x 2 row tiles x 64 lanes x 16 B).
+// LDS of prefill_mfma after the decode (every region of the decode is free then): codes [RB][B][16 B]
+// at 0 (rows of exactly B blocks), scales [RB][B] after them, then the partial sums of the MFMA phase
+// (RB/16 row tiles x 16 waves x 64 lanes x 16 B).
 constexpr uint32_t PF_A = 0;
-constexpr uint32_t PF_PART_OCTETS = 16u * 2u * 64u * 16u;
-__host__ __device__ inline uint32_t pf_sa(uint32_t rb, uint32_t bp) { return rb * bp * 16u; }
-__host__ __device__ inline uint32_t pf_part(uint32_t rb, uint32_t bp) { return (pf_sa(rb, bp) + rb * bp + 15u) & ~15u; }
-__host__ __device__ inline bool pf_lds_tient(uint32_t rb, uint32_t bp) { return pf_part(rb, bp) + PF_PART_OCTETS <= LDS_ENT; }
+__host__ __device__ inline uint32_t pf_sa(uint32_t rb, uint32_t b) { return rb * b * 16u; }
+__host__ __device__ inline uint32_t pf_part(uint32_t rb, uint32_t b) { return (pf_sa(rb, b) + rb * b + 15u) & ~15u; }
+__host__ __device__ inline uint32_t pf_part_octets(uint32_t rb) { return (rb / 16u) * 16u * 64u * 16u; }
+__host__ __device__ inline bool pf_lds_tient(uint32_t rb, uint32_t b) { return pf_part(rb, b) + pf_part_octets(rb) <= LDS_GEMV; }
 
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 
@@ -287,16 +287,16 @@ struct Operande_b {
     bool valide;
 };
 
-// acc_rt += A_rt (k-step ks) x B over pieces p0 .. p0 + NP - 1: their loads are issued before the MFMAs.
-// This lane's B bytes 0-15 are half `demi` of block 4 ks + `bloc`, bytes 16-31 the same half of block
-// 4 ks + 2 + `bloc`; its scale is block 4 ks + lg's.
-// Pieces p0 .. p0 + NP - 1 with p < P take part (P wave-uniform); every load of the batch goes out
-// before the first MFMA (addresses of invalid columns or unused pieces are clamped to piece 0 of the
-// column's first valid source, so no load sits under a branch).
+// acc[rt] += A_rt (k-step ks) x B over pieces p0 .. p0 + NP - 1 for the nrt row tiles of the band: the
+// pieces' loads are issued before the MFMAs, and each feeds every row tile. This lane's B bytes 0-15
+// are half `demi` of block 4 ks + `bloc`, bytes 16-31 the same half of block 4 ks + 2 + `bloc`; its
+// scale is block 4 ks + lg's. Pieces p0 .. p0 + NP - 1 with p < P take part (P wave-uniform); the
+// addresses of invalid columns or unused pieces are clamped to piece 0 of the column's first valid
+// source, so no load sits under a branch.
 template <uint32_t NP>
-__device__ __forceinline__ void produit_pieces(f32x4& acc0, f32x4& acc1, const u32x4& a0, const u32x4& a1,
-                                               uint32_t sa0, uint32_t sa1, const Operande_b& ob, uint32_t p0,
-                                               uint32_t ks, uint32_t nrt, uint32_t P = PF_PIECES) {
+__device__ __forceinline__ void produit_pieces(f32x4 (&acc)[4], const u32x4 (&a)[4], const uint32_t (&sa)[4],
+                                               const Operande_b& ob, uint32_t p0, uint32_t ks, uint32_t nrt,
+                                               uint32_t P) {
     u32x4 b0[NP], b1[NP];
     uint32_t sb[NP];
 #pragma unroll
@@ -311,20 +311,19 @@ __device__ __forceinline__ void produit_pieces(f32x4& acc0, f32x4& acc1, const u
             sb[p] = ECHELLE_UN;
         }
     }
-    const i32x8 ra0 = {int(a0.x), int(a0.y), int(a0.z), int(a0.w), 0, 0, 0, 0};
-    const i32x8 ra1 = {int(a1.x), int(a1.y), int(a1.z), int(a1.w), 0, 0, 0, 0};
-    i32x8 rb[NP];
+    i32x8 ra[4];
 #pragma unroll
-    for (uint32_t p = 0; p < NP; ++p)
-        rb[p] = i32x8{int(b0[p].x), int(b0[p].y), int(b0[p].z), int(b0[p].w),
-                      int(b1[p].x), int(b1[p].y), int(b1[p].z), int(b1[p].w)};
+    for (uint32_t rt = 0; rt < 4; ++rt) ra[rt] = i32x8{int(a[rt].x), int(a[rt].y), int(a[rt].z), int(a[rt].w), 0, 0, 0, 0};
 #pragma unroll
     for (uint32_t p = 0; p < NP; ++p) {
         if (p0 + p >= P) break;  // wave-uniform
-        acc0 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ra0, rb[p], acc0, 4, 0, 0, int(sa0), 0, int(sb[p]));
-        if (nrt == 2u)
-            acc1 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ra1, rb[p], acc1, 4, 0, 0, int(sa1), 0,
-                                                                    int(sb[p]));
+        const i32x8 rb = {int(b0[p].x), int(b0[p].y), int(b0[p].z), int(b0[p].w),
+                          int(b1[p].x), int(b1[p].y), int(b1[p].z), int(b1[p].w)};
+#pragma unroll
+        for (uint32_t rt = 0; rt < 4; ++rt)
+            if (rt < nrt)  // wave-uniform
+                acc[rt] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ra[rt], rb, acc[rt], 4, 0, 0, int(sa[rt]), 0,
+                                                                           int(sb[p]));
     }
     // The result of this MFMA (A fp4, B fp8) reaches its registers 11 to 12 wait states after issue
     // (measured); the compiler's hazard padding before a VALU read of it can be shorter. 16 wait states
@@ -413,8 +412,8 @@ __device__ __forceinline__ void decoder_tour(const EnteteRans& h, const DescFlux
     }
 }
 
-// A round's codes and scales into the band's LDS arrays: codes [row][Bp][16 B], scales [row][Bp].
-__device__ __forceinline__ void poser_tour(const TourBande& tb, uint32_t t, uint32_t N, uint32_t B, uint32_t Bp,
+// A round's codes and scales into the band's LDS arrays: codes [row][pas][16 B], scales [row][pas].
+__device__ __forceinline__ void poser_tour(const TourBande& tb, uint32_t t, uint32_t N, uint32_t B, uint32_t pas,
                                            uint32_t r0, uint32_t ba, uint32_t bb, uint32_t base, uint32_t a_sa) {
     const uint32_t v = __lane_id() & 31u, q = v >> 2;
     uint32_t beta = 8u * t * N + q;
@@ -422,7 +421,7 @@ __device__ __forceinline__ void poser_tour(const TourBande& tb, uint32_t t, uint
 #pragma unroll
     for (uint32_t mm = 0; mm < PF_NMAX; ++mm) {
         if (mm < tb.nb && beta >= ba && beta < bb) {
-            const uint32_t o = (ligne - r0) * Bp + blk;
+            const uint32_t o = (ligne - r0) * pas + blk;
             ecrire_lds<uint32_t>(base + PF_A + 16u * o + 4u * (v & 3u), tb.codes[mm]);
             if ((v & 3u) == 0u) ecrire_lds<uint8_t>(a_sa + o, uint8_t(tb.ech[mm >> 2] >> (8u * (mm & 3u))));
         }
@@ -437,9 +436,8 @@ __device__ __forceinline__ void poser_tour(const TourBande& tb, uint32_t t, uint
 
 // One band of rows [r0, r0 + nl) of matrix j of expert e against the expert's pairs: its tiles
 // decoded in up to two rounds of 32 (one tile per half-wavefront a round), stored in LDS as MXFP4,
-// then the block-scaled MFMA. With 64-row bands (4 row tiles) waves 0-7 take row tiles 0-1 and
-// waves 8-15 row tiles 2-3, each group splitting K over its 8 waves; with 16 or 32 rows all 16
-// waves split K.
+// then the block-scaled MFMA: each of the 16 waves takes every row tile of the band (up to 4) over
+// its share of K, so that each B load feeds every row tile and B is read once per band.
 template <uint32_t J>
 __device__ __forceinline__ void prefill_bande(const ParamsPrefill& pp, const uint32_t* __restrict__ luts,
                                               uint32_t* __restrict__ controle, uint8_t* lds) {
@@ -482,42 +480,41 @@ __device__ __forceinline__ void prefill_bande(const ParamsPrefill& pp, const uin
     __syncthreads();  // every tile decoded: the LUT, x and ring regions are free
 
     // ---- store the band's codes and scales
-    const uint32_t a_sa = base + pf_sa(RB, Bp), a_part = base + pf_part(RB, Bp);
+    const uint32_t a_sa = base + pf_sa(RB, B), a_part = base + pf_part(RB, B);
     const uint32_t haut = lane >= 32u ? 1u : 0u;
-    poser_tour(tour0, t00 + haut, N, B, Bp, r0, ba, bb, base, a_sa);
-    poser_tour(tour1, t01 + haut, N, B, Bp, r0, ba, bb, base, a_sa);
-    // padding: blocks B .. Bp - 1 of every row, then rows nl .. RB - 1 (zero codes, scale 1)
-    const uint32_t pad = Bp - B;
-    for (uint32_t i = threadIdx.x; i < nl * pad + (RB - nl) * Bp; i += blockDim.x) {
-        uint32_t o;
-        if (i < nl * pad) {
-            const uint32_t rl = i / pad;
-            o = rl * Bp + B + (i - rl * pad);
-        } else {
-            o = nl * Bp + (i - nl * pad);
-        }
+    poser_tour(tour0, t00 + haut, N, B, B, r0, ba, bb, base, a_sa);
+    poser_tour(tour1, t01 + haut, N, B, B, r0, ba, bb, base, a_sa);
+    // padding: rows nl .. RB - 1 of a last, partial band (zero codes, scale 1); blocks past B in the
+    // last k-step are zeroed where they are read
+    for (uint32_t i = threadIdx.x; i < (RB - nl) * B; i += blockDim.x) {
+        const uint32_t o = nl * B + i;
         ecrire_lds<u32x4>(base + PF_A + 16u * o, u32x4{0u, 0u, 0u, 0u});
         ecrire_lds<uint8_t>(a_sa + o, uint8_t(ECHELLE_UN));
     }
     __syncthreads();
 
-    // ---- MFMA: the waves of group g take row tiles 2g, 2g + 1 and the k-steps ks = (w mod VG) +
-    // VG i (4 blocks each) for every 16-pair tile; a group's partial sums are added in wave order.
-    const uint32_t nks = Bp / 4u, nrt = RB / 16u;
-    const uint32_t groupes = nrt > 2u ? 2u : 1u, VG = 16u / groupes;
-    const uint32_t g = w / VG, wg = w - g * VG;
-    const uint32_t nrt_g = min(2u, nrt - 2u * g);  // row tiles of this wave's group
+    // ---- MFMA: every wave takes all nrt row tiles and the units u = w, w + 16, ... of (k-step ks of 4
+    // blocks, pieces 2 pq and 2 pq + 1), K split 16 ways; the partial sums are added in wave order.
+    // Each B load feeds every row tile, and B is read once per band.
+    const uint32_t nks = (B + 3u) / 4u, nrt = RB / 16u;
     const uint32_t lr = lane & 15u, lg = lane >> 4;
-    constexpr uint32_t KS_MAX = PF_BP_MAX / 4u / 8u;  // k-steps per wave, 8 waves per group
-    // the A operands of k-step ks for this wave's row tiles, read from LDS where they are used
-    auto operande_a = [&](uint32_t rt, uint32_t ks, u32x4& a, uint32_t& sc) {
-        if (rt < nrt_g) {
-            const uint32_t o = (16u * (2u * g + rt) + lr) * Bp + 4u * ks + lg;
-            a = lire_lds<u32x4>(base + PF_A + 16u * o);
-            sc = lire_lds<uint8_t>(a_sa + o);
-        } else {
-            a = u32x4{0u, 0u, 0u, 0u};
-            sc = ECHELLE_UN;
+    // the A operands of k-step ks (all row tiles), read from LDS where they are used; blocks past B
+    // (the last k-step of a row whose B is not a multiple of 4) are zero with scale 1
+    auto operandes_a = [&](uint32_t ks, u32x4 (&a)[4], uint32_t (&sc)[4]) {
+        const uint32_t blk = 4u * ks + lg;
+        const bool dans = blk < B;
+#pragma unroll
+        for (uint32_t rt = 0; rt < 4; ++rt) {
+            if (rt < nrt) {  // wave-uniform
+                const uint32_t o = (16u * rt + lr) * B + (dans ? blk : B - 1u);
+                const u32x4 v = lire_lds<u32x4>(base + PF_A + 16u * o);
+                const uint32_t e = lire_lds<uint8_t>(a_sa + o);
+                a[rt] = dans ? v : u32x4{0u, 0u, 0u, 0u};
+                sc[rt] = dans ? e : ECHELLE_UN;
+            } else {
+                a[rt] = u32x4{0u, 0u, 0u, 0u};
+                sc[rt] = ECHELLE_UN;
+            }
         }
     };
     const uint32_t P = uniforme32(min(reinterpret_cast<const uint32_t*>(pp.pieces)[J == 2u ? 0 : 1], PF_PIECES));
@@ -537,32 +534,30 @@ __device__ __forceinline__ void prefill_bande(const ParamsPrefill& pp, const uin
         const uint32_t src = J == 2u ? c / pp.k : c;
         const Operande_b ob{bq + uint64_t(src) * PF_PIECES * Bp * 32u, bs + uint64_t(src) * PF_PIECES * Bp, Bp,
                             bloc_b, demi_b, lg, valide};
-        f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+        f32x4 acc[4];
 #pragma unroll
-        for (uint32_t i = 0; i < KS_MAX; ++i) {
-            const uint32_t ks = wg + VG * i;
-            if (ks >= nks) continue;  // wave-uniform
-            u32x4 a0, a1;
-            uint32_t s0, s1;
-            operande_a(0u, ks, a0, s0);
-            operande_a(1u, ks, a1, s1);
-            for (uint32_t p0 = 0; p0 < P; p0 += 2u) {
-                if (p0 + 1u < P)
-                    produit_pieces<2>(acc0, acc1, a0, a1, s0, s1, ob, p0, ks, nrt_g, P);
-                else
-                    produit_pieces<1>(acc0, acc1, a0, a1, s0, s1, ob, p0, ks, nrt_g, P);
-            }
+        for (uint32_t rt = 0; rt < 4; ++rt) acc[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        const uint32_t npp = (P + 1u) / 2u, U = nks * npp;
+        for (uint32_t u = w; u < U; u += 16u) {  // wave-uniform
+            const uint32_t ks = u / npp, p0 = 2u * (u - ks * npp);
+            u32x4 a[4];
+            uint32_t sa[4];
+            operandes_a(ks, a, sa);
+            if (p0 + 1u < P)
+                produit_pieces<2>(acc, a, sa, ob, p0, ks, nrt, P);
+            else
+                produit_pieces<1>(acc, a, sa, ob, p0, ks, nrt, P);
         }
-        ecrire_lds<f32x4>(a_part + ((w * 2u + 0u) * 64u + lane) * 16u, acc0);
-        ecrire_lds<f32x4>(a_part + ((w * 2u + 1u) * 64u + lane) * 16u, acc1);
+#pragma unroll
+        for (uint32_t rt = 0; rt < 4; ++rt)
+            if (rt < nrt) ecrire_lds<f32x4>(a_part + ((rt * 16u + w) * 64u + lane) * 16u, acc[rt]);
         __syncthreads();
         if (threadIdx.x < nrt * 256u) {
             const uint32_t rt = threadIdx.x >> 8, reste = threadIdx.x & 255u;
-            const uint32_t gg = rt >> 1, rl = rt & 1u;  // the row tile's group and its tile in the group
             const uint32_t ln = reste >> 2, r = reste & 3u;
             float s = 0.0f;
-            for (uint32_t ww = 0; ww < VG; ++ww)
-                s += lire_lds<float>(a_part + (((gg * VG + ww) * 2u + rl) * 64u + ln) * 16u + 4u * r);
+            for (uint32_t ww = 0; ww < 16u; ++ww)
+                s += lire_lds<float>(a_part + ((rt * 16u + ww) * 64u + ln) * 16u + 4u * r);
             const uint32_t ligne = 16u * rt + 4u * (ln >> 4) + r, jeton = 16u * tt + (ln & 15u);
             if (ligne < nl && jeton < n_e) {
                 const uint32_t cc = paires[debut_e + jeton];
@@ -639,9 +634,8 @@ uint32_t bp_de(uint32_t C) { return ((C / 32u + 3u) / 4u) * 4u; }
 // the 64 tiles a block decodes in two rounds and whose codes, scales and partial sums fit the LDS;
 // 0 if none does.
 uint32_t rb_de(uint32_t B, uint32_t N) {
-    const uint32_t bp = ((B + 3u) / 4u) * 4u;
     for (uint32_t rb = trc::PF_RB_MAX; rb >= 16; rb /= 2)
-        if ((rb * B - 1u) / (8u * N) + 2u <= 32u * trc::PF_TOURS && trc::pf_lds_tient(rb, bp)) return rb;
+        if ((rb * B - 1u) / (8u * N) + 2u <= 32u * trc::PF_TOURS && trc::pf_lds_tient(rb, B)) return rb;
     return 0;
 }
 
