@@ -412,24 +412,20 @@ __device__ __forceinline__ void decoder_tour(const EnteteRans& h, const DescFlux
     }
 }
 
-// A round's codes and scales into the band's LDS arrays: codes [row][pas][16 B], scales [row][pas].
-__device__ __forceinline__ void poser_tour(const TourBande& tb, uint32_t t, uint32_t N, uint32_t B, uint32_t pas,
-                                           uint32_t r0, uint32_t ba, uint32_t bb, uint32_t base, uint32_t a_sa) {
+// A round's codes and scales into the band's LDS arrays: codes [row][B][16 B], scales [row][B]. Rows
+// hold exactly B blocks, so block beta of the matrix sits at index beta - ba of the band (ba = its
+// first block), and no row tracking is needed.
+__device__ __forceinline__ void poser_tour(const TourBande& tb, uint32_t t, uint32_t N, uint32_t ba, uint32_t bb,
+                                           uint32_t base, uint32_t a_sa) {
     const uint32_t v = __lane_id() & 31u, q = v >> 2;
-    uint32_t beta = 8u * t * N + q;
-    uint32_t ligne = beta / B, blk = beta - ligne * B;
+    const uint32_t beta0 = 8u * t * N + q;
 #pragma unroll
     for (uint32_t mm = 0; mm < PF_NMAX; ++mm) {
+        const uint32_t beta = beta0 + 8u * mm;
         if (mm < tb.nb && beta >= ba && beta < bb) {
-            const uint32_t o = (ligne - r0) * pas + blk;
+            const uint32_t o = beta - ba;
             ecrire_lds<uint32_t>(base + PF_A + 16u * o + 4u * (v & 3u), tb.codes[mm]);
             if ((v & 3u) == 0u) ecrire_lds<uint8_t>(a_sa + o, uint8_t(tb.ech[mm >> 2] >> (8u * (mm & 3u))));
-        }
-        beta += 8u;
-        blk += 8u;
-        if (blk >= B) {  // B >= 8: one row at most
-            blk -= B;
-            ++ligne;
         }
     }
 }
@@ -482,8 +478,8 @@ __device__ __forceinline__ void prefill_bande(const ParamsPrefill& pp, const uin
     // ---- store the band's codes and scales
     const uint32_t a_sa = base + pf_sa(RB, B), a_part = base + pf_part(RB, B);
     const uint32_t haut = lane >= 32u ? 1u : 0u;
-    poser_tour(tour0, t00 + haut, N, B, B, r0, ba, bb, base, a_sa);
-    poser_tour(tour1, t01 + haut, N, B, B, r0, ba, bb, base, a_sa);
+    poser_tour(tour0, t00 + haut, N, ba, bb, base, a_sa);
+    poser_tour(tour1, t01 + haut, N, ba, bb, base, a_sa);
     // padding: rows nl .. RB - 1 of a last, partial band (zero codes, scale 1); blocks past B in the
     // last k-step are zeroed where they are read
     for (uint32_t i = threadIdx.x; i < (RB - nl) * B; i += blockDim.x) {
