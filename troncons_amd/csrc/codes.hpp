@@ -78,10 +78,13 @@ __device__ __forceinline__ Avance lire_avance(const EnteteRans& hc, const DescFl
 
 // One DELTA step with the reference-format LUT s | (f-1) << 8 | b << 20 read from device memory
 // (its lines stay in the L1: every tile start of the block reads it), words from the ring.
-template <bool TOUS_ACTIFS>
+// EN_LDS: the entry comes from the block's LDS copy at byte address `lutd_lds`, else from device
+// memory.
+template <bool TOUS_ACTIFS, bool EN_LDS>
 __device__ __forceinline__ uint32_t pas_delta(uint32_t& x, uint32_t o2, uint32_t& compte, gptr<uint32_t> lutd,
-                                              uint32_t anneau, uint32_t decal, uint32_t masque_inf, bool actif) {
-    const uint32_t e = lutd[x & (M - 1u)];
+                                              uint32_t lutd_lds, uint32_t anneau, uint32_t decal, uint32_t masque_inf,
+                                              bool actif) {
+    const uint32_t e = EN_LDS ? lire_lds<uint32_t>(lutd_lds + 4u * (x & (M - 1u))) : lutd[x & (M - 1u)];
     const uint32_t y = __umul24(((e >> 8) & 0xFFFu) + 1u, x >> PROBA_BITS) + (e >> 20);
     const bool besoin = (TOUS_ACTIFS || actif) && (y < L);
     const uint64_t vote = __builtin_amdgcn_ballot_w64(besoin);
@@ -158,9 +161,11 @@ __device__ __forceinline__ Avance premiere_avance(const PrepCodes& p, uint32_t R
 
 // CODES_CTX tiles -> partial sums of W x, x in LDS, the tiles' entries decoded here from DELTA.
 // `avance0`: premiere_avance(p), read by the caller. lutd: the job's DELTA LUT (reference format) in
-// device memory. The caller stages the decode LUTs and x in LDS and does not wait: each wavefront
-// decodes its first tiles' DELTA (its own ring and entry areas, the DELTA LUT from device memory)
-// and only then passes the block's barrier, once, before its first CODES step reads them.
+// device memory. The caller stages the decode LUTs and x in LDS and, for the first tiles, a copy of
+// the DELTA LUT over the entry area, without waiting: every wavefront passes the block's barrier
+// before its first DELTA step (which reads that copy: an LDS read where the device-memory LUT would
+// cost an L2 round trip per step, all waves waiting at once), and a second one before its first
+// entries overwrite it. Later tiles read the DELTA LUT from device memory through the caches.
 __device__ __forceinline__ void corps_codes(const Tache& tc, const PrepCodes& p, uint8_t* lds, const uint32_t* lutd_,
                                             uint32_t* __restrict__ controle, const Avance& avance0, const Grille& g) {
     const EnteteRans& h = p.hc;
@@ -191,7 +196,8 @@ __device__ __forceinline__ void corps_codes(const Tache& tc, const PrepCodes& p,
     const uint32_t mots_d = uint32_t(reinterpret_cast<const uint8_t*>(hd.mots) - p.fd.p);
     uint32_t hors_l = 0, pointeur = 0;
     Avance av = avance0;
-    bool barriere = true;  // wave-uniform: the block's LUT and x barrier is still to pass
+    bool premiere = true;  // wave-uniform: the block's two first-tile barriers are still to pass
+    const uint32_t a_lutd = base + LDS_ENT;
     for (uint32_t t0 = 2u * vague; t0 < hT; t0 += 2u * n_vagues) {
         const uint32_t t = t0 + (haut ? 1u : 0u);
         const bool tuile = t < hT;
@@ -218,15 +224,28 @@ __device__ __forceinline__ void corps_codes(const Tache& tc, const PrepCodes& p,
                 if (long_d) ecrire_lds<u32x4>(a_anneau + 512u + 16u * v, suite);
             }
         }
+        if (premiere) barriere_lds();  // the staged LUTs and x are visible
         uint32_t xd = cur.xd, od = ((mots_d + 2u * cur.dDebut) & 15u), mot = 0;
-        for (uint32_t md = 0; md <= saut_max; ++md) {
-            const bool actif = tuile && md <= saut;
-            uint32_t compte = 0, m4 = 0;
+        auto delta = [&](auto en_lds) {
+            constexpr bool EN_LDS = decltype(en_lds)::value;
+            for (uint32_t md = 0; md <= saut_max; ++md) {
+                const bool actif = tuile && md <= saut;
+                uint32_t compte = 0, m4 = 0;
 #pragma unroll
-            for (uint32_t k = 0; k < 4; ++k)
-                m4 |= pas_delta<false>(xd, od, compte, lutd, a_anneau, decal, masque_inf, actif) << (8u * k);
-            od += 2u * compte;
-            if (md == saut) mot = m4;
+                for (uint32_t k = 0; k < 4; ++k)
+                    m4 |= pas_delta<false, EN_LDS>(xd, od, compte, lutd, a_lutd, a_anneau, decal, masque_inf, actif)
+                          << (8u * k);
+                od += 2u * compte;
+                if (md == saut) mot = m4;
+            }
+        };
+        if (premiere)  // wave-uniform
+            delta(std::true_type{});
+        else
+            delta(std::false_type{});
+        if (premiere) {
+            barriere_lds();  // no wave reads the DELTA LUT copy any more: the entry area is free
+            premiere = false;
         }
         // the DELTA tile's end checks, by the half that decoded its last macro-step
         const uint32_t tau = t >> (dN - 1u);
@@ -237,10 +256,6 @@ __device__ __forceinline__ void corps_codes(const Tache& tc, const PrepCodes& p,
         }
         // 2. the tile's 128 block entries
         if (tuile) ecrire_lds<u32x4>(a_ent + 16u * v, entrees_de_delta(mot, cur, 128u * t + 4u * v, nblocs, p.B));
-        if (barriere) {
-            barriere_lds();
-            barriere = false;
-        }
         // 3. the CODES words over the DELTA ones, and the next pair's streams read ahead
         ecrire_lds<u32x4>(a_anneau + 16u * v, cur.mots0);
         ecrire_lds<u32x4>(a_anneau + 512u + 16u * v, cur.mots1);
@@ -327,7 +342,10 @@ __device__ __forceinline__ void corps_codes(const Tache& tc, const PrepCodes& p,
             pointeur += (v == 0 && debut + (a.o2 - o0) / 2u != attendu) ? 1u : 0u;
         }
     }
-    if (barriere) barriere_lds();  // a wavefront without tiles still takes its part in it
+    if (premiere) {  // a wavefront without tiles still takes its part in both
+        barriere_lds();
+        barriere_lds();
+    }
     verser_controle(controle, hors_l, pointeur);
 }
 

@@ -204,12 +204,16 @@ __device__ __forceinline__ void codes_bloc(const trc::Taches& taches, const uint
     // The prologue is a chain of dependent device-memory reads (logits -> top-k -> the expert's
     // record -> its first tiles' heads -> their words). Everything that does not depend on the
     // top-k's outcome is issued first, unconditionally (indices clamped), in the order it is waited
-    // for: the logits; the job's DELTA LUT, which every tile start then reads through the caches
-    // (loaded here only to bring its lines in, and waited for with the decode LUTs); the decode
-    // LUTs; x (its address and width do not depend on the expert).
+    // for: the logits; the job's DELTA LUT (staged in LDS for the first tiles' DELTA, its lines also
+    // brought into the caches for the later tiles' reads); the decode LUTs; x (its address and
+    // width do not depend on the expert).
     const gptr<float> lg_src = glob<float>(topk ? reinterpret_cast<const void*>(pm.logits) : reinterpret_cast<const void*>(luts));
     const float lg_v = lg_src[min(threadIdx.x, (topk ? pm.E : 1u) - 1u)];
-    const uint32_t lutd_chaud = glob<uint32_t>(luts + uint64_t(j) * 4u * M)[4u * min(threadIdx.x, M / 4u - 1u)];
+    constexpr uint32_t LOT_D = (M / 4u + FILS - 1u) / FILS;  // 16-byte groups of the DELTA LUT per thread
+    u32x4 lutd_v[LOT_D];
+#pragma unroll
+    for (uint32_t k = 0; k < LOT_D; ++k)
+        lutd_v[k] = glob<u32x4>(luts + uint64_t(j) * 4u * M)[min(k * FILS + threadIdx.x, M / 4u - 1u)];
     // gate/up: the directory's records of matrix j, one 128-byte line each, so that the one the
     // top-k picks is read from the caches
     const uint32_t rep_chaud =
@@ -279,7 +283,7 @@ __device__ __forceinline__ void codes_bloc(const trc::Taches& taches, const uint
     // issued here, ahead of the LDS staging below (which waits on the earlier loads only)
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
-    asm volatile("" ::"v"(lutd_chaud), "v"(rep_chaud));  // complete before the decode LUTs, issued after them
+    asm volatile("" ::"v"(rep_chaud));  // complete before the decode LUTs, issued after it
 #pragma unroll
     for (uint32_t i = 0; i < 4; ++i) {
         const uint32_t k = threadIdx.x + i * FILS;
@@ -288,8 +292,13 @@ __device__ __forceinline__ void codes_bloc(const trc::Taches& taches, const uint
     if (threadIdx.x < 8u)
         *reinterpret_cast<u32x4*>(lds + LDS_X + COLONNE_NULLE * 128u + 16u * threadIdx.x) = u32x4{0u, 0u, 0u, 0u};
     charge_lut.poser(reinterpret_cast<uint2*>(lds + LDS_LUT));
-    // the block's barrier (LDS only: the read-ahead stays in flight) is passed in corps_codes,
-    // after each wavefront's first DELTA decode
+    // the DELTA LUT copy over the entry area (free since the top-k's last barrier)
+#pragma unroll
+    for (uint32_t k = 0; k < LOT_D; ++k)
+        if (k * FILS + threadIdx.x < M / 4u)
+            *reinterpret_cast<u32x4*>(lds + LDS_ENT + 16u * (k * FILS + threadIdx.x)) = lutd_v[k];
+    // the block's barriers (LDS only: the read-ahead stays in flight) are passed in corps_codes,
+    // around each wavefront's first DELTA decode
     corps_codes(tc, p, lds, luts + uint64_t(j) * 4u * M, controle, avance0, g);
 }
 
