@@ -97,24 +97,28 @@ __device__ __forceinline__ uint32_t pas_delta(uint32_t& x, uint32_t o2, uint32_t
     return e & 0xFFu;
 }
 
-// The 4 block entries of lane v (blocks 4v .. 4v + 3 of CODES tile t) from its 4 delta bytes.
+// The 4 block entries of lane v (blocks 4v .. 4v + 3 of CODES tile t) from its 4 delta bytes, the
+// four at once on packed bytes (no branch): e - 128 = (med + delta) mod 256 byte-wise without carries
+// between bytes, the row's median being med0 up to the row's end and med1 after it (B >= 8: one row
+// change at most); kappa = 0 below 128, 1 at 128, 2 above, from bit 7 of delta and an exact
+// byte-wise zero test of delta ^ 0x80.
 __device__ __forceinline__ u32x4 entrees_de_delta(uint32_t mot, const Avance& a, uint32_t bloc0, uint32_t nblocs,
                                                   const Diviseur& divB) {
-    u32x4 s;
     const uint32_t B = divB.d;
-    const uint32_t ligne0 = divB.quotient(bloc0);
-    uint32_t col = bloc0 - ligne0 * B, ligne = ligne0;
+    const uint32_t col0 = bloc0 - divB.quotient(bloc0) * B;
+    const uint32_t reste = B - col0;  // blocks left in the row from block 4v (>= 1)
+    const uint32_t apres = reste >= 4u ? 0u : (0xFFFFFFFFu << (8u * reste));
+    const uint32_t medp = ((a.med0 * 0x01010101u) & ~apres) | ((a.med1 * 0x01010101u) & apres);
+    const uint32_t ep = ((medp & 0x7F7F7F7Fu) + (mot & 0x7F7F7F7Fu)) ^ ((medp ^ mot) & 0x80808080u);
+    const uint32_t v = mot ^ 0x80808080u;
+    const uint32_t nul = ~(((v & 0x7F7F7F7Fu) + 0x7F7F7F7Fu) | v | 0x7F7F7F7Fu);  // bit 7: delta byte == 128
+    u32x4 s;
 #pragma unroll
     for (uint32_t k = 0; k < 4; ++k) {
-        const uint32_t d = (mot >> (8u * k)) & 255u;
-        const uint32_t med = ligne == ligne0 ? a.med0 : a.med1;
-        s[k] = bloc0 + k < nblocs ? entree_bloc((med + d - 128u) & 255u, classe_delta(d), col, col == 0u)
-                                  : ENTREE_BOURRAGE;
-        ++col;
-        if (col == B) {  // B >= 8: four blocks span at most two rows
-            col = 0;
-            ++ligne;
-        }
+        const uint32_t col = k < reste ? col0 + k : k - reste;
+        const uint32_t ctx = 2u * ((mot >> (8u * k + 7u)) & 1u) - ((nul >> (8u * k + 7u)) & 1u);
+        const uint32_t ent = (col << 7) | (ctx << 15) | (((ep >> (8u * k)) & 255u) << ENT_EXP) | (col == 0u ? ENT_LIGNE : 0u);
+        s[k] = bloc0 + k < nblocs ? ent : ENTREE_BOURRAGE;
     }
     return s;
 }
@@ -198,6 +202,11 @@ __device__ __forceinline__ void corps_codes(const Tache& tc, const PrepCodes& p,
     Avance av = avance0;
     bool premiere = true;  // wave-uniform: the block's two first-tile barriers are still to pass
     const uint32_t a_lutd = base + LDS_ENT;
+    // Issue priority by progress: a wavefront decodes its first tile pair at a raised priority and
+    // drops it afterwards, so that the SIMD's wavefronts still on their first pair are issued ahead
+    // of those already on the next one; their ends then come closer together, and the launch's tail
+    // (the last wavefronts running alone on their SIMDs) gets shorter.
+    __builtin_amdgcn_s_setprio(2);
     for (uint32_t t0 = 2u * vague; t0 < hT; t0 += 2u * n_vagues) {
         const uint32_t t = t0 + (haut ? 1u : 0u);
         const bool tuile = t < hT;
@@ -341,6 +350,7 @@ __device__ __forceinline__ void corps_codes(const Tache& tc, const PrepCodes& p,
             hors_l += (x != L) ? 1u : 0u;
             pointeur += (v == 0 && debut + (a.o2 - o0) / 2u != attendu) ? 1u : 0u;
         }
+        __builtin_amdgcn_s_setprio(0);
     }
     if (premiere) {  // a wavefront without tiles still takes its part in both
         barriere_lds();
