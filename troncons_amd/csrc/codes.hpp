@@ -202,11 +202,12 @@ __device__ __forceinline__ void corps_codes(const Tache& tc, const PrepCodes& p,
     Avance av = avance0;
     bool premiere = true;  // wave-uniform: the block's two first-tile barriers are still to pass
     const uint32_t a_lutd = base + LDS_ENT;
-    // Issue priority by progress: a wavefront decodes its first tile pair at a raised priority and
-    // drops it afterwards, so that the SIMD's wavefronts still on their first pair are issued ahead
-    // of those already on the next one; their ends then come closer together, and the launch's tail
-    // (the last wavefronts running alone on their SIMDs) gets shorter.
-    __builtin_amdgcn_s_setprio(2);
+    // Issue priority by progress: a wavefront decodes its first tile pair at priority 3, then 2 from
+    // the pair's ninth macro-step, its second pair at 1 and then 0, so that on a SIMD the wavefronts
+    // that are behind are issued ahead of those further on: their ends come closer together, and the
+    // launch's tail (the last wavefronts running alone on their SIMDs) gets shorter.
+    uint32_t paire_n = 0;
+    __builtin_amdgcn_s_setprio(3);
     for (uint32_t t0 = 2u * vague; t0 < hT; t0 += 2u * n_vagues) {
         const uint32_t t = t0 + (haut ? 1u : 0u);
         const bool tuile = t < hT;
@@ -339,6 +340,12 @@ __device__ __forceinline__ void corps_codes(const Tache& tc, const PrepCodes& p,
         };
         uint32_t m = 0;
         for (; m + 1u < nb_min; m += 2u) {
+            if (m == 8u) {
+                if (paire_n == 0u)
+                    __builtin_amdgcn_s_setprio(2);
+                else
+                    __builtin_amdgcn_s_setprio(0);
+            }
             macro(std::true_type{}, m);
             macro(std::true_type{}, m + 1u);
         }
@@ -350,7 +357,11 @@ __device__ __forceinline__ void corps_codes(const Tache& tc, const PrepCodes& p,
             hors_l += (x != L) ? 1u : 0u;
             pointeur += (v == 0 && debut + (a.o2 - o0) / 2u != attendu) ? 1u : 0u;
         }
-        __builtin_amdgcn_s_setprio(0);
+        if (paire_n == 0u)
+            __builtin_amdgcn_s_setprio(1);
+        else
+            __builtin_amdgcn_s_setprio(0);
+        ++paire_n;
     }
     if (premiere) {  // a wavefront without tiles still takes its part in both
         barriere_lds();
