@@ -369,11 +369,12 @@ def bench_prefill(args, c0, dims, E, k, C, fz, flux, dev, espace, x_tok, n_fils,
         "metric": f"config5 us per {T}-position prefill batch (top-{k} of {E}, Zipf 1.1)",
         "value": round(us, 1), "unit": "us/batch", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(ms / args.steps, 4), "higher_is_better": False, "scaling": "weak",
-        "vs_baseline": None, "dtype": "u32 rANS / fp4 x fp8-pieces MFMA, f32 accumulate",
+        "vs_baseline": None,
+        "dtype": "u32 rANS / gate-up bf16 MFMA (x in bf16 pieces), down fp4 x fp8-pieces MFMA, f32 accumulate",
         "data": "synthetic (seeded MXFP4 law A, E8M0 in [119,125], bf16 N(0,1) activations, Zipf(1.1) routing)",
         "config": {"workload": f"config5: batched prefill, {T} positions, top-{k} of {E} gpt-oss-120b experts "
                                "(.trc v1.2 rANS-coded), each chosen expert decoded once into LDS, grouped GEMM "
-                               "on block-scaled FP4 MFMA", "positions": T, "experts": E, "k": k,
+                               "on MFMA", "positions": T, "experts": E, "k": k,
                    "n_codes": args.n_codes, "n_delta": args.n_delta},
         "tokens_per_s": round(T / (us * 1e-6), 1),
         "experts_decoded": int(len(choisis)),
@@ -382,7 +383,7 @@ def bench_prefill(args, c0, dims, E, k, C, fz, flux, dev, espace, x_tok, n_fils,
         "compressed_bytes": octets,
         "gbps_compressed": round(octets / (us * 1e-6) / 1e9, 1),
         "useful_tflops": round(flops / (us * 1e-6) / 1e12, 2),
-        "fp8_pieces": {"x": int(pieces[0]), "act": int(pieces[1])},
+        "pieces": {"x_bf16": int(pieces[0]), "act_fp8": int(pieces[1])},
         "kernel_us": kern,
         "roofline": {
             "bound": "hbm", "kernel": "prefill_mfma (gate/up launch + down launch: decode + MFMA)",

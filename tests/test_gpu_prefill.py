@@ -4,8 +4,9 @@ Each position's residual is checked against the reference's own chain run by the
 (position, slot) — gemv_mxfp4 gate and up, swiglu_oai, gemv_mxfp4 down, then the ordered combine
 (trc-modele/src/lib.rs:688-710, passe.cuh:598-622) — and against the same computation in f64 from the
 uncompressed weights: within 1e-5 * max|change| of both, per position (the fused path's GEMV
-tolerance; the MFMA's block sums are exact by construction, so only the fp32 accumulation order and
-a 2^-20 activation remainder differ). Decoded weights are checked bit for bit by the other suites.
+tolerance: gate and up multiply exact bf16 pieces of x, down exact fp8 pieces of act, so only the
+fp32 accumulation order and a 2^-20 remainder of act differ). Decoded weights are checked bit for bit
+by the other suites.
 """
 from __future__ import annotations
 
@@ -85,7 +86,7 @@ class Couche:
         assert list(hote(ctl, np.uint32)) == [0, 0, 0, 0]
 
 
-def _lancer(fz, couche, E, dims, x, idx, w, residu0, N):
+def _lancer(fz, couche, E, dims, x, idx, w, residu0, N, pieces=None):
     T, k = idx.shape
     xd, idd, wd, res = dev(x), dev(idx), dev(w), dev(residu0)
     ctl = zeros(16)
@@ -93,6 +94,8 @@ def _lancer(fz, couche, E, dims, x, idx, w, residu0, N):
     print(f"prefill: T={T} k={k} E={E} dims={list(dims.lignes)}x{list(dims.colonnes)} N={N}", flush=True)
     fz.prefill_moe(vue(couche.rep), E, vue(couche.luts), dims, vue(xd), T, vue(idd), vue(wd), k, vue(res), vue(ctl),
                    vue(tr), *N)
+    if pieces is not None:  # the workspace starts with the pieces used by x and by act
+        pieces.extend(int(v) for v in hote(tr, np.uint32)[:2])
     return hote(res, np.float32).reshape(T, -1), hote(ctl, np.uint32)
 
 
@@ -141,6 +144,30 @@ def test_prefill_ragged_blocks(fz):
     couche.c.liberer()
 
 
+@pytest.mark.parametrize("bits", [24, 16])
+def test_prefill_f32_activations(fz, bits):
+    """x with full f32 significands (gate and up then take three bf16 pieces of x) or with 16-bit ones
+    (two pieces), on the ragged layer and on the small one."""
+    for graine, dims, E, T, k in [(61, DimsExpert.de([352, 352, 288], [288, 288, 352]), 5, 21, 3),
+                                  (71, DimsExpert.de([256, 256, 256], [256, 256, 256]), 6, 40, 4)]:
+        N = (8, 8)
+        C = dims.colonnes[0]
+        couche = Couche(fz, graine, E, dims, N)
+        idx, w = _routage(graine + 1, T, E, k, zipf=1.1)
+        rng = np.random.default_rng(graine + 2)
+        x = rng.standard_normal((T, C)).astype(np.float32)
+        x *= np.exp2(rng.integers(-6, 7, size=(T, C))).astype(np.float32)  # a wide range within each block
+        if bits == 16:
+            x = (x.view(np.uint32) & np.uint32(0xFFFFFF00)).view(np.float32)
+        residu0 = np.zeros((T, dims.lignes[2]), np.float32)
+        pieces = []
+        got, ctl = _lancer(fz, couche, E, dims, x, idx, w, residu0, N, pieces)
+        assert list(ctl) == [0, 0, 0, 0]
+        assert pieces[0] == (3 if bits == 24 else 2), pieces
+        _verifier(got, residu0, x, idx, w, _slots(graine, E, dims), dims)
+        couche.c.liberer()
+
+
 def test_prefill_gpt_oss_shape(fz):
     """Config-5 shape family: 2880 x 2880 gpt-oss experts, N = 16 / 4, 16 positions over 8 experts
     with Zipf routing; also determinism (a second call gives the same bits)."""
@@ -149,8 +176,10 @@ def test_prefill_gpt_oss_shape(fz):
     idx, w = _routage(52, T, E, k, zipf=1.1)
     x = np.stack([O.synth_normale_bf16(53, 4, i, 2880, 1.0) for i in range(T)])
     residu0 = np.zeros((T, 2880), np.float32)
-    got, ctl = _lancer(fz, couche, E, GPT, x, idx, w, residu0, N)
+    pieces = []
+    got, ctl = _lancer(fz, couche, E, GPT, x, idx, w, residu0, N, pieces)
     assert list(ctl) == [0, 0, 0, 0]
+    assert pieces[0] == 1, pieces  # bf16 activations: one bf16 piece of x
     got2, _ = _lancer(fz, couche, E, GPT, x, idx, w, residu0, N)
     assert (got == got2).all()
     _verifier(got, residu0, x, idx, w, _slots(51, E, GPT), GPT)

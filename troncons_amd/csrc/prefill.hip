@@ -7,15 +7,21 @@
 //
 //   prefill_grouper       (position, slot) pairs grouped by expert, in position order within an
 //                         expert (the reference's par_expert lists, trc-ordo/src/lib.rs:815-823);
-//   prefill_quant_x       each position's x split into fp8 pieces with E8M0 block scales;
+//   prefill_quant_x       each position's x split into bf16 pieces (hi + mid + lo = x);
 //   fusion_echelles       (prefill mode) DELTA -> block entries of every chosen expert's matrices;
-//   prefill_mfma_gu       gate and up: bands decoded into LDS, MFMA against the expert's positions,
-//                         + bias -> gu;
+//   prefill_mfma_gu       gate and up: bands decoded into LDS, bf16 MFMA (the weights converted from
+//                         MXFP4 where they are read) against the expert's positions, + bias -> gu;
 //   prefill_swiglu_quant  act = swiglu_oai(gate, up) per pair, split into fp8 pieces;
 //   prefill_mfma_bas      down -> s, one row of D per pair (the reference's pos.s layout);
 //   prefill_combiner      x_i += ((w0 s_i0 + w1 s_i1) + ...) in slot order, no FMA.
 //
-// Activations in pieces. The MFMA's B operand here is fp8 E4M3 with one E8M0 scale per 32 values,
+// x in bf16 pieces (gate and up). x_f32 = hi + mid + lo with hi = bf16(x), mid = bf16(x - hi) and
+// lo = bf16(x - hi - mid), each difference exact in f32: hi leaves at most 16 significant bits, mid
+// at most 8, which lo holds. A weight, e2m1 x 2^(e - 127), is exact in bf16 too, so every product
+// of v_mfma_f32_16x16x32_bf16 is exact and y differs from the f32 GEMV only by the fp32 accumulation
+// order. Pieces that are zero for every position are skipped: bf16 activations need one.
+//
+// act in pieces (down). The MFMA's B operand here is fp8 E4M3 with one E8M0 scale per 32 values,
 // and the MFMA adds the 32 products of a block in a fixed-point sum that keeps about 14 bits below
 // the block's largest product. A block of activations a is written as a = sum_p q_p 2^k_p: piece p
 // takes, at scale 2^k_p (the residual's maximum in [128, 256) * 2^k_p), the round-to-nearest E4M3 of
@@ -46,7 +52,9 @@ namespace trc {
 
 constexpr uint32_t PF_FILS = 1024;        // 16 wavefronts: 32 tiles decoded per band
 constexpr uint32_t PF_NMAX = 16;          // macro-steps per CODES_CTX tile held in registers
-constexpr uint32_t PF_PIECES = 5;         // fp8 pieces per activation block
+constexpr uint32_t PF_PIECES = 5;         // fp8 pieces per act block
+constexpr uint32_t PF_PIECES_BF = 3;      // bf16 pieces per x block
+constexpr uint32_t PF_QX_FILS = 192;      // prefill_quant_x threads: one per x block, PF_BP_MAX + 1 at most
 constexpr uint32_t PF_BP_MAX = 128;       // padded blocks per row (4096 columns)
 constexpr uint32_t PF_PAIRES_MAX = 16384; // positions x k per call
 constexpr uint32_t ECHELLE_UN = 127u;     // E8M0 1.0
@@ -64,6 +72,8 @@ __host__ __device__ inline uint32_t pf_part_octets(uint32_t rb) { return (rb / 1
 __host__ __device__ inline bool pf_lds_tient(uint32_t rb, uint32_t b) { return pf_part(rb, b) + pf_part_octets(rb) <= LDS_GEMV; }
 
 typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 struct ParamsPrefill {
     uint64_t repertoire;   // MatricePartie[E][3] of the mounted layer
@@ -72,12 +82,14 @@ struct ParamsPrefill {
     uint64_t compte;       // u32[E] pairs per expert
     uint64_t debut;        // u32[E] first pair of expert e in `paires`
     uint64_t paires;       // u32[T*k] pair c = i*k + slot, grouped by expert
-    uint64_t pieces;       // u32[4]: [0] pieces used by x, [1] by act
+    uint64_t pieces;       // u32[4]: [0] bf16 pieces used by x, [1] fp8 pieces used by act
     uint64_t indices;      // u32[T*k] chosen experts
     uint64_t poids;        // f32[T*k] their weights
     uint64_t x;            // f32[T][C]
     uint64_t residus;      // f32[T][D]
-    uint64_t xq, xs;       // x pieces: xq[((i*PF_PIECES + p)*bp[0] + b)*32], xs[(i*PF_PIECES + p)*bp[0] + b]
+    uint64_t xb;           // x pieces, bf16: xb[((i*PF_PIECES_BF + p)*bx + b)*32 + j], j in the order
+                           // of the weight block's nibbles: x[32 b + (j >> 1) + 16 (j & 1)]; block
+                           // b = C/32 (the last of the bx = C/32 + 1) is zero
     uint64_t gu;           // f32[T*k][2][R]
     uint64_t aq, as;       // act pieces per pair, bp[2] blocks per row
     uint64_t s;            // f32[T*k][D]
@@ -85,6 +97,7 @@ struct ParamsPrefill {
     uint32_t bp[3];        // padded blocks per row (multiple of 4)
     uint32_t rb[3];        // rows per band (16, 32 or 64)
     uint32_t T, k, E, D;
+    uint32_t bx;           // x blocks per piece row: C/32 + 1
 };
 
 // Splits 32 values (natural order a[0..31]) into pieces: writes PF_PIECES x 32 bytes (piece stride
@@ -223,14 +236,17 @@ prefill_grouper(ParamsPrefill pp, uint32_t* __restrict__ controle) {
     }
 }
 
-// x pieces: block (position i), thread b = column block b (padding blocks b >= B get zeros).
-extern "C" __global__ void __launch_bounds__(trc::PF_BP_MAX)
+// x pieces: block (position i), thread b = column block b (block B gets zeros). Word q
+// of a 64-byte piece block holds values q (low half) and q + 16 (high half), as byte q of a weight
+// block holds weights q and q + 16. An infinite or NaN value stays whole in hi (its residual is set
+// to 0), so a product with it is what the f32 product is.
+extern "C" __global__ void __launch_bounds__(trc::PF_QX_FILS)
 prefill_quant_x(ParamsPrefill pp) {
     using namespace trc;
     const uint32_t i = blockIdx.x, b = threadIdx.x;
-    const uint32_t C = pp.colonnes[0], B = C / 32u, Bp = pp.bp[0];
+    const uint32_t C = pp.colonnes[0], B = C / 32u, Bx = pp.bx;
     uint32_t P = 0;
-    if (b < Bp) {
+    if (b < Bx) {
         float a[32];
         const gptr<f32x4> x4 = glob<f32x4>(reinterpret_cast<const float*>(pp.x) + uint64_t(i) * C + 32u * b);
 #pragma unroll
@@ -242,9 +258,27 @@ prefill_quant_x(ParamsPrefill pp) {
             a[4 * g + 2] = v.z;
             a[4 * g + 3] = v.w;
         }
-        const uint64_t base = uint64_t(i) * PF_PIECES * Bp + b;
-        P = pieces_bloc(a, reinterpret_cast<uint8_t*>(pp.xq) + base * 32u, uint64_t(Bp) * 32u,
-                        reinterpret_cast<uint8_t*>(pp.xs) + base, Bp);
+        uint8_t* dst = reinterpret_cast<uint8_t*>(pp.xb) + (uint64_t(i) * PF_PIECES_BF * Bx + b) * 64u;
+#pragma unroll
+        for (uint32_t p = 0; p < PF_PIECES_BF; ++p) {
+            uint32_t mots[16];
+            uint32_t nz = 0;
+#pragma unroll
+            for (uint32_t q = 0; q < 16; ++q) {
+                const __bf16 h0 = __bf16(a[q]), h1 = __bf16(a[q + 16]);
+                const uint32_t b0 = __builtin_bit_cast(uint16_t, h0), b1 = __builtin_bit_cast(uint16_t, h1);
+                const float f0 = __uint_as_float(b0 << 16), f1 = __uint_as_float(b1 << 16);
+                a[q] = __builtin_isfinite(f0) ? a[q] - f0 : 0.0f;  // exact
+                a[q + 16] = __builtin_isfinite(f1) ? a[q + 16] - f1 : 0.0f;
+                mots[q] = b0 | (b1 << 16);
+                nz |= mots[q];
+            }
+#pragma unroll
+            for (uint32_t g = 0; g < 4; ++g)
+                *reinterpret_cast<u32x4*>(dst + uint64_t(p) * Bx * 64u + 16u * g) =
+                    u32x4{mots[4 * g], mots[4 * g + 1], mots[4 * g + 2], mots[4 * g + 3]};
+            if (nz & 0x7FFF7FFFu) P = p + 1u;
+        }
     }
     P = max_vague(P);
     if (__lane_id() == 0 && P) atomicMax(reinterpret_cast<uint32_t*>(pp.pieces), P);
@@ -328,6 +362,56 @@ __device__ __forceinline__ void produit_pieces(f32x4 (&acc)[4], const u32x4 (&a)
     // The result of this MFMA (A fp4, B fp8) reaches its registers 11 to 12 wait states after issue
     // (measured); the compiler's hazard padding before a VALU read of it can be shorter. 16 wait states
     // here, fenced so that nothing is scheduled across them, cover every reader.
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_nop 15");
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+// acc[rt] += A_rt x B over the k-steps ks = w, w + 16, ... < B (one 32-value block each) and the
+// pieces p < NP of x, for the nrt row tiles of the band, on v_mfma_f32_16x16x32_bf16. Lane g*16 + n
+// holds, for A, weights 4g .. 4g + 3 and 16 + 4g .. 19 + 4g of row n of the tile (byte 4g .. 4g + 3
+// of its code block, converted with the block's E8M0 scale) and, for B, the same values of x for
+// column n: the MFMA adds the products of each lane group's eight K values, so any order common to A
+// and B gives the dot product. The B loads of KB k-steps are issued before their MFMAs. Columns past
+// the expert's pairs load a valid position; their sums are never stored.
+template <uint32_t NP, uint32_t KB, uint32_t NRT>
+__device__ __forceinline__ void produit_bf16(f32x4 (&acc)[4], const uint8_t* xsrc, uint64_t pas_p, uint32_t w,
+                                             uint32_t B, uint32_t a_codes, uint32_t a_sa, uint32_t lr, uint32_t lg) {
+    for (uint32_t ks0 = w; ks0 < B; ks0 += 16u * KB) {  // wave-uniform
+        u32x4 bq[KB][NP];
+#pragma unroll
+        for (uint32_t q = 0; q < KB; ++q) {
+            const uint32_t ks = min(ks0 + 16u * q, B);  // block B of x is zero
+#pragma unroll
+            for (uint32_t p = 0; p < NP; ++p) bq[q][p] = *glob<u32x4>(xsrc + p * pas_p + 64u * ks);
+        }
+        __builtin_amdgcn_sched_barrier(0);  // every load issued before the first MFMA waits
+#pragma unroll
+        for (uint32_t q = 0; q < KB; ++q) {
+            // straight-line code, so that the B loads above stay ahead of every MFMA: a k-step past B
+            // multiplies block B - 1 of the weights by x's zero block
+            const uint32_t ks = min(ks0 + 16u * q, B - 1u);
+            bf16x8 a[NRT];
+#pragma unroll
+            for (uint32_t rt = 0; rt < NRT; ++rt) {
+                const uint32_t o = (16u * rt + lr) * B + ks;
+                const uint32_t mot = lire_lds<uint32_t>(a_codes + 16u * o + 4u * lg);
+                const float sc = __uint_as_float(uint32_t(lire_lds<uint8_t>(a_sa + o)) << 23);
+                const bf16x2 p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(mot, sc, 0);
+                const bf16x2 p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(mot, sc, 1);
+                const bf16x2 p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(mot, sc, 2);
+                const bf16x2 p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(mot, sc, 3);
+                a[rt] = bf16x8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+            }
+#pragma unroll
+            for (uint32_t p = 0; p < NP; ++p) {
+                const bf16x8 bv = __builtin_bit_cast(bf16x8, bq[q][p]);
+#pragma unroll
+                for (uint32_t rt = 0; rt < NRT; ++rt)
+                    acc[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[rt], bv, acc[rt], 0, 0, 0);
+            }
+        }
+    }
     __builtin_amdgcn_sched_barrier(0);
     asm volatile("s_nop 15");
     __builtin_amdgcn_sched_barrier(0);
@@ -513,11 +597,12 @@ __device__ __forceinline__ void prefill_bande(const ParamsPrefill& pp, const uin
             }
         }
     };
-    const uint32_t P = uniforme32(min(reinterpret_cast<const uint32_t*>(pp.pieces)[J == 2u ? 0 : 1], PF_PIECES));
+    const uint32_t P = uniforme32(J == 2u ? min(reinterpret_cast<const uint32_t*>(pp.pieces)[0], PF_PIECES_BF)
+                                          : min(reinterpret_cast<const uint32_t*>(pp.pieces)[1], PF_PIECES));
     const uint32_t debut_e = uniforme32(reinterpret_cast<const uint32_t*>(pp.debut)[e]);
     const uint32_t* paires = reinterpret_cast<const uint32_t*>(pp.paires);
-    const uint8_t* bq = reinterpret_cast<const uint8_t*>(J == 2u ? pp.xq : pp.aq);
-    const uint8_t* bs = reinterpret_cast<const uint8_t*>(J == 2u ? pp.xs : pp.as);
+    const uint8_t* bq = reinterpret_cast<const uint8_t*>(pp.aq);
+    const uint8_t* bs = reinterpret_cast<const uint8_t*>(pp.as);
     const float* biais = reinterpret_cast<const float*>(m.biais.p);
     const uint32_t demi_b = 16u * (lg & 1u), bloc_b = lg >> 1;
     const uint32_t n_tt = (n_e + 15u) / 16u;
@@ -527,22 +612,44 @@ __device__ __forceinline__ void prefill_bande(const ParamsPrefill& pp, const uin
         const bool valide = tok < n_e;
         const uint32_t c = c_suiv;
         c_suiv = tok + 16u < n_e ? paires[debut_e + tok + 16u] : 0u;
-        const uint32_t src = J == 2u ? c / pp.k : c;
-        const Operande_b ob{bq + uint64_t(src) * PF_PIECES * Bp * 32u, bs + uint64_t(src) * PF_PIECES * Bp, Bp,
-                            bloc_b, demi_b, lg, valide};
         f32x4 acc[4];
 #pragma unroll
         for (uint32_t rt = 0; rt < 4; ++rt) acc[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
-        const uint32_t npp = (P + 1u) / 2u, U = nks * npp;
-        for (uint32_t u = w; u < U; u += 16u) {  // wave-uniform
-            const uint32_t ks = u / npp, p0 = 2u * (u - ks * npp);
-            u32x4 a[4];
-            uint32_t sa[4];
-            operandes_a(ks, a, sa);
-            if (p0 + 1u < P)
-                produit_pieces<2>(acc, a, sa, ob, p0, ks, nrt, P);
-            else
-                produit_pieces<1>(acc, a, sa, ob, p0, ks, nrt, P);
+        if constexpr (J == 2u) {
+            const uint64_t pas_p = uint64_t(pp.bx) * 64u;
+            const uint8_t* xsrc = reinterpret_cast<const uint8_t*>(pp.xb) + uint64_t(c / pp.k) * PF_PIECES_BF * pas_p +
+                                  16u * lg;
+            const uint32_t wu = uniforme32(w);
+            auto produit = [&](auto np, auto kb) {
+                constexpr uint32_t NP = decltype(np)::value, KB = decltype(kb)::value;
+                if (nrt == 4u)
+                    produit_bf16<NP, KB, 4>(acc, xsrc, pas_p, wu, B, base + PF_A, a_sa, lr, lg);
+                else if (nrt == 2u)
+                    produit_bf16<NP, KB, 2>(acc, xsrc, pas_p, wu, B, base + PF_A, a_sa, lr, lg);
+                else
+                    produit_bf16<NP, KB, 1>(acc, xsrc, pas_p, wu, B, base + PF_A, a_sa, lr, lg);
+            };
+            using U = uint32_t;
+            if (P == 1u)
+                produit(std::integral_constant<U, 1>{}, std::integral_constant<U, 6>{});
+            else if (P == 2u)
+                produit(std::integral_constant<U, 2>{}, std::integral_constant<U, 3>{});
+            else if (P == 3u)
+                produit(std::integral_constant<U, 3>{}, std::integral_constant<U, 2>{});
+        } else {
+            const Operande_b ob{bq + uint64_t(c) * PF_PIECES * Bp * 32u, bs + uint64_t(c) * PF_PIECES * Bp, Bp,
+                                bloc_b, demi_b, lg, valide};
+            const uint32_t npp = (P + 1u) / 2u, U = nks * npp;
+            for (uint32_t u = w; u < U; u += 16u) {  // wave-uniform
+                const uint32_t ks = u / npp, p0 = 2u * (u - ks * npp);
+                u32x4 a[4];
+                uint32_t sa[4];
+                operandes_a(ks, a, sa);
+                if (p0 + 1u < P)
+                    produit_pieces<2>(acc, a, sa, ob, p0, ks, nrt, P);
+                else
+                    produit_pieces<1>(acc, a, sa, ob, p0, ks, nrt, P);
+            }
         }
 #pragma unroll
         for (uint32_t rt = 0; rt < 4; ++rt)
@@ -636,7 +743,7 @@ uint32_t rb_de(uint32_t B, uint32_t N) {
 }
 
 struct Disposition {
-    uint64_t pieces, compte, debut, paires, ech, pas_ech, xq, xs, gu, aq, as, s, total;
+    uint64_t pieces, compte, debut, paires, ech, pas_ech, xb, gu, aq, as, s, total;
 };
 
 int disposer(const trc_dims_expert* dims, uint32_t E, uint32_t T, uint32_t k, uint32_t n_codes, Disposition& d) {
@@ -673,10 +780,8 @@ int disposer(const trc_dims_expert* dims, uint32_t E, uint32_t T, uint32_t k, ui
     d.pas_ech = trc::octets_entrees(Rm, C);
     d.ech = p;
     p += 3ull * E * d.pas_ech;
-    d.xq = p;
-    p += al(32ull * T * trc::PF_PIECES * bp0);
-    d.xs = p;
-    p += al(1ull * T * trc::PF_PIECES * bp0);
+    d.xb = p;
+    p += al(64ull * T * trc::PF_PIECES_BF * (C / 32u + 1u));
     d.gu = p;
     p += al(4ull * n * 2u * R);
     d.aq = p;
@@ -737,8 +842,7 @@ extern "C" int trc_prefill_moe(trc_vue repertoire, uint32_t experts, trc_vue lut
     pp.poids = poids.adresse;
     pp.x = x.adresse;
     pp.residus = residus.adresse;
-    pp.xq = b + d.xq;
-    pp.xs = b + d.xs;
+    pp.xb = b + d.xb;
     pp.gu = b + d.gu;
     pp.aq = b + d.aq;
     pp.as = b + d.as;
@@ -750,6 +854,7 @@ extern "C" int trc_prefill_moe(trc_vue repertoire, uint32_t experts, trc_vue lut
         pp.rb[j] = rb_de(dims->colonnes[j] / 32, n_codes);
     }
     pp.T = T;
+    pp.bx = C / 32u + 1u;
     pp.k = k;
     pp.E = experts;
     pp.D = D;
@@ -771,7 +876,7 @@ extern "C" int trc_prefill_moe(trc_vue repertoire, uint32_t experts, trc_vue lut
     const uint32_t* l = reinterpret_cast<const uint32_t*>(luts.adresse);
     const uint32_t Rm = D > R ? D : R;
     TRC_LANCER(prefill_grouper, dim3(1), dim3(1024), f, pp, ctl);
-    TRC_LANCER(prefill_quant_x, dim3(T), dim3(trc::PF_BP_MAX), f, pp);
+    TRC_LANCER(prefill_quant_x, dim3(T), dim3(trc::PF_QX_FILS), f, pp);
     r = trc::lancer_echelles_prefill(pm, Rm, C, n_delta, l, ctl, f);
     if (r != TRC_OK) return r;
     TRC_LANCER(prefill_mfma_gu, dim3((R + pp.rb[0] - 1) / pp.rb[0], 2 * experts), dim3(trc::PF_FILS), f, pp, l, ctl);
