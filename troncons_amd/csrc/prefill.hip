@@ -1,7 +1,8 @@
 // prefill.hip — batched prefill of a resident MoE layer on gfx950 (T positions, top-k each): every
 // chosen expert is rANS-decoded once, band of rows by band of rows, into LDS as MXFP4 (E2M1 codes,
-// E8M0 block scales) and multiplied against all the positions that chose it on the block-scaled FP4
-// MFMA (v_mfma_scale_f32_16x16x128_f8f6f4, fp32 accumulation). The reference runs the same layer as
+// E8M0 block scales) and multiplied against all the positions that chose it on the bf16 MFMA
+// (v_mfma_f32_16x16x32_bf16, fp32 accumulation), the weights converted to bf16 (exactly) where they
+// are read and the activations split into exact bf16 pieces. The reference runs the same layer as
 // one decode per chosen expert then one GEMV chain per (position, slot) (trc-ordo/src/lib.rs:782-945,
 // expert_pos and combiner_pos, trc-modele/src/lib.rs:688-710). Launches, one stream:
 //
@@ -11,32 +12,21 @@
 //   fusion_echelles       (prefill mode) DELTA -> block entries of every chosen expert's matrices;
 //   prefill_mfma_gu       gate and up: bands decoded into LDS, bf16 MFMA (the weights converted from
 //                         MXFP4 where they are read) against the expert's positions, + bias -> gu;
-//   prefill_swiglu_quant  act = swiglu_oai(gate, up) per pair, split into fp8 pieces;
-//   prefill_mfma_bas      down -> s, one row of D per pair (the reference's pos.s layout);
+//   prefill_swiglu_quant  act = swiglu_oai(gate, up) per pair, split into bf16 pieces;
+//   prefill_mfma_bas      down -> s, one row of D per pair (the reference's pos.s layout), bf16 MFMA;
 //   prefill_combiner      x_i += ((w0 s_i0 + w1 s_i1) + ...) in slot order, no FMA.
 //
-// x in bf16 pieces (gate and up). x_f32 = hi + mid + lo with hi = bf16(x), mid = bf16(x - hi) and
-// lo = bf16(x - hi - mid), each difference exact in f32: hi leaves at most 16 significant bits, mid
-// at most 8, which lo holds. A weight, e2m1 x 2^(e - 127), is exact in bf16 too, so every product
-// of v_mfma_f32_16x16x32_bf16 is exact and y differs from the f32 GEMV only by the fp32 accumulation
-// order. Pieces that are zero for every position are skipped: bf16 activations need one.
+// Activations in bf16 pieces. A row v of f32 activations (x for gate and up, act for down) is
+// written as v = hi + mid + lo with hi = bf16(v), mid = bf16(v - hi) and lo = bf16(v - hi - mid),
+// each difference exact in f32: hi leaves at most 16 significant bits, mid at most 8, which lo
+// holds. A weight, e2m1 x 2^(e - 127), is exact in bf16 too, so every product of
+// v_mfma_f32_16x16x32_bf16 is exact and y differs from the f32 GEMV only by the fp32 accumulation
+// order. Pieces that are zero for every row of the call are skipped: bf16 activations need one.
 //
-// act in pieces (down). The MFMA's B operand here is fp8 E4M3 with one E8M0 scale per 32 values,
-// and the MFMA adds the 32 products of a block in a fixed-point sum that keeps about 14 bits below
-// the block's largest product. A block of activations a is written as a = sum_p q_p 2^k_p: piece p
-// takes, at scale 2^k_p (the residual's maximum in [128, 256) * 2^k_p), the round-to-nearest E4M3 of
-// every residual value whose scaled magnitude is at least 8 and leaves the smaller ones to the next
-// piece. Piece values stay in {0} u [8, 256], so products (E2M1 x E4M3, 6 significant bits) span at
-// most 8 binades and every block sum is exact; each piece takes at least 4 bits off the residual, and
-// pieces stop once it is below 2^-20 of the block's maximum (5 pieces at most). y then differs from
-// the f32 GEMV by the fp32 accumulation order and that 2^-20 remainder.
-//
-// MFMA operand layout (16x16x128, measured on gfx950): A (fp4, 16 bytes per lane): lane g*16 + r
-// holds row r, K = 32 g + j at nibble j (low nibble first). B (fp8, 32 bytes per lane): lane g*16 + n
-// holds column n, K = 16 g + b at bytes b < 16 and K = 64 + 16 g + (b - 16) at bytes b >= 16. Scales:
-// lane g*16 + r (+n) gives the scale of 32-block g. C: lane g*16 + n holds rows 4 g .. 4 g + 3 of
-// column n. A weight block (16 code bytes: byte i holds weights i and 16 + i) is one lane's A data,
-// so piece byte j of a block holds activation (j >> 1) + 16 (j & 1).
+// MFMA operand layout (v_mfma_f32_16x16x32_bf16): lane g*16 + r holds 8 K values of row r of A and
+// the same 8 K values of column r of B; C: lane g*16 + n holds rows 4 g .. 4 g + 3 of column n. A
+// weight block is 16 code bytes, byte i holding weights i (low nibble) and 16 + i, so lane g takes
+// bytes 4g .. 4g + 3 and a piece block stores value (j >> 1) + 16 (j & 1) at position j.
 #include <hip/hip_runtime.h>
 
 #include <cstring>
@@ -52,9 +42,8 @@ namespace trc {
 
 constexpr uint32_t PF_FILS = 1024;        // 16 wavefronts: 32 tiles decoded per band
 constexpr uint32_t PF_NMAX = 16;          // macro-steps per CODES_CTX tile held in registers
-constexpr uint32_t PF_PIECES = 5;         // fp8 pieces per act block
-constexpr uint32_t PF_PIECES_BF = 3;      // bf16 pieces per x block
-constexpr uint32_t PF_QX_FILS = 192;      // prefill_quant_x threads: one per x block, PF_BP_MAX + 1 at most
+constexpr uint32_t PF_PIECES_BF = 3;      // bf16 pieces per activation block
+constexpr uint32_t PF_Q_FILS = 192;       // threads of the piece kernels: one per block, PF_BP_MAX + 1 at most
 constexpr uint32_t PF_BP_MAX = 128;       // padded blocks per row (4096 columns)
 constexpr uint32_t PF_PAIRES_MAX = 16384; // positions x k per call
 constexpr uint32_t ECHELLE_UN = 127u;     // E8M0 1.0
@@ -71,7 +60,6 @@ __host__ __device__ inline uint32_t pf_part(uint32_t rb, uint32_t b) { return (p
 __host__ __device__ inline uint32_t pf_part_octets(uint32_t rb) { return (rb / 16u) * 16u * 64u * 16u; }
 __host__ __device__ inline bool pf_lds_tient(uint32_t rb, uint32_t b) { return pf_part(rb, b) + pf_part_octets(rb) <= LDS_GEMV; }
 
-typedef int i32x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
@@ -82,7 +70,7 @@ struct ParamsPrefill {
     uint64_t compte;       // u32[E] pairs per expert
     uint64_t debut;        // u32[E] first pair of expert e in `paires`
     uint64_t paires;       // u32[T*k] pair c = i*k + slot, grouped by expert
-    uint64_t pieces;       // u32[4]: [0] bf16 pieces used by x, [1] fp8 pieces used by act
+    uint64_t pieces;       // u32[4]: [0] bf16 pieces used by x, [1] by act
     uint64_t indices;      // u32[T*k] chosen experts
     uint64_t poids;        // f32[T*k] their weights
     uint64_t x;            // f32[T][C]
@@ -91,59 +79,39 @@ struct ParamsPrefill {
                            // of the weight block's nibbles: x[32 b + (j >> 1) + 16 (j & 1)]; block
                            // b = C/32 (the last of the bx = C/32 + 1) is zero
     uint64_t gu;           // f32[T*k][2][R]
-    uint64_t aq, as;       // act pieces per pair, bp[2] blocks per row
+    uint64_t ab;           // act pieces per pair, like xb with bact blocks per piece row
     uint64_t s;            // f32[T*k][D]
     uint32_t lignes[3], colonnes[3];
-    uint32_t bp[3];        // padded blocks per row (multiple of 4)
     uint32_t rb[3];        // rows per band (16, 32 or 64)
     uint32_t T, k, E, D;
-    uint32_t bx;           // x blocks per piece row: C/32 + 1
+    uint32_t bx, bact;     // blocks per piece row of x and act: C/32 + 1, R/32 + 1
 };
 
-// Splits 32 values (natural order a[0..31]) into pieces: writes PF_PIECES x 32 bytes (piece stride
-// `pas_q` bytes, byte j = value (j >> 1) + 16 (j & 1)) and PF_PIECES scale bytes (stride `pas_s`);
-// returns the pieces used.
-__device__ __forceinline__ uint32_t pieces_bloc(const float (&a)[32], uint8_t* q, uint64_t pas_q, uint8_t* sc,
-                                                uint64_t pas_s) {
-    float r[32];
-#pragma unroll
-    for (uint32_t j = 0; j < 32; ++j) r[j] = a[(j >> 1) + 16u * (j & 1u)];
-    float m0 = 0.0f;
-#pragma unroll
-    for (uint32_t j = 0; j < 32; ++j) m0 = fmaxf(m0, fabsf(r[j]));
-    const float seuil = m0 * 0x1p-20f;
+// Splits 32 values (natural order a[0..31]) into PF_PIECES_BF bf16 pieces of 64 bytes each (piece
+// stride `pas` bytes), word q holding values q (low half) and q + 16 (high half); returns the pieces
+// that are not all zero. An infinite or NaN value stays whole in hi (its residual is set to 0), so a
+// product with it is what the f32 product is.
+__device__ __forceinline__ uint32_t pieces_bf16(float (&a)[32], uint8_t* dst, uint64_t pas) {
     uint32_t P = 0;
-    for (uint32_t p = 0; p < PF_PIECES; ++p) {
-        float mr = 0.0f;
 #pragma unroll
-        for (uint32_t j = 0; j < 32; ++j) mr = fmaxf(mr, fabsf(r[j]));
-        const int E = int((__float_as_uint(mr) >> 23) & 255u) - 127;
-        const bool fini = !(mr > seuil) || E < -119;
-        u32x4 mots[2] = {u32x4{0u, 0u, 0u, 0u}, u32x4{0u, 0u, 0u, 0u}};
-        int k = 0;
-        if (!fini) {
-            k = E - 7;  // |r| 2^-k < 256
+    for (uint32_t p = 0; p < PF_PIECES_BF; ++p) {
+        uint32_t mots[16];
+        uint32_t nz = 0;
 #pragma unroll
-            for (uint32_t g = 0; g < 8; ++g) {
-                float v[4];
-#pragma unroll
-                for (uint32_t i = 0; i < 4; ++i) {
-                    const float t = __builtin_amdgcn_ldexpf(r[4 * g + i], -k);
-                    v[i] = fabsf(t) >= 8.0f ? t : 0.0f;  // smaller values wait for the next piece
-                }
-                int w = __builtin_amdgcn_cvt_pk_fp8_f32(v[0], v[1], 0, false);
-                w = __builtin_amdgcn_cvt_pk_fp8_f32(v[2], v[3], w, true);
-                r[4 * g + 0] -= __builtin_amdgcn_ldexpf(__builtin_amdgcn_cvt_f32_fp8(w, 0), k);  // exact
-                r[4 * g + 1] -= __builtin_amdgcn_ldexpf(__builtin_amdgcn_cvt_f32_fp8(w, 1), k);
-                r[4 * g + 2] -= __builtin_amdgcn_ldexpf(__builtin_amdgcn_cvt_f32_fp8(w, 2), k);
-                r[4 * g + 3] -= __builtin_amdgcn_ldexpf(__builtin_amdgcn_cvt_f32_fp8(w, 3), k);
-                mots[g >> 2][g & 3u] = uint32_t(w);
-            }
-            P = p + 1;
+        for (uint32_t q = 0; q < 16; ++q) {
+            const __bf16 h0 = __bf16(a[q]), h1 = __bf16(a[q + 16]);
+            const uint32_t b0 = __builtin_bit_cast(uint16_t, h0), b1 = __builtin_bit_cast(uint16_t, h1);
+            const float f0 = __uint_as_float(b0 << 16), f1 = __uint_as_float(b1 << 16);
+            a[q] = __builtin_isfinite(f0) ? a[q] - f0 : 0.0f;  // exact
+            a[q + 16] = __builtin_isfinite(f1) ? a[q + 16] - f1 : 0.0f;
+            mots[q] = b0 | (b1 << 16);
+            nz |= mots[q];
         }
-        *reinterpret_cast<u32x4*>(q + p * pas_q) = mots[0];
-        *reinterpret_cast<u32x4*>(q + p * pas_q + 16) = mots[1];
-        sc[p * pas_s] = uint8_t(fini ? ECHELLE_UN : uint32_t(k + 127));
+#pragma unroll
+        for (uint32_t g = 0; g < 4; ++g)
+            *reinterpret_cast<u32x4*>(dst + p * pas + 16u * g) =
+                u32x4{mots[4 * g], mots[4 * g + 1], mots[4 * g + 2], mots[4 * g + 3]};
+        if (nz & 0x7FFF7FFFu) P = p + 1u;
     }
     return P;
 }
@@ -236,11 +204,8 @@ prefill_grouper(ParamsPrefill pp, uint32_t* __restrict__ controle) {
     }
 }
 
-// x pieces: block (position i), thread b = column block b (block B gets zeros). Word q
-// of a 64-byte piece block holds values q (low half) and q + 16 (high half), as byte q of a weight
-// block holds weights q and q + 16. An infinite or NaN value stays whole in hi (its residual is set
-// to 0), so a product with it is what the f32 product is.
-extern "C" __global__ void __launch_bounds__(trc::PF_QX_FILS)
+// x pieces: block (position i), thread b = column block b (block B gets zeros).
+extern "C" __global__ void __launch_bounds__(trc::PF_Q_FILS)
 prefill_quant_x(ParamsPrefill pp) {
     using namespace trc;
     const uint32_t i = blockIdx.x, b = threadIdx.x;
@@ -258,41 +223,23 @@ prefill_quant_x(ParamsPrefill pp) {
             a[4 * g + 2] = v.z;
             a[4 * g + 3] = v.w;
         }
-        uint8_t* dst = reinterpret_cast<uint8_t*>(pp.xb) + (uint64_t(i) * PF_PIECES_BF * Bx + b) * 64u;
-#pragma unroll
-        for (uint32_t p = 0; p < PF_PIECES_BF; ++p) {
-            uint32_t mots[16];
-            uint32_t nz = 0;
-#pragma unroll
-            for (uint32_t q = 0; q < 16; ++q) {
-                const __bf16 h0 = __bf16(a[q]), h1 = __bf16(a[q + 16]);
-                const uint32_t b0 = __builtin_bit_cast(uint16_t, h0), b1 = __builtin_bit_cast(uint16_t, h1);
-                const float f0 = __uint_as_float(b0 << 16), f1 = __uint_as_float(b1 << 16);
-                a[q] = __builtin_isfinite(f0) ? a[q] - f0 : 0.0f;  // exact
-                a[q + 16] = __builtin_isfinite(f1) ? a[q + 16] - f1 : 0.0f;
-                mots[q] = b0 | (b1 << 16);
-                nz |= mots[q];
-            }
-#pragma unroll
-            for (uint32_t g = 0; g < 4; ++g)
-                *reinterpret_cast<u32x4*>(dst + uint64_t(p) * Bx * 64u + 16u * g) =
-                    u32x4{mots[4 * g], mots[4 * g + 1], mots[4 * g + 2], mots[4 * g + 3]};
-            if (nz & 0x7FFF7FFFu) P = p + 1u;
-        }
+        P = pieces_bf16(a, reinterpret_cast<uint8_t*>(pp.xb) + (uint64_t(i) * PF_PIECES_BF * Bx + b) * 64u,
+                        uint64_t(Bx) * 64u);
     }
     P = max_vague(P);
     if (__lane_id() == 0 && P) atomicMax(reinterpret_cast<uint32_t*>(pp.pieces), P);
 }
 
-// act pieces: block (pair c), thread b = block b of act = swiglu_oai(gate, up) rows 32b .. 32b+31.
-extern "C" __global__ void __launch_bounds__(trc::PF_BP_MAX)
+// act pieces: block (pair c), thread b = block b of act = swiglu_oai(gate, up) rows 32b .. 32b+31
+// (block R/32 gets zeros).
+extern "C" __global__ void __launch_bounds__(trc::PF_Q_FILS)
 prefill_swiglu_quant(ParamsPrefill pp) {
     using namespace trc;
     const uint32_t c = blockIdx.x, b = threadIdx.x;
-    const uint32_t R = pp.lignes[0], B2 = R / 32u, Bp = pp.bp[2];
+    const uint32_t R = pp.lignes[0], B2 = R / 32u, Ba = pp.bact;
     if (reinterpret_cast<const uint32_t*>(pp.indices)[c] >= pp.E) return;
     uint32_t P = 0;
-    if (b < Bp) {
+    if (b < Ba) {
         float a[32];
         const float* g = reinterpret_cast<const float*>(pp.gu) + uint64_t(c) * 2u * R;
         const float* u = g + R;
@@ -302,70 +249,14 @@ prefill_swiglu_quant(ParamsPrefill pp) {
 #pragma unroll
             for (uint32_t t = 0; t < 32; ++t) a[t] = swiglu_oai_f(g[32u * b + t], u[32u * b + t]);
         }
-        const uint64_t base = uint64_t(c) * PF_PIECES * Bp + b;
-        P = pieces_bloc(a, reinterpret_cast<uint8_t*>(pp.aq) + base * 32u, uint64_t(Bp) * 32u,
-                        reinterpret_cast<uint8_t*>(pp.as) + base, Bp);
+        P = pieces_bf16(a, reinterpret_cast<uint8_t*>(pp.ab) + (uint64_t(c) * PF_PIECES_BF * Ba + b) * 64u,
+                        uint64_t(Ba) * 64u);
     }
     P = max_vague(P);
     if (__lane_id() == 0 && P) atomicMax(reinterpret_cast<uint32_t*>(pp.pieces) + 1, P);
 }
 
 namespace trc {
-
-// B operand source of one column (pair) of a 16-pair tile: its pieces, PF_PIECES x Bp blocks of 32
-// bytes, and their scales.
-struct Operande_b {
-    const uint8_t* q;
-    const uint8_t* s;
-    uint32_t Bp, bloc, demi, lg;
-    bool valide;
-};
-
-// acc[rt] += A_rt (k-step ks) x B over pieces p0 .. p0 + NP - 1 for the nrt row tiles of the band: the
-// pieces' loads are issued before the MFMAs, and each feeds every row tile. This lane's B bytes 0-15
-// are half `demi` of block 4 ks + `bloc`, bytes 16-31 the same half of block 4 ks + 2 + `bloc`; its
-// scale is block 4 ks + lg's. Pieces p0 .. p0 + NP - 1 with p < P take part (P wave-uniform); the
-// addresses of invalid columns or unused pieces are clamped to piece 0 of the column's first valid
-// source, so no load sits under a branch.
-template <uint32_t NP>
-__device__ __forceinline__ void produit_pieces(f32x4 (&acc)[4], const u32x4 (&a)[4], const uint32_t (&sa)[4],
-                                               const Operande_b& ob, uint32_t p0, uint32_t ks, uint32_t nrt,
-                                               uint32_t P) {
-    u32x4 b0[NP], b1[NP];
-    uint32_t sb[NP];
-#pragma unroll
-    for (uint32_t p = 0; p < NP; ++p) {
-        const bool pris = ob.valide && p0 + p < P;
-        const uint64_t o = uint64_t(pris ? p0 + p : 0u) * ob.Bp + 4u * ks;
-        b0[p] = *glob<u32x4>(ob.q + (o + ob.bloc) * 32u + ob.demi);
-        b1[p] = *glob<u32x4>(ob.q + (o + 2u + ob.bloc) * 32u + ob.demi);
-        sb[p] = ob.s[o + ob.lg];
-        if (!pris) {
-            b0[p] = b1[p] = u32x4{0u, 0u, 0u, 0u};
-            sb[p] = ECHELLE_UN;
-        }
-    }
-    i32x8 ra[4];
-#pragma unroll
-    for (uint32_t rt = 0; rt < 4; ++rt) ra[rt] = i32x8{int(a[rt].x), int(a[rt].y), int(a[rt].z), int(a[rt].w), 0, 0, 0, 0};
-#pragma unroll
-    for (uint32_t p = 0; p < NP; ++p) {
-        if (p0 + p >= P) break;  // wave-uniform
-        const i32x8 rb = {int(b0[p].x), int(b0[p].y), int(b0[p].z), int(b0[p].w),
-                          int(b1[p].x), int(b1[p].y), int(b1[p].z), int(b1[p].w)};
-#pragma unroll
-        for (uint32_t rt = 0; rt < 4; ++rt)
-            if (rt < nrt)  // wave-uniform
-                acc[rt] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ra[rt], rb, acc[rt], 4, 0, 0, int(sa[rt]), 0,
-                                                                           int(sb[p]));
-    }
-    // The result of this MFMA (A fp4, B fp8) reaches its registers 11 to 12 wait states after issue
-    // (measured); the compiler's hazard padding before a VALU read of it can be shorter. 16 wait states
-    // here, fenced so that nothing is scheduled across them, cover every reader.
-    __builtin_amdgcn_sched_barrier(0);
-    asm volatile("s_nop 15");
-    __builtin_amdgcn_sched_barrier(0);
-}
 
 // acc[rt] += A_rt x B over the k-steps ks = w, w + 16, ... < B (one 32-value block each) and the
 // pieces p < NP of x, for the nrt row tiles of the band, on v_mfma_f32_16x16x32_bf16. Lane g*16 + n
@@ -516,8 +407,9 @@ __device__ __forceinline__ void poser_tour(const TourBande& tb, uint32_t t, uint
 
 // One band of rows [r0, r0 + nl) of matrix j of expert e against the expert's pairs: its tiles
 // decoded in up to two rounds of 32 (one tile per half-wavefront a round), stored in LDS as MXFP4,
-// then the block-scaled MFMA: each of the 16 waves takes every row tile of the band (up to 4) over
-// its share of K, so that each B load feeds every row tile and B is read once per band.
+// then the bf16 MFMA (weights converted where they are read): each of the 16 waves takes every row
+// tile of the band (up to 4) over its share of K, so that each B load feeds every row tile and B is
+// read once per band.
 template <uint32_t J>
 __device__ __forceinline__ void prefill_bande(const ParamsPrefill& pp, const uint32_t* __restrict__ luts,
                                               uint32_t* __restrict__ controle, uint8_t* lds) {
@@ -525,7 +417,7 @@ __device__ __forceinline__ void prefill_bande(const ParamsPrefill& pp, const uin
     const uint32_t n_e = uniforme32(reinterpret_cast<const uint32_t*>(pp.compte)[e]);
     if (n_e == 0u) return;
     const uint32_t R = choisir(pp.lignes, j), C = choisir(pp.colonnes, j), B = C / 32u;
-    const uint32_t Bp = choisir(pp.bp, j), RB = choisir(pp.rb, j);
+    const uint32_t RB = choisir(pp.rb, j);
     const uint32_t r0 = blockIdx.x * RB;
     if (r0 >= R) return;
     const uint32_t nl = min(RB, R - r0);
@@ -564,8 +456,7 @@ __device__ __forceinline__ void prefill_bande(const ParamsPrefill& pp, const uin
     const uint32_t haut = lane >= 32u ? 1u : 0u;
     poser_tour(tour0, t00 + haut, N, ba, bb, base, a_sa);
     poser_tour(tour1, t01 + haut, N, ba, bb, base, a_sa);
-    // padding: rows nl .. RB - 1 of a last, partial band (zero codes, scale 1); blocks past B in the
-    // last k-step are zeroed where they are read
+    // padding: rows nl .. RB - 1 of a last, partial band (zero codes, scale 1)
     for (uint32_t i = threadIdx.x; i < (RB - nl) * B; i += blockDim.x) {
         const uint32_t o = nl * B + i;
         ecrire_lds<u32x4>(base + PF_A + 16u * o, u32x4{0u, 0u, 0u, 0u});
@@ -573,84 +464,45 @@ __device__ __forceinline__ void prefill_bande(const ParamsPrefill& pp, const uin
     }
     __syncthreads();
 
-    // ---- MFMA: every wave takes all nrt row tiles and the units u = w, w + 16, ... of (k-step ks of 4
-    // blocks, pieces 2 pq and 2 pq + 1), K split 16 ways; the partial sums are added in wave order.
-    // Each B load feeds every row tile, and B is read once per band.
-    const uint32_t nks = (B + 3u) / 4u, nrt = RB / 16u;
+    // ---- MFMA: every wave takes all nrt row tiles and the k-steps (blocks) ks = w, w + 16, ..., K
+    // split 16 ways; the partial sums are added in wave order. Each B load feeds every row tile, and
+    // B is read once per band.
+    const uint32_t nrt = RB / 16u;
     const uint32_t lr = lane & 15u, lg = lane >> 4;
-    // the A operands of k-step ks (all row tiles), read from LDS where they are used; blocks past B
-    // (the last k-step of a row whose B is not a multiple of 4) are zero with scale 1
-    auto operandes_a = [&](uint32_t ks, u32x4 (&a)[4], uint32_t (&sc)[4]) {
-        const uint32_t blk = 4u * ks + lg;
-        const bool dans = blk < B;
-#pragma unroll
-        for (uint32_t rt = 0; rt < 4; ++rt) {
-            if (rt < nrt) {  // wave-uniform
-                const uint32_t o = (16u * rt + lr) * B + (dans ? blk : B - 1u);
-                const u32x4 v = lire_lds<u32x4>(base + PF_A + 16u * o);
-                const uint32_t e = lire_lds<uint8_t>(a_sa + o);
-                a[rt] = dans ? v : u32x4{0u, 0u, 0u, 0u};
-                sc[rt] = dans ? e : ECHELLE_UN;
-            } else {
-                a[rt] = u32x4{0u, 0u, 0u, 0u};
-                sc[rt] = ECHELLE_UN;
-            }
-        }
-    };
-    const uint32_t P = uniforme32(J == 2u ? min(reinterpret_cast<const uint32_t*>(pp.pieces)[0], PF_PIECES_BF)
-                                          : min(reinterpret_cast<const uint32_t*>(pp.pieces)[1], PF_PIECES));
+    const uint32_t P = uniforme32(min(reinterpret_cast<const uint32_t*>(pp.pieces)[J == 2u ? 0 : 1], PF_PIECES_BF));
     const uint32_t debut_e = uniforme32(reinterpret_cast<const uint32_t*>(pp.debut)[e]);
     const uint32_t* paires = reinterpret_cast<const uint32_t*>(pp.paires);
-    const uint8_t* bq = reinterpret_cast<const uint8_t*>(pp.aq);
-    const uint8_t* bs = reinterpret_cast<const uint8_t*>(pp.as);
     const float* biais = reinterpret_cast<const float*>(m.biais.p);
-    const uint32_t demi_b = 16u * (lg & 1u), bloc_b = lg >> 1;
+    const uint64_t pas_p = uint64_t(J == 2u ? pp.bx : pp.bact) * 64u;
+    const uint8_t* bsrc = reinterpret_cast<const uint8_t*>(J == 2u ? pp.xb : pp.ab) + 16u * lg;
+    const uint32_t wu = uniforme32(w);
     const uint32_t n_tt = (n_e + 15u) / 16u;
     uint32_t c_suiv = n_e > lr ? paires[debut_e + lr] : 0u;
     for (uint32_t tt = 0; tt < n_tt; ++tt) {
         const uint32_t tok = 16u * tt + lr;
-        const bool valide = tok < n_e;
         const uint32_t c = c_suiv;
         c_suiv = tok + 16u < n_e ? paires[debut_e + tok + 16u] : 0u;
+        // column source: position c / k's x for gate and up, pair c's act for down
+        const uint8_t* src = bsrc + uint64_t(J == 2u ? c / pp.k : c) * PF_PIECES_BF * pas_p;
         f32x4 acc[4];
 #pragma unroll
         for (uint32_t rt = 0; rt < 4; ++rt) acc[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
-        if constexpr (J == 2u) {
-            const uint64_t pas_p = uint64_t(pp.bx) * 64u;
-            const uint8_t* xsrc = reinterpret_cast<const uint8_t*>(pp.xb) + uint64_t(c / pp.k) * PF_PIECES_BF * pas_p +
-                                  16u * lg;
-            const uint32_t wu = uniforme32(w);
-            auto produit = [&](auto np, auto kb) {
-                constexpr uint32_t NP = decltype(np)::value, KB = decltype(kb)::value;
-                if (nrt == 4u)
-                    produit_bf16<NP, KB, 4>(acc, xsrc, pas_p, wu, B, base + PF_A, a_sa, lr, lg);
-                else if (nrt == 2u)
-                    produit_bf16<NP, KB, 2>(acc, xsrc, pas_p, wu, B, base + PF_A, a_sa, lr, lg);
-                else
-                    produit_bf16<NP, KB, 1>(acc, xsrc, pas_p, wu, B, base + PF_A, a_sa, lr, lg);
-            };
-            using U = uint32_t;
-            if (P == 1u)
-                produit(std::integral_constant<U, 1>{}, std::integral_constant<U, 6>{});
-            else if (P == 2u)
-                produit(std::integral_constant<U, 2>{}, std::integral_constant<U, 3>{});
-            else if (P == 3u)
-                produit(std::integral_constant<U, 3>{}, std::integral_constant<U, 2>{});
-        } else {
-            const Operande_b ob{bq + uint64_t(c) * PF_PIECES * Bp * 32u, bs + uint64_t(c) * PF_PIECES * Bp, Bp,
-                                bloc_b, demi_b, lg, valide};
-            const uint32_t npp = (P + 1u) / 2u, U = nks * npp;
-            for (uint32_t u = w; u < U; u += 16u) {  // wave-uniform
-                const uint32_t ks = u / npp, p0 = 2u * (u - ks * npp);
-                u32x4 a[4];
-                uint32_t sa[4];
-                operandes_a(ks, a, sa);
-                if (p0 + 1u < P)
-                    produit_pieces<2>(acc, a, sa, ob, p0, ks, nrt, P);
-                else
-                    produit_pieces<1>(acc, a, sa, ob, p0, ks, nrt, P);
-            }
-        }
+        auto produit = [&](auto np, auto kb) {
+            constexpr uint32_t NP = decltype(np)::value, KB = decltype(kb)::value;
+            if (nrt == 4u)
+                produit_bf16<NP, KB, 4>(acc, src, pas_p, wu, B, base + PF_A, a_sa, lr, lg);
+            else if (nrt == 2u)
+                produit_bf16<NP, KB, 2>(acc, src, pas_p, wu, B, base + PF_A, a_sa, lr, lg);
+            else
+                produit_bf16<NP, KB, 1>(acc, src, pas_p, wu, B, base + PF_A, a_sa, lr, lg);
+        };
+        using U = uint32_t;
+        if (P == 1u)
+            produit(std::integral_constant<U, 1>{}, std::integral_constant<U, 6>{});
+        else if (P == 2u)
+            produit(std::integral_constant<U, 2>{}, std::integral_constant<U, 3>{});
+        else if (P == 3u)
+            produit(std::integral_constant<U, 3>{}, std::integral_constant<U, 2>{});
 #pragma unroll
         for (uint32_t rt = 0; rt < 4; ++rt)
             if (rt < nrt) ecrire_lds<f32x4>(a_part + ((rt * 16u + w) * 64u + lane) * 16u, acc[rt]);
@@ -731,7 +583,6 @@ namespace {
 using trc::usage;
 
 uint64_t al(uint64_t x) { return (x + 255u) & ~uint64_t(255); }
-uint32_t bp_de(uint32_t C) { return ((C / 32u + 3u) / 4u) * 4u; }
 
 // Rows per band: 64, 32 or 16, the most whose CODES_CTX tiles (N macro-steps of 8 blocks each) fit
 // the 64 tiles a block decodes in two rounds and whose codes, scales and partial sums fit the LDS;
@@ -743,7 +594,7 @@ uint32_t rb_de(uint32_t B, uint32_t N) {
 }
 
 struct Disposition {
-    uint64_t pieces, compte, debut, paires, ech, pas_ech, xb, gu, aq, as, s, total;
+    uint64_t pieces, compte, debut, paires, ech, pas_ech, xb, gu, ab, s, total;
 };
 
 int disposer(const trc_dims_expert* dims, uint32_t E, uint32_t T, uint32_t k, uint32_t n_codes, Disposition& d) {
@@ -767,7 +618,6 @@ int disposer(const trc_dims_expert* dims, uint32_t E, uint32_t T, uint32_t k, ui
         return usage("prefill : %u positions x %u (au plus %u paires)", T, k, trc::PF_PAIRES_MAX);
     const uint32_t Rm = D > R ? D : R;
     const uint64_t n = uint64_t(T) * k;
-    const uint64_t bp0 = bp_de(C), bp2 = bp_de(R);
     uint64_t p = 0;
     d.pieces = p;
     p += al(16);
@@ -784,10 +634,8 @@ int disposer(const trc_dims_expert* dims, uint32_t E, uint32_t T, uint32_t k, ui
     p += al(64ull * T * trc::PF_PIECES_BF * (C / 32u + 1u));
     d.gu = p;
     p += al(4ull * n * 2u * R);
-    d.aq = p;
-    p += al(32ull * n * trc::PF_PIECES * bp2);
-    d.as = p;
-    p += al(1ull * n * trc::PF_PIECES * bp2);
+    d.ab = p;
+    p += al(64ull * n * trc::PF_PIECES_BF * (R / 32u + 1u));
     d.s = p;
     p += al(4ull * n * D);
     d.total = p;
@@ -844,17 +692,16 @@ extern "C" int trc_prefill_moe(trc_vue repertoire, uint32_t experts, trc_vue lut
     pp.residus = residus.adresse;
     pp.xb = b + d.xb;
     pp.gu = b + d.gu;
-    pp.aq = b + d.aq;
-    pp.as = b + d.as;
+    pp.ab = b + d.ab;
     pp.s = b + d.s;
     for (int j = 0; j < 3; ++j) {
         pp.lignes[j] = dims->lignes[j];
         pp.colonnes[j] = dims->colonnes[j];
-        pp.bp[j] = bp_de(dims->colonnes[j]);
         pp.rb[j] = rb_de(dims->colonnes[j] / 32, n_codes);
     }
     pp.T = T;
     pp.bx = C / 32u + 1u;
+    pp.bact = R / 32u + 1u;
     pp.k = k;
     pp.E = experts;
     pp.D = D;
@@ -876,11 +723,11 @@ extern "C" int trc_prefill_moe(trc_vue repertoire, uint32_t experts, trc_vue lut
     const uint32_t* l = reinterpret_cast<const uint32_t*>(luts.adresse);
     const uint32_t Rm = D > R ? D : R;
     TRC_LANCER(prefill_grouper, dim3(1), dim3(1024), f, pp, ctl);
-    TRC_LANCER(prefill_quant_x, dim3(T), dim3(trc::PF_QX_FILS), f, pp);
+    TRC_LANCER(prefill_quant_x, dim3(T), dim3(trc::PF_Q_FILS), f, pp);
     r = trc::lancer_echelles_prefill(pm, Rm, C, n_delta, l, ctl, f);
     if (r != TRC_OK) return r;
     TRC_LANCER(prefill_mfma_gu, dim3((R + pp.rb[0] - 1) / pp.rb[0], 2 * experts), dim3(trc::PF_FILS), f, pp, l, ctl);
-    TRC_LANCER(prefill_swiglu_quant, dim3(T * k), dim3(trc::PF_BP_MAX), f, pp);
+    TRC_LANCER(prefill_swiglu_quant, dim3(T * k), dim3(trc::PF_Q_FILS), f, pp);
     TRC_LANCER(prefill_mfma_bas, dim3((D + pp.rb[2] - 1) / pp.rb[2], experts), dim3(trc::PF_FILS), f, pp, l, ctl);
     TRC_LANCER(prefill_combiner, dim3((D + 255) / 256, T), dim3(256), f, pp);
     return TRC_OK;
