@@ -444,10 +444,19 @@ __device__ __forceinline__ void prefill_bande(const ParamsPrefill& pp, const uin
     const gptr<u32x4> ent16 = glob<u32x4>(reinterpret_cast<const void*>(pp.ech + uint64_t(e * 3u + j) * pp.pas_ech));
     uint32_t hors_l = 0, pointeur = 0;
     TourBande tour0, tour1;
-    tour0.nb = tour1.nb = 0u;
     const uint32_t t00 = t_a + 2u * w, t01 = t00 + 32u;
-    if (t00 <= t_b) decoder_tour(h, m.codes, ent16, t00, t_b, ba, base, tour0, hors_l, pointeur);
-    if (t01 <= t_b) decoder_tour(h, m.codes, ent16, t01, t_b, ba, base, tour1, hors_l, pointeur);
+    // one copy of the decode code for both rounds (a smaller hot loop for the instruction cache)
+#pragma nounroll
+    for (uint32_t r = 0; r < PF_TOURS; ++r) {
+        const uint32_t t0 = r ? t01 : t00;
+        TourBande tb;
+        tb.nb = 0u;
+        if (t0 <= t_b) decoder_tour(h, m.codes, ent16, t0, t_b, ba, base, tb, hors_l, pointeur);
+        if (r == 0)
+            tour0 = tb;
+        else
+            tour1 = tb;
+    }
     verser_controle(controle, hors_l, pointeur);
     __syncthreads();  // every tile decoded: the LUT, x and ring regions are free
 
