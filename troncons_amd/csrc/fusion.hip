@@ -92,7 +92,7 @@ fusion_echelles(trc::Taches taches, const uint32_t* __restrict__ luts, uint32_t*
         if (threadIdx.x == 0 && blockIdx.x == 0) atomicAdd(&controle[CTL_FORMAT], 1u);
         return;
     }
-    const TeteTuile tete0 = premiere_tete(p.h);  // in flight with the medians
+    const TeteTuile tete0 = tete_course(p.h);  // in flight with the medians
     if (tc.lignes <= MED_LDS_MAX) copier_vers_lds(p.fm.p, tc.lignes, p.fm.longueur, med);
     charge_lut.poser(luts + (uint64_t(j_bloc) * 4u + 0u) * M, lut, M / 4u);
     __syncthreads();
@@ -505,11 +505,12 @@ uint32_t grille_tuiles(uint64_t octets, uint32_t N, uint32_t tuiles_par_bloc) {
 
 constexpr uint32_t TUILES_ECHELLES = trc::FILS_ECHELLES_FUSION / 32;
 
-// Grid of a DELTA pass over `blocs` blocks: sized as for tiles of at least 4 macro-steps, so that with
-// shorter tiles each wavefront loops over several tile pairs and a block's prologue (LUT, record,
-// medians, top-k) serves more than one tile pair.
+// Grid of a DELTA pass over `blocs` blocks: each half-wavefront takes a run of about 8 macro-steps
+// (whole tiles, at least one), so that a block's prologue (LUT, record, medians, top-k) and a ring's
+// opening serve several tiles.
 uint32_t grille_echelles(uint64_t blocs, uint32_t n_delta) {
-    return grille_tuiles(blocs, n_delta > 4u ? n_delta : 4u, TUILES_ECHELLES);
+    const uint32_t n = n_delta ? n_delta : 1u;
+    return grille_tuiles(blocs, n * (n < 8u ? 8u / n : 1u), TUILES_ECHELLES);
 }
 
 // Workspace of one matrix job: block entries (u32 per block + staging margin), then partial sums.

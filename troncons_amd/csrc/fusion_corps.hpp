@@ -335,9 +335,35 @@ __device__ __forceinline__ PrepEchelles preparer_echelles(const Tache& tc, const
     return p;
 }
 
+// The DELTA pass gives each half-wavefront a run of consecutive tiles, [t_deb, t_fin): the runs of
+// the grid's half-wavefronts split the stream's T tiles evenly. A run's tiles are stored one after
+// the other, so one word ring carries the whole run and is opened once.
+constexpr uint32_t ECH_KMAX = 8;  // tiles of a run whose initial states are held in registers at once
+
+__device__ __forceinline__ void course_echelles(uint32_t T, uint32_t& t_deb, uint32_t& t_fin) {
+    const uint32_t D = gridDim.x * (blockDim.x >> 5), d = blockIdx.x * (blockDim.x >> 5) + (threadIdx.x >> 5);
+    t_deb = uint32_t(uint64_t(T) * d / D);
+    t_fin = uint32_t(uint64_t(T) * (d + 1u) / D);
+}
+
+// The run's word origin (debut[t_deb]) in `debut` and the word where it must end (debut[t_fin], or W
+// at the stream's end) in `attendu`; loads clamped, so that no branch surrounds them.
+__device__ __forceinline__ TeteTuile tete_course(const EnteteRans& h) {
+    uint32_t t_deb, t_fin;
+    course_echelles(h.T, t_deb, t_fin);
+    const gptr<uint32_t> debut = glob<uint32_t>(h.debut);
+    TeteTuile r;
+    r.x = L;
+    r.debut = debut[min(t_deb, h.T - 1u)];
+    const uint32_t fin = debut[min(t_fin, h.T - 1u)];
+    r.attendu = t_fin < h.T ? fin : h.W;
+    return r;
+}
+
 // DELTA tiles -> one entry per block (entree_bloc) with e = (med[row] + delta - 128) mod 256 and
-// kappa = the class of delta; blocks past the matrix (stream padding) get the padding entry.
-// `tete0`: premiere_tete(p.h), read by the caller before its barrier.
+// kappa = the class of delta; blocks past the matrix (stream padding) get the padding entry. Each
+// tile starts from its own initial states and must end in state L; the run must end on the next
+// run's first word. `tete0`: tete_course(p.h), read by the caller before its barrier.
 __device__ __forceinline__ void corps_echelles_fusion(const Tache& tc, const PrepEchelles& p, const uint2* lut,
                                                       const uint8_t* med_lds, uint8_t* anneaux,
                                                       uint32_t* __restrict__ controle, const TeteTuile& tete0) {
@@ -349,66 +375,78 @@ __device__ __forceinline__ void corps_echelles_fusion(const Tache& tc, const Pre
     const uint32_t v = lane & 31u;
     const bool haut = lane >= 32u;
     const uint32_t decal = haut ? 32u : 0u, masque_inf = (1u << v) - 1u;
-    const uint32_t vagues_bloc = blockDim.x >> 6;
-    const uint32_t vague = blockIdx.x * vagues_bloc + (threadIdx.x >> 6);
-    const uint32_t n_vagues = gridDim.x * vagues_bloc;
-    const uint32_t lds = ((threadIdx.x >> 5) & (2u * vagues_bloc - 1u)) * OCTETS_ANNEAU;
-    const uint32_t nmacro = h.P / 128u;
-    uint32_t hors_l = 0, pointeur = 0;
-    TeteTuile tete = tete0;
-    for (uint32_t t0 = 2u * vague; t0 < h.T; t0 += 2u * n_vagues) {
-        const uint32_t t = t0 + (haut ? 1u : 0u);
-        const bool tuile = t < h.T;
-        const uint32_t nb_a = min(h.N, nmacro - t0 * h.N);
-        const uint32_t nb_b = (t0 + 1u < h.T) ? min(h.N, nmacro - (t0 + 1u) * h.N) : 0u;
-        const uint32_t nb = haut ? nb_b : nb_a;
-        uint32_t x = tete.x;
-        const uint32_t debut = tete.debut, attendu = tete.attendu;
-        tete = lire_tete(h, t + 2u * n_vagues, v);
-        Anneau a = ouvrir_anneau(h, p.fd, debut, lds, anneaux, v, tuile);
-        const uint32_t o0 = a.o2;
-        uint32_t b0 = 4u * ((tuile ? t : t0) * h.N * VOIES + v);
-        uint32_t ligne = b0 / B, reste = b0 - ligne * B;
-        auto macro = [&](auto tous, uint32_t m) {
-            constexpr bool TOUS = decltype(tous)::value;
-            const bool actif = TOUS || m < nb;
-            uint32_t mot = 0;
+    const uint32_t lds = (threadIdx.x >> 5) * OCTETS_ANNEAU;
+    const uint32_t N = h.N, nmacro = h.P / 128u;
+    uint32_t t_deb, t_fin;
+    course_echelles(h.T, t_deb, t_fin);
+    const uint32_t nt = t_fin - t_deb;
+    // the wave's two runs, for wave-uniform loop bounds
+    const uint32_t nt_lo = uint32_t(__builtin_amdgcn_readlane(int(nt), 0));
+    const uint32_t nt_hi = uint32_t(__builtin_amdgcn_readlane(int(nt), 32));
+    const uint32_t td_lo = uint32_t(__builtin_amdgcn_readlane(int(t_deb), 0));
+    const uint32_t td_hi = uint32_t(__builtin_amdgcn_readlane(int(t_deb), 32));
+    const uint32_t nt_max = max(nt_lo, nt_hi);
+    Anneau a = ouvrir_anneau(h, p.fd, tete0.debut, lds, anneaux, v, nt > 0u);
+    const uint32_t o0 = a.o2;
+    uint32_t x = L;
+    uint32_t hors_l = 0;
+    uint32_t b0 = 4u * (t_deb * N * VOIES + v);
+    uint32_t ligne = b0 / B, reste = b0 - ligne * B;
+    auto macro = [&](auto tous, bool actif_t) {
+        constexpr bool TOUS = decltype(tous)::value;
+        const bool actif = TOUS || actif_t;
+        uint32_t mot = 0;
 #pragma unroll
-            for (uint32_t k = 0; k < 4; ++k)
-                mot |= (pas_anneau<TOUS>(x, a, lut, anneaux, decal, masque_inf, actif) >> 24) << (8u * k);
-            avancer_anneau(a, anneaux, v, actif);
-            if (actif) {
-                u32x4 sortie;
+        for (uint32_t k = 0; k < 4; ++k)
+            mot |= (pas_anneau<TOUS>(x, a, lut, anneaux, decal, masque_inf, actif) >> 24) << (8u * k);
+        avancer_anneau(a, anneaux, v, actif);
+        if (actif) {
+            u32x4 sortie;
 #pragma unroll
-                for (uint32_t k = 0; k < 4; ++k) {
-                    uint32_t rk = ligne, qk = reste + k;
-                    while (qk >= B) {
-                        qk -= B;
-                        ++rk;
-                    }
-                    const uint32_t d = (mot >> (8u * k)) & 255u;
-                    const uint32_t mk = rk < R ? uint32_t(med[rk]) : 0u;
-                    sortie[k] = b0 + k < nblocs ? entree_bloc((mk + d - 128u) & 255u, classe_delta(d), qk, qk == 0u)
-                                                : ENTREE_BOURRAGE;
+            for (uint32_t k = 0; k < 4; ++k) {
+                uint32_t rk = ligne, qk = reste + k;
+                while (qk >= B) {
+                    qk -= B;
+                    ++rk;
                 }
-                ecrire_global<u32x4>(ech + b0, sortie);  // the workspace covers the stream's padding
+                const uint32_t d = (mot >> (8u * k)) & 255u;
+                const uint32_t mk = rk < R ? uint32_t(med[rk]) : 0u;
+                sortie[k] = b0 + k < nblocs ? entree_bloc((mk + d - 128u) & 255u, classe_delta(d), qk, qk == 0u)
+                                            : ENTREE_BOURRAGE;
             }
+            ecrire_global<u32x4>(ech + b0, sortie);  // the workspace covers the stream's padding
             b0 += 4u * VOIES;
             reste += 4u * VOIES;
             while (reste >= B) {
                 reste -= B;
                 ++ligne;
             }
-        };
-        const uint32_t nb_min = min(nb_a, nb_b);
-        uint32_t m = 0;
-        for (; m < nb_min; ++m) macro(std::true_type{}, m);
-        for (; m < nb_a; ++m) macro(std::false_type{}, m);
-        if (tuile) {
-            hors_l += (x != L) ? 1u : 0u;
-            pointeur += (v == 0 && debut + (a.o2 - o0) / 2u != attendu) ? 1u : 0u;
+        }
+    };
+    const gptr<uint32_t> etats = glob<uint32_t>(h.etats);
+    for (uint32_t k0 = 0; k0 < nt_max; k0 += ECH_KMAX) {  // wave-uniform
+        uint32_t etat[ECH_KMAX];
+#pragma unroll
+        for (uint32_t kk = 0; kk < ECH_KMAX; ++kk)
+            etat[kk] = etats[min(t_deb + k0 + kk, h.T - 1u) * VOIES + v];
+#pragma unroll
+        for (uint32_t kk = 0; kk < ECH_KMAX; ++kk) {
+            const uint32_t k = k0 + kk;
+            if (k >= nt_max) break;  // wave-uniform
+            // macro-steps of the two halves' k-th tiles (0 past a run's end), wave-uniform
+            const uint32_t nb_lo = k < nt_lo ? min(N, nmacro - (td_lo + k) * N) : 0u;
+            const uint32_t nb_hi = k < nt_hi ? min(N, nmacro - (td_hi + k) * N) : 0u;
+            const uint32_t nb = haut ? nb_hi : nb_lo;
+            const bool tuile = k < nt;
+            if (tuile) x = etat[kk];
+            const uint32_t nb_min = min(nb_lo, nb_hi), nb_max = max(nb_lo, nb_hi);
+            uint32_t m = 0;
+            for (; m < nb_min; ++m) macro(std::true_type{}, true);
+            for (; m < nb_max; ++m) macro(std::false_type{}, m < nb);
+            if (tuile) hors_l += (x != L) ? 1u : 0u;
         }
     }
+    const uint32_t pointeur = (v == 0 && nt > 0u && tete0.debut + (a.o2 - o0) / 2u != tete0.attendu) ? 1u : 0u;
     verser_controle(controle, hors_l, pointeur);
 }
 
