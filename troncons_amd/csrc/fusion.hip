@@ -40,7 +40,7 @@
 // then the medians. In a MoE layer (TACHES_MOE_DELTA) every block first runs the router's top-k on
 // the logits itself (wavefront 0; the result is deterministic, so all blocks agree) and block
 // (0, 0) publishes the indices and weights for the later passes: no block waits for another.
-extern "C" __global__ void __launch_bounds__(trc::FILS_ECHELLES_FUSION)
+extern "C" __global__ void __launch_bounds__(trc::FILS_ECHELLES_FUSION) __attribute__((amdgpu_waves_per_eu(8)))
 fusion_echelles(trc::Taches taches, const uint32_t* __restrict__ luts, uint32_t* __restrict__ controle) {
     using namespace trc;
     __shared__ uint2 lut[M];
@@ -96,7 +96,10 @@ fusion_echelles(trc::Taches taches, const uint32_t* __restrict__ luts, uint32_t*
     if (tc.lignes <= MED_LDS_MAX) copier_vers_lds(p.fm.p, tc.lignes, p.fm.longueur, med);
     charge_lut.poser(luts + (uint64_t(j_bloc) * 4u + 0u) * M, lut, M / 4u);
     __syncthreads();
-    corps_echelles_fusion(tc, p, lut, med, anneaux, controle, tete0);
+    if (tc.lignes <= MED_LDS_MAX)  // uniform
+        corps_echelles_fusion<true>(tc, p, lut, med, anneaux, controle, tete0);
+    else
+        corps_echelles_fusion<false>(tc, p, lut, med, anneaux, controle, tete0);
 }
 
 namespace trc {

@@ -291,6 +291,20 @@ struct PrepEchelles {
 
 // A tile's head: its lanes' initial states, its first word, and the word its decode must end on
 // (the next tile's first, or W). Read one tile ahead, so that no decode waits for these loads.
+// LDS addresses (32-bit) of an LDS array.
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
+__device__ __forceinline__ uint32_t adresse_lds(const void* p) {
+    return uint32_t(reinterpret_cast<uintptr_t>((const lds_u8*)(p)));  // address-space cast
+}
+template <typename T>
+__device__ __forceinline__ T lire_lds(uint32_t a) {
+    return *reinterpret_cast<const __attribute__((address_space(3))) T*>(uintptr_t(a));
+}
+template <typename T>
+__device__ __forceinline__ void ecrire_lds(uint32_t a, T v) {
+    *reinterpret_cast<__attribute__((address_space(3))) T*>(uintptr_t(a)) = v;
+}
+
 struct TeteTuile {
     uint32_t x, debut, attendu;
 };
@@ -338,7 +352,7 @@ __device__ __forceinline__ PrepEchelles preparer_echelles(const Tache& tc, const
 // The DELTA pass gives each half-wavefront a run of consecutive tiles, [t_deb, t_fin): the runs of
 // the grid's half-wavefronts split the stream's T tiles evenly. A run's tiles are stored one after
 // the other, so one word ring carries the whole run and is opened once.
-constexpr uint32_t ECH_KMAX = 8;  // tiles of a run whose initial states are held in registers at once
+constexpr uint32_t ECH_KMAX = 4;  // tiles of a run whose initial states are held in registers at once
 
 __device__ __forceinline__ void course_echelles(uint32_t T, uint32_t& t_deb, uint32_t& t_fin) {
     const uint32_t D = gridDim.x * (blockDim.x >> 5), d = blockIdx.x * (blockDim.x >> 5) + (threadIdx.x >> 5);
@@ -363,13 +377,21 @@ __device__ __forceinline__ TeteTuile tete_course(const EnteteRans& h) {
 // DELTA tiles -> one entry per block (entree_bloc) with e = (med[row] + delta - 128) mod 256 and
 // kappa = the class of delta; blocks past the matrix (stream padding) get the padding entry. Each
 // tile starts from its own initial states and must end in state L; the run must end on the next
-// run's first word. `tete0`: tete_course(p.h), read by the caller before its barrier.
+// run's first word. The medians are read from LDS (MED_LDS = true: med_lds holds them) or from the
+// stream. A lane's 4 blocks of a macro-step lie in at most two rows when B >= 4; narrower rows take
+// a loop. `tete0`: tete_course(p.h), read by the caller before its barrier.
+template <bool MED_LDS>
 __device__ __forceinline__ void corps_echelles_fusion(const Tache& tc, const PrepEchelles& p, const uint2* lut,
                                                       const uint8_t* med_lds, uint8_t* anneaux,
                                                       uint32_t* __restrict__ controle, const TeteTuile& tete0) {
     const EnteteRans& h = p.h;
     const uint32_t R = tc.lignes, B = tc.colonnes / 32u, nblocs = R * B;
-    const uint8_t* med = R <= MED_LDS_MAX ? med_lds : p.fm.p;
+    const uint32_t a_med = adresse_lds(med_lds);
+    const gptr<uint8_t> med_g = glob<uint8_t>(p.fm.p);
+    auto mediane = [&](uint32_t r) -> uint32_t {  // r < R
+        return MED_LDS ? uint32_t(lire_lds<uint8_t>(a_med + r)) : uint32_t(med_g[r]);
+    };
+    const uint32_t q128 = 128u / B, r128 = 128u - q128 * B;  // a macro-step's 128 blocks per lane group
     uint32_t* ech = reinterpret_cast<uint32_t*>(tc.ech);
     const uint32_t lane = __lane_id();
     const uint32_t v = lane & 31u;
@@ -402,22 +424,39 @@ __device__ __forceinline__ void corps_echelles_fusion(const Tache& tc, const Pre
         avancer_anneau(a, anneaux, v, actif);
         if (actif) {
             u32x4 sortie;
+            if (B >= 4u) {  // uniform
+                const uint32_t m0 = ligne < R ? mediane(ligne) : 0u;
+                const uint32_t m1 = ligne + 1u < R ? mediane(ligne + 1u) : 0u;
 #pragma unroll
-            for (uint32_t k = 0; k < 4; ++k) {
-                uint32_t rk = ligne, qk = reste + k;
-                while (qk >= B) {
-                    qk -= B;
-                    ++rk;
+                for (uint32_t k = 0; k < 4; ++k) {
+                    const bool suivante = reste + k >= B;
+                    const uint32_t qk = reste + k - (suivante ? B : 0u);
+                    const uint32_t d = (mot >> (8u * k)) & 255u;
+                    const uint32_t mk = suivante ? m1 : m0;
+                    sortie[k] = b0 + k < nblocs
+                                    ? entree_bloc((mk + d - 128u) & 255u, classe_delta(d), qk, qk == 0u)
+                                    : ENTREE_BOURRAGE;
                 }
-                const uint32_t d = (mot >> (8u * k)) & 255u;
-                const uint32_t mk = rk < R ? uint32_t(med[rk]) : 0u;
-                sortie[k] = b0 + k < nblocs ? entree_bloc((mk + d - 128u) & 255u, classe_delta(d), qk, qk == 0u)
-                                            : ENTREE_BOURRAGE;
+            } else {
+#pragma unroll
+                for (uint32_t k = 0; k < 4; ++k) {
+                    uint32_t rk = ligne, qk = reste + k;
+                    while (qk >= B) {
+                        qk -= B;
+                        ++rk;
+                    }
+                    const uint32_t d = (mot >> (8u * k)) & 255u;
+                    const uint32_t mk = rk < R ? mediane(rk) : 0u;
+                    sortie[k] = b0 + k < nblocs
+                                    ? entree_bloc((mk + d - 128u) & 255u, classe_delta(d), qk, qk == 0u)
+                                    : ENTREE_BOURRAGE;
+                }
             }
             ecrire_global<u32x4>(ech + b0, sortie);  // the workspace covers the stream's padding
             b0 += 4u * VOIES;
-            reste += 4u * VOIES;
-            while (reste >= B) {
+            ligne += q128;
+            reste += r128;
+            if (reste >= B) {
                 reste -= B;
                 ++ligne;
             }
@@ -610,20 +649,6 @@ __device__ __forceinline__ void corps_gemv_xg(const Tache& tc, const PrepGemv& p
 // row start. Each lane keeps one accumulator for the tile's current row; a macro-step in which a
 // row starts (at most one per half: a row has >= 8 blocks) takes the slow path that closes the
 // row. Stream padding blocks read the zero slot of x, so no per-block validity test is needed.
-
-// LDS addresses (32-bit) of the single LDS array.
-typedef __attribute__((address_space(3))) uint8_t lds_u8;
-__device__ __forceinline__ uint32_t adresse_lds(const void* p) {
-    return uint32_t(reinterpret_cast<uintptr_t>((const lds_u8*)(p)));  // address-space cast
-}
-template <typename T>
-__device__ __forceinline__ T lire_lds(uint32_t a) {
-    return *reinterpret_cast<const __attribute__((address_space(3))) T*>(uintptr_t(a));
-}
-template <typename T>
-__device__ __forceinline__ void ecrire_lds(uint32_t a, T v) {
-    *reinterpret_cast<__attribute__((address_space(3))) T*>(uintptr_t(a)) = v;
-}
 
 // A tile's word ring (as Anneau, with absolute LDS addresses; `lds` is 1 KiB aligned). Chunks are
 // addressed by 32-bit offsets from the stream's start, which both tiles of a wavefront share.
