@@ -43,8 +43,8 @@ namespace trc {
 constexpr uint32_t PF_FILS = 1024;        // 16 wavefronts: 32 tiles decoded per band
 constexpr uint32_t PF_NMAX = 16;          // macro-steps per CODES_CTX tile held in registers
 constexpr uint32_t PF_PIECES_BF = 3;      // bf16 pieces per activation block
-constexpr uint32_t PF_Q_FILS = 192;       // threads of the piece kernels: one per block, PF_BP_MAX + 1 at most
-constexpr uint32_t PF_BP_MAX = 128;       // padded blocks per row (4096 columns)
+constexpr uint32_t PF_Q_FILS = 256;       // threads per block of the piece kernels (16 per 32-value block)
+constexpr uint32_t PF_BP_MAX = 128;       // blocks per row at most (4096 columns)
 constexpr uint32_t PF_PAIRES_MAX = 16384; // positions x k per call
 constexpr uint32_t ECHELLE_UN = 127u;     // E8M0 1.0
 
@@ -85,33 +85,25 @@ struct ParamsPrefill {
     uint32_t rb[3];        // rows per band (16, 32 or 64)
     uint32_t T, k, E, D;
     uint32_t bx, bact;     // blocks per piece row of x and act: C/32 + 1, R/32 + 1
+    uint32_t quatre;       // the combine takes 4 rows per thread (D % 4 == 0, residus 16-byte aligned)
 };
 
-// Splits 32 values (natural order a[0..31]) into PF_PIECES_BF bf16 pieces of 64 bytes each (piece
-// stride `pas` bytes), word q holding values q (low half) and q + 16 (high half); returns the pieces
-// that are not all zero. An infinite or NaN value stays whole in hi (its residual is set to 0), so a
-// product with it is what the f32 product is.
-__device__ __forceinline__ uint32_t pieces_bf16(float (&a)[32], uint8_t* dst, uint64_t pas) {
+// Splits values q and q + 16 of a 32-value block into PF_PIECES_BF bf16 pieces: word q of each
+// 64-byte piece block (piece stride `pas` bytes) holds value q (low half) and q + 16 (high half).
+// Returns the pieces that are not both zero. An infinite or NaN value stays whole in hi (its
+// residual is set to 0), so a product with it is what the f32 product is.
+__device__ __forceinline__ uint32_t pieces_bf16(float a0, float a1, uint8_t* dst, uint64_t pas) {
     uint32_t P = 0;
 #pragma unroll
     for (uint32_t p = 0; p < PF_PIECES_BF; ++p) {
-        uint32_t mots[16];
-        uint32_t nz = 0;
-#pragma unroll
-        for (uint32_t q = 0; q < 16; ++q) {
-            const __bf16 h0 = __bf16(a[q]), h1 = __bf16(a[q + 16]);
-            const uint32_t b0 = __builtin_bit_cast(uint16_t, h0), b1 = __builtin_bit_cast(uint16_t, h1);
-            const float f0 = __uint_as_float(b0 << 16), f1 = __uint_as_float(b1 << 16);
-            a[q] = __builtin_isfinite(f0) ? a[q] - f0 : 0.0f;  // exact
-            a[q + 16] = __builtin_isfinite(f1) ? a[q + 16] - f1 : 0.0f;
-            mots[q] = b0 | (b1 << 16);
-            nz |= mots[q];
-        }
-#pragma unroll
-        for (uint32_t g = 0; g < 4; ++g)
-            *reinterpret_cast<u32x4*>(dst + p * pas + 16u * g) =
-                u32x4{mots[4 * g], mots[4 * g + 1], mots[4 * g + 2], mots[4 * g + 3]};
-        if (nz & 0x7FFF7FFFu) P = p + 1u;
+        const __bf16 h0 = __bf16(a0), h1 = __bf16(a1);
+        const uint32_t b0 = __builtin_bit_cast(uint16_t, h0), b1 = __builtin_bit_cast(uint16_t, h1);
+        const float f0 = __uint_as_float(b0 << 16), f1 = __uint_as_float(b1 << 16);
+        a0 = __builtin_isfinite(f0) ? a0 - f0 : 0.0f;  // exact
+        a1 = __builtin_isfinite(f1) ? a1 - f1 : 0.0f;
+        const uint32_t mot = b0 | (b1 << 16);
+        *reinterpret_cast<uint32_t*>(dst + p * pas) = mot;
+        if (mot & 0x7FFF7FFFu) P = p + 1u;
     }
     return P;
 }
@@ -120,6 +112,14 @@ __device__ __forceinline__ uint32_t max_vague(uint32_t v) {
 #pragma unroll
     for (int d = 32; d > 0; d >>= 1) v = max(v, uint32_t(__shfl_xor(int(v), d)));
     return v;
+}
+
+// *compteur = max(*compteur, the wave's P). The counter only grows, so a wave whose P does not
+// exceed the value it reads needs no atomic: most waves of a call then leave the address alone.
+__device__ __forceinline__ void noter_pieces(uint32_t* compteur, uint32_t P) {
+    P = max_vague(P);
+    if (__lane_id() == 0 && P && P > __hip_atomic_load(compteur, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+        atomicMax(compteur, P);
 }
 
 }  // namespace trc
@@ -204,56 +204,45 @@ prefill_grouper(ParamsPrefill pp, uint32_t* __restrict__ controle) {
     }
 }
 
-// x pieces: block (position i), thread b = column block b (block B gets zeros).
+// x pieces: block i (position i); thread g takes, for (b, q) = (g / 16, g % 16), g + 256 k, values q
+// and q + 16 of block b (block B gets zeros), so that a wave's loads and stores are contiguous.
 extern "C" __global__ void __launch_bounds__(trc::PF_Q_FILS)
 prefill_quant_x(ParamsPrefill pp) {
     using namespace trc;
-    const uint32_t i = blockIdx.x, b = threadIdx.x;
+    const uint32_t i = blockIdx.x;
     const uint32_t C = pp.colonnes[0], B = C / 32u, Bx = pp.bx;
     uint32_t P = 0;
-    if (b < Bx) {
-        float a[32];
-        const gptr<f32x4> x4 = glob<f32x4>(reinterpret_cast<const float*>(pp.x) + uint64_t(i) * C + 32u * b);
-#pragma unroll
-        for (uint32_t g = 0; g < 8; ++g) {
-            f32x4 v = {0.f, 0.f, 0.f, 0.f};
-            if (b < B) v = x4[g];
-            a[4 * g] = v.x;
-            a[4 * g + 1] = v.y;
-            a[4 * g + 2] = v.z;
-            a[4 * g + 3] = v.w;
-        }
-        P = pieces_bf16(a, reinterpret_cast<uint8_t*>(pp.xb) + (uint64_t(i) * PF_PIECES_BF * Bx + b) * 64u,
-                        uint64_t(Bx) * 64u);
+    for (uint32_t g = threadIdx.x; g < Bx * 16u; g += PF_Q_FILS) {
+        const uint32_t b = g >> 4, q = g & 15u;
+        const float* x = reinterpret_cast<const float*>(pp.x) + uint64_t(i) * C + 32u * b + q;
+        const float a0 = b < B ? x[0] : 0.0f, a1 = b < B ? x[16] : 0.0f;
+        P = max(P, pieces_bf16(a0, a1,
+                               reinterpret_cast<uint8_t*>(pp.xb) + (uint64_t(i) * PF_PIECES_BF * Bx + b) * 64u + 4u * q,
+                               uint64_t(Bx) * 64u));
     }
-    P = max_vague(P);
-    if (__lane_id() == 0 && P) atomicMax(reinterpret_cast<uint32_t*>(pp.pieces), P);
+    noter_pieces(reinterpret_cast<uint32_t*>(pp.pieces), P);
 }
 
-// act pieces: block (pair c), thread b = block b of act = swiglu_oai(gate, up) rows 32b .. 32b+31
-// (block R/32 gets zeros).
+// act pieces: block c (pair c); thread g takes, for (b, q) = (g / 16, g % 16), g + 256 k, rows
+// 32b + q and 32b + q + 16 of act = swiglu_oai(gate, up) (block R/32 gets zeros).
 extern "C" __global__ void __launch_bounds__(trc::PF_Q_FILS)
 prefill_swiglu_quant(ParamsPrefill pp) {
     using namespace trc;
-    const uint32_t c = blockIdx.x, b = threadIdx.x;
+    const uint32_t c = blockIdx.x;
     const uint32_t R = pp.lignes[0], B2 = R / 32u, Ba = pp.bact;
     if (reinterpret_cast<const uint32_t*>(pp.indices)[c] >= pp.E) return;
     uint32_t P = 0;
-    if (b < Ba) {
-        float a[32];
-        const float* g = reinterpret_cast<const float*>(pp.gu) + uint64_t(c) * 2u * R;
-        const float* u = g + R;
-#pragma unroll
-        for (uint32_t t = 0; t < 32; ++t) a[t] = 0.0f;
-        if (b < B2) {
-#pragma unroll
-            for (uint32_t t = 0; t < 32; ++t) a[t] = swiglu_oai_f(g[32u * b + t], u[32u * b + t]);
-        }
-        P = pieces_bf16(a, reinterpret_cast<uint8_t*>(pp.ab) + (uint64_t(c) * PF_PIECES_BF * Ba + b) * 64u,
-                        uint64_t(Ba) * 64u);
+    for (uint32_t g = threadIdx.x; g < Ba * 16u; g += PF_Q_FILS) {
+        const uint32_t b = g >> 4, q = g & 15u;
+        const float* gt = reinterpret_cast<const float*>(pp.gu) + uint64_t(c) * 2u * R + 32u * b + q;
+        const float* up = gt + R;
+        const float a0 = b < B2 ? swiglu_oai_f(gt[0], up[0]) : 0.0f;
+        const float a1 = b < B2 ? swiglu_oai_f(gt[16], up[16]) : 0.0f;
+        P = max(P, pieces_bf16(a0, a1,
+                               reinterpret_cast<uint8_t*>(pp.ab) + (uint64_t(c) * PF_PIECES_BF * Ba + b) * 64u + 4u * q,
+                               uint64_t(Ba) * 64u));
     }
-    P = max_vague(P);
-    if (__lane_id() == 0 && P) atomicMax(reinterpret_cast<uint32_t*>(pp.pieces) + 1, P);
+    noter_pieces(reinterpret_cast<uint32_t*>(pp.pieces) + 1, P);
 }
 
 namespace trc {
@@ -552,13 +541,17 @@ prefill_mfma_bas(ParamsPrefill pp, const uint32_t* __restrict__ luts, uint32_t* 
 
 // x_i[r] += ((w0 s_i0[r] + w1 s_i1[r]) + w2 s_i2[r]) + ..., each product and sum rounded on its own
 // (combiner_pos, trc-modele/src/lib.rs:706-710 -> passe.cuh:611-622); positions whose experts are
-// not all valid, mounted matrices are left alone.
+// not all valid, mounted matrices are left alone. A thread takes 4 consecutive rows when pp.quatre
+// (16-byte loads and stores), else one.
 extern "C" __global__ void __launch_bounds__(256)
 prefill_combiner(ParamsPrefill pp) {
 #pragma clang fp contract(off)
     using namespace trc;
-    const uint32_t i = blockIdx.y, r = blockIdx.x * 256u + threadIdx.x;
+    const uint32_t i = blockIdx.y, g = blockIdx.x * 256u + threadIdx.x;
     const uint32_t k = pp.k, D = pp.D;
+    const bool quatre = pp.quatre != 0u;
+    const uint32_t r = quatre ? 4u * g : g;
+    if (r >= D) return;
     const uint32_t* idx = reinterpret_cast<const uint32_t*>(pp.indices) + uint64_t(i) * k;
     bool ok = true;
     for (uint32_t s = 0; s < k; ++s) {
@@ -568,16 +561,31 @@ prefill_combiner(ParamsPrefill pp) {
             for (uint32_t j = 0; j < 3; ++j)
                 ok = ok && reinterpret_cast<const MatricePartie*>(pp.repertoire)[e * 3u + j].bon != 0u;
     }
-    if (!ok || r >= D) return;
+    if (!ok) return;
     const float* w = reinterpret_cast<const float*>(pp.poids) + uint64_t(i) * k;
     const float* s = reinterpret_cast<const float*>(pp.s) + uint64_t(i) * k * D;
-    float acc = w[0] * s[r];
-    for (uint32_t q = 1; q < k; ++q) {
-        const float p = w[q] * s[uint64_t(q) * D + r];
-        acc = acc + p;
-    }
     float* x = reinterpret_cast<float*>(pp.residus) + uint64_t(i) * D;
-    x[r] = x[r] + acc;
+    if (quatre) {
+        const float w0 = w[0];
+        f32x4 v = *reinterpret_cast<const f32x4*>(s + r);
+        f32x4 acc = {w0 * v.x, w0 * v.y, w0 * v.z, w0 * v.w};
+        for (uint32_t q = 1; q < k; ++q) {
+            const float wq = w[q];
+            v = *reinterpret_cast<const f32x4*>(s + uint64_t(q) * D + r);
+            const f32x4 p = {wq * v.x, wq * v.y, wq * v.z, wq * v.w};
+            acc = f32x4{acc.x + p.x, acc.y + p.y, acc.z + p.z, acc.w + p.w};
+        }
+        f32x4 xr = *reinterpret_cast<const f32x4*>(x + r);
+        xr = f32x4{xr.x + acc.x, xr.y + acc.y, xr.z + acc.z, xr.w + acc.w};
+        *reinterpret_cast<f32x4*>(x + r) = xr;
+    } else {
+        float acc = w[0] * s[r];
+        for (uint32_t q = 1; q < k; ++q) {
+            const float p = w[q] * s[uint64_t(q) * D + r];
+            acc = acc + p;
+        }
+        x[r] = x[r] + acc;
+    }
 }
 
 // ============================================================================ C-ABI launch layer
@@ -711,6 +719,7 @@ extern "C" int trc_prefill_moe(trc_vue repertoire, uint32_t experts, trc_vue lut
     pp.T = T;
     pp.bx = C / 32u + 1u;
     pp.bact = R / 32u + 1u;
+    pp.quatre = (D % 4u == 0u && residus.adresse % 16u == 0u) ? 1u : 0u;
     pp.k = k;
     pp.E = experts;
     pp.D = D;
@@ -738,6 +747,7 @@ extern "C" int trc_prefill_moe(trc_vue repertoire, uint32_t experts, trc_vue lut
     TRC_LANCER(prefill_mfma_gu, dim3((R + pp.rb[0] - 1) / pp.rb[0], 2 * experts), dim3(trc::PF_FILS), f, pp, l, ctl);
     TRC_LANCER(prefill_swiglu_quant, dim3(T * k), dim3(trc::PF_Q_FILS), f, pp);
     TRC_LANCER(prefill_mfma_bas, dim3((D + pp.rb[2] - 1) / pp.rb[2], experts), dim3(trc::PF_FILS), f, pp, l, ctl);
-    TRC_LANCER(prefill_combiner, dim3((D + 255) / 256, T), dim3(256), f, pp);
+    const uint32_t fils_comb = pp.quatre ? D / 4u : D;  // threads per position
+    TRC_LANCER(prefill_combiner, dim3((fils_comb + 255) / 256, T), dim3(256), f, pp);
     return TRC_OK;
 }
