@@ -126,80 +126,95 @@ __device__ __forceinline__ void noter_pieces(uint32_t* compteur, uint32_t P) {
 
 using trc::ParamsPrefill;
 
-// One block of 1024 threads: thread (chunk c, expert e) counts and then lists the pairs of chunk c
-// that chose e (8 chunks when E <= 128, else 4); chunks are concatenated in order, so each expert's
-// pairs keep position order. Also clears the piece counters of the call. Indices >= E are format
-// errors (the reference bails, trc-ordo/src/lib.rs:817-819) and join no list.
+// One block of 1024 threads groups the pairs by expert, in position order within an expert. Wave w
+// takes the pairs of its contiguous share, 64 at a time: the lanes holding the same expert find
+// each other with one ballot per bit of the index, and a pair's rank among the wave's earlier pairs
+// of its expert is the count of those lanes below it plus the wave's running count (kept in LDS).
+// The experts' starts are an exclusive prefix of the totals; a wave's pairs of expert e follow the
+// earlier waves' ones. Also clears the piece counters of the call. Indices >= E are format errors
+// (the reference bails, trc-ordo/src/lib.rs:817-819) and join no list.
 extern "C" __global__ void __launch_bounds__(1024)
 prefill_grouper(ParamsPrefill pp, uint32_t* __restrict__ controle) {
     using namespace trc;
-    __shared__ u32x4 idx4[PF_PAIRES_MAX / 4];
-    __shared__ uint32_t cpt[1024];
+    constexpr uint32_t VAGUES = 16;
+    __shared__ uint32_t cpt[VAGUES][EXPERTS_MAX];  // per wave: its pairs of each expert so far, then its base
+    __shared__ uint16_t rang[PF_PAIRES_MAX];       // a pair's rank among its wave's pairs of its expert
     __shared__ uint32_t deb[EXPERTS_MAX];
-    const uint32_t n = pp.T * pp.k, E = pp.E, n4 = (n + 3u) / 4u;
+    const uint32_t n = pp.T * pp.k, E = pp.E;
     const uint32_t* indices = reinterpret_cast<const uint32_t*>(pp.indices);
-    uint32_t* idx = reinterpret_cast<uint32_t*>(idx4);
-    uint32_t mauvais = 0;
-    for (uint32_t i = threadIdx.x; i < 4u * n4; i += blockDim.x) {
-        const uint32_t v = i < n ? indices[i] : 0xFFFFFFFFu;  // padding joins no list
-        idx[i] = v;
-        mauvais += (i < n && v >= E) ? 1u : 0u;
-    }
+    const uint32_t lane = __lane_id(), w = threadIdx.x >> 6;
+    for (uint32_t i = threadIdx.x; i < VAGUES * EXPERTS_MAX; i += blockDim.x) (&cpt[0][0])[i] = 0u;
     if (threadIdx.x < 4u) reinterpret_cast<uint32_t*>(pp.pieces)[threadIdx.x] = 0u;
-    mauvais = somme_vague_u32(mauvais);
-    if (__lane_id() == 0 && mauvais) atomicAdd(&controle[CTL_FORMAT], mauvais);
     __syncthreads();
-    const uint32_t Ep = E <= 128u ? 128u : EXPERTS_MAX, tranches = 1024u / Ep;
-    const uint32_t e = threadIdx.x % Ep, c = threadIdx.x / Ep;
-    const uint32_t lo = uint32_t(uint64_t(c) * n4 / tranches), hi = uint32_t(uint64_t(c + 1) * n4 / tranches);
-    uint32_t nb = 0;
-    if (e < E)
-        for (uint32_t i = lo; i < hi; ++i) {
-            const u32x4 v = idx4[i];
-            nb += (v.x == e ? 1u : 0u) + (v.y == e ? 1u : 0u) + (v.z == e ? 1u : 0u) + (v.w == e ? 1u : 0u);
+    const uint32_t par_vague = (n + VAGUES - 1u) / VAGUES;
+    const uint32_t p0 = min(n, w * par_vague), p1 = min(n, p0 + par_vague);
+    const uint64_t dessous = (uint64_t(1) << lane) - 1u;
+    uint32_t mauvais = 0;
+    for (uint32_t b = p0; b < p1; b += 64u) {  // wave-uniform
+        const uint32_t p = b + lane;
+        const uint32_t e = p < p1 ? indices[p] : 0xFFFFFFFFu;
+        const bool valide = e < E;
+        mauvais += (p < p1 && !valide) ? 1u : 0u;
+        uint64_t meme = __builtin_amdgcn_ballot_w64(valide);
+#pragma unroll
+        for (uint32_t bit = 0; bit < 8; ++bit) {  // E <= 256
+            const bool un = (e >> bit) & 1u;
+            const uint64_t v = __builtin_amdgcn_ballot_w64(un);
+            meme &= un ? v : ~v;
         }
-    cpt[threadIdx.x] = nb;
+        const uint32_t avant = __popcll(meme & dessous);
+        const uint32_t ee = valide ? e : 0u;
+        const uint32_t deja = valide ? cpt[w][ee] : 0u;
+        if (valide) rang[p] = uint16_t(deja + avant);
+        // the group's highest lane raises the wave's count of the expert
+        if (valide && (meme >> lane) == 1u) cpt[w][ee] = deja + avant + 1u;
+    }
+    mauvais = somme_vague_u32(mauvais);
+    if (lane == 0 && mauvais) atomicAdd(&controle[CTL_FORMAT], mauvais);
+    __syncthreads();
+    // per expert e (thread e): total and the waves' bases, then the experts' exclusive prefix
+    uint32_t total = 0;
+    if (threadIdx.x < EXPERTS_MAX) {
+        for (uint32_t v = 0; v < VAGUES; ++v) {
+            const uint32_t c = cpt[v][threadIdx.x];
+            cpt[v][threadIdx.x] = total;
+            total += c;
+        }
+        deb[threadIdx.x] = total;
+    }
     __syncthreads();
     if (threadIdx.x < 64u) {  // exclusive prefix over experts, 4 per lane
-        uint32_t tot[EXPERTS_MAX / 64];
+        uint32_t t[EXPERTS_MAX / 64];
         uint32_t local = 0;
 #pragma unroll
         for (uint32_t q = 0; q < EXPERTS_MAX / 64; ++q) {
-            const uint32_t ee = threadIdx.x * (EXPERTS_MAX / 64) + q;
-            uint32_t t = 0;
-            if (ee < Ep)
-                for (uint32_t cc = 0; cc < tranches; ++cc) t += cpt[cc * Ep + ee];
-            tot[q] = t;
-            local += t;
+            t[q] = deb[threadIdx.x * (EXPERTS_MAX / 64) + q];
+            local += t[q];
         }
         uint32_t incl = local;
         for (int d = 1; d < 64; d <<= 1) {
-            const uint32_t t = uint32_t(__shfl_up(int(incl), d));
-            if (int(threadIdx.x) >= d) incl += t;
+            const uint32_t u = uint32_t(__shfl_up(int(incl), d));
+            if (int(threadIdx.x) >= d) incl += u;
         }
-        uint32_t s = incl - local;
+        uint32_t s0 = incl - local;
 #pragma unroll
         for (uint32_t q = 0; q < EXPERTS_MAX / 64; ++q) {
             const uint32_t ee = threadIdx.x * (EXPERTS_MAX / 64) + q;
-            deb[ee] = s;
+            deb[ee] = s0;
             if (ee < E) {
-                reinterpret_cast<uint32_t*>(pp.debut)[ee] = s;
-                reinterpret_cast<uint32_t*>(pp.compte)[ee] = tot[q];
+                reinterpret_cast<uint32_t*>(pp.debut)[ee] = s0;
+                reinterpret_cast<uint32_t*>(pp.compte)[ee] = t[q];
             }
-            s += tot[q];
+            s0 += t[q];
         }
     }
     __syncthreads();
-    if (e < E) {
-        uint32_t pos = deb[e];
-        for (uint32_t cc = 0; cc < c; ++cc) pos += cpt[cc * Ep + e];
-        uint32_t* paires = reinterpret_cast<uint32_t*>(pp.paires);
-        for (uint32_t i = lo; i < hi; ++i) {
-            const u32x4 v = idx4[i];
-            if (v.x == e) paires[pos++] = 4u * i;
-            if (v.y == e) paires[pos++] = 4u * i + 1u;
-            if (v.z == e) paires[pos++] = 4u * i + 2u;
-            if (v.w == e) paires[pos++] = 4u * i + 3u;
+    uint32_t* paires = reinterpret_cast<uint32_t*>(pp.paires);
+    for (uint32_t b = p0; b < p1; b += 64u) {
+        const uint32_t p = b + lane;
+        if (p < p1) {
+            const uint32_t e = indices[p];
+            if (e < E) paires[deb[e] + cpt[w][e] + rang[p]] = p;
         }
     }
 }
