@@ -269,43 +269,68 @@ namespace trc {
 // column n: the MFMA adds the products of each lane group's eight K values, so any order common to A
 // and B gives the dot product. The B loads of KB k-steps are issued before their MFMAs. Columns past
 // the expert's pairs load a valid position; their sums are never stored.
+template <uint32_t NP, uint32_t KB>
+__device__ __forceinline__ void charger_b(u32x4 (&bq)[KB][NP], const uint8_t* xsrc, uint64_t pas_p, uint32_t ks0,
+                                          uint32_t B) {
+#pragma unroll
+    for (uint32_t q = 0; q < KB; ++q) {
+        const uint32_t ks = min(ks0 + 16u * q, B);  // block B of an activation row is zero
+#pragma unroll
+        for (uint32_t p = 0; p < NP; ++p) bq[q][p] = *glob<u32x4>(xsrc + p * pas_p + 64u * ks);
+    }
+}
+
 template <uint32_t NP, uint32_t KB, uint32_t NRT>
+__device__ __forceinline__ void calculer_b(f32x4 (&acc)[4], const u32x4 (&bq)[KB][NP], uint32_t ks0, uint32_t B,
+                                           uint32_t a_codes, uint32_t a_sa, uint32_t lr, uint32_t lg) {
+#pragma unroll
+    for (uint32_t q = 0; q < KB; ++q) {
+        // straight-line code, so that the B loads stay ahead of every MFMA: a k-step past B
+        // multiplies block B - 1 of the weights by the activations' zero block
+        const uint32_t ks = min(ks0 + 16u * q, B - 1u);
+        bf16x8 a[NRT];
+#pragma unroll
+        for (uint32_t rt = 0; rt < NRT; ++rt) {
+            const uint32_t o = (16u * rt + lr) * B + ks;
+            const uint32_t mot = lire_lds<uint32_t>(a_codes + 16u * o + 4u * lg);
+            const float sc = __uint_as_float(uint32_t(lire_lds<uint8_t>(a_sa + o)) << 23);
+            const bf16x2 p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(mot, sc, 0);
+            const bf16x2 p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(mot, sc, 1);
+            const bf16x2 p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(mot, sc, 2);
+            const bf16x2 p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(mot, sc, 3);
+            a[rt] = bf16x8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+        }
+#pragma unroll
+        for (uint32_t p = 0; p < NP; ++p) {
+            const bf16x8 bv = __builtin_bit_cast(bf16x8, bq[q][p]);
+#pragma unroll
+            for (uint32_t rt = 0; rt < NRT; ++rt)
+                acc[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[rt], bv, acc[rt], 0, 0, 0);
+        }
+    }
+}
+
+// The whole product of a column tile; PRE: the first batch of B (k-steps w, w + 16, ...) is already
+// in `pre` (loaded before the band's store, so that its latency hides behind it).
+constexpr uint32_t PF_KB1 = 6;  // k-steps per batch of B loads with one piece
+
+template <uint32_t NP, uint32_t KB, uint32_t NRT, bool PRE>
 __device__ __forceinline__ void produit_bf16(f32x4 (&acc)[4], const uint8_t* xsrc, uint64_t pas_p, uint32_t w,
-                                             uint32_t B, uint32_t a_codes, uint32_t a_sa, uint32_t lr, uint32_t lg) {
-    for (uint32_t ks0 = w; ks0 < B; ks0 += 16u * KB) {  // wave-uniform
+                                             uint32_t B, uint32_t a_codes, uint32_t a_sa, uint32_t lr, uint32_t lg,
+                                             const u32x4 (&pre)[PF_KB1][1]) {
+    static_assert(!PRE || (NP == 1u && KB == PF_KB1), "the first batch is preloaded for one piece only");
+    uint32_t ks0 = w;
+    if constexpr (PRE) {
+        if (ks0 < B) {  // wave-uniform
+            calculer_b<1, PF_KB1, NRT>(acc, pre, ks0, B, a_codes, a_sa, lr, lg);
+            ks0 += 16u * KB;
+        }
+    }
+    for (; ks0 < B; ks0 += 16u * KB) {  // wave-uniform
         u32x4 bq[KB][NP];
-#pragma unroll
-        for (uint32_t q = 0; q < KB; ++q) {
-            const uint32_t ks = min(ks0 + 16u * q, B);  // block B of x is zero
-#pragma unroll
-            for (uint32_t p = 0; p < NP; ++p) bq[q][p] = *glob<u32x4>(xsrc + p * pas_p + 64u * ks);
-        }
+        charger_b<NP, KB>(bq, xsrc, pas_p, ks0, B);
         __builtin_amdgcn_sched_barrier(0);  // every load issued before the first MFMA waits
-#pragma unroll
-        for (uint32_t q = 0; q < KB; ++q) {
-            // straight-line code, so that the B loads above stay ahead of every MFMA: a k-step past B
-            // multiplies block B - 1 of the weights by x's zero block
-            const uint32_t ks = min(ks0 + 16u * q, B - 1u);
-            bf16x8 a[NRT];
-#pragma unroll
-            for (uint32_t rt = 0; rt < NRT; ++rt) {
-                const uint32_t o = (16u * rt + lr) * B + ks;
-                const uint32_t mot = lire_lds<uint32_t>(a_codes + 16u * o + 4u * lg);
-                const float sc = __uint_as_float(uint32_t(lire_lds<uint8_t>(a_sa + o)) << 23);
-                const bf16x2 p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(mot, sc, 0);
-                const bf16x2 p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(mot, sc, 1);
-                const bf16x2 p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(mot, sc, 2);
-                const bf16x2 p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(mot, sc, 3);
-                a[rt] = bf16x8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
-            }
-#pragma unroll
-            for (uint32_t p = 0; p < NP; ++p) {
-                const bf16x8 bv = __builtin_bit_cast(bf16x8, bq[q][p]);
-#pragma unroll
-                for (uint32_t rt = 0; rt < NRT; ++rt)
-                    acc[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[rt], bv, acc[rt], 0, 0, 0);
-            }
-        }
+        calculer_b<NP, KB, NRT>(acc, bq, ks0, B, a_codes, a_sa, lr, lg);
     }
     __builtin_amdgcn_sched_barrier(0);
     asm volatile("s_nop 15");
@@ -462,6 +487,19 @@ __device__ __forceinline__ void prefill_bande(const ParamsPrefill& pp, const uin
             tour1 = tb;
     }
     verser_controle(controle, hors_l, pointeur);
+    // the first column tile's activations (one piece: the usual case) are requested now, so that
+    // their latency hides behind the store of the codes
+    const uint32_t lr = lane & 15u, lg = lane >> 4;
+    const uint32_t P = uniforme32(min(reinterpret_cast<const uint32_t*>(pp.pieces)[J == 2u ? 0 : 1], PF_PIECES_BF));
+    const uint32_t debut_e = uniforme32(reinterpret_cast<const uint32_t*>(pp.debut)[e]);
+    const uint32_t* paires = reinterpret_cast<const uint32_t*>(pp.paires);
+    const uint64_t pas_p = uint64_t(J == 2u ? pp.bx : pp.bact) * 64u;
+    const uint8_t* bsrc = reinterpret_cast<const uint8_t*>(J == 2u ? pp.xb : pp.ab) + 16u * lg;
+    const uint32_t wu = uniforme32(w);
+    uint32_t c_suiv = n_e > lr ? paires[debut_e + lr] : 0u;
+    u32x4 pre[PF_KB1][1];
+    const bool avance = P == 1u && wu < B;
+    if (avance) charger_b<1, PF_KB1>(pre, bsrc + uint64_t(J == 2u ? c_suiv / pp.k : c_suiv) * PF_PIECES_BF * pas_p, pas_p, wu, B);
     __syncthreads();  // every tile decoded: the LUT, x and ring regions are free
 
     // ---- store the band's codes and scales
@@ -481,17 +519,11 @@ __device__ __forceinline__ void prefill_bande(const ParamsPrefill& pp, const uin
     // split 16 ways; the partial sums are added in wave order. Each B load feeds every row tile, and
     // B is read once per band.
     const uint32_t nrt = RB / 16u;
-    const uint32_t lr = lane & 15u, lg = lane >> 4;
-    const uint32_t P = uniforme32(min(reinterpret_cast<const uint32_t*>(pp.pieces)[J == 2u ? 0 : 1], PF_PIECES_BF));
-    const uint32_t debut_e = uniforme32(reinterpret_cast<const uint32_t*>(pp.debut)[e]);
-    const uint32_t* paires = reinterpret_cast<const uint32_t*>(pp.paires);
     const float* biais = reinterpret_cast<const float*>(m.biais.p);
-    const uint64_t pas_p = uint64_t(J == 2u ? pp.bx : pp.bact) * 64u;
-    const uint8_t* bsrc = reinterpret_cast<const uint8_t*>(J == 2u ? pp.xb : pp.ab) + 16u * lg;
-    const uint32_t wu = uniforme32(w);
     const uint32_t n_tt = (n_e + 15u) / 16u;
-    uint32_t c_suiv = n_e > lr ? paires[debut_e + lr] : 0u;
-    for (uint32_t tt = 0; tt < n_tt; ++tt) {
+    // one 16-pair column tile; the first is peeled off the loop so that its preloaded B dies there
+    auto tuile = [&](uint32_t tt, auto premier) {
+        constexpr bool PREMIER = decltype(premier)::value;
         const uint32_t tok = 16u * tt + lr;
         const uint32_t c = c_suiv;
         c_suiv = tok + 16u < n_e ? paires[debut_e + tok + 16u] : 0u;
@@ -500,22 +532,24 @@ __device__ __forceinline__ void prefill_bande(const ParamsPrefill& pp, const uin
         f32x4 acc[4];
 #pragma unroll
         for (uint32_t rt = 0; rt < 4; ++rt) acc[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
-        auto produit = [&](auto np, auto kb) {
+        auto produit = [&](auto np, auto kb, auto pre_t) {
             constexpr uint32_t NP = decltype(np)::value, KB = decltype(kb)::value;
+            constexpr bool PRE = decltype(pre_t)::value;
             if (nrt == 4u)
-                produit_bf16<NP, KB, 4>(acc, src, pas_p, wu, B, base + PF_A, a_sa, lr, lg);
+                produit_bf16<NP, KB, 4, PRE>(acc, src, pas_p, wu, B, base + PF_A, a_sa, lr, lg, pre);
             else if (nrt == 2u)
-                produit_bf16<NP, KB, 2>(acc, src, pas_p, wu, B, base + PF_A, a_sa, lr, lg);
+                produit_bf16<NP, KB, 2, PRE>(acc, src, pas_p, wu, B, base + PF_A, a_sa, lr, lg, pre);
             else
-                produit_bf16<NP, KB, 1>(acc, src, pas_p, wu, B, base + PF_A, a_sa, lr, lg);
+                produit_bf16<NP, KB, 1, PRE>(acc, src, pas_p, wu, B, base + PF_A, a_sa, lr, lg, pre);
         };
         using U = uint32_t;
         if (P == 1u)
-            produit(std::integral_constant<U, 1>{}, std::integral_constant<U, 6>{});
+            produit(std::integral_constant<U, 1>{}, std::integral_constant<U, PF_KB1>{},
+                    std::integral_constant<bool, PREMIER>{});
         else if (P == 2u)
-            produit(std::integral_constant<U, 2>{}, std::integral_constant<U, 3>{});
+            produit(std::integral_constant<U, 2>{}, std::integral_constant<U, 3>{}, std::false_type{});
         else if (P == 3u)
-            produit(std::integral_constant<U, 3>{}, std::integral_constant<U, 2>{});
+            produit(std::integral_constant<U, 3>{}, std::integral_constant<U, 2>{}, std::false_type{});
 #pragma unroll
         for (uint32_t rt = 0; rt < 4; ++rt)
             if (rt < nrt) ecrire_lds<f32x4>(a_part + ((rt * 16u + w) * 64u + lane) * 16u, acc[rt]);
@@ -537,7 +571,9 @@ __device__ __forceinline__ void prefill_bande(const ParamsPrefill& pp, const uin
             }
         }
         __syncthreads();
-    }
+    };
+    tuile(0u, std::true_type{});  // n_e >= 1
+    for (uint32_t tt = 1; tt < n_tt; ++tt) tuile(tt, std::false_type{});
 }
 
 }  // namespace trc
