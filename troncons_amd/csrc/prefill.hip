@@ -269,20 +269,26 @@ namespace trc {
 // column n: the MFMA adds the products of each lane group's eight K values, so any order common to A
 // and B gives the dot product. The B loads of KB k-steps are issued before their MFMAs. Columns past
 // the expert's pairs load a valid position; their sums are never stored.
-template <uint32_t NP, uint32_t KB>
-__device__ __forceinline__ void charger_b(u32x4 (&bq)[KB][NP], const uint8_t* xsrc, uint64_t pas_p, uint32_t ks0,
+// A batch of B loads: PF_LOT 16-byte loads per lane, KB = PF_LOT / NP k-steps of NP pieces each;
+// bq[q * NP + p] is piece p of k-step ks0 + 16 q.
+constexpr uint32_t PF_LOT = 6;
+
+template <uint32_t NP>
+__device__ __forceinline__ void charger_b(u32x4 (&bq)[PF_LOT], const uint8_t* xsrc, uint64_t pas_p, uint32_t ks0,
                                           uint32_t B) {
+    constexpr uint32_t KB = PF_LOT / NP;
 #pragma unroll
     for (uint32_t q = 0; q < KB; ++q) {
         const uint32_t ks = min(ks0 + 16u * q, B);  // block B of an activation row is zero
 #pragma unroll
-        for (uint32_t p = 0; p < NP; ++p) bq[q][p] = *glob<u32x4>(xsrc + p * pas_p + 64u * ks);
+        for (uint32_t p = 0; p < NP; ++p) bq[q * NP + p] = *glob<u32x4>(xsrc + p * pas_p + 64u * ks);
     }
 }
 
-template <uint32_t NP, uint32_t KB, uint32_t NRT>
-__device__ __forceinline__ void calculer_b(f32x4 (&acc)[4], const u32x4 (&bq)[KB][NP], uint32_t ks0, uint32_t B,
+template <uint32_t NP, uint32_t NRT>
+__device__ __forceinline__ void calculer_b(f32x4 (&acc)[4], const u32x4 (&bq)[PF_LOT], uint32_t ks0, uint32_t B,
                                            uint32_t a_codes, uint32_t a_sa, uint32_t lr, uint32_t lg) {
+    constexpr uint32_t KB = PF_LOT / NP;
 #pragma unroll
     for (uint32_t q = 0; q < KB; ++q) {
         // straight-line code, so that the B loads stay ahead of every MFMA: a k-step past B
@@ -302,7 +308,7 @@ __device__ __forceinline__ void calculer_b(f32x4 (&acc)[4], const u32x4 (&bq)[KB
         }
 #pragma unroll
         for (uint32_t p = 0; p < NP; ++p) {
-            const bf16x8 bv = __builtin_bit_cast(bf16x8, bq[q][p]);
+            const bf16x8 bv = __builtin_bit_cast(bf16x8, bq[q * NP + p]);
 #pragma unroll
             for (uint32_t rt = 0; rt < NRT; ++rt)
                 acc[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[rt], bv, acc[rt], 0, 0, 0);
@@ -312,25 +318,23 @@ __device__ __forceinline__ void calculer_b(f32x4 (&acc)[4], const u32x4 (&bq)[KB
 
 // The whole product of a column tile; PRE: the first batch of B (k-steps w, w + 16, ...) is already
 // in `pre` (loaded before the band's store, so that its latency hides behind it).
-constexpr uint32_t PF_KB1 = 6;  // k-steps per batch of B loads with one piece
-
-template <uint32_t NP, uint32_t KB, uint32_t NRT, bool PRE>
+template <uint32_t NP, uint32_t NRT, bool PRE>
 __device__ __forceinline__ void produit_bf16(f32x4 (&acc)[4], const uint8_t* xsrc, uint64_t pas_p, uint32_t w,
                                              uint32_t B, uint32_t a_codes, uint32_t a_sa, uint32_t lr, uint32_t lg,
-                                             const u32x4 (&pre)[PF_KB1][1]) {
-    static_assert(!PRE || (NP == 1u && KB == PF_KB1), "the first batch is preloaded for one piece only");
+                                             const u32x4 (&pre)[PF_LOT]) {
+    constexpr uint32_t KB = PF_LOT / NP;
     uint32_t ks0 = w;
     if constexpr (PRE) {
         if (ks0 < B) {  // wave-uniform
-            calculer_b<1, PF_KB1, NRT>(acc, pre, ks0, B, a_codes, a_sa, lr, lg);
+            calculer_b<NP, NRT>(acc, pre, ks0, B, a_codes, a_sa, lr, lg);
             ks0 += 16u * KB;
         }
     }
     for (; ks0 < B; ks0 += 16u * KB) {  // wave-uniform
-        u32x4 bq[KB][NP];
-        charger_b<NP, KB>(bq, xsrc, pas_p, ks0, B);
+        u32x4 bq[PF_LOT];
+        charger_b<NP>(bq, xsrc, pas_p, ks0, B);
         __builtin_amdgcn_sched_barrier(0);  // every load issued before the first MFMA waits
-        calculer_b<NP, KB, NRT>(acc, bq, ks0, B, a_codes, a_sa, lr, lg);
+        calculer_b<NP, NRT>(acc, bq, ks0, B, a_codes, a_sa, lr, lg);
     }
     __builtin_amdgcn_sched_barrier(0);
     asm volatile("s_nop 15");
@@ -487,8 +491,8 @@ __device__ __forceinline__ void prefill_bande(const ParamsPrefill& pp, const uin
             tour1 = tb;
     }
     verser_controle(controle, hors_l, pointeur);
-    // the first column tile's activations (one piece: the usual case) are requested now, so that
-    // their latency hides behind the store of the codes
+    // the first batch of the first column tile's activations is requested now, so that its latency
+    // hides behind the store of the codes
     const uint32_t lr = lane & 15u, lg = lane >> 4;
     const uint32_t P = uniforme32(min(reinterpret_cast<const uint32_t*>(pp.pieces)[J == 2u ? 0 : 1], PF_PIECES_BF));
     const uint32_t debut_e = uniforme32(reinterpret_cast<const uint32_t*>(pp.debut)[e]);
@@ -497,9 +501,18 @@ __device__ __forceinline__ void prefill_bande(const ParamsPrefill& pp, const uin
     const uint8_t* bsrc = reinterpret_cast<const uint8_t*>(J == 2u ? pp.xb : pp.ab) + 16u * lg;
     const uint32_t wu = uniforme32(w);
     uint32_t c_suiv = n_e > lr ? paires[debut_e + lr] : 0u;
-    u32x4 pre[PF_KB1][1];
-    const bool avance = P == 1u && wu < B;
-    if (avance) charger_b<1, PF_KB1>(pre, bsrc + uint64_t(J == 2u ? c_suiv / pp.k : c_suiv) * PF_PIECES_BF * pas_p, pas_p, wu, B);
+    u32x4 pre[PF_LOT];
+    {
+        const uint8_t* src0 = bsrc + uint64_t(J == 2u ? c_suiv / pp.k : c_suiv) * PF_PIECES_BF * pas_p;
+        if (wu < B) {  // wave-uniform
+            if (P == 1u)
+                charger_b<1>(pre, src0, pas_p, wu, B);
+            else if (P == 2u)
+                charger_b<2>(pre, src0, pas_p, wu, B);
+            else if (P == 3u)
+                charger_b<3>(pre, src0, pas_p, wu, B);
+        }
+    }
     __syncthreads();  // every tile decoded: the LUT, x and ring regions are free
 
     // ---- store the band's codes and scales
@@ -532,24 +545,22 @@ __device__ __forceinline__ void prefill_bande(const ParamsPrefill& pp, const uin
         f32x4 acc[4];
 #pragma unroll
         for (uint32_t rt = 0; rt < 4; ++rt) acc[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
-        auto produit = [&](auto np, auto kb, auto pre_t) {
-            constexpr uint32_t NP = decltype(np)::value, KB = decltype(kb)::value;
-            constexpr bool PRE = decltype(pre_t)::value;
+        auto produit = [&](auto np) {
+            constexpr uint32_t NP = decltype(np)::value;
             if (nrt == 4u)
-                produit_bf16<NP, KB, 4, PRE>(acc, src, pas_p, wu, B, base + PF_A, a_sa, lr, lg, pre);
+                produit_bf16<NP, 4, PREMIER>(acc, src, pas_p, wu, B, base + PF_A, a_sa, lr, lg, pre);
             else if (nrt == 2u)
-                produit_bf16<NP, KB, 2, PRE>(acc, src, pas_p, wu, B, base + PF_A, a_sa, lr, lg, pre);
+                produit_bf16<NP, 2, PREMIER>(acc, src, pas_p, wu, B, base + PF_A, a_sa, lr, lg, pre);
             else
-                produit_bf16<NP, KB, 1, PRE>(acc, src, pas_p, wu, B, base + PF_A, a_sa, lr, lg, pre);
+                produit_bf16<NP, 1, PREMIER>(acc, src, pas_p, wu, B, base + PF_A, a_sa, lr, lg, pre);
         };
         using U = uint32_t;
         if (P == 1u)
-            produit(std::integral_constant<U, 1>{}, std::integral_constant<U, PF_KB1>{},
-                    std::integral_constant<bool, PREMIER>{});
+            produit(std::integral_constant<U, 1>{});
         else if (P == 2u)
-            produit(std::integral_constant<U, 2>{}, std::integral_constant<U, 3>{}, std::false_type{});
+            produit(std::integral_constant<U, 2>{});
         else if (P == 3u)
-            produit(std::integral_constant<U, 3>{}, std::integral_constant<U, 2>{}, std::false_type{});
+            produit(std::integral_constant<U, 3>{});
 #pragma unroll
         for (uint32_t rt = 0; rt < 4; ++rt)
             if (rt < nrt) ecrire_lds<f32x4>(a_part + ((rt * 16u + w) * 64u + lane) * 16u, acc[rt]);
