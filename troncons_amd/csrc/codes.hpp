@@ -321,8 +321,11 @@ __device__ __forceinline__ void corps_codes(const Tache& tc, const PrepCodes& p,
             d = fmaf(w3.x, xa.w, d);
             d = fmaf(w3.y, xb.w, d);
             const float c = __builtin_amdgcn_ldexpf(d, int(ent << 7) >> 24);
-            const bool nouvelle = int(ent) < 0 && !(m == 0u && q == 0u && actif);
-            const uint64_t vote = __builtin_amdgcn_ballot_w64(nouvelle);
+            // lanes whose block starts a row, except the tile's first block (lanes q == 0 of macro-step
+            // 0 in each half): that row's sum goes to the tile's first slot. The entries of inactive
+            // lanes are padding, which starts no row.
+            const uint64_t vote =
+                __builtin_amdgcn_ballot_w64(int(ent) < 0) & (m == 0u ? ~0x0000000F0000000Full : ~0ull);
             if (vote == 0) {
                 if (TOUS || actif) acc += c;
             } else {
