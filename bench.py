@@ -12,7 +12,7 @@ Other measurement modes (not the driver's line): --config 1 (one down_proj matri
 expert MLP), both rotating over the 128 experts; --config 4 (a token through L resident MoE layers,
 default 36, about 52 GB of parts; --ordo streams them from a .trc file through the native scheduler,
 with --prechargement / --biais-cache); --config 5 (a batched prefill of 512 positions with Zipf
-routing, grouped GEMM on the block-scaled FP4 MFMA); --config 6 (a whole decode step: embedding,
+routing, grouped GEMM on the bf16 MFMA); --config 6 (a whole decode step: embedding,
 L gpt-oss layers of Q8_0 attention and fused compressed MoE, the 201088-row head, argmax).
 """
 from __future__ import annotations
