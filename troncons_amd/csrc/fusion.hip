@@ -508,12 +508,12 @@ uint32_t grille_tuiles(uint64_t octets, uint32_t N, uint32_t tuiles_par_bloc) {
 
 constexpr uint32_t TUILES_ECHELLES = trc::FILS_ECHELLES_FUSION / 32;
 
-// Grid of a DELTA pass over `blocs` blocks: each half-wavefront takes a run of about 8 macro-steps
+// Grid of a DELTA pass over `blocs` blocks: each half-wavefront takes a run of about 16 macro-steps
 // (whole tiles, at least one), so that a block's prologue (LUT, record, medians, top-k) and a ring's
 // opening serve several tiles.
 uint32_t grille_echelles(uint64_t blocs, uint32_t n_delta) {
     const uint32_t n = n_delta ? n_delta : 1u;
-    return grille_tuiles(blocs, n * (n < 8u ? 8u / n : 1u), TUILES_ECHELLES);
+    return grille_tuiles(blocs, n * (n < 16u ? 16u / n : 1u), TUILES_ECHELLES);
 }
 
 // Workspace of one matrix job: block entries (u32 per block + staging margin), then partial sums.

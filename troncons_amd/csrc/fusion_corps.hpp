@@ -463,11 +463,20 @@ __device__ __forceinline__ void corps_echelles_fusion(const Tache& tc, const Pre
         }
     };
     const gptr<uint32_t> etats = glob<uint32_t>(h.etats);
+    // the initial states of ECH_KMAX tiles at a time; the next group's are requested while the
+    // current group decodes
+    uint32_t suiv[ECH_KMAX];
+#pragma unroll
+    for (uint32_t kk = 0; kk < ECH_KMAX; ++kk) suiv[kk] = etats[min(t_deb + kk, h.T - 1u) * VOIES + v];
     for (uint32_t k0 = 0; k0 < nt_max; k0 += ECH_KMAX) {  // wave-uniform
         uint32_t etat[ECH_KMAX];
 #pragma unroll
-        for (uint32_t kk = 0; kk < ECH_KMAX; ++kk)
-            etat[kk] = etats[min(t_deb + k0 + kk, h.T - 1u) * VOIES + v];
+        for (uint32_t kk = 0; kk < ECH_KMAX; ++kk) etat[kk] = suiv[kk];
+        if (k0 + ECH_KMAX < nt_max) {  // wave-uniform
+#pragma unroll
+            for (uint32_t kk = 0; kk < ECH_KMAX; ++kk)
+                suiv[kk] = etats[min(t_deb + k0 + ECH_KMAX + kk, h.T - 1u) * VOIES + v];
+        }
 #pragma unroll
         for (uint32_t kk = 0; kk < ECH_KMAX; ++kk) {
             const uint32_t k = k0 + kk;
