@@ -168,6 +168,22 @@ def test_prefill_f32_activations(fz, bits):
         couche.c.liberer()
 
 
+def test_prefill_wide_rows(fz):
+    """4096-wide matrices: the band is 32 rows (two MFMA row tiles), so the passes over one and two
+    column tiles run with nrt = 2; Zipf routing gives the first expert more than 16 pairs."""
+    E, T, k, N = 3, 20, 2, (1, 16)
+    dims = DimsExpert.de([4096, 4096, 4096], [4096, 4096, 4096])
+    couche = Couche(fz, 81, E, dims, N)
+    idx, w = _routage(82, T, E, k, zipf=1.1)
+    assert np.bincount(idx.reshape(-1), minlength=E).max() > 16
+    x = np.stack([O.synth_normale_bf16(83, 4, i, 4096, 1.0) for i in range(T)])
+    residu0 = np.zeros((T, 4096), np.float32)
+    got, ctl = _lancer(fz, couche, E, dims, x, idx, w, residu0, N)
+    assert list(ctl) == [0, 0, 0, 0]
+    _verifier(got, residu0, x, idx, w, _slots(81, E, dims), dims)
+    couche.c.liberer()
+
+
 def test_prefill_gpt_oss_shape(fz):
     """Config-5 shape family: 2880 x 2880 gpt-oss experts, N = 16 / 4, 16 positions over 8 experts
     with Zipf routing; also determinism (a second call gives the same bits)."""

@@ -273,19 +273,19 @@ namespace trc {
 // bq[q * NP + p] is piece p of k-step ks0 + 16 q.
 constexpr uint32_t PF_LOT = 6;
 
-template <uint32_t NP>
+template <uint32_t NP, uint32_t PAS>
 __device__ __forceinline__ void charger_b(u32x4 (&bq)[PF_LOT], const uint8_t* xsrc, uint64_t pas_p, uint32_t ks0,
                                           uint32_t B) {
     constexpr uint32_t KB = PF_LOT / NP;
 #pragma unroll
     for (uint32_t q = 0; q < KB; ++q) {
-        const uint32_t ks = min(ks0 + 16u * q, B);  // block B of an activation row is zero
+        const uint32_t ks = min(ks0 + PAS * q, B);  // block B of an activation row is zero
 #pragma unroll
         for (uint32_t p = 0; p < NP; ++p) bq[q * NP + p] = *glob<u32x4>(xsrc + p * pas_p + 64u * ks);
     }
 }
 
-template <uint32_t NP, uint32_t NRT>
+template <uint32_t NP, uint32_t NRT, uint32_t PAS>
 __device__ __forceinline__ void calculer_b(f32x4 (&acc)[4], const u32x4 (&bq)[PF_LOT], uint32_t ks0, uint32_t B,
                                            uint32_t a_codes, uint32_t a_sa, uint32_t lr, uint32_t lg) {
     constexpr uint32_t KB = PF_LOT / NP;
@@ -293,7 +293,7 @@ __device__ __forceinline__ void calculer_b(f32x4 (&acc)[4], const u32x4 (&bq)[PF
     for (uint32_t q = 0; q < KB; ++q) {
         // straight-line code, so that the B loads stay ahead of every MFMA: a k-step past B
         // multiplies block B - 1 of the weights by the activations' zero block
-        const uint32_t ks = min(ks0 + 16u * q, B - 1u);
+        const uint32_t ks = min(ks0 + PAS * q, B - 1u);
         bf16x8 a[NRT];
 #pragma unroll
         for (uint32_t rt = 0; rt < NRT; ++rt) {
@@ -316,9 +316,9 @@ __device__ __forceinline__ void calculer_b(f32x4 (&acc)[4], const u32x4 (&bq)[PF
     }
 }
 
-// The whole product of a column tile; PRE: the first batch of B (k-steps w, w + 16, ...) is already
-// in `pre` (loaded before the band's store, so that its latency hides behind it).
-template <uint32_t NP, uint32_t NRT, bool PRE>
+// The whole product of a column tile over the k-steps w, w + PAS, ...; PRE: the first batch of B is
+// already in `pre` (loaded before the band's store, so that its latency hides behind it).
+template <uint32_t NP, uint32_t NRT, bool PRE, uint32_t PAS>
 __device__ __forceinline__ void produit_bf16(f32x4 (&acc)[4], const uint8_t* xsrc, uint64_t pas_p, uint32_t w,
                                              uint32_t B, uint32_t a_codes, uint32_t a_sa, uint32_t lr, uint32_t lg,
                                              const u32x4 (&pre)[PF_LOT]) {
@@ -326,15 +326,15 @@ __device__ __forceinline__ void produit_bf16(f32x4 (&acc)[4], const uint8_t* xsr
     uint32_t ks0 = w;
     if constexpr (PRE) {
         if (ks0 < B) {  // wave-uniform
-            calculer_b<NP, NRT>(acc, pre, ks0, B, a_codes, a_sa, lr, lg);
-            ks0 += 16u * KB;
+            calculer_b<NP, NRT, PAS>(acc, pre, ks0, B, a_codes, a_sa, lr, lg);
+            ks0 += PAS * KB;
         }
     }
-    for (; ks0 < B; ks0 += 16u * KB) {  // wave-uniform
+    for (; ks0 < B; ks0 += PAS * KB) {  // wave-uniform
         u32x4 bq[PF_LOT];
-        charger_b<NP>(bq, xsrc, pas_p, ks0, B);
+        charger_b<NP, PAS>(bq, xsrc, pas_p, ks0, B);
         __builtin_amdgcn_sched_barrier(0);  // every load issued before the first MFMA waits
-        calculer_b<NP, NRT>(acc, bq, ks0, B, a_codes, a_sa, lr, lg);
+        calculer_b<NP, NRT, PAS>(acc, bq, ks0, B, a_codes, a_sa, lr, lg);
     }
     __builtin_amdgcn_sched_barrier(0);
     asm volatile("s_nop 15");
@@ -500,17 +500,32 @@ __device__ __forceinline__ void prefill_bande(const ParamsPrefill& pp, const uin
     const uint64_t pas_p = uint64_t(J == 2u ? pp.bx : pp.bact) * 64u;
     const uint8_t* bsrc = reinterpret_cast<const uint8_t*>(J == 2u ? pp.xb : pp.ab) + 16u * lg;
     const uint32_t wu = uniforme32(w);
-    uint32_t c_suiv = n_e > lr ? paires[debut_e + lr] : 0u;
+    // Column tiles of 16 pairs go two at a time while two remain, waves 0-7 on the first and 8-15
+    // on the second (K split 8 ways), then one at a time (K split 16 ways).
+    const uint32_t n_tt = (n_e + 15u) / 16u;
+    const bool duo0 = n_tt >= 2u;
+    // the first pass's tile and K share of this wave, and its column
+    const uint32_t g0 = duo0 ? wu >> 3 : 0u, wk0 = duo0 ? (wu & 7u) : wu;
+    const uint32_t tok0 = 16u * g0 + lr;
+    const uint32_t c0 = tok0 < n_e ? paires[debut_e + tok0] : paires[debut_e];
     u32x4 pre[PF_LOT];
     {
-        const uint8_t* src0 = bsrc + uint64_t(J == 2u ? c_suiv / pp.k : c_suiv) * PF_PIECES_BF * pas_p;
-        if (wu < B) {  // wave-uniform
+        const uint8_t* src0 = bsrc + uint64_t(J == 2u ? c0 / pp.k : c0) * PF_PIECES_BF * pas_p;
+        auto charger0 = [&](auto np) {
+            constexpr uint32_t NP = decltype(np)::value;
+            if (duo0)
+                charger_b<NP, 8>(pre, src0, pas_p, wk0, B);
+            else
+                charger_b<NP, 16>(pre, src0, pas_p, wk0, B);
+        };
+        using U = uint32_t;
+        if (wk0 < B) {  // wave-uniform
             if (P == 1u)
-                charger_b<1>(pre, src0, pas_p, wu, B);
+                charger0(std::integral_constant<U, 1>{});
             else if (P == 2u)
-                charger_b<2>(pre, src0, pas_p, wu, B);
+                charger0(std::integral_constant<U, 2>{});
             else if (P == 3u)
-                charger_b<3>(pre, src0, pas_p, wu, B);
+                charger0(std::integral_constant<U, 3>{});
         }
     }
     __syncthreads();  // every tile decoded: the LUT, x and ring regions are free
@@ -533,13 +548,15 @@ __device__ __forceinline__ void prefill_bande(const ParamsPrefill& pp, const uin
     // B is read once per band.
     const uint32_t nrt = RB / 16u;
     const float* biais = reinterpret_cast<const float*>(m.biais.p);
-    const uint32_t n_tt = (n_e + 15u) / 16u;
-    // one 16-pair column tile; the first is peeled off the loop so that its preloaded B dies there
-    auto tuile = [&](uint32_t tt, auto premier) {
+    // one pass over NT column tiles from tile tt; the first pass is peeled off the loop so that its
+    // preloaded B dies there
+    auto passe = [&](uint32_t tt, auto nt_t, auto premier) {
+        constexpr uint32_t NT = decltype(nt_t)::value;
         constexpr bool PREMIER = decltype(premier)::value;
-        const uint32_t tok = 16u * tt + lr;
-        const uint32_t c = c_suiv;
-        c_suiv = tok + 16u < n_e ? paires[debut_e + tok + 16u] : 0u;
+        constexpr uint32_t PAS = 16u / NT, VG = 16u / NT;  // waves per tile
+        const uint32_t g = NT == 2u ? wu >> 3 : 0u, wk = NT == 2u ? (wu & 7u) : wu;
+        const uint32_t tok = 16u * (tt + g) + lr;
+        const uint32_t c = PREMIER ? c0 : (tok < n_e ? paires[debut_e + tok] : paires[debut_e]);
         // column source: position c / k's x for gate and up, pair c's act for down
         const uint8_t* src = bsrc + uint64_t(J == 2u ? c / pp.k : c) * PF_PIECES_BF * pas_p;
         f32x4 acc[4];
@@ -548,11 +565,11 @@ __device__ __forceinline__ void prefill_bande(const ParamsPrefill& pp, const uin
         auto produit = [&](auto np) {
             constexpr uint32_t NP = decltype(np)::value;
             if (nrt == 4u)
-                produit_bf16<NP, 4, PREMIER>(acc, src, pas_p, wu, B, base + PF_A, a_sa, lr, lg, pre);
+                produit_bf16<NP, 4, PREMIER, PAS>(acc, src, pas_p, wk, B, base + PF_A, a_sa, lr, lg, pre);
             else if (nrt == 2u)
-                produit_bf16<NP, 2, PREMIER>(acc, src, pas_p, wu, B, base + PF_A, a_sa, lr, lg, pre);
+                produit_bf16<NP, 2, PREMIER, PAS>(acc, src, pas_p, wk, B, base + PF_A, a_sa, lr, lg, pre);
             else
-                produit_bf16<NP, 1, PREMIER>(acc, src, pas_p, wu, B, base + PF_A, a_sa, lr, lg, pre);
+                produit_bf16<NP, 1, PREMIER, PAS>(acc, src, pas_p, wk, B, base + PF_A, a_sa, lr, lg, pre);
         };
         using U = uint32_t;
         if (P == 1u)
@@ -561,30 +578,45 @@ __device__ __forceinline__ void prefill_bande(const ParamsPrefill& pp, const uin
             produit(std::integral_constant<U, 2>{});
         else if (P == 3u)
             produit(std::integral_constant<U, 3>{});
+        // partial sums: [tile g][row tile][wave of the tile][lane], nrt x 16 KiB for either pass shape
 #pragma unroll
         for (uint32_t rt = 0; rt < 4; ++rt)
-            if (rt < nrt) ecrire_lds<f32x4>(a_part + ((rt * 16u + w) * 64u + lane) * 16u, acc[rt]);
+            if (rt < nrt) ecrire_lds<f32x4>(a_part + (((g * nrt + rt) * VG + wk) * 64u + lane) * 16u, acc[rt]);
         __syncthreads();
-        if (threadIdx.x < nrt * 256u) {
-            const uint32_t rt = threadIdx.x >> 8, reste = threadIdx.x & 255u;
-            const uint32_t ln = reste >> 2, r = reste & 3u;
-            float s = 0.0f;
-            for (uint32_t ww = 0; ww < 16u; ++ww)
-                s += lire_lds<float>(a_part + ((rt * 16u + ww) * 64u + ln) * 16u + 4u * r);
-            const uint32_t ligne = 16u * rt + 4u * (ln >> 4) + r, jeton = 16u * tt + (ln & 15u);
-            if (ligne < nl && jeton < n_e) {
-                const uint32_t cc = paires[debut_e + jeton];
-                const float y = s + biais[r0 + ligne];
-                if (J == 2u)
-                    reinterpret_cast<float*>(pp.gu)[(uint64_t(cc) * 2u + j) * R + r0 + ligne] = y;
-                else
-                    reinterpret_cast<float*>(pp.s)[uint64_t(cc) * pp.D + r0 + ligne] = y;
+#pragma unroll
+        for (uint32_t u = 0; u < NT; ++u) {
+            const uint32_t o = threadIdx.x + 1024u * u;  // output (tile gg, row tile, column, row)
+            const uint32_t gg = NT == 2u ? o / (nrt * 256u) : 0u, reste_o = o - gg * (nrt * 256u);
+            if (gg < NT && reste_o < nrt * 256u) {
+                const uint32_t rt = reste_o >> 8, reste = reste_o & 255u;
+                const uint32_t ln = reste >> 2, r = reste & 3u;
+                float s = 0.0f;
+                for (uint32_t ww = 0; ww < VG; ++ww)
+                    s += lire_lds<float>(a_part + (((gg * nrt + rt) * VG + ww) * 64u + ln) * 16u + 4u * r);
+                const uint32_t ligne = 16u * rt + 4u * (ln >> 4) + r, jeton = 16u * (tt + gg) + (ln & 15u);
+                if (ligne < nl && jeton < n_e) {
+                    const uint32_t cc = paires[debut_e + jeton];
+                    const float y = s + biais[r0 + ligne];
+                    if (J == 2u)
+                        reinterpret_cast<float*>(pp.gu)[(uint64_t(cc) * 2u + j) * R + r0 + ligne] = y;
+                    else
+                        reinterpret_cast<float*>(pp.s)[uint64_t(cc) * pp.D + r0 + ligne] = y;
+                }
             }
         }
         __syncthreads();
     };
-    tuile(0u, std::true_type{});  // n_e >= 1
-    for (uint32_t tt = 1; tt < n_tt; ++tt) tuile(tt, std::false_type{});
+    using U2 = uint32_t;
+    uint32_t tt = 0;
+    if (duo0) {
+        passe(0u, std::integral_constant<U2, 2>{}, std::true_type{});
+        tt = 2u;
+    } else {
+        passe(0u, std::integral_constant<U2, 1>{}, std::true_type{});  // n_e >= 1
+        tt = 1u;
+    }
+    for (; tt + 1u < n_tt; tt += 2u) passe(tt, std::integral_constant<U2, 2>{}, std::false_type{});
+    if (tt < n_tt) passe(tt, std::integral_constant<U2, 1>{}, std::false_type{});
 }
 
 }  // namespace trc
