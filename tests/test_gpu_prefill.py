@@ -4,9 +4,8 @@ Each position's residual is checked against the reference's own chain run by the
 (position, slot) — gemv_mxfp4 gate and up, swiglu_oai, gemv_mxfp4 down, then the ordered combine
 (trc-modele/src/lib.rs:688-710, passe.cuh:598-622) — and against the same computation in f64 from the
 uncompressed weights: within 1e-5 * max|change| of both, per position (the fused path's GEMV
-tolerance: gate and up multiply exact bf16 pieces of x, down exact fp8 pieces of act, so only the
-fp32 accumulation order and a 2^-20 remainder of act differ). Decoded weights are checked bit for bit
-by the other suites.
+tolerance: gate and up multiply exact bf16 pieces of x, down exact bf16 pieces of act, so only the
+fp32 accumulation order differs). Decoded weights are checked bit for bit by the other suites.
 """
 from __future__ import annotations
 
@@ -181,6 +180,24 @@ def test_prefill_wide_rows(fz):
     got, ctl = _lancer(fz, couche, E, dims, x, idx, w, residu0, N)
     assert list(ctl) == [0, 0, 0, 0]
     _verifier(got, residu0, x, idx, w, _slots(81, E, dims), dims)
+    couche.c.liberer()
+
+
+def test_prefill_band_heights(fz):
+    """Band heights by row width: gate and up are 3072 wide (96 blocks a row: 64-row bands, four
+    MFMA row tiles), down is 256 wide (8 blocks: 80-row bands, five row tiles) over 3072 rows, so its
+    last band holds 32 rows and 48 padding rows; Zipf routing gives one expert more than 32 pairs,
+    so the paired and single column-tile passes both run at both heights."""
+    E, T, k, N = 3, 40, 2, (1, 16)
+    dims = DimsExpert.de([256, 256, 3072], [3072, 3072, 256])
+    couche = Couche(fz, 91, E, dims, N)
+    idx, w = _routage(92, T, E, k, zipf=1.1)
+    assert np.bincount(idx.reshape(-1), minlength=E).max() > 32
+    x = np.stack([O.synth_normale_bf16(93, 4, i, 3072, 1.0) for i in range(T)])
+    residu0 = np.stack([O.synth_normale_bf16(94, 4, i, 3072, 0.5) for i in range(T)])
+    got, ctl = _lancer(fz, couche, E, dims, x, idx, w, residu0, N)
+    assert list(ctl) == [0, 0, 0, 0]
+    _verifier(got, residu0, x, idx, w, _slots(91, E, dims), dims)
     couche.c.liberer()
 
 

@@ -49,15 +49,16 @@ constexpr uint32_t PF_PAIRES_MAX = 16384; // positions x k per call
 constexpr uint32_t ECHELLE_UN = 127u;     // E8M0 1.0
 
 constexpr uint32_t PF_TOURS = 2;          // decode rounds per band: a band's tiles are at most 64
-constexpr uint32_t PF_RB_MAX = 64;         // rows per band
+constexpr uint32_t PF_RB_MAX = 80;         // rows per band
+constexpr uint32_t PF_RT_MAX = PF_RB_MAX / 16u;  // row tiles per band
 
 // LDS of prefill_mfma after the decode (every region of the decode is free then): codes [RB][B][16 B]
-// at 0 (rows of exactly B blocks), scales [RB][B] after them, then the partial sums of the MFMA phase
-// (RB/16 row tiles x 16 waves x 64 lanes x 16 B).
+// at 0 (rows of exactly B blocks), scales [RB][B] after them, then the partial sums of the MFMA phase,
+// half the waves' at a time (RB/16 row tiles x 8 waves x 64 lanes x 16 B).
 constexpr uint32_t PF_A = 0;
 __host__ __device__ inline uint32_t pf_sa(uint32_t rb, uint32_t b) { return rb * b * 16u; }
 __host__ __device__ inline uint32_t pf_part(uint32_t rb, uint32_t b) { return (pf_sa(rb, b) + rb * b + 15u) & ~15u; }
-__host__ __device__ inline uint32_t pf_part_octets(uint32_t rb) { return (rb / 16u) * 16u * 64u * 16u; }
+__host__ __device__ inline uint32_t pf_part_octets(uint32_t rb) { return (rb / 16u) * 8u * 64u * 16u; }
 __host__ __device__ inline bool pf_lds_tient(uint32_t rb, uint32_t b) { return pf_part(rb, b) + pf_part_octets(rb) <= LDS_GEMV; }
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -82,7 +83,7 @@ struct ParamsPrefill {
     uint64_t ab;           // act pieces per pair, like xb with bact blocks per piece row
     uint64_t s;            // f32[T*k][D]
     uint32_t lignes[3], colonnes[3];
-    uint32_t rb[3];        // rows per band (16, 32 or 64)
+    uint32_t rb[3];        // rows per band (16, 32, 64 or 80)
     uint32_t T, k, E, D;
     uint32_t bx, bact;     // blocks per piece row of x and act: C/32 + 1, R/32 + 1
     uint32_t quatre;       // the combine takes 4 rows per thread (D % 4 == 0, residus 16-byte aligned)
@@ -286,7 +287,7 @@ __device__ __forceinline__ void charger_b(u32x4 (&bq)[PF_LOT], const uint8_t* xs
 }
 
 template <uint32_t NP, uint32_t NRT, uint32_t PAS>
-__device__ __forceinline__ void calculer_b(f32x4 (&acc)[4], const u32x4 (&bq)[PF_LOT], uint32_t ks0, uint32_t B,
+__device__ __forceinline__ void calculer_b(f32x4 (&acc)[PF_RT_MAX], const u32x4 (&bq)[PF_LOT], uint32_t ks0, uint32_t B,
                                            uint32_t a_codes, uint32_t a_sa, uint32_t lr, uint32_t lg) {
     constexpr uint32_t KB = PF_LOT / NP;
 #pragma unroll
@@ -319,7 +320,7 @@ __device__ __forceinline__ void calculer_b(f32x4 (&acc)[4], const u32x4 (&bq)[PF
 // The whole product of a column tile over the k-steps w, w + PAS, ...; PRE: the first batch of B is
 // already in `pre` (loaded before the band's store, so that its latency hides behind it).
 template <uint32_t NP, uint32_t NRT, bool PRE, uint32_t PAS>
-__device__ __forceinline__ void produit_bf16(f32x4 (&acc)[4], const uint8_t* xsrc, uint64_t pas_p, uint32_t w,
+__device__ __forceinline__ void produit_bf16(f32x4 (&acc)[PF_RT_MAX], const uint8_t* xsrc, uint64_t pas_p, uint32_t w,
                                              uint32_t B, uint32_t a_codes, uint32_t a_sa, uint32_t lr, uint32_t lg,
                                              const u32x4 (&pre)[PF_LOT]) {
     constexpr uint32_t KB = PF_LOT / NP;
@@ -441,7 +442,7 @@ __device__ __forceinline__ void poser_tour(const TourBande& tb, uint32_t t, uint
 // One band of rows [r0, r0 + nl) of matrix j of expert e against the expert's pairs: its tiles
 // decoded in up to two rounds of 32 (one tile per half-wavefront a round), stored in LDS as MXFP4,
 // then the bf16 MFMA (weights converted where they are read): each of the 16 waves takes every row
-// tile of the band (up to 4) over its share of K, so that each B load feeds every row tile and B is
+// tile of the band (up to 5) over its share of K, so that each B load feeds every row tile and B is
 // read once per band.
 template <uint32_t J>
 __device__ __forceinline__ void prefill_bande(const ParamsPrefill& pp, const uint32_t* __restrict__ luts,
@@ -559,12 +560,14 @@ __device__ __forceinline__ void prefill_bande(const ParamsPrefill& pp, const uin
         const uint32_t c = PREMIER ? c0 : (tok < n_e ? paires[debut_e + tok] : paires[debut_e]);
         // column source: position c / k's x for gate and up, pair c's act for down
         const uint8_t* src = bsrc + uint64_t(J == 2u ? c / pp.k : c) * PF_PIECES_BF * pas_p;
-        f32x4 acc[4];
+        f32x4 acc[PF_RT_MAX];
 #pragma unroll
-        for (uint32_t rt = 0; rt < 4; ++rt) acc[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (uint32_t rt = 0; rt < PF_RT_MAX; ++rt) acc[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
         auto produit = [&](auto np) {
             constexpr uint32_t NP = decltype(np)::value;
-            if (nrt == 4u)
+            if (nrt == 5u)
+                produit_bf16<NP, 5, PREMIER, PAS>(acc, src, pas_p, wk, B, base + PF_A, a_sa, lr, lg, pre);
+            else if (nrt == 4u)
                 produit_bf16<NP, 4, PREMIER, PAS>(acc, src, pas_p, wk, B, base + PF_A, a_sa, lr, lg, pre);
             else if (nrt == 2u)
                 produit_bf16<NP, 2, PREMIER, PAS>(acc, src, pas_p, wk, B, base + PF_A, a_sa, lr, lg, pre);
@@ -578,21 +581,39 @@ __device__ __forceinline__ void prefill_bande(const ParamsPrefill& pp, const uin
             produit(std::integral_constant<U, 2>{});
         else if (P == 3u)
             produit(std::integral_constant<U, 3>{});
-        // partial sums: [tile g][row tile][wave of the tile][lane], nrt x 16 KiB for either pass shape
+        // partial sums: [tile g][row tile][wave of the tile's first half][lane], nrt x 8 KiB for either
+        // pass shape. The second half of a tile's waves stores its sums, the first half adds them to
+        // its own (wave wk + MI to wave wk) and stores the results, which are added in wave order.
+        constexpr uint32_t MI = VG / 2u;
+        const bool second = wk >= MI;
+        const uint32_t wl = second ? wk - MI : wk;
+        const uint32_t a_moi = a_part + ((g * nrt * MI + wl) * 64u + lane) * 16u;  // row tile rt: + rt MI KiB
+        if (second) {
 #pragma unroll
-        for (uint32_t rt = 0; rt < 4; ++rt)
-            if (rt < nrt) ecrire_lds<f32x4>(a_part + (((g * nrt + rt) * VG + wk) * 64u + lane) * 16u, acc[rt]);
+            for (uint32_t rt = 0; rt < PF_RT_MAX; ++rt)
+                if (rt < nrt) ecrire_lds<f32x4>(a_moi + rt * MI * 1024u, acc[rt]);
+        }
         __syncthreads();
+        if (!second) {
 #pragma unroll
-        for (uint32_t u = 0; u < NT; ++u) {
+            for (uint32_t rt = 0; rt < PF_RT_MAX; ++rt)
+                if (rt < nrt) {
+                    const f32x4 autre = lire_lds<f32x4>(a_moi + rt * MI * 1024u);
+                    ecrire_lds<f32x4>(a_moi + rt * MI * 1024u, acc[rt] + autre);
+                }
+        }
+        __syncthreads();
+        constexpr uint32_t TOURS_SOMME = (NT * PF_RT_MAX * 256u + 1023u) / 1024u;
+#pragma unroll
+        for (uint32_t u = 0; u < TOURS_SOMME; ++u) {
             const uint32_t o = threadIdx.x + 1024u * u;  // output (tile gg, row tile, column, row)
             const uint32_t gg = NT == 2u ? o / (nrt * 256u) : 0u, reste_o = o - gg * (nrt * 256u);
             if (gg < NT && reste_o < nrt * 256u) {
                 const uint32_t rt = reste_o >> 8, reste = reste_o & 255u;
                 const uint32_t ln = reste >> 2, r = reste & 3u;
                 float s = 0.0f;
-                for (uint32_t ww = 0; ww < VG; ++ww)
-                    s += lire_lds<float>(a_part + (((gg * nrt + rt) * VG + ww) * 64u + ln) * 16u + 4u * r);
+                for (uint32_t ww = 0; ww < MI; ++ww)
+                    s += lire_lds<float>(a_part + (((gg * nrt + rt) * MI + ww) * 64u + ln) * 16u + 4u * r);
                 const uint32_t ligne = 16u * rt + 4u * (ln >> 4) + r, jeton = 16u * (tt + gg) + (ln & 15u);
                 if (ligne < nl && jeton < n_e) {
                     const uint32_t cc = paires[debut_e + jeton];
@@ -695,11 +716,12 @@ using trc::usage;
 
 uint64_t al(uint64_t x) { return (x + 255u) & ~uint64_t(255); }
 
-// Rows per band: 64, 32 or 16, the most whose CODES_CTX tiles (N macro-steps of 8 blocks each) fit
-// the 64 tiles a block decodes in two rounds and whose codes, scales and partial sums fit the LDS;
-// 0 if none does.
+// Rows per band: 80, 64, 32 or 16, the most whose CODES_CTX tiles (N macro-steps of 8 blocks each)
+// fit the 64 tiles a block decodes in two rounds and whose codes, scales and partial sums fit the LDS;
+// 0 if none does. The more of the 64 tile slots a band fills, the fewer wavefronts idle in the second
+// round (gpt-oss rows: 80 rows are 56.25 tiles, 64 rows 45).
 uint32_t rb_de(uint32_t B, uint32_t N) {
-    for (uint32_t rb = trc::PF_RB_MAX; rb >= 16; rb /= 2)
+    for (const uint32_t rb : {trc::PF_RB_MAX, 64u, 32u, 16u})
         if ((rb * B - 1u) / (8u * N) + 2u <= 32u * trc::PF_TOURS && trc::pf_lds_tient(rb, B)) return rb;
     return 0;
 }
