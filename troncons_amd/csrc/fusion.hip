@@ -21,6 +21,7 @@
 // deterministic, without floating-point atomics.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstring>
 #include <mutex>
 
@@ -508,12 +509,16 @@ uint32_t grille_tuiles(uint64_t octets, uint32_t N, uint32_t tuiles_par_bloc) {
 
 constexpr uint32_t TUILES_ECHELLES = trc::FILS_ECHELLES_FUSION / 32;
 
-// Grid of a DELTA pass over `blocs` blocks: each half-wavefront takes a run of about 16 macro-steps
-// (whole tiles, at least one), so that a block's prologue (LUT, record, medians, top-k) and a ring's
-// opening serve several tiles.
-uint32_t grille_echelles(uint64_t blocs, uint32_t n_delta) {
+// Grid of a DELTA pass over `travaux` matrices of `blocs` blocks: each half-wavefront takes a run of
+// whole tiles, so that a block's prologue (LUT, record, medians, top-k) and a ring's opening serve
+// several tiles; runs of about 16 macro-steps when the launch has work for more than 8192
+// half-wavefronts (a 1024-thread block per CU) at that length, shorter ones down to a single tile
+// when it has less, so that a small launch (one token's matrices) keeps its parallelism.
+uint32_t grille_echelles(uint64_t blocs, uint32_t n_delta, uint32_t travaux) {
     const uint32_t n = n_delta ? n_delta : 1u;
-    return grille_tuiles(blocs, n * (n < 16u ? 16u / n : 1u), TUILES_ECHELLES);
+    const uint64_t par_demi = ((blocs + 127u) / 128u) * travaux / 8192u;  // macro-steps per half at 8192 halves
+    const uint64_t tuiles = std::min<uint64_t>(std::max<uint64_t>(par_demi / n, 1u), n < 16u ? 16u / n : 1u);
+    return grille_tuiles(blocs, uint32_t(n * tuiles), TUILES_ECHELLES);
 }
 
 // Workspace of one matrix job: block entries (u32 per block + staging margin), then partial sums.
@@ -601,7 +606,7 @@ int lancer_echelles_prefill(const ParamsMoe& pm, uint32_t R, uint32_t C, uint32_
                             uint32_t* ctl, hipStream_t f) {
     const Taches t = par_moe(pm, TACHES_PREFILL_DELTA, 0);
     TRC_LANCER_N("fusion_echelles/prefill", fusion_echelles,
-                 dim3(grille_echelles(uint64_t(R) * (C / 32), n_delta), 3 * pm.E),
+                 dim3(grille_echelles(uint64_t(R) * (C / 32), n_delta, 3 * pm.E), 3 * pm.E),
                  dim3(FILS_ECHELLES_FUSION), f, t, luts, ctl);
     return TRC_OK;
 }
@@ -653,7 +658,7 @@ extern "C" int trc_gemv_fusionnee(trc_vue partie, uint32_t j, trc_vue luts, uint
         return TRC_OK;
     }
     const Taches tv = par_valeur(&t, 1);
-    TRC_LANCER(fusion_echelles, dim3(grille_echelles(uint64_t(lignes) * B, n_delta), 1),
+    TRC_LANCER(fusion_echelles, dim3(grille_echelles(uint64_t(lignes) * B, n_delta, 1), 1),
                dim3(trc::FILS_ECHELLES_FUSION), f, tv, l, ctl);
     TRC_LANCER_GEMV("fusion_gemv", forme_gemv(lignes, colonnes, n_codes, 1), f, tv, l, ctl);
     TRC_LANCER(fusion_finir, dim3((lignes + 255) / 256, 1), dim3(256), f, tv, reinterpret_cast<float*>(y.adresse), 0u);
@@ -726,7 +731,7 @@ extern "C" int trc_expert_fusionne(trc_vue partie, trc_vue luts, const trc_dims_
         return TRC_OK;
     }
     const Taches trois = par_valeur(t, 3), bas = par_valeur(t + 2, 1);
-    TRC_LANCER(fusion_echelles, dim3(grille_echelles(uint64_t(Rm) * (Cm / 32), n_delta), 3),
+    TRC_LANCER(fusion_echelles, dim3(grille_echelles(uint64_t(Rm) * (Cm / 32), n_delta, 3), 3),
                dim3(trc::FILS_ECHELLES_FUSION), f, trois, l, ctl);
     TRC_LANCER_GEMV("fusion_gemv", forme_gemv(R, C, n_codes, 2), f, trois, l, ctl);
     TRC_LANCER(fusion_finir_swiglu, dim3((R + 255) / 256, 1), dim3(256), f, trois, reinterpret_cast<float*>(act), R);
@@ -884,7 +889,7 @@ int couche_moe(trc_vue repertoire, uint32_t experts, trc_vue luts, const trc_dim
         TRC_LANCER(fusion_finir_combiner, dim3((D + 255) / 256), dim3(256), f, t_bas);
         return TRC_OK;
     }
-    TRC_LANCER(fusion_echelles, dim3(grille_echelles(uint64_t(R) * (C / 32), n_delta), 3 * k),
+    TRC_LANCER(fusion_echelles, dim3(grille_echelles(uint64_t(R) * (C / 32), n_delta, 3 * k), 3 * k),
                dim3(trc::FILS_ECHELLES_FUSION), f, t_delta, l, ctl);
     TRC_LANCER_N("fusion_gemv/gate_up", fusion_gemv, forme_gemv(R, C, n_codes, 2 * k).grille,
                  forme_gemv(R, C, n_codes, 2 * k).bloc, f, t_gu, l, ctl);
