@@ -7,6 +7,8 @@
 //                    dequantised and multiplied in registers;
 //   fusion_finir     y[r] = fixed-order sum of the row's tile partials + bias;
 //   fusion_finir_swiglu    the same for gate and up, then the gpt-oss clamped SwiGLU (one expert);
+//   fusion_codes     (N_codes 16, N_delta 1 or 2) the CODES pass decoding each tile's DELTA itself;
+//                    fusion_codes_swiglu, its MoE down form, builds its x (the SwiGLU row) itself;
 //   fusion_finir_combiner  the same for the k down products, then the weighted combine;
 //   fusion_routeur   (MoE layer) router logits; the first pass after it runs the top-k, and every
 //                    later kernel derives its jobs on the device from the chosen indices.
@@ -192,10 +194,11 @@ fusion_gemv(trc::Taches taches, const uint32_t* __restrict__ luts, uint32_t* __r
 // block, by ranks over the logits: the reference's order and tie rule, deterministic, so all blocks
 // agree; block (0, 0) publishes indices and weights), take their expert's matrix from the directory
 // and publish the selected experts' three records (resolus) for the down pass and the combine.
-// Down launches read x from the experts' SwiGLU rows (fusion_finir_swiglu).
+// Down launches read x from the experts' SwiGLU rows (fusion_finir_swiglu) or, with SW
+// (fusion_codes_swiglu), build it themselves in their prologue.
 constexpr uint32_t OPT_TOPK = 2u;
 
-template <uint32_t FILS>
+template <uint32_t FILS, bool SW = false>
 __device__ __forceinline__ void codes_bloc(const trc::Taches& taches, const uint32_t* __restrict__ luts,
                                            uint32_t* __restrict__ controle) {
     using namespace trc;
@@ -226,12 +229,31 @@ __device__ __forceinline__ void codes_bloc(const trc::Taches& taches, const uint
     ChargeLutBloc<FILS> charge_lut;
     charge_lut.demarrer(lut_src);
     const Tache tx = topk ? uniforme(tache_moe_e(pm, blockIdx.y >> 1, j, 0u)) : uniforme(taches[blockIdx.y]);
-    const bool x_lds = tx.colonnes <= X_LDS_MAX && tx.x != 0;
+    const bool x_lds = tx.colonnes <= X_LDS_MAX && (SW || tx.x != 0);
     const uint32_t n16 = x_lds ? tx.colonnes / 4u : 0u;
-    const gptr<u32x4> x_src = glob<u32x4>(x_lds ? reinterpret_cast<const void*>(tx.x) : reinterpret_cast<const void*>(luts));
+    const gptr<u32x4> x_src = glob<u32x4>(x_lds && !SW ? reinterpret_cast<const void*>(tx.x) : reinterpret_cast<const void*>(luts));
     u32x4 xv[4];
+    // SW (MoE down job i): x = swiglu_oai(gate row, up row) of expert i, finished from the gate/up
+    // partial sums as fusion_finir_swiglu does (somme_fin, same order, same bits). Rows r = thread +
+    // q FILS, q < SW_Q: the partial sums (two per row and matrix: a row spans at most two of the
+    // 128-block tiles) are loaded here with the LUTs, the biases once the gate and up records are
+    // read, and the SwiGLU is computed while the first tiles' read-ahead is in flight.
+    constexpr uint32_t SW_Q = (X_LDS_MAX + FILS - 1u) / FILS;
+    const uint32_t i_sw = blockIdx.y;
+    const Tache tg = tache_moe(pm, i_sw, 0u), tu = tache_moe(pm, i_sw, 1u);
+    const uint32_t R_sw = tx.colonnes;  // gate/up rows = down columns
+    u32x2 pg[SW ? SW_Q : 1], pu[SW ? SW_Q : 1];
+    if (SW) {
 #pragma unroll
-    for (uint32_t i = 0; i < 4; ++i) xv[i] = x_src[min(threadIdx.x + i * FILS, n16 > 0u ? n16 - 1u : 0u)];
+        for (uint32_t q = 0; q < SW_Q; ++q) {
+            const uint32_t r = min(threadIdx.x + q * FILS, R_sw - 1u);
+            pg[q] = *glob<u32x2>(reinterpret_cast<const void*>(tg.partiels + 8ull * r));
+            pu[q] = *glob<u32x2>(reinterpret_cast<const void*>(tu.partiels + 8ull * r));
+        }
+    } else {
+#pragma unroll
+        for (uint32_t i = 0; i < 4; ++i) xv[i] = x_src[min(threadIdx.x + i * FILS, n16 > 0u ? n16 - 1u : 0u)];
+    }
     Tache tc;
     if (topk) {
         // the top-k in the entry area (free until the tiles start)
@@ -275,7 +297,7 @@ __device__ __forceinline__ void codes_bloc(const trc::Taches& taches, const uint
         tc = tx;
     }
     const PrepCodes p = preparer_codes(tc, obtenir_matrice_scalaire(tc));
-    const bool bon = p.bon && x_lds;  // uniform over the block
+    const bool bon = p.bon && x_lds && (!SW || tg.kmax == 2u);  // uniform over the block
     if (!bon) {
         if (threadIdx.x == 0 && blockIdx.x == 0) atomicAdd(&controle[CTL_FORMAT], 1u);
         return;
@@ -283,15 +305,57 @@ __device__ __forceinline__ void codes_bloc(const trc::Taches& taches, const uint
     // the first tile pair's streams (one branch-free batch of loads, left in flight), then x and
     // the decode LUTs into LDS: their loads were issued before, so no wait here drains the
     // read-ahead
+    // SW: the gate and up records (scalar loads from the resolved records), then their biases,
+    // issued before the read-ahead so that waiting for them does not wait for it
+    float bg[SW ? SW_Q : 1], bu[SW ? SW_Q : 1];
+    bool sw_bon = false;
+    uint32_t sw_bpt = 128u;
+    if (SW) {
+        const MatricePartie mg = lire_matrice_constante(tg.matrice), mu = lire_matrice_constante(tu.matrice);
+        const uint32_t Bg = tg.colonnes / 32u;
+        sw_bon = mg.bon != 0 && mu.bon != 0 && mg.cN == 16u && mu.cN == 16u && Bg >= 8u &&
+                 (Bg - 1u) / 128u + 2u <= tg.kmax && tg.lignes >= R_sw && tu.lignes >= R_sw;
+        sw_bpt = 8u * mg.cN;
+        const gptr<float> big = glob<float>(sw_bon ? reinterpret_cast<const void*>(mg.biais.p) : reinterpret_cast<const void*>(luts));
+        const gptr<float> biu = glob<float>(sw_bon ? reinterpret_cast<const void*>(mu.biais.p) : reinterpret_cast<const void*>(luts));
+#pragma unroll
+        for (uint32_t q = 0; q < SW_Q; ++q) {
+            const uint32_t r = sw_bon ? min(threadIdx.x + q * FILS, R_sw - 1u) : 0u;
+            bg[q] = big[r];
+            bu[q] = biu[r];
+        }
+    }
     const Avance avance0 = premiere_avance<true>(p, tc.lignes, g);
     // issued here, ahead of the LDS staging below (which waits on the earlier loads only)
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
     asm volatile("" ::"v"(rep_chaud));  // complete before the decode LUTs, issued after it
+    if (SW) {
+        const uint32_t Bg = tg.colonnes / 32u;
 #pragma unroll
-    for (uint32_t i = 0; i < 4; ++i) {
-        const uint32_t k = threadIdx.x + i * FILS;
-        if (k < n16) *reinterpret_cast<u32x4*>(lds + LDS_X + 16u * k) = xv[i];
+        for (uint32_t q = 0; q < SW_Q; ++q) {
+            const uint32_t r = threadIdx.x + q * FILS;
+            if (r < R_sw) {
+                float v = 0.0f;
+                if (sw_bon) {
+                    // somme_fin: p[0], + p[1] when the row reaches a second tile, then + bias
+                    const bool deux = (r * Bg + Bg - 1u) / sw_bpt != (r * Bg) / sw_bpt;
+                    float sg = __uint_as_float(pg[q].x), su = __uint_as_float(pu[q].x);
+                    if (deux) {
+                        sg += __uint_as_float(pg[q].y);
+                        su += __uint_as_float(pu[q].y);
+                    }
+                    v = swiglu_oai_f(sg + bg[q], su + bu[q]);
+                }
+                *reinterpret_cast<float*>(lds + LDS_X + 4u * r) = v;
+            }
+        }
+    } else {
+#pragma unroll
+        for (uint32_t i = 0; i < 4; ++i) {
+            const uint32_t k = threadIdx.x + i * FILS;
+            if (k < n16) *reinterpret_cast<u32x4*>(lds + LDS_X + 16u * k) = xv[i];
+        }
     }
     if (threadIdx.x < 8u)
         *reinterpret_cast<u32x4*>(lds + LDS_X + COLONNE_NULLE * 128u + 16u * threadIdx.x) = u32x4{0u, 0u, 0u, 0u};
@@ -317,6 +381,11 @@ fusion_codes_512(trc::Taches taches, const uint32_t* __restrict__ luts, uint32_t
 extern "C" __global__ void __launch_bounds__(256)
 fusion_codes_256(trc::Taches taches, const uint32_t* __restrict__ luts, uint32_t* __restrict__ controle) {
     codes_bloc<256>(taches, luts, controle);
+}
+// MoE down pass that builds its x (the SwiGLU of expert blockIdx.y's gate and up rows) itself.
+extern "C" __global__ void __launch_bounds__(1024)
+fusion_codes_swiglu(trc::Taches taches, const uint32_t* __restrict__ luts, uint32_t* __restrict__ controle) {
+    codes_bloc<1024, true>(taches, luts, controle);
 }
 
 // The CODES kernel compiled for the launch's block size (1024, 512 or 256 threads).
@@ -877,15 +946,18 @@ int couche_moe(trc_vue repertoire, uint32_t experts, trc_vue luts, const trc_dim
                    reinterpret_cast<const uint16_t*>(routeur.adresse), reinterpret_cast<const float*>(x.adresse),
                    reinterpret_cast<const float*>(routeur_biais.adresse), reinterpret_cast<float*>(logits), experts, C);
     }
-    // The k SwiGLU rows are finished once per expert (fusion_finir_swiglu) between gate/up and down:
-    // measured against every down block building them, that launch saves more than it costs.
     if (interne) {
-        // five launches: router, gate/up (top-k, DELTA and CODES), the k SwiGLU rows, down (DELTA and
-        // CODES), combine
+        // four launches: router, gate/up (top-k, DELTA and CODES), down (the SwiGLU rows of its
+        // expert, DELTA and CODES), combine; with blocks under 1024 threads the k SwiGLU rows are
+        // finished once per expert by their own launch between gate/up and down
         const FormeGemv fgu = forme_gemv(R, C, n_codes, 2 * k), fb = forme_gemv(D, R, n_codes, k);
         TRC_LANCER_CODES("fusion_codes/gate_up", fgu, f, t_gu_topk, l, ctl);
-        TRC_LANCER(fusion_finir_swiglu, dim3((R + 255) / 256, k), dim3(256), f, t_gu, reinterpret_cast<float*>(act), R);
-        TRC_LANCER_CODES("fusion_codes/down", fb, f, t_bas, l, ctl);
+        if (fb.bloc.x == 1024) {
+            TRC_LANCER_N("fusion_codes/down", fusion_codes_swiglu, fb.grille, fb.bloc, f, t_bas, l, ctl);
+        } else {
+            TRC_LANCER(fusion_finir_swiglu, dim3((R + 255) / 256, k), dim3(256), f, t_gu, reinterpret_cast<float*>(act), R);
+            TRC_LANCER_CODES("fusion_codes/down", fb, f, t_bas, l, ctl);
+        }
         TRC_LANCER(fusion_finir_combiner, dim3((D + 255) / 256), dim3(256), f, t_bas);
         return TRC_OK;
     }
