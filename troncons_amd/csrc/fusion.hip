@@ -197,6 +197,10 @@ fusion_gemv(trc::Taches taches, const uint32_t* __restrict__ luts, uint32_t* __r
 // Down launches read x from the experts' SwiGLU rows (fusion_finir_swiglu) or, with SW
 // (fusion_codes_swiglu), build it themselves in their prologue.
 constexpr uint32_t OPT_TOPK = 2u;
+// MoE launches: each CODES block copies its share of its matrix's bias to ParamsMoe::biais (rows
+// blockIdx.x * n .. of n = ceil(R / gridDim.x)), the down pass's SwiGLU prologue reads the gate and
+// up copies and the combine the down ones: their loads then need no record first.
+constexpr uint32_t OPT_BIAIS = 4u;
 
 template <uint32_t FILS, bool SW = false>
 __device__ __forceinline__ void codes_bloc(const trc::Taches& taches, const uint32_t* __restrict__ luts,
@@ -243,12 +247,23 @@ __device__ __forceinline__ void codes_bloc(const trc::Taches& taches, const uint
     const Tache tg = tache_moe(pm, i_sw, 0u), tu = tache_moe(pm, i_sw, 1u);
     const uint32_t R_sw = tx.colonnes;  // gate/up rows = down columns
     u32x2 pg[SW ? SW_Q : 1], pu[SW ? SW_Q : 1];
+    float bg[SW ? SW_Q : 1], bu[SW ? SW_Q : 1];
+    const bool copies = (taches.options & OPT_BIAIS) != 0u;
+    const uint32_t Rm_moe = max(pm.lignes[0], pm.lignes[2]);
     if (SW) {
+        // with OPT_BIAIS the biases come from the gate/up pass's copies, loaded here with the partial
+        // sums; else from the records, below
+        const gptr<float> cg = glob<float>(copies ? reinterpret_cast<const void*>(pm.biais + 4ull * (i_sw * 3u) * Rm_moe)
+                                                  : reinterpret_cast<const void*>(luts));
+        const gptr<float> cu = glob<float>(copies ? reinterpret_cast<const void*>(pm.biais + 4ull * (i_sw * 3u + 1u) * Rm_moe)
+                                                  : reinterpret_cast<const void*>(luts));
 #pragma unroll
         for (uint32_t q = 0; q < SW_Q; ++q) {
             const uint32_t r = min(threadIdx.x + q * FILS, R_sw - 1u);
             pg[q] = *glob<u32x2>(reinterpret_cast<const void*>(tg.partiels + 8ull * r));
             pu[q] = *glob<u32x2>(reinterpret_cast<const void*>(tu.partiels + 8ull * r));
+            bg[q] = cg[copies ? r : 0u];
+            bu[q] = cu[copies ? r : 0u];
         }
     } else {
 #pragma unroll
@@ -296,7 +311,8 @@ __device__ __forceinline__ void codes_bloc(const trc::Taches& taches, const uint
     } else {
         tc = tx;
     }
-    const PrepCodes p = preparer_codes(tc, obtenir_matrice_scalaire(tc));
+    const MatricePartie mrec = obtenir_matrice_scalaire(tc);
+    const PrepCodes p = preparer_codes(tc, mrec);
     const bool bon = p.bon && x_lds && (!SW || tg.kmax == 2u);  // uniform over the block
     if (!bon) {
         if (threadIdx.x == 0 && blockIdx.x == 0) atomicAdd(&controle[CTL_FORMAT], 1u);
@@ -305,9 +321,13 @@ __device__ __forceinline__ void codes_bloc(const trc::Taches& taches, const uint
     // the first tile pair's streams (one branch-free batch of loads, left in flight), then x and
     // the decode LUTs into LDS: their loads were issued before, so no wait here drains the
     // read-ahead
-    // SW: the gate and up records (scalar loads from the resolved records), then their biases,
-    // issued before the read-ahead so that waiting for them does not wait for it
-    float bg[SW ? SW_Q : 1], bu[SW ? SW_Q : 1];
+    // OPT_BIAIS: this block's share of its matrix's bias, copied after its tiles
+    const uint32_t i_moe = topk ? (blockIdx.y >> 1) : blockIdx.y, j_moe = topk ? j : 2u;
+    const uint32_t n_copie = (tc.lignes + g.blocs_x - 1u) / g.blocs_x, r_copie = blockIdx.x * n_copie + threadIdx.x;
+    const float b_copie = glob<float>(copies ? reinterpret_cast<const void*>(mrec.biais.p) : reinterpret_cast<const void*>(luts))
+        [copies ? min(r_copie, tc.lignes - 1u) : 0u];
+    // SW: the gate and up records (scalar loads from the resolved records) and, without OPT_BIAIS,
+    // their biases, issued before the read-ahead so that waiting for them does not wait for it
     bool sw_bon = false;
     uint32_t sw_bpt = 128u;
     if (SW) {
@@ -316,13 +336,15 @@ __device__ __forceinline__ void codes_bloc(const trc::Taches& taches, const uint
         sw_bon = mg.bon != 0 && mu.bon != 0 && mg.cN == 16u && mu.cN == 16u && Bg >= 8u &&
                  (Bg - 1u) / 128u + 2u <= tg.kmax && tg.lignes >= R_sw && tu.lignes >= R_sw;
         sw_bpt = 8u * mg.cN;
-        const gptr<float> big = glob<float>(sw_bon ? reinterpret_cast<const void*>(mg.biais.p) : reinterpret_cast<const void*>(luts));
-        const gptr<float> biu = glob<float>(sw_bon ? reinterpret_cast<const void*>(mu.biais.p) : reinterpret_cast<const void*>(luts));
+        if (!copies) {
+            const gptr<float> big = glob<float>(sw_bon ? reinterpret_cast<const void*>(mg.biais.p) : reinterpret_cast<const void*>(luts));
+            const gptr<float> biu = glob<float>(sw_bon ? reinterpret_cast<const void*>(mu.biais.p) : reinterpret_cast<const void*>(luts));
 #pragma unroll
-        for (uint32_t q = 0; q < SW_Q; ++q) {
-            const uint32_t r = sw_bon ? min(threadIdx.x + q * FILS, R_sw - 1u) : 0u;
-            bg[q] = big[r];
-            bu[q] = biu[r];
+            for (uint32_t q = 0; q < SW_Q; ++q) {
+                const uint32_t r = sw_bon ? min(threadIdx.x + q * FILS, R_sw - 1u) : 0u;
+                bg[q] = big[r];
+                bu[q] = biu[r];
+            }
         }
     }
     const Avance avance0 = premiere_avance<true>(p, tc.lignes, g);
@@ -368,6 +390,8 @@ __device__ __forceinline__ void codes_bloc(const trc::Taches& taches, const uint
     // the block's barriers (LDS only: the read-ahead stays in flight) are passed in corps_codes,
     // around each wavefront's first DELTA decode
     corps_codes(tc, p, lds, luts + uint64_t(j) * 4u * M, controle, avance0, g);
+    if (copies && threadIdx.x < n_copie && r_copie < tc.lignes)
+        reinterpret_cast<float*>(pm.biais)[uint64_t(i_moe * 3u + j_moe) * Rm_moe + r_copie] = b_copie;
 }
 
 extern "C" __global__ void __launch_bounds__(1024)
@@ -445,11 +469,45 @@ fusion_finir_swiglu(trc::Taches taches, float* __restrict__ act, uint32_t R) {
 }
 
 // residu[r] += ((w0 s0[r] + w1 s1[r]) + w2 s2[r]) + ... over the k down jobs (MoE layer).
+// OPT_BIAIS (one row per thread, 2 partial-sum slots per row): the row's residual, partial sums and
+// bias copies are loaded before the records are read, so that both take one round trip.
 extern "C" __global__ void __launch_bounds__(256)
 fusion_finir_combiner(trc::Taches taches) {
     using namespace trc;
     __shared__ Fin fins[TOPK_MAX];
     const ParamsMoe& moe = taches.moe;
+    if ((taches.options & OPT_BIAIS) != 0u) {
+#pragma clang fp contract(off)
+        const uint32_t D = moe.lignes[2], Rm = max(moe.lignes[0], moe.lignes[2]);
+        const uint32_t r = blockIdx.x * 256u + threadIdx.x, rr = min(r, D - 1u);
+        const float res = reinterpret_cast<const float*>(moe.residu)[rr];
+        u32x2 p[TOPK_MAX];
+        float bi[TOPK_MAX], w[TOPK_MAX];
+#pragma unroll
+        for (uint32_t i = 0; i < TOPK_MAX; ++i) {
+            const uint32_t ii = min(i, moe.k - 1u);
+            p[i] = *glob<u32x2>(reinterpret_cast<const void*>(tache_moe(moe, ii, 2u).partiels + 8ull * rr));
+            bi[i] = glob<float>(reinterpret_cast<const void*>(moe.biais))[uint64_t(ii * 3u + 2u) * Rm + rr];
+            w[i] = glob<float>(reinterpret_cast<const void*>(moe.poids))[ii];
+        }
+        preparer_fins(taches, 0, moe.k, fins);
+        if (r >= D) return;
+        for (uint32_t i = 0; i < moe.k; ++i)
+            if (!fins[i].bon || r >= fins[i].lignes || fins[i].kmax != 2u) return;
+        float s = 0.0f;
+#pragma unroll
+        for (uint32_t i = 0; i < TOPK_MAX; ++i) {
+            if (i < moe.k) {
+                float si = __uint_as_float(p[i].x);
+                if (partiels_en_plus(fins[i], r) >= 1u) si += __uint_as_float(p[i].y);
+                si = si + bi[i];
+                const float pr = w[i] * si;
+                s = i == 0 ? pr : s + pr;
+            }
+        }
+        reinterpret_cast<float*>(moe.residu)[r] = res + s;
+        return;
+    }
     preparer_fins(taches, 0, moe.k, fins);
     combiner_lignes(fins, moe.k, reinterpret_cast<const float*>(moe.poids), reinterpret_cast<float*>(moe.residu),
                     moe.lignes[2], blockIdx.x * 256u + threadIdx.x, gridDim.x * 256u);
@@ -841,7 +899,7 @@ extern "C" uint64_t trc_taille_travail_couche_moe(const trc_dims_expert* dims, u
     const uint32_t R = dims->lignes[0], C = dims->colonnes[0];
     const uint32_t Rm = dims->lignes[2] > R ? dims->lignes[2] : R;
     const uint32_t Cm = dims->colonnes[2] > C ? dims->colonnes[2] : C;
-    return al(4ull * experts) + al(3ull * k * sizeof(trc::MatricePartie)) + al(4ull * k * R) +
+    return al(4ull * experts) + al(3ull * k * sizeof(trc::MatricePartie)) + al(4ull * k * R) + al(12ull * k * Rm) +
            3ull * k * pas_tache(Rm, Cm, n_codes);
 }
 
@@ -901,6 +959,8 @@ int couche_moe(trc_vue repertoire, uint32_t experts, trc_vue luts, const trc_dim
     p += al(3ull * k * sizeof(trc::MatricePartie));
     const uint64_t act = p;
     p += al(4ull * k * R);
+    const uint64_t biais = p;
+    p += al(12ull * k * Rm);
     const uint64_t morceaux = p;
 
     trc::ParamsMoe pm;
@@ -929,6 +989,7 @@ int couche_moe(trc_vue repertoire, uint32_t experts, trc_vue luts, const trc_dim
         pm.pas = pas_tache_interne(Rm, Cm);
     }
     pm.act = act;  // the down jobs' x: the experts' SwiGLU rows
+    pm.biais = biais;
     const Taches t_delta = par_moe(pm, trc::TACHES_MOE_DELTA, 0), t_gu = par_moe(pm, trc::TACHES_MOE_GU, 0),
                  t_bas = par_moe(pm, trc::TACHES_MOE_BAS, 0), t_gu_topk = par_moe(pm, trc::TACHES_MOE_GU, OPT_TOPK);
     const hipStream_t f = flux_de(flux);
@@ -951,6 +1012,17 @@ int couche_moe(trc_vue repertoire, uint32_t experts, trc_vue luts, const trc_dim
         // expert, DELTA and CODES), combine; with blocks under 1024 threads the k SwiGLU rows are
         // finished once per expert by their own launch between gate/up and down
         const FormeGemv fgu = forme_gemv(R, C, n_codes, 2 * k), fb = forme_gemv(D, R, n_codes, k);
+        // bias copies when every block's share of rows fits its threads
+        const bool copies = fb.bloc.x == 1024 && (R + fgu.grille.x - 1) / fgu.grille.x <= fgu.bloc.x &&
+                            (D + fb.grille.x - 1) / fb.grille.x <= fb.bloc.x && pm.kmax[2] == 2u;
+        if (copies) {
+            const Taches gu_c = par_moe(pm, trc::TACHES_MOE_GU, OPT_TOPK | OPT_BIAIS),
+                         bas_c = par_moe(pm, trc::TACHES_MOE_BAS, OPT_BIAIS);
+            TRC_LANCER_CODES("fusion_codes/gate_up", fgu, f, gu_c, l, ctl);
+            TRC_LANCER_N("fusion_codes/down", fusion_codes_swiglu, fb.grille, fb.bloc, f, bas_c, l, ctl);
+            TRC_LANCER(fusion_finir_combiner, dim3((D + 255) / 256), dim3(256), f, bas_c);
+            return TRC_OK;
+        }
         TRC_LANCER_CODES("fusion_codes/gate_up", fgu, f, t_gu_topk, l, ctl);
         if (fb.bloc.x == 1024) {
             TRC_LANCER_N("fusion_codes/down", fusion_codes_swiglu, fb.grille, fb.bloc, f, t_bas, l, ctl);

@@ -158,6 +158,8 @@ struct ParamsMoe {
     uint64_t pas;         // workspace bytes per piece
     uint64_t compte;      // (prefill) u32[E] positions that chose expert e; experts with 0 are skipped
     uint64_t act;         // f32[k][colonnes[2]] the experts' SwiGLU rows, the down jobs' x (0: built by the down pass)
+    uint64_t biais;       // f32[k][3][max(lignes)] the selected matrices' biases, copied by their CODES passes
+                          // (OPT_BIAIS), so that later launches read them without the records
     uint32_t lignes[3], colonnes[3], kmax[3];
     uint32_t k, E;
 };
