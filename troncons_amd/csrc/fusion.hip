@@ -910,11 +910,12 @@ extern "C" uint64_t trc_taille_travail_couche_moe(const trc_dims_expert* dims, u
 // u32[3][4][4096]. No host sync: the selection flows from the router to the expert kernels through
 // device memory, and every kernel derives its jobs from the top-k indices (checked against
 // `experts` before the directory is read). Streams of 16 macro-steps per CODES tile and 1 or 2 per
-// DELTA tile take five launches: router logits; gate/up CODES pass (2k jobs, each block running the
-// top-k first, each tile's DELTA decoded in the kernel); the k SwiGLU rows; down CODES pass (k, x
-// = the expert's SwiGLU row); finish + combine. Other tile lengths add a DELTA pass (3k matrices,
-// with the top-k) before the gate/up pass. No cross-block synchronisation inside a launch. Rows are
-// limited to X_LDS_MAX columns (x in LDS).
+// DELTA tile take four launches: router logits; gate/up CODES pass (2k jobs, each block running the
+// top-k first, each tile's DELTA decoded in the kernel); down CODES pass (k, each block building its
+// x, the expert's SwiGLU row, from the gate/up partial sums in its prologue); finish + combine.
+// With down blocks under 1024 threads the k SwiGLU rows take a launch of their own before down.
+// Other tile lengths add a DELTA pass (3k matrices, with the top-k) before the gate/up pass. No
+// cross-block synchronisation inside a launch. Rows are limited to X_LDS_MAX columns (x in LDS).
 namespace {
 // The fused MoE layer; with `norme`, the router takes RMSNorm(residu) with `norme` into x first
 // (x is then written, not read, by the router).
