@@ -961,7 +961,9 @@ def main():
     atteint = (octets_gu + octets_bas) / (duree_us * 1e-6) / 1e9
     trafic = trafic_mesure() if n_couches == 1 else None
     roofline = {
-        "bound": "hbm", "kernel": f"{nom_codes} (gate/up launch + down launch)",
+        "bound": "hbm",
+        "kernel": ("fusion_codes (gate/up launch) + fusion_codes_swiglu (down launch)" if nom_codes == "fusion_codes"
+                   else "fusion_gemv (gate/up launch + down launch)"),
         "achieved": round(float(atteint), 1), "peak": PIC_HBM, "unit": "GB/s",
         "frac": round(float(atteint / PIC_HBM), 4), "traffic": trafic,
         "traffic_source": (f"{FICHIER_PMC.relative_to(RACINE)}: rocprofv3 --pmc FETCH_SIZE then WRITE_SIZE per "
