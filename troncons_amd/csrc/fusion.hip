@@ -251,8 +251,8 @@ __device__ __forceinline__ void codes_bloc(const trc::Taches& taches, const uint
     const bool copies = (taches.options & OPT_BIAIS) != 0u;
     const uint32_t Rm_moe = max(pm.lignes[0], pm.lignes[2]);
     if (SW) {
-        // with OPT_BIAIS the biases come from the gate/up pass's copies, loaded here with the partial
-        // sums; else from the records, below
+        // the biases come from the gate/up pass's copies (SW launches carry OPT_BIAIS), loaded here
+        // with the partial sums
         const gptr<float> cg = glob<float>(copies ? reinterpret_cast<const void*>(pm.biais + 4ull * (i_sw * 3u) * Rm_moe)
                                                   : reinterpret_cast<const void*>(luts));
         const gptr<float> cu = glob<float>(copies ? reinterpret_cast<const void*>(pm.biais + 4ull * (i_sw * 3u + 1u) * Rm_moe)
@@ -313,7 +313,7 @@ __device__ __forceinline__ void codes_bloc(const trc::Taches& taches, const uint
     }
     const MatricePartie mrec = obtenir_matrice_scalaire(tc);
     const PrepCodes p = preparer_codes(tc, mrec);
-    const bool bon = p.bon && x_lds && (!SW || tg.kmax == 2u);  // uniform over the block
+    const bool bon = p.bon && x_lds && (!SW || (tg.kmax == 2u && copies));  // uniform over the block
     if (!bon) {
         if (threadIdx.x == 0 && blockIdx.x == 0) atomicAdd(&controle[CTL_FORMAT], 1u);
         return;
@@ -326,8 +326,7 @@ __device__ __forceinline__ void codes_bloc(const trc::Taches& taches, const uint
     const uint32_t n_copie = (tc.lignes + g.blocs_x - 1u) / g.blocs_x, r_copie = blockIdx.x * n_copie + threadIdx.x;
     const float b_copie = glob<float>(copies ? reinterpret_cast<const void*>(mrec.biais.p) : reinterpret_cast<const void*>(luts))
         [copies ? min(r_copie, tc.lignes - 1u) : 0u];
-    // SW: the gate and up records (scalar loads from the resolved records) and, without OPT_BIAIS,
-    // their biases, issued before the read-ahead so that waiting for them does not wait for it
+    // SW: the gate and up records (scalar loads from the resolved records), for their checks
     bool sw_bon = false;
     uint32_t sw_bpt = 128u;
     if (SW) {
@@ -336,16 +335,6 @@ __device__ __forceinline__ void codes_bloc(const trc::Taches& taches, const uint
         sw_bon = mg.bon != 0 && mu.bon != 0 && mg.cN == 16u && mu.cN == 16u && Bg >= 8u &&
                  (Bg - 1u) / 128u + 2u <= tg.kmax && tg.lignes >= R_sw && tu.lignes >= R_sw;
         sw_bpt = 8u * mg.cN;
-        if (!copies) {
-            const gptr<float> big = glob<float>(sw_bon ? reinterpret_cast<const void*>(mg.biais.p) : reinterpret_cast<const void*>(luts));
-            const gptr<float> biu = glob<float>(sw_bon ? reinterpret_cast<const void*>(mu.biais.p) : reinterpret_cast<const void*>(luts));
-#pragma unroll
-            for (uint32_t q = 0; q < SW_Q; ++q) {
-                const uint32_t r = sw_bon ? min(threadIdx.x + q * FILS, R_sw - 1u) : 0u;
-                bg[q] = big[r];
-                bu[q] = biu[r];
-            }
-        }
     }
     const Avance avance0 = premiere_avance<true>(p, tc.lignes, g);
     // issued here, ahead of the LDS staging below (which waits on the earlier loads only)
@@ -913,7 +902,8 @@ extern "C" uint64_t trc_taille_travail_couche_moe(const trc_dims_expert* dims, u
 // DELTA tile take four launches: router logits; gate/up CODES pass (2k jobs, each block running the
 // top-k first, each tile's DELTA decoded in the kernel); down CODES pass (k, each block building its
 // x, the expert's SwiGLU row, from the gate/up partial sums in its prologue); finish + combine.
-// With down blocks under 1024 threads the k SwiGLU rows take a launch of their own before down.
+// With down blocks under 1024 threads (or a block's share of bias rows past its threads) the k SwiGLU
+// rows take a launch of their own before down.
 // Other tile lengths add a DELTA pass (3k matrices, with the top-k) before the gate/up pass. No
 // cross-block synchronisation inside a launch. Rows are limited to X_LDS_MAX columns (x in LDS).
 namespace {
@@ -1010,8 +1000,9 @@ int couche_moe(trc_vue repertoire, uint32_t experts, trc_vue luts, const trc_dim
     }
     if (interne) {
         // four launches: router, gate/up (top-k, DELTA and CODES), down (the SwiGLU rows of its
-        // expert, DELTA and CODES), combine; with blocks under 1024 threads the k SwiGLU rows are
-        // finished once per expert by their own launch between gate/up and down
+        // expert, DELTA and CODES), combine; with down blocks under 1024 threads, or a block's share
+        // of bias rows past its threads, the k SwiGLU rows are finished once per expert by their own
+        // launch between gate/up and down
         const FormeGemv fgu = forme_gemv(R, C, n_codes, 2 * k), fb = forme_gemv(D, R, n_codes, k);
         // bias copies when every block's share of rows fits its threads
         const bool copies = fb.bloc.x == 1024 && (R + fgu.grille.x - 1) / fgu.grille.x <= fgu.bloc.x &&
@@ -1025,12 +1016,8 @@ int couche_moe(trc_vue repertoire, uint32_t experts, trc_vue luts, const trc_dim
             return TRC_OK;
         }
         TRC_LANCER_CODES("fusion_codes/gate_up", fgu, f, t_gu_topk, l, ctl);
-        if (fb.bloc.x == 1024) {
-            TRC_LANCER_N("fusion_codes/down", fusion_codes_swiglu, fb.grille, fb.bloc, f, t_bas, l, ctl);
-        } else {
-            TRC_LANCER(fusion_finir_swiglu, dim3((R + 255) / 256, k), dim3(256), f, t_gu, reinterpret_cast<float*>(act), R);
-            TRC_LANCER_CODES("fusion_codes/down", fb, f, t_bas, l, ctl);
-        }
+        TRC_LANCER(fusion_finir_swiglu, dim3((R + 255) / 256, k), dim3(256), f, t_gu, reinterpret_cast<float*>(act), R);
+        TRC_LANCER_CODES("fusion_codes/down", fb, f, t_bas, l, ctl);
         TRC_LANCER(fusion_finir_combiner, dim3((D + 255) / 256), dim3(256), f, t_bas);
         return TRC_OK;
     }
