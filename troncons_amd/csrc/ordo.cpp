@@ -409,11 +409,23 @@ struct trc_ordo {
             lecteurs->soumettre({uint16_t(l), experts[i], dst, lg_max, cfg.verifier, i});
             ++en_vol;
         }
-        for (uint32_t i = 0; i < k; ++i) {
+        // From here on an error is kept in `echec` (the first one wins) and returned only once every
+        // read this layer submitted or took over has landed, so that no completion is left for a later
+        // token to pick up with this layer's indices.
+        int echec = TRC_OK;
+        std::string message;
+        auto noter_echec = [&](int r, const std::string& m) {
+            if (r != TRC_OK && echec == TRC_OK) {
+                echec = r;
+                message = m;
+            }
+        };
+        for (uint32_t i = 0; i < k && echec == TRC_OK; ++i) {
             if (d[i].sorte != TRC_DECISION_DEFAUT_RAM) continue;
             const trc_entree_repertoire* en = trc_fichier_entree(f, uint16_t(l), experts[i]);
-            TRC_OK_OU_RENDRE(envoyer_et_decoder(l, i, tiedes + uint64_t(d[i].tiede) * lg_max, en->longueur[0],
-                                                d[i].emplacement, flux));
+            const int r = envoyer_et_decoder(l, i, tiedes + uint64_t(d[i].tiede) * lg_max, en->longueur[0],
+                                             d[i].emplacement, flux);
+            if (r != TRC_OK) noter_echec(r, trc_derniere_erreur());
         }
         for (uint32_t i = 0; i < k; ++i) {
             if (pf_de[i] < 0) continue;
@@ -423,15 +435,15 @@ struct trc_ordo {
                 ++en_vol;
                 continue;
             }
+            if (echec != TRC_OK) continue;
             if (p.statut != TRC_OK) {
-                trc::derniere_erreur() = p.message;
-                return p.statut;
+                noter_echec(p.statut, p.message);
+                continue;
             }
-            TRC_OK_OU_RENDRE(envoyer_et_decoder(l, i, pf_hote + uint64_t(pf_de[i]) * lg_max, p.octets,
-                                                d[i].emplacement, flux));
+            const int r = envoyer_et_decoder(l, i, pf_hote + uint64_t(pf_de[i]) * lg_max, p.octets,
+                                             d[i].emplacement, flux);
+            if (r != TRC_OK) noter_echec(r, trc_derniere_erreur());
         }
-        int echec = TRC_OK;
-        std::string message;
         auto traiter = [&](Lecteurs::Fin x) {
             const uint8_t* src;
             uint32_t i;
@@ -455,16 +467,12 @@ struct trc_ordo {
             }
             --en_vol;
             if (x.statut != TRC_OK) {
-                echec = x.statut;
-                message = x.message;
+                noter_echec(x.statut, x.message);
                 return;
             }
             if (echec != TRC_OK) return;
             const int r = envoyer_et_decoder(l, i, src, x.octets, d[i].emplacement, flux);
-            if (r != TRC_OK) {
-                echec = r;
-                message = trc_derniere_erreur();
-            }
+            if (r != TRC_OK) noter_echec(r, trc_derniere_erreur());
         };
         // the reads ahead for layer l+1, queued behind layer l's own (Moteur::pas, lib.rs:1194-1215):
         // set (l+1) % 2 is reused once the reads still landing in it have landed; its copies to the
