@@ -274,10 +274,11 @@ namespace trc {
 // bq[q * NP + p] is piece p of k-step ks0 + 16 q.
 constexpr uint32_t PF_LOT = 6;
 
-template <uint32_t NP, uint32_t PAS>
+// LOT <= PF_LOT: the loads of a batch actually used (KB = LOT / NP k-steps, at least one).
+template <uint32_t NP, uint32_t PAS, uint32_t LOT>
 __device__ __forceinline__ void charger_b(u32x4 (&bq)[PF_LOT], const uint8_t* xsrc, uint64_t pas_p, uint32_t ks0,
                                           uint32_t B) {
-    constexpr uint32_t KB = PF_LOT / NP;
+    constexpr uint32_t KB = LOT / NP > 0u ? LOT / NP : 1u;
 #pragma unroll
     for (uint32_t q = 0; q < KB; ++q) {
         const uint32_t ks = min(ks0 + PAS * q, B);  // block B of an activation row is zero
@@ -286,10 +287,10 @@ __device__ __forceinline__ void charger_b(u32x4 (&bq)[PF_LOT], const uint8_t* xs
     }
 }
 
-template <uint32_t NP, uint32_t NRT, uint32_t PAS>
+template <uint32_t NP, uint32_t NRT, uint32_t PAS, uint32_t LOT>
 __device__ __forceinline__ void calculer_b(f32x4 (&acc)[PF_RT_MAX], const u32x4 (&bq)[PF_LOT], uint32_t ks0, uint32_t B,
                                            uint32_t a_codes, uint32_t a_sa, uint32_t lr, uint32_t lg) {
-    constexpr uint32_t KB = PF_LOT / NP;
+    constexpr uint32_t KB = LOT / NP > 0u ? LOT / NP : 1u;
 #pragma unroll
     for (uint32_t q = 0; q < KB; ++q) {
         // straight-line code, so that the B loads stay ahead of every MFMA: a k-step past B
@@ -319,23 +320,23 @@ __device__ __forceinline__ void calculer_b(f32x4 (&acc)[PF_RT_MAX], const u32x4 
 
 // The whole product of a column tile over the k-steps w, w + PAS, ...; PRE: the first batch of B is
 // already in `pre` (loaded before the band's store, so that its latency hides behind it).
-template <uint32_t NP, uint32_t NRT, bool PRE, uint32_t PAS>
+template <uint32_t NP, uint32_t NRT, bool PRE, uint32_t PAS, uint32_t LOT>
 __device__ __forceinline__ void produit_bf16(f32x4 (&acc)[PF_RT_MAX], const uint8_t* xsrc, uint64_t pas_p, uint32_t w,
                                              uint32_t B, uint32_t a_codes, uint32_t a_sa, uint32_t lr, uint32_t lg,
                                              const u32x4 (&pre)[PF_LOT]) {
-    constexpr uint32_t KB = PF_LOT / NP;
+    constexpr uint32_t KB = LOT / NP > 0u ? LOT / NP : 1u;
     uint32_t ks0 = w;
     if constexpr (PRE) {
         if (ks0 < B) {  // wave-uniform
-            calculer_b<NP, NRT, PAS>(acc, pre, ks0, B, a_codes, a_sa, lr, lg);
+            calculer_b<NP, NRT, PAS, LOT>(acc, pre, ks0, B, a_codes, a_sa, lr, lg);
             ks0 += PAS * KB;
         }
     }
     for (; ks0 < B; ks0 += PAS * KB) {  // wave-uniform
         u32x4 bq[PF_LOT];
-        charger_b<NP, PAS>(bq, xsrc, pas_p, ks0, B);
+        charger_b<NP, PAS, LOT>(bq, xsrc, pas_p, ks0, B);
         __builtin_amdgcn_sched_barrier(0);  // every load issued before the first MFMA waits
-        calculer_b<NP, NRT, PAS>(acc, bq, ks0, B, a_codes, a_sa, lr, lg);
+        calculer_b<NP, NRT, PAS, LOT>(acc, bq, ks0, B, a_codes, a_sa, lr, lg);
     }
     __builtin_amdgcn_sched_barrier(0);
     asm volatile("s_nop 15");
@@ -509,15 +510,18 @@ __device__ __forceinline__ void prefill_bande(const ParamsPrefill& pp, const uin
     const uint32_t g0 = duo0 ? wu >> 3 : 0u, wk0 = duo0 ? (wu & 7u) : wu;
     const uint32_t tok0 = 16u * g0 + lr;
     const uint32_t c0 = tok0 < n_e ? paires[debut_e + tok0] : paires[debut_e];
+    // loads per B batch: six for gate/up (x: one piece), three for down (act: three pieces), which
+    // measured faster there than six
+    constexpr uint32_t LOT = J == 2u ? PF_LOT : 3u;
     u32x4 pre[PF_LOT];
     {
         const uint8_t* src0 = bsrc + uint64_t(J == 2u ? c0 / pp.k : c0) * PF_PIECES_BF * pas_p;
         auto charger0 = [&](auto np) {
             constexpr uint32_t NP = decltype(np)::value;
             if (duo0)
-                charger_b<NP, 8>(pre, src0, pas_p, wk0, B);
+                charger_b<NP, 8, LOT>(pre, src0, pas_p, wk0, B);
             else
-                charger_b<NP, 16>(pre, src0, pas_p, wk0, B);
+                charger_b<NP, 16, LOT>(pre, src0, pas_p, wk0, B);
         };
         using U = uint32_t;
         if (wk0 < B) {  // wave-uniform
@@ -566,13 +570,13 @@ __device__ __forceinline__ void prefill_bande(const ParamsPrefill& pp, const uin
         auto produit = [&](auto np) {
             constexpr uint32_t NP = decltype(np)::value;
             if (nrt == 5u)
-                produit_bf16<NP, 5, PREMIER, PAS>(acc, src, pas_p, wk, B, base + PF_A, a_sa, lr, lg, pre);
+                produit_bf16<NP, 5, PREMIER, PAS, LOT>(acc, src, pas_p, wk, B, base + PF_A, a_sa, lr, lg, pre);
             else if (nrt == 4u)
-                produit_bf16<NP, 4, PREMIER, PAS>(acc, src, pas_p, wk, B, base + PF_A, a_sa, lr, lg, pre);
+                produit_bf16<NP, 4, PREMIER, PAS, LOT>(acc, src, pas_p, wk, B, base + PF_A, a_sa, lr, lg, pre);
             else if (nrt == 2u)
-                produit_bf16<NP, 2, PREMIER, PAS>(acc, src, pas_p, wk, B, base + PF_A, a_sa, lr, lg, pre);
+                produit_bf16<NP, 2, PREMIER, PAS, LOT>(acc, src, pas_p, wk, B, base + PF_A, a_sa, lr, lg, pre);
             else
-                produit_bf16<NP, 1, PREMIER, PAS>(acc, src, pas_p, wk, B, base + PF_A, a_sa, lr, lg, pre);
+                produit_bf16<NP, 1, PREMIER, PAS, LOT>(acc, src, pas_p, wk, B, base + PF_A, a_sa, lr, lg, pre);
         };
         using U = uint32_t;
         if (P == 1u)
