@@ -627,13 +627,13 @@ constexpr uint32_t TUILES_ECHELLES = trc::FILS_ECHELLES_FUSION / 32;
 
 // Grid of a DELTA pass over `travaux` matrices of `blocs` blocks: each half-wavefront takes a run of
 // whole tiles, so that a block's prologue (LUT, record, medians, top-k) and a ring's opening serve
-// several tiles; runs of about 16 macro-steps when the launch has work for more than 8192
+// several tiles; runs of about 32 macro-steps when the launch has work for more than 8192
 // half-wavefronts (a 1024-thread block per CU) at that length, shorter ones down to a single tile
 // when it has less, so that a small launch (one token's matrices) keeps its parallelism.
 uint32_t grille_echelles(uint64_t blocs, uint32_t n_delta, uint32_t travaux) {
     const uint32_t n = n_delta ? n_delta : 1u;
     const uint64_t par_demi = ((blocs + 127u) / 128u) * travaux / 8192u;  // macro-steps per half at 8192 halves
-    const uint64_t tuiles = std::min<uint64_t>(std::max<uint64_t>(par_demi / n, 1u), n < 16u ? 16u / n : 1u);
+    const uint64_t tuiles = std::min<uint64_t>(std::max<uint64_t>(par_demi / n, 1u), n < 32u ? 32u / n : 1u);
     return grille_tuiles(blocs, uint32_t(n * tuiles), TUILES_ECHELLES);
 }
 
