@@ -199,7 +199,7 @@ def test_prefill_refuses_unsupported_shapes_before_launching():
 def test_driver_half_refuses_bad_arguments_before_any_hip_call():
     """The driver half's contract checks (trc-cuda/src/lib.rs:448-451, 521-524, 591-623) run before
     the runtime is touched, so they answer without a device."""
-    l = _lib.charger()
+    l = K.bibliotheque()  # declared return types: the error text is a char pointer
     from troncons_amd import pilote  # noqa: F401  (declares the argument types)
     V = K._Vue
     h = C.c_void_p()
