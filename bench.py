@@ -30,6 +30,7 @@ sys.path.insert(0, str(RACINE))
 
 METRIQUE = "MoE layer us/token @batch1 top-4; compressed-weight HBM GB/s (% of peak)"
 PIC_HBM = 8000.0  # GB/s, MI355X
+PART_CPU_PAR_GPU = 16  # host CPUs a one-GPU box grants this process
 C_GPT = 2880
 
 
@@ -776,7 +777,10 @@ def main():
     dev = torch.device("cuda:0")
     dims = DimsExpert.gpt_oss()
     E, k, C = args.experts, args.k, C_GPT
-    n_fils = min(16, os.cpu_count() or 1)
+    # every CPU this process may run on (its affinity mask), up to the 16 host CPUs that the GPU
+    # boxes grant each GPU: the encoder's threads and the CPU baseline's all-core leg use them all
+    utilisables = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    n_fils = max(1, min(utilisables, PART_CPU_PAR_GPU))
     fz = fusion.Fusion()
     flux = torch.cuda.current_stream()
     V = VueCarte.de

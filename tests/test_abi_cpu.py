@@ -178,22 +178,30 @@ def test_wrappers_refuse_wrong_sizes_carte_rs_468():
 
 
 def test_prefill_refuses_unsupported_shapes_before_launching():
-    """The batched prefill holds a tile's decoded bytes in registers (at most 16 macro-steps per
-    CODES_CTX tile) and a row's blocks in LDS (at most 4096 columns): other shapes are usage errors,
-    returned before any HIP call."""
+    """The batched prefill keeps a row's blocks in LDS (at most 4096 columns) and at most 16384
+    (position, slot) pairs a call: other shapes are usage errors, returned before any HIP call. Any
+    CODES_CTX tile length is taken: up to 16 macro-steps the band kernels decode their tiles, longer
+    tiles (the reference encoder's 256, rans.rs:32) are decoded once per chosen expert into a slot
+    of the reference layout, which the workspace then holds for every expert of the layer."""
     from troncons_amd import fusion
 
     fz = fusion.Fusion()
     dims = DimsExpert.gpt_oss()
     v = VueCarte(1 << 20, 1 << 40)
-    assert fusion.taille_travail_prefill(dims, 128, 512, 4, 16) > 0
-    assert fusion.taille_travail_prefill(dims, 128, 512, 4, 32) == 0
+    court = fusion.taille_travail_prefill(dims, 128, 512, 4, 16)
+    assert court > 0
+    for n in (17, 32, 256):
+        long_ = fusion.taille_travail_prefill(dims, 128, 512, 4, n)
+        assert long_ > court and long_ >= 128 * K.taille_emplacement(dims)
+    assert fusion.taille_travail_prefill(dims, 128, 512, 4, 0) == 0
     assert fusion.taille_travail_prefill(DimsExpert.de([256, 256, 256], [8192, 8192, 256]), 8, 4, 4, 8) == 0
     assert fusion.taille_travail_prefill(dims, 128, 8192, 4, 16) == 0  # more than 16384 pairs
     with pytest.raises(K.ErreurUsage):
-        fz.prefill_moe(v, 128, v, dims, v, 512, v, v, 4, v, v, v, 4, 32, f=0)
+        fz.prefill_moe(v, 128, v, dims, v, 512, v, v, 4, v, v, v, 4, 0, f=0)
     with pytest.raises(K.ErreurUsage):  # workspace too small
         fz.prefill_moe(v, 128, v, dims, v, 512, v, v, 4, v, v, VueCarte(1 << 20, 4096), 4, 16, f=0)
+    with pytest.raises(K.ErreurUsage):  # long tiles: the slots do not fit a short-tile workspace
+        fz.prefill_moe(v, 128, v, dims, v, 512, v, v, 4, v, v, VueCarte(1 << 20, court), 256, 256, f=0)
 
 
 def test_driver_half_refuses_bad_arguments_before_any_hip_call():

@@ -235,6 +235,31 @@ def test_attention_random_against_oracle(k, position, fenetre):
     assert np.abs(got - ref).max() <= 3e-6 * np.abs(ref).max()
 
 
+def test_attention_first_chunk_of_minus_inf_scores(k):
+    """Positions 0..63 (the first chunk of the first wavefront) hold keys with a -inf component
+    against a positive query component: their scores are -inf and their weights 0, since the
+    reference's maximum includes the sink before any exponential (passe.cuh:306-371). The output
+    stays finite and meets the random-head tolerances."""
+    position = 300
+    rng = np.random.default_rng(17)
+    p = ParamsAttention.gpt_oss(position, 0)
+    po = O.attention_gpt_oss(position, 0)
+    q = rng.standard_normal(64 * 64).astype(np.float32)
+    q.reshape(64, 64)[:, 5] = np.abs(q.reshape(64, 64)[:, 5]) + 0.25
+    ck = (rng.standard_normal((position + 1) * 512) * 0.5).astype(np.float16)
+    ck.reshape(position + 1, 8, 64)[:64, :, 5] = -np.inf
+    ck = ck.view(np.uint16)
+    cv = rng.standard_normal((position + 1) * 512).astype(np.float16).view(np.uint16)
+    puits = rng.standard_normal(64).astype(np.float32)
+    got = _attention(k, q, ck, cv, puits, p)
+    assert np.isfinite(got).all()
+    ref = O.attention(q, ck, cv, puits, po)
+    ref64 = attention_f64(q, ck, cv, puits, po)
+    assert np.isfinite(ref).all() and np.isfinite(ref64).all()
+    assert np.abs(got - ref64).max() <= 1e-6 * np.abs(ref64).max()
+    assert np.abs(got - ref).max() <= 3e-6 * np.abs(ref).max()
+
+
 def test_argmax_ties_nan_and_random(k):
     v = np.zeros(100_000, np.float32)
     v[0] = np.nan

@@ -235,3 +235,65 @@ def test_prefill_bad_indices_counted_and_skipped(fz):
     valides = [i not in (3, 7) for i in range(T)]
     _verifier(got, residu0, x, idx, w, _slots(61, E, dims), dims, valides)
     couche.c.liberer()
+
+
+def _decaler_debut_delta(partie: np.ndarray, j: int, t: int) -> np.ndarray:
+    """The part with the first word of DELTA tile t of matrix j moved one word later, kept inside
+    [start[t-1], start[t+1]] (the starts stay monotonic; only the tile boundary is wrong)."""
+    p = partie.copy()
+    n = int.from_bytes(p[10:12].tobytes(), "little")
+    (d,) = [64 + 16 * i for i in range(n) if p[64 + 16 * i] == 3 and p[64 + 16 * i + 1] == j]  # DELTA = kind 3
+    dec = int.from_bytes(p[d + 4:d + 8].tobytes(), "little")
+    T = int.from_bytes(p[dec + 8:dec + 12].tobytes(), "little")
+    debuts = p[dec + 16:dec + 16 + 4 * T].view(np.uint32)
+    assert 0 < t < T - 1 and debuts[t] + 1 <= debuts[t + 1]
+    debuts[t] += 1
+    return p
+
+
+def test_prefill_delta_interior_tile_start_counted(fz):
+    """The prefill's DELTA pass decodes runs of consecutive tiles through one word ring (about 5
+    tiles per half-wavefront for 8 gpt-oss experts at N_delta = 1). A tile start moved inside a run
+    leaves the decoded bytes intact, but the reference flags the tile before it (its words do not
+    end on the next tile's first word, rans.rs:442-448): the pass must count it in the pointer word."""
+    E, T, k, N = 8, 4, 4, (1, 8)
+    couche = Couche(fz, 101, E, GPT, N)
+    idx = np.array([[0, 1, 2, 3], [4, 5, 6, 0], [7, 0, 1, 2], [0, 3, 5, 7]], np.uint32)
+    w = np.full((T, k), 0.25, np.float32)
+    x = np.stack([O.synth_normale_bf16(103, 4, i, 2880, 1.0) for i in range(T)])
+    residu0 = np.zeros((T, 2880), np.float32)
+    _, ctl = _lancer(fz, couche, E, GPT, x, idx, w, residu0, N)
+    assert list(ctl) == [0, 0, 0, 0]
+    # tile 1 of expert 0's gate DELTA stream: the second tile of the first run
+    abime = _decaler_debut_delta(couche.c.partie(0), 0, 1)
+    couche.parts[0].copy_(torch.from_numpy(abime))
+    _, ctl = _lancer(fz, couche, E, GPT, x, idx, w, residu0, N)
+    assert ctl[2] >= 1 and ctl[1] == 0, list(ctl)
+    couche.c.liberer()
+
+
+def test_prefill_reference_tile_lengths_gpt_oss_shape(fz):
+    """Streams written with the reference encoder's tile lengths (N = 256 for DELTA and CODES_CTX,
+    rans.rs:32): the chosen experts are decoded once into slots, the bands read them. 8 gpt-oss
+    experts, 16 positions with Zipf routing: every position within 1e-5 of the oracle chain and of
+    f64; a flipped bit in a chosen expert's CODES_CTX stream is counted."""
+    E, T, k, N = 8, 16, 4, (256, 256)
+    couche = Couche(fz, 111, E, GPT, N)
+    idx, w = _routage(112, T, E, k, zipf=1.1)
+    x = np.stack([O.synth_normale_bf16(113, 4, i, 2880, 1.0) for i in range(T)])
+    residu0 = np.stack([O.synth_normale_bf16(113, 5, i, 2880, 0.5) for i in range(T)])
+    got, ctl = _lancer(fz, couche, E, GPT, x, idx, w, residu0, N)
+    assert list(ctl) == [0, 0, 0, 0]
+    _verifier(got, residu0, x, idx, w, _slots(111, E, GPT), GPT)
+    # a flipped bit in the middle of expert idx[0, 0]'s up CODES_CTX stream
+    e0 = int(idx[0, 0])
+    p = couche.c.partie(e0)
+    n = int.from_bytes(p[10:12].tobytes(), "little")
+    (d,) = [64 + 16 * i for i in range(n) if p[64 + 16 * i] == 4 and p[64 + 16 * i + 1] == 1]  # CODES_CTX = kind 4
+    dec = int.from_bytes(p[d + 4:d + 8].tobytes(), "little")
+    lon = int.from_bytes(p[d + 8:d + 12].tobytes(), "little")
+    p[dec + lon // 2] ^= 0x10
+    couche.parts[e0].copy_(torch.from_numpy(p))
+    _, ctl = _lancer(fz, couche, E, GPT, x, idx, w, residu0, N)
+    assert ctl[0] + ctl[2] > 0 and ctl[1] == 0, list(ctl)
+    couche.c.liberer()

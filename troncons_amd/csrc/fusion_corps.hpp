@@ -378,10 +378,13 @@ __device__ __forceinline__ TeteTuile tete_course(const EnteteRans& h) {
 
 // DELTA tiles -> one entry per block (entree_bloc) with e = (med[row] + delta - 128) mod 256 and
 // kappa = the class of delta; blocks past the matrix (stream padding) get the padding entry. Each
-// tile starts from its own initial states and must end in state L; the run must end on the next
-// run's first word. The medians are read from LDS (MED_LDS = true: med_lds holds them) or from the
-// stream. A lane's 4 blocks of a macro-step lie in at most two rows when B >= 4; narrower rows take
-// a loop. `tete0`: tete_course(p.h), read by the caller before its barrier.
+// tile starts from its own initial states and must end in state L, its word pointer on the next
+// tile's first word (or W after the last tile), as the reference checks every tile
+// (commun.cuh:240-246, rans.rs:442-448): a run's ring carries the words across its tiles, so a tile
+// start inside the run is checked where the previous tile ends. The medians are read from LDS
+// (MED_LDS = true: med_lds holds them) or from the stream. A lane's 4 blocks of a macro-step lie in
+// at most two rows when B >= 4; narrower rows take a loop. `tete0`: tete_course(p.h), read by the
+// caller before its barrier.
 template <bool MED_LDS>
 __device__ __forceinline__ void corps_echelles_fusion(const Tache& tc, const PrepEchelles& p, const uint2* lut,
                                                       const uint8_t* med_lds, uint8_t* anneaux,
@@ -413,7 +416,7 @@ __device__ __forceinline__ void corps_echelles_fusion(const Tache& tc, const Pre
     Anneau a = ouvrir_anneau(h, p.fd, tete0.debut, lds, anneaux, v, nt > 0u);
     const uint32_t o0 = a.o2;
     uint32_t x = L;
-    uint32_t hors_l = 0;
+    uint32_t hors_l = 0, pointeur = 0;
     uint32_t b0 = 4u * (t_deb * N * VOIES + v);
     uint32_t ligne = b0 / B, reste = b0 - ligne * B;
     auto macro = [&](auto tous, bool actif_t) {
@@ -465,19 +468,28 @@ __device__ __forceinline__ void corps_echelles_fusion(const Tache& tc, const Pre
         }
     };
     const gptr<uint32_t> etats = glob<uint32_t>(h.etats);
-    // the initial states of ECH_KMAX tiles at a time; the next group's are requested while the
-    // current group decodes
-    uint32_t suiv[ECH_KMAX];
+    const gptr<uint32_t> debuts = glob<uint32_t>(h.debut);
+    // the initial states of ECH_KMAX tiles at a time, with the first word of the tile after each
+    // (where each must end); the next group's are requested while the current group decodes
+    uint32_t suiv[ECH_KMAX], suiv_fin[ECH_KMAX];
 #pragma unroll
-    for (uint32_t kk = 0; kk < ECH_KMAX; ++kk) suiv[kk] = etats[min(t_deb + kk, h.T - 1u) * VOIES + v];
+    for (uint32_t kk = 0; kk < ECH_KMAX; ++kk) {
+        suiv[kk] = etats[min(t_deb + kk, h.T - 1u) * VOIES + v];
+        suiv_fin[kk] = debuts[min(t_deb + kk + 1u, h.T - 1u)];
+    }
     for (uint32_t k0 = 0; k0 < nt_max; k0 += ECH_KMAX) {  // wave-uniform
-        uint32_t etat[ECH_KMAX];
+        uint32_t etat[ECH_KMAX], fin_mots[ECH_KMAX];
 #pragma unroll
-        for (uint32_t kk = 0; kk < ECH_KMAX; ++kk) etat[kk] = suiv[kk];
+        for (uint32_t kk = 0; kk < ECH_KMAX; ++kk) {
+            etat[kk] = suiv[kk];
+            fin_mots[kk] = suiv_fin[kk];
+        }
         if (k0 + ECH_KMAX < nt_max) {  // wave-uniform
 #pragma unroll
-            for (uint32_t kk = 0; kk < ECH_KMAX; ++kk)
+            for (uint32_t kk = 0; kk < ECH_KMAX; ++kk) {
                 suiv[kk] = etats[min(t_deb + k0 + ECH_KMAX + kk, h.T - 1u) * VOIES + v];
+                suiv_fin[kk] = debuts[min(t_deb + k0 + ECH_KMAX + kk + 1u, h.T - 1u)];
+            }
         }
 #pragma unroll
         for (uint32_t kk = 0; kk < ECH_KMAX; ++kk) {
@@ -493,10 +505,13 @@ __device__ __forceinline__ void corps_echelles_fusion(const Tache& tc, const Pre
             uint32_t m = 0;
             for (; m < nb_min; ++m) macro(std::true_type{}, true);
             for (; m < nb_max; ++m) macro(std::false_type{}, m < nb);
-            if (tuile) hors_l += (x != L) ? 1u : 0u;
+            if (tuile) {
+                hors_l += (x != L) ? 1u : 0u;
+                const uint32_t attendu = t_deb + k + 1u < h.T ? fin_mots[kk] : h.W;
+                pointeur += (v == 0 && tete0.debut + (a.o2 - o0) / 2u != attendu) ? 1u : 0u;
+            }
         }
     }
-    const uint32_t pointeur = (v == 0 && nt > 0u && tete0.debut + (a.o2 - o0) / 2u != tete0.attendu) ? 1u : 0u;
     verser_controle(controle, hors_l, pointeur);
 }
 

@@ -514,8 +514,11 @@ __device__ __forceinline__ void attention_tete(const float* __restrict__ q, cons
         const bool ok = c0 + lane < n;
         const float s = ok ? produit_cle(qs, cles + uint64_t(case_de(lane)) * dkv) * p.echelle : -INFINITY;
         const float m2 = fmaxf(m, max_vague(s));
-        const float alpha = expf(m - m2);  // 0 for the first chunk (m = -inf)
-        const float e = expf(s - m2);      // 0 for lanes past the end
+        // While every score so far is -inf (keys with an infinite component), m2 is -inf and
+        // exp(-inf - -inf) would be NaN: no term has weight yet, as in the reference, whose maximum
+        // includes the sink before any exponential (passe.cuh:306-371).
+        const float alpha = m == -INFINITY ? 0.0f : expf(m - m2);  // 0 for the first chunk (m = -inf)
+        const float e = m2 == -INFINITY ? 0.0f : expf(s - m2);      // 0 for lanes past the end
         z = fmaf(z, alpha, somme_vague(e));
         poids[w][lane] = e;  // read back by this wavefront only, in program order
         const uint32_t nc = min(64u, n - c0);

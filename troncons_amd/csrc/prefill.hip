@@ -12,6 +12,12 @@
 //   fusion_echelles       (prefill mode) DELTA -> block entries of every chosen expert's matrices;
 //   prefill_mfma_gu       gate and up: bands decoded into LDS, bf16 MFMA (the weights converted from
 //                         MXFP4 where they are read) against the expert's positions, + bias -> gu;
+//
+// Streams whose CODES_CTX tiles are longer than the 16 macro-steps a band holds in registers (the
+// reference encoder writes 256, rans.rs:32) take two slot-decoder launches instead of the DELTA pass
+// (prefill_emplacements_echelles, prefill_emplacements_codes: every chosen expert decoded once into
+// a slot of the reference's layout, all of them at once, so the long chains run side by side), and
+// the band kernels copy their band's codes and scales from the slot instead of decoding them.
 //   prefill_swiglu_quant  act = swiglu_oai(gate, up) per pair, split into bf16 pieces;
 //   prefill_mfma_bas      down -> s, one row of D per pair (the reference's pos.s layout), bf16 MFMA;
 //   prefill_combiner      x_i += ((w0 s_i0 + w1 s_i1) + ...) in slot order, no FMA.
@@ -29,11 +35,13 @@
 // bytes 4g .. 4g + 3 and a piece block stores value (j >> 1) + 16 (j & 1) at position j.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstring>
 
 #include "anneau.hpp"
 #include "chrono.hpp"
 #include "commun.hpp"
+#include "emplacement.hpp"
 #include "erreurs.hpp"
 #include "fusion_corps.hpp"
 #include "selection.hpp"
@@ -41,6 +49,7 @@
 namespace trc {
 
 constexpr uint32_t PF_FILS = 1024;        // 16 wavefronts: 32 tiles decoded per band
+constexpr uint32_t PF_FILS_CODES_SLOT = 1024;  // long tiles' CODES_CTX slot decoder: 32 tiles per block
 constexpr uint32_t PF_NMAX = 16;          // macro-steps per CODES_CTX tile held in registers
 constexpr uint32_t PF_PIECES_BF = 3;      // bf16 pieces per activation block
 constexpr uint32_t PF_Q_FILS = 256;       // threads per block of the piece kernels (16 per 32-value block)
@@ -87,7 +96,21 @@ struct ParamsPrefill {
     uint32_t T, k, E, D;
     uint32_t bx, bact;     // blocks per piece row of x and act: C/32 + 1, R/32 + 1
     uint32_t quatre;       // the combine takes 4 rows per thread (D % 4 == 0, residus 16-byte aligned)
+    uint64_t emplacements; // long tiles: expert e's slot (reference layout) at emplacements + e * pas_emplacement,
+                           // decoded by the slot decoders; 0: the band kernels decode their tiles
+    uint64_t pas_emplacement;
 };
+
+// The slot layout of a prefill's experts (the reference's, abi.rs:76-122).
+__device__ __forceinline__ trc_dims_expert dims_prefill(const ParamsPrefill& pp) {
+    trc_dims_expert d;
+#pragma unroll
+    for (uint32_t j = 0; j < 3; ++j) {
+        d.lignes[j] = pp.lignes[j];
+        d.colonnes[j] = pp.colonnes[j];
+    }
+    return d;
+}
 
 // Splits values q and q + 16 of a 32-value block into PF_PIECES_BF bf16 pieces: word q of each
 // 64-byte piece block (piece stride `pas` bytes) holds value q (low half) and q + 16 (high half).
@@ -259,6 +282,46 @@ prefill_swiglu_quant(ParamsPrefill pp) {
                                uint64_t(Ba) * 64u));
     }
     noter_pieces(reinterpret_cast<uint32_t*>(pp.pieces) + 1, P);
+}
+
+// Long tiles: DELTA of matrix j = blockIdx.y of expert e = blockIdx.z -> the scales and biases of
+// the expert's slot, for every expert that a position chose; streams from the mounted directory,
+// whose record carries the reader's checks (a failed record is a format error, counted once here
+// and once by the band kernels, as the DELTA pass and the band kernels count it for short tiles).
+extern "C" __global__ void __launch_bounds__(trc::FILS_ECHELLES)
+prefill_emplacements_echelles(ParamsPrefill pp, const uint32_t* __restrict__ luts, uint32_t* __restrict__ controle) {
+    using namespace trc;
+    __shared__ LdsEchelles<FILS_ECHELLES> s;
+    const uint32_t e = blockIdx.z, j = blockIdx.y;
+    if (reinterpret_cast<const uint32_t*>(pp.compte)[e] == 0u) return;
+    const MatricePartie m = lire_matrice_constante(pp.repertoire + uint64_t(e * 3u + j) * sizeof(MatricePartie));
+    const uint32_t R = choisir(pp.lignes, j), B = choisir(pp.colonnes, j) / 32u;
+    if (m.bon == 0u) {
+        if (blockIdx.x == 0 && threadIdx.x == 0) atomicAdd(&controle[CTL_FORMAT], 1u);
+        return;
+    }
+    const trc_disposition disp = disposition(dims_prefill(pp), j);
+    uint8_t* mat = reinterpret_cast<uint8_t*>(pp.emplacements + uint64_t(e) * pp.pas_emplacement + disp.base);
+    echelles_vers_emplacement<FILS_ECHELLES>(m.delta, m.med, m.biais, entete_de(m.delta, m.dP, m.dN, m.dT, m.dW), R, B,
+                                             mat, disp, luts + uint64_t(j) * 4u * M, controle, s);
+}
+
+// Long tiles: CODES_CTX of matrix j = blockIdx.y of expert e = blockIdx.z -> the code bytes of the
+// expert's slot (contexts from the slot's scales, decoded by the launch before). 1024-thread blocks:
+// 32 tiles per block, the three decode tables staged once for them.
+extern "C" __global__ void __launch_bounds__(trc::PF_FILS_CODES_SLOT)
+prefill_emplacements_codes(ParamsPrefill pp, const uint32_t* __restrict__ luts, uint32_t* __restrict__ controle) {
+    using namespace trc;
+    __shared__ LdsCodesT<PF_FILS_CODES_SLOT> s;
+    const uint32_t e = blockIdx.z, j = blockIdx.y;
+    if (reinterpret_cast<const uint32_t*>(pp.compte)[e] == 0u) return;
+    const MatricePartie m = lire_matrice_constante(pp.repertoire + uint64_t(e * 3u + j) * sizeof(MatricePartie));
+    if (m.bon == 0u) return;  // counted by the DELTA launch
+    const uint32_t R = choisir(pp.lignes, j), B = choisir(pp.colonnes, j) / 32u;
+    const trc_disposition disp = disposition(dims_prefill(pp), j);
+    uint8_t* mat = reinterpret_cast<uint8_t*>(pp.emplacements + uint64_t(e) * pp.pas_emplacement + disp.base);
+    codes_vers_emplacement<PF_FILS_CODES_SLOT>(m.codes, m.med, entete_de(m.codes, m.cP, m.cN, m.cT, m.cW), R, B, mat,
+                                               disp, luts + (uint64_t(j) * 4u + 1u) * M, controle, s);
 }
 
 namespace trc {
@@ -457,6 +520,8 @@ __device__ __forceinline__ void prefill_bande(const ParamsPrefill& pp, const uin
     if (r0 >= R) return;
     const uint32_t nl = min(RB, R - r0);
     const uint32_t* lut_src = luts + (uint64_t(j) * 4u + 1u) * M;
+    // long tiles: the band's codes and scales come from the expert's slot, nothing is decoded here
+    const bool depuis_emplacement = pp.emplacements != 0u;
     ChargeLut<3> charge_lut;
     charge_lut.demarrer(lut_src, 3u * M / 4u);
     const MatricePartie m = *reinterpret_cast<const MatricePartie*>(pp.repertoire + uint64_t(e * 3u + j) * sizeof(MatricePartie));
@@ -464,8 +529,9 @@ __device__ __forceinline__ void prefill_bande(const ParamsPrefill& pp, const uin
     const uint32_t N = h.N;
     const uint32_t ba = r0 * B, bb = (r0 + nl) * B;  // the band's blocks
     const uint32_t t_a = N ? (ba / 8u) / N : 0u, t_b = N ? ((bb - 1u) / 8u) / N : 0u;
-    const bool bon = m.bon != 0u && N >= 1u && N <= PF_NMAX && t_b < h.T && t_b - t_a < 32u * PF_TOURS;
-    charge_lut.poser(lut_src, reinterpret_cast<uint2*>(lds + LDS_LUT), 3u * M / 4u);
+    const bool bon = m.bon != 0u &&
+                     (depuis_emplacement || (N >= 1u && N <= PF_NMAX && t_b < h.T && t_b - t_a < 32u * PF_TOURS));
+    if (!depuis_emplacement) charge_lut.poser(lut_src, reinterpret_cast<uint2*>(lds + LDS_LUT), 3u * M / 4u);
     if (!bon) {
         if (blockIdx.x == 0 && threadIdx.x == 0) atomicAdd(&controle[CTL_FORMAT], 1u);
         return;
@@ -479,10 +545,11 @@ __device__ __forceinline__ void prefill_bande(const ParamsPrefill& pp, const uin
     const gptr<u32x4> ent16 = glob<u32x4>(reinterpret_cast<const void*>(pp.ech + uint64_t(e * 3u + j) * pp.pas_ech));
     uint32_t hors_l = 0, pointeur = 0;
     TourBande tour0, tour1;
+    tour0.nb = tour1.nb = 0u;
     const uint32_t t00 = t_a + 2u * w, t01 = t00 + 32u;
     // one copy of the decode code for both rounds (a smaller hot loop for the instruction cache)
 #pragma nounroll
-    for (uint32_t r = 0; r < PF_TOURS; ++r) {
+    for (uint32_t r = 0; r < (depuis_emplacement ? 0u : PF_TOURS); ++r) {
         const uint32_t t0 = r ? t01 : t00;
         TourBande tb;
         tb.nb = 0u;
@@ -538,8 +605,20 @@ __device__ __forceinline__ void prefill_bande(const ParamsPrefill& pp, const uin
     // ---- store the band's codes and scales
     const uint32_t a_sa = base + pf_sa(RB, B), a_part = base + pf_part(RB, B);
     const uint32_t haut = lane >= 32u ? 1u : 0u;
-    poser_tour(tour0, t00 + haut, N, ba, bb, base, a_sa);
-    poser_tour(tour1, t01 + haut, N, ba, bb, base, a_sa);
+    if (depuis_emplacement) {
+        // the band's blocks [ba, bb) of the slot: 16 code bytes each (16-byte aligned), one scale byte each
+        const trc_disposition disp = disposition(dims_prefill(pp), j);
+        const uint8_t* mat = reinterpret_cast<const uint8_t*>(pp.emplacements + uint64_t(e) * pp.pas_emplacement + disp.base);
+        const gptr<u32x4> codes = glob<u32x4>(mat + 16ull * ba);
+        const gptr<uint8_t> echelles = glob<uint8_t>(mat + disp.echelles + ba);
+        for (uint32_t i = threadIdx.x; i < nl * B; i += blockDim.x) {
+            ecrire_lds<u32x4>(base + PF_A + 16u * i, codes[i]);
+            ecrire_lds<uint8_t>(a_sa + i, echelles[i]);
+        }
+    } else {
+        poser_tour(tour0, t00 + haut, N, ba, bb, base, a_sa);
+        poser_tour(tour1, t01 + haut, N, ba, bb, base, a_sa);
+    }
     // padding: rows nl .. RB - 1 of a last, partial band (zero codes, scale 1)
     for (uint32_t i = threadIdx.x; i < (RB - nl) * B; i += blockDim.x) {
         const uint32_t o = nl * B + i;
@@ -724,14 +803,18 @@ uint64_t al(uint64_t x) { return (x + 255u) & ~uint64_t(255); }
 // fit the 64 tiles a block decodes in two rounds and whose codes, scales and partial sums fit the LDS;
 // 0 if none does. The more of the 64 tile slots a band fills, the fewer wavefronts idle in the second
 // round (gpt-oss rows: 80 rows are 56.25 tiles, 64 rows 45).
+// Long tiles (N > 16: bands copied from the slots, nothing decoded per band): the LDS alone decides.
+bool tuiles_longues(uint32_t N) { return N > trc::PF_NMAX; }
+
 uint32_t rb_de(uint32_t B, uint32_t N) {
     for (const uint32_t rb : {trc::PF_RB_MAX, 64u, 32u, 16u})
-        if ((rb * B - 1u) / (8u * N) + 2u <= 32u * trc::PF_TOURS && trc::pf_lds_tient(rb, B)) return rb;
+        if ((tuiles_longues(N) || (rb * B - 1u) / (8u * N) + 2u <= 32u * trc::PF_TOURS) && trc::pf_lds_tient(rb, B))
+            return rb;
     return 0;
 }
 
 struct Disposition {
-    uint64_t pieces, compte, debut, paires, ech, pas_ech, xb, gu, ab, s, total;
+    uint64_t pieces, compte, debut, paires, ech, pas_ech, xb, gu, ab, s, emplacements, pas_emplacement, total;
 };
 
 int disposer(const trc_dims_expert* dims, uint32_t E, uint32_t T, uint32_t k, uint32_t n_codes, Disposition& d) {
@@ -746,8 +829,7 @@ int disposer(const trc_dims_expert* dims, uint32_t E, uint32_t T, uint32_t k, ui
         return usage("prefill : au plus %u colonnes (%u x %u)", 32u * trc::PF_BP_MAX, R, C);
     for (int j = 0; j < 3; ++j)
         if (dims->colonnes[j] / 32 < 8) return usage("matrice %d : moins de 8 blocs par ligne", j);
-    if (n_codes == 0 || n_codes > trc::PF_NMAX)
-        return usage("prefill : N de CODES_CTX %u (1 a %u macro-pas par tuile)", n_codes, trc::PF_NMAX);
+    if (n_codes == 0 || n_codes > 65535) return usage("prefill : N de CODES_CTX %u", n_codes);
     for (int j = 0; j < 3; ++j)
         if (rb_de(dims->colonnes[j] / 32, n_codes) == 0) return usage("prefill : N = %u trop petit", n_codes);
     if (E == 0 || E > trc::EXPERTS_MAX || k == 0 || k > trc::TOPK_MAX || k > E) return usage("top-%u sur %u", k, E);
@@ -764,9 +846,19 @@ int disposer(const trc_dims_expert* dims, uint32_t E, uint32_t T, uint32_t k, ui
     p += al(4ull * E);
     d.paires = p;
     p += al(4ull * n);
-    d.pas_ech = trc::octets_entrees(Rm, C);
-    d.ech = p;
-    p += 3ull * E * d.pas_ech;
+    d.pas_ech = 0;
+    d.ech = 0;
+    d.emplacements = 0;
+    d.pas_emplacement = 0;
+    if (tuiles_longues(n_codes)) {  // one slot per expert of the layer (the chosen ones are decoded)
+        d.pas_emplacement = trc_taille_emplacement(dims);
+        d.emplacements = p;
+        p += uint64_t(E) * d.pas_emplacement;
+    } else {  // the DELTA pass's block entries
+        d.pas_ech = trc::octets_entrees(Rm, C);
+        d.ech = p;
+        p += 3ull * E * d.pas_ech;
+    }
     d.xb = p;
     p += al(64ull * T * trc::PF_PIECES_BF * (C / 32u + 1u));
     d.gu = p;
@@ -827,6 +919,8 @@ extern "C" int trc_prefill_moe(trc_vue repertoire, uint32_t experts, trc_vue lut
     pp.poids = poids.adresse;
     pp.x = x.adresse;
     pp.residus = residus.adresse;
+    pp.emplacements = d.pas_emplacement ? b + d.emplacements : 0u;
+    pp.pas_emplacement = d.pas_emplacement;
     pp.xb = b + d.xb;
     pp.gu = b + d.gu;
     pp.ab = b + d.ab;
@@ -862,8 +956,24 @@ extern "C" int trc_prefill_moe(trc_vue repertoire, uint32_t experts, trc_vue lut
     const uint32_t Rm = D > R ? D : R;
     TRC_LANCER(prefill_grouper, dim3(1), dim3(1024), f, pp, ctl);
     TRC_LANCER(prefill_quant_x, dim3(T), dim3(trc::PF_Q_FILS), f, pp);
-    r = trc::lancer_echelles_prefill(pm, Rm, C, n_delta, l, ctl, f);
-    if (r != TRC_OK) return r;
+    if (pp.emplacements != 0) {
+        // long tiles: every chosen expert decoded once into its slot (scales, then codes), grids of
+        // tile pairs over the largest of the three matrices (the bodies loop over the tiles)
+        uint32_t td = 1, tc = 1;
+        for (int j = 0; j < 3; ++j) {
+            const uint64_t blocs = uint64_t(dims->lignes[j]) * (dims->colonnes[j] / 32);
+            td = std::max<uint32_t>(td, uint32_t(((blocs + 127) / 128 + n_delta - 1) / n_delta));
+            tc = std::max<uint32_t>(tc, uint32_t(((blocs * 16 + 127) / 128 + n_codes - 1) / n_codes));
+        }
+        constexpr uint32_t tuiles_d = trc::FILS_ECHELLES / 32, tuiles_c = trc::PF_FILS_CODES_SLOT / 32;
+        TRC_LANCER(prefill_emplacements_echelles, dim3((td + tuiles_d - 1) / tuiles_d, 3, experts),
+                   dim3(trc::FILS_ECHELLES), f, pp, l, ctl);
+        TRC_LANCER(prefill_emplacements_codes, dim3((tc + tuiles_c - 1) / tuiles_c, 3, experts),
+                   dim3(trc::PF_FILS_CODES_SLOT), f, pp, l, ctl);
+    } else {
+        r = trc::lancer_echelles_prefill(pm, Rm, C, n_delta, l, ctl, f);
+        if (r != TRC_OK) return r;
+    }
     TRC_LANCER(prefill_mfma_gu, dim3((R + pp.rb[0] - 1) / pp.rb[0], 2 * experts), dim3(trc::PF_FILS), f, pp, l, ctl);
     TRC_LANCER(prefill_swiglu_quant, dim3(T * k), dim3(trc::PF_Q_FILS), f, pp);
     TRC_LANCER(prefill_mfma_bas, dim3((D + pp.rb[2] - 1) / pp.rb[2], experts), dim3(trc::PF_FILS), f, pp, l, ctl);
