@@ -33,6 +33,7 @@ struct Avance {
     uint32_t dAttendu;     // DELTA: the word its decode must end on
     u32x4 dmots;           // DELTA: bytes 16v of its 16-aligned word area (its first 512 bytes)
     uint32_t med0, med1;   // medians of the rows of blocks 4v and 4v + 3 of the CODES tile
+    uint32_t rang0;        // the row of block 4v
 };
 
 // 16 bytes at byte `o` of a stream of `n` bytes (f.p 16-aligned), read at an address clamped to the
@@ -61,6 +62,7 @@ __device__ __forceinline__ Avance lire_avance(const EnteteRans& hc, const DescFl
     a.dDebut = a.dAttendu = 0;
     a.dmots = u32x4{0u, 0u, 0u, 0u};
     a.med0 = a.med1 = 0;
+    a.rang0 = 0;
     if (DELTA) {
         const uint32_t tau = t >> (hd.N - 1u);  // t / N_delta, N_delta being 1 or 2
         const TeteTuile td = lire_tete_borne(hd, tau, v);
@@ -70,8 +72,11 @@ __device__ __forceinline__ Avance lire_avance(const EnteteRans& hc, const DescFl
         const uint32_t base_d = uint32_t(reinterpret_cast<const uint8_t*>(hd.mots) - fd.p) + 2u * td.debut;
         a.dmots = lire16_flux(fd.p, fd.longueur, (base_d & ~15u) + 16u * v);
         const uint32_t bloc0 = 128u * t + 4u * v;
-        a.med0 = uint32_t(glob<uint8_t>(med)[min(B.quotient(bloc0), R - 1u)]);
-        a.med1 = uint32_t(glob<uint8_t>(med)[min(B.quotient(bloc0 + 3u), R - 1u)]);
+        // B >= 8: block 4v + 3 is in row rang0 or the next one
+        a.rang0 = B.quotient(bloc0);
+        const uint32_t rang3 = a.rang0 + (bloc0 + 3u - a.rang0 * B.d >= B.d ? 1u : 0u);
+        a.med0 = uint32_t(glob<uint8_t>(med)[min(a.rang0, R - 1u)]);
+        a.med1 = uint32_t(glob<uint8_t>(med)[min(rang3, R - 1u)]);
     }
     return a;
 }
@@ -97,30 +102,74 @@ __device__ __forceinline__ uint32_t pas_delta(uint32_t& x, uint32_t o2, uint32_t
     return e & 0xFFu;
 }
 
-// The 4 block entries of lane v (blocks 4v .. 4v + 3 of CODES tile t) from its 4 delta bytes, the
-// four at once on packed bytes (no branch): e - 128 = (med + delta) mod 256 byte-wise without carries
-// between bytes, the row's median being med0 up to the row's end and med1 after it (B >= 8: one row
-// change at most); kappa = 0 below 128, 1 at 128, 2 above, from bit 7 of delta and an exact
-// byte-wise zero test of delta ^ 0x80.
-__device__ __forceinline__ u32x4 entrees_de_delta(uint32_t mot, const Avance& a, uint32_t bloc0, uint32_t nblocs,
-                                                  const Diviseur& divB) {
-    const uint32_t B = divB.d;
-    const uint32_t col0 = bloc0 - divB.quotient(bloc0) * B;
-    const uint32_t reste = B - col0;  // blocks left in the row from block 4v (>= 1)
-    const uint32_t apres = reste >= 4u ? 0u : (0xFFFFFFFFu << (8u * reste));
-    const uint32_t medp = ((a.med0 * 0x01010101u) & ~apres) | ((a.med1 * 0x01010101u) & apres);
-    const uint32_t ep = ((medp & 0x7F7F7F7Fu) + (mot & 0x7F7F7F7Fu)) ^ ((medp ^ mot) & 0x80808080u);
-    const uint32_t v = mot ^ 0x80808080u;
-    const uint32_t nul = ~(((v & 0x7F7F7F7Fu) + 0x7F7F7F7Fu) | v | 0x7F7F7F7Fu);  // bit 7: delta byte == 128
+// Block entries of the CODES pass (LDS only; the separate DELTA pass keeps entree_bloc's layout):
+//   bits 7-13   column block b (x byte offset b * 128 in LDS; 127 = the zero slot),
+//   bits 15-16  context kappa (LUT byte offset kappa * 32 KiB),
+//   bits 23-30  the block's biased E8M0 exponent e,
+//   bit 31      the block starts a row.
+// Read as an f32, an entry is +-(1.f) * 2^(e - 127). v_cvt_scalef32_pk_f32_fp4 takes only the
+// exponent field of its scale operand (its sign and mantissa bits are ignored), so with the entry
+// as scale it returns the block's weights E2M1 * 2^(e - 127) = k * 2^(e - 128) themselves, exact for
+// e <= 252 (inf / NaN above). Padding: the zero slot with e = 127 (scale 1).
+constexpr uint32_t ENTC_EXP = 23u;
+constexpr uint32_t ENTC_BOURRAGE = (COLONNE_NULLE << 7) | (127u << ENTC_EXP);
+// e - 128 of an entry (the scale of the tiles outside the scale-in-conversion range).
+__device__ __forceinline__ int exposant_entree(uint32_t ent) { return int((ent ^ 0x40000000u) << 1) >> 24; }
+
+// A lane's 4 entries (blocks 4v .. 4v + 3 of its CODES tile) and what its tile needs to know of them.
+struct EntreesLane {
     u32x4 s;
-#pragma unroll
-    for (uint32_t k = 0; k < 4; ++k) {
-        const uint32_t col = k < reste ? col0 + k : k - reste;
-        const uint32_t ctx = 2u * ((mot >> (8u * k + 7u)) & 1u) - ((nul >> (8u * k + 7u)) & 1u);
-        const uint32_t ent = (col << 7) | (ctx << 15) | (((ep >> (8u * k)) & 255u) << ENT_EXP) | (col == 0u ? ENT_LIGNE : 0u);
-        s[k] = bloc0 + k < nblocs ? ent : ENTREE_BOURRAGE;
+    bool ligne;  // one of the 4 blocks starts a row (the tile's own first block excepted)
+    bool ech;    // every exponent e of the 4 lies in [64, 191]. The weights with the block scale
+                 // folded in are then 2^(e-128) times the doubled E2M1 values, exactly, and every
+                 // product and sum of the dot product with them is 2^(e-128) times the one without
+                 // them, bit for bit, unless it leaves the normal f32 range (|x| beyond about 2^60
+                 // or below 2^-60)
+};
+
+// The 4 block entries of lane v (blocks 4v .. 4v + 3 of CODES tile t) from its 4 delta bytes,
+// computed on packed bytes (byte k for block 4v + k) and gathered with byte permutes, no branch
+// outside the stream's last tile:
+//   e       = (med + delta - 128) mod 256, i.e. (med + delta) mod 256 with bit 7 flipped, added
+//             byte-wise without carries between bytes, med being the median of row rang0 up to
+//             the row's end and of the next row after it (B >= 8: one row change at most);
+//   kappa   = 0 below 128, 1 at 128, 2 above (bit 7 of delta, and an exact byte-wise zero test of
+//             delta ^ 0x80);
+//   column  = (4v + k - row start) per byte, the row start a byte-wise zero test of it.
+// Byte k of the four packed values is entry k shifted right by 7: [column, kappa, e, row start].
+__device__ __forceinline__ EntreesLane entrees_de_delta(uint32_t mot, const Avance& a, uint32_t bloc0, uint32_t nblocs,
+                                                        const Diviseur& divB, uint32_t masque_ligne) {
+    const uint32_t B = divB.d;
+    const uint32_t col0 = bloc0 - a.rang0 * B;
+    const uint32_t reste = B - col0;  // blocks left in the row from block 4v (>= 1)
+    const uint32_t apres = reste >= 4u ? 0u : (0xFFFFFFFFu << (8u * reste));  // bytes k >= reste
+    const uint32_t medp = __builtin_amdgcn_perm(a.med1, a.med0, apres & 0x04040404u);
+    uint32_t ee = ((medp & 0x7F7F7F7Fu) + (mot & 0x7F7F7F7Fu)) ^ ((medp ^ mot) & 0x80808080u) ^ 0x80808080u;
+    const uint32_t vd = mot ^ 0x80808080u;
+    const uint32_t nul = ~(((vd & 0x7F7F7F7Fu) + 0x7F7F7F7Fu) | vd | 0x7F7F7F7Fu);  // bit 7: delta byte == 128
+    uint32_t kp = ((mot >> 6) & 0x02020202u) - (nul >> 7);
+    uint32_t colp = __builtin_amdgcn_perm(0u, col0, 0x00000000u) + 0x03020100u - ((B * 0x01010101u) & apres);
+    uint32_t rp = ~(((colp & 0x7F7F7F7Fu) + 0x7F7F7F7Fu) | colp | 0x7F7F7F7Fu) >> 7;  // 1 where the column is 0
+    const uint32_t n_vrais = nblocs > bloc0 ? nblocs - bloc0 : 0u;
+    if (n_vrais < 4u) {
+        // blocks past the matrix: padding (the zero slot, context 0, e = 127, no row start)
+        const uint32_t pad = 0xFFFFFFFFu << (8u * n_vrais);
+        colp |= pad & 0x7F7F7F7Fu;
+        kp &= ~pad;
+        ee = (ee & ~pad) | (pad & 0x7F7F7F7Fu);
+        rp &= ~pad;
     }
-    return s;
+    EntreesLane r;
+    // e in [64, 191] <=> bits 7 and 6 of e differ
+    r.ech = ((ee ^ (ee << 1)) & 0x80808080u) == 0x80808080u;
+    r.ligne = (rp & masque_ligne) != 0u;
+    const uint32_t lo = __builtin_amdgcn_perm(kp, colp, 0x05010400u), hi = __builtin_amdgcn_perm(kp, colp, 0x07030602u);
+    const uint32_t lo2 = __builtin_amdgcn_perm(rp, ee, 0x05010400u), hi2 = __builtin_amdgcn_perm(rp, ee, 0x07030602u);
+    r.s[0] = __builtin_amdgcn_perm(lo2, lo, 0x05040100u) << 7;
+    r.s[1] = __builtin_amdgcn_perm(lo2, lo, 0x07060302u) << 7;
+    r.s[2] = __builtin_amdgcn_perm(hi2, hi, 0x05040100u) << 7;
+    r.s[3] = __builtin_amdgcn_perm(hi2, hi, 0x07060302u) << 7;
+    return r;
 }
 
 // The launch's block size (a kernel's compile-time constant) and x-extent, the latter read once at
@@ -202,6 +251,8 @@ __device__ __forceinline__ void corps_codes(const Tache& tc, const PrepCodes& p,
     Avance av = avance0;
     bool premiere = true;  // wave-uniform: the block's two first-tile barriers are still to pass
     const uint32_t a_lutd = base + LDS_ENT;
+    // the row-start bytes that count for `ligne`: all but the tile's own first block (lane 0, byte 0)
+    const uint32_t masque_ligne = v == 0u ? 0x01010100u : 0x01010101u;
     // Issue priority by progress: a wavefront decodes its first tile pair at priority 3, then 2 from
     // the pair's ninth macro-step, its second pair at 1 and then 0, so that on a SIMD the wavefronts
     // that are behind are issued ahead of those further on: their ends come closer together, and the
@@ -264,8 +315,15 @@ __device__ __forceinline__ void corps_codes(const Tache& tc, const PrepCodes& p,
             hors_l += (xd != L) ? 1u : 0u;
             pointeur += (v == 0 && cur.dDebut + (od - ((mots_d + 2u * cur.dDebut) & 15u)) / 2u != cur.dAttendu) ? 1u : 0u;
         }
-        // 2. the tile's 128 block entries
-        if (tuile) ecrire_lds<u32x4>(a_ent + 16u * v, entrees_de_delta(mot, cur, 128u * t + 4u * v, nblocs, p.B));
+        // 2. the tile's 128 block entries, which macro-steps start a row (macro-step m covers the
+        // blocks of lanes 2m and 2m + 1: bit 2m of `lignes_m`), and whether the wavefront's two
+        // tiles take the block scale inside the conversion
+        const EntreesLane el = entrees_de_delta(mot, cur, 128u * t + 4u * v, nblocs, p.B, masque_ligne);
+        if (tuile) ecrire_lds<u32x4>(a_ent + 16u * v, el.s);
+        const uint64_t vl = __builtin_amdgcn_ballot_w64(tuile && el.ligne);
+        uint32_t lignes_m = uint32_t(vl) | uint32_t(vl >> 32);
+        lignes_m = (lignes_m | (lignes_m >> 1)) & 0x55555555u;
+        const bool ech = __builtin_amdgcn_ballot_w64(tuile && !el.ech) == 0;
         // 3. the CODES words over the DELTA ones, and the next pair's streams read ahead
         ecrire_lds<u32x4>(a_anneau + 16u * v, cur.mots0);
         ecrire_lds<u32x4>(a_anneau + 512u + 16u * v, cur.mots1);
@@ -289,13 +347,18 @@ __device__ __forceinline__ void corps_codes(const Tache& tc, const PrepCodes& p,
         uint32_t rho = p.B.quotient(m0 * 8u);
         const uint32_t rho0 = rho, case0 = t - (rho0 * B) / 128u;  // first tile of row rho0 (128 blocks per tile)
         auto ecrire = [&](float s) { partiels[rho * kmax + (rho == rho0 ? case0 : 0u)] = s; };
-        uint32_t ent_suiv = tuile ? lire_lds<uint32_t>(a_ent_q) : ENTREE_BOURRAGE;
+        uint32_t ent_suiv = tuile ? lire_lds<uint32_t>(a_ent_q) : ENTC_BOURRAGE;
         const uint32_t nb_min = min(nb_a, nb_b);
         float acc = 0.0f;
-        auto macro = [&](auto tous, uint32_t m) {
+        // One macro-step. TOUS: every lane of both halves active. ECH: the block scale inside the
+        // conversion (the wavefront's entries are in the exact range). CONNUE: `ligne` says whether a
+        // row starts in this macro-step (from lignes_m); otherwise the entries' row flags are voted.
+        auto macro = [&](auto tous, auto echelle, auto connue, uint32_t m, bool ligne) {
             constexpr bool TOUS = decltype(tous)::value;
+            constexpr bool ECH = decltype(echelle)::value;
+            constexpr bool CONNUE = decltype(connue)::value;
             const bool actif = TOUS || m < nb;
-            const uint32_t ent = actif ? ent_suiv : ENTREE_BOURRAGE;
+            const uint32_t ent = actif ? ent_suiv : ENTC_BOURRAGE;
             const uint32_t ax = (ent & ENT_X) | a_x;
             const f32x4 xa = lire_lds<f32x4>(ax);
             const f32x4 xb = lire_lds<f32x4>(ax + 64u);
@@ -308,10 +371,14 @@ __device__ __forceinline__ void corps_codes(const Tache& tc, const PrepCodes& p,
             const uint32_t e3 = pas_r<TOUS>(x, a.o2, compte, lt, a_anneau, decal, masque_inf, actif);
             a.o2 += 2u * compte;
             avancer_anneau_r(a, v, actif);
-            const f32x2 w0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(e0, 2.0f, 3);
-            const f32x2 w1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(e1, 2.0f, 3);
-            const f32x2 w2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(e2, 2.0f, 3);
-            const f32x2 w3 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(e3, 2.0f, 3);
+            // byte 3 of each LUT word is the decoded code byte. ECH: scaled by the entry (its exponent
+            // field is e), the weights themselves; otherwise doubled by 2.0 into the reference's
+            // k = {0,1,2,3,4,6,8,12} and the dot product scaled by 2^(e-128) after. Both exact.
+            const float sc = ECH ? __uint_as_float(ent) : 2.0f;
+            const f32x2 w0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(e0, sc, 3);
+            const f32x2 w1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(e1, sc, 3);
+            const f32x2 w2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(e2, sc, 3);
+            const f32x2 w3 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(e3, sc, 3);
             float d = w0.x * xa.x;
             d = fmaf(w0.y, xb.x, d);
             d = fmaf(w1.x, xa.y, d);
@@ -320,40 +387,62 @@ __device__ __forceinline__ void corps_codes(const Tache& tc, const PrepCodes& p,
             d = fmaf(w2.y, xb.z, d);
             d = fmaf(w3.x, xa.w, d);
             d = fmaf(w3.y, xb.w, d);
-            const float c = __builtin_amdgcn_ldexpf(d, int(ent << 7) >> 24);
+            const float c = ECH ? d : __builtin_amdgcn_ldexpf(d, exposant_entree(ent));
             // lanes whose block starts a row, except the tile's first block (lanes q == 0 of macro-step
             // 0 in each half): that row's sum goes to the tile's first slot. The entries of inactive
             // lanes are padding, which starts no row.
-            const uint64_t vote =
-                __builtin_amdgcn_ballot_w64(int(ent) < 0) & (m == 0u ? ~0x0000000F0000000Full : ~0ull);
-            if (vote == 0) {
-                if (TOUS || actif) acc += c;
-            } else {
+            auto voter = [&]() {
+                return __builtin_amdgcn_ballot_w64(int(ent) < 0) & (m == 0u ? ~0x0000000F0000000Full : ~0ull);
+            };
+            uint64_t vote = 0;
+            if (!CONNUE) vote = voter();
+            // the sum with this macro-step's contribution, kept unless a row ends here
+            float suite = (TOUS || actif) ? acc + c : acc;
+            if (CONNUE ? ligne : vote != 0) {
+                if (CONNUE) vote = voter();
                 const uint32_t moitie = uint32_t(vote >> decal);
                 const uint32_t premier = moitie != 0u ? uint32_t(__builtin_ctz(moitie)) : 32u;
                 const bool apres = v >= premier;
-                if (!apres && (TOUS || actif)) acc += c;
-                const float s = somme_demi_f32(acc);
+                const float s = somme_demi_f32(apres ? acc : suite);
                 if (moitie != 0u) {
                     if (v == 0 && actif && rho < R) ecrire(s);
-                    acc = apres ? c : 0.0f;
+                    suite = apres && (TOUS || actif) ? c : 0.0f;
                     ++rho;
                 }
             }
+            acc = suite;
         };
-        uint32_t m = 0;
-        for (; m + 1u < nb_min; m += 2u) {
-            if (m == 8u) {
-                if (paire_n == 0u)
-                    __builtin_amdgcn_s_setprio(2);
-                else
-                    __builtin_amdgcn_s_setprio(0);
+        const auto prio_milieu = [&]() {
+            if (paire_n == 0u)
+                __builtin_amdgcn_s_setprio(2);
+            else
+                __builtin_amdgcn_s_setprio(0);
+        };
+        if (nb_min == 16u) {
+            // both tiles whole (wave-uniform): 16 macro-steps unrolled, the row starts known from
+            // the entries (a scalar test per macro-step), entry reads at constant offsets
+            auto tour = [&](auto echelle) {
+#pragma unroll 1
+                for (uint32_t mm = 0; mm < 16u; mm += 2u) {
+                    if (mm == 8u) prio_milieu();
+                    macro(std::true_type{}, echelle, std::true_type{}, mm, ((lignes_m >> (2u * mm)) & 1u) != 0u);
+                    macro(std::true_type{}, echelle, std::true_type{}, mm + 1u, ((lignes_m >> (2u * mm + 2u)) & 1u) != 0u);
+                }
+            };
+            if (ech)
+                tour(std::true_type{});
+            else
+                tour(std::false_type{});
+        } else {
+            uint32_t m = 0;
+            for (; m + 1u < nb_min; m += 2u) {
+                if (m == 8u) prio_milieu();
+                macro(std::true_type{}, std::false_type{}, std::false_type{}, m, false);
+                macro(std::true_type{}, std::false_type{}, std::false_type{}, m + 1u, false);
             }
-            macro(std::true_type{}, m);
-            macro(std::true_type{}, m + 1u);
+            if (m < nb_min) macro(std::true_type{}, std::false_type{}, std::false_type{}, m++, false);
+            for (; m < nb_a; ++m) macro(std::false_type{}, std::false_type{}, std::false_type{}, m, false);
         }
-        if (m < nb_min) macro(std::true_type{}, m++);
-        for (; m < nb_a; ++m) macro(std::false_type{}, m);
         const float s = somme_demi_f32(acc);
         if (tuile) {
             if (v == 0 && rho < R) ecrire(s);
