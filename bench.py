@@ -13,7 +13,8 @@ expert MLP), both rotating over the 128 experts; --config 4 (a token through L r
 default 36, about 52 GB of parts; --ordo streams them from a .trc file through the native scheduler,
 with --prechargement / --biais-cache); --config 5 (a batched prefill of 512 positions with Zipf
 routing, grouped GEMM on the bf16 MFMA); --config 6 (a whole decode step: embedding,
-L gpt-oss layers of Q8_0 attention and fused compressed MoE, the 201088-row head, argmax).
+L gpt-oss layers of Q8_0 attention and fused compressed MoE, the 201088-row head, argmax); --noyaux
+(the reference kernel API over decoded VRAM slots: batched MXFP4 GEMVs of a layer step).
 """
 from __future__ import annotations
 
@@ -401,17 +402,18 @@ def bench_prefill(args, c0, dims, E, k, C, fz, flux, dev, espace, x_tok, n_fils,
 
 
 def bench_flux(args, E, k, C, dims, dev, flux, fz, x_tok, n_fils):
-    """Config 4, streaming variant: the layers' parts live in pinned host memory. Per layer and token:
-    router (gemv_f32 + routeur_topk) on the compute stream, the k indices copied to the host (the
-    per-layer host sync of the reference scheduler, trc-ordo/src/lib.rs:1054-1370), the k chosen parts
-    copied by hipMemcpyAsync on a side stream, each expert decoded and applied (trc_expert_fusionne) as
-    soon as its copy has landed, then the ordered combine. Also timed: the copies alone and the
-    compute alone (parts already on the device), for the overlap."""
+    """Config 4, streaming variant, through the native engine (csrc/diffusion.cpp): the layers' parts
+    live in pinned host memory. Per layer and token: router (gemv_f32 + routeur_topk into a mapped
+    mailbox) on the compute stream, one host wait (the reference scheduler's per-layer sync,
+    trc-ordo/src/lib.rs:1054-1128), the k chosen parts copied on the engine's copy stream, each
+    expert's fused decode and MLP (trc_expert_fusionne) started on its copy's event, then the
+    ordered combine. Also timed, for the overlap: the same copies alone (hipMemcpyAsync of the
+    routed parts, one stream) and the same compute alone (the routed parts already on the device)."""
     import numpy as np
     import torch
 
-    from troncons_amd import codeur, fusion
     from troncons_amd import noyaux as K
+    from troncons_amd.diffusion import Diffusion
     from troncons_amd.noyaux import VueCarte
     V = VueCarte.de
     nk = K.Noyaux()
@@ -421,7 +423,7 @@ def bench_flux(args, E, k, C, dims, dev, flux, fz, x_tok, n_fils):
     t0 = time.perf_counter()
     for l in range(L):
         if fichier is None:
-            h = SourceSynth(args.graine, l, E, dims, args.n_delta, args.n_codes, n_fils)
+            h = SourceSynth(args.graine, l, E, dims, args.n_delta_m, args.n_codes_m, n_fils)
         else:
             h = SourceFichier(fichier, l, E)
         t = np.array([h.taille(e) for e in range(E)], np.int64)
@@ -445,70 +447,75 @@ def bench_flux(args, E, k, C, dims, dev, flux, fz, x_tok, n_fils):
         print(f"bench: layer {l} encoded into pinned host memory ({pin.numel() / 1e9:.2f} GB)", file=sys.stderr,
               flush=True)
     t_gen = time.perf_counter() - t0
-    tmax = int(max(t.max() for t in tailles))
-    arrivees = [torch.empty(tmax + 256, dtype=torch.uint8, device=dev) for _ in range(k)]
-    arr = [a[(-a.data_ptr()) % 256:][:tmax] for a in arrivees]
+    moteur = Diffusion([(epingles[l], decal[l], tailles[l], vluts[l][1], V(routeurs[l])) for l in range(L)], E, k, dims,
+                       args.n_delta, args.n_codes)
     xs = torch.from_numpy(x_tok).to(dev)
     vx = [V(xs, 4 * C * t, 4 * C) for t in range(len(x_tok))]
-    logits = torch.zeros(E, dtype=torch.float32, device=dev)
-    idx = torch.zeros(8, dtype=torch.int32, device=dev)
-    poids = torch.zeros(8, dtype=torch.float32, device=dev)
-    idx_h = torch.zeros(8, dtype=torch.int32, pin_memory=True)
-    sorties = torch.zeros(k * C, dtype=torch.float32, device=dev)
     residu = torch.zeros(C, dtype=torch.float32, device=dev)
-    ctl = torch.zeros(4, dtype=torch.int32, device=dev)
-    tr_t = torch.empty(fusion.taille_travail_expert(dims, args.n_codes) + 256, dtype=torch.uint8, device=dev)
-    tr = VueCarte(tr_t.data_ptr() + (-tr_t.data_ptr()) % 256, fusion.taille_travail_expert(dims, args.n_codes))
-    copie = torch.cuda.Stream(device=dev)
-    ev_idx = torch.cuda.Event()
-    ev_arr = [torch.cuda.Event() for _ in range(k)]
-    copie_ok, calcul_ok = [True], [True]
-    octets = [0]
+    n_tok = args.steps + args.warmup
 
     def pas(s):
+        moteur.jeton(vx[s % len(vx)], V(residu), f=flux)
+
+    s0 = moteur.stats()
+    ms = temps(pas, args.steps, args.warmup, flux)
+    s1 = moteur.stats()
+    assert (moteur.controle() == 0).all(), f"control words {moteur.controle()}"
+    octets_tok = (s1["octets_copies"] - s0["octets_copies"]) / n_tok
+    attente_couche = (s1["us_attente_routeur"] - s0["us_attente_routeur"]) / (n_tok * L)
+    # the routing of the timed tokens (x fixed per token: the same choices every time)
+    choix = []
+    for s in range(args.steps):
+        choix.append([moteur.couche(l, vx[s % len(vx)], V(residu), f=flux) for l in range(L)])
+    torch.cuda.synchronize()
+    # copies alone: the routed parts, one stream, in the engine's order
+    tmax = int(max(t.max() for t in tailles))
+    arr = [torch.empty(tmax, dtype=torch.uint8, device=dev) for _ in range(k)]
+    copie = torch.cuda.Stream(device=dev)
+
+    def pas_copies(s):
+        with torch.cuda.stream(copie):
+            for l in range(L):
+                for q, e in enumerate(choix[s % args.steps][l]):
+                    n, o = int(tailles[l][e]), int(decal[l][e])
+                    arr[q][:n].copy_(epingles[l][o:o + n], non_blocking=True)
+        flux.wait_stream(copie)
+
+    ms_copie = temps(pas_copies, args.steps, min(args.warmup, args.steps), flux)
+    # compute alone: the same launches over the routed parts already on the device
+    from troncons_amd import fusion
+    presents = {}
+    for s in range(args.steps):
+        for l in range(L):
+            for e in choix[s][l]:
+                if (l, int(e)) not in presents:
+                    n, o = int(tailles[l][e]), int(decal[l][e])
+                    t = torch.empty(n + 256, dtype=torch.uint8, device=dev)
+                    v = t[(-t.data_ptr()) % 256:][:n]
+                    v.copy_(epingles[l][o:o + n])
+                    presents[(l, int(e))] = v
+    logits = torch.zeros(E, dtype=torch.float32, device=dev)
+    idx = torch.zeros(16, dtype=torch.int32, device=dev)
+    poids = torch.zeros(16, dtype=torch.float32, device=dev)
+    sorties = torch.zeros(k * C, dtype=torch.float32, device=dev)
+    ctl = torch.zeros(4, dtype=torch.int32, device=dev)
+    n_tr = fusion.taille_travail_expert(dims, args.n_codes)
+    tr_t = torch.empty(n_tr + 256, dtype=torch.uint8, device=dev)
+    tr = VueCarte(tr_t.data_ptr() + (-tr_t.data_ptr()) % 256, n_tr)
+
+    def pas_calcul(s):
         x = vx[s % len(vx)]
         for l in range(L):
             nk.gemv_f32(V(routeurs[l]), x, None, V(logits), E, C, f=flux)
             nk.routeur_topk(V(logits), E, k, V(idx), V(poids), f=flux)
-            idx_h.copy_(idx, non_blocking=True)
-            ev_idx.record(flux)
-            ev_idx.synchronize()
-            sel = idx_h.numpy()[:k]
-            if copie_ok[0]:
-                with torch.cuda.stream(copie):
-                    for q, e in enumerate(sel):
-                        n = int(tailles[l][e])
-                        o = int(decal[l][e])
-                        arr[q][:n].copy_(epingles[l][o:o + n], non_blocking=True)
-                        ev_arr[q].record(copie)
-                        octets[0] += n
-            if calcul_ok[0]:
-                for q, e in enumerate(sel):
-                    if copie_ok[0]:
-                        flux.wait_event(ev_arr[q])
-                    # compute alone: the arrival buffers keep layer 0's parts 0..k-1 (and its LUTs)
-                    n = int(tailles[l][e]) if copie_ok[0] else int(tailles[0][q])
-                    lut = vluts[l][1] if copie_ok[0] else vluts[0][1]
-                    fz.expert_fusionne(VueCarte(arr[q].data_ptr(), n), lut, dims, x, V(sorties, 4 * C * q, 4 * C),
-                                       V(ctl), tr, args.n_delta, args.n_codes, f=flux)
-                nk.combiner(V(residu), V(sorties), C, V(poids), k, C, f=flux)
-            elif copie_ok[0]:
-                for q in range(k):
-                    flux.wait_event(ev_arr[q])
+            for q, e in enumerate(choix[s % args.steps][l]):
+                fz.expert_fusionne(V(presents[(l, int(e))]), vluts[l][1], dims, x, V(sorties, 4 * C * q, 4 * C), V(ctl),
+                                   tr, args.n_delta, args.n_codes, f=flux)
+            nk.combiner(V(residu), V(sorties), C, V(poids), k, C, f=flux)
 
-    # the arrival buffers hold valid parts before the compute-only pass
-    with torch.cuda.stream(copie):
-        for q in range(k):
-            n = int(tailles[0][q])
-            arr[q][:n].copy_(epingles[0][int(decal[0][q]):int(decal[0][q]) + n], non_blocking=True)
-    torch.cuda.synchronize()
-    ms = temps(pas, args.steps, args.warmup, flux)
-    assert (ctl.cpu().numpy() == 0).all(), f"control words {ctl.cpu().numpy()}"
-    octets_tok = octets[0] / (args.steps + args.warmup)
-    calcul_ok[0] = False
-    ms_copie = temps(pas, args.steps, args.warmup, flux)
-    calcul_ok[0], copie_ok[0] = True, False
-    ms_calcul = temps(pas, args.steps, args.warmup, flux)
+    ms_calcul = temps(pas_calcul, args.steps, min(args.warmup, args.steps), flux)
+    assert (ctl.cpu().numpy() == 0).all()
+    moteur.detruire()
     us, us_c, us_k = (m * 1e3 / args.steps for m in (ms, ms_copie, ms_calcul))
     recouvrement = (us_c + us_k - us) / min(us_c, us_k)
     ligne = {
@@ -517,16 +524,18 @@ def bench_flux(args, E, k, C, dims, dev, flux, fz, x_tok, n_fils):
         "ms_per_step": round(ms / args.steps, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
         "dtype": "u32 rANS / f32 GEMV",
         "data": "synthetic (seeded MXFP4 law A, E8M0 in [119,125], bf16 N(0,1) activations, bf16 N(0,0.02) router)",
-        "config": {"workload": f"config4 streaming variant: a token through {L} MoE layers x {E} gpt-oss-120b "
-                               "experts kept in pinned host memory; per layer the router's top-4 is read by the "
-                               "host, the 4 parts are copied (hipMemcpyAsync, side stream) and each expert is "
-                               "decoded as soon as its copy lands", "layers": L, "experts": E, "k": k,
-                   "n_codes": args.n_codes, "n_delta": args.n_delta},
+        "config": {"workload": f"config4 streaming variant, native engine (trc_diffusion): a token through {L} MoE "
+                               f"layers x {E} gpt-oss-120b experts kept in pinned host memory; per layer one mailbox "
+                               "wait, the 4 chosen parts copied on a side stream, each expert decoded in its fused "
+                               "MLP as soon as its copy lands", "layers": L, "experts": E, "k": k,
+                   "n_codes": args.n_codes, "n_delta": args.n_delta,
+                   "n_codes_per_matrix": list(args.n_codes_m), "n_delta_per_matrix": list(args.n_delta_m)},
         "h2d_bytes_per_token": int(octets_tok),
         "h2d_gbps": round(octets_tok / (us * 1e-6) / 1e9, 2),
         "copies_only_us": round(us_c, 1), "h2d_gbps_copies_only": round(octets_tok / (us_c * 1e-6) / 1e9, 2),
         "compute_only_us": round(us_k, 1),
         "overlap": round(recouvrement, 3),
+        "host_wait_per_layer_us": round(attente_couche, 1),
         "per_layer_us": round(us / L, 1),
         "setup_s": round(t_gen, 1),
     }
@@ -616,6 +625,132 @@ def bench_ordo(args, E, k, C, dims, dev, n_fils):
     }
     o.detruire()
     return ligne
+
+
+def bench_noyaux(args, c0, dims, E, k, C, dev, flux, x_tok):
+    """The reference kernel API over decoded slots (the native scheduler's layer once every part is
+    in a VRAM slot; Modele::fin_couche, trc-modele/src/lib.rs:533-553): S experts are decoded once
+    into slots (trc_decoder_lot), then a step takes k of them, in rotation so that a step's slots
+    come from HBM (the S slots exceed the 256 MB Infinity Cache), through trc_gemv_lot over the 2k
+    gate/up matrices, trc_swiglu_oai, trc_gemv_lot over the k down matrices and trc_combiner. The
+    two batched GEMVs are timed by events around each launch over the same steps."""
+    import numpy as np
+    import torch
+
+    from troncons_amd import noyaux as K
+    N = K.Noyaux()
+    V = K.VueCarte.de
+    S = max(args.emplacements or 32, k)
+    te = K.taille_emplacement(dims)
+    R, D = dims.lignes[0], dims.lignes[2]
+    pas_e = (te + 255) // 256 * 256
+    slots = torch.empty(S * pas_e + 256, dtype=torch.uint8, device=dev)
+    base = slots.data_ptr() + (-slots.data_ptr()) % 256
+    ctl = torch.zeros(4 * S, dtype=torch.int32, device=dev)
+    dd = b"".join(K.DescDecodage(c0.vue_partie(e).adresse, base + s * pas_e, c0.luts.data_ptr(),
+                                 ctl.data_ptr() + 16 * s).octets() for s, e in enumerate(range(S)))
+    descs_dec = torch.from_numpy(np.frombuffer(dd, np.uint8).copy()).to(dev)
+    t = time.perf_counter()
+    N.decoder_lot(V(descs_dec, 0, len(dd)), S, dims, f=flux)
+    torch.cuda.synchronize()
+    t_dec = time.perf_counter() - t
+    assert (ctl.cpu().numpy() == 0).all(), "slot decode control words"
+    disp = [K.disposition(dims, j) for j in range(3)]
+    xs = torch.from_numpy(x_tok).to(dev)
+    g = torch.zeros(k * R, dtype=torch.float32, device=dev)
+    u = torch.zeros_like(g)
+    a = torch.zeros_like(g)
+    sorties = torch.zeros(k * D, dtype=torch.float32, device=dev)
+    residu = torch.zeros(D, dtype=torch.float32, device=dev)
+    poids = torch.full((k,), 1.0 / k, dtype=torch.float32, device=dev)
+    n_rot = S // k
+    T = x_tok.shape[0]
+
+    def descs_pour(r, tok):
+        gu, bas = [], []
+        for i in range(k):
+            sl = base + ((r * k + i) % S) * pas_e
+            x = xs.data_ptr() + 4 * C * tok
+            gu.append(bytes(K.DescGemv(sl + disp[0].base, x, g.data_ptr() + 4 * R * i, R, C)))
+            gu.append(bytes(K.DescGemv(sl + disp[1].base, x, u.data_ptr() + 4 * R * i, R, C)))
+            bas.append(bytes(K.DescGemv(sl + disp[2].base, a.data_ptr() + 4 * R * i, sorties.data_ptr() + 4 * D * i,
+                                        D, R)))
+        return b"".join(gu) + b"".join(bas)
+
+    dg = b"".join(descs_pour(r, r % T) for r in range(n_rot))
+    descs = torch.from_numpy(np.frombuffer(dg, np.uint8).copy()).to(dev)
+    pas_d = 3 * k * 32
+    ev = []
+
+    def pas(s, chrono=False):
+        r = s % n_rot
+        o = r * pas_d
+        e0 = torch.cuda.Event(enable_timing=True) if chrono else None
+        if chrono:
+            e0.record(flux)
+        N.gemv_lot(V(descs, o, 2 * k * 32), 2 * k, R, f=flux)
+        if chrono:
+            e1 = torch.cuda.Event(enable_timing=True)
+            e1.record(flux)
+        N.swiglu_oai(V(g), V(u), V(a), k * R, f=flux)
+        if chrono:
+            e2 = torch.cuda.Event(enable_timing=True)
+            e2.record(flux)
+        N.gemv_lot(V(descs, o + 2 * k * 32, k * 32), k, D, f=flux)
+        if chrono:
+            e3 = torch.cuda.Event(enable_timing=True)
+            e3.record(flux)
+            ev.append((e0, e1, e2, e3))
+        N.combiner(V(residu), V(sorties), D, V(poids), k, D, f=flux)
+
+    ms = temps(pas, args.steps, args.warmup, flux)
+    evincer_caches()
+    for s in range(args.steps):
+        pas(s, chrono=True)
+    torch.cuda.synchronize()
+    gu_us = float(np.mean([e0.elapsed_time(e1) for e0, e1, _e2, _e3 in ev])) * 1e3
+    bas_us = float(np.mean([e2.elapsed_time(e3) for _e0, _e1, e2, e3 in ev])) * 1e3
+    # the reference's own throughput case (banc_k's gemv_mxfp4_lot): the 3k matrices of k experts
+    # as one batch of independent products, each against the token's x
+    d12 = b"".join(bytes(K.DescGemv(base + ((r * k + i) % S) * pas_e + disp[j].base, xs.data_ptr() + 4 * C * (r % T),
+                                    sorties.data_ptr() + 4 * D * i, dims.lignes[j], dims.colonnes[j]))
+                   for r in range(n_rot) for i in range(k) for j in range(3))
+    descs12 = torch.from_numpy(np.frombuffer(d12, np.uint8).copy()).to(dev)
+    evincer_caches()
+    ev12 = []
+    for s in range(args.steps):
+        a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a0.record(flux)
+        N.gemv_lot(V(descs12, (s % n_rot) * 3 * k * 32, 3 * k * 32), 3 * k, max(dims.lignes), f=flux)
+        a1.record(flux)
+        ev12.append((a0, a1))
+    torch.cuda.synchronize()
+    lot_us = float(np.mean([a0.elapsed_time(a1) for a0, a1 in ev12])) * 1e3
+    octets_mat = disp[0].pas  # one matrix of the slot: codes, scales, biases
+    o_gu, o_bas = 2 * k * octets_mat, k * octets_mat
+    us = ms / args.steps * 1e3
+    return {
+        "metric": "reference kernel API over decoded slots: us per layer step (k experts), batched MXFP4 GEMV GB/s",
+        "value": round(us, 2), "unit": "us/step", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms / args.steps, 5), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32 GEMV over MXFP4 slots (reference operation order)",
+        "data": "synthetic (seeded MXFP4 law A, E8M0 in [119,125], bf16 N(0,1) activations)",
+        "config": {"workload": f"{S} gpt-oss experts decoded once into VRAM slots ({S * te / 1e9:.2f} GB); a step: "
+                               f"trc_gemv_lot over {2 * k} gate/up matrices, trc_swiglu_oai, trc_gemv_lot over "
+                               f"{k} down matrices, trc_combiner; {k} slots per step in rotation", "slots": S, "k": k},
+        "gemv_lot_us": {"gate_up": round(gu_us, 2), "down": round(bas_us, 2),
+                        "method": "CUDA events around each launch on the launch's stream (includes the launch gap)"},
+        "gemv_lot_bytes": {"gate_up": o_gu, "down": o_bas},
+        "gemv_lot_gbps": {"gate_up": round(o_gu / gu_us / 1e3, 1), "down": round(o_bas / bas_us / 1e3, 1)},
+        "gemv_lot_frac_hbm": {"gate_up": round(o_gu / gu_us / 1e3 / PIC_HBM, 4),
+                              "down": round(o_bas / bas_us / 1e3 / PIC_HBM, 4)},
+        "gemv_lot_all_matrices": {"matrices": 3 * k, "bytes": 3 * k * octets_mat, "us": round(lot_us, 2),
+                                  "gbps": round(3 * k * octets_mat / lot_us / 1e3, 1),
+                                  "frac_hbm": round(3 * k * octets_mat / lot_us / 1e3 / PIC_HBM, 4),
+                                  "method": "one trc_gemv_lot over the 3k matrices of k slots (independent "
+                                            "products, as the reference's banc_k times gemv_mxfp4_lot), events"},
+        "slot_decode_s": round(t_dec, 3),
+    }
 
 
 def VueCarte_de(t, decalage, octets):
@@ -749,10 +884,19 @@ def main():
     ap.add_argument("--prechargement", action="store_true",
                     help="--ordo: each layer predicts the next layer's experts (its router over the normed residual) "
                          "and reads their parts ahead")
+    ap.add_argument("--noyaux", action="store_true",
+                    help="the reference kernel API over decoded slots: trc_gemv_lot over a layer step's k experts "
+                         "(--emplacements slots decoded once, default 32)")
     ap.add_argument("--experts", type=int, default=128)
     ap.add_argument("--k", type=int, default=4)
     ap.add_argument("--n-codes", type=int, default=16, help="macro-steps per CODES_CTX tile written by the encoder")
     ap.add_argument("--n-delta", type=int, default=1, help="macro-steps per DELTA tile written by the encoder")
+    ap.add_argument("--n-codes-gu", type=int, default=None, dest="n_codes_gu",
+                    help="the same for the gate and up matrices (the format stores N per stream); default for "
+                         "configs 3 and 4 with the default 16 / 1: 32, else --n-codes")
+    ap.add_argument("--n-delta-gu", type=int, default=None, dest="n_delta_gu",
+                    help="the same for the gate and up matrices; default for configs 3 and 4 with the default "
+                         "16 / 1: 2, else --n-delta")
     ap.add_argument("--graine", type=int, default=2026)
     ap.add_argument("--tokens", type=int, default=1000, help="seeded activations of the sweep")
     ap.add_argument("--distance-octets", type=float, default=512e6, dest="distance_octets",
@@ -762,6 +906,17 @@ def main():
     ap.add_argument("--calibrer-copie", action="store_true",
                     help="also run three plain 64 MiB device copies (counter calibration under rocprofv3 --pmc)")
     args = ap.parse_args()
+    # per-matrix tile lengths of the synthetic layers (gate, up, down); the API calls take the down
+    # matrix's, which size the workspace and choose the launch plan
+    # gate/up at 32 / 2 by default for the decode step (fewer tile starts in the larger launch; the
+    # down launch keeps 16 / 1, whose tiles fill the chip's wavefronts)
+    defaut_gu = args.config in (3, 4) and args.n_codes == 16 and args.n_delta == 1 and not args.fichier
+    if args.n_codes_gu is None:
+        args.n_codes_gu = 32 if defaut_gu else args.n_codes
+    if args.n_delta_gu is None:
+        args.n_delta_gu = 2 if defaut_gu else args.n_delta
+    args.n_codes_m = (args.n_codes_gu,) * 2 + (args.n_codes,)
+    args.n_delta_m = (args.n_delta_gu,) * 2 + (args.n_delta,)
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for {args.gpus}); the expert-parallel "
               "sharding across GPUs is a design, not run here.", file=sys.stderr)
@@ -805,7 +960,7 @@ def main():
     for l in range(n_couches):
         t = time.perf_counter()
         if fichier is None:
-            source = SourceSynth(args.graine, l, E, dims, args.n_delta, args.n_codes, n_fils)
+            source = SourceSynth(args.graine, l, E, dims, args.n_delta_m, args.n_codes_m, n_fils)
         else:
             source = SourceFichier(fichier, l, E)
         t_gen += time.perf_counter() - t
@@ -815,6 +970,9 @@ def main():
               f"({t_gen:.1f} s so far)", file=sys.stderr, flush=True)
     c0 = couches[0]
     x_tok = np.stack([codeur.synth_normale_bf16(args.graine, 4, t, C, 1.0) for t in range(args.tokens)])
+    if args.noyaux:
+        print(json.dumps(bench_noyaux(args, c0, dims, E, k, C, dev, flux, x_tok)), flush=True)
+        return
     xs = torch.from_numpy(x_tok).to(dev)
     vx = [V(xs, 4 * C * t, 4 * C) for t in range(args.tokens)]
     ctl = torch.zeros(4, dtype=torch.int32, device=dev)
@@ -993,8 +1151,9 @@ def main():
         "scaling": "weak", "vs_baseline": None, "dtype": "u32 rANS / f32 GEMV",
         "data": "synthetic (seeded MXFP4 law A, E8M0 in [119,125], bf16 N(0,1) activations, bf16 N(0,0.02) router)",
         "config": {"workload": workload, "experts": E, "k": k, "hidden": C, "layers": n_couches,
-                   "n_codes": args.n_codes, "n_delta": args.n_delta, "tokens": args.steps,
-                   "sweep_tokens": args.tokens, "mean_part_bytes": int(c0.utiles.mean())},
+                   "n_codes": args.n_codes, "n_delta": args.n_delta,
+                   "n_codes_per_matrix": list(args.n_codes_m), "n_delta_per_matrix": list(args.n_delta_m),
+                   "tokens": args.steps, "sweep_tokens": args.tokens, "mean_part_bytes": int(c0.utiles.mean())},
         "gbps_compressed": round(float(gbps), 1),
         "frac_hbm_layer": round(float(gbps / PIC_HBM), 4),
         "compressed_bytes_per_token": int(octets_tok.mean()),

@@ -380,7 +380,10 @@ int trc_couche_moe_fusionnee(trc_vue repertoire, uint32_t experts, trc_vue luts,
  * ends) as its workspace; it calls no allocating routine. A step needing more than the scratch
  * (trc_taille_travail_couche_moe) is a usage error. Every call on a device shares that device's
  * scratch: calls that overlap on one device (two streams, two threads) race; serialise them. The
- * scratch is taken on the device of `flux` (the current device if flux is null). */
+ * scratch is taken on the device of `flux` (the current device if flux is null); its device address
+ * is resolved once per device, by trc_contexte_creer (the library's set-up of a device) or else at
+ * the first call there. A caller that captures the step into a HIP graph creates the device's
+ * context, or makes one call, before the capture: the captured call then makes no runtime query. */
 uint64_t trc_octets_scratch(void);
 int trc_couche_moe_fusionnee_sans_alloc(trc_vue repertoire, uint32_t experts, trc_vue luts,
                                         const trc_dims_expert* dims, trc_vue routeur, trc_vue routeur_biais,
@@ -779,6 +782,42 @@ int trc_ordo_emplacement(const trc_ordo* o, uint16_t couche, uint16_t expert, tr
 int trc_ordo_temoin(const trc_ordo* o, uint16_t couche, uint16_t expert, void* flux, uint64_t* empreinte);
 void trc_ordo_detruire(trc_ordo* o);
 
+/* -------------------------- the streamed MoE layer on the fused path (host over HIP; trc-ordo)
+ *
+ * The expert part of Moteur::pas with every coded part in RAM (trc-ordo/src/lib.rs:1054-1128,
+ * 1328-1370) on the fused kernels, without slots: per layer the router (gemv_f32 + routeur_topk)
+ * writes the k indices into a mapped mailbox, the host waits once and reads them, the k parts are
+ * copied from pinned host memory on the engine's copy stream, each expert's trc_expert_fusionne
+ * starts on its copy's event, then trc_combiner. Two sets of k arrival buffers alternate between
+ * consecutive layers. Residuals equal the resident step's (trc_couche_moe_fusionnee) bit for bit. */
+typedef struct {
+    const void* parties;       /* pinned host memory holding the layer's level-0 parts */
+    const uint64_t* decalages; /* host u64[experts]: byte offset of expert e's part (16-byte aligned) */
+    const uint64_t* tailles;   /* host u64[experts]: its length */
+    trc_vue luts;              /* device u32[3][4][4096]: the layer's LUTs */
+    trc_vue routeur;           /* device f32[experts][C]: the router (gemv_f32 over the widened rows) */
+} trc_couche_hote;
+typedef struct {
+    uint64_t couches;           /* layers run */
+    uint64_t octets_copies;     /* bytes copied host -> device */
+    double us_attente_routeur;  /* host time spent waiting for the routers' events */
+} trc_stats_diffusion;
+typedef struct trc_diffusion trc_diffusion;
+/* The engine over n_couches layers (the arrays are copied; the pinned memory, LUTs and routers must
+ * outlive it), arrival buffers sized for the largest part. n_delta / n_codes as for
+ * trc_expert_fusionne. */
+int trc_diffusion_creer(const trc_couche_hote* couches, uint32_t n_couches, uint32_t experts, uint32_t k,
+                        const trc_dims_expert* dims, uint32_t n_delta, uint32_t n_codes, trc_diffusion** sortie);
+/* Layer `couche` for x on the compute stream flux: residu += combine of its k experts; the chosen
+ * indices are written to choisis[k] when it is not null. */
+int trc_diffusion_couche(trc_diffusion* m, uint32_t couche, trc_vue x, trc_vue residu, void* flux, uint32_t* choisis);
+/* Every layer in turn for one token (the same x, as trc_ordo_jeton). */
+int trc_diffusion_jeton(trc_diffusion* m, trc_vue x, trc_vue residu, void* flux);
+int trc_diffusion_stats(const trc_diffusion* m, trc_stats_diffusion* s);
+/* Copies out the control words of the fused experts (all zero on a good run); synchronous. */
+int trc_diffusion_controle(const trc_diffusion* m, uint32_t* mots);
+void trc_diffusion_detruire(trc_diffusion* m);
+
 /* ---------------------------------------- encoder front-end (host only; role of bins/trc-codeur) */
 
 /* The seeded synthetic workload (nibble law "A", E8M0 scales in [119,125], bf16 N(0,0.02) biases).
@@ -801,10 +840,21 @@ uint64_t trc_codeur_partie(uint16_t couche, uint16_t expert, const trc_dims_expe
                            const uint8_t* const* blocs17, const float* const* biais, const uint16_t* const* freqs4,
                            int canonique, uint32_t N_delta, uint32_t N_codes, uint8_t* out, uint64_t cap,
                            uint32_t* utiles);
+/* The same with the tile lengths of each matrix j = 0, 1, 2 (N_delta[j], N_codes[j]; the format
+ * stores N per stream, decisions/ARCHITECTURE.md:581, and the reference decoders honour it,
+ * commun.cuh:149-157). No counterpart in the reference encoder, which always writes 256. */
+uint64_t trc_codeur_partie_n(uint16_t couche, uint16_t expert, const trc_dims_expert* dims,
+                             const uint8_t* const* blocs17, const float* const* biais, const uint16_t* const* freqs4,
+                             int canonique, const uint32_t* N_delta, const uint32_t* N_codes, uint8_t* out,
+                             uint64_t cap, uint32_t* utiles);
 /* A whole synthetic layer (tables from all its experts, v1.2 parts), built on n_fils threads. */
 typedef struct trc_couche_synth trc_couche_synth;
 trc_couche_synth* trc_synth_couche(uint64_t graine, uint32_t couche, uint32_t n_experts, const trc_dims_expert* dims,
                                    uint32_t N_delta, uint32_t N_codes, uint32_t n_fils);
+/* The same with per-matrix tile lengths (N_delta[3], N_codes[3]). */
+trc_couche_synth* trc_synth_couche_n(uint64_t graine, uint32_t couche, uint32_t n_experts,
+                                     const trc_dims_expert* dims, const uint32_t* N_delta, const uint32_t* N_codes,
+                                     uint32_t n_fils);
 uint64_t trc_synth_couche_taille(const trc_couche_synth* c, uint32_t expert);
 uint32_t trc_synth_couche_utiles(const trc_couche_synth* c, uint32_t expert);
 const uint8_t* trc_synth_couche_partie(const trc_couche_synth* c, uint32_t expert);

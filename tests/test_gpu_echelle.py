@@ -281,48 +281,27 @@ def test_36_layers_resident_and_streamed(fz, pool):
     del blocs, couches
     torch.cuda.empty_cache()
 
-    # streaming variant: pool in pinned host memory; per layer the router (gemv_f32 over the widened
-    # bf16 rows, then routeur_topk) on the compute stream, the k indices read by the host, the chosen
-    # parts copied on a side stream, each expert run by trc_expert_fusionne once its copy has landed,
-    # then the ordered combine
-    nk = K.Noyaux()
+    # streaming variant through the native engine (trc_diffusion_*): the pool in pinned host memory;
+    # per layer the router (gemv_f32 over the widened bf16 rows, then routeur_topk into the mapped
+    # mailbox) on the compute stream, one host wait, the chosen parts copied on the engine's copy
+    # stream, each expert run by trc_expert_fusionne once its copy has landed, then the combine
+    from troncons_amd.diffusion import Diffusion
     epingle = torch.from_numpy(pool.hote).pin_memory()
-    tmax = int(pool.tailles.max())
-    arrivees = [zeros(tmax) for _ in range(KTOP)]
     r32 = [dev(((r16_h.astype(np.uint32) << 16).view(np.float32))) for r16_h in (_r16(r) for r in routeurs)]
     calcul = torch.cuda.current_stream()
-    copie = torch.cuda.Stream()
-    logits, idx, w = zeros(4 * E), zeros(32), zeros(32)
-    idx_h = torch.zeros(8, dtype=torch.int32).pin_memory()
-    sorties_d = zeros(4 * C_ * KTOP)
+    couches_h = [(epingle, pool.decal[perms[l]], pool.tailles[perms[l]], vue(luts[l]), vue(r32[l])) for l in range(L)]
+    moteur = Diffusion(couches_h, E, KTOP, GPT, *N)
     res2 = zeros(4 * C_)
-    ctl = zeros(16)
-    tr2 = zeros(fusion.taille_travail_expert(GPT, N[1]))
-    ev_idx = torch.cuda.Event()
-    ev = [torch.cuda.Event() for _ in range(KTOP)]
     for l in range(L):
-        nk.gemv_f32(vue(r32[l]), vue(xd), None, vue(logits), E, C_, f=calcul)
-        nk.routeur_topk(vue(logits), E, KTOP, vue(idx), vue(w), f=calcul)
-        idx_h.copy_(idx.view(torch.int32)[:8], non_blocking=True)
-        ev_idx.record(calcul)
-        ev_idx.synchronize()
-        sel = idx_h.numpy()[:KTOP].astype(np.int64)
-        assert (sel == par_couche[l][0]).all(), l
-        with torch.cuda.stream(copie):
-            for q, e in enumerate(sel):
-                p = int(perms[l][e])
-                arrivees[q][:int(pool.tailles[p])].copy_(
-                    epingle[int(pool.decal[p]):int(pool.decal[p] + pool.tailles[p])], non_blocking=True)
-                ev[q].record(copie)
-        for q, e in enumerate(sel):
-            calcul.wait_event(ev[q])
-            p = int(perms[l][e])
-            fz.expert_fusionne(vue(arrivees[q], 0, int(pool.tailles[p])), vue(luts[l]), GPT, vue(xd),
-                               vue(sorties_d, 4 * C_ * q, 4 * C_), vue(ctl), vue(tr2), *N, f=calcul)
-        nk.combiner(vue(res2), vue(sorties_d), C_, vue(w), KTOP, C_, f=calcul)
+        sel = moteur.couche(l, vue(xd), vue(res2), f=calcul)
+        assert (sel.astype(np.int64) == par_couche[l][0]).all(), l
         torch.cuda.synchronize()
-        assert list(hote(ctl, np.uint32)) == [0, 0, 0, 0], l
         got = hote(res2, np.float32)
         assert (got.view(np.uint32) == par_couche[l][2].view(np.uint32)).all(), \
             (l, np.abs(got - par_couche[l][2]).max())
+    assert list(moteur.controle()) == [0, 0, 0, 0]
+    st = moteur.stats()
+    assert st["couches"] == L and st["octets_copies"] == sum(
+        int(pool.tailles[perms[l][e]]) for l in range(L) for e in par_couche[l][0])
+    moteur.detruire()
     print("config4: streamed run equals the resident run at every layer", flush=True)

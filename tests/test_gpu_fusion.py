@@ -44,7 +44,7 @@ def _slot_j(ex, j):
     return ex.attendu[d.base:d.base + d.pas]
 
 
-@pytest.mark.parametrize("N", [(256, 256), (32, 32), (8, 16), (4, 1), (1, 16), (2, 16)])
+@pytest.mark.parametrize("N", [(256, 256), (32, 32), (8, 16), (4, 1), (1, 16), (2, 16), (2, 32)])
 def test_fused_gemv_one_matrix_config1(fz, N):
     ex = Expert(2026, GPT, N_delta=N[0], N_codes=N[1])
     x = O.synth_normale_bf16(2026, 1, 0, 2880, 1.0)
@@ -77,7 +77,7 @@ def _expert_exact(seed, dims):
     return blocs, biais
 
 
-@pytest.mark.parametrize("N", [(256, 256), (16, 32), (3, 7), (1, 16), (2, 16)])
+@pytest.mark.parametrize("N", [(256, 256), (16, 32), (3, 7), (1, 16), (2, 16), (2, 32)])
 def test_fused_gemv_bit_exact_on_integer_fixture(fz, N):
     dims = GPT
     blocs, biais = _expert_exact(7, dims)
@@ -94,7 +94,39 @@ def test_fused_gemv_bit_exact_on_integer_fixture(fz, N):
         assert (y.view(np.uint32) == y64.view(np.uint32)).all()
 
 
-@pytest.mark.parametrize("N", [(2, 3), (1, 16), (2, 16)])
+@pytest.mark.parametrize("N", [(1, 16), (2, 32)])
+def test_fused_gemv_scales_outside_the_folded_range(fz, N):
+    """Tiles whose exponents leave [64, 191] take the ldexp form instead of the scale folded into the
+    conversion: rows 0-999 have e in [192, 200], rows 1000-1999 in [40, 63], the rest in [119, 125]
+    (the fold), with tiles straddling the bands; each band within 1e-5 * its max|y| of f64."""
+    dims = GPT
+    rng = np.random.default_rng(13)
+    blocs, biais = [], []
+    for j in range(3):
+        r, c = dims.lignes[j], dims.colonnes[j]
+        nb = r * (c // 32)
+        ligne = np.repeat(np.arange(r), c // 32)
+        e = np.where(ligne < 1000, rng.integers(192, 201, nb),
+                     np.where(ligne < 2000, rng.integers(40, 64, nb), rng.integers(119, 126, nb))).astype(np.uint8)
+        bl = np.zeros((nb, 17), np.uint8)
+        bl[:, 0] = e
+        bl[:, 1:] = rng.integers(0, 256, (nb, 16), dtype=np.uint8)
+        blocs.append(bl.reshape(-1))
+        biais.append(np.zeros(r, np.float32))
+    freqs = [codeur.tables([blocs[j]], 2880, 90) for j in range(3)]
+    partie, _ = codeur.partie(blocs, biais, freqs, dims, N_delta=N[0], N_codes=N[1])
+    luts = O.luts_couche([[freqs[j][t] for t in range(4)] for j in range(3)])
+    x = O.synth_normale_bf16(13, 1, 0, 2880, 1.0)
+    for j in (0, 2):
+        y, ctl = _gemv(fz, partie, luts, j, 2880, 2880, x, *N)
+        assert list(ctl) == [0, 0, 0, 0]
+        slot = O.blocs_vers_soa(blocs[j], 2880, 2880, biais[j], canonique=True)
+        y64 = O.gemv_mxfp4_f64(slot, x, 2880, 2880)
+        for a, b in ((0, 1000), (1000, 2000), (2000, 2880)):
+            assert np.abs(y[a:b] - y64[a:b]).max() <= TOL * np.abs(y64[a:b]).max(), (j, a)
+
+
+@pytest.mark.parametrize("N", [(2, 3), (1, 16), (2, 16), (2, 32)])
 def test_fused_gemv_small_shapes_and_break(fz, N):
     dims = DimsExpert.de([300, 300, 257], [256, 256, 320])
     ex = Expert(5, dims, N_delta=N[0], N_codes=N[1])
@@ -160,7 +192,7 @@ def _mlp_oracle(ex, x, dims):
     return s, s64
 
 
-@pytest.mark.parametrize("N", [(256, 256), (32, 32), (8, 16), (1, 16), (2, 16)])
+@pytest.mark.parametrize("N", [(256, 256), (32, 32), (8, 16), (1, 16), (2, 16), (2, 32)])
 def test_fused_expert_config2(fz, N):
     ex = Expert(2027, GPT, N_delta=N[0], N_codes=N[1])
     x = O.synth_normale_bf16(2027, 1, 0, 2880, 1.0)
@@ -176,10 +208,13 @@ def test_fused_expert_config2(fz, N):
     assert np.abs(got - s64).max() <= TOL * np.abs(s64).max()
 
 
-@pytest.mark.parametrize("N", [(16, 32), (1, 16), (2, 16)])
+@pytest.mark.parametrize("N", [(16, 32), (1, 16), (2, 16), ((2, 2, 1), (32, 32, 16))])
 def test_fused_moe_layer_config3(fz, N):
+    """N: (N_delta, N_codes), one value for the three matrices or one per matrix (the bench's
+    gate/up at 2/32, down at 1/16); the layer step is called with the down matrix's."""
     E, k = 12, 4
     couche = codeur.CoucheSynthetique(2028, 0, E, GPT, N_delta=N[0], N_codes=N[1])
+    N = tuple(n if isinstance(n, int) else n[2] for n in N)
     freqs = couche.freqs()
     luts = O.luts_couche([[freqs[j][t] for t in range(4)] for j in range(3)])
     parts = [dev(couche.partie(e)) for e in range(E)]

@@ -66,6 +66,47 @@ def test_allocation_free_step_equals_the_allocating_one():
         couche.c.liberer()
 
 
+def test_allocation_free_step_replays_from_a_graph():
+    """The step captured into a HIP graph after the device's context is created (which resolves the
+    scratch address): every replay, with eager copies and synchronisations between them, gives the
+    allocating step's routing, weights and residual bits."""
+    from troncons_amd import pilote
+    fz = fusion.Fusion()
+    graine, E, dims, k, N = 2052, 16, DimsExpert.gpt_oss(), 4, (1, 16)
+    couche = Couche(fz, graine, E, dims, N)
+    C_, D = dims.colonnes[0], dims.lignes[2]
+    x = O.synth_normale_bf16(graine, 4, 0, C_, 1.0)
+    residu0 = O.synth_normale_bf16(graine, 5, 0, D, 0.5)
+    a = _pas(fz, couche, E, dims, k, N, x, residu0, False)
+    assert list(a[3]) == [0, 0, 0, 0]
+    ctx = pilote.Contexte(0)
+    xd, r0, res = dev(x), dev(residu0), dev(residu0)
+    idx, w, ctl = zeros(32), zeros(32), zeros(16)
+    args = (vue(couche.rep), E, vue(couche.luts), dims, vue(couche.r16), None, vue(xd), k, vue(res), vue(idx),
+            vue(w), vue(ctl))
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    print("no-alloc graph test: capturing the step", flush=True)
+    with torch.cuda.graph(g, stream=s):
+        fz.couche_moe_sans_alloc(*args, *N, f=s)
+    for rep in range(3):
+        res.copy_(r0)
+        ctl.zero_()
+        idx.zero_()
+        torch.cuda.synchronize()
+        print(f"no-alloc graph test: replay {rep}", flush=True)
+        g.replay()
+        torch.cuda.synchronize()
+        assert list(hote(ctl, np.uint32)) == [0, 0, 0, 0], rep
+        assert (hote(idx, np.uint32)[:k] == a[1]).all(), rep
+        assert (hote(w, np.float32)[:k].view(np.uint32) == a[2].view(np.uint32)).all(), rep
+        assert (hote(res, np.float32).view(np.uint32) == a[0].view(np.uint32)).all(), rep
+    del g
+    ctx.detruire()
+    couche.c.liberer()
+
+
 def test_step_larger_than_the_scratch_is_refused():
     fz = fusion.Fusion()
     dims, E, k, N = DimsExpert.gpt_oss(), 128, 8, (4, 16)

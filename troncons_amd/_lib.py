@@ -15,7 +15,8 @@ CSRC = PAQUET / "csrc"
 LIB_PATH = PAQUET / "libtroncons_hip.so"
 
 SOURCES_HIP = ["noyaux.hip", "fusion.hip", "prefill.hip", "passe.hip", "pilote.hip"]
-SOURCES_CPP = ["hote.cpp", "codeur.cpp", "chrono.cpp", "conteneur.cpp", "cache.cpp", "ordo.cpp", "modele.cpp"]
+SOURCES_CPP = ["hote.cpp", "codeur.cpp", "chrono.cpp", "conteneur.cpp", "cache.cpp", "ordo.cpp", "modele.cpp",
+               "diffusion.cpp"]
 
 # -packed-fp32-ops off: v_pk_* f32 forms are avoided on these boxes (the host pass warns that it
 # does not know the feature; harmless).

@@ -30,6 +30,13 @@ def _declarer(l):
     l.trc_synth_couche.argtypes = [C.c_uint64, C.c_uint32, C.c_uint32, C.POINTER(DimsExpert), C.c_uint32, C.c_uint32,
                                    C.c_uint32]
     l.trc_synth_couche.restype = C.c_void_p
+    l.trc_codeur_partie_n.argtypes = [C.c_uint16, C.c_uint16, C.POINTER(DimsExpert), C.POINTER(_u8p),
+                                      C.POINTER(_f32p), C.POINTER(_u16p), C.c_int, C.POINTER(C.c_uint32),
+                                      C.POINTER(C.c_uint32), _u8p, C.c_uint64, C.POINTER(C.c_uint32)]
+    l.trc_codeur_partie_n.restype = C.c_uint64
+    l.trc_synth_couche_n.argtypes = [C.c_uint64, C.c_uint32, C.c_uint32, C.POINTER(DimsExpert),
+                                     C.POINTER(C.c_uint32), C.POINTER(C.c_uint32), C.c_uint32]
+    l.trc_synth_couche_n.restype = C.c_void_p
     l.trc_synth_couche_taille.argtypes = [C.c_void_p, C.c_uint32]
     l.trc_synth_couche_taille.restype = C.c_uint64
     l.trc_synth_couche_utiles.argtypes = [C.c_void_p, C.c_uint32]
@@ -83,7 +90,15 @@ def tables(blocs_experts, R: int, B: int, canonique: bool = True) -> np.ndarray:
     return out.reshape(4, 256)
 
 
+def par_matrice(N) -> "C.Array":
+    """Tile lengths of the three matrices: one N for all, or (N_gate, N_up, N_down)."""
+    t = [int(N)] * 3 if isinstance(N, (int, np.integer)) else [int(n) for n in N]
+    assert len(t) == 3, N
+    return (C.c_uint32 * 3)(*t)
+
+
 def partie(blocs, biais, freqs, dims: DimsExpert, couche=0, expert=0, canonique=True, N_delta=256, N_codes=256):
+    """A level-0 part; N_delta / N_codes: macro-steps per tile, one value or one per matrix."""
     bl = [np.ascontiguousarray(b, np.uint8) for b in blocs]
     bi = [np.ascontiguousarray(b, np.float32) for b in biais]
     fr = [np.ascontiguousarray(f, np.uint16).reshape(-1) for f in freqs]
@@ -91,12 +106,12 @@ def partie(blocs, biais, freqs, dims: DimsExpert, couche=0, expert=0, canonique=
     pi = (_f32p * 3)(*[_p(a, _f32p) for a in bi])
     pf = (_u16p * 3)(*[_p(a, _u16p) for a in fr])
     u = C.c_uint32()
-    args = (couche, expert, C.byref(dims), pb, pi, pf, int(canonique), N_delta, N_codes)
-    n = _l().trc_codeur_partie(*args, _u8p(), 0, C.byref(u))
+    args = (couche, expert, C.byref(dims), pb, pi, pf, int(canonique), par_matrice(N_delta), par_matrice(N_codes))
+    n = _l().trc_codeur_partie_n(*args, _u8p(), 0, C.byref(u))
     if n == 0:
         _statut(1)
     out = np.zeros(n, np.uint8)
-    _l().trc_codeur_partie(*args, _p(out, _u8p), n, C.byref(u))
+    _l().trc_codeur_partie_n(*args, _p(out, _u8p), n, C.byref(u))
     return out.tobytes(), u.value
 
 
@@ -126,7 +141,8 @@ class CoucheSynthetique:
             n_fils = min(16, os.cpu_count() or 1)
         self.dims = dims
         self.n = n_experts
-        self._h = _l().trc_synth_couche(graine, couche, n_experts, C.byref(dims), N_delta, N_codes, n_fils)
+        self._h = _l().trc_synth_couche_n(graine, couche, n_experts, C.byref(dims), par_matrice(N_delta),
+                                          par_matrice(N_codes), n_fils)
         if not self._h:
             _statut(1)
 

@@ -34,6 +34,7 @@ struct Avance {
     u32x4 dmots;           // DELTA: bytes 16v of its 16-aligned word area (its first 512 bytes)
     uint32_t med0, med1;   // medians of the rows of blocks 4v and 4v + 3 of the CODES tile
     uint32_t rang0;        // the row of block 4v
+    uint32_t med0b, med1b, rang0b;  // the same for blocks 128 + 4v .. of a tile of 32 macro-steps
 };
 
 // 16 bytes at byte `o` of a stream of `n` bytes (f.p 16-aligned), read at an address clamped to the
@@ -48,6 +49,8 @@ __device__ __forceinline__ u32x4 lire16_flux(const uint8_t* p, uint32_t n, uint3
 // load is unconditional, at an index clamped inside its stream (h.T >= 1): no branch surrounds
 // them, so the compiler can count them, and a wait for an earlier load leaves these in flight. A
 // tile past the stream reads the last tile's data, which its half never decodes nor checks.
+// The CODES tile has hc.N = 16 or 32 macro-steps (128 or 256 blocks) and covers DELTA macro-steps
+// hc.N / 16 * t .. (DELTA tile t / N_delta for 16, DELTA tile t for 32 with N_delta = 2).
 template <bool DELTA>
 __device__ __forceinline__ Avance lire_avance(const EnteteRans& hc, const DescFlux& fc, const EnteteRans& hd,
                                               const DescFlux& fd, const uint8_t* med, uint32_t R, const Diviseur& B,
@@ -61,22 +64,28 @@ __device__ __forceinline__ Avance lire_avance(const EnteteRans& hc, const DescFl
     a.xd = L;
     a.dDebut = a.dAttendu = 0;
     a.dmots = u32x4{0u, 0u, 0u, 0u};
-    a.med0 = a.med1 = 0;
-    a.rang0 = 0;
+    a.med0 = a.med1 = a.med0b = a.med1b = 0;
+    a.rang0 = a.rang0b = 0;
     if (DELTA) {
-        const uint32_t tau = t >> (hd.N - 1u);  // t / N_delta, N_delta being 1 or 2
+        const uint32_t moitie = hc.N >> 5;  // 1 for tiles of 32 macro-steps
+        const uint32_t tau = (t << moitie) >> (hd.N - 1u);  // N_delta being 1 or 2
         const TeteTuile td = lire_tete_borne(hd, tau, v);
         a.xd = td.x;
         a.dDebut = td.debut;
         a.dAttendu = td.attendu;
         const uint32_t base_d = uint32_t(reinterpret_cast<const uint8_t*>(hd.mots) - fd.p) + 2u * td.debut;
         a.dmots = lire16_flux(fd.p, fd.longueur, (base_d & ~15u) + 16u * v);
-        const uint32_t bloc0 = 128u * t + 4u * v;
         // B >= 8: block 4v + 3 is in row rang0 or the next one
+        const uint32_t bloc0 = ((128u * t) << moitie) + 4u * v;
         a.rang0 = B.quotient(bloc0);
         const uint32_t rang3 = a.rang0 + (bloc0 + 3u - a.rang0 * B.d >= B.d ? 1u : 0u);
         a.med0 = uint32_t(glob<uint8_t>(med)[min(a.rang0, R - 1u)]);
         a.med1 = uint32_t(glob<uint8_t>(med)[min(rang3, R - 1u)]);
+        const uint32_t bloc0b = bloc0 + (moitie << 7);
+        a.rang0b = B.quotient(bloc0b);
+        const uint32_t rang3b = a.rang0b + (bloc0b + 3u - a.rang0b * B.d >= B.d ? 1u : 0u);
+        a.med0b = uint32_t(glob<uint8_t>(med)[min(a.rang0b, R - 1u)]);
+        a.med1b = uint32_t(glob<uint8_t>(med)[min(rang3b, R - 1u)]);
     }
     return a;
 }
@@ -127,23 +136,24 @@ struct EntreesLane {
                  // or below 2^-60)
 };
 
-// The 4 block entries of lane v (blocks 4v .. 4v + 3 of CODES tile t) from its 4 delta bytes,
-// computed on packed bytes (byte k for block 4v + k) and gathered with byte permutes, no branch
+// The 4 block entries of lane v (blocks 4v .. 4v + 3 of a 128-block half of a CODES tile) from its
+// 4 delta bytes, computed on packed bytes (byte k for block 4v + k) and gathered with byte permutes, no branch
 // outside the stream's last tile:
 //   e       = (med + delta - 128) mod 256, i.e. (med + delta) mod 256 with bit 7 flipped, added
-//             byte-wise without carries between bytes, med being the median of row rang0 up to
-//             the row's end and of the next row after it (B >= 8: one row change at most);
+//             byte-wise without carries between bytes, med being med0 (the median of row rang0,
+//             block 4v's) up to the row's end and med1 after it (B >= 8: one row change at most);
 //   kappa   = 0 below 128, 1 at 128, 2 above (bit 7 of delta, and an exact byte-wise zero test of
 //             delta ^ 0x80);
 //   column  = (4v + k - row start) per byte, the row start a byte-wise zero test of it.
 // Byte k of the four packed values is entry k shifted right by 7: [column, kappa, e, row start].
-__device__ __forceinline__ EntreesLane entrees_de_delta(uint32_t mot, const Avance& a, uint32_t bloc0, uint32_t nblocs,
-                                                        const Diviseur& divB, uint32_t masque_ligne) {
+__device__ __forceinline__ EntreesLane entrees_de_delta(uint32_t mot, uint32_t med0, uint32_t med1, uint32_t rang0,
+                                                        uint32_t bloc0, uint32_t nblocs, const Diviseur& divB,
+                                                        uint32_t masque_ligne) {
     const uint32_t B = divB.d;
-    const uint32_t col0 = bloc0 - a.rang0 * B;
+    const uint32_t col0 = bloc0 - rang0 * B;
     const uint32_t reste = B - col0;  // blocks left in the row from block 4v (>= 1)
     const uint32_t apres = reste >= 4u ? 0u : (0xFFFFFFFFu << (8u * reste));  // bytes k >= reste
-    const uint32_t medp = __builtin_amdgcn_perm(a.med1, a.med0, apres & 0x04040404u);
+    const uint32_t medp = __builtin_amdgcn_perm(med1, med0, apres & 0x04040404u);
     uint32_t ee = ((medp & 0x7F7F7F7Fu) + (mot & 0x7F7F7F7Fu)) ^ ((medp ^ mot) & 0x80808080u) ^ 0x80808080u;
     const uint32_t vd = mot ^ 0x80808080u;
     const uint32_t nul = ~(((vd & 0x7F7F7F7Fu) + 0x7F7F7F7Fu) | vd | 0x7F7F7F7Fu);  // bit 7: delta byte == 128
@@ -192,8 +202,9 @@ struct PrepCodes {
 __device__ __forceinline__ PrepCodes preparer_codes(const Tache& tc, const MatricePartie& m) {
     const uint32_t B = tc.colonnes / 32u;
     PrepCodes p;
-    p.bon = m.bon != 0 && tc.colonnes % 32u == 0 && B >= 8u && tc.lignes > 0 && m.cN == 16u &&
-            (m.dN == 1u || m.dN == 2u) && (B - 1u) / (8u * m.cN) + 2u <= tc.kmax;
+    p.bon = m.bon != 0 && tc.colonnes % 32u == 0 && B >= 8u && tc.lignes > 0 &&
+            ((m.cN == 16u && (m.dN == 1u || m.dN == 2u)) || (m.cN == 32u && m.dN == 2u)) &&
+            (B - 1u) / (8u * m.cN) + 2u <= tc.kmax;
     p.fc = m.codes;
     p.fd = m.delta;
     p.hc = entete_de(m.codes, m.cP, m.cN, m.cT, m.cW);
@@ -219,8 +230,17 @@ __device__ __forceinline__ Avance premiere_avance(const PrepCodes& p, uint32_t R
 // before its first DELTA step (which reads that copy: an LDS read where the device-memory LUT would
 // cost an L2 round trip per step, all waves waiting at once), and a second one before its first
 // entries overwrite it. Later tiles read the DELTA LUT from device memory through the caches.
-__device__ __forceinline__ void corps_codes(const Tache& tc, const PrepCodes& p, uint8_t* lds, const uint32_t* lutd_,
-                                            uint32_t* __restrict__ controle, const Avance& avance0, const Grille& g) {
+// NC: macro-steps per CODES tile, 16 (DELTA tiles of 1 or 2) or 32 (DELTA tiles of 2: CODES tile t
+// is DELTA tile t). A tile of 32 keeps 128 entries in LDS like one of 16: the entries of its
+// second 128 blocks are built with the first ones, held in registers, and written over slots that
+// the tile has passed (lanes 0-15 at macro-step 8 for macro-steps 16-23, lanes 16-31 at
+// macro-step 16 for 24-31); entry slot s serves macro-steps s and s + 16.
+template <uint32_t NC>
+__device__ __forceinline__ void corps_codes_n(const Tache& tc, const PrepCodes& p, uint8_t* lds,
+                                              const uint32_t* lutd_, uint32_t* __restrict__ controle,
+                                              const Avance& avance0, const Grille& g) {
+    static_assert(NC == 16u || NC == 32u, "CODES tiles of 16 or 32 macro-steps");
+    constexpr uint32_t BPT = 8u * NC;  // blocks per CODES tile
     const EnteteRans& h = p.hc;
     const EnteteRans& hd = p.hd;
     const uint32_t R = tc.lignes, B = tc.colonnes / 32u, nblocs = R * B;
@@ -254,7 +274,7 @@ __device__ __forceinline__ void corps_codes(const Tache& tc, const PrepCodes& p,
     // the row-start bytes that count for `ligne`: all but the tile's own first block (lane 0, byte 0)
     const uint32_t masque_ligne = v == 0u ? 0x01010100u : 0x01010101u;
     // Issue priority by progress: a wavefront decodes its first tile pair at priority 3, then 2 from
-    // the pair's ninth macro-step, its second pair at 1 and then 0, so that on a SIMD the wavefronts
+    // the pair's middle macro-step, its second pair at 1 and then 0, so that on a SIMD the wavefronts
     // that are behind are issued ahead of those further on: their ends come closer together, and the
     // launch's tail (the last wavefronts running alone on their SIMDs) gets shorter.
     uint32_t paire_n = 0;
@@ -268,10 +288,11 @@ __device__ __forceinline__ void corps_codes(const Tache& tc, const PrepCodes& p,
         const uint32_t m0 = (tuile ? t : t0) * hN;
         const Avance cur = av;
 
-        // 1. DELTA: the half's DELTA tile from its start to macro-step t mod N_delta (DELTA tile
-        // t / N_delta covers CODES tiles t - t mod N_delta ..), words from the ring
-        const uint32_t saut = t & (dN - 1u);   // DELTA macro-steps before this tile's (N_delta 1 or 2)
-        const uint32_t saut_max = uniforme32(dN == 1u ? 0u : 1u);
+        // 1. DELTA. NC = 16: the half's DELTA tile from its start to macro-step t mod N_delta (DELTA
+        // tile t / N_delta covers CODES tiles t - t mod N_delta ..). NC = 32: DELTA tile t, both
+        // macro-steps. Words from the ring.
+        const uint32_t saut = NC == 32u ? 1u : (t & (dN - 1u));  // last DELTA macro-step needed
+        const uint32_t saut_max = NC == 32u ? 1u : uniforme32(dN == 1u ? 0u : 1u);
         ecrire_lds<u32x4>(a_anneau + 16u * v, cur.dmots);
         {
             // two DELTA macro-steps can read up to 512 + 15 bytes: when the DELTA tile's words pass
@@ -286,18 +307,25 @@ __device__ __forceinline__ void corps_codes(const Tache& tc, const PrepCodes& p,
             }
         }
         if (premiere) barriere_lds();  // the staged LUTs and x are visible
-        uint32_t xd = cur.xd, od = ((mots_d + 2u * cur.dDebut) & 15u), mot = 0;
+        const uint32_t tau = NC == 32u ? t : (t >> (dN - 1u));
+        const uint32_t nbd = tau < dT ? min(dN, nmacro_d - tau * dN) : 0u;  // macro-steps of DELTA tile tau
+        uint32_t xd = cur.xd, od = ((mots_d + 2u * cur.dDebut) & 15u), mot = 0, mot_b = 0;
         auto delta = [&](auto en_lds) {
             constexpr bool EN_LDS = decltype(en_lds)::value;
             for (uint32_t md = 0; md <= saut_max; ++md) {
-                const bool actif = tuile && md <= saut;
+                const bool actif = tuile && md <= saut && md < nbd;
                 uint32_t compte = 0, m4 = 0;
 #pragma unroll
                 for (uint32_t k = 0; k < 4; ++k)
                     m4 |= pas_delta<false, EN_LDS>(xd, od, compte, lutd, a_lutd, a_anneau, decal, masque_inf, actif)
                           << (8u * k);
                 od += 2u * compte;
-                if (md == saut) mot = m4;
+                if (NC == 32u) {
+                    if (md == 0u) mot = m4;
+                    else mot_b = m4;
+                } else if (md == saut) {
+                    mot = m4;
+                }
             }
         };
         if (premiere)  // wave-uniform
@@ -309,21 +337,32 @@ __device__ __forceinline__ void corps_codes(const Tache& tc, const PrepCodes& p,
             premiere = false;
         }
         // the DELTA tile's end checks, by the half that decoded its last macro-step
-        const uint32_t tau = t >> (dN - 1u);
-        const uint32_t nbd = tau < dT ? min(dN, nmacro_d - tau * dN) : 0u;
-        if (tuile && saut + 1u == nbd) {
+        if (tuile && (NC == 32u ? nbd > 0u : saut + 1u == nbd)) {
             hors_l += (xd != L) ? 1u : 0u;
             pointeur += (v == 0 && cur.dDebut + (od - ((mots_d + 2u * cur.dDebut) & 15u)) / 2u != cur.dAttendu) ? 1u : 0u;
         }
-        // 2. the tile's 128 block entries, which macro-steps start a row (macro-step m covers the
-        // blocks of lanes 2m and 2m + 1: bit 2m of `lignes_m`), and whether the wavefront's two
-        // tiles take the block scale inside the conversion
-        const EntreesLane el = entrees_de_delta(mot, cur, 128u * t + 4u * v, nblocs, p.B, masque_ligne);
+        // 2. the tile's block entries, which macro-steps start a row (macro-step m covers the
+        // blocks of lanes 2m and 2m + 1: bit 2m of `lignes_m`, bit 2(m - 16) of `lignes_mb`), and
+        // whether the wavefront's two tiles take the block scale inside the conversion
+        const EntreesLane el = entrees_de_delta(mot, cur.med0, cur.med1, cur.rang0, BPT * t + 4u * v, nblocs, p.B,
+                                                masque_ligne);
         if (tuile) ecrire_lds<u32x4>(a_ent + 16u * v, el.s);
         const uint64_t vl = __builtin_amdgcn_ballot_w64(tuile && el.ligne);
         uint32_t lignes_m = uint32_t(vl) | uint32_t(vl >> 32);
         lignes_m = (lignes_m | (lignes_m >> 1)) & 0x55555555u;
-        const bool ech = __builtin_amdgcn_ballot_w64(tuile && !el.ech) == 0;
+        bool ech_v = el.ech;
+        u32x4 ent_b = u32x4{ENTC_BOURRAGE, ENTC_BOURRAGE, ENTC_BOURRAGE, ENTC_BOURRAGE};
+        uint32_t lignes_mb = 0;
+        if (NC == 32u) {
+            const EntreesLane eb = entrees_de_delta(mot_b, cur.med0b, cur.med1b, cur.rang0b, BPT * t + 128u + 4u * v,
+                                                    nblocs, p.B, 0x01010101u);
+            ent_b = eb.s;
+            const uint64_t vb = __builtin_amdgcn_ballot_w64(tuile && eb.ligne);
+            lignes_mb = uint32_t(vb) | uint32_t(vb >> 32);
+            lignes_mb = (lignes_mb | (lignes_mb >> 1)) & 0x55555555u;
+            ech_v = ech_v && eb.ech;
+        }
+        const bool ech = __builtin_amdgcn_ballot_w64(tuile && !ech_v) == 0;
         // 3. the CODES words over the DELTA ones, and the next pair's streams read ahead
         ecrire_lds<u32x4>(a_anneau + 16u * v, cur.mots0);
         ecrire_lds<u32x4>(a_anneau + 512u + 16u * v, cur.mots1);
@@ -345,7 +384,7 @@ __device__ __forceinline__ void corps_codes(const Tache& tc, const PrepCodes& p,
         const uint32_t debut = cur.tete.debut, attendu = cur.tete.attendu;
         const uint32_t o0 = a.o2;
         uint32_t rho = p.B.quotient(m0 * 8u);
-        const uint32_t rho0 = rho, case0 = t - (rho0 * B) / 128u;  // first tile of row rho0 (128 blocks per tile)
+        const uint32_t rho0 = rho, case0 = t - (rho0 * B) / BPT;  // first tile of row rho0
         auto ecrire = [&](float s) { partiels[rho * kmax + (rho == rho0 ? case0 : 0u)] = s; };
         uint32_t ent_suiv = tuile ? lire_lds<uint32_t>(a_ent_q) : ENTC_BOURRAGE;
         const uint32_t nb_min = min(nb_a, nb_b);
@@ -357,6 +396,10 @@ __device__ __forceinline__ void corps_codes(const Tache& tc, const PrepCodes& p,
             constexpr bool TOUS = decltype(tous)::value;
             constexpr bool ECH = decltype(echelle)::value;
             constexpr bool CONNUE = decltype(connue)::value;
+            if (NC == 32u && (m == 8u || m == 16u)) {
+                // the second 128 blocks' entries over the slots this tile has passed (wave-uniform test)
+                if ((v < 16u) == (m == 8u) && tuile) ecrire_lds<u32x4>(a_ent + 16u * v, ent_b);
+            }
             const bool actif = TOUS || m < nb;
             const uint32_t ent = actif ? ent_suiv : ENTC_BOURRAGE;
             const uint32_t ax = (ent & ENT_X) | a_x;
@@ -418,15 +461,19 @@ __device__ __forceinline__ void corps_codes(const Tache& tc, const PrepCodes& p,
             else
                 __builtin_amdgcn_s_setprio(0);
         };
-        if (nb_min == 16u) {
-            // both tiles whole (wave-uniform): 16 macro-steps unrolled, the row starts known from
-            // the entries (a scalar test per macro-step), entry reads at constant offsets
+        // bit 2m of the row-start masks: macro-step m of the first 16 in lignes_m, of the next in lignes_mb
+        const auto ligne_en = [&](uint32_t m) {
+            return (((m < 16u ? lignes_m : lignes_mb) >> (2u * (m & 15u))) & 1u) != 0u;
+        };
+        if (nb_min == NC) {
+            // both tiles whole (wave-uniform): macro-steps in pairs, the row starts known from the
+            // entries (a scalar test per macro-step)
             auto tour = [&](auto echelle) {
 #pragma unroll 1
-                for (uint32_t mm = 0; mm < 16u; mm += 2u) {
-                    if (mm == 8u) prio_milieu();
-                    macro(std::true_type{}, echelle, std::true_type{}, mm, ((lignes_m >> (2u * mm)) & 1u) != 0u);
-                    macro(std::true_type{}, echelle, std::true_type{}, mm + 1u, ((lignes_m >> (2u * mm + 2u)) & 1u) != 0u);
+                for (uint32_t mm = 0; mm < NC; mm += 2u) {
+                    if (mm == NC / 2u) prio_milieu();
+                    macro(std::true_type{}, echelle, std::true_type{}, mm, ligne_en(mm));
+                    macro(std::true_type{}, echelle, std::true_type{}, mm + 1u, ligne_en(mm + 1u));
                 }
             };
             if (ech)
@@ -436,7 +483,7 @@ __device__ __forceinline__ void corps_codes(const Tache& tc, const PrepCodes& p,
         } else {
             uint32_t m = 0;
             for (; m + 1u < nb_min; m += 2u) {
-                if (m == 8u) prio_milieu();
+                if (m == NC / 2u) prio_milieu();
                 macro(std::true_type{}, std::false_type{}, std::false_type{}, m, false);
                 macro(std::true_type{}, std::false_type{}, std::false_type{}, m + 1u, false);
             }
@@ -460,6 +507,15 @@ __device__ __forceinline__ void corps_codes(const Tache& tc, const PrepCodes& p,
         barriere_lds();
     }
     verser_controle(controle, hors_l, pointeur);
+}
+
+// The CODES pass for the job's tile length (uniform over the block: one matrix per block).
+__device__ __forceinline__ void corps_codes(const Tache& tc, const PrepCodes& p, uint8_t* lds, const uint32_t* lutd_,
+                                            uint32_t* __restrict__ controle, const Avance& avance0, const Grille& g) {
+    if (uniforme32(p.hc.N) == 32u)
+        corps_codes_n<32>(tc, p, lds, lutd_, controle, avance0, g);
+    else
+        corps_codes_n<16>(tc, p, lds, lutd_, controle, avance0, g);
 }
 
 }  // namespace trc

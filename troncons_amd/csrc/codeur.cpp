@@ -394,12 +394,30 @@ int trc_codeur_tables(const uint8_t* const* blocs17, uint32_t n_experts, uint32_
 
 // One level-0 part of an expert (3 matrices). Returns the part length (multiple of 4096) and
 // writes it to `out` when cap suffices; 0 on error.
+namespace {
+bool n_valides(const uint32_t* N_delta, const uint32_t* N_codes) {
+    if (N_delta == nullptr || N_codes == nullptr) return false;
+    for (int j = 0; j < 3; ++j)
+        if (N_delta[j] == 0 || N_codes[j] == 0 || N_delta[j] > 65535 || N_codes[j] > 65535) return false;
+    return true;
+}
+}  // namespace
+
 uint64_t trc_codeur_partie(uint16_t couche, uint16_t expert, const trc_dims_expert* dims,
                            const uint8_t* const* blocs17, const float* const* biais, const uint16_t* const* freqs4,
                            int canon, uint32_t N_delta, uint32_t N_codes, uint8_t* out, uint64_t cap,
                            uint32_t* utiles) {
-    if (dims == nullptr || trc_dims_verifier(dims) != TRC_OK || N_delta == 0 || N_codes == 0 || N_delta > 65535 ||
-        N_codes > 65535) {
+    const uint32_t nd[3] = {N_delta, N_delta, N_delta}, nc[3] = {N_codes, N_codes, N_codes};
+    return trc_codeur_partie_n(couche, expert, dims, blocs17, biais, freqs4, canon, nd, nc, out, cap, utiles);
+}
+
+// The same with the tile lengths of each matrix j (N_delta[j], N_codes[j]): the format stores N per
+// stream (decisions/ARCHITECTURE.md:581), so a part may mix them.
+uint64_t trc_codeur_partie_n(uint16_t couche, uint16_t expert, const trc_dims_expert* dims,
+                             const uint8_t* const* blocs17, const float* const* biais, const uint16_t* const* freqs4,
+                             int canon, const uint32_t* N_delta, const uint32_t* N_codes, uint8_t* out, uint64_t cap,
+                             uint32_t* utiles) {
+    if (dims == nullptr || trc_dims_verifier(dims) != TRC_OK || !n_valides(N_delta, N_codes)) {
         trc::usage("dimensions ou N faux");
         return 0;
     }
@@ -407,7 +425,7 @@ uint64_t trc_codeur_partie(uint16_t couche, uint16_t expert, const trc_dims_expe
     for (uint8_t j = 0; j < 3; ++j) {
         Prepa p;
         preparer(blocs17[j], dims->lignes[j], dims->colonnes[j] / 32, canon != 0, p);
-        if (!coder_matrice(p, dims->lignes[j], biais[j], freqs4[j], j, N_delta, N_codes, flux)) {
+        if (!coder_matrice(p, dims->lignes[j], biais[j], freqs4[j], j, N_delta[j], N_codes[j], flux)) {
             trc::usage("symbole absent de sa table (matrice %u)", j);
             return 0;
         }
@@ -423,7 +441,15 @@ uint64_t trc_codeur_partie(uint16_t couche, uint16_t expert, const trc_dims_expe
 // all of them (pass 1), parts coded with those tables (pass 2), n_fils threads.
 trc_couche_synth* trc_synth_couche(uint64_t graine, uint32_t couche, uint32_t n_experts, const trc_dims_expert* dims,
                                    uint32_t N_delta, uint32_t N_codes, uint32_t n_fils) {
-    if (dims == nullptr || n_experts == 0 || trc_dims_verifier(dims) != TRC_OK) {
+    const uint32_t nd[3] = {N_delta, N_delta, N_delta}, nc[3] = {N_codes, N_codes, N_codes};
+    return trc_synth_couche_n(graine, couche, n_experts, dims, nd, nc, n_fils);
+}
+
+// The same with per-matrix tile lengths.
+trc_couche_synth* trc_synth_couche_n(uint64_t graine, uint32_t couche, uint32_t n_experts,
+                                     const trc_dims_expert* dims, const uint32_t* N_delta, const uint32_t* N_codes,
+                                     uint32_t n_fils) {
+    if (dims == nullptr || n_experts == 0 || trc_dims_verifier(dims) != TRC_OK || !n_valides(N_delta, N_codes)) {
         trc::usage("couche synthetique : arguments faux");
         return nullptr;
     }
@@ -490,7 +516,8 @@ trc_couche_synth* trc_synth_couche(uint64_t graine, uint32_t couche, uint32_t n_
         for (uint8_t j = 0; j < 3; ++j) {
             Prepa p;
             preparer(pb[j], dims->lignes[j], B[j], true, p);
-            if (!coder_matrice(p, dims->lignes[j], pi[j], &c->freqs[j][0][0], j, N_delta, N_codes, flux)) echec = true;
+            if (!coder_matrice(p, dims->lignes[j], pi[j], &c->freqs[j][0][0], j, N_delta[j], N_codes[j], flux))
+                echec = true;
         }
         uint32_t u = 0;
         c->parties[e] = assembler(uint16_t(couche), uint16_t(e), 3, flux, u);

@@ -36,6 +36,7 @@
 #include "selection.hpp"
 #include "norme.hpp"
 #include "passe.hpp"
+#include "scratch.hpp"
 
 
 // The layer's LUTs u32[3][4][4096] (reference format) are shared by all jobs of a launch. A
@@ -332,8 +333,8 @@ __device__ __forceinline__ void codes_bloc(const trc::Taches& taches, const uint
     if (SW) {
         const MatricePartie mg = lire_matrice_constante(tg.matrice), mu = lire_matrice_constante(tu.matrice);
         const uint32_t Bg = tg.colonnes / 32u;
-        sw_bon = mg.bon != 0 && mu.bon != 0 && mg.cN == 16u && mu.cN == 16u && Bg >= 8u &&
-                 (Bg - 1u) / 128u + 2u <= tg.kmax && tg.lignes >= R_sw && tu.lignes >= R_sw;
+        sw_bon = mg.bon != 0 && mu.bon != 0 && (mg.cN == 16u || mg.cN == 32u) && mu.cN == mg.cN && Bg >= 8u &&
+                 (Bg - 1u) / (8u * mg.cN) + 2u <= tg.kmax && tg.lignes >= R_sw && tu.lignes >= R_sw;
         sw_bpt = 8u * mg.cN;
     }
     const Avance avance0 = premiere_avance<true>(p, tc.lignes, g);
@@ -645,9 +646,12 @@ uint64_t pas_tache(uint32_t R, uint32_t C, uint32_t n_codes) {
 }
 
 // The CODES pass decodes each tile's DELTA itself (fusion_codes, codes.hpp) for streams of 16
-// macro-steps per CODES tile and 1 or 2 per DELTA tile: no DELTA launch, no block entries. Other
-// tile lengths take the DELTA pass, whose block entries go through the workspace.
-bool delta_interne(uint32_t n_delta, uint32_t n_codes) { return n_codes == 16 && (n_delta == 1 || n_delta == 2); }
+// macro-steps per CODES tile and 1 or 2 per DELTA tile, or 32 and 2: no DELTA launch, no block
+// entries. In that plan each matrix may take either form (the kernels read N from its streams).
+// Other tile lengths take the DELTA pass, whose block entries go through the workspace.
+bool delta_interne(uint32_t n_delta, uint32_t n_codes) {
+    return (n_codes == 16 && (n_delta == 1 || n_delta == 2)) || (n_codes == 32 && n_delta == 2);
+}
 
 // Workspace piece of one matrix job in the internal-DELTA mode: its partial sums only.
 uint64_t pas_tache_interne(uint32_t R, uint32_t C) { return al(4ull * R * kmax_pour(C, 16)); }
@@ -1052,16 +1056,8 @@ __device__ __align__(256) uint8_t scratch[OCTETS_SCRATCH];
 std::mutex verrou_scratch;
 void* adresse_scratch[CARTES_MAX] = {};
 
-// The device address of `scratch` on the device of `flux`, taken once per device.
-int scratch_de(void* flux, void** adresse) {
-    int d = -1;
-    hipDevice_t dh = 0;
-    if (flux != nullptr && hipStreamGetDevice(reinterpret_cast<hipStream_t>(flux), &dh) == hipSuccess) {
-        d = int(dh);
-    } else {
-        const hipError_t e = hipGetDevice(&d);
-        if (e != hipSuccess) return trc::erreur_hip("hipGetDevice", e);
-    }
+// The device address of `scratch` on device d, taken once (with d current) and kept.
+int resoudre_scratch(int d, void** adresse) {
     if (d < 0 || d >= CARTES_MAX) return usage("carte %d hors des %d que la memoire statique couvre", d, CARTES_MAX);
     std::lock_guard<std::mutex> g(verrou_scratch);
     if (adresse_scratch[d] == nullptr) {
@@ -1079,7 +1075,26 @@ int scratch_de(void* flux, void** adresse) {
     *adresse = adresse_scratch[d];
     return TRC_OK;
 }
+
+// The scratch address on the device of `flux` (the current device if flux is null). Resolved by
+// trc_contexte_creer (trc::preparer_scratch) for a context's device, else at this first call.
+int scratch_de(void* flux, void** adresse) {
+    int d = -1;
+    hipDevice_t dh = 0;
+    if (flux != nullptr && hipStreamGetDevice(reinterpret_cast<hipStream_t>(flux), &dh) == hipSuccess) {
+        d = int(dh);
+    } else {
+        const hipError_t e = hipGetDevice(&d);
+        if (e != hipSuccess) return trc::erreur_hip("hipGetDevice", e);
+    }
+    return resoudre_scratch(d, adresse);
+}
 }  // namespace
+
+int trc::preparer_scratch(int carte) {
+    void* p = nullptr;
+    return resoudre_scratch(carte, &p);
+}
 
 extern "C" uint64_t trc_octets_scratch(void) { return OCTETS_SCRATCH; }
 

@@ -16,6 +16,7 @@
 #include <string>
 
 #include "erreurs.hpp"
+#include "scratch.hpp"
 
 struct trc_contexte {
     int ordinal = 0;
@@ -89,6 +90,10 @@ int trc_contexte_creer(uint32_t ordinal, uint32_t attente, trc_contexte** sortie
     // as with the primary context's flags: refused once the device is active, the runtime's stay
     (void)hipSetDeviceFlags(drapeaux_attente(attente));
     (void)hipGetLastError();
+    // the library's per-device set-up: the allocation-free step's scratch address, so that a step
+    // captured into a graph later makes no runtime query of its own
+    const int rs = trc::preparer_scratch(int(ordinal));
+    if (rs != TRC_OK) return rs;
     auto* c = new trc_contexte;
     c->ordinal = int(ordinal);
     unsigned d = 0;
