@@ -400,8 +400,10 @@ uint64_t trc_taille_travail_prefill(const trc_dims_expert* dims, uint32_t expert
  * (the routers' output, debut_couche_pos); residus: f32[positions][D], residus[i] += ((w_i0 s_i0 +
  * w_i1 s_i1) + ...). Each chosen expert is decoded once, into LDS, and applied to all its positions
  * on the bf16 MFMA (MXFP4 weights are exact in bf16; x and the SwiGLU rows are split into exact bf16
- * pieces); CODES_CTX tiles of at most 16 macro-steps (n_codes <= 16), rows of at most 4096 columns.
- * An index >= experts counts one format error and leaves its position alone. */
+ * pieces); rows of at most 4096 columns. Tiles of at most 16 macro-steps (n_codes <= 16) are decoded
+ * band by band straight into LDS; longer ones (the reference encoder's 256) are first decoded once
+ * per chosen expert into a slot of the workspace, from which the bands are copied. An index >=
+ * experts counts one format error and leaves its position alone. */
 int trc_prefill_moe(trc_vue repertoire, uint32_t experts, trc_vue luts, const trc_dims_expert* dims, trc_vue x,
                     uint32_t positions, trc_vue indices, trc_vue poids, uint32_t k, trc_vue residus,
                     trc_vue controle, trc_vue travail, uint32_t n_delta, uint32_t n_codes, void* flux);

@@ -61,10 +61,16 @@ __device__ __forceinline__ void copier_biais(const uint8_t* __restrict__ src, ui
         ecrire_global<uint32_t>(dst + 4u * i, glob<uint32_t>(src)[i]);
 }
 
+// The decoded bytes (byte 3 of each LUT word of a macro-step's four steps) as one word, step k in
+// byte k: two byte permutes and an or.
+__device__ __forceinline__ uint32_t octets_hauts(uint32_t e0, uint32_t e1, uint32_t e2, uint32_t e3) {
+    return __builtin_amdgcn_perm(e1, e0, 0x0c0c0703u) | __builtin_amdgcn_perm(e3, e2, 0x07030c0cu);
+}
+
 template <uint32_t FILS>
 struct LdsEchelles {
     uint2 lut[M];
-    __attribute__((aligned(16))) uint8_t anneaux[(FILS / 32u) * OCTETS_ANNEAU];
+    __attribute__((aligned(OCTETS_ANNEAU))) uint8_t anneaux[(FILS / 32u) * OCTETS_ANNEAU];
     __attribute__((aligned(16))) uint8_t med[MED_LDS_MAX];
 };
 
@@ -92,6 +98,8 @@ __device__ __forceinline__ void echelles_vers_emplacement(const DescFlux& fd, co
     const Diviseur parB = Diviseur::de(B);
     const uint32_t vague = blockIdx.x * (FILS / 64u) + (threadIdx.x >> 6), n_vagues = gridDim.x * (FILS / 64u);
     const uint32_t nmacro = h.P / 128u;
+    const uint32_t a_lut = adresse_lds(&s.lut[0]);
+    const uint32_t a_anneau = adresse_lds(s.anneaux) + d.demi * OCTETS_ANNEAU;
     uint8_t* ech = mat + disp.echelles;
     uint32_t hors_l = 0, pointeur = 0;
     for (uint32_t t0 = 2u * vague; t0 < h.T; t0 += 2u * n_vagues) {
@@ -101,17 +109,23 @@ __device__ __forceinline__ void echelles_vers_emplacement(const DescFlux& fd, co
         const uint32_t nb = tuile ? min(h.N, nmacro - t * h.N) : 0u;
         uint32_t x = tuile ? h.etats[t * VOIES + d.v] : L;
         const uint32_t debut = tuile ? h.debut[t] : 0u;
-        Anneau a = ouvrir_anneau(h, fd, debut, d.demi * OCTETS_ANNEAU, s.anneaux, d.v, tuile);
+        AnneauR a = ouvrir_anneau_r(h, fd, debut, a_anneau, d.v, tuile);
         const uint32_t o0 = a.o2;
-        for (uint32_t m = 0; m < pas_bas; ++m) {
-            const bool actif = m < nb;
-            uint32_t deltas = 0;
-#pragma unroll
-            for (uint32_t k = 0; k < 4; ++k)
-                deltas |= (pas_anneau<false>(x, a, s.lut, s.anneaux, d.decal, d.masque_inf, actif) >> 24) << (8u * k);
-            avancer_anneau(a, s.anneaux, d.v, actif);
+        // macro-steps where both tiles of the wavefront are active take the branch-free step
+        const uint32_t n_tous = t0 + 1u < h.T ? min(pas_bas, min(h.N, nmacro - (t0 + 1u) * h.N)) : 0u;
+        auto macro = [&](auto tous, uint32_t m) {
+            constexpr bool TOUS = decltype(tous)::value;
+            const bool actif = TOUS || m < nb;
+            uint32_t compte = 0;
+            const uint32_t e0 = pas_r<TOUS>(x, a.o2, compte, a_lut, a_anneau, d.decal, d.masque_inf, actif);
+            const uint32_t e1 = pas_r<TOUS>(x, a.o2, compte, a_lut, a_anneau, d.decal, d.masque_inf, actif);
+            const uint32_t e2 = pas_r<TOUS>(x, a.o2, compte, a_lut, a_anneau, d.decal, d.masque_inf, actif);
+            const uint32_t e3 = pas_r<TOUS>(x, a.o2, compte, a_lut, a_anneau, d.decal, d.masque_inf, actif);
+            a.o2 += 2u * compte;
+            avancer_anneau_r(a, d.v, actif);
+            const uint32_t deltas = octets_hauts(e0, e1, e2, e3);
             const uint32_t b0 = 4u * ((t * h.N + m) * VOIES + d.v);
-            if (!actif || b0 >= nblocs) continue;  // stream padding past the last block
+            if (!actif || b0 >= nblocs) return;  // stream padding past the last block
             const uint32_t r0 = parB.quotient(b0), c0 = b0 - r0 * B;
             uint32_t e4 = 0;
 #pragma unroll
@@ -125,7 +139,10 @@ __device__ __forceinline__ void echelles_vers_emplacement(const DescFlux& fd, co
             } else {
                 for (uint32_t k = 0; b0 + k < nblocs; ++k) ech[b0 + k] = uint8_t(e4 >> (8u * k));
             }
-        }
+        };
+        uint32_t m = 0;
+        for (; m < n_tous; ++m) macro(std::true_type{}, m);
+        for (; m < pas_bas; ++m) macro(std::false_type{}, m);
         if (tuile) verifier_tuile(h, t, x, debut, (a.o2 - o0) / 2u, d.v, hors_l, pointeur);
     }
     verser_controle(controle, hors_l, pointeur);
@@ -164,7 +181,7 @@ constexpr uint32_t FILS_CODES_SLOT = FILS_CODES;
 template <uint32_t FILS>
 struct LdsCodesT {
     uint2 lut[3][M];
-    __attribute__((aligned(16))) uint8_t anneaux[(FILS / 32u) * OCTETS_ANNEAU];
+    __attribute__((aligned(OCTETS_ANNEAU))) uint8_t anneaux[(FILS / 32u) * OCTETS_ANNEAU];
     __attribute__((aligned(16))) uint8_t ctx[FILS / 32u][128];
     __attribute__((aligned(16))) uint8_t med[MED_LDS_MAX];
 };
@@ -216,6 +233,8 @@ __device__ __forceinline__ void codes_vers_emplacement(const DescFlux& fc, const
     const uint32_t nmacro = h.P / 128u;
     const uint32_t mots_utiles = 4u * nblocs;
     const uint32_t a_ctx = adresse_lds(&s.ctx[d.demi][0]);
+    const uint32_t a_lut = adresse_lds(&s.lut[0][0]);
+    const uint32_t a_anneau = adresse_lds(s.anneaux) + d.demi * OCTETS_ANNEAU;
     uint32_t* codes = reinterpret_cast<uint32_t*>(mat);
     uint32_t hors_l = 0, pointeur = 0;
     for (uint32_t t0 = 2u * vague; t0 < h.T; t0 += 2u * n_vagues) {
@@ -227,25 +246,32 @@ __device__ __forceinline__ void codes_vers_emplacement(const DescFlux& fc, const
         uint32_t x = tuile ? h.etats[t * VOIES + d.v] : L;
         const uint32_t debut = tuile ? h.debut[t] : 0u;
         uint32_t e_vol = tuile ? lire_echelles4(ech, 8u * g0 + 4u * d.v, nblocs) : 0u;
-        Anneau a = ouvrir_anneau(h, fc, debut, d.demi * OCTETS_ANNEAU, s.anneaux, d.v, tuile);
+        AnneauR a = ouvrir_anneau_r(h, fc, debut, a_anneau, d.v, tuile);
         const uint32_t o0 = a.o2;
-        for (uint32_t m = 0; m < pas_bas; ++m) {
-            const bool actif = m < nb;
+        const uint32_t n_tous = t0 + 1u < h.T ? min(pas_bas, min(h.N, nmacro - (t0 + 1u) * h.N)) : 0u;
+        auto macro = [&](auto tous, uint32_t m) {
+            constexpr bool TOUS = decltype(tous)::value;
+            const bool actif = TOUS || m < nb;
             if ((m & 15u) == 0u) {  // a new group of 16 macro-steps: its contexts into LDS, the next group's scales requested
                 const uint32_t b0 = 8u * (g0 + m) + 4u * d.v;
                 ecrire_lds<uint32_t>(a_ctx + 4u * d.v, actif ? contextes4(e_vol, b0, nblocs, parB, B, med) : 0u);
                 if (m + 16u < nb) e_vol = lire_echelles4(ech, b0 + 128u, nblocs);
             }
             const uint32_t kappa = lire_lds<uint8_t>(a_ctx + 8u * (m & 15u) + (d.v >> 2));
-            const uint2* lt = &s.lut[0][0] + kappa * M;
-            uint32_t mot = 0;
-#pragma unroll
-            for (uint32_t k = 0; k < 4; ++k)
-                mot |= (pas_anneau<false>(x, a, lt, s.anneaux, d.decal, d.masque_inf, actif) >> 24) << (8u * k);
-            avancer_anneau(a, s.anneaux, d.v, actif);
+            const uint32_t lt = a_lut + kappa * (M * 8u);
+            uint32_t compte = 0;
+            const uint32_t e0 = pas_r<TOUS>(x, a.o2, compte, lt, a_anneau, d.decal, d.masque_inf, actif);
+            const uint32_t e1 = pas_r<TOUS>(x, a.o2, compte, lt, a_anneau, d.decal, d.masque_inf, actif);
+            const uint32_t e2 = pas_r<TOUS>(x, a.o2, compte, lt, a_anneau, d.decal, d.masque_inf, actif);
+            const uint32_t e3 = pas_r<TOUS>(x, a.o2, compte, lt, a_anneau, d.decal, d.masque_inf, actif);
+            a.o2 += 2u * compte;
+            avancer_anneau_r(a, d.v, actif);
             const uint32_t w = (g0 + m) * VOIES + d.v;
-            if (actif && w < mots_utiles) ecrire_global<uint32_t>(codes + w, mot);
-        }
+            if (actif && w < mots_utiles) ecrire_global<uint32_t>(codes + w, octets_hauts(e0, e1, e2, e3));
+        };
+        uint32_t m = 0;
+        for (; m < n_tous; ++m) macro(std::true_type{}, m);
+        for (; m < pas_bas; ++m) macro(std::false_type{}, m);
         if (tuile) verifier_tuile(h, t, x, debut, (a.o2 - o0) / 2u, d.v, hors_l, pointeur);
     }
     verser_controle(controle, hors_l, pointeur);

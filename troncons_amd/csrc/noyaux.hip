@@ -211,90 +211,93 @@ __device__ __forceinline__ void gemv_mxfp4_demi(const uint8_t* __restrict__ mat,
 }
 
 // The same rows for matrices of at most GEMV_X_COLONNES columns, x staged in LDS once per block of
-// GEMV_X_FILS threads (32 rows: 8 halves x 4), every code and scale load of a lane issued before
-// the block's barrier. A lane's blocks are l, l + 32, l + 64 (B <= 96); the arithmetic of
-// each row is gemv_mxfp4_demi's, so the bits are the same. x lies in LDS as 144 bytes per block
-// (32 f32 and 16 bytes of padding): lane l's reads of its block start 4 banks past lane l - 1's,
-// so each group of 8 lanes covers the 32 banks once. The scales of a half's rows, contiguous in the
-// slot, come in as 4-byte words (4 loads per lane instead of one byte load per row and block: the
-// vector memory unit takes as long over a byte load as over a 16-byte one) and are read back from
-// LDS byte by byte.
-constexpr uint32_t GEMV_X_FILS = 256;
-constexpr uint32_t GEMV_X_PAR_DEMI = 4;                                // rows per half-wavefront
-constexpr uint32_t GEMV_X_BLOCS = 3;                                   // blocks per lane at most
-constexpr uint32_t GEMV_X_COLONNES = 32u * 32u * GEMV_X_BLOCS;         // 3072
-constexpr uint32_t GEMV_X_PAS = 144;                                   // LDS bytes per block of x
-constexpr uint32_t GEMV_X_LIGNES = (GEMV_X_FILS / 32u) * GEMV_X_PAR_DEMI;  // 32 rows per block
-constexpr uint32_t GEMV_X_ECH_DEMI = 4u * (GEMV_X_PAR_DEMI * 32u * GEMV_X_BLOCS / 4u + 1u);  // scale bytes per half
-constexpr uint32_t GEMV_X_LDS = (GEMV_X_COLONNES / 32u) * GEMV_X_PAS + (GEMV_X_FILS / 32u) * GEMV_X_ECH_DEMI;
+// FILS threads (FILS / 32 halves of PD rows each), every code and scale load of a lane issued
+// before the block's barrier. A lane's blocks are l, l + 32, l + 64 (B <= 96); the arithmetic of
+// each row is gemv_mxfp4_demi's, so the bits are the same whatever the block shape. x lies in LDS
+// as 144 bytes per block (32 f32 and 16 bytes of padding): lane l's reads of its block start 4
+// banks past lane l - 1's, so each group of 8 lanes covers the 32 banks once. The scales of a
+// half's rows, contiguous in the slot, come in as 4-byte words (the vector memory unit takes as
+// long over a byte load as over a 16-byte one) and are read back from LDS byte by byte.
+constexpr uint32_t GEMV_X_BLOCS = 3;                            // blocks per lane at most
+constexpr uint32_t GEMV_X_COLONNES = 32u * 32u * GEMV_X_BLOCS;  // 3072
+constexpr uint32_t GEMV_X_PAS = 144;                            // LDS bytes per block of x
 
-template <uint32_t NB>  // blocks per lane: ceil(B / 32)
+template <uint32_t FILS, uint32_t PD>  // threads per block, rows per half-wavefront
+struct FormeGemvX {
+    static constexpr uint32_t DEMIS = FILS / 32u;
+    static constexpr uint32_t LIGNES = DEMIS * PD;                              // rows per block
+    static constexpr uint32_t MOTS_ECH = PD * 32u * GEMV_X_BLOCS / 4u + 1u;     // scale words per half
+    static constexpr uint32_t ECH_DEMI = 4u * MOTS_ECH;
+    static constexpr uint32_t NE = (MOTS_ECH + 31u) / 32u;                     // scale words per lane
+    static constexpr uint32_t NX = (GEMV_X_COLONNES / 4u + FILS - 1u) / FILS;  // float4 of x per thread
+    static constexpr uint32_t LDS = (GEMV_X_COLONNES / 32u) * GEMV_X_PAS + DEMIS * ECH_DEMI;
+};
+
+template <uint32_t FILS, uint32_t PD, uint32_t NB>  // NB: blocks per lane, ceil(B / 32)
 __device__ __forceinline__ void gemv_mxfp4_x_lds_n(const uint8_t* __restrict__ mat, const float* __restrict__ x,
                                                    float* __restrict__ y, uint32_t R, uint32_t C, uint32_t r_bloc,
                                                    uint8_t* __restrict__ xl) {
+    using F = FormeGemvX<FILS, PD>;
     const uint32_t B = C / 32u;
     const uint32_t l = threadIdx.x & 31u;
-    const uint32_t r0 = r_bloc + (threadIdx.x >> 5) * GEMV_X_PAR_DEMI;
+    const uint32_t r0 = r_bloc + (threadIdx.x >> 5) * PD;
     const trc_disposition d = disposition_matrice(R, C);
     const gptr<u32x4> codes = glob<u32x4>(mat);
     const gptr<uint32_t> ech32 = glob<uint32_t>(mat + d.echelles);  // 256-aligned region of R * B bytes
     const gptr<f32x4> x4 = glob<f32x4>(x);
     // x first, then the scale words: the waits before their LDS stores leave the code loads, issued
     // after them, in flight
-    constexpr uint32_t NX = (GEMV_X_COLONNES / 4u + GEMV_X_FILS - 1u) / GEMV_X_FILS;  // float4 of x per thread
-    f32x4 xv[NX];
+    f32x4 xv[F::NX];
 #pragma unroll
-    for (uint32_t k = 0; k < NX; ++k) xv[k] = x4[min(threadIdx.x + k * GEMV_X_FILS, C / 4u - 1u)];
-    // the half's scale bytes [r0 B, (r0 + 4) B) as the words from the one holding byte r0 B
-    constexpr uint32_t NE = GEMV_X_ECH_DEMI / 4u / 32u + 1u;  // scale words per lane
+    for (uint32_t k = 0; k < F::NX; ++k) xv[k] = x4[min(threadIdx.x + k * FILS, C / 4u - 1u)];
+    // the half's scale bytes [r0 B, (r0 + PD) B) as the words from the one holding byte r0 B
     const uint32_t o0 = r0 * B, a0 = o0 >> 2, dernier_mot = (R * B + 3u) / 4u - 1u;
-    uint32_t ev[NE];
+    uint32_t ev[F::NE];
 #pragma unroll
-    for (uint32_t k = 0; k < NE; ++k) ev[k] = ech32[min(a0 + l + 32u * k, dernier_mot)];
-    u32x4 q[GEMV_X_PAR_DEMI][NB];
+    for (uint32_t k = 0; k < F::NE; ++k) ev[k] = ech32[min(a0 + l + 32u * k, dernier_mot)];
+    u32x4 q[PD][NB];
     // block by block, so that the arithmetic of a lane's first block waits for its loads only
     // (vector memory completes in order)
 #pragma unroll
     for (uint32_t j = 0; j < NB; ++j) {
         const uint32_t b = min(l + 32u * j, B - 1u);  // past B: a block reloaded, never used
 #pragma unroll
-        for (uint32_t i = 0; i < GEMV_X_PAR_DEMI; ++i) q[i][j] = codes[uint64_t(min(r0 + i, R - 1u)) * B + b];
+        for (uint32_t i = 0; i < PD; ++i) q[i][j] = codes[uint64_t(min(r0 + i, R - 1u)) * B + b];
     }
 #pragma unroll
-    for (uint32_t k = 0; k < NX; ++k) {
-        const uint32_t g = threadIdx.x + k * GEMV_X_FILS;  // float4 g: block g / 8, quarter g % 8
+    for (uint32_t k = 0; k < F::NX; ++k) {
+        const uint32_t g = threadIdx.x + k * FILS;  // float4 g: block g / 8, quarter g % 8
         if (g < C / 4u) *reinterpret_cast<f32x4*>(xl + (g >> 3) * GEMV_X_PAS + 16u * (g & 7u)) = xv[k];
     }
-    uint8_t* el = xl + (GEMV_X_COLONNES / 32u) * GEMV_X_PAS + (threadIdx.x >> 5) * GEMV_X_ECH_DEMI;
+    uint8_t* el = xl + (GEMV_X_COLONNES / 32u) * GEMV_X_PAS + (threadIdx.x >> 5) * F::ECH_DEMI;
 #pragma unroll
-    for (uint32_t k = 0; k < NE; ++k)
-        if (4u * (l + 32u * k) < GEMV_X_ECH_DEMI) *reinterpret_cast<uint32_t*>(el + 4u * (l + 32u * k)) = ev[k];
+    for (uint32_t k = 0; k < F::NE; ++k)
+        if (4u * (l + 32u * k) < F::ECH_DEMI) *reinterpret_cast<uint32_t*>(el + 4u * (l + 32u * k)) = ev[k];
     __syncthreads();
     // scale of row i, block b: byte (o0 & 3) + i B + b of the half's words (rows past R: unused)
     const uint8_t* el_r = el + (o0 & 3u);
-    float acc[GEMV_X_PAR_DEMI] = {};
+    float acc[PD] = {};
 #pragma unroll
     for (uint32_t j = 0; j < NB; ++j) {
         const uint32_t b = l + 32u * j;
         if (b < B) {
             // word by word (x values 4t .. 4t + 3 and 16 + 4t ..): each row's chain keeps
             // chaine_bloc's order, and only two float4 of x are live at a time
-            float p[GEMV_X_PAR_DEMI] = {};
+            float p[PD] = {};
 #pragma unroll
             for (uint32_t t = 0; t < 4; ++t) {
                 const f32x4 xa = *reinterpret_cast<const f32x4*>(xl + b * GEMV_X_PAS + 16u * t);
                 const f32x4 xb = *reinterpret_cast<const f32x4*>(xl + b * GEMV_X_PAS + 64u + 16u * t);
 #pragma unroll
-                for (uint32_t i = 0; i < GEMV_X_PAR_DEMI; ++i) p[i] = chaine_mot(q[i][j][t], xa, xb, p[i]);
+                for (uint32_t i = 0; i < PD; ++i) p[i] = chaine_mot(q[i][j][t], xa, xb, p[i]);
             }
 #pragma unroll
-            for (uint32_t i = 0; i < GEMV_X_PAR_DEMI; ++i)
-                acc[i] = fmaf(echelle_e8m0(el_r[i * B + b]), p[i], acc[i]);
+            for (uint32_t i = 0; i < PD; ++i) acc[i] = fmaf(echelle_e8m0(el_r[i * B + b]), p[i], acc[i]);
         }
     }
     const gptr<float> biais = glob<float>(mat + d.biais);
 #pragma unroll
-    for (uint32_t i = 0; i < GEMV_X_PAR_DEMI; ++i) {
+    for (uint32_t i = 0; i < PD; ++i) {
         const float s = arbre_32(acc[i]);
         if (l == 0u && r0 + i < R) y[r0 + i] = s + biais[r0 + i];
     }
@@ -302,46 +305,49 @@ __device__ __forceinline__ void gemv_mxfp4_x_lds_n(const uint8_t* __restrict__ m
 
 // gemv_mxfp4_x_lds_n for the matrix's blocks per lane (uniform over the block), so that only the
 // loads a lane can use are held in registers.
+template <uint32_t FILS, uint32_t PD>
 __device__ __forceinline__ void gemv_mxfp4_x_lds(const uint8_t* __restrict__ mat, const float* __restrict__ x,
                                                  float* __restrict__ y, uint32_t R, uint32_t C, uint32_t r_bloc,
                                                  uint8_t* __restrict__ xl) {
     const uint32_t nb = (C / 32u + 31u) / 32u;
     if (nb <= 1u)
-        gemv_mxfp4_x_lds_n<1>(mat, x, y, R, C, r_bloc, xl);
+        gemv_mxfp4_x_lds_n<FILS, PD, 1>(mat, x, y, R, C, r_bloc, xl);
     else if (nb == 2u)
-        gemv_mxfp4_x_lds_n<2>(mat, x, y, R, C, r_bloc, xl);
+        gemv_mxfp4_x_lds_n<FILS, PD, 2>(mat, x, y, R, C, r_bloc, xl);
     else
-        gemv_mxfp4_x_lds_n<3>(mat, x, y, R, C, r_bloc, xl);
+        gemv_mxfp4_x_lds_n<FILS, PD, 3>(mat, x, y, R, C, r_bloc, xl);
 }
 
 }  // namespace trc
 
-// y = W x + b, x in LDS (C <= GEMV_X_COLONNES): 32 rows per block of 256 threads.
-extern "C" __global__ void __launch_bounds__(trc::GEMV_X_FILS)
+// y = W x + b, x in LDS (C <= GEMV_X_COLONNES): FormeGemvX<FILS, PD>::LIGNES rows per block.
+template <uint32_t FILS, uint32_t PD>
+__global__ void __launch_bounds__(FILS)
 gemv_mxfp4_x(const uint8_t* __restrict__ matrice, const float* __restrict__ x, float* __restrict__ y, uint32_t R,
              uint32_t C) {
-    __shared__ __attribute__((aligned(16))) uint8_t xl[trc::GEMV_X_LDS];
-    trc::gemv_mxfp4_x_lds(matrice, x, y, R, C, blockIdx.x * trc::GEMV_X_LIGNES, xl);
+    __shared__ __attribute__((aligned(16))) uint8_t xl[trc::FormeGemvX<FILS, PD>::LDS];
+    trc::gemv_mxfp4_x_lds<FILS, PD>(matrice, x, y, R, C, blockIdx.x * trc::FormeGemvX<FILS, PD>::LIGNES, xl);
 }
 
-// The batch form: grid y = product, 32 rows per block; a product wider than GEMV_X_COLONNES takes
-// gemv_mxfp4_demi for the same rows (each half-wavefront its two). Both branches are uniform over
-// the block (its rows belong to one product), so the barrier of the LDS form is reached by all.
-extern "C" __global__ void __launch_bounds__(trc::GEMV_X_FILS)
-gemv_mxfp4_lot_x(const trc::DescGemv* __restrict__ descs) {
-    __shared__ __attribute__((aligned(16))) uint8_t xl[trc::GEMV_X_LDS];
+// The batch form: grid y = product; a product wider than GEMV_X_COLONNES takes gemv_mxfp4_demi for
+// the same rows (each half-wavefront two at a time). Both branches are uniform over the block (its
+// rows belong to one product), so the barrier of the LDS form is reached by all.
+template <uint32_t FILS, uint32_t PD>
+__global__ void __launch_bounds__(FILS) gemv_mxfp4_lot_x(const trc::DescGemv* __restrict__ descs) {
+    using F = trc::FormeGemvX<FILS, PD>;
+    __shared__ __attribute__((aligned(16))) uint8_t xl[F::LDS];
     const trc::DescGemv dsc = descs[blockIdx.y];
-    const uint32_t r_bloc = blockIdx.x * trc::GEMV_X_LIGNES;
+    const uint32_t r_bloc = blockIdx.x * F::LIGNES;
     if (r_bloc >= dsc.lignes || dsc.colonnes % 32u != 0) return;
     if (dsc.colonnes > trc::GEMV_X_COLONNES) {
         for (uint32_t r0 = r_bloc + (threadIdx.x >> 5) * trc::GEMV_LIGNES_PAR_DEMI;
-             r0 < min(r_bloc + trc::GEMV_X_LIGNES, dsc.lignes); r0 += (trc::GEMV_X_FILS / 32u) * trc::GEMV_LIGNES_PAR_DEMI)
+             r0 < min(r_bloc + F::LIGNES, dsc.lignes); r0 += F::DEMIS * trc::GEMV_LIGNES_PAR_DEMI)
             trc::gemv_mxfp4_demi(reinterpret_cast<const uint8_t*>(dsc.matrice), reinterpret_cast<const float*>(dsc.x),
                                  reinterpret_cast<float*>(dsc.y), dsc.lignes, dsc.colonnes, r0, threadIdx.x & 31u);
         return;
     }
-    trc::gemv_mxfp4_x_lds(reinterpret_cast<const uint8_t*>(dsc.matrice), reinterpret_cast<const float*>(dsc.x),
-                          reinterpret_cast<float*>(dsc.y), dsc.lignes, dsc.colonnes, r_bloc, xl);
+    trc::gemv_mxfp4_x_lds<FILS, PD>(reinterpret_cast<const uint8_t*>(dsc.matrice), reinterpret_cast<const float*>(dsc.x),
+                                    reinterpret_cast<float*>(dsc.y), dsc.lignes, dsc.colonnes, r_bloc, xl);
 }
 
 // y = W x + b for one slot matrix: 8 halves x 2 rows per block of 256 threads.
@@ -596,6 +602,26 @@ extern "C" int trc_copier_brut(trc_vue partie, trc_vue emplacement, const trc_di
     return trc::apres_lancement("copier_brut");
 }
 
+namespace {
+
+template <uint32_t FILS, uint32_t PD>
+int lancer_gemv_lot_x_forme(const trc::DescGemv* descs, uint32_t n, uint32_t lignes_max, hipStream_t f) {
+    constexpr uint32_t L = trc::FormeGemvX<FILS, PD>::LIGNES;
+    hipLaunchKernelGGL((gemv_mxfp4_lot_x<FILS, PD>), dim3((lignes_max + L - 1) / L, n), dim3(FILS), 0, f, descs);
+    return trc::apres_lancement("gemv_mxfp4_lot_x");
+}
+
+// The block shape of a batch of n products of at most lignes_max rows: one row per
+// half-wavefront (32 VGPRs, so that a CU holds many wavefronts whose loads and arithmetic overlap),
+// 16 halves per block, or 8 when that leaves fewer than 512 blocks. Measured on MI355X over 4, 8
+// and 12 gpt-oss matrices against 2 and 4 rows per half and 4 to 32 halves per block.
+int lancer_gemv_lot_x(const trc::DescGemv* descs, uint32_t n, uint32_t lignes_max, hipStream_t f) {
+    if (uint64_t(n) * ((lignes_max + 15u) / 16u) < 512u) return lancer_gemv_lot_x_forme<256, 1>(descs, n, lignes_max, f);
+    return lancer_gemv_lot_x_forme<512, 1>(descs, n, lignes_max, f);
+}
+
+}  // namespace
+
 extern "C" int trc_gemv(trc_vue matrice, trc_vue x, trc_vue y, uint32_t lignes, uint32_t colonnes, void* flux) {
     TRC_VERIFIER(lignes > 0 && colonnes > 0 && colonnes % 32 == 0, "forme %u x %u", lignes, colonnes);
     const uint64_t pas = trc::disposition_matrice(lignes, colonnes).pas;
@@ -606,10 +632,10 @@ extern "C" int trc_gemv(trc_vue matrice, trc_vue x, trc_vue y, uint32_t lignes, 
                  "x trop court ou non aligne sur 16");
     TRC_VERIFIER(y.adresse != 0 && y.octets >= 4ull * lignes, "y trop court");
     if (colonnes <= trc::GEMV_X_COLONNES) {
-        hipLaunchKernelGGL(gemv_mxfp4_x, dim3((lignes + trc::GEMV_X_LIGNES - 1) / trc::GEMV_X_LIGNES),
-                           dim3(trc::GEMV_X_FILS), 0, flux_de(flux), reinterpret_cast<const uint8_t*>(matrice.adresse),
-                           reinterpret_cast<const float*>(x.adresse), reinterpret_cast<float*>(y.adresse), lignes,
-                           colonnes);
+        constexpr uint32_t L = trc::FormeGemvX<256, 1>::LIGNES;  // a single product: 8 rows per block
+        hipLaunchKernelGGL((gemv_mxfp4_x<256, 1>), dim3((lignes + L - 1) / L), dim3(256), 0, flux_de(flux),
+                           reinterpret_cast<const uint8_t*>(matrice.adresse), reinterpret_cast<const float*>(x.adresse),
+                           reinterpret_cast<float*>(y.adresse), lignes, colonnes);
         return trc::apres_lancement("gemv_mxfp4_x");
     }
     hipLaunchKernelGGL(gemv_mxfp4, dim3((lignes + trc::GEMV_LIGNES_PAR_BLOC - 1) / trc::GEMV_LIGNES_PAR_BLOC),
@@ -623,9 +649,7 @@ extern "C" int trc_gemv_lot(trc_vue descs, uint32_t n, uint32_t lignes_max, void
     TRC_VERIFIER(n > 0 && n <= 65535, "lot de %u produits", n);
     TRC_VERIFIER(descs.adresse != 0 && descs.octets >= uint64_t(n) * sizeof(trc_desc_gemv), "descripteurs trop courts");
     TRC_VERIFIER(lignes_max > 0, "lignes_max nul");
-    hipLaunchKernelGGL(gemv_mxfp4_lot_x, dim3((lignes_max + trc::GEMV_X_LIGNES - 1) / trc::GEMV_X_LIGNES, n),
-                       dim3(trc::GEMV_X_FILS), 0, flux_de(flux), reinterpret_cast<const trc::DescGemv*>(descs.adresse));
-    return trc::apres_lancement("gemv_mxfp4_lot_x");
+    return lancer_gemv_lot_x(reinterpret_cast<const trc::DescGemv*>(descs.adresse), n, lignes_max, flux_de(flux));
 }
 
 extern "C" int trc_gemv_f32(trc_vue w, trc_vue x, trc_vue biais, trc_vue y, uint32_t lignes, uint32_t colonnes,

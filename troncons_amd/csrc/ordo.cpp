@@ -600,7 +600,7 @@ int trc_ordo_jeton(trc_ordo* o, trc_vue x, trc_vue residu, void* flux) {
             // token, since its cache holds slots that were never made ready
             const std::string m = trc_derniere_erreur();
             o->lecteurs->vider();
-            hipStreamSynchronize(o->copie);
+            (void)hipStreamSynchronize(o->copie);
             o->en_echec = true;
             o->message_echec = m;
             trc::derniere_erreur() = m;

@@ -57,6 +57,7 @@ constexpr uint32_t PF_BP_MAX = 128;       // blocks per row at most (4096 column
 constexpr uint32_t PF_PAIRES_MAX = 16384; // positions x k per call
 constexpr uint32_t ECHELLE_UN = 127u;     // E8M0 1.0
 
+constexpr uint32_t PF_LOT_COPIE = 4;     // loads per thread in flight when a band is copied from a slot
 constexpr uint32_t PF_TOURS = 2;          // decode rounds per band: a band's tiles are at most 64
 constexpr uint32_t PF_RB_MAX = 80;         // rows per band
 constexpr uint32_t PF_RT_MAX = PF_RB_MAX / 16u;  // row tiles per band
@@ -508,7 +509,7 @@ __device__ __forceinline__ void poser_tour(const TourBande& tb, uint32_t t, uint
 // then the bf16 MFMA (weights converted where they are read): each of the 16 waves takes every row
 // tile of the band (up to 5) over its share of K, so that each B load feeds every row tile and B is
 // read once per band.
-template <uint32_t J>
+template <uint32_t J, bool EMPL>  // EMPL: long tiles, the band copied from the expert's slot
 __device__ __forceinline__ void prefill_bande(const ParamsPrefill& pp, const uint32_t* __restrict__ luts,
                                               uint32_t* __restrict__ controle, uint8_t* lds) {
     const uint32_t e = blockIdx.y / J, j = J == 2u ? (blockIdx.y & 1u) : 2u;
@@ -521,9 +522,9 @@ __device__ __forceinline__ void prefill_bande(const ParamsPrefill& pp, const uin
     const uint32_t nl = min(RB, R - r0);
     const uint32_t* lut_src = luts + (uint64_t(j) * 4u + 1u) * M;
     // long tiles: the band's codes and scales come from the expert's slot, nothing is decoded here
-    const bool depuis_emplacement = pp.emplacements != 0u;
+    constexpr bool depuis_emplacement = EMPL;
     ChargeLut<3> charge_lut;
-    charge_lut.demarrer(lut_src, 3u * M / 4u);
+    if (!depuis_emplacement) charge_lut.demarrer(lut_src, 3u * M / 4u);
     const MatricePartie m = *reinterpret_cast<const MatricePartie*>(pp.repertoire + uint64_t(e * 3u + j) * sizeof(MatricePartie));
     const EnteteRans h = entete_de(m.codes, m.cP, m.cN, m.cT, m.cW);
     const uint32_t N = h.N;
@@ -609,11 +610,36 @@ __device__ __forceinline__ void prefill_bande(const ParamsPrefill& pp, const uin
         // the band's blocks [ba, bb) of the slot: 16 code bytes each (16-byte aligned), one scale byte each
         const trc_disposition disp = disposition(dims_prefill(pp), j);
         const uint8_t* mat = reinterpret_cast<const uint8_t*>(pp.emplacements + uint64_t(e) * pp.pas_emplacement + disp.base);
+        // (batches of PF_LOT_COPIE loads per thread issued before their stores, and the scales as the
+        // 4-byte words of the 256-aligned scale array that cover the band: the vector memory unit
+        // takes as long over a byte load as over a 16-byte one)
+        const uint32_t n = nl * B;
         const gptr<u32x4> codes = glob<u32x4>(mat + 16ull * ba);
-        const gptr<uint8_t> echelles = glob<uint8_t>(mat + disp.echelles + ba);
-        for (uint32_t i = threadIdx.x; i < nl * B; i += blockDim.x) {
-            ecrire_lds<u32x4>(base + PF_A + 16u * i, codes[i]);
-            ecrire_lds<uint8_t>(a_sa + i, echelles[i]);
+        for (uint32_t i0 = 0; i0 < n; i0 += PF_LOT_COPIE * PF_FILS) {
+            u32x4 c[PF_LOT_COPIE];
+#pragma unroll
+            for (uint32_t k = 0; k < PF_LOT_COPIE; ++k) c[k] = codes[min(i0 + threadIdx.x + k * PF_FILS, n - 1u)];
+#pragma unroll
+            for (uint32_t k = 0; k < PF_LOT_COPIE; ++k) {
+                const uint32_t i = i0 + threadIdx.x + k * PF_FILS;
+                if (i < n) ecrire_lds<u32x4>(base + PF_A + 16u * i, c[k]);
+            }
+        }
+        const gptr<uint32_t> ech32 = glob<uint32_t>(mat + disp.echelles);
+        const uint32_t w0 = ba >> 2, nw = ((bb + 3u) >> 2) - w0;
+        for (uint32_t i0 = 0; i0 < nw; i0 += PF_LOT_COPIE * PF_FILS) {
+            uint32_t e4[PF_LOT_COPIE];
+#pragma unroll
+            for (uint32_t k = 0; k < PF_LOT_COPIE; ++k) e4[k] = ech32[w0 + min(i0 + threadIdx.x + k * PF_FILS, nw - 1u)];
+#pragma unroll
+            for (uint32_t k = 0; k < PF_LOT_COPIE; ++k) {
+                const uint32_t i = i0 + threadIdx.x + k * PF_FILS;
+#pragma unroll
+                for (uint32_t o = 0; o < 4u; ++o) {
+                    const uint32_t blk = 4u * (w0 + i) + o;
+                    if (i < nw && blk >= ba && blk < bb) ecrire_lds<uint8_t>(a_sa + blk - ba, uint8_t(e4[k] >> (8u * o)));
+                }
+            }
         }
     } else {
         poser_tour(tour0, t00 + haut, N, ba, bb, base, a_sa);
@@ -728,13 +754,26 @@ __device__ __forceinline__ void prefill_bande(const ParamsPrefill& pp, const uin
 extern "C" __global__ void __launch_bounds__(trc::PF_FILS)
 prefill_mfma_gu(ParamsPrefill pp, const uint32_t* __restrict__ luts, uint32_t* __restrict__ controle) {
     __shared__ __attribute__((aligned(16384))) uint8_t lds[trc::LDS_GEMV];
-    trc::prefill_bande<2>(pp, luts, controle, lds);
+    trc::prefill_bande<2, false>(pp, luts, controle, lds);
 }
 
 extern "C" __global__ void __launch_bounds__(trc::PF_FILS)
 prefill_mfma_bas(ParamsPrefill pp, const uint32_t* __restrict__ luts, uint32_t* __restrict__ controle) {
     __shared__ __attribute__((aligned(16384))) uint8_t lds[trc::LDS_GEMV];
-    trc::prefill_bande<1>(pp, luts, controle, lds);
+    trc::prefill_bande<1, false>(pp, luts, controle, lds);
+}
+
+// The same over long tiles: each band copied from its expert's slot.
+extern "C" __global__ void __launch_bounds__(trc::PF_FILS)
+prefill_mfma_gu_emplacement(ParamsPrefill pp, const uint32_t* __restrict__ luts, uint32_t* __restrict__ controle) {
+    __shared__ __attribute__((aligned(16384))) uint8_t lds[trc::LDS_GEMV];
+    trc::prefill_bande<2, true>(pp, luts, controle, lds);
+}
+
+extern "C" __global__ void __launch_bounds__(trc::PF_FILS)
+prefill_mfma_bas_emplacement(ParamsPrefill pp, const uint32_t* __restrict__ luts, uint32_t* __restrict__ controle) {
+    __shared__ __attribute__((aligned(16384))) uint8_t lds[trc::LDS_GEMV];
+    trc::prefill_bande<1, true>(pp, luts, controle, lds);
 }
 
 // x_i[r] += ((w0 s_i0[r] + w1 s_i1[r]) + w2 s_i2[r]) + ..., each product and sum rounded on its own
@@ -974,9 +1013,17 @@ extern "C" int trc_prefill_moe(trc_vue repertoire, uint32_t experts, trc_vue lut
         r = trc::lancer_echelles_prefill(pm, Rm, C, n_delta, l, ctl, f);
         if (r != TRC_OK) return r;
     }
-    TRC_LANCER(prefill_mfma_gu, dim3((R + pp.rb[0] - 1) / pp.rb[0], 2 * experts), dim3(trc::PF_FILS), f, pp, l, ctl);
+    if (pp.emplacements != 0)
+        TRC_LANCER(prefill_mfma_gu_emplacement, dim3((R + pp.rb[0] - 1) / pp.rb[0], 2 * experts), dim3(trc::PF_FILS), f,
+                   pp, l, ctl);
+    else
+        TRC_LANCER(prefill_mfma_gu, dim3((R + pp.rb[0] - 1) / pp.rb[0], 2 * experts), dim3(trc::PF_FILS), f, pp, l, ctl);
     TRC_LANCER(prefill_swiglu_quant, dim3(T * k), dim3(trc::PF_Q_FILS), f, pp);
-    TRC_LANCER(prefill_mfma_bas, dim3((D + pp.rb[2] - 1) / pp.rb[2], experts), dim3(trc::PF_FILS), f, pp, l, ctl);
+    if (pp.emplacements != 0)
+        TRC_LANCER(prefill_mfma_bas_emplacement, dim3((D + pp.rb[2] - 1) / pp.rb[2], experts), dim3(trc::PF_FILS), f,
+                   pp, l, ctl);
+    else
+        TRC_LANCER(prefill_mfma_bas, dim3((D + pp.rb[2] - 1) / pp.rb[2], experts), dim3(trc::PF_FILS), f, pp, l, ctl);
     const uint32_t fils_comb = pp.quatre ? D / 4u : D;  // threads per position
     TRC_LANCER(prefill_combiner, dim3((fils_comb + 255) / 256, T), dim3(256), f, pp);
     return TRC_OK;
