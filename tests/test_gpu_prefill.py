@@ -297,3 +297,31 @@ def test_prefill_reference_tile_lengths_gpt_oss_shape(fz):
     _, ctl = _lancer(fz, couche, E, GPT, x, idx, w, residu0, N)
     assert ctl[0] + ctl[2] > 0 and ctl[1] == 0, list(ctl)
     couche.c.liberer()
+
+
+@pytest.mark.parametrize("N", [(1, 16), (2, 16), (2, 32)])
+def test_prefill_delta_in_codes_gpt_oss_shape(fz, N):
+    """Tile lengths whose DELTA the CODES pass decodes itself (16 with DELTA tiles of 1 or 2, 32 with
+    2): the chosen experts are decoded into slots by one launch that decodes each tile's DELTA with
+    it, the bands read the slots. 8 gpt-oss experts, 16 positions with Zipf routing, against the
+    oracle chain and f64; a flipped bit in a chosen expert's DELTA stream is counted."""
+    E, T, k = 8, 16, 4
+    couche = Couche(fz, 121, E, GPT, N)
+    idx, w = _routage(122, T, E, k, zipf=1.1)
+    x = np.stack([O.synth_normale_bf16(123, 4, i, 2880, 1.0) for i in range(T)])
+    residu0 = np.stack([O.synth_normale_bf16(123, 5, i, 2880, 0.5) for i in range(T)])
+    got, ctl = _lancer(fz, couche, E, GPT, x, idx, w, residu0, N)
+    assert list(ctl) == [0, 0, 0, 0]
+    _verifier(got, residu0, x, idx, w, _slots(121, E, GPT), GPT)
+    # a flipped bit in the middle of expert idx[0, 0]'s down DELTA stream
+    e0 = int(idx[0, 0])
+    p = couche.c.partie(e0)
+    n = int.from_bytes(p[10:12].tobytes(), "little")
+    (d,) = [64 + 16 * i for i in range(n) if p[64 + 16 * i] == 3 and p[64 + 16 * i + 1] == 2]  # DELTA = kind 3
+    dec = int.from_bytes(p[d + 4:d + 8].tobytes(), "little")
+    lon = int.from_bytes(p[d + 8:d + 12].tobytes(), "little")
+    p[dec + lon // 2] ^= 0x10
+    couche.parts[e0].copy_(torch.from_numpy(p))
+    _, ctl = _lancer(fz, couche, E, GPT, x, idx, w, residu0, N)
+    assert ctl[0] + ctl[2] > 0 and ctl[1] == 0, list(ctl)
+    couche.c.liberer()

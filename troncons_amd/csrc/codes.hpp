@@ -129,6 +129,7 @@ __device__ __forceinline__ int exposant_entree(uint32_t ent) { return int((ent ^
 struct EntreesLane {
     u32x4 s;
     bool ligne;  // one of the 4 blocks starts a row (the tile's own first block excepted)
+    uint32_t e4;  // the 4 blocks' E8M0 exponents e, block 4v + k in byte k (127 past the matrix)
     bool ech;    // every exponent e of the 4 lies in [64, 191]. The weights with the block scale
                  // folded in are then 2^(e-128) times the doubled E2M1 values, exactly, and every
                  // product and sum of the dot product with them is 2^(e-128) times the one without
@@ -170,6 +171,7 @@ __device__ __forceinline__ EntreesLane entrees_de_delta(uint32_t mot, uint32_t m
         rp &= ~pad;
     }
     EntreesLane r;
+    r.e4 = ee;
     // e in [64, 191] <=> bits 7 and 6 of e differ
     r.ech = ((ee ^ (ee << 1)) & 0x80808080u) == 0x80808080u;
     r.ligne = (rp & masque_ligne) != 0u;
@@ -189,6 +191,12 @@ struct Grille {
     uint32_t fils, blocs_x;
 };
 
+// Tile lengths whose DELTA the CODES pass decodes itself: CODES tiles of 16 macro-steps with DELTA
+// tiles of 1 or 2, or 32 with 2.
+__host__ __device__ constexpr bool delta_dans_codes(uint32_t n_delta, uint32_t n_codes) {
+    return (n_codes == 16u && (n_delta == 1u || n_delta == 2u)) || (n_codes == 32u && n_delta == 2u);
+}
+
 // What the CODES pass needs of a job in the internal-DELTA mode: both streams' headers, the
 // medians, the DELTA LUT. bon: every check passed and the tile lengths are the mode's.
 struct PrepCodes {
@@ -203,7 +211,7 @@ __device__ __forceinline__ PrepCodes preparer_codes(const Tache& tc, const Matri
     const uint32_t B = tc.colonnes / 32u;
     PrepCodes p;
     p.bon = m.bon != 0 && tc.colonnes % 32u == 0 && B >= 8u && tc.lignes > 0 &&
-            ((m.cN == 16u && (m.dN == 1u || m.dN == 2u)) || (m.cN == 32u && m.dN == 2u)) &&
+            delta_dans_codes(m.dN, m.cN) &&
             (B - 1u) / (8u * m.cN) + 2u <= tc.kmax;
     p.fc = m.codes;
     p.fd = m.delta;
@@ -221,6 +229,82 @@ __device__ __forceinline__ Avance premiere_avance(const PrepCodes& p, uint32_t R
     const uint32_t vague = blockIdx.x * (g.fils >> 6) + (threadIdx.x >> 6);
     return lire_avance<DELTA>(p.hc, p.fc, p.hd, p.fd, p.med, R, p.B, 2u * vague + (__lane_id() >= 32u ? 1u : 0u),
                               __lane_id() & 31u);
+}
+
+// The DELTA stage of a tile pair, shared by the CODES pass and the slot decoder: the half's DELTA
+// words landed in its ring, its DELTA macro-step(s) decoded (mot; mot_b: the second one of a tile
+// of 32 macro-steps), the block's two first-tile barriers passed (premiere), the DELTA tile's end
+// checks counted by the half that decoded its last macro-step.
+struct ContexteDelta {
+    gptr<uint32_t> lutd;  // the job's DELTA LUT (reference format) in device memory
+    uint32_t a_lutd;      // its LDS copy (the entry area, for the first tiles)
+    uint32_t a_anneau, decal, masque_inf, v;
+    uint32_t mots_d;      // offset of the DELTA stream's words from its start
+    uint32_t dN, dT, nmacro_d;
+};
+
+template <uint32_t NC>
+__device__ __forceinline__ void delta_de_tuile(const PrepCodes& p, const ContexteDelta& cd, const Avance& cur,
+                                               uint32_t t, bool tuile, bool& premiere, uint32_t& hors_l,
+                                               uint32_t& pointeur, uint32_t& mot, uint32_t& mot_b) {
+    const gptr<uint32_t> lutd = cd.lutd;
+    const uint32_t a_lutd = cd.a_lutd, a_anneau = cd.a_anneau, decal = cd.decal, masque_inf = cd.masque_inf;
+    const uint32_t v = cd.v, mots_d = cd.mots_d, dN = cd.dN, dT = cd.dT, nmacro_d = cd.nmacro_d;
+    // NC = 16: the half's DELTA tile from its start to macro-step t mod N_delta (DELTA tile
+    // t / N_delta covers CODES tiles t - t mod N_delta ..). NC = 32: DELTA tile t, both macro-steps.
+    // Words from the ring.
+    const uint32_t saut = NC == 32u ? 1u : (t & (dN - 1u));  // last DELTA macro-step needed
+    const uint32_t saut_max = NC == 32u ? 1u : uniforme32(dN == 1u ? 0u : 1u);
+    ecrire_lds<u32x4>(a_anneau + 16u * v, cur.dmots);
+    {
+        // two DELTA macro-steps can read up to 512 + 15 bytes: when the DELTA tile's words pass
+        // the 512 read ahead (rare: about 50 bytes per macro-step here), the rest is read now
+        const uint32_t o_d = (mots_d + 2u * cur.dDebut) & 15u;
+        const bool long_d = tuile && o_d + 2u * (cur.dAttendu - cur.dDebut) > 512u;
+        if (__builtin_amdgcn_ballot_w64(long_d) != 0) {
+            const uint32_t g0d = (mots_d + 2u * cur.dDebut) & ~15u;
+            const u32x4 suite = long_d ? lire16_flux(p.fd.p, p.fd.longueur, g0d + 512u + 16u * v)
+                                       : u32x4{0u, 0u, 0u, 0u};
+            if (long_d) ecrire_lds<u32x4>(a_anneau + 512u + 16u * v, suite);
+        }
+    }
+    if (premiere) barriere_lds();  // the staged LUTs and x are visible
+    const uint32_t tau = NC == 32u ? t : (t >> (dN - 1u));
+    const uint32_t nbd = tau < dT ? min(dN, nmacro_d - tau * dN) : 0u;  // macro-steps of DELTA tile tau
+    uint32_t xd = cur.xd, od = ((mots_d + 2u * cur.dDebut) & 15u);
+    mot = 0;
+    mot_b = 0;
+    auto delta = [&](auto en_lds) {
+        constexpr bool EN_LDS = decltype(en_lds)::value;
+        for (uint32_t md = 0; md <= saut_max; ++md) {
+            const bool actif = tuile && md <= saut && md < nbd;
+            uint32_t compte = 0, m4 = 0;
+#pragma unroll
+            for (uint32_t k = 0; k < 4; ++k)
+                m4 |= pas_delta<false, EN_LDS>(xd, od, compte, lutd, a_lutd, a_anneau, decal, masque_inf, actif)
+                      << (8u * k);
+            od += 2u * compte;
+            if (NC == 32u) {
+                if (md == 0u) mot = m4;
+                else mot_b = m4;
+            } else if (md == saut) {
+                mot = m4;
+            }
+        }
+    };
+    if (premiere)  // wave-uniform
+        delta(std::true_type{});
+    else
+        delta(std::false_type{});
+    if (premiere) {
+        barriere_lds();  // no wave reads the DELTA LUT copy any more: the entry area is free
+        premiere = false;
+    }
+    // the DELTA tile's end checks, by the half that decoded its last macro-step
+    if (tuile && (NC == 32u ? nbd > 0u : saut + 1u == nbd)) {
+        hors_l += (xd != L) ? 1u : 0u;
+        pointeur += (v == 0 && cur.dDebut + (od - ((mots_d + 2u * cur.dDebut) & 15u)) / 2u != cur.dAttendu) ? 1u : 0u;
+    }
 }
 
 // CODES_CTX tiles -> partial sums of W x, x in LDS, the tiles' entries decoded here from DELTA.
@@ -271,6 +355,7 @@ __device__ __forceinline__ void corps_codes_n(const Tache& tc, const PrepCodes& 
     Avance av = avance0;
     bool premiere = true;  // wave-uniform: the block's two first-tile barriers are still to pass
     const uint32_t a_lutd = base + LDS_ENT;
+    const ContexteDelta cd{lutd, a_lutd, a_anneau, decal, masque_inf, v, mots_d, dN, dT, nmacro_d};
     // the row-start bytes that count for `ligne`: all but the tile's own first block (lane 0, byte 0)
     const uint32_t masque_ligne = v == 0u ? 0x01010100u : 0x01010101u;
     // Issue priority by progress: a wavefront decodes its first tile pair at priority 3, then 2 from
@@ -288,59 +373,9 @@ __device__ __forceinline__ void corps_codes_n(const Tache& tc, const PrepCodes& 
         const uint32_t m0 = (tuile ? t : t0) * hN;
         const Avance cur = av;
 
-        // 1. DELTA. NC = 16: the half's DELTA tile from its start to macro-step t mod N_delta (DELTA
-        // tile t / N_delta covers CODES tiles t - t mod N_delta ..). NC = 32: DELTA tile t, both
-        // macro-steps. Words from the ring.
-        const uint32_t saut = NC == 32u ? 1u : (t & (dN - 1u));  // last DELTA macro-step needed
-        const uint32_t saut_max = NC == 32u ? 1u : uniforme32(dN == 1u ? 0u : 1u);
-        ecrire_lds<u32x4>(a_anneau + 16u * v, cur.dmots);
-        {
-            // two DELTA macro-steps can read up to 512 + 15 bytes: when the DELTA tile's words pass
-            // the 512 read ahead (rare: about 50 bytes per macro-step here), the rest is read now
-            const uint32_t o_d = (mots_d + 2u * cur.dDebut) & 15u;
-            const bool long_d = tuile && o_d + 2u * (cur.dAttendu - cur.dDebut) > 512u;
-            if (__builtin_amdgcn_ballot_w64(long_d) != 0) {
-                const uint32_t g0d = (mots_d + 2u * cur.dDebut) & ~15u;
-                const u32x4 suite = long_d ? lire16_flux(p.fd.p, p.fd.longueur, g0d + 512u + 16u * v)
-                                           : u32x4{0u, 0u, 0u, 0u};
-                if (long_d) ecrire_lds<u32x4>(a_anneau + 512u + 16u * v, suite);
-            }
-        }
-        if (premiere) barriere_lds();  // the staged LUTs and x are visible
-        const uint32_t tau = NC == 32u ? t : (t >> (dN - 1u));
-        const uint32_t nbd = tau < dT ? min(dN, nmacro_d - tau * dN) : 0u;  // macro-steps of DELTA tile tau
-        uint32_t xd = cur.xd, od = ((mots_d + 2u * cur.dDebut) & 15u), mot = 0, mot_b = 0;
-        auto delta = [&](auto en_lds) {
-            constexpr bool EN_LDS = decltype(en_lds)::value;
-            for (uint32_t md = 0; md <= saut_max; ++md) {
-                const bool actif = tuile && md <= saut && md < nbd;
-                uint32_t compte = 0, m4 = 0;
-#pragma unroll
-                for (uint32_t k = 0; k < 4; ++k)
-                    m4 |= pas_delta<false, EN_LDS>(xd, od, compte, lutd, a_lutd, a_anneau, decal, masque_inf, actif)
-                          << (8u * k);
-                od += 2u * compte;
-                if (NC == 32u) {
-                    if (md == 0u) mot = m4;
-                    else mot_b = m4;
-                } else if (md == saut) {
-                    mot = m4;
-                }
-            }
-        };
-        if (premiere)  // wave-uniform
-            delta(std::true_type{});
-        else
-            delta(std::false_type{});
-        if (premiere) {
-            barriere_lds();  // no wave reads the DELTA LUT copy any more: the entry area is free
-            premiere = false;
-        }
-        // the DELTA tile's end checks, by the half that decoded its last macro-step
-        if (tuile && (NC == 32u ? nbd > 0u : saut + 1u == nbd)) {
-            hors_l += (xd != L) ? 1u : 0u;
-            pointeur += (v == 0 && cur.dDebut + (od - ((mots_d + 2u * cur.dDebut) & 15u)) / 2u != cur.dAttendu) ? 1u : 0u;
-        }
+        // 1. DELTA
+        uint32_t mot, mot_b;
+        delta_de_tuile<NC>(p, cd, cur, t, tuile, premiere, hors_l, pointeur, mot, mot_b);
         // 2. the tile's block entries, which macro-steps start a row (macro-step m covers the
         // blocks of lanes 2m and 2m + 1: bit 2m of `lignes_m`, bit 2(m - 16) of `lignes_mb`), and
         // whether the wavefront's two tiles take the block scale inside the conversion
@@ -503,6 +538,160 @@ __device__ __forceinline__ void corps_codes_n(const Tache& tc, const PrepCodes& 
         ++paire_n;
     }
     if (premiere) {  // a wavefront without tiles still takes its part in both
+        barriere_lds();
+        barriere_lds();
+    }
+    verser_controle(controle, hors_l, pointeur);
+}
+
+// 4 scale bytes of blocks b0 .. b0 + 3 (b0 % 4 == 0) into a slot's 256-aligned scale array, those
+// past the matrix left alone.
+__device__ __forceinline__ void poser_echelles(uint8_t* ech, uint32_t b0, uint32_t e4, uint32_t nblocs, bool tuile) {
+    if (!tuile || b0 >= nblocs) return;
+    if (b0 + 4u <= nblocs) {
+        ecrire_global<uint32_t>(reinterpret_cast<uint32_t*>(ech + b0), e4);
+    } else {
+        for (uint32_t k = 0; b0 + k < nblocs; ++k) ech[b0 + k] = uint8_t(e4 >> (8u * k));
+    }
+}
+
+// The same tiles decoded into a slot instead of multiplied: CODES_CTX tiles of NC macro-steps, each
+// with its DELTA decoded by its half-wavefront as in corps_codes_n (read one tile ahead, entries in
+// LDS for the contexts), give the matrix's code bytes (codes, in stream order: the reference's
+// [R][B][16 B]) and E8M0 scales (ech, [R][B]). The LDS regions are the CODES pass's (x unused).
+// avance0: premiere_avance(p), read by the caller before it stages the LUTs.
+template <uint32_t NC>
+__device__ __forceinline__ void corps_codes_emplacement_n(const PrepCodes& p, uint32_t R, uint8_t* __restrict__ codes8,
+                                                          uint8_t* __restrict__ ech, uint8_t* lds, const uint32_t* lutd_,
+                                                          uint32_t* __restrict__ controle, const Avance& avance0,
+                                                          const Grille& g) {
+    static_assert(NC == 16u || NC == 32u, "CODES tiles of 16 or 32 macro-steps");
+    constexpr uint32_t BPT = 8u * NC;
+    const EnteteRans& h = p.hc;
+    const EnteteRans& hd = p.hd;
+    const uint32_t B = p.B.d, nblocs = R * B, mots_utiles = 4u * nblocs;
+    uint32_t* __restrict__ codes = reinterpret_cast<uint32_t*>(codes8);
+    const gptr<uint32_t> lutd = glob<uint32_t>(lutd_);
+    const uint32_t lane = __lane_id();
+    const uint32_t v = lane & 31u;
+    const bool haut = lane >= 32u;
+    const uint32_t decal = haut ? 32u : 0u, masque_inf = (1u << v) - 1u;
+    const uint32_t q = v >> 2;
+    const uint32_t vagues_bloc = g.fils >> 6;
+    const uint32_t vague = uniforme32(blockIdx.x * vagues_bloc + (threadIdx.x >> 6));
+    const uint32_t n_vagues = g.blocs_x * vagues_bloc;
+    const uint32_t demi = (threadIdx.x >> 5) & (2u * vagues_bloc - 1u);
+    const uint32_t base = adresse_lds(lds);
+    const uint32_t a_lut = base + LDS_LUT;
+    const uint32_t a_anneau = base + LDS_ANNEAUX + demi * OCTETS_ANNEAU;
+    const uint32_t a_ent = base + LDS_ENT + demi * (ENT_PAR_TUILE * 4u);
+    const uint32_t a_ent_q = a_ent + 4u * q;
+    const uint32_t a_etage = base + LDS_X + demi * 512u;  // x's region: 32 halves x 4 macro-steps x 128 B
+    const uint32_t hN = uniforme32(h.N), hT = uniforme32(h.T), nmacro = uniforme32(h.P / 128u);
+    const uint32_t dN = uniforme32(hd.N), dT = uniforme32(hd.T), nmacro_d = uniforme32(hd.P / 128u);
+    const uint32_t mots_c = uint32_t(reinterpret_cast<const uint8_t*>(h.mots) - p.fc.p);
+    const uint32_t mots_d = uint32_t(reinterpret_cast<const uint8_t*>(hd.mots) - p.fd.p);
+    uint32_t hors_l = 0, pointeur = 0;
+    Avance av = avance0;
+    bool premiere = true;  // wave-uniform: the block's two first-tile barriers are still to pass
+    const ContexteDelta cd{lutd, base + LDS_ENT, a_anneau, decal, masque_inf, v, mots_d, dN, dT, nmacro_d};
+    for (uint32_t t0 = 2u * vague; t0 < hT; t0 += 2u * n_vagues) {
+        const uint32_t t = t0 + (haut ? 1u : 0u);
+        const bool tuile = t < hT;
+        const uint32_t nb_a = min(hN, nmacro - t0 * hN);
+        const uint32_t nb_b = (t0 + 1u < hT) ? min(hN, nmacro - (t0 + 1u) * hN) : 0u;
+        const uint32_t nb = haut ? nb_b : nb_a;
+        const uint32_t m0 = (tuile ? t : t0) * hN;
+        const Avance cur = av;
+        uint32_t mot, mot_b;
+        delta_de_tuile<NC>(p, cd, cur, t, tuile, premiere, hors_l, pointeur, mot, mot_b);
+        // the entries (contexts) into LDS, the scales into the slot
+        const EntreesLane el = entrees_de_delta(mot, cur.med0, cur.med1, cur.rang0, BPT * t + 4u * v, nblocs, p.B,
+                                                0x01010101u);
+        if (tuile) ecrire_lds<u32x4>(a_ent + 16u * v, el.s);
+        poser_echelles(ech, BPT * t + 4u * v, el.e4, nblocs, tuile);
+        u32x4 ent_b = u32x4{ENTC_BOURRAGE, ENTC_BOURRAGE, ENTC_BOURRAGE, ENTC_BOURRAGE};
+        if (NC == 32u) {
+            const EntreesLane eb = entrees_de_delta(mot_b, cur.med0b, cur.med1b, cur.rang0b, BPT * t + 128u + 4u * v,
+                                                    nblocs, p.B, 0x01010101u);
+            ent_b = eb.s;
+            poser_echelles(ech, BPT * t + 128u + 4u * v, eb.e4, nblocs, tuile);
+        }
+        // the CODES words over the DELTA ones, and the next pair's streams read ahead
+        ecrire_lds<u32x4>(a_anneau + 16u * v, cur.mots0);
+        ecrire_lds<u32x4>(a_anneau + 512u + 16u * v, cur.mots1);
+        av = lire_avance<true>(h, p.fc, hd, p.fd, p.med, R, p.B, t + 2u * n_vagues, v);
+        AnneauR a;
+        {
+            const uint32_t mot0 = mots_c + 2u * cur.tete.debut;
+            a.flux = p.fc.p;
+            a.g0 = mot0 & ~15u;
+            a.fin = p.fc.longueur;
+            a.lds = a_anneau;
+            a.o2 = mot0 - a.g0;
+            a.charge = OCTETS_ANNEAU / OCTETS_MORCEAU;
+            a.limite = a.charge * OCTETS_MORCEAU - FENETRE;
+            a.vol = u32x2{0u, 0u};
+            a.en_vol = false;
+        }
+        uint32_t x = cur.tete.x;
+        const uint32_t debut = cur.tete.debut, attendu = cur.tete.attendu;
+        const uint32_t o0 = a.o2;
+        uint32_t ent_suiv = tuile ? lire_lds<uint32_t>(a_ent_q) : ENTC_BOURRAGE;
+        const uint32_t nb_min = min(nb_a, nb_b);
+        // GROUPE (both tiles whole): a macro-step's words go to the half's 512-byte staging area,
+        // and every 4 macro-steps each lane stores 16 contiguous bytes of them (a quarter of the
+        // global store instructions); otherwise each lane stores its word
+        auto macro = [&](auto tous, auto groupe, uint32_t m) {
+            constexpr bool TOUS = decltype(tous)::value;
+            constexpr bool GROUPE = decltype(groupe)::value;
+            if (NC == 32u && (m == 8u || m == 16u)) {
+                // the second 128 blocks' entries over the slots this tile has passed (wave-uniform test)
+                if ((v < 16u) == (m == 8u) && tuile) ecrire_lds<u32x4>(a_ent + 16u * v, ent_b);
+            }
+            const bool actif = TOUS || m < nb;
+            const uint32_t ent = actif ? ent_suiv : ENTC_BOURRAGE;
+            ent_suiv = lire_lds<uint32_t>(a_ent_q + 32u * ((m + 1u) & 15u));
+            const uint32_t lt = a_lut + (ent & ENT_CTX);
+            uint32_t compte = 0;
+            const uint32_t e0 = pas_r<TOUS>(x, a.o2, compte, lt, a_anneau, decal, masque_inf, actif);
+            const uint32_t e1 = pas_r<TOUS>(x, a.o2, compte, lt, a_anneau, decal, masque_inf, actif);
+            const uint32_t e2 = pas_r<TOUS>(x, a.o2, compte, lt, a_anneau, decal, masque_inf, actif);
+            const uint32_t e3 = pas_r<TOUS>(x, a.o2, compte, lt, a_anneau, decal, masque_inf, actif);
+            a.o2 += 2u * compte;
+            avancer_anneau_r(a, v, actif);
+            // byte 3 of each LUT word is the decoded code byte
+            const uint32_t mot_c = __builtin_amdgcn_perm(e1, e0, 0x0C0C0703u) | __builtin_amdgcn_perm(e3, e2, 0x07030C0Cu);
+            if (GROUPE) {
+                ecrire_lds<uint32_t>(a_etage + 128u * (m & 3u) + 4u * v, mot_c);
+                if ((m & 3u) == 3u) {
+                    // lane v: words 4v .. 4v + 3 of the 4 macro-steps (macro-step v / 8, lanes 4 (v % 8) ..)
+                    const u32x4 c = lire_lds<u32x4>(a_etage + 16u * v);
+                    const uint32_t w = (m0 + m - 3u) * VOIES + 4u * v;
+                    if (tuile && w < mots_utiles) ecrire_global<u32x4>(codes + w, c);
+                }
+            } else {
+                const uint32_t w = (m0 + m) * VOIES + v;
+                if (actif && w < mots_utiles) ecrire_global<uint32_t>(codes + w, mot_c);
+            }
+        };
+        if (nb_min == NC) {
+#pragma unroll 1
+            for (uint32_t mm = 0; mm < NC; mm += 2u) {
+                macro(std::true_type{}, std::true_type{}, mm);
+                macro(std::true_type{}, std::true_type{}, mm + 1u);
+            }
+        } else {
+            uint32_t m = 0;
+            for (; m < nb_min; ++m) macro(std::true_type{}, std::false_type{}, m);
+            for (; m < nb_a; ++m) macro(std::false_type{}, std::false_type{}, m);
+        }
+        if (tuile) {
+            hors_l += (x != L) ? 1u : 0u;
+            pointeur += (v == 0 && debut + (a.o2 - o0) / 2u != attendu) ? 1u : 0u;
+        }
+    }
+    if (premiere) {  // a wavefront without tiles still takes its part in both barriers
         barriere_lds();
         barriere_lds();
     }

@@ -649,9 +649,7 @@ uint64_t pas_tache(uint32_t R, uint32_t C, uint32_t n_codes) {
 // macro-steps per CODES tile and 1 or 2 per DELTA tile, or 32 and 2: no DELTA launch, no block
 // entries. In that plan each matrix may take either form (the kernels read N from its streams).
 // Other tile lengths take the DELTA pass, whose block entries go through the workspace.
-bool delta_interne(uint32_t n_delta, uint32_t n_codes) {
-    return (n_codes == 16 && (n_delta == 1 || n_delta == 2)) || (n_codes == 32 && n_delta == 2);
-}
+bool delta_interne(uint32_t n_delta, uint32_t n_codes) { return trc::delta_dans_codes(n_delta, n_codes); }
 
 // Workspace piece of one matrix job in the internal-DELTA mode: its partial sums only.
 uint64_t pas_tache_interne(uint32_t R, uint32_t C) { return al(4ull * R * kmax_pour(C, 16)); }

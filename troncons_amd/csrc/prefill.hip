@@ -40,6 +40,7 @@
 
 #include "anneau.hpp"
 #include "chrono.hpp"
+#include "codes.hpp"
 #include "commun.hpp"
 #include "emplacement.hpp"
 #include "erreurs.hpp"
@@ -57,6 +58,8 @@ constexpr uint32_t PF_BP_MAX = 128;       // blocks per row at most (4096 column
 constexpr uint32_t PF_PAIRES_MAX = 16384; // positions x k per call
 constexpr uint32_t ECHELLE_UN = 127u;     // E8M0 1.0
 
+constexpr uint32_t PF_FILS_RAPIDE = 1024;   // slot decoder with each tile's DELTA: 32 tiles per block
+constexpr uint32_t PF_PAIRES_RAPIDE = 8;    // its tile pairs per wavefront (the LUT staging amortised over them)
 constexpr uint32_t PF_LOT_COPIE = 4;     // loads per thread in flight when a band is copied from a slot
 constexpr uint32_t PF_TOURS = 2;          // decode rounds per band: a band's tiles are at most 64
 constexpr uint32_t PF_RB_MAX = 80;         // rows per band
@@ -323,6 +326,58 @@ prefill_emplacements_codes(ParamsPrefill pp, const uint32_t* __restrict__ luts, 
     uint8_t* mat = reinterpret_cast<uint8_t*>(pp.emplacements + uint64_t(e) * pp.pas_emplacement + disp.base);
     codes_vers_emplacement<PF_FILS_CODES_SLOT>(m.codes, m.med, entete_de(m.codes, m.cP, m.cN, m.cT, m.cW), R, B, mat,
                                                disp, luts + (uint64_t(j) * 4u + 1u) * M, controle, s);
+}
+
+// Tiles whose DELTA the CODES pass decodes itself (N_codes = 16 with N_delta 1 or 2, 32 with 2):
+// matrix j = blockIdx.y of every chosen expert e = blockIdx.z decoded into its slot, scales and
+// codes in one pass, by the CODES pass's tile machinery (read one tile ahead, each tile's DELTA
+// decoded by its half-wavefront, entries in LDS; codes.hpp). The prologue issues the loads that do
+// not depend on the record first (the DELTA LUT, staged in LDS for the first tiles, and the decode
+// LUTs), then the record, then the first tiles' streams.
+extern "C" __global__ void __launch_bounds__(trc::PF_FILS_RAPIDE)
+prefill_emplacements_delta_interne(ParamsPrefill pp, const uint32_t* __restrict__ luts,
+                                   uint32_t* __restrict__ controle) {
+    using namespace trc;
+    __shared__ __attribute__((aligned(16384))) uint8_t lds[LDS_GEMV];
+    constexpr uint32_t FILS = PF_FILS_RAPIDE;
+    const uint32_t e = blockIdx.z, j = blockIdx.y;
+    if (uniforme32(reinterpret_cast<const uint32_t*>(pp.compte)[e]) == 0u) return;
+    const Grille g{FILS, uniforme32(gridDim.x)};
+    const uint32_t R = choisir(pp.lignes, j), C = choisir(pp.colonnes, j);
+    constexpr uint32_t LOT_D = (M / 4u + FILS - 1u) / FILS;  // 16-byte groups of the DELTA LUT per thread
+    u32x4 lutd_v[LOT_D];
+#pragma unroll
+    for (uint32_t k = 0; k < LOT_D; ++k)
+        lutd_v[k] = glob<u32x4>(luts + uint64_t(j) * 4u * M)[min(k * FILS + threadIdx.x, M / 4u - 1u)];
+    ChargeLutBloc<FILS> charge_lut;
+    charge_lut.demarrer(luts + (uint64_t(j) * 4u + 1u) * M);
+    const MatricePartie m = lire_matrice_constante(pp.repertoire + uint64_t(e * 3u + j) * sizeof(MatricePartie));
+    Tache tc{};
+    tc.lignes = R;
+    tc.colonnes = C;
+    tc.kmax = 0xFFFFFFFFu;  // no partial sums here
+    const PrepCodes p = preparer_codes(tc, m);
+    if (!p.bon) {  // uniform over the block; counted once here and once by the band kernels
+        if (blockIdx.x == 0 && threadIdx.x == 0) atomicAdd(&controle[CTL_FORMAT], 1u);
+        return;
+    }
+    const trc_disposition disp = disposition(dims_prefill(pp), j);
+    uint8_t* mat = reinterpret_cast<uint8_t*>(pp.emplacements + uint64_t(e) * pp.pas_emplacement + disp.base);
+    const Avance avance0 = premiere_avance<true>(p, R, g);
+    // issued here, ahead of the LDS staging below (which waits on the earlier loads only)
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    charge_lut.poser(reinterpret_cast<uint2*>(lds + LDS_LUT));
+#pragma unroll
+    for (uint32_t k = 0; k < LOT_D; ++k)
+        if (k * FILS + threadIdx.x < M / 4u)
+            *reinterpret_cast<u32x4*>(lds + LDS_ENT + 16u * (k * FILS + threadIdx.x)) = lutd_v[k];
+    if (uniforme32(p.hc.N) == 32u)
+        corps_codes_emplacement_n<32>(p, R, mat, mat + disp.echelles, lds, luts + uint64_t(j) * 4u * M, controle,
+                                      avance0, g);
+    else
+        corps_codes_emplacement_n<16>(p, R, mat, mat + disp.echelles, lds, luts + uint64_t(j) * 4u * M, controle,
+                                      avance0, g);
 }
 
 namespace trc {
@@ -842,8 +897,9 @@ uint64_t al(uint64_t x) { return (x + 255u) & ~uint64_t(255); }
 // fit the 64 tiles a block decodes in two rounds and whose codes, scales and partial sums fit the LDS;
 // 0 if none does. The more of the 64 tile slots a band fills, the fewer wavefronts idle in the second
 // round (gpt-oss rows: 80 rows are 56.25 tiles, 64 rows 45).
-// Long tiles (N > 16: bands copied from the slots, nothing decoded per band): the LDS alone decides.
-bool tuiles_longues(uint32_t N) { return N > trc::PF_NMAX; }
+// Tiles of 16 macro-steps or more (bands copied from the slots, nothing decoded per band): the LDS
+// alone decides.
+bool tuiles_longues(uint32_t N) { return N >= trc::PF_NMAX; }
 
 uint32_t rb_de(uint32_t B, uint32_t N) {
     for (const uint32_t rb : {trc::PF_RB_MAX, 64u, 32u, 16u})
@@ -995,7 +1051,18 @@ extern "C" int trc_prefill_moe(trc_vue repertoire, uint32_t experts, trc_vue lut
     const uint32_t Rm = D > R ? D : R;
     TRC_LANCER(prefill_grouper, dim3(1), dim3(1024), f, pp, ctl);
     TRC_LANCER(prefill_quant_x, dim3(T), dim3(trc::PF_Q_FILS), f, pp);
-    if (pp.emplacements != 0) {
+    if (pp.emplacements != 0 && trc::delta_dans_codes(n_delta, n_codes)) {
+        // every chosen expert decoded once into its slot, each tile's DELTA with it:
+        // PF_PAIRES_RAPIDE tile pairs per wavefront over the largest of the three matrices
+        uint32_t tc = 1;
+        for (int j = 0; j < 3; ++j) {
+            const uint64_t blocs = uint64_t(dims->lignes[j]) * (dims->colonnes[j] / 32);
+            tc = std::max<uint32_t>(tc, uint32_t(((blocs * 16 + 127) / 128 + n_codes - 1) / n_codes));
+        }
+        constexpr uint32_t tuiles_bloc = trc::PF_FILS_RAPIDE / 32 * trc::PF_PAIRES_RAPIDE;
+        TRC_LANCER(prefill_emplacements_delta_interne, dim3((tc + tuiles_bloc - 1) / tuiles_bloc, 3, experts),
+                   dim3(trc::PF_FILS_RAPIDE), f, pp, l, ctl);
+    } else if (pp.emplacements != 0) {
         // long tiles: every chosen expert decoded once into its slot (scales, then codes), grids of
         // tile pairs over the largest of the three matrices (the bodies loop over the tiles)
         uint32_t td = 1, tc = 1;
