@@ -902,6 +902,9 @@ def main():
     ap.add_argument("--distance-octets", type=float, default=512e6, dest="distance_octets",
                     help="config 3: compressed bytes of other parts read between two uses of an expert")
     ap.add_argument("--sans-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--graphe", type=int, default=0, metavar="N",
+                    help="configs 3 and 4: issue the timed steps as HIP graph replays of N steps each, captured "
+                         "before the timed region (0: one host call per step)")
     ap.add_argument("--budget-cpu", type=float, default=12.0, help="seconds of single-thread CPU baseline work")
     ap.add_argument("--calibrer-copie", action="store_true",
                     help="also run three plain 64 MiB device copies (counter calibration under rocprofv3 --pmc)")
@@ -1049,11 +1052,11 @@ def main():
     n_tr = fusion.taille_travail_couche(dims, E, k, args.n_codes)
     _tr, tr = espace(n_tr)
 
-    def jeton(t, ligne):
+    def jeton(t, ligne, f=None):
         """Token t of the sweep through the layer(s); its selection lands in row `ligne`."""
         for l, c in enumerate(couches):
             fz.couche_moe(c.vrep, E, c.vluts, dims, c.vr16, None, vx[t], k, vres, vi[ligne][l], vw[ligne][l],
-                          vctl, tr, args.n_delta, args.n_codes, f=flux)
+                          vctl, tr, args.n_delta, args.n_codes, f=flux if f is None else f)
 
     # The routing of the whole sweep, read from the product path itself (untimed), then the timed
     # schedule: tokens of the sweep in order, a token taken only if none of its experts (layer 0) was
@@ -1076,15 +1079,33 @@ def main():
 
     for s in range(args.warmup):
         jeton(hors_plan[s % len(hors_plan)], (args.steps + s) % n_sel)
+    graphes = []
+    if args.graphe > 0:
+        # the timed steps captured ahead (the same launches, arguments and order as the host calls)
+        s_cap = torch.cuda.Stream(device=dev)
+        s_cap.wait_stream(flux)
+        for g0 in range(0, args.steps, args.graphe):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=s_cap):
+                for s in range(g0, min(g0 + args.graphe, args.steps)):
+                    jeton(plan[s], s, f=s_cap)
+            graphes.append(g)
+        flux.wait_stream(s_cap)
     evincer()
     torch.cuda.synchronize()
     debut, fin = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     debut.record(flux)
-    for s in range(args.steps):
-        jeton(plan[s], s)
+    if graphes:
+        with torch.cuda.stream(flux):
+            for g in graphes:
+                g.replay()
+    else:
+        for s in range(args.steps):
+            jeton(plan[s], s)
     fin.record(flux)
     torch.cuda.synchronize()
     ms = debut.elapsed_time(fin)
+    del graphes
     assert (ctl.cpu().numpy() == 0).all(), f"control words {ctl.cpu().numpy()}"
     sel = sel_i[:args.steps, :, :k].cpu().numpy()
     octets_tok = sum(couches[l].utiles[sel[:, l, :]].sum(axis=1) for l in range(n_couches))
@@ -1153,7 +1174,9 @@ def main():
         "config": {"workload": workload, "experts": E, "k": k, "hidden": C, "layers": n_couches,
                    "n_codes": args.n_codes, "n_delta": args.n_delta,
                    "n_codes_per_matrix": list(args.n_codes_m), "n_delta_per_matrix": list(args.n_delta_m),
-                   "tokens": args.steps, "sweep_tokens": args.tokens, "mean_part_bytes": int(c0.utiles.mean())},
+                   "tokens": args.steps, "sweep_tokens": args.tokens, "mean_part_bytes": int(c0.utiles.mean()),
+                   "issue": (f"HIP graph replays of {args.graphe} steps, captured before the timed region"
+                             if args.graphe > 0 else "one host call per step (trc_couche_moe_fusionnee)")},
         "gbps_compressed": round(float(gbps), 1),
         "frac_hbm_layer": round(float(gbps / PIC_HBM), 4),
         "compressed_bytes_per_token": int(octets_tok.mean()),
