@@ -180,17 +180,18 @@ def test_wrappers_refuse_wrong_sizes_carte_rs_468():
 def test_prefill_refuses_unsupported_shapes_before_launching():
     """The batched prefill keeps a row's blocks in LDS (at most 4096 columns) and at most 16384
     (position, slot) pairs a call: other shapes are usage errors, returned before any HIP call. Any
-    CODES_CTX tile length is taken: up to 16 macro-steps the band kernels decode their tiles, longer
-    tiles (the reference encoder's 256, rans.rs:32) are decoded once per chosen expert into a slot
-    of the reference layout, which the workspace then holds for every expert of the layer."""
+    CODES_CTX tile length is taken: below 16 macro-steps the band kernels decode their tiles, tiles
+    of 16 or more (the bench's 16 and 32, the reference encoder's 256, rans.rs:32) are decoded once
+    per chosen expert into a slot of the reference layout, which the workspace then holds for every
+    expert of the layer."""
     from troncons_amd import fusion
 
     fz = fusion.Fusion()
     dims = DimsExpert.gpt_oss()
     v = VueCarte(1 << 20, 1 << 40)
-    court = fusion.taille_travail_prefill(dims, 128, 512, 4, 16)
+    court = fusion.taille_travail_prefill(dims, 128, 512, 4, 8)
     assert court > 0
-    for n in (17, 32, 256):
+    for n in (16, 17, 32, 256):
         long_ = fusion.taille_travail_prefill(dims, 128, 512, 4, n)
         assert long_ > court and long_ >= 128 * K.taille_emplacement(dims)
     assert fusion.taille_travail_prefill(dims, 128, 512, 4, 0) == 0
