@@ -1,8 +1,9 @@
 """GPU parity at the workloads' real sizes, through the C-ABI.
 
-- Config 3: the fused MoE layer over 128 resident gpt-oss-120b experts (N_delta 2, N_codes 16, the
-  bench's encoding: each tile's DELTA decoded inside the CODES kernels), 20 seeded tokens, some
-  with tied router rows and some with NaN rows. Indices
+- Config 3: the fused MoE layer over 128 resident gpt-oss-120b experts in the bench's encoding
+  (gate and up: CODES_CTX tiles of 32 macro-steps, DELTA tiles of 2; down: 16 and 1; each tile's
+  DELTA decoded inside the CODES kernels), 20 seeded tokens, some with tied router rows and some
+  with NaN rows. Indices
   must equal the oracle's routeur_topk on the oracle's router logits (reference gemv_f32 order),
   weights within 1e-6, and the residual within 1e-5 * max|change| of the f64 MLP chain computed from
   the uncompressed weights (and, for the first tokens, of the reference's own f32 chain).
@@ -33,7 +34,9 @@ from troncons_amd.noyaux import DimsExpert, VueCarte  # noqa: E402
 
 GPT = DimsExpert.gpt_oss()
 C_ = 2880
-E, KTOP, N = 128, 4, (2, 16)
+E, KTOP = 128, 4
+N_MATRICES = ((2, 2, 1), (32, 32, 16))  # (N_delta, N_codes) per matrix (gate, up, down): the bench's
+N = (1, 16)  # what the API calls take: the down matrix's, which size the workspace and choose the plan
 GRAINE = 2040
 TOL = 1e-5
 
@@ -47,7 +50,7 @@ class Pool:
     address table, the mounted directory, the LUTs, and the parts in host memory."""
 
     def __init__(self, fz):
-        self.c = codeur.CoucheSynthetique(GRAINE, 0, E, GPT, N_delta=N[0], N_codes=N[1])
+        self.c = codeur.CoucheSynthetique(GRAINE, 0, E, GPT, N_delta=N_MATRICES[0], N_codes=N_MATRICES[1])
         self.parts = [self.c.partie(e) for e in range(E)]
         tailles = np.array([p.size for p in self.parts], np.int64)
         self.tailles = tailles
@@ -145,7 +148,7 @@ def test_moe_layer_128_experts(fz, pool):
         routeur = _routeur_jeton(base, x, t)
         xd, res, rd = dev(x), dev(residu0), dev(_r16(routeur))
         idx, w, ctl = zeros(32), zeros(32), zeros(16)
-        print(f"config3 token {t}: 128 experts, k=4, N={N}", flush=True)
+        print(f"config3 token {t}: 128 experts, k=4, N={N_MATRICES}", flush=True)
         fz.couche_moe(vue(rep), E, vue(pool.luts), GPT, vue(rd), None, vue(xd), KTOP, vue(res), vue(idx), vue(w),
                       vue(ctl), vue(tr), *N)
         assert list(hote(ctl, np.uint32)) == [0, 0, 0, 0], t

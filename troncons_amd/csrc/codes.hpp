@@ -668,7 +668,8 @@ __device__ __forceinline__ void corps_codes_emplacement_n(const PrepCodes& p, ui
                     // lane v: words 4v .. 4v + 3 of the 4 macro-steps (macro-step v / 8, lanes 4 (v % 8) ..)
                     const u32x4 c = lire_lds<u32x4>(a_etage + 16u * v);
                     const uint32_t w = (m0 + m - 3u) * VOIES + 4u * v;
-                    if (tuile && w < mots_utiles) ecrire_global<u32x4>(codes + w, c);
+                    if (tuile && w < mots_utiles)  // read back by another launch: no reuse in the L2
+                        __builtin_nontemporal_store(c, reinterpret_cast<u32x4*>(codes + w));
                 }
             } else {
                 const uint32_t w = (m0 + m) * VOIES + v;
