@@ -811,7 +811,9 @@ typedef struct trc_diffusion trc_diffusion;
 int trc_diffusion_creer(const trc_couche_hote* couches, uint32_t n_couches, uint32_t experts, uint32_t k,
                         const trc_dims_expert* dims, uint32_t n_delta, uint32_t n_codes, trc_diffusion** sortie);
 /* Layer `couche` for x on the compute stream flux: residu += combine of its k experts; the chosen
- * indices are written to choisis[k] when it is not null. */
+ * indices are written to choisis[k] when it is not null. A layer that fails part-way (an index out
+ * of range in the mailbox, a launch error) leaves the engine refusing every later call, after its
+ * queued copies and launches have drained (fail-stop, as the reference engine). */
 int trc_diffusion_couche(trc_diffusion* m, uint32_t couche, trc_vue x, trc_vue residu, void* flux, uint32_t* choisis);
 /* Every layer in turn for one token (the same x, as trc_ordo_jeton). */
 int trc_diffusion_jeton(trc_diffusion* m, trc_vue x, trc_vue residu, void* flux);

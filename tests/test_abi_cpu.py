@@ -224,3 +224,37 @@ def test_driver_half_refuses_bad_arguments_before_any_hip_call():
     assert l.trc_evenement_ms_depuis(None, None, None) == 1
     assert l.trc_hote_allouer(None, 0, 0, C.byref(h), None, None) == 1
     assert l.trc_carte_allouer(None, 0, C.byref(V())) == 1
+
+
+def test_streamed_layer_engine_refuses_bad_arguments_before_any_hip_call():
+    """trc_diffusion_creer and trc_diffusion_couche check their arguments before the runtime is
+    touched: no layers, a top-k above the experts or above 8, shapes the fused path refuses, parts
+    not 16-byte aligned, a router too short, a null engine."""
+    from troncons_amd import diffusion as Df
+    l = Df._l()
+    dims = DimsExpert.gpt_oss()
+    E, k = 8, 4
+    dec = (C.c_uint64 * E)(*[4096 * e for e in range(E)])
+    tai = (C.c_uint64 * E)(*([4096] * E))
+    V = K._Vue
+    luts, routeur = V(1 << 20, 4 * 3 * 4 * 4096), V(1 << 24, 4 * E * 2880)
+    bonne = Df.CoucheHote(1 << 30, dec, tai, luts, routeur)
+    h = C.c_void_p()
+
+    def creer(couches, n, experts=E, kk=k, d=dims, nd=1, nc=16):
+        return l.trc_diffusion_creer(couches, n, experts, kk, C.byref(d), nd, nc, C.byref(h))
+
+    tab = (Df.CoucheHote * 1)(bonne)
+    assert creer(None, 0) == 1
+    assert creer(tab, 1, kk=0) == 1
+    assert creer(tab, 1, kk=9, experts=16) == 1
+    assert creer(tab, 1, experts=3, kk=4) == 1
+    assert creer(tab, 1, d=DimsExpert.de([2880, 2880, 2880], [2880, 2880, 2048])) == 1
+    assert creer(tab, 1, nc=0) == 1
+    mal = (Df.CoucheHote * 1)(Df.CoucheHote((1 << 30) + 8, dec, tai, luts, routeur))
+    assert creer(mal, 1) == 1 and b"align" in l.trc_derniere_erreur()
+    court = (Df.CoucheHote * 1)(Df.CoucheHote(1 << 30, dec, tai, luts, V(1 << 24, 16)))
+    assert creer(court, 1) == 1 and b"routeur" in l.trc_derniere_erreur()
+    assert h.value is None
+    assert l.trc_diffusion_couche(None, 0, V(1 << 20, 4 * 2880), V(1 << 21, 4 * 2880), None, None) == 1
+    assert l.trc_diffusion_jeton(None, V(1 << 20, 4 * 2880), V(1 << 21, 4 * 2880), None) == 1

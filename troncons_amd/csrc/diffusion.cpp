@@ -23,6 +23,7 @@
 #include <chrono>
 #include <cstring>
 #include <memory>
+#include <string>
 #include <vector>
 
 #include "commun.hpp"
@@ -76,6 +77,9 @@ struct trc_diffusion {
     uint32_t sequence = 0;
     uint64_t n_couches_faites = 0;
     trc_stats_diffusion st{};
+    // fail-stop, as the reference engine (which panics): after a layer failed part-way, copies and
+    // launches of it may still be in flight over the arrival buffers, so later layers are refused
+    bool en_echec = false;
 
     ~trc_diffusion() {
         for (auto& v : ev_arr)
@@ -217,10 +221,20 @@ extern "C" void trc_diffusion_detruire(trc_diffusion* m) {
 extern "C" int trc_diffusion_couche(trc_diffusion* m, uint32_t couche, trc_vue x, trc_vue residu, void* flux,
                                     uint32_t* choisis) {
     if (m == nullptr) return trc::usage("moteur nul");
+    if (m->en_echec) return trc::usage("moteur arrete par une erreur precedente");
     if (couche >= m->couches.size()) return trc::usage("couche %u sur %zu", couche, m->couches.size());
     if (x.adresse == 0 || x.octets < 4ull * m->C || x.adresse % 16 != 0) return trc::usage("x trop court ou non aligne");
     if (residu.adresse == 0 || residu.octets < 4ull * m->D) return trc::usage("residu trop court");
-    return m->couche(couche, x, residu, flux, choisis);
+    const int r = m->couche(couche, x, residu, flux, choisis);
+    if (r != TRC_OK) {
+        // drain what the failed layer queued, keep the error's message
+        const std::string message = trc_derniere_erreur();
+        (void)hipStreamSynchronize(m->copie);
+        (void)hipStreamSynchronize(reinterpret_cast<hipStream_t>(flux));
+        m->en_echec = true;
+        trc::derniere_erreur() = message;
+    }
+    return r;
 }
 
 extern "C" int trc_diffusion_jeton(trc_diffusion* m, trc_vue x, trc_vue residu, void* flux) {

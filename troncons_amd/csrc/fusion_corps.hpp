@@ -926,11 +926,16 @@ __device__ __forceinline__ void preparer_fins(const Taches& taches, uint32_t pre
 }
 
 
-// gpt-oss clamped SwiGLU in f64, one rounding (the reference swiglu_oai, passe.cuh:598-605).
+// gpt-oss clamped SwiGLU, the reference swiglu_oai's expression (passe.cuh:598-605): g <- min(g, 7),
+// u <- clamp(u, -7, 7), g / (1 + exp(-1.702 g)) * (u + 1), evaluated in f32 with the device
+// library's expf and IEEE division, a few ulp from the reference, which evaluates it in f64 and
+// rounds once (the reference-API kernel swiglu_oai does that too). Every fused path (the down
+// pass's prologue, fusion_finir_swiglu, the prefill's act pieces) takes this one, so their bits
+// agree with each other.
 __device__ __forceinline__ float swiglu_oai_f(float g, float u) {
-    const double gv = fmin(double(g), 7.0);
-    const double uv = fmin(fmax(double(u), -7.0), 7.0);
-    return float(gv / (1.0 + exp(-1.702 * gv)) * (uv + 1.0));
+    const float gv = fminf(g, 7.0f);
+    const float uv = fminf(fmaxf(u, -7.0f), 7.0f);
+    return gv / (1.0f + expf(-1.702f * gv)) * (uv + 1.0f);
 }
 
 }  // namespace trc
