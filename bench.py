@@ -788,7 +788,7 @@ def bench_modele(args, dims, flux):
     from troncons_amd.noyaux import ParamsRope
     h = Mo.Hyper(couches=args.couches, d=C_GPT, tetes=64, tetes_kv=8, experts=args.experts, actifs=args.k,
                  vocab=VOCAB_GPT, eps=1e-5, rope=ParamsRope.gpt_oss(), fenetre=128, contexte=4096, dims=dims,
-                 n_delta=args.n_delta, n_codes=args.n_codes)
+                 n_delta=args.n_delta, n_codes=args.n_codes, n_delta_gu=args.n_delta_gu, n_codes_gu=args.n_codes_gu)
     if args.steps + args.warmup > h.contexte:
         raise SystemExit(f"--steps + --warmup above the context of {h.contexte} positions")
     t0 = time.perf_counter()
@@ -825,7 +825,8 @@ def bench_modele(args, dims, flux):
                                "even layers windowed on 128, f16 KV; fused compressed MoE top-4 of 128), "
                                f"{h.vocab}-row Q8_0 head, argmax", "layers": h.couches, "hidden": h.d,
                    "experts": h.experts, "k": h.actifs, "vocab": h.vocab, "n_codes": h.n_codes,
-                   "n_delta": h.n_delta, "positions": f"0..{args.steps + args.warmup - 1}"},
+                   "n_delta": h.n_delta, "n_codes_per_matrix": list(args.n_codes_m),
+                   "n_delta_per_matrix": list(args.n_delta_m), "positions": f"0..{args.steps + args.warmup - 1}"},
         "bytes_per_token": {"attention_q8_0": int(attention), "head_q8_0": int(tete),
                             "experts_compressed_estimate": int(experts)},
         "gbps_effective": round((attention + tete + experts) / (us * 1e-6) / 1e9, 1),
@@ -930,10 +931,10 @@ def main():
     ap.add_argument("--n-delta", type=int, default=1, help="macro-steps per DELTA tile written by the encoder")
     ap.add_argument("--n-codes-gu", type=int, default=None, dest="n_codes_gu",
                     help="the same for the gate and up matrices (the format stores N per stream); default for "
-                         "configs 3 and 4 with the default 16 / 1: 32, else --n-codes")
+                         "configs 3, 4 and 6 with the default 16 / 1: 32, else --n-codes")
     ap.add_argument("--n-delta-gu", type=int, default=None, dest="n_delta_gu",
-                    help="the same for the gate and up matrices; default for configs 3 and 4 with the default "
-                         "16 / 1: 2, else --n-delta")
+                    help="the same for the gate and up matrices; default for configs 3, 4 and 6 with the "
+                         "default 16 / 1: 2, else --n-delta")
     ap.add_argument("--graine", type=int, default=2026)
     ap.add_argument("--tokens", type=int, default=1000, help="seeded activations of the sweep")
     ap.add_argument("--distance-octets", type=float, default=512e6, dest="distance_octets",
@@ -950,7 +951,7 @@ def main():
     # matrix's, which size the workspace and choose the launch plan
     # gate/up at 32 / 2 by default for the decode step (fewer tile starts in the larger launch; the
     # down launch keeps 16 / 1, whose tiles fill the chip's wavefronts)
-    defaut_gu = args.config in (3, 4) and args.n_codes == 16 and args.n_delta == 1 and not args.fichier
+    defaut_gu = args.config in (3, 4, 6) and args.n_codes == 16 and args.n_delta == 1 and not args.fichier
     if args.n_codes_gu is None:
         args.n_codes_gu = 32 if defaut_gu else args.n_codes
     if args.n_delta_gu is None:

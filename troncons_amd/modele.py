@@ -39,6 +39,10 @@ class Hyper:
     dt: int = 64
     n_delta: int = 4
     n_codes: int = 16
+    # the synthetic model's gate and up matrices at other tile lengths than down (None: the same);
+    # n_delta / n_codes, down's, are what the launches take
+    n_delta_gu: int | None = None
+    n_codes_gu: int | None = None
 
     def anneau(self, l: int) -> int:
         """lib.rs:140-143: the sliding window on even layers, the full cache on odd ones."""
@@ -90,7 +94,9 @@ def _ech(c: int) -> float:
 def couche_synthetique(h: Hyper, graine: int, l: int, rng) -> PoidsCouche:
     """Layer `l` of a seeded model: attention drawn from `rng`, experts coded by the encoder."""
     d, dq, dkv = h.d, h.dq, h.dkv
-    synth = codeur.CoucheSynthetique(graine, l, h.experts, h.dims, N_delta=h.n_delta, N_codes=h.n_codes)
+    nd = h.n_delta if h.n_delta_gu is None else (h.n_delta_gu, h.n_delta_gu, h.n_delta)
+    nc = h.n_codes if h.n_codes_gu is None else (h.n_codes_gu, h.n_codes_gu, h.n_codes)
+    synth = codeur.CoucheSynthetique(graine, l, h.experts, h.dims, N_delta=nd, N_codes=nc)
     routeur = (rng.standard_normal((h.experts, d)) * (1.0 / np.sqrt(d))).astype(np.float32)
     p = PoidsCouche(
         attn_norm=(1.0 + 0.1 * rng.standard_normal(d)).astype(np.float32),
