@@ -253,6 +253,59 @@ def test_fused_moe_layer_config3(fz, N):
     couche.liberer()
 
 
+def _couche_oracle(graine, E, k, x, avant, routeur):
+    """The reference layer step on the CPU: router logits, top-k, each chosen expert's MLP in the
+    reference's f32 order, the ordered combine into `avant`; also the f64 sum of the products."""
+    logits = O.gemv_f32(routeur, x)
+    oi, ow = O.routeur_topk(logits, k)
+    sorties, sorties64 = [], []
+    for e in oi:
+        bl, bi = codeur.synth_expert(graine, 0, int(e), GPT)
+        ex = type("E", (), {})()
+        ex.attendu = np.concatenate([O.blocs_vers_soa(bl[j], 2880, 2880, bi[j], canonique=True) for j in range(3)])
+        s, s64 = _mlp_oracle(ex, x, GPT)
+        sorties.append(s)
+        sorties64.append(s64)
+    ref = O.combiner(avant, np.concatenate(sorties), 2880, ow, k, 2880)
+    ref64 = avant.astype(np.float64) + sum(float(ow[i]) * sorties64[i] for i in range(k))
+    return oi, ow, ref, ref64
+
+
+@pytest.mark.parametrize("k", [1, 2, 6, 8])
+def test_fused_moe_layer_topk_sizes_and_reused_workspace(fz, k):
+    """The bench's encoding (gate and up 2/32, down 1/16) at top-1, 2, 6 and 8. The workspace starts
+    as 0xFF bytes and serves two steps in a row, the second adding into the first's residual with
+    another x: nothing in the step may depend on the workspace's earlier contents."""
+    E = 12
+    couche = codeur.CoucheSynthetique(2029, 0, E, GPT, N_delta=(2, 2, 1), N_codes=(32, 32, 16))
+    freqs = couche.freqs()
+    luts = O.luts_couche([[freqs[j][t] for t in range(4)] for j in range(3)])
+    parts = [dev(couche.partie(e)) for e in range(E)]
+    table = dev(np.array([p.data_ptr() for p in parts], np.uint64))
+    rep, ctl0 = zeros(fusion.taille_repertoire(E)), zeros(16)
+    fz.monter_couche(vue(table), E, GPT, vue(rep), vue(ctl0))
+    assert list(hote(ctl0, np.uint32)) == [0, 0, 0, 0]
+    routeur = np.stack([O.synth_normale_bf16(2029, 3, e, 2880, 0.02) for e in range(E)])
+    r16 = (routeur.view(np.uint32) >> 16).astype(np.uint16)
+    avant = O.synth_normale_bf16(2029, 5, 0, 2880, 1.0)
+    l, rd, res = dev(luts), dev(r16), dev(avant)
+    tr = dev(np.full(fusion.taille_travail_couche(GPT, E, k, 16), 0xFF, np.uint8))
+    for pas in range(2):
+        x = O.synth_normale_bf16(2029, 4, pas, 2880, 1.0)
+        xd = dev(x)
+        idx, w, ctl = zeros(32), zeros(32), zeros(16)
+        fz.couche_moe(vue(rep), E, vue(l), GPT, vue(rd), None, vue(xd), k, vue(res), vue(idx), vue(w), vue(ctl),
+                      vue(tr), 1, 16)
+        got = hote(res, np.float32).copy()
+        assert list(hote(ctl, np.uint32)) == [0, 0, 0, 0]
+        oi, ow, ref, ref64 = _couche_oracle(2029, E, k, x, avant, routeur)
+        assert (hote(idx, np.uint32)[:k] == oi).all() and np.abs(hote(w, np.float32)[:k] - ow).max() <= 1e-6
+        assert np.abs(got - ref).max() <= TOL * np.abs(ref).max(), (k, pas)
+        assert np.abs(got - ref64).max() <= TOL * np.abs(ref64).max(), (k, pas)
+        avant = got
+    couche.liberer()
+
+
 @pytest.mark.parametrize("N", [(16, 32), (2, 16)])
 def test_fused_moe_router_ties_and_order(fz, N):
     """The fused layer's top-k on tied logits: experts 2 and 9 get identical router rows, as do 5 and
