@@ -60,7 +60,8 @@ constexpr uint32_t ECHELLE_UN = 127u;     // E8M0 1.0
 
 constexpr uint32_t PF_FILS_RAPIDE = 1024;   // slot decoder with each tile's DELTA: 32 tiles per block
 constexpr uint32_t PF_PAIRES_RAPIDE = 8;    // its tile pairs per wavefront (the LUT staging amortised over them)
-constexpr uint32_t PF_LOT_COPIE = 4;     // loads per thread in flight when a band is copied from a slot
+constexpr uint32_t PF_LOT_COPIE = 8;     // 16-byte loads per thread in flight when a band is copied from a slot
+constexpr uint32_t PF_LOT_ECH = PF_LOT_COPIE / 4u;  // scale words with them (4 blocks per word)
 constexpr uint32_t PF_TOURS = 2;          // decode rounds per band: a band's tiles are at most 64
 constexpr uint32_t PF_RB_MAX = 80;         // rows per band
 constexpr uint32_t PF_RT_MAX = PF_RB_MAX / 16u;  // row tiles per band
@@ -578,17 +579,44 @@ __device__ __forceinline__ void prefill_bande(const ParamsPrefill& pp, const uin
     const uint32_t* lut_src = luts + (uint64_t(j) * 4u + 1u) * M;
     // long tiles: the band's codes and scales come from the expert's slot, nothing is decoded here
     constexpr bool depuis_emplacement = EMPL;
+    const uint32_t ba = r0 * B, bb = (r0 + nl) * B;  // the band's blocks
+    // the band's blocks [ba, bb) of the slot: 16 code bytes each (16-byte aligned), one scale byte
+    // each, read as the 4-byte words of the 256-aligned scale array that cover the band (the vector
+    // memory unit takes as long over a byte load as over a 16-byte one). The first batch (PF_LOT_COPIE
+    // 16-byte loads and PF_LOT_ECH words per thread: the whole band up to PF_LOT_COPIE * PF_FILS
+    // blocks) is requested before anything else, its stores wait until the LDS is free.
+    const uint32_t n_copie = nl * B;
+    const uint8_t* mat = EMPL ? reinterpret_cast<const uint8_t*>(pp.emplacements + uint64_t(e) * pp.pas_emplacement +
+                                                                 disposition(dims_prefill(pp), j).base)
+                              : nullptr;
+    const gptr<u32x4> codes_c = glob<u32x4>(EMPL ? mat + 16ull * ba : reinterpret_cast<const uint8_t*>(lut_src));
+    const gptr<uint32_t> ech32 =
+        glob<uint32_t>(EMPL ? mat + disposition(dims_prefill(pp), j).echelles : reinterpret_cast<const uint8_t*>(lut_src));
+    const uint32_t w0 = ba >> 2, nw = ((bb + 3u) >> 2) - w0;
+    u32x4 c_copie[EMPL ? PF_LOT_COPIE : 1u];
+    uint32_t e_copie[EMPL ? PF_LOT_ECH : 1u];
+    auto charger_copie = [&](uint32_t i0, uint32_t m0) {
+#pragma unroll
+        for (uint32_t k = 0; k < PF_LOT_COPIE; ++k) c_copie[k] = codes_c[min(i0 + threadIdx.x + k * PF_FILS, n_copie - 1u)];
+#pragma unroll
+        for (uint32_t k = 0; k < PF_LOT_ECH; ++k) e_copie[k] = ech32[w0 + min(m0 + threadIdx.x + k * PF_FILS, nw - 1u)];
+    };
+    if constexpr (EMPL) charger_copie(0u, 0u);
+    // the pieces count and the expert's first pair, requested with them (used after the decode)
+    const uint32_t p_brut = glob<uint32_t>(reinterpret_cast<const void*>(pp.pieces))[J == 2u ? 0 : 1];
+    const uint32_t debut_brut = glob<uint32_t>(reinterpret_cast<const void*>(pp.debut))[e];
     ChargeLut<3> charge_lut;
     if (!depuis_emplacement) charge_lut.demarrer(lut_src, 3u * M / 4u);
     const MatricePartie m = *reinterpret_cast<const MatricePartie*>(pp.repertoire + uint64_t(e * 3u + j) * sizeof(MatricePartie));
     const EnteteRans h = entete_de(m.codes, m.cP, m.cN, m.cT, m.cW);
     const uint32_t N = h.N;
-    const uint32_t ba = r0 * B, bb = (r0 + nl) * B;  // the band's blocks
     const uint32_t t_a = N ? (ba / 8u) / N : 0u, t_b = N ? ((bb - 1u) / 8u) / N : 0u;
     const bool bon = m.bon != 0u &&
                      (depuis_emplacement || (N >= 1u && N <= PF_NMAX && t_b < h.T && t_b - t_a < 32u * PF_TOURS));
     if (!depuis_emplacement) charge_lut.poser(lut_src, reinterpret_cast<uint2*>(lds + LDS_LUT), 3u * M / 4u);
-    if (!bon) {
+    // (long tiles: checked once the band is stored, so that the copy's loads are not held back
+    // behind the record's)
+    if (!depuis_emplacement && !bon) {
         if (blockIdx.x == 0 && threadIdx.x == 0) atomicAdd(&controle[CTL_FORMAT], 1u);
         return;
     }
@@ -619,8 +647,8 @@ __device__ __forceinline__ void prefill_bande(const ParamsPrefill& pp, const uin
     // the first batch of the first column tile's activations is requested now, so that its latency
     // hides behind the store of the codes
     const uint32_t lr = lane & 15u, lg = lane >> 4;
-    const uint32_t P = uniforme32(min(reinterpret_cast<const uint32_t*>(pp.pieces)[J == 2u ? 0 : 1], PF_PIECES_BF));
-    const uint32_t debut_e = uniforme32(reinterpret_cast<const uint32_t*>(pp.debut)[e]);
+    const uint32_t P = uniforme32(min(p_brut, PF_PIECES_BF));
+    const uint32_t debut_e = uniforme32(debut_brut);
     const uint32_t* paires = reinterpret_cast<const uint32_t*>(pp.paires);
     const uint64_t pas_p = uint64_t(J == 2u ? pp.bx : pp.bact) * 64u;
     const uint8_t* bsrc = reinterpret_cast<const uint8_t*>(J == 2u ? pp.xb : pp.ab) + 16u * lg;
@@ -661,44 +689,31 @@ __device__ __forceinline__ void prefill_bande(const ParamsPrefill& pp, const uin
     // ---- store the band's codes and scales
     const uint32_t a_sa = base + pf_sa(RB, B), a_part = base + pf_part(RB, B);
     const uint32_t haut = lane >= 32u ? 1u : 0u;
-    if (depuis_emplacement) {
-        // the band's blocks [ba, bb) of the slot: 16 code bytes each (16-byte aligned), one scale byte each
-        const trc_disposition disp = disposition(dims_prefill(pp), j);
-        const uint8_t* mat = reinterpret_cast<const uint8_t*>(pp.emplacements + uint64_t(e) * pp.pas_emplacement + disp.base);
-        // (batches of PF_LOT_COPIE loads per thread issued before their stores, and the scales as the
-        // 4-byte words of the 256-aligned scale array that cover the band: the vector memory unit
-        // takes as long over a byte load as over a 16-byte one)
-        const uint32_t n = nl * B;
-        const gptr<u32x4> codes = glob<u32x4>(mat + 16ull * ba);
-        for (uint32_t i0 = 0; i0 < n; i0 += PF_LOT_COPIE * PF_FILS) {
-            u32x4 c[PF_LOT_COPIE];
-#pragma unroll
-            for (uint32_t k = 0; k < PF_LOT_COPIE; ++k) c[k] = codes[min(i0 + threadIdx.x + k * PF_FILS, n - 1u)];
+    if constexpr (EMPL) {
+        for (uint32_t i0 = 0, m0 = 0; i0 < n_copie; i0 += PF_LOT_COPIE * PF_FILS, m0 += PF_LOT_ECH * PF_FILS) {
+            if (i0 > 0u) charger_copie(i0, m0);  // bands past one batch
 #pragma unroll
             for (uint32_t k = 0; k < PF_LOT_COPIE; ++k) {
                 const uint32_t i = i0 + threadIdx.x + k * PF_FILS;
-                if (i < n) ecrire_lds<u32x4>(base + PF_A + 16u * i, c[k]);
+                if (i < n_copie) ecrire_lds<u32x4>(base + PF_A + 16u * i, c_copie[k]);
             }
-        }
-        const gptr<uint32_t> ech32 = glob<uint32_t>(mat + disp.echelles);
-        const uint32_t w0 = ba >> 2, nw = ((bb + 3u) >> 2) - w0;
-        for (uint32_t i0 = 0; i0 < nw; i0 += PF_LOT_COPIE * PF_FILS) {
-            uint32_t e4[PF_LOT_COPIE];
 #pragma unroll
-            for (uint32_t k = 0; k < PF_LOT_COPIE; ++k) e4[k] = ech32[w0 + min(i0 + threadIdx.x + k * PF_FILS, nw - 1u)];
-#pragma unroll
-            for (uint32_t k = 0; k < PF_LOT_COPIE; ++k) {
-                const uint32_t i = i0 + threadIdx.x + k * PF_FILS;
+            for (uint32_t k = 0; k < PF_LOT_ECH; ++k) {
+                const uint32_t i = m0 + threadIdx.x + k * PF_FILS;
 #pragma unroll
                 for (uint32_t o = 0; o < 4u; ++o) {
                     const uint32_t blk = 4u * (w0 + i) + o;
-                    if (i < nw && blk >= ba && blk < bb) ecrire_lds<uint8_t>(a_sa + blk - ba, uint8_t(e4[k] >> (8u * o)));
+                    if (i < nw && blk >= ba && blk < bb) ecrire_lds<uint8_t>(a_sa + blk - ba, uint8_t(e_copie[k] >> (8u * o)));
                 }
             }
         }
     } else {
         poser_tour(tour0, t00 + haut, N, ba, bb, base, a_sa);
         poser_tour(tour1, t01 + haut, N, ba, bb, base, a_sa);
+    }
+    if (depuis_emplacement && !bon) {  // uniform over the block
+        if (blockIdx.x == 0 && threadIdx.x == 0) atomicAdd(&controle[CTL_FORMAT], 1u);
+        return;
     }
     // padding: rows nl .. RB - 1 of a last, partial band (zero codes, scale 1)
     for (uint32_t i = threadIdx.x; i < (RB - nl) * B; i += blockDim.x) {
