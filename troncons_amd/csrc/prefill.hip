@@ -819,7 +819,210 @@ __device__ __forceinline__ void prefill_bande(const ParamsPrefill& pp, const uin
     if (tt < n_tt) passe(tt, std::integral_constant<U2, 1>{}, std::false_type{});
 }
 
+// ------------------------------------------------- band kernels over the slots, two blocks per CU
+// Long tiles: every chosen expert sits decoded in its slot, so a band is a copy (one batch of loads,
+// issued first), then the MFMA passes. A block holds one band of PFE_RB rows with PFE_FILS threads
+// in under half the LDS, so that two blocks share a CU and one's copy and prologue run under the
+// other's MFMA passes and reductions. Same operands, k-steps and pass shapes as prefill_bande, with
+// 8 wavefronts: one column tile at a time splits K 8 ways, two at a time 4 ways each. Used for gate
+// and up (x: one bf16 piece); down, whose act has three pieces, reads 2.5 times the activation bytes
+// over bands of 32 rows and measured faster with prefill_bande's bands of 80 (289 against 407 us for
+// config 5, gate/up 433 against 463 us).
+constexpr uint32_t PFE_FILS = 512;
+constexpr uint32_t PFE_RB = 32;                  // rows per band: 2 row tiles
+constexpr uint32_t PFE_NRT = PFE_RB / 16u;
+constexpr uint32_t PFE_LOT = 8;                  // 16-byte code loads per thread: 4096 blocks a batch
+constexpr uint32_t PFE_LOT_ECH = PFE_LOT / 4u;   // scale words with them
+constexpr uint32_t PFE_PART = PFE_NRT * 4u * 64u * 16u;  // partial sums: row tiles x 4 waves x 64 lanes x 16 B
+constexpr uint32_t PFE_LDS = PFE_RB * PF_BP_MAX * 16u + PFE_RB * PF_BP_MAX + PFE_PART;
+static_assert(PFE_LDS <= LDS_GEMV / 2u, "two blocks per CU");
+
+template <uint32_t J>
+__device__ __forceinline__ void prefill_bande_empl(const ParamsPrefill& pp, uint32_t* __restrict__ controle, uint8_t* lds) {
+    constexpr uint32_t FILS = PFE_FILS, NRT = PFE_NRT, RB = PFE_RB;
+    const uint32_t e = blockIdx.y / J, j = J == 2u ? (blockIdx.y & 1u) : 2u;
+    const uint32_t n_e = uniforme32(reinterpret_cast<const uint32_t*>(pp.compte)[e]);
+    if (n_e == 0u) return;
+    const uint32_t R = choisir(pp.lignes, j), C = choisir(pp.colonnes, j), B = C / 32u;
+    const uint32_t r0 = blockIdx.x * RB;
+    if (r0 >= R) return;
+    const uint32_t nl = min(RB, R - r0);
+    const uint32_t ba = r0 * B, bb = (r0 + nl) * B;  // the band's blocks
+    // the band's blocks [ba, bb) of the slot (16 code bytes each) and the 4-byte words of the scale
+    // array that cover them, requested before anything else; stored once the pass is set up
+    const uint32_t n = nl * B;
+    const trc_disposition disp = disposition(dims_prefill(pp), j);
+    const uint8_t* mat = reinterpret_cast<const uint8_t*>(pp.emplacements + uint64_t(e) * pp.pas_emplacement + disp.base);
+    const gptr<u32x4> codes = glob<u32x4>(mat + 16ull * ba);
+    const gptr<uint32_t> ech32 = glob<uint32_t>(mat + disp.echelles);
+    const uint32_t w0 = ba >> 2, nw = ((bb + 3u) >> 2) - w0;
+    u32x4 c[PFE_LOT];
+    uint32_t e4[PFE_LOT_ECH];
+    auto charger_copie = [&](uint32_t i0, uint32_t m0) {
+#pragma unroll
+        for (uint32_t k = 0; k < PFE_LOT; ++k) c[k] = codes[min(i0 + threadIdx.x + k * FILS, n - 1u)];
+#pragma unroll
+        for (uint32_t k = 0; k < PFE_LOT_ECH; ++k) e4[k] = ech32[w0 + min(m0 + threadIdx.x + k * FILS, nw - 1u)];
+    };
+    charger_copie(0u, 0u);
+    const uint32_t p_brut = glob<uint32_t>(reinterpret_cast<const void*>(pp.pieces))[J == 2u ? 0 : 1];
+    const uint32_t debut_brut = glob<uint32_t>(reinterpret_cast<const void*>(pp.debut))[e];
+    const MatricePartie m = *reinterpret_cast<const MatricePartie*>(pp.repertoire + uint64_t(e * 3u + j) * sizeof(MatricePartie));
+    const uint32_t lane = __lane_id(), lr = lane & 15u, lg = lane >> 4;
+    const uint32_t wu = uniforme32(threadIdx.x >> 6);
+    const uint32_t base = adresse_lds(lds);
+    const uint32_t P = uniforme32(min(p_brut, PF_PIECES_BF));
+    const uint32_t debut_e = uniforme32(debut_brut);
+    const uint32_t* paires = reinterpret_cast<const uint32_t*>(pp.paires);
+    const uint64_t pas_p = uint64_t(J == 2u ? pp.bx : pp.bact) * 64u;
+    const uint8_t* bsrc = reinterpret_cast<const uint8_t*>(J == 2u ? pp.xb : pp.ab) + 16u * lg;
+    // Column tiles of 16 pairs go two at a time while two remain, waves 0-3 on the first and 4-7 on
+    // the second (K split 4 ways), then one at a time (K split 8 ways). The first batch of the first
+    // pass's activations is requested before the band is stored.
+    const uint32_t n_tt = (n_e + 15u) / 16u;
+    const bool duo0 = n_tt >= 2u;
+    const uint32_t g0 = duo0 ? wu >> 2 : 0u, wk0 = duo0 ? (wu & 3u) : wu;
+    const uint32_t tok0 = 16u * g0 + lr;
+    const uint32_t c0 = tok0 < n_e ? paires[debut_e + tok0] : paires[debut_e];
+    constexpr uint32_t LOT = J == 2u ? PF_LOT : 3u;
+    u32x4 pre[PF_LOT];
+    {
+        const uint8_t* src0 = bsrc + uint64_t(J == 2u ? c0 / pp.k : c0) * PF_PIECES_BF * pas_p;
+        auto charger0 = [&](auto np) {
+            constexpr uint32_t NP = decltype(np)::value;
+            if (duo0)
+                charger_b<NP, 4, LOT>(pre, src0, pas_p, wk0, B);
+            else
+                charger_b<NP, 8, LOT>(pre, src0, pas_p, wk0, B);
+        };
+        using U = uint32_t;
+        if (wk0 < B) {  // wave-uniform
+            if (P == 1u)
+                charger0(std::integral_constant<U, 1>{});
+            else if (P == 2u)
+                charger0(std::integral_constant<U, 2>{});
+            else if (P == 3u)
+                charger0(std::integral_constant<U, 3>{});
+        }
+    }
+    // ---- the band into LDS: codes [row][B][16 B], scales [row][B], zero padding rows
+    const uint32_t a_sa = base + pf_sa(RB, B), a_part = base + pf_part(RB, B);
+    for (uint32_t i0 = 0, m0 = 0; i0 < n || m0 < nw; i0 += PFE_LOT * FILS, m0 += PFE_LOT_ECH * FILS) {
+        if (i0 > 0u) charger_copie(i0, m0);  // bands past one batch
+#pragma unroll
+        for (uint32_t k = 0; k < PFE_LOT; ++k) {
+            const uint32_t i = i0 + threadIdx.x + k * FILS;
+            if (i < n) ecrire_lds<u32x4>(base + PF_A + 16u * i, c[k]);
+        }
+#pragma unroll
+        for (uint32_t k = 0; k < PFE_LOT_ECH; ++k) {
+            const uint32_t i = m0 + threadIdx.x + k * FILS;
+#pragma unroll
+            for (uint32_t o = 0; o < 4u; ++o) {
+                const uint32_t blk = 4u * (w0 + i) + o;
+                if (i < nw && blk >= ba && blk < bb) ecrire_lds<uint8_t>(a_sa + blk - ba, uint8_t(e4[k] >> (8u * o)));
+            }
+        }
+    }
+    if (m.bon == 0u) {  // uniform over the block; checked after the copy so that its loads go first
+        if (blockIdx.x == 0 && threadIdx.x == 0) atomicAdd(&controle[CTL_FORMAT], 1u);
+        return;
+    }
+    for (uint32_t i = threadIdx.x; i < (RB - nl) * B; i += FILS) {
+        const uint32_t o = nl * B + i;
+        ecrire_lds<u32x4>(base + PF_A + 16u * o, u32x4{0u, 0u, 0u, 0u});
+        ecrire_lds<uint8_t>(a_sa + o, uint8_t(ECHELLE_UN));
+    }
+    __syncthreads();
+
+    // ---- MFMA passes (as prefill_bande's, 8 wavefronts)
+    const float* biais = reinterpret_cast<const float*>(m.biais.p);
+    auto passe = [&](uint32_t tt, auto nt_t, auto premier) {
+        constexpr uint32_t NT = decltype(nt_t)::value;
+        constexpr bool PREMIER = decltype(premier)::value;
+        constexpr uint32_t PAS = 8u / NT, VG = 8u / NT;  // waves per tile
+        const uint32_t g = NT == 2u ? wu >> 2 : 0u, wk = NT == 2u ? (wu & 3u) : wu;
+        const uint32_t tok = 16u * (tt + g) + lr;
+        const uint32_t cl = PREMIER ? c0 : (tok < n_e ? paires[debut_e + tok] : paires[debut_e]);
+        const uint8_t* src = bsrc + uint64_t(J == 2u ? cl / pp.k : cl) * PF_PIECES_BF * pas_p;
+        f32x4 acc[PF_RT_MAX];
+#pragma unroll
+        for (uint32_t rt = 0; rt < PF_RT_MAX; ++rt) acc[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        auto produit = [&](auto np) {
+            constexpr uint32_t NP = decltype(np)::value;
+            produit_bf16<NP, NRT, PREMIER, PAS, LOT>(acc, src, pas_p, wk, B, base + PF_A, a_sa, lr, lg, pre);
+        };
+        using U = uint32_t;
+        if (P == 1u)
+            produit(std::integral_constant<U, 1>{});
+        else if (P == 2u)
+            produit(std::integral_constant<U, 2>{});
+        else if (P == 3u)
+            produit(std::integral_constant<U, 3>{});
+        // partial sums: [tile g][row tile][wave of the tile's first half][lane]. The second half of a
+        // tile's waves stores its sums, the first half adds them to its own and stores the results,
+        // which are added in wave order.
+        constexpr uint32_t MI = VG / 2u;
+        const bool second = wk >= MI;
+        const uint32_t wl = second ? wk - MI : wk;
+        const uint32_t a_moi = a_part + ((g * NRT * MI + wl) * 64u + lane) * 16u;  // row tile rt: + rt MI KiB
+        if (second) {
+#pragma unroll
+            for (uint32_t rt = 0; rt < NRT; ++rt) ecrire_lds<f32x4>(a_moi + rt * MI * 1024u, acc[rt]);
+        }
+        __syncthreads();
+        if (!second) {
+#pragma unroll
+            for (uint32_t rt = 0; rt < NRT; ++rt) {
+                const f32x4 autre = lire_lds<f32x4>(a_moi + rt * MI * 1024u);
+                ecrire_lds<f32x4>(a_moi + rt * MI * 1024u, acc[rt] + autre);
+            }
+        }
+        __syncthreads();
+        constexpr uint32_t TOURS_SOMME = (NT * NRT * 256u + FILS - 1u) / FILS;
+#pragma unroll
+        for (uint32_t u = 0; u < TOURS_SOMME; ++u) {
+            const uint32_t o = threadIdx.x + FILS * u;  // output (tile gg, row tile, column, row)
+            const uint32_t gg = NT == 2u ? o / (NRT * 256u) : 0u, reste_o = o - gg * (NRT * 256u);
+            if (gg < NT && reste_o < NRT * 256u) {
+                const uint32_t rt = reste_o >> 8, reste = reste_o & 255u;
+                const uint32_t ln = reste >> 2, r = reste & 3u;
+                float s = 0.0f;
+                for (uint32_t ww = 0; ww < MI; ++ww)
+                    s += lire_lds<float>(a_part + (((gg * NRT + rt) * MI + ww) * 64u + ln) * 16u + 4u * r);
+                const uint32_t ligne = 16u * rt + 4u * (ln >> 4) + r, jeton = 16u * (tt + gg) + (ln & 15u);
+                if (ligne < nl && jeton < n_e) {
+                    const uint32_t cc = paires[debut_e + jeton];
+                    const float y = s + biais[r0 + ligne];
+                    if (J == 2u)
+                        reinterpret_cast<float*>(pp.gu)[(uint64_t(cc) * 2u + j) * R + r0 + ligne] = y;
+                    else
+                        reinterpret_cast<float*>(pp.s)[uint64_t(cc) * pp.D + r0 + ligne] = y;
+                }
+            }
+        }
+        __syncthreads();
+    };
+    using U2 = uint32_t;
+    uint32_t tt = 0;
+    if (duo0) {
+        passe(0u, std::integral_constant<U2, 2>{}, std::true_type{});
+        tt = 2u;
+    } else {
+        passe(0u, std::integral_constant<U2, 1>{}, std::true_type{});  // n_e >= 1
+        tt = 1u;
+    }
+    for (; tt + 1u < n_tt; tt += 2u) passe(tt, std::integral_constant<U2, 2>{}, std::false_type{});
+    if (tt < n_tt) passe(tt, std::integral_constant<U2, 1>{}, std::false_type{});
+}
+
 }  // namespace trc
+
+extern "C" __global__ void __launch_bounds__(trc::PFE_FILS) __attribute__((amdgpu_waves_per_eu(4)))
+prefill_bande_gu_emplacement(ParamsPrefill pp, uint32_t* __restrict__ controle) {
+    __shared__ __attribute__((aligned(16))) uint8_t lds[trc::PFE_LDS];
+    trc::prefill_bande_empl<2>(pp, controle, lds);
+}
 
 extern "C" __global__ void __launch_bounds__(trc::PF_FILS)
 prefill_mfma_gu(ParamsPrefill pp, const uint32_t* __restrict__ luts, uint32_t* __restrict__ controle) {
@@ -833,13 +1036,8 @@ prefill_mfma_bas(ParamsPrefill pp, const uint32_t* __restrict__ luts, uint32_t* 
     trc::prefill_bande<1, false>(pp, luts, controle, lds);
 }
 
-// The same over long tiles: each band copied from its expert's slot.
-extern "C" __global__ void __launch_bounds__(trc::PF_FILS)
-prefill_mfma_gu_emplacement(ParamsPrefill pp, const uint32_t* __restrict__ luts, uint32_t* __restrict__ controle) {
-    __shared__ __attribute__((aligned(16384))) uint8_t lds[trc::LDS_GEMV];
-    trc::prefill_bande<2, true>(pp, luts, controle, lds);
-}
-
+// Down over long tiles: each band copied from its expert's slot (gate and up take
+// prefill_bande_gu_emplacement).
 extern "C" __global__ void __launch_bounds__(trc::PF_FILS)
 prefill_mfma_bas_emplacement(ParamsPrefill pp, const uint32_t* __restrict__ luts, uint32_t* __restrict__ controle) {
     __shared__ __attribute__((aligned(16384))) uint8_t lds[trc::LDS_GEMV];
@@ -1096,8 +1294,8 @@ extern "C" int trc_prefill_moe(trc_vue repertoire, uint32_t experts, trc_vue lut
         if (r != TRC_OK) return r;
     }
     if (pp.emplacements != 0)
-        TRC_LANCER(prefill_mfma_gu_emplacement, dim3((R + pp.rb[0] - 1) / pp.rb[0], 2 * experts), dim3(trc::PF_FILS), f,
-                   pp, l, ctl);
+        TRC_LANCER(prefill_bande_gu_emplacement, dim3((R + trc::PFE_RB - 1) / trc::PFE_RB, 2 * experts),
+                   dim3(trc::PFE_FILS), f, pp, ctl);
     else
         TRC_LANCER(prefill_mfma_gu, dim3((R + pp.rb[0] - 1) / pp.rb[0], 2 * experts), dim3(trc::PF_FILS), f, pp, l, ctl);
     TRC_LANCER(prefill_swiglu_quant, dim3(T * k), dim3(trc::PF_Q_FILS), f, pp);
