@@ -36,13 +36,15 @@ C_GPT = 2880
 
 
 FICHIER_PMC = RACINE / "profiles" / "moe_config3_pmc.md"
+FICHIER_PMC_PREFILL = RACINE / "profiles" / "prefill_config5_pmc.md"
 
 
-def trafic_mesure():
-    """HBM bytes per CODES launch (mean of the gate/up and down launches) from the committed counter
-    summary (two rocprofv3 --pmc runs, FETCH_SIZE then WRITE_SIZE, scaled by a copy kernel), or None."""
+def trafic_mesure(fichier=FICHIER_PMC):
+    """HBM bytes per launch of the bench's dominant kernel (config 3: mean of the gate/up and down
+    CODES launches; config 5: the slot decoder) from the committed counter summary (two rocprofv3
+    --pmc runs, FETCH_SIZE then WRITE_SIZE, scaled by a copy kernel), or None."""
     try:
-        for ligne in FICHIER_PMC.read_text().splitlines():
+        for ligne in fichier.read_text().splitlines():
             if ligne.startswith("traffic_per_launch_bytes"):
                 return int(ligne.split("=")[1])
     except (OSError, ValueError):
@@ -366,7 +368,15 @@ def bench_prefill(args, c0, dims, E, k, C, fz, flux, dev, espace, x_tok, n_fils,
     octets = int(c0.utiles[choisis].sum())
     octets_codes = int(c0.octets_codes[choisis].sum())
     flops = 2.0 * 3 * C * C * idx.size
-    t_mfma = (kern.get("prefill_mfma_gu", 0.0) + kern.get("prefill_mfma_bas", 0.0)) * 1e-6
+    # the MFMA launches: band kernels that decode their tiles (short tiles), or that copy their bands
+    # from the slots the slot decoder wrote (the bench's tile lengths)
+    t_mfma = sum(v for n, v in kern.items() if n.startswith(("prefill_mfma", "prefill_bande"))) * 1e-6
+    t_dec = kern.get("prefill_emplacements_delta_interne", 0.0) * 1e-6
+    # slot decoder: reads the chosen experts' CODES_CTX, DELTA and MEDIANES streams, writes their
+    # slots' code blocks (16 bytes) and scale bytes
+    octets_dec = int(c0.octets_codes[choisis].sum() + c0.octets_echelles[choisis].sum()
+                     + len(choisis) * sum(dims.lignes[j] * (dims.colonnes[j] // 32) * 17 for j in range(3)))
+    trafic_dec = trafic_mesure(FICHIER_PMC_PREFILL)
     ligne = {
         "metric": f"config5 us per {T}-position prefill batch (top-{k} of {E}, Zipf 1.1)",
         "value": round(us, 1), "unit": "us/batch", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -375,8 +385,8 @@ def bench_prefill(args, c0, dims, E, k, C, fz, flux, dev, espace, x_tok, n_fils,
         "dtype": "u32 rANS / bf16 MFMA (MXFP4 weights exact in bf16, activations in exact bf16 pieces), f32 accumulate",
         "data": "synthetic (seeded MXFP4 law A, E8M0 in [119,125], bf16 N(0,1) activations, Zipf(1.1) routing)",
         "config": {"workload": f"config5: batched prefill, {T} positions, top-{k} of {E} gpt-oss-120b experts "
-                               "(.trc v1.2 rANS-coded), each chosen expert decoded once into LDS, grouped GEMM "
-                               "on MFMA", "positions": T, "experts": E, "k": k,
+                               "(.trc v1.2 rANS-coded), each chosen expert decoded once (into its slot for tiles of "
+                               "16 or more macro-steps, else band by band into LDS), grouped GEMM on MFMA", "positions": T, "experts": E, "k": k,
                    "n_codes": args.n_codes, "n_delta": args.n_delta},
         "tokens_per_s": round(T / (us * 1e-6), 1),
         "experts_decoded": int(len(choisis)),
@@ -388,6 +398,17 @@ def bench_prefill(args, c0, dims, E, k, C, fz, flux, dev, espace, x_tok, n_fils,
         "bf16_pieces": {"x": int(pieces[0]), "act": int(pieces[1])},
         "kernel_us": kern,
         "roofline": {
+            "bound": "hbm", "kernel": "prefill_emplacements_delta_interne (the chosen experts decoded into slots)",
+            "achieved": round(octets_dec / t_dec / 1e9, 1), "peak": PIC_HBM, "unit": "GB/s",
+            "frac": round(octets_dec / t_dec / 1e9 / PIC_HBM, 4), "traffic": trafic_dec,
+            "traffic_source": (f"{FICHIER_PMC_PREFILL.relative_to(RACINE)}: rocprofv3 --pmc FETCH_SIZE then "
+                               "WRITE_SIZE per dispatch of the decoder, scaled by a 64 MiB copy kernel; not "
+                               "measured in this run"),
+            "bytes_per_launch": octets_dec, "avg_launch_us": round(t_dec * 1e6, 1),
+            "mfma_kernels_us": round(t_mfma * 1e6, 1),
+            "mfma_useful_tflops": round(flops / t_mfma / 1e12, 2) if t_mfma else None,
+            "mfma_peak_tflops": 2500.0,  # dense bf16
+        } if t_dec else {
             "bound": "hbm", "kernel": "prefill_mfma (gate/up launch + down launch: decode + MFMA)",
             "achieved": round(octets_codes / t_mfma / 1e9, 1) if t_mfma else None, "peak": PIC_HBM, "unit": "GB/s",
             "frac": round(octets_codes / t_mfma / 1e9 / PIC_HBM, 4) if t_mfma else None, "traffic": None,
