@@ -18,6 +18,7 @@ pytestmark = pytest.mark.gpu
 import oracle_ffi as O  # noqa: E402
 from gpu_outils import dev, hote, vue, zeros  # noqa: E402
 from troncons_amd import codeur, fusion  # noqa: E402
+from troncons_amd import noyaux as K  # noqa: E402
 from troncons_amd.noyaux import DimsExpert  # noqa: E402
 
 TOL = 1e-5
@@ -129,9 +130,12 @@ def test_prefill_small_layer_zipf_routing(fz, N):
     couche.c.liberer()
 
 
-def test_prefill_ragged_blocks(fz):
-    """Rows of 9 and 11 blocks (padded to 12 for the 4-block MFMA step), 288-wide layer."""
-    E, T, k, N = 5, 21, 3, (8, 8)
+@pytest.mark.parametrize("N", [(8, 8), (1, 16)])
+def test_prefill_ragged_blocks(fz, N):
+    """Rows of 9 and 11 blocks (padded to 12 for the 4-block MFMA step), 288-wide layer; with
+    N = (1, 16) the experts go through their slots (gate and up in bands of 32 rows: 11 and 9
+    bands)."""
+    E, T, k = 5, 21, 3
     dims = DimsExpert.de([352, 352, 288], [288, 288, 352])
     couche = Couche(fz, 41, E, dims, N)
     idx, w = _routage(42, T, E, k)
@@ -143,13 +147,13 @@ def test_prefill_ragged_blocks(fz):
     couche.c.liberer()
 
 
+@pytest.mark.parametrize("N", [(8, 8), (1, 16)])
 @pytest.mark.parametrize("bits", [24, 16])
-def test_prefill_f32_activations(fz, bits):
+def test_prefill_f32_activations(fz, bits, N):
     """x with full f32 significands (gate and up then take three bf16 pieces of x) or with 16-bit ones
-    (two pieces), on the ragged layer and on the small one."""
+    (two pieces), on the ragged layer and on the small one; N = (1, 16) takes the slot path."""
     for graine, dims, E, T, k in [(61, DimsExpert.de([352, 352, 288], [288, 288, 352]), 5, 21, 3),
                                   (71, DimsExpert.de([256, 256, 256], [256, 256, 256]), 6, 40, 4)]:
-        N = (8, 8)
         C = dims.colonnes[0]
         couche = Couche(fz, graine, E, dims, N)
         idx, w = _routage(graine + 1, T, E, k, zipf=1.1)
@@ -324,4 +328,47 @@ def test_prefill_delta_in_codes_gpt_oss_shape(fz, N):
     couche.parts[e0].copy_(torch.from_numpy(p))
     _, ctl = _lancer(fz, couche, E, GPT, x, idx, w, residu0, N)
     assert ctl[0] + ctl[2] > 0 and ctl[1] == 0, list(ctl)
+    couche.c.liberer()
+
+
+def _al(n):
+    return (n + 255) // 256 * 256
+
+
+@pytest.mark.parametrize("N", [(1, 16), (2, 16), (2, 32), ((2, 2, 1), (32, 32, 16)), (256, 256)])
+def test_prefill_slots_bit_exact(fz, N):
+    """The slot decoders' output itself, byte for byte: after a prefill whose routing chooses every
+    expert, each expert's slot in the workspace holds exactly the code bytes and E8M0 scales of the
+    oracle's canonical SoA slot (the reference decoder's output, -0 folded into +0). Tiles whose
+    DELTA the CODES pass decodes (16/1, 16/2, 32/2, the bench's per-matrix encoding: the decode
+    step's tile machinery) and the reference encoder's 256/256 (the generic slot decoders). The
+    slots follow the piece counters, the per-expert counts and starts and the pair list, each
+    256-byte aligned; the bias area of a slot is not written by the decoders and is not compared."""
+    E, T, k = 4, 8, 4
+    appel = tuple(n if isinstance(n, int) else n[2] for n in N)  # the call takes the down matrix's
+    couche = Couche(fz, 131, E, GPT, N)
+    idx = np.stack([np.random.default_rng(132 + i).permutation(E) for i in range(T)]).astype(np.uint32)
+    w = np.full((T, k), 0.25, np.float32)
+    x = np.stack([O.synth_normale_bf16(133, 4, i, 2880, 1.0) for i in range(T)])
+    xd, idd, wd, res = dev(x), dev(idx), dev(w), dev(np.zeros((T, 2880), np.float32))
+    ctl = zeros(16)
+    tr = zeros(fusion.taille_travail_prefill(GPT, E, T, k, appel[1]))
+    print(f"prefill slots: E={E} T={T} N={N}", flush=True)
+    fz.prefill_moe(vue(couche.rep), E, vue(couche.luts), GPT, vue(xd), T, vue(idd), vue(wd), k, vue(res), vue(ctl),
+                   vue(tr), *appel)
+    assert list(hote(ctl, np.uint32)) == [0, 0, 0, 0]
+    ws = hote(tr)
+    pas = K.taille_emplacement(GPT)
+    o = _al(16) + 2 * _al(4 * E) + _al(4 * T * k)
+    attendus = _slots(131, E, GPT)
+    for e in range(E):
+        slot = ws[o + e * pas:o + (e + 1) * pas]
+        for j in range(3):
+            d = O.disposition_j(list(GPT.lignes), list(GPT.colonnes), j)
+            nb = GPT.lignes[j] * (GPT.colonnes[j] // 32)
+            a = attendus[e][j]
+            # codes at the matrix's base, scales at its echelles offset (both in the oracle's layout)
+            assert (slot[d.base:d.base + 16 * nb] == a[:16 * nb]).all(), (e, j, "codes")
+            assert (slot[d.base + d.echelles:d.base + d.echelles + nb] == a[d.echelles:d.echelles + nb]).all(), \
+                (e, j, "scales")
     couche.c.liberer()
