@@ -329,13 +329,13 @@ __device__ __forceinline__ void codes_bloc(const trc::Taches& taches, const uint
         [copies ? min(r_copie, tc.lignes - 1u) : 0u];
     // SW: the gate and up records (scalar loads from the resolved records), for their checks
     bool sw_bon = false;
-    uint32_t sw_bpt = 128u;
+    uint32_t sw_lg = 7u;  // log2 of the gate/up tiles' block count (8 N_codes: 128 or 256)
     if (SW) {
         const MatricePartie mg = lire_matrice_constante(tg.matrice), mu = lire_matrice_constante(tu.matrice);
         const uint32_t Bg = tg.colonnes / 32u;
         sw_bon = mg.bon != 0 && mu.bon != 0 && (mg.cN == 16u || mg.cN == 32u) && mu.cN == mg.cN && Bg >= 8u &&
                  (Bg - 1u) / (8u * mg.cN) + 2u <= tg.kmax && tg.lignes >= R_sw && tu.lignes >= R_sw;
-        sw_bpt = 8u * mg.cN;
+        sw_lg = mg.cN == 32u ? 8u : 7u;
     }
     const Avance avance0 = premiere_avance<true>(p, tc.lignes, g);
     // issued here, ahead of the LDS staging below (which waits on the earlier loads only)
@@ -351,7 +351,7 @@ __device__ __forceinline__ void codes_bloc(const trc::Taches& taches, const uint
                 float v = 0.0f;
                 if (sw_bon) {
                     // somme_fin: p[0], + p[1] when the row reaches a second tile, then + bias
-                    const bool deux = (r * Bg + Bg - 1u) / sw_bpt != (r * Bg) / sw_bpt;
+                    const bool deux = (r * Bg + Bg - 1u) >> sw_lg != (r * Bg) >> sw_lg;
                     float sg = __uint_as_float(pg[q].x), su = __uint_as_float(pu[q].x);
                     if (deux) {
                         sg += __uint_as_float(pg[q].y);
@@ -467,35 +467,43 @@ fusion_finir_combiner(trc::Taches taches) {
     __shared__ Fin fins[TOPK_MAX];
     const ParamsMoe& moe = taches.moe;
     if ((taches.options & OPT_BIAIS) != 0u) {
+        // KM: the jobs loaded per row, 4 for a top-4 (or less) layer, else TOPK_MAX
+        auto combiner = [&](auto km) {
 #pragma clang fp contract(off)
-        const uint32_t D = moe.lignes[2], Rm = max(moe.lignes[0], moe.lignes[2]);
-        const uint32_t r = blockIdx.x * 256u + threadIdx.x, rr = min(r, D - 1u);
-        const float res = reinterpret_cast<const float*>(moe.residu)[rr];
-        u32x2 p[TOPK_MAX];
-        float bi[TOPK_MAX], w[TOPK_MAX];
+            constexpr uint32_t KM = decltype(km)::value;
+            const uint32_t D = moe.lignes[2], Rm = max(moe.lignes[0], moe.lignes[2]);
+            const uint32_t r = blockIdx.x * 256u + threadIdx.x, rr = min(r, D - 1u);
+            const float res = reinterpret_cast<const float*>(moe.residu)[rr];
+            u32x2 p[KM];
+            float bi[KM], w[KM];
 #pragma unroll
-        for (uint32_t i = 0; i < TOPK_MAX; ++i) {
-            const uint32_t ii = min(i, moe.k - 1u);
-            p[i] = *glob<u32x2>(reinterpret_cast<const void*>(tache_moe(moe, ii, 2u).partiels + 8ull * rr));
-            bi[i] = glob<float>(reinterpret_cast<const void*>(moe.biais))[uint64_t(ii * 3u + 2u) * Rm + rr];
-            w[i] = glob<float>(reinterpret_cast<const void*>(moe.poids))[ii];
-        }
-        preparer_fins(taches, 0, moe.k, fins);
-        if (r >= D) return;
-        for (uint32_t i = 0; i < moe.k; ++i)
-            if (!fins[i].bon || r >= fins[i].lignes || fins[i].kmax != 2u) return;
-        float s = 0.0f;
-#pragma unroll
-        for (uint32_t i = 0; i < TOPK_MAX; ++i) {
-            if (i < moe.k) {
-                float si = __uint_as_float(p[i].x);
-                if (partiels_en_plus(fins[i], r) >= 1u) si += __uint_as_float(p[i].y);
-                si = si + bi[i];
-                const float pr = w[i] * si;
-                s = i == 0 ? pr : s + pr;
+            for (uint32_t i = 0; i < KM; ++i) {
+                const uint32_t ii = min(i, moe.k - 1u);
+                p[i] = *glob<u32x2>(reinterpret_cast<const void*>(tache_moe(moe, ii, 2u).partiels + 8ull * rr));
+                bi[i] = glob<float>(reinterpret_cast<const void*>(moe.biais))[uint64_t(ii * 3u + 2u) * Rm + rr];
+                w[i] = glob<float>(reinterpret_cast<const void*>(moe.poids))[ii];
             }
-        }
-        reinterpret_cast<float*>(moe.residu)[r] = res + s;
+            preparer_fins(taches, 0, moe.k, fins);
+            if (r >= D) return;
+            for (uint32_t i = 0; i < moe.k; ++i)
+                if (!fins[i].bon || r >= fins[i].lignes || fins[i].kmax != 2u) return;
+            float s = 0.0f;
+#pragma unroll
+            for (uint32_t i = 0; i < KM; ++i) {
+                if (i < moe.k) {
+                    float si = __uint_as_float(p[i].x);
+                    if (partiels_en_plus(fins[i], r) >= 1u) si += __uint_as_float(p[i].y);
+                    si = si + bi[i];
+                    const float pr = w[i] * si;
+                    s = i == 0 ? pr : s + pr;
+                }
+            }
+            reinterpret_cast<float*>(moe.residu)[r] = res + s;
+        };
+        if (moe.k <= 4u)  // uniform
+            combiner(std::integral_constant<uint32_t, 4>{});
+        else
+            combiner(std::integral_constant<uint32_t, TOPK_MAX>{});
         return;
     }
     preparer_fins(taches, 0, moe.k, fins);

@@ -885,9 +885,16 @@ struct Fin {
     uint32_t bon;
 };
 
-// The partial sums of row r after its first: tiles (rB + B - 1) / bpt - rB / bpt.
+// The partial sums of row r after its first: tiles (rB + B - 1) / bpt - rB / bpt (shifts when the
+// tiles hold a power-of-two number of blocks, as every CODES_CTX tile of 16 or 32 macro-steps does;
+// the test is uniform).
 __device__ __forceinline__ uint32_t partiels_en_plus(const Fin& f, uint32_t r) {
-    return (r * f.B + f.B - 1u) / f.bpt - (r * f.B) / f.bpt;
+    const uint32_t a = r * f.B, b = a + f.B - 1u;
+    if ((f.bpt & (f.bpt - 1u)) == 0u) {
+        const uint32_t lg = uint32_t(__builtin_ctz(f.bpt));
+        return (b >> lg) - (a >> lg);
+    }
+    return b / f.bpt - a / f.bpt;
 }
 
 // Whole wavefront (uniform job).
