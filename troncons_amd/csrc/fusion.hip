@@ -542,7 +542,14 @@ __device__ __forceinline__ void routeur_lignes(const uint16_t* __restrict__ W, c
         if (blockIdx.x == 0)
             for (uint32_t i = threadIdx.x; i < C4; i += blockDim.x) reinterpret_cast<f32x4*>(h2)[i] = xs[i];
     } else if (X_LDS) {
-        for (uint32_t i = threadIdx.x; i < C4; i += blockDim.x) xs[i] = xg[i];
+        // every load of x first, then the stores: one round trip (C <= X_LDS_MAX, 256 threads)
+        constexpr uint32_t NX = (X_LDS_MAX / 4u + 255u) / 256u;
+        f32x4 xv[NX];
+#pragma unroll
+        for (uint32_t k = 0; k < NX; ++k) xv[k] = xg[min(threadIdx.x + 256u * k, C4 - 1u)];
+#pragma unroll
+        for (uint32_t k = 0; k < NX; ++k)
+            if (threadIdx.x + 256u * k < C4) xs[threadIdx.x + 256u * k] = xv[k];
         __syncthreads();
     }
     float acc = 0.0f;
