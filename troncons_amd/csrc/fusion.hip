@@ -203,14 +203,17 @@ constexpr uint32_t OPT_TOPK = 2u;
 // up copies and the combine the down ones: their loads then need no record first.
 constexpr uint32_t OPT_BIAIS = 4u;
 
-template <uint32_t FILS, bool SW = false>
+// SW: the MoE down launch (TACHES_MOE_BAS with OPT_BIAIS); GU: the MoE gate/up launch
+// (TACHES_MOE_GU with OPT_TOPK | OPT_BIAIS). Both know their jobs' mode and options at compile time,
+// so that no read of them precedes the prologue's first loads.
+template <uint32_t FILS, bool SW = false, bool GU = false>
 __device__ __forceinline__ void codes_bloc(const trc::Taches& taches, const uint32_t* __restrict__ luts,
                                            uint32_t* __restrict__ controle) {
     using namespace trc;
     __shared__ __attribute__((aligned(16384))) uint8_t lds[LDS_GEMV];
     const Grille g{FILS, uniforme32(gridDim.x)};
-    const bool topk = (taches.options & OPT_TOPK) != 0u;
-    const uint32_t j = topk ? (blockIdx.y & 1u) : min(uniforme32(taches[blockIdx.y].j), 2u);
+    const bool topk = GU || (!SW && (taches.options & OPT_TOPK) != 0u);
+    const uint32_t j = SW ? 2u : (topk ? (blockIdx.y & 1u) : min(uniforme32(taches[blockIdx.y].j), 2u));
     const uint32_t* lut_src = luts + (uint64_t(j) * 4u + 1u) * M;
     const ParamsMoe& pm = taches.moe;
     // The prologue is a chain of dependent device-memory reads (logits -> top-k -> the expert's
@@ -233,7 +236,8 @@ __device__ __forceinline__ void codes_bloc(const trc::Taches& taches, const uint
             [topk ? 32u * (3u * min(threadIdx.x, pm.E - 1u) + j) : 0u];
     ChargeLutBloc<FILS> charge_lut;
     charge_lut.demarrer(lut_src);
-    const Tache tx = topk ? uniforme(tache_moe_e(pm, blockIdx.y >> 1, j, 0u)) : uniforme(taches[blockIdx.y]);
+    const Tache tx = topk ? uniforme(tache_moe_e(pm, blockIdx.y >> 1, j, 0u))
+                          : (SW ? uniforme(tache_moe(pm, blockIdx.y, 2u)) : uniforme(taches[blockIdx.y]));
     const bool x_lds = tx.colonnes <= X_LDS_MAX && (SW || tx.x != 0);
     const uint32_t n16 = x_lds ? tx.colonnes / 4u : 0u;
     const gptr<u32x4> x_src = glob<u32x4>(x_lds && !SW ? reinterpret_cast<const void*>(tx.x) : reinterpret_cast<const void*>(luts));
@@ -249,7 +253,7 @@ __device__ __forceinline__ void codes_bloc(const trc::Taches& taches, const uint
     const uint32_t R_sw = tx.colonnes;  // gate/up rows = down columns
     u32x2 pg[SW ? SW_Q : 1], pu[SW ? SW_Q : 1];
     float bg[SW ? SW_Q : 1], bu[SW ? SW_Q : 1];
-    const bool copies = (taches.options & OPT_BIAIS) != 0u;
+    const bool copies = SW || GU || (taches.options & OPT_BIAIS) != 0u;
     const uint32_t Rm_moe = max(pm.lignes[0], pm.lignes[2]);
     if (SW) {
         // the biases come from the gate/up pass's copies (SW launches carry OPT_BIAIS), loaded here
@@ -273,9 +277,13 @@ __device__ __forceinline__ void codes_bloc(const trc::Taches& taches, const uint
     Tache tc;
     if (topk) {
         // the top-k in the entry area (free until the tiles start)
+        // every thread stores its logit (threads past E a copy of logit E - 1, never read): a store
+        // under a condition would let the compiler move the logits' load down to it, behind the LUT
+        // loads, whose completion the top-k would then wait for
+        static_assert(4u * FILS + 4u * TOPK_MAX <= 32u * ENT_PAR_TUILE * 4u, "logits and choices in the entry area");
         float* lg = reinterpret_cast<float*>(lds + LDS_ENT);
-        uint32_t* choisis = reinterpret_cast<uint32_t*>(lds + LDS_ENT + 4u * EXPERTS_MAX);
-        if (threadIdx.x < pm.E) lg[threadIdx.x] = lg_v;
+        uint32_t* choisis = reinterpret_cast<uint32_t*>(lds + LDS_ENT + 4u * FILS);
+        lg[threadIdx.x] = lg_v;
         if (threadIdx.x < TOPK_MAX) choisis[threadIdx.x] = 0xFFFFFFFFu;
         barriere_lds();
         choisir_topk(lg, pm.E, pm.k, choisis, FILS);
@@ -387,6 +395,11 @@ __device__ __forceinline__ void codes_bloc(const trc::Taches& taches, const uint
 extern "C" __global__ void __launch_bounds__(1024)
 fusion_codes(trc::Taches taches, const uint32_t* __restrict__ luts, uint32_t* __restrict__ controle) {
     codes_bloc<1024>(taches, luts, controle);
+}
+// The MoE gate/up launch with bias copies (TACHES_MOE_GU, OPT_TOPK | OPT_BIAIS), 1024-thread blocks.
+extern "C" __global__ void __launch_bounds__(1024)
+fusion_codes_gu(trc::Taches taches, const uint32_t* __restrict__ luts, uint32_t* __restrict__ controle) {
+    codes_bloc<1024, false, true>(taches, luts, controle);
 }
 extern "C" __global__ void __launch_bounds__(512)
 fusion_codes_512(trc::Taches taches, const uint32_t* __restrict__ luts, uint32_t* __restrict__ controle) {
@@ -1027,7 +1040,10 @@ int couche_moe(trc_vue repertoire, uint32_t experts, trc_vue luts, const trc_dim
         if (copies) {
             const Taches gu_c = par_moe(pm, trc::TACHES_MOE_GU, OPT_TOPK | OPT_BIAIS),
                          bas_c = par_moe(pm, trc::TACHES_MOE_BAS, OPT_BIAIS);
-            TRC_LANCER_CODES("fusion_codes/gate_up", fgu, f, gu_c, l, ctl);
+            if (fgu.bloc.x == 1024)
+                TRC_LANCER_N("fusion_codes/gate_up", fusion_codes_gu, fgu.grille, fgu.bloc, f, gu_c, l, ctl);
+            else
+                TRC_LANCER_CODES("fusion_codes/gate_up", fgu, f, gu_c, l, ctl);
             TRC_LANCER_N("fusion_codes/down", fusion_codes_swiglu, fb.grille, fb.bloc, f, bas_c, l, ctl);
             TRC_LANCER(fusion_finir_combiner, dim3((D + 255) / 256), dim3(256), f, bas_c);
             return TRC_OK;
