@@ -193,7 +193,7 @@ fusion_gemv(trc::Taches taches, const uint32_t* __restrict__ luts, uint32_t* __r
 // CODES pass with each tile's DELTA decoded in the kernel (codes.hpp; streams with N_codes = 16 and
 // N_delta 1 or 2), x in LDS. MoE gate/up launches with OPT_TOPK run the router's top-k first (every
 // block, by ranks over the logits: the reference's order and tie rule, deterministic, so all blocks
-// agree; block (0, 0) publishes indices and weights), take their expert's matrix from the directory
+// agree; one wavefront publishes indices and weights), take their expert's matrix from the directory
 // and publish the selected experts' three records (resolus) for the down pass and the combine.
 // Down launches read x from the experts' SwiGLU rows (fusion_finir_swiglu) or, with SW
 // (fusion_codes_swiglu), build it themselves in their prologue.
@@ -288,23 +288,35 @@ __device__ __forceinline__ void codes_bloc(const trc::Taches& taches, const uint
         barriere_lds();
         choisir_topk(lg, pm.E, pm.k, choisis, FILS);
         barriere_lds();
-        if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x < 64u) {
-            float w[TOPK_MAX];
-            poids_topk(lg, choisis, pm.k, w);
-            if (threadIdx.x < pm.k) {
-                float wr = w[0];
-#pragma unroll
-                for (uint32_t r = 1; r < TOPK_MAX; ++r) wr = threadIdx.x == r ? w[r] : wr;
-                typedef __attribute__((address_space(1))) uint32_t* GU32;
-                typedef __attribute__((address_space(1))) float* GF32;
-                ((GU32)(pm.indices))[threadIdx.x] = choisis[threadIdx.x];
-                ((GF32)(pm.poids))[threadIdx.x] = wr;
-            }
+        // indices and weights: one wavefront, the last of the first matrix's last block (the tile
+        // schedule leaves it without a tile pair when the matrix has fewer pairs than wavefronts),
+        // reads the chosen experts and their logits before the barrier and computes the f64 softmax
+        // after it, so that no other wavefront waits for it
+        const bool poids_ici = blockIdx.y == 0 && blockIdx.x == g.blocs_x - 1u && (threadIdx.x >> 6) == FILS / 64u - 1u;
+        uint32_t ch = 0xFFFFFFFFu;
+        float choisi[TOPK_MAX];
+        if (poids_ici) {  // wave-uniform
+            ch = choisis[min(__lane_id(), TOPK_MAX - 1u)];
+            logits_choisis(lg, choisis, pm.k, choisi);
         }
         const uint32_t i = blockIdx.y >> 1;
         const uint32_t e = uniforme32(choisis[i]);
         // every wave has read the top-k from the entry area before any overwrites it
         barriere_lds();
+        if (poids_ici) {
+            float w[TOPK_MAX];
+            poids_de_logits(choisi, pm.k, w);
+            const uint32_t v = __lane_id();
+            if (v < pm.k) {
+                float wr = w[0];
+#pragma unroll
+                for (uint32_t r = 1; r < TOPK_MAX; ++r) wr = v == r ? w[r] : wr;
+                typedef __attribute__((address_space(1))) uint32_t* GU32;
+                typedef __attribute__((address_space(1))) float* GF32;
+                ((GU32)(pm.indices))[v] = ch;
+                ((GF32)(pm.poids))[v] = wr;
+            }
+        }
         tc = uniforme(tache_moe_e(pm, i, j, e));
         // the selected experts' records for the later passes (gate with down, and up), read with
         // scalar loads from the directory, which nothing writes during the step

@@ -121,12 +121,15 @@ __device__ __forceinline__ void choisir_topk(const float* lg, uint32_t E, uint32
     }
 }
 
-// The weights of topk_vague from the chosen experts' logits (same f64 softmax, one rounding each).
-__device__ __forceinline__ void poids_topk(const float* lg, const uint32_t* choisis, uint32_t k,
-                                           float (&poids)[TOPK_MAX]) {
-    float choisi[TOPK_MAX];
+// The chosen experts' logits in rank order (-inf past k or past the non-NaN logits).
+__device__ __forceinline__ void logits_choisis(const float* lg, const uint32_t* choisis, uint32_t k,
+                                               float (&choisi)[TOPK_MAX]) {
 #pragma unroll
     for (uint32_t r = 0; r < TOPK_MAX; ++r) choisi[r] = (r < k && choisis[r] != 0xFFFFFFFFu) ? lg[choisis[r]] : -INFINITY;
+}
+
+// The weights of topk_vague from the chosen experts' logits (same f64 softmax, one rounding each).
+__device__ __forceinline__ void poids_de_logits(const float (&choisi)[TOPK_MAX], uint32_t k, float (&poids)[TOPK_MAX]) {
     double e[TOPK_MAX];
     const double m = choisi[0];
     double z = 0.0;
@@ -140,6 +143,13 @@ __device__ __forceinline__ void poids_topk(const float* lg, const uint32_t* choi
     }
 #pragma unroll
     for (uint32_t r = 0; r < TOPK_MAX; ++r) poids[r] = r < k ? float(e[r] / z) : 0.0f;
+}
+
+__device__ __forceinline__ void poids_topk(const float* lg, const uint32_t* choisis, uint32_t k,
+                                           float (&poids)[TOPK_MAX]) {
+    float choisi[TOPK_MAX];
+    logits_choisis(lg, choisis, k, choisi);
+    poids_de_logits(choisi, k, poids);
 }
 
 }  // namespace trc
