@@ -275,6 +275,7 @@ __device__ __forceinline__ void codes_bloc(const trc::Taches& taches, const uint
         for (uint32_t i = 0; i < 4; ++i) xv[i] = x_src[min(threadIdx.x + i * FILS, n16 > 0u ? n16 - 1u : 0u)];
     }
     Tache tc;
+    uint32_t e_choisi = 0xFFFFFFFFu;  // topk: the block's chosen expert
     if (topk) {
         // the top-k in the entry area (free until the tiles start)
         // every thread stores its logit (threads past E a copy of logit E - 1, never read): a store
@@ -293,10 +294,11 @@ __device__ __forceinline__ void codes_bloc(const trc::Taches& taches, const uint
         // reads the chosen experts and their logits before the barrier and computes the f64 softmax
         // after it, so that no other wavefront waits for it
         const bool poids_ici = blockIdx.y == 0 && blockIdx.x == g.blocs_x - 1u && (threadIdx.x >> 6) == FILS / 64u - 1u;
-        uint32_t ch = 0xFFFFFFFFu;
+        uint32_t ch = 0xFFFFFFFFu, ch3 = 0xFFFFFFFFu;
         float choisi[TOPK_MAX];
         if (poids_ici) {  // wave-uniform
             ch = choisis[min(__lane_id(), TOPK_MAX - 1u)];
+            ch3 = choisis[min(__lane_id() / 3u, TOPK_MAX - 1u)];
             logits_choisis(lg, choisis, pm.k, choisi);
         }
         const uint32_t i = blockIdx.y >> 1;
@@ -304,9 +306,24 @@ __device__ __forceinline__ void codes_bloc(const trc::Taches& taches, const uint
         // every wave has read the top-k from the entry area before any overwrites it
         barriere_lds();
         if (poids_ici) {
+            // the selected experts' records for the later passes: lane l < 3k copies the directory's
+            // record (expert l / 3, matrix l % 3) to resolus (the directory is not written during
+            // the step; an index past the experts gets a zero record, bon = 0)
+            const uint32_t v = __lane_id(), ir = v / 3u, jr = v - 3u * ir;
+            if (v < 3u * pm.k) {
+                const gptr<u32x4> src = glob<u32x4>(reinterpret_cast<const void*>(
+                    pm.repertoire + uint64_t(min(ch3, pm.E - 1u) * 3u + jr) * sizeof(MatricePartie)));
+                u32x4 q[sizeof(MatricePartie) / 16u];
+#pragma unroll
+                for (uint32_t k = 0; k < sizeof(MatricePartie) / 16u; ++k)
+                    q[k] = ch3 < pm.E ? src[k] : u32x4{0u, 0u, 0u, 0u};
+                typedef __attribute__((address_space(1))) u32x4* GU32X4;
+                GU32X4 dst = (GU32X4)(pm.resolus + uint64_t(ir * 3u + jr) * sizeof(MatricePartie));
+#pragma unroll
+                for (uint32_t k = 0; k < sizeof(MatricePartie) / 16u; ++k) dst[k] = q[k];
+            }
             float w[TOPK_MAX];
             poids_de_logits(choisi, pm.k, w);
-            const uint32_t v = __lane_id();
             if (v < pm.k) {
                 float wr = w[0];
 #pragma unroll
@@ -318,21 +335,40 @@ __device__ __forceinline__ void codes_bloc(const trc::Taches& taches, const uint
             }
         }
         tc = uniforme(tache_moe_e(pm, i, j, e));
-        // the selected experts' records for the later passes (gate with down, and up), read with
-        // scalar loads from the directory, which nothing writes during the step
-        if (blockIdx.x == 0 && threadIdx.x < 64u) {
-            const MatricePartie r = tc.matrice != 0 ? lire_matrice_constante(tc.matrice) : MatricePartie{};
-            if (threadIdx.x == 0) ecrire_matrice(reinterpret_cast<void*>(pm.resolus + uint64_t(i * 3u + j) * sizeof(MatricePartie)), r);
-            if (j == 0) {
-                const MatricePartie r2 = e < pm.E ? lire_matrice_constante(pm.repertoire + uint64_t(e * 3u + 2u) * sizeof(MatricePartie))
-                                                  : MatricePartie{};
-                if (threadIdx.x == 0) ecrire_matrice(reinterpret_cast<void*>(pm.resolus + uint64_t(i * 3u + 2u) * sizeof(MatricePartie)), r2);
-            }
-        }
+        e_choisi = e;
     } else {
         tc = tx;
     }
-    const MatricePartie mrec = obtenir_matrice_scalaire(tc);
+    // SW: the gate and up records' N_codes and check flags, requested with the job's record and
+    // checked before the job's (a check after the branch below would let the compiler move their
+    // loads down to it, a round trip of their own)
+    bool sw_bon = false;
+    uint32_t sw_lg = 7u;  // log2 of the gate/up tiles' block count (8 N_codes: 128 or 256)
+    MatricePartie mrec;
+    if (SW) {
+        // the down job's record is a resolved one (never absent), read with the gate and up
+        // records' fields in one batch; the checks in bitwise form, so that no branch splits them
+        u32x4 gu{lire_u32_constante(tg.matrice + offsetof(MatricePartie, cN)),
+                 lire_u32_constante(tg.matrice + offsetof(MatricePartie, bon)),
+                 lire_u32_constante(tu.matrice + offsetof(MatricePartie, cN)),
+                 lire_u32_constante(tu.matrice + offsetof(MatricePartie, bon))};
+        mrec = lire_matrice_groupee(tc.matrice, gu);
+        const uint32_t g_cN = gu[0], g_bon = gu[1], u_cN = gu[2], u_bon = gu[3];
+        const uint32_t Bg = tg.colonnes / 32u;
+        const uint32_t lg = g_cN == 32u ? 8u : 7u;
+        sw_bon = (g_bon != 0) & (u_bon != 0) & ((g_cN == 16u) | (g_cN == 32u)) & (u_cN == g_cN) & (Bg >= 8u) &
+                 (((Bg - 1u) >> lg) + 2u <= tg.kmax) & (tg.lignes >= R_sw) & (tu.lignes >= R_sw);
+        sw_lg = lg;
+    } else if (GU) {
+        // the chosen expert's record from the directory (an index past the experts, a slot the
+        // top-k left empty, reads the last expert's record and fails its checks), in one batch
+        u32x4 rien{0u, 0u, 0u, 0u};
+        const uint32_t e_mat = uniforme32(min(e_choisi, pm.E - 1u));
+        mrec = lire_matrice_groupee(pm.repertoire + uint64_t(e_mat * 3u + j) * sizeof(MatricePartie), rien);
+        mrec.bon = e_choisi < pm.E ? mrec.bon : 0u;
+    } else {
+        mrec = obtenir_matrice_scalaire(tc);
+    }
     const PrepCodes p = preparer_codes(tc, mrec);
     const bool bon = p.bon && x_lds && (!SW || (tg.kmax == 2u && copies));  // uniform over the block
     if (!bon) {
@@ -348,20 +384,11 @@ __device__ __forceinline__ void codes_bloc(const trc::Taches& taches, const uint
     const float b_copie = glob<float>(copies ? reinterpret_cast<const void*>(mrec.biais.p) : reinterpret_cast<const void*>(luts))
         [copies ? min(r_copie, tc.lignes - 1u) : 0u];
     // SW: the gate and up records (scalar loads from the resolved records), for their checks
-    bool sw_bon = false;
-    uint32_t sw_lg = 7u;  // log2 of the gate/up tiles' block count (8 N_codes: 128 or 256)
-    if (SW) {
-        const MatricePartie mg = lire_matrice_constante(tg.matrice), mu = lire_matrice_constante(tu.matrice);
-        const uint32_t Bg = tg.colonnes / 32u;
-        sw_bon = mg.bon != 0 && mu.bon != 0 && (mg.cN == 16u || mg.cN == 32u) && mu.cN == mg.cN && Bg >= 8u &&
-                 (Bg - 1u) / (8u * mg.cN) + 2u <= tg.kmax && tg.lignes >= R_sw && tu.lignes >= R_sw;
-        sw_lg = mg.cN == 32u ? 8u : 7u;
-    }
     const Avance avance0 = premiere_avance<true>(p, tc.lignes, g);
     // issued here, ahead of the LDS staging below (which waits on the earlier loads only)
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
-    asm volatile("" ::"v"(rep_chaud));  // complete before the decode LUTs, issued after it
+    if (topk) asm volatile("" ::"v"(rep_chaud));  // complete before the decode LUTs, issued after it
     if (SW) {
         const uint32_t Bg = tg.colonnes / 32u;
 #pragma unroll

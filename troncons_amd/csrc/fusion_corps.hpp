@@ -136,6 +136,38 @@ __device__ __forceinline__ MatricePartie lire_matrice_constante(uint64_t adresse
     return *reinterpret_cast<const MatricePartie*>(adresse);  // host pass of a device function: never run
 #endif
 }
+// The same, its seven 16-byte words (the eighth is reserve) read with scalar loads that are all
+// issued before any is used: the empty asm takes every word (and `extra`, values the caller read
+// just before, such as other records' fields), so one wait covers them all. Without it the
+// compiler moves each field's load down to its first use, one round trip after another.
+__device__ __forceinline__ MatricePartie lire_matrice_groupee(uint64_t adresse, u32x4& extra) {
+    struct Mots {
+        u32x4 w[8];
+    } m;
+#if defined(__HIP_DEVICE_COMPILE__)
+    typedef const __attribute__((address_space(4))) u32x4* MotsConstants;
+    const MotsConstants q = reinterpret_cast<MotsConstants>(adresse);
+#pragma unroll
+    for (uint32_t k = 0; k < 7u; ++k) m.w[k] = q[k];
+    asm volatile("" : "+s"(m.w[0]), "+s"(m.w[1]), "+s"(m.w[2]), "+s"(m.w[3]), "+s"(m.w[4]), "+s"(m.w[5]),
+                 "+s"(m.w[6]), "+s"(extra));
+#else
+    const u32x4* q = reinterpret_cast<const u32x4*>(adresse);  // host pass of a device function: never run
+    for (uint32_t k = 0; k < 7u; ++k) m.w[k] = q[k];
+#endif
+    m.w[7] = u32x4{0u, 0u, 0u, 0u};
+    static_assert(sizeof(Mots) == sizeof(MatricePartie), "a record is 8 words");
+    return __builtin_bit_cast(MatricePartie, m);
+}
+
+// One u32 of such a record, by a scalar load.
+__device__ __forceinline__ uint32_t lire_u32_constante(uint64_t adresse) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    return *reinterpret_cast<const __attribute__((address_space(4))) uint32_t*>(adresse);
+#else
+    return *reinterpret_cast<const uint32_t*>(adresse);  // host pass of a device function: never run
+#endif
+}
 __device__ __forceinline__ MatricePartie obtenir_matrice_scalaire(const Tache& tc) {
     if (tc.matrice != 0) return lire_matrice_constante(tc.matrice);
     return analyser_matrice(reinterpret_cast<const uint8_t*>(tc.partie), tc.j, tc.lignes, tc.colonnes);
