@@ -473,17 +473,19 @@ def bench_flux(args, E, k, C, dims, dev, flux, fz, x_tok, n_fils):
     xs = torch.from_numpy(x_tok).to(dev)
     vx = [V(xs, 4 * C * t, 4 * C) for t in range(len(x_tok))]
     residu = torch.zeros(C, dtype=torch.float32, device=dev)
-    n_tok = args.steps + args.warmup
+    # tokens run between the two stats reads: the GPU warm-up's, the warm-up and the timed ones
+    n_tok = [0]
 
     def pas(s):
+        n_tok[0] += 1
         moteur.jeton(vx[s % len(vx)], V(residu), f=flux)
 
     s0 = moteur.stats()
     ms = temps(pas, args.steps, args.warmup, flux)
     s1 = moteur.stats()
     assert (moteur.controle() == 0).all(), f"control words {moteur.controle()}"
-    octets_tok = (s1["octets_copies"] - s0["octets_copies"]) / n_tok
-    attente_couche = (s1["us_attente_routeur"] - s0["us_attente_routeur"]) / (n_tok * L)
+    octets_tok = (s1["octets_copies"] - s0["octets_copies"]) / n_tok[0]
+    attente_couche = (s1["us_attente_routeur"] - s0["us_attente_routeur"]) / (n_tok[0] * L)
     # the routing of the timed tokens (x fixed per token: the same choices every time)
     choix = []
     for s in range(args.steps):
@@ -1205,7 +1207,7 @@ def main():
     trafic = trafic_mesure() if n_couches == 1 else None
     roofline = {
         "bound": "hbm",
-        "kernel": ("fusion_codes (gate/up launch) + fusion_codes_swiglu (down launch)" if nom_codes == "fusion_codes"
+        "kernel": ("fusion_codes_gu (gate/up launch) + fusion_codes_swiglu (down launch)" if nom_codes == "fusion_codes"
                    else "fusion_gemv (gate/up launch + down launch)"),
         "achieved": round(float(atteint), 1), "peak": PIC_HBM, "unit": "GB/s",
         "frac": round(float(atteint / PIC_HBM), 4), "traffic": trafic,
