@@ -512,7 +512,8 @@ fusion_finir_swiglu(trc::Taches taches, float* __restrict__ act, uint32_t R) {
 
 // residu[r] += ((w0 s0[r] + w1 s1[r]) + w2 s2[r]) + ... over the k down jobs (MoE layer).
 // OPT_BIAIS (one row per thread, 2 partial-sum slots per row): the row's residual, partial sums and
-// bias copies are loaded before the records are read, so that both take one round trip.
+// bias copies are loaded before the records' fields are read (scalar loads), so that both take one
+// round trip.
 extern "C" __global__ void __launch_bounds__(256)
 fusion_finir_combiner(trc::Taches taches) {
     using namespace trc;
@@ -525,7 +526,7 @@ fusion_finir_combiner(trc::Taches taches) {
             constexpr uint32_t KM = decltype(km)::value;
             const uint32_t D = moe.lignes[2], Rm = max(moe.lignes[0], moe.lignes[2]);
             const uint32_t r = blockIdx.x * 256u + threadIdx.x, rr = min(r, D - 1u);
-            const float res = reinterpret_cast<const float*>(moe.residu)[rr];
+            const float res = glob<float>(reinterpret_cast<const void*>(moe.residu))[rr];
             u32x2 p[KM];
             float bi[KM], w[KM];
 #pragma unroll
@@ -535,16 +536,39 @@ fusion_finir_combiner(trc::Taches taches) {
                 bi[i] = glob<float>(reinterpret_cast<const void*>(moe.biais))[uint64_t(ii * 3u + 2u) * Rm + rr];
                 w[i] = glob<float>(reinterpret_cast<const void*>(moe.poids))[ii];
             }
-            preparer_fins(taches, 0, moe.k, fins);
-            if (r >= D) return;
-            for (uint32_t i = 0; i < moe.k; ++i)
-                if (!fins[i].bon || r >= fins[i].lignes || fins[i].kmax != 2u) return;
+            // the selected down records' N_codes and check flag (written by the gate/up launch), read
+            // with scalar loads into registers, all issued before any is used (the empty asm takes
+            // them all, so one wait covers them); the checks in bitwise form, one return: no LDS copy
+            // of the records, no barrier, no round trip per job
+            uint32_t cn[KM], bn[KM];
+#pragma unroll
+            for (uint32_t i = 0; i < KM; ++i) {
+                const uint64_t rec = tache_moe(moe, min(i, moe.k - 1u), 2u).matrice;
+                cn[i] = lire_u32_constante(rec + offsetof(MatricePartie, cN));
+                bn[i] = lire_u32_constante(rec + offsetof(MatricePartie, bon));
+            }
+#pragma unroll
+            for (uint32_t i = 0; i < KM; ++i) asm volatile("" : "+s"(cn[i]), "+s"(bn[i]));
+            Fin f[KM];
+            bool ok = r < D;
+#pragma unroll
+            for (uint32_t i = 0; i < KM; ++i) {
+                const Tache t = tache_moe(moe, min(i, moe.k - 1u), 2u);
+                f[i].B = t.colonnes / 32u;
+                f[i].bpt = 8u * max(cn[i], 1u);
+                f[i].kmax = t.kmax;
+                f[i].lignes = t.lignes;
+                // (B - 1) / bpt + 2 <= kmax, without the division
+                f[i].bon = (bn[i] != 0u) & (f[i].B >= 8u) & (t.kmax >= 2u) & (f[i].B - 1u < (t.kmax - 1u) * f[i].bpt);
+                ok &= (i >= moe.k) | (f[i].bon & (r < f[i].lignes) & (f[i].kmax == 2u));
+            }
+            if (!ok) return;
             float s = 0.0f;
 #pragma unroll
             for (uint32_t i = 0; i < KM; ++i) {
                 if (i < moe.k) {
                     float si = __uint_as_float(p[i].x);
-                    if (partiels_en_plus(fins[i], r) >= 1u) si += __uint_as_float(p[i].y);
+                    if (partiels_en_plus(f[i], r) >= 1u) si += __uint_as_float(p[i].y);
                     si = si + bi[i];
                     const float pr = w[i] * si;
                     s = i == 0 ? pr : s + pr;
