@@ -420,7 +420,9 @@ __device__ __forceinline__ void corps_codes_n(const Tache& tc, const PrepCodes& 
         const uint32_t o0 = a.o2;
         uint32_t rho = p.B.quotient(m0 * 8u);
         const uint32_t rho0 = rho, case0 = t - (rho0 * B) / BPT;  // first tile of row rho0
-        auto ecrire = [&](float s) { partiels[rho * kmax + (rho == rho0 ? case0 : 0u)] = s; };
+        // a global store: a flat one would also count on the LDS counter, and the next LUT read's
+        // wait would then wait for the store's completion
+        auto ecrire = [&](float s) { ecrire_global<float>(partiels + rho * kmax + (rho == rho0 ? case0 : 0u), s); };
         uint32_t ent_suiv = tuile ? lire_lds<uint32_t>(a_ent_q) : ENTC_BOURRAGE;
         const uint32_t nb_min = min(nb_a, nb_b);
         float acc = 0.0f;
@@ -551,7 +553,7 @@ __device__ __forceinline__ void poser_echelles(uint8_t* ech, uint32_t b0, uint32
     if (b0 + 4u <= nblocs) {
         ecrire_global<uint32_t>(reinterpret_cast<uint32_t*>(ech + b0), e4);
     } else {
-        for (uint32_t k = 0; b0 + k < nblocs; ++k) ech[b0 + k] = uint8_t(e4 >> (8u * k));
+        for (uint32_t k = 0; b0 + k < nblocs; ++k) ecrire_global<uint8_t>(ech + b0 + k, uint8_t(e4 >> (8u * k)));
     }
 }
 
@@ -669,7 +671,7 @@ __device__ __forceinline__ void corps_codes_emplacement_n(const PrepCodes& p, ui
                     const u32x4 c = lire_lds<u32x4>(a_etage + 16u * v);
                     const uint32_t w = (m0 + m - 3u) * VOIES + 4u * v;
                     if (tuile && w < mots_utiles)  // read back by another launch: no reuse in the L2
-                        __builtin_nontemporal_store(c, reinterpret_cast<u32x4*>(codes + w));
+                        ecrire_global_nt<u32x4>(codes + w, c);
                 }
             } else {
                 const uint32_t w = (m0 + m) * VOIES + v;

@@ -428,7 +428,7 @@ __device__ __forceinline__ void codes_bloc(const trc::Taches& taches, const uint
     // around each wavefront's first DELTA decode
     corps_codes(tc, p, lds, luts + uint64_t(j) * 4u * M, controle, avance0, g);
     if (copies && threadIdx.x < n_copie && r_copie < tc.lignes)
-        reinterpret_cast<float*>(pm.biais)[uint64_t(i_moe * 3u + j_moe) * Rm_moe + r_copie] = b_copie;
+        ecrire_global<float>(reinterpret_cast<float*>(pm.biais) + uint64_t(i_moe * 3u + j_moe) * Rm_moe + r_copie, b_copie);
 }
 
 extern "C" __global__ void __launch_bounds__(1024)
@@ -574,7 +574,7 @@ fusion_finir_combiner(trc::Taches taches) {
                     s = i == 0 ? pr : s + pr;
                 }
             }
-            reinterpret_cast<float*>(moe.residu)[r] = res + s;
+            ecrire_global<float>(reinterpret_cast<float*>(moe.residu) + r, res + s);
         };
         if (moe.k <= 4u)  // uniform
             combiner(std::integral_constant<uint32_t, 4>{});

@@ -312,6 +312,11 @@ template <typename T>
 __device__ __forceinline__ void ecrire_global(void* p, T v) {
     *(__attribute__((address_space(1))) T*)(p) = v;
 }
+// The same with the nontemporal hint (data read back by another launch: no reuse in the L2).
+template <typename T>
+__device__ __forceinline__ void ecrire_global_nt(void* p, T v) {
+    __builtin_nontemporal_store(v, (__attribute__((address_space(1))) T*)(p));
+}
 
 // Context class of a block from its DELTA symbol (decodeur.cuh:185-192, rans.rs:481-486).
 __device__ __forceinline__ uint32_t classe_delta(uint32_t d) { return d < 128u ? 0u : (d == 128u ? 1u : 2u); }

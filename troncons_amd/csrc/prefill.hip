@@ -342,7 +342,7 @@ prefill_emplacements_delta_interne(ParamsPrefill pp, const uint32_t* __restrict_
     __shared__ __attribute__((aligned(16384))) uint8_t lds[LDS_GEMV];
     constexpr uint32_t FILS = PF_FILS_RAPIDE;
     const uint32_t e = blockIdx.z, j = blockIdx.y;
-    if (uniforme32(reinterpret_cast<const uint32_t*>(pp.compte)[e]) == 0u) return;
+    if (uniforme32(glob<uint32_t>(reinterpret_cast<const void*>(pp.compte))[e]) == 0u) return;
     const Grille g{FILS, uniforme32(gridDim.x)};
     const uint32_t R = choisir(pp.lignes, j), C = choisir(pp.colonnes, j);
     constexpr uint32_t LOT_D = (M / 4u + FILS - 1u) / FILS;  // 16-byte groups of the DELTA LUT per thread
@@ -569,7 +569,7 @@ template <uint32_t J, bool EMPL>  // EMPL: long tiles, the band copied from the 
 __device__ __forceinline__ void prefill_bande(const ParamsPrefill& pp, const uint32_t* __restrict__ luts,
                                               uint32_t* __restrict__ controle, uint8_t* lds) {
     const uint32_t e = blockIdx.y / J, j = J == 2u ? (blockIdx.y & 1u) : 2u;
-    const uint32_t n_e = uniforme32(reinterpret_cast<const uint32_t*>(pp.compte)[e]);
+    const uint32_t n_e = uniforme32(glob<uint32_t>(reinterpret_cast<const void*>(pp.compte))[e]);
     if (n_e == 0u) return;
     const uint32_t R = choisir(pp.lignes, j), C = choisir(pp.colonnes, j), B = C / 32u;
     const uint32_t RB = choisir(pp.rb, j);
@@ -607,7 +607,7 @@ __device__ __forceinline__ void prefill_bande(const ParamsPrefill& pp, const uin
     const uint32_t debut_brut = glob<uint32_t>(reinterpret_cast<const void*>(pp.debut))[e];
     ChargeLut<3> charge_lut;
     if (!depuis_emplacement) charge_lut.demarrer(lut_src, 3u * M / 4u);
-    const MatricePartie m = *reinterpret_cast<const MatricePartie*>(pp.repertoire + uint64_t(e * 3u + j) * sizeof(MatricePartie));
+    const MatricePartie m = lire_matrice_constante(pp.repertoire + uint64_t(e * 3u + j) * sizeof(MatricePartie));
     const EnteteRans h = entete_de(m.codes, m.cP, m.cN, m.cT, m.cW);
     const uint32_t N = h.N;
     const uint32_t t_a = N ? (ba / 8u) / N : 0u, t_b = N ? ((bb - 1u) / 8u) / N : 0u;
@@ -649,7 +649,7 @@ __device__ __forceinline__ void prefill_bande(const ParamsPrefill& pp, const uin
     const uint32_t lr = lane & 15u, lg = lane >> 4;
     const uint32_t P = uniforme32(min(p_brut, PF_PIECES_BF));
     const uint32_t debut_e = uniforme32(debut_brut);
-    const uint32_t* paires = reinterpret_cast<const uint32_t*>(pp.paires);
+    const gptr<uint32_t> paires = glob<uint32_t>(reinterpret_cast<const void*>(pp.paires));
     const uint64_t pas_p = uint64_t(J == 2u ? pp.bx : pp.bact) * 64u;
     const uint8_t* bsrc = reinterpret_cast<const uint8_t*>(J == 2u ? pp.xb : pp.ab) + 16u * lg;
     const uint32_t wu = uniforme32(w);
@@ -727,7 +727,7 @@ __device__ __forceinline__ void prefill_bande(const ParamsPrefill& pp, const uin
     // split 16 ways; the partial sums are added in wave order. Each B load feeds every row tile, and
     // B is read once per band.
     const uint32_t nrt = RB / 16u;
-    const float* biais = reinterpret_cast<const float*>(m.biais.p);
+    const gptr<float> biais = glob<float>(reinterpret_cast<const void*>(m.biais.p));
     // one pass over NT column tiles from tile tt; the first pass is peeled off the loop so that its
     // preloaded B dies there
     auto passe = [&](uint32_t tt, auto nt_t, auto premier) {
@@ -798,9 +798,9 @@ __device__ __forceinline__ void prefill_bande(const ParamsPrefill& pp, const uin
                     const uint32_t cc = paires[debut_e + jeton];
                     const float y = s + biais[r0 + ligne];
                     if (J == 2u)
-                        reinterpret_cast<float*>(pp.gu)[(uint64_t(cc) * 2u + j) * R + r0 + ligne] = y;
+                        ecrire_global<float>(reinterpret_cast<float*>(pp.gu) + (uint64_t(cc) * 2u + j) * R + r0 + ligne, y);
                     else
-                        reinterpret_cast<float*>(pp.s)[uint64_t(cc) * pp.D + r0 + ligne] = y;
+                        ecrire_global<float>(reinterpret_cast<float*>(pp.s) + uint64_t(cc) * pp.D + r0 + ligne, y);
                 }
             }
         }
@@ -841,7 +841,7 @@ template <uint32_t J>
 __device__ __forceinline__ void prefill_bande_empl(const ParamsPrefill& pp, uint32_t* __restrict__ controle, uint8_t* lds) {
     constexpr uint32_t FILS = PFE_FILS, NRT = PFE_NRT, RB = PFE_RB;
     const uint32_t e = blockIdx.y / J, j = J == 2u ? (blockIdx.y & 1u) : 2u;
-    const uint32_t n_e = uniforme32(reinterpret_cast<const uint32_t*>(pp.compte)[e]);
+    const uint32_t n_e = uniforme32(glob<uint32_t>(reinterpret_cast<const void*>(pp.compte))[e]);
     if (n_e == 0u) return;
     const uint32_t R = choisir(pp.lignes, j), C = choisir(pp.colonnes, j), B = C / 32u;
     const uint32_t r0 = blockIdx.x * RB;
@@ -867,13 +867,13 @@ __device__ __forceinline__ void prefill_bande_empl(const ParamsPrefill& pp, uint
     charger_copie(0u, 0u);
     const uint32_t p_brut = glob<uint32_t>(reinterpret_cast<const void*>(pp.pieces))[J == 2u ? 0 : 1];
     const uint32_t debut_brut = glob<uint32_t>(reinterpret_cast<const void*>(pp.debut))[e];
-    const MatricePartie m = *reinterpret_cast<const MatricePartie*>(pp.repertoire + uint64_t(e * 3u + j) * sizeof(MatricePartie));
+    const MatricePartie m = lire_matrice_constante(pp.repertoire + uint64_t(e * 3u + j) * sizeof(MatricePartie));
     const uint32_t lane = __lane_id(), lr = lane & 15u, lg = lane >> 4;
     const uint32_t wu = uniforme32(threadIdx.x >> 6);
     const uint32_t base = adresse_lds(lds);
     const uint32_t P = uniforme32(min(p_brut, PF_PIECES_BF));
     const uint32_t debut_e = uniforme32(debut_brut);
-    const uint32_t* paires = reinterpret_cast<const uint32_t*>(pp.paires);
+    const gptr<uint32_t> paires = glob<uint32_t>(reinterpret_cast<const void*>(pp.paires));
     const uint64_t pas_p = uint64_t(J == 2u ? pp.bx : pp.bact) * 64u;
     const uint8_t* bsrc = reinterpret_cast<const uint8_t*>(J == 2u ? pp.xb : pp.ab) + 16u * lg;
     // Column tiles of 16 pairs go two at a time while two remain, waves 0-3 on the first and 4-7 on
@@ -936,7 +936,7 @@ __device__ __forceinline__ void prefill_bande_empl(const ParamsPrefill& pp, uint
     __syncthreads();
 
     // ---- MFMA passes (as prefill_bande's, 8 wavefronts)
-    const float* biais = reinterpret_cast<const float*>(m.biais.p);
+    const gptr<float> biais = glob<float>(reinterpret_cast<const void*>(m.biais.p));
     auto passe = [&](uint32_t tt, auto nt_t, auto premier) {
         constexpr uint32_t NT = decltype(nt_t)::value;
         constexpr bool PREMIER = decltype(premier)::value;
@@ -995,9 +995,9 @@ __device__ __forceinline__ void prefill_bande_empl(const ParamsPrefill& pp, uint
                     const uint32_t cc = paires[debut_e + jeton];
                     const float y = s + biais[r0 + ligne];
                     if (J == 2u)
-                        reinterpret_cast<float*>(pp.gu)[(uint64_t(cc) * 2u + j) * R + r0 + ligne] = y;
+                        ecrire_global<float>(reinterpret_cast<float*>(pp.gu) + (uint64_t(cc) * 2u + j) * R + r0 + ligne, y);
                     else
-                        reinterpret_cast<float*>(pp.s)[uint64_t(cc) * pp.D + r0 + ligne] = y;
+                        ecrire_global<float>(reinterpret_cast<float*>(pp.s) + uint64_t(cc) * pp.D + r0 + ligne, y);
                 }
             }
         }
