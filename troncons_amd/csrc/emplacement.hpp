@@ -137,7 +137,7 @@ __device__ __forceinline__ void echelles_vers_emplacement(const DescFlux& fd, co
             if (b0 + 4u <= nblocs) {
                 ecrire_global<uint32_t>(ech + b0, e4);  // b0 % 4 == 0 and the scales are 256-aligned
             } else {
-                for (uint32_t k = 0; b0 + k < nblocs; ++k) ech[b0 + k] = uint8_t(e4 >> (8u * k));
+                for (uint32_t k = 0; b0 + k < nblocs; ++k) ecrire_global<uint8_t>(ech + b0 + k, uint8_t(e4 >> (8u * k)));
             }
         };
         uint32_t m = 0;

@@ -572,7 +572,7 @@ __device__ __forceinline__ PrepGemv preparer_gemv(const Tache& tc, const Matrice
 // Row bookkeeping shared by both CODES bodies: the (row, tile) partial slot of row r for tile t.
 __device__ __forceinline__ void ecrire_partiel(float* partiels, uint32_t kmax, uint32_t r, uint32_t t, uint32_t B,
                                                uint32_t bpt, float s) {
-    partiels[r * kmax + (t - premiere_tuile(r, B, bpt))] = s;
+    ecrire_global<float>(partiels + r * kmax + (t - premiere_tuile(r, B, bpt)), s);
 }
 
 // CODES_CTX tiles -> partial sums of W x with x read from device memory (rows of any width; the
@@ -840,7 +840,7 @@ __device__ __forceinline__ void corps_gemv_rapide(const Tache& tc, const PrepGem
         // partial slot of (row, t): rows that start inside tile t use slot 0, the tile's first row
         // (which may start in an earlier tile) its own offset, computed once
         const uint32_t rho0 = rho, case0 = t - premiere_tuile(rho0, B, bpt);
-        auto ecrire = [&](float s) { partiels[rho * kmax + (rho == rho0 ? case0 : 0u)] = s; };
+        auto ecrire = [&](float s) { ecrire_global<float>(partiels + rho * kmax + (rho == rho0 ? case0 : 0u), s); };
         uint32_t ent_suiv = tuile ? lire_lds<uint32_t>(a_ent_q) : ENTREE_BOURRAGE;
         const uint32_t nb_min = min(nb_a, nb_b);
         float acc = 0.0f;
