@@ -97,7 +97,7 @@ __device__ __forceinline__ void gemv_q8_0_rangees(const uint8_t* __restrict__ W,
     const uint32_t B = C / 32u;
     const uint64_t octets_ligne = uint64_t(B) * Q8_OCTETS_BLOC;
     const uintptr_t fin_matrice = reinterpret_cast<uintptr_t>(W) + uint64_t(R) * octets_ligne;
-    const f32x4* x4 = reinterpret_cast<const f32x4*>(x);
+    const f32x4* x4 = reinterpret_cast<const f32x4*>(x);  // x may be in LDS: a generic pointer
     float acc[LIGNES];
     uintptr_t lig[LIGNES];
 #pragma unroll
@@ -119,14 +119,14 @@ __device__ __forceinline__ void gemv_q8_0_rangees(const uint8_t* __restrict__ W,
                 const uintptr_t a = lig[i] + uint64_t(b) * Q8_OCTETS_BLOC;
                 const uintptr_t a4 = a & ~uintptr_t(3);
                 decal[it][i] = uint32_t(a - a4);  // 0 or 2: where d starts in the window
-                const uint32_t* fen = reinterpret_cast<const uint32_t*>(a4);
+                const gptr<uint32_t> fen = glob<uint32_t>(reinterpret_cast<const void*>(a4));
 #pragma unroll
                 for (uint32_t t = 0; t < 8; ++t) w[it][i][t] = fen[t];
                 // dword 8 holds the last codes, read as two halves: the high one lies past the block
                 // when d sits at byte 0 and is then unused, so its address is clamped to the matrix
                 // (no branch around a load, so no load waits for another)
-                const uint16_t* h8 = reinterpret_cast<const uint16_t*>(fen + 8);
-                const uint16_t* h9 = reinterpret_cast<const uint16_t*>(min(a4 + 34u, fin_matrice - 2u));
+                const gptr<uint16_t> h8 = glob<uint16_t>(reinterpret_cast<const void*>(a4 + 32u));
+                const gptr<uint16_t> h9 = glob<uint16_t>(reinterpret_cast<const void*>(min(a4 + 34u, fin_matrice - 2u)));
                 w[it][i][8] = uint32_t(h8[0]) | (uint32_t(h9[0]) << 16);
             }
         }
@@ -177,7 +177,7 @@ constexpr uint32_t lignes_bloc() {
 
 // x (C floats, C a multiple of 32) copied into the block's LDS with 16-byte loads.
 __device__ __forceinline__ void x_vers_lds(const float* __restrict__ x, f32x4* xs, uint32_t C) {
-    const f32x4* x4 = reinterpret_cast<const f32x4*>(x);
+    const gptr<f32x4> x4 = glob<f32x4>(x);
     for (uint32_t j = threadIdx.x; j < C / 4u; j += FILS_PASSE) xs[j] = x4[j];
     __syncthreads();
 }
@@ -201,7 +201,7 @@ gemv_q8_0(const uint8_t* __restrict__ W, const float* __restrict__ x, const floa
     const uint32_t B = C / 32u;
     const uint64_t octets_ligne = uint64_t(B) * Q8_OCTETS_BLOC;
     const uintptr_t fin_matrice = reinterpret_cast<uintptr_t>(W) + uint64_t(R) * octets_ligne;
-    const f32x4* x4 = reinterpret_cast<const f32x4*>(x);
+    const gptr<f32x4> x4 = glob<f32x4>(x);
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     uint32_t lig[4];
 #pragma unroll
@@ -222,14 +222,14 @@ gemv_q8_0(const uint8_t* __restrict__ W, const float* __restrict__ x, const floa
                                 uint64_t(b) * Q8_OCTETS_BLOC;
             const uintptr_t a4 = a & ~uintptr_t(3);
             const uint32_t decal = uint32_t(a - a4);
-            const uint32_t* fen = reinterpret_cast<const uint32_t*>(a4);
+            const gptr<uint32_t> fen = glob<uint32_t>(reinterpret_cast<const void*>(a4));
             uint32_t w[9];
 #pragma unroll
             for (uint32_t t = 0; t < 8; ++t) w[t] = fen[t];
             // dword 8 as two halves: the high one lies past the block when d sits at byte 0 and is
             // then unused, so its address is clamped to the matrix (no branch around a load)
-            const uint16_t* h8 = reinterpret_cast<const uint16_t*>(fen + 8);
-            const uint16_t* h9 = reinterpret_cast<const uint16_t*>(min(a4 + 34u, fin_matrice - 2u));
+            const gptr<uint16_t> h8 = glob<uint16_t>(reinterpret_cast<const void*>(a4 + 32u));
+            const gptr<uint16_t> h9 = glob<uint16_t>(reinterpret_cast<const void*>(min(a4 + 34u, fin_matrice - 2u)));
             w[8] = uint32_t(h8[0]) | (uint32_t(h9[0]) << 16);
             const float d = f16_vers_f32(decal ? (w[0] >> 16) : (w[0] & 0xFFFFu));
             const uint32_t bits = 8u * (2u + decal);
